@@ -1,0 +1,293 @@
+"""ctypes binding of the C oracle.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module, and only as the checker of the HIP path.  States are dicts of numpy
+arrays with a leading env dimension, keyed by the reference's State leaf names
+plus "environment_root" (uint32[L, 2]) and "episode_index" (uint32[L]).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+from nanorts_amd.content import GameConfig
+from nanorts_amd.model import LEAF_NAMES, STATE_LEAVES, STRATEGY_CODES, leaf_shape
+
+HERE = Path(__file__).resolve().parent
+LIBRARY_PATH = HERE / "libnanorts_oracle.so"
+REF_PATH = HERE / "_ref" / "libref_draws.so"
+
+MAX_TYPES = 8
+
+
+def build() -> None:
+    """Compile the oracle (and oracle/_ref when the reference checkout exists)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def _load() -> ctypes.CDLL:
+    if not LIBRARY_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIBRARY_PATH))
+    lib.nro_rollout.restype = ctypes.c_int32
+    lib.nro_state_violations.restype = ctypes.c_int32
+    lib.nro_conflict_draw.restype = ctypes.c_int32
+    lib.nro_randint01.restype = ctypes.c_int32
+    return lib
+
+
+_I32x8 = ctypes.c_int32 * MAX_TYPES
+
+
+class Game(ctypes.Structure):
+    _fields_ = [
+        ("height", ctypes.c_int32), ("width", ctypes.c_int32), ("cells", ctypes.c_int32),
+        ("neutral", ctypes.c_int32), ("capacity", ctypes.c_int32), ("entities", ctypes.c_int32),
+        ("types", ctypes.c_int32), ("offsets", ctypes.c_int32), ("strategy", ctypes.c_int32),
+        ("max_cycles", ctypes.c_int32),
+        ("cost", _I32x8), ("hit_points", _I32x8), ("produce_time", _I32x8), ("move_time", _I32x8),
+        ("attack_time", _I32x8), ("harvest_time", _I32x8), ("attack_range", _I32x8), ("attack_damage", _I32x8),
+        ("harvest_amount", _I32x8), ("sight_radius", _I32x8), ("is_resource", _I32x8), ("is_stockpile", _I32x8),
+        ("can_harvest", _I32x8), ("can_move", _I32x8), ("can_attack", _I32x8),
+        ("produces", ctypes.c_int32 * (MAX_TYPES * MAX_TYPES)),
+        ("terrain", ctypes.c_void_p),
+    ]
+
+
+_STATE_FIELDS = list(LEAF_NAMES) + ["environment_root", "episode_index"]
+
+
+class State(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in _STATE_FIELDS]
+
+
+class Commands(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in
+                ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")]
+
+
+class StepOut(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in
+                ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
+                 "admitted_attack")]
+
+
+class EnvOut(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in
+                ("reward", "done", "terminated", "truncated", "winner", "spawn_overflowed", "feature_maps",
+                 "scalars")]
+
+
+def _ptr(array: np.ndarray | None) -> ctypes.c_void_p | None:
+    if array is None:
+        return None
+    assert array.flags["C_CONTIGUOUS"], "oracle buffers must be C-contiguous"
+    return ctypes.c_void_p(array.ctypes.data)
+
+
+class Oracle:
+    """The oracle bound to one game configuration."""
+
+    def __init__(self, game: GameConfig):
+        self.lib = _load()
+        self.game = game
+        bucket = game.bucket
+        cols = game.columns
+        self._terrain = np.ascontiguousarray(game.terrain.reshape(-1).astype(np.uint8))
+        g = Game()
+        g.height, g.width, g.cells = bucket.height, bucket.width, bucket.cell_count
+        g.neutral, g.capacity, g.entities = bucket.neutral_capacity, bucket.per_player_capacity, bucket.entity_capacity
+        g.types, g.offsets = bucket.unit_type_capacity, bucket.attack_offset_capacity
+        g.strategy = STRATEGY_CODES[bucket.conflict_strategy]
+        g.max_cycles = game.max_cycles
+        T = bucket.unit_type_capacity
+        for name in ("cost", "hit_points", "produce_time", "move_time", "attack_time", "harvest_time",
+                     "attack_range", "attack_damage", "harvest_amount", "sight_radius", "is_resource",
+                     "is_stockpile", "can_harvest", "can_move", "can_attack"):
+            arr = getattr(g, name)
+            for t in range(T):
+                arr[t] = int(cols[name][t])
+        for p in range(T):
+            for q in range(T):
+                g.produces[p * MAX_TYPES + q] = int(cols["produces"][p, q])
+        g.terrain = self._terrain.ctypes.data
+        self.g = g
+        self.initial = batch_initial(game, 1, np.zeros((1, 2), np.uint32))
+        self._initial_struct = state_struct(self.initial)
+        self.width = 22 + T + bucket.attack_offset_capacity
+
+    # -- helpers ---------------------------------------------------------
+    def _s(self, state: dict[str, np.ndarray]) -> State:
+        return state_struct(state)
+
+    def core_step(self, state, commands: dict[str, np.ndarray], keys: np.ndarray) -> dict[str, np.ndarray]:
+        L = state["time"].shape[0]
+        T = self.game.bucket.unit_type_capacity
+        out = {"terminated": np.zeros(L, np.uint8), "truncated": np.zeros(L, np.uint8),
+               "reward": np.zeros((L, 2), np.float32), "admitted_harvest": np.zeros((L, 2), np.int32),
+               "admitted_return": np.zeros((L, 2), np.int32), "admitted_produce": np.zeros((L, 2, T), np.int32),
+               "admitted_attack": np.zeros((L, 2, 3), np.int32)}
+        keep = [np.ascontiguousarray(commands[f], np.int32) for f, _ in Commands._fields_]
+        c = Commands(*[_ptr(a) for a in keep])
+        o = StepOut(*[_ptr(out[f]) for f, _ in StepOut._fields_])
+        keys = np.ascontiguousarray(keys, np.uint32)
+        s = self._s(state)
+        self.lib.nro_core_step(ctypes.byref(self.g), ctypes.byref(s), ctypes.byref(c), _ptr(keys),
+                               ctypes.c_int64(L), ctypes.byref(o))
+        return out
+
+    def legality_rows(self, state) -> np.ndarray:
+        L = state["time"].shape[0]
+        rows = np.zeros((L, 2, self.game.bucket.per_player_capacity, self.width), np.uint8)
+        self.lib.nro_legality_rows(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L), _ptr(rows))
+        return rows.astype(bool)
+
+    def avail_rows(self, state) -> np.ndarray:
+        L = state["time"].shape[0]
+        rows = np.zeros((L, 2, self.game.bucket.per_player_capacity, self.width), np.uint8)
+        self.lib.nro_avail_rows(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L), _ptr(rows))
+        return rows.astype(bool)
+
+    def avail_words(self, state) -> np.ndarray:
+        L = state["time"].shape[0]
+        words = np.zeros((L, 2, self.game.bucket.per_player_capacity, 3), np.uint32)
+        self.lib.nro_avail_words(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L), _ptr(words))
+        return words
+
+    def visible_cells(self, state, observer: int) -> np.ndarray:
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        cells = np.zeros((L, b.height, b.width), np.uint8)
+        self.lib.nro_visible_cells(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L),
+                                   ctypes.c_int32(observer), _ptr(cells))
+        return cells.astype(bool)
+
+    def symbolic(self, state, partial: bool) -> tuple[np.ndarray, np.ndarray]:
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        maps = np.zeros((L, 2, b.height, b.width, 6), np.uint8)
+        scalars = np.zeros((L, 2, 4), np.int32)
+        self.lib.nro_symbolic(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L),
+                              ctypes.c_int32(int(partial)), _ptr(maps), _ptr(scalars))
+        return maps, scalars
+
+    def pixels(self, state, partial: bool, tiles: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        image = np.zeros((L, 2, 16 * b.height, 16 * b.width, 3), np.uint8)
+        scalars = np.zeros((L, 2, 4), np.int32)
+        tiles = np.ascontiguousarray(tiles, np.uint8)
+        self.lib.nro_pixels(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L),
+                            ctypes.c_int32(int(partial)), _ptr(tiles), _ptr(image), _ptr(scalars))
+        return image, scalars
+
+    def decode_actions(self, state, actions: np.ndarray) -> dict[str, np.ndarray]:
+        L = state["time"].shape[0]
+        C = self.game.bucket.per_player_capacity
+        out = {f: np.zeros((L, 2, C), np.int32) for f, _ in Commands._fields_}
+        c = Commands(*[_ptr(out[f]) for f, _ in Commands._fields_])
+        actions = np.ascontiguousarray(actions, np.int32)
+        self.lib.nro_decode_actions(ctypes.byref(self.g), ctypes.byref(self._s(state)), _ptr(actions),
+                                    ctypes.c_int64(L), ctypes.byref(c))
+        return out
+
+    def sample_actions(self, rows: np.ndarray, sample_key, step: int, env0: int = 0) -> np.ndarray:
+        L = rows.shape[0]
+        C = self.game.bucket.per_player_capacity
+        rows = np.ascontiguousarray(rows, np.uint8)
+        key = np.ascontiguousarray(np.asarray(sample_key, np.uint32).reshape(2))
+        actions = np.zeros((L, 2, C, 7), np.int32)
+        self.lib.nro_sample_actions(ctypes.byref(self.g), _ptr(rows), _ptr(key), ctypes.c_int32(step),
+                                    ctypes.c_int64(env0), ctypes.c_int64(L), _ptr(actions))
+        return actions
+
+    def reset_where_done(self, state, done: np.ndarray) -> None:
+        L = state["time"].shape[0]
+        done = np.ascontiguousarray(done, np.uint8)
+        self.lib.nro_reset_where_done(ctypes.byref(self.g), ctypes.byref(self._initial_struct),
+                                      ctypes.byref(self._s(state)), _ptr(done), ctypes.c_int64(L))
+
+    def env_step(self, state, actions: np.ndarray, partial: bool, observe: bool = True) -> dict[str, np.ndarray]:
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        out = {"reward": np.zeros((L, 2), np.float32), "done": np.zeros(L, np.uint8),
+               "terminated": np.zeros(L, np.uint8), "truncated": np.zeros(L, np.uint8),
+               "winner": np.zeros(L, np.int32), "spawn_overflowed": np.zeros(L, np.uint8),
+               "feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if observe else None,
+               "scalars": np.zeros((L, 2, 4), np.int32) if observe else None}
+        o = EnvOut(*[_ptr(out[f]) for f, _ in EnvOut._fields_])
+        actions = np.ascontiguousarray(actions, np.int32)
+        self.lib.nro_env_step(ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)),
+                              _ptr(actions), ctypes.c_int64(L), ctypes.c_int32(int(partial)), ctypes.byref(o))
+        return out
+
+    def rollout(self, state, sample_key, step0: int, steps: int, partial: bool, threads: int = 1,
+                record_actions: bool = False, record: bool = True) -> dict[str, np.ndarray]:
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        key = np.ascontiguousarray(np.asarray(sample_key, np.uint32).reshape(2))
+        out = {
+            "rewards": np.zeros((steps, L, 2), np.float32) if record else None,
+            "dones": np.zeros((steps, L), np.uint8) if record else None,
+            "actions": np.zeros((steps, L, 2, b.per_player_capacity, 7), np.int32) if record_actions else None,
+            "feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if record else None,
+            "scalars": np.zeros((L, 2, 4), np.int32) if record else None,
+        }
+        used = self.lib.nro_rollout(
+            ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)), _ptr(key),
+            ctypes.c_int32(step0), ctypes.c_int32(steps), ctypes.c_int64(L), ctypes.c_int32(int(partial)),
+            ctypes.c_int32(threads), _ptr(out["rewards"]), _ptr(out["dones"]), _ptr(out["actions"]),
+            _ptr(out["feature_maps"]), _ptr(out["scalars"]))
+        out["threads"] = used
+        return out
+
+    def violations(self, state) -> np.ndarray:
+        L = state["time"].shape[0]
+        s = self._s(state)
+        return np.asarray([self.lib.nro_state_violations(ctypes.byref(self.g), ctypes.byref(s), ctypes.c_int64(l))
+                           for l in range(L)], np.int32)
+
+
+def state_struct(state: dict[str, np.ndarray]) -> State:
+    for name in _STATE_FIELDS:
+        if name in state:
+            assert state[name].flags["C_CONTIGUOUS"], name
+    return State(*[_ptr(state.get(name)) for name in _STATE_FIELDS])
+
+
+def batch_initial(game: GameConfig, L: int, roots: np.ndarray) -> dict[str, np.ndarray]:
+    """L copies of the decided initial state with the given env roots."""
+    state = {leaf.name: np.ascontiguousarray(np.broadcast_to(game.initial_state[leaf.name],
+                                                             (L, *leaf_shape(leaf, game.bucket))).copy())
+             for leaf in STATE_LEAVES}
+    state["environment_root"] = np.ascontiguousarray(np.asarray(roots, np.uint32).reshape(L, 2))
+    state["episode_index"] = np.zeros(L, np.uint32)
+    return state
+
+
+def copy_state(state: dict[str, np.ndarray]) -> dict[str, np.ndarray]:
+    return {k: v.copy() for k, v in state.items()}
+
+
+# -- RNG helpers -------------------------------------------------------------
+def threefry2x32(lib_or_none, key, x) -> tuple[int, int]:
+    lib = lib_or_none or _load()
+    k = (ctypes.c_uint32 * 2)(*[int(v) & 0xFFFFFFFF for v in key])
+    xs = (ctypes.c_uint32 * 2)(*[int(v) & 0xFFFFFFFF for v in x])
+    lib.nro_threefry2x32(k, xs)
+    return int(xs[0]), int(xs[1])
+
+
+def load_library() -> ctypes.CDLL:
+    return _load()
+
+
+def load_reference_draws() -> ctypes.CDLL | None:
+    """oracle/_ref: the reference's own RNG header built with hipcc, or None."""
+    if not REF_PATH.exists() and os.path.isdir("/root/reference"):
+        build()
+    return ctypes.CDLL(str(REF_PATH)) if REF_PATH.exists() else None
