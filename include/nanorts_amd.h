@@ -1,0 +1,223 @@
+/*
+ * nanorts_amd: MI355X (gfx950) kernels for the NanoRTS batched game hot path.
+ *
+ * The C ABI below is the drop-in boundary.  Every entry point takes plain
+ * device pointers and sizes, runs asynchronously on the given HIP stream
+ * (`stream` is a hipStream_t; NULL is the default stream), allocates no
+ * device memory, and returns NANORTS_OK or an error code; the message of the
+ * last failure on the calling thread is nanorts_last_error().
+ *
+ * Layouts are the reference's pytree leaves with a leading lane (env) dim L,
+ * exactly as jax.vmap hands them to its XLA FFI handlers
+ * (src/nanorts/model/state.py:33-84, src/nanorts/kernels/batching.py:41-100):
+ *   per-slot leaves [L][E], entity_at [L][H][W], scalars [L], per-player [L][2].
+ * Index leaves (cell, pending_target_cell, entity_at) are int16, which the
+ * reference selects whenever the extents fit (src/nanorts/model/leaf.py:85-98).
+ */
+#ifndef NANORTS_AMD_H
+#define NANORTS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NANORTS_OK 0
+#define NANORTS_INVALID_ARGUMENT 1
+#define NANORTS_INTERNAL 2
+
+#define NANORTS_MAX_TYPES 8
+
+#define NANORTS_CANCEL_BOTH 0
+#define NANORTS_CANCEL_RANDOM 1
+#define NANORTS_CANCEL_ALTERNATING 2
+
+/* Device pointers to the State leaves of L envs, in the reference's leaf
+ * order, plus the EnvironmentState extras (src/nanorts/adapters/lifecycle.py:24-31). */
+typedef struct nanorts_state {
+    int32_t* birth;                 /* [L][E] */
+    int8_t* unit_type;              /* [L][E] */
+    int8_t* owner;                  /* [L][E] */
+    int16_t* cell;                  /* [L][E] */
+    int16_t* hit_points;            /* [L][E] */
+    int32_t* carried_resources;     /* [L][E] */
+    int8_t* pending_kind;           /* [L][E] */
+    int8_t* pending_direction;      /* [L][E] */
+    int32_t* pending_none_duration; /* [L][E] */
+    int16_t* pending_target_cell;   /* [L][E] */
+    int8_t* pending_produced_type;  /* [L][E] */
+    int32_t* pending_issued_at;     /* [L][E] */
+    int32_t* pending_completes_at;  /* [L][E] */
+    int32_t* pending_order;         /* [L][E] */
+    int16_t* entity_at;             /* [L][H][W] */
+    int32_t* time;                  /* [L] */
+    int32_t* player_resources;      /* [L][2] */
+    int32_t* next_birth;            /* [L] */
+    int32_t* next_pending_order;    /* [L] */
+    int32_t* alternating_conflict_count; /* [L] */
+    uint8_t* game_over;             /* [L] bool */
+    int32_t* winner;                /* [L] */
+    int32_t* spawn_overflow;        /* [L][2] telemetry.spawn_overflow */
+    uint32_t* environment_root;     /* [L][2] key data; NULL where unused */
+    uint32_t* episode_index;        /* [L]; NULL where unused */
+} nanorts_state;
+
+/* The static game: BucketSpec extents, the unit type table columns
+ * (src/nanorts/model/unit_types.py:16-148; packed by the reference as the
+ * `table` and `timings` operands, src/nanorts/core/unit_tables.py:9-48), the
+ * terrain (device bool[H][W]) and the decided initial State of one env
+ * (device rows, L = 1) that an auto-reset copies in. */
+typedef struct nanorts_game {
+    int32_t height, width, cells;
+    int32_t neutral, capacity, entities; /* N, C, E = N + 2C */
+    int32_t types;                       /* T <= 8 */
+    int32_t offsets;                     /* attack window cells (2R+1)^2 <= 49 */
+    int32_t strategy;                    /* NANORTS_CANCEL_* */
+    int32_t max_cycles;
+    int32_t cost[NANORTS_MAX_TYPES];
+    int32_t hit_points[NANORTS_MAX_TYPES];
+    int32_t produce_time[NANORTS_MAX_TYPES];
+    int32_t move_time[NANORTS_MAX_TYPES];
+    int32_t attack_time[NANORTS_MAX_TYPES];
+    int32_t harvest_time[NANORTS_MAX_TYPES];
+    int32_t attack_range[NANORTS_MAX_TYPES];
+    int32_t attack_damage[NANORTS_MAX_TYPES];
+    int32_t harvest_amount[NANORTS_MAX_TYPES];
+    int32_t sight_radius[NANORTS_MAX_TYPES];
+    int32_t is_resource[NANORTS_MAX_TYPES];
+    int32_t is_stockpile[NANORTS_MAX_TYPES];
+    int32_t can_harvest[NANORTS_MAX_TYPES];
+    int32_t can_move[NANORTS_MAX_TYPES];
+    int32_t can_attack[NANORTS_MAX_TYPES];
+    int32_t produces[NANORTS_MAX_TYPES * NANORTS_MAX_TYPES]; /* [producer * 8 + produced] */
+    const uint8_t* terrain;  /* device bool[H][W] */
+    nanorts_state initial;   /* device rows of one decided initial env */
+} nanorts_game;
+
+/* Commands [L][2][C] per field (src/nanorts/model/commands.py:22-35). */
+typedef struct nanorts_commands {
+    const int32_t* kind;
+    const int32_t* direction;
+    const int32_t* none_duration;
+    const int32_t* target_cell;
+    const int32_t* produced_type;
+    const int32_t* request_order;
+} nanorts_commands;
+
+/* core.step results besides the state (StepResult minus the per-slot event
+ * records, which nothing in the reference consumes).  Any pointer may be NULL. */
+typedef struct nanorts_step_results {
+    uint8_t* terminated;        /* [L] bool */
+    uint8_t* truncated;         /* [L] bool */
+    float* reward;              /* [L][2] */
+    int32_t* admitted_harvest;  /* [L][2] */
+    int32_t* admitted_return;   /* [L][2] */
+    int32_t* admitted_produce;  /* [L][2][T] */
+    int32_t* admitted_attack;   /* [L][2][3] by target owner + 1 */
+} nanorts_step_results;
+
+/* env.step outputs through the JaxMARL surface.  Any pointer may be NULL. */
+typedef struct nanorts_env_results {
+    float* reward;            /* [L][2] */
+    uint8_t* done;            /* [L] bool */
+    uint8_t* terminated;      /* [L] bool */
+    uint8_t* truncated;       /* [L] bool */
+    int32_t* winner;          /* [L] winner of the ending state */
+    uint8_t* spawn_overflowed;/* [L] bool */
+    uint8_t* feature_maps;    /* [L][2][H][W][6] of the post-reset state */
+    int32_t* scalars;         /* [L][2][4] */
+    uint8_t* final_feature_maps; /* [L][2][H][W][6] of the ending state */
+    int32_t* final_scalars;      /* [L][2][4] */
+    float* reward_components;    /* [L][2][6] MicroRTS-Py shaped components */
+} nanorts_env_results;
+
+/* Outputs of a fused rollout.  Any pointer may be NULL. */
+typedef struct nanorts_rollout_results {
+    float* rewards;         /* [steps][L][2] */
+    uint8_t* dones;         /* [steps][L] bool */
+    int32_t* actions;       /* [steps][L][2][C][7] sampled actions */
+    uint8_t* feature_maps;  /* [depth][L][2][H][W][6]; step t writes slot t % depth */
+    int32_t* scalars;       /* [depth][L][2][4] */
+    int32_t depth;          /* ring depth of feature_maps / scalars, >= 1 */
+} nanorts_rollout_results;
+
+const char* nanorts_build_id(void);
+const char* nanorts_targets(void);
+const char* nanorts_last_error(void);
+
+/* Runs a wave64 ballot / prefix-count / shuffle probe on each listed device;
+ * returns "" when every device passes, else a static description.
+ * Replaces src/nanorts/kernels/cuda/registry.cu:174-183 (nanorts_self_check). */
+const char* nanorts_self_check(const int32_t* devices, int64_t n);
+
+/* core.step: Java admission order, durative timers, conflict resolution,
+ * completion in pending order, outcome.  State leaves are updated in place.
+ * `key` is [key_lanes][2] episode-root key data (key_lanes 1 broadcasts).
+ * Replaces the FFI target nanorts_step (src/nanorts/core/cuda/step.cu:653-698,
+ * called from src/nanorts/core/cycle.py:123-134). */
+int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
+                 int64_t key_lanes, nanorts_commands commands, nanorts_step_results results);
+
+/* Factored legality rows bool[L][2][C][22+T+O] (active units, availability not
+ * applied).  Replaces nanorts_legality (src/nanorts/core/cuda/legality.cu:535-545). */
+int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows);
+
+/* The same rows as contiguous 96-bit words uint32[L][2][C][3].  Replaces
+ * nanorts_legality_words (src/nanorts/core/cuda/legality.cu:547-561). */
+int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           uint32_t* words);
+
+/* get_avail_actions masks: rows & available, only NONE on unavailable rows
+ * (src/nanorts/adapters/jaxmarl/actions.py:28-41), as bool rows and/or words. */
+int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                          uint8_t* rows, uint32_t* words);
+
+/* Sight-radius visibility bool[L][H][W] of `observer`'s block.  Replaces
+ * nanorts_visible_cells (src/nanorts/observations/cuda/visibility.cu:86-138). */
+int nanorts_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                          int32_t observer, uint8_t* cells);
+
+/* Symbolic uint8 observations of both agents
+ * (src/nanorts/observations/symbolic.py:130-180). */
+int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+                    uint8_t* feature_maps, int32_t* scalars);
+
+/* Pixel observations uint8[L][2][16H][16W][3] from a tile table
+ * uint8[2(1+3T)][16][16][3] (src/nanorts/observations/pixels.py:71-88,
+ * src/nanorts/rendering/raster.py:53-127). */
+int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+                   const uint8_t* tiles, uint8_t* image, int32_t* scalars);
+
+/* Auto-reset: envs whose done flag is set get the initial State and
+ * episode_index + 1.  Replaces nanorts_reset_where_done
+ * (src/nanorts/adapters/cuda/reset.cu:160-222). */
+int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                             const uint8_t* done);
+
+/* env.step of the JaxMARL facade in one launch: decode int32[L][2][C][7]
+ * actions, core.step keyed by the episode root, advance (auto-reset) and
+ * observe (src/nanorts/adapters/jaxmarl/env.py:72-184). */
+int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                     const int32_t* actions, int32_t partial, nanorts_env_results results);
+
+/* The synthetic harness's integer uniform-over-legal sampler: actions
+ * int32[L][2][C][7] from avail words uint32[L][2][C][3] for rollout step
+ * `step`, envs numbered from env0. */
+int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
+                           const uint32_t* sample_key /* host [2] */, int32_t step, int64_t env0,
+                           int32_t* actions);
+
+/* Fused rollout of `steps` cycles with the state resident in LDS: per step
+ * masks -> sample -> decode -> core.step -> auto-reset -> observe.  Bit-equal
+ * to calling avail_actions, sample_actions and env_step once per step. */
+int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                    const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
+                    int64_t env0,
+                    nanorts_rollout_results results);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,1287 @@
+// Device engine of the NanoRTS hot path for gfx950 (CDNA4, wave64).
+//
+// One wavefront owns one game.  The game's state rows are staged in LDS (the
+// per-wave "env block"); the unit type table and the terrain are staged once
+// per workgroup.  Wave-parallel phases use 64-bit ballots, mbcnt prefix counts
+// and a shuffle prefix-min; the inherently sequential parts of the reference's
+// semantics (requests admitted one at a time, completions applied one at a
+// time) run as wave-uniform code with lane 0 writing.
+//
+// Semantics follow the reference JAX program (citations relative to the
+// reference root, N/ = src/nanorts/); integer behaviour follows XLA: wrapping
+// int32 arithmetic, floor division/modulo, gathers that wrap a negative index
+// once then clamp, masked scatters that drop out-of-range indices.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nanorts_amd.h"
+
+#define AS3 __attribute__((address_space(3)))
+#define NR_DEV __device__ __forceinline__
+
+namespace nr {
+
+constexpr int kWave = 64;
+constexpr int32_t kAbsent = -1;
+constexpr int32_t kKindNone = 0;
+constexpr int32_t kKindMove = 1;
+constexpr int32_t kKindHarvest = 2;
+constexpr int32_t kKindReturn = 3;
+constexpr int32_t kKindProduce = 4;
+constexpr int32_t kKindAttack = 5;
+constexpr int32_t kKindUnknown = 6;  // any issued kind outside 0..5
+constexpr int32_t kNoCap = 0x7fffffff;
+constexpr int32_t kCrossStride = 1 << 15;
+
+// Unit table fields, tab[field * 8 + type] in LDS.
+enum : int {
+    F_COST = 0,
+    F_HP,
+    F_PRODUCE_TIME,
+    F_MOVE_TIME,
+    F_ATTACK_TIME,
+    F_HARVEST_TIME,
+    F_RANGE,
+    F_DAMAGE,
+    F_AMOUNT,
+    F_SIGHT,
+    F_FLAGS,
+    F_PRODUCES,
+    F_COUNT
+};
+enum : int { FL_RESOURCE = 1, FL_STOCKPILE = 2, FL_HARVEST = 4, FL_MOVE = 8, FL_ATTACK = 16 };
+
+// Per-env scalar leaves in LDS.
+enum : int {
+    S_TIME = 0,
+    S_RES0,
+    S_RES1,
+    S_NEXT_BIRTH,
+    S_NEXT_ORDER,
+    S_ALT,
+    S_GAME_OVER,
+    S_WINNER,
+    S_SO0,
+    S_SO1,
+    S_ROOT0,
+    S_ROOT1,
+    S_EPISODE,
+    S_COUNT = 16
+};
+
+// Byte offsets of one env block (relative to the block) and of the
+// workgroup header.  Computed on the host (see layout_for in nanorts_amd.hip).
+struct Layout {
+    int32_t hdr_bytes;  // tab + terrain
+    int32_t env_bytes;  // one wave's block, 16-byte multiple
+    int32_t o_terrain;  // in the header
+    int32_t o_birth, o_carried, o_pnone, o_pissued, o_pcompl, o_porder;
+    int32_t o_cell, o_hp, o_ptarget, o_entity;
+    int32_t o_utype, o_owner, o_pkind, o_pdir, o_pptype;
+    int32_t o_scal;
+    int32_t b_events;  // admitted counts, outside the phase union
+    // Phase union.  Admission: commands, keys, lists.  Completion: member
+    // records, keys.  Observation: seen bitmap, staging, unit list.  Masks:
+    // staged words.
+    int32_t c_kind, c_dir, c_ptype, c_target, c_none, c_rank;
+    int32_t b_pkey, b_keys, b_tmp, b_order, b_rank;
+    int32_t m_rec, m_keys, m_tmp;
+    int32_t v_seen, v_stage, b_units;
+    int32_t v_words;
+};
+
+// Kernel-side copy of the game (passed by value as a kernel argument).
+struct KGame {
+    int32_t H, W, cells, N, C, E, T, O, strategy, max_cycles;
+    int32_t side, radius, rank_bits, seen_words, stage_cells, sight_max;
+    int32_t tab[F_COUNT * 8];
+    const uint8_t* terrain;
+    nanorts_state initial;
+    Layout lay;
+};
+
+// ---------------------------------------------------------------------------
+// integer helpers
+// ---------------------------------------------------------------------------
+NR_DEV int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+NR_DEV int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+NR_DEV int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+NR_DEV int32_t clampi(int32_t v, int32_t lo, int32_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+NR_DEV int32_t imin(int32_t a, int32_t b) { return a < b ? a : b; }
+NR_DEV int32_t floor_div(int32_t a, int32_t b) {
+    const int32_t q = a / b, r = a % b;
+    return (r != 0 && ((r < 0) != (b < 0))) ? q - 1 : q;
+}
+NR_DEV int32_t floor_mod(int32_t a, int32_t b) {
+    const int32_t r = a % b;
+    return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
+}
+NR_DEV int32_t gidx(int32_t i, int32_t n) { return clampi(i < 0 ? i + n : i, 0, n - 1); }
+NR_DEV int32_t dir_dx(int32_t d) { return d == 1 ? 1 : (d == 3 ? -1 : 0); }
+NR_DEV int32_t dir_dy(int32_t d) { return d == 0 ? -1 : (d == 2 ? 1 : 0); }
+
+// ---------------------------------------------------------------------------
+// wave primitives
+// ---------------------------------------------------------------------------
+NR_DEV int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+NR_DEV uint64_t ballot(bool p) { return (uint64_t)__ballot(p); }
+NR_DEV int32_t count_below(uint64_t mask) {
+    return (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+NR_DEV int32_t popc(uint64_t m) { return __popcll(m); }
+NR_DEV int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+// LDS writes of one lane made visible to the other lanes of the wave.
+NR_DEV void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+NR_DEV int32_t wave_inclusive_min(int32_t v, int lane) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int32_t o = __shfl_up(v, (unsigned)d, kWave);
+        if (lane >= d) v = v < o ? v : o;
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// threefry2x32 (Random123 Threefry-2x32-20) and JAX's key plumbing in
+// partitionable mode: fold_in(k, d) = split(k)[d] = threefry(k, (0, d)).
+// ---------------------------------------------------------------------------
+NR_DEV uint32_t rotl(uint32_t x, uint32_t d) { return (x << d) | (x >> (32u - d)); }
+NR_DEV void threefry(uint32_t k0, uint32_t k1, uint32_t& x0, uint32_t& x1) {
+    const uint32_t k2 = k0 ^ k1 ^ 0x1BD11BDAu;
+    x0 += k0;
+    x1 += k1;
+#define NR_R(r)          \
+    x0 += x1;            \
+    x1 = rotl(x1, r);    \
+    x1 ^= x0;
+    NR_R(13) NR_R(15) NR_R(26) NR_R(6) x0 += k1; x1 += k2 + 1u;
+    NR_R(17) NR_R(29) NR_R(16) NR_R(24) x0 += k2; x1 += k0 + 2u;
+    NR_R(13) NR_R(15) NR_R(26) NR_R(6) x0 += k0; x1 += k1 + 3u;
+    NR_R(17) NR_R(29) NR_R(16) NR_R(24) x0 += k1; x1 += k2 + 4u;
+    NR_R(13) NR_R(15) NR_R(26) NR_R(6) x0 += k2; x1 += k0 + 5u;
+#undef NR_R
+}
+NR_DEV void fold_in(uint32_t& k0, uint32_t& k1, uint32_t data) {
+    uint32_t x0 = 0u, x1 = data;
+    threefry(k0, k1, x0, x1);
+    k0 = x0;
+    k1 = x1;
+}
+// jax.random.randint(k, (), 0, 2) = (b0 ^ b1) % 2 with (b0, b1) =
+// threefry(split(k)[1], (0, 0)) (N/core/cuda/conflict_draw.cuh:47-55 restates it).
+NR_DEV int32_t randint01(uint32_t k0, uint32_t k1) {
+    uint32_t s0 = 0u, s1 = 1u;
+    threefry(k0, k1, s0, s1);
+    uint32_t b0 = 0u, b1 = 0u;
+    threefry(s0, s1, b0, b1);
+    return (int32_t)((b0 ^ b1) & 1u);
+}
+
+// ---------------------------------------------------------------------------
+// LDS views
+// ---------------------------------------------------------------------------
+struct Hdr {
+    AS3 int32_t* tab;
+    AS3 uint8_t* terrain;
+};
+
+struct Env {
+    AS3 uint8_t* base;
+    AS3 int32_t* birth;
+    AS3 int32_t* carried;
+    AS3 int32_t* pnone;
+    AS3 int32_t* pissued;
+    AS3 int32_t* pcompl;
+    AS3 int32_t* porder;
+    AS3 int16_t* cell;
+    AS3 int16_t* hp;
+    AS3 int16_t* ptarget;
+    AS3 int16_t* entity;
+    AS3 int8_t* utype;
+    AS3 int8_t* owner;
+    AS3 int8_t* pkind;
+    AS3 int8_t* pdir;
+    AS3 int8_t* pptype;
+    AS3 int32_t* sc;
+};
+
+NR_DEV Env env_view(const KGame& g, AS3 uint8_t* base) {
+    const Layout& y = g.lay;
+    Env e;
+    e.base = base;
+    e.birth = (AS3 int32_t*)(base + y.o_birth);
+    e.carried = (AS3 int32_t*)(base + y.o_carried);
+    e.pnone = (AS3 int32_t*)(base + y.o_pnone);
+    e.pissued = (AS3 int32_t*)(base + y.o_pissued);
+    e.pcompl = (AS3 int32_t*)(base + y.o_pcompl);
+    e.porder = (AS3 int32_t*)(base + y.o_porder);
+    e.cell = (AS3 int16_t*)(base + y.o_cell);
+    e.hp = (AS3 int16_t*)(base + y.o_hp);
+    e.ptarget = (AS3 int16_t*)(base + y.o_ptarget);
+    e.entity = (AS3 int16_t*)(base + y.o_entity);
+    e.utype = (AS3 int8_t*)(base + y.o_utype);
+    e.owner = (AS3 int8_t*)(base + y.o_owner);
+    e.pkind = (AS3 int8_t*)(base + y.o_pkind);
+    e.pdir = (AS3 int8_t*)(base + y.o_pdir);
+    e.pptype = (AS3 int8_t*)(base + y.o_pptype);
+    e.sc = (AS3 int32_t*)(base + y.o_scal);
+    return e;
+}
+
+template <typename T>
+NR_DEV AS3 T* at(const Env& e, int32_t offset) {
+    return (AS3 T*)(e.base + offset);
+}
+
+NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field * 8 + type]; }
+
+// Stage the unit table and terrain for the workgroup (all threads call; a
+// __syncthreads follows in the kernel).
+NR_DEV void load_header(const KGame& g, const Hdr& h) {
+    for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
+    for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = g.terrain[i] ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// HBM <-> LDS row copies (16-byte, 4-byte or 1-byte granules by alignment)
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+NR_DEV void copy_in(AS3 uint8_t* dst, const uint8_t* src, int32_t nbytes, int lane) {
+    const uintptr_t a = (uintptr_t)src;
+    if (((a | (uintptr_t)nbytes) & 15u) == 0) {
+        const int32_t n = nbytes >> 4;
+        for (int32_t i = lane; i < n; i += kWave) ((AS3 u32x4*)dst)[i] = ((const u32x4*)src)[i];
+    } else if (((a | (uintptr_t)nbytes) & 3u) == 0) {
+        const int32_t n = nbytes >> 2;
+        for (int32_t i = lane; i < n; i += kWave) ((AS3 uint32_t*)dst)[i] = ((const uint32_t*)src)[i];
+    } else {
+        for (int32_t i = lane; i < nbytes; i += kWave) dst[i] = src[i];
+    }
+}
+
+NR_DEV void copy_out(uint8_t* dst, const AS3 uint8_t* src, int32_t nbytes, int lane) {
+    const uintptr_t a = (uintptr_t)dst;
+    if (((a | (uintptr_t)nbytes) & 15u) == 0) {
+        const int32_t n = nbytes >> 4;
+        for (int32_t i = lane; i < n; i += kWave) ((u32x4*)dst)[i] = ((const AS3 u32x4*)src)[i];
+    } else if (((a | (uintptr_t)nbytes) & 3u) == 0) {
+        const int32_t n = nbytes >> 2;
+        for (int32_t i = lane; i < n; i += kWave) ((uint32_t*)dst)[i] = ((const AS3 uint32_t*)src)[i];
+    } else {
+        for (int32_t i = lane; i < nbytes; i += kWave) dst[i] = src[i];
+    }
+}
+
+// Which leaves a kernel needs staged.
+enum : uint32_t {
+    LD_BIRTH = 1u << 0,
+    LD_UTYPE = 1u << 1,
+    LD_OWNER = 1u << 2,
+    LD_CELL = 1u << 3,
+    LD_HP = 1u << 4,
+    LD_CARRIED = 1u << 5,
+    LD_PKIND = 1u << 6,
+    LD_PDIR = 1u << 7,
+    LD_PNONE = 1u << 8,
+    LD_PTARGET = 1u << 9,
+    LD_PPTYPE = 1u << 10,
+    LD_PISSUED = 1u << 11,
+    LD_PCOMPL = 1u << 12,
+    LD_PORDER = 1u << 13,
+    LD_ENTITY = 1u << 14,
+    LD_SCALARS = 1u << 15,
+    LD_ALL = 0xFFFFu,
+};
+
+NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, uint32_t which, int lane) {
+    const int64_t E = g.E, cells = g.cells;
+#define NR_IN(flag, field, member, type) \
+    if (which & flag) copy_in((AS3 uint8_t*)e.member, (const uint8_t*)(s.field + l * E), (int32_t)(E * sizeof(type)), lane);
+    NR_IN(LD_BIRTH, birth, birth, int32_t)
+    NR_IN(LD_UTYPE, unit_type, utype, int8_t)
+    NR_IN(LD_OWNER, owner, owner, int8_t)
+    NR_IN(LD_CELL, cell, cell, int16_t)
+    NR_IN(LD_HP, hit_points, hp, int16_t)
+    NR_IN(LD_CARRIED, carried_resources, carried, int32_t)
+    NR_IN(LD_PKIND, pending_kind, pkind, int8_t)
+    NR_IN(LD_PDIR, pending_direction, pdir, int8_t)
+    NR_IN(LD_PNONE, pending_none_duration, pnone, int32_t)
+    NR_IN(LD_PTARGET, pending_target_cell, ptarget, int16_t)
+    NR_IN(LD_PPTYPE, pending_produced_type, pptype, int8_t)
+    NR_IN(LD_PISSUED, pending_issued_at, pissued, int32_t)
+    NR_IN(LD_PCOMPL, pending_completes_at, pcompl, int32_t)
+    NR_IN(LD_PORDER, pending_order, porder, int32_t)
+#undef NR_IN
+    if (which & LD_ENTITY)
+        copy_in((AS3 uint8_t*)e.entity, (const uint8_t*)(s.entity_at + l * cells), (int32_t)(cells * 2), lane);
+    if ((which & LD_SCALARS) && lane < S_COUNT) {
+        int32_t v = 0;
+        switch (lane) {
+            case S_TIME: v = s.time[l]; break;
+            case S_RES0: v = s.player_resources[2 * l]; break;
+            case S_RES1: v = s.player_resources[2 * l + 1]; break;
+            case S_NEXT_BIRTH: v = s.next_birth[l]; break;
+            case S_NEXT_ORDER: v = s.next_pending_order[l]; break;
+            case S_ALT: v = s.alternating_conflict_count[l]; break;
+            case S_GAME_OVER: v = s.game_over[l] ? 1 : 0; break;
+            case S_WINNER: v = s.winner[l]; break;
+            case S_SO0: v = s.spawn_overflow[2 * l]; break;
+            case S_SO1: v = s.spawn_overflow[2 * l + 1]; break;
+            case S_ROOT0: v = s.environment_root ? (int32_t)s.environment_root[2 * l] : 0; break;
+            case S_ROOT1: v = s.environment_root ? (int32_t)s.environment_root[2 * l + 1] : 0; break;
+            case S_EPISODE: v = s.episode_index ? (int32_t)s.episode_index[l] : 0; break;
+            default: break;
+        }
+        e.sc[lane] = v;
+    }
+    wave_sync();
+}
+
+NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    const int64_t E = g.E, cells = g.cells;
+#define NR_OUT(field, member, type) \
+    copy_out((uint8_t*)(s.field + l * E), (const AS3 uint8_t*)e.member, (int32_t)(E * sizeof(type)), lane);
+    NR_OUT(birth, birth, int32_t)
+    NR_OUT(unit_type, utype, int8_t)
+    NR_OUT(owner, owner, int8_t)
+    NR_OUT(cell, cell, int16_t)
+    NR_OUT(hit_points, hp, int16_t)
+    NR_OUT(carried_resources, carried, int32_t)
+    NR_OUT(pending_kind, pkind, int8_t)
+    NR_OUT(pending_direction, pdir, int8_t)
+    NR_OUT(pending_none_duration, pnone, int32_t)
+    NR_OUT(pending_target_cell, ptarget, int16_t)
+    NR_OUT(pending_produced_type, pptype, int8_t)
+    NR_OUT(pending_issued_at, pissued, int32_t)
+    NR_OUT(pending_completes_at, pcompl, int32_t)
+    NR_OUT(pending_order, porder, int32_t)
+#undef NR_OUT
+    copy_out((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
+    if (lane < S_COUNT) {
+        const int32_t v = e.sc[lane];
+        switch (lane) {
+            case S_TIME: s.time[l] = v; break;
+            case S_RES0: s.player_resources[2 * l] = v; break;
+            case S_RES1: s.player_resources[2 * l + 1] = v; break;
+            case S_NEXT_BIRTH: s.next_birth[l] = v; break;
+            case S_NEXT_ORDER: s.next_pending_order[l] = v; break;
+            case S_ALT: s.alternating_conflict_count[l] = v; break;
+            case S_GAME_OVER: s.game_over[l] = v ? 1 : 0; break;
+            case S_WINNER: s.winner[l] = v; break;
+            case S_SO0: s.spawn_overflow[2 * l] = v; break;
+            case S_SO1: s.spawn_overflow[2 * l + 1] = v; break;
+            case S_EPISODE:
+                if (s.episode_index) s.episode_index[l] = (uint32_t)v;
+                break;
+            default: break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// board helpers (N/core/board.py)
+// ---------------------------------------------------------------------------
+struct Nb {
+    bool free, occupied;
+    int32_t slot, unit_type, owner;
+};
+
+// N/core/board.py:23-56
+NR_DEV Nb neighbour(const KGame& g, const Hdr& h, const Env& e, int32_t cell, int32_t direction) {
+    const int32_t x = floor_mod(cell, g.W), y = floor_div(cell, g.W);
+    const int32_t known = clampi(direction, 0, 3);
+    const int32_t nx = x + dir_dx(known), ny = y + dir_dy(known);
+    const bool on = direction >= 0 && direction < 4 && nx >= 0 && nx < g.W && ny >= 0 && ny < g.H;
+    Nb n;
+    n.free = false;
+    n.occupied = false;
+    n.slot = 0;
+    n.unit_type = 0;
+    n.owner = kAbsent;
+    if (on) {
+        const int32_t nc = ny * g.W + nx;
+        const int32_t occ = e.entity[nc];
+        n.occupied = occ != kAbsent;
+        n.free = !n.occupied && h.terrain[nc] == 0;
+        if (n.occupied) {
+            n.slot = occ;
+            const int32_t s = gidx(occ, g.E);
+            n.unit_type = clampi(e.utype[s], 0, g.T - 1);
+            n.owner = e.owner[s];
+        }
+    }
+    return n;
+}
+
+// N/core/board.py:59-64 (no bounds check; may wrap rows)
+NR_DEV int32_t reserved_position(const KGame& g, int32_t cell, int32_t direction) {
+    const int32_t known = clampi(direction, 0, 3);
+    return wadd(cell, dir_dx(known) + dir_dy(known) * g.W);
+}
+
+// N/core/admission.py:310-319 with each kind's duration.
+NR_DEV int32_t action_duration(const KGame& g, const Hdr& h, int32_t actor_type, int32_t kind, int32_t none_duration,
+                               int32_t produced_type) {
+    const int32_t actor = clampi(actor_type, 0, g.T - 1);
+    switch (kind) {
+        case kKindNone: return none_duration;
+        case kKindMove: return tabv(h, F_MOVE_TIME, actor);
+        case kKindHarvest: return tabv(h, F_HARVEST_TIME, actor);
+        case kKindReturn: return tabv(h, F_MOVE_TIME, actor);
+        case kKindProduce: return tabv(h, F_PRODUCE_TIME, clampi(produced_type, 0, g.T - 1));
+        case kKindAttack: return tabv(h, F_ATTACK_TIME, actor);
+        default: return 0;
+    }
+}
+
+NR_DEV bool claims_position(int32_t kind) { return kind == kKindMove || kind == kKindProduce; }
+
+// ---------------------------------------------------------------------------
+// Command canonical forms.  Only these properties of a command's int32
+// fields are ever observed by the reference's step, so each is stored in a
+// narrow form that preserves them:
+//   kind: -1 absent, 0..5, or 6 for any other value (no duration, never legal)
+//   direction: -1 for d < 0, 4 for d > 3 (is_direction false, clip as d)
+//   produced_type: -1 below range, T above (range check false, clip as v)
+//   target_cell: -1 off the board (never a legal target, never stored)
+// ---------------------------------------------------------------------------
+NR_DEV int32_t canon_kind(int32_t k) { return k == kAbsent ? kAbsent : ((k >= 0 && k <= 5) ? k : kKindUnknown); }
+NR_DEV int32_t canon_dir(int32_t d) { return d < 0 ? -1 : (d > 3 ? 4 : d); }
+NR_DEV int32_t canon_ptype(int32_t t, int32_t T) { return t < 0 ? -1 : (t >= T ? T : t); }
+NR_DEV int32_t canon_target(int32_t c, int32_t cells) { return (c >= 0 && c < cells) ? c : -1; }
+
+// N/core/kinds/*.py is_valid for one request (Request.of, action_kind.py:15-40).
+NR_DEV bool can_execute(const KGame& g, const Hdr& h, const Env& e, int32_t slot, int32_t kind, int32_t dir,
+                        int32_t target, int32_t ptype) {
+    const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
+    const int32_t owner = e.owner[slot];
+    const int32_t carried = e.carried[slot];
+    const int32_t cell = e.cell[slot];
+    const int32_t flags = tabv(h, F_FLAGS, actor);
+    switch (kind) {
+        case kKindNone: return true;
+        case kKindMove: {
+            const Nb n = neighbour(g, h, e, cell, dir);
+            return (flags & FL_MOVE) && n.free;
+        }
+        case kKindHarvest: {
+            const Nb n = neighbour(g, h, e, cell, dir);
+            return (flags & FL_HARVEST) && carried == 0 && n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_RESOURCE);
+        }
+        case kKindReturn: {
+            const Nb n = neighbour(g, h, e, cell, dir);
+            return (flags & FL_HARVEST) && carried > 0 && n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_STOCKPILE) &&
+                   n.owner == owner;
+        }
+        case kKindProduce: {
+            if (ptype < 0 || ptype >= g.T) return false;
+            const Nb n = neighbour(g, h, e, cell, dir);
+            const int32_t balance = e.sc[S_RES0 + clampi(owner, 0, 1)];
+            return ((tabv(h, F_PRODUCES, actor) >> ptype) & 1) && balance >= tabv(h, F_COST, ptype) && n.free;
+        }
+        case kKindAttack: {
+            if (target < 0 || target >= g.cells) return false;
+            const int32_t occ = e.entity[target];
+            if (occ == kAbsent) return false;
+            const int32_t target_owner = e.owner[gidx(occ, g.E)];
+            const int32_t range = tabv(h, F_RANGE, actor);
+            const int32_t dx = floor_mod(target, g.W) - floor_mod(cell, g.W);
+            const int32_t dy = floor_div(target, g.W) - floor_div(cell, g.W);
+            return (flags & FL_ATTACK) && target_owner >= 0 && target_owner != owner &&
+                   wadd(wmul(dx, dx), wmul(dy, dy)) <= wmul(range, range);
+        }
+        default: return false;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Admission (N/core/admission.py, N/core/pending.py:28-44,
+// N/core/reservations.py)
+// ---------------------------------------------------------------------------
+struct Events {
+    bool enabled;
+};
+
+// Request order and pending ranking for this cycle.  Returns the number of
+// issued requests; region B holds `order` (owned positions in admission
+// order) and `rank` (pending entries in ranking order, count in *n_rank).
+NR_DEV int32_t order_requests(const KGame& g, const Env& e, int lane, int32_t* n_rank_out) {
+    const Layout& y = g.lay;
+    const int32_t N = g.N, C = g.C, owned = 2 * C;
+    AS3 int8_t* ckind = at<int8_t>(e, y.c_kind);
+    AS3 int16_t* crank = at<int16_t>(e, y.c_rank);
+    AS3 uint64_t* keys = at<uint64_t>(e, y.b_keys);
+    AS3 int16_t* tmp = at<int16_t>(e, y.b_tmp);
+    AS3 int16_t* order = at<int16_t>(e, y.b_order);
+    AS3 int16_t* rank = at<int16_t>(e, y.b_rank);
+    AS3 int32_t* pkey = at<int32_t>(e, y.b_pkey);
+
+    // issued = active & kind != ABSENT, compacted in owned-position order,
+    // keyed (player, rank, birth) as in _issued_player_rank_key (:224-234).
+    int32_t n = 0;
+    for (int32_t base = 0; base < owned; base += kWave) {
+        const int32_t p = base + lane;
+        bool issued = false;
+        int32_t birth = 0;
+        if (p < owned) {
+            birth = e.birth[N + p];
+            issued = birth != kAbsent && ckind[p] != kAbsent;
+        }
+        const uint64_t m = ballot(issued);
+        if (issued) {
+            const int32_t at_ = n + count_below(m);
+            const uint32_t hi = ((uint32_t)(p / C) << g.rank_bits) | (uint32_t)crank[p];
+            keys[at_] = ((uint64_t)hi << 32) | (uint64_t)((uint32_t)birth ^ 0x80000000u);
+            tmp[at_] = (int16_t)p;
+        }
+        n += popc(m);
+    }
+    wave_sync();
+    // rank by count; ties (impossible for distinct births) by owned position
+    for (int32_t i = lane; i < n; i += kWave) {
+        const uint64_t ki = keys[i];
+        int32_t pos = 0;
+        for (int32_t j = 0; j < n; ++j) {
+            const uint64_t kj = keys[j];
+            pos += (kj < ki) || (kj == ki && j < i);
+        }
+        order[pos] = tmp[i];
+    }
+    wave_sync();
+    // pending keys after this cycle's appends (pending.py:37-44)
+    for (int32_t p = lane; p < owned; p += kWave) {
+        const int32_t held = e.porder[N + p];
+        pkey[p] = held == kAbsent ? kNoCap : held;
+    }
+    wave_sync();
+    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    int32_t appended = 0;
+    for (int32_t base = 0; base < n; base += kWave) {
+        const int32_t i = base + lane;
+        bool appends = false;
+        int32_t p = 0;
+        if (i < n) {
+            p = order[i];
+            appends = e.porder[N + p] == kAbsent;
+        }
+        const uint64_t m = ballot(appends);
+        if (appends) pkey[p] = wadd(next_order, appended + count_below(m));
+        appended += popc(m);
+    }
+    wave_sync();
+    // ranking: neutral pending entries first in slot order, then owned
+    // entries by (key, position); entries that cannot be pending this cycle
+    // (key INT_MAX and no pending action) are left out, which does not change
+    // the relative order of the others.
+    int32_t nr = 0;
+    for (int32_t base = 0; base < N; base += kWave) {
+        const int32_t s = base + lane;
+        const bool pend = s < N && e.pkind[s] != kAbsent;
+        const uint64_t m = ballot(pend);
+        if (pend) rank[nr + count_below(m)] = (int16_t)s;
+        nr += popc(m);
+    }
+    int32_t no = 0;
+    for (int32_t base = 0; base < owned; base += kWave) {
+        const int32_t p = base + lane;
+        bool inc = false;
+        int32_t k = 0;
+        if (p < owned) {
+            k = pkey[p];
+            inc = k != kNoCap || e.pkind[N + p] != kAbsent;
+        }
+        const uint64_t m = ballot(inc);
+        if (inc) {
+            const int32_t at_ = no + count_below(m);
+            keys[at_] = ((uint64_t)((uint32_t)k ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)p;
+            tmp[at_] = (int16_t)p;
+        }
+        no += popc(m);
+    }
+    wave_sync();
+    for (int32_t i = lane; i < no; i += kWave) {
+        const uint64_t ki = keys[i];
+        int32_t pos = 0;
+        for (int32_t j = 0; j < no; ++j) pos += keys[j] < ki;
+        rank[nr + pos] = (int16_t)(N + tmp[i]);
+    }
+    wave_sync();
+    *n_rank_out = nr + no;
+    return n;
+}
+
+// One request: N/core/admission.py:242-289 (_admit_one) with
+// reservations.resolve (N/core/reservations.py:69-111).
+NR_DEV void admit_one(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t p, int32_t n_rank, uint32_t key0,
+                      uint32_t key1, bool count_events) {
+    const Layout& y = g.lay;
+    const int32_t slot = g.N + p;
+    const int32_t player = p / g.C;
+    const int32_t kind0 = uni(at<int8_t>(e, y.c_kind)[p]);
+    const int32_t dir = uni(at<int8_t>(e, y.c_dir)[p]);
+    const int32_t ptype = uni(at<int8_t>(e, y.c_ptype)[p]);
+    const int32_t target = uni(at<int16_t>(e, y.c_target)[p]);
+    const int32_t none0 = uni(at<int32_t>(e, y.c_none)[p]);
+    const int32_t time = uni(e.sc[S_TIME]);
+    const int32_t cell = uni(e.cell[slot]);
+    const int32_t unit_type = uni(e.utype[slot]);
+    const int32_t owner = uni(e.owner[slot]);
+
+    const int32_t requested = action_duration(g, h, unit_type, kind0, none0, ptype);
+    // _none_if_illegal
+    const bool legal = uni(can_execute(g, h, e, slot, kind0, dir, target, ptype) ? 1 : 0) != 0;
+    int32_t kind = legal ? kind0 : kKindNone;
+    int32_t none = legal ? none0 : requested;
+    // _none_if_blocked
+    if (claims_position(kind)) {
+        const int32_t pos = gidx(reserved_position(g, cell, dir), g.cells);
+        if (h.terrain[pos] != 0 || e.entity[pos] != kAbsent) {
+            kind = kKindNone;
+            none = requested;
+        }
+    }
+    // _count_admitted (:406-429)
+    if (count_events && lane == 0) {
+        AS3 int32_t* ev = at<int32_t>(e, y.b_events);
+        if (kind == kKindHarvest) ev[player] += 1;
+        if (kind == kKindReturn) ev[2 + player] += 1;
+        if (kind == kKindProduce) ev[4 + player * 8 + clampi(ptype, 0, g.T - 1)] += 1;
+        if (kind == kKindAttack) {
+            const int32_t occ = e.entity[clampi(target, 0, g.cells - 1)];
+            const int32_t towner = occ == kAbsent ? kAbsent : e.owner[clampi(occ, 0, g.E - 1)];
+            if (towner + 1 >= 0 && towner + 1 < 3) ev[20 + player * 3 + towner + 1] += 1;
+        }
+    }
+    // _requested_reservation (:340-349) and resolve
+    const bool req_claims = claims_position(kind);
+    const int32_t req_cost = kind == kKindProduce ? tabv(h, F_COST, clampi(ptype, 0, g.T - 1)) : 0;
+    if (req_claims || req_cost != 0) {
+        const int32_t req_pos = reserved_position(g, cell, dir);
+        const int32_t req_player = clampi(owner, 0, 1);
+        const int32_t balance = uni(e.sc[S_RES0 + req_player]);
+        const int32_t alt = uni(e.sc[S_ALT]);
+        AS3 int16_t* rank = at<int16_t>(e, y.b_rank);
+        int32_t same_total = 0;
+        bool any_cross = false;
+        int32_t cap = kNoCap;
+        uint32_t ek0 = key0, ek1 = key1;
+        bool have_event_key = false;
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        for (int32_t base = 0; base < n_rank; base += kWave) {
+            const int32_t j = base + lane;
+            bool same = false, cross = false;
+            int32_t dur = 0, entry = 0;
+            if (j < n_rank) {
+                entry = rank[j];
+                const int32_t k = e.pkind[entry];
+                if (k != kAbsent) {
+                    const int32_t epl = clampi(e.owner[entry], 0, 1);
+                    const int32_t ept = e.pptype[entry];
+                    const int32_t ecost = k == kKindProduce ? tabv(h, F_COST, clampi(ept, 0, g.T - 1)) : 0;
+                    const bool eclaims = claims_position(k);
+                    const int32_t epos = reserved_position(g, e.cell[entry], e.pdir[entry]);
+                    const bool shared = eclaims && req_claims && epos == req_pos;
+                    const int32_t claimed = wadd(epl == req_player ? ecost : 0, req_cost);
+                    const bool over = req_cost != 0 && claimed > 0 && claimed > balance;
+                    const bool conflict = shared || over;
+                    const bool crossc = e.pissued[entry] != time;
+                    const int32_t d = action_duration(g, h, e.utype[entry], k, e.pnone[entry], ept);
+                    const int32_t packed = wadd(wmul(d, 4), (conflict && !crossc ? 2 : 0) + (conflict && crossc ? 1 : 0));
+                    dur = packed >> 2;
+                    same = ((packed >> 1) & 1) != 0;
+                    cross = (packed & 1) != 0;
+                }
+            }
+            const uint64_t sm = ballot(same), cm = ballot(cross);
+            if ((sm | cm) == 0ull) continue;
+            const int32_t same_before = same_total + popc(sm & below);
+            const bool cross_before = any_cross || (cm & below) != 0ull;
+            bool cancels_req = true, cancels_pend = true;
+            if (g.strategy == NANORTS_CANCEL_ALTERNATING) {
+                cancels_req = floor_mod(wadd(alt, same_before), 2) == 0;
+                cancels_pend = !cancels_req;
+            } else if (g.strategy == NANORTS_CANCEL_RANDOM) {
+                if (!have_event_key && sm != 0ull) {
+                    // _event_key (N/core/reservations.py:297-300)
+                    fold_in(ek0, ek1, (uint32_t)time);
+                    fold_in(ek0, ek1, (uint32_t)uni(e.birth[slot]));
+                    fold_in(ek0, ek1, 0u);
+                    have_event_key = true;
+                }
+                int32_t draw = 0;
+                if (same) {
+                    uint32_t d0 = ek0, d1 = ek1;
+                    fold_in(d0, d1, (uint32_t)same_before);
+                    draw = randint01(d0, d1);
+                }
+                cancels_req = draw == 0;
+                cancels_pend = !cancels_req;
+            }
+            // _settle_durations (:169-192) for this chunk
+            int32_t incl = wave_inclusive_min((same && cancels_req) ? dur : kNoCap, lane);
+            incl = imin(incl, cap);
+            int32_t excl = __shfl_up(incl, 1u, kWave);
+            if (lane == 0) excl = cap;
+            const int32_t before = cross_before ? -1 : imin(requested, excl);
+            if (same && cancels_pend) {
+                // _cancel_pending (:207-228)
+                const int32_t settled = imin(dur, before);
+                const int32_t d2 = wadd(wmul(settled, 2), 1) >> 1;
+                e.pkind[entry] = (int8_t)kKindNone;
+                e.pdir[entry] = (int8_t)kAbsent;
+                e.pnone[entry] = d2;
+                e.ptarget[entry] = (int16_t)kAbsent;
+                e.pptype[entry] = (int8_t)kAbsent;
+                e.pcompl[entry] = wadd(e.pissued[entry], d2);
+            }
+            same_total += popc(sm);
+            any_cross = any_cross || cm != 0ull;
+            cap = __shfl(incl, kWave - 1, kWave);
+        }
+        if (g.strategy == NANORTS_CANCEL_ALTERNATING && lane == 0) e.sc[S_ALT] = wadd(alt, same_total);
+        if (any_cross || cap != kNoCap) {
+            kind = kKindNone;
+            none = any_cross ? -1 : imin(requested, cap);
+        }
+        wave_sync();
+    }
+    // _assign_pending_action (:374-403)
+    const int32_t duration = kind == kKindNone ? none : requested;
+    if (lane == 0) {
+        const int32_t held = e.porder[slot];
+        const int32_t next_order = e.sc[S_NEXT_ORDER];
+        e.pkind[slot] = (int8_t)kind;
+        e.pdir[slot] = (int8_t)((kind == kKindMove || kind == kKindHarvest || kind == kKindReturn || kind == kKindProduce)
+                                    ? dir
+                                    : kAbsent);
+        e.pnone[slot] = kind == kKindNone ? none : 0;
+        e.ptarget[slot] = (int16_t)(kind == kKindAttack ? target : kAbsent);
+        e.pptype[slot] = (int8_t)(kind == kKindProduce ? ptype : kAbsent);
+        e.pissued[slot] = time;
+        e.pcompl[slot] = wadd(time, duration);
+        e.porder[slot] = held == kAbsent ? next_order : held;
+        if (held == kAbsent) e.sc[S_NEXT_ORDER] = wadd(next_order, 1);
+    }
+    wave_sync();
+}
+
+// admission.admit (N/core/admission.py:181-197)
+NR_DEV void admit(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1,
+                  bool count_events) {
+    const Layout& y = g.lay;
+    if (count_events) {
+        if (lane < 32) at<int32_t>(e, y.b_events)[lane] = 0;
+        wave_sync();
+    }
+    int32_t n_rank = 0;
+    const int32_t n = order_requests(g, e, lane, &n_rank);
+    AS3 int16_t* order = at<int16_t>(e, y.b_order);
+    for (int32_t i = 0; i < n; ++i) {
+        const int32_t p = uni(order[i]);
+        admit_one(g, h, e, lane, p, n_rank, key0, key1, count_events);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Completion (N/core/pending.py:47-76, N/core/completion.py)
+// ---------------------------------------------------------------------------
+// Member record: 5 dwords.
+//   [0] slot | kind << 16 | dir << 24   [1] target(16) | ptype(8) << 16 | owner(8) << 24
+//   [2] unit_type(8) | cell(16) << 8    [3] birth   [4] carried
+NR_DEV void remove_slot(const Env& e, int32_t s) {
+    e.birth[s] = kAbsent;
+    e.utype[s] = (int8_t)kAbsent;
+    e.owner[s] = (int8_t)kAbsent;
+    e.cell[s] = (int16_t)kAbsent;
+    e.hp[s] = 0;
+    e.carried[s] = 0;
+    e.pkind[s] = (int8_t)kAbsent;
+    e.pdir[s] = (int8_t)kAbsent;
+    e.pnone[s] = 0;
+    e.ptarget[s] = (int16_t)kAbsent;
+    e.pptype[s] = (int8_t)kAbsent;
+    e.pissued[s] = 0;
+    e.pcompl[s] = 0;
+    e.porder[s] = kAbsent;
+}
+
+// N/core/completion.py:134-180 (_take_turn) for the member record `r`, with
+// each kind's _complete (move.py:19-27, harvest.py:24-45, return_.py:25-43,
+// produce.py:47-81, attack.py:78-98).
+NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, AS3 const int32_t* r) {
+    const int32_t w0 = uni(r[0]), w1 = uni(r[1]), w2 = uni(r[2]);
+    const int32_t slot = w0 & 0xFFFF;
+    const int32_t kind = (int8_t)((w0 >> 16) & 0xFF);
+    const int32_t dir = (int8_t)((w0 >> 24) & 0xFF);
+    const int32_t target = (int16_t)(w1 & 0xFFFF);
+    const int32_t ptype = (int8_t)((w1 >> 16) & 0xFF);
+    const int32_t owner = (int8_t)((w1 >> 24) & 0xFF);
+    const int32_t utype = (int8_t)(w2 & 0xFF);
+    const int32_t rcell = (int16_t)((w2 >> 8) & 0xFFFF);
+    const int32_t rbirth = uni(r[3]);
+    const int32_t rcarried = uni(r[4]);
+    const int32_t actor = clampi(utype, 0, g.T - 1);
+    const int32_t player = clampi(owner, 0, 1);
+    const int32_t cur_birth = uni(e.birth[slot]);
+    const bool alive = cur_birth != kAbsent && cur_birth == rbirth;
+    const int32_t dest = reserved_position(g, rcell, dir);
+    bool removal = false;
+    int32_t removed = 0;
+    if (kind == kKindMove) {
+        if (alive && lane == 0) {
+            if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)slot;
+            if (rcell >= 0 && rcell < g.cells) e.entity[rcell] = (int16_t)kAbsent;
+            e.cell[slot] = (int16_t)dest;
+        }
+    } else if (kind == kKindHarvest) {
+        const Nb n = neighbour(g, h, e, rcell, dir);
+        const bool harvesting = uni(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_RESOURCE) ? 1 : 0) != 0;
+        if (harvesting) {
+            const int32_t stack = uni(n.slot);
+            const int32_t amount = tabv(h, F_AMOUNT, actor);
+            const int32_t left = wsub(uni(e.carried[stack]), amount);
+            if (lane == 0) {
+                e.carried[stack] = left;
+                if (alive) e.carried[slot] = amount;
+            }
+            if (left <= 0) {
+                removal = true;
+                removed = stack;
+            }
+        }
+    } else if (kind == kKindReturn) {
+        const Nb n = neighbour(g, h, e, rcell, dir);
+        const bool returning =
+            uni(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_STOCKPILE) && rcarried > 0 ? 1 : 0) != 0;
+        if (returning && lane == 0) {
+            if (alive) e.carried[slot] = 0;
+            e.sc[S_RES0 + player] = wadd(e.sc[S_RES0 + player], rcarried);
+        }
+    } else if (kind == kKindProduce) {
+        const int32_t newborn_type = clampi(ptype, 0, g.T - 1);
+        const int32_t balance = wsub(uni(e.sc[S_RES0 + player]), tabv(h, F_COST, newborn_type));
+        if (balance >= 0) {
+            // units.lowest_free_slot (N/core/units.py:12-18)
+            const int32_t block = g.N + player * g.C;
+            int32_t newborn = -1;
+            for (int32_t base = 0; base < g.C && newborn < 0; base += kWave) {
+                const int32_t i = base + lane;
+                const bool free = i < g.C && e.birth[block + i] == kAbsent;
+                const uint64_t m = ballot(free);
+                if (m != 0ull) newborn = block + base + (int32_t)__builtin_ctzll(m);
+            }
+            newborn = uni(newborn);
+            if (lane == 0) {
+                if (newborn >= 0) {
+                    const int32_t birth = e.sc[S_NEXT_BIRTH];
+                    e.sc[S_RES0 + player] = balance;
+                    if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)newborn;
+                    e.birth[newborn] = birth;
+                    e.utype[newborn] = (int8_t)newborn_type;
+                    e.owner[newborn] = (int8_t)player;
+                    e.cell[newborn] = (int16_t)dest;
+                    e.hp[newborn] = (int16_t)tabv(h, F_HP, newborn_type);
+                    e.sc[S_NEXT_BIRTH] = wadd(birth, 1);
+                } else {
+                    e.sc[S_SO0 + player] = wadd(e.sc[S_SO0 + player], 1);
+                }
+            }
+        }
+    } else if (kind == kKindAttack) {
+        const int32_t occ = uni(e.entity[clampi(target, 0, g.cells - 1)]);
+        if (occ != kAbsent) {
+            const int32_t victim = occ;
+            const int32_t left = wsub(uni(e.hp[gidx(victim, g.E)]), tabv(h, F_DAMAGE, actor));
+            if (lane == 0) e.hp[victim] = (int16_t)left;
+            if (left <= 0) {
+                removal = true;
+                removed = victim;
+            }
+        }
+    }
+    if (removal) {
+        wave_sync();
+        if (lane == 0) {
+            const int32_t c = e.cell[gidx(removed, g.E)];
+            if (c >= 0 && c < g.cells) e.entity[c] = (int16_t)kAbsent;
+            remove_slot(e, removed);
+        }
+    }
+    wave_sync();
+}
+
+// pending.select + completion.apply (N/core/completion.py:106-117).
+NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e, int lane) {
+    const Layout& y = g.lay;
+    const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
+    if (lane == 0) e.sc[S_TIME] = time;
+    AS3 uint64_t* keys = at<uint64_t>(e, y.m_keys);
+    AS3 int16_t* tmp = at<int16_t>(e, y.m_tmp);
+    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);
+    // members = due & not NONE among owned slots, keyed by pending order
+    int32_t n = 0;
+    for (int32_t base = 0; base < 2 * g.C; base += kWave) {
+        const int32_t p = base + lane;
+        bool acting = false;
+        int32_t s = 0;
+        if (p < 2 * g.C) {
+            s = g.N + p;
+            const int32_t k = e.pkind[s];
+            acting = k != kAbsent && k != kKindNone && e.pcompl[s] <= time;
+        }
+        const uint64_t m = ballot(acting);
+        if (acting) {
+            const int32_t at_ = n + count_below(m);
+            keys[at_] = ((uint64_t)((uint32_t)e.porder[s] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)p;
+            tmp[at_] = (int16_t)s;
+        }
+        n += popc(m);
+    }
+    wave_sync();
+    // snapshot the retained actors in member order (:120-131)
+    for (int32_t i = lane; i < n; i += kWave) {
+        const uint64_t ki = keys[i];
+        int32_t pos = 0;
+        for (int32_t j = 0; j < n; ++j) pos += keys[j] < ki;
+        const int32_t s = tmp[i];
+        AS3 int32_t* r = rec + 5 * pos;
+        r[0] = (s & 0xFFFF) | ((e.pkind[s] & 0xFF) << 16) | ((e.pdir[s] & 0xFF) << 24);
+        r[1] = (e.ptarget[s] & 0xFFFF) | ((e.pptype[s] & 0xFF) << 16) | ((e.owner[s] & 0xFF) << 24);
+        r[2] = (e.utype[s] & 0xFF) | ((e.cell[s] & 0xFFFF) << 8);
+        r[3] = e.birth[s];
+        r[4] = e.carried[s];
+    }
+    wave_sync();
+    // clear every due pending action (pending.clear)
+    for (int32_t s = lane; s < g.E; s += kWave) {
+        if (e.pkind[s] != kAbsent && e.pcompl[s] <= time) {
+            e.pkind[s] = (int8_t)kAbsent;
+            e.pdir[s] = (int8_t)kAbsent;
+            e.pnone[s] = 0;
+            e.ptarget[s] = (int16_t)kAbsent;
+            e.pptype[s] = (int8_t)kAbsent;
+            e.pissued[s] = 0;
+            e.pcompl[s] = 0;
+            e.porder[s] = kAbsent;
+        }
+    }
+    wave_sync();
+    for (int32_t i = 0; i < n; ++i) take_turn(g, h, e, lane, rec + 5 * i);
+}
+
+// outcome.decide (N/core/outcome.py:11-25)
+NR_DEV void decide(const KGame& g, const Env& e, int lane) {
+    bool alive[2] = {false, false};
+    for (int32_t pl = 0; pl < 2; ++pl) {
+        uint64_t any = 0;
+        for (int32_t base = 0; base < g.C; base += kWave) {
+            const int32_t i = base + lane;
+            any |= ballot(i < g.C && e.birth[g.N + pl * g.C + i] != kAbsent);
+        }
+        alive[pl] = any != 0ull;
+    }
+    const int32_t count = (alive[0] ? 1 : 0) + (alive[1] ? 1 : 0);
+    if (lane == 0) {
+        e.sc[S_GAME_OVER] = count <= 1 ? 1 : 0;
+        e.sc[S_WINNER] = count == 1 ? (alive[0] ? 0 : 1) : kAbsent;
+    }
+    wave_sync();
+}
+
+// core.step (N/core/__init__.py:99-110) on the staged env.
+NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1,
+                      bool count_events) {
+    admit(g, h, e, lane, key0, key1, count_events);
+    complete(g, h, e, lane);
+    decide(g, e, lane);
+}
+
+// Copy the initial State into the staged env: core.reset ignores its key
+// (N/core/__init__.py:30-32) and lifecycle.advance takes every leaf from it
+// (N/adapters/lifecycle.py:53-79).
+NR_DEV void reset_env(const KGame& g, const Env& e, int lane) {
+    const int32_t episode = uni(e.sc[S_EPISODE]);
+    const int32_t root0 = uni(e.sc[S_ROOT0]), root1 = uni(e.sc[S_ROOT1]);
+    load_env(g, g.initial, 0, e, LD_ALL, lane);
+    if (lane == 0) {
+        e.sc[S_ROOT0] = root0;
+        e.sc[S_ROOT1] = root1;
+        e.sc[S_EPISODE] = (int32_t)((uint32_t)episode + 1u);
+    }
+    wave_sync();
+    decide(g, e, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Legality (N/core/legality.py:32-64, kinds' _legality; row layout
+// N/adapters/factors.py:31-62): bit 0..5 kind, 6.. move, 10.. harvest,
+// 14.. return, 18.. produce direction, 22.. produce type, 22+T.. attack.
+// ---------------------------------------------------------------------------
+struct Row {
+    uint32_t w[3];
+};
+
+NR_DEV void set_bit(Row& r, int32_t b) {
+    const uint32_t bit = 1u << (b & 31);
+    const int32_t w = b >> 5;
+    r.w[0] |= w == 0 ? bit : 0u;
+    r.w[1] |= w == 1 ? bit : 0u;
+    r.w[2] |= w == 2 ? bit : 0u;
+}
+
+NR_DEV Row legality_row(const KGame& g, const Hdr& h, const Env& e, int32_t slot) {
+    Row r;
+    r.w[0] = r.w[1] = r.w[2] = 0u;
+    if (e.birth[slot] == kAbsent) return r;
+    const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
+    const int32_t owner = e.owner[slot];
+    const int32_t carried = e.carried[slot];
+    const int32_t cell = e.cell[slot];
+    const int32_t flags = tabv(h, F_FLAGS, actor);
+    const int32_t balance = e.sc[S_RES0 + clampi(owner, 0, 1)];
+    uint32_t affordable = 0u;
+    for (int32_t t = 0; t < g.T; ++t)
+        if (balance >= tabv(h, F_COST, t)) affordable |= 1u << t;
+    const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
+    set_bit(r, kKindNone);
+    uint32_t produce_types = 0u;
+    const int32_t x = floor_mod(cell, g.W), yy = floor_div(cell, g.W);
+#pragma unroll
+    for (int32_t d = 0; d < 4; ++d) {
+        const int32_t nx = x + dir_dx(d), ny = yy + dir_dy(d);
+        if (nx < 0 || nx >= g.W || ny < 0 || ny >= g.H) continue;
+        const int32_t nc = ny * g.W + nx;
+        const int32_t occ = e.entity[nc];
+        if (occ == kAbsent) {
+            if (h.terrain[nc] == 0) {
+                if (flags & FL_MOVE) {
+                    set_bit(r, 6 + d);
+                    set_bit(r, kKindMove);
+                }
+                if (types != 0u) {
+                    set_bit(r, 18 + d);
+                    produce_types |= types;
+                }
+            }
+        } else {
+            const int32_t s = gidx(occ, g.E);
+            const int32_t nflags = tabv(h, F_FLAGS, clampi(e.utype[s], 0, g.T - 1));
+            if ((flags & FL_HARVEST) && carried == 0 && (nflags & FL_RESOURCE)) {
+                set_bit(r, 10 + d);
+                set_bit(r, kKindHarvest);
+            }
+            if ((flags & FL_HARVEST) && carried > 0 && (nflags & FL_STOCKPILE) && e.owner[s] == owner) {
+                set_bit(r, 14 + d);
+                set_bit(r, kKindReturn);
+            }
+        }
+    }
+    if (produce_types != 0u) {
+        set_bit(r, kKindProduce);
+        for (int32_t t = 0; t < g.T; ++t)
+            if ((produce_types >> t) & 1u) set_bit(r, 22 + t);
+    }
+    if (flags & FL_ATTACK) {
+        const int32_t range = tabv(h, F_RANGE, actor);
+        const int32_t reach = imin(range, g.radius);
+        const int32_t first = 22 + g.T;
+        bool any = false;
+        for (int32_t dy = -reach; dy <= reach; ++dy) {
+            const int32_t ty = yy + dy;
+            if (ty < 0 || ty >= g.H) continue;
+            for (int32_t dx = -reach; dx <= reach; ++dx) {
+                if (dx * dx + dy * dy > range * range) continue;
+                const int32_t tx = x + dx;
+                if (tx < 0 || tx >= g.W) continue;
+                const int32_t occ = e.entity[ty * g.W + tx];
+                if (occ == kAbsent) continue;
+                const int32_t towner = e.owner[gidx(occ, g.E)];
+                if (towner >= 0 && towner != owner) {
+                    set_bit(r, first + (g.radius + dy) * g.side + (g.radius + dx));
+                    any = true;
+                }
+            }
+        }
+        if (any) set_bit(r, kKindAttack);
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// The synthetic harness sampler (uniform over each factor's legal values):
+//   k_env = fold_in(fold_in(sample_key, step), env);
+//   (w0, w1) = threefry(k_env, (p, 0)), (w2, w3) = threefry(k_env, (p, 1));
+//   factor f draws the 16-bit half f of w0..w3 (low half first) and takes the
+//   (h mod popcount)-th set bit of its mask, or 0 when the mask is empty.
+// A row whose only set bit is NONE samples all zeros.
+// ---------------------------------------------------------------------------
+NR_DEV uint64_t row_bits(const Row& r, int32_t lo, int32_t width) {
+    const uint64_t low = (uint64_t)r.w[0] | ((uint64_t)r.w[1] << 32);
+    const uint64_t high = (uint64_t)r.w[2];
+    uint64_t v;
+    if (lo == 0) v = low;
+    else if (lo < 64) v = (low >> lo) | (high << (64 - lo));
+    else v = high >> (lo - 64);
+    return width >= 64 ? v : (v & ((1ull << width) - 1ull));
+}
+
+NR_DEV int32_t select_set_bit(uint64_t m, int32_t k) {
+    for (int32_t i = 0; i < k; ++i) m &= m - 1ull;
+    return (int32_t)__builtin_ctzll(m);
+}
+
+NR_DEV bool only_none(const Row& r) { return r.w[0] == 1u && r.w[1] == 0u && r.w[2] == 0u; }
+
+NR_DEV void sample_row(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1, int32_t p, int32_t a[7]) {
+    if (only_none(r)) {
+#pragma unroll
+        for (int f = 0; f < 7; ++f) a[f] = 0;
+        return;
+    }
+    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
+    threefry(ke0, ke1, w0, w1);
+    threefry(ke0, ke1, w2, w3);
+    const uint32_t words[4] = {w0, w1, w2, w3};
+    const int32_t lo[7] = {0, 6, 10, 14, 18, 22, 22 + g.T};
+    const int32_t wid[7] = {6, 4, 4, 4, 4, g.T, g.O};
+#pragma unroll
+    for (int f = 0; f < 7; ++f) {
+        const uint32_t hh = (words[f >> 1] >> (16 * (f & 1))) & 0xFFFFu;
+        const uint64_t m = row_bits(r, lo[f], wid[f]);
+        const int32_t count = popc(m);
+        a[f] = count > 0 ? select_set_bit(m, (int32_t)(hh % (uint32_t)count)) : 0;
+    }
+}
+
+// decode_actions for one row (N/adapters/jaxmarl/actions.py:61-84,
+// N/adapters/factors.py:117-151), stored in canonical command form.
+NR_DEV void decode_row(const KGame& g, const Env& e, int32_t p, bool available, const int32_t a[7]) {
+    const Layout& y = g.lay;
+    const int32_t kind = a[0];
+    int32_t dir = kAbsent;
+    if (kind == kKindMove) dir = a[1];
+    else if (kind == kKindHarvest) dir = a[2];
+    else if (kind == kKindReturn) dir = a[3];
+    else if (kind == kKindProduce) dir = a[4];
+    const int32_t ptype = kind == kKindProduce ? a[5] : kAbsent;
+    int32_t target = kAbsent;
+    if (kind == kKindAttack) {
+        const int32_t cell = e.cell[g.N + p];
+        const int32_t tx = wadd(floor_mod(cell, g.W), floor_mod(a[6], g.side) - g.radius);
+        const int32_t ty = wadd(floor_div(cell, g.W), floor_div(a[6], g.side) - g.radius);
+        if (tx >= 0 && tx < g.W && ty >= 0 && ty < g.H) target = ty * g.W + tx;
+    }
+    at<int8_t>(e, y.c_kind)[p] = (int8_t)(available ? canon_kind(kind) : kAbsent);
+    at<int8_t>(e, y.c_dir)[p] = (int8_t)(available ? canon_dir(dir) : kAbsent);
+    at<int8_t>(e, y.c_ptype)[p] = (int8_t)(available ? canon_ptype(ptype, g.T) : kAbsent);
+    at<int16_t>(e, y.c_target)[p] = (int16_t)(available ? target : kAbsent);
+    at<int32_t>(e, y.c_none)[p] = available ? (kind == kKindNone ? 1 : 0) : 0;
+    at<int16_t>(e, y.c_rank)[p] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Observations (N/observations/visibility.py:56-71, symbolic.py:130-180)
+// ---------------------------------------------------------------------------
+// Sight-radius visibility of `observer` as a bitmap seen[H][seen_words].
+NR_DEV void stamp_visibility(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t observer) {
+    const Layout& y = g.lay;
+    AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);
+    AS3 int16_t* units = at<int16_t>(e, y.b_units);
+    const int32_t nwords = g.H * g.seen_words;
+    for (int32_t i = lane; i < nwords; i += kWave) seen[i] = 0u;
+    const int32_t block = g.N + observer * g.C;
+    int32_t n = 0;
+    for (int32_t base = 0; base < g.C; base += kWave) {
+        const int32_t i = base + lane;
+        const bool act = i < g.C && e.birth[block + i] != kAbsent;
+        const uint64_t m = ballot(act);
+        if (act) units[n + count_below(m)] = (int16_t)(block + i);
+        n += popc(m);
+    }
+    wave_sync();
+    const int32_t rows = 2 * g.sight_max + 1;
+    const int32_t items = n * rows;
+    for (int32_t w = lane; w < items; w += kWave) {
+        const int32_t u = w / rows;
+        const int32_t dy = w - u * rows - g.sight_max;
+        const int32_t s = units[u];
+        const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
+        if (dy < -r || dy > r) continue;
+        const int32_t cell = e.cell[s];
+        const int32_t cy = floor_div(cell, g.W) + dy;
+        if (cy < 0 || cy >= g.H) continue;
+        const int32_t rem = r * r - dy * dy;
+        int32_t hw = r;
+        while (hw * hw > rem) --hw;
+        const int32_t cx = floor_mod(cell, g.W);
+        const int32_t x0 = cx - hw < 0 ? 0 : cx - hw;
+        const int32_t x1 = cx + hw >= g.W ? g.W - 1 : cx + hw;
+        if (x0 > x1) continue;
+        for (int32_t wd = x0 >> 5; wd <= (x1 >> 5); ++wd) {
+            const int32_t a = x0 > wd * 32 ? x0 - wd * 32 : 0;
+            const int32_t b = x1 < wd * 32 + 31 ? x1 - wd * 32 : 31;
+            const uint32_t bits = (b - a == 31) ? 0xFFFFFFFFu : (((1u << (b - a + 1)) - 1u) << a);
+            __atomic_fetch_or(&seen[cy * g.seen_words + wd], bits, __ATOMIC_RELAXED);
+        }
+    }
+    wave_sync();
+}
+
+NR_DEV bool seen_at(const KGame& g, const Env& e, int32_t c) {
+    const AS3 uint32_t* seen = at<uint32_t>(e, g.lay.v_seen);
+    const int32_t yy = c / g.W, x = c - yy * g.W;
+    return (seen[yy * g.seen_words + (x >> 5)] >> (x & 31)) & 1u;
+}
+
+// Symbolic uint8 feature maps and scalars of one observer, written to
+// maps[H][W][6] and scalars[4] in global memory.
+NR_DEV void observe_player(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t player, bool partial,
+                           uint8_t* maps, int32_t* scalars) {
+    const Layout& y = g.lay;
+    if (partial) stamp_visibility(g, h, e, lane, player);
+    AS3 uint8_t* stage = at<uint8_t>(e, y.v_stage);
+    for (int32_t c0 = 0; c0 < g.cells; c0 += g.stage_cells) {
+        const int32_t n = imin(g.stage_cells, g.cells - c0);
+        for (int32_t i = lane; i < n; i += kWave) {
+            const int32_t c = c0 + i;
+            const int32_t occ = e.entity[c];
+            uint32_t hp = 0, carried = 0, type = 0, kind = 0, owner = 0;
+            if (occ != kAbsent) {
+                const int32_t s = clampi(occ, 0, g.E - 1);
+                hp = (uint32_t)(int32_t)e.hp[s] & 0xFFu;
+                carried = (uint32_t)e.carried[s] & 0xFFu;
+                type = (uint32_t)((int32_t)e.utype[s] + 1) & 0xFFu;
+                const int32_t pk = e.pkind[s];
+                kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
+                owner = (uint32_t)((int32_t)e.owner[s] + 1) & 0x3u;
+            }
+            if (partial && !(owner == (uint32_t)(player + 1) || seen_at(g, e, c))) hp = carried = type = kind = owner = 0;
+            const uint32_t rel = owner > 0 ? (uint32_t)((((int32_t)owner - 1 + player) & 1) + 1) : 0u;
+            AS3 uint16_t* out = (AS3 uint16_t*)(stage + i * 6);
+            out[0] = (uint16_t)(hp | (carried << 8));
+            out[1] = (uint16_t)(rel | (type << 8));
+            out[2] = (uint16_t)(kind | ((uint32_t)h.terrain[c] << 8));
+        }
+        wave_sync();
+        copy_out(maps + (size_t)c0 * 6, stage, n * 6, lane);
+        wave_sync();
+    }
+    if (lane < 4) {
+        int32_t v;
+        if (lane == 0) v = e.sc[S_RES0 + player];
+        else if (lane == 1) v = e.sc[S_RES0 + (player ^ 1)];
+        else if (lane == 2) v = e.sc[S_TIME];
+        else v = e.sc[S_ALT];
+        scalars[lane] = v;
+    }
+}
+
+}  // namespace nr

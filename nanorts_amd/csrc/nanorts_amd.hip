@@ -1,0 +1,765 @@
+// gfx950 kernels and the C-ABI entry points of nanorts_amd.
+//
+// Launch shape: one wave64 per game, WPB games per workgroup; dynamic LDS =
+// workgroup header (unit table + terrain) + WPB env blocks.  No entry point
+// allocates device memory; all run asynchronously on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/nanorts_amd.h"
+#include "engine.h"
+
+using namespace nr;
+
+#ifndef NANORTS_BUILD_ID
+#define NANORTS_BUILD_ID "dev"
+#endif
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& message) {
+    g_error = message;
+    return code;
+}
+
+int32_t align16(int32_t v) { return (v + 15) & ~15; }
+
+struct Shape {
+    KGame g;
+    int wpb;        // waves (games) per workgroup
+    int32_t lds;    // dynamic LDS bytes per workgroup
+};
+
+bool valid_game(const nanorts_game* game, std::string* why) {
+    if (!game) {
+        *why = "game is NULL";
+        return false;
+    }
+    if (game->height <= 0 || game->width <= 0 || game->cells != game->height * game->width) {
+        *why = "game extents are inconsistent (cells != height * width)";
+        return false;
+    }
+    if (game->cells > 32767 || game->entities > 32767) {
+        *why = "this build lays out int16 cell and slot indices only (cells and entities <= 32767)";
+        return false;
+    }
+    if (game->capacity <= 0 || game->neutral < 0 || game->entities != game->neutral + 2 * game->capacity) {
+        *why = "entities != neutral + 2 * capacity";
+        return false;
+    }
+    if (game->types <= 0 || game->types > NANORTS_MAX_TYPES) {
+        *why = "types must be in 1..8";
+        return false;
+    }
+    int side = 1;
+    while (side * side < game->offsets) ++side;
+    if (side * side != game->offsets || side % 2 == 0 || 22 + game->types + game->offsets > 96) {
+        *why = "offsets must be an odd square and a mask row must fit 96 bits";
+        return false;
+    }
+    if (game->strategy < 0 || game->strategy > 2) {
+        *why = "strategy must be 0 (CANCEL_BOTH), 1 (CANCEL_RANDOM) or 2 (CANCEL_ALTERNATING)";
+        return false;
+    }
+    if (!game->terrain) {
+        *why = "terrain is NULL";
+        return false;
+    }
+    return true;
+}
+
+bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
+    if (!valid_game(game, why)) return false;
+    KGame& g = out->g;
+    std::memset(&g, 0, sizeof(g));
+    g.H = game->height;
+    g.W = game->width;
+    g.cells = game->cells;
+    g.N = game->neutral;
+    g.C = game->capacity;
+    g.E = game->entities;
+    g.T = game->types;
+    g.O = game->offsets;
+    g.strategy = game->strategy;
+    g.max_cycles = game->max_cycles;
+    int side = 1;
+    while (side * side < g.O) ++side;
+    g.side = side;
+    g.radius = (side - 1) / 2;
+    int bits = 0;
+    for (int v = g.C - 1; v > 0; v >>= 1) ++bits;
+    g.rank_bits = bits < 1 ? 1 : bits;
+    g.seen_words = (g.W + 31) / 32;
+    g.stage_cells = g.cells < 256 ? g.cells : 256;
+    g.sight_max = 0;
+    for (int t = 0; t < g.T; ++t) {
+        g.tab[F_COST * 8 + t] = game->cost[t];
+        g.tab[F_HP * 8 + t] = game->hit_points[t];
+        g.tab[F_PRODUCE_TIME * 8 + t] = game->produce_time[t];
+        g.tab[F_MOVE_TIME * 8 + t] = game->move_time[t];
+        g.tab[F_ATTACK_TIME * 8 + t] = game->attack_time[t];
+        g.tab[F_HARVEST_TIME * 8 + t] = game->harvest_time[t];
+        g.tab[F_RANGE * 8 + t] = game->attack_range[t];
+        g.tab[F_DAMAGE * 8 + t] = game->attack_damage[t];
+        g.tab[F_AMOUNT * 8 + t] = game->harvest_amount[t];
+        g.tab[F_SIGHT * 8 + t] = game->sight_radius[t];
+        g.tab[F_FLAGS * 8 + t] = (game->is_resource[t] ? FL_RESOURCE : 0) | (game->is_stockpile[t] ? FL_STOCKPILE : 0) |
+                                 (game->can_harvest[t] ? FL_HARVEST : 0) | (game->can_move[t] ? FL_MOVE : 0) |
+                                 (game->can_attack[t] ? FL_ATTACK : 0);
+        int32_t produces = 0;
+        for (int u = 0; u < g.T; ++u)
+            if (game->produces[t * NANORTS_MAX_TYPES + u]) produces |= 1 << u;
+        g.tab[F_PRODUCES * 8 + t] = produces;
+        if (game->sight_radius[t] > g.sight_max) g.sight_max = game->sight_radius[t];
+        if (game->sight_radius[t] < 0 || game->sight_radius[t] > 64) {
+            *why = "sight radius out of range";
+            return false;
+        }
+    }
+    g.terrain = game->terrain;
+    g.initial = game->initial;
+
+    Layout& y = g.lay;
+    const int32_t E = g.E, C2 = 2 * g.C, cells = g.cells;
+    y.o_terrain = F_COUNT * 8 * 4;
+    y.hdr_bytes = align16(y.o_terrain + cells);
+    int32_t o = 0;
+    auto take = [&o](int32_t bytes) {
+        const int32_t at = o;
+        o += align16(bytes);
+        return at;
+    };
+    y.o_birth = take(E * 4);
+    y.o_carried = take(E * 4);
+    y.o_pnone = take(E * 4);
+    y.o_pissued = take(E * 4);
+    y.o_pcompl = take(E * 4);
+    y.o_porder = take(E * 4);
+    y.o_cell = take(E * 2);
+    y.o_hp = take(E * 2);
+    y.o_ptarget = take(E * 2);
+    y.o_entity = take(cells * 2);
+    y.o_utype = take(E);
+    y.o_owner = take(E);
+    y.o_pkind = take(E);
+    y.o_pdir = take(E);
+    y.o_pptype = take(E);
+    y.o_scal = take(S_COUNT * 4);
+    y.b_events = take(32 * 4);
+    const int32_t union0 = o;
+    // admission
+    y.c_kind = take(C2);
+    y.c_dir = take(C2);
+    y.c_ptype = take(C2);
+    y.c_target = take(C2 * 2);
+    y.c_none = take(C2 * 4);
+    y.c_rank = take(C2 * 2);
+    y.b_pkey = take(C2 * 4);
+    y.b_keys = take(C2 * 8);
+    y.b_tmp = take(C2 * 2);
+    y.b_order = take(C2 * 2);
+    y.b_rank = take(E * 2);
+    const int32_t admission_end = o;
+    // completion (the commands are dead by then)
+    o = union0;
+    y.m_rec = take(C2 * 20);
+    y.m_keys = take(C2 * 8);
+    y.m_tmp = take(C2 * 2);
+    const int32_t completion_end = o;
+    // observation
+    o = union0;
+    y.v_seen = take(g.H * g.seen_words * 4);
+    y.v_stage = take(g.stage_cells * 6);
+    y.b_units = take(g.C * 2);
+    const int32_t observe_end = o;
+    // masks
+    o = union0;
+    y.v_words = take(C2 * 12);
+    const int32_t masks_end = o;
+    int32_t end = admission_end;
+    if (completion_end > end) end = completion_end;
+    if (observe_end > end) end = observe_end;
+    if (masks_end > end) end = masks_end;
+    y.env_bytes = align16(end);
+
+    int max_lds = 65536;
+    int device = 0;
+    if (hipGetDevice(&device) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+            max_lds = v;
+    }
+    int wpb = 4;
+    while (wpb > 1 && y.hdr_bytes + wpb * y.env_bytes > max_lds) --wpb;
+    if (y.hdr_bytes + wpb * y.env_bytes > max_lds) {
+        *why = "one game's LDS block (" + std::to_string(y.hdr_bytes + y.env_bytes) + " bytes) exceeds the " +
+               std::to_string(max_lds) + " bytes a workgroup may allocate";
+        return false;
+    }
+    out->wpb = wpb;
+    out->lds = y.hdr_bytes + wpb * y.env_bytes;
+    return true;
+}
+
+template <typename Kernel, typename... Args>
+int launch(Kernel kernel, const Shape& sh, int64_t lanes, hipStream_t stream, Args... args) {
+    if (lanes <= 0) return NANORTS_OK;
+    const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds, stream,
+                       sh.g, lanes, args...);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
+}
+
+bool state_complete(const nanorts_state& s) {
+    return s.birth && s.unit_type && s.owner && s.cell && s.hit_points && s.carried_resources && s.pending_kind &&
+           s.pending_direction && s.pending_none_duration && s.pending_target_cell && s.pending_produced_type &&
+           s.pending_issued_at && s.pending_completes_at && s.pending_order && s.entity_at && s.time &&
+           s.player_resources && s.next_birth && s.next_pending_order && s.alternating_conflict_count && s.game_over &&
+           s.winner && s.spawn_overflow;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+#define NR_KERNEL_PROLOGUE                                                        \
+    extern __shared__ __align__(16) uint8_t nr_lds[];                             \
+    AS3 uint8_t* lds = (AS3 uint8_t*)nr_lds;                                      \
+    Hdr hdr;                                                                      \
+    hdr.tab = (AS3 int32_t*)lds;                                                  \
+    hdr.terrain = lds + g.lay.o_terrain;                                          \
+    load_header(g, hdr);                                                          \
+    __syncthreads();                                                              \
+    const int lane = lane_id();                                                   \
+    const int wave = (int)(threadIdx.x >> 6);                                     \
+    const int64_t l = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;             \
+    if (l >= lanes) return;                                                       \
+    const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
+
+// Canonical commands from the reference's int32 Commands operands.
+NR_DEV void stage_commands(const KGame& g, const Env& e, int64_t l, const nanorts_commands& c, int lane) {
+    const Layout& y = g.lay;
+    const int32_t owned = 2 * g.C;
+    const int32_t top = (1 << g.rank_bits) - 1;
+    for (int32_t p = lane; p < owned; p += kWave) {
+        const int64_t i = l * owned + p;
+        at<int8_t>(e, y.c_kind)[p] = (int8_t)canon_kind(c.kind[i]);
+        at<int8_t>(e, y.c_dir)[p] = (int8_t)canon_dir(c.direction[i]);
+        at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(c.produced_type[i], g.T);
+        at<int16_t>(e, y.c_target)[p] = (int16_t)canon_target(c.target_cell[i], g.cells);
+        at<int32_t>(e, y.c_none)[p] = c.none_duration[i];
+        const int32_t ro = c.request_order[i];
+        at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(ro == kAbsent ? 0 : ro, 0, top);
+    }
+    wave_sync();
+}
+
+NR_DEV void write_events(const KGame& g, const Env& e, int64_t l, const nanorts_step_results& r, int lane) {
+    const AS3 int32_t* ev = at<int32_t>(e, g.lay.b_events);
+    if (r.admitted_harvest && lane < 2) r.admitted_harvest[2 * l + lane] = ev[lane];
+    if (r.admitted_return && lane < 2) r.admitted_return[2 * l + lane] = ev[2 + lane];
+    if (r.admitted_produce && lane < 2 * g.T) {
+        const int32_t pl = lane / g.T, t = lane % g.T;
+        r.admitted_produce[(2 * l + pl) * g.T + t] = ev[4 + pl * 8 + t];
+    }
+    if (r.admitted_attack && lane < 6) r.admitted_attack[6 * l + lane] = ev[20 + lane];
+}
+
+__global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_state s, const uint32_t* key, int64_t key_lanes,
+                       nanorts_commands c, nanorts_step_results r) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    stage_commands(g, e, l, c, lane);
+    const int64_t kl = key_lanes == 1 ? 0 : l;
+    const uint32_t k0 = key[2 * kl], k1 = key[2 * kl + 1];
+    const bool events = r.admitted_harvest || r.admitted_return || r.admitted_produce || r.admitted_attack;
+    core_step(g, hdr, e, lane, k0, k1, events);
+    store_env(g, s, l, e, lane);
+    if (lane == 0) {
+        const bool over = e.sc[S_GAME_OVER] != 0;
+        const bool trunc = !over && e.sc[S_TIME] >= g.max_cycles;
+        if (r.terminated) r.terminated[l] = over ? 1 : 0;
+        if (r.truncated) r.truncated[l] = trunc ? 1 : 0;
+        if (r.reward) {
+            const int32_t winner = e.sc[S_WINNER];
+            for (int p = 0; p < 2; ++p) r.reward[2 * l + p] = (over || trunc) ? (p == winner ? 1.0f : -1.0f) : 0.0f;
+        }
+    }
+    if (events) write_events(g, e, l, r, lane);
+}
+
+// Legality words of every owned row into the staged words area; `merge`
+// applies availability (only NONE on unavailable rows).
+NR_DEV void stage_words(const KGame& g, const Hdr& h, const Env& e, int lane, bool merge) {
+    AS3 uint32_t* words = at<uint32_t>(e, g.lay.v_words);
+    for (int32_t p = lane; p < 2 * g.C; p += kWave) {
+        const int32_t s = g.N + p;
+        Row r;
+        const bool available = e.birth[s] != kAbsent && e.pkind[s] == kAbsent;
+        if (merge && !available) {
+            r.w[0] = 1u;
+            r.w[1] = r.w[2] = 0u;
+        } else {
+            r = legality_row(g, h, e, s);
+        }
+        words[3 * p] = r.w[0];
+        words[3 * p + 1] = r.w[1];
+        words[3 * p + 2] = r.w[2];
+    }
+    wave_sync();
+}
+
+NR_DEV void emit_rows(const KGame& g, const Env& e, int64_t l, uint8_t* rows, int lane) {
+    const AS3 uint32_t* words = at<uint32_t>(e, g.lay.v_words);
+    const int32_t width = 22 + g.T + g.O;
+    const int32_t total = 2 * g.C * width;
+    uint8_t* out = rows + l * (int64_t)total;
+    if ((((uintptr_t)out) & 3u) == 0 && (total & 3) == 0) {
+        for (int32_t d = lane; d < total / 4; d += kWave) {
+            uint32_t v = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int32_t b = 4 * d + k;
+                const int32_t row = b / width, bit = b - row * width;
+                v |= ((words[3 * row + (bit >> 5)] >> (bit & 31)) & 1u) << (8 * k);
+            }
+            ((uint32_t*)out)[d] = v;
+        }
+    } else {
+        for (int32_t b = lane; b < total; b += kWave) {
+            const int32_t row = b / width, bit = b - row * width;
+            out[b] = (uint8_t)((words[3 * row + (bit >> 5)] >> (bit & 31)) & 1u);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_legality(KGame g, int64_t lanes, nanorts_state s, int32_t merge, uint8_t* rows, uint32_t* words) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_CARRIED | LD_PKIND | LD_ENTITY | LD_SCALARS,
+             lane);
+    stage_words(g, hdr, e, lane, merge != 0);
+    if (words) copy_out((uint8_t*)(words + l * 2 * g.C * 3), at<uint8_t>(e, g.lay.v_words), 2 * g.C * 12, lane);
+    if (rows) emit_rows(g, e, l, rows, lane);
+}
+
+__global__ __launch_bounds__(256) void k_visible(KGame g, int64_t lanes, nanorts_state s, int32_t observer, uint8_t* cells) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_BIRTH | LD_UTYPE | LD_CELL, lane);
+    stamp_visibility(g, hdr, e, lane, observer);
+    for (int32_t c = lane; c < g.cells; c += kWave) cells[l * g.cells + c] = seen_at(g, e, c) ? 1 : 0;
+}
+
+NR_DEV void observe_both(const KGame& g, const Hdr& h, const Env& e, int64_t slot, int lane, bool partial,
+                         uint8_t* maps, int32_t* scalars) {
+    const int64_t per = (int64_t)g.cells * 6;
+    for (int32_t p = 0; p < 2; ++p) {
+        observe_player(g, h, e, lane, p, partial, maps ? maps + (slot * 2 + p) * per : nullptr,
+                       scalars ? scalars + (slot * 2 + p) * 4 : nullptr);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_observe(KGame g, int64_t lanes, nanorts_state s, int32_t partial, uint8_t* maps, int32_t* scalars) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e,
+             LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_HP | LD_CARRIED | LD_PKIND | LD_ENTITY | LD_SCALARS, lane);
+    observe_both(g, hdr, e, l, lane, partial != 0, maps, scalars);
+}
+
+__global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_state s, const uint8_t* done) {
+    NR_KERNEL_PROLOGUE
+    if (!done[l]) return;
+    load_env(g, s, l, e, LD_SCALARS, lane);
+    reset_env(g, e, lane);
+    store_env(g, s, l, e, lane);
+}
+
+// Decode int32[2C][7] actions of env l into canonical commands.
+NR_DEV void stage_actions(const KGame& g, const Env& e, int64_t l, const int32_t* actions, int lane) {
+    const int32_t owned = 2 * g.C;
+    for (int32_t p = lane; p < owned; p += kWave) {
+        const int32_t* row = actions + (l * owned + p) * 7;
+        int32_t a[7];
+#pragma unroll
+        for (int f = 0; f < 7; ++f) a[f] = row[f];
+        const int32_t s = g.N + p;
+        const bool available = e.birth[s] != kAbsent && e.pkind[s] == kAbsent;
+        decode_row(g, e, p, available, a);
+    }
+    wave_sync();
+}
+
+// After core.step: outcome, rewards, optional final observation, auto-reset.
+NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
+                        const nanorts_env_results& r, bool events) {
+    const bool over = uni(e.sc[S_GAME_OVER]) != 0;
+    const int32_t time = uni(e.sc[S_TIME]);
+    const int32_t winner = uni(e.sc[S_WINNER]);
+    const bool trunc = !over && time >= g.max_cycles;
+    const bool done = over || trunc;
+    if (lane == 0) {
+        if (r.reward)
+            for (int p = 0; p < 2; ++p) r.reward[2 * l + p] = done ? (p == winner ? 1.0f : -1.0f) : 0.0f;
+        if (r.done) r.done[l] = done ? 1 : 0;
+        if (r.terminated) r.terminated[l] = over ? 1 : 0;
+        if (r.truncated) r.truncated[l] = trunc ? 1 : 0;
+        if (r.winner) r.winner[l] = winner;
+        if (r.spawn_overflowed) r.spawn_overflowed[l] = (e.sc[S_SO0] > 0 || e.sc[S_SO1] > 0) ? 1 : 0;
+    }
+    if (events && r.reward_components && lane < 2) {
+        // N/adapters/rewards.py:47-71 (encode_components)
+        const AS3 int32_t* ev = at<int32_t>(e, g.lay.b_events);
+        const int p = lane, o = lane ^ 1;
+        const AS3 int32_t* prod = ev + 4 + p * 8;
+        float* out = r.reward_components + (2 * l + p) * 6;
+        out[0] = over ? (winner == p ? 1.0f : -1.0f) : 0.0f;
+        out[1] = (float)(ev[p] + ev[2 + p]);
+        out[2] = (float)prod[3];
+        out[3] = (float)(prod[1] + prod[2]);
+        out[4] = (float)(ev[20 + p * 3 + o + 1] - ev[20 + p * 3 + p + 1]);
+        out[5] = (float)(prod[4] + prod[5] + prod[6]);
+    }
+    if (r.final_feature_maps || r.final_scalars) observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
+    if (done) reset_env(g, e, lane);
+    return done;
+}
+
+__global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanorts_state s, const int32_t* actions, int32_t partial,
+                           nanorts_env_results r) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    stage_actions(g, e, l, actions, lane);
+    uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
+    fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
+    const bool events = r.reward_components != nullptr;
+    core_step(g, hdr, e, lane, k0, k1, events);
+    finish_step(g, hdr, e, l, lane, partial != 0, r, events);
+    store_env(g, s, l, e, lane);
+    if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
+}
+
+__global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const uint32_t* words, uint32_t key0, uint32_t key1, int32_t step,
+                         int64_t env0, int32_t* actions) {
+    NR_KERNEL_PROLOGUE
+    (void)e;
+    uint32_t k0 = key0, k1 = key1;
+    fold_in(k0, k1, (uint32_t)step);
+    fold_in(k0, k1, (uint32_t)(env0 + l));
+    const int32_t owned = 2 * g.C;
+    for (int32_t p = lane; p < owned; p += kWave) {
+        Row r;
+        const uint32_t* w = words + (l * owned + p) * 3;
+        r.w[0] = w[0];
+        r.w[1] = w[1];
+        r.w[2] = w[2];
+        int32_t a[7];
+        sample_row(g, r, k0, k1, p, a);
+        int32_t* out = actions + (l * owned + p) * 7;
+#pragma unroll
+        for (int f = 0; f < 7; ++f) out[f] = a[f];
+    }
+}
+
+// Fused rollout: the state stays staged in LDS across `steps` cycles.
+__global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts_state s, uint32_t key0, uint32_t key1, int32_t step0,
+                          int32_t steps, int32_t partial, int64_t env0, nanorts_rollout_results out) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    const int32_t owned = 2 * g.C;
+    const nanorts_env_results none = {};
+    for (int32_t t = 0; t < steps; ++t) {
+        const int32_t step = step0 + t;
+        // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
+        uint32_t ke0 = key0, ke1 = key1;
+        fold_in(ke0, ke1, (uint32_t)step);
+        fold_in(ke0, ke1, (uint32_t)(env0 + l));
+        for (int32_t p = lane; p < owned; p += kWave) {
+            const int32_t sl = g.N + p;
+            const bool available = e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent;
+            int32_t a[7] = {0, 0, 0, 0, 0, 0, 0};
+            if (available) {
+                const Row r = legality_row(g, hdr, e, sl);
+                sample_row(g, r, ke0, ke1, p, a);
+            }
+            if (out.actions) {
+                int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+#pragma unroll
+                for (int f = 0; f < 7; ++f) dst[f] = a[f];
+            }
+            decode_row(g, e, p, available, a);
+        }
+        wave_sync();
+        // env.step
+        uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
+        fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
+        core_step(g, hdr, e, lane, k0, k1, false);
+        nanorts_env_results r = none;
+        if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
+        if (out.dones) r.done = out.dones + (int64_t)t * lanes;
+        // finish_step indexes outputs by l; shift the per-step bases
+        finish_step(g, hdr, e, l, lane, partial != 0, r, false);
+        if (out.feature_maps || out.scalars) {
+            const int64_t ring = out.depth > 0 ? (int64_t)(t % out.depth) : 0;
+            observe_both(g, hdr, e, ring * lanes + l, lane, partial != 0, out.feature_maps, out.scalars);
+        }
+    }
+    store_env(g, s, l, e, lane);
+}
+
+// Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
+__global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_state s, int32_t partial, const uint8_t* tiles, uint8_t* image,
+                         int32_t* scalars) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e,
+             LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_HP | LD_CARRIED | LD_PKIND | LD_ENTITY | LD_SCALARS, lane);
+    const int32_t occupant_states = 1 + 3 * g.T;
+    const int64_t row_bytes = (int64_t)g.W * 16 * 3;
+    const int64_t per = (int64_t)g.H * 16 * row_bytes;
+    for (int32_t pl = 0; pl < 2; ++pl) {
+        if (partial) stamp_visibility(g, hdr, e, lane, pl);
+        uint8_t* img = image + (l * 2 + pl) * per;
+        // one lane writes one 4-pixel (12-byte) run of one sprite row
+        const int32_t runs = g.cells * 16 * 4;
+        for (int32_t w = lane; w < runs; w += kWave) {
+            const int32_t c = w >> 6;
+            const int32_t py = (w >> 2) & 15;
+            const int32_t px0 = (w & 3) * 4;
+            const int32_t occ = e.entity[c];
+            bool present = occ != kAbsent;
+            const int32_t sl = clampi(occ, 0, g.E - 1);
+            if (present && partial) {
+                const int32_t cell_of = clampi(e.cell[sl], 0, g.cells - 1);
+                present = e.birth[sl] != kAbsent && (e.owner[sl] == pl || seen_at(g, e, cell_of));
+            }
+            int32_t owner = present ? e.owner[sl] : kAbsent;
+            if (owner >= 0) owner = (owner + pl) & 1;
+            const int32_t type = present ? e.utype[sl] : kAbsent;
+            const int32_t pk = present ? e.pkind[sl] : 0;
+            const int32_t kind = pk > 0 ? pk : 0;
+            const int32_t carried = present ? e.carried[sl] : 0;
+            const int32_t hp = present ? e.hp[sl] : 0;
+            const int32_t occupant = present ? 1 + (owner + 1) * g.T + type : 0;
+            const int32_t tile = gidx((hdr.terrain[c] ? occupant_states : 0) + occupant, 2 * occupant_states);
+            const uint8_t* src = tiles + ((int64_t)tile * 256 + py * 16 + px0) * 3;
+            uint8_t px[12];
+#pragma unroll
+            for (int k = 0; k < 12; ++k) px[k] = src[k];
+            if (present && py >= 12 && py <= 14) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int32_t x = px0 + k;
+                    if (x < 1 || x >= 15) continue;
+                    const int32_t position = x - 1;
+                    bool lit;
+                    if (py == 12) lit = kind == position + 1;
+                    else if (py == 13) lit = ((carried >> position) & 1) != 0;
+                    else lit = hp > position;
+                    px[3 * k] = px[3 * k + 1] = px[3 * k + 2] = lit ? 0xFF : 0x00;
+                }
+            }
+            const int32_t cy = c / g.W, cx = c - cy * g.W;
+            uint8_t* dst = img + (int64_t)(cy * 16 + py) * row_bytes + (int64_t)(cx * 16 + px0) * 3;
+            if ((((uintptr_t)dst) & 3u) == 0) {
+                uint32_t* d4 = (uint32_t*)dst;
+                d4[0] = px[0] | (px[1] << 8) | (px[2] << 16) | ((uint32_t)px[3] << 24);
+                d4[1] = px[4] | (px[5] << 8) | (px[6] << 16) | ((uint32_t)px[7] << 24);
+                d4[2] = px[8] | (px[9] << 8) | (px[10] << 16) | ((uint32_t)px[11] << 24);
+            } else {
+                for (int k = 0; k < 12; ++k) dst[k] = px[k];
+            }
+        }
+        wave_sync();
+        if (scalars && lane < 4) {
+            int32_t v;
+            if (lane == 0) v = e.sc[S_RES0 + pl];
+            else if (lane == 1) v = e.sc[S_RES0 + (pl ^ 1)];
+            else if (lane == 2) v = e.sc[S_TIME];
+            else v = e.sc[S_ALT];
+            scalars[(l * 2 + pl) * 4 + lane] = v;
+        }
+    }
+}
+
+// wave64 semantics probe: ballot, mbcnt prefix counts, shuffles, prefix-min.
+__global__ void k_probe(int32_t* out) {
+    const int lane = lane_id();
+    const uint64_t m = ballot((lane % 3) == 0);
+    const int32_t below = count_below(m);
+    const int32_t up = __shfl_up(lane, 1u, kWave);
+    const int32_t mn = wave_inclusive_min(100 - lane, lane);
+    const bool ok = popc(m) == 22 && below == (lane + 2) / 3 && (lane == 0 || up == lane - 1) && mn == 100 - lane;
+    const uint64_t all = ballot(ok);
+    if (lane == 0) out[0] = all == ~0ull ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
+
+const char* nanorts_targets(void) {
+    return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
+           "nanorts_observe,nanorts_pixels,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
+           "nanorts_rollout";
+}
+
+const char* nanorts_last_error(void) { return g_error.c_str(); }
+
+const char* nanorts_self_check(const int32_t* devices, int64_t n) {
+    static thread_local std::string result;
+    result.clear();
+    int current = 0;
+    (void)hipGetDevice(&current);
+    for (int64_t i = 0; i < n; ++i) {
+        if (hipSetDevice(devices[i]) != hipSuccess) {
+            result = "cannot select device " + std::to_string(devices[i]);
+            break;
+        }
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, devices[i]) != hipSuccess || prop.warpSize != 64) {
+            result = "device " + std::to_string(devices[i]) + " does not run 64-wide wavefronts";
+            break;
+        }
+        int32_t* d = nullptr;
+        if (hipMalloc(&d, sizeof(int32_t)) != hipSuccess) {
+            result = "probe allocation failed";
+            break;
+        }
+        int32_t h = 0;
+        hipLaunchKernelGGL(k_probe, dim3(1), dim3(64), 0, nullptr, d);
+        const bool copied = hipMemcpy(&h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+        (void)hipFree(d);
+        if (!copied || h != 1) {
+            result = "wave64 probe failed on device " + std::to_string(devices[i]);
+            break;
+        }
+    }
+    (void)hipSetDevice(current);
+    return result.c_str();
+}
+
+#define NR_SHAPE(game)                                                   \
+    Shape sh;                                                            \
+    {                                                                    \
+        std::string why;                                                 \
+        if (!shape_for(game, &sh, &why)) return fail(NANORTS_INVALID_ARGUMENT, why); \
+    }
+
+#define NR_STATE(state)                                                                      \
+    if (!state_complete(state)) return fail(NANORTS_INVALID_ARGUMENT, "a State leaf pointer is NULL");
+
+int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
+                 int64_t key_lanes, nanorts_commands commands, nanorts_step_results results) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!key || (key_lanes != 1 && key_lanes != lanes))
+        return fail(NANORTS_INVALID_ARGUMENT, "key must be [1][2] or [lanes][2]");
+    if (!commands.kind || !commands.direction || !commands.none_duration || !commands.target_cell ||
+        !commands.produced_type || !commands.request_order)
+        return fail(NANORTS_INVALID_ARGUMENT, "a Commands field pointer is NULL");
+    return launch(k_step, sh, lanes, (hipStream_t)stream, state, key, key_lanes, commands, results);
+}
+
+int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!rows) return fail(NANORTS_INVALID_ARGUMENT, "rows is NULL");
+    return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, rows, (uint32_t*)nullptr);
+}
+
+int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           uint32_t* words) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!words) return fail(NANORTS_INVALID_ARGUMENT, "words is NULL");
+    return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, (uint8_t*)nullptr, words);
+}
+
+int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows,
+                          uint32_t* words) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!rows && !words) return fail(NANORTS_INVALID_ARGUMENT, "rows and words are both NULL");
+    return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 1, rows, words);
+}
+
+int nanorts_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t observer,
+                          uint8_t* cells) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (observer < 0 || observer > 1) return fail(NANORTS_INVALID_ARGUMENT, "observer must be 0 or 1");
+    if (!cells) return fail(NANORTS_INVALID_ARGUMENT, "cells is NULL");
+    return launch(k_visible, sh, lanes, (hipStream_t)stream, state, observer, cells);
+}
+
+int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+                    uint8_t* feature_maps, int32_t* scalars) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!feature_maps && !scalars) return fail(NANORTS_INVALID_ARGUMENT, "no output requested");
+    return launch(k_observe, sh, lanes, (hipStream_t)stream, state, partial, feature_maps, scalars);
+}
+
+int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+                   const uint8_t* tiles, uint8_t* image, int32_t* scalars) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!tiles || !image) return fail(NANORTS_INVALID_ARGUMENT, "tiles and image are required");
+    return launch(k_pixels, sh, lanes, (hipStream_t)stream, state, partial, tiles, image, scalars);
+}
+
+int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                             const uint8_t* done) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!done) return fail(NANORTS_INVALID_ARGUMENT, "done is NULL");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    return launch(k_reset, sh, lanes, (hipStream_t)stream, state, done);
+}
+
+int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const int32_t* actions,
+                     int32_t partial, nanorts_env_results results) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "env.step needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results);
+}
+
+int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
+                           const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
+    NR_SHAPE(game)
+    if (!avail_words || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
+    return launch(k_sample, sh, lanes, (hipStream_t)stream, avail_words, sample_key[0], sample_key[1], step, env0,
+                  actions);
+}
+
+int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                    const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
+                    nanorts_rollout_results results) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!sample_key) return fail(NANORTS_INVALID_ARGUMENT, "sample_key is NULL");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "a rollout needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    if (steps < 0) return fail(NANORTS_INVALID_ARGUMENT, "steps must be >= 0");
+    if ((results.feature_maps || results.scalars) && results.depth < 1)
+        return fail(NANORTS_INVALID_ARGUMENT, "depth must be >= 1");
+    return launch(k_rollout, sh, lanes, (hipStream_t)stream, state, sample_key[0], sample_key[1], step0, steps, partial,
+                  env0, results);
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+"""ctypes binding of the C ABI in include/nanorts_amd.h.
+
+This is the Python side of the drop-in boundary: the same entry points an XLA
+FFI handler would wrap.  Loading fails loudly when the library is missing;
+there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from nanorts_amd import build as _build
+
+MAX_TYPES = 8
+
+_VP = ctypes.c_void_p
+_I32x8 = ctypes.c_int32 * MAX_TYPES
+
+STATE_FIELDS = (
+    "birth", "unit_type", "owner", "cell", "hit_points", "carried_resources", "pending_kind",
+    "pending_direction", "pending_none_duration", "pending_target_cell", "pending_produced_type",
+    "pending_issued_at", "pending_completes_at", "pending_order", "entity_at", "time", "player_resources",
+    "next_birth", "next_pending_order", "alternating_conflict_count", "game_over", "winner", "spawn_overflow",
+    "environment_root", "episode_index",
+)
+
+
+class State(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in STATE_FIELDS]
+
+
+class Game(ctypes.Structure):
+    _fields_ = [
+        ("height", ctypes.c_int32), ("width", ctypes.c_int32), ("cells", ctypes.c_int32),
+        ("neutral", ctypes.c_int32), ("capacity", ctypes.c_int32), ("entities", ctypes.c_int32),
+        ("types", ctypes.c_int32), ("offsets", ctypes.c_int32), ("strategy", ctypes.c_int32),
+        ("max_cycles", ctypes.c_int32),
+        ("cost", _I32x8), ("hit_points", _I32x8), ("produce_time", _I32x8), ("move_time", _I32x8),
+        ("attack_time", _I32x8), ("harvest_time", _I32x8), ("attack_range", _I32x8), ("attack_damage", _I32x8),
+        ("harvest_amount", _I32x8), ("sight_radius", _I32x8), ("is_resource", _I32x8), ("is_stockpile", _I32x8),
+        ("can_harvest", _I32x8), ("can_move", _I32x8), ("can_attack", _I32x8),
+        ("produces", ctypes.c_int32 * (MAX_TYPES * MAX_TYPES)),
+        ("terrain", _VP),
+        ("initial", State),
+    ]
+
+
+class Commands(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in
+                ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")]
+
+
+class StepResults(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in
+                ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
+                 "admitted_attack")]
+
+
+class EnvResults(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in
+                ("reward", "done", "terminated", "truncated", "winner", "spawn_overflowed", "feature_maps", "scalars",
+                 "final_feature_maps", "final_scalars", "reward_components")]
+
+
+class RolloutResults(ctypes.Structure):
+    _fields_ = [("rewards", _VP), ("dones", _VP), ("actions", _VP), ("feature_maps", _VP), ("scalars", _VP),
+                ("depth", ctypes.c_int32)]
+
+
+# Every extern "C" symbol include/nanorts_amd.h declares.
+EXPORTS = (
+    "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_self_check", "nanorts_step",
+    "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
+    "nanorts_observe", "nanorts_pixels", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
+    "nanorts_rollout",
+)
+
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_GP = ctypes.POINTER(Game)
+
+_SIGNATURES = {
+    "nanorts_build_id": (ctypes.c_char_p, []),
+    "nanorts_targets": (ctypes.c_char_p, []),
+    "nanorts_last_error": (ctypes.c_char_p, []),
+    "nanorts_self_check": (ctypes.c_char_p, [_VP, _I64]),
+    "nanorts_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I64, Commands, StepResults]),
+    "nanorts_legality": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_legality_words": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_avail_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _VP]),
+    "nanorts_visible_cells": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP]),
+    "nanorts_observe": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP]),
+    "nanorts_pixels": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP, _VP]),
+    "nanorts_reset_where_done": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
+    "nanorts_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
+    "nanorts_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
+}
+
+_LIBRARY: ctypes.CDLL | None = None
+
+
+class NativeError(RuntimeError):
+    """An entry point of the kernel library returned an error code."""
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load the in-tree kernel library, building it only when none is built."""
+    global _LIBRARY
+    if _LIBRARY is not None and path is None:
+        return _LIBRARY
+    target = Path(path) if path is not None else _build.library_path()
+    if not target.exists():
+        if path is not None:
+            raise RuntimeError(f"no kernel library at {target}")
+        _build.build()
+    lib = ctypes.CDLL(str(target))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path is None:
+        _LIBRARY = lib
+    return lib
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        message = load().nanorts_last_error().decode()
+        raise NativeError(f"{what} failed with code {code}: {message}")
