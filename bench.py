@@ -1,0 +1,300 @@
+"""Throughput of the NanoRTS hot path on one MI355X.
+
+Workload: basesWorkers16x16, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM,
+partial observability, 65536 games, seeded uniform-random legal actions for
+both players, auto-reset on done.  One step is one env.step cycle of every
+game: legality masks -> sampled actions -> decode -> core.step -> auto-reset
+-> symbolic observations of both agents written to HBM.  The timed loop runs
+the fused rollout kernel (state resident in LDS for `--chunk` cycles per
+launch); the per-call path (masks, sampler and env.step as three launches per
+cycle) is timed beside it and reported in `config`.
+
+Prints one JSON line (rank 0, N=1).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+MAP = "basesWorkers16x16"
+NUM_ENVS = 65536
+METRIC = "env-steps/sec (both players) at 16x16 × 65536 envs; % HBM roofline"
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--envs", type=int, default=NUM_ENVS)
+    ap.add_argument("--chunk", type=int, default=100, help="cycles per fused launch")
+    ap.add_argument("--depth", type=int, default=2, help="observation ring depth in HBM")
+    ap.add_argument("--per-call-steps", type=int, default=20)
+    ap.add_argument("--cpu-envs", type=int, default=2048)
+    ap.add_argument("--cpu-steps", type=int, default=400)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
+    ap.add_argument("--profile-child", choices=("rollout", "copy"), default=None, help=argparse.SUPPRESS)
+    return ap.parse_args()
+
+
+def state_bytes(bucket) -> int:
+    from nanorts_amd.model import STATE_LEAVES, leaf_shape
+
+    total = 0
+    for leaf in STATE_LEAVES:
+        n = 1
+        for d in leaf_shape(leaf, bucket):
+            n *= d
+        total += n * leaf.dtype.itemsize
+    return total + 8 + 4  # environment_root + episode_index
+
+
+def step_bytes(bucket) -> int:
+    """Algorithmic HBM bytes written per env-step by the fused rollout:
+    both agents' feature maps and scalars, rewards and the done flag."""
+    return 2 * bucket.cell_count * 6 + 2 * 4 * 4 + 2 * 4 + 1
+
+
+def make_env(envs: int):
+    import nanorts_amd
+    from nanorts_amd import env as envmod
+
+    game = nanorts_amd.map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM", max_cycles=5000)
+    env = nanorts_amd.make("NanoRTS", scenario=game, partial_observability=True, final_observation=False)
+    _, state = env.reset(envmod.env_roots(0, envs))
+    return game, env, state
+
+
+def run_rollout(env, state, steps: int, chunk: int, depth: int, step0: int, events=None):
+    """Run `steps` cycles in launches of `chunk`; returns per-launch ms when
+    `events` is requested."""
+    import torch
+
+    done = 0
+    times = []
+    while done < steps:
+        n = min(chunk, steps - done)
+        if events:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+        env.rollout(state, n, (11, 13), step0=step0 + done, record=True, observation_depth=depth)
+        if events:
+            b.record()
+            times.append((a, b, n))
+        done += n
+    return times
+
+
+def copy_bandwidth() -> float:
+    import torch
+
+    n = 1 << 28  # 1 GiB of int32
+    src = torch.empty(n, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    reps = 10
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    return 2 * n * 4 * reps / (a.elapsed_time(b) / 1e3) / 1e9
+
+
+def cpu_baseline(envs: int, steps: int) -> dict:
+    """The oracle (plain-C restatement of the reference step, masks and
+    encoders) timed on the host cores over a bounded sample."""
+    from nanorts_amd import env as envmod
+    from nanorts_amd.content import map_name_to_scenario
+    from oracle.oracle import Oracle, batch_initial
+
+    game = map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM", max_cycles=5000)
+    oracle = Oracle(game)
+    state = batch_initial(game, envs, envmod.env_roots(0, envs))
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    used = oracle.rollout(state, (11, 13), 0, steps, True, threads=threads, record=False)["threads"]
+    dt = time.perf_counter() - t0
+    return {"value": round(envs * steps / dt, 1), "unit": "env-steps/s", "cores": int(used), "kind": "port",
+            "sample": f"{envs} games x {steps} cycles of the same workload (oracle rollout: masks, sampler, "
+                      f"env.step, auto-reset, partial-observability symbolic obs) on {used} host threads, "
+                      f"{dt:.1f} s"}
+
+
+def child(args) -> None:
+    """Short runs under rocprofv3 --pmc (traffic counters)."""
+    import torch
+
+    if args.profile_child == "copy":
+        n = 1 << 26  # 256 MiB
+        src = torch.ones(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
+    game, env, state = make_env(args.envs)
+    run_rollout(env, state, 4 * args.chunk, args.chunk, args.depth, 0)
+    torch.cuda.synchronize()
+
+
+def pmc_traffic(args, per_launch_steps: int) -> dict | None:
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the rollout kernel,
+    each scaled by what the counter reads for a plain copy of known size."""
+    import csv
+    import shutil
+    import tempfile
+
+    rocprof = shutil.which("rocprofv3")
+    if rocprof is None or args.traffic == "off":
+        return None
+    env = dict(os.environ)
+
+    def counters(mode: str, counter: str) -> list[float]:
+        out = Path(tempfile.mkdtemp(prefix="nr_pmc_", dir=os.environ.get("TMPDIR", "/tmp")))
+        cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", str(out), "-o", "pmc",
+               "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--profile-child", mode,
+               "--envs", str(args.envs), "--chunk", str(args.chunk), "--depth", str(args.depth)]
+        subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=180)
+        values = []
+        for path in out.rglob("*counter_collection.csv"):
+            with open(path) as fh:
+                for row in csv.DictReader(fh):
+                    name = row.get("Kernel_Name", "")
+                    want = "k_rollout" in name if mode == "rollout" else ("copy" in name.lower() or "elementwise" in name.lower())
+                    if want and row.get("Counter_Name") == counter:
+                        values.append(float(row["Counter_Value"]))
+        shutil.rmtree(out, ignore_errors=True)
+        return values
+
+    try:
+        copy_bytes = 2 * (1 << 26) * 4  # read + write of the 256 MiB copy
+        fetch_copy = counters("copy", "FETCH_SIZE")
+        write_copy = counters("copy", "WRITE_SIZE")
+        fetch = counters("rollout", "FETCH_SIZE")
+        write = counters("rollout", "WRITE_SIZE")
+        if not (fetch_copy and write_copy and fetch and write):
+            return None
+        # a copy of B bytes fetches B/2 and writes B/2
+        f_scale = (copy_bytes / 2) / (sorted(fetch_copy)[len(fetch_copy) // 2] * 1024)
+        w_scale = (copy_bytes / 2) / (sorted(write_copy)[len(write_copy) // 2] * 1024)
+        f = sorted(fetch)[len(fetch) // 2] * 1024 * f_scale
+        w = sorted(write)[len(write) // 2] * 1024 * w_scale
+        return {"fetch_bytes": f, "write_bytes": w, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+    except Exception:
+        return None
+
+
+def main() -> None:
+    args = parse()
+    if args.profile_child:
+        child(args)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the env path shards by env with no exchange, and this run has no "
+              f"multi-GPU configuration (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    torch.cuda.set_device(0)
+    game, env, state = make_env(args.envs)
+    L = args.envs
+    chunk = max(1, min(args.chunk, args.steps))
+    # warmup
+    run_rollout(env, state, args.warmup, chunk, args.depth, 0)
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` cycles
+    t0 = time.perf_counter()
+    times = run_rollout(env, state, args.steps, chunk, args.depth, args.warmup, events=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [a.elapsed_time(b) for a, b, _ in times]
+    full = [ms for (a, b, n), ms in zip(times, launch_ms) if n == chunk] or launch_ms
+    avg_launch_s = sum(full) / len(full) / 1e3
+    value = L * args.steps / wall
+    ms_per_step = wall * 1e3 / args.steps
+
+    b = game.bucket
+    sbytes = state_bytes(b)
+    per_step = step_bytes(b)
+    per_launch_bytes = L * (chunk * per_step + 2 * sbytes)
+    achieved = per_launch_bytes / avg_launch_s / 1e9
+
+    # per-call path: masks (words) -> sampler -> env.step, 3 launches per cycle
+    pc_rate = None
+    if args.per_call_steps > 0:
+        _, pc_state = env.reset(__import__("nanorts_amd.env", fromlist=["env_roots"]).env_roots(1, L))
+        def per_call(n, base):
+            nonlocal pc_state
+            for t in range(n):
+                words = env.get_avail_actions(pc_state, form="words")
+                acts = env.sample_actions(torch.stack([words[a] for a in env.agents], 1), (11, 13), base + t)
+                _, pc_state, _, _, _ = env.step(None, pc_state, acts, donate=True)
+        per_call(3, 0)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        per_call(args.per_call_steps, 3)
+        torch.cuda.synchronize()
+        pc_rate = L * args.per_call_steps / (time.perf_counter() - t1)
+
+    bw = copy_bandwidth()
+    traffic = pmc_traffic(args, chunk)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_envs, args.cpu_steps)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic: seeded uniform-random legal actions from the shipped basesWorkers16x16 map",
+        "config": {
+            "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, partial_observability, "
+                        f"{L} games, max_cycles 5000, auto-reset, fused rollout {chunk} cycles/launch",
+            "games": L, "slots_per_player": b.per_player_capacity, "entity_capacity": b.entity_capacity,
+            "per_call_env_steps_per_s": None if pc_rate is None else round(pc_rate, 1),
+            "copy_kernel_GBps": round(bw, 1),
+            "algorithmic_bytes_per_env_step": per_step,
+            "state_bytes_per_env": sbytes,
+            "observation_ring_depth": args.depth,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
+            "kernel": "k_rollout",
+            "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "algorithmic_bytes_per_launch": per_launch_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    if traffic is not None:
+        line["roofline"]["traffic_detail"] = traffic
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -71,10 +71,18 @@ enum : int {
     S_COUNT = 16
 };
 
+// One row leaf of the initial State: global source, LDS destination, bytes.
+struct Seg {
+    const uint8_t* src;
+    int32_t dst;
+    int32_t bytes;
+};
+
 // Byte offsets of one env block (relative to the block) and of the
 // workgroup header.  Computed on the host (see layout_for in nanorts_amd.hip).
 struct Layout {
-    int32_t hdr_bytes;  // tab + terrain
+    int32_t hdr_bytes;  // tab + reset segments + terrain
+    int32_t o_seg;
     int32_t env_bytes;  // one wave's block, 16-byte multiple
     int32_t o_terrain;  // in the header
     int32_t o_birth, o_carried, o_pnone, o_pissued, o_pcompl, o_porder;
@@ -90,6 +98,7 @@ struct Layout {
     int32_t m_rec, m_keys, m_tmp;
     int32_t v_seen, v_stage, b_units;
     int32_t v_words;
+    int32_t a_av, a_fk, a_fn, a_list;  // env-path admission: available list, final kinds/durations, entry list
 };
 
 // Kernel-side copy of the game (passed by value as a kernel argument).
@@ -100,6 +109,8 @@ struct KGame {
     const uint8_t* terrain;
     nanorts_state initial;
     Layout lay;
+    int32_t nseg;
+    Seg seg[16];
 };
 
 // ---------------------------------------------------------------------------
@@ -190,6 +201,7 @@ NR_DEV int32_t randint01(uint32_t k0, uint32_t k1) {
 struct Hdr {
     AS3 int32_t* tab;
     AS3 uint8_t* terrain;
+    AS3 Seg* seg;
 };
 
 struct Env {
@@ -235,6 +247,15 @@ NR_DEV Env env_view(const KGame& g, AS3 uint8_t* base) {
     return e;
 }
 
+// Rebuild the view from an opaque copy of the base so the per-lane
+// addresses derived from it are recomputed in each phase instead of staying
+// live (in registers) across the whole step.
+NR_DEV Env refresh(const KGame& g, const Env& e) {
+    uint32_t b = (uint32_t)(uintptr_t)e.base;
+    asm volatile("" : "+s"(b));
+    return env_view(g, (AS3 uint8_t*)(uintptr_t)b);
+}
+
 template <typename T>
 NR_DEV AS3 T* at(const Env& e, int32_t offset) {
     return (AS3 T*)(e.base + offset);
@@ -246,6 +267,14 @@ NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field 
 // __syncthreads follows in the kernel).
 NR_DEV void load_header(const KGame& g, const Hdr& h) {
     for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            h.seg[k].src = g.seg[k].src;
+            h.seg[k].dst = g.seg[k].dst;
+            h.seg[k].bytes = g.seg[k].bytes;
+        }
+    }
     for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = g.terrain[i] ? 1 : 0;
 }
 
@@ -816,18 +845,10 @@ NR_DEV void remove_slot(const Env& e, int32_t s) {
 // N/core/completion.py:134-180 (_take_turn) for the member record `r`, with
 // each kind's _complete (move.py:19-27, harvest.py:24-45, return_.py:25-43,
 // produce.py:47-81, attack.py:78-98).
-NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, AS3 const int32_t* r) {
-    const int32_t w0 = uni(r[0]), w1 = uni(r[1]), w2 = uni(r[2]);
-    const int32_t slot = w0 & 0xFFFF;
-    const int32_t kind = (int8_t)((w0 >> 16) & 0xFF);
-    const int32_t dir = (int8_t)((w0 >> 24) & 0xFF);
-    const int32_t target = (int16_t)(w1 & 0xFFFF);
-    const int32_t ptype = (int8_t)((w1 >> 16) & 0xFF);
-    const int32_t owner = (int8_t)((w1 >> 24) & 0xFF);
-    const int32_t utype = (int8_t)(w2 & 0xFF);
-    const int32_t rcell = (int16_t)((w2 >> 8) & 0xFFFF);
-    const int32_t rbirth = uni(r[3]);
-    const int32_t rcarried = uni(r[4]);
+// The member's retained values are wave-uniform arguments.
+NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t slot, int32_t kind, int32_t dir,
+                      int32_t target, int32_t ptype, int32_t owner, int32_t utype, int32_t rcell, int32_t rbirth,
+                      int32_t rcarried) {
     const int32_t actor = clampi(utype, 0, g.T - 1);
     const int32_t player = clampi(owner, 0, 1);
     const int32_t cur_birth = uni(e.birth[slot]);
@@ -919,31 +940,79 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, AS3 
 }
 
 // pending.select + completion.apply (N/core/completion.py:106-117).
-NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e, int lane) {
+NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
-    AS3 uint64_t* keys = at<uint64_t>(e, y.m_keys);
     AS3 int16_t* tmp = at<int16_t>(e, y.m_tmp);
-    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);
-    // members = due & not NONE among owned slots, keyed by pending order
+    // members = due & not NONE among owned slots (slot order here)
     int32_t n = 0;
     for (int32_t base = 0; base < 2 * g.C; base += kWave) {
         const int32_t p = base + lane;
         bool acting = false;
-        int32_t s = 0;
         if (p < 2 * g.C) {
-            s = g.N + p;
+            const int32_t s = g.N + p;
             const int32_t k = e.pkind[s];
             acting = k != kAbsent && k != kKindNone && e.pcompl[s] <= time;
         }
         const uint64_t m = ballot(acting);
-        if (acting) {
-            const int32_t at_ = n + count_below(m);
-            keys[at_] = ((uint64_t)((uint32_t)e.porder[s] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)p;
-            tmp[at_] = (int16_t)s;
-        }
+        if (acting) tmp[n + count_below(m)] = (int16_t)(g.N + p);
         n += popc(m);
+    }
+    wave_sync();
+    if (n <= kWave) {
+        // lane i holds member i's retained actor (:120-131); turns run in
+        // pending order, ties by slot
+        int32_t s = 0, ord = 0, kind = 0, dir = 0, target = 0, ptype = 0, owner = 0, utype = 0, rcell = 0, rbirth = 0,
+                rcarried = 0;
+        if (lane < n) {
+            s = tmp[lane];
+            ord = e.porder[s];
+            kind = e.pkind[s];
+            dir = e.pdir[s];
+            target = e.ptarget[s];
+            ptype = e.pptype[s];
+            owner = e.owner[s];
+            utype = e.utype[s];
+            rcell = e.cell[s];
+            rbirth = e.birth[s];
+            rcarried = e.carried[s];
+        }
+        int32_t rank = 0;
+        for (int32_t j = 0; j < n; ++j) {
+            const int32_t oj = __builtin_amdgcn_readlane(ord, j);
+            const int32_t sj = __builtin_amdgcn_readlane(s, j);
+            rank += (oj < ord) || (oj == ord && sj < s);
+        }
+        wave_sync();
+        for (int32_t sl = lane; sl < g.E; sl += kWave) {
+            if (e.pkind[sl] != kAbsent && e.pcompl[sl] <= time) {
+                e.pkind[sl] = (int8_t)kAbsent;
+                e.pdir[sl] = (int8_t)kAbsent;
+                e.pnone[sl] = 0;
+                e.ptarget[sl] = (int16_t)kAbsent;
+                e.pptype[sl] = (int8_t)kAbsent;
+                e.pissued[sl] = 0;
+                e.pcompl[sl] = 0;
+                e.porder[sl] = kAbsent;
+            }
+        }
+        wave_sync();
+        for (int32_t k = 0; k < n; ++k) {
+            const int32_t li = (int32_t)__builtin_ctzll(ballot(lane < n && rank == k));
+#define NR_RL(v) __builtin_amdgcn_readlane(v, li)
+            take_turn(g, h, e, lane, NR_RL(s), NR_RL(kind), NR_RL(dir), NR_RL(target), NR_RL(ptype), NR_RL(owner),
+                      NR_RL(utype), NR_RL(rcell), NR_RL(rbirth), NR_RL(rcarried));
+#undef NR_RL
+        }
+        return;
+    }
+    AS3 uint64_t* keys = at<uint64_t>(e, y.m_keys);
+    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);
+    for (int32_t i = lane; i < n; i += kWave) {
+        const int32_t s = tmp[i];
+        keys[i] = ((uint64_t)((uint32_t)e.porder[s] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)s;
     }
     wave_sync();
     // snapshot the retained actors in member order (:120-131)
@@ -974,11 +1043,18 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e, int lane) {
         }
     }
     wave_sync();
-    for (int32_t i = 0; i < n; ++i) take_turn(g, h, e, lane, rec + 5 * i);
+    for (int32_t i = 0; i < n; ++i) {
+        AS3 const int32_t* r = rec + 5 * i;
+        const int32_t w0 = uni(r[0]), w1 = uni(r[1]), w2 = uni(r[2]);
+        take_turn(g, h, e, lane, w0 & 0xFFFF, (int8_t)((w0 >> 16) & 0xFF), (int8_t)((w0 >> 24) & 0xFF),
+                  (int16_t)(w1 & 0xFFFF), (int8_t)((w1 >> 16) & 0xFF), (int8_t)((w1 >> 24) & 0xFF),
+                  (int8_t)(w2 & 0xFF), (int16_t)((w2 >> 8) & 0xFFFF), uni(r[3]), uni(r[4]));
+    }
 }
 
 // outcome.decide (N/core/outcome.py:11-25)
-NR_DEV void decide(const KGame& g, const Env& e, int lane) {
+NR_DEV void decide(const KGame& g, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
     bool alive[2] = {false, false};
     for (int32_t pl = 0; pl < 2; ++pl) {
         uint64_t any = 0;
@@ -1006,15 +1082,36 @@ NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint
 
 // Copy the initial State into the staged env: core.reset ignores its key
 // (N/core/__init__.py:30-32) and lifecycle.advance takes every leaf from it
-// (N/adapters/lifecycle.py:53-79).
-NR_DEV void reset_env(const KGame& g, const Env& e, int lane) {
+// (N/adapters/lifecycle.py:53-79).  The row leaves are copied through one
+// runtime-indexed loop over g.seg so no per-leaf address stays live.
+NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
     const int32_t episode = uni(e.sc[S_EPISODE]);
-    const int32_t root0 = uni(e.sc[S_ROOT0]), root1 = uni(e.sc[S_ROOT1]);
-    load_env(g, g.initial, 0, e, LD_ALL, lane);
-    if (lane == 0) {
-        e.sc[S_ROOT0] = root0;
-        e.sc[S_ROOT1] = root1;
-        e.sc[S_EPISODE] = (int32_t)((uint32_t)episode + 1u);
+#pragma nounroll
+    for (int32_t k = 0; k < g.nseg; ++k) {
+        const AS3 Seg* sg = h.seg + k;
+        const uint8_t* src = (const uint8_t*)(((uint64_t)(uint32_t)uni((int32_t)(uint32_t)(uintptr_t)sg->src)) |
+                                              ((uint64_t)(uint32_t)uni((int32_t)((uintptr_t)sg->src >> 32)) << 32));
+        copy_in(e.base + uni(sg->dst), src, uni(sg->bytes), lane);
+    }
+    if (lane < S_COUNT) {
+        const nanorts_state& s = g.initial;
+        int32_t v = e.sc[lane];
+        switch (lane) {
+            case S_TIME: v = s.time[0]; break;
+            case S_RES0: v = s.player_resources[0]; break;
+            case S_RES1: v = s.player_resources[1]; break;
+            case S_NEXT_BIRTH: v = s.next_birth[0]; break;
+            case S_NEXT_ORDER: v = s.next_pending_order[0]; break;
+            case S_ALT: v = s.alternating_conflict_count[0]; break;
+            case S_GAME_OVER: v = s.game_over[0] ? 1 : 0; break;
+            case S_WINNER: v = s.winner[0]; break;
+            case S_SO0: v = s.spawn_overflow[0]; break;
+            case S_SO1: v = s.spawn_overflow[1]; break;
+            case S_EPISODE: v = (int32_t)((uint32_t)episode + 1u); break;
+            default: break;
+        }
+        e.sc[lane] = v;
     }
     wave_sync();
     decide(g, e, lane);

@@ -11,6 +11,7 @@
 
 #include "../../include/nanorts_amd.h"
 #include "engine.h"
+#include "envstep.h"
 
 using namespace nr;
 
@@ -126,7 +127,8 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
 
     Layout& y = g.lay;
     const int32_t E = g.E, C2 = 2 * g.C, cells = g.cells;
-    y.o_terrain = F_COUNT * 8 * 4;
+    y.o_seg = F_COUNT * 8 * 4;
+    y.o_terrain = y.o_seg + 16 * (int32_t)sizeof(Seg);
     y.hdr_bytes = align16(y.o_terrain + cells);
     int32_t o = 0;
     auto take = [&o](int32_t bytes) {
@@ -164,6 +166,10 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.b_tmp = take(C2 * 2);
     y.b_order = take(C2 * 2);
     y.b_rank = take(E * 2);
+    y.a_av = take(C2 * 2);
+    y.a_fk = take(kWave * 4);
+    y.a_fn = take(kWave * 4);
+    y.a_list = take(E * 2);
     const int32_t admission_end = o;
     // completion (the commands are dead by then)
     o = union0;
@@ -173,8 +179,8 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     const int32_t completion_end = o;
     // observation
     o = union0;
-    y.v_seen = take(g.H * g.seen_words * 4);
-    y.v_stage = take(g.stage_cells * 6);
+    y.v_seen = take(2 * g.H * g.seen_words * 4);
+    y.v_stage = take(2 * g.stage_cells * 6);
     y.b_units = take(g.C * 2);
     const int32_t observe_end = o;
     // masks
@@ -186,6 +192,27 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     if (observe_end > end) end = observe_end;
     if (masks_end > end) end = masks_end;
     y.env_bytes = align16(end);
+
+    // initial State rows -> env block (reset_env)
+    const nanorts_state& init = game->initial;
+    const struct {
+        const void* src;
+        int32_t dst, bytes;
+    } rows[15] = {
+        {init.birth, y.o_birth, E * 4}, {init.unit_type, y.o_utype, E}, {init.owner, y.o_owner, E},
+        {init.cell, y.o_cell, E * 2}, {init.hit_points, y.o_hp, E * 2}, {init.carried_resources, y.o_carried, E * 4},
+        {init.pending_kind, y.o_pkind, E}, {init.pending_direction, y.o_pdir, E},
+        {init.pending_none_duration, y.o_pnone, E * 4}, {init.pending_target_cell, y.o_ptarget, E * 2},
+        {init.pending_produced_type, y.o_pptype, E}, {init.pending_issued_at, y.o_pissued, E * 4},
+        {init.pending_completes_at, y.o_pcompl, E * 4}, {init.pending_order, y.o_porder, E * 4},
+        {init.entity_at, y.o_entity, cells * 2},
+    };
+    g.nseg = 15;
+    for (int k = 0; k < 15; ++k) {
+        g.seg[k].src = (const uint8_t*)rows[k].src;
+        g.seg[k].dst = rows[k].dst;
+        g.seg[k].bytes = rows[k].bytes;
+    }
 
     int max_lds = 65536;
     int device = 0;
@@ -237,10 +264,11 @@ bool state_complete(const nanorts_state& s) {
     Hdr hdr;                                                                      \
     hdr.tab = (AS3 int32_t*)lds;                                                  \
     hdr.terrain = lds + g.lay.o_terrain;                                          \
+    hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);                                      \
     load_header(g, hdr);                                                          \
     __syncthreads();                                                              \
     const int lane = lane_id();                                                   \
-    const int wave = (int)(threadIdx.x >> 6);                                     \
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));     \
     const int64_t l = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;             \
     if (l >= lanes) return;                                                       \
     const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
@@ -361,10 +389,9 @@ __global__ __launch_bounds__(256) void k_visible(KGame g, int64_t lanes, nanorts
 NR_DEV void observe_both(const KGame& g, const Hdr& h, const Env& e, int64_t slot, int lane, bool partial,
                          uint8_t* maps, int32_t* scalars) {
     const int64_t per = (int64_t)g.cells * 6;
-    for (int32_t p = 0; p < 2; ++p) {
-        observe_player(g, h, e, lane, p, partial, maps ? maps + (slot * 2 + p) * per : nullptr,
-                       scalars ? scalars + (slot * 2 + p) * 4 : nullptr);
-    }
+    observe_all(g, h, e, lane, partial, maps ? maps + (slot * 2) * per : nullptr,
+                maps ? maps + (slot * 2 + 1) * per : nullptr, scalars ? scalars + slot * 8 : nullptr,
+                scalars ? scalars + slot * 8 + 4 : nullptr);
 }
 
 __global__ __launch_bounds__(256) void k_observe(KGame g, int64_t lanes, nanorts_state s, int32_t partial, uint8_t* maps, int32_t* scalars) {
@@ -378,7 +405,7 @@ __global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_s
     NR_KERNEL_PROLOGUE
     if (!done[l]) return;
     load_env(g, s, l, e, LD_SCALARS, lane);
-    reset_env(g, e, lane);
+    reset_env(g, hdr, e, lane);
     store_env(g, s, l, e, lane);
 }
 
@@ -428,7 +455,7 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
         out[5] = (float)(prod[4] + prod[5] + prod[6]);
     }
     if (r.final_feature_maps || r.final_scalars) observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
-    if (done) reset_env(g, e, lane);
+    if (done) reset_env(g, h, e, lane);
     return done;
 }
 
@@ -436,11 +463,23 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
                            nanorts_env_results r) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
-    stage_actions(g, e, l, actions, lane);
+    bool irregular = false;
+    const int32_t n = compact_available(g, e, lane, &irregular);
+    const int32_t owned = 2 * g.C;
+    AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
+    for (int32_t i = lane; i < n; i += kWave) {
+        const int32_t p = av[i];
+        const int32_t* row = actions + (l * owned + p) * 7;
+        int32_t a[7];
+#pragma unroll
+        for (int f = 0; f < 7; ++f) a[f] = row[f];
+        decode_row(g, e, p, true, a);
+    }
+    wave_sync();
     uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
     const bool events = r.reward_components != nullptr;
-    core_step(g, hdr, e, lane, k0, k1, events);
+    env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular);
     finish_step(g, hdr, e, l, lane, partial != 0, r, events);
     store_env(g, s, l, e, lane);
     if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
@@ -475,36 +514,47 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
     load_env(g, s, l, e, LD_ALL, lane);
     const int32_t owned = 2 * g.C;
     const nanorts_env_results none = {};
+    const Env e0 = e;
     for (int32_t t = 0; t < steps; ++t) {
+        const Env e = refresh(g, e0);
         const int32_t step = step0 + t;
         // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
+        bool irregular = false;
+        const int32_t n = compact_available(g, e, lane, &irregular);
         uint32_t ke0 = key0, ke1 = key1;
         fold_in(ke0, ke1, (uint32_t)step);
         fold_in(ke0, ke1, (uint32_t)(env0 + l));
-        for (int32_t p = lane; p < owned; p += kWave) {
-            const int32_t sl = g.N + p;
-            const bool available = e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent;
-            int32_t a[7] = {0, 0, 0, 0, 0, 0, 0};
-            if (available) {
-                const Row r = legality_row(g, hdr, e, sl);
-                sample_row(g, r, ke0, ke1, p, a);
-            }
+        AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
+        for (int32_t i = lane; i < n; i += kWave) {
+            const int32_t p = av[i];
+            const Row r = legality_row(g, hdr, e, g.N + p);
+            int32_t a[7];
+            sample_row(g, r, ke0, ke1, p, a);
             if (out.actions) {
                 int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
 #pragma unroll
                 for (int f = 0; f < 7; ++f) dst[f] = a[f];
             }
-            decode_row(g, e, p, available, a);
+            decode_row(g, e, p, true, a);
+        }
+        if (out.actions) {
+            // unavailable rows sample all zeros
+            for (int32_t p = lane; p < owned; p += kWave) {
+                const int32_t sl = g.N + p;
+                if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
+                int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+#pragma unroll
+                for (int f = 0; f < 7; ++f) dst[f] = 0;
+            }
         }
         wave_sync();
         // env.step
         uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
         fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
-        core_step(g, hdr, e, lane, k0, k1, false);
+        env_core_step(g, hdr, e, lane, k0, k1, false, n, irregular);
         nanorts_env_results r = none;
         if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
         if (out.dones) r.done = out.dones + (int64_t)t * lanes;
-        // finish_step indexes outputs by l; shift the per-step bases
         finish_step(g, hdr, e, l, lane, partial != 0, r, false);
         if (out.feature_maps || out.scalars) {
             const int64_t ring = out.depth > 0 ? (int64_t)(t % out.depth) : 0;
