@@ -68,7 +68,11 @@ enum : int {
     S_ROOT0,
     S_ROOT1,
     S_EPISODE,
-    S_COUNT = 16
+    S_UNITS0,  // active units of player 0 / 1, kept by the env path for decide
+    S_UNITS1,
+    S_NAV,    // available units listed by summarize
+    S_IRREG,  // 1 when an available unit holds a pending order
+    S_COUNT = 20
 };
 
 // One row leaf of the initial State: global source, LDS destination, bytes.
@@ -90,6 +94,8 @@ struct Layout {
     int32_t o_utype, o_owner, o_pkind, o_pdir, o_pptype;
     int32_t o_scal;
     int32_t b_events;  // admitted counts, outside the phase union
+    int32_t o_bm;      // occupancy bitmaps (6 planes), outside the union
+    int32_t o_word;    // occupant word per slot, outside the union
     // Phase union.  Admission: commands, keys, lists.  Completion: member
     // records, keys.  Observation: seen bitmap, staging, unit list.  Masks:
     // staged words.
@@ -911,6 +917,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
                     e.cell[newborn] = (int16_t)dest;
                     e.hp[newborn] = (int16_t)tabv(h, F_HP, newborn_type);
                     e.sc[S_NEXT_BIRTH] = wadd(birth, 1);
+                    e.sc[S_UNITS0 + player] += 1;
                 } else {
                     e.sc[S_SO0 + player] = wadd(e.sc[S_SO0 + player], 1);
                 }
@@ -933,122 +940,112 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
         if (lane == 0) {
             const int32_t c = e.cell[gidx(removed, g.E)];
             if (c >= 0 && c < g.cells) e.entity[c] = (int16_t)kAbsent;
+            if (removed >= g.N && removed < g.E && e.birth[removed] != kAbsent) {
+                const int32_t owner_block = (removed - g.N) / g.C;
+                e.sc[S_UNITS0 + owner_block] -= 1;
+            }
             remove_slot(e, removed);
         }
     }
     wave_sync();
 }
 
-// pending.select + completion.apply (N/core/completion.py:106-117).
+// pending.select + completion.apply (N/core/completion.py:106-117).  One
+// pass over the slots records each acting member's retained actor (the
+// pre-clear snapshot, :120-131) and clears every due pending action.
 NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
-    AS3 int16_t* tmp = at<int16_t>(e, y.m_tmp);
-    // members = due & not NONE among owned slots (slot order here)
+    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][5] in slot order
     int32_t n = 0;
-    for (int32_t base = 0; base < 2 * g.C; base += kWave) {
-        const int32_t p = base + lane;
+    for (int32_t base = 0; base < g.E; base += kWave) {
+        const int32_t s = base + lane;
         bool acting = false;
-        if (p < 2 * g.C) {
-            const int32_t s = g.N + p;
+        int32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0, r4 = 0;
+        if (s < g.E) {
             const int32_t k = e.pkind[s];
-            acting = k != kAbsent && k != kKindNone && e.pcompl[s] <= time;
+            const bool due = k != kAbsent && e.pcompl[s] <= time;
+            if (due) {
+                acting = k != kKindNone && s >= g.N;
+                if (acting) {
+                    r0 = (s & 0xFFFF) | ((k & 0xFF) << 16) | ((e.pdir[s] & 0xFF) << 24);
+                    r1 = (e.ptarget[s] & 0xFFFF) | ((e.pptype[s] & 0xFF) << 16) | ((e.owner[s] & 0xFF) << 24);
+                    r2 = (e.utype[s] & 0xFF) | ((e.cell[s] & 0xFFFF) << 8);
+                    r3 = e.birth[s];
+                    r4 = e.porder[s];
+                }
+                e.pkind[s] = (int8_t)kAbsent;
+                e.pdir[s] = (int8_t)kAbsent;
+                e.pnone[s] = 0;
+                e.ptarget[s] = (int16_t)kAbsent;
+                e.pptype[s] = (int8_t)kAbsent;
+                e.pissued[s] = 0;
+                e.pcompl[s] = 0;
+                e.porder[s] = kAbsent;
+            }
         }
         const uint64_t m = ballot(acting);
-        if (acting) tmp[n + count_below(m)] = (int16_t)(g.N + p);
+        if (acting) {
+            AS3 int32_t* r = rec + 6 * (n + count_below(m));
+            r[0] = r0;
+            r[1] = r1;
+            r[2] = r2;
+            r[3] = r3;
+            r[4] = e.carried[s];
+            r[5] = r4;
+        }
         n += popc(m);
     }
     wave_sync();
     if (n <= kWave) {
-        // lane i holds member i's retained actor (:120-131); turns run in
-        // pending order, ties by slot
-        int32_t s = 0, ord = 0, kind = 0, dir = 0, target = 0, ptype = 0, owner = 0, utype = 0, rcell = 0, rbirth = 0,
-                rcarried = 0;
+        int32_t w0 = 0, w1 = 0, w2 = 0, rb = 0, rc = 0, ord = 0;
         if (lane < n) {
-            s = tmp[lane];
-            ord = e.porder[s];
-            kind = e.pkind[s];
-            dir = e.pdir[s];
-            target = e.ptarget[s];
-            ptype = e.pptype[s];
-            owner = e.owner[s];
-            utype = e.utype[s];
-            rcell = e.cell[s];
-            rbirth = e.birth[s];
-            rcarried = e.carried[s];
+            AS3 const int32_t* r = rec + 6 * lane;
+            w0 = r[0];
+            w1 = r[1];
+            w2 = r[2];
+            rb = r[3];
+            rc = r[4];
+            ord = r[5];
         }
+        // members act in pending order (pending.batch_order :55-60), ties by slot
         int32_t rank = 0;
         for (int32_t j = 0; j < n; ++j) {
             const int32_t oj = __builtin_amdgcn_readlane(ord, j);
-            const int32_t sj = __builtin_amdgcn_readlane(s, j);
-            rank += (oj < ord) || (oj == ord && sj < s);
+            rank += (oj < ord) || (oj == ord && j < lane);
         }
-        wave_sync();
-        for (int32_t sl = lane; sl < g.E; sl += kWave) {
-            if (e.pkind[sl] != kAbsent && e.pcompl[sl] <= time) {
-                e.pkind[sl] = (int8_t)kAbsent;
-                e.pdir[sl] = (int8_t)kAbsent;
-                e.pnone[sl] = 0;
-                e.ptarget[sl] = (int16_t)kAbsent;
-                e.pptype[sl] = (int8_t)kAbsent;
-                e.pissued[sl] = 0;
-                e.pcompl[sl] = 0;
-                e.porder[sl] = kAbsent;
-            }
-        }
-        wave_sync();
         for (int32_t k = 0; k < n; ++k) {
             const int32_t li = (int32_t)__builtin_ctzll(ballot(lane < n && rank == k));
-#define NR_RL(v) __builtin_amdgcn_readlane(v, li)
-            take_turn(g, h, e, lane, NR_RL(s), NR_RL(kind), NR_RL(dir), NR_RL(target), NR_RL(ptype), NR_RL(owner),
-                      NR_RL(utype), NR_RL(rcell), NR_RL(rbirth), NR_RL(rcarried));
-#undef NR_RL
+            const int32_t a = __builtin_amdgcn_readlane(w0, li), b = __builtin_amdgcn_readlane(w1, li),
+                          c = __builtin_amdgcn_readlane(w2, li);
+            take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
+                      (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
+                      (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
+                      __builtin_amdgcn_readlane(rc, li));
         }
         return;
     }
+    // more members than lanes: order through LDS keys
     AS3 uint64_t* keys = at<uint64_t>(e, y.m_keys);
-    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);
-    for (int32_t i = lane; i < n; i += kWave) {
-        const int32_t s = tmp[i];
-        keys[i] = ((uint64_t)((uint32_t)e.porder[s] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)s;
-    }
+    AS3 int16_t* pos = at<int16_t>(e, y.m_tmp);
+    for (int32_t i = lane; i < n; i += kWave)
+        keys[i] = ((uint64_t)((uint32_t)rec[6 * i + 5] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)i;
     wave_sync();
-    // snapshot the retained actors in member order (:120-131)
     for (int32_t i = lane; i < n; i += kWave) {
         const uint64_t ki = keys[i];
-        int32_t pos = 0;
-        for (int32_t j = 0; j < n; ++j) pos += keys[j] < ki;
-        const int32_t s = tmp[i];
-        AS3 int32_t* r = rec + 5 * pos;
-        r[0] = (s & 0xFFFF) | ((e.pkind[s] & 0xFF) << 16) | ((e.pdir[s] & 0xFF) << 24);
-        r[1] = (e.ptarget[s] & 0xFFFF) | ((e.pptype[s] & 0xFF) << 16) | ((e.owner[s] & 0xFF) << 24);
-        r[2] = (e.utype[s] & 0xFF) | ((e.cell[s] & 0xFFFF) << 8);
-        r[3] = e.birth[s];
-        r[4] = e.carried[s];
+        int32_t r = 0;
+        for (int32_t j = 0; j < n; ++j) r += keys[j] < ki;
+        pos[r] = (int16_t)i;
     }
     wave_sync();
-    // clear every due pending action (pending.clear)
-    for (int32_t s = lane; s < g.E; s += kWave) {
-        if (e.pkind[s] != kAbsent && e.pcompl[s] <= time) {
-            e.pkind[s] = (int8_t)kAbsent;
-            e.pdir[s] = (int8_t)kAbsent;
-            e.pnone[s] = 0;
-            e.ptarget[s] = (int16_t)kAbsent;
-            e.pptype[s] = (int8_t)kAbsent;
-            e.pissued[s] = 0;
-            e.pcompl[s] = 0;
-            e.porder[s] = kAbsent;
-        }
-    }
-    wave_sync();
-    for (int32_t i = 0; i < n; ++i) {
-        AS3 const int32_t* r = rec + 5 * i;
-        const int32_t w0 = uni(r[0]), w1 = uni(r[1]), w2 = uni(r[2]);
-        take_turn(g, h, e, lane, w0 & 0xFFFF, (int8_t)((w0 >> 16) & 0xFF), (int8_t)((w0 >> 24) & 0xFF),
-                  (int16_t)(w1 & 0xFFFF), (int8_t)((w1 >> 16) & 0xFF), (int8_t)((w1 >> 24) & 0xFF),
-                  (int8_t)(w2 & 0xFF), (int16_t)((w2 >> 8) & 0xFFFF), uni(r[3]), uni(r[4]));
+    for (int32_t k = 0; k < n; ++k) {
+        AS3 const int32_t* r = rec + 6 * uni(pos[k]);
+        const int32_t a = uni(r[0]), b = uni(r[1]), c = uni(r[2]);
+        take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
+                  (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
+                  (int16_t)((c >> 8) & 0xFFFF), uni(r[3]), uni(r[4]));
     }
 }
 
@@ -1068,6 +1065,34 @@ NR_DEV void decide(const KGame& g, const Env& e_in, int lane) {
     if (lane == 0) {
         e.sc[S_GAME_OVER] = count <= 1 ? 1 : 0;
         e.sc[S_WINNER] = count == 1 ? (alive[0] ? 0 : 1) : kAbsent;
+    }
+    wave_sync();
+}
+
+// Active units per player, for decide_counted.
+NR_DEV void count_units(const KGame& g, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    int32_t count[2] = {0, 0};
+    for (int32_t pl = 0; pl < 2; ++pl) {
+        for (int32_t base = 0; base < g.C; base += kWave) {
+            const int32_t i = base + lane;
+            count[pl] += popc(ballot(i < g.C && e.birth[g.N + pl * g.C + i] != kAbsent));
+        }
+    }
+    if (lane == 0) {
+        e.sc[S_UNITS0] = count[0];
+        e.sc[S_UNITS1] = count[1];
+    }
+    wave_sync();
+}
+
+// outcome.decide from the kept unit counts.
+NR_DEV void decide_counted(const Env& e, int lane) {
+    const bool a0 = uni(e.sc[S_UNITS0]) > 0, a1 = uni(e.sc[S_UNITS1]) > 0;
+    const int32_t count = (a0 ? 1 : 0) + (a1 ? 1 : 0);
+    if (lane == 0) {
+        e.sc[S_GAME_OVER] = count <= 1 ? 1 : 0;
+        e.sc[S_WINNER] = count == 1 ? (a0 ? 0 : 1) : kAbsent;
     }
     wave_sync();
 }
@@ -1114,7 +1139,8 @@ NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
         e.sc[lane] = v;
     }
     wave_sync();
-    decide(g, e, lane);
+    count_units(g, e, lane);
+    decide_counted(e, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1217,7 +1243,7 @@ NR_DEV Row legality_row(const KGame& g, const Hdr& h, const Env& e, int32_t slot
 //   k_env = fold_in(fold_in(sample_key, step), env);
 //   (w0, w1) = threefry(k_env, (p, 0)), (w2, w3) = threefry(k_env, (p, 1));
 //   factor f draws the 16-bit half f of w0..w3 (low half first) and takes the
-//   (h mod popcount)-th set bit of its mask, or 0 when the mask is empty.
+//   ((h * popcount) >> 16)-th set bit of its mask, or 0 when the mask is empty.
 // A row whose only set bit is NONE samples all zeros.
 // ---------------------------------------------------------------------------
 NR_DEV uint64_t row_bits(const Row& r, int32_t lo, int32_t width) {
@@ -1254,7 +1280,7 @@ NR_DEV void sample_row(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1,
         const uint32_t hh = (words[f >> 1] >> (16 * (f & 1))) & 0xFFFFu;
         const uint64_t m = row_bits(r, lo[f], wid[f]);
         const int32_t count = popc(m);
-        a[f] = count > 0 ? select_set_bit(m, (int32_t)(hh % (uint32_t)count)) : 0;
+        a[f] = count > 0 ? select_set_bit(m, (int32_t)((hh * (uint32_t)count) >> 16)) : 0;
     }
 }
 

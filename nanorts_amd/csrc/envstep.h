@@ -50,7 +50,7 @@ NR_DEV int32_t compact_available(const KGame& g, const Env& e_in, int lane, bool
 // Admission over the n available units listed by compact_available, whose
 // canonical commands are staged in the command arrays.
 NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, uint32_t key0, uint32_t key1,
-                      bool count_events, int32_t n, bool irregular) {
+                      bool count_events, int32_t n, bool irregular, bool known_legal) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     if (irregular || n > kWave) return false;
@@ -111,10 +111,14 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
         const int32_t owner = e.owner[slot];
         birth = e.birth[slot];
         req = action_duration(g, h, e.utype[slot], kind0, none0, ptype);
-        const bool legal = can_execute(g, h, e, slot, kind0, dir, target, ptype);
+        // A command sampled from this cycle's masks is legal and unblocked:
+        // every mask factor is legal for some value of the others, and the
+        // produce factors are independent (free direction and affordable
+        // type), so the sampled combination passes is_valid.
+        const bool legal = known_legal || can_execute(g, h, e, slot, kind0, dir, target, ptype);
         kind1 = legal ? kind0 : kKindNone;
         none1 = legal ? none0 : req;
-        if (claims_position(kind1)) {
+        if (!known_legal && claims_position(kind1)) {
             const int32_t at_ = gidx(reserved_position(g, cell, dir), g.cells);
             if (h.terrain[at_] != 0 || e.entity[at_] != kAbsent) {
                 kind1 = kKindNone;
@@ -261,19 +265,142 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
 
 // core.step of the env path.
 NR_DEV void env_core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1,
-                          bool count_events, int32_t n, bool irregular) {
+                          bool count_events, int32_t n, bool irregular, bool known_legal) {
     if (count_events) {
         if (lane < 32) at<int32_t>(e, g.lay.b_events)[lane] = 0;
         wave_sync();
     }
-    if (!admit_env(g, h, e, lane, key0, key1, count_events, n, irregular)) {
+    if (!admit_env(g, h, e, lane, key0, key1, count_events, n, irregular, known_legal)) {
         int32_t n_rank = 0;
         const int32_t issued = order_requests(g, e, lane, &n_rank);
         AS3 int16_t* order = at<int16_t>(e, g.lay.b_order);
         for (int32_t i = 0; i < issued; ++i) admit_one(g, h, e, lane, uni(order[i]), n_rank, key0, key1, count_events);
     }
     complete(g, h, e, lane);
-    decide(g, e, lane);
+    decide_counted(e, lane);
+}
+
+// Per-cycle occupancy bitmaps, rows of g.seen_words 32-bit words:
+//   0 blocked (occupied or wall), 1/2 units of player 0/1, 3 resources,
+//   4/5 stockpiles of player 0/1.
+NR_DEV void build_bitmaps(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    AS3 uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
+    const int32_t plane = g.H * g.seen_words;
+    for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = 0u;
+    wave_sync();
+    for (int32_t c = lane; c < g.cells; c += kWave) {
+        const int32_t occ = e.entity[c];
+        const bool wall = h.terrain[c] != 0;
+        if (occ == kAbsent && !wall) continue;
+        const int32_t yy = c / g.W, x = c - yy * g.W;
+        const int32_t word = yy * g.seen_words + (x >> 5);
+        const uint32_t bit = 1u << (x & 31);
+        __atomic_fetch_or(&bm[word], bit, __ATOMIC_RELAXED);
+        if (occ == kAbsent) continue;
+        const int32_t s = gidx(occ, g.E);
+        const int32_t o = e.owner[s];
+        const int32_t fl = tabv(h, F_FLAGS, clampi(e.utype[s], 0, g.T - 1));
+        if (o == 0 || o == 1) {
+            __atomic_fetch_or(&bm[(1 + o) * plane + word], bit, __ATOMIC_RELAXED);
+            if (fl & FL_STOCKPILE) __atomic_fetch_or(&bm[(4 + o) * plane + word], bit, __ATOMIC_RELAXED);
+        }
+        if (fl & FL_RESOURCE) __atomic_fetch_or(&bm[3 * plane + word], bit, __ATOMIC_RELAXED);
+    }
+    wave_sync();
+}
+
+// Bits [x0, x0 + nbits) of a bitmap row; positions off the row read 0.
+NR_DEV uint32_t row_window(AS3 const uint32_t* row, int32_t words, int32_t x0, int32_t nbits) {
+    int32_t lead = 0;
+    if (x0 < 0) {
+        lead = -x0;
+        x0 = 0;
+    }
+    const int32_t w = x0 >> 5;
+    uint64_t v = 0;
+    if (w < words) v = row[w];
+    if (w + 1 < words) v |= (uint64_t)row[w + 1] << 32;
+    v = (v >> (x0 & 31)) << lead;
+    return (uint32_t)v & ((1u << nbits) - 1u);
+}
+
+// legality_row from the bitmaps (same bits; owners of owned slots are 0/1).
+NR_DEV Row legality_row_bm(const KGame& g, const Hdr& h, const Env& e, int32_t slot) {
+    Row r;
+    r.w[0] = r.w[1] = r.w[2] = 0u;
+    if (e.birth[slot] == kAbsent) return r;
+    const int32_t owner = e.owner[slot];
+    if (owner != 0 && owner != 1) return legality_row(g, h, e, slot);
+    const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
+    const int32_t carried = e.carried[slot];
+    const int32_t cell = e.cell[slot];
+    const int32_t flags = tabv(h, F_FLAGS, actor);
+    const int32_t balance = e.sc[S_RES0 + owner];
+    uint32_t affordable = 0u;
+    for (int32_t t = 0; t < g.T; ++t)
+        if (balance >= tabv(h, F_COST, t)) affordable |= 1u << t;
+    const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
+    const int32_t x = floor_mod(cell, g.W), yy = floor_div(cell, g.W);
+    const int32_t words = g.seen_words, plane = g.H * words;
+    AS3 const uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
+    // 3-bit windows (x-1 .. x+1) of the rows above, at and below the unit
+    uint32_t blk[3] = {7u, 7u, 7u}, res[3] = {0u, 0u, 0u}, stk[3] = {0u, 0u, 0u};
+#pragma unroll
+    for (int32_t k = 0; k < 3; ++k) {
+        const int32_t ry = yy - 1 + k;
+        if (ry < 0 || ry >= g.H) continue;
+        AS3 const uint32_t* row = bm + ry * words;
+        blk[k] = row_window(row, words, x - 1, 3);
+        res[k] = row_window(row + 3 * plane, words, x - 1, 3);
+        stk[k] = row_window(row + (4 + owner) * plane, words, x - 1, 3);
+        if (x - 1 < 0) blk[k] |= 1u;
+        if (x + 1 >= g.W) blk[k] |= 4u;
+    }
+    // direction d -> (row k, bit b): up (0,1) right (1,2) down (2,1) left (1,0)
+    uint32_t free4 = 0u, res4 = 0u, stk4 = 0u;
+    const int32_t dk[4] = {0, 1, 2, 1}, db[4] = {1, 2, 1, 0};
+#pragma unroll
+    for (int32_t d = 0; d < 4; ++d) {
+        free4 |= (((blk[dk[d]] >> db[d]) & 1u) ^ 1u) << d;
+        res4 |= ((res[dk[d]] >> db[d]) & 1u) << d;
+        stk4 |= ((stk[dk[d]] >> db[d]) & 1u) << d;
+    }
+    r.w[0] = 1u;  // NONE
+    if (flags & FL_MOVE) r.w[0] |= free4 << 6;
+    if ((flags & FL_HARVEST) && carried == 0) r.w[0] |= res4 << 10;
+    if ((flags & FL_HARVEST) && carried > 0) r.w[0] |= stk4 << 14;
+    if (types != 0u) r.w[0] |= free4 << 18;
+    const uint32_t produce_types = free4 != 0u ? types : 0u;
+    r.w[0] |= produce_types << 22;
+    r.w[0] |= ((r.w[0] >> 6) & 15u ? 1u : 0u) << kKindMove;
+    r.w[0] |= ((r.w[0] >> 10) & 15u ? 1u : 0u) << kKindHarvest;
+    r.w[0] |= ((r.w[0] >> 14) & 15u ? 1u : 0u) << kKindReturn;
+    r.w[0] |= (produce_types ? 1u : 0u) << kKindProduce;
+    if (flags & FL_ATTACK) {
+        const int32_t range = tabv(h, F_RANGE, actor);
+        const int32_t reach = imin(range, g.radius);
+        AS3 const uint32_t* enemy = bm + (2 - owner) * plane;
+        uint64_t att = 0;
+        for (int32_t dy = -reach; dy <= reach; ++dy) {
+            const int32_t ty = yy + dy;
+            if (ty < 0 || ty >= g.H) continue;
+            const int32_t rem = range * range - dy * dy;
+            int32_t hw = reach;
+            while (hw * hw > rem) --hw;
+            const uint32_t span = ((1u << (2 * hw + 1)) - 1u) << (reach - hw);
+            const uint32_t bits = row_window(enemy + ty * words, words, x - reach, 2 * reach + 1) & span;
+            att |= (uint64_t)bits << ((g.radius + dy) * g.side + g.radius - reach);
+        }
+        if (att != 0ull) {
+            r.w[0] |= 1u << kKindAttack;
+            const int32_t first = 22 + g.T;  // < 32
+            r.w[0] |= (uint32_t)(att << first);
+            r.w[1] |= (uint32_t)(att >> (32 - first));
+            r.w[2] |= (uint32_t)(att >> (64 - first));
+        }
+    }
+    return r;
 }
 
 // Symbolic observations of both agents in one pass over the cells
@@ -285,77 +412,88 @@ NR_DEV void observe_all(const KGame& g, const Hdr& h, const Env& e_in, int lane,
     AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);  // [2][H][seen_words]
     const int32_t plane = g.H * g.seen_words;
     if (partial) {
-        AS3 int16_t* units = at<int16_t>(e, y.b_units);
         for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;
-        int32_t n = 0;
+        wave_sync();
+        // each lane stamps the sight disk of one active unit, row by row
         for (int32_t base = 0; base < 2 * g.C; base += kWave) {
             const int32_t i = base + lane;
-            const bool act = i < 2 * g.C && e.birth[g.N + i] != kAbsent;
-            const uint64_t m = ballot(act);
-            if (act) units[n + count_below(m)] = (int16_t)(g.N + i);
-            n += popc(m);
-        }
-        wave_sync();
-        const int32_t rows = 2 * g.sight_max + 1;
-        const int32_t items = n * rows;
-        for (int32_t w = lane; w < items; w += kWave) {
-            const int32_t u = w / rows;
-            const int32_t dy = w - u * rows - g.sight_max;
-            const int32_t s = units[u];
+            if (i >= 2 * g.C) continue;
+            const int32_t s = g.N + i;
+            if (e.birth[s] == kAbsent) continue;
             const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
-            if (dy < -r || dy > r) continue;
             const int32_t cell = e.cell[s];
-            const int32_t cy = floor_div(cell, g.W) + dy;
-            if (cy < 0 || cy >= g.H) continue;
-            const int32_t rem = r * r - dy * dy;
+            const int32_t cx = floor_mod(cell, g.W), cy = floor_div(cell, g.W);
+            AS3 uint32_t* mine = seen + (i / g.C) * plane;
             int32_t hw = r;
-            while (hw * hw > rem) --hw;
-            const int32_t cx = floor_mod(cell, g.W);
-            const int32_t x0 = cx - hw < 0 ? 0 : cx - hw;
-            const int32_t x1 = cx + hw >= g.W ? g.W - 1 : cx + hw;
-            if (x0 > x1) continue;
-            AS3 uint32_t* row = seen + ((s - g.N) / g.C) * plane + cy * g.seen_words;
-            for (int32_t wd = x0 >> 5; wd <= (x1 >> 5); ++wd) {
-                const int32_t a = x0 > wd * 32 ? x0 - wd * 32 : 0;
-                const int32_t b = x1 < wd * 32 + 31 ? x1 - wd * 32 : 31;
-                const uint32_t bits = (b - a == 31) ? 0xFFFFFFFFu : (((1u << (b - a + 1)) - 1u) << a);
-                __atomic_fetch_or(&row[wd], bits, __ATOMIC_RELAXED);
+            for (int32_t dy = 0; dy <= r; ++dy) {
+                const int32_t rem = r * r - dy * dy;
+                while (hw * hw > rem) --hw;
+                const int32_t x0 = cx - hw < 0 ? 0 : cx - hw;
+                const int32_t x1 = cx + hw >= g.W ? g.W - 1 : cx + hw;
+                if (x0 > x1) continue;
+                for (int32_t side = 0; side < (dy == 0 ? 1 : 2); ++side) {
+                    const int32_t ry = side == 0 ? cy - dy : cy + dy;
+                    if (ry < 0 || ry >= g.H) continue;
+                    for (int32_t wd = x0 >> 5; wd <= (x1 >> 5); ++wd) {
+                        const int32_t a = x0 > wd * 32 ? x0 - wd * 32 : 0;
+                        const int32_t b = x1 < wd * 32 + 31 ? x1 - wd * 32 : 31;
+                        const uint32_t bits = (b - a == 31) ? 0xFFFFFFFFu : (((1u << (b - a + 1)) - 1u) << a);
+                        __atomic_fetch_or(&mine[ry * g.seen_words + wd], bits, __ATOMIC_RELAXED);
+                    }
+                }
             }
         }
         wave_sync();
     }
     AS3 uint8_t* stage0 = at<uint8_t>(e, y.v_stage);
     AS3 uint8_t* stage1 = stage0 + g.stage_cells * 6;
+    constexpr int kPer = 4;  // cells per lane per staging block (stage_cells <= 256)
     for (int32_t c0 = 0; c0 < g.cells; c0 += g.stage_cells) {
         const int32_t nc = imin(g.stage_cells, g.cells - c0);
-        for (int32_t i = lane; i < nc; i += kWave) {
-            const int32_t c = c0 + i;
-            const int32_t occ = e.entity[c];
-            uint32_t hp = 0, carried = 0, type = 0, kind = 0, owner = 0;
-            if (occ != kAbsent) {
-                const int32_t s = clampi(occ, 0, g.E - 1);
-                hp = (uint32_t)(int32_t)e.hp[s] & 0xFFu;
-                carried = (uint32_t)e.carried[s] & 0xFFu;
-                type = (uint32_t)((int32_t)e.utype[s] + 1) & 0xFFu;
+        // gather first (independent loads), then encode and stage
+        int32_t occ[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int32_t i = lane + k * kWave;
+            occ[k] = i < nc ? (int32_t)e.entity[c0 + i] : kAbsent;
+        }
+        uint32_t word[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            word[k] = 0u;
+            if (occ[k] != kAbsent) {
+                const int32_t s = clampi(occ[k], 0, g.E - 1);
+                const uint32_t hp = (uint32_t)(int32_t)e.hp[s] & 0xFFu;
+                const uint32_t carried = (uint32_t)e.carried[s] & 0xFFu;
+                const uint32_t type = (uint32_t)((int32_t)e.utype[s] + 1) & 0xFFu;
                 const int32_t pk = e.pkind[s];
-                kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
-                owner = (uint32_t)((int32_t)e.owner[s] + 1) & 0x3u;
+                const uint32_t kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
+                const uint32_t owner = (uint32_t)((int32_t)e.owner[s] + 1) & 0x3u;
+                word[k] = hp | (carried << 8) | (type << 16) | (kind << 24) | (owner << 28);
             }
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int32_t i = lane + k * kWave;
+            if (i >= nc) continue;
+            const int32_t c = c0 + i;
             const uint32_t terrain = (uint32_t)h.terrain[c] << 8;
+            const uint32_t w = word[k];
+            const uint32_t owner = w >> 28;
             const int32_t yy = c / g.W, x = c - yy * g.W;
 #pragma unroll
             for (int32_t pl = 0; pl < 2; ++pl) {
                 bool shown = true;
                 if (partial) {
-                    const uint32_t word = seen[pl * plane + yy * g.seen_words + (x >> 5)];
-                    shown = owner == (uint32_t)(pl + 1) || ((word >> (x & 31)) & 1u);
+                    const uint32_t sw = seen[pl * plane + yy * g.seen_words + (x >> 5)];
+                    shown = owner == (uint32_t)(pl + 1) || ((sw >> (x & 31)) & 1u);
                 }
                 AS3 uint16_t* out = (AS3 uint16_t*)((pl == 0 ? stage0 : stage1) + i * 6);
                 if (shown) {
                     const uint32_t rel = owner > 0 ? (uint32_t)((((int32_t)owner - 1 + pl) & 1) + 1) : 0u;
-                    out[0] = (uint16_t)(hp | (carried << 8));
-                    out[1] = (uint16_t)(rel | (type << 8));
-                    out[2] = (uint16_t)(kind | terrain);
+                    out[0] = (uint16_t)(w & 0xFFFFu);
+                    out[1] = (uint16_t)(rel | (((w >> 16) & 0xFFu) << 8));
+                    out[2] = (uint16_t)(((w >> 24) & 0xFu) | terrain);
                 } else {
                     out[0] = 0;
                     out[1] = 0;

@@ -153,6 +153,11 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_pptype = take(E);
     y.o_scal = take(S_COUNT * 4);
     y.b_events = take(32 * 4);
+    y.o_bm = take(6 * g.H * g.seen_words * 4);
+    y.o_word = take(E * 4);
+    y.v_seen = take(2 * g.H * g.seen_words * 4);
+    y.a_av = take(C2 * 2);
+    y.b_units = take(C2 * 2);
     const int32_t union0 = o;
     // admission
     y.c_kind = take(C2);
@@ -166,22 +171,19 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.b_tmp = take(C2 * 2);
     y.b_order = take(C2 * 2);
     y.b_rank = take(E * 2);
-    y.a_av = take(C2 * 2);
     y.a_fk = take(kWave * 4);
     y.a_fn = take(kWave * 4);
     y.a_list = take(E * 2);
     const int32_t admission_end = o;
     // completion (the commands are dead by then)
     o = union0;
-    y.m_rec = take(C2 * 20);
+    y.m_rec = take(C2 * 24);
     y.m_keys = take(C2 * 8);
     y.m_tmp = take(C2 * 2);
     const int32_t completion_end = o;
     // observation
     o = union0;
-    y.v_seen = take(2 * g.H * g.seen_words * 4);
     y.v_stage = take(2 * g.stage_cells * 6);
-    y.b_units = take(g.C * 2);
     const int32_t observe_end = o;
     // masks
     o = union0;
@@ -463,6 +465,7 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
                            nanorts_env_results r) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
     bool irregular = false;
     const int32_t n = compact_available(g, e, lane, &irregular);
     const int32_t owned = 2 * g.C;
@@ -479,7 +482,7 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
     uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
     const bool events = r.reward_components != nullptr;
-    env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular);
+    env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular, false);
     finish_step(g, hdr, e, l, lane, partial != 0, r, events);
     store_env(g, s, l, e, lane);
     if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
@@ -512,6 +515,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
                           int32_t steps, int32_t partial, int64_t env0, nanorts_rollout_results out) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
     const int32_t owned = 2 * g.C;
     const nanorts_env_results none = {};
     const Env e0 = e;
@@ -521,13 +525,14 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
         bool irregular = false;
         const int32_t n = compact_available(g, e, lane, &irregular);
+        build_bitmaps(g, hdr, e, lane);
         uint32_t ke0 = key0, ke1 = key1;
         fold_in(ke0, ke1, (uint32_t)step);
         fold_in(ke0, ke1, (uint32_t)(env0 + l));
         AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
         for (int32_t i = lane; i < n; i += kWave) {
             const int32_t p = av[i];
-            const Row r = legality_row(g, hdr, e, g.N + p);
+            const Row r = legality_row_bm(g, hdr, e, g.N + p);
             int32_t a[7];
             sample_row(g, r, ke0, ke1, p, a);
             if (out.actions) {
@@ -551,7 +556,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         // env.step
         uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
         fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
-        env_core_step(g, hdr, e, lane, k0, k1, false, n, irregular);
+        env_core_step(g, hdr, e, lane, k0, k1, false, n, irregular, true);
         nanorts_env_results r = none;
         if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
         if (out.dones) r.done = out.dones + (int64_t)t * lanes;

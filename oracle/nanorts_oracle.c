@@ -1200,8 +1200,9 @@ void nro_decode_actions(const nro_game* g, const nro_state* s, const int32_t* ac
 /*   (w0,w1) = threefry(k_env, (agent*C + row, 0)),                           */
 /*   (w2,w3) = threefry(k_env, (agent*C + row, 1))                            */
 /*   factor f draws h_f = 16-bit half f of w0..w3 (low half first);          */
-/*   value = the (h_f mod popcount)-th set bit of the factor's mask, or 0     */
-/*   when the factor has no set bit (argmax over all -inf is 0).              */
+/*   value = the ((h_f * popcount) >> 16)-th set bit of the factor's mask    */
+/*   (multiply-shift range reduction), or 0 when the factor has no set bit   */
+/*   (argmax over all -inf is 0).                                            */
 /* Rows with only the NONE bit set come out as all zeros.                    */
 /* ------------------------------------------------------------------------ */
 static void factor_bounds(const nro_game* g, int32_t lo[7], int32_t width[7]) {
@@ -1242,7 +1243,7 @@ static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sa
             for (int32_t b = 0; b < wid[f]; ++b) count += row[lo[f] + b] != 0;
             int32_t value = 0;
             if (count > 0) {
-                int32_t k = (int32_t)(h % (uint32_t)count);
+                int32_t k = (int32_t)((h * (uint32_t)count) >> 16);
                 for (int32_t b = 0; b < wid[f]; ++b) {
                     if (row[lo[f] + b]) {
                         if (k == 0) {
