@@ -126,6 +126,7 @@ def cpu_baseline(envs: int, steps: int) -> dict:
     oracle = Oracle(game)
     state = batch_initial(game, envs, envmod.env_roots(0, envs))
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(threads, 16))  # one GPU's share of the host cores
     t0 = time.perf_counter()
     used = oracle.rollout(state, (11, 13), 0, steps, True, threads=threads, record=False)["threads"]
     dt = time.perf_counter() - t0
