@@ -189,6 +189,14 @@ int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state,
 int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
                    const uint8_t* tiles, uint8_t* image, int32_t* scalars);
 
+/* Pixel observations uint8[images][16H][16W][3] from symbolic feature maps
+ * uint8[images][H][W][6] (images = L * 2 agents) and the same tile table;
+ * equal to nanorts_pixels of the state the maps were encoded from.  Replaces
+ * pixels_from_symbolic (src/nanorts/observations/pixels.py:91-110); tiles and
+ * image must be 16-byte aligned. */
+int nanorts_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
+                             const uint8_t* tiles, uint8_t* image);
+
 /* Auto-reset: envs whose done flag is set get the initial State and
  * episode_index + 1.  Replaces nanorts_reset_where_done
  * (src/nanorts/adapters/cuda/reset.cu:160-222). */

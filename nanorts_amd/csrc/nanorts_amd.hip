@@ -643,6 +643,67 @@ __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_
     }
 }
 
+// Pixel observations from symbolic feature maps (pixels_from_symbolic,
+// N/observations/pixels.py:91-110): the maps carry presence (type != 0),
+// the observer-relative owner, type, pending kind, carried resources, hit
+// points and terrain, which is all the tile pick and glyph band read.  One
+// thread writes one 16-pixel (48-byte) sprite row of one cell; consecutive
+// threads take consecutive cells of one image row, so a wave's stores are
+// contiguous.  HBM-write-bound: 768 bytes written per cell per image.
+__global__ __launch_bounds__(256) void k_pixels_from_maps(int32_t H, int32_t W, int32_t T, int64_t images,
+                                                          const uint8_t* maps, const uint8_t* tiles, uint8_t* image) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per_image = (int64_t)H * 16 * W;
+    if (t >= images * per_image) return;
+    const int64_t m = t / per_image;
+    const int32_t r = (int32_t)(t - m * per_image);
+    const int32_t Y = r / W, cx = r - Y * W;
+    const int32_t cy = Y >> 4, py = Y & 15;
+    const uint8_t* f = maps + ((m * H + cy) * W + cx) * 6;
+    const int32_t hp = f[0], carried = f[1], owner = (int32_t)f[2] - 1, type = f[3], kind = f[4], terrain = f[5];
+    const bool present = type != 0;
+    const int32_t states = 1 + 3 * T;
+    const int32_t occupant = present ? 1 + (owner + 1) * T + (type - 1) : 0;
+    const int32_t tile = gidx(terrain * states + occupant, 2 * states);
+    const u32x4* src = (const u32x4*)(tiles + (int64_t)tile * 768 + py * 48);
+    u32x4 v[3] = {src[0], src[1], src[2]};
+    if (present && py >= 12 && py <= 14) {
+        uint8_t px[48];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w = v[k][j];
+                px[16 * k + 4 * j + 0] = (uint8_t)w;
+                px[16 * k + 4 * j + 1] = (uint8_t)(w >> 8);
+                px[16 * k + 4 * j + 2] = (uint8_t)(w >> 16);
+                px[16 * k + 4 * j + 3] = (uint8_t)(w >> 24);
+            }
+#pragma unroll
+        for (int x = 1; x < 15; ++x) {
+            const int32_t position = x - 1;
+            bool lit;
+            if (py == 12) lit = kind == position + 1;
+            else if (py == 13) lit = ((carried >> position) & 1) != 0;
+            else lit = hp > position;
+            const uint8_t c = lit ? 0xFF : 0x00;
+            px[3 * x] = px[3 * x + 1] = px[3 * x + 2] = c;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int b = 16 * k + 4 * j;
+                v[k][j] = (uint32_t)px[b] | ((uint32_t)px[b + 1] << 8) | ((uint32_t)px[b + 2] << 16) |
+                          ((uint32_t)px[b + 3] << 24);
+            }
+    }
+    u32x4* dst = (u32x4*)(image + (m * H * 16 + Y) * (int64_t)W * 48 + (int64_t)cx * 48);
+    dst[0] = v[0];
+    dst[1] = v[1];
+    dst[2] = v[2];
+}
+
 // wave64 semantics probe: ballot, mbcnt prefix counts, shuffles, prefix-min.
 __global__ void k_probe(int32_t* out) {
     const int lane = lane_id();
@@ -664,7 +725,7 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
-           "nanorts_observe,nanorts_pixels,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
+           "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
            "nanorts_rollout";
 }
 
@@ -771,6 +832,25 @@ int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, 
     NR_STATE(state)
     if (!tiles || !image) return fail(NANORTS_INVALID_ARGUMENT, "tiles and image are required");
     return launch(k_pixels, sh, lanes, (hipStream_t)stream, state, partial, tiles, image, scalars);
+}
+
+int nanorts_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
+                             const uint8_t* tiles, uint8_t* image) {
+    NR_SHAPE(game)
+    (void)sh;
+    if (images < 0) return fail(NANORTS_INVALID_ARGUMENT, "images must be >= 0");
+    if (images == 0) return NANORTS_OK;
+    if (!feature_maps || !tiles || !image) return fail(NANORTS_INVALID_ARGUMENT, "feature_maps, tiles and image are required");
+    if ((((uintptr_t)tiles) & 15u) != 0 || (((uintptr_t)image) & 15u) != 0)
+        return fail(NANORTS_INVALID_ARGUMENT, "tiles and image must be 16-byte aligned");
+    const int64_t threads = images * (int64_t)game->height * 16 * game->width;
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffLL) return fail(NANORTS_INVALID_ARGUMENT, "too many images for one launch");
+    hipLaunchKernelGGL(k_pixels_from_maps, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, game->height,
+                       game->width, game->types, images, feature_maps, tiles, image);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("k_pixels_from_maps launch: ") + hipGetErrorString(err));
+    return NANORTS_OK;
 }
 
 int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,

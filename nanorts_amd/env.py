@@ -263,25 +263,21 @@ class NanoRTS:
             "spawn_overflowed": torch.empty(L, dtype=torch.bool, device=d),
         }
         symbolic = self.layout.surface == "symbolic"
-        maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d) if symbolic else None
-        scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d) if symbolic else None
+        # the pixel surface renders from the symbolic maps the step writes
+        maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
+        scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d)
         fmaps = fscal = None
-        if self.final_observation and symbolic:
+        if self.final_observation:
             fmaps = torch.empty_like(maps)
             fscal = torch.empty_like(scalars)
         comps = torch.empty((L, 2, 6), dtype=torch.float32, device=d) if self.layout.reward_components else None
-        if not symbolic and self.final_observation:
-            final_obs = self.get_obs(EnvironmentState(nxt.core_state, nxt.environment_root, nxt.episode_index))
         results = native.EnvResults(
             _ptr(out["reward"]), _ptr(out["done"]), _ptr(out["terminated"]), _ptr(out["truncated"]),
             _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
             _ptr(comps))
         native.check(self.lib.nanorts_env_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), self.partial,
                                                results), "nanorts_env_step")
-        if symbolic:
-            obs = self._symbolic(maps, scalars)
-        else:
-            obs = self.get_obs(nxt)
+        obs = self._symbolic(maps, scalars) if symbolic else self._pixels(maps, scalars)
         rewards = {agent: out["reward"][:, p] for p, agent in enumerate(self.agents)}
         dones = {agent: out["done"] for agent in self.agents} | {ALL_AGENTS: out["done"]}
         infos: dict[str, Any] = {
@@ -290,7 +286,7 @@ class NanoRTS:
             "spawn_overflowed": out["spawn_overflowed"], "final_valid": out["done"],
         }
         if self.final_observation:
-            infos["final_observation"] = self._symbolic(fmaps, fscal) if symbolic else final_obs
+            infos["final_observation"] = self._symbolic(fmaps, fscal) if symbolic else self._pixels(fmaps, fscal)
         if comps is not None:
             infos["reward_components"] = {agent: comps[:, p] for p, agent in enumerate(self.agents)}
         return obs, nxt, rewards, dones, infos
@@ -423,6 +419,29 @@ class NanoRTS:
     # -------------------------------------------------------------- helpers
     def _symbolic(self, maps: torch.Tensor, scalars: torch.Tensor) -> dict[str, SymbolicObservation]:
         return {agent: SymbolicObservation(maps[:, p], scalars[:, p]) for p, agent in enumerate(self.agents)}
+
+    def pixels_from_maps(self, maps: torch.Tensor) -> torch.Tensor:
+        """uint8[..., 16H, 16W, 3] images of symbolic maps uint8[..., H, W, 6]
+        (src/nanorts/observations/pixels.py:91-110)."""
+        b = self.bucket
+        if self._tiles is None:
+            from nanorts_amd import rendering
+
+            self._tiles = torch.as_tensor(rendering.tile_table(b.unit_type_capacity), device=self.device)
+        maps = maps.contiguous()
+        if maps.dtype != torch.uint8 or tuple(maps.shape[-3:]) != (b.height, b.width, 6):
+            raise ModelError(f"feature maps are {maps.dtype} {tuple(maps.shape)}, expected uint8 [..., "
+                             f"{b.height}, {b.width}, 6]")
+        lead = tuple(maps.shape[:-3])
+        images = int(np.prod(lead)) if lead else 1
+        image = torch.empty((*lead, 16 * b.height, 16 * b.width, 3), dtype=torch.uint8, device=self.device)
+        native.check(self.lib.nanorts_pixels_from_maps(_stream(), self.dev.ref, images, _ptr(maps), _ptr(self._tiles),
+                                                       _ptr(image)), "nanorts_pixels_from_maps")
+        return image
+
+    def _pixels(self, maps: torch.Tensor, scalars: torch.Tensor) -> dict[str, PixelObservation]:
+        image = self.pixels_from_maps(maps)
+        return {agent: PixelObservation(image[:, p], scalars[:, p]) for p, agent in enumerate(self.agents)}
 
     def _stack_actions(self, actions: dict[str, torch.Tensor], L: int) -> torch.Tensor:
         if set(actions) != set(self.agents):

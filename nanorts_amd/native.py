@@ -71,7 +71,7 @@ class RolloutResults(ctypes.Structure):
 EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_self_check", "nanorts_step",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
-    "nanorts_observe", "nanorts_pixels", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
+    "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout",
 )
 
@@ -91,6 +91,7 @@ _SIGNATURES = {
     "nanorts_visible_cells": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP]),
     "nanorts_observe": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP]),
     "nanorts_pixels": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP, _VP]),
+    "nanorts_pixels_from_maps": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _VP]),
     "nanorts_reset_where_done": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
     "nanorts_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
     "nanorts_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),

@@ -131,6 +131,58 @@ def test_fused_rollout_matches_oracle(case, oracle_threads):
     assert_states_equal(st, to_host(dev), f"{case} rollout")
 
 
+@pytest.mark.parametrize("case", ["16x16-random-partial", "melee-both", "gow-alternating"])
+def test_pixels(case, oracle_threads):
+    """nanorts_pixels (from the state) and nanorts_pixels_from_maps (from the
+    symbolic maps) against the oracle's renderer, both observability modes."""
+    import torch
+
+    from nanorts_amd import rendering
+
+    game, _ = game_for(case)
+    gow = case.startswith("gow")
+    L = 4 if gow else 32
+    oracle, st = advanced_states(game, L, 40 if gow else 120, True, oracle_threads, seed=4)
+    tiles = rendering.tile_table(game.bucket.unit_type_capacity)
+    for partial in (False, True):
+        env = _env(game, partial, surface="pixels")
+        dev = to_device(env, st)
+        want_image, want_scalars = oracle.pixels(st, partial, tiles)
+        obs = env.get_obs(dev)
+        for i, agent in enumerate(env.agents):
+            np.testing.assert_array_equal(obs[agent].image.cpu().numpy(), want_image[:, i])
+            np.testing.assert_array_equal(obs[agent].scalars.cpu().numpy(), want_scalars[:, i])
+        sym = _env(game, partial).get_obs(dev)
+        maps = torch.stack([sym[a].feature_maps for a in env.agents], 1)
+        np.testing.assert_array_equal(env.pixels_from_maps(maps).cpu().numpy(), want_image)
+
+
+def test_pixel_surface_env_step(oracle_threads):
+    """env.step on the pixel surface: published images against the oracle's
+    renderer of the post-step (auto-reset) state, cycle by cycle."""
+    import torch
+
+    from nanorts_amd import rendering
+
+    game, partial = game_for("barracks-random")
+    L = 16
+    oracle, st = advanced_states(game, L, 100, partial, oracle_threads, seed=8)
+    tiles = rendering.tile_table(game.bucket.unit_type_capacity)
+    env = _env(game, partial, surface="pixels")
+    dev = to_device(env, st)
+    for t in range(12):
+        words = env.get_avail_actions(dev, form="words")
+        acts = env.sample_actions(torch.stack([words[a] for a in env.agents], 1), (2, 3), t)
+        obs, dev, rewards, dones, infos = env.step(None, dev, acts, donate=True)
+        oracle.env_step(st, np.stack([acts[a].cpu().numpy() for a in env.agents], 1), partial, observe=False)
+        want_image, want_scalars = oracle.pixels(st, partial, tiles)
+        for i, agent in enumerate(env.agents):
+            np.testing.assert_array_equal(obs[agent].image.cpu().numpy(), want_image[:, i], err_msg=f"cycle {t}")
+            np.testing.assert_array_equal(obs[agent].scalars.cpu().numpy(), want_scalars[:, i])
+        final = infos["final_observation"]
+        assert final[env.agents[0]].image.shape == obs[env.agents[0]].image.shape
+
+
 def test_reset_where_done(oracle_threads):
     import torch
 
