@@ -40,8 +40,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--chunk", type=int, default=100, help="cycles per fused launch")
     ap.add_argument("--depth", type=int, default=2, help="observation ring depth in HBM")
     ap.add_argument("--per-call-steps", type=int, default=20)
-    ap.add_argument("--cpu-envs", type=int, default=2048)
-    ap.add_argument("--cpu-steps", type=int, default=400)
+    ap.add_argument("--cpu-envs", type=int, default=4096)
+    ap.add_argument("--cpu-steps", type=int, default=3000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
     ap.add_argument("--profile-child", choices=("rollout", "copy"), default=None, help=argparse.SUPPRESS)

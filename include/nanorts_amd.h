@@ -146,6 +146,12 @@ const char* nanorts_build_id(void);
 const char* nanorts_targets(void);
 const char* nanorts_last_error(void);
 
+/* Least LDS bytes one workgroup may allocate over the listed devices (0 on
+ * error).  Replaces nanorts_shared_opt_in
+ * (src/nanorts/kernels/cuda/registry.cu:224-226), which the reference's
+ * loader binds (src/nanorts/kernels/library.py:42-46). */
+int64_t nanorts_shared_opt_in(const int32_t* devices, int64_t n);
+
 /* Runs a wave64 ballot / prefix-count / shuffle probe on each listed device;
  * returns "" when every device passes, else a static description.
  * Replaces src/nanorts/kernels/cuda/registry.cu:174-183 (nanorts_self_check). */

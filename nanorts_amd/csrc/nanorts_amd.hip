@@ -731,6 +731,19 @@ const char* nanorts_targets(void) {
 
 const char* nanorts_last_error(void) { return g_error.c_str(); }
 
+int64_t nanorts_shared_opt_in(const int32_t* devices, int64_t n) {
+    int64_t least = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        int bytes = 0;
+        if (!devices || hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, devices[i]) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        least = i == 0 ? bytes : (bytes < least ? bytes : least);
+    }
+    return least;
+}
+
 const char* nanorts_self_check(const int32_t* devices, int64_t n) {
     static thread_local std::string result;
     result.clear();

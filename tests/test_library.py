@@ -13,7 +13,7 @@ ROOT = Path(__file__).resolve().parent.parent
 
 def declared_entry_points() -> list[str]:
     text = (ROOT / "include" / "nanorts_amd.h").read_text()
-    return sorted(set(re.findall(r"^(?:const char\*|int)\s+(nanorts_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:const char\*|int|int64_t)\s+(nanorts_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declarations_match_binding():
