@@ -72,6 +72,7 @@ enum : int {
     S_UNITS1,
     S_NAV,    // available units listed by summarize
     S_IRREG,  // 1 when an available unit holds a pending order
+    S_NUNITS, // active owned units listed by summarize
     S_COUNT = 20
 };
 
@@ -89,13 +90,15 @@ struct Layout {
     int32_t o_seg;
     int32_t env_bytes;  // one wave's block, 16-byte multiple
     int32_t o_terrain;  // in the header
+    int32_t o_disk;     // in the header: sight-disk row masks [R + 1][2R + 1]
     int32_t o_birth, o_carried, o_pnone, o_pissued, o_pcompl, o_porder;
     int32_t o_cell, o_hp, o_ptarget, o_entity;
     int32_t o_utype, o_owner, o_pkind, o_pdir, o_pptype;
     int32_t o_scal;
     int32_t b_events;  // admitted counts, outside the phase union
     int32_t o_bm;      // occupancy bitmaps (6 planes), outside the union
-    int32_t o_word;    // occupant word per slot, outside the union
+    int32_t o_lo;      // occupant word per slot (player 0's view), outside the union
+    int32_t o_fl;      // occupant flags per slot: kind | resource << 4 | stockpile << 5
     // Phase union.  Admission: commands, keys, lists.  Completion: member
     // records, keys.  Observation: seen bitmap, staging, unit list.  Masks:
     // staged words.
@@ -111,6 +114,7 @@ struct Layout {
 struct KGame {
     int32_t H, W, cells, N, C, E, T, O, strategy, max_cycles;
     int32_t side, radius, rank_bits, seen_words, stage_cells, sight_max;
+    int32_t fast_obs;  // 4-cell observation groups and disk-table stamping apply
     int32_t tab[F_COUNT * 8];
     const uint8_t* terrain;
     nanorts_state initial;
@@ -208,6 +212,7 @@ struct Hdr {
     AS3 int32_t* tab;
     AS3 uint8_t* terrain;
     AS3 Seg* seg;
+    AS3 uint32_t* disk;
 };
 
 struct Env {
@@ -282,6 +287,21 @@ NR_DEV void load_header(const KGame& g, const Hdr& h) {
         }
     }
     for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = g.terrain[i] ? 1 : 0;
+    if (g.fast_obs) {
+        // disk[r][dy + R]: bits R - w .. R + w with w = floor(sqrt(r^2 - dy^2)),
+        // 0 when |dy| > r (R = sight_max <= 15)
+        const int32_t R = g.sight_max, span = 2 * R + 1;
+        for (int i = threadIdx.x; i < (R + 1) * span; i += blockDim.x) {
+            const int32_t r = i / span, dy = i - r * span - R;
+            uint32_t m = 0u;
+            if (dy * dy <= r * r) {
+                int32_t w = r;
+                while (w * w > r * r - dy * dy) --w;
+                m = ((2u << (2 * w)) - 1u) << (R - w);
+            }
+            h.disk[i] = m;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -11,7 +11,7 @@
 
 #include "../../include/nanorts_amd.h"
 #include "engine.h"
-#include "envstep.h"
+#include "rollout.h"
 
 using namespace nr;
 
@@ -127,9 +127,11 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
 
     Layout& y = g.lay;
     const int32_t E = g.E, C2 = 2 * g.C, cells = g.cells;
+    g.fast_obs = (g.W % 4 == 0 && g.sight_max <= 15) ? 1 : 0;
     y.o_seg = F_COUNT * 8 * 4;
     y.o_terrain = y.o_seg + 16 * (int32_t)sizeof(Seg);
-    y.hdr_bytes = align16(y.o_terrain + cells);
+    y.o_disk = align16(y.o_terrain + cells);
+    y.hdr_bytes = align16(y.o_disk + (g.fast_obs ? (g.sight_max + 1) * (2 * g.sight_max + 1) * 4 : 0));
     int32_t o = 0;
     auto take = [&o](int32_t bytes) {
         const int32_t at = o;
@@ -154,7 +156,8 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_scal = take(S_COUNT * 4);
     y.b_events = take(32 * 4);
     y.o_bm = take(6 * g.H * g.seen_words * 4);
-    y.o_word = take(E * 4);
+    y.o_lo = take(E * 4);
+    y.o_fl = take(E);
     y.v_seen = take(2 * g.H * g.seen_words * 4);
     y.a_av = take(C2 * 2);
     y.b_units = take(C2 * 2);
@@ -267,6 +270,7 @@ bool state_complete(const nanorts_state& s) {
     hdr.tab = (AS3 int32_t*)lds;                                                  \
     hdr.terrain = lds + g.lay.o_terrain;                                          \
     hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);                                      \
+    hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);                               \
     load_header(g, hdr);                                                          \
     __syncthreads();                                                              \
     const int lane = lane_id();                                                   \
@@ -510,7 +514,10 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
     }
 }
 
-// Fused rollout: the state stays staged in LDS across `steps` cycles.
+// Fused rollout: the state stays staged in LDS across `steps` cycles.  With
+// the per-cycle summary (rollout.h) each cycle is: sample from the masks of
+// the summarised state -> decode -> core.step -> finish (reward, done,
+// auto-reset) -> summarise the new state, which writes its observation.
 __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts_state s, uint32_t key0, uint32_t key1, int32_t step0,
                           int32_t steps, int32_t partial, int64_t env0, nanorts_rollout_results out) {
     NR_KERNEL_PROLOGUE
@@ -518,14 +525,25 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
     count_units(g, e, lane);
     const int32_t owned = 2 * g.C;
     const nanorts_env_results none = {};
+    const bool fast = g.fast_obs && ((((uintptr_t)out.feature_maps) & 7u) == 0);
+    const int64_t per = (int64_t)g.cells * 6;
+    if (fast) summarize(g, hdr, e, lane, partial != 0, nullptr, nullptr, nullptr, nullptr);
+    uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
+    fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const Env e0 = e;
     for (int32_t t = 0; t < steps; ++t) {
         const Env e = refresh(g, e0);
         const int32_t step = step0 + t;
         // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
         bool irregular = false;
-        const int32_t n = compact_available(g, e, lane, &irregular);
-        build_bitmaps(g, hdr, e, lane);
+        int32_t n;
+        if (fast) {
+            n = uni(e.sc[S_NAV]);
+            irregular = uni(e.sc[S_IRREG]) != 0;
+        } else {
+            n = compact_available(g, e, lane, &irregular);
+            build_bitmaps(g, hdr, e, lane);
+        }
         uint32_t ke0 = key0, ke1 = key1;
         fold_in(ke0, ke1, (uint32_t)step);
         fold_in(ke0, ke1, (uint32_t)(env0 + l));
@@ -534,7 +552,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
             const int32_t p = av[i];
             const Row r = legality_row_bm(g, hdr, e, g.N + p);
             int32_t a[7];
-            sample_row(g, r, ke0, ke1, p, a);
+            sample_row_fast(g, r, ke0, ke1, p, a);
             if (out.actions) {
                 int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
 #pragma unroll
@@ -553,17 +571,31 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
             }
         }
         wave_sync();
-        // env.step
-        uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
-        fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
-        env_core_step(g, hdr, e, lane, k0, k1, false, n, irregular, true);
+        // env.step: core.step keyed by fold_in(env root, episode)
+        if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true)) {
+            if (fast) mark_unavailable(g, e, lane);
+            int32_t n_rank = 0;
+            const int32_t issued = order_requests(g, e, lane, &n_rank);
+            AS3 int16_t* order = at<int16_t>(e, g.lay.b_order);
+            for (int32_t i = 0; i < issued; ++i) admit_one(g, hdr, e, lane, uni(order[i]), n_rank, ek0, ek1, false);
+        }
+        complete(g, hdr, e, lane);
+        decide_counted(e, lane);
         nanorts_env_results r = none;
         if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
         if (out.dones) r.done = out.dones + (int64_t)t * lanes;
-        finish_step(g, hdr, e, l, lane, partial != 0, r, false);
-        if (out.feature_maps || out.scalars) {
-            const int64_t ring = out.depth > 0 ? (int64_t)(t % out.depth) : 0;
-            observe_both(g, hdr, e, ring * lanes + l, lane, partial != 0, out.feature_maps, out.scalars);
+        if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) {
+            ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
+            ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
+            fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+        }
+        const int64_t slot = (out.depth > 0 ? (int64_t)(t % out.depth) : 0) * lanes + l;
+        if (fast) {
+            uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
+            int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
+            summarize(g, hdr, e, lane, partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+        } else if (out.feature_maps || out.scalars) {
+            observe_both(g, hdr, e, slot, lane, partial != 0, out.feature_maps, out.scalars);
         }
     }
     store_env(g, s, l, e, lane);

@@ -1,0 +1,260 @@
+// The per-cycle summary of the fused env path and the sampling phase that
+// reads it.
+//
+// `summarize` runs once after every cycle (and once after the state is
+// loaded).  In three passes it derives everything the next cycle's masks,
+// admission and this cycle's observation need from the post-step state:
+//   slots: the occupant word and flags of every live slot, the list of
+//          available owned positions and of active owned units;
+//   units: the sight disks of both players, stamped row by row from a
+//          precomputed disk table (N/observations/visibility.py:56-71);
+//   cells: four consecutive cells per lane -> the six occupancy bitmaps of
+//          the masks, and both agents' symbolic feature maps
+//          (N/observations/symbolic.py:130-180) packed into dwords and
+//          stored straight to HBM.
+#pragma once
+
+#include "envstep.h"
+
+namespace nr {
+
+// k-th set bit (0-based) of m by halving popcounts; m has more than k bits.
+NR_DEV int32_t select_bit(uint64_t m, int32_t k) {
+    int32_t pos = 0;
+    uint32_t v = (uint32_t)m;
+    const int32_t c32 = popc((uint64_t)v);
+    if (k >= c32) {
+        k -= c32;
+        v = (uint32_t)(m >> 32);
+        pos = 32;
+    }
+#pragma unroll
+    for (int32_t half = 16; half >= 1; half >>= 1) {
+        const uint32_t lowmask = (1u << half) - 1u;
+        const int32_t c = __popc(v & lowmask);
+        if (k >= c) {
+            k -= c;
+            v >>= half;
+            pos += half;
+        }
+    }
+    return pos;
+}
+
+// sample_row with the select above (same draws, same result).
+NR_DEV void sample_row_fast(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1, int32_t p, int32_t a[7]) {
+    if (only_none(r)) {
+#pragma unroll
+        for (int f = 0; f < 7; ++f) a[f] = 0;
+        return;
+    }
+    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
+    threefry(ke0, ke1, w0, w1);
+    threefry(ke0, ke1, w2, w3);
+    const uint32_t words[4] = {w0, w1, w2, w3};
+    const int32_t lo[7] = {0, 6, 10, 14, 18, 22, 22 + g.T};
+    const int32_t wid[7] = {6, 4, 4, 4, 4, g.T, g.O};
+#pragma unroll
+    for (int f = 0; f < 7; ++f) {
+        const uint32_t hh = (words[f >> 1] >> (16 * (f & 1))) & 0xFFFFu;
+        const uint64_t m = row_bits(r, lo[f], wid[f]);
+        const int32_t count = popc(m);
+        a[f] = count > 0 ? select_bit(m, (int32_t)((hh * (uint32_t)count) >> 16)) : 0;
+    }
+}
+
+// Pass over the slots: occupant words, available list, unit list.
+NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
+    AS3 uint32_t* olo = at<uint32_t>(e, y.o_lo);
+    AS3 uint8_t* ofl = at<uint8_t>(e, y.o_fl);
+    AS3 int16_t* av = at<int16_t>(e, y.a_av);
+    AS3 int16_t* units = at<int16_t>(e, y.b_units);
+    int32_t nav = 0, nunits = 0;
+    bool odd = false;
+    for (int32_t base = 0; base < g.E; base += kWave) {
+        const int32_t s = base + lane;
+        bool alive = false, available = false;
+        if (s < g.E) {
+            alive = e.birth[s] != kAbsent;
+            if (alive) {
+                const int32_t ty = e.utype[s];
+                const int32_t ow = e.owner[s];
+                const uint32_t rel0 = ow == 0 ? 1u : (ow == 1 ? 2u : 0u);
+                olo[s] = ((uint32_t)(int32_t)e.hp[s] & 0xFFu) | (((uint32_t)e.carried[s] & 0xFFu) << 8) |
+                         (rel0 << 16) | (((uint32_t)(ty + 1) & 0xFFu) << 24);
+                const int32_t pk = e.pkind[s];
+                const int32_t fl = tabv(h, F_FLAGS, clampi(ty, 0, g.T - 1));
+                ofl[s] = (uint8_t)(((pk > 0 ? pk : 0) & 0xF) | ((fl & FL_RESOURCE) ? 16 : 0) |
+                                   ((fl & FL_STOCKPILE) ? 32 : 0));
+                available = s >= g.N && pk == kAbsent;
+                if (available && e.porder[s] != kAbsent) odd = true;
+            }
+        }
+        const bool unit = alive && s >= g.N;
+        const uint64_t ma = ballot(available);
+        if (available) av[nav + count_below(ma)] = (int16_t)(s - g.N);
+        nav += popc(ma);
+        const uint64_t mu = ballot(unit);
+        if (unit) units[nunits + count_below(mu)] = (int16_t)s;
+        nunits += popc(mu);
+    }
+    const bool irregular = ballot(odd) != 0ull;
+    if (lane == 0) {
+        e.sc[S_NAV] = nav;
+        e.sc[S_NUNITS] = nunits;
+        e.sc[S_IRREG] = irregular ? 1 : 0;
+    }
+    wave_sync();
+}
+
+// Sight disks of both players into seen[2][H][words].
+NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
+    AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);
+    const int32_t words = g.seen_words, plane = g.H * words;
+    for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;
+    wave_sync();
+    const int32_t nunits = uni(e.sc[S_NUNITS]);
+    AS3 const int16_t* units = at<int16_t>(e, y.b_units);
+    const int32_t R = g.sight_max, span = 2 * R + 1;
+    for (int32_t base = 0; base < nunits; base += kWave) {
+        const int32_t i = base + lane;
+        int32_t r = -1, cx = 0, cy = 0;
+        AS3 uint32_t* mine = seen;
+        if (i < nunits) {
+            const int32_t s = units[i];
+            r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
+            const int32_t cell = e.cell[s];
+            cx = floor_mod(cell, g.W);
+            cy = floor_div(cell, g.W);
+            mine = seen + ((s - g.N) >= g.C ? plane : 0);
+        }
+        AS3 const uint32_t* disk = h.disk + (r < 0 ? 0 : r) * span;
+        for (int32_t dy = -R; dy <= R; ++dy) {
+            const int32_t row = cy + dy;
+            if (r < 0 || dy < -r || dy > r || row < 0 || row >= g.H) continue;
+            const uint64_t m = disk[dy + R];
+            const int32_t x0 = cx - R;
+            for (int32_t wd = 0; wd < words; ++wd) {
+                const int32_t sh = x0 - 32 * wd;
+                uint64_t bits = sh >= 0 ? (sh < 64 ? m << sh : 0ull) : (-sh < 64 ? m >> (-sh) : 0ull);
+                uint32_t b32 = (uint32_t)bits;
+                const int32_t valid = g.W - 32 * wd;
+                if (valid < 32) b32 &= (1u << valid) - 1u;
+                if (b32 != 0u) __atomic_fetch_or(&mine[row * words + wd], b32, __ATOMIC_RELAXED);
+            }
+        }
+    }
+    wave_sync();
+}
+
+// Pass over the cells, four per lane (W % 4 == 0): bitmaps for the masks and
+// both agents' feature maps.  maps0/maps1 may be null (no observation).
+NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool partial, bool bitmaps,
+                            uint8_t* maps0, uint8_t* maps1) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
+    const int32_t words = g.seen_words, plane = g.H * words;
+    AS3 uint32_t* bm = at<uint32_t>(e, y.o_bm);
+    if (bitmaps) {
+        for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = 0u;
+        wave_sync();
+    }
+    AS3 const uint32_t* olo = at<uint32_t>(e, y.o_lo);
+    AS3 const uint8_t* ofl = at<uint8_t>(e, y.o_fl);
+    AS3 const uint32_t* seen = at<uint32_t>(e, y.v_seen);
+    const bool obs = maps0 != nullptr;
+    for (int32_t base = 0; base < g.cells; base += 4 * kWave) {
+        const int32_t c0 = base + 4 * lane;
+        if (c0 >= g.cells) continue;
+        const uint64_t ent = *(AS3 const uint64_t*)(e.entity + c0);
+        const uint32_t ter = *(AS3 const uint32_t*)(h.terrain + c0);
+        const int32_t yy = c0 / g.W, x = c0 - yy * g.W;
+        const int32_t word = yy * words + (x >> 5), shift = x & 31;
+        uint32_t lo[4], fl[4];
+        uint32_t occ_n = 0u, p0_n = 0u, p1_n = 0u, res_n = 0u, stk0_n = 0u, stk1_n = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int32_t occ = (int16_t)(uint16_t)(ent >> (16 * k));
+            lo[k] = 0u;
+            fl[k] = 0u;
+            if (occ != kAbsent) {
+                const int32_t sl = gidx(occ, g.E);
+                lo[k] = olo[sl];
+                fl[k] = ofl[sl];
+            }
+            const uint32_t rel = (lo[k] >> 16) & 3u;
+            occ_n |= (occ != kAbsent || ((ter >> (8 * k)) & 0xFFu) != 0u ? 1u : 0u) << k;
+            p0_n |= (rel == 1u ? 1u : 0u) << k;
+            p1_n |= (rel == 2u ? 1u : 0u) << k;
+            res_n |= ((fl[k] >> 4) & 1u) << k;
+            stk0_n |= (((fl[k] >> 5) & 1u) & (rel == 1u ? 1u : 0u)) << k;
+            stk1_n |= (((fl[k] >> 5) & 1u) & (rel == 2u ? 1u : 0u)) << k;
+        }
+        if (bitmaps) {
+            if (occ_n) __atomic_fetch_or(&bm[word], occ_n << shift, __ATOMIC_RELAXED);
+            if (p0_n) __atomic_fetch_or(&bm[plane + word], p0_n << shift, __ATOMIC_RELAXED);
+            if (p1_n) __atomic_fetch_or(&bm[2 * plane + word], p1_n << shift, __ATOMIC_RELAXED);
+            if (res_n) __atomic_fetch_or(&bm[3 * plane + word], res_n << shift, __ATOMIC_RELAXED);
+            if (stk0_n) __atomic_fetch_or(&bm[4 * plane + word], stk0_n << shift, __ATOMIC_RELAXED);
+            if (stk1_n) __atomic_fetch_or(&bm[5 * plane + word], stk1_n << shift, __ATOMIC_RELAXED);
+        }
+        if (!obs) continue;
+#pragma unroll
+        for (int32_t pl = 0; pl < 2; ++pl) {
+            const uint32_t own = pl == 0 ? p0_n : p1_n;
+            const uint32_t vis = partial ? ((seen[pl * plane + word] >> shift) & 15u) | own : 15u;
+            uint32_t l4[4], h4[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const bool shown = (vis >> k) & 1u;
+                uint32_t v = lo[k];
+                if (pl == 1 && ((v >> 16) & 3u) != 0u) v ^= 3u << 16;
+                l4[k] = shown ? v : 0u;
+                h4[k] = (shown ? (fl[k] & 0xFu) : 0u) | (((ter >> (8 * k)) & 0xFFu) << 8);
+            }
+            uint64_t* dst = (uint64_t*)((pl == 0 ? maps0 : maps1) + (int64_t)c0 * 6);
+            dst[0] = (uint64_t)l4[0] | ((uint64_t)(h4[0] | (l4[1] << 16)) << 32);
+            dst[1] = (uint64_t)((l4[1] >> 16) | (h4[1] << 16)) | ((uint64_t)l4[2] << 32);
+            dst[2] = (uint64_t)(h4[2] | (l4[3] << 16)) | ((uint64_t)((l4[3] >> 16) | (h4[3] << 16)) << 32);
+        }
+    }
+    wave_sync();
+}
+
+// The summary of the current state; the observation is written when
+// maps0/maps1 are given (8-byte aligned), scalars when scalars0/1 are.
+NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool partial, uint8_t* maps0,
+                      uint8_t* maps1, int32_t* scalars0, int32_t* scalars1) {
+    summarize_slots(g, h, e, lane);
+    if (partial && maps0) summarize_visibility(g, h, e, lane);
+    summarize_cells(g, h, e, lane, partial, true, maps0, maps1);
+    if (scalars0 && lane < 8) {
+        const int32_t pl = lane >> 2, f = lane & 3;
+        int32_t v;
+        if (f == 0) v = e.sc[S_RES0 + pl];
+        else if (f == 1) v = e.sc[S_RES0 + (pl ^ 1)];
+        else if (f == 2) v = e.sc[S_TIME];
+        else v = e.sc[S_ALT];
+        (pl == 0 ? scalars0 : scalars1)[f] = v;
+    }
+}
+
+// Commands of the positions the summary did not list as available.
+NR_DEV void mark_unavailable(const KGame& g, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
+    AS3 int8_t* ckind = at<int8_t>(e, y.c_kind);
+    AS3 int16_t* crank = at<int16_t>(e, y.c_rank);
+    for (int32_t p = lane; p < 2 * g.C; p += kWave) {
+        const int32_t s = g.N + p;
+        if (!(e.birth[s] != kAbsent && e.pkind[s] == kAbsent)) ckind[p] = (int8_t)kAbsent;
+        crank[p] = 0;
+    }
+    wave_sync();
+}
+
+}  // namespace nr
