@@ -114,7 +114,9 @@ struct Layout {
 struct KGame {
     int32_t H, W, cells, N, C, E, T, O, strategy, max_cycles;
     int32_t side, radius, rank_bits, seen_words, stage_cells, sight_max;
-    int32_t fast_obs;  // 4-cell observation groups and disk-table stamping apply
+    int32_t fast_obs;  // 4-cell observation groups and the disk table apply
+    int32_t disk_r;    // radius of the disk table: max(sight radius, attack range) <= 15
+    int32_t wshift;    // log2(W) when W is a power of two, else -1
     int32_t tab[F_COUNT * 8];
     const uint8_t* terrain;
     nanorts_state initial;
@@ -140,6 +142,9 @@ NR_DEV int32_t floor_mod(int32_t a, int32_t b) {
     return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
 }
 NR_DEV int32_t gidx(int32_t i, int32_t n) { return clampi(i < 0 ? i + n : i, 0, n - 1); }
+// floor_mod / floor_div of a cell index by the board width
+NR_DEV int32_t cell_x(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c & (g.W - 1)) : floor_mod(c, g.W); }
+NR_DEV int32_t cell_y(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c >> g.wshift) : floor_div(c, g.W); }
 NR_DEV int32_t dir_dx(int32_t d) { return d == 1 ? 1 : (d == 3 ? -1 : 0); }
 NR_DEV int32_t dir_dy(int32_t d) { return d == 0 ? -1 : (d == 2 ? 1 : 0); }
 
@@ -289,8 +294,8 @@ NR_DEV void load_header(const KGame& g, const Hdr& h) {
     for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = g.terrain[i] ? 1 : 0;
     if (g.fast_obs) {
         // disk[r][dy + R]: bits R - w .. R + w with w = floor(sqrt(r^2 - dy^2)),
-        // 0 when |dy| > r (R = sight_max <= 15)
-        const int32_t R = g.sight_max, span = 2 * R + 1;
+        // 0 when |dy| > r (R = disk_r <= 15)
+        const int32_t R = g.disk_r, span = 2 * R + 1;
         for (int i = threadIdx.x; i < (R + 1) * span; i += blockDim.x) {
             const int32_t r = i / span, dy = i - r * span - R;
             uint32_t m = 0u;
@@ -451,7 +456,7 @@ struct Nb {
 
 // N/core/board.py:23-56
 NR_DEV Nb neighbour(const KGame& g, const Hdr& h, const Env& e, int32_t cell, int32_t direction) {
-    const int32_t x = floor_mod(cell, g.W), y = floor_div(cell, g.W);
+    const int32_t x = cell_x(g, cell), y = cell_y(g, cell);
     const int32_t known = clampi(direction, 0, 3);
     const int32_t nx = x + dir_dx(known), ny = y + dir_dy(known);
     const bool on = direction >= 0 && direction < 4 && nx >= 0 && nx < g.W && ny >= 0 && ny < g.H;
@@ -548,8 +553,8 @@ NR_DEV bool can_execute(const KGame& g, const Hdr& h, const Env& e, int32_t slot
             if (occ == kAbsent) return false;
             const int32_t target_owner = e.owner[gidx(occ, g.E)];
             const int32_t range = tabv(h, F_RANGE, actor);
-            const int32_t dx = floor_mod(target, g.W) - floor_mod(cell, g.W);
-            const int32_t dy = floor_div(target, g.W) - floor_div(cell, g.W);
+            const int32_t dx = cell_x(g, target) - cell_x(g, cell);
+            const int32_t dy = cell_y(g, target) - cell_y(g, cell);
             return (flags & FL_ATTACK) && target_owner >= 0 && target_owner != owner &&
                    wadd(wmul(dx, dx), wmul(dy, dy)) <= wmul(range, range);
         }
@@ -1196,7 +1201,7 @@ NR_DEV Row legality_row(const KGame& g, const Hdr& h, const Env& e, int32_t slot
     const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
     set_bit(r, kKindNone);
     uint32_t produce_types = 0u;
-    const int32_t x = floor_mod(cell, g.W), yy = floor_div(cell, g.W);
+    const int32_t x = cell_x(g, cell), yy = cell_y(g, cell);
 #pragma unroll
     for (int32_t d = 0; d < 4; ++d) {
         const int32_t nx = x + dir_dx(d), ny = yy + dir_dy(d);
@@ -1318,8 +1323,8 @@ NR_DEV void decode_row(const KGame& g, const Env& e, int32_t p, bool available, 
     int32_t target = kAbsent;
     if (kind == kKindAttack) {
         const int32_t cell = e.cell[g.N + p];
-        const int32_t tx = wadd(floor_mod(cell, g.W), floor_mod(a[6], g.side) - g.radius);
-        const int32_t ty = wadd(floor_div(cell, g.W), floor_div(a[6], g.side) - g.radius);
+        const int32_t tx = wadd(cell_x(g, cell), floor_mod(a[6], g.side) - g.radius);
+        const int32_t ty = wadd(cell_y(g, cell), floor_div(a[6], g.side) - g.radius);
         if (tx >= 0 && tx < g.W && ty >= 0 && ty < g.H) target = ty * g.W + tx;
     }
     at<int8_t>(e, y.c_kind)[p] = (int8_t)(available ? canon_kind(kind) : kAbsent);
@@ -1359,12 +1364,12 @@ NR_DEV void stamp_visibility(const KGame& g, const Hdr& h, const Env& e, int lan
         const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
         if (dy < -r || dy > r) continue;
         const int32_t cell = e.cell[s];
-        const int32_t cy = floor_div(cell, g.W) + dy;
+        const int32_t cy = cell_y(g, cell) + dy;
         if (cy < 0 || cy >= g.H) continue;
         const int32_t rem = r * r - dy * dy;
         int32_t hw = r;
         while (hw * hw > rem) --hw;
-        const int32_t cx = floor_mod(cell, g.W);
+        const int32_t cx = cell_x(g, cell);
         const int32_t x0 = cx - hw < 0 ? 0 : cx - hw;
         const int32_t x1 = cx + hw >= g.W ? g.W - 1 : cx + hw;
         if (x0 > x1) continue;

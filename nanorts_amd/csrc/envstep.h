@@ -341,7 +341,7 @@ NR_DEV Row legality_row_bm(const KGame& g, const Hdr& h, const Env& e, int32_t s
     for (int32_t t = 0; t < g.T; ++t)
         if (balance >= tabv(h, F_COST, t)) affordable |= 1u << t;
     const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
-    const int32_t x = floor_mod(cell, g.W), yy = floor_div(cell, g.W);
+    const int32_t x = cell_x(g, cell), yy = cell_y(g, cell);
     const int32_t words = g.seen_words, plane = g.H * words;
     AS3 const uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
     // 3-bit windows (x-1 .. x+1) of the rows above, at and below the unit
@@ -382,15 +382,28 @@ NR_DEV Row legality_row_bm(const KGame& g, const Hdr& h, const Env& e, int32_t s
         const int32_t reach = imin(range, g.radius);
         AS3 const uint32_t* enemy = bm + (2 - owner) * plane;
         uint64_t att = 0;
-        for (int32_t dy = -reach; dy <= reach; ++dy) {
-            const int32_t ty = yy + dy;
-            if (ty < 0 || ty >= g.H) continue;
-            const int32_t rem = range * range - dy * dy;
-            int32_t hw = reach;
-            while (hw * hw > rem) --hw;
-            const uint32_t span = ((1u << (2 * hw + 1)) - 1u) << (reach - hw);
-            const uint32_t bits = row_window(enemy + ty * words, words, x - reach, 2 * reach + 1) & span;
-            att |= (uint64_t)bits << ((g.radius + dy) * g.side + g.radius - reach);
+        if (g.fast_obs && range >= 0 && range <= g.disk_r) {
+            // rows of the attack disk from the disk table, clipped to the window
+            AS3 const uint32_t* disk = h.disk + range * (2 * g.disk_r + 1) + g.disk_r;
+            const uint32_t window = (2u << (2 * reach)) - 1u;
+            for (int32_t dy = -g.radius; dy <= g.radius; ++dy) {
+                const int32_t ty = yy + dy;
+                if (dy < -reach || dy > reach || ty < 0 || ty >= g.H) continue;
+                const uint32_t span = (disk[dy] >> (g.disk_r - reach)) & window;
+                const uint32_t bits = row_window(enemy + ty * words, words, x - reach, 2 * reach + 1) & span;
+                att |= (uint64_t)bits << ((g.radius + dy) * g.side + g.radius - reach);
+            }
+        } else {
+            for (int32_t dy = -reach; dy <= reach; ++dy) {
+                const int32_t ty = yy + dy;
+                if (ty < 0 || ty >= g.H) continue;
+                const int32_t rem = range * range - dy * dy;
+                int32_t hw = reach;
+                while (hw * hw > rem) --hw;
+                const uint32_t span = ((1u << (2 * hw + 1)) - 1u) << (reach - hw);
+                const uint32_t bits = row_window(enemy + ty * words, words, x - reach, 2 * reach + 1) & span;
+                att |= (uint64_t)bits << ((g.radius + dy) * g.side + g.radius - reach);
+            }
         }
         if (att != 0ull) {
             r.w[0] |= 1u << kKindAttack;
@@ -422,7 +435,7 @@ NR_DEV void observe_all(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             if (e.birth[s] == kAbsent) continue;
             const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
             const int32_t cell = e.cell[s];
-            const int32_t cx = floor_mod(cell, g.W), cy = floor_div(cell, g.W);
+            const int32_t cx = cell_x(g, cell), cy = cell_y(g, cell);
             AS3 uint32_t* mine = seen + (i / g.C) * plane;
             int32_t hw = r;
             for (int32_t dy = 0; dy <= r; ++dy) {

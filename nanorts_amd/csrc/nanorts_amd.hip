@@ -127,11 +127,17 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
 
     Layout& y = g.lay;
     const int32_t E = g.E, C2 = 2 * g.C, cells = g.cells;
-    g.fast_obs = (g.W % 4 == 0 && g.sight_max <= 15) ? 1 : 0;
+    g.disk_r = g.sight_max;
+    for (int t = 0; t < g.T; ++t)
+        if (game->attack_range[t] > g.disk_r) g.disk_r = game->attack_range[t];
+    g.fast_obs = (g.W % 4 == 0 && g.disk_r <= 15) ? 1 : 0;
+    g.wshift = -1;
+    for (int b = 0; b < 16; ++b)
+        if ((1 << b) == g.W) g.wshift = b;
     y.o_seg = F_COUNT * 8 * 4;
     y.o_terrain = y.o_seg + 16 * (int32_t)sizeof(Seg);
     y.o_disk = align16(y.o_terrain + cells);
-    y.hdr_bytes = align16(y.o_disk + (g.fast_obs ? (g.sight_max + 1) * (2 * g.sight_max + 1) * 4 : 0));
+    y.hdr_bytes = align16(y.o_disk + (g.fast_obs ? (g.disk_r + 1) * (2 * g.disk_r + 1) * 4 : 0));
     int32_t o = 0;
     auto take = [&o](int32_t bytes) {
         const int32_t at = o;
@@ -548,11 +554,42 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         fold_in(ke0, ke1, (uint32_t)step);
         fold_in(ke0, ke1, (uint32_t)(env0 + l));
         AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
+        // draw words: with n <= 32 the two threefry blocks of a position run
+        // on two lanes at once; otherwise each lane computes both
+        const bool paired = n <= kWave / 2;
+        const bool narrow = fast && g.seen_words == 1;
+        uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
+        if (paired) {
+            const int32_t u = lane >> 1;
+            uint32_t dx0 = u < n ? (uint32_t)av[u] : 0u, dx1 = (uint32_t)(lane & 1);
+            threefry(ke0, ke1, dx0, dx1);
+            // every lane active: lane u takes lanes 2u and 2u + 1
+            pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
+            pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
+            pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
+            pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
+        }
         for (int32_t i = lane; i < n; i += kWave) {
             const int32_t p = av[i];
-            const Row r = legality_row_bm(g, hdr, e, g.N + p);
+            const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p) : legality_row_bm(g, hdr, e, g.N + p);
+            uint32_t words[4];
+            if (paired) {
+                words[0] = pw0;
+                words[1] = pw1;
+                words[2] = pw2;
+                words[3] = pw3;
+            } else {
+                uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
+                threefry(ke0, ke1, w0, w1);
+                threefry(ke0, ke1, w2, w3);
+                words[0] = w0;
+                words[1] = w1;
+                words[2] = w2;
+                words[3] = w3;
+            }
             int32_t a[7];
-            sample_row_fast(g, r, ke0, ke1, p, a);
+            if (g.T <= 8) sample_row_words8(g, r, words, a);
+            else sample_row_words(g, r, words, a);
             if (out.actions) {
                 int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
 #pragma unroll

@@ -41,17 +41,14 @@ NR_DEV int32_t select_bit(uint64_t m, int32_t k) {
     return pos;
 }
 
-// sample_row with the select above (same draws, same result).
-NR_DEV void sample_row_fast(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1, int32_t p, int32_t a[7]) {
+// sample_row with the select above (same draws, same result), given the
+// position's four draw words threefry(k_env, (p, 0)) ++ threefry(k_env, (p, 1)).
+NR_DEV void sample_row_words(const KGame& g, const Row& r, const uint32_t words[4], int32_t a[7]) {
     if (only_none(r)) {
 #pragma unroll
         for (int f = 0; f < 7; ++f) a[f] = 0;
         return;
     }
-    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
-    threefry(ke0, ke1, w0, w1);
-    threefry(ke0, ke1, w2, w3);
-    const uint32_t words[4] = {w0, w1, w2, w3};
     const int32_t lo[7] = {0, 6, 10, 14, 18, 22, 22 + g.T};
     const int32_t wid[7] = {6, 4, 4, 4, 4, g.T, g.O};
 #pragma unroll
@@ -61,6 +58,138 @@ NR_DEV void sample_row_fast(const KGame& g, const Row& r, uint32_t ke0, uint32_t
         const int32_t count = popc(m);
         a[f] = count > 0 ? select_bit(m, (int32_t)((hh * (uint32_t)count) >> 16)) : 0;
     }
+}
+
+// k-th set bit of an 8-bit mask (more than k bits set), by halving.
+NR_DEV int32_t select_bit8(uint32_t v, int32_t k) {
+    int32_t pos = 0;
+    int32_t c = __popc(v & 15u);
+    if (k >= c) {
+        k -= c;
+        v >>= 4;
+        pos = 4;
+    }
+    c = __popc(v & 3u);
+    if (k >= c) {
+        k -= c;
+        v >>= 2;
+        pos += 2;
+    }
+    return pos + ((k >= (int32_t)(v & 1u)) ? 1 : 0);
+}
+
+// sample_row_words for T <= 8 and 22 + T <= 32: the first six factors lie
+// in word 0 and select within 8 bits.
+NR_DEV void sample_row_words8(const KGame& g, const Row& r, const uint32_t words[4], int32_t a[7]) {
+    if (only_none(r)) {
+#pragma unroll
+        for (int f = 0; f < 7; ++f) a[f] = 0;
+        return;
+    }
+    const int32_t lo[6] = {0, 6, 10, 14, 18, 22};
+#pragma unroll
+    for (int f = 0; f < 6; ++f) {
+        const int32_t wid = f == 0 ? 6 : (f == 5 ? g.T : 4);
+        const uint32_t hh = (words[f >> 1] >> (16 * (f & 1))) & 0xFFFFu;
+        const uint32_t m = (r.w[0] >> lo[f]) & ((1u << wid) - 1u);
+        const int32_t count = __popc(m);
+        a[f] = count > 0 ? select_bit8(m, (int32_t)((hh * (uint32_t)count) >> 16)) : 0;
+    }
+    const uint32_t hh = words[3] & 0xFFFFu;  // factor 6: low half of word 3
+    const uint64_t m = row_bits(r, 22 + g.T, g.O);
+    const int32_t count = popc(m);
+    a[6] = count > 0 ? select_bit(m, (int32_t)((hh * (uint32_t)count) >> 16)) : 0;
+}
+
+// legality_row_bm for boards of at most 32 columns (one bitmap word per
+// row) with the disk table: the four neighbours and the attack window come
+// from whole-row words.  Same bits as legality_row_bm.
+NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t slot) {
+    Row r;
+    r.w[0] = r.w[1] = r.w[2] = 0u;
+    if (e.birth[slot] == kAbsent) return r;
+    const int32_t owner = e.owner[slot];
+    if (owner != 0 && owner != 1) return legality_row(g, h, e, slot);
+    const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
+    const int32_t carried = e.carried[slot];
+    const int32_t cell = e.cell[slot];
+    const int32_t flags = tabv(h, F_FLAGS, actor);
+    const int32_t balance = e.sc[S_RES0 + owner];
+    uint32_t affordable = 0u;
+    for (int32_t t = 0; t < g.T; ++t)
+        if (balance >= tabv(h, F_COST, t)) affordable |= 1u << t;
+    const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
+    const int32_t x = cell_x(g, cell), yy = cell_y(g, cell);
+    const int32_t H = g.H;
+    AS3 const uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
+    AS3 const uint32_t* blk = bm;
+    AS3 const uint32_t* res = bm + 3 * H;
+    AS3 const uint32_t* stk = bm + (4 + owner) * H;
+    const bool has_up = yy - 1 >= 0 && yy - 1 < H, has_dn = yy + 1 >= 0 && yy + 1 < H;
+    const bool has_mid = yy >= 0 && yy < H;
+    const int32_t ru = has_up ? yy - 1 : 0, rd = has_dn ? yy + 1 : 0, rm = has_mid ? yy : 0;
+    const uint32_t b_up = has_up ? blk[ru] : 0xFFFFFFFFu, b_dn = has_dn ? blk[rd] : 0xFFFFFFFFu;
+    const uint32_t b_mid = has_mid ? blk[rm] : 0xFFFFFFFFu;
+    const uint32_t r_up = has_up ? res[ru] : 0u, r_dn = has_dn ? res[rd] : 0u, r_mid = has_mid ? res[rm] : 0u;
+    const uint32_t s_up = has_up ? stk[ru] : 0u, s_dn = has_dn ? stk[rd] : 0u, s_mid = has_mid ? stk[rm] : 0u;
+    // x - 1 .. x + 1 of the middle rows: bit 0 left, bit 2 right; off the
+    // board is blocked and holds nothing
+    const bool inx = x >= 0 && x < g.W;
+    const uint64_t outside = ~0ull << (g.W + 1);
+    const uint32_t bw = inx ? (uint32_t)(((((uint64_t)b_mid << 1) | 1ull | outside) >> x) & 7ull) : 7u;
+    const uint32_t rw = inx ? (uint32_t)((((uint64_t)r_mid << 1) >> x) & 7ull) : 0u;
+    const uint32_t sw = inx ? (uint32_t)((((uint64_t)s_mid << 1) >> x) & 7ull) : 0u;
+    const uint32_t xb = inx ? (uint32_t)x : 0u;
+    const uint32_t bu = inx ? (b_up >> xb) & 1u : 1u, bd = inx ? (b_dn >> xb) & 1u : 1u;
+    const uint32_t blocked4 = bu | (((bw >> 2) & 1u) << 1) | (bd << 2) | ((bw & 1u) << 3);
+    const uint32_t free4 = ~blocked4 & 15u;
+    const uint32_t res4 = inx ? (((r_up >> xb) & 1u) | (((rw >> 2) & 1u) << 1) | (((r_dn >> xb) & 1u) << 2) |
+                                 ((rw & 1u) << 3))
+                              : 0u;
+    const uint32_t stk4 = inx ? (((s_up >> xb) & 1u) | (((sw >> 2) & 1u) << 1) | (((s_dn >> xb) & 1u) << 2) |
+                                 ((sw & 1u) << 3))
+                              : 0u;
+    r.w[0] = 1u;  // NONE
+    if (flags & FL_MOVE) r.w[0] |= free4 << 6;
+    if ((flags & FL_HARVEST) && carried == 0) r.w[0] |= res4 << 10;
+    if ((flags & FL_HARVEST) && carried > 0) r.w[0] |= stk4 << 14;
+    if (types != 0u) r.w[0] |= free4 << 18;
+    const uint32_t produce_types = free4 != 0u ? types : 0u;
+    r.w[0] |= produce_types << 22;
+    r.w[0] |= ((r.w[0] >> 6) & 15u ? 1u : 0u) << kKindMove;
+    r.w[0] |= ((r.w[0] >> 10) & 15u ? 1u : 0u) << kKindHarvest;
+    r.w[0] |= ((r.w[0] >> 14) & 15u ? 1u : 0u) << kKindReturn;
+    r.w[0] |= (produce_types ? 1u : 0u) << kKindProduce;
+    if (flags & FL_ATTACK) {
+        const int32_t range = tabv(h, F_RANGE, actor);
+        const int32_t reach = imin(range, g.radius);
+        AS3 const uint32_t* enemy = bm + (2 - owner) * H;
+        uint64_t att = 0;
+        if (range >= 0 && range <= g.disk_r && inx) {
+            AS3 const uint32_t* disk = h.disk + range * (2 * g.disk_r + 1) + g.disk_r;
+            const uint32_t window = (2u << (2 * reach)) - 1u;
+            const int32_t left = x - reach;
+            for (int32_t dy = -g.radius; dy <= g.radius; ++dy) {
+                const int32_t ty = yy + dy;
+                if (dy < -reach || dy > reach || ty < 0 || ty >= H) continue;
+                const uint32_t row = enemy[ty];
+                const uint32_t span = (disk[dy] >> (g.disk_r - reach)) & window;
+                const uint32_t bits = (left >= 0 ? (row >> left) : (row << (-left))) & span;
+                att |= (uint64_t)bits << ((g.radius + dy) * g.side + g.radius - reach);
+            }
+        } else {
+            // general window (never taken for the shipped unit tables)
+            return legality_row_bm(g, h, e, slot);
+        }
+        if (att != 0ull) {
+            r.w[0] |= 1u << kKindAttack;
+            const int32_t first = 22 + g.T;  // < 32
+            r.w[0] |= (uint32_t)(att << first);
+            r.w[1] |= (uint32_t)(att >> (32 - first));
+            r.w[2] |= (uint32_t)(att >> (64 - first));
+        }
+    }
+    return r;
 }
 
 // Pass over the slots: occupant words, available list, unit list.
@@ -109,17 +238,51 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
     wave_sync();
 }
 
-// Sight disks of both players into seen[2][H][words].
+// Sight disks of both players into seen[2][H][words].  With H <= 32 a lane
+// takes (unit k, row) for U = 64 / H units at a time and ORs the unit's disk
+// row into a per-lane accumulator of its player; the U partial rows are
+// OR-ed across lanes at the end, so the bitmap is written once, without
+// atomics.  Taller boards stamp (unit, dy) rows with LDS atomics.
 NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);
     const int32_t words = g.seen_words, plane = g.H * words;
-    for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;
-    wave_sync();
     const int32_t nunits = uni(e.sc[S_NUNITS]);
     AS3 const int16_t* units = at<int16_t>(e, y.b_units);
-    const int32_t R = g.sight_max, span = 2 * R + 1;
+    const int32_t R = g.disk_r, span = 2 * R + 1;
+    if (g.H <= 32 && words == 1) {
+        const int32_t U = kWave / g.H;
+        const int32_t k = lane / g.H, row = lane - k * g.H;
+        const uint32_t rowmask = g.W >= 32 ? 0xFFFFFFFFu : ((1u << g.W) - 1u);
+        uint32_t acc0 = 0u, acc1 = 0u;
+        for (int32_t base = 0; base < nunits; base += U) {
+            const int32_t i = base + k;
+            if (k >= U || i >= nunits) continue;
+            const int32_t s = units[i];
+            const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
+            const int32_t cell = e.cell[s];
+            const int32_t dy = row - cell_y(g, cell);
+            if (dy < -r || dy > r) continue;
+            const uint64_t m = h.disk[r * span + dy + R];
+            const int32_t x0 = cell_x(g, cell) - R;
+            const uint32_t bits = (uint32_t)(x0 >= 0 ? m << x0 : m >> (-x0)) & rowmask;
+            if ((s - g.N) >= g.C) acc1 |= bits;
+            else acc0 |= bits;
+        }
+        for (int32_t j = 1; j < U; ++j) {
+            acc0 |= (uint32_t)__shfl((int)acc0, lane + j * g.H, kWave);
+            acc1 |= (uint32_t)__shfl((int)acc1, lane + j * g.H, kWave);
+        }
+        if (lane < g.H) {
+            seen[lane] = acc0;
+            seen[plane + lane] = acc1;
+        }
+        wave_sync();
+        return;
+    }
+    for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;
+    wave_sync();
     for (int32_t base = 0; base < nunits; base += kWave) {
         const int32_t i = base + lane;
         int32_t r = -1, cx = 0, cy = 0;
@@ -128,8 +291,8 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
             const int32_t s = units[i];
             r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
             const int32_t cell = e.cell[s];
-            cx = floor_mod(cell, g.W);
-            cy = floor_div(cell, g.W);
+            cx = cell_x(g, cell);
+            cy = cell_y(g, cell);
             mine = seen + ((s - g.N) >= g.C ? plane : 0);
         }
         AS3 const uint32_t* disk = h.disk + (r < 0 ? 0 : r) * span;
