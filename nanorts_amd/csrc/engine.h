@@ -73,6 +73,7 @@ enum : int {
     S_NAV,    // available units listed by summarize
     S_IRREG,  // 1 when an available unit holds a pending order
     S_NUNITS, // active owned units listed by summarize
+    S_NA,     // pending MOVE / PRODUCE entries listed by summarize
     S_COUNT = 20
 };
 

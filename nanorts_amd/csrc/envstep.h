@@ -49,8 +49,10 @@ NR_DEV int32_t compact_available(const KGame& g, const Env& e_in, int lane, bool
 
 // Admission over the n available units listed by compact_available, whose
 // canonical commands are staged in the command arrays.
+// With `listed`, the summary of the state (rollout.h) already listed the
+// entries and folded their preconditions into `irregular`.
 NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, uint32_t key0, uint32_t key1,
-                      bool count_events, int32_t n, bool irregular, bool known_legal) {
+                      bool count_events, int32_t n, bool irregular, bool known_legal, bool listed = false) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     if (irregular || n > kWave) return false;
@@ -65,7 +67,8 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
     AS3 int16_t* list = at<int16_t>(e, y.a_list);
     int32_t nA = 0;
     bool bad = false;
-    for (int32_t base = 0; base < g.E; base += kWave) {
+    if (listed) nA = uni(e.sc[S_NA]);
+    for (int32_t base = 0; base < (listed ? 0 : g.E); base += kWave) {
         const int32_t s = base + lane;
         bool entry = false;
         if (s < g.E) {
@@ -145,11 +148,15 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
         conflicting = claims_position(kind1) || cost1 != 0;
     }
     // Java admission order (_ordered_requests :200-221): player, then birth.
-    int32_t rank = 0;
+    // crank orders the requests that can conflict among themselves.
+    const uint64_t conflicting_lanes = ballot(conflicting);
+    int32_t rank = 0, crank = 0;
     for (int32_t j = 0; j < n; ++j) {
         const int32_t plj = __builtin_amdgcn_readlane(pl, j);
         const int32_t bj = __builtin_amdgcn_readlane(birth, j);
-        rank += (plj < pl) || (plj == pl && (bj < birth || (bj == birth && j < lane)));
+        const bool before = (plj < pl) || (plj == pl && (bj < birth || (bj == birth && j < lane)));
+        rank += before;
+        crank += before && ((conflicting_lanes >> j) & 1ull);
     }
     // Sequential conflict resolution over the requests that can conflict.
     const int32_t bal0 = uni(e.sc[S_RES0]), bal1 = uni(e.sc[S_RES1]);
@@ -159,10 +166,9 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
     int32_t posB = 0, costB = 0, playerB = 0, durB = 0, rlB = 0, nB = 0;
     bool liveB = false;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    const uint64_t conflicting_lanes = ballot(conflicting);
-    for (int32_t k = 0; k < n && conflicting_lanes != 0ull; ++k) {
-        const int32_t li = (int32_t)__builtin_ctzll(ballot(lane < n && rank == k));
-        if (((conflicting_lanes >> li) & 1ull) == 0ull) continue;
+    const int32_t nconf = popc(conflicting_lanes);
+    for (int32_t k = 0; k < nconf; ++k) {
+        const int32_t li = (int32_t)__builtin_ctzll(ballot(conflicting && crank == k));
         const int32_t rkind = __builtin_amdgcn_readlane(kind1, li);
         const int32_t rnone = __builtin_amdgcn_readlane(none1, li);
         const int32_t rreq = __builtin_amdgcn_readlane(req, li);

@@ -609,7 +609,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         }
         wave_sync();
         // env.step: core.step keyed by fold_in(env root, episode)
-        if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true)) {
+        if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
             if (fast) mark_unavailable(g, e, lane);
             int32_t n_rank = 0;
             const int32_t issued = order_requests(g, e, lane, &n_rank);

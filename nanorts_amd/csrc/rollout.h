@@ -200,12 +200,26 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
     AS3 uint8_t* ofl = at<uint8_t>(e, y.o_fl);
     AS3 int16_t* av = at<int16_t>(e, y.a_av);
     AS3 int16_t* units = at<int16_t>(e, y.b_units);
-    int32_t nav = 0, nunits = 0;
+    AS3 int16_t* entries = at<int16_t>(e, y.a_list);
+    const int32_t time = uni(e.sc[S_TIME]);
+    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    int32_t nav = 0, nunits = 0, nA = 0;
     bool odd = false;
     for (int32_t base = 0; base < g.E; base += kWave) {
         const int32_t s = base + lane;
-        bool alive = false, available = false;
+        bool alive = false, available = false, entry = false;
         if (s < g.E) {
+            // pending entries for the env-path admission: MOVE / PRODUCE
+            // pending from earlier cycles, in slot order (see admit_env)
+            const int32_t k = e.pkind[s];
+            if (k != kAbsent) {
+                const int32_t ord = e.porder[s];
+                if (s < g.N || ord == kAbsent || ord >= next_order) odd = true;
+                if (k == kKindMove || k == kKindProduce) {
+                    entry = true;
+                    if (e.pissued[s] == time) odd = true;
+                }
+            }
             alive = e.birth[s] != kAbsent;
             if (alive) {
                 const int32_t ty = e.utype[s];
@@ -222,6 +236,9 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
             }
         }
         const bool unit = alive && s >= g.N;
+        const uint64_t me = ballot(entry);
+        if (entry && nA + count_below(me) < kWave) entries[nA + count_below(me)] = (int16_t)s;
+        nA += popc(me);
         const uint64_t ma = ballot(available);
         if (available) av[nav + count_below(ma)] = (int16_t)(s - g.N);
         nav += popc(ma);
@@ -229,10 +246,12 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
         if (unit) units[nunits + count_below(mu)] = (int16_t)s;
         nunits += popc(mu);
     }
-    const bool irregular = ballot(odd) != 0ull;
+    // irregular: the env-path admission does not apply (admit_env)
+    const bool irregular = ballot(odd) != 0ull || nA > kWave || next_order > 0x7fffffff - kWave;
     if (lane == 0) {
         e.sc[S_NAV] = nav;
         e.sc[S_NUNITS] = nunits;
+        e.sc[S_NA] = nA;
         e.sc[S_IRREG] = irregular ? 1 : 0;
     }
     wave_sync();
