@@ -273,6 +273,17 @@ NR_DEV Env refresh(const KGame& g, const Env& e) {
     return env_view(g, (AS3 uint8_t*)(uintptr_t)b);
 }
 
+// The game read again from the kernel-argument segment, where a kernel that
+// takes KGame as its first argument finds it at offset 0.  Fields used after
+// this call are reloaded (scalar loads) instead of being kept live in scalar
+// registers across a whole kernel, which would spill them to vector lanes.
+typedef const __attribute__((address_space(4))) KGame* KGameArg;
+NR_DEV const KGame& fresh_game() {
+    KGameArg p = (KGameArg)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const KGame*)p;
+}
+
 template <typename T>
 NR_DEV AS3 T* at(const Env& e, int32_t offset) {
     return (AS3 T*)(e.base + offset);

@@ -524,118 +524,138 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
 // the per-cycle summary (rollout.h) each cycle is: sample from the masks of
 // the summarised state -> decode -> core.step -> finish (reward, done,
 // auto-reset) -> summarise the new state, which writes its observation.
+// Each phase of the cycle takes a fresh view of the game (fresh_game), so
+// the game's fields are reloaded per phase rather than held across the loop.
 __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts_state s, uint32_t key0, uint32_t key1, int32_t step0,
                           int32_t steps, int32_t partial, int64_t env0, nanorts_rollout_results out) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    const int32_t owned = 2 * g.C;
-    const nanorts_env_results none = {};
     const bool fast = g.fast_obs && ((((uintptr_t)out.feature_maps) & 7u) == 0);
-    const int64_t per = (int64_t)g.cells * 6;
     if (fast) summarize(g, hdr, e, lane, partial != 0, nullptr, nullptr, nullptr, nullptr);
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const Env e0 = e;
     for (int32_t t = 0; t < steps; ++t) {
-        const Env e = refresh(g, e0);
         const int32_t step = step0 + t;
-        // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
         bool irregular = false;
         int32_t n;
-        if (fast) {
-            n = uni(e.sc[S_NAV]);
-            irregular = uni(e.sc[S_IRREG]) != 0;
-        } else {
-            n = compact_available(g, e, lane, &irregular);
-            build_bitmaps(g, hdr, e, lane);
-        }
-        uint32_t ke0 = key0, ke1 = key1;
-        fold_in(ke0, ke1, (uint32_t)step);
-        fold_in(ke0, ke1, (uint32_t)(env0 + l));
-        AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
-        // draw words: with n <= 32 the two threefry blocks of a position run
-        // on two lanes at once; otherwise each lane computes both
-        const bool paired = n <= kWave / 2;
-        const bool narrow = fast && g.seen_words == 1;
-        uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
-        if (paired) {
-            const int32_t u = lane >> 1;
-            uint32_t dx0 = u < n ? (uint32_t)av[u] : 0u, dx1 = (uint32_t)(lane & 1);
-            threefry(ke0, ke1, dx0, dx1);
-            // every lane active: lane u takes lanes 2u and 2u + 1
-            pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
-            pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
-            pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
-            pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
-        }
-        for (int32_t i = lane; i < n; i += kWave) {
-            const int32_t p = av[i];
-            const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p) : legality_row_bm(g, hdr, e, g.N + p);
-            uint32_t words[4];
-            if (paired) {
-                words[0] = pw0;
-                words[1] = pw1;
-                words[2] = pw2;
-                words[3] = pw3;
+        {
+            // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
+            const KGame& g = fresh_game();
+            const Env e = refresh(g, e0);
+            const int32_t owned = 2 * g.C;
+            if (fast) {
+                n = uni(e.sc[S_NAV]);
+                irregular = uni(e.sc[S_IRREG]) != 0;
             } else {
-                uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
-                threefry(ke0, ke1, w0, w1);
-                threefry(ke0, ke1, w2, w3);
-                words[0] = w0;
-                words[1] = w1;
-                words[2] = w2;
-                words[3] = w3;
+                n = compact_available(g, e, lane, &irregular);
+                build_bitmaps(g, hdr, e, lane);
             }
-            int32_t a[7];
-            if (g.T <= 8) sample_row_words8(g, r, words, a);
-            else sample_row_words(g, r, words, a);
+            uint32_t ke0 = key0, ke1 = key1;
+            fold_in(ke0, ke1, (uint32_t)step);
+            fold_in(ke0, ke1, (uint32_t)(env0 + l));
+            AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
+            // draw words: with n <= 32 the two threefry blocks of a position run
+            // on two lanes at once; otherwise each lane computes both
+            const bool paired = n <= kWave / 2;
+            const bool narrow = fast && g.seen_words == 1;
+            uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
+            if (paired) {
+                const int32_t u = lane >> 1;
+                uint32_t dx0 = u < n ? (uint32_t)av[u] : 0u, dx1 = (uint32_t)(lane & 1);
+                threefry(ke0, ke1, dx0, dx1);
+                // every lane active: lane u takes lanes 2u and 2u + 1
+                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
+                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
+                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
+                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
+            }
+            for (int32_t i = lane; i < n; i += kWave) {
+                const int32_t p = av[i];
+                const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p) : legality_row_bm(g, hdr, e, g.N + p);
+                uint32_t words[4];
+                if (paired) {
+                    words[0] = pw0;
+                    words[1] = pw1;
+                    words[2] = pw2;
+                    words[3] = pw3;
+                } else {
+                    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
+                    threefry(ke0, ke1, w0, w1);
+                    threefry(ke0, ke1, w2, w3);
+                    words[0] = w0;
+                    words[1] = w1;
+                    words[2] = w2;
+                    words[3] = w3;
+                }
+                int32_t a[7];
+                if (g.T <= 8) sample_row_words8(g, r, words, a);
+                else sample_row_words(g, r, words, a);
+                if (out.actions) {
+                    int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+#pragma unroll
+                    for (int f = 0; f < 7; ++f) dst[f] = a[f];
+                }
+                decode_row(g, e, p, true, a);
+            }
             if (out.actions) {
-                int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+                // unavailable rows sample all zeros
+                for (int32_t p = lane; p < owned; p += kWave) {
+                    const int32_t sl = g.N + p;
+                    if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
+                    int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
 #pragma unroll
-                for (int f = 0; f < 7; ++f) dst[f] = a[f];
+                    for (int f = 0; f < 7; ++f) dst[f] = 0;
+                }
             }
-            decode_row(g, e, p, true, a);
+            wave_sync();
         }
-        if (out.actions) {
-            // unavailable rows sample all zeros
-            for (int32_t p = lane; p < owned; p += kWave) {
-                const int32_t sl = g.N + p;
-                if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
-                int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
-#pragma unroll
-                for (int f = 0; f < 7; ++f) dst[f] = 0;
+        {
+            // env.step: core.step keyed by fold_in(env root, episode)
+            const KGame& g = fresh_game();
+            const Env e = refresh(g, e0);
+            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
+                if (fast) mark_unavailable(g, e, lane);
+                int32_t n_rank = 0;
+                const int32_t issued = order_requests(g, e, lane, &n_rank);
+                AS3 int16_t* order = at<int16_t>(e, g.lay.b_order);
+                for (int32_t i = 0; i < issued; ++i) admit_one(g, hdr, e, lane, uni(order[i]), n_rank, ek0, ek1, false);
             }
         }
-        wave_sync();
-        // env.step: core.step keyed by fold_in(env root, episode)
-        if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
-            if (fast) mark_unavailable(g, e, lane);
-            int32_t n_rank = 0;
-            const int32_t issued = order_requests(g, e, lane, &n_rank);
-            AS3 int16_t* order = at<int16_t>(e, g.lay.b_order);
-            for (int32_t i = 0; i < issued; ++i) admit_one(g, hdr, e, lane, uni(order[i]), n_rank, ek0, ek1, false);
+        {
+            const KGame& g = fresh_game();
+            const Env e = refresh(g, e0);
+            complete(g, hdr, e, lane);
+            decide_counted(e, lane);
         }
-        complete(g, hdr, e, lane);
-        decide_counted(e, lane);
-        nanorts_env_results r = none;
-        if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
-        if (out.dones) r.done = out.dones + (int64_t)t * lanes;
-        if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) {
-            ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
-            ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
-            fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+        {
+            const KGame& g = fresh_game();
+            const Env e = refresh(g, e0);
+            nanorts_env_results r = {};
+            if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
+            if (out.dones) r.done = out.dones + (int64_t)t * lanes;
+            if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) {
+                ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
+                ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
+                fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+            }
         }
-        const int64_t slot = (out.depth > 0 ? (int64_t)(t % out.depth) : 0) * lanes + l;
-        if (fast) {
-            uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
-            int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
-            summarize(g, hdr, e, lane, partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
-        } else if (out.feature_maps || out.scalars) {
-            observe_both(g, hdr, e, slot, lane, partial != 0, out.feature_maps, out.scalars);
+        {
+            const KGame& g = fresh_game();
+            const Env e = refresh(g, e0);
+            const int64_t per = (int64_t)g.cells * 6;
+            const int64_t slot = (out.depth > 0 ? (int64_t)(t % out.depth) : 0) * lanes + l;
+            if (fast) {
+                uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
+                int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
+                summarize(g, hdr, e, lane, partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+            } else if (out.feature_maps || out.scalars) {
+                observe_both(g, hdr, e, slot, lane, partial != 0, out.feature_maps, out.scalars);
+            }
         }
     }
-    store_env(g, s, l, e, lane);
+    store_env(fresh_game(), s, l, e, lane);
 }
 
 // Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
