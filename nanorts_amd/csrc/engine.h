@@ -1322,9 +1322,10 @@ NR_DEV void sample_row(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1,
 }
 
 // decode_actions for one row (N/adapters/jaxmarl/actions.py:61-84,
-// N/adapters/factors.py:117-151), stored in canonical command form.
-NR_DEV void decode_row(const KGame& g, const Env& e, int32_t p, bool available, const int32_t a[7]) {
-    const Layout& y = g.lay;
+// N/adapters/factors.py:117-151) of an available unit, in canonical command
+// form.
+NR_DEV void decode_values(const KGame& g, const Env& e, int32_t p, const int32_t a[7], int32_t* kind_out,
+                          int32_t* dir_out, int32_t* ptype_out, int32_t* target_out, int32_t* none_out) {
     const int32_t kind = a[0];
     int32_t dir = kAbsent;
     if (kind == kKindMove) dir = a[1];
@@ -1339,11 +1340,24 @@ NR_DEV void decode_row(const KGame& g, const Env& e, int32_t p, bool available, 
         const int32_t ty = wadd(cell_y(g, cell), floor_div(a[6], g.side) - g.radius);
         if (tx >= 0 && tx < g.W && ty >= 0 && ty < g.H) target = ty * g.W + tx;
     }
-    at<int8_t>(e, y.c_kind)[p] = (int8_t)(available ? canon_kind(kind) : kAbsent);
-    at<int8_t>(e, y.c_dir)[p] = (int8_t)(available ? canon_dir(dir) : kAbsent);
-    at<int8_t>(e, y.c_ptype)[p] = (int8_t)(available ? canon_ptype(ptype, g.T) : kAbsent);
+    *kind_out = canon_kind(kind);
+    *dir_out = canon_dir(dir);
+    *ptype_out = canon_ptype(ptype, g.T);
+    *target_out = target;
+    *none_out = kind == kKindNone ? 1 : 0;
+}
+
+// decode_row: the same values staged in the command arrays (ABSENT when the
+// unit is not available).
+NR_DEV void decode_row(const KGame& g, const Env& e, int32_t p, bool available, const int32_t a[7]) {
+    const Layout& y = g.lay;
+    int32_t kind, dir, ptype, target, none;
+    decode_values(g, e, p, a, &kind, &dir, &ptype, &target, &none);
+    at<int8_t>(e, y.c_kind)[p] = (int8_t)(available ? kind : kAbsent);
+    at<int8_t>(e, y.c_dir)[p] = (int8_t)(available ? dir : kAbsent);
+    at<int8_t>(e, y.c_ptype)[p] = (int8_t)(available ? ptype : kAbsent);
     at<int16_t>(e, y.c_target)[p] = (int16_t)(available ? target : kAbsent);
-    at<int32_t>(e, y.c_none)[p] = available ? (kind == kKindNone ? 1 : 0) : 0;
+    at<int32_t>(e, y.c_none)[p] = available ? none : 0;
     at<int16_t>(e, y.c_rank)[p] = 0;
 }
 

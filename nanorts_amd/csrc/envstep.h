@@ -47,23 +47,87 @@ NR_DEV int32_t compact_available(const KGame& g, const Env& e_in, int lane, bool
     return n;
 }
 
-// Admission over the n available units listed by compact_available, whose
-// canonical commands are staged in the command arrays.
-// With `listed`, the summary of the state (rollout.h) already listed the
-// entries and folded their preconditions into `irregular`.
-NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, uint32_t key0, uint32_t key1,
-                      bool count_events, int32_t n, bool irregular, bool known_legal, bool listed = false) {
-    const Env e = refresh(g, e_in);
+// One request per lane (lane i = the i-th available unit): _admit_one up to
+// the reservation (N/core/admission.py:242-289).
+struct Reqs {
+    int32_t p, slot, kind1, none1, req, dir, ptype, target, pos1, cost1, player1, birth, pl;
+    bool conflicting;
+};
+
+// The request fields that follow from a canonical command of slot N + p.
+NR_DEV void request_of(const KGame& g, const Hdr& h, const Env& e, int32_t p, int32_t kind0, int32_t dir, int32_t ptype,
+                       int32_t target, int32_t none0, bool known_legal, bool count_events, Reqs& q) {
     const Layout& y = g.lay;
-    if (irregular || n > kWave) return false;
+    q.p = p;
+    q.slot = g.N + p;
+    q.pl = p >= g.C ? 1 : 0;
+    q.dir = dir;
+    q.ptype = ptype;
+    q.target = target;
+    const int32_t slot = q.slot;
+    const int32_t cell = e.cell[slot];
+    const int32_t owner = e.owner[slot];
+    q.birth = e.birth[slot];
+    q.req = action_duration(g, h, e.utype[slot], kind0, none0, ptype);
+    // A command sampled from this cycle's masks is legal and unblocked:
+    // every mask factor is legal for some value of the others, and the
+    // produce factors are independent (free direction and affordable
+    // type), so the sampled combination passes is_valid.
+    const bool legal = known_legal || can_execute(g, h, e, slot, kind0, dir, target, ptype);
+    int32_t kind1 = legal ? kind0 : kKindNone;
+    int32_t none1 = legal ? none0 : q.req;
+    if (!known_legal && claims_position(kind1)) {
+        const int32_t at_ = gidx(reserved_position(g, cell, dir), g.cells);
+        if (h.terrain[at_] != 0 || e.entity[at_] != kAbsent) {
+            kind1 = kKindNone;
+            none1 = q.req;
+        }
+    }
+    if (count_events) {
+        // _count_admitted (:406-429)
+        AS3 uint32_t* ev = at<uint32_t>(e, y.b_events);
+        const int32_t pl = q.pl;
+        int32_t idx = -1;
+        if (kind1 == kKindHarvest) idx = pl;
+        else if (kind1 == kKindReturn) idx = 2 + pl;
+        else if (kind1 == kKindProduce) idx = 4 + pl * 8 + clampi(ptype, 0, g.T - 1);
+        else if (kind1 == kKindAttack) {
+            const int32_t occ = e.entity[clampi(target, 0, g.cells - 1)];
+            const int32_t towner = occ == kAbsent ? kAbsent : e.owner[clampi(occ, 0, g.E - 1)];
+            if (towner + 1 >= 0 && towner + 1 < 3) idx = 20 + pl * 3 + towner + 1;
+        }
+        if (idx >= 0) __atomic_fetch_add(&ev[idx], 1u, __ATOMIC_RELAXED);
+    }
+    q.kind1 = kind1;
+    q.none1 = none1;
+    q.cost1 = kind1 == kKindProduce ? tabv(h, F_COST, clampi(ptype, 0, g.T - 1)) : 0;
+    q.pos1 = reserved_position(g, cell, dir);
+    q.player1 = clampi(owner, 0, 1);
+    q.conflicting = claims_position(kind1) || q.cost1 != 0;
+}
+
+NR_DEV void no_request(Reqs& q) {
+    q.p = q.slot = 0;
+    q.kind1 = kAbsent;
+    q.none1 = q.req = 0;
+    q.dir = q.ptype = q.target = kAbsent;
+    q.pos1 = q.cost1 = q.player1 = q.birth = q.pl = 0;
+    q.conflicting = false;
+}
+
+// Entries that can conflict: pending MOVE / PRODUCE (the only kinds that
+// claim a position or cost resources).  Those pending at the start of the
+// cycle were issued earlier, so every conflict with them is cross-cycle and
+// they all rank before this cycle's appends; their order among themselves
+// then does not matter (N/core/reservations.py:154-192).  With `listed`, the
+// summary of the state (rollout.h) already listed them and folded their
+// preconditions into `irregular`.  Lane i < nA receives entry i.
+NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, bool listed, int32_t* nA_out,
+                          int32_t* posA, int32_t* costA, int32_t* playerA) {
+    const Layout& y = g.lay;
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
     if (next_order > 0x7fffffff - kWave) return false;
-    // Entries that can conflict: pending MOVE / PRODUCE (the only kinds that
-    // claim a position or cost resources).  Those pending at the start of
-    // the cycle were issued earlier, so every conflict with them is
-    // cross-cycle and they all rank before this cycle's appends; their order
-    // among themselves then does not matter (N/core/reservations.py:154-192).
     AS3 int16_t* list = at<int16_t>(e, y.a_list);
     int32_t nA = 0;
     bool bad = false;
@@ -88,65 +152,67 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
     }
     if (ballot(bad) != 0ull || nA > kWave) return false;
     wave_sync();
-    int32_t posA = 0, costA = 0, playerA = 0;
+    *posA = 0;
+    *costA = 0;
+    *playerA = 0;
     if (lane < nA) {
         const int32_t s = list[lane];
         const int32_t k = e.pkind[s];
-        playerA = clampi(e.owner[s], 0, 1);
-        costA = k == kKindProduce ? tabv(h, F_COST, clampi(e.pptype[s], 0, g.T - 1)) : 0;
-        posA = reserved_position(g, e.cell[s], e.pdir[s]);
+        *playerA = clampi(e.owner[s], 0, 1);
+        *costA = k == kKindProduce ? tabv(h, F_COST, clampi(e.pptype[s], 0, g.T - 1)) : 0;
+        *posA = reserved_position(g, e.cell[s], e.pdir[s]);
     }
-    // Requests, lane i = i-th available unit: _admit_one up to the
-    // reservation (N/core/admission.py:242-289), in parallel.
-    int32_t p = 0, slot = 0, kind1 = kAbsent, none1 = 0, req = 0, dir = kAbsent, ptype = kAbsent, target = kAbsent;
-    int32_t pos1 = 0, cost1 = 0, player1 = 0, birth = 0, pl = 0;
-    bool conflicting = false;
+    *nA_out = nA;
+    return true;
+}
+
+NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
+                          int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q);
+// The requests of q (built from sampled, known-legal commands) staged in
+// the command arrays for the general admission.
+NR_DEV void stage_requests(const KGame& g, const Env& e_in, int lane, int32_t n, const Reqs& q) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
     if (lane < n) {
-        p = at<int16_t>(e, y.a_av)[lane];
-        slot = g.N + p;
-        pl = p / g.C;
-        const int32_t kind0 = at<int8_t>(e, y.c_kind)[p];
-        dir = at<int8_t>(e, y.c_dir)[p];
-        ptype = at<int8_t>(e, y.c_ptype)[p];
-        target = at<int16_t>(e, y.c_target)[p];
-        const int32_t none0 = at<int32_t>(e, y.c_none)[p];
-        const int32_t cell = e.cell[slot];
-        const int32_t owner = e.owner[slot];
-        birth = e.birth[slot];
-        req = action_duration(g, h, e.utype[slot], kind0, none0, ptype);
-        // A command sampled from this cycle's masks is legal and unblocked:
-        // every mask factor is legal for some value of the others, and the
-        // produce factors are independent (free direction and affordable
-        // type), so the sampled combination passes is_valid.
-        const bool legal = known_legal || can_execute(g, h, e, slot, kind0, dir, target, ptype);
-        kind1 = legal ? kind0 : kKindNone;
-        none1 = legal ? none0 : req;
-        if (!known_legal && claims_position(kind1)) {
-            const int32_t at_ = gidx(reserved_position(g, cell, dir), g.cells);
-            if (h.terrain[at_] != 0 || e.entity[at_] != kAbsent) {
-                kind1 = kKindNone;
-                none1 = req;
-            }
-        }
-        if (count_events) {
-            // _count_admitted (:406-429)
-            AS3 uint32_t* ev = at<uint32_t>(e, y.b_events);
-            int32_t idx = -1;
-            if (kind1 == kKindHarvest) idx = pl;
-            else if (kind1 == kKindReturn) idx = 2 + pl;
-            else if (kind1 == kKindProduce) idx = 4 + pl * 8 + clampi(ptype, 0, g.T - 1);
-            else if (kind1 == kKindAttack) {
-                const int32_t occ = e.entity[clampi(target, 0, g.cells - 1)];
-                const int32_t towner = occ == kAbsent ? kAbsent : e.owner[clampi(occ, 0, g.E - 1)];
-                if (towner + 1 >= 0 && towner + 1 < 3) idx = 20 + pl * 3 + towner + 1;
-            }
-            if (idx >= 0) __atomic_fetch_add(&ev[idx], 1u, __ATOMIC_RELAXED);
-        }
-        cost1 = kind1 == kKindProduce ? tabv(h, F_COST, clampi(ptype, 0, g.T - 1)) : 0;
-        pos1 = reserved_position(g, cell, dir);
-        player1 = clampi(owner, 0, 1);
-        conflicting = claims_position(kind1) || cost1 != 0;
+        at<int8_t>(e, y.c_kind)[q.p] = (int8_t)q.kind1;
+        at<int8_t>(e, y.c_dir)[q.p] = (int8_t)q.dir;
+        at<int8_t>(e, y.c_ptype)[q.p] = (int8_t)q.ptype;
+        at<int16_t>(e, y.c_target)[q.p] = (int16_t)q.target;
+        at<int32_t>(e, y.c_none)[q.p] = q.none1;
+        at<int16_t>(e, y.c_rank)[q.p] = 0;
     }
+    wave_sync();
+}
+
+// Admission over the n available units listed by compact_available, whose
+// canonical commands are staged in the command arrays.
+NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, uint32_t key0, uint32_t key1,
+                      bool count_events, int32_t n, bool irregular, bool known_legal, bool listed = false) {
+    const Env e = refresh(g, e_in);
+    const Layout& y = g.lay;
+    if (irregular || n > kWave) return false;
+    int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
+    if (!admit_entries(g, h, e, lane, listed, &nA, &posA, &costA, &playerA)) return false;
+    Reqs q;
+    no_request(q);
+    if (lane < n) {
+        const int32_t p = at<int16_t>(e, y.a_av)[lane];
+        request_of(g, h, e, p, at<int8_t>(e, y.c_kind)[p], at<int8_t>(e, y.c_dir)[p], at<int8_t>(e, y.c_ptype)[p],
+                   at<int16_t>(e, y.c_target)[p], at<int32_t>(e, y.c_none)[p], known_legal, count_events, q);
+    }
+    admit_resolve(g, h, e, lane, key0, key1, n, nA, posA, costA, playerA, q);
+    return true;
+}
+
+// Rank, conflict resolution and pending assignment of the requests in q.
+NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
+                          int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q) {
+    const Layout& y = g.lay;
+    const int32_t time = uni(e.sc[S_TIME]);
+    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    const int32_t slot = q.slot, kind1 = q.kind1, none1 = q.none1, req = q.req, dir = q.dir, ptype = q.ptype;
+    const int32_t target = q.target, pos1 = q.pos1, cost1 = q.cost1, player1 = q.player1, birth = q.birth, pl = q.pl;
+    const bool conflicting = q.conflicting;
     // Java admission order (_ordered_requests :200-221): player, then birth.
     // crank orders the requests that can conflict among themselves.
     const uint64_t conflicting_lanes = ballot(conflicting);
@@ -266,7 +332,6 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
         if (g.strategy == NANORTS_CANCEL_ALTERNATING) e.sc[S_ALT] = alt;
     }
     wave_sync();
-    return true;
 }
 
 // core.step of the env path.

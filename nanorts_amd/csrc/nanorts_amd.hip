@@ -540,6 +540,11 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         const int32_t step = step0 + t;
         bool irregular = false;
         int32_t n;
+        // fused: the sampled commands go straight into the admission's
+        // request registers (no staging through the command arrays)
+        bool fused = false;
+        Reqs q;
+        no_request(q);
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             const KGame& g = fresh_game();
@@ -548,6 +553,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
             if (fast) {
                 n = uni(e.sc[S_NAV]);
                 irregular = uni(e.sc[S_IRREG]) != 0;
+                fused = !irregular && n <= kWave;
             } else {
                 n = compact_available(g, e, lane, &irregular);
                 build_bitmaps(g, hdr, e, lane);
@@ -597,7 +603,13 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
 #pragma unroll
                     for (int f = 0; f < 7; ++f) dst[f] = a[f];
                 }
-                decode_row(g, e, p, true, a);
+                if (fused) {
+                    int32_t kind, dir, ptype, target, none;
+                    decode_values(g, e, p, a, &kind, &dir, &ptype, &target, &none);
+                    request_of(g, hdr, e, p, kind, dir, ptype, target, none, true, false, q);
+                } else {
+                    decode_row(g, e, p, true, a);
+                }
             }
             if (out.actions) {
                 // unavailable rows sample all zeros
@@ -615,7 +627,13 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
             // env.step: core.step keyed by fold_in(env root, episode)
             const KGame& g = fresh_game();
             const Env e = refresh(g, e0);
-            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
+            int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
+            if (fused && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA)) {
+                admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
+            } else if (fused || !admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
+                // general admission; a fused cycle (which the summary's
+                // irregular flag keeps off this path) stages its requests first
+                if (fused) stage_requests(g, e, lane, n, q);
                 if (fast) mark_unavailable(g, e, lane);
                 int32_t n_rank = 0;
                 const int32_t issued = order_requests(g, e, lane, &n_rank);
