@@ -105,8 +105,9 @@ struct Layout {
     // staged words.
     int32_t c_kind, c_dir, c_ptype, c_target, c_none, c_rank;
     int32_t b_pkey, b_keys, b_tmp, b_order, b_rank;
-    int32_t m_rec, m_keys, m_tmp;
+    int32_t m_rec, m_tmp;
     int32_t v_seen, v_stage, b_units;
+    int32_t v_oseen;  // observe_all's seen bitmaps (beside its staging)
     int32_t v_words;
     int32_t a_av, a_fk, a_fn, a_list;  // env-path admission: available list, final kinds/durations, entry list
 };
@@ -995,7 +996,7 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
-    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][5] in slot order
+    AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
     int32_t n = 0;
     for (int32_t base = 0; base < g.E; base += kWave) {
         const int32_t s = base + lane;
@@ -1064,16 +1065,15 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
         }
         return;
     }
-    // more members than lanes: order through LDS keys
-    AS3 uint64_t* keys = at<uint64_t>(e, y.m_keys);
+    // more members than lanes: rank each record by (pending order, slot)
     AS3 int16_t* pos = at<int16_t>(e, y.m_tmp);
-    for (int32_t i = lane; i < n; i += kWave)
-        keys[i] = ((uint64_t)((uint32_t)rec[6 * i + 5] ^ 0x80000000u) << 32) | (uint64_t)(uint32_t)i;
-    wave_sync();
     for (int32_t i = lane; i < n; i += kWave) {
-        const uint64_t ki = keys[i];
+        const int32_t oi = rec[6 * i + 5];
         int32_t r = 0;
-        for (int32_t j = 0; j < n; ++j) r += keys[j] < ki;
+        for (int32_t j = 0; j < n; ++j) {
+            const int32_t oj = rec[6 * j + 5];
+            r += (oj < oi) || (oj == oi && j < i);
+        }
         pos[r] = (int16_t)i;
     }
     wave_sync();
@@ -1413,49 +1413,6 @@ NR_DEV bool seen_at(const KGame& g, const Env& e, int32_t c) {
     const AS3 uint32_t* seen = at<uint32_t>(e, g.lay.v_seen);
     const int32_t yy = c / g.W, x = c - yy * g.W;
     return (seen[yy * g.seen_words + (x >> 5)] >> (x & 31)) & 1u;
-}
-
-// Symbolic uint8 feature maps and scalars of one observer, written to
-// maps[H][W][6] and scalars[4] in global memory.
-NR_DEV void observe_player(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t player, bool partial,
-                           uint8_t* maps, int32_t* scalars) {
-    const Layout& y = g.lay;
-    if (partial) stamp_visibility(g, h, e, lane, player);
-    AS3 uint8_t* stage = at<uint8_t>(e, y.v_stage);
-    for (int32_t c0 = 0; c0 < g.cells; c0 += g.stage_cells) {
-        const int32_t n = imin(g.stage_cells, g.cells - c0);
-        for (int32_t i = lane; i < n; i += kWave) {
-            const int32_t c = c0 + i;
-            const int32_t occ = e.entity[c];
-            uint32_t hp = 0, carried = 0, type = 0, kind = 0, owner = 0;
-            if (occ != kAbsent) {
-                const int32_t s = clampi(occ, 0, g.E - 1);
-                hp = (uint32_t)(int32_t)e.hp[s] & 0xFFu;
-                carried = (uint32_t)e.carried[s] & 0xFFu;
-                type = (uint32_t)((int32_t)e.utype[s] + 1) & 0xFFu;
-                const int32_t pk = e.pkind[s];
-                kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
-                owner = (uint32_t)((int32_t)e.owner[s] + 1) & 0x3u;
-            }
-            if (partial && !(owner == (uint32_t)(player + 1) || seen_at(g, e, c))) hp = carried = type = kind = owner = 0;
-            const uint32_t rel = owner > 0 ? (uint32_t)((((int32_t)owner - 1 + player) & 1) + 1) : 0u;
-            AS3 uint16_t* out = (AS3 uint16_t*)(stage + i * 6);
-            out[0] = (uint16_t)(hp | (carried << 8));
-            out[1] = (uint16_t)(rel | (type << 8));
-            out[2] = (uint16_t)(kind | ((uint32_t)h.terrain[c] << 8));
-        }
-        wave_sync();
-        copy_out(maps + (size_t)c0 * 6, stage, n * 6, lane);
-        wave_sync();
-    }
-    if (lane < 4) {
-        int32_t v;
-        if (lane == 0) v = e.sc[S_RES0 + player];
-        else if (lane == 1) v = e.sc[S_RES0 + (player ^ 1)];
-        else if (lane == 2) v = e.sc[S_TIME];
-        else v = e.sc[S_ALT];
-        scalars[lane] = v;
-    }
 }
 
 }  // namespace nr

@@ -493,7 +493,7 @@ NR_DEV void observe_all(const KGame& g, const Hdr& h, const Env& e_in, int lane,
                         uint8_t* maps1, int32_t* scalars0, int32_t* scalars1) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
-    AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);  // [2][H][seen_words]
+    AS3 uint32_t* seen = at<uint32_t>(e, y.v_oseen);  // [2][H][seen_words]
     const int32_t plane = g.H * g.seen_words;
     if (partial) {
         for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;

@@ -160,48 +160,67 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_pdir = take(E);
     y.o_pptype = take(E);
     y.o_scal = take(S_COUNT * 4);
-    y.b_events = take(32 * 4);
-    y.o_bm = take(6 * g.H * g.seen_words * 4);
-    y.o_lo = take(E * 4);
-    y.o_fl = take(E);
-    y.v_seen = take(2 * g.H * g.seen_words * 4);
-    y.a_av = take(C2 * 2);
-    y.b_units = take(C2 * 2);
+    y.b_events = take(32 * 4);  // admission -> finish, across completion
+    // Phase union, by lifetime:
+    //   persistent from sampling to admission: the command arrays at 0;
+    //   persistent from the summary to sampling / admission: bitmaps,
+    //     available list, entry list after them;
+    //   temporaries: the summary's occupant words, unit list and seen
+    //     bitmaps over the (then dead) command arrays; the fast admission's
+    //     final kinds / durations after the entry list; the general
+    //     admission's keys and lists over everything but the command
+    //     arrays; completion records and observation staging over all.
     const int32_t union0 = o;
-    // admission
     y.c_kind = take(C2);
     y.c_dir = take(C2);
     y.c_ptype = take(C2);
     y.c_target = take(C2 * 2);
     y.c_none = take(C2 * 4);
     y.c_rank = take(C2 * 2);
+    const int32_t commands_end = o;
+    y.o_bm = take(6 * g.H * g.seen_words * 4);
+    y.a_av = take(C2 * 2);
+    y.a_list = take(E * 2);
+    y.a_fk = take(kWave * 4);
+    y.a_fn = take(kWave * 4);
+    int32_t end = o;
+    // general admission
+    o = commands_end;
     y.b_pkey = take(C2 * 4);
     y.b_keys = take(C2 * 8);
     y.b_tmp = take(C2 * 2);
     y.b_order = take(C2 * 2);
     y.b_rank = take(E * 2);
-    y.a_fk = take(kWave * 4);
-    y.a_fn = take(kWave * 4);
-    y.a_list = take(E * 2);
-    const int32_t admission_end = o;
-    // completion (the commands are dead by then)
+    if (o > end) end = o;
+    // summary temporaries (the command arrays are dead then)
+    o = union0;
+    y.o_lo = take(E * 4);
+    y.o_fl = take(E);
+    y.b_units = take(C2 * 2);
+    y.v_seen = take(2 * g.H * g.seen_words * 4);
+    if (o > commands_end) {
+        // larger boards: after the persistent lists instead
+        o = end;
+        y.o_lo = take(E * 4);
+        y.o_fl = take(E);
+        y.b_units = take(C2 * 2);
+        y.v_seen = take(2 * g.H * g.seen_words * 4);
+    }
+    if (o > end) end = o;
+    // completion
     o = union0;
     y.m_rec = take(C2 * 24);
-    y.m_keys = take(C2 * 8);
     y.m_tmp = take(C2 * 2);
-    const int32_t completion_end = o;
-    // observation
+    if (o > end) end = o;
+    // observation staging (observe_all) with its seen bitmaps
     o = union0;
+    y.v_oseen = take(2 * g.H * g.seen_words * 4);
     y.v_stage = take(2 * g.stage_cells * 6);
-    const int32_t observe_end = o;
-    // masks
+    if (o > end) end = o;
+    // masks staging (k_legality)
     o = union0;
     y.v_words = take(C2 * 12);
-    const int32_t masks_end = o;
-    int32_t end = admission_end;
-    if (completion_end > end) end = completion_end;
-    if (observe_end > end) end = observe_end;
-    if (masks_end > end) end = masks_end;
+    if (o > end) end = o;
     y.env_bytes = align16(end);
 
     // initial State rows -> env block (reset_env)
