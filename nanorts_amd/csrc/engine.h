@@ -100,6 +100,9 @@ struct Layout {
     int32_t o_bm;      // occupancy bitmaps (6 planes), outside the union
     int32_t o_lo;      // occupant word per slot (player 0's view), outside the union
     int32_t o_fl;      // occupant flags per slot: kind | resource << 4 | stockpile << 5
+    int32_t o_live;    // bitmap of live slots (birth != ABSENT), 64 slots per word
+    int32_t o_slist;   // the summary's list of live slots
+    int32_t m_list;    // completion's list of live slots
     // Phase union.  Admission: commands, keys, lists.  Completion: member
     // records, keys.  Observation: seen bitmap, staging, unit list.  Masks:
     // staged words.
@@ -863,6 +866,21 @@ NR_DEV void admit(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t
     }
 }
 
+// The live slots in ascending order into list; returns their count.
+NR_DEV int32_t live_list(const KGame& g, const Env& e, int lane, AS3 int16_t* list) {
+    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
+    int32_t n = 0;
+    for (int32_t w = 0; w * kWave < g.E; ++w) {
+        const uint64_t lw = live[w];
+        const uint64_t m = ((uint64_t)(uint32_t)uni((int32_t)(uint32_t)(lw >> 32)) << 32) |
+                           (uint64_t)(uint32_t)uni((int32_t)(uint32_t)lw);
+        if ((m >> lane) & 1ull) list[n + count_below(m)] = (int16_t)(w * kWave + lane);
+        n += popc(m);
+    }
+    wave_sync();
+    return n;
+}
+
 // ---------------------------------------------------------------------------
 // Completion (N/core/pending.py:47-76, N/core/completion.py)
 // ---------------------------------------------------------------------------
@@ -950,6 +968,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
                     e.sc[S_RES0 + player] = balance;
                     if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)newborn;
                     e.birth[newborn] = birth;
+                    at<uint64_t>(e, g.lay.o_live)[newborn >> 6] |= 1ull << (newborn & 63);
                     e.utype[newborn] = (int8_t)newborn_type;
                     e.owner[newborn] = (int8_t)player;
                     e.cell[newborn] = (int16_t)dest;
@@ -982,6 +1001,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
                 const int32_t owner_block = (removed - g.N) / g.C;
                 e.sc[S_UNITS0 + owner_block] -= 1;
             }
+            if (removed >= 0 && removed < g.E) at<uint64_t>(e, g.lay.o_live)[removed >> 6] &= ~(1ull << (removed & 63));
             remove_slot(e, removed);
         }
     }
@@ -997,12 +1017,16 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
     AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
+    // only live slots hold pending actions
+    AS3 int16_t* slots = at<int16_t>(e, y.m_list);
+    const int32_t nlive = live_list(g, e, lane, slots);
     int32_t n = 0;
-    for (int32_t base = 0; base < g.E; base += kWave) {
-        const int32_t s = base + lane;
+    for (int32_t base = 0; base < nlive; base += kWave) {
+        const int32_t i = base + lane;
+        const int32_t s = i < nlive ? slots[i] : 0;
         bool acting = false;
         int32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0, r4 = 0;
-        if (s < g.E) {
+        if (i < nlive) {
             const int32_t k = e.pkind[s];
             const bool due = k != kAbsent && e.pcompl[s] <= time;
             if (due) {
@@ -1107,21 +1131,26 @@ NR_DEV void decide(const KGame& g, const Env& e_in, int lane) {
 }
 
 // Active units per player, for decide_counted.
+// Also rebuilds the live-slot bitmap, which take_turn then keeps.
 NR_DEV void count_units(const KGame& g, const Env& e_in, int lane) {
     const Env e = refresh(g, e_in);
-    int32_t count[2] = {0, 0};
-    for (int32_t pl = 0; pl < 2; ++pl) {
-        for (int32_t base = 0; base < g.C; base += kWave) {
-            const int32_t i = base + lane;
-            count[pl] += popc(ballot(i < g.C && e.birth[g.N + pl * g.C + i] != kAbsent));
-        }
+    AS3 uint64_t* live = at<uint64_t>(e, g.lay.o_live);
+    int32_t count0 = 0, count1 = 0;
+    for (int32_t base = 0; base < g.E; base += kWave) {
+        const int32_t s = base + lane;
+        const bool alive = s < g.E && e.birth[s] != kAbsent;
+        const uint64_t m = ballot(alive);
+        if (lane == 0) live[base >> 6] = m;
+        count0 += popc(ballot(alive && s >= g.N && s < g.N + g.C));
+        count1 += popc(ballot(alive && s >= g.N + g.C));
     }
     if (lane == 0) {
-        e.sc[S_UNITS0] = count[0];
-        e.sc[S_UNITS1] = count[1];
+        e.sc[S_UNITS0] = count0;
+        e.sc[S_UNITS1] = count1;
     }
     wave_sync();
 }
+
 
 // outcome.decide from the kept unit counts.
 NR_DEV void decide_counted(const Env& e, int lane) {

@@ -161,6 +161,7 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_pptype = take(E);
     y.o_scal = take(S_COUNT * 4);
     y.b_events = take(32 * 4);  // admission -> finish, across completion
+    y.o_live = take(((E + 63) / 64) * 8);
     // Phase union, by lifetime:
     //   persistent from sampling to admission: the command arrays at 0;
     //   persistent from the summary to sampling / admission: bitmaps,
@@ -198,6 +199,7 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_fl = take(E);
     y.b_units = take(C2 * 2);
     y.v_seen = take(2 * g.H * g.seen_words * 4);
+    y.o_slist = take(E * 2);
     if (o > commands_end) {
         // larger boards: after the persistent lists instead
         o = end;
@@ -205,12 +207,14 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
         y.o_fl = take(E);
         y.b_units = take(C2 * 2);
         y.v_seen = take(2 * g.H * g.seen_words * 4);
+        y.o_slist = take(E * 2);
     }
     if (o > end) end = o;
     // completion
     o = union0;
     y.m_rec = take(C2 * 24);
     y.m_tmp = take(C2 * 2);
+    y.m_list = take(E * 2);
     if (o > end) end = o;
     // observation staging (observe_all) with its seen bitmaps
     o = union0;
@@ -337,6 +341,7 @@ __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_st
                        nanorts_commands c, nanorts_step_results r) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
     stage_commands(g, e, l, c, lane);
     const int64_t kl = key_lanes == 1 ? 0 : l;
     const uint32_t k0 = key[2 * kl], k1 = key[2 * kl + 1];

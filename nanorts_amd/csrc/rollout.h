@@ -203,12 +203,16 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
     AS3 int16_t* entries = at<int16_t>(e, y.a_list);
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    // only live slots hold units or pending actions
+    AS3 int16_t* slots = at<int16_t>(e, y.o_slist);
+    const int32_t nlive = live_list(g, e, lane, slots);
     int32_t nav = 0, nunits = 0, nA = 0;
     bool odd = false;
-    for (int32_t base = 0; base < g.E; base += kWave) {
-        const int32_t s = base + lane;
+    for (int32_t base = 0; base < nlive; base += kWave) {
+        const int32_t i = base + lane;
+        const int32_t s = i < nlive ? slots[i] : 0;
         bool alive = false, available = false, entry = false;
-        if (s < g.E) {
+        if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
             // pending from earlier cycles, in slot order (see admit_env)
             const int32_t k = e.pkind[s];
