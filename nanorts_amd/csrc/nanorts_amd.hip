@@ -548,20 +548,59 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
 // the per-cycle summary (rollout.h) each cycle is: sample from the masks of
 // the summarised state -> decode -> core.step -> finish (reward, done,
 // auto-reset) -> summarise the new state, which writes its observation.
-// Each phase of the cycle takes a fresh view of the game (fresh_game), so
-// the game's fields are reloaded per phase rather than held across the loop.
-__global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts_state s, uint32_t key0, uint32_t key1, int32_t step0,
-                          int32_t steps, int32_t partial, int64_t env0, nanorts_rollout_results out) {
+//
+// The kernel takes one argument struct and every phase of the cycle reads
+// it again from the kernel-argument segment (fresh_rollout_args), together
+// with the LDS views derived from it, so that almost nothing but the loop
+// counters and keys stays live in scalar registers across the cycle.
+struct RolloutArgs {
+    KGame g;  // first: fresh_game() reads it at offset 0
+    int64_t lanes;
+    nanorts_state s;
+    uint32_t key0, key1;
+    int32_t step0, steps, partial;
+    int64_t env0;
+    nanorts_rollout_results out;
+};
+typedef const __attribute__((address_space(4))) RolloutArgs* RolloutArgsArg;
+NR_DEV const RolloutArgs& fresh_rollout_args() {
+    RolloutArgsArg p = (RolloutArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const RolloutArgs*)p;
+}
+NR_DEV Hdr header_view(const KGame& g) {
+    extern __shared__ __align__(16) uint8_t nr_lds[];
+    AS3 uint8_t* lds = (AS3 uint8_t*)nr_lds;
+    Hdr h;
+    h.tab = (AS3 int32_t*)lds;
+    h.terrain = lds + g.lay.o_terrain;
+    h.seg = (AS3 Seg*)(lds + g.lay.o_seg);
+    h.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);
+    return h;
+}
+NR_DEV Env wave_env(const KGame& g, int wave) {
+    extern __shared__ __align__(16) uint8_t nr_lds[];
+    return env_view(g, (AS3 uint8_t*)nr_lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
+}
+#define NR_ROLLOUT_PHASE                              \
+    const RolloutArgs& a = fresh_rollout_args();      \
+    const KGame& g = a.g;                             \
+    const Hdr hdr = header_view(g);                   \
+    const Env e = wave_env(g, wave);                  \
+    (void)hdr;
+
+__global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
+    const KGame& g = args.g;
+    const int64_t lanes = args.lanes;
     NR_KERNEL_PROLOGUE
-    load_env(g, s, l, e, LD_ALL, lane);
+    load_env(g, args.s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    const bool fast = g.fast_obs && ((((uintptr_t)out.feature_maps) & 7u) == 0);
-    if (fast) summarize(g, hdr, e, lane, partial != 0, nullptr, nullptr, nullptr, nullptr);
+    const bool fast = g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0);
+    if (fast) summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
-    const Env e0 = e;
+    const int32_t steps = args.steps;
     for (int32_t t = 0; t < steps; ++t) {
-        const int32_t step = step0 + t;
         bool irregular = false;
         int32_t n;
         // fused: the sampled commands go straight into the admission's
@@ -571,8 +610,9 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         no_request(q);
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
-            const KGame& g = fresh_game();
-            const Env e = refresh(g, e0);
+            NR_ROLLOUT_PHASE
+            const nanorts_rollout_results& out = a.out;
+            const int32_t step = a.step0 + t;
             const int32_t owned = 2 * g.C;
             if (fast) {
                 n = uni(e.sc[S_NAV]);
@@ -582,9 +622,9 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
                 n = compact_available(g, e, lane, &irregular);
                 build_bitmaps(g, hdr, e, lane);
             }
-            uint32_t ke0 = key0, ke1 = key1;
+            uint32_t ke0 = a.key0, ke1 = a.key1;
             fold_in(ke0, ke1, (uint32_t)step);
-            fold_in(ke0, ke1, (uint32_t)(env0 + l));
+            fold_in(ke0, ke1, (uint32_t)(a.env0 + l));
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
             // draw words: with n <= 32 the two threefry blocks of a position run
             // on two lanes at once; otherwise each lane computes both
@@ -619,20 +659,20 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
                     words[2] = w2;
                     words[3] = w3;
                 }
-                int32_t a[7];
-                if (g.T <= 8) sample_row_words8(g, r, words, a);
-                else sample_row_words(g, r, words, a);
+                int32_t act[7];
+                if (g.T <= 8) sample_row_words8(g, r, words, act);
+                else sample_row_words(g, r, words, act);
                 if (out.actions) {
                     int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
 #pragma unroll
-                    for (int f = 0; f < 7; ++f) dst[f] = a[f];
+                    for (int f = 0; f < 7; ++f) dst[f] = act[f];
                 }
                 if (fused) {
                     int32_t kind, dir, ptype, target, none;
-                    decode_values(g, e, p, a, &kind, &dir, &ptype, &target, &none);
+                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                     request_of(g, hdr, e, p, kind, dir, ptype, target, none, true, false, q);
                 } else {
-                    decode_row(g, e, p, true, a);
+                    decode_row(g, e, p, true, act);
                 }
             }
             if (out.actions) {
@@ -649,8 +689,7 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
         }
         {
             // env.step: core.step keyed by fold_in(env root, episode)
-            const KGame& g = fresh_game();
-            const Env e = refresh(g, e0);
+            NR_ROLLOUT_PHASE
             int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
             if (fused && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA)) {
                 admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
@@ -666,38 +705,39 @@ __global__ __launch_bounds__(256) void k_rollout(KGame g, int64_t lanes, nanorts
             }
         }
         {
-            const KGame& g = fresh_game();
-            const Env e = refresh(g, e0);
+            NR_ROLLOUT_PHASE
             complete(g, hdr, e, lane);
             decide_counted(e, lane);
         }
         {
-            const KGame& g = fresh_game();
-            const Env e = refresh(g, e0);
+            NR_ROLLOUT_PHASE
             nanorts_env_results r = {};
-            if (out.rewards) r.reward = out.rewards + (int64_t)t * lanes * 2;
-            if (out.dones) r.done = out.dones + (int64_t)t * lanes;
-            if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) {
+            if (a.out.rewards) r.reward = a.out.rewards + (int64_t)t * lanes * 2;
+            if (a.out.dones) r.done = a.out.dones + (int64_t)t * lanes;
+            if (finish_step(g, hdr, e, l, lane, a.partial != 0, r, false)) {
                 ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
                 ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
                 fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
             }
         }
         {
-            const KGame& g = fresh_game();
-            const Env e = refresh(g, e0);
+            NR_ROLLOUT_PHASE
+            const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
             const int64_t slot = (out.depth > 0 ? (int64_t)(t % out.depth) : 0) * lanes + l;
             if (fast) {
                 uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
                 int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
-                summarize(g, hdr, e, lane, partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
             } else if (out.feature_maps || out.scalars) {
-                observe_both(g, hdr, e, slot, lane, partial != 0, out.feature_maps, out.scalars);
+                observe_both(g, hdr, e, slot, lane, a.partial != 0, out.feature_maps, out.scalars);
             }
         }
     }
-    store_env(fresh_game(), s, l, e, lane);
+    {
+        NR_ROLLOUT_PHASE
+        store_env(g, a.s, l, e, lane);
+    }
 }
 
 // Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
@@ -1037,8 +1077,26 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
     if (steps < 0) return fail(NANORTS_INVALID_ARGUMENT, "steps must be >= 0");
     if ((results.feature_maps || results.scalars) && results.depth < 1)
         return fail(NANORTS_INVALID_ARGUMENT, "depth must be >= 1");
-    return launch(k_rollout, sh, lanes, (hipStream_t)stream, state, sample_key[0], sample_key[1], step0, steps, partial,
-                  env0, results);
+    if (lanes <= 0) return NANORTS_OK;
+    const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    RolloutArgs args;
+    std::memset(&args, 0, sizeof(args));
+    args.g = sh.g;
+    args.lanes = lanes;
+    args.s = state;
+    args.key0 = sample_key[0];
+    args.key1 = sample_key[1];
+    args.step0 = step0;
+    args.steps = steps;
+    args.partial = partial;
+    args.env0 = env0;
+    args.out = results;
+    hipLaunchKernelGGL(k_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
+                       (hipStream_t)stream, args);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
 }
 
 }  // extern "C"
