@@ -605,9 +605,10 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
         int32_t n;
         // fused: the sampled commands go straight into the admission's
         // request registers (no staging through the command arrays)
-        bool fused = false;
+        bool fused = false, listed = false;
         Reqs q;
         no_request(q);
+        int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
@@ -622,6 +623,9 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 n = compact_available(g, e, lane, &irregular);
                 build_bitmaps(g, hdr, e, lane);
             }
+            // the pending entries of the admission, loaded early so their
+            // latency overlaps the sampling
+            if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
             uint32_t ke0 = a.key0, ke1 = a.key1;
             fold_in(ke0, ke1, (uint32_t)step);
             fold_in(ke0, ke1, (uint32_t)(a.env0 + l));
@@ -690,8 +694,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
         {
             // env.step: core.step keyed by fold_in(env root, episode)
             NR_ROLLOUT_PHASE
-            int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
-            if (fused && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA)) {
+            if (fused && listed) {
                 admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
             } else if (fused || !admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
                 // general admission; a fused cycle (which the summary's

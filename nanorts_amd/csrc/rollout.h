@@ -165,7 +165,15 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
         const int32_t reach = imin(range, g.radius);
         AS3 const uint32_t* enemy = bm + (2 - owner) * H;
         uint64_t att = 0;
-        if (range >= 0 && range <= g.disk_r && inx) {
+        if (range == 1 && g.radius >= 1 && inx) {
+            // range 1: the four neighbours (the unit's own cell never holds
+            // an enemy), read like the move directions
+            const uint32_t e_up = has_up ? enemy[ru] : 0u, e_dn = has_dn ? enemy[rd] : 0u;
+            const uint32_t ew = (uint32_t)((((uint64_t)(has_mid ? enemy[rm] : 0u) << 1) >> x) & 7ull);
+            const int32_t c0 = g.radius * g.side + g.radius;
+            att = ((uint64_t)((e_up >> xb) & 1u) << (c0 - g.side)) | ((uint64_t)(ew & 1u) << (c0 - 1)) |
+                  ((uint64_t)((ew >> 2) & 1u) << (c0 + 1)) | ((uint64_t)((e_dn >> xb) & 1u) << (c0 + g.side));
+        } else if (range >= 0 && range <= g.disk_r && inx) {
             AS3 const uint32_t* disk = h.disk + range * (2 * g.disk_r + 1) + g.disk_r;
             const uint32_t window = (2u << (2 * reach)) - 1u;
             const int32_t left = x - reach;
