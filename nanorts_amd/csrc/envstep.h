@@ -217,12 +217,23 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
     // crank orders the requests that can conflict among themselves.
     const uint64_t conflicting_lanes = ballot(conflicting);
     int32_t rank = 0, crank = 0;
-    for (int32_t j = 0; j < n; ++j) {
-        const int32_t plj = __builtin_amdgcn_readlane(pl, j);
-        const int32_t bj = __builtin_amdgcn_readlane(birth, j);
-        const bool before = (plj < pl) || (plj == pl && (bj < birth || (bj == birth && j < lane)));
-        rank += before;
-        crank += before && ((conflicting_lanes >> j) & 1ull);
+    if (ballot(lane < n && (birth < 0 || birth >= (1 << 24))) == 0ull) {
+        // one 32-bit key per request: player, birth, lane
+        const uint32_t key = lane < n ? ((uint32_t)pl << 31) | ((uint32_t)birth << 6) | (uint32_t)lane : 0xFFFFFFFFu;
+        for (int32_t j = 0; j < n; ++j) {
+            const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int32_t)key, j);
+            const int32_t before = kj < key ? 1 : 0;
+            rank += before;
+            crank += ((conflicting_lanes >> j) & 1ull) ? before : 0;
+        }
+    } else {
+        for (int32_t j = 0; j < n; ++j) {
+            const int32_t plj = __builtin_amdgcn_readlane(pl, j);
+            const int32_t bj = __builtin_amdgcn_readlane(birth, j);
+            const bool before = (plj < pl) || (plj == pl && (bj < birth || (bj == birth && j < lane)));
+            rank += before;
+            crank += before && ((conflicting_lanes >> j) & 1ull);
+        }
     }
     // Sequential conflict resolution over the requests that can conflict.
     const int32_t bal0 = uni(e.sc[S_RES0]), bal1 = uni(e.sc[S_RES1]);
