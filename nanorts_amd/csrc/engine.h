@@ -1020,6 +1020,56 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     // only live slots hold pending actions
     AS3 int16_t* slots = at<int16_t>(e, y.m_list);
     const int32_t nlive = live_list(g, e, lane, slots);
+    if (nlive <= kWave) {
+        // one live slot per lane: the members' retained actors stay in
+        // their lanes and are ranked and read from there
+        const int32_t s = lane < nlive ? slots[lane] : 0;
+        bool acting = false;
+        int32_t w0 = 0, w1 = 0, w2 = 0, rb = 0, rc = 0, ord = 0;
+        if (lane < nlive) {
+            const int32_t k = e.pkind[s];
+            const bool due = k != kAbsent && e.pcompl[s] <= time;
+            if (due) {
+                acting = k != kKindNone && s >= g.N;
+                if (acting) {
+                    w0 = (s & 0xFFFF) | ((k & 0xFF) << 16) | ((e.pdir[s] & 0xFF) << 24);
+                    w1 = (e.ptarget[s] & 0xFFFF) | ((e.pptype[s] & 0xFF) << 16) | ((e.owner[s] & 0xFF) << 24);
+                    w2 = (e.utype[s] & 0xFF) | ((e.cell[s] & 0xFFFF) << 8);
+                    rb = e.birth[s];
+                    rc = e.carried[s];
+                    ord = e.porder[s];
+                }
+                e.pkind[s] = (int8_t)kAbsent;
+                e.pdir[s] = (int8_t)kAbsent;
+                e.pnone[s] = 0;
+                e.ptarget[s] = (int16_t)kAbsent;
+                e.pptype[s] = (int8_t)kAbsent;
+                e.pissued[s] = 0;
+                e.pcompl[s] = 0;
+                e.porder[s] = kAbsent;
+            }
+        }
+        wave_sync();
+        const uint64_t members = ballot(acting);
+        const int32_t n = popc(members);
+        // members act in pending order (pending.batch_order :55-60), ties by slot
+        int32_t rank = 0;
+        for (uint64_t m = members; m != 0ull; m &= m - 1ull) {
+            const int32_t j = (int32_t)__builtin_ctzll(m);
+            const int32_t oj = __builtin_amdgcn_readlane(ord, j);
+            rank += (oj < ord) || (oj == ord && j < lane);
+        }
+        for (int32_t k = 0; k < n; ++k) {
+            const int32_t li = (int32_t)__builtin_ctzll(ballot(acting && rank == k));
+            const int32_t a = __builtin_amdgcn_readlane(w0, li), b = __builtin_amdgcn_readlane(w1, li),
+                          c = __builtin_amdgcn_readlane(w2, li);
+            take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
+                      (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
+                      (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
+                      __builtin_amdgcn_readlane(rc, li));
+        }
+        return;
+    }
     int32_t n = 0;
     for (int32_t base = 0; base < nlive; base += kWave) {
         const int32_t i = base + lane;
