@@ -243,7 +243,7 @@ def main() -> None:
             nonlocal pc_state
             for t in range(n):
                 words = env.get_avail_actions(pc_state, form="words")
-                acts = env.sample_actions(torch.stack([words[a] for a in env.agents], 1), (11, 13), base + t)
+                acts = env.sample_actions(words, (11, 13), base + t)
                 _, pc_state, _, _, _ = env.step(None, pc_state, acts, donate=True)
         per_call(3, 0)
         torch.cuda.synchronize()

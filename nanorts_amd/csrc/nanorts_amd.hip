@@ -408,6 +408,44 @@ NR_DEV void emit_rows(const KGame& g, const Env& e, int64_t l, uint8_t* rows, in
 
 __global__ __launch_bounds__(256) void k_legality(KGame g, int64_t lanes, nanorts_state s, int32_t merge, uint8_t* rows, uint32_t* words) {
     NR_KERNEL_PROLOGUE
+    if (merge && g.fast_obs && g.seen_words == 1) {
+        // get_avail_actions from the summary's occupancy bitmaps: rows of
+        // the available units, NONE only for every other position
+        load_env(g, s, l, e,
+                 LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_HP | LD_CARRIED | LD_PKIND | LD_PISSUED | LD_PORDER |
+                     LD_ENTITY | LD_SCALARS,
+                 lane);
+        count_units(g, e, lane);
+        summarize_slots(g, hdr, e, lane);
+        summarize_cells(g, hdr, e, lane, false, true, nullptr, nullptr);
+        const int32_t n = uni(e.sc[S_NAV]);
+        if (n <= kWave) {
+            int32_t p = 0;
+            Row r;
+            r.w[0] = r.w[1] = r.w[2] = 0u;
+            if (lane < n) {
+                p = at<int16_t>(e, g.lay.a_av)[lane];
+                r = legality_row_w1(g, hdr, e, g.N + p);
+            }
+            wave_sync();
+            AS3 uint32_t* vw = at<uint32_t>(e, g.lay.v_words);
+            for (int32_t q = lane; q < 2 * g.C; q += kWave) {
+                vw[3 * q] = 1u;
+                vw[3 * q + 1] = 0u;
+                vw[3 * q + 2] = 0u;
+            }
+            wave_sync();
+            if (lane < n) {
+                vw[3 * p] = r.w[0];
+                vw[3 * p + 1] = r.w[1];
+                vw[3 * p + 2] = r.w[2];
+            }
+            wave_sync();
+            if (words) copy_out((uint8_t*)(words + l * 2 * g.C * 3), (AS3 const uint8_t*)vw, 2 * g.C * 12, lane);
+            if (rows) emit_rows(g, e, l, rows, lane);
+            return;
+        }
+    }
     load_env(g, s, l, e, LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_CARRIED | LD_PKIND | LD_ENTITY | LD_SCALARS,
              lane);
     stage_words(g, hdr, e, lane, merge != 0);
@@ -462,7 +500,7 @@ NR_DEV void stage_actions(const KGame& g, const Env& e, int64_t l, const int32_t
 
 // After core.step: outcome, rewards, optional final observation, auto-reset.
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
-                        const nanorts_env_results& r, bool events) {
+                        const nanorts_env_results& r, bool events, bool fast_obs = false) {
     const bool over = uni(e.sc[S_GAME_OVER]) != 0;
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t winner = uni(e.sc[S_WINNER]);
@@ -490,7 +528,14 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
         out[4] = (float)(ev[20 + p * 3 + o + 1] - ev[20 + p * 3 + p + 1]);
         out[5] = (float)(prod[4] + prod[5] + prod[6]);
     }
-    if (r.final_feature_maps || r.final_scalars) observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
+    if (fast_obs && (r.final_feature_maps || r.final_scalars)) {
+        const int64_t per = (int64_t)g.cells * 6;
+        uint8_t* m0 = r.final_feature_maps ? r.final_feature_maps + (l * 2) * per : nullptr;
+        int32_t* s0 = r.final_scalars ? r.final_scalars + l * 8 : nullptr;
+        summarize(g, h, e, lane, partial, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+    } else if (r.final_feature_maps || r.final_scalars) {
+        observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
+    }
     if (done) reset_env(g, h, e, lane);
     return done;
 }
@@ -500,26 +545,68 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    bool irregular = false;
-    const int32_t n = compact_available(g, e, lane, &irregular);
     const int32_t owned = 2 * g.C;
-    AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
-    for (int32_t i = lane; i < n; i += kWave) {
-        const int32_t p = av[i];
-        const int32_t* row = actions + (l * owned + p) * 7;
-        int32_t a[7];
-#pragma unroll
-        for (int f = 0; f < 7; ++f) a[f] = row[f];
-        decode_row(g, e, p, true, a);
-    }
-    wave_sync();
     uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
     const bool events = r.reward_components != nullptr;
-    env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular, false);
-    finish_step(g, hdr, e, l, lane, partial != 0, r, events);
+    // the summary path encodes observations with 8-byte stores
+    const bool fast = g.fast_obs && ((((uintptr_t)r.feature_maps) | ((uintptr_t)r.final_feature_maps)) & 7u) == 0;
+    bool fused = false;
+    if (fast) {
+        // lists of the summary, then decode straight into the admission's
+        // request registers (no staging through the command arrays)
+        summarize_slots(g, hdr, e, lane);
+        const int32_t n = uni(e.sc[S_NAV]);
+        int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
+        fused = uni(e.sc[S_IRREG]) == 0 && n <= kWave && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
+        if (fused) {
+            if (events) {
+                if (lane < 32) at<int32_t>(e, g.lay.b_events)[lane] = 0;
+                wave_sync();
+            }
+            Reqs q;
+            no_request(q);
+            if (lane < n) {
+                const int32_t p = at<int16_t>(e, g.lay.a_av)[lane];
+                const int32_t* row = actions + (l * owned + p) * 7;
+                int32_t a[7];
+#pragma unroll
+                for (int f = 0; f < 7; ++f) a[f] = row[f];
+                int32_t kind, dir, ptype, target, none;
+                decode_values(g, e, p, a, &kind, &dir, &ptype, &target, &none);
+                request_of(g, hdr, e, p, kind, dir, ptype, target, none, false, events, q);
+            }
+            wave_sync();
+            admit_resolve(g, hdr, e, lane, k0, k1, n, nA, posA, costA, playerA, q);
+            complete(g, hdr, e, lane);
+            decide_counted(e, lane);
+        }
+    }
+    if (!fused) {
+        bool irregular = false;
+        const int32_t n = compact_available(g, e, lane, &irregular);
+        AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
+        for (int32_t i = lane; i < n; i += kWave) {
+            const int32_t p = av[i];
+            const int32_t* row = actions + (l * owned + p) * 7;
+            int32_t a[7];
+#pragma unroll
+            for (int f = 0; f < 7; ++f) a[f] = row[f];
+            decode_row(g, e, p, true, a);
+        }
+        wave_sync();
+        env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular, false);
+    }
+    finish_step(g, hdr, e, l, lane, partial != 0, r, events, fast);
     store_env(g, s, l, e, lane);
-    if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
+    if (fast) {
+        const int64_t per = (int64_t)g.cells * 6;
+        uint8_t* m0 = r.feature_maps ? r.feature_maps + (l * 2) * per : nullptr;
+        int32_t* s0 = r.scalars ? r.scalars + l * 8 : nullptr;
+        summarize(g, hdr, e, lane, partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+    } else if (r.feature_maps || r.scalars) {
+        observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const uint32_t* words, uint32_t key0, uint32_t key1, int32_t step,

@@ -382,9 +382,14 @@ class NanoRTS:
         native.check(self.lib.nanorts_reset_where_done(_stream(), self.dev.ref, state.native(), state.num_envs,
                                                        _ptr(done)), "nanorts_reset_where_done")
 
-    def sample_actions(self, words: torch.Tensor, sample_key, step: int, env0: int = 0) -> dict[str, torch.Tensor]:
+    def sample_actions(self, words, sample_key, step: int, env0: int = 0) -> dict[str, torch.Tensor]:
         """The synthetic harness's integer uniform-over-legal sampler on
-        get_avail_actions(form="words") output stacked as [L, 2, C, 3]."""
+        get_avail_actions(form="words") output: the per-agent dict, or the
+        words stacked as [L, 2, C, 3]."""
+        if isinstance(words, dict):
+            per_agent = [words[a] for a in self.agents]
+            stacked = self._agent_stack(per_agent)
+            words = stacked if stacked is not None else torch.stack(per_agent, dim=1)
         words = words.contiguous()
         L = words.shape[0]
         b = self.bucket
@@ -443,10 +448,33 @@ class NanoRTS:
         image = self.pixels_from_maps(maps)
         return {agent: PixelObservation(image[:, p], scalars[:, p]) for p, agent in enumerate(self.agents)}
 
+    def _agent_stack(self, per_agent: list[torch.Tensor]) -> torch.Tensor | None:
+        """The [L, 2, ...] tensor the per-agent values are views of (agent p
+        = base[:, p], as sample_actions and get_avail_actions return them),
+        or None when they are separate tensors."""
+        a0, a1 = per_agent
+        if not (isinstance(a0, torch.Tensor) and isinstance(a1, torch.Tensor)) or a0.device != self.device:
+            return None
+        if a0.dtype != a1.dtype or a0.shape != a1.shape or a0.dim() < 1 or a1.device != a0.device:
+            return None
+        inner = a0[0].numel() if a0.shape[0] > 0 else 0
+        row = tuple(a0.shape[1:])
+        dense = [1]
+        for extent in reversed(row[1:]):
+            dense.insert(0, dense[0] * extent)
+        if a0.shape[0] == 0 or tuple(a0.stride()[1:]) != tuple(dense[:len(row)]) or a0.stride() != a1.stride():
+            return None
+        if a0.stride(0) != 2 * inner or a1.data_ptr() != a0.data_ptr() + inner * a0.element_size():
+            return None
+        return torch.as_strided(a0, (a0.shape[0], 2, *row), (2 * inner, inner, *a0.stride()[1:]))
+
     def _stack_actions(self, actions: dict[str, torch.Tensor], L: int) -> torch.Tensor:
         if set(actions) != set(self.agents):
             raise ModelError(f"actions are keyed by {sorted(actions)}, expected {self.agents}")
-        stacked = torch.stack([torch.as_tensor(actions[a], device=self.device) for a in self.agents], dim=1)
+        per_agent = [torch.as_tensor(actions[a], device=self.device) for a in self.agents]
+        stacked = self._agent_stack(per_agent)
+        if stacked is None:
+            stacked = torch.stack(per_agent, dim=1)
         if stacked.dtype != torch.int32:
             raise ModelError(f"actions have dtype {stacked.dtype}, expected int32")
         if tuple(stacked.shape) != (L, 2, *self.layout.actions_shape):
