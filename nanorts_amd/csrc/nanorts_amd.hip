@@ -408,44 +408,6 @@ NR_DEV void emit_rows(const KGame& g, const Env& e, int64_t l, uint8_t* rows, in
 
 __global__ __launch_bounds__(256) void k_legality(KGame g, int64_t lanes, nanorts_state s, int32_t merge, uint8_t* rows, uint32_t* words) {
     NR_KERNEL_PROLOGUE
-    if (merge && g.fast_obs && g.seen_words == 1) {
-        // get_avail_actions from the summary's occupancy bitmaps: rows of
-        // the available units, NONE only for every other position
-        load_env(g, s, l, e,
-                 LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_HP | LD_CARRIED | LD_PKIND | LD_PISSUED | LD_PORDER |
-                     LD_ENTITY | LD_SCALARS,
-                 lane);
-        count_units(g, e, lane);
-        summarize_slots(g, hdr, e, lane);
-        summarize_cells(g, hdr, e, lane, false, true, nullptr, nullptr);
-        const int32_t n = uni(e.sc[S_NAV]);
-        if (n <= kWave) {
-            int32_t p = 0;
-            Row r;
-            r.w[0] = r.w[1] = r.w[2] = 0u;
-            if (lane < n) {
-                p = at<int16_t>(e, g.lay.a_av)[lane];
-                r = legality_row_w1(g, hdr, e, g.N + p);
-            }
-            wave_sync();
-            AS3 uint32_t* vw = at<uint32_t>(e, g.lay.v_words);
-            for (int32_t q = lane; q < 2 * g.C; q += kWave) {
-                vw[3 * q] = 1u;
-                vw[3 * q + 1] = 0u;
-                vw[3 * q + 2] = 0u;
-            }
-            wave_sync();
-            if (lane < n) {
-                vw[3 * p] = r.w[0];
-                vw[3 * p + 1] = r.w[1];
-                vw[3 * p + 2] = r.w[2];
-            }
-            wave_sync();
-            if (words) copy_out((uint8_t*)(words + l * 2 * g.C * 3), (AS3 const uint8_t*)vw, 2 * g.C * 12, lane);
-            if (rows) emit_rows(g, e, l, rows, lane);
-            return;
-        }
-    }
     load_env(g, s, l, e, LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_CARRIED | LD_PKIND | LD_ENTITY | LD_SCALARS,
              lane);
     stage_words(g, hdr, e, lane, merge != 0);
