@@ -602,14 +602,15 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
 // it again from the kernel-argument segment (fresh_rollout_args), together
 // with the LDS views derived from it, so that almost nothing but the loop
 // counters and keys stays live in scalar registers across the cycle.
+constexpr int32_t kRolloutChunk = 128;  // cycles per launch (one step key each)
 struct RolloutArgs {
     KGame g;  // first: fresh_game() reads it at offset 0
     int64_t lanes;
     nanorts_state s;
-    uint32_t key0, key1;
-    int32_t step0, steps, partial;
+    int32_t t0, steps, partial;  // cycles t0 .. t0 + steps - 1 of the caller's rollout
     int64_t env0;
     nanorts_rollout_results out;
+    uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
 };
 typedef const __attribute__((address_space(4))) RolloutArgs* RolloutArgsArg;
 NR_DEV const RolloutArgs& fresh_rollout_args() {
@@ -662,8 +663,8 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
             const nanorts_rollout_results& out = a.out;
-            const int32_t step = a.step0 + t;
             const int32_t owned = 2 * g.C;
+            const int64_t tt = (int64_t)a.t0 + t;  // cycle index within the caller's rollout
             if (fast) {
                 n = uni(e.sc[S_NAV]);
                 irregular = uni(e.sc[S_IRREG]) != 0;
@@ -675,8 +676,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             // the pending entries of the admission, loaded early so their
             // latency overlaps the sampling
             if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
-            uint32_t ke0 = a.key0, ke1 = a.key1;
-            fold_in(ke0, ke1, (uint32_t)step);
+            uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
             fold_in(ke0, ke1, (uint32_t)(a.env0 + l));
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
             // draw words: with n <= 32 the two threefry blocks of a position run
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 if (g.T <= 8) sample_row_words8(g, r, words, act);
                 else sample_row_words(g, r, words, act);
                 if (out.actions) {
-                    int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+                    int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
 #pragma unroll
                     for (int f = 0; f < 7; ++f) dst[f] = act[f];
                 }
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 for (int32_t p = lane; p < owned; p += kWave) {
                     const int32_t sl = g.N + p;
                     if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
-                    int32_t* dst = out.actions + (((int64_t)t * lanes + l) * owned + p) * 7;
+                    int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
 #pragma unroll
                     for (int f = 0; f < 7; ++f) dst[f] = 0;
                 }
@@ -764,8 +764,9 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
         {
             NR_ROLLOUT_PHASE
             nanorts_env_results r = {};
-            if (a.out.rewards) r.reward = a.out.rewards + (int64_t)t * lanes * 2;
-            if (a.out.dones) r.done = a.out.dones + (int64_t)t * lanes;
+            const int64_t tt = (int64_t)a.t0 + t;
+            if (a.out.rewards) r.reward = a.out.rewards + tt * lanes * 2;
+            if (a.out.dones) r.done = a.out.dones + tt * lanes;
             if (finish_step(g, hdr, e, l, lane, a.partial != 0, r, false)) {
                 ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
                 ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
@@ -776,7 +777,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             NR_ROLLOUT_PHASE
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
-            const int64_t slot = (out.depth > 0 ? (int64_t)(t % out.depth) : 0) * lanes + l;
+            const int64_t slot = (out.depth > 0 ? (((int64_t)a.t0 + t) % out.depth) : 0) * lanes + l;
             if (fast) {
                 uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
                 int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
@@ -937,6 +938,31 @@ __global__ void k_probe(int32_t* out) {
     const bool ok = popc(m) == 22 && below == (lane + 2) / 3 && (lane == 0 || up == lane - 1) && mn == 100 - lane;
     const uint64_t all = ballot(ok);
     if (lane == 0) out[0] = all == ~0ull ? 1 : 0;
+}
+
+// Host threefry2x32 (20 rounds) and fold_in(k, d) = threefry(k, (0, d)), the
+// same published Random123 cipher the kernels evaluate.
+static uint32_t host_rotl(uint32_t x, uint32_t d) { return (x << d) | (x >> (32u - d)); }
+static void host_threefry(uint32_t k0, uint32_t k1, uint32_t& x0, uint32_t& x1) {
+    static const uint32_t rot[8] = {13, 15, 26, 6, 17, 29, 16, 24};
+    const uint32_t ks[3] = {k0, k1, k0 ^ k1 ^ 0x1BD11BDAu};
+    x0 += ks[0];
+    x1 += ks[1];
+    for (uint32_t block = 0; block < 5; ++block) {
+        for (uint32_t i = 0; i < 4; ++i) {
+            x0 += x1;
+            x1 = host_rotl(x1, rot[(block & 1u) * 4 + i]);
+            x1 ^= x0;
+        }
+        x0 += ks[(block + 1) % 3];
+        x1 += ks[(block + 2) % 3] + block + 1u;
+    }
+}
+static void host_fold_in(uint32_t& k0, uint32_t& k1, uint32_t data) {
+    uint32_t x0 = 0u, x1 = data;
+    host_threefry(k0, k1, x0, x1);
+    k0 = x0;
+    k1 = x1;
 }
 
 // ---------------------------------------------------------------------------
@@ -1129,25 +1155,35 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
     if (steps < 0) return fail(NANORTS_INVALID_ARGUMENT, "steps must be >= 0");
     if ((results.feature_maps || results.scalars) && results.depth < 1)
         return fail(NANORTS_INVALID_ARGUMENT, "depth must be >= 1");
-    if (lanes <= 0) return NANORTS_OK;
+    if (lanes <= 0 || steps == 0) return NANORTS_OK;
     const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
     if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
-    RolloutArgs args;
-    std::memset(&args, 0, sizeof(args));
-    args.g = sh.g;
-    args.lanes = lanes;
-    args.s = state;
-    args.key0 = sample_key[0];
-    args.key1 = sample_key[1];
-    args.step0 = step0;
-    args.steps = steps;
-    args.partial = partial;
-    args.env0 = env0;
-    args.out = results;
-    hipLaunchKernelGGL(k_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
-                       (hipStream_t)stream, args);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    // launches of at most kRolloutChunk cycles; the state stays in HBM
+    // between them, so the result does not depend on the split
+    for (int32_t t0 = 0; t0 < steps; t0 += kRolloutChunk) {
+        RolloutArgs args;
+        std::memset(&args, 0, sizeof(args));
+        args.g = sh.g;
+        args.lanes = lanes;
+        args.s = state;
+        args.t0 = t0;
+        args.steps = steps - t0 < kRolloutChunk ? steps - t0 : kRolloutChunk;
+        args.partial = partial;
+        args.env0 = env0;
+        args.out = results;
+        for (int32_t t = 0; t < args.steps; ++t) {
+            // the sampler's per-cycle key: fold_in(sample_key, step)
+            uint32_t k0 = sample_key[0], k1 = sample_key[1];
+            host_fold_in(k0, k1, (uint32_t)(step0 + t0 + t));
+            args.step_keys[2 * t] = k0;
+            args.step_keys[2 * t + 1] = k1;
+        }
+        hipLaunchKernelGGL(k_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
+                           (hipStream_t)stream, args);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess)
+            return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    }
     return NANORTS_OK;
 }
 
