@@ -1356,8 +1356,8 @@ NR_DEV Row legality_row(const KGame& g, const Hdr& h, const Env& e, int32_t slot
 
 // ---------------------------------------------------------------------------
 // The synthetic harness sampler (uniform over each factor's legal values):
-//   k_env = fold_in(fold_in(sample_key, step), env);
-//   (w0, w1) = threefry(k_env, (p, 0)), (w2, w3) = threefry(k_env, (p, 1));
+//   k_step = fold_in(sample_key, step);
+//   (w0, w1) = threefry(k_step, (env, 2p)), (w2, w3) = threefry(k_step, (env, 2p + 1));
 //   factor f draws the 16-bit half f of w0..w3 (low half first) and takes the
 //   ((h * popcount) >> 16)-th set bit of its mask, or 0 when the mask is empty.
 // A row whose only set bit is NONE samples all zeros.
@@ -1379,15 +1379,15 @@ NR_DEV int32_t select_set_bit(uint64_t m, int32_t k) {
 
 NR_DEV bool only_none(const Row& r) { return r.w[0] == 1u && r.w[1] == 0u && r.w[2] == 0u; }
 
-NR_DEV void sample_row(const KGame& g, const Row& r, uint32_t ke0, uint32_t ke1, int32_t p, int32_t a[7]) {
+NR_DEV void sample_row(const KGame& g, const Row& r, uint32_t ks0, uint32_t ks1, uint32_t env, int32_t p, int32_t a[7]) {
     if (only_none(r)) {
 #pragma unroll
         for (int f = 0; f < 7; ++f) a[f] = 0;
         return;
     }
-    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
-    threefry(ke0, ke1, w0, w1);
-    threefry(ke0, ke1, w2, w3);
+    uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
+    threefry(ks0, ks1, w0, w1);
+    threefry(ks0, ks1, w2, w3);
     const uint32_t words[4] = {w0, w1, w2, w3};
     const int32_t lo[7] = {0, 6, 10, 14, 18, 22, 22 + g.T};
     const int32_t wid[7] = {6, 4, 4, 4, 4, g.T, g.O};

@@ -577,7 +577,7 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
     (void)e;
     uint32_t k0 = key0, k1 = key1;
     fold_in(k0, k1, (uint32_t)step);
-    fold_in(k0, k1, (uint32_t)(env0 + l));
+    const uint32_t env = (uint32_t)(env0 + l);
     const int32_t owned = 2 * g.C;
     for (int32_t p = lane; p < owned; p += kWave) {
         Row r;
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
         r.w[1] = w[1];
         r.w[2] = w[2];
         int32_t a[7];
-        sample_row(g, r, k0, k1, p, a);
+        sample_row(g, r, k0, k1, env, p, a);
         int32_t* out = actions + (l * owned + p) * 7;
 #pragma unroll
         for (int f = 0; f < 7; ++f) out[f] = a[f];
@@ -676,8 +676,8 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             // the pending entries of the admission, loaded early so their
             // latency overlaps the sampling
             if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
-            uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
-            fold_in(ke0, ke1, (uint32_t)(a.env0 + l));
+            const uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
+            const uint32_t env = (uint32_t)(a.env0 + l);
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
             // draw words: with n <= 32 the two threefry blocks of a position run
             // on two lanes at once; otherwise each lane computes both
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired) {
                 const int32_t u = lane >> 1;
-                uint32_t dx0 = u < n ? (uint32_t)av[u] : 0u, dx1 = (uint32_t)(lane & 1);
+                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
                 // every lane active: lane u takes lanes 2u and 2u + 1
                 pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
@@ -704,7 +704,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                     words[2] = pw2;
                     words[3] = pw3;
                 } else {
-                    uint32_t w0 = (uint32_t)p, w1 = 0u, w2 = (uint32_t)p, w3 = 1u;
+                    uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
                     threefry(ke0, ke1, w0, w1);
                     threefry(ke0, ke1, w2, w3);
                     words[0] = w0;

@@ -42,7 +42,7 @@ NR_DEV int32_t select_bit(uint64_t m, int32_t k) {
 }
 
 // sample_row with the select above (same draws, same result), given the
-// position's four draw words threefry(k_env, (p, 0)) ++ threefry(k_env, (p, 1)).
+// position's four draw words threefry(k_step, (env, 2p)) ++ threefry(k_step, (env, 2p + 1)).
 NR_DEV void sample_row_words(const KGame& g, const Row& r, const uint32_t words[4], int32_t a[7]) {
     if (only_none(r)) {
 #pragma unroll

@@ -1196,9 +1196,9 @@ void nro_decode_actions(const nro_game* g, const nro_state* s, const int32_t* ac
 /* ------------------------------------------------------------------------ */
 /* Synthetic harness sampler (this build's own definition, replacing the     */
 /* README's float jax.random.categorical with an integer uniform draw):       */
-/*   k_env = fold_in(fold_in(sample_key, step), env)                          */
-/*   (w0,w1) = threefry(k_env, (agent*C + row, 0)),                           */
-/*   (w2,w3) = threefry(k_env, (agent*C + row, 1))                            */
+/*   k_step = fold_in(sample_key, step), p = agent*C + row                    */
+/*   (w0,w1) = threefry(k_step, (env, 2p)),                                   */
+/*   (w2,w3) = threefry(k_step, (env, 2p + 1))                                */
 /*   factor f draws h_f = 16-bit half f of w0..w3 (low half first);          */
 /*   value = the ((h_f * popcount) >> 16)-th set bit of the factor's mask    */
 /*   (multiply-shift range reduction), or 0 when the factor has no set bit   */
@@ -1220,9 +1220,8 @@ static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sa
     const int32_t C = g->capacity, width = row_width(g);
     int32_t lo[7], wid[7];
     factor_bounds(g, lo, wid);
-    uint32_t kt[2], ke[2];
+    uint32_t kt[2];
     nro_fold_in(sample_key, (uint32_t)step, kt);
-    nro_fold_in(kt, (uint32_t)env, ke);
     for (int32_t p = 0; p < 2 * C; ++p) {
         const uint8_t* row = rows + (size_t)p * width;
         int32_t* out = actions + (size_t)p * 7;
@@ -1233,9 +1232,9 @@ static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sa
             for (int f = 0; f < 7; ++f) out[f] = 0;
             continue;
         }
-        uint32_t w01[2] = {(uint32_t)p, 0u}, w23[2] = {(uint32_t)p, 1u};
-        nro_threefry2x32(ke, w01);
-        nro_threefry2x32(ke, w23);
+        uint32_t w01[2] = {(uint32_t)env, (uint32_t)(2 * p)}, w23[2] = {(uint32_t)env, (uint32_t)(2 * p + 1)};
+        nro_threefry2x32(kt, w01);
+        nro_threefry2x32(kt, w23);
         const uint32_t words[4] = {w01[0], w01[1], w23[0], w23[1]};
         for (int f = 0; f < 7; ++f) {
             const uint32_t h = (words[f / 2] >> (16 * (f % 2))) & 0xFFFFu;
