@@ -195,16 +195,16 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     if (o > end) end = o;
     // summary temporaries (the command arrays are dead then)
     o = union0;
-    y.o_lo = take(E * 4);
-    y.o_fl = take(E);
+    y.o_lo = take((E + 1) * 4);  // + the empty-cell sentinel
+    y.o_fl = take(E + 1);
     y.b_units = take(C2 * 2);
     y.v_seen = take(2 * g.H * g.seen_words * 4);
     y.o_slist = take(E * 2);
     if (o > commands_end) {
         // larger boards: after the persistent lists instead
         o = end;
-        y.o_lo = take(E * 4);
-        y.o_fl = take(E);
+        y.o_lo = take((E + 1) * 4);
+        y.o_fl = take(E + 1);
         y.b_units = take(C2 * 2);
         y.v_seen = take(2 * g.H * g.seen_words * 4);
         y.o_slist = take(E * 2);

@@ -234,15 +234,22 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
             }
             alive = e.birth[s] != kAbsent;
             if (alive) {
+                // occupant word: hp | carried << 8 | owner' << 16 | pending
+                // kind << 18 | (type + 1) << 24, owner' = 1 player 0, 2
+                // player 1, 0 neutral; plane flags: bit 0 occupied, 1 / 2
+                // unit of player 0 / 1, 3 resource, 4 / 5 stockpile of player
+                // 0 / 1 (the rows of the occupancy bitmaps)
                 const int32_t ty = e.utype[s];
                 const int32_t ow = e.owner[s];
                 const uint32_t rel0 = ow == 0 ? 1u : (ow == 1 ? 2u : 0u);
-                olo[s] = ((uint32_t)(int32_t)e.hp[s] & 0xFFu) | (((uint32_t)e.carried[s] & 0xFFu) << 8) |
-                         (rel0 << 16) | (((uint32_t)(ty + 1) & 0xFFu) << 24);
                 const int32_t pk = e.pkind[s];
+                olo[s] = ((uint32_t)(int32_t)e.hp[s] & 0xFFu) | (((uint32_t)e.carried[s] & 0xFFu) << 8) |
+                         (rel0 << 16) | ((uint32_t)((pk > 0 ? pk : 0) & 7) << 18) |
+                         (((uint32_t)(ty + 1) & 0xFFu) << 24);
                 const int32_t fl = tabv(h, F_FLAGS, clampi(ty, 0, g.T - 1));
-                ofl[s] = (uint8_t)(((pk > 0 ? pk : 0) & 0xF) | ((fl & FL_RESOURCE) ? 16 : 0) |
-                                   ((fl & FL_STOCKPILE) ? 32 : 0));
+                const uint32_t stk = (fl & FL_STOCKPILE) ? 1u : 0u;
+                ofl[s] = (uint8_t)(1u | (rel0 << 1) | ((fl & FL_RESOURCE) ? 8u : 0u) | ((stk & (rel0 & 1u)) << 4) |
+                                   ((stk & (rel0 >> 1)) << 5));
                 available = s >= g.N && pk == kAbsent;
                 if (available && e.porder[s] != kAbsent) odd = true;
             }
@@ -261,6 +268,9 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
     // irregular: the env-path admission does not apply (admit_env)
     const bool irregular = ballot(odd) != 0ull || nA > kWave || next_order > 0x7fffffff - kWave;
     if (lane == 0) {
+        // the empty cell's sentinel (index E) of the occupant arrays
+        olo[g.E] = 0u;
+        ofl[g.E] = 0u;
         e.sc[S_NAV] = nav;
         e.sc[S_NUNITS] = nunits;
         e.sc[S_NA] = nA;
@@ -361,34 +371,34 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
     AS3 const uint8_t* ofl = at<uint8_t>(e, y.o_fl);
     AS3 const uint32_t* seen = at<uint32_t>(e, y.v_seen);
     const bool obs = maps0 != nullptr;
+    // bits 0, 8, 16, 24 of x -> bits 0..3
+    auto nibble = [](uint32_t x) {
+        x |= x >> 7;
+        x |= x >> 14;
+        return x & 15u;
+    };
     for (int32_t base = 0; base < g.cells; base += 4 * kWave) {
         const int32_t c0 = base + 4 * lane;
         if (c0 >= g.cells) continue;
         const uint64_t ent = *(AS3 const uint64_t*)(e.entity + c0);
-        const uint32_t ter = *(AS3 const uint32_t*)(h.terrain + c0);
+        const uint32_t ter = *(AS3 const uint32_t*)(h.terrain + c0);  // one 0/1 byte per cell
         const int32_t yy = c0 / g.W, x = c0 - yy * g.W;
         const int32_t word = yy * words + (x >> 5), shift = x & 31;
-        uint32_t lo[4], fl[4];
-        uint32_t occ_n = 0u, p0_n = 0u, p1_n = 0u, res_n = 0u, stk0_n = 0u, stk1_n = 0u;
+        // the occupants' words and flags; an empty cell reads the zero
+        // sentinel at index E (ABSENT -> 0xFFFFFFFF -> min E)
+        uint32_t lo[4], F = 0u;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int32_t occ = (int16_t)(uint16_t)(ent >> (16 * k));
-            lo[k] = 0u;
-            fl[k] = 0u;
-            if (occ != kAbsent) {
-                const int32_t sl = gidx(occ, g.E);
-                lo[k] = olo[sl];
-                fl[k] = ofl[sl];
-            }
-            const uint32_t rel = (lo[k] >> 16) & 3u;
-            occ_n |= (occ != kAbsent || ((ter >> (8 * k)) & 0xFFu) != 0u ? 1u : 0u) << k;
-            p0_n |= (rel == 1u ? 1u : 0u) << k;
-            p1_n |= (rel == 2u ? 1u : 0u) << k;
-            res_n |= ((fl[k] >> 4) & 1u) << k;
-            stk0_n |= (((fl[k] >> 5) & 1u) & (rel == 1u ? 1u : 0u)) << k;
-            stk1_n |= (((fl[k] >> 5) & 1u) & (rel == 2u ? 1u : 0u)) << k;
+            const uint32_t idx = __builtin_elementwise_min((uint32_t)(int32_t)(int16_t)(uint16_t)(ent >> (16 * k)),
+                                                           (uint32_t)g.E);
+            lo[k] = olo[idx];
+            F |= (uint32_t)ofl[idx] << (8 * k);
         }
+        const uint32_t occ_n = nibble((F & 0x01010101u) | ter);
+        const uint32_t p0_n = nibble((F >> 1) & 0x01010101u), p1_n = nibble((F >> 2) & 0x01010101u);
         if (bitmaps) {
+            const uint32_t res_n = nibble((F >> 3) & 0x01010101u);
+            const uint32_t stk0_n = nibble((F >> 4) & 0x01010101u), stk1_n = nibble((F >> 5) & 0x01010101u);
             if (occ_n) __atomic_fetch_or(&bm[word], occ_n << shift, __ATOMIC_RELAXED);
             if (p0_n) __atomic_fetch_or(&bm[plane + word], p0_n << shift, __ATOMIC_RELAXED);
             if (p1_n) __atomic_fetch_or(&bm[2 * plane + word], p1_n << shift, __ATOMIC_RELAXED);
@@ -397,6 +407,16 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
             if (stk1_n) __atomic_fetch_or(&bm[5 * plane + word], stk1_n << shift, __ATOMIC_RELAXED);
         }
         if (!obs) continue;
+        // per cell: the word without the kind bits, the kind byte and the
+        // terrain byte (shown to both players)
+        uint32_t clean[4], kindb[4], terb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            clean[k] = lo[k] & ~(7u << 18);
+            kindb[k] = (lo[k] >> 18) & 7u;
+            terb[k] = ((ter >> (8 * k)) & 0xFFu) << 8;
+        }
+        const uint32_t owned_n = p0_n | p1_n;
 #pragma unroll
         for (int32_t pl = 0; pl < 2; ++pl) {
             const uint32_t own = pl == 0 ? p0_n : p1_n;
@@ -405,10 +425,10 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const bool shown = (vis >> k) & 1u;
-                uint32_t v = lo[k];
-                if (pl == 1 && ((v >> 16) & 3u) != 0u) v ^= 3u << 16;
+                // player 1 sees owners 1 <-> 2 swapped (neutral stays 0)
+                const uint32_t v = pl == 1 ? clean[k] ^ (((owned_n >> k) & 1u) ? (3u << 16) : 0u) : clean[k];
                 l4[k] = shown ? v : 0u;
-                h4[k] = (shown ? (fl[k] & 0xFu) : 0u) | (((ter >> (8 * k)) & 0xFFu) << 8);
+                h4[k] = (shown ? kindb[k] : 0u) | terb[k];
             }
             uint64_t* dst = (uint64_t*)((pl == 0 ? maps0 : maps1) + (int64_t)c0 * 6);
             dst[0] = (uint64_t)l4[0] | ((uint64_t)(h4[0] | (l4[1] << 16)) << 32);
