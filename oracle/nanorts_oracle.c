@@ -14,6 +14,19 @@
  *  - residue.masked_set writes only where position == index
  *    (N/core/residue.py:24-26), so an out-of-range index is a no-op;
  *  - a store into a narrower leaf truncates (jnp.asarray(new, old.dtype)).
+ *
+ * How each part is pinned (tests/test_oracle.py, tests/test_rendering.py):
+ * threefry by Random123 known answers and JAX's classic split vector; fold_in,
+ * randint01 and the CANCEL_RANDOM draw by the reference's own
+ * conflict_draw.cuh (oracle/_ref, and golden vectors from it); admission,
+ * durations, completion and outcome by hand-traced cycles on the 8x8 map;
+ * masks against admission by brute force over every single command;
+ * visibility, symbolic and pixel observations by closed forms; the state
+ * invariants over long rollouts of every case.
+ * Parity unpinned: the exact settled durations of cancelled pendings when
+ * several conflicts meet in one cycle (_settle_durations,
+ * N/core/reservations.py:169-204) -- restated here, covered by the invariants
+ * and the single-conflict races, with no reference vectors to compare.
  */
 #include "nanorts_oracle.h"
 
