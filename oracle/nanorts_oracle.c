@@ -1504,3 +1504,8 @@ int32_t nro_state_violations(const nro_game* g, const nro_state* s, int64_t l) {
     }
     return bits;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Scripted bots and the learner-vs-bot seat (bots.c shares the env view).   */
+/* ------------------------------------------------------------------------ */
+#include "bots.c"

@@ -166,6 +166,40 @@ int32_t nro_rollout(const nro_game* g, const nro_state* initial, nro_state* s,
                     int32_t partial, int32_t threads, float* rewards, uint8_t* dones,
                     int32_t* actions, uint8_t* last_feature_maps, int32_t* last_scalars);
 
+/* Carry of an abstraction-family bot (AbstractActions,
+ * src/nanorts/bots/abstraction.py:70-81): [L][C] rows and next_order [L]. */
+typedef struct nro_abstract {
+    int32_t* kind;
+    int32_t* unit_birth;
+    int32_t* order;
+    int32_t* target;
+    int32_t* target_birth;
+    int32_t* base;
+    int32_t* base_birth;
+    int32_t* cell;
+    int32_t* unit_type;
+    uint8_t* trained;
+    int32_t* next_order;
+} nro_abstract;
+
+/* family.act (src/nanorts/bots/family.py:34-41): strategy 0 WorkerRush,
+ * 1 barracks rush training `trained_type` (LightRush: 4).  Commands for both
+ * players [L][2][C] (the other player's rows empty); carry updated in place. */
+void nro_abstraction_act(const nro_game* g, const nro_state* s, int64_t L, int32_t strategy,
+                         int32_t trained_type, const int32_t* player, nro_abstract* carry,
+                         nro_commands* out);
+/* abstraction.empty_actions for envs [0, L). */
+void nro_empty_actions(const nro_game* g, nro_abstract* carry, int64_t L);
+/* pathfinding.search over open cells bool[H*W]: returns the first step
+ * direction or -1; out = {found, step, distance, pops}. */
+int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start, int32_t target,
+                  int32_t range, int32_t out[4]);
+/* seat.step_seat with the learner at `learner`: actions [L][C][7] are the
+ * learner's rows; the bot plays 1 - learner. */
+void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, int64_t L, int32_t strategy,
+                   int32_t trained_type, int32_t learner, nro_abstract* carry, const int32_t* actions,
+                   int32_t partial, nro_env_out* out);
+
 /* Invariant check (src/nanorts/model/state.py:87-165); returns a bitmask of
  * violated invariants for env l, 0 when the state is well formed. */
 int32_t nro_state_violations(const nro_game* g, const nro_state* s, int64_t l);

@@ -37,7 +37,19 @@ def _load() -> ctypes.CDLL:
     lib.nro_state_violations.restype = ctypes.c_int32
     lib.nro_conflict_draw.restype = ctypes.c_int32
     lib.nro_randint01.restype = ctypes.c_int32
+    lib.nro_astar.restype = ctypes.c_int32
     return lib
+
+
+def astar(open_cells: np.ndarray, start: int, target: int, range_: int) -> tuple[int, int, int, int]:
+    """pathfinding.search over bool[H, W] open cells: (found, step, distance, pops)."""
+    lib = _load()
+    H, W = open_cells.shape
+    cells = np.ascontiguousarray(open_cells.reshape(-1).astype(np.uint8))
+    out = (ctypes.c_int32 * 4)()
+    lib.nro_astar(_ptr(cells), ctypes.c_int32(W), ctypes.c_int32(H), ctypes.c_int32(start), ctypes.c_int32(target),
+                  ctypes.c_int32(range_), out)
+    return int(out[0]), int(out[1]), int(out[2]), int(out[3])
 
 
 _I32x8 = ctypes.c_int32 * MAX_TYPES
@@ -80,6 +92,22 @@ class EnvOut(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in
                 ("reward", "done", "terminated", "truncated", "winner", "spawn_overflowed", "feature_maps",
                  "scalars")]
+
+
+ABSTRACT_FIELDS = ("kind", "unit_birth", "order", "target", "target_birth", "base", "base_birth", "cell",
+                   "unit_type", "trained", "next_order")
+
+
+class Abstract(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in ABSTRACT_FIELDS]
+
+
+def empty_carry(L: int, C: int) -> dict[str, np.ndarray]:
+    """abstraction.empty_actions for L envs (src/nanorts/bots/abstraction.py:118-133)."""
+    carry = {f: np.full((L, C), -1, np.int32) for f in ABSTRACT_FIELDS[:9]}
+    carry["trained"] = np.zeros((L, C), np.uint8)
+    carry["next_order"] = np.zeros(L, np.int32)
+    return carry
 
 
 def _ptr(array: np.ndarray | None) -> ctypes.c_void_p | None:
@@ -243,6 +271,39 @@ class Oracle:
             ctypes.c_int32(threads), _ptr(out["rewards"]), _ptr(out["dones"]), _ptr(out["actions"]),
             _ptr(out["feature_maps"]), _ptr(out["scalars"]))
         out["threads"] = used
+        return out
+
+    def abstraction_act(self, state, carry: dict[str, np.ndarray], strategy: int, trained_type: int,
+                        player) -> dict[str, np.ndarray]:
+        """family.act: the bot's commands [L][2][C] per field; `carry` is updated in place."""
+        L = state["time"].shape[0]
+        C = self.game.bucket.per_player_capacity
+        out = {f: np.zeros((L, 2, C), np.int32) for f, _ in Commands._fields_}
+        c = Commands(*[_ptr(out[f]) for f, _ in Commands._fields_])
+        players = np.ascontiguousarray(np.broadcast_to(np.asarray(player, np.int32), (L,)))
+        a = Abstract(*[_ptr(carry[f]) for f in ABSTRACT_FIELDS])
+        self.lib.nro_abstraction_act(ctypes.byref(self.g), ctypes.byref(self._s(state)), ctypes.c_int64(L),
+                                     ctypes.c_int32(strategy), ctypes.c_int32(trained_type), _ptr(players),
+                                     ctypes.byref(a), ctypes.byref(c))
+        return out
+
+    def seat_step(self, state, carry: dict[str, np.ndarray], strategy: int, trained_type: int, learner: int,
+                  actions: np.ndarray, partial: bool, observe: bool = True) -> dict[str, np.ndarray]:
+        """step_seat with the learner's action rows [L][C][7]; state and carry updated in place."""
+        L = state["time"].shape[0]
+        b = self.game.bucket
+        out = {"reward": np.zeros((L, 2), np.float32), "done": np.zeros(L, np.uint8),
+               "terminated": np.zeros(L, np.uint8), "truncated": np.zeros(L, np.uint8),
+               "winner": np.zeros(L, np.int32), "spawn_overflowed": np.zeros(L, np.uint8),
+               "feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if observe else None,
+               "scalars": np.zeros((L, 2, 4), np.int32) if observe else None}
+        o = EnvOut(*[_ptr(out[f]) for f, _ in EnvOut._fields_])
+        a = Abstract(*[_ptr(carry[f]) for f in ABSTRACT_FIELDS])
+        actions = np.ascontiguousarray(actions, np.int32)
+        self.lib.nro_seat_step(ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)),
+                               ctypes.c_int64(L), ctypes.c_int32(strategy), ctypes.c_int32(trained_type),
+                               ctypes.c_int32(learner), ctypes.byref(a), _ptr(actions), ctypes.c_int32(int(partial)),
+                               ctypes.byref(o))
         return out
 
     def violations(self, state) -> np.ndarray:

@@ -1,0 +1,293 @@
+"""Pins of the scripted-bot part of the CPU oracle (CPU only, no GPU).
+
+The A* search is checked against a second formulation written from the
+reference's program form (src/nanorts/bots/pathfinding.py:170-245: a global
+argmin over f * (cells + 1) + (cells - sequence) keys, where the oracle keeps
+stacks of buckets) and against breadth-first distances.  The bot's decisions
+are checked by a cycle traced by hand on the shipped 8x8 map, the ring walk of
+building sites by an independent perimeter walk, the Commands contract of the
+reference (src/nanorts/model/commands.py:37-70), and whole games against a
+passive opponent (WorkerRush wins, LightRush builds barracks and trains light
+units).
+"""
+from __future__ import annotations
+
+from collections import deque
+
+import numpy as np
+import pytest
+
+from nanorts_amd.content import map_name_to_scenario
+from nanorts_amd.model import STATE_LEAVES, UnitTypeTableVersion
+from oracle import oracle as orc
+from oracle.oracle import Oracle, batch_initial, empty_carry
+
+NONE, MOVE, HARVEST, RETURN, PRODUCE, ATTACK = range(6)
+UP, RIGHT, DOWN, LEFT = range(4)
+RESOURCE, BASE, BARRACKS, WORKER, LIGHT = 0, 1, 2, 3, 4
+WORKER_RUSH, BARRACKS_RUSH = 0, 1
+STEPS = ((0, -1), (1, 0), (0, 1), (-1, 0))
+
+
+# ---------------------------------------------------------------------------
+# A*
+# ---------------------------------------------------------------------------
+def astar_by_keys(free: np.ndarray, start: int, target: int, range_: int):
+    """The search in the program's key form: every open cell holds
+    f * (cells + 1) + (cells - sequence); the least key is popped."""
+    H, W = free.shape
+    cells = H * W
+    closed = 2**31 - 1
+    blocked, unseen = closed - 1, closed - 2
+    key = np.where(free.reshape(-1), unseen, blocked).astype(np.int64)
+    after = np.full(cells, -1, np.int64)
+    tx, ty = target % W, target // W
+
+    def manhattan(c):
+        return abs(c % W - tx) + abs(c // W - ty)
+
+    if 0 <= start < cells:
+        key[start] = manhattan(start) * (cells + 1) + cells
+        after[start] = start
+    inserted, goal, pops, searching = 1, -1, 0, True
+    while searching and pops < cells:
+        cell = int(np.argmin(key))
+        k = int(key[cell])
+        exhausted = k >= unseen
+        reached = not exhausted and (cell % W - tx) ** 2 + (cell // W - ty) ** 2 <= range_ * range_
+        expands = not exhausted and not reached
+        if expands:
+            g = k // (cells + 1) - manhattan(cell)
+            fresh = []
+            for dx, dy in STEPS:
+                x, y = cell % W + dx, cell // W + dy
+                if 0 <= x < W and 0 <= y < H and key[y * W + x] == unseen:
+                    fresh.append(y * W + x)
+            key[cell] = closed
+            for n in fresh:
+                key[n] = (g + 1 + manhattan(n)) * (cells + 1) + (cells - inserted)
+                after[n] = n if cell == start else after[cell]
+                inserted += 1
+        if reached:
+            goal = cell
+        searching = expands
+        pops += 0 if exhausted else 1
+    if goal < 0:
+        return 0, -1, -1, pops
+    offset = int(after[goal]) - start
+    # jnp.select: the first matching case wins (on a one-wide board -1 is LEFT)
+    step = next((d for o, d in ((W, DOWN), (-1, LEFT), (-W, UP), (1, RIGHT)) if offset == o), -1)
+    return 1, step, int(key[goal]) // (cells + 1) - manhattan(goal), pops
+
+
+def bfs(free: np.ndarray, start: int):
+    H, W = free.shape
+    dist = np.full(H * W, -1, np.int64)
+    dist[start] = 0
+    queue = deque([start])
+    while queue:
+        c = queue.popleft()
+        for dx, dy in STEPS:
+            x, y = c % W + dx, c // W + dy
+            n = y * W + x
+            if 0 <= x < W and 0 <= y < H and free.reshape(-1)[n] and dist[n] < 0:
+                dist[n] = dist[c] + 1
+                queue.append(n)
+    return dist
+
+
+def test_astar_matches_key_formulation_and_bfs():
+    rng = np.random.default_rng(5)
+    for trial in range(400):
+        H, W = int(rng.integers(1, 9)), int(rng.integers(1, 9))
+        free = rng.random((H, W)) < rng.uniform(0.5, 0.95)
+        start, target = int(rng.integers(0, H * W)), int(rng.integers(0, H * W))
+        if trial % 3:
+            free.reshape(-1)[start] = False  # a unit stands on its start cell
+        range_ = int(rng.integers(0, 4))
+        got = orc.astar(free, start, target, range_)
+        assert got == astar_by_keys(free, start, target, range_), (trial, H, W, start, target, range_)
+        # completeness and, for a point goal, optimality
+        open_ = free.copy()
+        open_.reshape(-1)[start] = True
+        dist = bfs(open_, start)
+        cells = np.arange(H * W)
+        within = (cells % W - target % W) ** 2 + (cells // W - target // W) ** 2 <= range_ * range_
+        reachable = within & (dist >= 0)
+        assert got[0] == int(reachable.any())
+        if range_ == 0 and got[0]:
+            assert got[2] == dist[target]
+        if got[0] and got[2] > 0 and W > 1:
+            first = start + {UP: -W, RIGHT: 1, DOWN: W, LEFT: -1}[got[1]]
+            assert open_.reshape(-1)[first] and dist[first] == 1
+
+
+def test_astar_last_inserted_first_among_equal_f():
+    """Open 3x3 board from the centre to the bottom-right corner: right and
+    down tie on f; down, pushed later, is expanded first."""
+    free = np.ones((3, 3), bool)
+    assert orc.astar(free, 4, 8, 0)[:3] == (1, DOWN, 2)
+    free[2, 1] = False  # below the centre blocked: right leads
+    assert orc.astar(free, 4, 8, 0)[:3] == (1, RIGHT, 2)
+
+
+# ---------------------------------------------------------------------------
+# Bots on basesWorkers8x8: slots 0/1 piles at cells 0 / 63; player 0 base
+# (slot 2, birth 2) at 10 and worker (slot 3, birth 4) at 9; player 1 base
+# (slot 49, birth 3) at 53 and worker (slot 50, birth 5) at 54; balances 5/5.
+# ---------------------------------------------------------------------------
+def _eight(utt=UnitTypeTableVersion.ORIGINAL_FINETUNED, max_cycles=5000):
+    game = map_name_to_scenario("basesWorkers8x8", utt=utt, max_cycles=max_cycles)
+    return game, Oracle(game), batch_initial(game, 1, np.asarray([[1, 2]], np.uint32))
+
+
+def test_worker_rush_first_cycle_by_hand():
+    game, o, st = _eight()
+    C = game.bucket.per_player_capacity
+    carry = empty_carry(1, C)
+    cmds = o.abstraction_act(st, carry, WORKER_RUSH, LIGHT, 1)
+    # player 0's rows stay empty
+    assert (cmds["kind"][0, 0] == -1).all() and (cmds["request_order"][0, 0] == -1).all()
+    k, d, t, r = (cmds[f][0, 1] for f in ("kind", "direction", "produced_type", "request_order"))
+    # the base trains a worker toward the nearer pile: below it (cell 61) is
+    # 2 from pile 63, above and left are 4
+    assert (k[0], d[0], t[0], r[0]) == (PRODUCE, DOWN, WORKER, 0)
+    # the worker heads for pile 63: right (55) and down (62) tie on f; down
+    # was pushed last and is reached first
+    assert (k[1], d[1], r[1]) == (MOVE, DOWN, 1)
+    assert (k[2:] == -1).all()
+    # carry: TRAIN (executed, so trained) and HARVEST of pile 1 to base 49
+    assert carry["kind"][0, :2].tolist() == [3, 2] and carry["trained"][0, :2].tolist() == [1, 0]
+    assert carry["target"][0, 1] == 1 and carry["target_birth"][0, 1] == 1
+    assert carry["base"][0, 1] == 49 and carry["base_birth"][0, 1] == 3
+    assert carry["order"][0, :2].tolist() == [0, 1] and carry["next_order"][0] == 2
+    assert carry["unit_type"][0, 0] == WORKER and (carry["kind"][0, 2:] == -1).all()
+
+
+def test_worker_rush_second_cycle_drops_the_trained_entry():
+    """The TRAIN entry was executed, so the next act sees it completed unless
+    the base is chosen again; the base is busy producing, so it is not."""
+    game, o, st = _eight()
+    C = game.bucket.per_player_capacity
+    carry = empty_carry(1, C)
+    cmds = o.abstraction_act(st, carry, WORKER_RUSH, LIGHT, 1)
+    merged = {f: v.copy() for f, v in cmds.items()}
+    merged["kind"][0, 0, :] = -1
+    o.core_step(st, merged, np.asarray([[1, 2]], np.uint32))
+    assert st["pending_kind"][0, 49] == PRODUCE and st["pending_kind"][0, 50] == MOVE
+    cmds = o.abstraction_act(st, carry, WORKER_RUSH, LIGHT, 1)
+    assert (cmds["kind"][0, 1] == -1).all()  # both units busy: nothing issued
+    assert carry["kind"][0, 0] == -1 and carry["kind"][0, 1] == 2 and carry["next_order"][0] == 1
+
+
+def _ring_walk(H, W, desired):
+    """Cells around `desired` ring by ring: top side left to right, right side
+    downward, bottom side left to right, left side downward."""
+    x0, y0 = desired % W, desired // W
+    for ring in range(1, max(H, W)):
+        side = [(x0 + dx, y0 - ring) for dx in range(-ring, ring + 1)]
+        side += [(x0 + ring, y0 + dy) for dy in range(-ring + 1, ring + 1)]
+        side += [(x0 + dx, y0 + ring) for dx in range(-ring, ring)]
+        side += [(x0 - ring, y0 + dy) for dy in range(-ring + 1, ring)]
+        for x, y in side:
+            if 0 <= x < W and 0 <= y < H:
+                yield y * W + x
+
+
+def _clear(st, slot):
+    st["entity_at"].reshape(1, -1)[0, int(st["cell"][0, slot])] = -1
+    for leaf in STATE_LEAVES:
+        if leaf.kind == "slot":
+            st[leaf.name][0, slot] = leaf.fill
+
+
+def _place(st, slot, cell):
+    st["entity_at"].reshape(1, -1)[0, int(st["cell"][0, slot])] = -1
+    st["entity_at"].reshape(1, -1)[0, cell] = slot
+    st["cell"][0, slot] = cell
+
+
+@pytest.mark.parametrize("worker_cell", [54, 27, 0 + 8, 36])
+def test_build_site_follows_the_ring_walk(worker_cell):
+    """Without a base and with 10 resources, WorkerRush's worker builds one at
+    the first open cell of the ring walk around it."""
+    game, o, st = _eight()
+    H, W = game.bucket.height, game.bucket.width
+    C = game.bucket.per_player_capacity
+    _clear(st, 49)
+    _place(st, 50, worker_cell)
+    st["player_resources"][0, 1] = 10
+    carry = empty_carry(1, C)
+    o.abstraction_act(st, carry, WORKER_RUSH, LIGHT, 1)
+    occupied = st["entity_at"].reshape(-1) != -1
+    want = next(c for c in _ring_walk(H, W, worker_cell) if not occupied[c] and not game.terrain.reshape(-1)[c])
+    assert carry["kind"][0, 1] == 4 and carry["unit_type"][0, 1] == BASE and carry["cell"][0, 1] == want
+
+
+def _check_commands(cmds, st, game, bot):
+    """Commands.check_values (src/nanorts/model/commands.py:37-70) plus the
+    translate contract: only available units of the bot get a command, the
+    issued request orders are 0..k-1, fillers wait 10."""
+    C, N = game.bucket.per_player_capacity, game.bucket.neutral_capacity
+    for l in range(cmds["kind"].shape[0]):
+        assert (cmds["kind"][l, 1 - bot] == -1).all()
+        kind, order = cmds["kind"][l, bot], cmds["request_order"][l, bot]
+        slots = N + bot * C + np.arange(C)
+        available = (st["birth"][l, slots] != -1) & (st["pending_kind"][l, slots] == -1)
+        issued = kind != -1
+        assert (issued == available).all()
+        assert (order[~issued] == -1).all()
+        assert sorted(order[issued].tolist()) == list(range(int(issued.sum())))
+        filler = kind == NONE
+        assert (cmds["none_duration"][l, bot][filler] == 10).all()
+
+
+def _seat_games(strategy, trained, envs, steps, utt=UnitTypeTableVersion.ORIGINAL_FINETUNED, passive=False,
+                seed=3):
+    game = map_name_to_scenario("basesWorkers8x8", utt=utt, max_cycles=5000)
+    o = Oracle(game)
+    C = game.bucket.per_player_capacity
+    st = batch_initial(game, envs, np.stack([np.arange(envs), np.arange(envs) + 7], 1).astype(np.uint32))
+    carry = empty_carry(envs, C)
+    log = []
+    for t in range(steps):
+        if passive:
+            actions = np.zeros((envs, C, 7), np.int32)
+        else:
+            rows = o.avail_rows(st)
+            actions = o.sample_actions(rows, (seed, seed + 9), t)[:, 0]
+        probe = {k: v.copy() for k, v in carry.items()}
+        cmds = o.abstraction_act({k: v.copy() for k, v in st.items()}, probe, strategy, trained, 1)
+        _check_commands(cmds, st, game, 1)
+        out = o.seat_step(st, carry, strategy, trained, 0, actions, False, observe=False)
+        assert (o.violations(st) == 0).all(), t
+        log.append((out, st["unit_type"].copy(), st["owner"].copy(), st["birth"].copy()))
+    return game, st, carry, log
+
+
+def test_worker_rush_beats_a_passive_opponent():
+    game, st, carry, log = _seat_games(WORKER_RUSH, LIGHT, 2, 700, passive=True)
+    ends = [(t, int(out["winner"][l])) for t, (out, *_) in enumerate(log) for l in range(2) if out["done"][l]]
+    assert ends, "no game ended"
+    assert all(w == 1 for _, w in ends)
+
+
+def test_light_rush_builds_barracks_and_trains_light_units():
+    game, st, carry, log = _seat_games(BARRACKS_RUSH, LIGHT, 2, 900, passive=True)
+    seen_barracks = seen_light = False
+    for out, utype, owner, birth in log:
+        live = birth != -1
+        seen_barracks |= bool(((utype == BARRACKS) & (owner == 1) & live).any())
+        seen_light |= bool(((utype == LIGHT) & (owner == 1) & live).any())
+    assert seen_barracks and seen_light
+
+
+@pytest.mark.parametrize("strategy", [WORKER_RUSH, BARRACKS_RUSH])
+def test_seat_rollout_keeps_invariants_against_random_play(strategy):
+    game, st, carry, log = _seat_games(strategy, LIGHT, 3, 250)
+    # the carry is empty after a reset and never names a dead unit's entry as standing
+    for l in range(3):
+        live = carry["kind"][l] != -1
+        assert (carry["order"][l][live] >= 0).all()
+        assert sorted(carry["order"][l][live].tolist()) == list(range(int(live.sum())))
+        assert carry["next_order"][l] == int(live.sum())
