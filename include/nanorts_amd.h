@@ -142,6 +142,26 @@ typedef struct nanorts_rollout_results {
     int32_t depth;          /* ring depth of feature_maps / scalars, >= 1 */
 } nanorts_rollout_results;
 
+/* Carry of an abstraction-family bot (AbstractActions,
+ * src/nanorts/bots/abstraction.py:70-81), [L][C] rows updated in place. */
+typedef struct nanorts_abstract_actions {
+    int32_t* kind;
+    int32_t* unit_birth;
+    int32_t* order;
+    int32_t* target;
+    int32_t* target_birth;
+    int32_t* base;
+    int32_t* base_birth;
+    int32_t* cell;
+    int32_t* unit_type;
+    uint8_t* trained;    /* [L][C] bool */
+    int32_t* next_order; /* [L] */
+} nanorts_abstract_actions;
+
+/* Abstraction-family strategies (src/nanorts/bots/family.py:14-17). */
+#define NANORTS_WORKER_RUSH 0
+#define NANORTS_BARRACKS_RUSH 1
+
 const char* nanorts_build_id(void);
 const char* nanorts_targets(void);
 const char* nanorts_last_error(void);
@@ -229,6 +249,31 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
                     const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
                     int64_t env0,
                     nanorts_rollout_results results);
+
+/* family.act of the rush strategies: WorkerRush (NANORTS_WORKER_RUSH) or the
+ * barracks rush training `trained_type` (NANORTS_BARRACKS_RUSH; LightRush
+ * trains type 4).  Writes commands int32[L][6][2][C] (kind, direction,
+ * none_duration, target_cell, produced_type, request_order; the other
+ * player's rows empty) and updates the carry in place.  `player` is
+ * [player_lanes] (1 broadcasts).  Replaces the FFI target
+ * nanorts_abstraction_act (src/nanorts/bots/cuda/abstraction_act.cu:1324),
+ * called through src/nanorts/bots/whole_act.py:125-162 from
+ * src/nanorts/bots/family.py:34-41. */
+int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            int32_t strategy, int32_t trained_type, const int32_t* player, int64_t player_lanes,
+                            nanorts_abstract_actions carry, int32_t* commands);
+
+/* seat.step_seat with a static learner seat in one launch: the bot plays
+ * 1 - learner from the current state, the learner's action rows
+ * int32[L][C][7] are decoded, the merged commands go through core.step under
+ * the episode root, auto-reset, and the carry is emptied where done.  Results
+ * as nanorts_env_step, for both agents.  Replaces step_seat
+ * (src/nanorts/bots/seat.py:94-152), which composes the bot's act,
+ * jaxmarl.request_against (src/nanorts/adapters/jaxmarl/env.py:78-96),
+ * core.step and respond. */
+int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                      int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
+                      const int32_t* actions, int32_t partial, nanorts_env_results results);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,184 @@
+"""Scripted opponents on the GPU: WorkerRush and LightRush, and the
+learner-vs-bot seat.
+
+Mirrors src/nanorts/bots/{bot,family,worker_rush,light_rush}.py (the `Bot`
+records and family.act) and src/nanorts/bots/seat.py (SeatEnv with a static
+seat): the bot's decisions run in the nanorts_abstraction_act kernel, and a
+whole seat step (bot act, learner decode, core.step, auto-reset, carry reset)
+is one nanorts_seat_step launch.  Every call is batched over L envs on the
+current HIP stream.
+"""
+from __future__ import annotations
+
+import dataclasses
+from typing import Any, Final
+
+import numpy as np
+import torch
+
+from nanorts_amd import native
+from nanorts_amd.content import GameConfig, with_unit_type_table
+from nanorts_amd.env import (
+    ALL_AGENTS,
+    NanoRTS,
+    EnvironmentState,
+    _ptr,
+    _stream,
+)
+from nanorts_amd.model import ModelError, UnitTypeTableVersion
+
+WORKER_RUSH: Final = 0
+BARRACKS_RUSH: Final = 1
+TYPE_LIGHT: Final = 4
+LEARNER: Final = "learner"
+SEAT_RULES: Final = ("player_0", "player_1")
+
+
+@dataclasses.dataclass(frozen=True)
+class Bot:
+    """An abstraction-family bot (src/nanorts/bots/bot.py:13-22): the
+    family strategy and the unit type its barracks train."""
+
+    name: str
+    strategy: int
+    trained: int = TYPE_LIGHT
+
+
+workerRushAI: Final = Bot("workerRushAI", WORKER_RUSH)  # src/nanorts/bots/worker_rush.py:18-20
+lightRushAI: Final = Bot("lightRushAI", BARRACKS_RUSH, TYPE_LIGHT)  # src/nanorts/bots/light_rush.py:20-22
+ROSTER: Final = {bot.name: bot for bot in (workerRushAI, lightRushAI)}
+
+
+def empty_actions(num_envs: int, capacity: int, device) -> dict[str, torch.Tensor]:
+    """abstraction.empty_actions for L envs (src/nanorts/bots/abstraction.py:118-133)."""
+    carry = {f: torch.full((num_envs, capacity), -1, dtype=torch.int32, device=device)
+             for f in native.ABSTRACT_FIELDS[:9]}
+    carry["trained"] = torch.zeros((num_envs, capacity), dtype=torch.bool, device=device)
+    carry["next_order"] = torch.zeros(num_envs, dtype=torch.int32, device=device)
+    return carry
+
+
+def _carry_struct(carry: dict[str, torch.Tensor]) -> native.AbstractActions:
+    return native.AbstractActions(*[_ptr(carry[f]) for f in native.ABSTRACT_FIELDS])
+
+
+def abstraction_act(env: NanoRTS, state: EnvironmentState, carry: dict[str, torch.Tensor], bot: Bot,
+                    player) -> dict[str, torch.Tensor]:
+    """family.act (src/nanorts/bots/family.py:34-41): Commands [L, 2, C] per
+    field for `player` (an int or int32[L]); the carry is updated in place."""
+    L = state.num_envs
+    C = env.bucket.per_player_capacity
+    players = torch.as_tensor(player, dtype=torch.int32, device=env.device).reshape(-1).contiguous()
+    commands = torch.empty((L, 6, 2, C), dtype=torch.int32, device=env.device)
+    native.check(env.lib.nanorts_abstraction_act(_stream(), env.dev.ref, state.native(), L, bot.strategy,
+                                                 bot.trained, _ptr(players), players.numel(), _carry_struct(carry),
+                                                 _ptr(commands)), "nanorts_abstraction_act")
+    names = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+    return {name: commands[:, f] for f, name in enumerate(names)}
+
+
+@dataclasses.dataclass
+class SeatState:
+    """src/nanorts/bots/seat.py:37-44"""
+
+    environment_state: EnvironmentState
+    carry: dict[str, torch.Tensor]
+    seat: torch.Tensor
+
+
+class SeatEnv:
+    """One learner against a scripted bot (src/nanorts/bots/seat.py:181-332)
+    with a static seat ("player_0" or "player_1")."""
+
+    def __init__(self, bot: Bot, *, scenario: GameConfig, utt: UnitTypeTableVersion | None = None,
+                 seat: str = "player_0", partial_observability: bool = False, final_observation: bool = True,
+                 device: str | torch.device | None = None):
+        if seat not in SEAT_RULES:
+            raise ModelError(f"SeatEnv refuses seat={seat!r}: this build takes {list(SEAT_RULES)}")
+        if bot.strategy not in (WORKER_RUSH, BARRACKS_RUSH):
+            raise ModelError(f"SeatEnv refuses bot {bot.name!r}: the rush family is built")
+        game = scenario if utt is None else with_unit_type_table(scenario, utt)
+        self.env = NanoRTS(game, partial_observability=partial_observability, final_observation=final_observation,
+                           device=device)
+        self.bot = bot
+        self.seat = seat
+        self.learner = SEAT_RULES.index(seat)
+        self.agents = [LEARNER]
+        self.game = game
+        self.device = self.env.device
+
+    def reset(self, key) -> tuple[dict[str, Any], SeatState]:
+        obs, state = self.env.reset(key)
+        L = state.num_envs
+        carry = empty_actions(L, self.env.bucket.per_player_capacity, self.device)
+        seat = torch.full((L,), self.learner, dtype=torch.int32, device=self.device)
+        return {LEARNER: obs[SEAT_RULES[self.learner]]}, SeatState(state, carry, seat)
+
+    def step(self, key, state: SeatState, actions: dict[str, torch.Tensor], reset_state=None, *,
+             donate: bool = False):
+        """seat.step_seat in one launch; the state (and carry) are updated in
+        place with donate=True, else copied first."""
+        del key
+        if reset_state is not None:
+            raise ModelError("SeatEnv.step refuses a reset_state: the auto-reset is the lifecycle's own")
+        env = self.env
+        nxt = state if donate else SeatState(state.environment_state.clone(),
+                                             {k: v.clone() for k, v in state.carry.items()}, state.seat.clone())
+        es = nxt.environment_state
+        L = es.num_envs
+        b = env.bucket
+        d = self.device
+        acts = torch.as_tensor(actions[LEARNER], device=d)
+        if acts.dtype != torch.int32 or tuple(acts.shape) != (L, b.per_player_capacity, 7):
+            raise ModelError(f"learner actions must be int32[{L}, {b.per_player_capacity}, 7]")
+        acts = acts.contiguous()
+        out = {
+            "reward": torch.empty((L, 2), dtype=torch.float32, device=d),
+            "done": torch.empty(L, dtype=torch.bool, device=d),
+            "terminated": torch.empty(L, dtype=torch.bool, device=d),
+            "truncated": torch.empty(L, dtype=torch.bool, device=d),
+            "winner": torch.empty(L, dtype=torch.int32, device=d),
+            "spawn_overflowed": torch.empty(L, dtype=torch.bool, device=d),
+        }
+        maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
+        scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d)
+        fmaps = torch.empty_like(maps) if env.final_observation else None
+        fscal = torch.empty_like(scalars) if env.final_observation else None
+        results = native.EnvResults(
+            _ptr(out["reward"]), _ptr(out["done"]), _ptr(out["terminated"]), _ptr(out["truncated"]),
+            _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
+            None)
+        native.check(env.lib.nanorts_seat_step(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+                                               self.bot.trained, self.learner, _carry_struct(nxt.carry), _ptr(acts),
+                                               env.partial, results), "nanorts_seat_step")
+        p = self.learner
+        obs = env._symbolic(maps, scalars)[SEAT_RULES[p]]
+        infos: dict[str, Any] = {
+            "terminated": out["terminated"], "truncated": out["truncated"], "winner": out["winner"],
+            "telemetry": {"spawn_overflow": es.core_state.spawn_overflow},
+            "spawn_overflowed": out["spawn_overflowed"], "final_valid": out["done"],
+        }
+        if env.final_observation:
+            infos["final_observation"] = {LEARNER: env._symbolic(fmaps, fscal)[SEAT_RULES[p]]}
+        return ({LEARNER: obs}, nxt, {LEARNER: out["reward"][:, p]}, {LEARNER: out["done"], ALL_AGENTS: out["done"]},
+                infos)
+
+    def get_avail_actions(self, state: SeatState, *, form: str = "rows") -> dict[str, torch.Tensor]:
+        return {LEARNER: self.env.get_avail_actions(state.environment_state, form=form)[SEAT_RULES[self.learner]]}
+
+    def get_obs(self, state: SeatState) -> dict[str, Any]:
+        return {LEARNER: self.env.get_obs(state.environment_state)[SEAT_RULES[self.learner]]}
+
+    def get_slot_cells(self, state: SeatState) -> dict[str, torch.Tensor]:
+        return {LEARNER: self.env.get_slot_cells(state.environment_state)[SEAT_RULES[self.learner]]}
+
+    def commands(self, state: SeatState) -> dict[str, torch.Tensor]:
+        """The bot's Commands for the current state (seat.seat_commands,
+        src/nanorts/bots/seat.py:155-161); the carry is updated in place."""
+        return abstraction_act(self.env, state.environment_state, state.carry, self.bot, 1 - self.learner)
+
+
+def carry_numpy(carry: dict[str, torch.Tensor]) -> dict[str, np.ndarray]:
+    out = {k: v.cpu().numpy() for k, v in carry.items()}
+    out["trained"] = out["trained"].astype(np.uint8)
+    return out

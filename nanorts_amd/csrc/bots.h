@@ -1,0 +1,875 @@
+// Scripted bots of the abstraction family on one wave per game: WorkerRush
+// and the barracks rush that LightRush runs (N/bots/rush.py), their
+// translation into Commands (N/bots/abstraction.py with the rush kinds
+// ATTACK / HARVEST / TRAIN / BUILD), and the A* search it calls
+// (N/bots/pathfinding.py).
+//
+// The game state is the wave's LDS env block.  The bot's own per-wave region
+// (after the env block) holds the carry (AbstractActions rows), the plan of
+// each unit, candidate lists and the search scratch.  Decisions are per unit,
+// one lane per own slot; the walk over the queued units is sequential as in
+// the reference (each search sees the cells claimed before it), and each
+// search runs on lane 0 over LDS stacks.
+#pragma once
+
+#include "engine.h"
+
+namespace nr {
+
+constexpr int32_t kLast = 0x7fffffff;
+constexpr int32_t kAbNone = -1;
+constexpr int32_t kAbAttack = 1;
+constexpr int32_t kAbHarvest = 2;
+constexpr int32_t kAbTrain = 3;
+constexpr int32_t kAbBuild = 4;
+constexpr int32_t kAbTrainDirection = 6;
+constexpr int32_t kTypeBase = 1;
+constexpr int32_t kTypeBarracks = 2;
+constexpr int32_t kTypeWorker = 3;
+constexpr int32_t kFillerDuration = 10;
+constexpr int32_t kWorkerRush = 0;
+constexpr int32_t kBarracksRush = 1;
+
+// Offsets in the bot region of one wave (computed on the host).
+struct BotLayout {
+    int32_t bytes;   // region size per wave
+    int32_t origin;  // region offset from the env block
+    // carry rows [C]
+    int32_t k_kind, k_ubirth, k_order, k_target, k_tbirth, k_base, k_bbirth, k_cell, k_utype, k_trained;
+    // per unit [C]
+    int32_t u_flags, u_rank, u_es, u_eb, u_goal, u_radius;
+    int32_t u_fkind, u_fdir, u_ftarget, u_fptype, u_fclaimed, u_fcost;
+    int32_t u_sel, u_dir, u_drank, u_queue;
+    // candidate slot lists [E]
+    int32_t l_enemy, l_resource, l_stock;
+    // search scratch [cells]
+    int32_t a_top, a_below, a_parent, a_seen;
+    // cell bitmaps [ceil(cells / 32)] words
+    int32_t m_claimed, m_free, m_used, m_kept, m_reserved;
+};
+
+// Device view of the carry (AbstractActions) of all lanes, [L][C] rows.
+struct BotCarry {
+    int32_t* row[9];  // kind, unit_birth, order, target, target_birth, base, base_birth, cell, unit_type
+    uint8_t* trained;
+    int32_t* next_order;
+};
+
+enum : int32_t { U_STANDING = 1, U_EXECUTES = 2 };
+enum : int32_t { SEL_NONE = 0, SEL_FALLBACK = 1, SEL_MOVED = 2 };
+
+struct Bot {
+    AS3 uint8_t* base;
+    int32_t player, block;
+    int32_t n_enemy, n_resource, n_stock;
+    int32_t next_order;
+    int32_t reserved0, reserved1;  // pending production cost per player
+};
+
+template <typename T>
+NR_DEV AS3 T* bv(const Bot& b, int32_t offset) {
+    return (AS3 T*)(b.base + offset);
+}
+
+NR_DEV int32_t wave_min(int32_t v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int32_t o = __shfl_xor(v, d, kWave);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+NR_DEV int32_t wave_sum(int32_t v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+NR_DEV int32_t bit_of(const AS3 uint32_t* m, int32_t c) { return (int32_t)((m[c >> 5] >> (c & 31)) & 1u); }
+NR_DEV void set_bit(AS3 uint32_t* m, int32_t c) { __atomic_fetch_or(&m[c >> 5], 1u << (c & 31), __ATOMIC_RELAXED); }
+
+NR_DEV int32_t type_flag(const KGame& g, const Hdr& h, int32_t t, int32_t flag) {
+    return (tabv(h, F_FLAGS, clampi(t, 0, g.T - 1)) & flag) != 0;
+}
+
+// ---------------------------------------------------------------------------
+// own_units (N/bots/abstraction.py:136-160)
+// ---------------------------------------------------------------------------
+struct Unit {
+    int32_t slot, birth, cell, type, carried;
+    bool present, available;
+};
+
+NR_DEV Unit unit_at(const KGame& g, const Env& e, const Bot& b, int32_t i) {
+    Unit u;
+    u.slot = b.block + i;
+    u.birth = e.birth[u.slot];
+    u.cell = e.cell[u.slot];
+    u.type = clampi(e.utype[u.slot], 0, g.T - 1);
+    u.carried = e.carried[u.slot];
+    u.present = u.birth != kAbsent;
+    u.available = u.present && e.pkind[u.slot] == kAbsent;
+    return u;
+}
+
+// Manhattan-nearest slot of a candidate list, ties by the lowest birth then
+// the lowest slot (rush._closest, N/bots/rush.py:30-45).
+NR_DEV void closest(const KGame& g, const Env& e, int32_t origin, const AS3 int16_t* list, int32_t n, int32_t* slot,
+                    int32_t* birth) {
+    const int32_t ox = floor_mod(origin, g.W), oy = floor_div(origin, g.W);
+    int32_t best = kAbsent, bd = kLast, bb = kLast;
+    for (int32_t k = 0; k < n; ++k) {
+        const int32_t j = list[k];
+        const int32_t c = e.cell[j];
+        const int32_t d = abs(ox - cell_x(g, c)) + abs(oy - cell_y(g, c));
+        const int32_t bj = e.birth[j];
+        if (d < bd || (d == bd && bj < bb)) {
+            bd = d;
+            bb = bj;
+            best = j;
+        }
+    }
+    *slot = best;
+    *birth = best == kAbsent ? kAbsent : bb;
+}
+
+// abstraction.put / _written (N/bots/abstraction.py:172-227) for unit i of
+// this lane; the caller advances next_order by C + 1 once per put.
+NR_DEV void put_unit(const KGame& g, const Bot& b, const Unit& u, int32_t i, bool last, int32_t kind, int32_t target,
+                     int32_t tbirth, int32_t base, int32_t bbirth, int32_t cell, int32_t utype, const BotLayout& y) {
+    AS3 int32_t* kk = bv<int32_t>(b, y.k_kind);
+    AS3 int32_t* ub = bv<int32_t>(b, y.k_ubirth);
+    const bool known = kk[i] != kAbNone && ub[i] == u.birth;
+    if (!known) bv<int32_t>(b, y.k_order)[i] = wadd(b.next_order, last ? g.C : (int32_t)bv<int16_t>(b, y.u_rank)[i]);
+    kk[i] = kind;
+    ub[i] = u.birth;
+    bv<int32_t>(b, y.k_target)[i] = target;
+    bv<int32_t>(b, y.k_tbirth)[i] = tbirth;
+    bv<int32_t>(b, y.k_base)[i] = base;
+    bv<int32_t>(b, y.k_bbirth)[i] = bbirth;
+    bv<int32_t>(b, y.k_cell)[i] = cell;
+    bv<int32_t>(b, y.k_utype)[i] = utype;
+    bv<uint8_t>(b, y.k_trained)[i] = 0;
+}
+
+NR_DEV bool is_entry(const Bot& b, const BotLayout& y, int32_t i, int32_t birth, int32_t kind) {
+    return bv<int32_t>(b, y.k_kind)[i] == kind && bv<int32_t>(b, y.k_ubirth)[i] == birth;
+}
+
+// ---------------------------------------------------------------------------
+// Setup: units, carry, candidate lists
+// ---------------------------------------------------------------------------
+NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
+                      const BotCarry& carry, int lane) {
+    const int32_t C = g.C;
+    for (int32_t i = lane; i < C; i += kWave) {
+        const int64_t at = l * C + i;
+#pragma unroll
+        for (int f = 0; f < 9; ++f) bv<int32_t>(b, y.k_kind + f * 4 * C)[i] = carry.row[f][at];
+        bv<uint8_t>(b, y.k_trained)[i] = carry.trained[at] ? 1 : 0;
+        const int32_t bi = e.birth[b.block + i];
+        int32_t r = 0;
+        for (int32_t j = 0; j < C; ++j) {
+            const int32_t bj = e.birth[b.block + j];
+            r += (bj != kAbsent && bj < bi) ? 1 : 0;
+        }
+        bv<int16_t>(b, y.u_rank)[i] = (int16_t)r;
+    }
+    b.next_order = carry.next_order[l];
+    // candidate lists in slot order: enemies (abstraction.enemies), resources
+    // and own stockpiles (rush.harvest_sites)
+    AS3 int16_t* le = bv<int16_t>(b, y.l_enemy);
+    AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
+    AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
+    int32_t ne = 0, nr_ = 0, ns = 0;
+    for (int32_t s0 = 0; s0 < g.E; s0 += kWave) {
+        const int32_t s = s0 + lane;
+        bool en = false, re = false, st = false;
+        if (s < g.E && e.birth[s] != kAbsent) {
+            const int32_t owner = e.owner[s], t = e.utype[s];
+            en = owner != kAbsent && owner != b.player;
+            re = type_flag(g, h, t, FL_RESOURCE);
+            st = type_flag(g, h, t, FL_STOCKPILE) && owner == b.player;
+        }
+        const uint64_t me = ballot(en), mr = ballot(re), ms = ballot(st);
+        if (en) le[ne + count_below(me)] = (int16_t)s;
+        if (re) lr[nr_ + count_below(mr)] = (int16_t)s;
+        if (st) ls[ns + count_below(ms)] = (int16_t)s;
+        ne += popc(me);
+        nr_ += popc(mr);
+        ns += popc(ms);
+    }
+    b.n_enemy = ne;
+    b.n_resource = nr_;
+    b.n_stock = ns;
+    wave_sync();
+    // nearest enemy of every unit
+    for (int32_t i = lane; i < C; i += kWave) {
+        int32_t es, eb;
+        closest(g, e, e.cell[b.block + i], le, ne, &es, &eb);
+        bv<int16_t>(b, y.u_es)[i] = (int16_t)es;
+        bv<int32_t>(b, y.u_eb)[i] = eb;
+    }
+    wave_sync();
+}
+
+// ---------------------------------------------------------------------------
+// Rush decisions (N/bots/rush.py)
+// ---------------------------------------------------------------------------
+// abstraction._building_site (N/bots/abstraction.py:247-283): the open cell
+// first in the ring walk around `desired`.
+NR_DEV int32_t building_site(const KGame& g, const Hdr& h, const Env& e, const Bot& b, const BotLayout& y,
+                             int32_t desired, int lane) {
+    const AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
+    const int32_t longest = g.W > g.H ? g.W : g.H;
+    const int32_t x0 = floor_mod(desired, g.W), y0 = floor_div(desired, g.W);
+    int32_t best = kLast, site = kAbsent;
+    for (int32_t c = lane; c < g.cells; c += kWave) {
+        const int32_t dx = cell_x(g, c) - x0, dy = cell_y(g, c) - y0;
+        const int32_t ax = abs(dx), ay = abs(dy);
+        const int32_t ring = ax > ay ? ax : ay;
+        if (ring == 0) continue;
+        const int32_t side = dy == -ring ? 0 : (dx == ring ? 1 : (dy == ring ? 2 : 3));
+        const int32_t along = ((side == 0 || side == 2) ? dx : dy) + ring;
+        const int32_t visit = (ring * 4 + side) * (2 * longest + 1) + along;
+        const bool open = h.terrain[c] == 0 && e.entity[c] == kAbsent && !bit_of(reserved, c);
+        if (open && visit < best) {
+            best = visit;
+            site = c;
+        }
+    }
+    const int32_t m = wave_min(best);
+    const uint64_t at = ballot(site != kAbsent && best == m);
+    return at == 0ull ? kAbsent : __builtin_amdgcn_readlane(site, (int32_t)__builtin_ctzll(at));
+}
+
+// The least-birth unit among `mask` lanes (mask bit k = unit i0 + k of
+// chunk), or -1; masks hold up to 8 chunks of 64 units.
+struct UnitMask {
+    uint64_t w[8];
+};
+
+NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const UnitMask& m, int lane) {
+    int32_t best = kLast, who = -1;
+    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
+        const int32_t i = i0 + lane;
+        if ((m.w[k] >> lane) & 1ull) {
+            const int32_t bi = e.birth[b.block + i];
+            if (bi < best) {
+                best = bi;
+                who = i;
+            }
+        }
+    }
+    const int32_t mn = wave_min(best);
+    const uint64_t at = ballot(who >= 0 && best == mn);
+    return at == 0ull ? -1 : __builtin_amdgcn_readlane(who, (int32_t)__builtin_ctzll(at));
+}
+
+NR_DEV bool in_mask(const UnitMask& m, int32_t i) { return (m.w[i >> 6] >> (i & 63)) & 1ull; }
+
+// abstraction.build_if_not_already_building (N/bots/abstraction.py:286-297)
+// for a one-unit builder (or none); marks the site in the reserved bitmap.
+NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
+                                  int32_t builder, int32_t unit_type, int lane) {
+    bool builds = false;
+    if (builder >= 0) {
+        const int32_t bb = e.birth[b.block + builder];
+        builds = !(is_entry(b, y, builder, bb, kAbBuild) && bv<int32_t>(b, y.k_utype)[builder] == unit_type);
+    }
+    builds = uni(builds ? 1 : 0) != 0;
+    if (builds) {
+        const int32_t site = building_site(g, h, e, b, y, e.cell[b.block + builder], lane);
+        if (lane == 0) {
+            const Unit u = unit_at(g, e, b, builder);
+            put_unit(g, b, u, builder, false, kAbBuild, kAbsent, kAbsent, kAbsent, kAbsent, site, unit_type, y);
+            if (site >= 0 && site < g.cells) set_bit(bv<uint32_t>(b, y.m_reserved), site);
+        }
+        wave_sync();
+    }
+    b.next_order = wadd(b.next_order, g.C + 1);
+}
+
+// rush.build_base (N/bots/rush.py:88-104): clears the reserved bitmap,
+// returns the builder or -1.
+NR_DEV int32_t build_base(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
+                          const UnitMask& workers, int lane) {
+    AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
+    for (int32_t w = lane; w < (g.cells + 31) / 32; w += kWave) reserved[w] = 0u;
+    bool any_base = false;
+    for (int32_t i0 = 0; i0 < g.C; i0 += kWave) {
+        const int32_t i = i0 + lane;
+        if (i < g.C) {
+            const Unit u = unit_at(g, e, b, i);
+            any_base |= u.present && u.type == kTypeBase;
+        }
+    }
+    any_base = ballot(any_base) != 0ull;
+    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    const bool builds = !any_base && res >= tabv(h, F_COST, kTypeBase);
+    const int32_t builder = builds ? first_of(g, e, b, workers, lane) : -1;
+    wave_sync();
+    build_unless_building(g, h, e, b, y, builder, kTypeBase, lane);
+    return builder;
+}
+
+// rush._harvest (N/bots/rush.py:156-181): returns the idle harvesters.
+NR_DEV UnitMask harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, const UnitMask& harvesters,
+                        int lane) {
+    UnitMask idle = {};
+    const AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
+    const AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
+    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
+        const int32_t i = i0 + lane;
+        bool chosen = false, lazy = false;
+        int32_t rs = kAbsent, rb = kAbsent, ss = kAbsent, sb = kAbsent;
+        Unit u = {};
+        if ((harvesters.w[k] >> lane) & 1ull) {
+            u = unit_at(g, e, b, i);
+            closest(g, e, u.cell, lr, b.n_resource, &rs, &rb);
+            closest(g, e, u.cell, ls, b.n_stock, &ss, &sb);
+            const bool carrying = u.carried > 0;
+            const bool harvesting = is_entry(b, y, i, u.birth, kAbHarvest);
+            const bool same_base = bv<int32_t>(b, y.k_base)[i] == ss && bv<int32_t>(b, y.k_bbirth)[i] == sb;
+            const bool same_target = bv<int32_t>(b, y.k_target)[i] == rs && bv<int32_t>(b, y.k_tbirth)[i] == rb;
+            const bool occupied = carrying ? ss != kAbsent : (ss != kAbsent && rs != kAbsent);
+            const bool unchanged = harvesting && same_base && (carrying || same_target);
+            chosen = occupied && !unchanged;
+            lazy = !occupied;
+            if (chosen)
+                put_unit(g, b, u, i, false, kAbHarvest, carrying ? kAbsent : rs, carrying ? kAbsent : rb, ss, sb,
+                         kAbsent, kAbsent, y);
+        }
+        idle.w[k] = ballot(lazy);
+    }
+    b.next_order = wadd(b.next_order, g.C + 1);
+    wave_sync();
+    return idle;
+}
+
+// rush._attack_nearest (N/bots/rush.py:61-70).
+NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, const UnitMask& attackers,
+                           const UnitMask* last, int lane) {
+    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
+        const int32_t i = i0 + lane;
+        if ((attackers.w[k] >> lane) & 1ull) {
+            const int32_t es = bv<int16_t>(b, y.u_es)[i];
+            if (es != kAbsent) {
+                const Unit u = unit_at(g, e, b, i);
+                const bool lst = last && ((last->w[k] >> lane) & 1ull);
+                put_unit(g, b, u, i, lst, kAbAttack, es, bv<int32_t>(b, y.u_eb)[i], kAbsent, kAbsent, kAbsent,
+                         kAbsent, y);
+            }
+        }
+    }
+    b.next_order = wadd(b.next_order, g.C + 1);
+    wave_sync();
+}
+
+// A put of TRAIN for the units `pick` selects.
+template <typename Pick>
+NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y, int32_t unit_type, Pick pick,
+                        int lane) {
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const Unit u = unit_at(g, e, b, i);
+        if (pick(u)) put_unit(g, b, u, i, false, kAbTrain, kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, unit_type, y);
+    }
+    b.next_order = wadd(b.next_order, g.C + 1);
+    wave_sync();
+}
+
+// rush._melee_units_attack with available_melee (N/bots/rush.py:73-85).
+NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
+    UnitMask m = {};
+    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
+        const int32_t i = i0 + lane;
+        bool melee = false;
+        if (i < g.C) {
+            const Unit u = unit_at(g, e, b, i);
+            melee = u.present && type_flag(g, h, u.type, FL_ATTACK) && !type_flag(g, h, u.type, FL_HARVEST) &&
+                    u.available;
+        }
+        m.w[k] = ballot(melee);
+    }
+    attack_nearest(g, e, b, y, m, nullptr, lane);
+}
+
+NR_DEV UnitMask workers_of(const KGame& g, const Hdr& h, const Env& e, const Bot& b, int lane) {
+    UnitMask m = {};
+    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
+        const int32_t i = i0 + lane;
+        bool w = false;
+        if (i < g.C) {
+            const Unit u = unit_at(g, e, b, i);
+            w = u.present && type_flag(g, h, u.type, FL_HARVEST);
+        }
+        m.w[k] = ballot(w);
+    }
+    return m;
+}
+
+NR_DEV UnitMask without(UnitMask m, int32_t i) {
+    if (i >= 0) m.w[i >> 6] &= ~(1ull << (i & 63));
+    return m;
+}
+
+// rush.worker_rush (N/bots/rush.py:213-220) with _rushing_workers (:204-210).
+NR_DEV void worker_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
+    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    const int32_t worker_cost = tabv(h, F_COST, kTypeWorker);
+    train_where(g, e, b, y, kTypeWorker,
+                [&](const Unit& u) { return u.present && u.type == kTypeBase && u.available && res >= worker_cost; },
+                lane);
+    melee_attack(g, h, e, b, y, lane);
+    const UnitMask workers = workers_of(g, h, e, b, lane);
+    const int32_t builder = build_base(g, h, e, b, y, workers, lane);
+    const int32_t harvester = first_of(g, e, b, without(workers, builder), lane);
+    UnitMask one = {};
+    if (harvester >= 0) one.w[harvester >> 6] = 1ull << (harvester & 63);
+    const UnitMask idle = harvest(g, e, b, y, one, lane);
+    UnitMask free = without(without(workers, builder), harvester);
+    for (int k = 0; k < 8; ++k) free.w[k] |= idle.w[k];
+    attack_nearest(g, e, b, y, free, &idle, lane);
+}
+
+// rush.barracks_rush (N/bots/rush.py:229-236) with train_at_base_and_barracks
+// (:107-133), build_base_and_barracks (:184-201) and _workers_behavior
+// (:223-226).
+NR_DEV void barracks_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
+                          int32_t trained_type, int lane) {
+    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    int32_t held = 0;
+    bool any_barracks = false;
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const Unit u = unit_at(g, e, b, i);
+        held += (u.present && u.type == kTypeWorker) ? 1 : 0;
+        any_barracks |= u.present && u.type == kTypeBarracks;
+    }
+    held = wave_sum(held);
+    any_barracks = ballot(any_barracks) != 0ull;
+    const int32_t worker_cost = tabv(h, F_COST, kTypeWorker);
+    train_where(g, e, b, y, kTypeWorker,
+                [&](const Unit& u) {
+                    return u.present && u.type == kTypeBase && u.available && held < 1 && res >= worker_cost;
+                },
+                lane);
+    const int32_t trained_cost = tabv(h, F_COST, clampi(trained_type, 0, g.T - 1));
+    train_where(g, e, b, y, trained_type,
+                [&](const Unit& u) { return u.present && u.type == kTypeBarracks && u.available && res >= trained_cost; },
+                lane);
+    melee_attack(g, h, e, b, y, lane);
+    const UnitMask workers = workers_of(g, h, e, b, lane);
+    const int32_t base_builder = build_base(g, h, e, b, y, workers, lane);
+    const int32_t used = base_builder >= 0 ? tabv(h, F_COST, kTypeBase) : 0;
+    const bool builds_barracks = !any_barracks && res >= wadd(tabv(h, F_COST, kTypeBarracks), used);
+    const UnitMask rest = without(workers, base_builder);
+    const int32_t barracks_builder = builds_barracks ? first_of(g, e, b, rest, lane) : -1;
+    build_unless_building(g, h, e, b, y, barracks_builder, kTypeBarracks, lane);
+    const UnitMask idle = harvest(g, e, b, y, without(rest, barracks_builder), lane);
+    attack_nearest(g, e, b, y, idle, nullptr, lane);
+}
+
+// ---------------------------------------------------------------------------
+// pathfinding.search (N/bots/pathfinding.py:170-245) on lane 0.
+// Open cells pop by least f = g + Manhattan(cell, target), the most recently
+// inserted first among equal f; neighbours are inserted up, right, down,
+// left; each cell once.  f grows by 0 or 2 per step, so stacks indexed by
+// (f - f_start) / 2 hold the open list.  Returns the first step's direction,
+// or -1 when no cell within `range` of the target is reachable or the start
+// is already within it.  seen[c] = 0 open, 1 blocked, 2 inserted; top[] = -1.
+// ---------------------------------------------------------------------------
+NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* top, AS3 int16_t* below, AS3 int16_t* parent,
+                                AS3 uint8_t* seen, int32_t start, int32_t target, int32_t range) {
+    const int32_t W = g.W, H = g.H;
+    const int32_t tx = floor_mod(target, W), ty = floor_div(target, W);
+    const int32_t r2 = (int32_t)((uint32_t)range * (uint32_t)range);
+    seen[start] = 2;
+    parent[start] = (int16_t)start;
+    below[start] = -1;
+    top[0] = (int16_t)start;
+    int32_t lowest = 0, open = 1;
+    while (open > 0) {
+        while (top[lowest] == -1) ++lowest;
+        const int32_t pos = top[lowest];
+        top[lowest] = below[pos];
+        --open;
+        const int32_t py = cell_y(g, pos), px = pos - py * W;
+        const int32_t dx = px - tx, dy = py - ty;
+        if (dx * dx + dy * dy <= r2) {
+            int32_t at = pos, above = parent[pos], last = pos;
+            while (above != at) {
+                last = at;
+                at = above;
+                above = parent[at];
+            }
+            if (last == at + W) return 2;
+            if (last == at - 1) return 3;
+            if (last == at - W) return 0;
+            if (last == at + 1) return 1;
+            return kAbsent;
+        }
+        const int32_t hcur = abs(dx) + abs(dy);
+#pragma unroll
+        for (int32_t d = 0; d < 4; ++d) {
+            const int32_t nx = px + dir_dx(d), ny = py + dir_dy(d);
+            if (nx < 0 || nx >= W || ny < 0 || ny >= H) continue;
+            const int32_t nb = ny * W + nx;
+            if (seen[nb] != 0) continue;
+            const int32_t stack = lowest + (1 + abs(nx - tx) + abs(ny - ty) - hcur) / 2;
+            seen[nb] = 2;
+            parent[nb] = (int16_t)pos;
+            below[nb] = top[stack];
+            top[stack] = (int16_t)nb;
+            ++open;
+        }
+    }
+    return kAbsent;
+}
+
+// ---------------------------------------------------------------------------
+// abstraction.translate with the rush kinds and filler duration 10
+// (N/bots/abstraction.py:300-319 and the helpers cited below).
+// ---------------------------------------------------------------------------
+NR_DEV int32_t sq_distance(const KGame& g, int32_t a, int32_t c) {
+    const int32_t dx = floor_mod(a, g.W) - floor_mod(c, g.W), dy = floor_div(a, g.W) - floor_div(c, g.W);
+    return wadd(wmul(dx, dx), wmul(dy, dy));
+}
+
+NR_DEV int32_t step_cell(const KGame& g, int32_t cell, int32_t direction) {
+    const int32_t d = clampi(direction, 0, 3);
+    return wadd(cell, dir_dy(d) * g.W + dir_dx(d));
+}
+
+// _adjacent_direction (N/bots/abstraction.py:399-407)
+NR_DEV int32_t adjacent_direction(const KGame& g, int32_t origin, int32_t goal) {
+    if (goal == kAbsent) return kAbsent;
+    const int32_t dx = floor_mod(goal, g.W) - floor_mod(origin, g.W), dy = floor_div(goal, g.W) - floor_div(origin, g.W);
+    for (int32_t d = 0; d < 4; ++d)
+        if (dx == dir_dx(d) && dy == dir_dy(d)) return d;
+    return kAbsent;
+}
+
+struct Desire {
+    int32_t kind, dir, target, ptype, claimed, cost;
+};
+
+NR_DEV Desire no_desire() { return Desire{kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, 0}; }
+
+NR_DEV bool within_balance(const Env& e, const Bot& b, int32_t p) {
+    const int32_t r = p == 0 ? b.reserved0 : b.reserved1;
+    return r == 0 || r <= e.sc[S_RES0 + p];
+}
+
+// _production with _produce_allowed (N/bots/abstraction.py:440-462, 368-380)
+NR_DEV Desire production(const KGame& g, const Hdr& h, const Env& e, const Bot& b, const BotLayout& y,
+                         int32_t direction, int32_t ptype, int32_t cell) {
+    const int32_t own = b.player;
+    const int32_t claimed = direction != kAbsent ? step_cell(g, cell, direction) : kAbsent;
+    const int32_t cost = tabv(h, F_COST, clampi(ptype, 0, g.T - 1));
+    const int32_t reserved = own == 0 ? b.reserved0 : b.reserved1;
+    const bool allowed = direction != kAbsent && !bit_of(bv<uint32_t>(b, y.m_claimed), clampi(claimed, 0, g.cells - 1)) &&
+                         (reserved == 0 || wadd(cost, reserved) <= e.sc[S_RES0 + own]) && within_balance(e, b, 1 - own);
+    if (!allowed) return no_desire();
+    return Desire{kKindProduce, direction, kAbsent, ptype, claimed, cost};
+}
+
+// _training_direction (N/bots/abstraction.py:465-489)
+NR_DEV int32_t training_direction(const KGame& g, const Hdr& h, const Env& e, const Bot& b, const BotLayout& y,
+                                  int32_t cell, int32_t produced) {
+    const bool harvests = type_flag(g, h, produced, FL_HARVEST);
+    const AS3 int16_t* near = harvests ? bv<int16_t>(b, y.l_resource) : bv<int16_t>(b, y.l_enemy);
+    const int32_t n = harvests ? b.n_resource : b.n_enemy;
+    const AS3 uint32_t* freem = bv<uint32_t>(b, y.m_free);
+    const int32_t cx = floor_mod(cell, g.W), cy = floor_div(cell, g.W);
+    int32_t best = kAbsent, best_score = 0;
+    for (int32_t d = 0; d < 4; ++d) {
+        const int32_t x = cx + dir_dx(d), yy = cy + dir_dy(d);
+        if (x < 0 || x >= g.W || yy < 0 || yy >= g.H || !bit_of(freem, yy * g.W + x)) continue;
+        int32_t nearest = kLast;
+        for (int32_t k = 0; k < n; ++k) {
+            const int32_t c = e.cell[near[k]];
+            const int32_t dist = abs(x - cell_x(g, c)) + abs(yy - cell_y(g, c));
+            nearest = dist < nearest ? dist : nearest;
+        }
+        const int32_t score = n > 0 ? -nearest : 0;
+        if (best == kAbsent || score > best_score) {
+            best = d;
+            best_score = score;
+        }
+    }
+    return best;
+}
+
+NR_DEV bool exists_slot(const KGame& g, const Env& e, int32_t slot, int32_t birth) {
+    return slot != kAbsent && e.birth[clampi(slot, 0, g.E - 1)] == birth;
+}
+
+NR_DEV int32_t cell_of_slot(const KGame& g, const Env& e, int32_t slot) {
+    return slot != kAbsent ? (int32_t)e.cell[clampi(slot, 0, g.E - 1)] : kAbsent;
+}
+
+// Usage, standing, plan and queue; returns the number of queued units.
+NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
+    const int32_t C = g.C, words = (g.cells + 31) / 32;
+    AS3 uint32_t* claimed = bv<uint32_t>(b, y.m_claimed);
+    AS3 uint32_t* freem = bv<uint32_t>(b, y.m_free);
+    for (int32_t w = lane; w < words; w += kWave) {
+        claimed[w] = 0u;
+        freem[w] = 0u;
+        bv<uint32_t>(b, y.m_used)[w] = 0u;
+        bv<uint32_t>(b, y.m_kept)[w] = 0u;
+    }
+    wave_sync();
+    // _pending_usage (N/bots/abstraction.py:331-359)
+    int32_t cost0 = 0, cost1 = 0;
+    for (int32_t s = lane; s < g.E; s += kWave) {
+        if (e.birth[s] == kAbsent) continue;
+        const int32_t kind = e.pkind[s];
+        if (kind == kKindMove || kind == kKindProduce) {
+            int32_t t = step_cell(g, e.cell[s], e.pdir[s]);
+            if (t < 0) t += g.cells;
+            if (t >= 0 && t < g.cells) set_bit(claimed, t);
+        }
+        if (kind == kKindProduce && s >= g.N) {
+            const int32_t c = tabv(h, F_COST, clampi(e.pptype[s], 0, g.T - 1));
+            if ((s - g.N) / C == 0) cost0 = wadd(cost0, c);
+            else cost1 = wadd(cost1, c);
+        }
+    }
+    b.reserved0 = wave_sum(cost0);
+    b.reserved1 = wave_sum(cost1);
+    wave_sync();
+    // _free_cells (:362-365)
+    for (int32_t c = lane; c < g.cells; c += kWave)
+        if (h.terrain[c] == 0 && e.entity[c] == kAbsent && !bit_of(claimed, c)) set_bit(freem, c);
+    wave_sync();
+    // _standing (:383-423) and _plan (:653-715) with _fallback (:575-650)
+    for (int32_t i = lane; i < C; i += kWave) {
+        const Unit u = unit_at(g, e, b, i);
+        const int32_t kind = bv<int32_t>(b, y.k_kind)[i];
+        const bool alive = kind != kAbNone && bv<int32_t>(b, y.k_ubirth)[i] == u.birth;
+        const bool carrying = u.carried > 0;
+        const int32_t kcell = bv<int32_t>(b, y.k_cell)[i];
+        const int32_t target = bv<int32_t>(b, y.k_target)[i];
+        const int32_t base = bv<int32_t>(b, y.k_base)[i];
+        const bool built_on = kcell != kAbsent && e.entity[clampi(kcell, 0, g.cells - 1)] != kAbsent;
+        const bool target_gone = !exists_slot(g, e, target, bv<int32_t>(b, y.k_tbirth)[i]);
+        bool completed = false;
+        if (kind == kAbAttack) completed = target_gone;
+        else if (kind == kAbHarvest) completed = carrying ? !exists_slot(g, e, base, bv<int32_t>(b, y.k_bbirth)[i]) : target_gone;
+        else if (kind == kAbTrain) completed = bv<uint8_t>(b, y.k_trained)[i] != 0;
+        else if (kind == kAbBuild) completed = built_on;
+        const bool standing = alive && !completed;
+        const bool executes = standing && u.available;
+        bv<uint8_t>(b, y.u_flags)[i] = (uint8_t)((standing ? U_STANDING : 0) | (executes ? U_EXECUTES : 0));
+        if (!executes) continue;
+        const int32_t target_cell = cell_of_slot(g, e, target);
+        const int32_t range = tabv(h, F_RANGE, u.type);
+        const bool in_range = sq_distance(g, u.cell, target_cell) <= wmul(range, range);
+        const int32_t harvest_goal = carrying ? cell_of_slot(g, e, base) : target_cell;
+        int32_t goal = kAbsent, radius = 0;
+        Desire fb = no_desire();
+        const int32_t utype = bv<int32_t>(b, y.k_utype)[i];
+        if (kind == kAbAttack) {
+            goal = target_cell;
+            radius = range;
+            if (in_range && target_cell != kAbsent) fb = Desire{kKindAttack, kAbsent, target_cell, kAbsent, kAbsent, 0};
+        } else if (kind == kAbHarvest) {
+            goal = harvest_goal;
+            radius = 1;
+            const int32_t d = adjacent_direction(g, u.cell, harvest_goal);
+            if (d != kAbsent) fb = Desire{carrying ? kKindReturn : kKindHarvest, d, kAbsent, kAbsent, kAbsent, 0};
+        } else if (kind == kAbTrain) {
+            fb = production(g, h, e, b, y, training_direction(g, h, e, b, y, u.cell, utype), utype, u.cell);
+        } else if (kind == kAbBuild) {
+            goal = kcell;
+            radius = 1;
+            fb = production(g, h, e, b, y, adjacent_direction(g, u.cell, kcell), utype, u.cell);
+        }
+        const bool searches = goal != kAbsent && !(kind == kAbAttack && in_range);
+        bv<int32_t>(b, y.u_goal)[i] = searches ? goal : u.cell;
+        bv<int32_t>(b, y.u_radius)[i] = searches ? radius : 0;
+        bv<int32_t>(b, y.u_fkind)[i] = fb.kind;
+        bv<int32_t>(b, y.u_fdir)[i] = fb.dir;
+        bv<int32_t>(b, y.u_ftarget)[i] = fb.target;
+        bv<int32_t>(b, y.u_fptype)[i] = fb.ptype;
+        bv<int32_t>(b, y.u_fclaimed)[i] = fb.claimed;
+        bv<int32_t>(b, y.u_fcost)[i] = fb.cost;
+    }
+    wave_sync();
+    // _queue (:800-801): executing units by order, ties by unit index
+    int32_t queued = 0;
+    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+        const int32_t i = i0 + lane;
+        const bool ex = i < C && (bv<uint8_t>(b, y.u_flags)[i] & U_EXECUTES);
+        if (ex) {
+            const int32_t oi = bv<int32_t>(b, y.k_order)[i];
+            int32_t r = 0;
+            for (int32_t j = 0; j < C; ++j) {
+                if (!(bv<uint8_t>(b, y.u_flags)[j] & U_EXECUTES)) continue;
+                const int32_t oj = bv<int32_t>(b, y.k_order)[j];
+                r += (oj < oi || (oj == oi && j < i)) ? 1 : 0;
+            }
+            bv<int16_t>(b, y.u_queue)[r] = (int16_t)i;
+        }
+        queued += popc(ballot(ex));
+    }
+    for (int32_t i = lane; i < C; i += kWave) {
+        bv<uint8_t>(b, y.u_sel)[i] = SEL_NONE;
+        bv<int16_t>(b, y.u_drank)[i] = (int16_t)kAbsent;
+    }
+    wave_sync();
+    return queued;
+}
+
+// _walked / _walk_step with _answer and _kept (N/bots/abstraction.py:718-797,
+// 904-952): returns kept_count.
+NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int32_t queued,
+                              int lane) {
+    (void)h;
+    AS3 uint32_t* claimed = bv<uint32_t>(b, y.m_claimed);
+    AS3 uint32_t* freem = bv<uint32_t>(b, y.m_free);
+    AS3 uint32_t* used = bv<uint32_t>(b, y.m_used);
+    AS3 uint32_t* kept_m = bv<uint32_t>(b, y.m_kept);
+    AS3 int16_t* top = bv<int16_t>(b, y.a_top);
+    AS3 int16_t* below = bv<int16_t>(b, y.a_below);
+    AS3 int16_t* parent = bv<int16_t>(b, y.a_parent);
+    AS3 uint8_t* seen = bv<uint8_t>(b, y.a_seen);
+    const int32_t own = b.player;
+    const bool moves_allowed = within_balance(e, b, 0) && within_balance(e, b, 1);
+    const int32_t reserved_own = own == 0 ? b.reserved0 : b.reserved1;
+    const int32_t balance = uni(e.sc[S_RES0 + own]);
+    int32_t kept_cost = 0, kept_count = 0;
+    for (int32_t q = 0; q < queued; ++q) {
+        const int32_t i = uni(bv<int16_t>(b, y.u_queue)[q]);
+        const int32_t start = uni(e.cell[b.block + i]);
+        const int32_t goal = uni(bv<int32_t>(b, y.u_goal)[i]);
+        const int32_t radius = uni(bv<int32_t>(b, y.u_radius)[i]);
+        int32_t step = kAbsent;
+        // the first pop is the start: already within range means no step
+        if (start >= 0 && start < g.cells && sq_distance(g, start, goal) > wmul(radius, radius)) {
+            for (int32_t c = lane; c < g.cells; c += kWave) {
+                top[c] = -1;
+                seen[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
+            }
+            wave_sync();
+            int32_t s = kAbsent;
+            if (lane == 0) s = astar_first_step(g, top, below, parent, seen, start, goal, radius);
+            step = __builtin_amdgcn_readfirstlane(s);
+            wave_sync();
+        }
+        int32_t sel, kind, claim, cost;
+        if (step != kAbsent) {
+            sel = moves_allowed ? SEL_MOVED : SEL_NONE;
+            kind = moves_allowed ? kKindMove : kAbsent;
+            claim = moves_allowed ? step_cell(g, start, step) : kAbsent;
+            cost = 0;
+        } else {
+            sel = SEL_FALLBACK;
+            kind = uni(bv<int32_t>(b, y.u_fkind)[i]);
+            claim = uni(bv<int32_t>(b, y.u_fclaimed)[i]);
+            cost = uni(bv<int32_t>(b, y.u_fcost)[i]);
+        }
+        const bool has_cell = claim != kAbsent && claim >= 0 && claim < g.cells;
+        const bool conflicting = has_cell && (bit_of(claimed, claim) || bit_of(kept_m, claim));
+        const bool overdrawn = cost > 0 && wadd(wadd(reserved_own, kept_cost), cost) > balance;
+        const bool kept = kind != kAbsent && !conflicting && !overdrawn;
+        if (lane == 0) {
+            if (has_cell) {
+                used[claim >> 5] |= 1u << (claim & 31);
+                if (kept) kept_m[claim >> 5] |= 1u << (claim & 31);
+            }
+            if (kept) {
+                bv<uint8_t>(b, y.u_sel)[i] = (uint8_t)sel;
+                bv<int8_t>(b, y.u_dir)[i] = (int8_t)step;
+                bv<int16_t>(b, y.u_drank)[i] = (int16_t)kept_count;
+            }
+        }
+        if (kept) {
+            kept_cost = wadd(kept_cost, cost);
+            ++kept_count;
+        }
+        wave_sync();
+    }
+    return kept_count;
+}
+
+// The decided command of unit i (_commands, N/bots/abstraction.py:1063-1096):
+// {kind, direction, none_duration, target_cell, produced_type, request_order}.
+NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLayout& y, int32_t i, int32_t kept_count,
+                         int32_t out[6]) {
+    const Unit u = unit_at(g, e, b, i);
+    const int32_t sel = bv<uint8_t>(b, y.u_sel)[i];
+    int32_t kind = kAbsent, dir = kAbsent, target = kAbsent, ptype = kAbsent;
+    if (sel == SEL_MOVED) {
+        kind = kKindMove;
+        dir = bv<int8_t>(b, y.u_dir)[i];
+    } else if (sel == SEL_FALLBACK) {
+        kind = bv<int32_t>(b, y.u_fkind)[i];
+        dir = bv<int32_t>(b, y.u_fdir)[i];
+        target = bv<int32_t>(b, y.u_ftarget)[i];
+        ptype = bv<int32_t>(b, y.u_fptype)[i];
+    }
+    const bool kept = sel != SEL_NONE;
+    const bool filler = u.available && !kept;
+    int32_t filler_rank = 0;
+    if (filler) {
+        for (int32_t j = 0; j < g.C; ++j) {
+            const Unit v = unit_at(g, e, b, j);
+            filler_rank += (v.available && bv<uint8_t>(b, y.u_sel)[j] == SEL_NONE && v.birth < u.birth) ? 1 : 0;
+        }
+    }
+    out[0] = kept ? kind : (filler ? kKindNone : kAbsent);
+    out[1] = kept ? dir : kAbsent;
+    out[2] = filler ? kFillerDuration : 0;  // no rush desire waits
+    out[3] = kept ? target : kAbsent;
+    out[4] = kept ? ptype : kAbsent;
+    out[5] = kept ? (int32_t)bv<int16_t>(b, y.u_drank)[i] : (filler ? wadd(kept_count, filler_rank) : kAbsent);
+}
+
+// _settled (N/bots/abstraction.py:1099-1119) into the carry rows of env l.
+NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry,
+                         bool reset, int lane) {
+    const int32_t C = g.C;
+    int32_t standing = 0;
+    for (int32_t i = lane; i < C; i += kWave) {
+        const int64_t at = l * C + i;
+        const int32_t fl = bv<uint8_t>(b, y.u_flags)[i];
+        const bool st = !reset && (fl & U_STANDING);
+        standing += st ? 1 : 0;
+        if (!st) {
+#pragma unroll
+            for (int f = 0; f < 9; ++f) carry.row[f][at] = kAbsent;
+            carry.trained[at] = 0;
+            continue;
+        }
+        const int32_t oi = bv<int32_t>(b, y.k_order)[i];
+        int32_t r = 0;
+        for (int32_t j = 0; j < C; ++j)
+            r += ((bv<uint8_t>(b, y.u_flags)[j] & U_STANDING) && bv<int32_t>(b, y.k_order)[j] < oi) ? 1 : 0;
+        const int32_t kind = bv<int32_t>(b, y.k_kind)[i];
+#pragma unroll
+        for (int f = 0; f < 9; ++f) carry.row[f][at] = bv<int32_t>(b, y.k_kind + f * 4 * C)[i];
+        carry.row[2][at] = r;
+        const bool trained = bv<uint8_t>(b, y.k_trained)[i] != 0 ||
+                             ((fl & U_EXECUTES) && (kind == kAbTrain || kind == kAbTrainDirection));
+        carry.trained[at] = trained ? 1 : 0;
+    }
+    standing = wave_sum(standing);
+    if (lane == 0) carry.next_order[l] = standing;
+}
+
+// family.act (N/bots/family.py:34-41): the rush decisions on the carry, then
+// translate's plan and walk.  Returns kept_count; commands come from
+// unit_command and the carry from settle_carry.
+NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
+                       const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane) {
+    bot_begin(g, h, e, b, y, l, carry, lane);
+    if (strategy == kWorkerRush) worker_rush(g, h, e, b, y, lane);
+    else barracks_rush(g, h, e, b, y, trained_type, lane);
+    const int32_t queued = translate_plan(g, h, e, b, y, lane);
+    return translate_walk(g, h, e, b, y, queued, lane);
+}
+
+}  // namespace nr

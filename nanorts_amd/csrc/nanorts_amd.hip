@@ -12,6 +12,7 @@
 #include "../../include/nanorts_amd.h"
 #include "engine.h"
 #include "rollout.h"
+#include "bots.h"
 
 using namespace nr;
 
@@ -71,6 +72,28 @@ bool valid_game(const nanorts_game* game, std::string* why) {
         *why = "terrain is NULL";
         return false;
     }
+    return true;
+}
+
+// Waves per workgroup that fit the device's LDS per workgroup (at most 4).
+bool fit_waves(Shape* out, std::string* why) {
+    const Layout& y = out->g.lay;
+    int max_lds = 65536;
+    int device = 0;
+    if (hipGetDevice(&device) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+            max_lds = v;
+    }
+    int wpb = 4;
+    while (wpb > 1 && y.hdr_bytes + wpb * y.env_bytes > max_lds) --wpb;
+    if (y.hdr_bytes + wpb * y.env_bytes > max_lds) {
+        *why = "one game's LDS block (" + std::to_string(y.hdr_bytes + y.env_bytes) + " bytes) exceeds the " +
+               std::to_string(max_lds) + " bytes a workgroup may allocate";
+        return false;
+    }
+    out->wpb = wpb;
+    out->lds = y.hdr_bytes + wpb * y.env_bytes;
     return true;
 }
 
@@ -248,23 +271,69 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
         g.seg[k].bytes = rows[k].bytes;
     }
 
-    int max_lds = 65536;
-    int device = 0;
-    if (hipGetDevice(&device) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
-            max_lds = v;
-    }
-    int wpb = 4;
-    while (wpb > 1 && y.hdr_bytes + wpb * y.env_bytes > max_lds) --wpb;
-    if (y.hdr_bytes + wpb * y.env_bytes > max_lds) {
-        *why = "one game's LDS block (" + std::to_string(y.hdr_bytes + y.env_bytes) + " bytes) exceeds the " +
-               std::to_string(max_lds) + " bytes a workgroup may allocate";
+    return fit_waves(out, why);
+}
+
+// Bot region after each env block (scripted bots, bots.h): the per-wave
+// stride grows by the region, the env offsets stay.
+bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::string* why) {
+    if (!shape_for(game, out, why)) return false;
+    KGame& g = out->g;
+    if (g.C > 512) {
+        *why = "the scripted bots take at most 512 slots per player";
         return false;
     }
-    out->wpb = wpb;
-    out->lds = y.hdr_bytes + wpb * y.env_bytes;
-    return true;
+    const int32_t C = g.C, E = g.E, cells = g.cells, words = (cells + 31) / 32;
+    std::memset(by, 0, sizeof(*by));
+    int32_t o = 0;
+    auto take = [&o](int32_t bytes) {
+        const int32_t at = o;
+        o += align16(bytes);
+        return at;
+    };
+    // the nine int32 carry rows back to back, in AbstractActions order
+    by->k_kind = take(9 * 4 * C);
+    by->k_ubirth = by->k_kind + 4 * C;
+    by->k_order = by->k_kind + 8 * C;
+    by->k_target = by->k_kind + 12 * C;
+    by->k_tbirth = by->k_kind + 16 * C;
+    by->k_base = by->k_kind + 20 * C;
+    by->k_bbirth = by->k_kind + 24 * C;
+    by->k_cell = by->k_kind + 28 * C;
+    by->k_utype = by->k_kind + 32 * C;
+    by->k_trained = take(C);
+    by->u_flags = take(C);
+    by->u_rank = take(2 * C);
+    by->u_es = take(2 * C);
+    by->u_eb = take(4 * C);
+    by->u_goal = take(4 * C);
+    by->u_radius = take(4 * C);
+    by->u_fkind = take(4 * C);
+    by->u_fdir = take(4 * C);
+    by->u_ftarget = take(4 * C);
+    by->u_fptype = take(4 * C);
+    by->u_fclaimed = take(4 * C);
+    by->u_fcost = take(4 * C);
+    by->u_sel = take(C);
+    by->u_dir = take(C);
+    by->u_drank = take(2 * C);
+    by->u_queue = take(2 * C);
+    by->l_enemy = take(2 * E);
+    by->l_resource = take(2 * E);
+    by->l_stock = take(2 * E);
+    by->a_top = take(2 * cells);
+    by->a_below = take(2 * cells);
+    by->a_parent = take(2 * cells);
+    by->a_seen = take(cells);
+    by->m_claimed = take(4 * words);
+    by->m_free = take(4 * words);
+    by->m_used = take(4 * words);
+    by->m_kept = take(4 * words);
+    by->m_reserved = take(4 * words);
+    by->bytes = align16(o);
+    by->origin = g.lay.env_bytes;
+    g.lay.env_bytes += by->bytes;
+    return fit_waves(out, why);
 }
 
 template <typename Kernel, typename... Args>
@@ -569,6 +638,82 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
     } else if (r.feature_maps || r.scalars) {
         observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
     }
+}
+
+// Scripted-bot arguments: the bot region layout, the carry and the strategy.
+struct BotArgs {
+    BotLayout y;
+    BotCarry carry;
+    int32_t strategy, trained;
+};
+
+// family.act for the rush strategies (N/bots/family.py:34-41): commands
+// int32[L][6][2][C] and the carry updated in place.
+__global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes, nanorts_state s, BotArgs a,
+                                                         const int32_t* player, int64_t player_lanes,
+                                                         int32_t* commands) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    Bot b;
+    b.base = e.base + a.y.origin;
+    b.player = clampi(player[player_lanes == 1 ? 0 : l], 0, 1);
+    b.block = g.N + b.player * g.C;
+    const int32_t kept = bot_act(g, hdr, e, b, a.y, l, a.carry, a.strategy, a.trained, lane);
+    const int32_t owned = 2 * g.C;
+    int32_t* out = commands + l * 6 * owned;
+    for (int32_t p = lane; p < owned; p += kWave) {
+        int32_t v[6] = {kAbsent, kAbsent, 0, kAbsent, kAbsent, kAbsent};
+        if (p / g.C == b.player) unit_command(g, e, b, a.y, p - b.player * g.C, kept, v);
+#pragma unroll
+        for (int f = 0; f < 6; ++f) out[f * owned + p] = v[f];
+    }
+    settle_carry(g, b, a.y, l, a.carry, false, lane);
+}
+
+// seat.step_seat with a static learner seat (N/bots/seat.py:94-152): the
+// bot's commands from the current state, the learner's rows decoded
+// (N/adapters/jaxmarl/env.py:78-96), core.step under the episode root,
+// auto-reset, the carry emptied where done, observations.
+__global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanorts_state s, BotArgs a, int32_t learner,
+                                                   const int32_t* actions, int32_t partial, nanorts_env_results r) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
+    uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
+    fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
+    Bot b;
+    b.base = e.base + a.y.origin;
+    b.player = 1 - learner;
+    b.block = g.N + b.player * g.C;
+    const int32_t kept = bot_act(g, hdr, e, b, a.y, l, a.carry, a.strategy, a.trained, lane);
+    const Layout& y = g.lay;
+    const int32_t top = (1 << g.rank_bits) - 1;
+    for (int32_t p = lane; p < 2 * g.C; p += kWave) {
+        const int32_t slot = g.N + p;
+        if (p / g.C == b.player) {
+            int32_t v[6];
+            unit_command(g, e, b, a.y, p - b.player * g.C, kept, v);
+            at<int8_t>(e, y.c_kind)[p] = (int8_t)canon_kind(v[0]);
+            at<int8_t>(e, y.c_dir)[p] = (int8_t)canon_dir(v[1]);
+            at<int32_t>(e, y.c_none)[p] = v[2];
+            at<int16_t>(e, y.c_target)[p] = (int16_t)canon_target(v[3], g.cells);
+            at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(v[4], g.T);
+            at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(v[5] == kAbsent ? 0 : v[5], 0, top);
+        } else {
+            const int32_t* row = actions + (l * g.C + (p - learner * g.C)) * 7;
+            int32_t act[7];
+#pragma unroll
+            for (int f = 0; f < 7; ++f) act[f] = row[f];
+            const bool available = e.birth[slot] != kAbsent && e.pkind[slot] == kAbsent;
+            decode_row(g, e, p, available, act);
+        }
+    }
+    wave_sync();
+    core_step(g, hdr, e, lane, k0, k1, false);
+    const bool done = finish_step(g, hdr, e, l, lane, partial != 0, r, false);
+    settle_carry(g, b, a.y, l, a.carry, done, lane);
+    store_env(g, s, l, e, lane);
+    if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
 }
 
 __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const uint32_t* words, uint32_t key0, uint32_t key1, int32_t step,
@@ -975,7 +1120,7 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_rollout";
+           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step";
 }
 
 const char* nanorts_last_error(void) { return g_error.c_str(); }
@@ -1133,6 +1278,58 @@ int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state
         return fail(NANORTS_INVALID_ARGUMENT, "env.step needs environment_root and episode_index");
     if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
     return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results);
+}
+
+static bool bot_args(const nanorts_game* game, Shape* sh, BotArgs* a, int32_t strategy, int32_t trained_type,
+                     const nanorts_abstract_actions& carry, std::string* why) {
+    if (strategy != NANORTS_WORKER_RUSH && strategy != NANORTS_BARRACKS_RUSH) {
+        *why = "strategy must be NANORTS_WORKER_RUSH or NANORTS_BARRACKS_RUSH";
+        return false;
+    }
+    if (!carry.kind || !carry.unit_birth || !carry.order || !carry.target || !carry.target_birth || !carry.base ||
+        !carry.base_birth || !carry.cell || !carry.unit_type || !carry.trained || !carry.next_order) {
+        *why = "a carry (AbstractActions) pointer is NULL";
+        return false;
+    }
+    if (!shape_for_bots(game, sh, &a->y, why)) return false;
+    int32_t* rows[9] = {carry.kind, carry.unit_birth, carry.order, carry.target, carry.target_birth,
+                        carry.base, carry.base_birth, carry.cell, carry.unit_type};
+    for (int f = 0; f < 9; ++f) a->carry.row[f] = rows[f];
+    a->carry.trained = carry.trained;
+    a->carry.next_order = carry.next_order;
+    a->strategy = strategy;
+    a->trained = trained_type;
+    return true;
+}
+
+int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            int32_t strategy, int32_t trained_type, const int32_t* player, int64_t player_lanes,
+                            nanorts_abstract_actions carry, int32_t* commands) {
+    NR_STATE(state)
+    if (!player || (player_lanes != 1 && player_lanes != lanes))
+        return fail(NANORTS_INVALID_ARGUMENT, "player must be [1] or [lanes]");
+    if (!commands) return fail(NANORTS_INVALID_ARGUMENT, "commands is NULL");
+    Shape sh;
+    BotArgs a;
+    std::string why;
+    if (!bot_args(game, &sh, &a, strategy, trained_type, carry, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
+    return launch(k_abstraction_act, sh, lanes, (hipStream_t)stream, state, a, player, player_lanes, commands);
+}
+
+int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                      int32_t trained_type, int32_t learner, nanorts_abstract_actions carry, const int32_t* actions,
+                      int32_t partial, nanorts_env_results results) {
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "the seat step needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    Shape sh;
+    BotArgs a;
+    std::string why;
+    if (!bot_args(game, &sh, &a, strategy, trained_type, carry, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
+    return launch(k_seat_step, sh, lanes, (hipStream_t)stream, state, a, learner, actions, partial, results);
 }
 
 int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,

@@ -67,12 +67,20 @@ class RolloutResults(ctypes.Structure):
                 ("depth", ctypes.c_int32)]
 
 
+ABSTRACT_FIELDS = ("kind", "unit_birth", "order", "target", "target_birth", "base", "base_birth", "cell",
+                   "unit_type", "trained", "next_order")
+
+
+class AbstractActions(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in ABSTRACT_FIELDS]
+
+
 # Every extern "C" symbol include/nanorts_amd.h declares.
 EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
-    "nanorts_rollout",
+    "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step",
 )
 
 _I64 = ctypes.c_int64
@@ -97,6 +105,9 @@ _SIGNATURES = {
     "nanorts_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
     "nanorts_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
     "nanorts_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
+    "nanorts_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
+    "nanorts_seat_step": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32,
+                                         EnvResults]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None
