@@ -275,6 +275,19 @@ int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state stat
                       int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                       const int32_t* actions, int32_t partial, nanorts_env_results results);
 
+/* Fused learner-vs-bot rollout of `steps` cycles with the state resident in
+ * LDS: per cycle the learner's rows from the synthetic harness's integer
+ * uniform-over-legal sampler (its avail words, `sample_key`, step
+ * step0 + t), the bot's act and the seat step as nanorts_seat_step.
+ * Bit-equal to calling nanorts_avail_actions, nanorts_sample_actions and
+ * nanorts_seat_step once per cycle with the learner's rows.  results.actions
+ * (when set) records the learner's rows [steps][L][C][7]; rewards, dones and
+ * the observation ring are those of nanorts_rollout. */
+int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                         int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
+                         const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
+                         int64_t env0, nanorts_rollout_results results);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,7 @@ current HIP stream.
 """
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 from typing import Any, Final
 
@@ -162,6 +163,32 @@ class SeatEnv:
             infos["final_observation"] = {LEARNER: env._symbolic(fmaps, fscal)[SEAT_RULES[p]]}
         return ({LEARNER: obs}, nxt, {LEARNER: out["reward"][:, p]}, {LEARNER: out["done"], ALL_AGENTS: out["done"]},
                 infos)
+
+    def rollout(self, state: SeatState, steps: int, sample_key, *, step0: int = 0, env0: int = 0,
+                record: bool = True, record_actions: bool = False, observation_depth: int = 1) -> dict[str, Any]:
+        """Fused rollout of `steps` cycles in place: the learner's rows from the
+        synthetic harness's uniform-over-legal sampler, the bot's act and the
+        seat step, with the state resident in LDS.  Bit-equal to
+        get_avail_actions(form="words") -> sample_actions -> step per cycle."""
+        env = self.env
+        es = state.environment_state
+        L = es.num_envs
+        b = env.bucket
+        d = self.device
+        rewards = torch.empty((steps, L, 2), dtype=torch.float32, device=d) if record else None
+        dones = torch.empty((steps, L), dtype=torch.bool, device=d) if record else None
+        actions = torch.empty((steps, L, b.per_player_capacity, 7), dtype=torch.int32, device=d) \
+            if record_actions else None
+        depth = max(1, int(observation_depth))
+        maps = torch.empty((depth, L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
+        scalars = torch.empty((depth, L, 2, 4), dtype=torch.int32, device=d)
+        key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
+        results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth)
+        native.check(env.lib.nanorts_seat_rollout(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+                                                  self.bot.trained, self.learner, _carry_struct(state.carry), key,
+                                                  int(step0), int(steps), env.partial, int(env0), results),
+                     "nanorts_seat_rollout")
+        return {"rewards": rewards, "dones": dones, "actions": actions, "feature_maps": maps, "scalars": scalars}
 
     def get_avail_actions(self, state: SeatState, *, form: str = "rows") -> dict[str, torch.Tensor]:
         return {LEARNER: self.env.get_avail_actions(state.environment_state, form=form)[SEAT_RULES[self.learner]]}

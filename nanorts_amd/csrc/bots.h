@@ -37,13 +37,13 @@ struct BotLayout {
     // carry rows [C]
     int32_t k_kind, k_ubirth, k_order, k_target, k_tbirth, k_base, k_bbirth, k_cell, k_utype, k_trained;
     // per unit [C]
-    int32_t u_flags, u_rank, u_es, u_eb, u_goal, u_radius;
+    int32_t u_flags, u_role, u_rank, u_es, u_eb, u_goal, u_radius;
     int32_t u_fkind, u_fdir, u_ftarget, u_fptype, u_fclaimed, u_fcost;
     int32_t u_sel, u_dir, u_drank, u_queue;
     // candidate slot lists [E]
     int32_t l_enemy, l_resource, l_stock;
     // search scratch [cells]
-    int32_t a_top, a_below, a_parent, a_seen;
+    int32_t a_below, a_mark;
     // cell bitmaps [ceil(cells / 32)] words
     int32_t m_claimed, m_free, m_used, m_kept, m_reserved;
 };
@@ -176,7 +176,11 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
         }
         bv<int16_t>(b, y.u_rank)[i] = (int16_t)r;
     }
-    b.next_order = carry.next_order[l];
+    // a vector load on one lane: in a fused rollout this word was written by
+    // the previous cycle's vector store, which the scalar cache does not see
+    int32_t next_order = 0;
+    if (lane == 0) next_order = __builtin_nontemporal_load(carry.next_order + l);
+    b.next_order = uni(next_order);
     // candidate lists in slot order: enemies (abstraction.enemies), resources
     // and own stockpiles (rush.harvest_sites)
     AS3 int16_t* le = bv<int16_t>(b, y.l_enemy);
@@ -244,30 +248,30 @@ NR_DEV int32_t building_site(const KGame& g, const Hdr& h, const Env& e, const B
     return at == 0ull ? kAbsent : __builtin_amdgcn_readlane(site, (int32_t)__builtin_ctzll(at));
 }
 
-// The least-birth unit among `mask` lanes (mask bit k = unit i0 + k of
-// chunk), or -1; masks hold up to 8 chunks of 64 units.
-struct UnitMask {
-    uint64_t w[8];
-};
+// Per-unit role bits of the rush decisions (u_role, one byte per own slot).
+enum : uint8_t { R_WORKER = 1, R_PICK = 2, R_IDLE = 4, R_LAST = 8 };
 
-NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const UnitMask& m, int lane) {
+NR_DEV AS3 uint8_t* roles(const Bot& b, const BotLayout& y) { return bv<uint8_t>(b, y.u_role); }
+
+// The unit of least birth among those whose role byte has any of `bits`
+// (rush.first_in_unit_order, N/bots/rush.py:56-58), excluding `skip0` and
+// `skip1`; -1 when there is none.
+NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const BotLayout& y, uint8_t bits, int32_t skip0,
+                        int32_t skip1, int lane) {
+    const AS3 uint8_t* r = roles(b, y);
     int32_t best = kLast, who = -1;
-    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
-        const int32_t i = i0 + lane;
-        if ((m.w[k] >> lane) & 1ull) {
-            const int32_t bi = e.birth[b.block + i];
-            if (bi < best) {
-                best = bi;
-                who = i;
-            }
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        if (!(r[i] & bits) || i == skip0 || i == skip1) continue;
+        const int32_t bi = e.birth[b.block + i];
+        if (bi < best) {
+            best = bi;
+            who = i;
         }
     }
     const int32_t mn = wave_min(best);
     const uint64_t at = ballot(who >= 0 && best == mn);
     return at == 0ull ? -1 : __builtin_amdgcn_readlane(who, (int32_t)__builtin_ctzll(at));
 }
-
-NR_DEV bool in_mask(const UnitMask& m, int32_t i) { return (m.w[i >> 6] >> (i & 63)) & 1ull; }
 
 // abstraction.build_if_not_already_building (N/bots/abstraction.py:286-297)
 // for a one-unit builder (or none); marks the site in the reserved bitmap.
@@ -291,77 +295,65 @@ NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bo
     b.next_order = wadd(b.next_order, g.C + 1);
 }
 
-// rush.build_base (N/bots/rush.py:88-104): clears the reserved bitmap,
-// returns the builder or -1.
-NR_DEV int32_t build_base(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
-                          const UnitMask& workers, int lane) {
+// rush.build_base (N/bots/rush.py:88-104) over the R_WORKER units: clears the
+// reserved bitmap, returns the builder or -1.
+NR_DEV int32_t build_base(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
     AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
     for (int32_t w = lane; w < (g.cells + 31) / 32; w += kWave) reserved[w] = 0u;
     bool any_base = false;
-    for (int32_t i0 = 0; i0 < g.C; i0 += kWave) {
-        const int32_t i = i0 + lane;
-        if (i < g.C) {
-            const Unit u = unit_at(g, e, b, i);
-            any_base |= u.present && u.type == kTypeBase;
-        }
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const Unit u = unit_at(g, e, b, i);
+        any_base |= u.present && u.type == kTypeBase;
     }
     any_base = ballot(any_base) != 0ull;
     const int32_t res = uni(e.sc[S_RES0 + b.player]);
     const bool builds = !any_base && res >= tabv(h, F_COST, kTypeBase);
-    const int32_t builder = builds ? first_of(g, e, b, workers, lane) : -1;
+    const int32_t builder = builds ? first_of(g, e, b, y, R_WORKER, -1, -1, lane) : -1;
     wave_sync();
     build_unless_building(g, h, e, b, y, builder, kTypeBase, lane);
     return builder;
 }
 
-// rush._harvest (N/bots/rush.py:156-181): returns the idle harvesters.
-NR_DEV UnitMask harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, const UnitMask& harvesters,
-                        int lane) {
-    UnitMask idle = {};
+// rush._harvest (N/bots/rush.py:156-181) for the R_PICK units; marks the
+// idle ones (no site to harvest) R_IDLE.
+NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, int lane) {
+    AS3 uint8_t* r = roles(b, y);
     const AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
     const AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
-    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
-        const int32_t i = i0 + lane;
-        bool chosen = false, lazy = false;
-        int32_t rs = kAbsent, rb = kAbsent, ss = kAbsent, sb = kAbsent;
-        Unit u = {};
-        if ((harvesters.w[k] >> lane) & 1ull) {
-            u = unit_at(g, e, b, i);
-            closest(g, e, u.cell, lr, b.n_resource, &rs, &rb);
-            closest(g, e, u.cell, ls, b.n_stock, &ss, &sb);
-            const bool carrying = u.carried > 0;
-            const bool harvesting = is_entry(b, y, i, u.birth, kAbHarvest);
-            const bool same_base = bv<int32_t>(b, y.k_base)[i] == ss && bv<int32_t>(b, y.k_bbirth)[i] == sb;
-            const bool same_target = bv<int32_t>(b, y.k_target)[i] == rs && bv<int32_t>(b, y.k_tbirth)[i] == rb;
-            const bool occupied = carrying ? ss != kAbsent : (ss != kAbsent && rs != kAbsent);
-            const bool unchanged = harvesting && same_base && (carrying || same_target);
-            chosen = occupied && !unchanged;
-            lazy = !occupied;
-            if (chosen)
-                put_unit(g, b, u, i, false, kAbHarvest, carrying ? kAbsent : rs, carrying ? kAbsent : rb, ss, sb,
-                         kAbsent, kAbsent, y);
-        }
-        idle.w[k] = ballot(lazy);
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const uint8_t role = r[i];
+        if (!(role & R_PICK)) continue;
+        const Unit u = unit_at(g, e, b, i);
+        int32_t rs, rb, ss, sb;
+        closest(g, e, u.cell, lr, b.n_resource, &rs, &rb);
+        closest(g, e, u.cell, ls, b.n_stock, &ss, &sb);
+        const bool carrying = u.carried > 0;
+        const bool harvesting = is_entry(b, y, i, u.birth, kAbHarvest);
+        const bool same_base = bv<int32_t>(b, y.k_base)[i] == ss && bv<int32_t>(b, y.k_bbirth)[i] == sb;
+        const bool same_target = bv<int32_t>(b, y.k_target)[i] == rs && bv<int32_t>(b, y.k_tbirth)[i] == rb;
+        const bool occupied = carrying ? ss != kAbsent : (ss != kAbsent && rs != kAbsent);
+        const bool unchanged = harvesting && same_base && (carrying || same_target);
+        if (occupied && !unchanged)
+            put_unit(g, b, u, i, false, kAbHarvest, carrying ? kAbsent : rs, carrying ? kAbsent : rb, ss, sb, kAbsent,
+                     kAbsent, y);
+        if (!occupied) r[i] = (uint8_t)(role | R_IDLE);
     }
     b.next_order = wadd(b.next_order, g.C + 1);
     wave_sync();
-    return idle;
 }
 
-// rush._attack_nearest (N/bots/rush.py:61-70).
-NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, const UnitMask& attackers,
-                           const UnitMask* last, int lane) {
-    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
-        const int32_t i = i0 + lane;
-        if ((attackers.w[k] >> lane) & 1ull) {
-            const int32_t es = bv<int16_t>(b, y.u_es)[i];
-            if (es != kAbsent) {
-                const Unit u = unit_at(g, e, b, i);
-                const bool lst = last && ((last->w[k] >> lane) & 1ull);
-                put_unit(g, b, u, i, lst, kAbAttack, es, bv<int32_t>(b, y.u_eb)[i], kAbsent, kAbsent, kAbsent,
-                         kAbsent, y);
-            }
-        }
+// rush._attack_nearest (N/bots/rush.py:61-70) for the units whose role has
+// any of `bits`; R_LAST units are stamped last.
+NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, uint8_t bits, int lane) {
+    const AS3 uint8_t* r = roles(b, y);
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const uint8_t role = r[i];
+        if (!(role & bits)) continue;
+        const int32_t es = bv<int16_t>(b, y.u_es)[i];
+        if (es == kAbsent) continue;
+        const Unit u = unit_at(g, e, b, i);
+        put_unit(g, b, u, i, (role & R_LAST) != 0, kAbAttack, es, bv<int32_t>(b, y.u_eb)[i], kAbsent, kAbsent,
+                 kAbsent, kAbsent, y);
     }
     b.next_order = wadd(b.next_order, g.C + 1);
     wave_sync();
@@ -379,39 +371,31 @@ NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y
     wave_sync();
 }
 
-// rush._melee_units_attack with available_melee (N/bots/rush.py:73-85).
+// rush._melee_units_attack with available_melee (N/bots/rush.py:73-85); also
+// marks the workers (present units that can harvest) R_WORKER.
 NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
-    UnitMask m = {};
-    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
-        const int32_t i = i0 + lane;
-        bool melee = false;
-        if (i < g.C) {
-            const Unit u = unit_at(g, e, b, i);
-            melee = u.present && type_flag(g, h, u.type, FL_ATTACK) && !type_flag(g, h, u.type, FL_HARVEST) &&
-                    u.available;
-        }
-        m.w[k] = ballot(melee);
+    AS3 uint8_t* r = roles(b, y);
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const Unit u = unit_at(g, e, b, i);
+        const bool harvests = type_flag(g, h, u.type, FL_HARVEST);
+        const bool melee = u.present && type_flag(g, h, u.type, FL_ATTACK) && !harvests && u.available;
+        r[i] = (uint8_t)((melee ? R_PICK : 0) | ((u.present && harvests) ? R_WORKER : 0));
     }
-    attack_nearest(g, e, b, y, m, nullptr, lane);
+    wave_sync();
+    attack_nearest(g, e, b, y, R_PICK, lane);
 }
 
-NR_DEV UnitMask workers_of(const KGame& g, const Hdr& h, const Env& e, const Bot& b, int lane) {
-    UnitMask m = {};
-    for (int32_t k = 0, i0 = 0; i0 < g.C; ++k, i0 += kWave) {
-        const int32_t i = i0 + lane;
-        bool w = false;
-        if (i < g.C) {
-            const Unit u = unit_at(g, e, b, i);
-            w = u.present && type_flag(g, h, u.type, FL_HARVEST);
-        }
-        m.w[k] = ballot(w);
+// Role bytes for a new decision: R_WORKER kept, `pick` units get R_PICK,
+// others lose R_PICK / R_IDLE / R_LAST.
+NR_DEV void mark_picks(const KGame& g, const Bot& b, const BotLayout& y, int32_t skip0, int32_t skip1, int32_t only,
+                       int lane) {
+    AS3 uint8_t* r = roles(b, y);
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const uint8_t w = r[i] & R_WORKER;
+        const bool pick = only >= 0 ? i == only : (w && i != skip0 && i != skip1);
+        r[i] = (uint8_t)(w | (pick ? R_PICK : 0));
     }
-    return m;
-}
-
-NR_DEV UnitMask without(UnitMask m, int32_t i) {
-    if (i >= 0) m.w[i >> 6] &= ~(1ull << (i & 63));
-    return m;
+    wave_sync();
 }
 
 // rush.worker_rush (N/bots/rush.py:213-220) with _rushing_workers (:204-210).
@@ -422,15 +406,21 @@ NR_DEV void worker_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, cons
                 [&](const Unit& u) { return u.present && u.type == kTypeBase && u.available && res >= worker_cost; },
                 lane);
     melee_attack(g, h, e, b, y, lane);
-    const UnitMask workers = workers_of(g, h, e, b, lane);
-    const int32_t builder = build_base(g, h, e, b, y, workers, lane);
-    const int32_t harvester = first_of(g, e, b, without(workers, builder), lane);
-    UnitMask one = {};
-    if (harvester >= 0) one.w[harvester >> 6] = 1ull << (harvester & 63);
-    const UnitMask idle = harvest(g, e, b, y, one, lane);
-    UnitMask free = without(without(workers, builder), harvester);
-    for (int k = 0; k < 8; ++k) free.w[k] |= idle.w[k];
-    attack_nearest(g, e, b, y, free, &idle, lane);
+    const int32_t builder = build_base(g, h, e, b, y, lane);
+    const int32_t harvester = first_of(g, e, b, y, R_WORKER, builder, -1, lane);
+    mark_picks(g, b, y, -1, -1, harvester < 0 ? g.C : harvester, lane);
+    harvest(g, e, b, y, lane);
+    // free = (workers - builder - harvester) | idle harvester; the idle
+    // harvester is stamped last
+    AS3 uint8_t* r = roles(b, y);
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const uint8_t role = r[i];
+        const bool idle = (role & R_IDLE) != 0;
+        const bool free = ((role & R_WORKER) && i != builder && i != harvester) || idle;
+        r[i] = (uint8_t)((role & R_WORKER) | (free ? R_PICK : 0) | (idle ? R_LAST : 0));
+    }
+    wave_sync();
+    attack_nearest(g, e, b, y, R_PICK, lane);
 }
 
 // rush.barracks_rush (N/bots/rush.py:229-236) with train_at_base_and_barracks
@@ -459,55 +449,51 @@ NR_DEV void barracks_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, co
                 [&](const Unit& u) { return u.present && u.type == kTypeBarracks && u.available && res >= trained_cost; },
                 lane);
     melee_attack(g, h, e, b, y, lane);
-    const UnitMask workers = workers_of(g, h, e, b, lane);
-    const int32_t base_builder = build_base(g, h, e, b, y, workers, lane);
+    const int32_t base_builder = build_base(g, h, e, b, y, lane);
     const int32_t used = base_builder >= 0 ? tabv(h, F_COST, kTypeBase) : 0;
     const bool builds_barracks = !any_barracks && res >= wadd(tabv(h, F_COST, kTypeBarracks), used);
-    const UnitMask rest = without(workers, base_builder);
-    const int32_t barracks_builder = builds_barracks ? first_of(g, e, b, rest, lane) : -1;
+    const int32_t barracks_builder = builds_barracks ? first_of(g, e, b, y, R_WORKER, base_builder, -1, lane) : -1;
     build_unless_building(g, h, e, b, y, barracks_builder, kTypeBarracks, lane);
-    const UnitMask idle = harvest(g, e, b, y, without(rest, barracks_builder), lane);
-    attack_nearest(g, e, b, y, idle, nullptr, lane);
+    mark_picks(g, b, y, base_builder, barracks_builder, -1, lane);
+    harvest(g, e, b, y, lane);
+    attack_nearest(g, e, b, y, R_IDLE, lane);
 }
 
 // ---------------------------------------------------------------------------
 // pathfinding.search (N/bots/pathfinding.py:170-245) on lane 0.
 // Open cells pop by least f = g + Manhattan(cell, target), the most recently
 // inserted first among equal f; neighbours are inserted up, right, down,
-// left; each cell once.  f grows by 0 or 2 per step, so stacks indexed by
-// (f - f_start) / 2 hold the open list.  Returns the first step's direction,
-// or -1 when no cell within `range` of the target is reachable or the start
-// is already within it.  seen[c] = 0 open, 1 blocked, 2 inserted; top[] = -1.
+// left; each cell once.  A neighbour's f is the popped cell's f or f + 2,
+// and every open cell has f_low or f_low + 2 (f_low = f of the last pop), so
+// the open list is two LIFO stacks linked through below[]: `cur` (f_low)
+// and `nxt` (f_low + 2).  mark[c]: 0 open, 1 blocked, 2 + d inserted with
+// first step d from the start.  Returns the first step's direction, or -1
+// when no cell within `range` of the target is reachable or the start is
+// already within it.
 // ---------------------------------------------------------------------------
-NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* top, AS3 int16_t* below, AS3 int16_t* parent,
-                                AS3 uint8_t* seen, int32_t start, int32_t target, int32_t range) {
+NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* below, AS3 uint8_t* mark, int32_t start, int32_t target,
+                                int32_t range) {
     const int32_t W = g.W, H = g.H;
     const int32_t tx = floor_mod(target, W), ty = floor_div(target, W);
     const int32_t r2 = (int32_t)((uint32_t)range * (uint32_t)range);
-    seen[start] = 2;
-    parent[start] = (int16_t)start;
+    mark[start] = 2;
+    int32_t cur = start, nxt = -1;
     below[start] = -1;
-    top[0] = (int16_t)start;
-    int32_t lowest = 0, open = 1;
-    while (open > 0) {
-        while (top[lowest] == -1) ++lowest;
-        const int32_t pos = top[lowest];
-        top[lowest] = below[pos];
-        --open;
+    while (true) {
+        if (cur < 0) {
+            if (nxt < 0) return kAbsent;
+            cur = nxt;
+            nxt = -1;
+        }
+        const int32_t pos = cur;
+        cur = below[pos];
         const int32_t py = cell_y(g, pos), px = pos - py * W;
         const int32_t dx = px - tx, dy = py - ty;
+        const int32_t first = (int32_t)mark[pos] - 3;  // -1 at the start
         if (dx * dx + dy * dy <= r2) {
-            int32_t at = pos, above = parent[pos], last = pos;
-            while (above != at) {
-                last = at;
-                at = above;
-                above = parent[at];
-            }
-            if (last == at + W) return 2;
-            if (last == at - 1) return 3;
-            if (last == at - W) return 0;
-            if (last == at + 1) return 1;
-            return kAbsent;
+            // the reference maps the step offset +W, -1, -W, +1 in that order:
+            // on a one-wide board an upward step (-W = -1) reads as LEFT
+            return (first == 0 && W == 1) ? 3 : first;
         }
         const int32_t hcur = abs(dx) + abs(dy);
 #pragma unroll
@@ -515,16 +501,17 @@ NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* top, AS3 int16_t* b
             const int32_t nx = px + dir_dx(d), ny = py + dir_dy(d);
             if (nx < 0 || nx >= W || ny < 0 || ny >= H) continue;
             const int32_t nb = ny * W + nx;
-            if (seen[nb] != 0) continue;
-            const int32_t stack = lowest + (1 + abs(nx - tx) + abs(ny - ty) - hcur) / 2;
-            seen[nb] = 2;
-            parent[nb] = (int16_t)pos;
-            below[nb] = top[stack];
-            top[stack] = (int16_t)nb;
-            ++open;
+            if (mark[nb] != 0) continue;
+            mark[nb] = (uint8_t)(3 + (first < 0 ? d : first));
+            if (abs(nx - tx) + abs(ny - ty) < hcur) {
+                below[nb] = (int16_t)cur;
+                cur = nb;
+            } else {
+                below[nb] = (int16_t)nxt;
+                nxt = nb;
+            }
         }
     }
-    return kAbsent;
 }
 
 // ---------------------------------------------------------------------------
@@ -732,10 +719,8 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
     AS3 uint32_t* freem = bv<uint32_t>(b, y.m_free);
     AS3 uint32_t* used = bv<uint32_t>(b, y.m_used);
     AS3 uint32_t* kept_m = bv<uint32_t>(b, y.m_kept);
-    AS3 int16_t* top = bv<int16_t>(b, y.a_top);
     AS3 int16_t* below = bv<int16_t>(b, y.a_below);
-    AS3 int16_t* parent = bv<int16_t>(b, y.a_parent);
-    AS3 uint8_t* seen = bv<uint8_t>(b, y.a_seen);
+    AS3 uint8_t* mark = bv<uint8_t>(b, y.a_mark);
     const int32_t own = b.player;
     const bool moves_allowed = within_balance(e, b, 0) && within_balance(e, b, 1);
     const int32_t reserved_own = own == 0 ? b.reserved0 : b.reserved1;
@@ -749,13 +734,10 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
         int32_t step = kAbsent;
         // the first pop is the start: already within range means no step
         if (start >= 0 && start < g.cells && sq_distance(g, start, goal) > wmul(radius, radius)) {
-            for (int32_t c = lane; c < g.cells; c += kWave) {
-                top[c] = -1;
-                seen[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
-            }
+            for (int32_t c = lane; c < g.cells; c += kWave) mark[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
             wave_sync();
             int32_t s = kAbsent;
-            if (lane == 0) s = astar_first_step(g, top, below, parent, seen, start, goal, radius);
+            if (lane == 0) s = astar_first_step(g, below, mark, start, goal, radius);
             step = __builtin_amdgcn_readfirstlane(s);
             wave_sync();
         }
@@ -830,13 +812,13 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
 
 // _settled (N/bots/abstraction.py:1099-1119) into the carry rows of env l.
 NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry,
-                         bool reset, int lane) {
+                         int lane) {
     const int32_t C = g.C;
     int32_t standing = 0;
     for (int32_t i = lane; i < C; i += kWave) {
         const int64_t at = l * C + i;
         const int32_t fl = bv<uint8_t>(b, y.u_flags)[i];
-        const bool st = !reset && (fl & U_STANDING);
+        const bool st = (fl & U_STANDING) != 0;
         standing += st ? 1 : 0;
         if (!st) {
 #pragma unroll
@@ -858,6 +840,17 @@ NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64
     }
     standing = wave_sum(standing);
     if (lane == 0) carry.next_order[l] = standing;
+}
+
+// abstraction.empty_actions into the carry rows of env l (a new episode).
+NR_DEV void clear_carry(const KGame& g, int64_t l, const BotCarry& carry, int lane) {
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const int64_t at = l * g.C + i;
+#pragma unroll
+        for (int f = 0; f < 9; ++f) carry.row[f][at] = kAbsent;
+        carry.trained[at] = 0;
+    }
+    if (lane == 0) carry.next_order[l] = 0;
 }
 
 // family.act (N/bots/family.py:34-41): the rush decisions on the carry, then

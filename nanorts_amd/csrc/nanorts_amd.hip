@@ -303,6 +303,7 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
     by->k_utype = by->k_kind + 32 * C;
     by->k_trained = take(C);
     by->u_flags = take(C);
+    by->u_role = take(C);
     by->u_rank = take(2 * C);
     by->u_es = take(2 * C);
     by->u_eb = take(4 * C);
@@ -321,18 +322,19 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
     by->l_enemy = take(2 * E);
     by->l_resource = take(2 * E);
     by->l_stock = take(2 * E);
-    by->a_top = take(2 * cells);
     by->a_below = take(2 * cells);
-    by->a_parent = take(2 * cells);
-    by->a_seen = take(cells);
+    by->a_mark = take(cells);
     by->m_claimed = take(4 * words);
     by->m_free = take(4 * words);
     by->m_used = take(4 * words);
     by->m_kept = take(4 * words);
     by->m_reserved = take(4 * words);
     by->bytes = align16(o);
-    by->origin = g.lay.env_bytes;
-    g.lay.env_bytes += by->bytes;
+    // The bot runs before admission and keeps nothing past it, so its region
+    // shares the env block's phase union, after the command arrays the bot
+    // writes.
+    by->origin = g.lay.c_rank + align16(4 * C);
+    if (by->origin + by->bytes > g.lay.env_bytes) g.lay.env_bytes = by->origin + by->bytes;
     return fit_waves(out, why);
 }
 
@@ -667,7 +669,7 @@ __global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes,
 #pragma unroll
         for (int f = 0; f < 6; ++f) out[f * owned + p] = v[f];
     }
-    settle_carry(g, b, a.y, l, a.carry, false, lane);
+    settle_carry(g, b, a.y, l, a.carry, lane);
 }
 
 // seat.step_seat with a static learner seat (N/bots/seat.py:94-152): the
@@ -708,10 +710,11 @@ __global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanor
             decode_row(g, e, p, available, act);
         }
     }
+    // the carry is written before the step, whose phases reuse the region
+    settle_carry(g, b, a.y, l, a.carry, lane);
     wave_sync();
     core_step(g, hdr, e, lane, k0, k1, false);
-    const bool done = finish_step(g, hdr, e, l, lane, partial != 0, r, false);
-    settle_carry(g, b, a.y, l, a.carry, done, lane);
+    if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) clear_carry(g, l, a.carry, lane);
     store_env(g, s, l, e, lane);
     if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
 }
@@ -938,6 +941,109 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
     }
 }
 
+// Fused learner-vs-bot rollout: per cycle the learner's rows sampled from
+// its masks (the integer uniform-over-legal sampler, as nanorts_sample_actions
+// on get_avail_actions words), the bot's act, the seat step and the
+// observations, with the state resident in LDS across the launch.
+struct SeatRolloutArgs {
+    KGame g;  // first: fresh_game() reads it at offset 0
+    int64_t lanes;
+    nanorts_state s;
+    BotArgs bot;
+    int32_t learner, t0, steps, partial;  // cycles t0 .. t0 + steps - 1 of the caller's rollout
+    int64_t env0;
+    nanorts_rollout_results out;
+    uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
+};
+
+__global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
+    const KGame& g = args.g;
+    const int64_t lanes = args.lanes;
+    NR_KERNEL_PROLOGUE
+    load_env(g, args.s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
+    uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
+    fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+    const BotArgs& ba = args.bot;
+    const int32_t learner = args.learner;
+    Bot b;
+    b.base = e.base + ba.y.origin;
+    b.player = 1 - learner;
+    b.block = g.N + b.player * g.C;
+    const nanorts_rollout_results& out = args.out;
+    const Layout& y = g.lay;
+    const uint32_t env = (uint32_t)(args.env0 + l);
+    for (int32_t t = 0; t < args.steps; ++t) {
+        const int64_t tt = (int64_t)args.t0 + t;
+        // the learner: masks -> sample -> decode (unavailable rows absent)
+        bool irregular = false;
+        const int32_t n = compact_available(g, e, lane, &irregular);
+        build_bitmaps(g, hdr, e, lane);
+        const uint32_t ke0 = args.step_keys[2 * t], ke1 = args.step_keys[2 * t + 1];
+        const AS3 int16_t* av = at<int16_t>(e, y.a_av);
+        for (int32_t i = lane; i < n; i += kWave) {
+            const int32_t p = av[i];
+            if (p / g.C != learner) continue;
+            const Row r = legality_row_bm(g, hdr, e, g.N + p);
+            uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
+            threefry(ke0, ke1, w0, w1);
+            threefry(ke0, ke1, w2, w3);
+            uint32_t words[4] = {w0, w1, w2, w3};
+            int32_t act[7];
+            if (g.T <= 8) sample_row_words8(g, r, words, act);
+            else sample_row_words(g, r, words, act);
+            if (out.actions) {
+                int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
+#pragma unroll
+                for (int f = 0; f < 7; ++f) dst[f] = act[f];
+            }
+            decode_row(g, e, p, true, act);
+        }
+        if (out.actions) {
+            // unavailable rows sample all zeros
+            for (int32_t i = lane; i < g.C; i += kWave) {
+                const int32_t sl = g.N + learner * g.C + i;
+                if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
+                int32_t* dst = out.actions + ((tt * lanes + l) * g.C + i) * 7;
+#pragma unroll
+                for (int f = 0; f < 7; ++f) dst[f] = 0;
+            }
+        }
+        wave_sync();
+        // the bot's rows
+        const int32_t kept = bot_act(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane);
+        const int32_t top = (1 << g.rank_bits) - 1;
+        for (int32_t i = lane; i < g.C; i += kWave) {
+            const int32_t p = b.player * g.C + i;
+            int32_t v[6];
+            unit_command(g, e, b, ba.y, i, kept, v);
+            at<int8_t>(e, y.c_kind)[p] = (int8_t)canon_kind(v[0]);
+            at<int8_t>(e, y.c_dir)[p] = (int8_t)canon_dir(v[1]);
+            at<int32_t>(e, y.c_none)[p] = v[2];
+            at<int16_t>(e, y.c_target)[p] = (int16_t)canon_target(v[3], g.cells);
+            at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(v[4], g.T);
+            at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(v[5] == kAbsent ? 0 : v[5], 0, top);
+        }
+        settle_carry(g, b, ba.y, l, ba.carry, lane);
+        wave_sync();
+        core_step(g, hdr, e, lane, ek0, ek1, false);
+        nanorts_env_results r = {};
+        if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
+        if (out.dones) r.done = out.dones + tt * lanes;
+        if (finish_step(g, hdr, e, l, lane, args.partial != 0, r, false)) {
+            clear_carry(g, l, ba.carry, lane);
+            ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
+            ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
+            fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+        }
+        if (out.feature_maps || out.scalars) {
+            const int64_t slot = (out.depth > 0 ? (tt % out.depth) : 0) * lanes + l;
+            observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
+        }
+    }
+    store_env(g, args.s, l, e, lane);
+}
+
 // Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
 __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_state s, int32_t partial, const uint8_t* tiles, uint8_t* image,
                          int32_t* scalars) {
@@ -1120,7 +1226,7 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step";
+           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout";
 }
 
 const char* nanorts_last_error(void) { return g_error.c_str(); }
@@ -1376,6 +1482,54 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
             args.step_keys[2 * t + 1] = k1;
         }
         hipLaunchKernelGGL(k_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
+                           (hipStream_t)stream, args);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess)
+            return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    }
+    return NANORTS_OK;
+}
+
+int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                         int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
+                         const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
+                         nanorts_rollout_results results) {
+    NR_STATE(state)
+    if (!sample_key) return fail(NANORTS_INVALID_ARGUMENT, "sample_key is NULL");
+    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "a rollout needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    if (steps < 0) return fail(NANORTS_INVALID_ARGUMENT, "steps must be >= 0");
+    if ((results.feature_maps || results.scalars) && results.depth < 1)
+        return fail(NANORTS_INVALID_ARGUMENT, "depth must be >= 1");
+    Shape sh;
+    BotArgs a;
+    std::string why;
+    if (!bot_args(game, &sh, &a, strategy, trained_type, carry, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
+    if (lanes <= 0 || steps == 0) return NANORTS_OK;
+    const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    for (int32_t t0 = 0; t0 < steps; t0 += kRolloutChunk) {
+        SeatRolloutArgs args;
+        std::memset(&args, 0, sizeof(args));
+        args.g = sh.g;
+        args.lanes = lanes;
+        args.s = state;
+        args.bot = a;
+        args.learner = learner;
+        args.t0 = t0;
+        args.steps = steps - t0 < kRolloutChunk ? steps - t0 : kRolloutChunk;
+        args.partial = partial;
+        args.env0 = env0;
+        args.out = results;
+        for (int32_t t = 0; t < args.steps; ++t) {
+            uint32_t k0 = sample_key[0], k1 = sample_key[1];
+            host_fold_in(k0, k1, (uint32_t)(step0 + t0 + t));
+            args.step_keys[2 * t] = k0;
+            args.step_keys[2 * t + 1] = k1;
+        }
+        hipLaunchKernelGGL(k_seat_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
                            (hipStream_t)stream, args);
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess)

@@ -80,7 +80,7 @@ EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
-    "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step",
+    "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
 )
 
 _I64 = ctypes.c_int64
@@ -108,6 +108,8 @@ _SIGNATURES = {
     "nanorts_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
     "nanorts_seat_step": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32,
                                          EnvResults]),
+    "nanorts_seat_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32, _I32,
+                                            _I32, _I64, RolloutResults]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None

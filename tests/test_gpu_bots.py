@@ -144,3 +144,38 @@ def test_seat_rollout_matches_oracle(case):
             assert_states_equal(st, to_host(sst.environment_state), where)
             _assert_carry_equal(carry, _carry_to_host(sst.carry), where)
     assert ended >= L  # every env finished at least one episode
+
+
+@pytest.mark.parametrize("case", list(SEAT_CASES))
+def test_fused_seat_rollout_matches_oracle(case):
+    """The fused seat rollout (learner sampled in the kernel) over whole
+    episodes against the oracle's seat steps on the same sampler: per-cycle
+    rewards and dones, the learner's recorded actions, the last observation,
+    the final state and carry."""
+    import torch
+
+    from nanorts_amd.bots import SeatState
+
+    game, partial, bot = _game(case)
+    o = Oracle(game)
+    C = game.bucket.per_player_capacity
+    L = 32
+    steps = game.max_cycles + 40
+    st = batch_initial(game, L, roots(L, 13))
+    carry = empty_carry(L, C)
+    seat = _seat_env(game, partial, bot)
+    sst = SeatState(to_device(seat.env, st), _carry_to_device(carry, seat.device),
+                    torch.zeros(L, dtype=torch.int32, device=seat.device))
+    key = (41, 43)
+    got = seat.rollout(sst, steps, key, record_actions=True)
+    rewards, dones, actions = (got[k].cpu().numpy() for k in ("rewards", "dones", "actions"))
+    for t in range(steps):
+        want_actions = _learner_actions(o, st, t)
+        np.testing.assert_array_equal(actions[t], want_actions, err_msg=f"{case} actions at cycle {t}")
+        want = o.seat_step(st, carry, bot, LIGHT, 0, want_actions, partial, observe=t == steps - 1)
+        np.testing.assert_array_equal(rewards[t], want["reward"], err_msg=f"{case} cycle {t}")
+        np.testing.assert_array_equal(dones[t], want["done"].astype(bool), err_msg=f"{case} cycle {t}")
+    assert_states_equal(st, to_host(sst.environment_state), f"{case} final state")
+    _assert_carry_equal(carry, _carry_to_host(sst.carry), f"{case} final carry")
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
+    np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
