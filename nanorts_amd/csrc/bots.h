@@ -40,6 +40,7 @@ struct BotLayout {
     int32_t u_flags, u_role, u_rank, u_es, u_eb, u_goal, u_radius;
     int32_t u_fkind, u_fdir, u_ftarget, u_fptype, u_fclaimed, u_fcost;
     int32_t u_sel, u_dir, u_drank, u_queue;
+    int32_t u_live, u_lbirth, u_list, u_lkey;  // live units and their births; a scratch list with keys
     // candidate slot lists [E]
     int32_t l_enemy, l_resource, l_stock;
     // search scratch [cells]
@@ -62,6 +63,7 @@ struct Bot {
     AS3 uint8_t* base;
     int32_t player, block;
     int32_t n_enemy, n_resource, n_stock;
+    int32_t n_live;  // own units present, listed in u_live
     int32_t next_order;
     int32_t reserved0, reserved1;  // pending production cost per player
 };
@@ -163,18 +165,27 @@ NR_DEV bool is_entry(const Bot& b, const BotLayout& y, int32_t i, int32_t birth,
 NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
                       const BotCarry& carry, int lane) {
     const int32_t C = g.C;
+    // live own units in slot order, with their births
+    AS3 int16_t* live = bv<int16_t>(b, y.u_live);
+    AS3 int32_t* lbirth = bv<int32_t>(b, y.u_lbirth);
+    int32_t n = 0;
+    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+        const int32_t i = i0 + lane;
+        const int32_t bi = i < C ? e.birth[b.block + i] : kAbsent;
+        const bool present = bi != kAbsent;
+        const uint64_t m = ballot(present);
+        if (present) {
+            live[n + count_below(m)] = (int16_t)i;
+            lbirth[n + count_below(m)] = bi;
+        }
+        n += popc(m);
+    }
+    b.n_live = n;
     for (int32_t i = lane; i < C; i += kWave) {
         const int64_t at = l * C + i;
 #pragma unroll
         for (int f = 0; f < 9; ++f) bv<int32_t>(b, y.k_kind + f * 4 * C)[i] = carry.row[f][at];
         bv<uint8_t>(b, y.k_trained)[i] = carry.trained[at] ? 1 : 0;
-        const int32_t bi = e.birth[b.block + i];
-        int32_t r = 0;
-        for (int32_t j = 0; j < C; ++j) {
-            const int32_t bj = e.birth[b.block + j];
-            r += (bj != kAbsent && bj < bi) ? 1 : 0;
-        }
-        bv<int16_t>(b, y.u_rank)[i] = (int16_t)r;
     }
     // a vector load on one lane: in a fused rollout this word was written by
     // the previous cycle's vector store, which the scalar cache does not see
@@ -208,8 +219,13 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     b.n_resource = nr_;
     b.n_stock = ns;
     wave_sync();
-    // nearest enemy of every unit
-    for (int32_t i = lane; i < C; i += kWave) {
+    // birth rank among the present units (abstraction._rank) and the
+    // nearest enemy of every live unit
+    for (int32_t k = lane; k < n; k += kWave) {
+        const int32_t i = live[k], bi = lbirth[k];
+        int32_t r = 0;
+        for (int32_t q = 0; q < n; ++q) r += lbirth[q] < bi ? 1 : 0;
+        bv<int16_t>(b, y.u_rank)[i] = (int16_t)r;
         int32_t es, eb;
         closest(g, e, e.cell[b.block + i], le, ne, &es, &eb);
         bv<int16_t>(b, y.u_es)[i] = (int16_t)es;
@@ -260,7 +276,8 @@ NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const BotLay
                         int32_t skip1, int lane) {
     const AS3 uint8_t* r = roles(b, y);
     int32_t best = kLast, who = -1;
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         if (!(r[i] & bits) || i == skip0 || i == skip1) continue;
         const int32_t bi = e.birth[b.block + i];
         if (bi < best) {
@@ -301,7 +318,8 @@ NR_DEV int32_t build_base(const KGame& g, const Hdr& h, const Env& e, Bot& b, co
     AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
     for (int32_t w = lane; w < (g.cells + 31) / 32; w += kWave) reserved[w] = 0u;
     bool any_base = false;
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         any_base |= u.present && u.type == kTypeBase;
     }
@@ -320,7 +338,8 @@ NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, in
     AS3 uint8_t* r = roles(b, y);
     const AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
     const AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         if (!(role & R_PICK)) continue;
         const Unit u = unit_at(g, e, b, i);
@@ -346,7 +365,8 @@ NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, in
 // any of `bits`; R_LAST units are stamped last.
 NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, uint8_t bits, int lane) {
     const AS3 uint8_t* r = roles(b, y);
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         if (!(role & bits)) continue;
         const int32_t es = bv<int16_t>(b, y.u_es)[i];
@@ -363,7 +383,8 @@ NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout
 template <typename Pick>
 NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y, int32_t unit_type, Pick pick,
                         int lane) {
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         if (pick(u)) put_unit(g, b, u, i, false, kAbTrain, kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, unit_type, y);
     }
@@ -375,7 +396,8 @@ NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y
 // marks the workers (present units that can harvest) R_WORKER.
 NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         const bool harvests = type_flag(g, h, u.type, FL_HARVEST);
         const bool melee = u.present && type_flag(g, h, u.type, FL_ATTACK) && !harvests && u.available;
@@ -390,7 +412,8 @@ NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, con
 NR_DEV void mark_picks(const KGame& g, const Bot& b, const BotLayout& y, int32_t skip0, int32_t skip1, int32_t only,
                        int lane) {
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t w = r[i] & R_WORKER;
         const bool pick = only >= 0 ? i == only : (w && i != skip0 && i != skip1);
         r[i] = (uint8_t)(w | (pick ? R_PICK : 0));
@@ -413,7 +436,8 @@ NR_DEV void worker_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, cons
     // free = (workers - builder - harvester) | idle harvester; the idle
     // harvester is stamped last
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         const bool idle = (role & R_IDLE) != 0;
         const bool free = ((role & R_WORKER) && i != builder && i != harvester) || idle;
@@ -431,7 +455,8 @@ NR_DEV void barracks_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, co
     const int32_t res = uni(e.sc[S_RES0 + b.player]);
     int32_t held = 0;
     bool any_barracks = false;
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += kWave) {
+        const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         held += (u.present && u.type == kTypeWorker) ? 1 : 0;
         any_barracks |= u.present && u.type == kTypeBarracks;
@@ -686,21 +711,28 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
     }
     wave_sync();
     // _queue (:800-801): executing units by order, ties by unit index
+    AS3 int16_t* list = bv<int16_t>(b, y.u_list);
+    AS3 int32_t* key = bv<int32_t>(b, y.u_lkey);
     int32_t queued = 0;
     for (int32_t i0 = 0; i0 < C; i0 += kWave) {
         const int32_t i = i0 + lane;
         const bool ex = i < C && (bv<uint8_t>(b, y.u_flags)[i] & U_EXECUTES);
+        const uint64_t m = ballot(ex);
         if (ex) {
-            const int32_t oi = bv<int32_t>(b, y.k_order)[i];
-            int32_t r = 0;
-            for (int32_t j = 0; j < C; ++j) {
-                if (!(bv<uint8_t>(b, y.u_flags)[j] & U_EXECUTES)) continue;
-                const int32_t oj = bv<int32_t>(b, y.k_order)[j];
-                r += (oj < oi || (oj == oi && j < i)) ? 1 : 0;
-            }
-            bv<int16_t>(b, y.u_queue)[r] = (int16_t)i;
+            list[queued + count_below(m)] = (int16_t)i;
+            key[queued + count_below(m)] = bv<int32_t>(b, y.k_order)[i];
         }
-        queued += popc(ballot(ex));
+        queued += popc(m);
+    }
+    wave_sync();
+    for (int32_t k = lane; k < queued; k += kWave) {
+        const int32_t oi = key[k];
+        int32_t r = 0;
+        for (int32_t q = 0; q < queued; ++q) {
+            const int32_t oq = key[q];
+            r += (oq < oi || (oq == oi && q < k)) ? 1 : 0;
+        }
+        bv<int16_t>(b, y.u_queue)[r] = list[k];
     }
     for (int32_t i = lane; i < C; i += kWave) {
         bv<uint8_t>(b, y.u_sel)[i] = SEL_NONE;
@@ -797,9 +829,12 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
     const bool filler = u.available && !kept;
     int32_t filler_rank = 0;
     if (filler) {
-        for (int32_t j = 0; j < g.C; ++j) {
-            const Unit v = unit_at(g, e, b, j);
-            filler_rank += (v.available && bv<uint8_t>(b, y.u_sel)[j] == SEL_NONE && v.birth < u.birth) ? 1 : 0;
+        const AS3 int16_t* live = bv<int16_t>(b, y.u_live);
+        const AS3 int32_t* lbirth = bv<int32_t>(b, y.u_lbirth);
+        for (int32_t q = 0; q < b.n_live; ++q) {
+            const int32_t j = live[q];
+            filler_rank += (e.pkind[b.block + j] == kAbsent && bv<uint8_t>(b, y.u_sel)[j] == SEL_NONE &&
+                            lbirth[q] < u.birth) ? 1 : 0;
         }
     }
     out[0] = kept ? kind : (filler ? kKindNone : kAbsent);
@@ -814,12 +849,21 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
 NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry,
                          int lane) {
     const int32_t C = g.C;
+    // the standing units with their orders
+    AS3 int32_t* key = bv<int32_t>(b, y.u_lkey);
     int32_t standing = 0;
+    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+        const int32_t i = i0 + lane;
+        const bool st = i < C && (bv<uint8_t>(b, y.u_flags)[i] & U_STANDING);
+        const uint64_t m = ballot(st);
+        if (st) key[standing + count_below(m)] = bv<int32_t>(b, y.k_order)[i];
+        standing += popc(m);
+    }
+    wave_sync();
     for (int32_t i = lane; i < C; i += kWave) {
         const int64_t at = l * C + i;
         const int32_t fl = bv<uint8_t>(b, y.u_flags)[i];
         const bool st = (fl & U_STANDING) != 0;
-        standing += st ? 1 : 0;
         if (!st) {
 #pragma unroll
             for (int f = 0; f < 9; ++f) carry.row[f][at] = kAbsent;
@@ -828,8 +872,7 @@ NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64
         }
         const int32_t oi = bv<int32_t>(b, y.k_order)[i];
         int32_t r = 0;
-        for (int32_t j = 0; j < C; ++j)
-            r += ((bv<uint8_t>(b, y.u_flags)[j] & U_STANDING) && bv<int32_t>(b, y.k_order)[j] < oi) ? 1 : 0;
+        for (int32_t q = 0; q < standing; ++q) r += key[q] < oi ? 1 : 0;
         const int32_t kind = bv<int32_t>(b, y.k_kind)[i];
 #pragma unroll
         for (int f = 0; f < 9; ++f) carry.row[f][at] = bv<int32_t>(b, y.k_kind + f * 4 * C)[i];
@@ -838,7 +881,6 @@ NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64
                              ((fl & U_EXECUTES) && (kind == kAbTrain || kind == kAbTrainDirection));
         carry.trained[at] = trained ? 1 : 0;
     }
-    standing = wave_sum(standing);
     if (lane == 0) carry.next_order[l] = standing;
 }
 

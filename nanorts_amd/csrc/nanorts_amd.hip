@@ -319,6 +319,10 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
     by->u_dir = take(C);
     by->u_drank = take(2 * C);
     by->u_queue = take(2 * C);
+    by->u_live = take(2 * C);
+    by->u_lbirth = take(4 * C);
+    by->u_list = take(2 * C);
+    by->u_lkey = take(4 * C);
     by->l_enemy = take(2 * E);
     by->l_resource = take(2 * E);
     by->l_stock = take(2 * E);
