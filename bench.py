@@ -9,6 +9,12 @@ the fused rollout kernel (state resident in LDS for `--chunk` cycles per
 launch); the per-call path (masks, sampler and env.step as three launches per
 cycle) is timed beside it and reported in `config`.
 
+`--workload seat-workerrush` / `seat-lightrush` measure the learner-vs-bot
+configuration instead: basesWorkers16x16, VERSION_ORIGINAL_FINETUNED,
+CANCEL_BOTH, max_cycles 3000, 32768 games, player_1 = WorkerRush or LightRush
+on the device, player_0 = seeded uniform-random legal actions, full episodes
+with auto-reset (the fused seat rollout kernel).
+
 Prints one JSON line (rank 0, N=1).
 """
 from __future__ import annotations
@@ -29,14 +35,16 @@ HBM_PEAK_GBPS = 8000.0
 MAP = "basesWorkers16x16"
 NUM_ENVS = 65536
 METRIC = "env-steps/sec (both players) at 16x16 × 65536 envs; % HBM roofline"
+SEAT_ENVS = 32768
 
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush"), default="headline")
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--envs", type=int, default=NUM_ENVS)
+    ap.add_argument("--envs", type=int, default=None)
     ap.add_argument("--chunk", type=int, default=100, help="cycles per fused launch")
     ap.add_argument("--depth", type=int, default=2, help="observation ring depth in HBM")
     ap.add_argument("--per-call-steps", type=int, default=20)
@@ -45,7 +53,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
     ap.add_argument("--profile-child", choices=("rollout", "copy"), default=None, help=argparse.SUPPRESS)
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.envs is None:
+        args.envs = NUM_ENVS if args.workload == "headline" else SEAT_ENVS
+    return args
 
 
 def state_bytes(bucket) -> int:
@@ -200,6 +211,109 @@ def pmc_traffic(args, per_launch_steps: int) -> dict | None:
         return None
 
 
+def carry_bytes(bucket) -> int:
+    """One env's bot carry (AbstractActions): nine int32 rows, a bool row and
+    next_order."""
+    return bucket.per_player_capacity * (9 * 4 + 1) + 4
+
+
+def cpu_seat_baseline(bot_name: str, envs: int, steps: int) -> dict:
+    """The oracle's seat loop (masks, the learner's sampler rows, bot act,
+    seat step) on one host thread over a bounded sample."""
+    from nanorts_amd import env as envmod
+    from nanorts_amd.content import map_name_to_scenario
+    from oracle.oracle import Oracle, batch_initial, empty_carry
+
+    game = map_name_to_scenario(MAP, max_cycles=3000)
+    oracle = Oracle(game)
+    state = batch_initial(game, envs, envmod.env_roots(0, envs))
+    carry = empty_carry(envs, game.bucket.per_player_capacity)
+    strategy = 0 if bot_name == "workerRushAI" else 1
+    t0 = time.perf_counter()
+    for t in range(steps):
+        actions = oracle.sample_actions(oracle.avail_rows(state), (11, 13), t)[:, 0].copy()
+        oracle.seat_step(state, carry, strategy, 4, 0, actions, False)
+    dt = time.perf_counter() - t0
+    return {"value": round(envs * steps / dt, 1), "unit": "env-steps/s", "cores": 1, "kind": "port",
+            "sample": f"{envs} games x {steps} cycles of the same workload (oracle: masks, learner sampler, "
+                      f"{bot_name} act, seat step, auto-reset, symbolic obs) on 1 host thread, {dt:.1f} s"}
+
+
+def main_seat(args) -> None:
+    import torch
+
+    import nanorts_amd
+    from nanorts_amd import bots
+    from nanorts_amd import env as envmod
+
+    torch.cuda.set_device(0)
+    bot = bots.workerRushAI if args.workload == "seat-workerrush" else bots.lightRushAI
+    game = nanorts_amd.map_name_to_scenario(MAP, max_cycles=3000)
+    seat = bots.SeatEnv(bot, scenario=game, final_observation=False)
+    L = args.envs
+    _, state = seat.reset(envmod.env_roots(0, L))
+    chunk = max(1, min(args.chunk, args.steps))
+
+    def run(steps, step0, events):
+        done, times = 0, []
+        while done < steps:
+            n = min(chunk, steps - done)
+            if events:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+            seat.rollout(state, n, (11, 13), step0=step0 + done, observation_depth=args.depth)
+            if events:
+                b.record()
+                times.append((a, b, n))
+            done += n
+        return times
+
+    run(args.warmup, 0, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    times = run(args.steps, args.warmup, True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [a.elapsed_time(b) for a, b, _ in times]
+    full = [ms for (a, b, n), ms in zip(times, launch_ms) if n == chunk] or launch_ms
+    avg_launch_s = sum(full) / len(full) / 1e3
+    b = game.bucket
+    per_step = step_bytes(b) + 2 * carry_bytes(b)
+    per_launch_bytes = L * (chunk * per_step + 2 * state_bytes(b))
+    achieved = per_launch_bytes / avg_launch_s / 1e9
+    cpu = None if args.no_cpu else cpu_seat_baseline(bot.name, args.cpu_envs // 4, args.cpu_steps // 15)
+    line = {
+        "metric": f"env-steps/sec (learner vs {bot.name}) at 16x16 × {L} envs; % HBM roofline",
+        "value": round(L * args.steps / wall, 1),
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic: player_0 seeded uniform-random legal actions, player_1 the scripted bot, shipped "
+                "basesWorkers16x16 map",
+        "config": {
+            "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_BOTH, max_cycles 3000, {L} games, player_1 "
+                        f"{bot.name} on the device, full episodes with auto-reset, fused seat rollout {chunk} "
+                        f"cycles/launch",
+            "games": L, "slots_per_player": b.per_player_capacity,
+            "algorithmic_bytes_per_env_step": per_step, "carry_bytes_per_env": carry_bytes(b),
+            "state_bytes_per_env": state_bytes(b), "observation_ring_depth": args.depth,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_seat_rollout",
+            "avg_launch_ms": round(avg_launch_s * 1e3, 4), "algorithmic_bytes_per_launch": per_launch_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
 def main() -> None:
     args = parse()
     if args.profile_child:
@@ -209,6 +323,9 @@ def main() -> None:
         print(f"bench.py measures one GPU: the env path shards by env with no exchange, and this run has no "
               f"multi-GPU configuration (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "headline":
+        main_seat(args)
+        return
     import torch
 
     torch.cuda.set_device(0)
