@@ -74,6 +74,7 @@ enum : int {
     S_IRREG,  // 1 when an available unit holds a pending order
     S_NUNITS, // active owned units listed by summarize
     S_NA,     // pending MOVE / PRODUCE entries listed by summarize
+    S_VISDIRTY,  // bit p: a unit of player p moved, spawned or died since its sight was last stamped
     S_COUNT = 20
 };
 
@@ -414,6 +415,7 @@ NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const En
             case S_ROOT0: v = s.environment_root ? (int32_t)s.environment_root[2 * l] : 0; break;
             case S_ROOT1: v = s.environment_root ? (int32_t)s.environment_root[2 * l + 1] : 0; break;
             case S_EPISODE: v = s.episode_index ? (int32_t)s.episode_index[l] : 0; break;
+            case S_VISDIRTY: v = 3; break;
             default: break;
         }
         e.sc[lane] = v;
@@ -923,6 +925,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
             if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)slot;
             if (rcell >= 0 && rcell < g.cells) e.entity[rcell] = (int16_t)kAbsent;
             e.cell[slot] = (int16_t)dest;
+            e.sc[S_VISDIRTY] |= 1 << player;
         }
     } else if (kind == kKindHarvest) {
         const Nb n = neighbour(g, h, e, rcell, dir);
@@ -975,6 +978,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
                     e.hp[newborn] = (int16_t)tabv(h, F_HP, newborn_type);
                     e.sc[S_NEXT_BIRTH] = wadd(birth, 1);
                     e.sc[S_UNITS0 + player] += 1;
+                    e.sc[S_VISDIRTY] |= 1 << player;
                 } else {
                     e.sc[S_SO0 + player] = wadd(e.sc[S_SO0 + player], 1);
                 }
@@ -1000,6 +1004,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
             if (removed >= g.N && removed < g.E && e.birth[removed] != kAbsent) {
                 const int32_t owner_block = (removed - g.N) / g.C;
                 e.sc[S_UNITS0 + owner_block] -= 1;
+                e.sc[S_VISDIRTY] |= 1 << owner_block;
             }
             if (removed >= 0 && removed < g.E) at<uint64_t>(e, g.lay.o_live)[removed >> 6] &= ~(1ull << (removed & 63));
             remove_slot(e, removed);
@@ -1250,6 +1255,7 @@ NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
             case S_SO0: v = s.spawn_overflow[0]; break;
             case S_SO1: v = s.spawn_overflow[1]; break;
             case S_EPISODE: v = (int32_t)((uint32_t)episode + 1u); break;
+            case S_VISDIRTY: v = 3; break;
             default: break;
         }
         e.sc[lane] = v;

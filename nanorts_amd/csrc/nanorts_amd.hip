@@ -933,7 +933,11 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             if (fast) {
                 uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
                 int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
-                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+                // the sight bitmaps persist in the event counters' words, which
+                // the rollout does not count, when both planes fit there
+                const int32_t kept = 2 * g.H * g.seen_words <= 32 ? g.lay.b_events : -1;
+                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr,
+                          kept);
             } else if (out.feature_maps || out.scalars) {
                 observe_both(g, hdr, e, slot, lane, a.partial != 0, out.feature_maps, out.scalars);
             }

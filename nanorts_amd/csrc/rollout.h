@@ -284,10 +284,13 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
 // row into a per-lane accumulator of its player; the U partial rows are
 // OR-ed across lanes at the end, so the bitmap is written once, without
 // atomics.  Taller boards stamp (unit, dy) rows with LDS atomics.
-NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+// Sight bitmaps of the players whose bit is set in `which` (the others'
+// planes are left as they are).
+NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane, int32_t seen_at,
+                                 int32_t which) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
-    AS3 uint32_t* seen = at<uint32_t>(e, y.v_seen);
+    AS3 uint32_t* seen = at<uint32_t>(e, seen_at);
     const int32_t words = g.seen_words, plane = g.H * words;
     const int32_t nunits = uni(e.sc[S_NUNITS]);
     AS3 const int16_t* units = at<int16_t>(e, y.b_units);
@@ -297,7 +300,10 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
         const int32_t k = lane / g.H, row = lane - k * g.H;
         const uint32_t rowmask = g.W >= 32 ? 0xFFFFFFFFu : ((1u << g.W) - 1u);
         uint32_t acc0 = 0u, acc1 = 0u;
-        for (int32_t base = 0; base < nunits; base += U) {
+        // the listed units are player 0's, then player 1's
+        const int32_t n0 = uni(e.sc[S_UNITS0]);
+        const int32_t first = (which & 1) ? 0 : n0, last = (which & 2) ? nunits : n0;
+        for (int32_t base = first; base < last; base += U) {
             const int32_t i = base + k;
             if (k >= U || i >= nunits) continue;
             const int32_t s = units[i];
@@ -316,8 +322,8 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
             acc1 |= (uint32_t)__shfl((int)acc1, lane + j * g.H, kWave);
         }
         if (lane < g.H) {
-            seen[lane] = acc0;
-            seen[plane + lane] = acc1;
+            if (which & 1) seen[lane] = acc0;
+            if (which & 2) seen[plane + lane] = acc1;
         }
         wave_sync();
         return;
@@ -358,7 +364,7 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
 // Pass over the cells, four per lane (W % 4 == 0): bitmaps for the masks and
 // both agents' feature maps.  maps0/maps1 may be null (no observation).
 NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool partial, bool bitmaps,
-                            uint8_t* maps0, uint8_t* maps1) {
+                            uint8_t* maps0, uint8_t* maps1, int32_t seen_at) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t words = g.seen_words, plane = g.H * words;
@@ -369,7 +375,7 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
     }
     AS3 const uint32_t* olo = at<uint32_t>(e, y.o_lo);
     AS3 const uint8_t* ofl = at<uint8_t>(e, y.o_fl);
-    AS3 const uint32_t* seen = at<uint32_t>(e, y.v_seen);
+    AS3 const uint32_t* seen = at<uint32_t>(e, seen_at);
     const bool obs = maps0 != nullptr;
     // bits 0, 8, 16, 24 of x -> bits 0..3
     auto nibble = [](uint32_t x) {
@@ -441,11 +447,19 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
 
 // The summary of the current state; the observation is written when
 // maps0/maps1 are given (8-byte aligned), scalars when scalars0/1 are.
+// `kept_seen` >= 0 is the LDS offset of sight bitmaps kept from the last
+// summary: they are stamped again only for a state whose units moved,
+// spawned or died since (S_VISDIRTY).
 NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool partial, uint8_t* maps0,
-                      uint8_t* maps1, int32_t* scalars0, int32_t* scalars1) {
+                      uint8_t* maps1, int32_t* scalars0, int32_t* scalars1, int32_t kept_seen = -1) {
     summarize_slots(g, h, e, lane);
-    if (partial && maps0) summarize_visibility(g, h, e, lane);
-    summarize_cells(g, h, e, lane, partial, true, maps0, maps1);
+    const int32_t seen_at = kept_seen >= 0 ? kept_seen : g.lay.v_seen;
+    const int32_t which = kept_seen >= 0 ? uni(e.sc[S_VISDIRTY]) & 3 : 3;
+    if (partial && maps0 && which != 0) {
+        summarize_visibility(g, h, e, lane, seen_at, which);
+        if (kept_seen >= 0 && lane == 0) e.sc[S_VISDIRTY] = 0;
+    }
+    summarize_cells(g, h, e, lane, partial, true, maps0, maps1, seen_at);
     if (scalars0 && lane < 8) {
         const int32_t pl = lane >> 2, f = lane & 3;
         int32_t v;
