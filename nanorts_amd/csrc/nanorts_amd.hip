@@ -864,20 +864,31 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                     words[2] = w2;
                     words[3] = w3;
                 }
-                int32_t act[7];
-                if (g.T <= 8) sample_row_words8(g, r, words, act);
-                else sample_row_words(g, r, words, act);
-                if (out.actions) {
-                    int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
+                int32_t kind, dir, ptype, target, none;
+                if (!out.actions && g.T <= 8) {
+                    // unrecorded: only the factors decode reads are drawn
+                    sample_decode8(g, e, p, r, words, &kind, &dir, &ptype, &target, &none);
+                } else {
+                    int32_t act[7];
+                    if (g.T <= 8) sample_row_words8(g, r, words, act);
+                    else sample_row_words(g, r, words, act);
+                    if (out.actions) {
+                        int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
 #pragma unroll
-                    for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                        for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                    }
+                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                 }
                 if (fused) {
-                    int32_t kind, dir, ptype, target, none;
-                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                     request_of(g, hdr, e, p, kind, dir, ptype, target, none, true, false, q);
                 } else {
-                    decode_row(g, e, p, true, act);
+                    const Layout& y = g.lay;
+                    at<int8_t>(e, y.c_kind)[p] = (int8_t)kind;
+                    at<int8_t>(e, y.c_dir)[p] = (int8_t)dir;
+                    at<int8_t>(e, y.c_ptype)[p] = (int8_t)ptype;
+                    at<int16_t>(e, y.c_target)[p] = (int16_t)target;
+                    at<int32_t>(e, y.c_none)[p] = none;
+                    at<int16_t>(e, y.c_rank)[p] = 0;
                 }
             }
             if (out.actions) {
