@@ -867,7 +867,8 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 int32_t kind, dir, ptype, target, none;
                 if (!out.actions && g.T <= 8) {
                     // unrecorded: only the factors decode reads are drawn
-                    sample_decode8(g, e, p, r, words, &kind, &dir, &ptype, &target, &none);
+                    sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype, &target,
+                                   &none);
                 } else {
                     int32_t act[7];
                     if (g.T <= 8) sample_row_words8(g, r, words, act);

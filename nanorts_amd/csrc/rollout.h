@@ -105,29 +105,31 @@ NR_DEV void sample_row_words8(const KGame& g, const Row& r, const uint32_t words
 // sample_row_words8's draws: the factor of the sampled kind alone (and the
 // produced type for PRODUCE) is selected, the others are not needed.  Same
 // results as sample_row_words8 followed by decode_values.
-NR_DEV void sample_decode8(const KGame& g, const Env& e, int32_t p, const Row& r, const uint32_t words[4],
-                           int32_t* kind_out, int32_t* dir_out, int32_t* ptype_out, int32_t* target_out,
-                           int32_t* none_out) {
+NR_DEV void sample_decode8(const KGame& g, const Env& e, int32_t p, const Row& r, uint32_t w0, uint32_t w1,
+                           uint32_t w2, uint32_t w3, int32_t* kind_out, int32_t* dir_out, int32_t* ptype_out,
+                           int32_t* target_out, int32_t* none_out) {
     int32_t kind = kKindNone, dir = kAbsent, ptype = kAbsent, target = kAbsent;
     if (!only_none(r)) {
         const uint32_t mk = r.w[0] & 63u;
-        kind = select_bit8(mk, (int32_t)(((words[0] & 0xFFFFu) * (uint32_t)__popc(mk)) >> 16));
+        kind = select_bit8(mk, (int32_t)(((w0 & 0xFFFFu) * (uint32_t)__popc(mk)) >> 16));
         if (kind >= kKindMove && kind <= kKindProduce) {
             // factor f = kind: bits 2 + 4f .. 5 + 4f, draw half f & 1 of word f >> 1
             const uint32_t m = (r.w[0] >> (2 + 4 * kind)) & 15u;
-            const uint32_t w = kind == kKindMove ? words[0] : (kind == kKindProduce ? words[2] : words[1]);
+            uint32_t w = w1;
+            if (kind == kKindMove) w = w0;
+            if (kind == kKindProduce) w = w2;
             const uint32_t hh = (kind & 1) ? (w >> 16) : (w & 0xFFFFu);
             const int32_t c = __popc(m);
             dir = c > 0 ? select_bit8(m, (int32_t)((hh * (uint32_t)c) >> 16)) : 0;
             if (kind == kKindProduce) {
                 const uint32_t mt = (r.w[0] >> 22) & ((1u << g.T) - 1u);
                 const int32_t ct = __popc(mt);
-                ptype = ct > 0 ? select_bit8(mt, (int32_t)(((words[2] >> 16) * (uint32_t)ct) >> 16)) : 0;
+                ptype = ct > 0 ? select_bit8(mt, (int32_t)(((w2 >> 16) * (uint32_t)ct) >> 16)) : 0;
             }
         } else if (kind == kKindAttack) {
             const uint64_t m = row_bits(r, 22 + g.T, g.O);
             const int32_t c = popc(m);
-            const int32_t off = c > 0 ? select_bit(m, (int32_t)(((words[3] & 0xFFFFu) * (uint32_t)c) >> 16)) : 0;
+            const int32_t off = c > 0 ? select_bit(m, (int32_t)(((w3 & 0xFFFFu) * (uint32_t)c) >> 16)) : 0;
             const int32_t cell = e.cell[g.N + p];
             const int32_t tx = wadd(cell_x(g, cell), floor_mod(off, g.side) - g.radius);
             const int32_t ty = wadd(cell_y(g, cell), floor_div(off, g.side) - g.radius);
