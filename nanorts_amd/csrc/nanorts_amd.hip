@@ -941,7 +941,10 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             NR_ROLLOUT_PHASE
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
-            const int64_t slot = (out.depth > 0 ? (((int64_t)a.t0 + t) % out.depth) : 0) * lanes + l;
+            // ring slot (t0 + t) % depth in 32 bits (a mask for powers of two)
+            const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)a.t0 + (uint32_t)t;
+            const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
+            const int64_t slot = (int64_t)ring * lanes + l;
             if (fast) {
                 uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
                 int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
@@ -1057,7 +1060,9 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
             fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
         }
         if (out.feature_maps || out.scalars) {
-            const int64_t slot = (out.depth > 0 ? (tt % out.depth) : 0) * lanes + l;
+            const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
+            const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
+            const int64_t slot = (int64_t)ring * lanes + l;
             observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
