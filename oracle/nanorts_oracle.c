@@ -1509,3 +1509,8 @@ int32_t nro_state_violations(const nro_game* g, const nro_state* s, int64_t l) {
 /* Scripted bots and the learner-vs-bot seat (bots.c shares the env view).   */
 /* ------------------------------------------------------------------------ */
 #include "bots.c"
+
+/* ------------------------------------------------------------------------ */
+/* GridNet action decode (gridnet.c shares the env view and legality rows).  */
+/* ------------------------------------------------------------------------ */
+#include "gridnet.c"

@@ -200,6 +200,11 @@ void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, in
                    int32_t trained_type, int32_t learner, nro_abstract* carry, const int32_t* actions,
                    int32_t partial, nro_env_out* out);
 
+/* GridNet decode_actions (src/nanorts/adapters/gridnet/actions.py:31-52):
+ * per-cell actions [L][2][H*W][7] -> Commands [L][2][C] per field. */
+void nro_gridnet_decode(const nro_game* g, const nro_state* s, const int32_t* actions, int64_t L,
+                        nro_commands* out);
+
 /* Invariant check (src/nanorts/model/state.py:87-165); returns a bitmask of
  * violated invariants for env l, 0 when the state is well formed. */
 int32_t nro_state_violations(const nro_game* g, const nro_state* s, int64_t l);

@@ -306,6 +306,17 @@ class Oracle:
                                ctypes.byref(o))
         return out
 
+    def gridnet_decode(self, state, actions: np.ndarray) -> dict[str, np.ndarray]:
+        """GridNet decode_actions: per-cell actions [L][2][H][W][7] -> Commands [L][2][C] per field."""
+        L = state["time"].shape[0]
+        C = self.game.bucket.per_player_capacity
+        out = {f: np.zeros((L, 2, C), np.int32) for f, _ in Commands._fields_}
+        c = Commands(*[_ptr(out[f]) for f, _ in Commands._fields_])
+        actions = np.ascontiguousarray(actions, np.int32)
+        self.lib.nro_gridnet_decode(ctypes.byref(self.g), ctypes.byref(self._s(state)), _ptr(actions),
+                                    ctypes.c_int64(L), ctypes.byref(c))
+        return out
+
     def violations(self, state) -> np.ndarray:
         L = state["time"].shape[0]
         s = self._s(state)

@@ -1,0 +1,123 @@
+"""Pins of the GridNet decode in the CPU oracle (CPU only, no GPU).
+
+The GridNet surface (src/nanorts/adapters/gridnet/actions.py) reads one
+action row per cell and keeps, per player in cell order, the rows whose
+claimed position is still free and whose cost does not overdraw
+(source_filter.py).  It is checked here by a cycle traced by hand on the
+shipped 8x8 map, and on many mid-game states against the JaxMARL decode (the
+kept rows decode to the same commands) and against the filter's own
+invariants (no two kept claims share a position, kept rows are ranked in cell
+order, dropped and silent units wait as NONE fillers ranked by birth).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from nanorts_amd.content import map_name_to_scenario
+from oracle.oracle import Oracle, batch_initial
+from tests.helpers import advanced_states, game_for
+
+NONE, MOVE, HARVEST, RETURN, PRODUCE, ATTACK = range(6)
+UP, RIGHT, DOWN, LEFT = range(4)
+WORKER = 3
+STEP = {UP: (0, -1), RIGHT: (1, 0), DOWN: (0, 1), LEFT: (-1, 0)}
+
+
+def _place(st, slot, cell):
+    st["entity_at"].reshape(1, -1)[0, int(st["cell"][0, slot])] = -1
+    st["entity_at"].reshape(1, -1)[0, cell] = slot
+    st["cell"][0, slot] = cell
+
+
+def test_two_claims_on_one_cell_by_hand():
+    """Player 0's worker (slot 3) moved to cell 1 and its base (slot 2, cell
+    10): the worker MOVEs right and the base PRODUCEs up, both into cell 2.
+    The worker's cell comes first, so it keeps the cell; the base waits as a
+    filler.  Player 1 sends NONE everywhere: both its units keep NONE with
+    duration -1, ranked by cell."""
+    game = map_name_to_scenario("basesWorkers8x8")
+    o = Oracle(game)
+    st = batch_initial(game, 1, np.asarray([[1, 2]], np.uint32))
+    _place(st, 3, 1)
+    H, W = game.bucket.height, game.bucket.width
+    actions = np.zeros((1, 2, H * W, 7), np.int32)
+    actions[0, 0, 1] = [MOVE, RIGHT, 0, 0, 0, 0, 0]
+    actions[0, 0, 10] = [PRODUCE, 0, 0, 0, UP, WORKER, 0]
+    c = o.gridnet_decode(st, actions)
+    C = game.bucket.per_player_capacity
+    pick = lambda p, i: tuple(int(c[f][0, p, i]) for f in
+                              ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order"))
+    assert pick(0, 1) == (MOVE, RIGHT, 0, -1, -1, 0)      # the worker (slot 3 = position 1)
+    assert pick(0, 0) == (NONE, -1, 1, -1, -1, 1)         # the base: dropped, filler after the survivor
+    assert pick(1, 0) == (NONE, -1, -1, -1, -1, 0)        # player 1's base at cell 53
+    assert pick(1, 1) == (NONE, -1, -1, -1, -1, 1)        # its worker at cell 54
+    assert (c["kind"][0, :, 2:] == -1).all() and (c["request_order"][0, :, 2:] == -1).all()
+    # without the worker's claim the base keeps its production; both rows
+    # are kept, ranked by cell (the worker's cell 1 first)
+    actions[0, 0, 1] = [NONE, 0, 0, 0, 0, 0, 0]
+    c = o.gridnet_decode(st, actions)
+    assert pick(0, 0) == (PRODUCE, UP, 0, -1, WORKER, 1) and pick(0, 1) == (NONE, -1, -1, -1, -1, 0)
+    del C
+
+
+def _gridnet_rows(game, st, per_agent):
+    """Per-cell actions [L][2][cells][7]: each unit's JaxMARL row at its cell."""
+    L = st["time"].shape[0]
+    N, C, cells = game.bucket.neutral_capacity, game.bucket.per_player_capacity, game.bucket.cell_count
+    out = np.zeros((L, 2, cells, 7), np.int32)
+    for l in range(L):
+        for p in range(2):
+            for i in range(C):
+                s = N + p * C + i
+                if st["birth"][l, s] != -1:
+                    out[l, p, st["cell"][l, s]] = per_agent[l, p, i]
+    return out
+
+
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "8x8-original-both", "barracks-random"])
+def test_kept_rows_decode_like_jaxmarl_and_keep_the_filter_invariants(case, oracle_threads):
+    game, partial = game_for(case)
+    oracle, st = advanced_states(game, 64, 300, partial, oracle_threads, seed=19)
+    rows = oracle.avail_rows(st)
+    sampled = oracle.sample_actions(rows, (7, 8), 3)
+    grid = oracle.gridnet_decode(st, _gridnet_rows(game, st, sampled))
+    jax_like = oracle.decode_actions(st, sampled)
+    b = game.bucket
+    N, C, W = b.neutral_capacity, b.per_player_capacity, b.width
+    kept_total = dropped_total = 0
+    for l in range(64):
+        for p in range(2):
+            slots = N + p * C + np.arange(C)
+            available = (st["birth"][l, slots] != -1) & (st["pending_kind"][l, slots] == -1)
+            order = grid["request_order"][l, p]
+            kind = grid["kind"][l, p]
+            assert ((kind == -1) == ~available).all()
+            assert (order[~available] == -1).all()
+            # kept rows: the JaxMARL command (NONE waits -1), ranked 0.. in cell order
+            fillers = available & (kind == NONE) & (grid["none_duration"][l, p] == 1)
+            kept = available & ~fillers
+            cells = st["cell"][l, slots]
+            kept_idx = np.nonzero(kept)[0]
+            assert sorted(order[kept].tolist()) == list(range(kept.sum()))
+            assert (np.argsort(cells[kept_idx]) == np.argsort(order[kept_idx])).all()
+            for i in kept_idx:
+                for f in ("kind", "direction", "target_cell", "produced_type"):
+                    assert grid[f][l, p, i] == jax_like[f][l, p, i], (l, p, i, f)
+                want_none = -1 if kind[i] == NONE else 0
+                assert grid["none_duration"][l, p, i] == want_none
+            # fillers: NONE for 1 cycle, ranked after the kept rows by birth
+            fill_idx = np.nonzero(fillers)[0]
+            births = st["birth"][l, slots][fill_idx]
+            assert (np.argsort(births, kind="stable") == np.argsort(order[fill_idx], kind="stable")).all()
+            assert sorted(order[fill_idx].tolist()) == list(range(kept.sum(), kept.sum() + len(fill_idx)))
+            # no two kept claims of a player share a position
+            claims = [cells[i] + STEP[grid["direction"][l, p, i]][0] + W * STEP[grid["direction"][l, p, i]][1]
+                      for i in kept_idx if kind[i] in (MOVE, PRODUCE)]
+            assert len(claims) == len(set(claims))
+            # a dropped row was a claim or a cost (the filter only drops those)
+            for i in fill_idx:
+                assert jax_like["kind"][l, p, i] in (MOVE, PRODUCE)
+                dropped_total += 1
+            kept_total += len(kept_idx)
+    assert kept_total > 100 and dropped_total > 0
