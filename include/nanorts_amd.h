@@ -162,6 +162,42 @@ typedef struct nanorts_abstract_actions {
 #define NANORTS_WORKER_RUSH 0
 #define NANORTS_BARRACKS_RUSH 1
 
+/* Writable Commands [L][2][C] per field. */
+typedef struct nanorts_command_buffers {
+    int32_t* kind;
+    int32_t* direction;
+    int32_t* none_duration;
+    int32_t* target_cell;
+    int32_t* produced_type;
+    int32_t* request_order;
+} nanorts_command_buffers;
+
+/* GridNet observation buffers (src/nanorts/adapters/gridnet/observation.py:17-72,
+ * layout.py:46-70).  Any pointer may be NULL. */
+typedef struct nanorts_gridnet_obs {
+    int32_t planes_form;  /* 0 one-hot [L][2][H][W][29], 1 indices int8 [L][2][H][W][6] */
+    int32_t planes_bytes; /* one-hot element bytes: 1 (uint8 / bool) or 4 (int32) */
+    void* planes;
+    uint8_t* source_mask; /* [L][2][H][W] bool */
+    int32_t mask_form;    /* 0 rows [L][2][H][W][78], 1 packed uint32 [L][2][H][W][3] */
+    int32_t mask_bytes;   /* rows element bytes: 1 or 4 */
+    void* action_mask;
+} nanorts_gridnet_obs;
+
+/* GridNet step outputs (src/nanorts/adapters/gridnet/env.py:30-58).  Any
+ * pointer may be NULL. */
+typedef struct nanorts_gridnet_results {
+    float* reward_components; /* [L][2][6] */
+    uint8_t* reward_dones;    /* [L][2][6] bool */
+    uint8_t* terminated;      /* [L] */
+    uint8_t* truncated;       /* [L] */
+    uint8_t* done;            /* [L] */
+    int32_t* winner;          /* [L] */
+    uint8_t* spawn_overflowed;/* [L] */
+    void* final_planes;       /* planes of the ending state, in observation's planes form */
+    nanorts_gridnet_obs observation; /* of the post-reset state */
+} nanorts_gridnet_results;
+
 const char* nanorts_build_id(void);
 const char* nanorts_targets(void);
 const char* nanorts_last_error(void);
@@ -287,6 +323,32 @@ int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state s
                          int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                          const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
                          int64_t env0, nanorts_rollout_results results);
+
+/* GridNet decode_actions: per-cell actions int32[L][2][H][W][7] -> Commands.
+ * Replaces the FFI target nanorts_gridnet_decode
+ * (src/nanorts/adapters/gridnet/cuda/decode.cu, called from
+ * src/nanorts/adapters/gridnet/actions.py:199-232); the legality words the
+ * reference passes in are derived in the kernel. */
+int nanorts_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, nanorts_command_buffers commands);
+
+/* GridNet observe: planes, source mask and action mask of the state
+ * (src/nanorts/adapters/gridnet/observation.py:27-72). */
+int nanorts_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            nanorts_gridnet_obs obs);
+
+/* GridNet step in one launch: decode, core.step keyed by the episode root,
+ * reward components and reward dones, the ending state's planes, auto-reset
+ * and the observation (src/nanorts/adapters/gridnet/env.py:65-118). */
+int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                         const int32_t* actions, nanorts_gridnet_results results);
+
+/* GridNet step_against: player 0 decoded from its per-cell actions
+ * int32[L][H][W][7], player 1 plays `commands` ([L][2][C] per field; player
+ * 0's rows are ignored), then as nanorts_gridnet_step
+ * (src/nanorts/adapters/gridnet/env.py:73-83). */
+int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                                 const int32_t* actions, nanorts_commands commands, nanorts_gridnet_results results);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
 SOURCES = (PACKAGE / "csrc" / "nanorts_amd.hip", PACKAGE / "csrc" / "engine.h", PACKAGE / "csrc" / "envstep.h", PACKAGE / "csrc" / "rollout.h",
-           PACKAGE / "csrc" / "bots.h",
+           PACKAGE / "csrc" / "bots.h", PACKAGE / "csrc" / "gridnet.h",
            ROOT / "include" / "nanorts_amd.h")
 OUTPUT = PACKAGE / "_lib" / "libnanorts_amd.so"
 ARCH = "gfx950"

@@ -13,6 +13,7 @@
 #include "engine.h"
 #include "rollout.h"
 #include "bots.h"
+#include "gridnet.h"
 
 using namespace nr;
 
@@ -271,6 +272,36 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
         g.seg[k].bytes = rows[k].bytes;
     }
 
+    return fit_waves(out, why);
+}
+
+// GridNet decode scratch (gridnet.h) in the env block's phase union, after
+// the command arrays the decode fills.
+bool shape_for_gridnet(const nanorts_game* game, Shape* out, GridLayout* gy, std::string* why) {
+    if (!shape_for(game, out, why)) return false;
+    KGame& g = out->g;
+    if (g.T != 7 || g.O != 49) {
+        *why = "the GridNet surface is pinned to 7 unit types and a 49-cell attack window";
+        return false;
+    }
+    const int32_t C = g.C, words = (g.cells + 2 * g.W + 1 + 31) / 32;
+    std::memset(gy, 0, sizeof(*gy));
+    int32_t o = 0;
+    auto take = [&o](int32_t bytes) {
+        const int32_t at = o;
+        o += align16(bytes);
+        return at;
+    };
+    gy->order = take(2 * C);
+    gy->list = take(2 * C);
+    gy->pos = take(2 * C);
+    gy->cost = take(4 * C);
+    gy->kept = take(C);
+    gy->base = take(4 * words);
+    gy->used = take(4 * words);
+    gy->bytes = align16(o);
+    gy->origin = g.lay.c_rank + align16(4 * C);
+    if (gy->origin + gy->bytes > g.lay.env_bytes) g.lay.env_bytes = gy->origin + gy->bytes;
     return fit_waves(out, why);
 }
 
@@ -1069,6 +1100,100 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
     store_env(g, args.s, l, e, lane);
 }
 
+// GridNet decode_actions (N/adapters/gridnet/actions.py:31-52) into Commands.
+__global__ __launch_bounds__(256) void k_gridnet_decode(KGame g, int64_t lanes, nanorts_state s, GridLayout gy,
+                                                        const int32_t* actions, nanorts_command_buffers out) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    const int32_t owned = 2 * g.C;
+    gridnet_decode(g, hdr, e, gy, actions + l * 2 * g.cells * 7, 2, lane,
+                   [&](int32_t p, int32_t kind, int32_t dir, int32_t none, int32_t target, int32_t ptype, int32_t order) {
+                       const int64_t at = l * owned + p;
+                       out.kind[at] = kind;
+                       out.direction[at] = dir;
+                       out.none_duration[at] = none;
+                       out.target_cell[at] = target;
+                       out.produced_type[at] = ptype;
+                       out.request_order[at] = order;
+                   });
+}
+
+// GridNet observe (N/adapters/gridnet/observation.py:27-72).
+__global__ __launch_bounds__(256) void k_gridnet_observe(KGame g, int64_t lanes, nanorts_state s, nanorts_gridnet_obs o) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    gridnet_observe(g, hdr, e, l, lane, o, o.planes);
+}
+
+// GridNet step (N/adapters/gridnet/env.py:65-118): decode, core.step keyed by
+// the episode root, reward components and dones, the ending state's planes,
+// auto-reset and the observation of the post-reset state.  With `against`,
+// step_against (env.py:73-83): player 0's rows are decoded from `actions`
+// ([L][H][W][7]) and player 1 plays the given Commands.
+__global__ __launch_bounds__(256) void k_gridnet_step(KGame g, int64_t lanes, nanorts_state s, GridLayout gy,
+                                                      const int32_t* actions, nanorts_commands given, int32_t against,
+                                                      nanorts_gridnet_results r) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
+    uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
+    fold_in(k0, k1, (uint32_t)uni(e.sc[S_EPISODE]));
+    const Layout& y = g.lay;
+    const int32_t top = (1 << g.rank_bits) - 1;
+    const int32_t players = against ? 1 : 2;
+    gridnet_decode(g, hdr, e, gy, actions + l * players * g.cells * 7, players, lane,
+                   [&](int32_t p, int32_t kind, int32_t dir, int32_t none, int32_t target, int32_t ptype, int32_t order) {
+                       at<int8_t>(e, y.c_kind)[p] = (int8_t)canon_kind(kind);
+                       at<int8_t>(e, y.c_dir)[p] = (int8_t)canon_dir(dir);
+                       at<int32_t>(e, y.c_none)[p] = none;
+                       at<int16_t>(e, y.c_target)[p] = (int16_t)canon_target(target, g.cells);
+                       at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(ptype, g.T);
+                       at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(order == kAbsent ? 0 : order, 0, top);
+                   });
+    if (against) {
+        for (int32_t p = g.C + lane; p < 2 * g.C; p += kWave) {
+            const int64_t i = l * 2 * g.C + p;
+            at<int8_t>(e, y.c_kind)[p] = (int8_t)canon_kind(given.kind[i]);
+            at<int8_t>(e, y.c_dir)[p] = (int8_t)canon_dir(given.direction[i]);
+            at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(given.produced_type[i], g.T);
+            at<int16_t>(e, y.c_target)[p] = (int16_t)canon_target(given.target_cell[i], g.cells);
+            at<int32_t>(e, y.c_none)[p] = given.none_duration[i];
+            const int32_t ro = given.request_order[i];
+            at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(ro == kAbsent ? 0 : ro, 0, top);
+        }
+    }
+    wave_sync();
+    core_step(g, hdr, e, lane, k0, k1, true);
+    // reward dones (N/adapters/rewards.py:30-44): column 0 done, column 1
+    // no resource pile left carrying resources
+    const bool over = uni(e.sc[S_GAME_OVER]) != 0;
+    const bool done = over || uni(e.sc[S_TIME]) >= g.max_cycles;
+    bool stacked = false;
+    for (int32_t sl = lane; sl < g.E; sl += kWave)
+        stacked |= e.birth[sl] != kAbsent && type_flag(g, hdr, e.utype[sl], FL_RESOURCE) && e.carried[sl] > 0;
+    stacked = ballot(stacked) != 0ull;
+    if (r.reward_dones && lane < 12) {
+        const int32_t c = lane % 6;
+        r.reward_dones[l * 12 + lane] = (c == 0 && done) || (c == 1 && !stacked) ? 1 : 0;
+    }
+    if (r.final_planes) {
+        nanorts_gridnet_obs planes_only = r.observation;
+        planes_only.source_mask = nullptr;
+        planes_only.action_mask = nullptr;
+        gridnet_observe(g, hdr, e, l, lane, planes_only, r.final_planes);
+    }
+    nanorts_env_results er = {};
+    er.terminated = r.terminated;
+    er.truncated = r.truncated;
+    er.done = r.done;
+    er.winner = r.winner;
+    er.spawn_overflowed = r.spawn_overflowed;
+    er.reward_components = r.reward_components;
+    finish_step(g, hdr, e, l, lane, false, er, true);
+    store_env(g, s, l, e, lane);
+    gridnet_observe(g, hdr, e, l, lane, r.observation, r.observation.planes);
+}
+
 // Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
 __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_state s, int32_t partial, const uint8_t* tiles, uint8_t* image,
                          int32_t* scalars) {
@@ -1251,7 +1376,8 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout";
+           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
+           "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against";
 }
 
 const char* nanorts_last_error(void) { return g_error.c_str(); }
@@ -1513,6 +1639,77 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
             return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
     }
     return NANORTS_OK;
+}
+
+static bool gridnet_obs_valid(const nanorts_gridnet_obs& o, std::string* why) {
+    if (o.planes && !(o.planes_form == 1 || (o.planes_form == 0 && (o.planes_bytes == 1 || o.planes_bytes == 4)))) {
+        *why = "planes_form must be 0 (one-hot, 1 or 4 bytes) or 1 (indices)";
+        return false;
+    }
+    if (o.action_mask && !(o.mask_form == 1 || (o.mask_form == 0 && (o.mask_bytes == 1 || o.mask_bytes == 4)))) {
+        *why = "mask_form must be 0 (rows, 1 or 4 bytes) or 1 (packed words)";
+        return false;
+    }
+    return true;
+}
+
+int nanorts_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, nanorts_command_buffers commands) {
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!commands.kind || !commands.direction || !commands.none_duration || !commands.target_cell ||
+        !commands.produced_type || !commands.request_order)
+        return fail(NANORTS_INVALID_ARGUMENT, "a Commands buffer pointer is NULL");
+    Shape sh;
+    GridLayout gy;
+    std::string why;
+    if (!shape_for_gridnet(game, &sh, &gy, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
+    return launch(k_gridnet_decode, sh, lanes, (hipStream_t)stream, state, gy, actions, commands);
+}
+
+int nanorts_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            nanorts_gridnet_obs obs) {
+    NR_STATE(state)
+    Shape sh;
+    GridLayout gy;
+    std::string why;
+    if (!shape_for_gridnet(game, &sh, &gy, &why) || !gridnet_obs_valid(obs, &why))
+        return fail(NANORTS_INVALID_ARGUMENT, why);
+    return launch(k_gridnet_observe, sh, lanes, (hipStream_t)stream, state, obs);
+}
+
+int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                         const int32_t* actions, nanorts_gridnet_results results) {
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "the GridNet step needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    Shape sh;
+    GridLayout gy;
+    std::string why;
+    if (!shape_for_gridnet(game, &sh, &gy, &why) || !gridnet_obs_valid(results.observation, &why))
+        return fail(NANORTS_INVALID_ARGUMENT, why);
+    const nanorts_commands none = {};
+    return launch(k_gridnet_step, sh, lanes, (hipStream_t)stream, state, gy, actions, none, 0, results);
+}
+
+int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                                 const int32_t* actions, nanorts_commands commands, nanorts_gridnet_results results) {
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!commands.kind || !commands.direction || !commands.none_duration || !commands.target_cell ||
+        !commands.produced_type || !commands.request_order)
+        return fail(NANORTS_INVALID_ARGUMENT, "a Commands operand is NULL");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "the GridNet step needs environment_root and episode_index");
+    if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
+    Shape sh;
+    GridLayout gy;
+    std::string why;
+    if (!shape_for_gridnet(game, &sh, &gy, &why) || !gridnet_obs_valid(results.observation, &why))
+        return fail(NANORTS_INVALID_ARGUMENT, why);
+    return launch(k_gridnet_step, sh, lanes, (hipStream_t)stream, state, gy, actions, commands, 1, results);
 }
 
 int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,

@@ -146,7 +146,9 @@ class DeviceGame:
         self.game = game
         self.device = device
         self.terrain = torch.as_tensor(game.terrain.reshape(-1).astype(np.uint8), device=device)
-        self.initial = {leaf.name: torch.as_tensor(np.ascontiguousarray(game.initial_state[leaf.name])[None].copy(),
+        # np.array keeps 0-d leaves 0-d (ascontiguousarray would make them
+        # 1-d), so a batch of L envs has scalar leaves of shape [L]
+        self.initial = {leaf.name: torch.as_tensor(np.array(game.initial_state[leaf.name], order="C")[None],
                                                    device=device) for leaf in STATE_LEAVES}
         cols = game.columns
         g = native.Game()

@@ -75,12 +75,25 @@ class AbstractActions(ctypes.Structure):
     _fields_ = [(name, _VP) for name in ABSTRACT_FIELDS]
 
 
+class GridNetObs(ctypes.Structure):
+    _fields_ = [("planes_form", ctypes.c_int32), ("planes_bytes", ctypes.c_int32), ("planes", _VP),
+                ("source_mask", _VP), ("mask_form", ctypes.c_int32), ("mask_bytes", ctypes.c_int32),
+                ("action_mask", _VP)]
+
+
+class GridNetResults(ctypes.Structure):
+    _fields_ = [(name, _VP) for name in
+                ("reward_components", "reward_dones", "terminated", "truncated", "done", "winner",
+                 "spawn_overflowed", "final_planes")] + [("observation", GridNetObs)]
+
+
 # Every extern "C" symbol include/nanorts_amd.h declares.
 EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
+    "nanorts_gridnet_decode", "nanorts_gridnet_observe", "nanorts_gridnet_step", "nanorts_gridnet_step_against",
 )
 
 _I64 = ctypes.c_int64
@@ -110,6 +123,11 @@ _SIGNATURES = {
                                          EnvResults]),
     "nanorts_seat_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32, _I32,
                                             _I32, _I64, RolloutResults]),
+    # the command buffers have the layout of Commands (six int32 pointers)
+    "nanorts_gridnet_decode": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands]),
+    "nanorts_gridnet_observe": (ctypes.c_int, [_VP, _GP, State, _I64, GridNetObs]),
+    "nanorts_gridnet_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, GridNetResults]),
+    "nanorts_gridnet_step_against": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, GridNetResults]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None

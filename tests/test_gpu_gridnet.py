@@ -1,0 +1,283 @@
+"""GPU parity of the GridNet surface against the C oracle and closed forms.
+
+decode_actions is compared bit for bit with the oracle's GridNet decode on
+mid-game states under per-cell actions that collide (legal rows at unit
+cells, random in-range rows elsewhere, and wild out-of-range values).  The
+observation is compared with its closed form: the one-hot (or index) of the
+oracle's full-observation feature maps clipped to the plane widths, the
+source mask of available own units, and the oracle's legality row at every
+source cell.  Whole GridNet steps (and step_against a given player 1) are
+compared cycle by cycle with the oracle's decode -> core.step keyed by the
+episode root, the reward components and reward dones restated from the
+step's events and ending state, the ending state's planes, auto-reset and
+the next observation.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+from nanorts_amd.model import (TYPE_BARRACKS, TYPE_BASE, TYPE_HEAVY, TYPE_LIGHT, TYPE_RANGED, TYPE_WORKER)
+from oracle.oracle import copy_state, load_library
+from tests.helpers import advanced_states, assert_states_equal, game_for, to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+SIZES = (6, 4, 4, 4, 4, 7, 49)
+WIDTHS = np.asarray((5, 5, 3, 8, 6, 2))
+OFFSETS = np.asarray((0, 5, 10, 13, 21, 27))
+FIELDS = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+
+
+def _say(*parts):
+    print(*parts, flush=True)
+    sys.stdout.flush()
+
+
+def _per_cell_actions(game, oracle, st, seed: int, wild: bool = False) -> np.ndarray:
+    """[L][2][cells][7]: random in-range rows everywhere (wild: any values),
+    and at 70% of the unit cells the unit's uniform-legal JaxMARL row."""
+    b = game.bucket
+    L, N, C, cells = st["time"].shape[0], b.neutral_capacity, b.per_player_capacity, b.cell_count
+    rng = np.random.default_rng(seed)
+    if wild:
+        acts = rng.integers(-70, 70, size=(L, 2, cells, 7), dtype=np.int32)
+    else:
+        acts = np.stack([rng.integers(0, s, size=(L, 2, cells), dtype=np.int32) for s in SIZES], -1)
+    legal = oracle.sample_actions(oracle.avail_rows(st), (seed, seed + 3), 0)
+    keep = rng.random((L, 2, C)) < 0.7
+    for l in range(L):
+        for p in range(2):
+            for i in range(C):
+                s = N + p * C + i
+                if st["birth"][l, s] != -1 and keep[l, p, i]:
+                    acts[l, p, st["cell"][l, s]] = legal[l, p, i]
+    return acts
+
+
+def _episode_roots(st) -> np.ndarray:
+    lib = load_library()
+    roots = st["environment_root"].reshape(-1, 2)
+    out = np.zeros_like(roots, dtype=np.uint32)
+    for l in range(roots.shape[0]):
+        k = (ctypes.c_uint32 * 2)(int(roots[l, 0]), int(roots[l, 1]))
+        o = (ctypes.c_uint32 * 2)()
+        lib.nro_fold_in(k, ctypes.c_uint32(int(st["episode_index"][l])), o)
+        out[l] = (o[0], o[1])
+    return out
+
+
+def _want_planes(oracle, st, form: str) -> np.ndarray:
+    maps = oracle.symbolic(st, False)[0].astype(np.int64)  # [L][2][H][W][6]
+    clipped = np.minimum(maps, WIDTHS - 1)
+    if form == "indices":
+        return clipped.astype(np.int8)
+    hot = np.zeros(maps.shape[:-1] + (29,), np.int64)
+    for f in range(6):
+        np.put_along_axis(hot, (OFFSETS[f] + clipped[..., f])[..., None], 1, axis=-1)
+    return hot
+
+
+def _want_masks(game, oracle, st) -> tuple[np.ndarray, np.ndarray]:
+    b = game.bucket
+    L, N, C, H, W = st["time"].shape[0], b.neutral_capacity, b.per_player_capacity, b.height, b.width
+    slot = st["entity_at"].reshape(L, H * W).astype(np.int64)
+    occupied = slot >= 0
+    s = np.clip(slot, 0, b.entity_capacity - 1)
+    owner = np.where(occupied, np.take_along_axis(st["owner"].astype(np.int64), s, 1), -1)
+    pending = np.take_along_axis(st["pending_kind"].astype(np.int64), s, 1)
+    available = occupied & (owner >= 0) & (pending == -1)
+    source = np.stack([available & (owner == p) for p in range(2)], 1)  # [L][2][cells]
+    rows = oracle.legality_rows(st).reshape(L, 2 * C, 78)
+    index = np.clip(slot - N, 0, 2 * C - 1)
+    at = np.take_along_axis(rows, index[..., None], 1)  # [L][cells][78]
+    mask = source[..., None] & at[:, None]
+    return source.reshape(L, 2, H, W), mask.reshape(L, 2, H, W, 78)
+
+
+def _pack(mask: np.ndarray) -> np.ndarray:
+    bits = mask.astype(np.uint64)
+    words = np.zeros(mask.shape[:-1] + (3,), np.uint64)
+    for lo, hi, w in ((0, 29, 0), (29, 61, 1), (61, 78, 2)):
+        words[..., w] = (bits[..., lo:hi] << np.arange(hi - lo, dtype=np.uint64)).sum(-1)
+    return words.astype(np.uint32)
+
+
+def _want_rewards(game, oracle_step_out, nxt, done) -> tuple[np.ndarray, np.ndarray]:
+    """encode_rewards (src/nanorts/adapters/rewards.py:30-71) from the step's
+    events and ending state."""
+    L = done.shape[0]
+    h, r = oracle_step_out["admitted_harvest"], oracle_step_out["admitted_return"]
+    prod, att = oracle_step_out["admitted_produce"], oracle_step_out["admitted_attack"]
+    comps = np.zeros((L, 2, 6), np.float32)
+    for p in range(2):
+        o = 1 - p
+        over = nxt["game_over"].astype(bool)
+        comps[:, p, 0] = np.where(over, np.where(nxt["winner"] == p, 1.0, -1.0), 0.0)
+        comps[:, p, 1] = h[:, p] + r[:, p]
+        comps[:, p, 2] = prod[:, p, TYPE_WORKER]
+        comps[:, p, 3] = prod[:, p, TYPE_BASE] + prod[:, p, TYPE_BARRACKS]
+        comps[:, p, 4] = att[:, p, o + 1] - att[:, p, p + 1]
+        comps[:, p, 5] = prod[:, p, TYPE_LIGHT] + prod[:, p, TYPE_HEAVY] + prod[:, p, TYPE_RANGED]
+    is_resource = np.asarray(game.columns["is_resource"]).astype(bool)
+    types = np.clip(nxt["unit_type"].astype(np.int64), 0, game.bucket.unit_type_capacity - 1)
+    stacked = ((nxt["birth"] != -1) & is_resource[types] & (nxt["carried_resources"] > 0)).any(1)
+    dones = np.zeros((L, 2, 6), bool)
+    dones[:, :, 0] = done[:, None]
+    dones[:, :, 1] = ~stacked[:, None]
+    return comps, dones
+
+
+def _surface(game, **kw):
+    import torch
+
+    from nanorts_amd import gridnet
+
+    torch.cuda.set_device(0)
+    return gridnet.GridNet(game, gridnet.prepare(game, **kw), device="cuda:0")
+
+
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "8x8-original-both", "barracks-random", "gow-alternating"])
+@pytest.mark.parametrize("wild", [False, True])
+def test_decode_matches_oracle(case, wild, oracle_threads):
+    import torch
+
+    _say(f"gridnet decode {case} wild={wild}")
+    game, partial = game_for(case)
+    L = 16 if case == "gow-alternating" else 96
+    oracle, st = advanced_states(game, L, 150, partial, oracle_threads, seed=23)
+    acts = _per_cell_actions(game, oracle, st, 5, wild)
+    want = oracle.gridnet_decode(st, acts)
+    g = _surface(game)
+    b = game.bucket
+    got = g.decode_actions(torch.as_tensor(acts.reshape(L, 2, b.height, b.width, 7), device="cuda:0"),
+                           to_device(g, st))
+    for f in FIELDS:
+        np.testing.assert_array_equal(got[f].cpu().numpy(), want[f], err_msg=f"{case}: {f}")
+
+
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random", "melee-both"])
+@pytest.mark.parametrize("form", [("one_hot", "int32", "rows", "int32"), ("one_hot", "uint8", "rows", "bool"),
+                                  ("one_hot", "bool", "packed", "int32"), ("indices", "int32", "rows", "uint8")])
+def test_observe_matches_closed_form(case, form, oracle_threads):
+    import torch
+
+    from nanorts_amd import gridnet
+
+    _say(f"gridnet observe {case} {form}")
+    planes_form, planes_dtype, mask_form, mask_dtype = form
+    game, partial = game_for(case)
+    oracle, st = advanced_states(game, 64, 120, partial, oracle_threads, seed=29)
+    g = _surface(game, planes_form=planes_form, planes_dtype=getattr(torch, planes_dtype), mask_form=mask_form,
+                 mask_dtype=getattr(torch, mask_dtype))
+    obs = g.observe(to_device(g, st))
+    want_planes = _want_planes(oracle, st, planes_form)
+    got_planes = obs.planes.cpu().numpy()
+    assert got_planes.dtype == (np.int8 if planes_form == "indices" else np.dtype(planes_dtype))
+    np.testing.assert_array_equal(got_planes.astype(np.int64).reshape(want_planes.shape), want_planes)
+    source, mask = _want_masks(game, oracle, st)
+    np.testing.assert_array_equal(obs.source_mask.cpu().numpy(), source)
+    if mask_form == "packed":
+        np.testing.assert_array_equal(obs.action_mask.cpu().numpy().view(np.uint32), _pack(mask))
+    else:
+        np.testing.assert_array_equal(obs.action_mask.cpu().numpy().astype(bool), mask)
+    np.testing.assert_array_equal(gridnet.unpack_mask(obs.action_mask, layout=g.layout).cpu().numpy(), mask)
+    np.testing.assert_array_equal(g.planes(to_device(g, st)).cpu().numpy(), got_planes)
+
+
+def _check_step(game, oracle, g, st, out, acts_cells, against=None):
+    """One oracle GridNet step on `st` (in place) checked against the kernel's `out`."""
+    b = game.bucket
+    L = st["time"].shape[0]
+    if against is None:
+        cmds = oracle.gridnet_decode(st, acts_cells)
+    else:
+        both = np.zeros((L, 2, b.cell_count, 7), np.int32)
+        both[:, 0] = acts_cells
+        cmds = oracle.gridnet_decode(st, both)
+        for f in FIELDS:
+            cmds[f][:, 1] = against[f][:, 1]
+    step = oracle.core_step(st, cmds, _episode_roots(st))
+    done = (step["terminated"] | step["truncated"]).astype(bool)
+    comps, rdones = _want_rewards(game, step, st, done)
+    np.testing.assert_array_equal(out.reward_components.cpu().numpy(), comps)
+    np.testing.assert_array_equal(out.reward_dones.cpu().numpy(), rdones)
+    np.testing.assert_array_equal(out.terminated.cpu().numpy(), step["terminated"].astype(bool))
+    np.testing.assert_array_equal(out.truncated.cpu().numpy(), step["truncated"].astype(bool))
+    np.testing.assert_array_equal(out.done.cpu().numpy(), done)
+    np.testing.assert_array_equal(out.winner.cpu().numpy(), st["winner"])
+    np.testing.assert_array_equal(out.spawn_overflowed.cpu().numpy(), (st["spawn_overflow"] > 0).any(1))
+    want_final = _want_planes(oracle, st, g.layout.planes_form)
+    np.testing.assert_array_equal(out.final_observation.cpu().numpy().astype(np.int64).reshape(want_final.shape),
+                                  want_final)
+    oracle.reset_where_done(st, done.astype(np.uint8))
+    assert_states_equal(st, to_host(out.environment_state))
+    want_planes = _want_planes(oracle, st, g.layout.planes_form)
+    np.testing.assert_array_equal(out.observation.planes.cpu().numpy().astype(np.int64).reshape(want_planes.shape),
+                                  want_planes)
+    source, mask = _want_masks(game, oracle, st)
+    np.testing.assert_array_equal(out.observation.source_mask.cpu().numpy(), source)
+    np.testing.assert_array_equal(out.observation.action_mask.cpu().numpy().astype(bool), mask)
+    return done
+
+
+@pytest.mark.parametrize("case", ["16x16-alternating", "barracks-random", "8x8-original-both"])
+def test_steps_match_oracle(case, oracle_threads):
+    import torch
+
+    _say(f"gridnet step {case}")
+    game, partial = game_for(case)
+    b = game.bucket
+    L = 48
+    # near the time limit for the short cases, so episodes end and reset
+    advance = {"16x16-alternating": 280, "barracks-random": 130, "8x8-original-both": 200}[case]
+    oracle, st = advanced_states(game, L, advance, partial, oracle_threads, seed=31)
+    g = _surface(game)
+    state = to_device(g, st)
+    ended = 0
+    for t in range(30):
+        acts = _per_cell_actions(game, oracle, st, 100 + t)
+        out = g.step(state, torch.as_tensor(acts.reshape(L, 2, b.height, b.width, 7), device="cuda:0"), donate=True)
+        ended += int(_check_step(game, oracle, g, st, out, acts).sum())
+        state = out.environment_state
+    if case != "8x8-original-both":
+        assert ended > 0
+
+
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random"])
+def test_step_against_matches_oracle(case, oracle_threads):
+    import torch
+
+    _say(f"gridnet step_against {case}")
+    game, partial = game_for(case)
+    b = game.bucket
+    L = 48
+    oracle, st = advanced_states(game, L, 120, partial, oracle_threads, seed=37)
+    g = _surface(game)
+    state = to_device(g, st)
+    for t in range(20):
+        acts = _per_cell_actions(game, oracle, st, 200 + t)[:, 0]
+        given = oracle.decode_actions(st, oracle.sample_actions(oracle.avail_rows(st), (7, 9), t))
+        gt = {f: torch.as_tensor(given[f], device="cuda:0") for f in FIELDS}
+        out = g.step_against(state, torch.as_tensor(acts.reshape(L, b.height, b.width, 7), device="cuda:0"), gt,
+                             donate=True)
+        _check_step(game, oracle, g, st, out, acts, against=given)
+        state = out.environment_state
+
+
+def test_reset_observes_the_initial_state(oracle_threads):
+    from nanorts_amd import gridnet  # noqa: F401
+
+    _say("gridnet reset")
+    game, _ = game_for("16x16-finetuned-both")
+    oracle, st = advanced_states(game, 8, 0, False, oracle_threads, seed=41)
+    g = _surface(game)
+    state, obs = g.reset(st["environment_root"])
+    got = to_host(state)
+    for name, want in st.items():
+        assert got[name].shape == want.shape, name
+    assert_states_equal(copy_state(st), got)
+    np.testing.assert_array_equal(obs.planes.cpu().numpy(), _want_planes(oracle, st, "one_hot"))

@@ -58,6 +58,12 @@ def test_two_claims_on_one_cell_by_hand():
     actions[0, 0, 1] = [NONE, 0, 0, 0, 0, 0, 0]
     c = o.gridnet_decode(st, actions)
     assert pick(0, 0) == (PRODUCE, UP, 0, -1, WORKER, 1) and pick(0, 1) == (NONE, -1, -1, -1, -1, 0)
+    # an ABSENT kind (-1) claims nothing and survives the filter, so it takes
+    # rank 0 in cell order; it submitted no command, so the worker still waits
+    # as an idle filler ranked after both survivors (actions.py:139-164)
+    actions[0, 0, 1] = [-1, 0, 0, 0, 0, 0, 0]
+    c = o.gridnet_decode(st, actions)
+    assert pick(0, 0) == (PRODUCE, UP, 0, -1, WORKER, 1) and pick(0, 1) == (NONE, -1, 1, -1, -1, 2)
     del C
 
 
