@@ -15,6 +15,12 @@ CANCEL_BOTH, max_cycles 3000, 32768 games, player_1 = WorkerRush or LightRush
 on the device, player_0 = seeded uniform-random legal actions, full episodes
 with auto-reset (the fused seat rollout kernel).
 
+`--workload gridnet` measures the GridNet surface: basesWorkers16x16,
+VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, 32768 games, one-hot int32 planes
+and the packed action mask; per cycle the harness sampler draws every
+source cell's row from the last observation's mask and one GridNet step
+launch decodes, steps, rewards, resets and observes.
+
 Prints one JSON line (rank 0, N=1).
 """
 from __future__ import annotations
@@ -36,12 +42,14 @@ MAP = "basesWorkers16x16"
 NUM_ENVS = 65536
 METRIC = "env-steps/sec (both players) at 16x16 × 65536 envs; % HBM roofline"
 SEAT_ENVS = 32768
+GRID_ENVS = 32768
 
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush"), default="headline")
+    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush", "gridnet"),
+                    default="headline")
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--envs", type=int, default=None)
@@ -55,7 +63,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--profile-child", choices=("rollout", "copy"), default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.envs is None:
-        args.envs = NUM_ENVS if args.workload == "headline" else SEAT_ENVS
+        args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS}.get(args.workload, SEAT_ENVS)
     return args
 
 
@@ -314,6 +322,147 @@ def main_seat(args) -> None:
     print(json.dumps(line))
 
 
+def gridnet_step_bytes(bucket) -> int:
+    """Algorithmic HBM bytes of one GridNet step of one env: the state read
+    and written, both players' per-cell actions, the ending state's planes and
+    the next observation (one-hot int32 planes, the source mask, the packed
+    action mask), the reward components and reward dones, and the four flags
+    and the winner."""
+    cells = bucket.cell_count
+    planes = 2 * cells * 29 * 4
+    return 2 * state_bytes(bucket) + 2 * cells * 7 * 4 + 2 * planes + 2 * cells + 2 * cells * 3 * 4 + 48 + 12 + 4 + 4
+
+
+def cpu_gridnet_baseline(envs: int, steps: int) -> dict:
+    """The oracle's GridNet cycle on one host thread over a bounded sample:
+    masks and planes from the oracle's legality rows and symbolic maps, the
+    harness sampler, decode, core.step keyed by the episode root, rewards,
+    auto-reset."""
+    import ctypes
+
+    import numpy as np
+
+    from nanorts_amd import env as envmod
+    from nanorts_amd.content import map_name_to_scenario
+    from oracle.oracle import Oracle, batch_initial, load_library
+
+    game = map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM")
+    b = game.bucket
+    oracle = Oracle(game)
+    lib = load_library()
+    L, N, C, H, W = envs, b.neutral_capacity, b.per_player_capacity, b.height, b.width
+    state = batch_initial(game, L, envmod.env_roots(0, L))
+    widths, offsets = np.asarray((5, 5, 3, 8, 6, 2)), np.asarray((0, 5, 10, 13, 21, 27))
+
+    def observe(st):
+        maps = np.minimum(oracle.symbolic(st, False)[0].astype(np.int64), widths - 1)
+        planes = np.zeros(maps.shape[:-1] + (29,), np.int32)
+        for f in range(6):
+            np.put_along_axis(planes, (offsets[f] + maps[..., f])[..., None], 1, axis=-1)
+        slot = st["entity_at"].reshape(L, H * W).astype(np.int64)
+        s = np.clip(slot, 0, b.entity_capacity - 1)
+        owner = np.where(slot >= 0, np.take_along_axis(st["owner"].astype(np.int64), s, 1), -1)
+        pending = np.take_along_axis(st["pending_kind"].astype(np.int64), s, 1)
+        source = np.stack([(slot >= 0) & (owner == p) & (pending == -1) for p in range(2)], 1)
+        rows = oracle.legality_rows(st).reshape(L, 2 * C, 78)
+        at = np.take_along_axis(rows, np.clip(slot - N, 0, 2 * C - 1)[..., None], 1)
+        return planes, source, source[..., None] & at[:, None]
+
+    def episode_roots(st):
+        out = np.zeros((L, 2), np.uint32)
+        for l in range(L):
+            k = (ctypes.c_uint32 * 2)(*[int(v) for v in st["environment_root"][l]])
+            o = (ctypes.c_uint32 * 2)()
+            lib.nro_fold_in(k, ctypes.c_uint32(int(st["episode_index"][l])), o)
+            out[l] = (o[0], o[1])
+        return out
+
+    _, _, mask = observe(state)
+    t0 = time.perf_counter()
+    for t in range(steps):
+        acts = oracle.gridnet_sample_actions(mask, (11, 13), t)
+        cmds = oracle.gridnet_decode(state, acts)
+        out = oracle.core_step(state, cmds, episode_roots(state))
+        observe(state)  # the ending state's planes
+        oracle.reset_where_done(state, (out["terminated"] | out["truncated"]).astype(np.uint8))
+        _, _, mask = observe(state)
+    dt = time.perf_counter() - t0
+    return {"value": round(envs * steps / dt, 1), "unit": "env-steps/s", "cores": 1, "kind": "port",
+            "sample": f"{envs} games x {steps} cycles of the same workload (oracle: harness sampler, GridNet decode, "
+                      f"core.step, planes and masks of the ending and next states, auto-reset) on 1 host thread, "
+                      f"{dt:.1f} s"}
+
+
+def main_gridnet(args) -> None:
+    import torch
+
+    import nanorts_amd
+    from nanorts_amd import env as envmod
+    from nanorts_amd import gridnet
+
+    torch.cuda.set_device(0)
+    game = nanorts_amd.map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM")
+    g = gridnet.GridNet(game, gridnet.prepare(game, mask_form="packed"), device="cuda:0")
+    L = args.envs
+    state, obs = g.reset(envmod.env_roots(0, L))
+    mask = obs.action_mask
+
+    def run(steps, step0, events):
+        nonlocal state, mask
+        times = []
+        for t in range(steps):
+            acts = g.sample_actions(mask, (11, 13), step0 + t)
+            if events:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+            out = g.step(state, acts, donate=True)
+            if events:
+                b.record()
+                times.append((a, b))
+            state, mask = out.environment_state, out.observation.action_mask
+        return times
+
+    run(args.warmup, 0, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    times = run(args.steps, args.warmup, True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg_launch_s = sum(a.elapsed_time(b) for a, b in times) / len(times) / 1e3
+    b = game.bucket
+    per_step = gridnet_step_bytes(b)
+    achieved = L * per_step / avg_launch_s / 1e9
+    cpu = None if args.no_cpu else cpu_gridnet_baseline(args.cpu_envs // 16, args.cpu_steps // 30)
+    line = {
+        "metric": f"env-steps/sec (GridNet surface, both players) at 16x16 × {L} envs; % HBM roofline",
+        "value": round(L * args.steps / wall, 1),
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic: seeded uniform-random legal per-cell actions for both players, shipped basesWorkers16x16 "
+                "map",
+        "config": {
+            "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, GridNet surface (one-hot int32 planes, "
+                        f"packed action mask), {L} games, max_cycles 5000, auto-reset; per cycle one sampler launch "
+                        f"and one GridNet step launch",
+            "games": L, "algorithmic_bytes_per_env_step": per_step, "state_bytes_per_env": state_bytes(b),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_gridnet_step",
+            "avg_launch_ms": round(avg_launch_s * 1e3, 4), "algorithmic_bytes_per_launch": L * per_step,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
 def main() -> None:
     args = parse()
     if args.profile_child:
@@ -323,6 +472,9 @@ def main() -> None:
         print(f"bench.py measures one GPU: the env path shards by env with no exchange, and this run has no "
               f"multi-GPU configuration (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "gridnet":
+        main_gridnet(args)
+        return
     if args.workload != "headline":
         main_seat(args)
         return

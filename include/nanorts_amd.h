@@ -350,6 +350,15 @@ int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state s
 int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                                  const int32_t* actions, nanorts_commands commands, nanorts_gridnet_results results);
 
+/* The synthetic harness's integer uniform-over-legal sampler on the GridNet
+ * surface: per-cell actions int32[L][2][H][W][7] from the packed action mask
+ * uint32[L][2][H][W][3] (mask_form 1), each cell drawn as
+ * nanorts_sample_actions draws a row, at position player * H * W + cell.
+ * No reference counterpart (the reference's harness samples with
+ * jax.random.categorical). */
+int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
+                                   const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions);
+
 #ifdef __cplusplus
 }
 #endif

@@ -776,6 +776,35 @@ __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const ui
     }
 }
 
+// The harness sampler on the GridNet surface: each cell's row of the packed
+// action mask (bits 0-28, 29-60, 61-77 of the 78-bit row) drawn as k_sample
+// draws a row, at position player * cells + cell.  A cell without a source
+// (an all-zero row) comes out as zeros, which is what the draw gives it too.
+__global__ __launch_bounds__(256) void k_gridnet_sample(KGame g, int64_t lanes, const uint32_t* mask, uint32_t key0,
+                                                        uint32_t key1, int32_t step, int64_t env0, int32_t* actions) {
+    NR_KERNEL_PROLOGUE
+    (void)e;
+    uint32_t k0 = key0, k1 = key1;
+    fold_in(k0, k1, (uint32_t)step);
+    const uint32_t env = (uint32_t)(env0 + l);
+    const int32_t rows = 2 * g.cells;
+    for (int32_t p = lane; p < rows; p += kWave) {
+        const uint32_t* w = mask + (l * rows + p) * 3;
+        const uint32_t p0 = w[0], p1 = w[1], p2 = w[2];
+        int32_t a[7] = {0, 0, 0, 0, 0, 0, 0};
+        if ((p0 | p1 | p2) != 0u) {
+            Row r;
+            r.w[0] = p0 | (p1 << 29);
+            r.w[1] = (p1 >> 3) | (p2 << 29);
+            r.w[2] = p2 >> 3;
+            sample_row(g, r, k0, k1, env, p, a);
+        }
+        int32_t* out = actions + (l * rows + p) * 7;
+#pragma unroll
+        for (int f = 0; f < 7; ++f) out[f] = a[f];
+    }
+}
+
 // Fused rollout: the state stays staged in LDS across `steps` cycles.  With
 // the per-cycle summary (rollout.h) each cycle is: sample from the masks of
 // the summarised state -> decode -> core.step -> finish (reward, done,
@@ -1377,7 +1406,7 @@ const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
            "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
-           "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against";
+           "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against,nanorts_gridnet_sample_actions";
 }
 
 const char* nanorts_last_error(void) { return g_error.c_str(); }
@@ -1594,6 +1623,16 @@ int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes
     NR_SHAPE(game)
     if (!avail_words || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
     return launch(k_sample, sh, lanes, (hipStream_t)stream, avail_words, sample_key[0], sample_key[1], step, env0,
+                  actions);
+}
+
+int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
+                                   const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
+    NR_SHAPE(game)
+    if (!mask || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
+    if (sh.g.T != 7 || sh.g.O != 49)
+        return fail(NANORTS_INVALID_ARGUMENT, "the GridNet surface is pinned to 7 unit types and a 49-cell attack window");
+    return launch(k_gridnet_sample, sh, lanes, (hipStream_t)stream, mask, sample_key[0], sample_key[1], step, env0,
                   actions);
 }
 

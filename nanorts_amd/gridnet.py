@@ -12,6 +12,7 @@ ending state's planes, auto-reset and the next observation).
 """
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 from typing import Any, Final
 
@@ -232,6 +233,25 @@ class GridNet:
         native.check(self.lib.nanorts_gridnet_decode(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs),
                      "nanorts_gridnet_decode")
         return out
+
+    def sample_actions(self, action_mask: torch.Tensor, sample_key, step: int, env0: int = 0) -> torch.Tensor:
+        """The synthetic harness's integer uniform-over-legal sampler on the
+        packed action mask [L, 2, H, W, 3]: per-cell actions int32[L, 2, H, W, 7]
+        (cells without a source draw zeros)."""
+        if self.layout.mask_form != "packed":
+            raise ModelError("GridNet.sample_actions reads the packed action mask: prepare(..., mask_form='packed')")
+        mask = action_mask.contiguous()
+        L = mask.shape[0]
+        b = self.game.bucket
+        if tuple(mask.shape) != (L, *self.layout.mask_shape):
+            raise ModelError(f"the action mask has shape {tuple(mask.shape)}, expected {(L, *self.layout.mask_shape)}")
+        key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
+        actions = torch.empty((L, PLAYER_COUNT, b.height, b.width, len(ACTION_FACTORS)), dtype=torch.int32,
+                              device=self.device)
+        native.check(self.lib.nanorts_gridnet_sample_actions(_stream(), self.dev.ref, L, _ptr(mask), key, int(step),
+                                                             int(env0), _ptr(actions)),
+                     "nanorts_gridnet_sample_actions")
+        return actions
 
     def step(self, state: EnvironmentState, actions: torch.Tensor, *, donate: bool = False) -> GridNetStep:
         """env.step (src/nanorts/adapters/gridnet/env.py:65-70); with

@@ -94,6 +94,7 @@ EXPORTS = (
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
     "nanorts_gridnet_decode", "nanorts_gridnet_observe", "nanorts_gridnet_step", "nanorts_gridnet_step_against",
+    "nanorts_gridnet_sample_actions",
 )
 
 _I64 = ctypes.c_int64
@@ -128,6 +129,7 @@ _SIGNATURES = {
     "nanorts_gridnet_observe": (ctypes.c_int, [_VP, _GP, State, _I64, GridNetObs]),
     "nanorts_gridnet_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, GridNetResults]),
     "nanorts_gridnet_step_against": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, GridNetResults]),
+    "nanorts_gridnet_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None

@@ -1228,14 +1228,14 @@ static void factor_bounds(const nro_game* g, int32_t lo[7], int32_t width[7]) {
     }
 }
 
-static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sample_key[2], int32_t step,
-                       int64_t env, int32_t* actions) {
-    const int32_t C = g->capacity, width = row_width(g);
+static void sample_positions(const nro_game* g, const uint8_t* rows, int32_t positions, const uint32_t sample_key[2],
+                             int32_t step, int64_t env, int32_t* actions) {
+    const int32_t width = row_width(g);
     int32_t lo[7], wid[7];
     factor_bounds(g, lo, wid);
     uint32_t kt[2];
     nro_fold_in(sample_key, (uint32_t)step, kt);
-    for (int32_t p = 0; p < 2 * C; ++p) {
+    for (int32_t p = 0; p < positions; ++p) {
         const uint8_t* row = rows + (size_t)p * width;
         int32_t* out = actions + (size_t)p * 7;
         int only_none = row[0];
@@ -1269,6 +1269,20 @@ static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sa
             out[f] = value;
         }
     }
+}
+
+static void sample_env(const nro_game* g, const uint8_t* rows, const uint32_t sample_key[2], int32_t step,
+                       int64_t env, int32_t* actions) {
+    sample_positions(g, rows, 2 * g->capacity, sample_key, step, env, actions);
+}
+
+/* The same sampler over GridNet's per-cell rows [2][cells][78], at position
+   player * cells + cell. */
+void nro_gridnet_sample_actions(const nro_game* g, const uint8_t* rows, const uint32_t sample_key[2], int32_t step,
+                                int64_t env0, int64_t L, int32_t* actions) {
+    const int32_t n = 2 * g->cells, width = row_width(g);
+    for (int64_t l = 0; l < L; ++l)
+        sample_positions(g, rows + (size_t)l * n * width, n, sample_key, step, env0 + l, actions + (size_t)l * n * 7);
 }
 
 void nro_sample_actions(const nro_game* g, const uint8_t* rows, const uint32_t sample_key[2], int32_t step,

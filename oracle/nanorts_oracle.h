@@ -205,6 +205,11 @@ void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, in
 void nro_gridnet_decode(const nro_game* g, const nro_state* s, const int32_t* actions, int64_t L,
                         nro_commands* out);
 
+/* The harness sampler over GridNet's per-cell rows [L][2][H*W][78] at
+ * position player * H*W + cell -> actions [L][2][H*W][7]. */
+void nro_gridnet_sample_actions(const nro_game* g, const uint8_t* rows, const uint32_t sample_key[2], int32_t step,
+                                int64_t env0, int64_t L, int32_t* actions);
+
 /* Invariant check (src/nanorts/model/state.py:87-165); returns a bitmask of
  * violated invariants for env l, 0 when the state is well formed. */
 int32_t nro_state_violations(const nro_game* g, const nro_state* s, int64_t l);

@@ -317,6 +317,17 @@ class Oracle:
                                     ctypes.c_int64(L), ctypes.byref(c))
         return out
 
+    def gridnet_sample_actions(self, rows: np.ndarray, sample_key, step: int, env0: int = 0) -> np.ndarray:
+        """The harness sampler over per-cell rows [L][2][cells][78] -> actions [L][2][cells][7]."""
+        L = rows.shape[0]
+        cells = self.game.bucket.cell_count
+        rows = np.ascontiguousarray(rows.reshape(L, 2, cells, self.width), np.uint8)
+        key = np.ascontiguousarray(np.asarray(sample_key, np.uint32).reshape(2))
+        actions = np.zeros((L, 2, cells, 7), np.int32)
+        self.lib.nro_gridnet_sample_actions(ctypes.byref(self.g), _ptr(rows), _ptr(key), ctypes.c_int32(step),
+                                            ctypes.c_int64(env0), ctypes.c_int64(L), _ptr(actions))
+        return actions
+
     def violations(self, state) -> np.ndarray:
         L = state["time"].shape[0]
         s = self._s(state)

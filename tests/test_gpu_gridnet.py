@@ -268,6 +268,19 @@ def test_step_against_matches_oracle(case, oracle_threads):
         state = out.environment_state
 
 
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random"])
+def test_sampler_matches_oracle(case, oracle_threads):
+    _say(f"gridnet sampler {case}")
+    game, partial = game_for(case)
+    oracle, st = advanced_states(game, 64, 150, partial, oracle_threads, seed=47)
+    g = _surface(game, mask_form="packed")
+    obs = g.observe(to_device(g, st))
+    got = g.sample_actions(obs.action_mask, (21, 22), 9, env0=3).cpu().numpy()
+    _, mask = _want_masks(game, oracle, st)
+    want = oracle.gridnet_sample_actions(mask, (21, 22), 9, env0=3)
+    np.testing.assert_array_equal(got.reshape(want.shape), want)
+
+
 def test_reset_observes_the_initial_state(oracle_threads):
     from nanorts_amd import gridnet  # noqa: F401
 

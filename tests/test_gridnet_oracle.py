@@ -127,3 +127,41 @@ def test_kept_rows_decode_like_jaxmarl_and_keep_the_filter_invariants(case, orac
                 dropped_total += 1
             kept_total += len(kept_idx)
     assert kept_total > 100 and dropped_total > 0
+
+
+def test_gridnet_sampler_draws_legal_values_with_the_row_sampler_counters(oracle_threads):
+    """The harness sampler over per-cell rows: a drawn factor is a set bit of
+    its mask (0 for an empty factor), a cell with no row draws zeros, and the
+    draw at flattened position q equals the row sampler's draw at its
+    position q (same step key, counters (env, 2q) and (env, 2q + 1))."""
+    game, partial = game_for("16x16-finetuned-both")
+    oracle, st = advanced_states(game, 24, 200, partial, oracle_threads, seed=43)
+    b = game.bucket
+    L, N, C, cells = 24, b.neutral_capacity, b.per_player_capacity, b.cell_count
+    legal = oracle.legality_rows(st)
+    rows = np.zeros((L, 2, cells, 78), bool)
+    for l in range(L):
+        for p in range(2):
+            for i in range(C):
+                s = N + p * C + i
+                if st["birth"][l, s] != -1 and st["pending_kind"][l, s] == -1:
+                    rows[l, p, st["cell"][l, s]] = legal[l, p, i]
+    got = oracle.gridnet_sample_actions(rows, (3, 4), 7, env0=5)
+    lo = np.cumsum((0, 6, 4, 4, 4, 4, 7))
+    widths = (6, 4, 4, 4, 4, 7, 49)
+    drawn = 0
+    for l in range(L):
+        for p in range(2):
+            for c in range(cells):
+                r = rows[l, p, c]
+                if not r.any():
+                    assert (got[l, p, c] == 0).all()
+                    continue
+                drawn += 1
+                for f in range(7):
+                    m = r[lo[f]:lo[f] + widths[f]]
+                    assert (m[got[l, p, c, f]] if m.any() else got[l, p, c, f] == 0)
+    assert drawn > 20
+    flat = rows.reshape(L, 2 * cells, 78)[:, :2 * C].reshape(L, 2, C, 78)
+    want = oracle.sample_actions(flat, (3, 4), 7, env0=5)
+    np.testing.assert_array_equal(got.reshape(L, 2 * cells, 7)[:, :2 * C], want.reshape(L, 2 * C, 7))
