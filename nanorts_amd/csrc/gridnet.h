@@ -214,84 +214,172 @@ NR_DEV void gridnet_decode(const KGame& g, const Hdr& h, const Env& e, const Gri
     }
 }
 
+// Wave-cooperative writers for 64-cell chunks: lane i holds the words of
+// cell c0 + i, and element j of the chunk's contiguous run is written by lane
+// j % 64 after fetching its cell's words from lane j / width with a shuffle,
+// so each store instruction covers one contiguous span.  Every lane runs the
+// same iterations, which keeps the shuffles' source lanes active.
+NR_DEV uint32_t lane_word(uint32_t v, int32_t src) { return (uint32_t)__shfl((int)v, src, kWave); }
+
+// n rows of Width 0/1 elements: bit b of the cell's row is bit b of w0..w2.
+template <typename T, int Width, int Words>
+NR_DEV void put_bit_rows(T* dst, int32_t n, uint32_t w0, uint32_t w1, uint32_t w2, int lane) {
+    const int32_t total = n * Width;
+    for (int32_t j0 = 0; j0 < total; j0 += kWave) {
+        const int32_t j = j0 + lane;
+        const int32_t jj = j < total ? j : total - 1;
+        const int32_t cell = jj / Width, bit = jj - cell * Width;
+        uint32_t w = lane_word(w0, cell);
+        if (Words > 1) {
+            const uint32_t b = lane_word(w1, cell), c = lane_word(w2, cell);
+            w = bit < 32 ? w : (bit < 64 ? b : c);
+        }
+        if (j < total) dst[j] = (T)((w >> (bit & 31)) & 1u);
+    }
+}
+
+// The same rows, four elements per store: int32 elements as 16-byte stores,
+// bytes packed four to a dword.  A run whose start or length does not fit
+// the wider store takes the element path.
+template <int Width, int Words>
+NR_DEV uint32_t row_bit_of(int32_t bit, uint32_t a0, uint32_t a1, uint32_t a2) {
+    uint32_t w = a0;
+    if (Words > 1) w = bit < 32 ? a0 : (bit < 64 ? a1 : a2);
+    return (w >> (bit & 31)) & 1u;
+}
+
+template <typename T, int Width, int Words>
+NR_DEV void put_bit_rows4(T* dst, int32_t n, uint32_t w0, uint32_t w1, uint32_t w2, int lane) {
+    const int32_t total = n * Width;
+    const uintptr_t align = sizeof(T) == 4 ? 15u : 3u;
+    if ((((uintptr_t)dst) & align) != 0u || (total & 3) != 0) {
+        put_bit_rows<T, Width, Words>(dst, n, w0, w1, w2, lane);
+        return;
+    }
+    const int32_t quads = total >> 2;
+    for (int32_t q0 = 0; q0 < quads; q0 += kWave) {
+        const int32_t q = q0 + lane;
+        const int32_t e0 = (q < quads ? q : quads - 1) * 4;
+        const int32_t ca = e0 / Width, cb = (e0 + 3) / Width;  // Width >= 4: at most two cells
+        const uint32_t a0 = lane_word(w0, ca), b0 = lane_word(w0, cb);
+        uint32_t a1 = 0u, a2 = 0u, b1 = 0u, b2 = 0u;
+        if (Words > 1) {
+            a1 = lane_word(w1, ca);
+            a2 = lane_word(w2, ca);
+            b1 = lane_word(w1, cb);
+            b2 = lane_word(w2, cb);
+        }
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int32_t b = e0 + k;
+            const bool first = b < (ca + 1) * Width;
+            const int32_t bit = b - (first ? ca : cb) * Width;
+            v[k] = first ? row_bit_of<Width, Words>(bit, a0, a1, a2) : row_bit_of<Width, Words>(bit, b0, b1, b2);
+        }
+        if (q < quads) {
+            if (sizeof(T) == 4) {
+                uint4 x;
+                x.x = v[0];
+                x.y = v[1];
+                x.z = v[2];
+                x.w = v[3];
+                ((uint4*)dst)[q] = x;
+            } else {
+                ((uint32_t*)dst)[q] = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
+            }
+        }
+    }
+}
+
 // GridNet observation of one env (N/adapters/gridnet/observation.py:27-72):
 // planes = one-hot of the full-observation feature maps clipped to the widths
 // 5, 5, 3, 8, 6, 2 (or the six clipped values), the source mask (cells of an
 // available unit of the player) and its legality row as the action mask
-// (rows, or packed into three words: bits 0-28, 29-60, 61-77).
+// (rows, or packed into three words: bits 0-28, 29-60, 61-77).  The wave
+// walks the board in 64-cell chunks, one cell per lane; the wide rows
+// (one-hot planes, mask rows) go out as contiguous runs, the narrow ones
+// (plane indices, packed words, the source mask) from each cell's lane.
 NR_DEV void gridnet_observe(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane,
                             const nanorts_gridnet_obs& o, void* planes_out) {
     const int32_t cells = g.cells;
     const int32_t widths[6] = {5, 5, 3, 8, 6, 2};
     const int32_t offsets[6] = {0, 5, 10, 13, 21, 27};
-    for (int32_t c = lane; c < cells; c += kWave) {
-        const int32_t occ = e.entity[c];
-        uint32_t word = 0u;
+    const bool rows_needed = o.source_mask || o.action_mask;
+    for (int32_t c0 = 0; c0 < cells; c0 += kWave) {
+        const int32_t c = c0 + lane, n = imin(kWave, cells - c0);
+        uint32_t word = 0u, terrain = 0u;
         int32_t owner = kAbsent, slot = 0;
         bool available = false;
-        if (occ != kAbsent) {
-            slot = clampi(occ, 0, g.E - 1);
-            const uint32_t hp = (uint32_t)(int32_t)e.hp[slot] & 0xFFu;
-            const uint32_t carried = (uint32_t)e.carried[slot] & 0xFFu;
-            const uint32_t type = (uint32_t)((int32_t)e.utype[slot] + 1) & 0xFFu;
-            const int32_t pk = e.pkind[slot];
-            const uint32_t kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
-            owner = e.owner[slot];
-            const uint32_t own = (uint32_t)(owner + 1) & 0x3u;
-            word = hp | (carried << 8) | (type << 16) | (kind << 24) | (own << 28);
-            available = owner >= 0 && pk == kAbsent;  // board_view.available
+        if (c < cells) {
+            const int32_t occ = e.entity[c];
+            if (occ != kAbsent) {
+                slot = clampi(occ, 0, g.E - 1);
+                const uint32_t hp = (uint32_t)(int32_t)e.hp[slot] & 0xFFu;
+                const uint32_t carried = (uint32_t)e.carried[slot] & 0xFFu;
+                const uint32_t type = (uint32_t)((int32_t)e.utype[slot] + 1) & 0xFFu;
+                const int32_t pk = e.pkind[slot];
+                const uint32_t kind = (uint32_t)(pk > 0 ? pk : 0) & 0xFu;
+                owner = e.owner[slot];
+                const uint32_t own = (uint32_t)(owner + 1) & 0x3u;
+                word = hp | (carried << 8) | (type << 16) | (kind << 24) | (own << 28);
+                available = owner >= 0 && pk == kAbsent;  // board_view.available
+            }
+            terrain = h.terrain[c] ? 1u : 0u;
         }
-        const uint32_t terrain = h.terrain[c] ? 1u : 0u;
         Row lr;
         lr.w[0] = lr.w[1] = lr.w[2] = 0u;
-        if (available && (o.source_mask || o.action_mask)) lr = legality_row(g, h, e, slot);
+        if (available && rows_needed) lr = legality_row(g, h, e, slot);
 #pragma unroll
         for (int32_t p = 0; p < 2; ++p) {
-            const int64_t at = (l * 2 + p) * cells + c;
+            const int64_t at0 = (l * 2 + p) * cells + c0;
             const uint32_t own = (word >> 28) & 3u;
             const uint32_t relabelled = own > 0 ? (uint32_t)(((int32_t)own - 1 + p) % 2 + 1) : 0u;
             const uint32_t fm[6] = {word & 0xFFu, (word >> 8) & 0xFFu, relabelled, (word >> 16) & 0xFFu,
                                     (word >> 24) & 0xFu, terrain};
             if (planes_out) {
                 if (o.planes_form == 1) {
-                    int8_t* dst = (int8_t*)planes_out + at * 6;
+                    uint32_t packed = 0u;  // six 3-bit clipped values
 #pragma unroll
-                    for (int f = 0; f < 6; ++f) dst[f] = (int8_t)imin((int32_t)fm[f], widths[f] - 1);
+                    for (int f = 0; f < 6; ++f) packed |= (uint32_t)imin((int32_t)fm[f], widths[f] - 1) << (3 * f);
+                    // six bytes per cell are written by their own lane, as
+                    // three 2-byte stores (a shuffle per element costs more
+                    // than it saves for so narrow a row)
+                    if (c < cells) {
+                        int16_t* dst = (int16_t*)((int8_t*)planes_out + (at0 + lane) * 6);
+#pragma unroll
+                        for (int k = 0; k < 3; ++k)
+                            dst[k] = (int16_t)(((packed >> (6 * k)) & 7u) | (((packed >> (6 * k + 3)) & 7u) << 8));
+                    }
                 } else {
                     uint32_t hot = 0u;  // 29 plane bits
 #pragma unroll
                     for (int f = 0; f < 6; ++f) hot |= 1u << (offsets[f] + imin((int32_t)fm[f], widths[f] - 1));
-                    if (o.planes_bytes == 4) {
-                        int32_t* dst = (int32_t*)planes_out + at * kPlaneCount;
-                        for (int b = 0; b < kPlaneCount; ++b) dst[b] = (int32_t)((hot >> b) & 1u);
-                    } else {
-                        uint8_t* dst = (uint8_t*)planes_out + at * kPlaneCount;
-                        for (int b = 0; b < kPlaneCount; ++b) dst[b] = (uint8_t)((hot >> b) & 1u);
-                    }
+                    if (o.planes_bytes == 4)
+                        put_bit_rows4<int32_t, kPlaneCount, 1>((int32_t*)planes_out + at0 * kPlaneCount, n, hot, 0u,
+                                                              0u, lane);
+                    else
+                        put_bit_rows4<uint8_t, kPlaneCount, 1>((uint8_t*)planes_out + at0 * kPlaneCount, n, hot, 0u,
+                                                              0u, lane);
                 }
             }
             const bool source = available && owner == p;
-            if (o.source_mask) o.source_mask[at] = source ? 1 : 0;
+            if (o.source_mask && c < cells) o.source_mask[at0 + lane] = source ? 1 : 0;
             if (o.action_mask) {
                 const uint32_t w0 = source ? lr.w[0] : 0u, w1 = source ? lr.w[1] : 0u, w2 = source ? lr.w[2] : 0u;
                 if (o.mask_form == 1) {
-                    uint32_t* dst = (uint32_t*)o.action_mask + at * 3;
-                    dst[0] = w0 & 0x1FFFFFFFu;
-                    dst[1] = (w0 >> 29) | (w1 << 3);
-                    dst[2] = ((w1 >> 29) | (w2 << 3)) & 0x1FFFFu;
-                } else if (o.mask_bytes == 4) {
-                    int32_t* dst = (int32_t*)o.action_mask + at * kMaskWidth;
-                    for (int b = 0; b < kMaskWidth; ++b) {
-                        const uint32_t w = b < 32 ? w0 : (b < 64 ? w1 : w2);
-                        dst[b] = (int32_t)((w >> (b & 31)) & 1u);
+                    if (c < cells) {
+                        uint32_t* dst = (uint32_t*)o.action_mask + (at0 + lane) * 3;
+                        dst[0] = w0 & 0x1FFFFFFFu;
+                        dst[1] = (w0 >> 29) | (w1 << 3);
+                        dst[2] = ((w1 >> 29) | (w2 << 3)) & 0x1FFFFu;
                     }
-                } else {
-                    uint8_t* dst = (uint8_t*)o.action_mask + at * kMaskWidth;
-                    for (int b = 0; b < kMaskWidth; ++b) {
-                        const uint32_t w = b < 32 ? w0 : (b < 64 ? w1 : w2);
-                        dst[b] = (uint8_t)((w >> (b & 31)) & 1u);
-                    }
-                }
+                } else if (o.mask_bytes == 4)
+                    put_bit_rows4<int32_t, kMaskWidth, 3>((int32_t*)o.action_mask + at0 * kMaskWidth, n, w0, w1, w2,
+                                                         lane);
+                else
+                    put_bit_rows4<uint8_t, kMaskWidth, 3>((uint8_t*)o.action_mask + at0 * kMaskWidth, n, w0, w1, w2,
+                                                         lane);
             }
         }
     }

@@ -131,6 +131,40 @@ def _want_rewards(game, oracle_step_out, nxt, done) -> tuple[np.ndarray, np.ndar
     return comps, dones
 
 
+ODD_MAP = """<rts.PhysicalGameState width="9" height="7">
+  <terrain>000000000000000000000100000000100000000000000000000000000000000</terrain>
+  <players>
+    <rts.Player ID="0" resources="8"></rts.Player>
+    <rts.Player ID="1" resources="8"></rts.Player>
+  </players>
+  <units>
+    <rts.units.Unit type="Resource" ID="1" player="-1" x="0" y="0" resources="20" hitpoints="1"></rts.units.Unit>
+    <rts.units.Unit type="Resource" ID="2" player="-1" x="8" y="6" resources="20" hitpoints="1"></rts.units.Unit>
+    <rts.units.Unit type="Base" ID="3" player="0" x="2" y="1" resources="0" hitpoints="10"></rts.units.Unit>
+    <rts.units.Unit type="Base" ID="4" player="1" x="6" y="5" resources="0" hitpoints="10"></rts.units.Unit>
+    <rts.units.Unit type="Worker" ID="5" player="0" x="1" y="1" resources="0" hitpoints="1"></rts.units.Unit>
+    <rts.units.Unit type="Worker" ID="6" player="1" x="7" y="5" resources="0" hitpoints="1"></rts.units.Unit>
+  </units>
+</rts.PhysicalGameState>
+"""
+
+
+def _game(case):
+    """The named case, or "odd-9x7": a 63-cell map, so rows of the second
+    player and the last chunk start at odd cells (the writers' element path)."""
+    if case != "odd-9x7":
+        return game_for(case)
+    import tempfile
+    from pathlib import Path
+
+    from nanorts_amd.content import load_game
+    from nanorts_amd.model import ConflictStrategy
+
+    path = Path(tempfile.mkdtemp(prefix="nr_map_")) / "odd9x7.xml"
+    path.write_text(ODD_MAP)
+    return load_game(path, conflict_strategy=ConflictStrategy.CANCEL_RANDOM, max_cycles=200), False
+
+
 def _surface(game, **kw):
     import torch
 
@@ -159,7 +193,7 @@ def test_decode_matches_oracle(case, wild, oracle_threads):
         np.testing.assert_array_equal(got[f].cpu().numpy(), want[f], err_msg=f"{case}: {f}")
 
 
-@pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random", "melee-both"])
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random", "melee-both", "odd-9x7"])
 @pytest.mark.parametrize("form", [("one_hot", "int32", "rows", "int32"), ("one_hot", "uint8", "rows", "bool"),
                                   ("one_hot", "bool", "packed", "int32"), ("indices", "int32", "rows", "uint8")])
 def test_observe_matches_closed_form(case, form, oracle_threads):
@@ -169,7 +203,7 @@ def test_observe_matches_closed_form(case, form, oracle_threads):
 
     _say(f"gridnet observe {case} {form}")
     planes_form, planes_dtype, mask_form, mask_dtype = form
-    game, partial = game_for(case)
+    game, partial = _game(case)
     oracle, st = advanced_states(game, 64, 120, partial, oracle_threads, seed=29)
     g = _surface(game, planes_form=planes_form, planes_dtype=getattr(torch, planes_dtype), mask_form=mask_form,
                  mask_dtype=getattr(torch, mask_dtype))
@@ -224,16 +258,16 @@ def _check_step(game, oracle, g, st, out, acts_cells, against=None):
     return done
 
 
-@pytest.mark.parametrize("case", ["16x16-alternating", "barracks-random", "8x8-original-both"])
+@pytest.mark.parametrize("case", ["16x16-alternating", "barracks-random", "8x8-original-both", "odd-9x7"])
 def test_steps_match_oracle(case, oracle_threads):
     import torch
 
     _say(f"gridnet step {case}")
-    game, partial = game_for(case)
+    game, partial = _game(case)
     b = game.bucket
     L = 48
     # near the time limit for the short cases, so episodes end and reset
-    advance = {"16x16-alternating": 280, "barracks-random": 130, "8x8-original-both": 200}[case]
+    advance = {"16x16-alternating": 280, "barracks-random": 130, "8x8-original-both": 200, "odd-9x7": 180}[case]
     oracle, st = advanced_states(game, L, advance, partial, oracle_threads, seed=31)
     g = _surface(game)
     state = to_device(g, st)
@@ -243,7 +277,7 @@ def test_steps_match_oracle(case, oracle_threads):
         out = g.step(state, torch.as_tensor(acts.reshape(L, 2, b.height, b.width, 7), device="cuda:0"), donate=True)
         ended += int(_check_step(game, oracle, g, st, out, acts).sum())
         state = out.environment_state
-    if case != "8x8-original-both":
+    if case not in ("8x8-original-both", "odd-9x7"):
         assert ended > 0
 
 
