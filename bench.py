@@ -60,7 +60,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-steps", type=int, default=3000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
-    ap.add_argument("--profile-child", choices=("rollout", "copy"), default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("rollout", "copy", "gridnet", "seat"), default=None,
+                    help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.envs is None:
         args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS}.get(args.workload, SEAT_ENVS)
@@ -167,13 +168,26 @@ def child(args) -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         return
+    if args.profile_child == "seat":
+        seat, state = make_seat(args.workload, args.envs)
+        for t in range(2):
+            seat.rollout(state, args.chunk, (11, 13), step0=t * args.chunk, observation_depth=args.depth)
+        torch.cuda.synchronize()
+        return
+    if args.profile_child == "gridnet":
+        g, state, mask = make_gridnet(args.envs)
+        for t in range(8):
+            out = g.step(state, g.sample_actions(mask, (11, 13), t), donate=True)
+            state, mask = out.environment_state, out.observation.action_mask
+        torch.cuda.synchronize()
+        return
     game, env, state = make_env(args.envs)
     run_rollout(env, state, 4 * args.chunk, args.chunk, args.depth, 0)
     torch.cuda.synchronize()
 
 
-def pmc_traffic(args, per_launch_steps: int) -> dict | None:
-    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the rollout kernel,
+def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel: str = "k_rollout") -> dict | None:
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the measured kernel,
     each scaled by what the counter reads for a plain copy of known size."""
     import csv
     import shutil
@@ -188,14 +202,15 @@ def pmc_traffic(args, per_launch_steps: int) -> dict | None:
         out = Path(tempfile.mkdtemp(prefix="nr_pmc_", dir=os.environ.get("TMPDIR", "/tmp")))
         cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", str(out), "-o", "pmc",
                "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--profile-child", mode,
-               "--envs", str(args.envs), "--chunk", str(args.chunk), "--depth", str(args.depth)]
+               "--workload", args.workload, "--envs", str(args.envs), "--chunk", str(args.chunk), "--depth",
+               str(args.depth)]
         subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=180)
         values = []
         for path in out.rglob("*counter_collection.csv"):
             with open(path) as fh:
                 for row in csv.DictReader(fh):
                     name = row.get("Kernel_Name", "")
-                    want = "k_rollout" in name if mode == "rollout" else ("copy" in name.lower() or "elementwise" in name.lower())
+                    want = kernel in name if mode != "copy" else ("copy" in name.lower() or "elementwise" in name.lower())
                     if want and row.get("Counter_Name") == counter:
                         values.append(float(row["Counter_Value"]))
         shutil.rmtree(out, ignore_errors=True)
@@ -205,8 +220,8 @@ def pmc_traffic(args, per_launch_steps: int) -> dict | None:
         copy_bytes = 2 * (1 << 26) * 4  # read + write of the 256 MiB copy
         fetch_copy = counters("copy", "FETCH_SIZE")
         write_copy = counters("copy", "WRITE_SIZE")
-        fetch = counters("rollout", "FETCH_SIZE")
-        write = counters("rollout", "WRITE_SIZE")
+        fetch = counters(mode, "FETCH_SIZE")
+        write = counters(mode, "WRITE_SIZE")
         if not (fetch_copy and write_copy and fetch and write):
             return None
         # a copy of B bytes fetches B/2 and writes B/2
@@ -247,7 +262,7 @@ def cpu_seat_baseline(bot_name: str, envs: int, steps: int) -> dict:
                       f"{bot_name} act, seat step, auto-reset, symbolic obs) on 1 host thread, {dt:.1f} s"}
 
 
-def main_seat(args) -> None:
+def make_seat(workload: str, envs: int):
     import torch
 
     import nanorts_amd
@@ -255,11 +270,19 @@ def main_seat(args) -> None:
     from nanorts_amd import env as envmod
 
     torch.cuda.set_device(0)
-    bot = bots.workerRushAI if args.workload == "seat-workerrush" else bots.lightRushAI
+    bot = bots.workerRushAI if workload == "seat-workerrush" else bots.lightRushAI
     game = nanorts_amd.map_name_to_scenario(MAP, max_cycles=3000)
     seat = bots.SeatEnv(bot, scenario=game, final_observation=False)
+    _, state = seat.reset(envmod.env_roots(0, envs))
+    return seat, state
+
+
+def main_seat(args) -> None:
+    import torch
+
+    seat, state = make_seat(args.workload, args.envs)
+    bot, game = seat.bot, seat.game
     L = args.envs
-    _, state = seat.reset(envmod.env_roots(0, L))
     chunk = max(1, min(args.chunk, args.steps))
 
     def run(steps, step0, events):
@@ -289,6 +312,7 @@ def main_seat(args) -> None:
     per_step = step_bytes(b) + 2 * carry_bytes(b)
     per_launch_bytes = L * (chunk * per_step + 2 * state_bytes(b))
     achieved = per_launch_bytes / avg_launch_s / 1e9
+    traffic = pmc_traffic(args, chunk, mode="seat", kernel="k_seat_rollout")
     cpu = None if args.no_cpu else cpu_seat_baseline(bot.name, args.cpu_envs // 4, args.cpu_steps // 15)
     line = {
         "metric": f"env-steps/sec (learner vs {bot.name}) at 16x16 × {L} envs; % HBM roofline",
@@ -314,11 +338,15 @@ def main_seat(args) -> None:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_seat_rollout",
-            "avg_launch_ms": round(avg_launch_s * 1e3, 4), "algorithmic_bytes_per_launch": per_launch_bytes,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
+            "kernel": "k_seat_rollout", "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "algorithmic_bytes_per_launch": per_launch_bytes,
         },
         "cpu_baseline": cpu,
     }
+    if traffic is not None:
+        line["roofline"]["traffic_detail"] = traffic
     print(json.dumps(line))
 
 
@@ -393,7 +421,7 @@ def cpu_gridnet_baseline(envs: int, steps: int) -> dict:
                       f"{dt:.1f} s"}
 
 
-def main_gridnet(args) -> None:
+def make_gridnet(envs: int):
     import torch
 
     import nanorts_amd
@@ -403,9 +431,16 @@ def main_gridnet(args) -> None:
     torch.cuda.set_device(0)
     game = nanorts_amd.map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM")
     g = gridnet.GridNet(game, gridnet.prepare(game, mask_form="packed"), device="cuda:0")
+    state, obs = g.reset(envmod.env_roots(0, envs))
+    return g, state, obs.action_mask
+
+
+def main_gridnet(args) -> None:
+    import torch
+
+    g, state, mask = make_gridnet(args.envs)
+    game = g.game
     L = args.envs
-    state, obs = g.reset(envmod.env_roots(0, L))
-    mask = obs.action_mask
 
     def run(steps, step0, events):
         nonlocal state, mask
@@ -432,6 +467,7 @@ def main_gridnet(args) -> None:
     b = game.bucket
     per_step = gridnet_step_bytes(b)
     achieved = L * per_step / avg_launch_s / 1e9
+    traffic = pmc_traffic(args, 1, mode="gridnet", kernel="k_gridnet_step")
     cpu = None if args.no_cpu else cpu_gridnet_baseline(args.cpu_envs // 16, args.cpu_steps // 30)
     line = {
         "metric": f"env-steps/sec (GridNet surface, both players) at 16x16 × {L} envs; % HBM roofline",
@@ -455,11 +491,15 @@ def main_gridnet(args) -> None:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_gridnet_step",
-            "avg_launch_ms": round(avg_launch_s * 1e3, 4), "algorithmic_bytes_per_launch": L * per_step,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
+            "kernel": "k_gridnet_step", "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "algorithmic_bytes_per_launch": L * per_step,
         },
         "cpu_baseline": cpu,
     }
+    if traffic is not None:
+        line["roofline"]["traffic_detail"] = traffic
     print(json.dumps(line))
 
 
