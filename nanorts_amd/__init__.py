@@ -11,7 +11,10 @@ a leading env dimension.
 from nanorts_amd.content import (
     CAPACITY_PROFILES,
     MAP_DIRECTORY,
+    ContentError,
     GameConfig,
+    UnitRecord,
+    build_game,
     load_game,
     map_name_to_scenario,
     scenario_names,
@@ -19,17 +22,24 @@ from nanorts_amd.content import (
     with_unit_type_table,
 )
 from nanorts_amd.model import ConflictStrategy, ModelError, UnitTypeTableVersion
+from nanorts_amd.rendering import RenderAssets, RenderError, prepare_assets
 
 __all__ = [
     "CAPACITY_PROFILES",
     "MAP_DIRECTORY",
     "ConflictStrategy",
+    "ContentError",
     "GameConfig",
     "ModelError",
+    "RenderAssets",
+    "RenderError",
+    "UnitRecord",
     "UnitTypeTableVersion",
+    "build_game",
     "load_game",
     "make",
     "map_name_to_scenario",
+    "prepare_assets",
     "scenario_names",
     "shipped_map",
     "with_unit_type_table",

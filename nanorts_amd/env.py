@@ -178,14 +178,14 @@ class DeviceGame:
 
 def make(env_id: str, *, scenario: GameConfig, utt: UnitTypeTableVersion | None = None, surface: str = "symbolic",
          partial_observability: bool = False, final_observation: bool = True, feature_dtype: Any = None,
-         reward_components: bool = False, device: str | torch.device | None = None) -> "NanoRTS":
+         reward_components: bool = False, device: str | torch.device | None = None, assets: Any = None) -> "NanoRTS":
     """src/nanorts/adapters/jaxmarl/facade.py:43-56"""
     if env_id not in ENVIRONMENT_IDS:
         raise ModelError(f"make refuses environment id {env_id!r}: the accepted ids are {list(ENVIRONMENT_IDS)}")
     game = scenario if utt is None else with_unit_type_table(scenario, utt)
     return NanoRTS(game, surface=surface, partial_observability=partial_observability,
                    final_observation=final_observation, feature_dtype=feature_dtype,
-                   reward_components=reward_components, device=device)
+                   reward_components=reward_components, device=device, assets=assets)
 
 
 class NanoRTS:
@@ -193,7 +193,7 @@ class NanoRTS:
 
     def __init__(self, scenario: GameConfig, *, surface: str = "symbolic", partial_observability: bool = False,
                  final_observation: bool = True, feature_dtype: Any = None, reward_components: bool = False,
-                 device: str | torch.device | None = None):
+                 device: str | torch.device | None = None, assets: Any = None):
         if surface not in SURFACES:
             raise ModelError(f"NanoRTS refuses surface={surface!r}: this release delivers {list(SURFACES)}")
         if feature_dtype not in (None, torch.uint8, np.uint8, "uint8"):
@@ -223,10 +223,26 @@ class NanoRTS:
         self.final_observation = final_observation
         self.partial = int(partial_observability)
         self._tiles: torch.Tensor | None = None
+        # the drawing table (src/nanorts/adapters/jaxmarl/layout.py:168-205):
+        # none under the symbolic surface; under the pixel surface the shipped
+        # sprite sheet unless an Asset set of 16-pixel cells is given
+        if surface == "symbolic" and assets is not None:
+            raise ModelError(f"NanoRTS refuses assets={type(assets).__name__} under surface=\"symbolic\": the symbolic "
+                             "surface renders nothing")
         if surface == "pixels":
             from nanorts_amd import rendering
 
-            self._tiles = torch.as_tensor(rendering.tile_table(b.unit_type_capacity), device=self.device)
+            if assets is None:
+                table = rendering.tile_table(b.unit_type_capacity)
+            else:
+                if assets.cell_pixels != rendering.SPRITE_PIXELS:
+                    raise ModelError(f"NanoRTS refuses an Asset set drawing {assets.cell_pixels} pixels per cell "
+                                     f"against the surface's {rendering.SPRITE_PIXELS}")
+                if assets.unit_type_capacity != b.unit_type_capacity:
+                    raise ModelError(f"NanoRTS refuses an Asset set drawing {assets.unit_type_capacity} unit types "
+                                     f"against the Bucket's {b.unit_type_capacity}")
+                table = np.ascontiguousarray(assets.tiles, np.uint8)
+            self._tiles = torch.as_tensor(table, device=self.device)
 
     # ------------------------------------------------------------------ API
     def reset(self, key) -> tuple[dict[str, Any], EnvironmentState]:

@@ -15,6 +15,7 @@ The PNG reader is a small stdlib (zlib) decoder for the non-interlaced
 """
 from __future__ import annotations
 
+import dataclasses
 import functools
 import struct
 import zlib
@@ -101,31 +102,104 @@ def occupant_states(types: int) -> int:
     return 1 + 3 * types
 
 
-@functools.lru_cache(maxsize=4)
-def tile_table(types: int = len(TYPE_STEMS)) -> np.ndarray:
-    """uint8[2 * (1 + 3T), 16, 16, 3]: index terrain * (1 + 3T) + occupant."""
-    if types != len(TYPE_STEMS):
-        raise RenderError(f"the sprite sheet draws {len(TYPE_STEMS)} unit types, the game has {types}")
-    sprites = {name: read_png(ART_DIRECTORY / f"{name}.png") for name in sprite_names()}
-    for name, image in sprites.items():
-        if image.shape != (SPRITE_PIXELS, SPRITE_PIXELS, 4):
-            raise RenderError(f"sprite {name} is {image.shape}, expected (16, 16, 4)")
+@dataclasses.dataclass(frozen=True, eq=False)
+class RenderAssets:
+    """A prepared tile table (src/nanorts/rendering/raster.py RenderAssets):
+    uint8[2 * (1 + 3T), cell_pixels, cell_pixels, 3]."""
+
+    tiles: np.ndarray
+    cell_pixels: int
+    unit_type_capacity: int
+
+
+def _class_name(index: int, types: int) -> str:
+    terrain, occupant = divmod(index, occupant_states(types))
+    if occupant == 0:
+        return f"{TERRAIN_NAMES[terrain]} + empty"
+    owner, unit_type = divmod(occupant - 1, types)
+    return f"{TERRAIN_NAMES[terrain]} + {OWNER_NAMES[owner]} {TYPE_STEMS[unit_type]}"
+
+
+def prepare_assets(bucket, cell_pixels: int = SPRITE_PIXELS, tiles=None) -> RenderAssets:
+    """src/nanorts/rendering/assets.py:52-195: the tile table from the
+    shipped sprite sheet (or `tiles`, a name -> 16x16 RGBA uint8 mapping
+    naming every sprite of sprite_names()), each sprite upscaled to
+    `cell_pixels` (a multiple of 16) with a ring of cell_pixels / 16 pixels.
+    Refuses a table whose tiles would be indistinguishable: two equal
+    composites, or two occupied tiles equal outside the glyph band."""
+    if cell_pixels <= 0 or cell_pixels % SPRITE_PIXELS:
+        raise RenderError(f"cell_pixels is {cell_pixels}, expected a positive integer multiple of the "
+                          f"{SPRITE_PIXELS}-pixel sprite side")
+    types = len(TYPE_STEMS)
+    if bucket.unit_type_capacity != types:
+        raise RenderError(f"BucketSpec.unit_type_capacity is {bucket.unit_type_capacity}, and an Asset set draws the "
+                          f"{types} types the supported unit type table holds")
+    names = sprite_names()
+    supplied = ({name: read_png(ART_DIRECTORY / f"{name}.png") for name in names} if tiles is None
+                else dict(tiles))
+    if set(supplied) != set(names):
+        raise RenderError(f"the Asset set does not name the Tile classes a Bucket of {types} unit types has: it is "
+                          f"missing {sorted(set(names) - set(supplied))} and holds an unused "
+                          f"{sorted(set(supplied) - set(names))}")
+    sprites = {}
+    for name in names:
+        image = np.asarray(supplied[name])
+        if image.shape != (SPRITE_PIXELS, SPRITE_PIXELS, 4) or image.dtype != np.uint8:
+            raise RenderError(f"the sprite {name!r} is {image.shape} {image.dtype}, expected a "
+                              f"({SPRITE_PIXELS}, {SPRITE_PIXELS}, 4) uint8 RGBA image")
+        sprites[name] = image
     for name in TERRAIN_NAMES:
         if not (sprites[name][..., 3] >= 128).all():
-            raise RenderError(f"terrain sprite {name} is not opaque")
-    ring = np.zeros((SPRITE_PIXELS, SPRITE_PIXELS), bool)
-    ring[0, :] = ring[-1, :] = ring[:, 0] = ring[:, -1] = True
+            raise RenderError(f"the terrain tile {name!r} is not fully opaque, and terrain is the ground every "
+                              "occupant is drawn over")
+    scale = cell_pixels // SPRITE_PIXELS
+
+    def up(image: np.ndarray) -> np.ndarray:
+        return np.repeat(np.repeat(image, scale, axis=0), scale, axis=1)
+
+    ring = np.zeros((cell_pixels, cell_pixels), bool)
+    ring[:scale, :] = ring[-scale:, :] = ring[:, :scale] = ring[:, -scale:] = True
     states = occupant_states(types)
-    table = np.zeros((2 * states, SPRITE_PIXELS, SPRITE_PIXELS, 3), np.uint8)
+    table = np.zeros((2 * states, cell_pixels, cell_pixels, 3), np.uint8)
     for terrain, tname in enumerate(TERRAIN_NAMES):
-        ground = sprites[tname][..., :3]
+        ground = up(sprites[tname])[..., :3]
         table[terrain * states] = ground
         for owner_bucket, oname in enumerate(OWNER_NAMES):
             for t, stem in enumerate(TYPE_STEMS):
-                art = sprites[f"{oname}-{stem}"]
+                art = up(sprites[f"{oname}-{stem}"])
                 tile = ground.copy()
                 tile[ring] = AURA_COLOURS[owner_bucket]
                 drawn = art[..., 3] >= 128
                 tile[drawn] = art[..., :3][drawn]
                 table[terrain * states + 1 + owner_bucket * types + t] = tile
-    return table
+    band_rows = slice(BAND_ROWS[0] * scale, (BAND_ROWS[-1] + 1) * scale)
+    band_cols = slice(BAND_COLUMN * scale, (BAND_COLUMN + BAND_WIDTH) * scale)
+    composites: dict[bytes, str] = {}
+    outside: dict[bytes, str] = {}
+    for index, tile in enumerate(table):
+        name = _class_name(index, types)
+        for seen, picture, verb in ((composites, tile.tobytes(), "composite"), (outside, None, "draw as")):
+            if picture is None:
+                if index % states == 0:
+                    continue
+                blanked = tile.copy()
+                blanked[band_rows, band_cols] = 0
+                picture = blanked.tobytes()
+            if picture in seen:
+                raise RenderError(f"the Tile classes {seen[picture]!r} and {name!r} {verb} the same picture, which "
+                                  "would make them indistinguishable in a Rendering")
+            seen[picture] = name
+    return RenderAssets(tiles=table, cell_pixels=cell_pixels, unit_type_capacity=types)
+
+
+@functools.lru_cache(maxsize=4)
+def tile_table(types: int = len(TYPE_STEMS)) -> np.ndarray:
+    """uint8[2 * (1 + 3T), 16, 16, 3] of the shipped sprite sheet: index
+    terrain * (1 + 3T) + occupant."""
+    if types != len(TYPE_STEMS):
+        raise RenderError(f"the sprite sheet draws {len(TYPE_STEMS)} unit types, the game has {types}")
+
+    class _Types:
+        unit_type_capacity = types
+
+    return prepare_assets(_Types()).tiles

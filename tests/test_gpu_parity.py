@@ -186,6 +186,30 @@ def test_pixel_surface_env_step(oracle_threads):
         assert final[env.agents[0]].image.shape == obs[env.agents[0]].image.shape
 
 
+def test_pixel_surface_with_a_custom_asset_set(oracle_threads):
+    """The pixel surface drawing a prepared Asset set other than the shipped
+    sheet (recoloured floor and player-0 sprites): images against the
+    oracle's renderer with the same table."""
+    from nanorts_amd import rendering
+
+    game, partial = game_for("16x16-random-partial")
+    oracle, st = advanced_states(game, 16, 80, partial, oracle_threads, seed=12)
+    sheet = {name: rendering.read_png(rendering.ART_DIRECTORY / f"{name}.png").copy()
+             for name in rendering.sprite_names()}
+    sheet["floor"][..., 1] ^= 0x30
+    for name in sheet:
+        if name.startswith("player0-"):
+            sheet[name][..., 2] ^= 0x55
+    assets = rendering.prepare_assets(game.bucket, tiles=sheet)
+    env = _env(game, partial, surface="pixels", assets=assets)
+    obs = env.get_obs(to_device(env, st))
+    want_image, _ = oracle.pixels(st, partial, assets.tiles)
+    default_image, _ = oracle.pixels(st, partial, rendering.tile_table(game.bucket.unit_type_capacity))
+    assert not np.array_equal(want_image, default_image)
+    for i, agent in enumerate(env.agents):
+        np.testing.assert_array_equal(obs[agent].image.cpu().numpy(), want_image[:, i])
+
+
 def test_reset_where_done(oracle_threads):
     import torch
 

@@ -80,3 +80,54 @@ def test_oracle_pixels_closed_form(case, partial):
     maps, want_scalars = _closed_symbolic(game, st, partial)
     np.testing.assert_array_equal(image, render_maps(maps, tiles, T))
     np.testing.assert_array_equal(scalars, want_scalars)
+
+
+def _bucket(types=7):
+    class B:
+        unit_type_capacity = types
+    return B()
+
+
+def _sheet():
+    return {name: rendering.read_png(rendering.ART_DIRECTORY / f"{name}.png") for name in rendering.sprite_names()}
+
+
+def test_prepare_assets_upscales_and_checks_the_sheet():
+    """prepare_assets (src/nanorts/rendering/assets.py:52-195): 16-pixel
+    cells give the shipped table; 32-pixel cells are its exact 2x upscale
+    (ground, art and the ring all scale by pixel repetition); every refusal
+    of the asset contract fires."""
+    base = rendering.prepare_assets(_bucket())
+    np.testing.assert_array_equal(base.tiles, rendering.tile_table(7))
+    double = rendering.prepare_assets(_bucket(), cell_pixels=32)
+    np.testing.assert_array_equal(double.tiles, np.repeat(np.repeat(base.tiles, 2, axis=1), 2, axis=2))
+    assert double.cell_pixels == 32 and double.unit_type_capacity == 7
+    for bad in (0, 24, -16):
+        with pytest.raises(rendering.RenderError):
+            rendering.prepare_assets(_bucket(), cell_pixels=bad)
+    with pytest.raises(rendering.RenderError):
+        rendering.prepare_assets(_bucket(6))
+    sheet = _sheet()
+    missing = dict(sheet)
+    del missing["player0-worker"]
+    with pytest.raises(rendering.RenderError, match="missing"):
+        rendering.prepare_assets(_bucket(), tiles=missing)
+    see_through = dict(sheet)
+    see_through["wall"] = sheet["wall"].copy()
+    see_through["wall"][0, 0, 3] = 0
+    with pytest.raises(rendering.RenderError, match="opaque"):
+        rendering.prepare_assets(_bucket(), tiles=see_through)
+    small = dict(sheet)
+    small["floor"] = sheet["floor"][:8]
+    with pytest.raises(rendering.RenderError, match="expected a"):
+        rendering.prepare_assets(_bucket(), tiles=small)
+    twins = dict(sheet)
+    twins["player0-light"] = sheet["player0-heavy"]
+    with pytest.raises(rendering.RenderError, match="indistinguishable"):
+        rendering.prepare_assets(_bucket(), tiles=twins)
+    # a recoloured sheet is accepted and changes only what it draws
+    tinted = {name: image.copy() for name, image in sheet.items()}
+    tinted["floor"][..., 0] ^= 0x40
+    custom = rendering.prepare_assets(_bucket(), tiles=tinted)
+    assert not np.array_equal(custom.tiles[0], base.tiles[0])
+    np.testing.assert_array_equal(custom.tiles[1 + 3 * 7], base.tiles[1 + 3 * 7])  # the wall + empty tile
