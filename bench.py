@@ -21,6 +21,12 @@ and the packed action mask; per cycle the harness sampler draws every
 source cell's row from the last observation's mask and one GridNet step
 launch decodes, steps, rewards, resets and observes.
 
+`--workload groups` measures the multi-group core.step: four groups of
+16384 games on basesWorkers16x16 (VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM,
+horizons 5000, 4000, 3000 and 2000: one bucket), each cycle stepping every
+group on uniformly random Commands (a pool of eight sets held in HBM) with
+one nanorts_step_groups launch; one launch per group is timed beside it.
+
 Prints one JSON line (rank 0, N=1).
 """
 from __future__ import annotations
@@ -43,12 +49,14 @@ NUM_ENVS = 65536
 METRIC = "env-steps/sec (both players) at 16x16 × 65536 envs; % HBM roofline"
 SEAT_ENVS = 32768
 GRID_ENVS = 32768
+GROUP_ENVS = 65536
+GROUP_HORIZONS = (5000, 4000, 3000, 2000)
 
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush", "gridnet"),
+    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush", "gridnet", "groups"),
                     default="headline")
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
@@ -64,7 +72,7 @@ def parse() -> argparse.Namespace:
                     help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.envs is None:
-        args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS}.get(args.workload, SEAT_ENVS)
+        args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS, "groups": GROUP_ENVS}.get(args.workload, SEAT_ENVS)
     return args
 
 
@@ -503,6 +511,135 @@ def main_gridnet(args) -> None:
     print(json.dumps(line))
 
 
+def core_step_bytes(bucket) -> int:
+    """Algorithmic HBM bytes of one core.step of one env: the state read and
+    written, the six int32 Commands fields of 2C positions, and the
+    terminated / truncated flags, rewards and admitted event counts."""
+    C, T = bucket.per_player_capacity, bucket.unit_type_capacity
+    return 2 * state_bytes(bucket) + 6 * 2 * C * 4 + 2 + 8 + 4 * (2 + 2 + 2 * T + 6)
+
+
+def main_groups(args) -> None:
+    import numpy as np
+    import torch
+
+    import nanorts_amd
+    from nanorts_amd import env as envmod
+    from nanorts_amd import groups
+
+    torch.cuda.set_device(0)
+    G = len(GROUP_HORIZONS)
+    per = args.envs // G
+    games = [nanorts_amd.map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM", max_cycles=h)
+             for h in GROUP_HORIZONS]
+    envs = [nanorts_amd.make("NanoRTS", scenario=g, final_observation=False, device="cuda:0") for g in games]
+    states = [env.reset(envmod.env_roots(i, per))[1] for i, env in enumerate(envs)]
+    b = games[0].bucket
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(5)
+    C, T, cells = b.per_player_capacity, b.unit_type_capacity, b.cell_count
+
+    def commands():
+        shape = (per, 2, C)
+        draw = lambda lo, hi: torch.randint(lo, hi, shape, generator=gen, device="cuda:0", dtype=torch.int32)
+        return {"kind": draw(0, 6), "direction": draw(0, 4), "none_duration": draw(1, 11),
+                "target_cell": draw(0, cells), "produced_type": draw(0, T), "request_order": draw(0, 2 * C)}
+
+    pool = [[commands() for _ in range(G)] for _ in range(8)]
+    keys = [torch.tensor([[7, i]], dtype=torch.int32, device="cuda:0") for i in range(G)]
+
+    def run(steps, together, events):
+        times = []
+        for t in range(steps):
+            cmds = pool[t % len(pool)]
+            reqs = [(keys[i], states[i], cmds[i], envs[i]) for i in range(G)]
+            if events:
+                a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+            if together:
+                groups.step_groups(reqs)
+            else:
+                for req in reqs:
+                    groups.step_groups([req])
+            if events:
+                e.record()
+                times.append((a, e))
+        return times
+
+    run(args.warmup, True, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    times = run(args.steps, True, True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg_launch_s = sum(a.elapsed_time(e) for a, e in times) / len(times) / 1e3
+    run(10, False, False)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    run(args.steps, False, False)
+    torch.cuda.synchronize()
+    apart = G * per * args.steps / (time.perf_counter() - t1)
+    per_step = core_step_bytes(b)
+    achieved = G * per * per_step / avg_launch_s / 1e9
+    line = {
+        "metric": f"env-steps/sec (core.step over {G} groups in one launch) at 16x16 × {G * per} envs; % HBM roofline",
+        "value": round(G * per * args.steps / wall, 1),
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic: uniformly random Commands (a pool of eight sets in HBM), shipped basesWorkers16x16 map",
+        "config": {
+            "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, {G} groups x {per} games, horizons "
+                        f"{list(GROUP_HORIZONS)}, one nanorts_step_groups launch per cycle",
+            "games": G * per, "groups": G, "algorithmic_bytes_per_env_step": per_step,
+            "one_launch_per_group_env_steps_per_s": round(apart, 1),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_step_groups",
+            "avg_launch_ms": round(avg_launch_s * 1e3, 4), "algorithmic_bytes_per_launch": G * per * per_step,
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_groups_baseline(args.cpu_envs // 4, args.cpu_steps // 10),
+    }
+    print(json.dumps(line))
+
+
+def cpu_groups_baseline(envs: int, steps: int) -> dict:
+    """The oracle's core.step on uniformly random Commands, one host thread."""
+    import numpy as np
+
+    from nanorts_amd import env as envmod
+    from nanorts_amd.content import map_name_to_scenario
+    from oracle.oracle import Oracle, batch_initial
+
+    game = map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM")
+    b = game.bucket
+    oracle = Oracle(game)
+    state = batch_initial(game, envs, envmod.env_roots(0, envs))
+    rng = np.random.default_rng(5)
+    C, T, cells = b.per_player_capacity, b.unit_type_capacity, b.cell_count
+    shape = (envs, 2, C)
+    pool = [{"kind": rng.integers(0, 6, shape, dtype=np.int32), "direction": rng.integers(0, 4, shape, dtype=np.int32),
+             "none_duration": rng.integers(1, 11, shape, dtype=np.int32),
+             "target_cell": rng.integers(0, cells, shape, dtype=np.int32),
+             "produced_type": rng.integers(0, T, shape, dtype=np.int32),
+             "request_order": rng.integers(0, 2 * C, shape, dtype=np.int32)} for _ in range(4)]
+    keys = np.tile(np.asarray([[7, 0]], np.uint32), (envs, 1))
+    t0 = time.perf_counter()
+    for t in range(steps):
+        oracle.core_step(state, pool[t % 4], keys)
+    dt = time.perf_counter() - t0
+    return {"value": round(envs * steps / dt, 1), "unit": "env-steps/s", "cores": 1, "kind": "port",
+            "sample": f"{envs} games x {steps} cycles of core.step on uniformly random Commands (oracle) on 1 host "
+                      f"thread, {dt:.1f} s"}
+
+
 def main() -> None:
     args = parse()
     if args.profile_child:
@@ -514,6 +651,9 @@ def main() -> None:
         sys.exit(2)
     if args.workload == "gridnet":
         main_gridnet(args)
+        return
+    if args.workload == "groups":
+        main_groups(args)
         return
     if args.workload != "headline":
         main_seat(args)

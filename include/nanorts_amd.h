@@ -221,6 +221,19 @@ const char* nanorts_self_check(const int32_t* devices, int64_t n);
 int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
                  int64_t key_lanes, nanorts_commands commands, nanorts_step_results results);
 
+/* core.step over up to 16 groups of lanes, in one launch per 4 groups.  The
+ * groups' games share one bucket (extents, capacities, unit types, attack
+ * window, strategy) and one unit table, and may differ in terrain and
+ * max_cycles; each group has its own State, keys ([lanes or 1][2]),
+ * Commands and results, with nanorts_step's meaning.  `games` holds one
+ * pointer per group.  Replaces the FFI target nanorts_step_groups
+ * (src/nanorts/core/cuda/step.cu:704-808, called from
+ * src/nanorts/core/cycle.py:137-175 through core.step_groups,
+ * src/nanorts/core/__init__.py:71-89). */
+int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
+                        const int64_t* lanes, const uint32_t* const* keys, const int64_t* key_lanes,
+                        const nanorts_commands* commands, const nanorts_step_results* results);
+
 /* Factored legality rows bool[L][2][C][22+T+O] (active units, availability not
  * applied).  Replaces nanorts_legality (src/nanorts/core/cuda/legality.cu:535-545). */
 int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows);

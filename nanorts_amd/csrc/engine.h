@@ -298,7 +298,7 @@ NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field 
 
 // Stage the unit table and terrain for the workgroup (all threads call; a
 // __syncthreads follows in the kernel).
-NR_DEV void load_header(const KGame& g, const Hdr& h) {
+NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
     for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
     if (threadIdx.x == 0) {
 #pragma unroll
@@ -308,7 +308,7 @@ NR_DEV void load_header(const KGame& g, const Hdr& h) {
             h.seg[k].bytes = g.seg[k].bytes;
         }
     }
-    for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = g.terrain[i] ? 1 : 0;
+    for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = terrain[i] ? 1 : 0;
     if (g.fast_obs) {
         // disk[r][dy + R]: bits R - w .. R + w with w = floor(sqrt(r^2 - dy^2)),
         // 0 when |dy| > r (R = disk_r <= 15)
@@ -325,6 +325,7 @@ NR_DEV void load_header(const KGame& g, const Hdr& h) {
         }
     }
 }
+NR_DEV void load_header(const KGame& g, const Hdr& h) { load_header(g, h, g.terrain); }
 
 // ---------------------------------------------------------------------------
 // HBM <-> LDS row copies (16-byte, 4-byte or 1-byte granules by alignment)

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/nanorts_amd.h"
 #include "engine.h"
@@ -457,6 +458,78 @@ __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_st
     if (lane == 0) {
         const bool over = e.sc[S_GAME_OVER] != 0;
         const bool trunc = !over && e.sc[S_TIME] >= g.max_cycles;
+        if (r.terminated) r.terminated[l] = over ? 1 : 0;
+        if (r.truncated) r.truncated[l] = trunc ? 1 : 0;
+        if (r.reward) {
+            const int32_t winner = e.sc[S_WINNER];
+            for (int p = 0; p < 2; ++p) r.reward[2 * l + p] = (over || trunc) ? (p == winner ? 1.0f : -1.0f) : 0.0f;
+        }
+    }
+    if (events) write_events(g, e, l, r, lane);
+}
+
+// core.step over several groups of lanes in one launch (step_groups,
+// N/core/cuda/step.cu:704-808): the groups share one bucket and unit table,
+// so one LDS shape serves every workgroup; each group brings its own State,
+// Commands, keys, results, terrain and horizon.  Workgroups are handed out
+// group after group (first_block), and every workgroup reads its group's
+// slot through the kernel-argument segment pointer, which a runtime index
+// into the slots needs.
+constexpr int32_t kGroupsPerLaunch = 4;
+struct GroupSlot {
+    nanorts_state s;
+    nanorts_commands c;
+    nanorts_step_results r;
+    const uint32_t* key;
+    int64_t key_lanes;
+    int64_t lanes;
+    const uint8_t* terrain;
+    int32_t max_cycles;
+    uint32_t first_block;
+};
+struct GroupsArgs {
+    KGame g;  // first: fresh_game() reads it at offset 0
+    int32_t count;
+    GroupSlot slot[kGroupsPerLaunch];
+};
+static_assert(sizeof(GroupsArgs) <= 4096, "the group table must fit the kernel-argument segment");
+typedef const __attribute__((address_space(4))) GroupsArgs* GroupsArgsArg;
+
+__global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
+    (void)args;
+    GroupsArgsArg ap = (GroupsArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    const GroupsArgs& a = *(const GroupsArgs*)ap;
+    const KGame& g = a.g;
+    int32_t gi = 0;
+    for (int32_t i = 1; i < a.count; ++i)
+        if (blockIdx.x >= a.slot[i].first_block) gi = i;
+    const GroupSlot& sl = a.slot[gi];
+    extern __shared__ __align__(16) uint8_t nr_lds[];
+    AS3 uint8_t* lds = (AS3 uint8_t*)nr_lds;
+    Hdr hdr;
+    hdr.tab = (AS3 int32_t*)lds;
+    hdr.terrain = lds + g.lay.o_terrain;
+    hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);
+    hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);
+    load_header(g, hdr, sl.terrain);
+    __syncthreads();
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t l = (int64_t)(blockIdx.x - sl.first_block) * (blockDim.x >> 6) + wave;
+    if (l >= sl.lanes) return;
+    const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
+    load_env(g, sl.s, l, e, LD_ALL, lane);
+    count_units(g, e, lane);
+    stage_commands(g, e, l, sl.c, lane);
+    const int64_t kl = sl.key_lanes == 1 ? 0 : l;
+    const uint32_t k0 = sl.key[2 * kl], k1 = sl.key[2 * kl + 1];
+    const nanorts_step_results r = sl.r;
+    const bool events = r.admitted_harvest || r.admitted_return || r.admitted_produce || r.admitted_attack;
+    core_step(g, hdr, e, lane, k0, k1, events);
+    store_env(g, sl.s, l, e, lane);
+    if (lane == 0) {
+        const bool over = e.sc[S_GAME_OVER] != 0;
+        const bool trunc = !over && e.sc[S_TIME] >= sl.max_cycles;
         if (r.terminated) r.terminated[l] = over ? 1 : 0;
         if (r.truncated) r.truncated[l] = trunc ? 1 : 0;
         if (r.reward) {
@@ -1405,7 +1478,7 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
+           "nanorts_step_groups,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
            "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against,nanorts_gridnet_sample_actions";
 }
 
@@ -1477,6 +1550,61 @@ int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, in
         !commands.produced_type || !commands.request_order)
         return fail(NANORTS_INVALID_ARGUMENT, "a Commands field pointer is NULL");
     return launch(k_step, sh, lanes, (hipStream_t)stream, state, key, key_lanes, commands, results);
+}
+
+int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
+                        const int64_t* lanes, const uint32_t* const* keys, const int64_t* key_lanes,
+                        const nanorts_commands* commands, const nanorts_step_results* results) {
+    if (groups < 1 || groups > 16) return fail(NANORTS_INVALID_ARGUMENT, "groups must be in [1, 16]");
+    if (!games || !states || !lanes || !keys || !key_lanes || !commands || !results)
+        return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
+    std::vector<Shape> shapes((size_t)groups);
+    for (int32_t i = 0; i < groups; ++i) {
+        std::string why;
+        if (!games[i] || !shape_for(games[i], &shapes[(size_t)i], &why))
+            return fail(NANORTS_INVALID_ARGUMENT, "group " + std::to_string(i) + ": " + why);
+        const KGame& a = shapes[0].g;
+        const KGame& b = shapes[(size_t)i].g;
+        if (a.H != b.H || a.W != b.W || a.N != b.N || a.C != b.C || a.T != b.T || a.O != b.O ||
+            a.strategy != b.strategy || std::memcmp(a.tab, b.tab, sizeof(a.tab)) != 0)
+            return fail(NANORTS_INVALID_ARGUMENT,
+                        "nanorts_step_groups: group " + std::to_string(i) + "'s bucket or unit table disagrees with group 0's");
+        if (!state_complete(states[i])) return fail(NANORTS_INVALID_ARGUMENT, "a State leaf pointer is NULL");
+        const nanorts_commands& c = commands[i];
+        if (!c.kind || !c.direction || !c.none_duration || !c.target_cell || !c.produced_type || !c.request_order)
+            return fail(NANORTS_INVALID_ARGUMENT, "a Commands field pointer is NULL");
+        if (lanes[i] < 0) return fail(NANORTS_INVALID_ARGUMENT, "lanes must be >= 0");
+        if (lanes[i] > 0 && (!keys[i] || (key_lanes[i] != 1 && key_lanes[i] != lanes[i])))
+            return fail(NANORTS_INVALID_ARGUMENT, "each group's key must be [1][2] or [lanes][2]");
+    }
+    const Shape& sh = shapes[0];
+    for (int32_t c0 = 0; c0 < groups; c0 += kGroupsPerLaunch) {
+        GroupsArgs args;
+        std::memset(&args, 0, sizeof(args));
+        args.g = sh.g;
+        int64_t blocks = 0;
+        for (int32_t i = c0; i < groups && i < c0 + kGroupsPerLaunch; ++i) {
+            if (lanes[i] == 0) continue;
+            GroupSlot& s = args.slot[args.count++];
+            s.s = states[i];
+            s.c = commands[i];
+            s.r = results[i];
+            s.key = keys[i];
+            s.key_lanes = key_lanes[i];
+            s.lanes = lanes[i];
+            s.terrain = games[i]->terrain;
+            s.max_cycles = games[i]->max_cycles;
+            s.first_block = (uint32_t)blocks;
+            blocks += (lanes[i] + sh.wpb - 1) / sh.wpb;
+            if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+        }
+        if (blocks == 0) continue;
+        hipLaunchKernelGGL(k_step_groups, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
+                           (hipStream_t)stream, args);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    }
+    return NANORTS_OK;
 }
 
 int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows) {

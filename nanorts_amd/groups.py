@@ -1,0 +1,249 @@
+"""Several groups of games in one batch.
+
+`step_groups` is core.step_groups (src/nanorts/core/__init__.py:63-89,
+src/nanorts/core/cycle.py:137-175): core.step for up to 16 groups of lanes,
+each with its own State, Commands and keys, in one kernel launch per four
+groups when the groups' games share one bucket and unit table (they may
+differ in terrain and horizon), else one launch per group.
+
+`GroupMix` is src/nanorts/bots/mix.py:17-275: a batch of groups, each an
+environment (the JaxMARL facade or a learner-vs-bot seat) with its own lanes,
+published agent-major: every output row is one agent of one lane, groups
+concatenated in order.  Each group steps in its own fused launch (decode,
+bot act, core.step, auto-reset, observe); the rows of all groups must have
+equal shapes, so the groups' environments publish equal observation and
+action spaces and equal infos.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from collections.abc import Sequence
+from typing import Any
+
+import numpy as np
+import torch
+
+from nanorts_amd import native
+from nanorts_amd.env import DeviceGame, EnvironmentState, State, _ptr, _stream
+from nanorts_amd.model import ModelError
+
+MAX_GROUPS = 16
+_COMMAND_FIELDS = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+
+
+def _device_game(holder: Any) -> DeviceGame:
+    """The DeviceGame of a facade (NanoRTS, SeatEnv, GridNet) or a DeviceGame."""
+    if isinstance(holder, DeviceGame):
+        return holder
+    for path in (("dev",), ("env", "dev")):
+        obj = holder
+        for name in path:
+            obj = getattr(obj, name, None)
+        if isinstance(obj, DeviceGame):
+            return obj
+    raise ModelError(f"step_groups takes a facade or a DeviceGame per request, not {type(holder).__name__}")
+
+
+def _tables_equal(a, b) -> bool:
+    return a.bucket == b.bucket and tuple(a.unit_types) == tuple(b.unit_types)
+
+
+def steps_together(games: Sequence[Any]) -> bool:
+    """src/nanorts/core/__init__.py:63-68: more than one game, all on one
+    bucket (and so one unit table and strategy)."""
+    games = [g.game if isinstance(g, DeviceGame) else g for g in games]
+    return 1 < len(games) <= MAX_GROUPS and all(_tables_equal(games[0], g) for g in games[1:])
+
+
+def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]]) -> list[dict[str, torch.Tensor]]:
+    """core.step over every request (key, state, commands, game holder), in
+    place: `key` is uint32 key data [L, 2] or [2] (host data, or an int32
+    device tensor holding it bit for bit); `state` an
+    EnvironmentState or the core State; `commands` int32[L, 2, C] per
+    field; the holder a facade or DeviceGame.  Returns each group's
+    terminated, truncated, reward and admitted event counts."""
+    if not requests:
+        return []
+    devs = [_device_game(holder) for *_, holder in requests]
+    prepared = []
+    for (key, state, commands, _), dev in zip(requests, devs, strict=True):
+        core = state.core_state if isinstance(state, EnvironmentState) else state
+        if not isinstance(core, State):
+            raise ModelError("step_groups takes an EnvironmentState or a core State per request")
+        L = int(core.leaves["time"].shape[0])
+        d = dev.device
+        if isinstance(key, torch.Tensor) and key.device == d and key.dtype == torch.int32:
+            keyt = key.reshape(-1, 2).contiguous()  # key data already on the device, bit for bit
+        else:
+            keyt = torch.as_tensor(np.ascontiguousarray(np.asarray(key.cpu() if isinstance(key, torch.Tensor) else key,
+                                                                   np.uint32).reshape(-1, 2)).view(np.int32), device=d)
+        if keyt.shape[0] not in (1, L):
+            raise ModelError(f"a step_groups key holds {keyt.shape[0]} keys for {L} lanes")
+        cmd = {f: commands[f].to(device=d, dtype=torch.int32).contiguous() for f in _COMMAND_FIELDS}
+        b = dev.game.bucket
+        out = {"terminated": torch.empty(L, dtype=torch.bool, device=d),
+               "truncated": torch.empty(L, dtype=torch.bool, device=d),
+               "reward": torch.empty((L, 2), dtype=torch.float32, device=d),
+               "admitted_harvest": torch.empty((L, 2), dtype=torch.int32, device=d),
+               "admitted_return": torch.empty((L, 2), dtype=torch.int32, device=d),
+               "admitted_produce": torch.empty((L, 2, b.unit_type_capacity), dtype=torch.int32, device=d),
+               "admitted_attack": torch.empty((L, 2, 3), dtype=torch.int32, device=d)}
+        leaves = core.leaves
+        st = native.State(*[_ptr(leaves[name]) for name in native.STATE_FIELDS[:-2]], None, None)
+        prepared.append((L, keyt, cmd, out, st))
+    lib = native.load()
+    results = [p[3] for p in prepared]
+    if len(devs) > 1 and all(_tables_equal(devs[0].game, d.game) for d in devs[1:]):
+        for c0 in range(0, len(prepared), MAX_GROUPS):
+            part, pdevs = prepared[c0:c0 + MAX_GROUPS], devs[c0:c0 + MAX_GROUPS]
+            G = len(part)
+            games = (ctypes.POINTER(native.Game) * G)(*[ctypes.pointer(d.struct) for d in pdevs])
+            states = (native.State * G)(*[p[4] for p in part])
+            lanes = (ctypes.c_int64 * G)(*[p[0] for p in part])
+            keys = (ctypes.c_void_p * G)(*[_ptr(p[1]) for p in part])
+            key_lanes = (ctypes.c_int64 * G)(*[p[1].shape[0] for p in part])
+            cmds = (native.Commands * G)(*[native.Commands(*[_ptr(p[2][f]) for f in _COMMAND_FIELDS]) for p in part])
+            outs = (native.StepResults * G)(*[native.StepResults(*[_ptr(p[3][f]) for f, _ in
+                                                                   native.StepResults._fields_]) for p in part])
+            native.check(lib.nanorts_step_groups(_stream(), G, games, states, lanes, keys, key_lanes, cmds, outs),
+                         "nanorts_step_groups")
+        return results
+    for dev, (L, keyt, cmd, out, st) in zip(devs, prepared, strict=True):
+        c = native.Commands(*[_ptr(cmd[f]) for f in _COMMAND_FIELDS])
+        r = native.StepResults(*[_ptr(out[f]) for f, _ in native.StepResults._fields_])
+        native.check(lib.nanorts_step(_stream(), dev.ref, st, L, _ptr(keyt), keyt.shape[0], c, r), "nanorts_step")
+    return results
+
+
+# ---------------------------------------------------------------------------
+# GroupMix
+# ---------------------------------------------------------------------------
+@dataclasses.dataclass(frozen=True)
+class Group:
+    """src/nanorts/bots/mix.py:17-19"""
+
+    environment: Any
+    lanes: int
+
+
+def _concat(parts: list[Any]) -> Any:
+    """Concatenate matching trees of tensors (dicts, dataclasses) along dim 0."""
+    first = parts[0]
+    if isinstance(first, torch.Tensor):
+        return torch.cat(parts)
+    if isinstance(first, dict):
+        return {k: _concat([p[k] for p in parts]) for k in first}
+    if dataclasses.is_dataclass(first):
+        return type(first)(**{f.name: _concat([getattr(p, f.name) for p in parts])
+                              for f in dataclasses.fields(first)})
+    raise ModelError(f"GroupMix cannot concatenate {type(first).__name__}")
+
+
+def _agents(env: Any) -> list[str]:
+    return list(env.agents)
+
+
+def _agent_major(per_agent: dict[str, Any], env: Any) -> Any:
+    return _concat([per_agent[a] for a in _agents(env)])
+
+
+def _info_rows(infos: dict[str, Any], env: Any) -> dict[str, Any]:
+    agents = _agents(env)
+    return {name: (_agent_major(value, env) if isinstance(value, dict) and list(value) == agents
+                   else _concat([value] * len(agents)))
+            for name, value in infos.items()}
+
+
+def _facade(env: Any) -> Any:
+    return getattr(env, "env", env)
+
+
+def _row_signature(env: Any) -> tuple:
+    """What every row of a group looks like: the observation and action
+    spaces and the infos a step publishes."""
+    f = _facade(env)
+    y = f.layout
+    return (y.surface, y.partial_observability, y.feature_maps_shape, y.actions_shape, y.mask_width,
+            y.final_observation, y.reward_components)
+
+
+class GroupMix:
+    """src/nanorts/bots/mix.py:22-275, batched over each group's lanes."""
+
+    def __init__(self, groups: Sequence[Group]) -> None:
+        self.groups = tuple(groups)
+        if not self.groups:
+            raise ModelError("GroupMix refuses an empty group list")
+        for index, group in enumerate(self.groups):
+            if not isinstance(group.lanes, int) or isinstance(group.lanes, bool) or group.lanes < 1:
+                raise ModelError(f"GroupMix refuses group {index}: lanes={group.lanes!r} is not a positive int")
+        signatures = [_row_signature(group.environment) for group in self.groups]
+        for index, signature in enumerate(signatures[1:], start=1):
+            if signature != signatures[0]:
+                raise ModelError(f"GroupMix refuses group {index}: its rows are not group 0's - the groups' "
+                                 "environments must publish equal observation and action spaces and equal infos, "
+                                 "so equal final_observation and reward_components flags")
+
+    @property
+    def lanes(self) -> int:
+        return sum(group.lanes for group in self.groups)
+
+    @property
+    def rows(self) -> int:
+        return sum(self._row_counts())
+
+    def slices(self) -> tuple[slice, ...]:
+        return tuple(self._bounds(self._row_counts()))
+
+    def reset(self, roots) -> tuple[Any, tuple[Any, ...]]:
+        """uint32 key data [lanes, 2] -> (agent-major observations, per-group states)."""
+        roots = np.asarray(roots.cpu() if isinstance(roots, torch.Tensor) else roots, np.uint32).reshape(-1, 2)
+        if roots.shape[0] != self.lanes:
+            raise ModelError(f"GroupMix.reset takes {self.lanes} roots, got {roots.shape[0]}")
+        observations, states = [], []
+        for group, bound in zip(self.groups, self._bounds(self._lane_counts()), strict=True):
+            obs, state = group.environment.reset(roots[bound])
+            observations.append(_agent_major(obs, group.environment))
+            states.append(state)
+        return _concat(observations), tuple(states)
+
+    def step(self, key, states: tuple[Any, ...], actions: torch.Tensor, *, donate: bool = False):
+        """Actions int32[rows, C, 7], agent-major per group -> (observations,
+        next states, rewards, dones, infos), each agent-major."""
+        if actions.shape[0] != self.rows:
+            raise ModelError(f"GroupMix.step takes {self.rows} action rows, got {actions.shape[0]}")
+        observations, following, rewards, dones, infos = [], [], [], [], []
+        for group, state, bound in zip(self.groups, states, self._bounds(self._row_counts()), strict=True):
+            env = group.environment
+            rows = actions[bound]
+            per_agent = dict(zip(_agents(env), torch.split(rows, group.lanes), strict=True))
+            obs, nxt, reward, done, info = env.step(key, state, per_agent, donate=donate)
+            observations.append(_agent_major(obs, env))
+            following.append(nxt)
+            rewards.append(_agent_major(reward, env))
+            dones.append(_agent_major({a: done[a] for a in _agents(env)}, env))
+            infos.append(_info_rows(info, env))
+        return _concat(observations), tuple(following), _concat(rewards), _concat(dones), _concat(infos)
+
+    def get_avail_actions(self, states: tuple[Any, ...]) -> torch.Tensor:
+        return _concat([_agent_major(group.environment.get_avail_actions(state), group.environment)
+                        for group, state in zip(self.groups, states, strict=True)])
+
+    def get_slot_cells(self, states: tuple[Any, ...]) -> torch.Tensor:
+        return _concat([_agent_major(group.environment.get_slot_cells(state), group.environment)
+                        for group, state in zip(self.groups, states, strict=True)])
+
+    def _lane_counts(self) -> list[int]:
+        return [group.lanes for group in self.groups]
+
+    def _row_counts(self) -> list[int]:
+        return [group.lanes * len(_agents(group.environment)) for group in self.groups]
+
+    @staticmethod
+    def _bounds(sizes: list[int]) -> list[slice]:
+        out, start = [], 0
+        for size in sizes:
+            out.append(slice(start, start + size))
+            start += size
+        return out

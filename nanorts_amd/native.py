@@ -90,6 +90,7 @@ class GridNetResults(ctypes.Structure):
 # Every extern "C" symbol include/nanorts_amd.h declares.
 EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
+    "nanorts_step_groups",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
@@ -108,6 +109,7 @@ _SIGNATURES = {
     "nanorts_shared_opt_in": (ctypes.c_int64, [_VP, _I64]),
     "nanorts_self_check": (ctypes.c_char_p, [_VP, _I64]),
     "nanorts_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I64, Commands, StepResults]),
+    "nanorts_step_groups": (ctypes.c_int, [_VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "nanorts_legality": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
     "nanorts_legality_words": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
     "nanorts_avail_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _VP]),
