@@ -1036,10 +1036,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 }
             }
             wave_sync();
-        }
-        {
             // env.step: core.step keyed by fold_in(env root, episode)
-            NR_ROLLOUT_PHASE
             if (fused && listed) {
                 admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
             } else if (fused || !admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
@@ -1057,9 +1054,6 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             NR_ROLLOUT_PHASE
             complete(g, hdr, e, lane);
             decide_counted(e, lane);
-        }
-        {
-            NR_ROLLOUT_PHASE
             nanorts_env_results r = {};
             const int64_t tt = (int64_t)a.t0 + t;
             if (a.out.rewards) r.reward = a.out.rewards + tt * lanes * 2;
@@ -1069,9 +1063,6 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
                 fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
             }
-        }
-        {
-            NR_ROLLOUT_PHASE
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
             // ring slot (t0 + t) % depth in 32 bits (a mask for powers of two)
