@@ -1403,7 +1403,7 @@ typedef struct rollout_job {
     nro_state* s;
     const uint32_t* sample_key;
     int32_t step0, steps, partial;
-    int64_t L, begin, end;
+    int64_t L, begin, end, env0;
     float* rewards;
     uint8_t* dones;
     int32_t* actions;
@@ -1427,7 +1427,7 @@ static void* rollout_worker(void* arg) {
             int32_t winner;
             int32_t scalars[8];
             avail_rows_one(g, &e, w.rows);
-            sample_env(g, w.rows, job->sample_key, step, l, w.actions);
+            sample_env(g, w.rows, job->sample_key, step, job->env0 + l, w.actions);
             if (job->actions)
                 memcpy(job->actions + ((size_t)t * job->L + l) * 2 * C * 7, w.actions, sizeof(int32_t) * 2 * C * 7);
             env_step_one(g, job->initial, &e, w.actions, job->partial, reward, &done, &terminated, &truncated,
@@ -1449,7 +1449,8 @@ static void* rollout_worker(void* arg) {
 
 int32_t nro_rollout(const nro_game* g, const nro_state* initial, nro_state* s, const uint32_t sample_key[2],
                     int32_t step0, int32_t steps, int64_t L, int32_t partial, int32_t threads, float* rewards,
-                    uint8_t* dones, int32_t* actions, uint8_t* last_feature_maps, int32_t* last_scalars) {
+                    uint8_t* dones, int32_t* actions, uint8_t* last_feature_maps, int32_t* last_scalars,
+                    int64_t env0) {
     if (threads < 1) threads = 1;
     if (threads > L) threads = (int32_t)(L > 0 ? L : 1);
     pthread_t* ids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
@@ -1464,6 +1465,7 @@ int32_t nro_rollout(const nro_game* g, const nro_state* initial, nro_state* s, c
         j->steps = steps;
         j->partial = partial;
         j->L = L;
+        j->env0 = env0;
         j->begin = L * t / threads;
         j->end = L * (t + 1) / threads;
         j->rewards = rewards;

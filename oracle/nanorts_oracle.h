@@ -157,14 +157,15 @@ void nro_env_step(const nro_game* g, const nro_state* initial, nro_state* s, con
                   int64_t L, int32_t partial, nro_env_out* out);
 
 /* Multi-threaded synthetic rollout: masks -> sample -> env.step for `steps`
- * cycles over envs [0, L).  Per-step rewards [steps][L][2] and dones
+ * cycles over envs [0, L), which the sampler numbers env0 + l.  Per-step
+ * rewards [steps][L][2] and dones
  * [steps][L] are recorded when non-NULL; actions [steps][L][2][C][7] too.
  * Feature maps and scalars of the last step go to `last_*` when non-NULL.
  * Returns the number of threads used. */
 int32_t nro_rollout(const nro_game* g, const nro_state* initial, nro_state* s,
                     const uint32_t sample_key[2], int32_t step0, int32_t steps, int64_t L,
                     int32_t partial, int32_t threads, float* rewards, uint8_t* dones,
-                    int32_t* actions, uint8_t* last_feature_maps, int32_t* last_scalars);
+                    int32_t* actions, uint8_t* last_feature_maps, int32_t* last_scalars, int64_t env0);
 
 /* Carry of an abstraction-family bot (AbstractActions,
  * src/nanorts/bots/abstraction.py:70-81): [L][C] rows and next_order [L]. */

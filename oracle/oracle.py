@@ -254,7 +254,7 @@ class Oracle:
         return out
 
     def rollout(self, state, sample_key, step0: int, steps: int, partial: bool, threads: int = 1,
-                record_actions: bool = False, record: bool = True) -> dict[str, np.ndarray]:
+                record_actions: bool = False, record: bool = True, env0: int = 0) -> dict[str, np.ndarray]:
         L = state["time"].shape[0]
         b = self.game.bucket
         key = np.ascontiguousarray(np.asarray(sample_key, np.uint32).reshape(2))
@@ -269,7 +269,7 @@ class Oracle:
             ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)), _ptr(key),
             ctypes.c_int32(step0), ctypes.c_int32(steps), ctypes.c_int64(L), ctypes.c_int32(int(partial)),
             ctypes.c_int32(threads), _ptr(out["rewards"]), _ptr(out["dones"]), _ptr(out["actions"]),
-            _ptr(out["feature_maps"]), _ptr(out["scalars"]))
+            _ptr(out["feature_maps"]), _ptr(out["scalars"]), ctypes.c_int64(env0))
         out["threads"] = used
         return out
 
