@@ -130,6 +130,7 @@ typedef struct nanorts_env_results {
     uint8_t* final_feature_maps; /* [L][2][H][W][6] of the ending state */
     int32_t* final_scalars;      /* [L][2][4] */
     float* reward_components;    /* [L][2][6] MicroRTS-Py shaped components */
+    int32_t* spawn_overflow;     /* [L][2] telemetry of the ending state */
 } nanorts_env_results;
 
 /* Outputs of a fused rollout.  Any pointer may be NULL. */
@@ -196,6 +197,7 @@ typedef struct nanorts_gridnet_results {
     uint8_t* spawn_overflowed;/* [L] */
     void* final_planes;       /* planes of the ending state, in observation's planes form */
     nanorts_gridnet_obs observation; /* of the post-reset state */
+    int32_t* spawn_overflow;  /* [L][2] telemetry of the ending state */
 } nanorts_gridnet_results;
 
 const char* nanorts_build_id(void);
@@ -283,6 +285,21 @@ int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_sta
  * observe (src/nanorts/adapters/jaxmarl/env.py:72-184). */
 int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                      const int32_t* actions, int32_t partial, nanorts_env_results results);
+
+/* env.step_env of the JaxMARL facade: as nanorts_env_step without the
+ * auto-reset, so the state, the observation and the rewards are those of the
+ * ending state (src/nanorts/adapters/jaxmarl/facade.py:130-165, transition
+ * in src/nanorts/adapters/jaxmarl/env.py:170-171). */
+int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, int32_t partial, nanorts_env_results results);
+
+/* The JaxMARL request (src/nanorts/adapters/jaxmarl/env.py:181-184):
+ * decode_actions of int32[L][2][C][7] action rows into Commands
+ * (src/nanorts/adapters/jaxmarl/actions.py:61-84) and, when `episode_keys`
+ * is not NULL, the episode roots fold_in(environment_root, episode_index)
+ * as uint32[L][2]. */
+int nanorts_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, nanorts_command_buffers commands, uint32_t* episode_keys);
 
 /* The synthetic harness's integer uniform-over-legal sampler: actions
  * int32[L][2][C][7] from avail words uint32[L][2][C][3] for rollout step

@@ -140,6 +140,7 @@ class SeatEnv:
             "truncated": torch.empty(L, dtype=torch.bool, device=d),
             "winner": torch.empty(L, dtype=torch.int32, device=d),
             "spawn_overflowed": torch.empty(L, dtype=torch.bool, device=d),
+            "spawn_overflow": torch.empty((L, 2), dtype=torch.int32, device=d),
         }
         maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
         scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d)
@@ -148,7 +149,7 @@ class SeatEnv:
         results = native.EnvResults(
             _ptr(out["reward"]), _ptr(out["done"]), _ptr(out["terminated"]), _ptr(out["truncated"]),
             _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
-            None)
+            None, _ptr(out["spawn_overflow"]))
         native.check(env.lib.nanorts_seat_step(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                self.bot.trained, self.learner, _carry_struct(nxt.carry), _ptr(acts),
                                                env.partial, results), "nanorts_seat_step")
@@ -156,7 +157,7 @@ class SeatEnv:
         obs = env._symbolic(maps, scalars)[SEAT_RULES[p]]
         infos: dict[str, Any] = {
             "terminated": out["terminated"], "truncated": out["truncated"], "winner": out["winner"],
-            "telemetry": {"spawn_overflow": es.core_state.spawn_overflow},
+            "telemetry": {"spawn_overflow": out["spawn_overflow"]},
             "spawn_overflowed": out["spawn_overflowed"], "final_valid": out["done"],
         }
         if env.final_observation:

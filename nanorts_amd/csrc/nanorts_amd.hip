@@ -641,7 +641,7 @@ NR_DEV void stage_actions(const KGame& g, const Env& e, int64_t l, const int32_t
 
 // After core.step: outcome, rewards, optional final observation, auto-reset.
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
-                        const nanorts_env_results& r, bool events, bool fast_obs = false) {
+                        const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true) {
     const bool over = uni(e.sc[S_GAME_OVER]) != 0;
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t winner = uni(e.sc[S_WINNER]);
@@ -655,6 +655,10 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
         if (r.truncated) r.truncated[l] = trunc ? 1 : 0;
         if (r.winner) r.winner[l] = winner;
         if (r.spawn_overflowed) r.spawn_overflowed[l] = (e.sc[S_SO0] > 0 || e.sc[S_SO1] > 0) ? 1 : 0;
+        if (r.spawn_overflow) {
+            r.spawn_overflow[2 * l] = e.sc[S_SO0];
+            r.spawn_overflow[2 * l + 1] = e.sc[S_SO1];
+        }
     }
     if (events && r.reward_components && lane < 2) {
         // N/adapters/rewards.py:47-71 (encode_components)
@@ -677,12 +681,12 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
     } else if (r.final_feature_maps || r.final_scalars) {
         observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
     }
-    if (done) reset_env(g, h, e, lane);
+    if (done && reset) reset_env(g, h, e, lane);
     return done;
 }
 
 __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanorts_state s, const int32_t* actions, int32_t partial,
-                           nanorts_env_results r) {
+                           nanorts_env_results r, int32_t reset) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
@@ -738,7 +742,7 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
         wave_sync();
         env_core_step(g, hdr, e, lane, k0, k1, events, n, irregular, false);
     }
-    finish_step(g, hdr, e, l, lane, partial != 0, r, events, fast);
+    finish_step(g, hdr, e, l, lane, partial != 0, r, events, fast, reset != 0);
     store_env(g, s, l, e, lane);
     if (fast) {
         const int64_t per = (int64_t)g.cells * 6;
@@ -1282,9 +1286,47 @@ __global__ __launch_bounds__(256) void k_gridnet_step(KGame g, int64_t lanes, na
     er.winner = r.winner;
     er.spawn_overflowed = r.spawn_overflowed;
     er.reward_components = r.reward_components;
+    er.spawn_overflow = r.spawn_overflow;
     finish_step(g, hdr, e, l, lane, false, er, true);
     store_env(g, s, l, e, lane);
     gridnet_observe(g, hdr, e, l, lane, r.observation, r.observation.planes);
+}
+
+// The JaxMARL request (N/adapters/jaxmarl/env.py:181-184): decode_actions
+// (N/adapters/jaxmarl/actions.py:61-84) into Commands, and the episode root
+// fold_in(environment_root, episode_index) that keys core.step.
+__global__ __launch_bounds__(256) void k_decode_actions(KGame g, int64_t lanes, nanorts_state s, const int32_t* actions,
+                                                        nanorts_command_buffers out, uint32_t* keys) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_BIRTH | LD_CELL | LD_PKIND | LD_SCALARS, lane);
+    const int32_t owned = 2 * g.C;
+    for (int32_t p = lane; p < owned; p += kWave) {
+        const int32_t slot = g.N + p;
+        const bool available = e.birth[slot] != kAbsent && e.pkind[slot] == kAbsent;
+        const int32_t* row = actions + (l * owned + p) * 7;
+        const int64_t at = l * owned + p;
+        int32_t kind = kAbsent, dir = kAbsent, none = 0, target = kAbsent, ptype = kAbsent;
+        if (available) {
+            const GridRow r = grid_row(g, row, e.cell[slot]);  // the factor helpers of factors.py:117-151
+            kind = r.kind;
+            dir = r.dir;
+            ptype = r.ptype;
+            target = r.target;
+            none = kind == kKindNone ? 1 : 0;
+        }
+        out.kind[at] = kind;
+        out.direction[at] = dir;
+        out.none_duration[at] = none;
+        out.target_cell[at] = target;
+        out.produced_type[at] = ptype;
+        out.request_order[at] = kAbsent;
+    }
+    if (keys && lane == 0) {
+        uint32_t k0 = (uint32_t)e.sc[S_ROOT0], k1 = (uint32_t)e.sc[S_ROOT1];
+        fold_in(k0, k1, (uint32_t)e.sc[S_EPISODE]);
+        keys[2 * l] = k0;
+        keys[2 * l + 1] = k1;
+    }
 }
 
 // Pixel observations (N/observations/pixels.py:71-88; N/rendering/raster.py:53-127).
@@ -1469,7 +1511,7 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_step_groups,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
+           "nanorts_step_groups,nanorts_env_transition,nanorts_decode_actions,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
            "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against,nanorts_gridnet_sample_actions";
 }
 
@@ -1682,7 +1724,30 @@ int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state
     if (!state.environment_root || !state.episode_index)
         return fail(NANORTS_INVALID_ARGUMENT, "env.step needs environment_root and episode_index");
     if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
-    return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results);
+    return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results, 1);
+}
+
+int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, int32_t partial, nanorts_env_results results) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!state.environment_root || !state.episode_index)
+        return fail(NANORTS_INVALID_ARGUMENT, "env.step_env needs environment_root and episode_index");
+    return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results, 0);
+}
+
+int nanorts_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                           const int32_t* actions, nanorts_command_buffers commands, uint32_t* episode_keys) {
+    NR_SHAPE(game)
+    NR_STATE(state)
+    if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
+    if (!commands.kind || !commands.direction || !commands.none_duration || !commands.target_cell ||
+        !commands.produced_type || !commands.request_order)
+        return fail(NANORTS_INVALID_ARGUMENT, "a Commands buffer pointer is NULL");
+    if (episode_keys && (!state.environment_root || !state.episode_index))
+        return fail(NANORTS_INVALID_ARGUMENT, "episode keys need environment_root and episode_index");
+    return launch(k_decode_actions, sh, lanes, (hipStream_t)stream, state, actions, commands, episode_keys);
 }
 
 static bool bot_args(const nanorts_game* game, Shape* sh, BotArgs* a, int32_t strategy, int32_t trained_type,

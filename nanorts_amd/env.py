@@ -137,6 +137,24 @@ class JaxMARLLayout:
         return AGENTS
 
 
+def _components(stepped: dict[str, torch.Tensor], over: torch.Tensor, winner: torch.Tensor) -> torch.Tensor:
+    """encode_components (src/nanorts/adapters/rewards.py:47-71) from a
+    core.step result's event counts and the ending state's game_over and
+    winner: float32[L, 2, 6]."""
+    prod, att = stepped["admitted_produce"], stepped["admitted_attack"]
+    L = prod.shape[0]
+    out = torch.zeros((L, 2, 6), dtype=torch.float32, device=prod.device)
+    for p in range(2):
+        o = 1 - p
+        out[:, p, 1] = (stepped["admitted_harvest"][:, p] + stepped["admitted_return"][:, p]).float()
+        out[:, p, 2] = prod[:, p, 3].float()
+        out[:, p, 3] = (prod[:, p, 1] + prod[:, p, 2]).float()
+        out[:, p, 4] = (att[:, p, o + 1] - att[:, p, p + 1]).float()
+        out[:, p, 5] = (prod[:, p, 4] + prod[:, p, 5] + prod[:, p, 6]).float()
+        out[:, p, 0] = torch.where(over, torch.where(winner == p, 1.0, -1.0), 0.0)
+    return out
+
+
 class DeviceGame:
     """The static game on the device: the native game struct, terrain and the
     decided initial State of one env."""
@@ -267,6 +285,68 @@ class NanoRTS:
         del key
         if reset_state is not None:
             raise ModelError("NanoRTS.step refuses a reset_state: the auto-reset is the lifecycle's own")
+        return self._fused_step(state, actions, donate, reset=True)
+
+    def step_env(self, key, state: EnvironmentState, actions: dict[str, torch.Tensor], *, donate: bool = False):
+        """env.step_env (src/nanorts/adapters/jaxmarl/facade.py:130-165): the
+        transition without the auto-reset; the observation, the final
+        observation and the state are the ending state's."""
+        del key
+        return self._fused_step(state, actions, donate, reset=False)
+
+    def step_request(self, state: EnvironmentState, actions: dict[str, torch.Tensor]):
+        """env.step_request (src/nanorts/adapters/jaxmarl/facade.py:121-122):
+        ((episode-root keys int32[L, 2] holding uint32 key data, the core
+        State, Commands int32[L, 2, C] per field), None), ready for
+        groups.step_groups or core_step."""
+        L = state.num_envs
+        b = self.bucket
+        d = self.device
+        acts = self._stack_actions(actions, L)
+        commands = {f: torch.empty((L, 2, b.per_player_capacity), dtype=torch.int32, device=d)
+                    for f, _ in native.Commands._fields_}
+        keys = torch.empty((L, 2), dtype=torch.int32, device=d)
+        bufs = native.Commands(*[_ptr(commands[f]) for f, _ in native.Commands._fields_])
+        native.check(self.lib.nanorts_decode_actions(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs,
+                                                     _ptr(keys)), "nanorts_decode_actions")
+        return (keys, state.core_state, commands), None
+
+    def step_response(self, state: EnvironmentState, carry, stepped: dict[str, torch.Tensor]):
+        """env.step_response (src/nanorts/adapters/jaxmarl/facade.py:124-128,
+        respond in src/nanorts/adapters/jaxmarl/env.py:99-127) on a state that
+        core.step has already advanced in place (`stepped` is its
+        terminated / truncated / reward / admitted event counts): rewards,
+        the ending state's observation, auto-reset and the next observation.
+        The state is updated in place."""
+        del carry
+        core = state.core_state
+        done = (stepped["terminated"] | stepped["truncated"]).to(torch.bool)
+        winner = core.winner.reshape(-1).to(torch.int32).clone()
+        telemetry = core.spawn_overflow.clone()
+        final = self.get_obs(state) if self.final_observation else None
+        over = core.game_over.reshape(-1).to(torch.bool)
+        comps = _components(stepped, over, winner) if self.layout.reward_components else None
+        self.reset_where_done(state, done)
+        obs = self.get_obs(state)
+        reward = stepped["reward"]
+        infos: dict[str, Any] = {
+            "terminated": stepped["terminated"].to(torch.bool), "truncated": stepped["truncated"].to(torch.bool),
+            "winner": winner, "telemetry": {"spawn_overflow": telemetry},
+            "spawn_overflowed": (telemetry > 0).any(dim=1), "final_valid": done,
+        }
+        if final is not None:
+            infos["final_observation"] = final
+        if comps is not None:
+            infos["reward_components"] = {agent: comps[:, p] for p, agent in enumerate(self.agents)}
+        return (obs, state, {agent: reward[:, p] for p, agent in enumerate(self.agents)},
+                {agent: done for agent in self.agents} | {ALL_AGENTS: done}, infos)
+
+    @property
+    def agent_classes(self) -> dict[str, list[str]]:
+        """src/nanorts/adapters/jaxmarl/facade.py:186-188"""
+        return {"player": list(self.agents)}
+
+    def _fused_step(self, state: EnvironmentState, actions: dict[str, torch.Tensor], donate: bool, reset: bool):
         nxt = state if donate else state.clone()
         L = nxt.num_envs
         b = self.bucket
@@ -279,32 +359,40 @@ class NanoRTS:
             "truncated": torch.empty(L, dtype=torch.bool, device=d),
             "winner": torch.empty(L, dtype=torch.int32, device=d),
             "spawn_overflowed": torch.empty(L, dtype=torch.bool, device=d),
+            "spawn_overflow": torch.empty((L, 2), dtype=torch.int32, device=d),
         }
         symbolic = self.layout.surface == "symbolic"
         # the pixel surface renders from the symbolic maps the step writes
         maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
         scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d)
         fmaps = fscal = None
-        if self.final_observation:
+        if self.final_observation and reset:
             fmaps = torch.empty_like(maps)
             fscal = torch.empty_like(scalars)
         comps = torch.empty((L, 2, 6), dtype=torch.float32, device=d) if self.layout.reward_components else None
         results = native.EnvResults(
             _ptr(out["reward"]), _ptr(out["done"]), _ptr(out["terminated"]), _ptr(out["truncated"]),
             _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
-            _ptr(comps))
-        native.check(self.lib.nanorts_env_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), self.partial,
-                                               results), "nanorts_env_step")
+            _ptr(comps), _ptr(out["spawn_overflow"]))
+        if reset:
+            native.check(self.lib.nanorts_env_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), self.partial,
+                                                   results), "nanorts_env_step")
+        else:
+            native.check(self.lib.nanorts_env_transition(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts),
+                                                         self.partial, results), "nanorts_env_transition")
         obs = self._symbolic(maps, scalars) if symbolic else self._pixels(maps, scalars)
         rewards = {agent: out["reward"][:, p] for p, agent in enumerate(self.agents)}
         dones = {agent: out["done"] for agent in self.agents} | {ALL_AGENTS: out["done"]}
         infos: dict[str, Any] = {
             "terminated": out["terminated"], "truncated": out["truncated"], "winner": out["winner"],
-            "telemetry": {"spawn_overflow": nxt.core_state.spawn_overflow},
+            "telemetry": {"spawn_overflow": out["spawn_overflow"]},
             "spawn_overflowed": out["spawn_overflowed"], "final_valid": out["done"],
         }
         if self.final_observation:
-            infos["final_observation"] = self._symbolic(fmaps, fscal) if symbolic else self._pixels(fmaps, fscal)
+            if reset:
+                infos["final_observation"] = self._symbolic(fmaps, fscal) if symbolic else self._pixels(fmaps, fscal)
+            else:
+                infos["final_observation"] = obs
         if comps is not None:
             infos["reward_components"] = {agent: comps[:, p] for p, agent in enumerate(self.agents)}
         return obs, nxt, rewards, dones, infos

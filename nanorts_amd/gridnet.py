@@ -288,11 +288,12 @@ class GridNet:
         flags = {k: torch.empty(L, dtype=torch.bool, device=d)
                  for k in ("terminated", "truncated", "done", "spawn_overflowed")}
         winner = torch.empty(L, dtype=torch.int32, device=d)
+        telemetry = torch.empty((L, PLAYER_COUNT), dtype=torch.int32, device=d)
         final = torch.empty((L, *y.planes_shape), dtype=y.planes_dtype, device=d)
         obs, struct = self._obs_buffers(L)
         results = native.GridNetResults(_ptr(comps), _ptr(rdones), _ptr(flags["terminated"]), _ptr(flags["truncated"]),
                                         _ptr(flags["done"]), _ptr(winner), _ptr(flags["spawn_overflowed"]),
-                                        _ptr(final), struct)
+                                        _ptr(final), struct, _ptr(telemetry))
         if given is None:
             code = self.lib.nanorts_gridnet_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), results)
             native.check(code, "nanorts_gridnet_step")
@@ -303,7 +304,7 @@ class GridNet:
             native.check(code, "nanorts_gridnet_step_against")
         return GridNetStep(environment_state=nxt, observation=obs, reward_components=comps, reward_dones=rdones,
                            terminated=flags["terminated"], truncated=flags["truncated"], done=flags["done"],
-                           winner=winner, telemetry={"spawn_overflow": nxt.core_state.spawn_overflow},
+                           winner=winner, telemetry={"spawn_overflow": telemetry},
                            spawn_overflowed=flags["spawn_overflowed"], final_observation=final,
                            final_valid=flags["done"])
 

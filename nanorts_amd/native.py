@@ -59,7 +59,7 @@ class StepResults(ctypes.Structure):
 class EnvResults(ctypes.Structure):
     _fields_ = [(name, _VP) for name in
                 ("reward", "done", "terminated", "truncated", "winner", "spawn_overflowed", "feature_maps", "scalars",
-                 "final_feature_maps", "final_scalars", "reward_components")]
+                 "final_feature_maps", "final_scalars", "reward_components", "spawn_overflow")]
 
 
 class RolloutResults(ctypes.Structure):
@@ -84,13 +84,13 @@ class GridNetObs(ctypes.Structure):
 class GridNetResults(ctypes.Structure):
     _fields_ = [(name, _VP) for name in
                 ("reward_components", "reward_dones", "terminated", "truncated", "done", "winner",
-                 "spawn_overflowed", "final_planes")] + [("observation", GridNetObs)]
+                 "spawn_overflowed", "final_planes")] + [("observation", GridNetObs), ("spawn_overflow", _VP)]
 
 
 # Every extern "C" symbol include/nanorts_amd.h declares.
 EXPORTS = (
     "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
-    "nanorts_step_groups",
+    "nanorts_step_groups", "nanorts_env_transition", "nanorts_decode_actions",
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
@@ -119,6 +119,8 @@ _SIGNATURES = {
     "nanorts_pixels_from_maps": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _VP]),
     "nanorts_reset_where_done": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
     "nanorts_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
+    "nanorts_env_transition": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
+    "nanorts_decode_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, _VP]),
     "nanorts_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
     "nanorts_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
     "nanorts_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
