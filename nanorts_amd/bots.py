@@ -92,15 +92,17 @@ class SeatEnv:
     with a static seat ("player_0" or "player_1")."""
 
     def __init__(self, bot: Bot, *, scenario: GameConfig, utt: UnitTypeTableVersion | None = None,
-                 seat: str = "player_0", partial_observability: bool = False, final_observation: bool = True,
+                 seat: str = "player_0", surface: str = "symbolic", partial_observability: bool = False,
+                 final_observation: bool = True, feature_dtype: Any = None, reward_components: bool = False,
                  device: str | torch.device | None = None):
         if seat not in SEAT_RULES:
             raise ModelError(f"SeatEnv refuses seat={seat!r}: this build takes {list(SEAT_RULES)}")
         if bot.strategy not in (WORKER_RUSH, BARRACKS_RUSH):
             raise ModelError(f"SeatEnv refuses bot {bot.name!r}: the rush family is built")
         game = scenario if utt is None else with_unit_type_table(scenario, utt)
-        self.env = NanoRTS(game, partial_observability=partial_observability, final_observation=final_observation,
-                           device=device)
+        self.env = NanoRTS(game, surface=surface, partial_observability=partial_observability,
+                           final_observation=final_observation, feature_dtype=feature_dtype,
+                           reward_components=reward_components, device=device)
         self.bot = bot
         self.seat = seat
         self.learner = SEAT_RULES.index(seat)
@@ -146,22 +148,26 @@ class SeatEnv:
         scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=d)
         fmaps = torch.empty_like(maps) if env.final_observation else None
         fscal = torch.empty_like(scalars) if env.final_observation else None
+        comps = torch.empty((L, 2, 6), dtype=torch.float32, device=d) if env.layout.reward_components else None
         results = native.EnvResults(
             _ptr(out["reward"]), _ptr(out["done"]), _ptr(out["terminated"]), _ptr(out["truncated"]),
             _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
-            None, _ptr(out["spawn_overflow"]))
+            _ptr(comps), _ptr(out["spawn_overflow"]))
         native.check(env.lib.nanorts_seat_step(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                self.bot.trained, self.learner, _carry_struct(nxt.carry), _ptr(acts),
                                                env.partial, results), "nanorts_seat_step")
         p = self.learner
-        obs = env._symbolic(maps, scalars)[SEAT_RULES[p]]
+        publish = env._symbolic if env.layout.surface == "symbolic" else env._pixels
+        obs = publish(maps, scalars)[SEAT_RULES[p]]
         infos: dict[str, Any] = {
             "terminated": out["terminated"], "truncated": out["truncated"], "winner": out["winner"],
             "telemetry": {"spawn_overflow": out["spawn_overflow"]},
             "spawn_overflowed": out["spawn_overflowed"], "final_valid": out["done"],
         }
         if env.final_observation:
-            infos["final_observation"] = {LEARNER: env._symbolic(fmaps, fscal)[SEAT_RULES[p]]}
+            infos["final_observation"] = {LEARNER: publish(fmaps, fscal)[SEAT_RULES[p]]}
+        if comps is not None:
+            infos["reward_components"] = {LEARNER: comps[:, p]}
         return ({LEARNER: obs}, nxt, {LEARNER: out["reward"][:, p]}, {LEARNER: out["done"], ALL_AGENTS: out["done"]},
                 infos)
 
@@ -190,6 +196,62 @@ class SeatEnv:
                                                   int(step0), int(steps), env.partial, int(env0), results),
                      "nanorts_seat_rollout")
         return {"rewards": rewards, "dones": dones, "actions": actions, "feature_maps": maps, "scalars": scalars}
+
+    def step_request(self, state: SeatState, actions: dict[str, torch.Tensor]):
+        """seat.step_request (src/nanorts/bots/seat.py:100-112, 249-258): the
+        bot's act on a copy of the carry, the learner's decoded rows and the
+        bot's Commands merged ((episode-root keys, core State, Commands),
+        the bot's new carry), ready for groups.step_groups."""
+        env = self.env
+        es = state.environment_state
+        L = es.num_envs
+        C = env.bucket.per_player_capacity
+        acts = torch.as_tensor(actions[LEARNER], device=self.device)
+        if acts.dtype != torch.int32 or tuple(acts.shape) != (L, C, 7):
+            raise ModelError(f"learner actions must be int32[{L}, {C}, 7]")
+        carry = {k: v.clone() for k, v in state.carry.items()}
+        bot_player = 1 - self.learner
+        bot_cmds = abstraction_act(env, es, carry, self.bot, bot_player)
+        rows = torch.zeros((L, 2, C, 7), dtype=torch.int32, device=self.device)
+        rows[:, self.learner] = acts
+        (keys, core, cmds), _ = env.step_request(es, {agent: rows[:, p] for p, agent in enumerate(env.agents)})
+        for name in cmds:
+            cmds[name][:, bot_player] = bot_cmds[name][:, bot_player]
+        return (keys, core, cmds), carry
+
+    def step_response(self, state: SeatState, carry: dict[str, torch.Tensor], stepped: dict[str, torch.Tensor]):
+        """seat.step_response (src/nanorts/bots/seat.py:115-152, 260-272) on a
+        state that core.step has advanced in place: the facade's response for
+        the learner, and the bot's new carry, emptied where the game ended.
+        The state is updated in place."""
+        obs, es, rewards, dones, infos = self.env.step_response(state.environment_state, None, stepped)
+        done = dones[ALL_AGENTS]
+        fresh = empty_actions(es.num_envs, self.env.bucket.per_player_capacity, self.device)
+        for name, value in carry.items():
+            mask = done.reshape((-1,) + (1,) * (value.dim() - 1))
+            state.carry[name] = torch.where(mask, fresh[name], value)
+        p = SEAT_RULES[self.learner]
+        out_infos = dict(infos)
+        if "final_observation" in infos:
+            out_infos["final_observation"] = {LEARNER: infos["final_observation"][p]}
+        if "reward_components" in infos:
+            out_infos["reward_components"] = {LEARNER: infos["reward_components"][p]}
+        return ({LEARNER: obs[p]}, state, {LEARNER: rewards[p]}, {LEARNER: done, ALL_AGENTS: done}, out_infos)
+
+    def observation_space(self, agent: str) -> dict[str, Any]:
+        if agent != LEARNER:
+            raise ModelError(f"SeatEnv has the one agent {LEARNER!r}, not {agent!r}")
+        return self.env.observation_space(SEAT_RULES[self.learner])
+
+    def action_space(self, agent: str) -> dict[str, Any]:
+        if agent != LEARNER:
+            raise ModelError(f"SeatEnv has the one agent {LEARNER!r}, not {agent!r}")
+        return self.env.action_space(SEAT_RULES[self.learner])
+
+    @property
+    def agent_classes(self) -> dict[str, list[str]]:
+        """src/nanorts/bots/seat.py:330-332"""
+        return {LEARNER: [LEARNER]}
 
     def get_avail_actions(self, state: SeatState, *, form: str = "rows") -> dict[str, torch.Tensor]:
         return {LEARNER: self.env.get_avail_actions(state.environment_state, form=form)[SEAT_RULES[self.learner]]}

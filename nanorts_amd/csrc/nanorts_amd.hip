@@ -825,8 +825,9 @@ __global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanor
     // the carry is written before the step, whose phases reuse the region
     settle_carry(g, b, a.y, l, a.carry, lane);
     wave_sync();
-    core_step(g, hdr, e, lane, k0, k1, false);
-    if (finish_step(g, hdr, e, l, lane, partial != 0, r, false)) clear_carry(g, l, a.carry, lane);
+    const bool events = r.reward_components != nullptr;
+    core_step(g, hdr, e, lane, k0, k1, events);
+    if (finish_step(g, hdr, e, l, lane, partial != 0, r, events)) clear_carry(g, l, a.carry, lane);
     store_env(g, s, l, e, lane);
     if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
 }

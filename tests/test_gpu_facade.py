@@ -146,3 +146,80 @@ def test_request_groups_response_equals_the_fused_step(case, oracle_threads):
     assert env.agent_classes == {"player": list(env.agents)}
     if case == "crowded":
         assert ended > 0
+
+
+@pytest.mark.parametrize("bot_name", ["workerRushAI", "lightRushAI"])
+def test_seat_request_response_equals_the_fused_seat_step(bot_name, oracle_threads):
+    import torch
+
+    from nanorts_amd import bots, groups
+    from nanorts_amd.content import map_name_to_scenario
+
+    _say(f"seat step_request/step_response {bot_name}")
+    torch.cuda.set_device(0)
+    # a horizon inside the 120 cycles, so every game ends (and resets) once
+    game = map_name_to_scenario("basesWorkers8x8", max_cycles=100)
+    bot = getattr(bots, bot_name)
+    seat = bots.SeatEnv(bot, scenario=game, reward_components=True, device="cuda:0")
+    keys = roots(32, 17)
+    _, fused = seat.reset(keys)
+    _, split = seat.reset(keys)
+    oracle = Oracle(game)
+    C = game.bucket.per_player_capacity
+    ended = 0
+    for t in range(120):
+        # the learner samples from its current masks
+        rows = np.zeros((32, 2, C, 78), bool)
+        rows[:, 0] = seat.get_avail_actions(fused)[bots.LEARNER].cpu().numpy()
+        learner = oracle.sample_actions(rows, (7, 8), t)[:, 0].copy()
+        acts = {bots.LEARNER: torch.as_tensor(learner, device="cuda:0")}
+        a = seat.step(None, fused, acts, donate=True)
+        (k, core, cmds), carry = seat.step_request(split, acts)
+        stepped = groups.step_groups([(k, core, cmds, seat)])[0]
+        b = seat.step_response(split, carry, stepped)
+        learner_agent = bots.LEARNER
+        assert torch.equal(a[0][learner_agent].feature_maps, b[0][learner_agent].feature_maps), f"cycle {t}"
+        assert torch.equal(a[2][learner_agent], b[2][learner_agent]), f"cycle {t} reward"
+        assert torch.equal(a[3][learner_agent], b[3][learner_agent])
+        assert torch.equal(a[4]["reward_components"][learner_agent], b[4]["reward_components"][learner_agent])
+        assert torch.equal(a[4]["final_observation"][learner_agent].feature_maps,
+                           b[4]["final_observation"][learner_agent].feature_maps)
+        for name in ("terminated", "truncated", "winner", "spawn_overflowed"):
+            assert torch.equal(a[4][name], b[4][name]), f"cycle {t} {name}"
+        assert_states_equal(to_host(fused.environment_state), to_host(split.environment_state), f"cycle {t}")
+        for name in fused.carry:
+            assert torch.equal(fused.carry[name], split.carry[name]), f"cycle {t} carry {name}"
+        ended += int(a[3]["__all__"].sum())
+    assert ended > 0
+    assert seat.agent_classes == {bots.LEARNER: [bots.LEARNER]}
+    assert seat.action_space(bots.LEARNER) == seat.env.action_space("player_0")
+
+
+def test_seat_on_the_pixel_surface(oracle_threads):
+    import torch
+
+    from nanorts_amd import bots, rendering
+    from nanorts_amd.content import map_name_to_scenario
+    from oracle.oracle import empty_carry
+
+    _say("seat pixels")
+    torch.cuda.set_device(0)
+    game = map_name_to_scenario("basesWorkers8x8", max_cycles=400)
+    seat = bots.SeatEnv(bots.lightRushAI, scenario=game, surface="pixels", seat="player_1", device="cuda:0")
+    keys = roots(8, 19)
+    obs, state = seat.reset(keys)
+    oracle = Oracle(game)
+    ref = batch_initial(game, 8, keys)
+    carry = empty_carry(8, game.bucket.per_player_capacity)
+    tiles = rendering.tile_table(game.bucket.unit_type_capacity)
+    for t in range(10):
+        learner = oracle.sample_actions(oracle.avail_rows(ref), (9, 10), t)[:, 1].copy()
+        obs, state, rewards, dones, infos = seat.step(None, state, {bots.LEARNER: torch.as_tensor(learner,
+                                                                                                 device="cuda:0")},
+                                                      donate=True)
+        want = oracle.seat_step(ref, carry, bots.lightRushAI.strategy, bots.lightRushAI.trained, 1, learner, False,
+                                observe=False)
+        image, scalars = oracle.pixels(ref, False, tiles)
+        np.testing.assert_array_equal(obs[bots.LEARNER].image.cpu().numpy(), image[:, 1], err_msg=f"cycle {t}")
+        np.testing.assert_array_equal(obs[bots.LEARNER].scalars.cpu().numpy(), scalars[:, 1])
+        np.testing.assert_array_equal(rewards[bots.LEARNER].cpu().numpy(), want["reward"][:, 1])
