@@ -177,6 +177,7 @@ class GridNet:
         if self.layout.bucket != game.bucket:
             raise ModelError("the GridNet layout was prepared for another bucket")
         self.game = game
+        self.bucket = game.bucket
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.dev = DeviceGame(game, self.device)
 
@@ -336,3 +337,236 @@ def unpack_mask(action_mask: torch.Tensor, *, layout: GridNetLayout) -> torch.Te
     bits = ((action_mask.to(torch.int32)[..., None] >> shifts) & 1) != 0
     bits = bits.reshape(*action_mask.shape[:-1], MASK_WORDS * 32)
     return torch.cat([bits[..., :head], bits[..., 32:32 + layout.action_factor_sizes[-1]]], dim=-1)
+
+
+# ---------------------------------------------------------------------------
+# The learner-vs-bot seat and the mix on the GridNet surface
+# (src/nanorts/bots/gridnet_seat.py): the learner is player 0, the bot
+# player 1; a step is the bot's act on a copy of its carry, then step_against
+# (one launch each), and the carry is emptied where the game ended.
+# ---------------------------------------------------------------------------
+@dataclasses.dataclass
+class GridNetSeatState:
+    """src/nanorts/bots/gridnet_seat.py:20-26"""
+
+    environment_state: EnvironmentState
+    carry: dict[str, torch.Tensor]
+
+
+@dataclasses.dataclass(frozen=True)
+class GridNetSeatStep:
+    """src/nanorts/bots/gridnet_seat.py:28-53: the learner's rows."""
+
+    seat_state: GridNetSeatState
+    observation: GridNetObservation
+    reward_components: torch.Tensor  # float32[L, 6]
+    reward_dones: torch.Tensor       # bool[L, 6]
+    terminated: torch.Tensor
+    truncated: torch.Tensor
+    done: torch.Tensor
+    winner: torch.Tensor
+    telemetry: dict[str, torch.Tensor]
+    spawn_overflowed: torch.Tensor
+    final_observation: torch.Tensor
+    final_valid: torch.Tensor
+
+
+LEARNER_PLAYER: Final = 0
+BOT_PLAYER: Final = 1
+
+
+def _learner(obs: GridNetObservation) -> GridNetObservation:
+    return GridNetObservation(obs.planes[:, LEARNER_PLAYER], obs.source_mask[:, LEARNER_PLAYER],
+                              obs.action_mask[:, LEARNER_PLAYER])
+
+
+class GridNetSeat:
+    """reset_gridnet_seat / step_gridnet_seat / gridnet_seat_commands
+    (src/nanorts/bots/gridnet_seat.py:56-95) with `bot` and `game` bound."""
+
+    def __init__(self, bot, game: GameConfig, layout: GridNetLayout | None = None, *,
+                 device: str | torch.device | None = None):
+        from nanorts_amd import bots
+
+        if bot.strategy not in (bots.WORKER_RUSH, bots.BARRACKS_RUSH):
+            raise ModelError(f"GridNetSeat refuses bot {bot.name!r}: the rush family is built")
+        self.bot = bot
+        self.grid = GridNet(game, layout, device=device)
+        self.game = game
+        self.layout = self.grid.layout
+        self.device = self.grid.device
+
+    def reset(self, environment_root) -> tuple[GridNetSeatState, GridNetObservation]:
+        from nanorts_amd import bots
+
+        state, obs = self.grid.reset(environment_root)
+        carry = bots.empty_actions(state.num_envs, self.game.bucket.per_player_capacity, self.device)
+        return GridNetSeatState(state, carry), _learner(obs)
+
+    def commands(self, seat_state: GridNetSeatState) -> tuple[dict[str, torch.Tensor], dict[str, torch.Tensor]]:
+        """gridnet_seat_commands: (the bot's new carry, its Commands [L, 2, C]
+        per field); the seat state's carry is left as it is."""
+        from nanorts_amd import bots
+
+        carry = {k: v.clone() for k, v in seat_state.carry.items()}
+        cmds = bots.abstraction_act(self.grid, seat_state.environment_state, carry, self.bot, BOT_PLAYER)
+        return carry, cmds
+
+    def step(self, seat_state: GridNetSeatState, actions: torch.Tensor, *, donate: bool = False) -> GridNetSeatStep:
+        """step_gridnet_seat: the learner's per-cell actions int32[L, H, W, 7]."""
+        from nanorts_amd import bots
+
+        carry, cmds = self.commands(seat_state)
+        out = self.grid.step_against(seat_state.environment_state, actions, cmds, donate=donate)
+        fresh = bots.empty_actions(out.environment_state.num_envs, self.game.bucket.per_player_capacity, self.device)
+        carry = {k: torch.where(out.done.reshape((-1,) + (1,) * (v.dim() - 1)), fresh[k], v) for k, v in carry.items()}
+        p = LEARNER_PLAYER
+        return GridNetSeatStep(seat_state=GridNetSeatState(out.environment_state, carry),
+                               observation=_learner(out.observation),
+                               reward_components=out.reward_components[:, p], reward_dones=out.reward_dones[:, p],
+                               terminated=out.terminated, truncated=out.truncated, done=out.done, winner=out.winner,
+                               telemetry=out.telemetry, spawn_overflowed=out.spawn_overflowed,
+                               final_observation=out.final_observation[:, p], final_valid=out.final_valid)
+
+
+@dataclasses.dataclass(frozen=True)
+class GridNetGroup:
+    """src/nanorts/bots/gridnet_seat.py:98-101"""
+
+    bot: Any
+    lanes: int
+
+
+@dataclasses.dataclass
+class GridNetMixState:
+    """src/nanorts/bots/gridnet_seat.py:104-109"""
+
+    self_play: EnvironmentState | None
+    seats: tuple[GridNetSeatState, ...]
+
+
+_MIX_FIELDS: Final = ("observation", "reward_components", "reward_dones", "terminated", "truncated", "done", "winner",
+                      "telemetry", "spawn_overflowed", "final_observation", "final_valid")
+
+
+@dataclasses.dataclass(frozen=True)
+class GridNetMixStep:
+    """src/nanorts/bots/gridnet_seat.py:112-127: one row per self-play player
+    (game-major) and one per seat lane, in that order."""
+
+    mix_state: GridNetMixState
+    observation: GridNetObservation
+    reward_components: torch.Tensor
+    reward_dones: torch.Tensor
+    terminated: torch.Tensor
+    truncated: torch.Tensor
+    done: torch.Tensor
+    winner: torch.Tensor
+    telemetry: dict[str, torch.Tensor]
+    spawn_overflowed: torch.Tensor
+    final_observation: torch.Tensor
+    final_valid: torch.Tensor
+
+
+def _rows_of_games(tree):
+    """[L, 2, ...] -> [2L, ...], game-major."""
+    if isinstance(tree, torch.Tensor):
+        return tree.reshape(tree.shape[0] * PLAYER_COUNT, *tree.shape[2:])
+    if isinstance(tree, dict):
+        return {k: _rows_of_games(v) for k, v in tree.items()}
+    return type(tree)(*[_rows_of_games(getattr(tree, f.name)) for f in dataclasses.fields(tree)])
+
+
+def _rows_of_lanes(tree):
+    """[L, ...] -> [2L, ...], each lane's value for both of its players."""
+    if isinstance(tree, torch.Tensor):
+        return torch.repeat_interleave(tree, PLAYER_COUNT, dim=0)
+    return {k: _rows_of_lanes(v) for k, v in tree.items()}
+
+
+def _joined(parts):
+    first = parts[0]
+    if isinstance(first, torch.Tensor):
+        return torch.cat(parts)
+    if isinstance(first, dict):
+        return {k: _joined([p[k] for p in parts]) for k in first}
+    return type(first)(*[_joined([getattr(p, f.name) for p in parts]) for f in dataclasses.fields(first)])
+
+
+class GridNetMix:
+    """src/nanorts/bots/gridnet_seat.py:130-214: `self_play` self-play games
+    and learner-vs-bot groups on one GridNet game and layout."""
+
+    def __init__(self, self_play: int, groups, game: GameConfig, layout: GridNetLayout | None = None, *,
+                 device: str | torch.device | None = None):
+        self.groups = tuple(groups)
+        if not isinstance(self_play, int) or isinstance(self_play, bool) or self_play < 0:
+            raise ModelError(f"GridNetMix refuses self_play={self_play!r}: it is a count of self-play games")
+        for index, group in enumerate(self.groups):
+            if not isinstance(group.lanes, int) or isinstance(group.lanes, bool) or group.lanes < 1:
+                raise ModelError(f"GridNetMix refuses group {index}: lanes={group.lanes!r} is not a positive int")
+            if not hasattr(group.bot, "strategy"):
+                raise ModelError(f"GridNetMix refuses group {index}: its bot is not a Bot")
+        self.self_play = self_play
+        if self.lanes == 0:
+            raise ModelError("GridNetMix refuses a mix of no lanes")
+        self.grid = GridNet(game, layout, device=device)
+        self.seats = tuple(GridNetSeat(group.bot, game, self.grid.layout, device=device) for group in self.groups)
+
+    @property
+    def lanes(self) -> int:
+        return self.self_play + sum(group.lanes for group in self.groups)
+
+    @property
+    def rows(self) -> int:
+        return PLAYER_COUNT * self.self_play + sum(group.lanes for group in self.groups)
+
+    def slices(self) -> tuple[slice, ...]:
+        sizes = ([PLAYER_COUNT * self.self_play] if self.self_play else []) + [g.lanes for g in self.groups]
+        out, start = [], 0
+        for size in sizes:
+            out.append(slice(start, start + size))
+            start += size
+        return tuple(out)
+
+    def reset(self, roots) -> tuple[GridNetMixState, GridNetObservation]:
+        roots = np.asarray(roots.cpu() if isinstance(roots, torch.Tensor) else roots, np.uint32).reshape(-1, 2)
+        if roots.shape[0] != self.lanes:
+            raise ModelError(f"GridNetMix.reset takes {self.lanes} roots, got {roots.shape[0]}")
+        rows, start, self_play, seats = [], 0, None, []
+        if self.self_play:
+            self_play, obs = self.grid.reset(roots[:self.self_play])
+            rows.append(_rows_of_games(obs))
+            start = self.self_play
+        for group, seat in zip(self.groups, self.seats, strict=True):
+            state, obs = seat.reset(roots[start:start + group.lanes])
+            seats.append(state)
+            rows.append(obs)
+            start += group.lanes
+        return GridNetMixState(self_play, tuple(seats)), _joined(rows)
+
+    def step(self, mix_state: GridNetMixState, actions: torch.Tensor, *, donate: bool = False) -> GridNetMixStep:
+        """Per-cell actions int32[rows, H, W, 7], one row per slice row."""
+        if actions.shape[0] != self.rows:
+            raise ModelError(f"GridNetMix.step takes {self.rows} action rows, got {actions.shape[0]}")
+        bounds = list(self.slices())
+        rows, self_play, seats = [], None, []
+        if self.self_play:
+            grids = actions[bounds.pop(0)].reshape(self.self_play, PLAYER_COUNT, *actions.shape[1:])
+            out = self.grid.step(mix_state.self_play, grids, donate=donate)
+            self_play = out.environment_state
+            rows.append({"observation": _rows_of_games(out.observation),
+                         "reward_components": _rows_of_games(out.reward_components),
+                         "reward_dones": _rows_of_games(out.reward_dones),
+                         "terminated": _rows_of_lanes(out.terminated), "truncated": _rows_of_lanes(out.truncated),
+                         "done": _rows_of_lanes(out.done), "winner": _rows_of_lanes(out.winner),
+                         "telemetry": _rows_of_lanes(out.telemetry),
+                         "spawn_overflowed": _rows_of_lanes(out.spawn_overflowed),
+                         "final_observation": _rows_of_games(out.final_observation),
+                         "final_valid": _rows_of_lanes(out.final_valid)})
+        for seat, state, bound in zip(self.seats, mix_state.seats, bounds, strict=True):
+            out = seat.step(state, actions[bound], donate=donate)
+            seats.append(out.seat_state)
+            rows.append({name: getattr(out, name) for name in _MIX_FIELDS})
+        joined = _joined(rows)
+        return GridNetMixStep(mix_state=GridNetMixState(self_play, tuple(seats)), **joined)

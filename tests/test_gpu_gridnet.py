@@ -22,7 +22,7 @@ import pytest
 
 from nanorts_amd.model import (TYPE_BARRACKS, TYPE_BASE, TYPE_HEAVY, TYPE_LIGHT, TYPE_RANGED, TYPE_WORKER)
 from oracle.oracle import copy_state, load_library
-from tests.helpers import advanced_states, assert_states_equal, game_for, to_device, to_host
+from tests.helpers import advanced_states, assert_states_equal, game_for, roots, to_device, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -328,3 +328,106 @@ def test_reset_observes_the_initial_state(oracle_threads):
         assert got[name].shape == want.shape, name
     assert_states_equal(copy_state(st), got)
     np.testing.assert_array_equal(obs.planes.cpu().numpy(), _want_planes(oracle, st, "one_hot"))
+
+
+@pytest.mark.parametrize("bot_name", ["workerRushAI", "lightRushAI"])
+def test_gridnet_seat_matches_oracle(bot_name, oracle_threads):
+    """step_gridnet_seat: the bot's act (player 1) on its carry, step_against
+    with the learner's per-cell rows, the carry emptied where the game ended."""
+    import torch
+
+    from nanorts_amd import bots, gridnet
+    from oracle.oracle import empty_carry
+
+    _say(f"gridnet seat {bot_name}")
+    torch.cuda.set_device(0)
+    from nanorts_amd.content import map_name_to_scenario
+
+    # a horizon inside the 80 cycles, so every game ends (and resets) once
+    game = map_name_to_scenario("basesWorkers8x8", max_cycles=60)
+    bot = getattr(bots, bot_name)
+    L = 24
+    oracle, st = advanced_states(game, L, 0, False, oracle_threads, seed=53)
+    seat = gridnet.GridNetSeat(bot, game, device="cuda:0")
+    state, obs = seat.reset(st["environment_root"])
+    carry = empty_carry(L, game.bucket.per_player_capacity)
+    b = game.bucket
+    ended = 0
+    for t in range(80):
+        learner = _per_cell_actions(game, oracle, st, 300 + t)[:, 0]
+        out = seat.step(state, torch.as_tensor(learner.reshape(L, b.height, b.width, 7), device="cuda:0"),
+                        donate=True)
+        state = out.seat_state
+        bot_cmds = oracle.abstraction_act(st, carry, bot.strategy, bot.trained, 1)
+        both = np.zeros((L, 2, b.cell_count, 7), np.int32)
+        both[:, 0] = learner
+        cmds = oracle.gridnet_decode(st, both)
+        for f in FIELDS:
+            cmds[f][:, 1] = bot_cmds[f][:, 1]
+        step = oracle.core_step(st, cmds, _episode_roots(st))
+        done = (step["terminated"] | step["truncated"]).astype(bool)
+        comps, rdones = _want_rewards(game, step, st, done)
+        np.testing.assert_array_equal(out.reward_components.cpu().numpy(), comps[:, 0], err_msg=f"cycle {t}")
+        np.testing.assert_array_equal(out.reward_dones.cpu().numpy(), rdones[:, 0])
+        np.testing.assert_array_equal(out.done.cpu().numpy(), done)
+        want_final = _want_planes(oracle, st, "one_hot")[:, 0]
+        np.testing.assert_array_equal(out.final_observation.cpu().numpy().astype(np.int64), want_final)
+        oracle.reset_where_done(st, done.astype(np.uint8))
+        for name in carry:
+            if name != "next_order":
+                carry[name][done] = -1 if name != "trained" else 0
+        carry["next_order"][done] = 0
+        assert_states_equal(st, to_host(state.environment_state), f"cycle {t}")
+        for name, want in carry.items():
+            np.testing.assert_array_equal(state.carry[name].cpu().numpy().astype(np.int64), want.astype(np.int64),
+                                          err_msg=f"cycle {t} carry {name}")
+        ended += int(done.sum())
+    assert ended > 0
+
+
+def test_gridnet_mix_rows(oracle_threads):
+    """GridNetMix: self-play rows (game-major, two per game) then the seat
+    groups' rows, each equal to its environment stepped on its own."""
+    import torch
+
+    from nanorts_amd import bots, gridnet
+
+    _say("gridnet mix")
+    torch.cuda.set_device(0)
+    game, _ = game_for("8x8-original-both")
+    b = game.bucket
+    mix = gridnet.GridNetMix(4, [gridnet.GridNetGroup(bots.workerRushAI, 3), gridnet.GridNetGroup(bots.lightRushAI, 2)],
+                             game, device="cuda:0")
+    assert mix.lanes == 9 and mix.rows == 13
+    assert [(s.start, s.stop) for s in mix.slices()] == [(0, 8), (8, 11), (11, 13)]
+    keys = roots(9, 61)
+    mstate, mobs = mix.reset(keys)
+    alone_self, _ = gridnet.GridNet(game, mix.grid.layout, device="cuda:0").reset(keys[:4])
+    solo = gridnet.GridNet(game, mix.grid.layout, device="cuda:0")
+    seat_w = gridnet.GridNetSeat(bots.workerRushAI, game, mix.grid.layout, device="cuda:0")
+    seat_l = gridnet.GridNetSeat(bots.lightRushAI, game, mix.grid.layout, device="cuda:0")
+    sw, _ = seat_w.reset(keys[4:7])
+    sl, _ = seat_l.reset(keys[7:9])
+    rng = np.random.default_rng(9)
+    for t in range(60):
+        acts = np.stack([rng.integers(0, s, size=(13, b.height, b.width), dtype=np.int32)
+                         for s in (6, 4, 4, 4, 4, 7, 49)], -1)
+        a = torch.as_tensor(acts, device="cuda:0")
+        m = mix.step(mstate, a)
+        mstate = m.mix_state
+        o = solo.step(alone_self, a[:8].reshape(4, 2, b.height, b.width, 7))
+        alone_self = o.environment_state
+        ow = seat_w.step(sw, a[8:11])
+        sw = ow.seat_state
+        ol = seat_l.step(sl, a[11:13])
+        sl = ol.seat_state
+        assert torch.equal(m.observation.planes[:8], o.observation.planes.reshape(8, *o.observation.planes.shape[2:]))
+        assert torch.equal(m.observation.planes[8:11], ow.observation.planes)
+        assert torch.equal(m.observation.action_mask[11:13], ol.observation.action_mask)
+        assert torch.equal(m.reward_components[:8], o.reward_components.reshape(8, 6))
+        assert torch.equal(m.done[:8], torch.repeat_interleave(o.done, 2))
+        assert torch.equal(m.done[8:11], ow.done) and torch.equal(m.done[11:13], ol.done)
+        assert torch.equal(m.winner[11:13], ol.winner)
+        assert torch.equal(m.final_observation[8:11], ow.final_observation)
+    for name in sw.carry:
+        assert torch.equal(mstate.seats[0].carry[name], sw.carry[name])
