@@ -341,6 +341,24 @@ int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state stat
                       int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                       const int32_t* actions, int32_t partial, nanorts_env_results results);
 
+/* nanorts_seat_step with a per-lane seat: seats int32[L] holds each lane's
+ * learner (0 or 1) on entry.  With draw != 0 (the "drawn" rule) a lane whose
+ * game ended takes the seat drawn from its next episode's root,
+ * randint(fold_in(episode_root, 2**32 - 2), (), 0, 2); otherwise the seats
+ * stay (a per-lane Player array).  Replaces step_seat with seat="drawn" or
+ * an Array seat (src/nanorts/bots/seat.py:94-152, 352-366). */
+int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
+                            nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
+                            nanorts_env_results results);
+
+/* The "drawn" rule's seat of each lane's current episode:
+ * randint(fold_in(fold_in(environment_root, episode_index), 2**32 - 2), (),
+ * 0, 2) into seats int32[L].  Replaces _episode_seat
+ * (src/nanorts/bots/seat.py:352-360) as reset_seat calls it (lines 74-78). */
+int nanorts_episode_seats(void* stream, const uint32_t* environment_root /* [L][2] */,
+                          const uint32_t* episode_index /* [L] */, int64_t lanes, int32_t* seats);
+
 /* Fused learner-vs-bot rollout of `steps` cycles with the state resident in
  * LDS: per cycle the learner's rows from the synthetic harness's integer
  * uniform-over-legal sampler (its avail words, `sample_key`, step
@@ -353,6 +371,16 @@ int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state s
                          int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                          const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
                          int64_t env0, nanorts_rollout_results results);
+
+/* nanorts_seat_rollout with per-lane seats as nanorts_seat_step_lanes: seats
+ * int32[L] is read at the start and holds the seats after the last cycle;
+ * seat_record (when set) receives the learner of every cycle [steps][L],
+ * which selects the learner's reward from results.rewards [steps][L][2]. */
+int nanorts_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                               int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
+                               int32_t* seat_record, nanorts_abstract_actions carry,
+                               const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps,
+                               int32_t partial, int64_t env0, nanorts_rollout_results results);
 
 /* GridNet decode_actions: per-cell actions int32[L][2][H][W][7] -> Commands.
  * Replaces the FFI target nanorts_gridnet_decode

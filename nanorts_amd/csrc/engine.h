@@ -215,6 +215,12 @@ NR_DEV int32_t randint01(uint32_t k0, uint32_t k1) {
     threefry(s0, s1, b0, b1);
     return (int32_t)((b0 ^ b1) & 1u);
 }
+// The "drawn" seat rule's learner for an episode root (N/bots/seat.py:352-360):
+// randint(fold_in(root, 2**32 - 2), (), 0, 2).
+NR_DEV int32_t episode_seat(uint32_t k0, uint32_t k1) {
+    fold_in(k0, k1, 0xFFFFFFFEu);
+    return randint01(k0, k1);
+}
 
 // ---------------------------------------------------------------------------
 // LDS views

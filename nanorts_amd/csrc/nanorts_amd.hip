@@ -784,13 +784,17 @@ __global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes,
     settle_carry(g, b, a.y, l, a.carry, lane);
 }
 
-// seat.step_seat with a static learner seat (N/bots/seat.py:94-152): the
-// bot's commands from the current state, the learner's rows decoded
-// (N/adapters/jaxmarl/env.py:78-96), core.step under the episode root,
-// auto-reset, the carry emptied where done, observations.
-__global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanorts_state s, BotArgs a, int32_t learner,
-                                                   const int32_t* actions, int32_t partial, nanorts_env_results r) {
+// seat.step_seat (N/bots/seat.py:94-152): the bot's commands from the current
+// state, the learner's rows decoded (N/adapters/jaxmarl/env.py:78-96),
+// core.step under the episode root, auto-reset, the carry emptied where done,
+// observations.  The learner is `fixed` for every lane, or seats[l] when
+// `seats` is set; with `draw` a lane whose game ended takes the seat drawn
+// from its next episode's root (N/bots/seat.py:121-125).
+__global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanorts_state s, BotArgs a, int32_t fixed,
+                                                   int32_t* seats, int32_t draw, const int32_t* actions,
+                                                   int32_t partial, nanorts_env_results r) {
     NR_KERNEL_PROLOGUE
+    const int32_t learner = seats ? clampi(uni(seats[l]), 0, 1) : fixed;
     load_env(g, s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
     uint32_t k0 = (uint32_t)uni(e.sc[S_ROOT0]), k1 = (uint32_t)uni(e.sc[S_ROOT1]);
@@ -827,9 +831,28 @@ __global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanor
     wave_sync();
     const bool events = r.reward_components != nullptr;
     core_step(g, hdr, e, lane, k0, k1, events);
-    if (finish_step(g, hdr, e, l, lane, partial != 0, r, events)) clear_carry(g, l, a.carry, lane);
+    if (finish_step(g, hdr, e, l, lane, partial != 0, r, events)) {
+        clear_carry(g, l, a.carry, lane);
+        if (seats && draw) {
+            uint32_t n0 = (uint32_t)uni(e.sc[S_ROOT0]), n1 = (uint32_t)uni(e.sc[S_ROOT1]);
+            fold_in(n0, n1, (uint32_t)uni(e.sc[S_EPISODE]));
+            const int32_t next = episode_seat(n0, n1);
+            if (lane == 0) seats[l] = next;
+        }
+    }
     store_env(g, s, l, e, lane);
     if (r.feature_maps || r.scalars) observe_both(g, hdr, e, l, lane, partial != 0, r.feature_maps, r.scalars);
+}
+
+// The "drawn" rule's learner of each lane's current episode
+// (N/bots/seat.py:74-78, 352-360): episode_seat(fold_in(root, episode)).
+__global__ __launch_bounds__(256) void k_episode_seats(int64_t lanes, const uint32_t* roots, const uint32_t* episodes,
+                                                       int32_t* seats) {
+    const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= lanes) return;
+    uint32_t k0 = roots[2 * l], k1 = roots[2 * l + 1];
+    fold_in(k0, k1, episodes[l]);
+    seats[l] = episode_seat(k0, k1);
 }
 
 __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const uint32_t* words, uint32_t key0, uint32_t key1, int32_t step,
@@ -1104,6 +1127,9 @@ struct SeatRolloutArgs {
     BotArgs bot;
     int32_t learner, t0, steps, partial;  // cycles t0 .. t0 + steps - 1 of the caller's rollout
     int64_t env0;
+    int32_t* seats;        // per-lane learners (or NULL: `learner` for every lane)
+    int32_t* seat_record;  // [steps][lanes] learner of each cycle, or NULL
+    int32_t draw;          // re-draw a lane's seat from its next episode root
     nanorts_rollout_results out;
     uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
 };
@@ -1117,7 +1143,7 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const BotArgs& ba = args.bot;
-    const int32_t learner = args.learner;
+    int32_t learner = args.seats ? clampi(uni(args.seats[l]), 0, 1) : args.learner;
     Bot b;
     b.base = e.base + ba.y.origin;
     b.player = 1 - learner;
@@ -1127,6 +1153,7 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
     const uint32_t env = (uint32_t)(args.env0 + l);
     for (int32_t t = 0; t < args.steps; ++t) {
         const int64_t tt = (int64_t)args.t0 + t;
+        if (args.seat_record && lane == 0) args.seat_record[tt * lanes + l] = learner;
         // the learner: masks -> sample -> decode (unavailable rows absent)
         bool irregular = false;
         const int32_t n = compact_available(g, e, lane, &irregular);
@@ -1187,6 +1214,11 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
             ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
             ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
             fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+            if (args.seats && args.draw) {
+                learner = episode_seat(ek0, ek1);
+                b.player = 1 - learner;
+                b.block = g.N + b.player * g.C;
+            }
         }
         if (out.feature_maps || out.scalars) {
             const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
@@ -1195,6 +1227,7 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
             observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
+    if (args.seats && lane == 0) args.seats[l] = learner;
     store_env(g, args.s, l, e, lane);
 }
 
@@ -1787,12 +1820,11 @@ int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_stat
     return launch(k_abstraction_act, sh, lanes, (hipStream_t)stream, state, a, player, player_lanes, commands);
 }
 
-int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
-                      int32_t trained_type, int32_t learner, nanorts_abstract_actions carry, const int32_t* actions,
-                      int32_t partial, nanorts_env_results results) {
-    NR_STATE(state)
+static int seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                     int32_t trained_type, int32_t learner, int32_t* seats, int32_t draw,
+                     nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
+                     nanorts_env_results results) {
     if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
-    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
     if (!state.environment_root || !state.episode_index)
         return fail(NANORTS_INVALID_ARGUMENT, "the seat step needs environment_root and episode_index");
     if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
@@ -1800,7 +1832,41 @@ int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state stat
     BotArgs a;
     std::string why;
     if (!bot_args(game, &sh, &a, strategy, trained_type, carry, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
-    return launch(k_seat_step, sh, lanes, (hipStream_t)stream, state, a, learner, actions, partial, results);
+    return launch(k_seat_step, sh, lanes, (hipStream_t)stream, state, a, learner, seats, draw, actions, partial,
+                  results);
+}
+
+int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                      int32_t trained_type, int32_t learner, nanorts_abstract_actions carry, const int32_t* actions,
+                      int32_t partial, nanorts_env_results results) {
+    NR_STATE(state)
+    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
+    return seat_step(stream, game, state, lanes, strategy, trained_type, learner, nullptr, 0, carry, actions, partial,
+                     results);
+}
+
+int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                            int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
+                            nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
+                            nanorts_env_results results) {
+    NR_STATE(state)
+    if (!seats) return fail(NANORTS_INVALID_ARGUMENT, "seats is NULL");
+    return seat_step(stream, game, state, lanes, strategy, trained_type, 0, seats, draw != 0, carry, actions, partial,
+                     results);
+}
+
+int nanorts_episode_seats(void* stream, const uint32_t* environment_root, const uint32_t* episode_index, int64_t lanes,
+                          int32_t* seats) {
+    if (!environment_root || !episode_index || !seats) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, "lanes must be >= 0");
+    if (lanes == 0) return NANORTS_OK;
+    const int64_t blocks = (lanes + 255) / 256;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    hipLaunchKernelGGL(k_episode_seats, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, lanes,
+                       environment_root, episode_index, seats);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
 }
 
 int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
@@ -1936,13 +2002,11 @@ int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts
     return launch(k_gridnet_step, sh, lanes, (hipStream_t)stream, state, gy, actions, commands, 1, results);
 }
 
-int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
-                         int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
-                         const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
-                         nanorts_rollout_results results) {
-    NR_STATE(state)
+static int seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                        int32_t trained_type, int32_t learner, int32_t* seats, int32_t draw, int32_t* seat_record,
+                        nanorts_abstract_actions carry, const uint32_t* sample_key, int32_t step0, int32_t steps,
+                        int32_t partial, int64_t env0, nanorts_rollout_results results) {
     if (!sample_key) return fail(NANORTS_INVALID_ARGUMENT, "sample_key is NULL");
-    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
     if (!state.environment_root || !state.episode_index)
         return fail(NANORTS_INVALID_ARGUMENT, "a rollout needs environment_root and episode_index");
     if (!state_complete(game->initial)) return fail(NANORTS_INVALID_ARGUMENT, "game->initial is incomplete");
@@ -1964,6 +2028,9 @@ int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state s
         args.s = state;
         args.bot = a;
         args.learner = learner;
+        args.seats = seats;
+        args.seat_record = seat_record;
+        args.draw = draw;
         args.t0 = t0;
         args.steps = steps - t0 < kRolloutChunk ? steps - t0 : kRolloutChunk;
         args.partial = partial;
@@ -1982,6 +2049,27 @@ int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state s
             return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
     }
     return NANORTS_OK;
+}
+
+int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+                         int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
+                         const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
+                         nanorts_rollout_results results) {
+    NR_STATE(state)
+    if (learner != 0 && learner != 1) return fail(NANORTS_INVALID_ARGUMENT, "learner must be 0 or 1");
+    return seat_rollout(stream, game, state, lanes, strategy, trained_type, learner, nullptr, 0, nullptr, carry,
+                        sample_key, step0, steps, partial, env0, results);
+}
+
+int nanorts_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+                               int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
+                               int32_t* seat_record, nanorts_abstract_actions carry, const uint32_t* sample_key,
+                               int32_t step0, int32_t steps, int32_t partial, int64_t env0,
+                               nanorts_rollout_results results) {
+    NR_STATE(state)
+    if (!seats) return fail(NANORTS_INVALID_ARGUMENT, "seats is NULL");
+    return seat_rollout(stream, game, state, lanes, strategy, trained_type, 0, seats, draw != 0, seat_record, carry,
+                        sample_key, step0, steps, partial, env0, results);
 }
 
 }  // extern "C"

@@ -94,6 +94,7 @@ EXPORTS = (
     "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
     "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
     "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
+    "nanorts_seat_step_lanes", "nanorts_seat_rollout_lanes", "nanorts_episode_seats",
     "nanorts_gridnet_decode", "nanorts_gridnet_observe", "nanorts_gridnet_step", "nanorts_gridnet_step_against",
     "nanorts_gridnet_sample_actions",
 )
@@ -128,6 +129,11 @@ _SIGNATURES = {
                                          EnvResults]),
     "nanorts_seat_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32, _I32,
                                             _I32, _I64, RolloutResults]),
+    "nanorts_seat_step_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, AbstractActions, _VP,
+                                               _I32, EnvResults]),
+    "nanorts_seat_rollout_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, _VP, AbstractActions,
+                                                  _VP, _I32, _I32, _I32, _I64, RolloutResults]),
+    "nanorts_episode_seats": (ctypes.c_int, [_VP, _VP, _VP, _I64, _VP]),
     # the command buffers have the layout of Commands (six int32 pointers)
     "nanorts_gridnet_decode": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands]),
     "nanorts_gridnet_observe": (ctypes.c_int, [_VP, _GP, State, _I64, GridNetObs]),

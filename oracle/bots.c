@@ -779,9 +779,20 @@ int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start,
  * (N/adapters/jaxmarl/env.py:78-96, every agent reading the same rows), the
  * merged commands stepped under the episode root, auto-reset, the carry back
  * to empty_actions where done. */
+/* N/bots/seat.py:352-360: the "drawn" rule's learner for an episode root,
+ * jax.random.randint(fold_in(root, 2**32 - 2), (), 0, 2). */
+int32_t nro_episode_seat(const uint32_t episode_root[2]) {
+    uint32_t k[2];
+    nro_fold_in(episode_root, 0xFFFFFFFEu, k);
+    return nro_randint01(k);
+}
+
+/* N/bots/seat.py:94-152: the learner of lane l is seats[l] when `seats` is
+ * set (else `learner`); with `draw`, a lane whose game ended takes the seat
+ * of its next episode's root (lines 121-125), otherwise it keeps its seat. */
 void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, int64_t L, int32_t strategy,
-                   int32_t trained_type, int32_t learner, nro_abstract* carry, const int32_t* actions,
-                   int32_t partial, nro_env_out* out) {
+                   int32_t trained_type, int32_t fixed, int32_t* seats, int32_t draw, nro_abstract* carry,
+                   const int32_t* actions, int32_t partial, nro_env_out* out) {
     const int32_t C = g->capacity, owned = 2 * C;
     work_t w;
     work_init(g, &w);
@@ -792,6 +803,7 @@ void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, in
     for (int64_t l = 0; l < L; ++l) {
         env_t e = env_of(g, s, l);
         ab_t a = ab_of(g, carry, l);
+        const int32_t learner = seats ? seats[l] : fixed;
         bot_act_one(g, &e, &b, &a, strategy, trained_type, 1 - learner, bot_cmds);
         const int32_t* rows = actions + (size_t)l * C * 7;
         memcpy(both, rows, sizeof(int32_t) * (size_t)C * 7);
@@ -811,6 +823,11 @@ void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, in
             reset_one(g, initial, &e);
             *e.episode += 1u;
             ab_empty(g, &a);
+            if (seats && draw) {
+                uint32_t next[2];
+                nro_fold_in(e.root, *e.episode, next);
+                seats[l] = nro_episode_seat(next);
+            }
         }
         if (out) {
             if (out->feature_maps) {

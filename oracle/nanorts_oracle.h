@@ -195,11 +195,15 @@ void nro_empty_actions(const nro_game* g, nro_abstract* carry, int64_t L);
  * direction or -1; out = {found, step, distance, pops}. */
 int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start, int32_t target,
                   int32_t range, int32_t out[4]);
-/* seat.step_seat with the learner at `learner`: actions [L][C][7] are the
- * learner's rows; the bot plays 1 - learner. */
+/* seat.step_seat: actions [L][C][7] are the learner's rows; the learner is
+ * seats[l] when `seats` is set, else `fixed`; the bot plays 1 - learner.
+ * With `draw`, a lane whose game ended takes nro_episode_seat of its next
+ * episode root. */
 void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, int64_t L, int32_t strategy,
-                   int32_t trained_type, int32_t learner, nro_abstract* carry, const int32_t* actions,
-                   int32_t partial, nro_env_out* out);
+                   int32_t trained_type, int32_t fixed, int32_t* seats, int32_t draw, nro_abstract* carry,
+                   const int32_t* actions, int32_t partial, nro_env_out* out);
+/* The "drawn" seat of an episode root: randint(fold_in(root, 2**32 - 2), 0, 2). */
+int32_t nro_episode_seat(const uint32_t episode_root[2]);
 
 /* GridNet decode_actions (src/nanorts/adapters/gridnet/actions.py:31-52):
  * per-cell actions [L][2][H*W][7] -> Commands [L][2][C] per field. */

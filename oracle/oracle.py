@@ -37,6 +37,7 @@ def _load() -> ctypes.CDLL:
     lib.nro_state_violations.restype = ctypes.c_int32
     lib.nro_conflict_draw.restype = ctypes.c_int32
     lib.nro_randint01.restype = ctypes.c_int32
+    lib.nro_episode_seat.restype = ctypes.c_int32
     lib.nro_astar.restype = ctypes.c_int32
     return lib
 
@@ -287,9 +288,12 @@ class Oracle:
                                      ctypes.byref(a), ctypes.byref(c))
         return out
 
-    def seat_step(self, state, carry: dict[str, np.ndarray], strategy: int, trained_type: int, learner: int,
-                  actions: np.ndarray, partial: bool, observe: bool = True) -> dict[str, np.ndarray]:
-        """step_seat with the learner's action rows [L][C][7]; state and carry updated in place."""
+    def seat_step(self, state, carry: dict[str, np.ndarray], strategy: int, trained_type: int, learner,
+                  actions: np.ndarray, partial: bool, observe: bool = True, draw: bool = False) -> dict[str, np.ndarray]:
+        """step_seat with the learner's action rows [L][C][7]; state and carry
+        updated in place.  `learner` is 0, 1 or an int32[L] array of per-lane
+        seats, which (with draw=True, the "drawn" rule) is updated in place
+        where a game ended."""
         L = state["time"].shape[0]
         b = self.game.bucket
         out = {"reward": np.zeros((L, 2), np.float32), "done": np.zeros(L, np.uint8),
@@ -300,10 +304,26 @@ class Oracle:
         o = EnvOut(*[_ptr(out[f]) for f, _ in EnvOut._fields_])
         a = Abstract(*[_ptr(carry[f]) for f in ABSTRACT_FIELDS])
         actions = np.ascontiguousarray(actions, np.int32)
+        seats = None
+        if isinstance(learner, np.ndarray):
+            seats = learner
+            if seats.dtype != np.int32 or seats.shape != (L,) or not seats.flags.c_contiguous:
+                raise ValueError(f"per-lane seats must be a contiguous int32[{L}] array")
         self.lib.nro_seat_step(ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)),
                                ctypes.c_int64(L), ctypes.c_int32(strategy), ctypes.c_int32(trained_type),
-                               ctypes.c_int32(learner), ctypes.byref(a), _ptr(actions), ctypes.c_int32(int(partial)),
-                               ctypes.byref(o))
+                               ctypes.c_int32(0 if seats is not None else int(learner)), _ptr(seats),
+                               ctypes.c_int32(int(draw)), ctypes.byref(a), _ptr(actions),
+                               ctypes.c_int32(int(partial)), ctypes.byref(o))
+        return out
+
+    def episode_seats(self, state) -> np.ndarray:
+        """The "drawn" seat of each lane's current episode root, int32[L]."""
+        lib = self.lib
+        out = np.zeros(state["time"].shape[0], np.int32)
+        for l, (root, ep) in enumerate(zip(state["environment_root"].reshape(-1, 2), state["episode_index"])):
+            k = (ctypes.c_uint32 * 2)()
+            lib.nro_fold_in((ctypes.c_uint32 * 2)(int(root[0]), int(root[1])), ctypes.c_uint32(int(ep)), k)
+            out[l] = lib.nro_episode_seat(k)
         return out
 
     def gridnet_decode(self, state, actions: np.ndarray) -> dict[str, np.ndarray]:

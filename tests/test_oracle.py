@@ -116,6 +116,36 @@ def test_oracle_draws_match_reference_live():
     assert 850 < ones < 1150  # a fair coin
 
 
+def test_drawn_seat_is_randint_of_the_seat_stream():
+    """The "drawn" seat (src/nanorts/bots/seat.py:32, 352-360) composes two
+    draws the golden vectors pin, fold_in and randint(…, 0, 2), with the seat
+    stream 2**32 - 2: it must equal that composition and differ from the
+    neighbouring streams (2**32 - 1, 0) and from the root's own draw, which a
+    dropped or wrong fold_in would give."""
+    import ctypes
+
+    lib = orc.load_library()
+    rng = np.random.default_rng(11)
+    ones, differs = 0, {0xFFFFFFFF: 0, 0: 0, None: 0}
+    for _ in range(2000):
+        root = (ctypes.c_uint32 * 2)(*[int(v) for v in rng.integers(0, 2**32, 2, dtype=np.uint64)])
+        got = lib.nro_episode_seat(root)
+
+        def draw(stream):
+            if stream is None:
+                return lib.nro_randint01(root)
+            k = (ctypes.c_uint32 * 2)()
+            lib.nro_fold_in(root, ctypes.c_uint32(stream), k)
+            return lib.nro_randint01(k)
+
+        assert got == draw(2**32 - 2)
+        for stream in differs:
+            differs[stream] += int(got != draw(stream))
+        ones += got
+    assert 850 < ones < 1150  # both seats, about evenly
+    assert all(count > 800 for count in differs.values()), differs
+
+
 # ---------------------------------------------------------------------------
 # Content
 # ---------------------------------------------------------------------------
