@@ -334,7 +334,7 @@ int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_stat
  * int32[L][C][7] are decoded, the merged commands go through core.step under
  * the episode root, auto-reset, and the carry is emptied where done.  Results
  * as nanorts_env_step, for both agents.  Replaces step_seat
- * (src/nanorts/bots/seat.py:94-152), which composes the bot's act,
+ * (src/nanorts/bots/seat.py:84-149), which composes the bot's act,
  * jaxmarl.request_against (src/nanorts/adapters/jaxmarl/env.py:78-96),
  * core.step and respond. */
 int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
@@ -346,7 +346,7 @@ int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state stat
  * game ended takes the seat drawn from its next episode's root,
  * randint(fold_in(episode_root, 2**32 - 2), (), 0, 2); otherwise the seats
  * stay (a per-lane Player array).  Replaces step_seat with seat="drawn" or
- * an Array seat (src/nanorts/bots/seat.py:94-152, 352-366). */
+ * an Array seat (src/nanorts/bots/seat.py:84-149, 352-366). */
 int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
                             nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
@@ -355,7 +355,7 @@ int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_stat
 /* The "drawn" rule's seat of each lane's current episode:
  * randint(fold_in(fold_in(environment_root, episode_index), 2**32 - 2), (),
  * 0, 2) into seats int32[L].  Replaces _episode_seat
- * (src/nanorts/bots/seat.py:352-360) as reset_seat calls it (lines 74-78). */
+ * (src/nanorts/bots/seat.py:352-360) as reset_seat calls it (line 77). */
 int nanorts_episode_seats(void* stream, const uint32_t* environment_root /* [L][2] */,
                           const uint32_t* episode_index /* [L] */, int64_t lanes, int32_t* seats);
 

@@ -159,7 +159,7 @@ class SeatEnv:
         return lanes.clone()
 
     def reset(self, key, seat=None) -> tuple[dict[str, Any], SeatState]:
-        """seat.reset_seat (src/nanorts/bots/seat.py:65-80); `seat` is the
+        """seat.reset_seat (src/nanorts/bots/seat.py:73-81); `seat` is the
         per-lane int32[L] seat of an env built by reset_seat."""
         obs, state = self.env.reset(key)
         L = state.num_envs
@@ -273,7 +273,7 @@ class SeatEnv:
         return 1 - self.learner if self.learner is not None else (1 - state.seat).contiguous()
 
     def step_request(self, state: SeatState, actions: dict[str, torch.Tensor]):
-        """seat.step_request (src/nanorts/bots/seat.py:100-112, 249-258): the
+        """seat.step_request (src/nanorts/bots/seat.py:100-111, 249-258): the
         bot's act on a copy of the carry, the learner's decoded rows and the
         bot's Commands merged ((episode-root keys, core State, Commands),
         the bot's new carry), ready for groups.step_groups."""
@@ -298,7 +298,7 @@ class SeatEnv:
         return (keys, core, cmds), carry
 
     def step_response(self, state: SeatState, carry: dict[str, torch.Tensor], stepped: dict[str, torch.Tensor]):
-        """seat.step_response (src/nanorts/bots/seat.py:115-152, 260-272) on a
+        """seat.step_response (src/nanorts/bots/seat.py:114-149, 260-272) on a
         state that core.step has advanced in place: the facade's response for
         the learner, the bot's new carry emptied where the game ended, and the
         next seat (drawn from the next episode's root where the game ended,
@@ -321,7 +321,7 @@ class SeatEnv:
                 {LEARNER: done, ALL_AGENTS: done}, out_infos)
 
     def observation_space(self, agent: str) -> dict[str, Any]:
-        """src/nanorts/bots/seat.py:206-211: player_0's space, the same for
+        """src/nanorts/bots/seat.py:208-213: player_0's space, the same for
         either seat."""
         if agent != LEARNER:
             raise ModelError(f"SeatEnv has the one agent {LEARNER!r}, not {agent!r}")
@@ -348,13 +348,13 @@ class SeatEnv:
 
     def commands(self, state: SeatState) -> dict[str, torch.Tensor]:
         """The bot's Commands for the current state (seat.seat_commands,
-        src/nanorts/bots/seat.py:155-161); the carry is updated in place."""
+        src/nanorts/bots/seat.py:152-157); the carry is updated in place."""
         return abstraction_act(self.env, state.environment_state, state.carry, self.bot, self._bot_players(state))
 
 
 @dataclasses.dataclass
 class SeatStep:
-    """src/nanorts/bots/seat.py:47-62"""
+    """src/nanorts/bots/seat.py:46-70"""
 
     seat_state: SeatState
     observation: Any
@@ -396,7 +396,7 @@ def _seat_env(bot: Bot, game: GameConfig, seat, options: dict[str, Any]) -> Seat
 
 def reset_seat(environment_root, game: GameConfig, *, bot: Bot, seat="player_0",
                **options) -> tuple[SeatState, Any]:
-    """seat.reset_seat (src/nanorts/bots/seat.py:65-80) over L envs: `seat`
+    """seat.reset_seat (src/nanorts/bots/seat.py:73-81) over L envs: `seat`
     is a rule ("player_0", "player_1", "drawn"), a Player index or an int32[L]
     per-lane seat; `options` are SeatEnv's (surface, partial_observability,
     final_observation, feature_dtype, reward_components, device)."""
@@ -407,7 +407,7 @@ def reset_seat(environment_root, game: GameConfig, *, bot: Bot, seat="player_0",
 
 def step_seat(seat_state: SeatState, actions: torch.Tensor, game: GameConfig, *, bot: Bot, seat="player_0",
               donate: bool = False, **options) -> SeatStep:
-    """seat.step_seat (src/nanorts/bots/seat.py:83-97) with the learner's
+    """seat.step_seat (src/nanorts/bots/seat.py:84-97) with the learner's
     actions int32[L, C, 7]; the same `seat` and options as reset_seat."""
     env = _seat_env(bot, game, seat, options)
     obs, state, reward, done, infos = env.step(None, seat_state, {LEARNER: actions}, donate=donate)
@@ -422,3 +422,30 @@ def carry_numpy(carry: dict[str, torch.Tensor]) -> dict[str, np.ndarray]:
     out = {k: v.cpu().numpy() for k, v in carry.items()}
     out["trained"] = out["trained"].astype(np.uint8)
     return out
+
+
+def seat_commands(seat_state: SeatState, game: GameConfig, *, bot: Bot, seat="player_0",
+                  **options) -> tuple[dict[str, torch.Tensor], dict[str, torch.Tensor]]:
+    """seat.seat_commands (src/nanorts/bots/seat.py:152-157): (the bot's new
+    carry, its Commands [L, 2, C] per field); the seat state is left as it is."""
+    env = _seat_env(bot, game, seat, options)
+    carry = {k: v.clone() for k, v in seat_state.carry.items()}
+    return carry, abstraction_act(env.env, seat_state.environment_state, carry, bot, env._bot_players(seat_state))
+
+
+def observe_seat(seat_state: SeatState, game: GameConfig, *, seat="player_0", **options) -> Any:
+    """seat.observe_seat (src/nanorts/bots/seat.py:160-164): the learner's
+    observation of each lane."""
+    return _seat_env(workerRushAI, game, seat, options).get_obs(seat_state)[LEARNER]
+
+
+def legal_seat_actions(seat_state: SeatState, game: GameConfig, *, seat="player_0", **options) -> torch.Tensor:
+    """seat.legal_seat_actions (src/nanorts/bots/seat.py:167-171): the
+    learner's masks bool[L, C, 78]."""
+    return _seat_env(workerRushAI, game, seat, options).get_avail_actions(seat_state)[LEARNER]
+
+
+def seat_slot_cells(seat_state: SeatState, game: GameConfig, *, seat="player_0", **options) -> torch.Tensor:
+    """seat.seat_slot_cells (src/nanorts/bots/seat.py:174-178): the learner's
+    slot cells int32[L, C]."""
+    return _seat_env(workerRushAI, game, seat, options).get_slot_cells(seat_state)[LEARNER]

@@ -784,12 +784,12 @@ __global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes,
     settle_carry(g, b, a.y, l, a.carry, lane);
 }
 
-// seat.step_seat (N/bots/seat.py:94-152): the bot's commands from the current
+// seat.step_seat (N/bots/seat.py:84-149): the bot's commands from the current
 // state, the learner's rows decoded (N/adapters/jaxmarl/env.py:78-96),
 // core.step under the episode root, auto-reset, the carry emptied where done,
 // observations.  The learner is `fixed` for every lane, or seats[l] when
 // `seats` is set; with `draw` a lane whose game ended takes the seat drawn
-// from its next episode's root (N/bots/seat.py:121-125).
+// from its next episode's root (N/bots/seat.py:119-123).
 __global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanorts_state s, BotArgs a, int32_t fixed,
                                                    int32_t* seats, int32_t draw, const int32_t* actions,
                                                    int32_t partial, nanorts_env_results r) {
@@ -845,7 +845,7 @@ __global__ __launch_bounds__(256) void k_seat_step(KGame g, int64_t lanes, nanor
 }
 
 // The "drawn" rule's learner of each lane's current episode
-// (N/bots/seat.py:74-78, 352-360): episode_seat(fold_in(root, episode)).
+// (N/bots/seat.py:77, 352-360): episode_seat(fold_in(root, episode)).
 __global__ __launch_bounds__(256) void k_episode_seats(int64_t lanes, const uint32_t* roots, const uint32_t* episodes,
                                                        int32_t* seats) {
     const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -12,7 +12,7 @@
  *                             stacks (equal to the program's argmin over
  *                             f * (cells + 1) + (cells - sequence) keys);
  *   N/bots/family.py:34-41    act (WORKER_RUSH = 0, BARRACKS_RUSH = 1);
- *   N/bots/seat.py:94-152     step_seat with a static learner seat.
+ *   N/bots/seat.py:84-149     step_seat with a static learner seat.
  *
  * The carry (AbstractActions, N/bots/abstraction.py:70-81) is nine int32
  * rows, a bool row and next_order per env.
@@ -774,7 +774,7 @@ int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start,
     return step;
 }
 
-/* step_seat (N/bots/seat.py:94-152) with the learner at a static seat: the
+/* step_seat (N/bots/seat.py:84-149) with the learner at a static seat: the
  * bot's commands from the current state, the learner's actions decoded
  * (N/adapters/jaxmarl/env.py:78-96, every agent reading the same rows), the
  * merged commands stepped under the episode root, auto-reset, the carry back
@@ -787,7 +787,7 @@ int32_t nro_episode_seat(const uint32_t episode_root[2]) {
     return nro_randint01(k);
 }
 
-/* N/bots/seat.py:94-152: the learner of lane l is seats[l] when `seats` is
+/* N/bots/seat.py:84-149: the learner of lane l is seats[l] when `seats` is
  * set (else `learner`); with `draw`, a lane whose game ended takes the seat
  * of its next episode's root (lines 121-125), otherwise it keeps its seat. */
 void nro_seat_step(const nro_game* g, const nro_state* initial, nro_state* s, int64_t L, int32_t strategy,

@@ -4,8 +4,8 @@ step_groups runs core.step for six groups (two maps of one bucket, three
 horizons, per-lane and broadcast keys) in one call, which the library splits
 into two launches; every group's state and outputs are compared bit for bit
 with the oracle's core.step of that group alone.  GroupMix publishes a
-facade group and two learner-vs-bot groups agent-major; its rows are
-compared with each environment stepped on its own.
+facade group and two learner-vs-bot groups (one under the drawn seat rule)
+agent-major; its rows are compared with each environment stepped on its own.
 """
 from __future__ import annotations
 
@@ -87,7 +87,7 @@ def test_group_mix_publishes_each_group_agent_major():
     plain, _, _ = _games()
     both = nanorts_amd.make("NanoRTS", scenario=plain, device="cuda:0")
     worker = bots.SeatEnv(bots.workerRushAI, scenario=plain, device="cuda:0")
-    light = bots.SeatEnv(bots.lightRushAI, scenario=plain, device="cuda:0")
+    light = bots.SeatEnv(bots.lightRushAI, scenario=plain, seat="drawn", device="cuda:0")
     lanes = (8, 6, 5)
     envs = (both, worker, light)
     mix = GroupMix([Group(env, n) for env, n in zip(envs, lanes)])

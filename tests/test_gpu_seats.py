@@ -215,6 +215,25 @@ def test_seat_functions_with_a_per_lane_seat():
     assert_states_equal(ref, to_host(state.environment_state), "final state")
     _carry_equal(carry, state.carry, "final")
     assert ended > 0
+    # the other seat functions read the learner's side of each lane
+    masks = bots.legal_seat_actions(state, game, seat=given, device="cuda:0").cpu().numpy()
+    np.testing.assert_array_equal(masks, _at(oracle.avail_rows(ref), given))
+    maps, scalars = oracle.symbolic(ref, False)
+    seen = bots.observe_seat(state, game, seat=given, device="cuda:0")
+    np.testing.assert_array_equal(seen.feature_maps.cpu().numpy(), _at(maps, given))
+    np.testing.assert_array_equal(seen.scalars.cpu().numpy(), _at(scalars, given))
+    n = game.bucket.neutral_capacity
+    cells = ref["cell"][:, n:].astype(np.int32).reshape(L, 2, -1)
+    np.testing.assert_array_equal(bots.seat_slot_cells(state, game, seat=given, device="cuda:0").cpu().numpy(),
+                                  _at(cells, given))
+    before = {k: v.clone() for k, v in state.carry.items()}
+    new_carry, cmds = bots.seat_commands(state, game, bot=bot, seat=given, device="cuda:0")
+    for name in before:
+        assert torch.equal(state.carry[name], before[name]), "seat_commands leaves the seat state's carry"
+    want = oracle.abstraction_act(ref, carry, bot.strategy, bot.trained, (1 - given).astype(np.int32))
+    for name, value in want.items():
+        np.testing.assert_array_equal(cmds[name].cpu().numpy(), value, err_msg=f"bot Commands {name}")
+    _carry_equal(carry, new_carry, "after seat_commands")
     one, _ = bots.reset_seat(keys, game, bot=bot, seat=1, device="cuda:0")
     assert torch.equal(one.seat, torch.ones(L, dtype=torch.int32, device="cuda:0"))
     drawn, _ = bots.reset_seat(keys, game, bot=bot, seat="drawn", device="cuda:0")
