@@ -245,3 +245,37 @@ def test_seat_functions_with_a_per_lane_seat():
                         device="cuda:0")
     with pytest.raises(ModelError):
         bots.SeatEnv(bot, scenario=game, seat="random", device="cuda:0")
+
+
+def test_drawn_seat_on_the_pixel_surface():
+    """The per-lane pick on images: each lane's learner image (at its drawn
+    seat) against the oracle's renderer, across an episode end."""
+    import torch
+
+    from nanorts_amd import bots, rendering
+
+    _say("drawn seat pixels")
+    torch.cuda.set_device(0)
+    game = _game()
+    bot = bots.lightRushAI
+    seat = bots.SeatEnv(bot, scenario=game, surface="pixels", seat="drawn", device="cuda:0")
+    L = 12
+    keys = roots(L, 41)
+    obs, sst = seat.reset(keys)
+    oracle = Oracle(game)
+    ref = batch_initial(game, L, keys)
+    carry = empty_carry(L, game.bucket.per_player_capacity)
+    seats = oracle.episode_seats(ref)
+    tiles = rendering.tile_table(game.bucket.unit_type_capacity)
+    image, _ = oracle.pixels(ref, False, tiles)
+    np.testing.assert_array_equal(obs[bots.LEARNER].image.cpu().numpy(), _at(image, seats))
+    for t in range(HORIZON + 4):
+        acts = np.ascontiguousarray(_at(oracle.sample_actions(oracle.avail_rows(ref), (43, 47), t), seats))
+        oracle.seat_step(ref, carry, bot.strategy, bot.trained, seats, acts, False, observe=False, draw=True)
+        obs, sst, _, _, _ = seat.step(None, sst, {bots.LEARNER: torch.as_tensor(acts, device="cuda:0")}, donate=True)
+        if t % 8 == 0 or t >= HORIZON - 2:
+            image, scalars = oracle.pixels(ref, False, tiles)
+            np.testing.assert_array_equal(obs[bots.LEARNER].image.cpu().numpy(), _at(image, seats),
+                                          err_msg=f"cycle {t}")
+            np.testing.assert_array_equal(obs[bots.LEARNER].scalars.cpu().numpy(), _at(scalars, seats))
+    np.testing.assert_array_equal(sst.seat.cpu().numpy(), seats)
