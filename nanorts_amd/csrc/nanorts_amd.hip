@@ -1545,7 +1545,8 @@ const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
 const char* nanorts_targets(void) {
     return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
            "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_step_groups,nanorts_env_transition,nanorts_decode_actions,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,nanorts_gridnet_decode,"
+           "nanorts_step_groups,nanorts_env_transition,nanorts_decode_actions,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,"
+           "nanorts_seat_step_lanes,nanorts_seat_rollout_lanes,nanorts_episode_seats,nanorts_gridnet_decode,"
            "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against,nanorts_gridnet_sample_actions";
 }
 

@@ -42,3 +42,35 @@ def test_invalid_game_is_refused_without_touching_a_device():
     code = lib.nanorts_legality_words(None, ctypes.byref(game), native.State(), 1, None)
     assert code == 1
     assert "cells" in lib.nanorts_last_error().decode()
+
+
+def test_targets_name_every_compute_entry_point():
+    lib = native.load()
+    targets = set(lib.nanorts_targets().decode().split(","))
+    meta = {"nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check"}
+    assert targets == set(declared_entry_points()) - meta
+
+
+def test_seat_entry_points_refuse_bad_arguments_without_touching_a_device():
+    """The per-lane seat entries validate before any launch: NULL seats, a
+    learner outside 0/1, NULL or negative-size episode seat operands."""
+    lib = native.load()
+    buf = (ctypes.c_uint8 * 64)()
+    addr = ctypes.cast(buf, ctypes.c_void_p)
+    state = native.State(*[addr] * len(native.STATE_FIELDS))
+    carry = native.AbstractActions(*[addr] * len(native.ABSTRACT_FIELDS))
+    results = native.EnvResults()
+    game = native.Game()
+    code = lib.nanorts_seat_step_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, carry, addr, 0, results)
+    assert code == 1 and "seats is NULL" in lib.nanorts_last_error().decode()
+    code = lib.nanorts_seat_step(None, ctypes.byref(game), state, 1, 0, 4, 2, carry, addr, 0, results)
+    assert code == 1 and "learner must be 0 or 1" in lib.nanorts_last_error().decode()
+    key = (ctypes.c_uint32 * 2)(1, 2)
+    code = lib.nanorts_seat_rollout_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, None, carry, key, 0, 1,
+                                          0, 0, native.RolloutResults())
+    assert code == 1 and "seats is NULL" in lib.nanorts_last_error().decode()
+    code = lib.nanorts_episode_seats(None, None, addr, 1, addr)
+    assert code == 1 and "NULL" in lib.nanorts_last_error().decode()
+    code = lib.nanorts_episode_seats(None, addr, addr, -1, addr)
+    assert code == 1 and "lanes" in lib.nanorts_last_error().decode()
+    assert lib.nanorts_episode_seats(None, addr, addr, 0, addr) == 0
