@@ -246,8 +246,9 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.v_oseen = take(2 * g.H * g.seen_words * 4);
     y.v_stage = take(2 * g.stage_cells * 6);
     if (o > end) end = o;
-    // masks staging (k_legality)
-    o = union0;
+    // masks staging (k_legality), after the occupancy bitmaps its rows read
+    o = y.o_bm;
+    take(6 * g.H * g.seen_words * 4);
     y.v_words = take(C2 * 12);
     if (o > end) end = o;
     y.env_bytes = align16(end);
@@ -542,7 +543,11 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
 
 // Legality words of every owned row into the staged words area; `merge`
 // applies availability (only NONE on unavailable rows).
+// The rows come from the occupancy bitmaps (legality_row_w1 on boards of at
+// most 32 columns, legality_row_bm otherwise), the same bits as legality_row.
 NR_DEV void stage_words(const KGame& g, const Hdr& h, const Env& e, int lane, bool merge) {
+    build_bitmaps(g, h, e, lane);
+    const bool narrow = g.fast_obs && g.seen_words == 1;
     AS3 uint32_t* words = at<uint32_t>(e, g.lay.v_words);
     for (int32_t p = lane; p < 2 * g.C; p += kWave) {
         const int32_t s = g.N + p;
@@ -552,7 +557,7 @@ NR_DEV void stage_words(const KGame& g, const Hdr& h, const Env& e, int lane, bo
             r.w[0] = 1u;
             r.w[1] = r.w[2] = 0u;
         } else {
-            r = legality_row(g, h, e, s);
+            r = narrow ? legality_row_w1(g, h, e, s) : legality_row_bm(g, h, e, s);
         }
         words[3 * p] = r.w[0];
         words[3 * p + 1] = r.w[1];
