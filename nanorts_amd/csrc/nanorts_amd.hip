@@ -277,6 +277,45 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     return fit_waves(out, why);
 }
 
+// A smaller env block for the kernels that read a few leaves: `masks` holds
+// the leaves the legality rows read, the occupancy bitmaps and the staged
+// words (k_legality); otherwise the block is empty (the samplers read only
+// the header).  Every other offset is 0 and unused by those kernels.  More
+// games then share a CU than the full block allows.
+bool shape_for_reader(const nanorts_game* game, bool masks, Shape* out, std::string* why) {
+    if (!shape_for(game, out, why)) return false;
+    KGame& g = out->g;
+    Layout& y = g.lay;
+    const Layout full = y;
+    std::memset(&y, 0, sizeof(y));
+    y.hdr_bytes = full.hdr_bytes;
+    y.o_seg = full.o_seg;
+    y.o_terrain = full.o_terrain;
+    y.o_disk = full.o_disk;
+    int32_t o = 0;
+    auto take = [&o](int32_t bytes) {
+        const int32_t at = o;
+        o += align16(bytes);
+        return at;
+    };
+    if (masks) {
+        const int32_t E = g.E;
+        y.o_birth = take(E * 4);
+        y.o_carried = take(E * 4);
+        y.o_cell = take(E * 2);
+        y.o_entity = take(g.cells * 2);
+        y.o_utype = take(E);
+        y.o_owner = take(E);
+        y.o_pkind = take(E);
+        y.o_scal = take(S_COUNT * 4);
+        y.o_bm = take(6 * g.H * g.seen_words * 4);
+        y.v_words = take(2 * g.C * 12);
+    }
+    y.env_bytes = align16(o > 16 ? o : 16);
+    g.nseg = 0;
+    return fit_waves(out, why);
+}
+
 // GridNet decode scratch (gridnet.h) in the env block's phase union, after
 // the command arrays the decode fills.
 bool shape_for_gridnet(const nanorts_game* game, Shape* out, GridLayout* gy, std::string* why) {
@@ -1610,6 +1649,13 @@ const char* nanorts_self_check(const int32_t* devices, int64_t n) {
         if (!shape_for(game, &sh, &why)) return fail(NANORTS_INVALID_ARGUMENT, why); \
     }
 
+#define NR_READER_SHAPE(game, masks)                                                  \
+    Shape sh;                                                                         \
+    {                                                                                 \
+        std::string why;                                                              \
+        if (!shape_for_reader(game, masks, &sh, &why)) return fail(NANORTS_INVALID_ARGUMENT, why); \
+    }
+
 #define NR_STATE(state)                                                                      \
     if (!state_complete(state)) return fail(NANORTS_INVALID_ARGUMENT, "a State leaf pointer is NULL");
 
@@ -1681,7 +1727,7 @@ int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const*
 }
 
 int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows) {
-    NR_SHAPE(game)
+    NR_READER_SHAPE(game, true)
     NR_STATE(state)
     if (!rows) return fail(NANORTS_INVALID_ARGUMENT, "rows is NULL");
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, rows, (uint32_t*)nullptr);
@@ -1689,7 +1735,7 @@ int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state
 
 int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            uint32_t* words) {
-    NR_SHAPE(game)
+    NR_READER_SHAPE(game, true)
     NR_STATE(state)
     if (!words) return fail(NANORTS_INVALID_ARGUMENT, "words is NULL");
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, (uint8_t*)nullptr, words);
@@ -1697,7 +1743,7 @@ int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state
 
 int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows,
                           uint32_t* words) {
-    NR_SHAPE(game)
+    NR_READER_SHAPE(game, true)
     NR_STATE(state)
     if (!rows && !words) return fail(NANORTS_INVALID_ARGUMENT, "rows and words are both NULL");
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 1, rows, words);
@@ -1877,7 +1923,7 @@ int nanorts_episode_seats(void* stream, const uint32_t* environment_root, const 
 
 int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
                            const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
-    NR_SHAPE(game)
+    NR_READER_SHAPE(game, false)
     if (!avail_words || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
     return launch(k_sample, sh, lanes, (hipStream_t)stream, avail_words, sample_key[0], sample_key[1], step, env0,
                   actions);
@@ -1885,7 +1931,7 @@ int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes
 
 int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
                                    const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
-    NR_SHAPE(game)
+    NR_READER_SHAPE(game, false)
     if (!mask || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
     if (sh.g.T != 7 || sh.g.O != 49)
         return fail(NANORTS_INVALID_ARGUMENT, "the GridNet surface is pinned to 7 unit types and a 49-cell attack window");
