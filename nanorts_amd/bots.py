@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
+import weakref
 from typing import Any, Final
 
 import numpy as np
@@ -370,7 +371,8 @@ class SeatStep:
     final_valid: torch.Tensor
 
 
-_SEAT_ENVS: dict[tuple, SeatEnv] = {}
+# The SeatEnvs behind the seat functions, per game and (bot, rule, options).
+_SEAT_ENVS: "weakref.WeakKeyDictionary[GameConfig, dict[tuple, SeatEnv]]" = weakref.WeakKeyDictionary()
 
 
 def _seat_env(bot: Bot, game: GameConfig, seat, options: dict[str, Any]) -> SeatEnv:
@@ -384,13 +386,14 @@ def _seat_env(bot: Bot, game: GameConfig, seat, options: dict[str, Any]) -> Seat
         rule = _PLAYERS[seat]
     else:
         rule = "lanes"
-    key = (bot, id(game), rule, tuple(sorted((k, str(v)) for k, v in options.items())))
-    env = _SEAT_ENVS.get(key)
-    if env is None or env.game is not game:
+    per_game = _SEAT_ENVS.setdefault(game, {})
+    key = (bot, rule, tuple(sorted((k, str(v)) for k, v in options.items())))
+    env = per_game.get(key)
+    if env is None:
         env = SeatEnv(bot, scenario=game, seat="drawn" if rule == "lanes" else rule, **options)
         if rule == "lanes":
             env.seat, env.draw = "lanes", False
-        _SEAT_ENVS[key] = env
+        per_game[key] = env
     return env
 
 
