@@ -385,8 +385,57 @@ enum : uint32_t {
     LD_ALL = 0xFFFFu,
 };
 
+// The staged leaves: flag, State field, Env member, element type, count.
+#define NR_LEAVES(X)                                                   \
+    X(LD_BIRTH, birth, birth, int32_t, E)                              \
+    X(LD_UTYPE, unit_type, utype, int8_t, E)                           \
+    X(LD_OWNER, owner, owner, int8_t, E)                               \
+    X(LD_CELL, cell, cell, int16_t, E)                                 \
+    X(LD_HP, hit_points, hp, int16_t, E)                               \
+    X(LD_CARRIED, carried_resources, carried, int32_t, E)              \
+    X(LD_PKIND, pending_kind, pkind, int8_t, E)                        \
+    X(LD_PDIR, pending_direction, pdir, int8_t, E)                     \
+    X(LD_PNONE, pending_none_duration, pnone, int32_t, E)              \
+    X(LD_PTARGET, pending_target_cell, ptarget, int16_t, E)            \
+    X(LD_PPTYPE, pending_produced_type, pptype, int8_t, E)             \
+    X(LD_PISSUED, pending_issued_at, pissued, int32_t, E)              \
+    X(LD_PCOMPL, pending_completes_at, pcompl, int32_t, E)             \
+    X(LD_PORDER, pending_order, porder, int32_t, E)                    \
+    X(LD_ENTITY, entity_at, entity, int16_t, cells)
+
+// Leaves of at most 1024 bytes (one 16-byte vector per lane), 16-byte
+// aligned: every requested leaf is loaded into registers before the first
+// LDS store, so the wave waits on memory once instead of once per leaf.
+// False (nothing done) when a leaf does not qualify.
+NR_DEV bool load_leaves_batched(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, uint32_t which,
+                                int lane) {
+    const int64_t E = g.E, cells = g.cells;
+    uint64_t bad = 0u;
+#define NR_CHECK(flag, field, member, type, count)                                                 \
+    if (which & flag) {                                                                            \
+        const int64_t bytes = count * (int64_t)sizeof(type);                                       \
+        bad |= ((uint64_t)(uintptr_t)(s.field + l * count) | (uint64_t)bytes) & 15u;               \
+        if (bytes > 16 * kWave) bad |= 1u;                                                         \
+    }
+    NR_LEAVES(NR_CHECK)
+#undef NR_CHECK
+    if (bad != 0u) return false;
+#define NR_LOAD(flag, field, member, type, count)                                                  \
+    u32x4 v_##member = {0u, 0u, 0u, 0u};                                                           \
+    const int32_t n_##member = (int32_t)((count * (int64_t)sizeof(type)) >> 4);                    \
+    if ((which & flag) && lane < n_##member) v_##member = ((const u32x4*)(s.field + l * count))[lane];
+    NR_LEAVES(NR_LOAD)
+#undef NR_LOAD
+#define NR_STORE(flag, field, member, type, count) \
+    if ((which & flag) && lane < n_##member) ((AS3 u32x4*)e.member)[lane] = v_##member;
+    NR_LEAVES(NR_STORE)
+#undef NR_STORE
+    return true;
+}
+
 NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, uint32_t which, int lane) {
     const int64_t E = g.E, cells = g.cells;
+    if (load_leaves_batched(g, s, l, e, which, lane)) which &= ~(uint32_t)(LD_SCALARS - 1u);
 #define NR_IN(flag, field, member, type) \
     if (which & flag) copy_in((AS3 uint8_t*)e.member, (const uint8_t*)(s.field + l * E), (int32_t)(E * sizeof(type)), lane);
     NR_IN(LD_BIRTH, birth, birth, int32_t)
