@@ -668,21 +668,6 @@ __global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_s
     store_env(g, s, l, e, lane);
 }
 
-// Decode int32[2C][7] actions of env l into canonical commands.
-NR_DEV void stage_actions(const KGame& g, const Env& e, int64_t l, const int32_t* actions, int lane) {
-    const int32_t owned = 2 * g.C;
-    for (int32_t p = lane; p < owned; p += kWave) {
-        const int32_t* row = actions + (l * owned + p) * 7;
-        int32_t a[7];
-#pragma unroll
-        for (int f = 0; f < 7; ++f) a[f] = row[f];
-        const int32_t s = g.N + p;
-        const bool available = e.birth[s] != kAbsent && e.pkind[s] == kAbsent;
-        decode_row(g, e, p, available, a);
-    }
-    wave_sync();
-}
-
 // After core.step: outcome, rewards, optional final observation, auto-reset.
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
                         const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true) {
