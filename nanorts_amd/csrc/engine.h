@@ -479,10 +479,39 @@ NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const En
     wave_sync();
 }
 
+// store_env's counterpart of load_leaves_batched: every leaf is read from
+// LDS before the first global store.  False (nothing done) when a leaf does
+// not qualify.
+NR_DEV bool store_leaves_batched(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    const int64_t E = g.E, cells = g.cells;
+    uint64_t bad = 0u;
+#define NR_CHECK(flag, field, member, type, count)                                                 \
+    {                                                                                              \
+        const int64_t bytes = count * (int64_t)sizeof(type);                                       \
+        bad |= ((uint64_t)(uintptr_t)(s.field + l * count) | (uint64_t)bytes) & 15u;               \
+        if (bytes > 16 * kWave) bad |= 1u;                                                         \
+    }
+    NR_LEAVES(NR_CHECK)
+#undef NR_CHECK
+    if (bad != 0u) return false;
+#define NR_READ(flag, field, member, type, count)                                                  \
+    u32x4 v_##member = {0u, 0u, 0u, 0u};                                                           \
+    const int32_t n_##member = (int32_t)((count * (int64_t)sizeof(type)) >> 4);                    \
+    if (lane < n_##member) v_##member = ((const AS3 u32x4*)e.member)[lane];
+    NR_LEAVES(NR_READ)
+#undef NR_READ
+#define NR_WRITE(flag, field, member, type, count) \
+    if (lane < n_##member) ((u32x4*)(s.field + l * count))[lane] = v_##member;
+    NR_LEAVES(NR_WRITE)
+#undef NR_WRITE
+    return true;
+}
+
 NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
     const int64_t E = g.E, cells = g.cells;
+    const bool batched = store_leaves_batched(g, s, l, e, lane);
 #define NR_OUT(field, member, type) \
-    copy_out((uint8_t*)(s.field + l * E), (const AS3 uint8_t*)e.member, (int32_t)(E * sizeof(type)), lane);
+    if (!batched) copy_out((uint8_t*)(s.field + l * E), (const AS3 uint8_t*)e.member, (int32_t)(E * sizeof(type)), lane);
     NR_OUT(birth, birth, int32_t)
     NR_OUT(unit_type, utype, int8_t)
     NR_OUT(owner, owner, int8_t)
@@ -498,7 +527,7 @@ NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const E
     NR_OUT(pending_completes_at, pcompl, int32_t)
     NR_OUT(pending_order, porder, int32_t)
 #undef NR_OUT
-    copy_out((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
+    if (!batched) copy_out((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
     if (lane < S_COUNT) {
         const int32_t v = e.sc[lane];
         switch (lane) {
