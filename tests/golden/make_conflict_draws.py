@@ -53,6 +53,27 @@ def main() -> None:
     for _ in range(12):
         k = key()
         out["race"].append({"root": k, "out": int(ref.ref_conflict_draw(U2(*k), 0, 5, 0))})
+    # Hand-traced rule tests (tests/test_oracle_rules.py), drawn from a
+    # stream of their own so the vectors above stay as they were:
+    #   "settle": one request with two same-cycle conflicts, the request's
+    #     slot born 3, ordinals 0 and 1 at time 0;
+    #   "race3": a three-unit race into one cell, the second and third
+    #     requests born 6 and 7, ordinal 0 each at time 0.
+    extra = np.random.default_rng(20261202)
+
+    def extra_key():
+        return [int(v) for v in extra.integers(0, 2**32, 2, dtype=np.uint64)]
+
+    out["settle"] = []
+    for _ in range(24):
+        k = extra_key()
+        out["settle"].append({"root": k, "time": 0, "birth": 3,
+                              "out": [int(ref.ref_conflict_draw(U2(*k), 0, 3, n)) for n in (0, 1)]})
+    out["race3"] = []
+    for _ in range(24):
+        k = extra_key()
+        out["race3"].append({"root": k, "time": 0, "births": [6, 7],
+                             "out": [int(ref.ref_conflict_draw(U2(*k), 0, b, 0)) for b in (6, 7)]})
     path = Path(__file__).with_name("conflict_draws.json")
     path.write_text(json.dumps(out, indent=1) + "\n")
     print(f"wrote {path}")

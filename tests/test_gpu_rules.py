@@ -1,0 +1,86 @@
+"""The hand-traced rule scenarios of tests/test_oracle_rules.py on the GPU.
+
+Every cycle of every scenario is also run through the HIP core.step
+(nanorts_amd.core.step -> the library's step entry) on a device copy of the
+state taken just before the cycle; after the cycle every State leaf and the
+step results must equal the oracle's, which those scenarios pin to values
+worked out by hand (a dead attacker still hits, a dead returner still
+credits, a dead producer still spawns, the admitted counts, the settled
+durations of two conflicts and of a three-unit race under every strategy).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests import test_oracle_rules as rules
+from tests.helpers import assert_states_equal
+
+pytestmark = pytest.mark.gpu
+
+FIELDS = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+
+
+class DeviceBoard(rules.Board):
+    """A Board whose every core.step also runs on the GPU."""
+
+    def before_step(self) -> None:
+        import torch
+
+        from nanorts_amd.env import State
+        from nanorts_amd.model import LEAF_NAMES
+
+        self.dev = State({name: torch.as_tensor(np.ascontiguousarray(self.st[name]), device="cuda:0")
+                          for name in LEAF_NAMES})
+
+    def after_step(self, commands: dict, out: dict) -> None:
+        import torch
+
+        from nanorts_amd import core
+
+        got = core.step(self.root.copy(), self.dev, {f: torch.as_tensor(commands[f], device="cuda:0") for f in FIELDS},
+                        self.game)
+        leaves = {name: t.cpu().numpy() for name, t in self.dev.leaves.items()}
+        want = {k: v for k, v in self.st.items() if k in leaves}
+        assert_states_equal(want, leaves, f"time {int(self.st['time'][0])}")
+        for name in ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
+                     "admitted_attack"):
+            np.testing.assert_array_equal(got[name].cpu().numpy().astype(out[name].dtype), out[name], err_msg=name)
+        self.cycles = getattr(self, "cycles", 0) + 1
+
+
+SCENARIOS = [
+    ("dead attacker", rules.test_dead_attacker_still_hits, ()),
+    ("dead returner", rules.test_dead_returner_still_credits, ()),
+    ("live returner", rules.test_live_returner_credits_and_empties_its_hands, ()),
+    ("dead producer", rules.test_dead_producer_still_spawns, ()),
+    ("admitted counts", rules.test_admitted_counts_follow_the_post_legality_kind, ()),
+    ("settle both", rules.test_two_conflicts_settle_durations, ("both", rules.BOTH, 0)),
+    ("settle alternating 0", rules.test_two_conflicts_settle_durations, ("alternating0", rules.ALTERNATING, 0)),
+    ("settle alternating 1", rules.test_two_conflicts_settle_durations, ("alternating1", rules.ALTERNATING, 1)),
+    ("settle random", rules.test_two_conflicts_settle_durations_random, ()),
+    ("settle plays out", rules.test_two_conflicts_play_out, ()),
+    ("race both", rules.test_three_unit_race, ("both", rules.BOTH, 0)),
+    ("race alternating 0", rules.test_three_unit_race, ("alternating0", rules.ALTERNATING, 0)),
+    ("race alternating 1", rules.test_three_unit_race, ("alternating1", rules.ALTERNATING, 1)),
+    ("race random", rules.test_three_unit_race_random, ()),
+    ("race arrival", rules.test_three_unit_race_the_mover_arrives_on_time, ()),
+]
+
+
+@pytest.mark.parametrize("label,scenario,args", SCENARIOS, ids=[s[0] for s in SCENARIOS])
+def test_rule_scenario_on_gpu(label, scenario, args, monkeypatch):
+    import torch
+
+    print(f"rule scenario {label}", flush=True)
+    torch.cuda.set_device(0)
+    boards = []
+
+    def make(*a, **k):
+        board = DeviceBoard(*a, **k)
+        boards.append(board)
+        return board
+
+    monkeypatch.setattr(rules, "BOARD", make)
+    scenario(*args)
+    assert boards and all(getattr(b, "cycles", 0) > 0 for b in boards)
