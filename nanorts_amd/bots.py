@@ -127,10 +127,10 @@ class SeatEnv:
                  final_observation: bool = True, feature_dtype: Any = None, reward_components: bool = False,
                  device: str | torch.device | None = None):
         if not isinstance(seat, str) or seat not in SEAT_RULES:
-            raise ModelError(f"SeatEnv refuses seat={seat!r}: the accepted rules are {list(SEAT_RULES)}; a per-lane "
-                             "seat goes through reset_seat / step_seat")
+            raise ModelError(f"seat={seat!r} is not a seat rule ({list(SEAT_RULES)}); per-lane seat arrays are taken by "
+                             "reset_seat / step_seat")
         if bot.strategy not in (WORKER_RUSH, BARRACKS_RUSH):
-            raise ModelError(f"SeatEnv refuses bot {bot.name!r}: the rush family is built")
+            raise ModelError(f"bot {bot.name!r} is not available here; the seat plays WorkerRush or LightRush")
         game = scenario if utt is None else with_unit_type_table(scenario, utt)
         self.env = NanoRTS(game, surface=surface, partial_observability=partial_observability,
                            final_observation=final_observation, feature_dtype=feature_dtype,
@@ -174,7 +174,7 @@ class SeatEnv:
         place with donate=True, else copied first."""
         del key
         if reset_state is not None:
-            raise ModelError("SeatEnv.step refuses a reset_state: the auto-reset is the lifecycle's own")
+            raise ModelError("step resets finished games to the content's start by itself; reset_state is not taken")
         env = self.env
         nxt = state if donate else SeatState(state.environment_state.clone(),
                                              {k: v.clone() for k, v in state.carry.items()}, state.seat.clone())
@@ -382,7 +382,7 @@ def _seat_env(bot: Bot, game: GameConfig, seat, options: dict[str, Any]) -> Seat
         rule = seat
     elif isinstance(seat, int) and not isinstance(seat, bool):
         if seat not in (0, 1):
-            raise ModelError(f"the seat functions refuse seat={seat}: a Player index is 0 or 1")
+            raise ModelError(f"seat={seat} names no player; use 0 or 1")
         rule = _PLAYERS[seat]
     else:
         rule = "lanes"

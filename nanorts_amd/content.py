@@ -1,16 +1,28 @@
-"""Map XML -> game configuration and initial state.
+"""Game content: a MicroRTS map document -> GameConfig (board, unit table,
+bucket shapes and the decided initial State of one env).
 
-Restates src/nanorts/content/{loading,normalize,scenarios}.py of the reference:
-the MicroRTS map document is parsed, the slot capacities are derived from the
-resource bound (normalize.py:87-154), units are placed in document order into
-the neutral / player-0 / player-1 slot blocks (normalize.py:180-231), and the
-shipped capacity profiles cap 16x16 at 70 slots per player (scenarios.py:20-42).
+Follows the reference's content package (src/nanorts/content/): the map XML
+(loading.py:34-113), six numbered acceptance clauses (acceptance.py), the
+bucket derived from the content (normalize.py:45-116), units placed in
+document order into their owner's slot block (normalize.py:119-170) and the
+shipped maps with their capacity profiles (scenarios.py).
+
+How it is organised here:
+- `read_map_xml` turns the XML into a `MapDocument` of plain values through
+  an `_XmlReader` that knows which clause each element belongs to;
+- `findings` walks a document and yields (clause, what is wrong) pairs in
+  clause order; `check_document` refuses on the first one;
+- `population_ceiling` is the most units one player can ever own, from the
+  map's wealth and the cheapest trainable unit; `derive_bucket` sizes the
+  slot blocks from it;
+- `_SlotCursor` hands out each block's next slot while the units are placed.
 """
 from __future__ import annotations
 
 import dataclasses
 import os
 import re
+from collections.abc import Iterator, Sequence
 from pathlib import Path
 from typing import Final
 from xml.etree import ElementTree
@@ -19,7 +31,6 @@ import numpy as np
 
 from nanorts_amd.model import (
     ABSENT,
-    KIND_ABSENT,
     OWNER_NEUTRAL,
     PLAYER_COUNT,
     STATE_LEAVES,
@@ -36,24 +47,39 @@ from nanorts_amd.model import (
 
 MAP_DIRECTORY: Final = Path(__file__).resolve().parent / "maps"
 
+# Slot profiles of the shipped maps (src/nanorts/content/scenarios.py:20-22):
+# a per-player capacity below the derived one, applied by map_name_to_scenario.
 CAPACITY_PROFILES: Final = {"basesWorkers8x8": 52, "basesWorkers16x16": 70}
 
-_INTEGER = re.compile(r"[+-]?[0-9]+")
+_SHIPPED: Final = {path.stem: path for path in sorted(MAP_DIRECTORY.rglob("*.xml"))}
+SCENARIO_NAMES: Final = tuple(sorted(_SHIPPED))
+
+_SIGNED_32: Final = range(-(2**31), 2**31)
+_HIT_POINT_RANGE: Final = range(0, 2**15)
+_WHOLE_NUMBER: Final = re.compile(r"[+-]?\d+")
 
 
 class ContentError(ModelError):
-    """A map document the loader refuses (src/nanorts/content/document.py:6-10).
-    `clause` names the acceptance clause the document breaks: 1 the document
-    and its extents, 2 the terrain payload, 3 binary terrain, 4 the player
-    records, 5 the unit records, 6 hit points."""
+    """Content the loader refuses.  `clause` is the acceptance clause it
+    breaks (src/nanorts/content/document.py:6-10): 1 the document and its
+    extents, 2 the terrain payload, 3 binary terrain, 4 the player records,
+    5 the unit records, 6 hit points; None for a refusal outside the
+    clauses (a bucket, a table, a full slot block)."""
 
     def __init__(self, message: str, *, clause: int | None = None) -> None:
         super().__init__(message)
         self.clause = clause
 
 
+def _refusal(clause: int, finding: str) -> ContentError:
+    return ContentError(f"clause {clause}: {finding}", clause=clause)
+
+
 @dataclasses.dataclass(frozen=True)
 class UnitRecord:
+    """One <rts.units.Unit> of a map (field order of the reference's
+    UnitRecord, src/nanorts/content/document.py:13-21)."""
+
     type: str
     id: int
     player: int
@@ -64,7 +90,10 @@ class UnitRecord:
 
 
 @dataclasses.dataclass(frozen=True)
-class ContentDocument:
+class MapDocument:
+    """A map as plain values: extents, terrain digits, the player records as
+    (ID, starting resources) and the unit records in document order."""
+
     width: int
     height: int
     terrain: str
@@ -90,326 +119,365 @@ class GameConfig:
         return unit_columns(self.unit_types)
 
 
-_INT32 = range(-(2**31), 2**31)
-_HIT_POINTS = range(2**15)
+# ---------------------------------------------------------------------------
+# Acceptance (src/nanorts/content/acceptance.py): findings in clause order
+# ---------------------------------------------------------------------------
+def _extent_findings(width: int, height: int) -> Iterator[tuple[int, str]]:
+    for label, value in (("width", width), ("height", height)):
+        if value not in _SIGNED_32:
+            yield 1, f"the {label} {value} does not fit a signed 32-bit integer"
+        elif value < 1:
+            yield 1, f"the {label} must be at least 1, not {value}"
 
 
-def _refuse(clause: int, message: str) -> ContentError:
-    return ContentError(f"clause {clause}: {message}", clause=clause)
+def _terrain_findings(terrain: str, width: int, height: int) -> Iterator[tuple[int, str]]:
+    cells = width * height
+    if len(terrain) != cells:
+        yield 2, f"a {width}x{height} board needs {cells} terrain digits, the map gives {len(terrain)}"
+        return
+    for index, char in enumerate(terrain):
+        if not ("0" <= char <= "9"):
+            yield 2, f"terrain character {index} is {char!r}, which is not a digit"
+            return
+    for index, char in enumerate(terrain):
+        if char not in "01":
+            yield 3, f"terrain digit {index} is {char}; a cell is open (0) or wall (1)"
+            return
 
 
-def _attribute(element: ElementTree.Element, name: str, clause: int) -> str:
-    text = element.get(name)
-    if text is None:
-        raise _refuse(clause, f"<{element.tag}> carries no {name!r} attribute")
-    return text
-
-
-def _integer(element: ElementTree.Element, name: str, clause: int) -> int:
-    text = _attribute(element, name, clause)
-    if _INTEGER.fullmatch(text) is None:
-        raise _refuse(clause, f"<{element.tag}> attribute {name}={text!r} is not an integer")
-    return int(text)
-
-
-def _child(root: ElementTree.Element, name: str, clause: int) -> ElementTree.Element:
-    child = root.find(name)
-    if child is None:
-        raise _refuse(clause, f"the document has no <{name}> element")
-    return child
-
-
-def _int32(value: int, subject: str, clause: int) -> None:
-    if value not in _INT32:
-        raise _refuse(clause, f"{subject} is {value}, outside the 32-bit signed range")
-
-
-def check_dimensions(width: int, height: int) -> None:
-    """Clause 1 (src/nanorts/content/acceptance.py:18-25)."""
-    for name, value in (("width", width), ("height", height)):
-        _int32(value, name, 1)
-        if value <= 0:
-            raise _refuse(1, f"{name} is {value}, expected a positive integer")
-
-
-def check_terrain_payload(terrain: str, width: int, height: int) -> None:
-    """Clause 2 (acceptance.py:28-42): one digit per cell."""
-    if len(terrain) != width * height:
-        raise _refuse(2, f"the <terrain> payload is {len(terrain)} characters against a {width}x{height} field of "
-                         f"{width * height} cells")
-    bad = next((i for i, ch in enumerate(terrain) if ch not in "0123456789"), None)
-    if bad is not None:
-        raise _refuse(2, f"the <terrain> payload holds {terrain[bad]!r} at index {bad}, and the payload is digits only")
-
-
-def check_terrain_digits(terrain: str) -> None:
-    """Clause 3 (acceptance.py:45-52): terrain is binary."""
-    bad = next((i for i, ch in enumerate(terrain) if ch not in "01"), None)
-    if bad is not None:
-        raise _refuse(3, f"the <terrain> payload holds the digit {terrain[bad]} at index {bad}, and terrain is binary")
-
-
-def check_players(players: tuple[tuple[int, int], ...]) -> None:
-    """Clause 4 (acceptance.py:55-69): two positional player records."""
+def _player_findings(players: Sequence[tuple[int, int]]) -> Iterator[tuple[int, str]]:
     if len(players) != PLAYER_COUNT:
-        raise _refuse(4, f"the document declares {len(players)} player records, expected exactly {PLAYER_COUNT}")
-    for expected, (declared, resources) in enumerate(players):
-        if declared != expected:
-            raise _refuse(4, f"player record {expected} declares ID {declared}, and the records are positional")
-        _int32(resources, f"player record {expected}'s resources", 4)
+        yield 4, f"the map lists {len(players)} players; a game has {PLAYER_COUNT}"
+        return
+    for position, (declared, resources) in enumerate(players):
+        if declared != position:
+            yield 4, f"the player listed at position {position} carries ID {declared}; IDs must count up from 0"
+        elif resources not in _SIGNED_32:
+            yield 4, f"player {position} starts with {resources} resources, beyond a signed 32-bit integer"
 
 
-def check_document(document: ContentDocument, table: tuple[UnitType, ...]) -> None:
-    """Every acceptance clause (acceptance.py:72-168) on a parsed or built
-    document: extents, terrain, players, then per unit in document order its
-    32-bit fields, a known type, a unique ID, a cell on the board that no
-    earlier unit holds and a declared owner (clause 5), then hit points in
-    [0, 2^15 - 1] (clause 6)."""
-    check_dimensions(document.width, document.height)
-    check_terrain_payload(document.terrain, document.width, document.height)
-    check_terrain_digits(document.terrain)
-    check_players(document.players)
-    names = {unit.name for unit in table}
-    declared = {player for player, _ in document.players}
+def _unit_findings(document: MapDocument, table: Sequence[UnitType]) -> Iterator[tuple[int, str]]:
+    known = {unit.name for unit in table}
+    owners = {declared for declared, _ in document.players}
     ids: set[int] = set()
-    held: dict[tuple[int, int], int] = {}
-    for position, unit in enumerate(document.units):
-        for field in ("id", "player", "x", "y", "hitpoints", "resources"):
-            _int32(getattr(unit, field), f"unit {position}'s {'ID' if field == 'id' else field}", 5)
-        if unit.type not in names:
-            raise _refuse(5, f"unit ID {unit.id} names the type {unit.type!r}, which the supported unit type table "
-                             "does not hold")
-        if unit.id in ids:
-            raise _refuse(5, f"unit ID {unit.id} is declared more than once")
+    holder: dict[tuple[int, int], int] = {}
+    for index, unit in enumerate(document.units):
+        numbers = (("ID", unit.id), ("player", unit.player), ("x", unit.x), ("y", unit.y),
+                   ("hitpoints", unit.hitpoints), ("resources", unit.resources))
+        wide = next((label for label, value in numbers if value not in _SIGNED_32), None)
+        if wide is not None:
+            yield 5, f"record {index} has a {wide} beyond a signed 32-bit integer"
+        elif unit.type not in known:
+            yield 5, f"unit {unit.id} is a {unit.type!r}, a type this unit table lacks"
+        elif unit.id in ids:
+            yield 5, f"two records share unit ID {unit.id}"
+        elif not (0 <= unit.x < document.width and 0 <= unit.y < document.height):
+            yield 5, f"unit {unit.id} at ({unit.x}, {unit.y}) lies off the {document.width}x{document.height} board"
+        elif (unit.x, unit.y) in holder:
+            yield 5, f"unit {unit.id} and unit {holder[unit.x, unit.y]} both stand on ({unit.x}, {unit.y})"
+        elif unit.player != OWNER_NEUTRAL and unit.player not in owners:
+            yield 5, f"unit {unit.id} belongs to player {unit.player}, whom the map does not list"
+        if wide is not None:
+            continue
         ids.add(unit.id)
-        if not (0 <= unit.x < document.width and 0 <= unit.y < document.height):
-            raise _refuse(5, f"unit ID {unit.id} sits at ({unit.x}, {unit.y}), outside the "
-                             f"{document.width}x{document.height} field")
-        if (unit.x, unit.y) in held:
-            raise _refuse(5, f"unit ID {unit.id} sits at ({unit.x}, {unit.y}), which unit ID "
-                             f"{held[unit.x, unit.y]} already occupies")
-        held[unit.x, unit.y] = unit.id
-        if unit.player != OWNER_NEUTRAL and unit.player not in declared:
-            raise _refuse(5, f"unit ID {unit.id} names player {unit.player}, which no player record declares")
+        holder.setdefault((unit.x, unit.y), unit.id)
+
+
+def _hit_point_findings(document: MapDocument) -> Iterator[tuple[int, str]]:
     for unit in document.units:
-        if unit.hitpoints not in _HIT_POINTS:
-            raise _refuse(6, f"unit ID {unit.id} declares {unit.hitpoints} hit points, outside "
-                             f"[0, {_HIT_POINTS.stop - 1}]")
+        if unit.hitpoints not in _HIT_POINT_RANGE:
+            yield 6, (f"unit {unit.id} has {unit.hitpoints} hit points; the int16 leaf holds "
+                      f"{_HIT_POINT_RANGE.start} to {_HIT_POINT_RANGE.stop - 1}")
 
 
-def parse_document(text: str) -> ContentDocument:
-    """The MicroRTS map XML (src/nanorts/content/loading.py:34-113); the
-    structural clauses are checked while reading, the rest by check_document."""
+def findings(document: MapDocument, table: Sequence[UnitType]) -> Iterator[tuple[int, str]]:
+    """Every broken acceptance clause of `document`, lowest clause first (and
+    clause 5 in record order)."""
+    yield from _extent_findings(document.width, document.height)
+    yield from _terrain_findings(document.terrain, document.width, document.height)
+    yield from _player_findings(document.players)
+    yield from _unit_findings(document, table)
+    yield from _hit_point_findings(document)
+
+
+def check_document(document: MapDocument, table: Sequence[UnitType]) -> None:
+    """Refuse `document` on the first broken clause (acceptance.py:158-164)."""
+    for clause, finding in findings(document, table):
+        raise _refusal(clause, finding)
+
+
+# ---------------------------------------------------------------------------
+# Map XML (src/nanorts/content/loading.py:34-113)
+# ---------------------------------------------------------------------------
+class _XmlReader:
+    """Reads the values of one element, refusing under `clause`."""
+
+    def __init__(self, element: ElementTree.Element, clause: int) -> None:
+        self.element, self.clause = element, clause
+
+    def text(self, name: str) -> str:
+        value = self.element.get(name)
+        if value is None:
+            raise _refusal(self.clause, f"a <{self.element.tag}> element lacks the {name!r} attribute")
+        return value
+
+    def number(self, name: str) -> int:
+        value = self.text(name)
+        if not _WHOLE_NUMBER.fullmatch(value):
+            raise _refusal(self.clause, f"<{self.element.tag}> gives {name}={value!r}, which is not a whole number")
+        return int(value)
+
+    def child(self, tag: str) -> ElementTree.Element:
+        found = self.element.find(tag)
+        if found is None:
+            raise _refusal(self.clause, f"the map has no <{tag}> section")
+        return found
+
+
+def read_map_xml(text: str) -> MapDocument:
+    """The document of a MicroRTS map XML.  The extents, terrain and player
+    records are checked as they are read (clauses 1-4); the unit records by
+    check_document."""
     try:
         root = ElementTree.fromstring(text)
     except ElementTree.ParseError as error:
-        raise _refuse(1, f"the document is not well formed XML: {error}") from error
-    width, height = _integer(root, "width", 1), _integer(root, "height", 1)
-    check_dimensions(width, height)
-    terrain = _child(root, "terrain", 2).text or ""
-    check_terrain_payload(terrain, width, height)
-    check_terrain_digits(terrain)
-    players = tuple((_integer(p, "ID", 4), _integer(p, "resources", 4)) for p in _child(root, "players", 4))
-    check_players(players)
-    units = tuple(
-        UnitRecord(type=_attribute(u, "type", 5), id=_integer(u, "ID", 5), player=_integer(u, "player", 5),
-                   x=_integer(u, "x", 5), y=_integer(u, "y", 5), hitpoints=_integer(u, "hitpoints", 5),
-                   resources=_integer(u, "resources", 5))
-        for u in _child(root, "units", 5))
-    return ContentDocument(width=width, height=height, terrain=terrain, players=players, units=units)
+        raise _refusal(1, f"the XML does not parse ({error})") from error
+    board = _XmlReader(root, 1)
+    width, height = board.number("width"), board.number("height")
+    for clause, finding in _extent_findings(width, height):
+        raise _refusal(clause, finding)
+    terrain = _XmlReader(root, 2).child("terrain").text or ""
+    for clause, finding in _terrain_findings(terrain, width, height):
+        raise _refusal(clause, finding)
+    players = tuple((reader.number("ID"), reader.number("resources"))
+                    for reader in (_XmlReader(p, 4) for p in _XmlReader(root, 4).child("players")))
+    for clause, finding in _player_findings(players):
+        raise _refusal(clause, finding)
+    units = []
+    for element in _XmlReader(root, 5).child("units"):
+        r = _XmlReader(element, 5)
+        units.append(UnitRecord(type=r.text("type"), id=r.number("ID"), player=r.number("player"), x=r.number("x"),
+                                y=r.number("y"), hitpoints=r.number("hitpoints"), resources=r.number("resources")))
+    return MapDocument(width=width, height=height, terrain=terrain, players=players, units=tuple(units))
 
 
-def _population(document: ContentDocument, owner: int) -> int:
-    return sum(1 for unit in document.units if unit.player == owner)
+# ---------------------------------------------------------------------------
+# Buckets (src/nanorts/content/normalize.py:45-116)
+# ---------------------------------------------------------------------------
+def _headcount(document: MapDocument, owner: int) -> int:
+    return sum(unit.player == owner for unit in document.units)
 
 
-def _resource_bound(document: ContentDocument, table: tuple[UnitType, ...]) -> int | None:
-    """src/nanorts/content/normalize.py:45-73: the most units a player can ever
-    own, from the resources on the map and the cheapest producible cost."""
-    produced = [unit for unit in table if unit.produced_by]
-    harvesters = [unit for unit in table if unit.can_harvest]
-    applies = (bool(produced) and bool(harvesters)
-               and all(unit.cost > 0 and not unit.is_resource for unit in produced)
-               and all(not unit.is_resource and unit.harvest_amount >= 0 for unit in harvesters))
-    if not applies:
+def population_ceiling(document: MapDocument, table: Sequence[UnitType]) -> int | None:
+    """The most units one player can ever own, or None when the table gives
+    no such bound (normalize.py:45-73).  The map's wealth is every unit's
+    resources, a resource pile counting its stock (at least 1) rounded up to
+    whole harvests of the largest harvest amount; a player can own its
+    starting units plus whatever its balance and all that wealth can buy at
+    the cheapest trainable cost."""
+    trainable = [unit for unit in table if unit.produced_by]
+    gatherers = [unit for unit in table if unit.can_harvest]
+    if not trainable or not gatherers:
         return None
-    types = {unit.name: unit for unit in table}
-    largest_harvest = max(unit.harvest_amount for unit in harvesters)
-    on_map = sum(max(unit.resources, 1) + largest_harvest - 1 if types[unit.type].is_resource
-                 else max(unit.resources, 0) for unit in document.units)
-    cheapest = min(unit.cost for unit in produced)
-    return max(_population(document, player) + max(0, balance + on_map) // cheapest
+    if any(unit.cost <= 0 or unit.is_resource for unit in trainable):
+        return None
+    if any(unit.is_resource or unit.harvest_amount < 0 for unit in gatherers):
+        return None
+    is_pile = {unit.name: unit.is_resource for unit in table}
+    grab = max(unit.harvest_amount for unit in gatherers)
+    wealth = 0
+    for unit in document.units:
+        wealth += max(unit.resources, 1) + grab - 1 if is_pile[unit.type] else max(unit.resources, 0)
+    price = min(unit.cost for unit in trainable)
+    return max(_headcount(document, player) + max(0, balance + wealth) // price
                for player, balance in document.players)
 
 
-def derive_bucket(document: ContentDocument, table: tuple[UnitType, ...], utt: UnitTypeTableVersion,
+def derive_bucket(document: MapDocument, table: Sequence[UnitType], utt: UnitTypeTableVersion,
                   conflict_strategy: ConflictStrategy) -> BucketSpec:
-    """src/nanorts/content/normalize.py:77-93"""
+    """The bucket the content implies (normalize.py:77-93): a neutral block
+    of the map's neutral units, player blocks of the population ceiling
+    clamped to [1, cells] (the cells when there is no ceiling), every type of
+    the table, and the square attack window of the longest range."""
     cells = document.width * document.height
-    bound = _resource_bound(document, table)
-    window = 2 * max(unit.attack_range for unit in table) + 1
-    return BucketSpec(
-        height=document.height, width=document.width,
-        neutral_capacity=_population(document, OWNER_NEUTRAL),
-        per_player_capacity=cells if bound is None else max(1, min(cells, bound)),
-        unit_type_capacity=len(table), attack_offset_capacity=window * window,
-        utt_identity=utt, conflict_strategy=conflict_strategy)
+    ceiling = population_ceiling(document, table)
+    side = 2 * max(unit.attack_range for unit in table) + 1
+    return BucketSpec(height=document.height, width=document.width,
+                      neutral_capacity=_headcount(document, OWNER_NEUTRAL),
+                      per_player_capacity=cells if ceiling is None else min(cells, max(1, ceiling)),
+                      unit_type_capacity=len(table), attack_offset_capacity=side * side, utt_identity=utt,
+                      conflict_strategy=conflict_strategy)
 
 
-def initial_state(document: ContentDocument, table: tuple[UnitType, ...], bucket: BucketSpec) -> dict[str, np.ndarray]:
-    """src/nanorts/content/normalize.py:119-154 + :157-170 (slot claims)."""
+_CHOSEN_BY_CALLER: Final = ("neutral_capacity", "per_player_capacity")
+
+
+def check_supplied_bucket(derived: BucketSpec, supplied: BucketSpec, document: MapDocument) -> None:
+    """A caller's bucket may resize the two slot blocks, each to any size from
+    the units the map puts in it up to the cell count, and must match the
+    derived bucket everywhere else (normalize.py:96-116)."""
+    problems = []
+    for field in dataclasses.fields(BucketSpec):
+        if field.name in _CHOSEN_BY_CALLER:
+            continue
+        mine, theirs = getattr(derived, field.name), getattr(supplied, field.name)
+        if mine != theirs:
+            problems.append(f"{field.name} {theirs!r} should be {mine!r}")
+    least = {"neutral_capacity": _headcount(document, OWNER_NEUTRAL),
+             "per_player_capacity": max(_headcount(document, p) for p in range(PLAYER_COUNT))}
+    for name, low in least.items():
+        size = getattr(supplied, name)
+        if size < low or size > derived.cell_count:
+            problems.append(f"{name} {size!r} should lie in [{low}, {derived.cell_count}] (the map's units in that "
+                            "block up to the cell count)")
+    if problems:
+        raise ContentError("the supplied bucket does not fit this content: " + ", ".join(problems))
+
+
+# ---------------------------------------------------------------------------
+# Initial state (src/nanorts/content/normalize.py:119-170)
+# ---------------------------------------------------------------------------
+class _SlotCursor:
+    """The next free slot of each block: neutral, player 0, player 1."""
+
+    def __init__(self, bucket: BucketSpec) -> None:
+        self.bounds = {OWNER_NEUTRAL: (0, bucket.neutral_capacity)}
+        for player in range(PLAYER_COUNT):
+            self.bounds[player] = (bucket.player_slot_start(player), bucket.per_player_capacity)
+        self.used = dict.fromkeys(self.bounds, 0)
+
+    def take(self, unit: UnitRecord) -> int:
+        start, size = self.bounds[unit.player]
+        if self.used[unit.player] == size:
+            owner = "the neutral" if unit.player == OWNER_NEUTRAL else f"player {unit.player}'s"
+            raise ContentError(f"unit {unit.id} finds {owner} block of {size} slots already full")
+        self.used[unit.player] += 1
+        return start + self.used[unit.player] - 1
+
+
+def initial_state(document: MapDocument, table: Sequence[UnitType], bucket: BucketSpec) -> dict[str, np.ndarray]:
+    """The State of one env at the start of an episode: each unit, born in
+    document order, in its block's next slot; the players' balances; the
+    outcome decided (outcome.decide, src/nanorts/core/outcome.py:11-25)."""
     state = {leaf.name: np.full(leaf_shape(leaf, bucket), leaf.fill, leaf.dtype) for leaf in STATE_LEAVES}
-    names = {unit.name: index for index, unit in enumerate(table)}
-    next_free = [0] * (PLAYER_COUNT + 1)
+    code = {unit.name: index for index, unit in enumerate(table)}
+    cursor = _SlotCursor(bucket)
     for birth, unit in enumerate(document.units):
-        if unit.type not in names:
-            raise ContentError(f"unit ID {unit.id} names the unknown type {unit.type!r}")
-        if unit.player == OWNER_NEUTRAL:
-            start, capacity, block = 0, bucket.neutral_capacity, "neutral"
-        else:
-            start, capacity, block = bucket.player_slot_start(unit.player), bucket.per_player_capacity, f"player {unit.player}"
-        offset = next_free[unit.player + 1]
-        if offset >= capacity:
-            raise ContentError(f"the {block} block holds {capacity} slots, which unit ID {unit.id} exceeds")
-        next_free[unit.player + 1] = offset + 1
-        slot = start + offset
-        state["birth"][slot] = birth
-        state["unit_type"][slot] = names[unit.type]
-        state["owner"][slot] = unit.player
-        state["cell"][slot] = unit.x + unit.y * bucket.width
-        state["hit_points"][slot] = unit.hitpoints
-        state["carried_resources"][slot] = unit.resources
+        if unit.type not in code:
+            raise ContentError(f"unit {unit.id} is a {unit.type!r}, a type this unit table lacks")
+        slot = cursor.take(unit)
+        for name, value in (("birth", birth), ("unit_type", code[unit.type]), ("owner", unit.player),
+                            ("cell", unit.y * bucket.width + unit.x), ("hit_points", unit.hitpoints),
+                            ("carried_resources", unit.resources)):
+            state[name][slot] = value
         state["entity_at"][unit.y, unit.x] = slot
-    state["player_resources"][:] = [resources for _, resources in document.players]
+    state["player_resources"][:] = [balance for _, balance in document.players]
     state["next_birth"][()] = len(document.units)
-    _decide(state, bucket)
+    owned = state["birth"][bucket.neutral_capacity:].reshape(PLAYER_COUNT, bucket.per_player_capacity) != ABSENT
+    standing = np.flatnonzero(owned.any(axis=1))
+    state["game_over"][()] = standing.size <= 1
+    state["winner"][()] = int(standing[0]) if standing.size == 1 else ABSENT
     return state
 
 
-def _decide(state: dict[str, np.ndarray], bucket: BucketSpec) -> None:
-    """outcome.decide (src/nanorts/core/outcome.py:11-25) on one env."""
-    owned = state["birth"][bucket.neutral_capacity:].reshape(PLAYER_COUNT, bucket.per_player_capacity)
-    surviving = (owned != ABSENT).any(axis=1)
-    count = int(surviving.sum())
-    state["game_over"][()] = count <= 1
-    state["winner"][()] = int(np.argmax(surviving)) if count == 1 else ABSENT
-
-
-_CALLER_CHOSEN = ("neutral_capacity", "per_player_capacity")
-
-
-def check_supplied_bucket(derived: BucketSpec, supplied: BucketSpec, document: ContentDocument) -> None:
-    """src/nanorts/content/normalize.py:96-116: a supplied BucketSpec agrees
-    with the derived one except for the two slot capacities, each of which
-    lies between the population the content puts in its block and the cell
-    count."""
-    wrong = [f"{field.name} is {getattr(supplied, field.name)!r}, expected {getattr(derived, field.name)!r}"
-             for field in dataclasses.fields(derived)
-             if field.name not in _CALLER_CHOSEN and getattr(supplied, field.name) != getattr(derived, field.name)]
-    floors = {"neutral_capacity": _population(document, OWNER_NEUTRAL),
-              "per_player_capacity": max(_population(document, p) for p in range(PLAYER_COUNT))}
-    for name, floor in floors.items():
-        chosen = getattr(supplied, name)
-        if not floor <= chosen <= derived.cell_count:
-            wrong.append(f"{name} is {chosen!r}, expected the inclusive interval [{floor}, {derived.cell_count}] "
-                         "between the population the content puts in that block and its cell count")
-    if wrong:
-        raise ContentError("the supplied BucketSpec disagrees with the content: " + "; ".join(wrong))
-
-
-def _table(utt, conflict_strategy) -> tuple[UnitTypeTableVersion, ConflictStrategy, tuple[UnitType, ...]]:
+# ---------------------------------------------------------------------------
+# Games
+# ---------------------------------------------------------------------------
+def _release(utt, conflict_strategy) -> tuple[UnitTypeTableVersion, ConflictStrategy, tuple[UnitType, ...]]:
+    """The unit table and strategy of the supported releases
+    (src/nanorts/content/loading.py:160-173)."""
     try:
         utt = UnitTypeTableVersion(utt)
     except ValueError:
-        raise ContentError(f"unit type table {utt!r} is outside the supported release matrix, which is "
-                           f"{[member.value for member in UnitTypeTableVersion]}") from None
+        raise ContentError(f"no unit type table is called {utt!r}; the supported ones are "
+                           f"{', '.join(v.value for v in UnitTypeTableVersion)}") from None
     try:
         conflict_strategy = ConflictStrategy(conflict_strategy)
     except ValueError:
-        raise ContentError(f"conflict strategy {conflict_strategy!r} is outside the supported release matrix, which "
-                           f"is {[member.value for member in ConflictStrategy]}") from None
+        raise ContentError(f"no conflict strategy is called {conflict_strategy!r}; the supported ones are "
+                           f"{', '.join(v.value for v in ConflictStrategy)}") from None
     return utt, conflict_strategy, TABLES[utt]
 
 
-def _assemble(document: ContentDocument, utt, conflict_strategy, max_cycles: int, bucket: BucketSpec | None,
-              name: str) -> GameConfig:
-    """src/nanorts/content/loading.py:176-188: accept, derive (or check the
-    supplied) bucket, place the units."""
-    utt, conflict_strategy, table = _table(utt, conflict_strategy)
+def _game(document: MapDocument, utt, conflict_strategy, max_cycles: int, bucket: BucketSpec | None,
+          name: str) -> GameConfig:
+    utt, conflict_strategy, table = _release(utt, conflict_strategy)
     check_document(document, table)
-    if max_cycles <= 0:
-        raise ContentError(f"max_cycles is {max_cycles}, expected a positive horizon")
-    derived = derive_bucket(document, table, utt, conflict_strategy)
+    if max_cycles < 1:
+        raise ContentError(f"the horizon max_cycles must be at least 1, not {max_cycles}")
+    shape = derive_bucket(document, table, utt, conflict_strategy)
     if bucket is not None:
-        check_supplied_bucket(derived, bucket, document)
-        derived = bucket
-    require_int16_indices(derived)
-    terrain = np.asarray([c == "1" for c in document.terrain], np.bool_).reshape(derived.height, derived.width)
-    return GameConfig(terrain=terrain, max_cycles=int(max_cycles), initial_state=initial_state(document, table, derived),
-                      unit_types=table, bucket=derived, name=name)
+        check_supplied_bucket(shape, bucket, document)
+        shape = bucket
+    require_int16_indices(shape)
+    walls = np.frombuffer(document.terrain.encode("ascii"), np.uint8) == ord("1")
+    return GameConfig(terrain=walls.reshape(shape.height, shape.width), max_cycles=int(max_cycles),
+                      initial_state=initial_state(document, table, shape), unit_types=table, bucket=shape, name=name)
 
 
 def load_game(path: str | os.PathLike[str], *, utt: UnitTypeTableVersion = UnitTypeTableVersion.ORIGINAL_FINETUNED,
               conflict_strategy: ConflictStrategy = ConflictStrategy.CANCEL_BOTH, max_cycles: int = 5000,
               bucket: BucketSpec | None = None) -> GameConfig:
-    """src/nanorts/content/loading.py:116-121"""
-    text = Path(path).read_text(encoding="utf-8")
-    return _assemble(parse_document(text), utt, conflict_strategy, max_cycles, bucket, Path(path).stem)
+    """A game from a map file (src/nanorts/content/loading.py:116-121)."""
+    source = Path(path)
+    return _game(read_map_xml(source.read_text(encoding="utf-8")), utt, conflict_strategy, max_cycles, bucket,
+                 source.stem)
 
 
-def build_game(*, width: int, height: int, terrain: str, players, units,
+def build_game(*, width: int, height: int, terrain: str, players: Sequence[int], units: Sequence[UnitRecord],
                utt: UnitTypeTableVersion = UnitTypeTableVersion.ORIGINAL_FINETUNED,
                conflict_strategy: ConflictStrategy = ConflictStrategy.CANCEL_BOTH, max_cycles: int = 5000,
                bucket: BucketSpec | None = None, name: str = "") -> GameConfig:
-    """src/nanorts/content/loading.py:124-133: the same game from fields
-    instead of a document; `players` lists each player's starting
-    resources."""
-    document = ContentDocument(width=width, height=height, terrain=terrain, players=tuple(enumerate(players)),
-                               units=tuple(units))
-    return _assemble(document, utt, conflict_strategy, max_cycles, bucket, name)
+    """A game from values instead of a file (src/nanorts/content/loading.py:124-133);
+    `players` lists each player's starting resources."""
+    document = MapDocument(width=width, height=height, terrain=terrain,
+                           players=tuple((index, balance) for index, balance in enumerate(players)), units=tuple(units))
+    return _game(document, utt, conflict_strategy, max_cycles, bucket, name)
 
 
+def with_unit_type_table(game: GameConfig, utt: UnitTypeTableVersion) -> GameConfig:
+    """The same content under another unit table, which must list the same
+    type names and give the same attack window
+    (src/nanorts/content/loading.py:136-157)."""
+    utt, _, table = _release(utt, game.bucket.conflict_strategy)
+    if utt == game.bucket.utt_identity:
+        return game
+    mine, theirs = [unit.name for unit in game.unit_types], [unit.name for unit in table]
+    if mine != theirs:
+        raise ContentError(f"table {utt} lists the types {theirs}; this game is built on {mine}")
+    side = 2 * max(unit.attack_range for unit in table) + 1
+    if side * side != game.bucket.attack_offset_capacity:
+        raise ContentError(f"table {utt} needs an attack window of {side * side} cells; this game's bucket has "
+                           f"{game.bucket.attack_offset_capacity}")
+    return dataclasses.replace(game, unit_types=table, bucket=dataclasses.replace(game.bucket, utt_identity=utt))
+
+
+# ---------------------------------------------------------------------------
+# Shipped maps (src/nanorts/content/scenarios.py)
+# ---------------------------------------------------------------------------
 def scenario_names() -> tuple[str, ...]:
-    return tuple(sorted(path.stem for path in MAP_DIRECTORY.glob("*.xml")))
+    """The names of the shipped maps (their file stems, one per map)."""
+    return SCENARIO_NAMES
 
 
 def shipped_map(name: str) -> Path:
-    path = MAP_DIRECTORY / f"{name}.xml"
-    if not path.is_file():
-        raise ModelError(f"scenario {name!r} is none of the shipped maps {list(scenario_names())}")
-    return path
+    """The file of a shipped map."""
+    try:
+        return _SHIPPED[name]
+    except KeyError:
+        raise ModelError(f"{name!r} is not a shipped map; scenario_names() lists the {len(SCENARIO_NAMES)} there "
+                         "are, and content.load_game(path) loads any other map file") from None
 
 
 def map_name_to_scenario(name: str, *, utt: UnitTypeTableVersion = UnitTypeTableVersion.ORIGINAL_FINETUNED,
                          conflict_strategy: ConflictStrategy = ConflictStrategy.CANCEL_BOTH, max_cycles: int = 5000,
                          capacity_profile: bool = True) -> GameConfig:
-    """src/nanorts/content/scenarios.py:25-42"""
-    path = shipped_map(name)
-    game = load_game(path, utt=utt, conflict_strategy=conflict_strategy, max_cycles=max_cycles)
-    profile = CAPACITY_PROFILES.get(name)
-    if profile is None or not capacity_profile or profile >= game.bucket.per_player_capacity:
+    """A shipped map as a game, its player blocks cut to the map's capacity
+    profile when it has one that is smaller than the derived capacity
+    (src/nanorts/content/scenarios.py:25-42)."""
+    game = load_game(shipped_map(name), utt=utt, conflict_strategy=conflict_strategy, max_cycles=max_cycles)
+    profile = CAPACITY_PROFILES.get(name) if capacity_profile else None
+    if profile is None or profile >= game.bucket.per_player_capacity:
         return game
-    return load_game(path, utt=utt, conflict_strategy=conflict_strategy, max_cycles=max_cycles,
+    return load_game(shipped_map(name), utt=utt, conflict_strategy=conflict_strategy, max_cycles=max_cycles,
                      bucket=dataclasses.replace(game.bucket, per_player_capacity=profile))
-
-
-def with_unit_type_table(game: GameConfig, utt: UnitTypeTableVersion) -> GameConfig:
-    """src/nanorts/content/loading.py:136-157: the same content under another
-    table, which must name the same types and derive the same attack window."""
-    utt, _, table = _table(utt, game.bucket.conflict_strategy)
-    if utt == game.bucket.utt_identity:
-        return game
-    names = tuple(unit.name for unit in table)
-    if names != tuple(unit.name for unit in game.unit_types):
-        raise ContentError(f"unit type table {utt} declares the types {list(names)}, which are not the scenario's "
-                           f"{[unit.name for unit in game.unit_types]}")
-    window = (2 * max(unit.attack_range for unit in table) + 1) ** 2
-    if window != game.bucket.attack_offset_capacity:
-        raise ContentError(f"unit type table {utt} derives an attack window of {window} offsets, not the scenario's "
-                           f"{game.bucket.attack_offset_capacity}")
-    bucket = dataclasses.replace(game.bucket, utt_identity=utt)
-    return dataclasses.replace(game, unit_types=table, bucket=bucket)
-
-
-def initial_pending_empty(state: dict[str, np.ndarray]) -> bool:
-    return bool(np.all(state["pending_kind"] == KIND_ABSENT))

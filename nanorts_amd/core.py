@@ -91,7 +91,7 @@ def legal_commands(state: Any, game: GameConfig, *, stored: str = "rows") -> tor
         out = torch.empty((L, 2, b.per_player_capacity, width), dtype=torch.bool, device=dev.device)
         native.check(lib.nanorts_legality(_stream(), dev.ref, _native_state(core), L, _ptr(out)), "nanorts_legality")
     else:
-        raise ModelError(f"legal_commands refuses stored={stored!r}: 'rows' or 'words'")
+        raise ModelError(f"stored={stored!r} is unknown; the legality grid comes as 'rows' or 'words'")
     return out
 
 
@@ -99,7 +99,7 @@ def visibility(game: GameConfig, state: Any, *, observer: int) -> torch.Tensor:
     """observations.visibility (src/nanorts/observations/visibility.py:36-47):
     the cells `observer` sees, bool[L, H, W]."""
     if observer not in (0, 1):
-        raise ModelError(f"visibility refuses observer={observer!r}: 0 or 1")
+        raise ModelError(f"observer={observer!r} names no player; use 0 or 1")
     core = _core(state)
     dev = device_game(game, _device_of(core))
     L = _lanes(core)
@@ -125,7 +125,7 @@ def symbolic(game: GameConfig, state: Any, *, observer: int, partial_observabili
     """observations.symbolic (src/nanorts/observations/symbolic.py:99-127):
     uint8[L, H, W, 6] feature maps and int32[L, 4] scalars of `observer`."""
     if observer not in (0, 1):
-        raise ModelError(f"symbolic refuses observer={observer!r}: 0 or 1")
+        raise ModelError(f"observer={observer!r} names no player; use 0 or 1")
     maps, scalars = _both_symbolic(game, _core(state), partial_observability)
     return SymbolicObservation(maps[:, observer], scalars[:, observer])
 
@@ -135,7 +135,7 @@ def pixels(game: GameConfig, state: Any, assets, *, observer: int, partial_obser
     uint8[L, 16H, 16W, 3] images and int32[L, 4] scalars of `observer`,
     drawn with a prepared Asset set of 16-pixel cells."""
     if observer not in (0, 1):
-        raise ModelError(f"pixels refuses observer={observer!r}: 0 or 1")
+        raise ModelError(f"observer={observer!r} names no player; use 0 or 1")
     if assets.cell_pixels != 16:
         raise ModelError("the pixel kernel draws 16-pixel cells")
     core = _core(state)

@@ -54,6 +54,63 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return t.data_ptr()
 
 
+# The feature-map dtypes the reference publishes
+# (src/nanorts/observations/symbolic.py:48-52), narrowest last.
+FEATURE_MAP_DTYPES: Final = (torch.int32, torch.int16, torch.uint8)
+_BYTE_CEILING: Final = 255
+
+
+def feature_bounds(game: GameConfig) -> dict[str, int]:
+    """The largest value each feature-map group can take for this content
+    (src/nanorts/observations/symbolic.py:186-199): hit points and carried
+    resources from the unit table and the initial units, the rest from the
+    vocabulary and the bucket."""
+    cols, start = game.columns, game.initial_state
+    return {
+        "hit_points": max(int(cols["hit_points"].max()), int(start["hit_points"].max())),
+        "carried_resources": max(int(cols["harvest_amount"].max()), int(start["carried_resources"].max())),
+        "owner": PLAYER_COUNT,
+        "unit_type": game.bucket.unit_type_capacity,
+        "pending_action_kind": ACTION_KIND_COUNT - 1,
+        "terrain": 1,
+    }
+
+
+def _as_feature_dtype(value: Any) -> torch.dtype | None:
+    if isinstance(value, torch.dtype):
+        return value if value in FEATURE_MAP_DTYPES else None
+    try:
+        name = np.dtype(value).name
+    except TypeError:
+        return None
+    return {"int32": torch.int32, "int16": torch.int16, "uint8": torch.uint8}.get(name)
+
+
+def feature_dtype(game: GameConfig, requested: Any = None) -> torch.dtype:
+    """The published feature-map dtype: `requested`, or the narrowest of
+    FEATURE_MAP_DTYPES whose range holds every bound of the content
+    (src/nanorts/adapters/jaxmarl/layout.py:146-158).  The kernels encode one
+    byte per feature, so content with a bound above 255 is refused here;
+    wider published dtypes are exact widenings of those bytes."""
+    bounds = feature_bounds(game)
+    largest = max(bounds.values())
+    if requested is None:
+        chosen = next(t for t in reversed(FEATURE_MAP_DTYPES) if torch.iinfo(t).max >= largest)
+    else:
+        chosen = _as_feature_dtype(requested)
+        if chosen is None:
+            raise ModelError(f"feature_dtype {requested!r} is not one of the published feature-map dtypes "
+                             f"{[str(t).removeprefix('torch.') for t in FEATURE_MAP_DTYPES]}")
+        too_big = {name: bound for name, bound in bounds.items() if bound > torch.iinfo(chosen).max}
+        if too_big:
+            raise ModelError(f"feature_dtype {requested!r} cannot hold this content's feature values: {too_big}")
+    if largest > _BYTE_CEILING:
+        wide = {name: bound for name, bound in bounds.items() if bound > _BYTE_CEILING}
+        raise ModelError(f"this content has feature values above {_BYTE_CEILING} ({wide}); the observation "
+                         "kernels encode one byte per feature, so such content is refused rather than wrapped")
+    return chosen
+
+
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -199,11 +256,19 @@ def make(env_id: str, *, scenario: GameConfig, utt: UnitTypeTableVersion | None 
          reward_components: bool = False, device: str | torch.device | None = None, assets: Any = None) -> "NanoRTS":
     """src/nanorts/adapters/jaxmarl/facade.py:43-56"""
     if env_id not in ENVIRONMENT_IDS:
-        raise ModelError(f"make refuses environment id {env_id!r}: the accepted ids are {list(ENVIRONMENT_IDS)}")
+        raise ModelError(f"there is no environment called {env_id!r}; this package registers {list(ENVIRONMENT_IDS)}")
     game = scenario if utt is None else with_unit_type_table(scenario, utt)
     return NanoRTS(game, surface=surface, partial_observability=partial_observability,
                    final_observation=final_observation, feature_dtype=feature_dtype,
                    reward_components=reward_components, device=device, assets=assets)
+
+
+def feature_dtype_for_surface(game: GameConfig, surface: str, requested: Any) -> torch.dtype:
+    """feature_dtype on the symbolic surface; the pixel surface publishes
+    uint8 images whatever the content (its glyphs draw bytes too), so the
+    bounds are checked there as well."""
+    chosen = feature_dtype(game, None if surface == "pixels" else requested)
+    return torch.uint8 if surface == "pixels" else chosen
 
 
 class NanoRTS:
@@ -213,15 +278,17 @@ class NanoRTS:
                  final_observation: bool = True, feature_dtype: Any = None, reward_components: bool = False,
                  device: str | torch.device | None = None, assets: Any = None):
         if surface not in SURFACES:
-            raise ModelError(f"NanoRTS refuses surface={surface!r}: this release delivers {list(SURFACES)}")
-        if feature_dtype not in (None, torch.uint8, np.uint8, "uint8"):
-            raise ModelError("this build publishes uint8 feature maps (the reference's default for these contents)")
+            raise ModelError(f"surface={surface!r} is unknown; choose one of {list(SURFACES)}")
+        if surface == "pixels" and feature_dtype is not None and _as_feature_dtype(feature_dtype) != torch.int32:
+            raise ModelError(f"feature_dtype={feature_dtype!r} has no meaning on the pixel surface, which publishes "
+                             "an image and no feature maps")
         for name, flag in (("partial_observability", partial_observability), ("final_observation", final_observation),
                            ("reward_components", reward_components)):
             if not isinstance(flag, bool):
-                raise ModelError(f"NanoRTS refuses {name}={flag!r}: it must be a bool")
+                raise ModelError(f"{name} must be True or False, not {flag!r}")
         if bool(scenario.initial_state["game_over"]):
-            raise ModelError("NanoRTS refuses a configuration whose initial State is already decided")
+            raise ModelError("this content's starting position is already won or drawn, so there is no game to step")
+        published = feature_dtype_for_surface(scenario, surface, feature_dtype)
         self.lib = native.load()
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.game = scenario
@@ -240,13 +307,14 @@ class NanoRTS:
                                     reward_components=reward_components)
         self.final_observation = final_observation
         self.partial = int(partial_observability)
+        self.feature_dtype = published
         self._tiles: torch.Tensor | None = None
         # the drawing table (src/nanorts/adapters/jaxmarl/layout.py:168-205):
         # none under the symbolic surface; under the pixel surface the shipped
         # sprite sheet unless an Asset set of 16-pixel cells is given
         if surface == "symbolic" and assets is not None:
-            raise ModelError(f"NanoRTS refuses assets={type(assets).__name__} under surface=\"symbolic\": the symbolic "
-                             "surface renders nothing")
+            raise ModelError(f"assets ({type(assets).__name__}) only apply to surface='pixels'; the symbolic surface draws "
+                             "no images")
         if surface == "pixels":
             from nanorts_amd import rendering
 
@@ -254,11 +322,11 @@ class NanoRTS:
                 table = rendering.tile_table(b.unit_type_capacity)
             else:
                 if assets.cell_pixels != rendering.SPRITE_PIXELS:
-                    raise ModelError(f"NanoRTS refuses an Asset set drawing {assets.cell_pixels} pixels per cell "
-                                     f"against the surface's {rendering.SPRITE_PIXELS}")
+                    raise ModelError(f"the pixel surface draws {rendering.SPRITE_PIXELS}-pixel cells; these assets were "
+                                     f"prepared for {assets.cell_pixels}")
                 if assets.unit_type_capacity != b.unit_type_capacity:
-                    raise ModelError(f"NanoRTS refuses an Asset set drawing {assets.unit_type_capacity} unit types "
-                                     f"against the Bucket's {b.unit_type_capacity}")
+                    raise ModelError(f"these assets draw {assets.unit_type_capacity} unit types; the game has "
+                                     f"{b.unit_type_capacity}")
                 table = np.ascontiguousarray(assets.tiles, np.uint8)
             self._tiles = torch.as_tensor(table, device=self.device)
 
@@ -284,7 +352,7 @@ class NanoRTS:
         state's buffers are updated in place (XLA donation)."""
         del key
         if reset_state is not None:
-            raise ModelError("NanoRTS.step refuses a reset_state: the auto-reset is the lifecycle's own")
+            raise ModelError("step resets finished games to the content's start by itself; reset_state is not taken")
         return self._fused_step(state, actions, donate, reset=True)
 
     def step_env(self, key, state: EnvironmentState, actions: dict[str, torch.Tensor], *, donate: bool = False):
@@ -412,7 +480,7 @@ class NanoRTS:
             native.check(self.lib.nanorts_avail_actions(_stream(), self.dev.ref, state.native(), L, None, _ptr(rows)),
                          "nanorts_avail_actions")
         else:
-            raise ModelError(f"get_avail_actions refuses form={form!r}: 'rows' or 'words'")
+            raise ModelError(f"form={form!r} is unknown; get_avail_actions returns 'rows' or 'words'")
         return {agent: rows[:, p] for p, agent in enumerate(self.agents)}
 
     def get_slot_cells(self, state: EnvironmentState) -> dict[str, torch.Tensor]:
@@ -529,6 +597,8 @@ class NanoRTS:
 
     # -------------------------------------------------------------- helpers
     def _symbolic(self, maps: torch.Tensor, scalars: torch.Tensor) -> dict[str, SymbolicObservation]:
+        if self.feature_dtype != torch.uint8:
+            maps = maps.to(self.feature_dtype)
         return {agent: SymbolicObservation(maps[:, p], scalars[:, p]) for p, agent in enumerate(self.agents)}
 
     def pixels_from_maps(self, maps: torch.Tensor) -> torch.Tensor:
@@ -591,7 +661,7 @@ class NanoRTS:
         b = self.bucket
         if self.layout.surface == "pixels":
             return {"image": ((16 * b.height, 16 * b.width, 3), torch.uint8), "scalars": ((4,), torch.int32)}
-        return {"feature_maps": (self.layout.feature_maps_shape, torch.uint8), "scalars": ((4,), torch.int32)}
+        return {"feature_maps": (self.layout.feature_maps_shape, self.feature_dtype), "scalars": ((4,), torch.int32)}
 
     def action_space(self, agent: str) -> dict[str, Any]:
         return {"shape": self.layout.actions_shape, "high": tuple(w - 1 for w in self.layout.action_widths)}

@@ -90,9 +90,8 @@ def _dtype(keyword: str, dtype: Any) -> torch.dtype:
         except TypeError:
             found = None
     if found not in OUTPUT_DTYPES:
-        raise ModelError(f"gridnet.prepare refuses {keyword}={dtype!r}: the Planes and the action mask publish one of "
-                         "['int32', 'uint8', 'bool'], each holding the surface's 0/1 values, with int32 the pinned "
-                         "MicroRTS-Py default")
+        raise ModelError(f"{keyword}={dtype!r} is not a GridNet output type; planes and masks hold 0/1 values as int32 "
+                         "(MicroRTS-Py's choice, the default), uint8 or bool")
     return found
 
 
@@ -100,37 +99,34 @@ def prepare(game: GameConfig, *, partial_observability: bool = False, planes_for
             planes_dtype: Any = torch.int32, mask_form: str = "rows", mask_dtype: Any = torch.int32) -> GridNetLayout:
     """src/nanorts/adapters/gridnet/layout.py:111-141 with its refusals (:144-231)."""
     if partial_observability is not False:
-        raise ModelError(f"gridnet.prepare refuses partial_observability={partial_observability!r}: MicroRTS-Py's "
-                         "31-plane partial-observation form is outside the supported release matrix")
+        raise ModelError(f"partial_observability={partial_observability!r}: the GridNet surface here is the fully "
+                         "observed one; MicroRTS-Py's 31-plane hidden-information form is not offered")
     bucket = game.bucket
     if bucket.unit_type_capacity != PLANE_WIDTHS[3] - 1:
-        raise ModelError(f"gridnet.prepare refuses BucketSpec.unit_type_capacity {bucket.unit_type_capacity}: the "
-                         f"pinned surface's type Plane group is {PLANE_WIDTHS[3]} wide and its produce-type factor "
-                         f"{ACTION_FACTOR_SIZES[5]} wide")
+        raise ModelError(f"a bucket of {bucket.unit_type_capacity} unit types does not fit GridNet, whose unit-type "
+                         f"planes are {PLANE_WIDTHS[3]} wide and whose produce-type factor has {ACTION_FACTOR_SIZES[5]} "
+                         "values")
     if bucket.attack_offset_capacity != ACTION_FACTOR_SIZES[6]:
-        raise ModelError(f"gridnet.prepare refuses BucketSpec.attack_offset_capacity {bucket.attack_offset_capacity}: "
-                         f"the pinned attack window is {ACTION_FACTOR_SIZES[6]}")
+        raise ModelError(f"an attack window of {bucket.attack_offset_capacity} cells does not fit GridNet's attack "
+                         f"factor of {ACTION_FACTOR_SIZES[6]} values")
     if planes_form not in PLANE_FORMS:
-        raise ModelError(f"gridnet.prepare refuses planes_form={planes_form!r}: the Planes publish one of "
-                         f"{list(PLANE_FORMS)}")
+        raise ModelError(f"planes_form={planes_form!r} is unknown; choose one of {list(PLANE_FORMS)}")
     if mask_form not in MASK_FORMS:
-        raise ModelError(f"gridnet.prepare refuses mask_form={mask_form!r}: the action mask publishes one of "
-                         f"{list(MASK_FORMS)}")
+        raise ModelError(f"mask_form={mask_form!r} is unknown; choose one of {list(MASK_FORMS)}")
     planes = _dtype("planes_dtype", planes_dtype)
     mask = _dtype("mask_dtype", mask_dtype)
     if planes_form == "indices":
         if planes != torch.int32:
-            raise ModelError(f"gridnet.prepare refuses planes_dtype={planes_dtype!r} beside planes_form='indices': the "
-                             "indices form publishes int8 Plane indices")
+            raise ModelError(f"planes_dtype={planes_dtype!r} conflicts with planes_form='indices', which always holds "
+                             "int8 indices")
         planes = PLANE_INDEX_DTYPE
     if mask_form == "packed":
         if mask != torch.int32:
-            raise ModelError(f"gridnet.prepare refuses mask_dtype={mask_dtype!r} beside mask_form='packed': the packed "
-                             "form publishes uint32 words")
+            raise ModelError(f"mask_dtype={mask_dtype!r} conflicts with mask_form='packed', which always holds uint32 "
+                             "words")
         mask = MASK_WORD_DTYPE
     if bool(game.initial_state["game_over"]):
-        raise ModelError("gridnet.prepare refuses a configuration whose initial State is already decided: a public "
-                         "environment steps only a playable State")
+        raise ModelError("this content's starting position is already won or drawn, so there is no game to step")
     return GridNetLayout(bucket=bucket, plane_widths=PLANE_WIDTHS, plane_offsets=_offsets(PLANE_WIDTHS),
                          plane_count=sum(PLANE_WIDTHS), action_factor_sizes=ACTION_FACTOR_SIZES,
                          mask_width=MASK_WIDTH, mask_offsets=_offsets(ACTION_FACTOR_SIZES), planes_form=planes_form,
@@ -389,7 +385,7 @@ class GridNetSeat:
         from nanorts_amd import bots
 
         if bot.strategy not in (bots.WORKER_RUSH, bots.BARRACKS_RUSH):
-            raise ModelError(f"GridNetSeat refuses bot {bot.name!r}: the rush family is built")
+            raise ModelError(f"bot {bot.name!r} is not available here; the seat plays WorkerRush or LightRush")
         self.bot = bot
         self.grid = GridNet(game, layout, device=device)
         self.game = game
@@ -501,15 +497,15 @@ class GridNetMix:
                  device: str | torch.device | None = None):
         self.groups = tuple(groups)
         if not isinstance(self_play, int) or isinstance(self_play, bool) or self_play < 0:
-            raise ModelError(f"GridNetMix refuses self_play={self_play!r}: it is a count of self-play games")
+            raise ModelError(f"self_play={self_play!r} should be the number of self-play games (an int)")
         for index, group in enumerate(self.groups):
             if not isinstance(group.lanes, int) or isinstance(group.lanes, bool) or group.lanes < 1:
-                raise ModelError(f"GridNetMix refuses group {index}: lanes={group.lanes!r} is not a positive int")
+                raise ModelError(f"group {index} asks for lanes={group.lanes!r}; give a positive int")
             if not hasattr(group.bot, "strategy"):
-                raise ModelError(f"GridNetMix refuses group {index}: its bot is not a Bot")
+                raise ModelError(f"group {index} holds no scripted Bot")
         self.self_play = self_play
         if self.lanes == 0:
-            raise ModelError("GridNetMix refuses a mix of no lanes")
+            raise ModelError("the mix has no games in it")
         self.grid = GridNet(game, layout, device=device)
         self.seats = tuple(GridNetSeat(group.bot, game, self.grid.layout, device=device) for group in self.groups)
 

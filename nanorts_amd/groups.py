@@ -174,16 +174,15 @@ class GroupMix:
     def __init__(self, groups: Sequence[Group]) -> None:
         self.groups = tuple(groups)
         if not self.groups:
-            raise ModelError("GroupMix refuses an empty group list")
+            raise ModelError("a GroupMix needs at least one group")
         for index, group in enumerate(self.groups):
             if not isinstance(group.lanes, int) or isinstance(group.lanes, bool) or group.lanes < 1:
-                raise ModelError(f"GroupMix refuses group {index}: lanes={group.lanes!r} is not a positive int")
+                raise ModelError(f"group {index} asks for lanes={group.lanes!r}; give a positive int")
         signatures = [_row_signature(group.environment) for group in self.groups]
         for index, signature in enumerate(signatures[1:], start=1):
             if signature != signatures[0]:
-                raise ModelError(f"GroupMix refuses group {index}: its rows are not group 0's - the groups' "
-                                 "environments must publish equal observation and action spaces and equal infos, "
-                                 "so equal final_observation and reward_components flags")
+                raise ModelError(f"group {index} publishes rows unlike group 0's; every group needs the same observation and "
+                                 "action spaces and the same final_observation and reward_components settings")
 
     @property
     def lanes(self) -> int:

@@ -112,83 +112,96 @@ class RenderAssets:
     unit_type_capacity: int
 
 
-def _class_name(index: int, types: int) -> str:
+def _tile_label(index: int, types: int) -> str:
+    """A readable name of tile `index` of the table, e.g. "wall under player1 heavy"."""
     terrain, occupant = divmod(index, occupant_states(types))
     if occupant == 0:
-        return f"{TERRAIN_NAMES[terrain]} + empty"
+        return f"empty {TERRAIN_NAMES[terrain]}"
     owner, unit_type = divmod(occupant - 1, types)
-    return f"{TERRAIN_NAMES[terrain]} + {OWNER_NAMES[owner]} {TYPE_STEMS[unit_type]}"
+    return f"{TERRAIN_NAMES[terrain]} under {OWNER_NAMES[owner]} {TYPE_STEMS[unit_type]}"
+
+
+def _first_repeat(pictures: np.ndarray) -> tuple[int, int] | None:
+    """(earlier, later) indices of the first row of `pictures` [n, bytes]
+    that repeats an earlier row, by the later index, or None."""
+    _, first, owner = np.unique(pictures, axis=0, return_index=True, return_inverse=True)
+    owner = owner.reshape(-1)
+    repeats = np.flatnonzero(first[owner] != np.arange(len(pictures)))
+    if repeats.size == 0:
+        return None
+    later = int(repeats[0])
+    return int(first[owner[later]]), later
+
+
+def _sprite_sheet(tiles) -> dict[str, np.ndarray]:
+    """The sprites of an Asset set, checked: every name of sprite_names() and
+    no other, each a 16x16 RGBA uint8 image, the terrain sprites opaque."""
+    names = sprite_names()
+    sheet = ({name: read_png(ART_DIRECTORY / f"{name}.png") for name in names} if tiles is None
+             else {name: np.asarray(image) for name, image in dict(tiles).items()})
+    lacking, extra = sorted(set(names) - set(sheet)), sorted(set(sheet) - set(names))
+    if lacking or extra:
+        raise RenderError(f"an Asset set names exactly the sprites {list(names)}; this one lacks {lacking} and "
+                          f"adds {extra}")
+    for name in names:
+        image = sheet[name]
+        if image.dtype != np.uint8 or image.shape != (SPRITE_PIXELS, SPRITE_PIXELS, 4):
+            raise RenderError(f"sprite {name!r} must be uint8 RGBA of {SPRITE_PIXELS}x{SPRITE_PIXELS} pixels, not "
+                              f"{image.dtype} {image.shape}")
+    for name in TERRAIN_NAMES:
+        if (sheet[name][..., 3] < 128).any():
+            raise RenderError(f"sprite {name!r} has see-through pixels; a terrain sprite is the ground of its "
+                              "cell and must cover all of it")
+    return sheet
 
 
 def prepare_assets(bucket, cell_pixels: int = SPRITE_PIXELS, tiles=None) -> RenderAssets:
-    """src/nanorts/rendering/assets.py:52-195: the tile table from the
-    shipped sprite sheet (or `tiles`, a name -> 16x16 RGBA uint8 mapping
-    naming every sprite of sprite_names()), each sprite upscaled to
-    `cell_pixels` (a multiple of 16) with a ring of cell_pixels / 16 pixels.
-    Refuses a table whose tiles would be indistinguishable: two equal
-    composites, or two occupied tiles equal outside the glyph band."""
-    if cell_pixels <= 0 or cell_pixels % SPRITE_PIXELS:
-        raise RenderError(f"cell_pixels is {cell_pixels}, expected a positive integer multiple of the "
-                          f"{SPRITE_PIXELS}-pixel sprite side")
+    """The tile table of an Asset set (src/nanorts/rendering/assets.py:52-67):
+    the shipped sprite sheet, or `tiles`, a mapping from every name of
+    sprite_names() to a 16x16 RGBA uint8 image.  Each cell tile is
+    `cell_pixels` square (a multiple of 16; sprites are upscaled by pixel
+    repetition).  Tile rules (assets.py:133-155): an empty cell is its terrain
+    sprite's RGB; an occupied cell is that ground with a ring cell_pixels / 16
+    pixels wide in the occupant owner's aura colour, under the occupant's
+    sprite wherever its alpha is at least 128.  The table is refused when two
+    tiles are equal, or two occupied tiles are equal once the glyph band is
+    blanked (assets.py:158-188): the picture would not tell them apart."""
+    if cell_pixels < SPRITE_PIXELS or cell_pixels % SPRITE_PIXELS:
+        raise RenderError(f"cell_pixels must be a positive multiple of the {SPRITE_PIXELS}-pixel sprite side, "
+                          f"not {cell_pixels}")
     types = len(TYPE_STEMS)
     if bucket.unit_type_capacity != types:
-        raise RenderError(f"BucketSpec.unit_type_capacity is {bucket.unit_type_capacity}, and an Asset set draws the "
-                          f"{types} types the supported unit type table holds")
-    names = sprite_names()
-    supplied = ({name: read_png(ART_DIRECTORY / f"{name}.png") for name in names} if tiles is None
-                else dict(tiles))
-    if set(supplied) != set(names):
-        raise RenderError(f"the Asset set does not name the Tile classes a Bucket of {types} unit types has: it is "
-                          f"missing {sorted(set(names) - set(supplied))} and holds an unused "
-                          f"{sorted(set(supplied) - set(names))}")
-    sprites = {}
-    for name in names:
-        image = np.asarray(supplied[name])
-        if image.shape != (SPRITE_PIXELS, SPRITE_PIXELS, 4) or image.dtype != np.uint8:
-            raise RenderError(f"the sprite {name!r} is {image.shape} {image.dtype}, expected a "
-                              f"({SPRITE_PIXELS}, {SPRITE_PIXELS}, 4) uint8 RGBA image")
-        sprites[name] = image
-    for name in TERRAIN_NAMES:
-        if not (sprites[name][..., 3] >= 128).all():
-            raise RenderError(f"the terrain tile {name!r} is not fully opaque, and terrain is the ground every "
-                              "occupant is drawn over")
-    scale = cell_pixels // SPRITE_PIXELS
+        raise RenderError(f"the sprite sheet draws {types} unit types; this bucket has "
+                          f"{bucket.unit_type_capacity}")
+    sheet = _sprite_sheet(tiles)
+    k = cell_pixels // SPRITE_PIXELS
 
-    def up(image: np.ndarray) -> np.ndarray:
-        return np.repeat(np.repeat(image, scale, axis=0), scale, axis=1)
+    def enlarge(stack: np.ndarray) -> np.ndarray:  # [..., 16, 16, C] -> [..., P, P, C]
+        return stack.repeat(k, axis=-3).repeat(k, axis=-2)
 
-    ring = np.zeros((cell_pixels, cell_pixels), bool)
-    ring[:scale, :] = ring[-scale:, :] = ring[:, :scale] = ring[:, -scale:] = True
-    states = occupant_states(types)
-    table = np.zeros((2 * states, cell_pixels, cell_pixels, 3), np.uint8)
-    for terrain, tname in enumerate(TERRAIN_NAMES):
-        ground = up(sprites[tname])[..., :3]
-        table[terrain * states] = ground
-        for owner_bucket, oname in enumerate(OWNER_NAMES):
-            for t, stem in enumerate(TYPE_STEMS):
-                art = up(sprites[f"{oname}-{stem}"])
-                tile = ground.copy()
-                tile[ring] = AURA_COLOURS[owner_bucket]
-                drawn = art[..., 3] >= 128
-                tile[drawn] = art[..., :3][drawn]
-                table[terrain * states + 1 + owner_bucket * types + t] = tile
-    band_rows = slice(BAND_ROWS[0] * scale, (BAND_ROWS[-1] + 1) * scale)
-    band_cols = slice(BAND_COLUMN * scale, (BAND_COLUMN + BAND_WIDTH) * scale)
-    composites: dict[bytes, str] = {}
-    outside: dict[bytes, str] = {}
-    for index, tile in enumerate(table):
-        name = _class_name(index, types)
-        for seen, picture, verb in ((composites, tile.tobytes(), "composite"), (outside, None, "draw as")):
-            if picture is None:
-                if index % states == 0:
-                    continue
-                blanked = tile.copy()
-                blanked[band_rows, band_cols] = 0
-                picture = blanked.tobytes()
-            if picture in seen:
-                raise RenderError(f"the Tile classes {seen[picture]!r} and {name!r} {verb} the same picture, which "
-                                  "would make them indistinguishable in a Rendering")
-            seen[picture] = name
+    ground = enlarge(np.stack([sheet[name][..., :3] for name in TERRAIN_NAMES]))            # [2, P, P, 3]
+    art = enlarge(np.stack([[sheet[f"{o}-{t}"] for t in TYPE_STEMS] for o in OWNER_NAMES]))  # [3, T, P, P, 4]
+    edge = np.zeros((cell_pixels, cell_pixels), bool)
+    edge[:k], edge[-k:], edge[:, :k], edge[:, -k:] = True, True, True, True
+    aura = np.asarray(AURA_COLOURS, np.uint8)[:, None, None, None, :]                        # [3, 1, 1, 1, 3]
+    ringed = np.where(edge[None, None, None, :, :, None], aura[None], ground[:, None, None])  # [2, 3, 1, P, P, 3]
+    painted = np.where((art[..., 3:] >= 128)[None], art[None, ..., :3], ringed)             # [2, 3, T, P, P, 3]
+    table = np.concatenate([ground[:, None], painted.reshape(2, 3 * types, cell_pixels, cell_pixels, 3)], axis=1)
+    table = np.ascontiguousarray(table.reshape(2 * occupant_states(types), cell_pixels, cell_pixels, 3))
+
+    clash = _first_repeat(table.reshape(len(table), -1))
+    if clash is not None:
+        a, b = clash
+        raise RenderError(f"the tiles for {_tile_label(a, types)} and {_tile_label(b, types)} are identical, so an "
+                          "image could not tell those cells apart")
+    occupied = np.flatnonzero(np.arange(len(table)) % occupant_states(types) != 0)
+    blanked = table[occupied].copy()
+    blanked[:, BAND_ROWS[0] * k:(BAND_ROWS[-1] + 1) * k, BAND_COLUMN * k:(BAND_COLUMN + BAND_WIDTH) * k] = 0
+    clash = _first_repeat(blanked.reshape(len(blanked), -1))
+    if clash is not None:
+        a, b = (int(occupied[i]) for i in clash)
+        raise RenderError(f"the tiles for {_tile_label(a, types)} and {_tile_label(b, types)} differ only inside "
+                          "the glyph band, which the hit point / carry / action glyphs overwrite")
     return RenderAssets(tiles=table, cell_pixels=cell_pixels, unit_type_capacity=types)
 
 

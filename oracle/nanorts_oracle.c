@@ -1342,11 +1342,31 @@ void nro_reset_where_done(const nro_game* g, const nro_state* initial, nro_state
     }
 }
 
+/* encode_components (N/adapters/rewards.py:47-71): per player win_loss,
+ * resource_gather, produce_worker, produce_building, attack,
+ * produce_combat_unit from the admitted counts and the ending state's
+ * outcome.  Type codes are the vocabulary's (N/model/unit_types.py:9-15). */
+static void reward_components(const env_t* e, const events_t* ev, float out[2][6]) {
+    enum { BASE = 1, BARRACKS = 2, WORKER = 3, LIGHT = 4, HEAVY = 5, RANGED = 6 };
+    for (int32_t p = 0; p < 2; ++p) {
+        const int32_t opponent = (p + 1) % 2;
+        out[p][0] = *e->game_over ? (*e->winner == p ? 1.0f : -1.0f) : 0.0f;
+        out[p][1] = (float)(ev->harvest[p] + ev->ret[p]);
+        out[p][2] = (float)ev->produce[p][WORKER];
+        out[p][3] = (float)(ev->produce[p][BASE] + ev->produce[p][BARRACKS]);
+        out[p][4] = (float)(ev->attack[p][opponent + 1] - ev->attack[p][p + 1]);
+        out[p][5] = (float)(ev->produce[p][LIGHT] + ev->produce[p][HEAVY] + ev->produce[p][RANGED]);
+    }
+}
+
 /* N/adapters/jaxmarl/env.py:72-184 for one env: request (decode, episode
- * root) -> core.step -> respond (advance + observe the post-reset state). */
+ * root) -> core.step -> respond (advance + observe the post-reset state).
+ * The ending state's observation (final_observation, :161-170) and the
+ * reward components (:173-174) are taken before the reset. */
 static void env_step_one(const nro_game* g, const nro_state* initial, const env_t* e, const int32_t* actions,
                          int32_t partial, float reward[2], int* done, int* terminated, int* truncated,
-                         int32_t* winner, int* overflowed, uint8_t* maps, int32_t* scalars, work_t* w) {
+                         int32_t* winner, int* overflowed, uint8_t* maps, int32_t* scalars, uint8_t* final_maps,
+                         int32_t* final_scalars, float components[2][6], work_t* w) {
     decode_one(g, e, actions, w->cmds);
     uint32_t root[2];
     nro_fold_in(e->root, *e->episode, root);
@@ -1355,6 +1375,12 @@ static void env_step_one(const nro_game* g, const nro_state* initial, const env_
     *done = *terminated || *truncated;
     *winner = *e->winner;
     *overflowed = e->spawn_overflow[0] > 0 || e->spawn_overflow[1] > 0;
+    if (components) reward_components(e, &ev, components);
+    if (final_maps) {
+        const int64_t per = (int64_t)g->cells * 6;
+        for (int32_t p = 0; p < 2; ++p)
+            symbolic_one(g, e, p, partial, final_maps + p * per, final_scalars + p * 4, w->seen);
+    }
     if (*done) {
         reset_one(g, initial, e);
         *e->episode += 1u;
@@ -1377,8 +1403,18 @@ void nro_env_step(const nro_game* g, const nro_state* initial, nro_state* s, con
         int32_t winner;
         uint8_t* maps = out && out->feature_maps ? out->feature_maps + (size_t)l * 2 * g->cells * 6 : NULL;
         int32_t* scal = out && out->scalars ? out->scalars + l * 8 : NULL;
+        uint8_t* fmaps = out && out->final_feature_maps && out->final_scalars
+                             ? out->final_feature_maps + (size_t)l * 2 * g->cells * 6
+                             : NULL;
+        int32_t* fscal = fmaps ? out->final_scalars + l * 8 : NULL;
+        float components[2][6];
+        const int wants_components = out && out->reward_components;
         env_step_one(g, initial, &e, actions + (size_t)l * owned * 7, partial, reward, &done, &terminated,
-                     &truncated, &winner, &overflowed, maps, scal, &w);
+                     &truncated, &winner, &overflowed, maps, scal, fmaps, fscal,
+                     wants_components ? components : NULL, &w);
+        if (wants_components)
+            for (int32_t p = 0; p < 2; ++p)
+                for (int32_t c = 0; c < 6; ++c) out->reward_components[(l * 2 + p) * 6 + c] = components[p][c];
         if (out) {
             if (out->reward) {
                 out->reward[2 * l] = reward[0];
@@ -1431,7 +1467,7 @@ static void* rollout_worker(void* arg) {
             if (job->actions)
                 memcpy(job->actions + ((size_t)t * job->L + l) * 2 * C * 7, w.actions, sizeof(int32_t) * 2 * C * 7);
             env_step_one(g, job->initial, &e, w.actions, job->partial, reward, &done, &terminated, &truncated,
-                         &winner, &overflowed, w.maps, scalars, &w);
+                         &winner, &overflowed, w.maps, scalars, NULL, NULL, NULL, &w);
             if (job->rewards) {
                 job->rewards[((size_t)t * job->L + l) * 2] = reward[0];
                 job->rewards[((size_t)t * job->L + l) * 2 + 1] = reward[1];

@@ -151,6 +151,9 @@ typedef struct nro_env_out {
     uint8_t* spawn_overflowed; /* [L] */
     uint8_t* feature_maps;  /* [L][2][H][W][6] or NULL */
     int32_t* scalars;       /* [L][2][4] or NULL */
+    uint8_t* final_feature_maps; /* [L][2][H][W][6] of the ending (pre-reset) state, or NULL */
+    int32_t* final_scalars;      /* [L][2][4] of the ending state, or NULL */
+    float* reward_components;    /* [L][2][6] (src/nanorts/adapters/rewards.py:47-71), or NULL */
 } nro_env_out;
 
 void nro_env_step(const nro_game* g, const nro_state* initial, nro_state* s, const int32_t* actions,

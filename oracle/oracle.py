@@ -92,7 +92,7 @@ class StepOut(ctypes.Structure):
 class EnvOut(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in
                 ("reward", "done", "terminated", "truncated", "winner", "spawn_overflowed", "feature_maps",
-                 "scalars")]
+                 "scalars", "final_feature_maps", "final_scalars", "reward_components")]
 
 
 ABSTRACT_FIELDS = ("kind", "unit_birth", "order", "target", "target_birth", "base", "base_birth", "cell",
@@ -240,15 +240,22 @@ class Oracle:
         self.lib.nro_reset_where_done(ctypes.byref(self.g), ctypes.byref(self._initial_struct),
                                       ctypes.byref(self._s(state)), _ptr(done), ctypes.c_int64(L))
 
-    def env_step(self, state, actions: np.ndarray, partial: bool, observe: bool = True) -> dict[str, np.ndarray]:
+    def env_step(self, state, actions: np.ndarray, partial: bool, observe: bool = True,
+                 final: bool = False) -> dict[str, np.ndarray]:
+        """env.step with auto-reset; with final=True also the ending state's
+        observation (final_feature_maps / final_scalars) and the reward
+        components [L, 2, 6]."""
         L = state["time"].shape[0]
         b = self.game.bucket
         out = {"reward": np.zeros((L, 2), np.float32), "done": np.zeros(L, np.uint8),
                "terminated": np.zeros(L, np.uint8), "truncated": np.zeros(L, np.uint8),
                "winner": np.zeros(L, np.int32), "spawn_overflowed": np.zeros(L, np.uint8),
                "feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if observe else None,
-               "scalars": np.zeros((L, 2, 4), np.int32) if observe else None}
-        o = EnvOut(*[_ptr(out[f]) for f, _ in EnvOut._fields_])
+               "scalars": np.zeros((L, 2, 4), np.int32) if observe else None,
+               "final_feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if final else None,
+               "final_scalars": np.zeros((L, 2, 4), np.int32) if final else None,
+               "reward_components": np.zeros((L, 2, 6), np.float32) if final else None}
+        o = EnvOut(*[_ptr(out.get(f)) for f, _ in EnvOut._fields_])
         actions = np.ascontiguousarray(actions, np.int32)
         self.lib.nro_env_step(ctypes.byref(self.g), ctypes.byref(self._initial_struct), ctypes.byref(self._s(state)),
                               _ptr(actions), ctypes.c_int64(L), ctypes.c_int32(int(partial)), ctypes.byref(o))
@@ -301,7 +308,7 @@ class Oracle:
                "winner": np.zeros(L, np.int32), "spawn_overflowed": np.zeros(L, np.uint8),
                "feature_maps": np.zeros((L, 2, b.height, b.width, 6), np.uint8) if observe else None,
                "scalars": np.zeros((L, 2, 4), np.int32) if observe else None}
-        o = EnvOut(*[_ptr(out[f]) for f, _ in EnvOut._fields_])
+        o = EnvOut(*[_ptr(out.get(f)) for f, _ in EnvOut._fields_])
         a = Abstract(*[_ptr(carry[f]) for f in ABSTRACT_FIELDS])
         actions = np.ascontiguousarray(actions, np.int32)
         seats = None

@@ -17,7 +17,7 @@ import pytest
 
 from nanorts_amd import content
 from nanorts_amd.content import (ContentError, UnitRecord, build_game, load_game, map_name_to_scenario,
-                                 parse_document, scenario_names, shipped_map, with_unit_type_table)
+                                 read_map_xml, scenario_names, shipped_map, with_unit_type_table)
 from nanorts_amd.model import ConflictStrategy, UnitTypeTableVersion
 
 BASE = """<rts.PhysicalGameState width="{w}" height="{h}">
@@ -97,7 +97,7 @@ def test_each_clause_refuses_with_its_number(tmp_path, text, clause):
 
 def test_build_game_equals_the_loaded_map():
     loaded = load_game(shipped_map("basesWorkers8x8"))
-    doc = parse_document(shipped_map("basesWorkers8x8").read_text())
+    doc = read_map_xml(shipped_map("basesWorkers8x8").read_text())
     built = build_game(width=doc.width, height=doc.height, terrain=doc.terrain,
                        players=[resources for _, resources in doc.players], units=doc.units)
     assert built.bucket == loaded.bucket
@@ -153,6 +153,24 @@ def test_another_unit_type_table_keeps_the_content():
     assert with_unit_type_table(game, UnitTypeTableVersion.ORIGINAL_FINETUNED) is game
     with pytest.raises(ContentError):
         with_unit_type_table(game, "no-such-table")
+
+
+def test_every_shipped_map_loads():
+    """All 138 maps the reference ships (src/nanorts/maps) load under both
+    unit tables, with int16 indices, a decided initial state and every unit
+    on its own cell."""
+    names = scenario_names()
+    assert len(names) == 138 and len(set(names)) == 138
+    for name in names:
+        for utt in UnitTypeTableVersion:
+            game = map_name_to_scenario(name, utt=utt)
+            st, b = game.initial_state, game.bucket
+            live = st["birth"] != -1
+            assert (st["entity_at"] != -1).sum() == live.sum(), name
+            cells = st["cell"][live].astype(np.int64)
+            assert len(set(cells.tolist())) == live.sum(), name
+            assert (st["entity_at"].reshape(-1)[cells] == np.flatnonzero(live)).all(), name
+            assert b.entity_capacity == b.neutral_capacity + 2 * b.per_player_capacity
 
 
 def test_unknown_names_are_refused():

@@ -427,3 +427,111 @@ def test_leaf_fills_used_by_the_scaffolding():
     """The Board helpers write the reference's canonical empties."""
     fills = {leaf.name: leaf.fill for leaf in STATE_LEAVES}
     assert fills["birth"] == ABSENT and fills["pending_kind"] == ABSENT and fills["entity_at"] == ABSENT
+
+
+# ---------------------------------------------------------------------------
+# env.step: reward components and the ending state's observation
+# (src/nanorts/adapters/rewards.py:47-71; adapters/jaxmarl/env.py:109-174)
+# ---------------------------------------------------------------------------
+def _rows(C: int, orders: dict) -> np.ndarray:
+    """int32[1, 2, C, 7] action rows, all zeros except the listed
+    (player, position) rows."""
+    a = np.zeros((1, 2, C, 7), np.int32)
+    for (player, pos), row in orders.items():
+        a[0, player, pos] = row
+    return a
+
+
+def test_reward_components_count_admitted_production():
+    """basesWorkersBarracks8x8 (ORIGINAL), cycle 0.  Player 0: the base trains
+    a Worker, the worker asks for Barracks (legal at balance 5, then cancelled
+    by the budget conflict with the base's Worker: 1 + 5 > 5), the barracks
+    trains a Light.  Player 1: the base trains a Worker, the barracks a Heavy,
+    the worker asks for a Base it cannot afford (illegal, not counted).
+    Components [win_loss, gather, worker, building, attack, combat]."""
+    bd = Board("basesWorkersBarracks8x8")
+    out = bd.o.env_step(bd.st, _rows(bd.C, {
+        (0, 0): [PRODUCE, 0, 0, 0, UP, WORKER, 0],
+        (0, 1): [PRODUCE, 0, 0, 0, DOWN, BARRACKS, 0],
+        (0, 2): [PRODUCE, 0, 0, 0, DOWN, LIGHT, 0],
+        (1, 0): [PRODUCE, 0, 0, 0, UP, WORKER, 0],
+        (1, 1): [PRODUCE, 0, 0, 0, UP, BASE, 0],
+        (1, 2): [PRODUCE, 0, 0, 0, UP, HEAVY, 0],
+    }), False, final=True)
+    assert out["reward_components"][0].tolist() == [[0, 0, 1, 1, 0, 1], [0, 0, 1, 0, 0, 1]]
+    assert bd.pending(3)[0] == NONE and bd.pending(2)[0] == NONE and bd.pending(4)[0] == PRODUCE
+
+
+def test_reward_components_gather_and_attack():
+    """basesWorkers8x8: player 0's worker at cell 1 harvests pile 0 (gather
+    1); player 1's worker at cell 62 harvests pile 1 (gather 1) while player
+    1's base cannot attack (illegal, not counted).  Then a return of player
+    0's worker counts as gather too."""
+    bd = Board("basesWorkers8x8")
+    bd.place(3, 1)
+    bd.place(50, 62)
+    out = bd.o.env_step(bd.st, _rows(bd.C, {(0, 1): [HARVEST, 0, LEFT, 0, 0, 0, 0],
+                                            (1, 1): [HARVEST, 0, RIGHT, 0, 0, 0, 0],
+                                            (1, 0): [ATTACK, 0, 0, 0, 0, 0, attack_offset(0, -1)]}),
+                        False, final=True)
+    assert out["reward_components"][0].tolist() == [[0, 1, 0, 0, 0, 0], [0, 1, 0, 0, 0, 0]]
+    for _ in range(20):  # harvests complete at 20
+        bd.o.env_step(bd.st, _rows(bd.C, {}), False)
+    assert int(bd.st["carried_resources"][0, 3]) == 1
+    bd.o.env_step(bd.st, _rows(bd.C, {(0, 1): [MOVE, DOWN, 0, 0, 0, 0, 0]}), False)
+    for _ in range(10):
+        bd.o.env_step(bd.st, _rows(bd.C, {}), False)
+    assert int(bd.st["cell"][0, 3]) == 9
+    out = bd.o.env_step(bd.st, _rows(bd.C, {(0, 1): [RETURN, 0, 0, RIGHT, 0, 0, 0]}), False, final=True)
+    assert out["reward_components"][0].tolist() == [[0, 1, 0, 0, 0, 0], [0, 0, 0, 0, 0, 0]]
+
+
+def test_final_observation_is_the_ending_state_and_win_loss():
+    """basesWorkers8x8, player 1 keeps only its worker, which trades blows
+    with player 0's worker (both die at time 5, as in the dead-attacker
+    test).  Cycle 0 counts one attack on the opponent each; at time 5 the
+    game ends with player 0 the sole survivor: win_loss (1, -1), rewards
+    (1, -1), the published observation is the fresh initial state's and the
+    final observation is the ending state's, each equal to the closed-form
+    symbolic encoding of that state."""
+    from oracle.oracle import copy_state
+    from tests.test_oracle import _closed_symbolic
+
+    bd = Board("basesWorkers8x8")
+    em = bd.st["entity_at"].reshape(-1)
+    em[53] = ABSENT
+    for leaf in STATE_LEAVES:
+        if leaf.kind == "slot":
+            bd.st[leaf.name][0, 49] = leaf.fill
+    bd.place(50, 17)
+    rows = _rows(bd.C, {(0, 1): [ATTACK, 0, 0, 0, 0, 0, attack_offset(0, 1)],
+                        (1, 1): [ATTACK, 0, 0, 0, 0, 0, attack_offset(0, -1)]})
+    out = bd.o.env_step(bd.st, rows, False, final=True)
+    assert out["reward_components"][0].tolist() == [[0, 0, 0, 0, 1, 0], [0, 0, 0, 0, 1, 0]]
+    for _ in range(3):
+        out = bd.o.env_step(bd.st, _rows(bd.C, {}), False, final=True)
+        assert not out["done"][0] and out["reward_components"][0].tolist() == [[0] * 6, [0] * 6]
+        # not done: the final observation is the published one
+        np.testing.assert_array_equal(out["final_feature_maps"], out["feature_maps"])
+    ending = copy_state(bd.st)
+    bd.o.core_step(ending, bd.o.decode_actions(ending, _rows(bd.C, {})), _episode_roots(ending))
+    out = bd.o.env_step(bd.st, _rows(bd.C, {}), False, final=True)
+    assert out["done"][0] and out["terminated"][0] and out["winner"][0] == 0
+    assert out["reward"][0].tolist() == [1.0, -1.0]
+    assert out["reward_components"][0].tolist() == [[1, 0, 0, 0, 0, 0], [-1, 0, 0, 0, 0, 0]]
+    assert ending["birth"][0, 3] == ABSENT and ending["birth"][0, 50] == ABSENT and int(ending["birth"][0, 2]) == 2
+    want_final, want_final_scalars = _closed_symbolic(bd.game, ending, False)
+    np.testing.assert_array_equal(out["final_feature_maps"], want_final)
+    np.testing.assert_array_equal(out["final_scalars"], want_final_scalars)
+    fresh = batch_initial(bd.game, 1, bd.root)
+    want_maps, want_scalars = _closed_symbolic(bd.game, fresh, False)
+    np.testing.assert_array_equal(out["feature_maps"], want_maps)
+    np.testing.assert_array_equal(out["scalars"], want_scalars)
+    assert int(bd.st["episode_index"][0]) == 1
+
+
+def _episode_roots(state) -> np.ndarray:
+    """fold_in(environment_root, episode_index) per env (lifecycle.py:34-37)."""
+    from nanorts_amd import keys as hostkeys
+
+    return np.stack([hostkeys.fold_in(r, int(e)) for r, e in zip(state["environment_root"], state["episode_index"])])

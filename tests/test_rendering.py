@@ -110,21 +110,27 @@ def test_prepare_assets_upscales_and_checks_the_sheet():
     sheet = _sheet()
     missing = dict(sheet)
     del missing["player0-worker"]
-    with pytest.raises(rendering.RenderError, match="missing"):
+    with pytest.raises(rendering.RenderError, match="lacks"):
         rendering.prepare_assets(_bucket(), tiles=missing)
     see_through = dict(sheet)
     see_through["wall"] = sheet["wall"].copy()
     see_through["wall"][0, 0, 3] = 0
-    with pytest.raises(rendering.RenderError, match="opaque"):
+    with pytest.raises(rendering.RenderError, match="see-through"):
         rendering.prepare_assets(_bucket(), tiles=see_through)
     small = dict(sheet)
     small["floor"] = sheet["floor"][:8]
-    with pytest.raises(rendering.RenderError, match="expected a"):
+    with pytest.raises(rendering.RenderError, match="must be uint8"):
         rendering.prepare_assets(_bucket(), tiles=small)
     twins = dict(sheet)
     twins["player0-light"] = sheet["player0-heavy"]
-    with pytest.raises(rendering.RenderError, match="indistinguishable"):
+    with pytest.raises(rendering.RenderError, match="identical"):
         rendering.prepare_assets(_bucket(), tiles=twins)
+    band = dict(sheet)
+    band["player0-light"] = sheet["player0-heavy"].copy()
+    band["player0-light"][13, 5, :3] ^= 0x01  # inside the glyph band
+    band["player0-light"][13, 5, 3] = 255
+    with pytest.raises(rendering.RenderError, match="glyph band"):
+        rendering.prepare_assets(_bucket(), tiles=band)
     # a recoloured sheet is accepted and changes only what it draws
     tinted = {name: image.copy() for name, image in sheet.items()}
     tinted["floor"][..., 0] ^= 0x40
