@@ -25,7 +25,7 @@ launch decodes, steps, rewards, resets and observes.
 16384 games on basesWorkers16x16 (VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM,
 horizons 5000, 4000, 3000 and 2000: one bucket), each cycle stepping every
 group on uniformly random Commands (a pool of eight sets held in HBM) with
-one nanorts_step_groups launch; one launch per group is timed beside it.
+one nanorts_amd_step_groups launch; one launch per group is timed beside it.
 
 Prints one JSON line (rank 0, N=1).
 """
@@ -45,6 +45,12 @@ if str(ROOT) not in sys.path:
 
 HBM_PEAK_GBPS = 8000.0
 MAP = "basesWorkers16x16"
+# Untimed cycles every game plays before the warmup and the timed region, so
+# that the timed cycles run from mid-game positions (the reference's README
+# measures from mid-game positions too), whatever --warmup is.
+MIDGAME = 200
+SIMDS = 256 * 4  # MI355X: 256 CUs of 4 SIMDs
+XCDS = 8
 NUM_ENVS = 65536
 METRIC = "env-steps/sec (both players) at 16x16 × 65536 envs; % HBM roofline"
 SEAT_ENVS = 32768
@@ -143,6 +149,20 @@ def copy_bandwidth() -> float:
     return 2 * n * 4 * reps / (a.elapsed_time(b) / 1e3) / 1e9
 
 
+def host_cpu() -> dict:
+    """The host's CPU model and core counts, for the CPU baseline's record."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "usable_cpus": usable}
+
+
 def cpu_baseline(envs: int, steps: int) -> dict:
     """The oracle (plain-C restatement of the reference step, masks and
     encoders) timed on the host cores over a bounded sample."""
@@ -153,15 +173,15 @@ def cpu_baseline(envs: int, steps: int) -> dict:
     game = map_name_to_scenario(MAP, conflict_strategy="CANCEL_RANDOM", max_cycles=5000)
     oracle = Oracle(game)
     state = batch_initial(game, envs, envmod.env_roots(0, envs))
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = max(1, min(threads, 16))  # one GPU's share of the host cores
+    host = host_cpu()
+    threads = max(1, min(host["usable_cpus"], 16))  # one GPU's share of the host cores
     t0 = time.perf_counter()
     used = oracle.rollout(state, (11, 13), 0, steps, True, threads=threads, record=False)["threads"]
     dt = time.perf_counter() - t0
     return {"value": round(envs * steps / dt, 1), "unit": "env-steps/s", "cores": int(used), "kind": "port",
             "sample": f"{envs} games x {steps} cycles of the same workload (oracle rollout: masks, sampler, "
-                      f"env.step, auto-reset, partial-observability symbolic obs) on {used} host threads, "
-                      f"{dt:.1f} s"}
+                      f"env.step, auto-reset, partial-observability symbolic obs) on {used} host threads "
+                      f"(one GPU's share of the box's cores), {dt:.1f} s", **host}
 
 
 def child(args) -> None:
@@ -189,55 +209,110 @@ def child(args) -> None:
             state, mask = out.environment_state, out.observation.action_mask
         torch.cuda.synchronize()
         return
+    # the headline's timed launch shape: the mid-game advance, then launches
+    # of `chunk` cycles (the caller passes the timed chunk)
     game, env, state = make_env(args.envs)
-    run_rollout(env, state, 4 * args.chunk, args.chunk, args.depth, 0)
+    run_rollout(env, state, MIDGAME, args.chunk, args.depth, 0)
+    run_rollout(env, state, PMC_LAUNCHES * args.chunk, args.chunk, args.depth, MIDGAME)
     torch.cuda.synchronize()
 
 
-def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel: str = "k_rollout") -> dict | None:
-    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the measured kernel,
-    each scaled by what the counter reads for a plain copy of known size."""
+PMC_LAUNCHES = 3  # timed-shape launches the headline's profile child runs after the advance
+
+
+def progress(message: str) -> None:
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f"bench: {message}", file=sys.stderr, flush=True)
+
+
+def pmc_counters(args, mode: str, kernel: str, counters: str, chunk: int) -> list[dict[str, float]]:
+    """One rocprofv3 --pmc pass over a profile child; per dispatch of
+    `kernel` (in dispatch order) the counter values and the duration in ns."""
     import csv
     import shutil
     import tempfile
 
     rocprof = shutil.which("rocprofv3")
-    if rocprof is None or args.traffic == "off":
+    if rocprof is None:
+        return []
+    progress(f"rocprofv3 --pmc {counters} over the {mode} child")
+    out = Path(tempfile.mkdtemp(prefix="nr_pmc_", dir=os.environ.get("TMPDIR", "/tmp")))
+    cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", *counters.split(), "-d", str(out), "-o", "pmc",
+           "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--profile-child", mode,
+           "--workload", args.workload, "--envs", str(args.envs), "--chunk", str(chunk), "--depth", str(args.depth)]
+    subprocess.run(cmd, env=dict(os.environ), capture_output=True, text=True, timeout=180)
+    rows: dict[int, dict[str, float]] = {}
+    for path in out.rglob("*counter_collection.csv"):
+        with open(path) as fh:
+            for row in csv.DictReader(fh):
+                name = row.get("Kernel_Name", "")
+                want = kernel in name if mode != "copy" else ("copy" in name.lower() or "elementwise" in name.lower())
+                if not want:
+                    continue
+                rec = rows.setdefault(int(row.get("Dispatch_Id") or len(rows)), {})
+                rec[row["Counter_Name"]] = rec.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+                if row.get("Start_Timestamp") and row.get("End_Timestamp"):
+                    rec["duration_ns"] = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
+    shutil.rmtree(out, ignore_errors=True)
+    return [rows[k] for k in sorted(rows)]
+
+
+def _median(values: list[float]) -> float:
+    return sorted(values)[len(values) // 2]
+
+
+def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel: str = "k_rollout",
+                last: int = 0) -> dict | None:
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the measured kernel's
+    launches of `per_launch_steps` cycles (the last `last` dispatches when
+    set, else every one), each scaled by what the counter reads for a plain
+    copy of known size."""
+    if args.traffic == "off":
         return None
-    env = dict(os.environ)
-
-    def counters(mode: str, counter: str) -> list[float]:
-        out = Path(tempfile.mkdtemp(prefix="nr_pmc_", dir=os.environ.get("TMPDIR", "/tmp")))
-        cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", str(out), "-o", "pmc",
-               "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--profile-child", mode,
-               "--workload", args.workload, "--envs", str(args.envs), "--chunk", str(args.chunk), "--depth",
-               str(args.depth)]
-        subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=180)
-        values = []
-        for path in out.rglob("*counter_collection.csv"):
-            with open(path) as fh:
-                for row in csv.DictReader(fh):
-                    name = row.get("Kernel_Name", "")
-                    want = kernel in name if mode != "copy" else ("copy" in name.lower() or "elementwise" in name.lower())
-                    if want and row.get("Counter_Name") == counter:
-                        values.append(float(row["Counter_Value"]))
-        shutil.rmtree(out, ignore_errors=True)
-        return values
-
     try:
         copy_bytes = 2 * (1 << 26) * 4  # read + write of the 256 MiB copy
-        fetch_copy = counters("copy", "FETCH_SIZE")
-        write_copy = counters("copy", "WRITE_SIZE")
-        fetch = counters(mode, "FETCH_SIZE")
-        write = counters(mode, "WRITE_SIZE")
+        fetch_copy = [r["FETCH_SIZE"] for r in pmc_counters(args, "copy", "", "FETCH_SIZE", 1) if "FETCH_SIZE" in r]
+        write_copy = [r["WRITE_SIZE"] for r in pmc_counters(args, "copy", "", "WRITE_SIZE", 1) if "WRITE_SIZE" in r]
+        fetch = [r["FETCH_SIZE"] for r in pmc_counters(args, mode, kernel, "FETCH_SIZE", per_launch_steps)
+                 if "FETCH_SIZE" in r]
+        write = [r["WRITE_SIZE"] for r in pmc_counters(args, mode, kernel, "WRITE_SIZE", per_launch_steps)
+                 if "WRITE_SIZE" in r]
+        if last:
+            fetch, write = fetch[-last:], write[-last:]
         if not (fetch_copy and write_copy and fetch and write):
             return None
         # a copy of B bytes fetches B/2 and writes B/2
-        f_scale = (copy_bytes / 2) / (sorted(fetch_copy)[len(fetch_copy) // 2] * 1024)
-        w_scale = (copy_bytes / 2) / (sorted(write_copy)[len(write_copy) // 2] * 1024)
-        f = sorted(fetch)[len(fetch) // 2] * 1024 * f_scale
-        w = sorted(write)[len(write) // 2] * 1024 * w_scale
-        return {"fetch_bytes": f, "write_bytes": w, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+        f_scale = (copy_bytes / 2) / (_median(fetch_copy) * 1024)
+        w_scale = (copy_bytes / 2) / (_median(write_copy) * 1024)
+        return {"fetch_bytes": _median(fetch) * 1024 * f_scale, "write_bytes": _median(write) * 1024 * w_scale,
+                "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "dispatches": len(fetch),
+                "cycles_per_dispatch": per_launch_steps}
+    except Exception:
+        return None
+
+
+def pmc_limiter(args, per_launch_steps: int, last: int) -> dict | None:
+    """VALU busy and lane use of the measured launches (one counter pass):
+    busy = SQ_ACTIVE_INST_VALU x 4 / SIMDs / GPU cycles of one XCD, lanes =
+    SQ_THREAD_CYCLES_VALU / (SQ_ACTIVE_INST_VALU x 64)."""
+    if args.traffic == "off":
+        return None
+    try:
+        rows = [r for r in pmc_counters(args, "rollout", "k_rollout",
+                                        "SQ_ACTIVE_INST_VALU SQ_THREAD_CYCLES_VALU GRBM_GUI_ACTIVE", per_launch_steps)
+                if "SQ_ACTIVE_INST_VALU" in r and "GRBM_GUI_ACTIVE" in r][-last:]
+        if not rows:
+            return None
+        busy, lanes = [], []
+        for r in rows:
+            gui = r["GRBM_GUI_ACTIVE"]
+            # the counter sums its XCDs when it reads more cycles than a
+            # 4 GHz clock gives in the dispatch's duration
+            if r.get("duration_ns") and gui > 4.0 * r["duration_ns"]:
+                gui /= XCDS
+            busy.append(r["SQ_ACTIVE_INST_VALU"] * 4 / SIMDS / gui)
+            lanes.append(r["SQ_THREAD_CYCLES_VALU"] / (r["SQ_ACTIVE_INST_VALU"] * 64))
+        return {"valu_busy": round(_median(busy), 3), "valu_lane_use": round(_median(lanes), 3)}
     except Exception:
         return None
 
@@ -596,7 +671,7 @@ def main_groups(args) -> None:
         "data": "synthetic: uniformly random Commands (a pool of eight sets in HBM), shipped basesWorkers16x16 map",
         "config": {
             "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, {G} groups x {per} games, horizons "
-                        f"{list(GROUP_HORIZONS)}, one nanorts_step_groups launch per cycle",
+                        f"{list(GROUP_HORIZONS)}, one nanorts_amd_step_groups launch per cycle",
             "games": G * per, "groups": G, "algorithmic_bytes_per_env_step": per_step,
             "one_launch_per_group_env_steps_per_s": round(apart, 1),
         },
@@ -664,12 +739,14 @@ def main() -> None:
     game, env, state = make_env(args.envs)
     L = args.envs
     chunk = max(1, min(args.chunk, args.steps))
-    # warmup
-    run_rollout(env, state, args.warmup, chunk, args.depth, 0)
+    # untimed: the mid-game advance, then the warmup
+    run_rollout(env, state, MIDGAME, chunk, args.depth, 0)
+    run_rollout(env, state, args.warmup, chunk, args.depth, MIDGAME)
     torch.cuda.synchronize()
+    progress(f"{MIDGAME} mid-game + {args.warmup} warmup cycles done")
     # timed region: exactly `steps` cycles
     t0 = time.perf_counter()
-    times = run_rollout(env, state, args.steps, chunk, args.depth, args.warmup, events=True)
+    times = run_rollout(env, state, args.steps, chunk, args.depth, MIDGAME + args.warmup, events=True)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     launch_ms = [a.elapsed_time(b) for a, b, _ in times]
@@ -701,8 +778,13 @@ def main() -> None:
         torch.cuda.synchronize()
         pc_rate = L * args.per_call_steps / (time.perf_counter() - t1)
 
+    progress(f"timed {args.steps} cycles: {value / 1e6:.1f} M env-steps/s; per-call path "
+             f"{0 if pc_rate is None else pc_rate / 1e6:.1f} M")
     bw = copy_bandwidth()
-    traffic = pmc_traffic(args, chunk)
+    traffic = pmc_traffic(args, chunk, last=PMC_LAUNCHES)
+    limiter = pmc_limiter(args, chunk, PMC_LAUNCHES)
+    if not args.no_cpu:
+        progress("CPU baseline")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_envs, args.cpu_steps)
 
     line = {
@@ -720,7 +802,8 @@ def main() -> None:
         "data": "synthetic: seeded uniform-random legal actions from the shipped basesWorkers16x16 map",
         "config": {
             "workload": f"{MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_RANDOM, partial_observability, "
-                        f"{L} games, max_cycles 5000, auto-reset, fused rollout {chunk} cycles/launch",
+                        f"{L} games, max_cycles 5000, auto-reset, fused rollout {chunk} cycles/launch, timed "
+                        f"from cycle {MIDGAME + args.warmup} ({MIDGAME} untimed mid-game cycles + warmup)",
             "games": L, "slots_per_player": b.per_player_capacity, "entity_capacity": b.entity_capacity,
             "per_call_env_steps_per_s": None if pc_rate is None else round(pc_rate, 1),
             "copy_kernel_GBps": round(bw, 1),
@@ -738,11 +821,18 @@ def main() -> None:
             "kernel": "k_rollout",
             "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes,
+            "cycles_per_launch": chunk,
         },
         "cpu_baseline": cpu,
     }
     if traffic is not None:
         line["roofline"]["traffic_detail"] = traffic
+    if limiter is not None:
+        # "bound" names the roofline the fraction is taken against (the path
+        # runs no MFMA); the counters say what limits the kernel below it
+        line["roofline"]["limiter"] = {
+            **limiter, "hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "verdict": "VALU issue" if limiter["valu_busy"] > 2 * achieved / HBM_PEAK_GBPS else "HBM"}
     print(json.dumps(line))
 
 

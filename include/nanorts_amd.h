@@ -5,7 +5,7 @@
  * device pointers and sizes, runs asynchronously on the given HIP stream
  * (`stream` is a hipStream_t; NULL is the default stream), allocates no
  * device memory, and returns NANORTS_OK or an error code; the message of the
- * last failure on the calling thread is nanorts_last_error().
+ * last failure on the calling thread is nanorts_amd_last_error().
  *
  * Layouts are the reference's pytree leaves with a leading lane (env) dim L,
  * exactly as jax.vmap hands them to its XLA FFI handlers
@@ -141,6 +141,8 @@ typedef struct nanorts_rollout_results {
     uint8_t* feature_maps;  /* [depth][L][2][H][W][6]; step t writes slot t % depth */
     int32_t* scalars;       /* [depth][L][2][4] */
     int32_t depth;          /* ring depth of feature_maps / scalars, >= 1 */
+    int32_t* general_admissions; /* [L] cycles of the launch admitted request by request (an irregular
+                                  * state or more than 64 requests); written by nanorts_amd_rollout only */
 } nanorts_rollout_results;
 
 /* Carry of an abstraction-family bot (AbstractActions,
@@ -200,97 +202,122 @@ typedef struct nanorts_gridnet_results {
     int32_t* spawn_overflow;  /* [L][2] telemetry of the ending state */
 } nanorts_gridnet_results;
 
-const char* nanorts_build_id(void);
-const char* nanorts_targets(void);
-const char* nanorts_last_error(void);
+const char* nanorts_amd_build_id(void);
+const char* nanorts_amd_entries(void);
+const char* nanorts_amd_last_error(void);
 
 /* Least LDS bytes one workgroup may allocate over the listed devices (0 on
  * error).  Replaces nanorts_shared_opt_in
  * (src/nanorts/kernels/cuda/registry.cu:224-226), which the reference's
  * loader binds (src/nanorts/kernels/library.py:42-46). */
-int64_t nanorts_shared_opt_in(const int32_t* devices, int64_t n);
+int64_t nanorts_amd_shared_opt_in(const int32_t* devices, int64_t n);
 
 /* Runs a wave64 ballot / prefix-count / shuffle probe on each listed device;
  * returns "" when every device passes, else a static description.
  * Replaces src/nanorts/kernels/cuda/registry.cu:174-183 (nanorts_self_check). */
-const char* nanorts_self_check(const int32_t* devices, int64_t n);
+const char* nanorts_amd_self_check(const int32_t* devices, int64_t n);
 
 /* core.step: Java admission order, durative timers, conflict resolution,
  * completion in pending order, outcome.  State leaves are updated in place.
  * `key` is [key_lanes][2] episode-root key data (key_lanes 1 broadcasts).
  * Replaces the FFI target nanorts_step (src/nanorts/core/cuda/step.cu:653-698,
  * called from src/nanorts/core/cycle.py:123-134). */
-int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
+int nanorts_amd_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
                  int64_t key_lanes, nanorts_commands commands, nanorts_step_results results);
+
+/* core.step in the operand and result order of the reference's FFI target
+ * nanorts_step (src/nanorts/core/cuda/step.cu:56-108, operands built by
+ * src/nanorts/core/cycle.py:123-134, 198-211): the body an XLA FFI handler of
+ * that name calls with its buffers' device pointers.
+ *   operands[33]: 0 key u32[key_lanes][2]; 1-6 Commands kind, direction,
+ *     none_duration, target_cell, produced_type, request_order
+ *     s32[command_lanes][2][C]; 7 terrain pred[1][H][W]; 8 table
+ *     s32[1][T][7+T]; 9 timings s32[1][T][7]; 10-32 the 23 state leaves in
+ *     nanorts_state order (the last is telemetry.spawn_overflow s32[L][2]).
+ *   results[31]: 0-22 the state leaves after the step (aliasing operands
+ *     10-32 in place; an unaliased result is first filled from its operand);
+ *     23 admitted_harvest s32[L][2]; 24 admitted_return s32[L][2];
+ *     25 admitted_produce s32[L][2][T]; 26 admitted_attack s32[L][2][3];
+ *     27 is_member pred[L][E]; 28 int32 records s32[L][E][6]; 29 index
+ *     records s16[L][E][4]; 30 int8 records s8[L][E][6].  The records are
+ *     written as no member (all zero): nothing in the reference reads them.
+ * key_lanes and command_lanes are 1 (an unbatched operand of extent 1, every
+ * lane reads row 0; src/nanorts/kernels/batching.py:63-79) or `lanes`.  Index
+ * leaves are int16.  Errors as every entry: NANORTS_INVALID_ARGUMENT for a
+ * NULL pointer, an extent or a strategy out of range, NANORTS_INTERNAL for a
+ * failed launch or copy. */
+int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
+                         int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
+                         int32_t capacity, int32_t types, int32_t offsets, int64_t strategy);
 
 /* core.step over up to 16 groups of lanes, in one launch per 4 groups.  The
  * groups' games share one bucket (extents, capacities, unit types, attack
  * window, strategy) and one unit table, and may differ in terrain and
  * max_cycles; each group has its own State, keys ([lanes or 1][2]),
- * Commands and results, with nanorts_step's meaning.  `games` holds one
+ * Commands and results, with nanorts_amd_step's meaning.  `games` holds one
  * pointer per group.  Replaces the FFI target nanorts_step_groups
  * (src/nanorts/core/cuda/step.cu:704-808, called from
  * src/nanorts/core/cycle.py:137-175 through core.step_groups,
  * src/nanorts/core/__init__.py:71-89). */
-int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
+int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
                         const int64_t* lanes, const uint32_t* const* keys, const int64_t* key_lanes,
                         const nanorts_commands* commands, const nanorts_step_results* results);
 
 /* Factored legality rows bool[L][2][C][22+T+O] (active units, availability not
  * applied).  Replaces nanorts_legality (src/nanorts/core/cuda/legality.cu:535-545). */
-int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows);
+int nanorts_amd_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows);
 
 /* The same rows as contiguous 96-bit words uint32[L][2][C][3].  Replaces
  * nanorts_legality_words (src/nanorts/core/cuda/legality.cu:547-561). */
-int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            uint32_t* words);
 
 /* get_avail_actions masks: rows & available, only NONE on unavailable rows
  * (src/nanorts/adapters/jaxmarl/actions.py:28-41), as bool rows and/or words. */
-int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                           uint8_t* rows, uint32_t* words);
 
 /* Sight-radius visibility bool[L][H][W] of `observer`'s block.  Replaces
  * nanorts_visible_cells (src/nanorts/observations/cuda/visibility.cu:86-138). */
-int nanorts_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                           int32_t observer, uint8_t* cells);
 
 /* Symbolic uint8 observations of both agents
  * (src/nanorts/observations/symbolic.py:130-180). */
-int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+int nanorts_amd_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
                     uint8_t* feature_maps, int32_t* scalars);
 
 /* Pixel observations uint8[L][2][16H][16W][3] from a tile table
  * uint8[2(1+3T)][16][16][3] (src/nanorts/observations/pixels.py:71-88,
  * src/nanorts/rendering/raster.py:53-127). */
-int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+int nanorts_amd_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
                    const uint8_t* tiles, uint8_t* image, int32_t* scalars);
 
 /* Pixel observations uint8[images][16H][16W][3] from symbolic feature maps
  * uint8[images][H][W][6] (images = L * 2 agents) and the same tile table;
- * equal to nanorts_pixels of the state the maps were encoded from.  Replaces
+ * equal to nanorts_amd_pixels of the state the maps were encoded from.  Replaces
  * pixels_from_symbolic (src/nanorts/observations/pixels.py:91-110); tiles and
  * image must be 16-byte aligned. */
-int nanorts_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
+int nanorts_amd_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
                              const uint8_t* tiles, uint8_t* image);
 
 /* Auto-reset: envs whose done flag is set get the initial State and
  * episode_index + 1.  Replaces nanorts_reset_where_done
  * (src/nanorts/adapters/cuda/reset.cu:160-222). */
-int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                              const uint8_t* done);
 
 /* env.step of the JaxMARL facade in one launch: decode int32[L][2][C][7]
  * actions, core.step keyed by the episode root, advance (auto-reset) and
  * observe (src/nanorts/adapters/jaxmarl/env.py:72-184). */
-int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                      const int32_t* actions, int32_t partial, nanorts_env_results results);
 
-/* env.step_env of the JaxMARL facade: as nanorts_env_step without the
+/* env.step_env of the JaxMARL facade: as nanorts_amd_env_step without the
  * auto-reset, so the state, the observation and the rewards are those of the
  * ending state (src/nanorts/adapters/jaxmarl/facade.py:130-165, transition
  * in src/nanorts/adapters/jaxmarl/env.py:170-171). */
-int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, int32_t partial, nanorts_env_results results);
 
 /* The JaxMARL request (src/nanorts/adapters/jaxmarl/env.py:181-184):
@@ -298,20 +325,20 @@ int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state
  * (src/nanorts/adapters/jaxmarl/actions.py:61-84) and, when `episode_keys`
  * is not NULL, the episode roots fold_in(environment_root, episode_index)
  * as uint32[L][2]. */
-int nanorts_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, nanorts_command_buffers commands, uint32_t* episode_keys);
 
 /* The synthetic harness's integer uniform-over-legal sampler: actions
  * int32[L][2][C][7] from avail words uint32[L][2][C][3] for rollout step
  * `step`, envs numbered from env0. */
-int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
+int nanorts_amd_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
                            const uint32_t* sample_key /* host [2] */, int32_t step, int64_t env0,
                            int32_t* actions);
 
 /* Fused rollout of `steps` cycles with the state resident in LDS: per step
  * masks -> sample -> decode -> core.step -> auto-reset -> observe.  Bit-equal
  * to calling avail_actions, sample_actions and env_step once per step. */
-int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                     const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
                     int64_t env0,
                     nanorts_rollout_results results);
@@ -325,7 +352,7 @@ int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state,
  * nanorts_abstraction_act (src/nanorts/bots/cuda/abstraction_act.cu:1324),
  * called through src/nanorts/bots/whole_act.py:125-162 from
  * src/nanorts/bots/family.py:34-41. */
-int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             int32_t strategy, int32_t trained_type, const int32_t* player, int64_t player_lanes,
                             nanorts_abstract_actions carry, int32_t* commands);
 
@@ -333,21 +360,21 @@ int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_stat
  * 1 - learner from the current state, the learner's action rows
  * int32[L][C][7] are decoded, the merged commands go through core.step under
  * the episode root, auto-reset, and the carry is emptied where done.  Results
- * as nanorts_env_step, for both agents.  Replaces step_seat
+ * as nanorts_amd_env_step, for both agents.  Replaces step_seat
  * (src/nanorts/bots/seat.py:84-149), which composes the bot's act,
  * jaxmarl.request_against (src/nanorts/adapters/jaxmarl/env.py:78-96),
  * core.step and respond. */
-int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                       int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                       const int32_t* actions, int32_t partial, nanorts_env_results results);
 
-/* nanorts_seat_step with a per-lane seat: seats int32[L] holds each lane's
+/* nanorts_amd_seat_step with a per-lane seat: seats int32[L] holds each lane's
  * learner (0 or 1) on entry.  With draw != 0 (the "drawn" rule) a lane whose
  * game ended takes the seat drawn from its next episode's root,
  * randint(fold_in(episode_root, 2**32 - 2), (), 0, 2); otherwise the seats
  * stay (a per-lane Player array).  Replaces step_seat with seat="drawn" or
  * an Array seat (src/nanorts/bots/seat.py:84-149, 352-366). */
-int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
                             nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
                             nanorts_env_results results);
@@ -356,27 +383,27 @@ int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_stat
  * randint(fold_in(fold_in(environment_root, episode_index), 2**32 - 2), (),
  * 0, 2) into seats int32[L].  Replaces _episode_seat
  * (src/nanorts/bots/seat.py:352-360) as reset_seat calls it (line 77). */
-int nanorts_episode_seats(void* stream, const uint32_t* environment_root /* [L][2] */,
+int nanorts_amd_episode_seats(void* stream, const uint32_t* environment_root /* [L][2] */,
                           const uint32_t* episode_index /* [L] */, int64_t lanes, int32_t* seats);
 
 /* Fused learner-vs-bot rollout of `steps` cycles with the state resident in
  * LDS: per cycle the learner's rows from the synthetic harness's integer
  * uniform-over-legal sampler (its avail words, `sample_key`, step
- * step0 + t), the bot's act and the seat step as nanorts_seat_step.
- * Bit-equal to calling nanorts_avail_actions, nanorts_sample_actions and
- * nanorts_seat_step once per cycle with the learner's rows.  results.actions
+ * step0 + t), the bot's act and the seat step as nanorts_amd_seat_step.
+ * Bit-equal to calling nanorts_amd_avail_actions, nanorts_amd_sample_actions and
+ * nanorts_amd_seat_step once per cycle with the learner's rows.  results.actions
  * (when set) records the learner's rows [steps][L][C][7]; rewards, dones and
- * the observation ring are those of nanorts_rollout. */
-int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+ * the observation ring are those of nanorts_amd_rollout. */
+int nanorts_amd_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                          int32_t strategy, int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                          const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps, int32_t partial,
                          int64_t env0, nanorts_rollout_results results);
 
-/* nanorts_seat_rollout with per-lane seats as nanorts_seat_step_lanes: seats
+/* nanorts_amd_seat_rollout with per-lane seats as nanorts_amd_seat_step_lanes: seats
  * int32[L] is read at the start and holds the seats after the last cycle;
  * seat_record (when set) receives the learner of every cycle [steps][L],
  * which selects the learner's reward from results.rewards [steps][L][2]. */
-int nanorts_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                                int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
                                int32_t* seat_record, nanorts_abstract_actions carry,
                                const uint32_t* sample_key /* host [2] */, int32_t step0, int32_t steps,
@@ -387,34 +414,34 @@ int nanorts_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_s
  * (src/nanorts/adapters/gridnet/cuda/decode.cu, called from
  * src/nanorts/adapters/gridnet/actions.py:199-232); the legality words the
  * reference passes in are derived in the kernel. */
-int nanorts_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, nanorts_command_buffers commands);
 
 /* GridNet observe: planes, source mask and action mask of the state
  * (src/nanorts/adapters/gridnet/observation.py:27-72). */
-int nanorts_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             nanorts_gridnet_obs obs);
 
 /* GridNet step in one launch: decode, core.step keyed by the episode root,
  * reward components and reward dones, the ending state's planes, auto-reset
  * and the observation (src/nanorts/adapters/gridnet/env.py:65-118). */
-int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                          const int32_t* actions, nanorts_gridnet_results results);
 
 /* GridNet step_against: player 0 decoded from its per-cell actions
  * int32[L][H][W][7], player 1 plays `commands` ([L][2][C] per field; player
- * 0's rows are ignored), then as nanorts_gridnet_step
+ * 0's rows are ignored), then as nanorts_amd_gridnet_step
  * (src/nanorts/adapters/gridnet/env.py:73-83). */
-int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                                  const int32_t* actions, nanorts_commands commands, nanorts_gridnet_results results);
 
 /* The synthetic harness's integer uniform-over-legal sampler on the GridNet
  * surface: per-cell actions int32[L][2][H][W][7] from the packed action mask
  * uint32[L][2][H][W][3] (mask_form 1), each cell drawn as
- * nanorts_sample_actions draws a row, at position player * H * W + cell.
+ * nanorts_amd_sample_actions draws a row, at position player * H * W + cell.
  * No reference counterpart (the reference's harness samples with
  * jax.random.categorical). */
-int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
+int nanorts_amd_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
                                    const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions);
 
 #ifdef __cplusplus

@@ -3,9 +3,9 @@ learner-vs-bot seat.
 
 Mirrors src/nanorts/bots/{bot,family,worker_rush,light_rush}.py (the `Bot`
 records and family.act) and src/nanorts/bots/seat.py (SeatEnv and the seat
-functions): the bot's decisions run in the nanorts_abstraction_act kernel,
+functions): the bot's decisions run in the nanorts_amd_abstraction_act kernel,
 and a whole seat step (bot act, learner decode, core.step, auto-reset, carry
-reset, the next seat) is one nanorts_seat_step launch.  Every call is
+reset, the next seat) is one nanorts_amd_seat_step launch.  Every call is
 batched over L envs on the current HIP stream.
 
 Seats follow src/nanorts/bots/seat.py:335-375: "player_0" and "player_1"
@@ -79,9 +79,9 @@ def abstraction_act(env: NanoRTS, state: EnvironmentState, carry: dict[str, torc
     C = env.bucket.per_player_capacity
     players = torch.as_tensor(player, dtype=torch.int32, device=env.device).reshape(-1).contiguous()
     commands = torch.empty((L, 6, 2, C), dtype=torch.int32, device=env.device)
-    native.check(env.lib.nanorts_abstraction_act(_stream(), env.dev.ref, state.native(), L, bot.strategy,
+    native.check(env.lib.nanorts_amd_abstraction_act(_stream(), env.dev.ref, state.native(), L, bot.strategy,
                                                  bot.trained, _ptr(players), players.numel(), _carry_struct(carry),
-                                                 _ptr(commands)), "nanorts_abstraction_act")
+                                                 _ptr(commands)), "nanorts_amd_abstraction_act")
     names = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
     return {name: commands[:, f] for f, name in enumerate(names)}
 
@@ -113,8 +113,8 @@ def episode_seats(env: NanoRTS, state: EnvironmentState) -> torch.Tensor:
     """The "drawn" rule's learner of each lane's current episode, int32[L]
     (_episode_seat, src/nanorts/bots/seat.py:352-360)."""
     out = torch.empty(state.num_envs, dtype=torch.int32, device=env.device)
-    native.check(env.lib.nanorts_episode_seats(_stream(), _ptr(state.environment_root), _ptr(state.episode_index),
-                                               state.num_envs, _ptr(out)), "nanorts_episode_seats")
+    native.check(env.lib.nanorts_amd_episode_seats(_stream(), _ptr(state.environment_root), _ptr(state.episode_index),
+                                               state.num_envs, _ptr(out)), "nanorts_amd_episode_seats")
     return out
 
 
@@ -206,17 +206,17 @@ class SeatEnv:
             _ptr(comps), _ptr(out["spawn_overflow"]))
         if self.learner is not None:
             current = nxt.seat
-            native.check(env.lib.nanorts_seat_step(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+            native.check(env.lib.nanorts_amd_seat_step(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                    self.bot.trained, self.learner, _carry_struct(nxt.carry),
-                                                   _ptr(acts), env.partial, results), "nanorts_seat_step")
+                                                   _ptr(acts), env.partial, results), "nanorts_amd_seat_step")
         else:
             if nxt.seat.dtype != torch.int32 or tuple(nxt.seat.shape) != (L,) or not nxt.seat.is_contiguous():
                 raise ModelError(f"the seat state's seat must be a contiguous int32[{L}]")
             current = nxt.seat.clone()
-            native.check(env.lib.nanorts_seat_step_lanes(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+            native.check(env.lib.nanorts_amd_seat_step_lanes(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                          self.bot.trained, _ptr(nxt.seat), int(self.draw),
                                                          _carry_struct(nxt.carry), _ptr(acts), env.partial, results),
-                         "nanorts_seat_step_lanes")
+                         "nanorts_amd_seat_step_lanes")
         publish = env._symbolic if env.layout.surface == "symbolic" else env._pixels
         obs = self._learners(publish(maps, scalars), nxt.seat)
         infos: dict[str, Any] = {
@@ -256,17 +256,17 @@ class SeatEnv:
         results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth)
         seats = None
         if self.learner is not None:
-            native.check(env.lib.nanorts_seat_rollout(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+            native.check(env.lib.nanorts_amd_seat_rollout(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                       self.bot.trained, self.learner, _carry_struct(state.carry), key,
                                                       int(step0), int(steps), env.partial, int(env0), results),
-                         "nanorts_seat_rollout")
+                         "nanorts_amd_seat_rollout")
         else:
             seats = torch.empty((steps, L), dtype=torch.int32, device=d) if record else None
-            native.check(env.lib.nanorts_seat_rollout_lanes(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
+            native.check(env.lib.nanorts_amd_seat_rollout_lanes(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
                                                             self.bot.trained, _ptr(state.seat), int(self.draw),
                                                             _ptr(seats), _carry_struct(state.carry), key, int(step0),
                                                             int(steps), env.partial, int(env0), results),
-                         "nanorts_seat_rollout_lanes")
+                         "nanorts_amd_seat_rollout_lanes")
         return {"rewards": rewards, "dones": dones, "actions": actions, "feature_maps": maps, "scalars": scalars,
                 "seats": seats}
 

@@ -84,12 +84,12 @@ def legal_commands(state: Any, game: GameConfig, *, stored: str = "rows") -> tor
     lib = native.load()
     if stored == "words":
         out = torch.empty((L, 2, b.per_player_capacity, 3), dtype=torch.int32, device=dev.device)
-        native.check(lib.nanorts_legality_words(_stream(), dev.ref, _native_state(core), L, _ptr(out)),
-                     "nanorts_legality_words")
+        native.check(lib.nanorts_amd_legality_words(_stream(), dev.ref, _native_state(core), L, _ptr(out)),
+                     "nanorts_amd_legality_words")
     elif stored == "rows":
         width = 6 + 4 * 4 + b.unit_type_capacity + b.attack_offset_capacity
         out = torch.empty((L, 2, b.per_player_capacity, width), dtype=torch.bool, device=dev.device)
-        native.check(lib.nanorts_legality(_stream(), dev.ref, _native_state(core), L, _ptr(out)), "nanorts_legality")
+        native.check(lib.nanorts_amd_legality(_stream(), dev.ref, _native_state(core), L, _ptr(out)), "nanorts_amd_legality")
     else:
         raise ModelError(f"stored={stored!r} is unknown; the legality grid comes as 'rows' or 'words'")
     return out
@@ -105,8 +105,8 @@ def visibility(game: GameConfig, state: Any, *, observer: int) -> torch.Tensor:
     L = _lanes(core)
     b = game.bucket
     out = torch.empty((L, b.height, b.width), dtype=torch.bool, device=dev.device)
-    native.check(native.load().nanorts_visible_cells(_stream(), dev.ref, _native_state(core), L, int(observer),
-                                                     _ptr(out)), "nanorts_visible_cells")
+    native.check(native.load().nanorts_amd_visible_cells(_stream(), dev.ref, _native_state(core), L, int(observer),
+                                                     _ptr(out)), "nanorts_amd_visible_cells")
     return out
 
 
@@ -116,8 +116,8 @@ def _both_symbolic(game: GameConfig, core: State, partial: bool) -> tuple[torch.
     b = game.bucket
     maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=dev.device)
     scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=dev.device)
-    native.check(native.load().nanorts_observe(_stream(), dev.ref, _native_state(core), L, int(bool(partial)),
-                                               _ptr(maps), _ptr(scalars)), "nanorts_observe")
+    native.check(native.load().nanorts_amd_observe(_stream(), dev.ref, _native_state(core), L, int(bool(partial)),
+                                               _ptr(maps), _ptr(scalars)), "nanorts_amd_observe")
     return maps, scalars
 
 
@@ -145,9 +145,9 @@ def pixels(game: GameConfig, state: Any, assets, *, observer: int, partial_obser
     tiles = torch.as_tensor(assets.tiles, device=dev.device).contiguous()
     image = torch.empty((L, 2, 16 * b.height, 16 * b.width, 3), dtype=torch.uint8, device=dev.device)
     scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=dev.device)
-    native.check(native.load().nanorts_pixels(_stream(), dev.ref, _native_state(core), L,
+    native.check(native.load().nanorts_amd_pixels(_stream(), dev.ref, _native_state(core), L,
                                               int(bool(partial_observability)), _ptr(tiles), _ptr(image),
-                                              _ptr(scalars)), "nanorts_pixels")
+                                              _ptr(scalars)), "nanorts_amd_pixels")
     return PixelObservation(image[:, observer], scalars[:, observer])
 
 
@@ -162,6 +162,6 @@ def pixels_from_symbolic(feature_maps: torch.Tensor, assets, game: GameConfig) -
     images = maps.numel() // (b.height * b.width * 6)
     tiles = torch.as_tensor(assets.tiles, device=maps.device).contiguous()
     out = torch.empty((*maps.shape[:-3], 16 * b.height, 16 * b.width, 3), dtype=torch.uint8, device=maps.device)
-    native.check(native.load().nanorts_pixels_from_maps(_stream(), dev.ref, images, _ptr(maps), _ptr(tiles),
-                                                        _ptr(out)), "nanorts_pixels_from_maps")
+    native.check(native.load().nanorts_amd_pixels_from_maps(_stream(), dev.ref, images, _ptr(maps), _ptr(tiles),
+                                                        _ptr(out)), "nanorts_amd_pixels_from_maps")
     return out

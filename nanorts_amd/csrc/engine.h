@@ -125,6 +125,10 @@ struct KGame {
     int32_t wshift;    // log2(W) when W is a power of two, else -1
     int32_t tab[F_COUNT * 8];
     const uint8_t* terrain;
+    // When set, the unit table comes from device operands in the reference's
+    // layout instead of tab (see load_header); NULL otherwise.
+    const int32_t* ref_table;    // [T][7 + T]
+    const int32_t* ref_timings;  // [T][7]
     nanorts_state initial;
     Layout lay;
     int32_t nseg;
@@ -304,8 +308,44 @@ NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field 
 
 // Stage the unit table and terrain for the workgroup (all threads call; a
 // __syncthreads follows in the kernel).
+// One entry of the LDS unit table from the reference's `table` and `timings`
+// operands (src/nanorts/core/unit_tables.py:9-48): table[t] = can_move,
+// can_harvest, is_resource, is_stockpile, can_attack, attack_range, cost,
+// produces[T]; timings[t] = move_time, harvest_time, attack_time,
+// produce_time, hit_points, attack_damage, harvest_amount.  The step reads no
+// sight radius, so F_SIGHT is 0.
+NR_DEV int32_t ref_table_entry(const KGame& g, int field, int32_t t) {
+    if (t >= g.T) return 0;
+    const int32_t* row = g.ref_table + t * (7 + g.T);
+    const int32_t* time = g.ref_timings + t * 7;
+    switch (field) {
+        case F_COST: return row[6];
+        case F_HP: return time[4];
+        case F_PRODUCE_TIME: return time[3];
+        case F_MOVE_TIME: return time[0];
+        case F_ATTACK_TIME: return time[2];
+        case F_HARVEST_TIME: return time[1];
+        case F_RANGE: return row[5];
+        case F_DAMAGE: return time[5];
+        case F_AMOUNT: return time[6];
+        case F_FLAGS:
+            return (row[2] ? FL_RESOURCE : 0) | (row[3] ? FL_STOCKPILE : 0) | (row[1] ? FL_HARVEST : 0) |
+                   (row[0] ? FL_MOVE : 0) | (row[4] ? FL_ATTACK : 0);
+        case F_PRODUCES: {
+            int32_t bits = 0;
+            for (int32_t u = 0; u < g.T; ++u) bits |= row[7 + u] ? 1 << u : 0;
+            return bits;
+        }
+        default: return 0;
+    }
+}
+
 NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
-    for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
+    if (g.ref_table) {
+        for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = ref_table_entry(g, i >> 3, i & 7);
+    } else {
+        for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
+    }
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int k = 0; k < 16; ++k) {

@@ -484,12 +484,14 @@ NR_DEV void write_events(const KGame& g, const Env& e, int64_t l, const nanorts_
     if (r.admitted_attack && lane < 6) r.admitted_attack[6 * l + lane] = ev[20 + lane];
 }
 
+// core.step on Commands [cmd_lanes][2][C] (cmd_lanes 1 broadcasts one row
+// to every lane, the reference's extent-1 operand) and keys [key_lanes][2].
 __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_state s, const uint32_t* key, int64_t key_lanes,
-                       nanorts_commands c, nanorts_step_results r) {
+                       nanorts_commands c, int64_t cmd_lanes, nanorts_step_results r) {
     NR_KERNEL_PROLOGUE
     load_env(g, s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    stage_commands(g, e, l, c, lane);
+    stage_commands(g, e, cmd_lanes == 1 ? 0 : l, c, lane);
     const int64_t kl = key_lanes == 1 ? 0 : l;
     const uint32_t k0 = key[2 * kl], k1 = key[2 * kl + 1];
     const bool events = r.admitted_harvest || r.admitted_return || r.admitted_produce || r.admitted_attack;
@@ -506,6 +508,22 @@ __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_st
         }
     }
     if (events) write_events(g, e, l, r, lane);
+}
+
+// Zero bytes [0, n) of a device buffer with 16-byte stores where the pointer
+// allows (a fill kernel rather than a memset node, so a captured graph
+// replays it correctly).
+__global__ __launch_bounds__(256) void k_zero_bytes(uint8_t* p, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t to_aligned = (int64_t)((16u - ((uintptr_t)p & 15u)) & 15u);
+    const int64_t head = to_aligned < n ? to_aligned : n;
+    const int64_t vecs = (n - head) >> 4;
+    for (int64_t k = i; k < head; k += stride) p[k] = 0;
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    v4* body = (v4*)(p + head);
+    for (int64_t k = i; k < vecs; k += stride) body[k] = v4{0u, 0u, 0u, 0u};
+    for (int64_t k = head + (vecs << 4) + i; k < n; k += stride) p[k] = 0;
 }
 
 // core.step over several groups of lanes in one launch (step_groups,
@@ -992,6 +1010,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const int32_t steps = args.steps;
+    int32_t general = 0;  // cycles admitted request by request
     for (int32_t t = 0; t < steps; ++t) {
         bool irregular = false;
         int32_t n;
@@ -1101,6 +1120,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
                 // irregular flag keeps off this path) stages its requests first
                 if (fused) stage_requests(g, e, lane, n, q);
                 if (fast) mark_unavailable(g, e, lane);
+                ++general;
                 int32_t n_rank = 0;
                 const int32_t issued = order_requests(g, e, lane, &n_rank);
                 AS3 int16_t* order = at<int16_t>(e, g.lay.b_order);
@@ -1142,11 +1162,12 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
     {
         NR_ROLLOUT_PHASE
         store_env(g, a.s, l, e, lane);
+        if (a.out.general_admissions && lane == 0) a.out.general_admissions[l] = general;
     }
 }
 
 // Fused learner-vs-bot rollout: per cycle the learner's rows sampled from
-// its masks (the integer uniform-over-legal sampler, as nanorts_sample_actions
+// its masks (the integer uniform-over-legal sampler, as nanorts_amd_sample_actions
 // on get_avail_actions words), the bot's act, the seat step and the
 // observations, with the state resident in LDS across the launch.
 struct SeatRolloutArgs {
@@ -1569,19 +1590,19 @@ static void host_fold_in(uint32_t& k0, uint32_t& k1, uint32_t data) {
 // ---------------------------------------------------------------------------
 extern "C" {
 
-const char* nanorts_build_id(void) { return NANORTS_BUILD_ID; }
+const char* nanorts_amd_build_id(void) { return NANORTS_BUILD_ID; }
 
-const char* nanorts_targets(void) {
-    return "nanorts_step,nanorts_legality,nanorts_legality_words,nanorts_avail_actions,nanorts_visible_cells,"
-           "nanorts_observe,nanorts_pixels,nanorts_pixels_from_maps,nanorts_reset_where_done,nanorts_env_step,nanorts_sample_actions,"
-           "nanorts_step_groups,nanorts_env_transition,nanorts_decode_actions,nanorts_rollout,nanorts_abstraction_act,nanorts_seat_step,nanorts_seat_rollout,"
-           "nanorts_seat_step_lanes,nanorts_seat_rollout_lanes,nanorts_episode_seats,nanorts_gridnet_decode,"
-           "nanorts_gridnet_observe,nanorts_gridnet_step,nanorts_gridnet_step_against,nanorts_gridnet_sample_actions";
+const char* nanorts_amd_entries(void) {
+    return "nanorts_amd_step,nanorts_amd_step_ffi,nanorts_amd_legality,nanorts_amd_legality_words,nanorts_amd_avail_actions,nanorts_amd_visible_cells,"
+           "nanorts_amd_observe,nanorts_amd_pixels,nanorts_amd_pixels_from_maps,nanorts_amd_reset_where_done,nanorts_amd_env_step,nanorts_amd_sample_actions,"
+           "nanorts_amd_step_groups,nanorts_amd_env_transition,nanorts_amd_decode_actions,nanorts_amd_rollout,nanorts_amd_abstraction_act,nanorts_amd_seat_step,nanorts_amd_seat_rollout,"
+           "nanorts_amd_seat_step_lanes,nanorts_amd_seat_rollout_lanes,nanorts_amd_episode_seats,nanorts_amd_gridnet_decode,"
+           "nanorts_amd_gridnet_observe,nanorts_amd_gridnet_step,nanorts_amd_gridnet_step_against,nanorts_amd_gridnet_sample_actions";
 }
 
-const char* nanorts_last_error(void) { return g_error.c_str(); }
+const char* nanorts_amd_last_error(void) { return g_error.c_str(); }
 
-int64_t nanorts_shared_opt_in(const int32_t* devices, int64_t n) {
+int64_t nanorts_amd_shared_opt_in(const int32_t* devices, int64_t n) {
     int64_t least = 0;
     for (int64_t i = 0; i < n; ++i) {
         int bytes = 0;
@@ -1594,7 +1615,7 @@ int64_t nanorts_shared_opt_in(const int32_t* devices, int64_t n) {
     return least;
 }
 
-const char* nanorts_self_check(const int32_t* devices, int64_t n) {
+const char* nanorts_amd_self_check(const int32_t* devices, int64_t n) {
     static thread_local std::string result;
     result.clear();
     int current = 0;
@@ -1644,7 +1665,7 @@ const char* nanorts_self_check(const int32_t* devices, int64_t n) {
 #define NR_STATE(state)                                                                      \
     if (!state_complete(state)) return fail(NANORTS_INVALID_ARGUMENT, "a State leaf pointer is NULL");
 
-int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
+int nanorts_amd_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const uint32_t* key,
                  int64_t key_lanes, nanorts_commands commands, nanorts_step_results results) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1653,10 +1674,117 @@ int nanorts_step(void* stream, const nanorts_game* game, nanorts_state state, in
     if (!commands.kind || !commands.direction || !commands.none_duration || !commands.target_cell ||
         !commands.produced_type || !commands.request_order)
         return fail(NANORTS_INVALID_ARGUMENT, "a Commands field pointer is NULL");
-    return launch(k_step, sh, lanes, (hipStream_t)stream, state, key, key_lanes, commands, results);
+    return launch(k_step, sh, lanes, (hipStream_t)stream, state, key, key_lanes, commands, lanes, results);
 }
 
-int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
+static int zero_bytes(hipStream_t stream, void* p, int64_t n) {
+    if (n <= 0) return NANORTS_OK;
+    const int64_t blocks64 = (n / 16 + 255) / 256;
+    const unsigned blocks = (unsigned)(blocks64 < 1 ? 1 : (blocks64 > 4096 ? 4096 : blocks64));
+    hipLaunchKernelGGL(k_zero_bytes, dim3(blocks), dim3(256), 0, stream, (uint8_t*)p, n);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
+}
+
+int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
+                         int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
+                         int32_t capacity, int32_t types, int32_t offsets, int64_t strategy) {
+    if (!operands || !results) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operands or results is NULL");
+    if (strategy < NANORTS_CANCEL_BOTH || strategy > NANORTS_CANCEL_ALTERNATING)
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: strategy must be 0, 1 or 2");
+    if (lanes < 0 || (lanes > 0 && (key_lanes != 1 && key_lanes != lanes)))
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the key operand holds 1 or `lanes` rows");
+    if (lanes > 0 && command_lanes != 1 && command_lanes != lanes)
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the Commands operands hold 1 or `lanes` rows");
+    for (int i = 0; i < 33; ++i)
+        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operand " + std::to_string(i) + " is NULL");
+    for (int i = 0; i < 31; ++i)
+        if (!results[i]) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: result " + std::to_string(i) + " is NULL");
+    // The bucket from the extents; the unit table columns stay zero here and
+    // come from the table / timings operands in the kernel.
+    nanorts_game game;
+    std::memset(&game, 0, sizeof(game));
+    game.height = height;
+    game.width = width;
+    game.cells = height * width;
+    game.neutral = neutral;
+    game.capacity = capacity;
+    game.entities = neutral + 2 * capacity;
+    game.types = types;
+    game.offsets = offsets;
+    game.strategy = (int32_t)strategy;
+    game.max_cycles = 0x7fffffff;  // truncation is not a result of this target
+    game.terrain = (const uint8_t*)operands[7];
+    NR_SHAPE(&game)
+    sh.g.ref_table = (const int32_t*)operands[8];
+    sh.g.ref_timings = (const int32_t*)operands[9];
+    const hipStream_t st = (hipStream_t)stream;
+    const int64_t E = game.entities, cells = game.cells;
+    // Bytes per lane of the 23 state leaves in the reference's order.
+    const int64_t leaf_bytes[23] = {E * 4, E, E, E * 2, E * 2, E * 4, E, E, E * 4, E * 2, E, E * 4, E * 4, E * 4,
+                                    cells * 2, 4, 8, 4, 4, 4, 1, 4, 8};
+    // Results alias operands 10.. in place; where they do not, the state is
+    // copied into the result buffers first and stepped there.
+    void* leaf[23];
+    for (int i = 0; i < 23; ++i) {
+        leaf[i] = results[i];
+        if (results[i] != operands[10 + i] && lanes > 0 &&
+            hipMemcpyAsync(results[i], operands[10 + i], (size_t)(leaf_bytes[i] * lanes), hipMemcpyDeviceToDevice, st) !=
+                hipSuccess)
+            return fail(NANORTS_INTERNAL, "nanorts_amd_step_ffi: copying an unaliased state leaf failed");
+    }
+    nanorts_state s;
+    std::memset(&s, 0, sizeof(s));
+    s.birth = (int32_t*)leaf[0];
+    s.unit_type = (int8_t*)leaf[1];
+    s.owner = (int8_t*)leaf[2];
+    s.cell = (int16_t*)leaf[3];
+    s.hit_points = (int16_t*)leaf[4];
+    s.carried_resources = (int32_t*)leaf[5];
+    s.pending_kind = (int8_t*)leaf[6];
+    s.pending_direction = (int8_t*)leaf[7];
+    s.pending_none_duration = (int32_t*)leaf[8];
+    s.pending_target_cell = (int16_t*)leaf[9];
+    s.pending_produced_type = (int8_t*)leaf[10];
+    s.pending_issued_at = (int32_t*)leaf[11];
+    s.pending_completes_at = (int32_t*)leaf[12];
+    s.pending_order = (int32_t*)leaf[13];
+    s.entity_at = (int16_t*)leaf[14];
+    s.time = (int32_t*)leaf[15];
+    s.player_resources = (int32_t*)leaf[16];
+    s.next_birth = (int32_t*)leaf[17];
+    s.next_pending_order = (int32_t*)leaf[18];
+    s.alternating_conflict_count = (int32_t*)leaf[19];
+    s.game_over = (uint8_t*)leaf[20];
+    s.winner = (int32_t*)leaf[21];
+    s.spawn_overflow = (int32_t*)leaf[22];
+    nanorts_commands c;
+    c.kind = (const int32_t*)operands[1];
+    c.direction = (const int32_t*)operands[2];
+    c.none_duration = (const int32_t*)operands[3];
+    c.target_cell = (const int32_t*)operands[4];
+    c.produced_type = (const int32_t*)operands[5];
+    c.request_order = (const int32_t*)operands[6];
+    nanorts_step_results r;
+    std::memset(&r, 0, sizeof(r));
+    r.admitted_harvest = (int32_t*)results[23];
+    r.admitted_return = (int32_t*)results[24];
+    r.admitted_produce = (int32_t*)results[25];
+    r.admitted_attack = (int32_t*)results[26];
+    // The per-slot event records (is_member pred[L][E], int32 [L][E][6],
+    // int16 [L][E][4], int8 [L][E][6]) are written as "no member": nothing
+    // in the reference reads them, and every record field then reads as its
+    // fill.
+    const int64_t record_bytes[4] = {E, E * 6 * 4, E * 4 * 2, E * 6};
+    for (int i = 0; i < 4; ++i) {
+        const int code = zero_bytes(st, results[27 + i], record_bytes[i] * lanes);
+        if (code != NANORTS_OK) return code;
+    }
+    return launch(k_step, sh, lanes, st, s, (const uint32_t*)operands[0], key_lanes, c, command_lanes, r);
+}
+
+int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
                         const int64_t* lanes, const uint32_t* const* keys, const int64_t* key_lanes,
                         const nanorts_commands* commands, const nanorts_step_results* results) {
     if (groups < 1 || groups > 16) return fail(NANORTS_INVALID_ARGUMENT, "groups must be in [1, 16]");
@@ -1672,7 +1800,7 @@ int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const*
         if (a.H != b.H || a.W != b.W || a.N != b.N || a.C != b.C || a.T != b.T || a.O != b.O ||
             a.strategy != b.strategy || std::memcmp(a.tab, b.tab, sizeof(a.tab)) != 0)
             return fail(NANORTS_INVALID_ARGUMENT,
-                        "nanorts_step_groups: group " + std::to_string(i) + "'s bucket or unit table disagrees with group 0's");
+                        "nanorts_amd_step_groups: group " + std::to_string(i) + "'s bucket or unit table disagrees with group 0's");
         if (!state_complete(states[i])) return fail(NANORTS_INVALID_ARGUMENT, "a State leaf pointer is NULL");
         const nanorts_commands& c = commands[i];
         if (!c.kind || !c.direction || !c.none_duration || !c.target_cell || !c.produced_type || !c.request_order)
@@ -1711,14 +1839,14 @@ int nanorts_step_groups(void* stream, int32_t groups, const nanorts_game* const*
     return NANORTS_OK;
 }
 
-int nanorts_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows) {
+int nanorts_amd_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows) {
     NR_READER_SHAPE(game, true)
     NR_STATE(state)
     if (!rows) return fail(NANORTS_INVALID_ARGUMENT, "rows is NULL");
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, rows, (uint32_t*)nullptr);
 }
 
-int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            uint32_t* words) {
     NR_READER_SHAPE(game, true)
     NR_STATE(state)
@@ -1726,7 +1854,7 @@ int nanorts_legality_words(void* stream, const nanorts_game* game, nanorts_state
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 0, (uint8_t*)nullptr, words);
 }
 
-int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows,
+int nanorts_amd_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows,
                           uint32_t* words) {
     NR_READER_SHAPE(game, true)
     NR_STATE(state)
@@ -1734,7 +1862,7 @@ int nanorts_avail_actions(void* stream, const nanorts_game* game, nanorts_state 
     return launch(k_legality, sh, lanes, (hipStream_t)stream, state, 1, rows, words);
 }
 
-int nanorts_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t observer,
+int nanorts_amd_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t observer,
                           uint8_t* cells) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1743,7 +1871,7 @@ int nanorts_visible_cells(void* stream, const nanorts_game* game, nanorts_state 
     return launch(k_visible, sh, lanes, (hipStream_t)stream, state, observer, cells);
 }
 
-int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+int nanorts_amd_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
                     uint8_t* feature_maps, int32_t* scalars) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1751,7 +1879,7 @@ int nanorts_observe(void* stream, const nanorts_game* game, nanorts_state state,
     return launch(k_observe, sh, lanes, (hipStream_t)stream, state, partial, feature_maps, scalars);
 }
 
-int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
+int nanorts_amd_pixels(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t partial,
                    const uint8_t* tiles, uint8_t* image, int32_t* scalars) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1759,7 +1887,7 @@ int nanorts_pixels(void* stream, const nanorts_game* game, nanorts_state state, 
     return launch(k_pixels, sh, lanes, (hipStream_t)stream, state, partial, tiles, image, scalars);
 }
 
-int nanorts_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
+int nanorts_amd_pixels_from_maps(void* stream, const nanorts_game* game, int64_t images, const uint8_t* feature_maps,
                              const uint8_t* tiles, uint8_t* image) {
     NR_SHAPE(game)
     (void)sh;
@@ -1778,7 +1906,7 @@ int nanorts_pixels_from_maps(void* stream, const nanorts_game* game, int64_t ima
     return NANORTS_OK;
 }
 
-int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                              const uint8_t* done) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1787,7 +1915,7 @@ int nanorts_reset_where_done(void* stream, const nanorts_game* game, nanorts_sta
     return launch(k_reset, sh, lanes, (hipStream_t)stream, state, done);
 }
 
-int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const int32_t* actions,
+int nanorts_amd_env_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, const int32_t* actions,
                      int32_t partial, nanorts_env_results results) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1798,7 +1926,7 @@ int nanorts_env_step(void* stream, const nanorts_game* game, nanorts_state state
     return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results, 1);
 }
 
-int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_env_transition(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, int32_t partial, nanorts_env_results results) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1808,7 +1936,7 @@ int nanorts_env_transition(void* stream, const nanorts_game* game, nanorts_state
     return launch(k_env_step, sh, lanes, (hipStream_t)stream, state, actions, partial, results, 0);
 }
 
-int nanorts_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_decode_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, nanorts_command_buffers commands, uint32_t* episode_keys) {
     NR_SHAPE(game)
     NR_STATE(state)
@@ -1843,7 +1971,7 @@ static bool bot_args(const nanorts_game* game, Shape* sh, BotArgs* a, int32_t st
     return true;
 }
 
-int nanorts_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_abstraction_act(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             int32_t strategy, int32_t trained_type, const int32_t* player, int64_t player_lanes,
                             nanorts_abstract_actions carry, int32_t* commands) {
     NR_STATE(state)
@@ -1873,7 +2001,7 @@ static int seat_step(void* stream, const nanorts_game* game, nanorts_state state
                   results);
 }
 
-int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+int nanorts_amd_seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
                       int32_t trained_type, int32_t learner, nanorts_abstract_actions carry, const int32_t* actions,
                       int32_t partial, nanorts_env_results results) {
     NR_STATE(state)
@@ -1882,7 +2010,7 @@ int nanorts_seat_step(void* stream, const nanorts_game* game, nanorts_state stat
                      results);
 }
 
-int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
                             nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
                             nanorts_env_results results) {
@@ -1892,7 +2020,7 @@ int nanorts_seat_step_lanes(void* stream, const nanorts_game* game, nanorts_stat
                      results);
 }
 
-int nanorts_episode_seats(void* stream, const uint32_t* environment_root, const uint32_t* episode_index, int64_t lanes,
+int nanorts_amd_episode_seats(void* stream, const uint32_t* environment_root, const uint32_t* episode_index, int64_t lanes,
                           int32_t* seats) {
     if (!environment_root || !episode_index || !seats) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
     if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, "lanes must be >= 0");
@@ -1906,7 +2034,7 @@ int nanorts_episode_seats(void* stream, const uint32_t* environment_root, const 
     return NANORTS_OK;
 }
 
-int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
+int nanorts_amd_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* avail_words,
                            const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
     NR_READER_SHAPE(game, false)
     if (!avail_words || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
@@ -1914,7 +2042,7 @@ int nanorts_sample_actions(void* stream, const nanorts_game* game, int64_t lanes
                   actions);
 }
 
-int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
+int nanorts_amd_gridnet_sample_actions(void* stream, const nanorts_game* game, int64_t lanes, const uint32_t* mask,
                                    const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
     NR_READER_SHAPE(game, false)
     if (!mask || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
@@ -1924,7 +2052,7 @@ int nanorts_gridnet_sample_actions(void* stream, const nanorts_game* game, int64
                   actions);
 }
 
-int nanorts_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                     const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
                     nanorts_rollout_results results) {
     NR_SHAPE(game)
@@ -1980,7 +2108,7 @@ static bool gridnet_obs_valid(const nanorts_gridnet_obs& o, std::string* why) {
     return true;
 }
 
-int nanorts_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, nanorts_command_buffers commands) {
     NR_STATE(state)
     if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
@@ -1994,7 +2122,7 @@ int nanorts_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state
     return launch(k_gridnet_decode, sh, lanes, (hipStream_t)stream, state, gy, actions, commands);
 }
 
-int nanorts_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                             nanorts_gridnet_obs obs) {
     NR_STATE(state)
     Shape sh;
@@ -2005,7 +2133,7 @@ int nanorts_gridnet_observe(void* stream, const nanorts_game* game, nanorts_stat
     return launch(k_gridnet_observe, sh, lanes, (hipStream_t)stream, state, obs);
 }
 
-int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                          const int32_t* actions, nanorts_gridnet_results results) {
     NR_STATE(state)
     if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
@@ -2021,7 +2149,7 @@ int nanorts_gridnet_step(void* stream, const nanorts_game* game, nanorts_state s
     return launch(k_gridnet_step, sh, lanes, (hipStream_t)stream, state, gy, actions, none, 0, results);
 }
 
-int nanorts_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_gridnet_step_against(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                                  const int32_t* actions, nanorts_commands commands, nanorts_gridnet_results results) {
     NR_STATE(state)
     if (!actions) return fail(NANORTS_INVALID_ARGUMENT, "actions is NULL");
@@ -2088,7 +2216,7 @@ static int seat_rollout(void* stream, const nanorts_game* game, nanorts_state st
     return NANORTS_OK;
 }
 
-int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
+int nanorts_amd_seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
                          int32_t trained_type, int32_t learner, nanorts_abstract_actions carry,
                          const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
                          nanorts_rollout_results results) {
@@ -2098,7 +2226,7 @@ int nanorts_seat_rollout(void* stream, const nanorts_game* game, nanorts_state s
                         sample_key, step0, steps, partial, env0, results);
 }
 
-int nanorts_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
+int nanorts_amd_seat_rollout_lanes(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                                int32_t strategy, int32_t trained_type, int32_t* seats, int32_t draw,
                                int32_t* seat_record, nanorts_abstract_actions carry, const uint32_t* sample_key,
                                int32_t step0, int32_t steps, int32_t partial, int64_t env0,

@@ -375,8 +375,8 @@ class NanoRTS:
                     for f, _ in native.Commands._fields_}
         keys = torch.empty((L, 2), dtype=torch.int32, device=d)
         bufs = native.Commands(*[_ptr(commands[f]) for f, _ in native.Commands._fields_])
-        native.check(self.lib.nanorts_decode_actions(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs,
-                                                     _ptr(keys)), "nanorts_decode_actions")
+        native.check(self.lib.nanorts_amd_decode_actions(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs,
+                                                     _ptr(keys)), "nanorts_amd_decode_actions")
         return (keys, state.core_state, commands), None
 
     def step_response(self, state: EnvironmentState, carry, stepped: dict[str, torch.Tensor]):
@@ -443,11 +443,11 @@ class NanoRTS:
             _ptr(out["winner"]), _ptr(out["spawn_overflowed"]), _ptr(maps), _ptr(scalars), _ptr(fmaps), _ptr(fscal),
             _ptr(comps), _ptr(out["spawn_overflow"]))
         if reset:
-            native.check(self.lib.nanorts_env_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), self.partial,
-                                                   results), "nanorts_env_step")
+            native.check(self.lib.nanorts_amd_env_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), self.partial,
+                                                   results), "nanorts_amd_env_step")
         else:
-            native.check(self.lib.nanorts_env_transition(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts),
-                                                         self.partial, results), "nanorts_env_transition")
+            native.check(self.lib.nanorts_amd_env_transition(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts),
+                                                         self.partial, results), "nanorts_amd_env_transition")
         obs = self._symbolic(maps, scalars) if symbolic else self._pixels(maps, scalars)
         rewards = {agent: out["reward"][:, p] for p, agent in enumerate(self.agents)}
         dones = {agent: out["done"] for agent in self.agents} | {ALL_AGENTS: out["done"]}
@@ -473,12 +473,12 @@ class NanoRTS:
         if form == "rows":
             rows = torch.empty((L, 2, b.per_player_capacity, self.layout.mask_width), dtype=torch.bool,
                                device=self.device)
-            native.check(self.lib.nanorts_avail_actions(_stream(), self.dev.ref, state.native(), L, _ptr(rows), None),
-                         "nanorts_avail_actions")
+            native.check(self.lib.nanorts_amd_avail_actions(_stream(), self.dev.ref, state.native(), L, _ptr(rows), None),
+                         "nanorts_amd_avail_actions")
         elif form == "words":
             rows = torch.empty((L, 2, b.per_player_capacity, 3), dtype=torch.int32, device=self.device)
-            native.check(self.lib.nanorts_avail_actions(_stream(), self.dev.ref, state.native(), L, None, _ptr(rows)),
-                         "nanorts_avail_actions")
+            native.check(self.lib.nanorts_amd_avail_actions(_stream(), self.dev.ref, state.native(), L, None, _ptr(rows)),
+                         "nanorts_amd_avail_actions")
         else:
             raise ModelError(f"form={form!r} is unknown; get_avail_actions returns 'rows' or 'words'")
         return {agent: rows[:, p] for p, agent in enumerate(self.agents)}
@@ -495,12 +495,12 @@ class NanoRTS:
         scalars = torch.empty((L, 2, 4), dtype=torch.int32, device=self.device)
         if self.layout.surface == "pixels":
             image = torch.empty((L, 2, 16 * b.height, 16 * b.width, 3), dtype=torch.uint8, device=self.device)
-            native.check(self.lib.nanorts_pixels(_stream(), self.dev.ref, state.native(), L, self.partial,
-                                                 _ptr(self._tiles), _ptr(image), _ptr(scalars)), "nanorts_pixels")
+            native.check(self.lib.nanorts_amd_pixels(_stream(), self.dev.ref, state.native(), L, self.partial,
+                                                 _ptr(self._tiles), _ptr(image), _ptr(scalars)), "nanorts_amd_pixels")
             return {agent: PixelObservation(image[:, p], scalars[:, p]) for p, agent in enumerate(self.agents)}
         maps = torch.empty((L, 2, b.height, b.width, 6), dtype=torch.uint8, device=self.device)
-        native.check(self.lib.nanorts_observe(_stream(), self.dev.ref, state.native(), L, self.partial, _ptr(maps),
-                                              _ptr(scalars)), "nanorts_observe")
+        native.check(self.lib.nanorts_amd_observe(_stream(), self.dev.ref, state.native(), L, self.partial, _ptr(maps),
+                                              _ptr(scalars)), "nanorts_amd_observe")
         return self._symbolic(maps, scalars)
 
     # ------------------------------------------------------- beyond the API
@@ -523,38 +523,38 @@ class NanoRTS:
                "admitted_attack": torch.empty((L, 2, 3), dtype=torch.int32, device=d)}
         c = native.Commands(*[_ptr(cmd[f]) for f, _ in native.Commands._fields_])
         r = native.StepResults(*[_ptr(out[f]) for f, _ in native.StepResults._fields_])
-        native.check(self.lib.nanorts_step(_stream(), self.dev.ref, state.native(), L, _ptr(keyt), keyt.shape[0], c,
-                                           r), "nanorts_step")
+        native.check(self.lib.nanorts_amd_step(_stream(), self.dev.ref, state.native(), L, _ptr(keyt), keyt.shape[0], c,
+                                           r), "nanorts_amd_step")
         return out
 
     def legality(self, state: EnvironmentState, *, form: str = "words") -> torch.Tensor:
         """Factored legality before availability (core.legal_commands), as the
-        reference's nanorts_legality[_words] targets publish it."""
+        reference's nanorts_amd_legality[_words] targets publish it."""
         L = state.num_envs
         b = self.bucket
         if form == "words":
             out = torch.empty((L, 2, b.per_player_capacity, 3), dtype=torch.int32, device=self.device)
-            native.check(self.lib.nanorts_legality_words(_stream(), self.dev.ref, state.native(), L, _ptr(out)),
-                         "nanorts_legality_words")
+            native.check(self.lib.nanorts_amd_legality_words(_stream(), self.dev.ref, state.native(), L, _ptr(out)),
+                         "nanorts_amd_legality_words")
         else:
             out = torch.empty((L, 2, b.per_player_capacity, self.layout.mask_width), dtype=torch.bool,
                               device=self.device)
-            native.check(self.lib.nanorts_legality(_stream(), self.dev.ref, state.native(), L, _ptr(out)),
-                         "nanorts_legality")
+            native.check(self.lib.nanorts_amd_legality(_stream(), self.dev.ref, state.native(), L, _ptr(out)),
+                         "nanorts_amd_legality")
         return out
 
     def visible_cells(self, state: EnvironmentState, observer: int) -> torch.Tensor:
         L = state.num_envs
         b = self.bucket
         out = torch.empty((L, b.height, b.width), dtype=torch.bool, device=self.device)
-        native.check(self.lib.nanorts_visible_cells(_stream(), self.dev.ref, state.native(), L, int(observer),
-                                                    _ptr(out)), "nanorts_visible_cells")
+        native.check(self.lib.nanorts_amd_visible_cells(_stream(), self.dev.ref, state.native(), L, int(observer),
+                                                    _ptr(out)), "nanorts_amd_visible_cells")
         return out
 
     def reset_where_done(self, state: EnvironmentState, done: torch.Tensor) -> None:
         done = done.to(device=self.device, dtype=torch.bool).contiguous()
-        native.check(self.lib.nanorts_reset_where_done(_stream(), self.dev.ref, state.native(), state.num_envs,
-                                                       _ptr(done)), "nanorts_reset_where_done")
+        native.check(self.lib.nanorts_amd_reset_where_done(_stream(), self.dev.ref, state.native(), state.num_envs,
+                                                       _ptr(done)), "nanorts_amd_reset_where_done")
 
     def sample_actions(self, words, sample_key, step: int, env0: int = 0) -> dict[str, torch.Tensor]:
         """The synthetic harness's integer uniform-over-legal sampler on
@@ -569,14 +569,17 @@ class NanoRTS:
         b = self.bucket
         key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
         actions = torch.empty((L, 2, b.per_player_capacity, 7), dtype=torch.int32, device=self.device)
-        native.check(self.lib.nanorts_sample_actions(_stream(), self.dev.ref, L, _ptr(words), key, int(step), int(env0),
-                                                     _ptr(actions)), "nanorts_sample_actions")
+        native.check(self.lib.nanorts_amd_sample_actions(_stream(), self.dev.ref, L, _ptr(words), key, int(step), int(env0),
+                                                     _ptr(actions)), "nanorts_amd_sample_actions")
         return {agent: actions[:, p] for p, agent in enumerate(self.agents)}
 
     def rollout(self, state: EnvironmentState, steps: int, sample_key, *, step0: int = 0, env0: int = 0,
-                record: bool = True, record_actions: bool = False, observation_depth: int = 1) -> dict[str, Any]:
+                record: bool = True, record_actions: bool = False, observation_depth: int = 1,
+                count_general: bool = False) -> dict[str, Any]:
         """Fused rollout: `steps` cycles of masks -> sample -> env.step with the
-        state resident in LDS, in place.  Bit-equal to the per-call API."""
+        state resident in LDS, in place.  Bit-equal to the per-call API.  With
+        count_general, out["general_admissions"] int32[L] counts each env's
+        cycles that took the request-at-a-time admission."""
         L = state.num_envs
         b = self.bucket
         d = self.device
@@ -589,10 +592,13 @@ class NanoRTS:
         maps = torch.empty((depth, L, 2, b.height, b.width, 6), dtype=torch.uint8, device=d)
         scalars = torch.empty((depth, L, 2, 4), dtype=torch.int32, device=d)
         key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
-        results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth)
-        native.check(self.lib.nanorts_rollout(_stream(), self.dev.ref, state.native(), L, key, int(step0), int(steps),
-                                              self.partial, int(env0), results), "nanorts_rollout")
-        out.update(rewards=rewards, dones=dones, actions=actions, feature_maps=maps, scalars=scalars)
+        general = torch.empty(L, dtype=torch.int32, device=d) if count_general else None
+        results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth,
+                                        _ptr(general))
+        native.check(self.lib.nanorts_amd_rollout(_stream(), self.dev.ref, state.native(), L, key, int(step0), int(steps),
+                                              self.partial, int(env0), results), "nanorts_amd_rollout")
+        out.update(rewards=rewards, dones=dones, actions=actions, feature_maps=maps, scalars=scalars,
+                   general_admissions=general)
         return out
 
     # -------------------------------------------------------------- helpers
@@ -616,8 +622,8 @@ class NanoRTS:
         lead = tuple(maps.shape[:-3])
         images = int(np.prod(lead)) if lead else 1
         image = torch.empty((*lead, 16 * b.height, 16 * b.width, 3), dtype=torch.uint8, device=self.device)
-        native.check(self.lib.nanorts_pixels_from_maps(_stream(), self.dev.ref, images, _ptr(maps), _ptr(self._tiles),
-                                                       _ptr(image)), "nanorts_pixels_from_maps")
+        native.check(self.lib.nanorts_amd_pixels_from_maps(_stream(), self.dev.ref, images, _ptr(maps), _ptr(self._tiles),
+                                                       _ptr(image)), "nanorts_amd_pixels_from_maps")
         return image
 
     def _pixels(self, maps: torch.Tensor, scalars: torch.Tensor) -> dict[str, PixelObservation]:

@@ -206,8 +206,8 @@ class GridNet:
     def observe(self, state: EnvironmentState) -> GridNetObservation:
         """observation.observe (src/nanorts/adapters/gridnet/observation.py:27-33)."""
         obs, struct = self._obs_buffers(state.num_envs)
-        native.check(self.lib.nanorts_gridnet_observe(_stream(), self.dev.ref, state.native(), state.num_envs, struct),
-                     "nanorts_gridnet_observe")
+        native.check(self.lib.nanorts_amd_gridnet_observe(_stream(), self.dev.ref, state.native(), state.num_envs, struct),
+                     "nanorts_amd_gridnet_observe")
         return obs
 
     def planes(self, state: EnvironmentState) -> torch.Tensor:
@@ -215,8 +215,8 @@ class GridNet:
         y = self.layout
         planes = torch.empty((state.num_envs, *y.planes_shape), dtype=y.planes_dtype, device=self.device)
         struct = self._obs_struct(planes, None, None)
-        native.check(self.lib.nanorts_gridnet_observe(_stream(), self.dev.ref, state.native(), state.num_envs, struct),
-                     "nanorts_gridnet_observe")
+        native.check(self.lib.nanorts_amd_gridnet_observe(_stream(), self.dev.ref, state.native(), state.num_envs, struct),
+                     "nanorts_amd_gridnet_observe")
         return planes
 
     def decode_actions(self, actions: torch.Tensor, state: EnvironmentState) -> dict[str, torch.Tensor]:
@@ -227,8 +227,8 @@ class GridNet:
         out = {f: torch.empty((L, PLAYER_COUNT, self.game.bucket.per_player_capacity), dtype=torch.int32,
                               device=self.device) for f in _COMMAND_FIELDS}
         bufs = native.Commands(*[_ptr(out[f]) for f in _COMMAND_FIELDS])
-        native.check(self.lib.nanorts_gridnet_decode(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs),
-                     "nanorts_gridnet_decode")
+        native.check(self.lib.nanorts_amd_gridnet_decode(_stream(), self.dev.ref, state.native(), L, _ptr(acts), bufs),
+                     "nanorts_amd_gridnet_decode")
         return out
 
     def sample_actions(self, action_mask: torch.Tensor, sample_key, step: int, env0: int = 0) -> torch.Tensor:
@@ -245,9 +245,9 @@ class GridNet:
         key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
         actions = torch.empty((L, PLAYER_COUNT, b.height, b.width, len(ACTION_FACTORS)), dtype=torch.int32,
                               device=self.device)
-        native.check(self.lib.nanorts_gridnet_sample_actions(_stream(), self.dev.ref, L, _ptr(mask), key, int(step),
+        native.check(self.lib.nanorts_amd_gridnet_sample_actions(_stream(), self.dev.ref, L, _ptr(mask), key, int(step),
                                                              int(env0), _ptr(actions)),
-                     "nanorts_gridnet_sample_actions")
+                     "nanorts_amd_gridnet_sample_actions")
         return actions
 
     def step(self, state: EnvironmentState, actions: torch.Tensor, *, donate: bool = False) -> GridNetStep:
@@ -292,13 +292,13 @@ class GridNet:
                                         _ptr(flags["done"]), _ptr(winner), _ptr(flags["spawn_overflowed"]),
                                         _ptr(final), struct, _ptr(telemetry))
         if given is None:
-            code = self.lib.nanorts_gridnet_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), results)
-            native.check(code, "nanorts_gridnet_step")
+            code = self.lib.nanorts_amd_gridnet_step(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), results)
+            native.check(code, "nanorts_amd_gridnet_step")
         else:
             c = native.Commands(*[_ptr(given[f]) for f in _COMMAND_FIELDS])
-            code = self.lib.nanorts_gridnet_step_against(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), c,
+            code = self.lib.nanorts_amd_gridnet_step_against(_stream(), self.dev.ref, nxt.native(), L, _ptr(acts), c,
                                                          results)
-            native.check(code, "nanorts_gridnet_step_against")
+            native.check(code, "nanorts_amd_gridnet_step_against")
         return GridNetStep(environment_state=nxt, observation=obs, reward_components=comps, reward_dones=rdones,
                            terminated=flags["terminated"], truncated=flags["truncated"], done=flags["done"],
                            winner=winner, telemetry={"spawn_overflow": telemetry},

@@ -106,13 +106,13 @@ def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]
             cmds = (native.Commands * G)(*[native.Commands(*[_ptr(p[2][f]) for f in _COMMAND_FIELDS]) for p in part])
             outs = (native.StepResults * G)(*[native.StepResults(*[_ptr(p[3][f]) for f, _ in
                                                                    native.StepResults._fields_]) for p in part])
-            native.check(lib.nanorts_step_groups(_stream(), G, games, states, lanes, keys, key_lanes, cmds, outs),
-                         "nanorts_step_groups")
+            native.check(lib.nanorts_amd_step_groups(_stream(), G, games, states, lanes, keys, key_lanes, cmds, outs),
+                         "nanorts_amd_step_groups")
         return results
     for dev, (L, keyt, cmd, out, st) in zip(devs, prepared, strict=True):
         c = native.Commands(*[_ptr(cmd[f]) for f in _COMMAND_FIELDS])
         r = native.StepResults(*[_ptr(out[f]) for f, _ in native.StepResults._fields_])
-        native.check(lib.nanorts_step(_stream(), dev.ref, st, L, _ptr(keyt), keyt.shape[0], c, r), "nanorts_step")
+        native.check(lib.nanorts_amd_step(_stream(), dev.ref, st, L, _ptr(keyt), keyt.shape[0], c, r), "nanorts_amd_step")
     return results
 
 

@@ -64,7 +64,7 @@ class EnvResults(ctypes.Structure):
 
 class RolloutResults(ctypes.Structure):
     _fields_ = [("rewards", _VP), ("dones", _VP), ("actions", _VP), ("feature_maps", _VP), ("scalars", _VP),
-                ("depth", ctypes.c_int32)]
+                ("depth", ctypes.c_int32), ("general_admissions", _VP)]
 
 
 ABSTRACT_FIELDS = ("kind", "unit_birth", "order", "target", "target_birth", "base", "base_birth", "cell",
@@ -89,14 +89,15 @@ class GridNetResults(ctypes.Structure):
 
 # Every extern "C" symbol include/nanorts_amd.h declares.
 EXPORTS = (
-    "nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check", "nanorts_step",
-    "nanorts_step_groups", "nanorts_env_transition", "nanorts_decode_actions",
-    "nanorts_legality", "nanorts_legality_words", "nanorts_avail_actions", "nanorts_visible_cells",
-    "nanorts_observe", "nanorts_pixels", "nanorts_pixels_from_maps", "nanorts_reset_where_done", "nanorts_env_step", "nanorts_sample_actions",
-    "nanorts_rollout", "nanorts_abstraction_act", "nanorts_seat_step", "nanorts_seat_rollout",
-    "nanorts_seat_step_lanes", "nanorts_seat_rollout_lanes", "nanorts_episode_seats",
-    "nanorts_gridnet_decode", "nanorts_gridnet_observe", "nanorts_gridnet_step", "nanorts_gridnet_step_against",
-    "nanorts_gridnet_sample_actions",
+    "nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in",
+    "nanorts_amd_self_check", "nanorts_amd_step", "nanorts_amd_step_ffi",
+    "nanorts_amd_step_groups", "nanorts_amd_env_transition", "nanorts_amd_decode_actions",
+    "nanorts_amd_legality", "nanorts_amd_legality_words", "nanorts_amd_avail_actions", "nanorts_amd_visible_cells",
+    "nanorts_amd_observe", "nanorts_amd_pixels", "nanorts_amd_pixels_from_maps", "nanorts_amd_reset_where_done", "nanorts_amd_env_step", "nanorts_amd_sample_actions",
+    "nanorts_amd_rollout", "nanorts_amd_abstraction_act", "nanorts_amd_seat_step", "nanorts_amd_seat_rollout",
+    "nanorts_amd_seat_step_lanes", "nanorts_amd_seat_rollout_lanes", "nanorts_amd_episode_seats",
+    "nanorts_amd_gridnet_decode", "nanorts_amd_gridnet_observe", "nanorts_amd_gridnet_step", "nanorts_amd_gridnet_step_against",
+    "nanorts_amd_gridnet_sample_actions",
 )
 
 _I64 = ctypes.c_int64
@@ -104,42 +105,43 @@ _I32 = ctypes.c_int32
 _GP = ctypes.POINTER(Game)
 
 _SIGNATURES = {
-    "nanorts_build_id": (ctypes.c_char_p, []),
-    "nanorts_targets": (ctypes.c_char_p, []),
-    "nanorts_last_error": (ctypes.c_char_p, []),
-    "nanorts_shared_opt_in": (ctypes.c_int64, [_VP, _I64]),
-    "nanorts_self_check": (ctypes.c_char_p, [_VP, _I64]),
-    "nanorts_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I64, Commands, StepResults]),
-    "nanorts_step_groups": (ctypes.c_int, [_VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
-    "nanorts_legality": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
-    "nanorts_legality_words": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
-    "nanorts_avail_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _VP]),
-    "nanorts_visible_cells": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP]),
-    "nanorts_observe": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP]),
-    "nanorts_pixels": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP, _VP]),
-    "nanorts_pixels_from_maps": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _VP]),
-    "nanorts_reset_where_done": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
-    "nanorts_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
-    "nanorts_env_transition": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
-    "nanorts_decode_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, _VP]),
-    "nanorts_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
-    "nanorts_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
-    "nanorts_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
-    "nanorts_seat_step": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32,
+    "nanorts_amd_build_id": (ctypes.c_char_p, []),
+    "nanorts_amd_entries": (ctypes.c_char_p, []),
+    "nanorts_amd_last_error": (ctypes.c_char_p, []),
+    "nanorts_amd_shared_opt_in": (ctypes.c_int64, [_VP, _I64]),
+    "nanorts_amd_self_check": (ctypes.c_char_p, [_VP, _I64]),
+    "nanorts_amd_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I64, Commands, StepResults]),
+    "nanorts_amd_step_ffi": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64]),
+    "nanorts_amd_step_groups": (ctypes.c_int, [_VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "nanorts_amd_legality": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_amd_legality_words": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_amd_avail_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _VP]),
+    "nanorts_amd_visible_cells": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP]),
+    "nanorts_amd_observe": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP]),
+    "nanorts_amd_pixels": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _VP, _VP, _VP]),
+    "nanorts_amd_pixels_from_maps": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _VP]),
+    "nanorts_amd_reset_where_done": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
+    "nanorts_amd_env_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
+    "nanorts_amd_env_transition": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, EnvResults]),
+    "nanorts_amd_decode_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, _VP]),
+    "nanorts_amd_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
+    "nanorts_amd_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
+    "nanorts_amd_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
+    "nanorts_amd_seat_step": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32,
                                          EnvResults]),
-    "nanorts_seat_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32, _I32,
+    "nanorts_amd_seat_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32, _I32,
                                             _I32, _I64, RolloutResults]),
-    "nanorts_seat_step_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, AbstractActions, _VP,
+    "nanorts_amd_seat_step_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, AbstractActions, _VP,
                                                _I32, EnvResults]),
-    "nanorts_seat_rollout_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, _VP, AbstractActions,
+    "nanorts_amd_seat_rollout_lanes": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I32, _VP, AbstractActions,
                                                   _VP, _I32, _I32, _I32, _I64, RolloutResults]),
-    "nanorts_episode_seats": (ctypes.c_int, [_VP, _VP, _VP, _I64, _VP]),
+    "nanorts_amd_episode_seats": (ctypes.c_int, [_VP, _VP, _VP, _I64, _VP]),
     # the command buffers have the layout of Commands (six int32 pointers)
-    "nanorts_gridnet_decode": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands]),
-    "nanorts_gridnet_observe": (ctypes.c_int, [_VP, _GP, State, _I64, GridNetObs]),
-    "nanorts_gridnet_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, GridNetResults]),
-    "nanorts_gridnet_step_against": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, GridNetResults]),
-    "nanorts_gridnet_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
+    "nanorts_amd_gridnet_decode": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands]),
+    "nanorts_amd_gridnet_observe": (ctypes.c_int, [_VP, _GP, State, _I64, GridNetObs]),
+    "nanorts_amd_gridnet_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, GridNetResults]),
+    "nanorts_amd_gridnet_step_against": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, GridNetResults]),
+    "nanorts_amd_gridnet_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None
@@ -165,11 +167,18 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         fn.restype = restype
         fn.argtypes = argtypes
     if path is None:
+        # The in-tree library must be the build of the sources beside it
+        # (the reference's loader refuses a digest mismatch the same way,
+        # src/nanorts/kernels/library.py:53-54).
+        built, sources = lib.nanorts_amd_build_id().decode(), _build.source_digest()
+        if built != sources:
+            raise RuntimeError(f"{target} was built from sources with digest {built}, but the sources here have "
+                               f"digest {sources}: rebuild it (python -m nanorts_amd.build)")
         _LIBRARY = lib
     return lib
 
 
 def check(code: int, what: str) -> None:
     if code != 0:
-        message = load().nanorts_last_error().decode()
+        message = load().nanorts_amd_last_error().decode()
         raise NativeError(f"{what} failed with code {code}: {message}")

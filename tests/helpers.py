@@ -27,6 +27,12 @@ CASES = {
                         True, True),
     "obstacle-alternating": ("basesWorkers8x8Obstacle", UnitTypeTableVersion.ORIGINAL,
                              ConflictStrategy.CANCEL_ALTERNATING, 120, True, False),
+    # widths that are not a multiple of 4: the kernels' general observation
+    # and summary branches
+    "10x10-random-partial": ("basesWorkers10x10", UnitTypeTableVersion.ORIGINAL_FINETUNED,
+                             ConflictStrategy.CANCEL_RANDOM, 5000, True, True),
+    "9x8-alternating": ("NoWhereToRun9x8", UnitTypeTableVersion.ORIGINAL, ConflictStrategy.CANCEL_ALTERNATING, 130,
+                        True, False),
 }
 
 

@@ -15,7 +15,7 @@ from oracle.oracle import copy_state
 pytestmark = pytest.mark.gpu
 
 FAST_CASES = ["8x8-original-both", "16x16-finetuned-both", "16x16-random-partial", "16x16-alternating",
-              "melee-both", "barracks-random", "obstacle-alternating"]
+              "melee-both", "barracks-random", "obstacle-alternating", "10x10-random-partial", "9x8-alternating"]
 
 
 def _env(game, partial, **kw):
@@ -52,7 +52,7 @@ def test_masks_visibility_observation(case, oracle_threads):
 
 @pytest.mark.parametrize("case", FAST_CASES)
 def test_core_step(case, oracle_threads):
-    """nanorts_step against core.step on decoded sampled actions, one cycle
+    """nanorts_amd_step against core.step on decoded sampled actions, one cycle
     from many mid-game states, with random episode-root keys."""
     game, partial = game_for(case)
     L = 128
@@ -77,16 +77,19 @@ def test_core_step(case, oracle_threads):
 @pytest.mark.parametrize("case", FAST_CASES)
 def test_env_step_per_call(case, oracle_threads):
     """The per-call path (avail words -> sampler -> env.step) cycle by cycle
-    against the oracle: actions, rewards, dones, infos, observations and the
-    whole state after every cycle."""
+    against the oracle: actions, rewards, dones, infos, observations, the
+    ending state's observation (final_observation), the reward components and
+    the whole state after every cycle."""
     import torch
 
+    print(f"env.step per call {case}", flush=True)
     game, partial = game_for(case)
     L, steps = 64, 60
     oracle, st = advanced_states(game, L, 80, partial, oracle_threads, seed=3)
     env = _env(game, partial, reward_components=True)
     dev = to_device(env, st)
     key = (17, 23)
+    ended = 0
     for t in range(steps):
         words = env.get_avail_actions(dev, form="words")
         stacked = torch.stack([words[a] for a in env.agents], 1)
@@ -96,8 +99,16 @@ def test_env_step_per_call(case, oracle_threads):
         got_actions = np.stack([acts[a].cpu().numpy() for a in env.agents], 1)
         np.testing.assert_array_equal(got_actions, want_actions, err_msg=f"actions at cycle {t}")
         obs, dev, rewards, dones, infos = env.step(None, dev, acts, donate=True)
-        want = oracle.env_step(st, want_actions, partial)
+        want = oracle.env_step(st, want_actions, partial, final=True)
         assert_states_equal(st, to_host(dev), f"{case} cycle {t}")
+        ended += int(want["done"].sum())
+        final = infos["final_observation"]
+        for i, agent in enumerate(env.agents):
+            np.testing.assert_array_equal(final[agent].feature_maps.cpu().numpy(), want["final_feature_maps"][:, i],
+                                          err_msg=f"final observation at cycle {t}")
+            np.testing.assert_array_equal(final[agent].scalars.cpu().numpy(), want["final_scalars"][:, i])
+            np.testing.assert_array_equal(infos["reward_components"][agent].cpu().numpy(),
+                                          want["reward_components"][:, i], err_msg=f"components at cycle {t}")
         got_reward = np.stack([rewards[a].cpu().numpy() for a in env.agents], 1)
         np.testing.assert_array_equal(got_reward, want["reward"])
         np.testing.assert_array_equal(dones["__all__"].cpu().numpy(), want["done"].astype(bool))
@@ -108,6 +119,8 @@ def test_env_step_per_call(case, oracle_threads):
         for i, agent in enumerate(env.agents):
             np.testing.assert_array_equal(obs[agent].feature_maps.cpu().numpy(), want["feature_maps"][:, i])
             np.testing.assert_array_equal(obs[agent].scalars.cpu().numpy(), want["scalars"][:, i])
+    if game.max_cycles <= 80 + steps:  # a horizon inside the run: episode ends were compared
+        assert ended > 0
 
 
 @pytest.mark.parametrize("case", FAST_CASES + ["16x16-noprofile-random"])
@@ -136,7 +149,7 @@ def test_fused_rollout_matches_oracle(case, recorded, oracle_threads):
 
 @pytest.mark.parametrize("case", ["16x16-random-partial", "melee-both", "gow-alternating"])
 def test_pixels(case, oracle_threads):
-    """nanorts_pixels (from the state) and nanorts_pixels_from_maps (from the
+    """nanorts_amd_pixels (from the state) and nanorts_amd_pixels_from_maps (from the
     symbolic maps) against the oracle's renderer, both observability modes."""
     import torch
 
@@ -231,8 +244,92 @@ def test_self_check_and_build_id():
     import ctypes
 
     dev = (ctypes.c_int32 * 1)(0)
-    assert lib.nanorts_self_check(dev, 1).decode() == ""
-    assert len(lib.nanorts_build_id().decode()) > 0
+    assert lib.nanorts_amd_self_check(dev, 1).decode() == ""
+    from nanorts_amd import build
+
+    assert lib.nanorts_amd_build_id().decode() == build.source_digest()
 
 
 _ = CASES
+
+
+def _crowded(game, L: int, units0: int = 72, units1: int = 12, seed: int = 5) -> dict:
+    """GardenOfWar64x64 starting states with `units0` extra Workers for player
+    0 and `units1` for player 1 on open cells, each born in its block's lowest
+    free slot: more available units than the 64 lanes of a wave."""
+    from oracle.oracle import batch_initial
+    from tests.helpers import roots
+
+    st = batch_initial(game, L, roots(L, seed))
+    b = game.bucket
+    rng = np.random.default_rng(seed)
+    worker = 3
+    hp = int(game.columns["hit_points"][worker])
+    walls = game.terrain.reshape(-1)
+    for l in range(L):
+        em = st["entity_at"][l].reshape(-1)
+        cells = rng.permutation(np.flatnonzero((em == -1) & ~walls))[:units0 + units1]
+        for k, cell in enumerate(cells):
+            player = 0 if k < units0 else 1
+            start = b.neutral_capacity + player * b.per_player_capacity
+            slot = start + int(np.flatnonzero(st["birth"][l, start:start + b.per_player_capacity] == -1)[0])
+            birth = int(st["next_birth"][l])
+            st["next_birth"][l] = birth + 1
+            st["birth"][l, slot], st["unit_type"][l, slot], st["owner"][l, slot] = birth, worker, player
+            st["cell"][l, slot], st["hit_points"][l, slot] = cell, hp
+            em[cell] = slot
+    return st
+
+
+def test_crowded_rollout_takes_the_general_admission(oracle_threads):
+    """With more than 64 available units a cycle's requests do not fit one
+    wave, and the fused rollout admits them request by request.  The
+    rollout's own count shows that path ran in every game, and the result
+    matches the oracle."""
+    from oracle.oracle import Oracle
+
+    print("crowded rollout", flush=True)
+    game, partial = game_for("gow-alternating")
+    L, steps = 8, 24
+    st = _crowded(game, L)
+    oracle = Oracle(game)
+    assert (oracle.violations(st) == 0).all()
+    assert ((st["birth"][:, game.bucket.neutral_capacity:] != -1).sum(1) > 64).all()
+    env = _env(game, partial)
+    dev = to_device(env, st)
+    got = env.rollout(dev, steps, (2, 7), record=True, count_general=True)
+    want = oracle.rollout(st, (2, 7), 0, steps, partial, threads=oracle_threads)
+    general = got["general_admissions"].cpu().numpy()
+    assert (general >= 1).all(), general
+    np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
+    np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
+    assert_states_equal(st, to_host(dev), "crowded rollout")
+    # an ordinary start never leaves the one-wave admission
+    plain = _env(game, partial)
+    fresh = to_device(plain, _crowded(game, L, units0=0, units1=0))
+    quiet = plain.rollout(fresh, 4, (2, 7), record=False, count_general=True)
+    assert (quiet["general_admissions"].cpu().numpy() == 0).all()
+
+
+def test_crowded_env_step_per_call(oracle_threads):
+    """env.step on the same crowded states, cycle by cycle, against the oracle."""
+    import torch
+
+    from oracle.oracle import Oracle
+
+    print("crowded env.step", flush=True)
+    game, partial = game_for("gow-alternating")
+    L = 8
+    st = _crowded(game, L, seed=6)
+    oracle = Oracle(game)
+    env = _env(game, partial)
+    dev = to_device(env, st)
+    for t in range(6):
+        words = env.get_avail_actions(dev, form="words")
+        acts = env.sample_actions(torch.stack([words[a] for a in env.agents], 1), (4, 4), t)
+        obs, dev, rewards, dones, infos = env.step(None, dev, acts, donate=True)
+        want = oracle.env_step(st, np.stack([acts[a].cpu().numpy() for a in env.agents], 1), partial)
+        assert_states_equal(st, to_host(dev), f"crowded cycle {t}")
+        for i, agent in enumerate(env.agents):
+            np.testing.assert_array_equal(obs[agent].feature_maps.cpu().numpy(), want["feature_maps"][:, i])

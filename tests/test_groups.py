@@ -44,7 +44,7 @@ def _call(lib, devs, template, L=2):
     key_lanes = (ctypes.c_int64 * max(G, 1))(*([1] * G))
     cmds = (native.Commands * max(G, 1))(*([native.Commands(*([buf.data_ptr()] * 6))] * G))
     outs = (native.StepResults * max(G, 1))(*([native.StepResults()] * G))
-    return lib.nanorts_step_groups(None, G, games, states, lanes, keys, key_lanes, cmds, outs)
+    return lib.nanorts_amd_step_groups(None, G, games, states, lanes, keys, key_lanes, cmds, outs)
 
 
 def test_the_library_refuses_groups_that_disagree():
@@ -54,5 +54,5 @@ def test_the_library_refuses_groups_that_disagree():
     da, dc, dd = DeviceGame(a, cpu), DeviceGame(c, cpu), DeviceGame(d, cpu)
     for devs, words in (([da, dc], "unit table"), ([da, dd], "bucket"), ([], "groups"), ([da] * 17, "groups")):
         assert _call(lib, devs, da) != 0
-        assert words in lib.nanorts_last_error().decode()
+        assert words in lib.nanorts_amd_last_error().decode()
     np.testing.assert_equal(groups.MAX_GROUPS, 16)

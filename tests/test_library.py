@@ -6,6 +6,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import pytest
+
 from nanorts_amd import build, native
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -28,10 +30,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_build_id_and_targets():
     lib = native.load()
-    assert lib.nanorts_build_id().decode() == build.source_digest()
-    targets = lib.nanorts_targets().decode().split(",")
-    for target in ("nanorts_step", "nanorts_legality", "nanorts_legality_words", "nanorts_visible_cells",
-                   "nanorts_reset_where_done"):
+    assert lib.nanorts_amd_build_id().decode() == build.source_digest()
+    targets = lib.nanorts_amd_entries().decode().split(",")
+    for target in ("nanorts_amd_step", "nanorts_amd_legality", "nanorts_amd_legality_words", "nanorts_amd_visible_cells",
+                   "nanorts_amd_reset_where_done"):
         assert target in targets
 
 
@@ -39,15 +41,15 @@ def test_invalid_game_is_refused_without_touching_a_device():
     lib = native.load()
     game = native.Game()
     game.height, game.width, game.cells = 4, 4, 17  # inconsistent
-    code = lib.nanorts_legality_words(None, ctypes.byref(game), native.State(), 1, None)
+    code = lib.nanorts_amd_legality_words(None, ctypes.byref(game), native.State(), 1, None)
     assert code == 1
-    assert "cells" in lib.nanorts_last_error().decode()
+    assert "cells" in lib.nanorts_amd_last_error().decode()
 
 
 def test_targets_name_every_compute_entry_point():
     lib = native.load()
-    targets = set(lib.nanorts_targets().decode().split(","))
-    meta = {"nanorts_build_id", "nanorts_targets", "nanorts_last_error", "nanorts_shared_opt_in", "nanorts_self_check"}
+    targets = set(lib.nanorts_amd_entries().decode().split(","))
+    meta = {"nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in", "nanorts_amd_self_check"}
     assert targets == set(declared_entry_points()) - meta
 
 
@@ -61,16 +63,65 @@ def test_seat_entry_points_refuse_bad_arguments_without_touching_a_device():
     carry = native.AbstractActions(*[addr] * len(native.ABSTRACT_FIELDS))
     results = native.EnvResults()
     game = native.Game()
-    code = lib.nanorts_seat_step_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, carry, addr, 0, results)
-    assert code == 1 and "seats is NULL" in lib.nanorts_last_error().decode()
-    code = lib.nanorts_seat_step(None, ctypes.byref(game), state, 1, 0, 4, 2, carry, addr, 0, results)
-    assert code == 1 and "learner must be 0 or 1" in lib.nanorts_last_error().decode()
+    code = lib.nanorts_amd_seat_step_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, carry, addr, 0, results)
+    assert code == 1 and "seats is NULL" in lib.nanorts_amd_last_error().decode()
+    code = lib.nanorts_amd_seat_step(None, ctypes.byref(game), state, 1, 0, 4, 2, carry, addr, 0, results)
+    assert code == 1 and "learner must be 0 or 1" in lib.nanorts_amd_last_error().decode()
     key = (ctypes.c_uint32 * 2)(1, 2)
-    code = lib.nanorts_seat_rollout_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, None, carry, key, 0, 1,
+    code = lib.nanorts_amd_seat_rollout_lanes(None, ctypes.byref(game), state, 1, 0, 4, None, 1, None, carry, key, 0, 1,
                                           0, 0, native.RolloutResults())
-    assert code == 1 and "seats is NULL" in lib.nanorts_last_error().decode()
-    code = lib.nanorts_episode_seats(None, None, addr, 1, addr)
-    assert code == 1 and "NULL" in lib.nanorts_last_error().decode()
-    code = lib.nanorts_episode_seats(None, addr, addr, -1, addr)
-    assert code == 1 and "lanes" in lib.nanorts_last_error().decode()
-    assert lib.nanorts_episode_seats(None, addr, addr, 0, addr) == 0
+    assert code == 1 and "seats is NULL" in lib.nanorts_amd_last_error().decode()
+    code = lib.nanorts_amd_episode_seats(None, None, addr, 1, addr)
+    assert code == 1 and "NULL" in lib.nanorts_amd_last_error().decode()
+    code = lib.nanorts_amd_episode_seats(None, addr, addr, -1, addr)
+    assert code == 1 and "lanes" in lib.nanorts_amd_last_error().decode()
+    assert lib.nanorts_amd_episode_seats(None, addr, addr, 0, addr) == 0
+
+
+# The reference's own C-ABI names: its registry functions
+# (src/nanorts/kernels/cuda/registry.cu:201-230) and its XLA FFI targets.  An
+# FFI shim defines these; the kernel library must not, or the two collide.
+REFERENCE_SYMBOLS = ("nanorts_build_id", "nanorts_targets", "nanorts_shared_opt_in", "nanorts_self_check",
+                     "nanorts_step", "nanorts_step_groups", "nanorts_legality", "nanorts_legality_words",
+                     "nanorts_visible_cells", "nanorts_reset_where_done", "nanorts_reset_packed_where_done",
+                     "nanorts_abstraction_act", "nanorts_gridnet_decode")
+
+
+def test_library_exports_no_reference_symbol():
+    lib = ctypes.CDLL(str(build.library_path()))
+    for name in REFERENCE_SYMBOLS:
+        assert not hasattr(lib, name), name
+
+
+def test_load_refuses_a_library_built_from_other_sources(monkeypatch):
+    monkeypatch.setattr(native, "_LIBRARY", None)
+    monkeypatch.setattr(native._build, "source_digest", lambda: "0" * 16)
+    with pytest.raises(RuntimeError, match="rebuild"):
+        native.load()
+
+
+def test_step_ffi_refuses_bad_arguments_without_touching_a_device():
+    """nanorts_amd_step_ffi validates its operand and result lists, extents
+    and strategy before any copy or launch."""
+    lib = native.load()
+    buf = (ctypes.c_uint8 * 64)()
+    addr = ctypes.cast(buf, ctypes.c_void_p).value
+    operands = (ctypes.c_void_p * 33)(*[addr] * 33)
+    results = (ctypes.c_void_p * 31)(*[addr] * 31)
+    ok = dict(lanes=4, key_lanes=1, command_lanes=4, height=8, width=8, neutral=2, capacity=47, types=7, offsets=49,
+              strategy=0)
+
+    def call(ops=operands, rets=results, **kw):
+        a = {**ok, **kw}
+        return lib.nanorts_amd_step_ffi(None, ops, rets, a["lanes"], a["key_lanes"], a["command_lanes"], a["height"],
+                                        a["width"], a["neutral"], a["capacity"], a["types"], a["offsets"],
+                                        a["strategy"])
+
+    assert call(strategy=3) == 1 and "strategy" in lib.nanorts_amd_last_error().decode()
+    assert call(key_lanes=2) == 1 and "key" in lib.nanorts_amd_last_error().decode()
+    assert call(command_lanes=3) == 1 and "Commands" in lib.nanorts_amd_last_error().decode()
+    holes = (ctypes.c_void_p * 33)(*[addr] * 33)
+    holes[8] = None  # the table operand
+    assert call(ops=holes) == 1 and "operand 8" in lib.nanorts_amd_last_error().decode()
+    assert call(offsets=48) == 1 and "odd square" in lib.nanorts_amd_last_error().decode()
+    assert call(ops=None) == 1
