@@ -217,6 +217,16 @@ int64_t nanorts_amd_shared_opt_in(const int32_t* devices, int64_t n);
  * Replaces src/nanorts/kernels/cuda/registry.cu:174-183 (nanorts_self_check). */
 const char* nanorts_amd_self_check(const int32_t* devices, int64_t n);
 
+/* The self check without a device allocation, for callers that cannot
+ * allocate (code under graph capture, serving loops).  No counterpart in the
+ * reference.  Runs `waves` probe waves (1..1024; more is refused with a
+ * message) on each listed device and returns "" when every wave passes;
+ * probe_words (host int32[waves], or NULL) receives the last device's probe
+ * words, 1 per passing wave.  The words live in a 4 KiB array of the
+ * library's own that every device holds until the process ends; calls that
+ * overlap on one device race on it. */
+const char* nanorts_amd_self_check_no_alloc(const int32_t* devices, int64_t n, int32_t waves, int32_t* probe_words);
+
 /* core.step: Java admission order, durative timers, conflict resolution,
  * completion in pending order, outcome.  State leaves are updated in place.
  * `key` is [key_lanes][2] episode-root key data (key_lanes 1 broadcasts).

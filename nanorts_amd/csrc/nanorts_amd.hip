@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1557,8 +1558,15 @@ __global__ void k_probe(int32_t* out) {
     const int32_t mn = wave_inclusive_min(100 - lane, lane);
     const bool ok = popc(m) == 22 && below == (lane + 2) / 3 && (lane == 0 || up == lane - 1) && mn == 100 - lane;
     const uint64_t all = ballot(ok);
-    if (lane == 0) out[0] = all == ~0ull ? 1 : 0;
+    if (lane == 0) out[blockIdx.x] = all == ~0ull ? 1 : 0;  // one word per probe wave (block of 64)
 }
+
+// Probe words of nanorts_amd_self_check_no_alloc: one per probe wave, in a
+// file-scope array each device holds until the process ends, so that check
+// allocates no device memory.  Host code reaches it only through the address
+// hipGetSymbolAddress returns on each device (probe_scratch below).
+constexpr int32_t kProbeScratchWords = 1024;
+static __device__ __align__(256) int32_t scratch[kProbeScratchWords];
 
 // Host threefry2x32 (20 rounds) and fold_in(k, d) = threefry(k, (0, d)), the
 // same published Random123 cipher the kernels evaluate.
@@ -1643,6 +1651,90 @@ const char* nanorts_amd_self_check(const int32_t* devices, int64_t n) {
             result = "wave64 probe failed on device " + std::to_string(devices[i]);
             break;
         }
+    }
+    (void)hipSetDevice(current);
+    return result.c_str();
+}
+
+}  // extern "C"
+
+namespace {
+std::mutex g_scratch_mutex;
+std::vector<int32_t*> g_scratch_address;  // per device ordinal
+
+// The device address of `scratch` on `device`, which must be current: taken
+// with hipGetSymbolAddress on the first call for that device and kept.
+bool probe_scratch(int device, int32_t** address, std::string* why) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (device < 0) {
+        *why = "no current device";
+        return false;
+    }
+    if ((int)g_scratch_address.size() <= device) g_scratch_address.resize((size_t)device + 1, nullptr);
+    if (!g_scratch_address[(size_t)device]) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p) {
+            *why = std::string("hipGetSymbolAddress of the probe scratch failed: ") + hipGetErrorString(err);
+            return false;
+        }
+        g_scratch_address[(size_t)device] = (int32_t*)p;
+    }
+    *address = g_scratch_address[(size_t)device];
+    return true;
+}
+}  // namespace
+
+extern "C" {
+
+const char* nanorts_amd_self_check_no_alloc(const int32_t* devices, int64_t n, int32_t waves, int32_t* probe_words) {
+    static thread_local std::string result;
+    static thread_local int32_t words[kProbeScratchWords];
+    result.clear();
+    if (waves < 1 || waves > kProbeScratchWords) {
+        result = "waves is " + std::to_string(waves) + "; the probe scratch holds 1 to " +
+                 std::to_string(kProbeScratchWords) + " waves";
+        return result.c_str();
+    }
+    if (n > 0 && !devices) {
+        result = "devices is NULL";
+        return result.c_str();
+    }
+    int current = 0;
+    (void)hipGetDevice(&current);
+    for (int64_t i = 0; i < n; ++i) {
+        if (hipSetDevice(devices[i]) != hipSuccess) {
+            result = "cannot select device " + std::to_string(devices[i]);
+            break;
+        }
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, devices[i]) != hipSuccess || prop.warpSize != 64) {
+            result = "device " + std::to_string(devices[i]) + " does not run 64-wide wavefronts";
+            break;
+        }
+        int32_t* address = nullptr;
+        std::string why;
+        if (!probe_scratch(devices[i], &address, &why)) {
+            result = why;
+            break;
+        }
+        // the scratch keeps the last call's words: clear the ones this call reads
+        hipLaunchKernelGGL(k_zero_bytes, dim3(1), dim3(256), 0, nullptr, (uint8_t*)address, (int64_t)waves * 4);
+        hipLaunchKernelGGL(k_probe, dim3((unsigned)waves), dim3(64), 0, nullptr, address);
+        if (hipGetLastError() != hipSuccess ||
+            hipMemcpy(words, address, sizeof(int32_t) * (size_t)waves, hipMemcpyDeviceToHost) != hipSuccess) {
+            result = "the probe launch or its read-back failed on device " + std::to_string(devices[i]);
+            break;
+        }
+        if (probe_words) std::memcpy(probe_words, words, sizeof(int32_t) * (size_t)waves);
+        for (int32_t w = 0; w < waves; ++w) {
+            if (words[w] != 1) {
+                result = "wave64 probe failed on device " + std::to_string(devices[i]) + " (wave " +
+                         std::to_string(w) + ")";
+                break;
+            }
+        }
+        if (!result.empty()) break;
     }
     (void)hipSetDevice(current);
     return result.c_str();

@@ -49,7 +49,8 @@ def test_invalid_game_is_refused_without_touching_a_device():
 def test_targets_name_every_compute_entry_point():
     lib = native.load()
     targets = set(lib.nanorts_amd_entries().decode().split(","))
-    meta = {"nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in", "nanorts_amd_self_check"}
+    meta = {"nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in",
+            "nanorts_amd_self_check", "nanorts_amd_self_check_no_alloc"}
     assert targets == set(declared_entry_points()) - meta
 
 
@@ -125,3 +126,11 @@ def test_step_ffi_refuses_bad_arguments_without_touching_a_device():
     assert call(ops=holes) == 1 and "operand 8" in lib.nanorts_amd_last_error().decode()
     assert call(offsets=48) == 1 and "odd square" in lib.nanorts_amd_last_error().decode()
     assert call(ops=None) == 1
+
+
+def test_no_alloc_self_check_refuses_sizes_beyond_its_scratch():
+    lib = native.load()
+    device = (ctypes.c_int32 * 1)(0)
+    for waves in (0, 1025, -1):
+        message = lib.nanorts_amd_self_check_no_alloc(device, 1, waves, None).decode()
+        assert "1 to 1024" in message, message
