@@ -49,6 +49,7 @@ enum : int {
     F_SIGHT,
     F_FLAGS,
     F_PRODUCES,
+    F_PACK,  // flags | produces << 8 | attack range << 16: one read for the legality rows
     F_COUNT
 };
 enum : int { FL_RESOURCE = 1, FL_STOCKPILE = 2, FL_HARVEST = 4, FL_MOVE = 8, FL_ATTACK = 16 };
@@ -93,6 +94,7 @@ struct Layout {
     int32_t env_bytes;  // one wave's block, 16-byte multiple
     int32_t o_terrain;  // in the header
     int32_t o_disk;     // in the header: sight-disk row masks [R + 1][2R + 1]
+    int32_t o_walls;    // in the header: wall bitmap rows [H][seen_words] (fast_obs layouts)
     int32_t o_birth, o_carried, o_pnone, o_pissued, o_pcompl, o_porder;
     int32_t o_cell, o_hp, o_ptarget, o_entity;
     int32_t o_utype, o_owner, o_pkind, o_pdir, o_pptype;
@@ -234,6 +236,7 @@ struct Hdr {
     AS3 uint8_t* terrain;
     AS3 Seg* seg;
     AS3 uint32_t* disk;
+    AS3 uint32_t* walls;
 };
 
 struct Env {
@@ -340,11 +343,16 @@ NR_DEV int32_t ref_table_entry(const KGame& g, int field, int32_t t) {
     }
 }
 
+NR_DEV int32_t table_entry(const KGame& g, int field, int32_t t) {
+    return g.ref_table ? ref_table_entry(g, field, t) : g.tab[field * 8 + t];
+}
+
 NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
-    if (g.ref_table) {
-        for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = ref_table_entry(g, i >> 3, i & 7);
-    } else {
-        for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) h.tab[i] = g.tab[i];
+    for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) {
+        const int field = i >> 3, t = i & 7;
+        h.tab[i] = field == F_PACK ? (table_entry(g, F_FLAGS, t) & 0xFF) | ((table_entry(g, F_PRODUCES, t) & 0xFF) << 8) |
+                                         (table_entry(g, F_RANGE, t) << 16)
+                                   : table_entry(g, field, t);
     }
     if (threadIdx.x == 0) {
 #pragma unroll
@@ -356,6 +364,13 @@ NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
     }
     for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = terrain[i] ? 1 : 0;
     if (g.fast_obs) {
+        // the walls as bitmap rows, the blocked plane every cycle starts from
+        for (int i = threadIdx.x; i < g.H * g.seen_words; i += blockDim.x) {
+            const int32_t row = i / g.seen_words, x0 = 32 * (i - row * g.seen_words);
+            uint32_t bits = 0u;
+            for (int32_t b = 0; b < 32 && x0 + b < g.W; ++b) bits |= (terrain[row * g.W + x0 + b] ? 1u : 0u) << b;
+            h.walls[i] = bits;
+        }
         // disk[r][dy + R]: bits R - w .. R + w with w = floor(sqrt(r^2 - dy^2)),
         // 0 when |dy| > r (R = disk_r <= 15)
         const int32_t R = g.disk_r, span = 2 * R + 1;

@@ -163,7 +163,8 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_seg = F_COUNT * 8 * 4;
     y.o_terrain = y.o_seg + 16 * (int32_t)sizeof(Seg);
     y.o_disk = align16(y.o_terrain + cells);
-    y.hdr_bytes = align16(y.o_disk + (g.fast_obs ? (g.disk_r + 1) * (2 * g.disk_r + 1) * 4 : 0));
+    y.o_walls = align16(y.o_disk + (g.fast_obs ? (g.disk_r + 1) * (2 * g.disk_r + 1) * 4 : 0));
+    y.hdr_bytes = align16(y.o_walls + (g.fast_obs ? g.H * g.seen_words * 4 : 0));
     int32_t o = 0;
     auto take = [&o](int32_t bytes) {
         const int32_t at = o;
@@ -293,6 +294,7 @@ bool shape_for_reader(const nanorts_game* game, bool masks, Shape* out, std::str
     y.o_seg = full.o_seg;
     y.o_terrain = full.o_terrain;
     y.o_disk = full.o_disk;
+    y.o_walls = full.o_walls;
     int32_t o = 0;
     auto take = [&o](int32_t bytes) {
         const int32_t at = o;
@@ -448,6 +450,7 @@ bool state_complete(const nanorts_state& s) {
     hdr.terrain = lds + g.lay.o_terrain;                                          \
     hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);                                      \
     hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);                               \
+    hdr.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);                             \
     load_header(g, hdr);                                                          \
     __syncthreads();                                                              \
     const int lane = lane_id();                                                   \
@@ -570,6 +573,7 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
     hdr.terrain = lds + g.lay.o_terrain;
     hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);
     hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);
+    hdr.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);
     load_header(g, hdr, sl.terrain);
     __syncthreads();
     const int lane = lane_id();
@@ -606,6 +610,7 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
 NR_DEV void stage_words(const KGame& g, const Hdr& h, const Env& e, int lane, bool merge) {
     build_bitmaps(g, h, e, lane);
     const bool narrow = g.fast_obs && g.seen_words == 1;
+    const Affordable aff = affordable_types(g, h, e, lane);
     AS3 uint32_t* words = at<uint32_t>(e, g.lay.v_words);
     for (int32_t p = lane; p < 2 * g.C; p += kWave) {
         const int32_t s = g.N + p;
@@ -615,7 +620,7 @@ NR_DEV void stage_words(const KGame& g, const Hdr& h, const Env& e, int lane, bo
             r.w[0] = 1u;
             r.w[1] = r.w[2] = 0u;
         } else {
-            r = narrow ? legality_row_w1(g, h, e, s) : legality_row_bm(g, h, e, s);
+            r = narrow ? legality_row_w1(g, h, e, s, aff) : legality_row_bm(g, h, e, s);
         }
         words[3 * p] = r.w[0];
         words[3 * p + 1] = r.w[1];
@@ -748,7 +753,7 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
     if (fast) {
         // lists of the summary, then decode straight into the admission's
         // request registers (no staging through the command arrays)
-        summarize_slots(g, hdr, e, lane);
+        summarize_slots(g, hdr, e, lane, false);
         const int32_t n = uni(e.sc[S_NAV]);
         int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
         fused = uni(e.sc[S_IRREG]) == 0 && n <= kWave && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
@@ -987,6 +992,7 @@ NR_DEV Hdr header_view(const KGame& g) {
     h.terrain = lds + g.lay.o_terrain;
     h.seg = (AS3 Seg*)(lds + g.lay.o_seg);
     h.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);
+    h.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);
     return h;
 }
 NR_DEV Env wave_env(const KGame& g, int wave) {
@@ -1045,6 +1051,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             // on two lanes at once; otherwise each lane computes both
             const bool paired = n <= kWave / 2;
             const bool narrow = fast && g.seen_words == 1;
+            const Affordable aff = affordable_types(g, hdr, e, lane);
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired) {
                 const int32_t u = lane >> 1;
@@ -1058,7 +1065,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             }
             for (int32_t i = lane; i < n; i += kWave) {
                 const int32_t p = av[i];
-                const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p) : legality_row_bm(g, hdr, e, g.N + p);
+                const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p, aff) : legality_row_bm(g, hdr, e, g.N + p);
                 uint32_t words[4];
                 if (paired) {
                     words[0] = pw0;

@@ -146,7 +146,21 @@ NR_DEV void sample_decode8(const KGame& g, const Env& e, int32_t p, const Row& r
 // legality_row_bm for boards of at most 32 columns (one bitmap word per
 // row) with the disk table: the four neighbours and the attack window come
 // from whole-row words.  Same bits as legality_row_bm.
-NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t slot) {
+// The unit types each player can afford at its current balance, bit t for
+// type t (the produce factor's validity, N/core/kinds/produce.py:25-35):
+// one compare per type on the first lanes, wave-uniform results.
+struct Affordable {
+    uint32_t player[2];
+};
+NR_DEV Affordable affordable_types(const KGame& g, const Hdr& h, const Env& e, int lane) {
+    const int32_t cost = lane < g.T ? tabv(h, F_COST, lane) : 0x7fffffff;
+    Affordable a;
+    a.player[0] = (uint32_t)ballot(lane < g.T && uni(e.sc[S_RES0]) >= cost);
+    a.player[1] = (uint32_t)ballot(lane < g.T && uni(e.sc[S_RES1]) >= cost);
+    return a;
+}
+
+NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t slot, const Affordable& aff) {
     Row r;
     r.w[0] = r.w[1] = r.w[2] = 0u;
     if (e.birth[slot] == kAbsent) return r;
@@ -155,12 +169,9 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
     const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
     const int32_t carried = e.carried[slot];
     const int32_t cell = e.cell[slot];
-    const int32_t flags = tabv(h, F_FLAGS, actor);
-    const int32_t balance = e.sc[S_RES0 + owner];
-    uint32_t affordable = 0u;
-    for (int32_t t = 0; t < g.T; ++t)
-        if (balance >= tabv(h, F_COST, t)) affordable |= 1u << t;
-    const uint32_t types = (uint32_t)tabv(h, F_PRODUCES, actor) & affordable;
+    const int32_t info = tabv(h, F_PACK, actor);
+    const int32_t flags = info & 0xFF;
+    const uint32_t types = ((uint32_t)info >> 8) & 0xFFu & (owner ? aff.player[1] : aff.player[0]);
     const int32_t x = cell_x(g, cell), yy = cell_y(g, cell);
     const int32_t H = g.H;
     AS3 const uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
@@ -203,7 +214,7 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
     r.w[0] |= ((r.w[0] >> 14) & 15u ? 1u : 0u) << kKindReturn;
     r.w[0] |= (produce_types ? 1u : 0u) << kKindProduce;
     if (flags & FL_ATTACK) {
-        const int32_t range = tabv(h, F_RANGE, actor);
+        const int32_t range = info >> 16;
         const int32_t reach = imin(range, g.radius);
         AS3 const uint32_t* enemy = bm + (2 - owner) * H;
         uint64_t att = 0;
@@ -242,10 +253,19 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
     return r;
 }
 
-// Pass over the slots: occupant words, available list, unit list.
-NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+// Pass over the slots: occupant words, available list, unit list, and (with
+// `bitmaps`) the six occupancy bitmaps of the next cycle's masks, stamped per
+// live slot over the wall rows: 0 blocked (occupied or wall), 1 / 2 units of
+// player 0 / 1, 3 resources, 4 / 5 stockpiles of player 0 / 1.
+NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
+    const int32_t words = g.seen_words, plane = g.H * words;
+    AS3 uint32_t* bm = at<uint32_t>(e, y.o_bm);
+    if (bitmaps) {
+        for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = i < plane ? h.walls[i] : 0u;
+        wave_sync();
+    }
     AS3 uint32_t* olo = at<uint32_t>(e, y.o_lo);
     AS3 uint8_t* ofl = at<uint8_t>(e, y.o_fl);
     AS3 int16_t* av = at<int16_t>(e, y.a_av);
@@ -290,8 +310,18 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
                          (((uint32_t)(ty + 1) & 0xFFu) << 24);
                 const int32_t fl = tabv(h, F_FLAGS, clampi(ty, 0, g.T - 1));
                 const uint32_t stk = (fl & FL_STOCKPILE) ? 1u : 0u;
-                ofl[s] = (uint8_t)(1u | (rel0 << 1) | ((fl & FL_RESOURCE) ? 8u : 0u) | ((stk & (rel0 & 1u)) << 4) |
-                                   ((stk & (rel0 >> 1)) << 5));
+                const uint32_t planes = 1u | (rel0 << 1) | ((fl & FL_RESOURCE) ? 8u : 0u) | ((stk & (rel0 & 1u)) << 4) |
+                                        ((stk & (rel0 >> 1)) << 5);
+                ofl[s] = (uint8_t)planes;
+                if (bitmaps) {
+                    const int32_t c = e.cell[s];
+                    const int32_t cy = cell_y(g, c), cx = c - cy * g.W;
+                    AS3 uint32_t* at_ = bm + cy * words + (cx >> 5);
+                    const uint32_t bit = 1u << (cx & 31);
+                    // planes is a 6-bit set: stamp each plane it names
+                    for (uint32_t rest = planes; rest != 0u; rest &= rest - 1u)
+                        __atomic_fetch_or(at_ + __builtin_ctz(rest) * plane, bit, __ATOMIC_RELAXED);
+                }
                 available = s >= g.N && pk == kAbsent;
                 if (available && e.porder[s] != kAbsent) odd = true;
             }
@@ -501,7 +531,7 @@ NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool
         summarize_visibility(g, h, e, lane, seen_at, which);
         if (kept_seen >= 0 && lane == 0) e.sc[S_VISDIRTY] = 0;
     }
-    summarize_cells(g, h, e, lane, partial, true, maps0, maps1, seen_at);
+    if (maps0) summarize_cells(g, h, e, lane, partial, false, maps0, maps1, seen_at);
     if (scalars0 && lane < 8) {
         const int32_t pl = lane >> 2, f = lane & 3;
         int32_t v;
