@@ -251,14 +251,20 @@ int nanorts_amd_step(void* stream, const nanorts_game* game, nanorts_state state
  *     27 is_member pred[L][E]; 28 int32 records s32[L][E][6]; 29 index
  *     records s16[L][E][4]; 30 int8 records s8[L][E][6].  The records are
  *     written as no member (all zero): nothing in the reference reads them.
- * key_lanes and command_lanes are 1 (an unbatched operand of extent 1, every
- * lane reads row 0; src/nanorts/kernels/batching.py:63-79) or `lanes`.  Index
- * leaves are int16.  Errors as every entry: NANORTS_INVALID_ARGUMENT for a
+ * Every size argument is an extent of those buffers, so a handler that sees
+ * only the buffers and the `strategy` attribute can pass them: lanes = the
+ * leading extent of result 0; key_lanes and command_lanes = the leading
+ * extents of operands 0 and 1, each 1 (an unbatched operand of extent 1,
+ * every lane reads row 0; src/nanorts/kernels/batching.py:63-79) or `lanes`;
+ * height and width from terrain; capacity = the last extent of operand 1;
+ * neutral = the entity extent of operand 10 minus 2 x capacity; types = the
+ * T extent of table.  The attack window of the legality rows plays no part in
+ * a step.  Index leaves are int16.  Errors as every entry: NANORTS_INVALID_ARGUMENT for a
  * NULL pointer, an extent or a strategy out of range, NANORTS_INTERNAL for a
  * failed launch or copy. */
 int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
                          int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
-                         int32_t capacity, int32_t types, int32_t offsets, int64_t strategy);
+                         int32_t capacity, int32_t types, int64_t strategy);
 
 /* core.step over up to 16 groups of lanes, in one launch per 4 groups.  The
  * groups' games share one bucket (extents, capacities, unit types, attack
@@ -282,6 +288,25 @@ int nanorts_amd_legality(void* stream, const nanorts_game* game, nanorts_state s
 int nanorts_amd_legality_words(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            uint32_t* words);
 
+/* Legality rows or words in the operand order of the reference's FFI targets
+ * nanorts_legality and nanorts_legality_words
+ * (src/nanorts/core/cuda/legality.cu:535-561, operands built by
+ * src/nanorts/core/legality.py:84-125): the body a handler of either name
+ * calls with its buffers' device pointers.
+ *   operands[9]: birth s32[L][E], unit_type s8[L][E], owner s8[L][E],
+ *     carried_resources s32[L][E], cell s16[L][E], entity_at s16[L][H][W],
+ *     player_resources s32[L][2], terrain pred[1][H][W], table s32[1][T][7+T].
+ *   result: rows bool[L][2][C][22+T+offsets] (words = 0) or uint32[L][2][C][3]
+ *     (words = 1).
+ * The sizes are extents: lanes = the result's leading extent; height and
+ * width of entity_at; entities = birth's second extent; capacity = the
+ * result's third extent; types = the table's second extent; offsets = the
+ * rows' last extent - 22 - T, or the words target's `offsets` attribute.
+ * Leaves hold one row per lane; terrain and table one shared row. */
+int nanorts_amd_legality_ffi(void* stream, const void* const* operands, void* result, int32_t words, int64_t lanes,
+                             int32_t height, int32_t width, int32_t entities, int32_t capacity, int32_t types,
+                             int32_t offsets);
+
 /* get_avail_actions masks: rows & available, only NONE on unavailable rows
  * (src/nanorts/adapters/jaxmarl/actions.py:28-41), as bool rows and/or words. */
 int nanorts_amd_avail_actions(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
@@ -291,6 +316,21 @@ int nanorts_amd_avail_actions(void* stream, const nanorts_game* game, nanorts_st
  * nanorts_visible_cells (src/nanorts/observations/cuda/visibility.cu:86-138). */
 int nanorts_amd_visible_cells(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                           int32_t observer, uint8_t* cells);
+
+/* Sight of one slot block in the operand order of the reference's FFI target
+ * nanorts_visible_cells (src/nanorts/observations/cuda/visibility.cu:86-158,
+ * called from src/nanorts/observations/visibility.py:85-103): every slot of
+ * [first, first + count) whose birth is not -1 and whose cell and type are in
+ * range marks the cells within radius[type] (dx^2 + dy^2 <= r^2) of its cell.
+ * birth s32, unit_type s8 and cell (cell_bytes = 1, 2 or 4) hold `slots`
+ * elements per row and one row per lane or one shared row (*_lanes = 1);
+ * radius s32[types] is shared; out bool[lanes][height][width]; the board is
+ * at most 48K cells.  The attributes first, count, width and height are the
+ * target's own. */
+int nanorts_amd_visible_cells_ffi(void* stream, const int32_t* birth, int64_t birth_lanes, const int8_t* unit_type,
+                                  int64_t unit_type_lanes, const void* cell, int32_t cell_bytes, int64_t cell_lanes,
+                                  int64_t slots, const int32_t* radius, int64_t types, uint8_t* out, int64_t lanes,
+                                  int64_t first, int64_t count, int32_t width, int32_t height);
 
 /* Symbolic uint8 observations of both agents
  * (src/nanorts/observations/symbolic.py:130-180). */
@@ -316,6 +356,19 @@ int nanorts_amd_pixels_from_maps(void* stream, const nanorts_game* game, int64_t
  * (src/nanorts/adapters/cuda/reset.cu:160-222). */
 int nanorts_amd_reset_where_done(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                              const uint8_t* done);
+
+/* The masked row select of the reference's FFI targets
+ * nanorts_reset_where_done and nanorts_reset_packed_where_done
+ * (src/nanorts/adapters/cuda/reset.cu:160-246, called from
+ * src/nanorts/adapters/lifecycle.py:108-134): for each of `leaves` (at most
+ * 32) row leaves, results[k] row l = done[l] ? reset_rows[k] row (l, or 0
+ * when reset_lanes[k] = 1) : ending[k] row l, rows of row_bytes[k] bytes.  A
+ * result that aliases its ending rows is written on done lanes only.  The
+ * packed target's handler passes its one shared uint8 row as reset_rows[k] =
+ * packed + each leaf's 16-byte-aligned offset, with reset_lanes[k] = 1. */
+int nanorts_amd_reset_rows_ffi(void* stream, const uint8_t* done, int64_t lanes, int32_t leaves,
+                               const void* const* reset_rows, const int64_t* reset_lanes, const void* const* ending,
+                               void* const* results, const int64_t* row_bytes);
 
 /* env.step of the JaxMARL facade in one launch: decode int32[L][2][C][7]
  * actions, core.step keyed by the episode root, advance (auto-reset) and

@@ -316,21 +316,22 @@ NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field 
 // can_harvest, is_resource, is_stockpile, can_attack, attack_range, cost,
 // produces[T]; timings[t] = move_time, harvest_time, attack_time,
 // produce_time, hit_points, attack_damage, harvest_amount.  The step reads no
-// sight radius, so F_SIGHT is 0.
+// sight radius, so F_SIGHT is 0; the legality targets pass no timings, whose
+// fields are then 0.
 NR_DEV int32_t ref_table_entry(const KGame& g, int field, int32_t t) {
     if (t >= g.T) return 0;
     const int32_t* row = g.ref_table + t * (7 + g.T);
-    const int32_t* time = g.ref_timings + t * 7;
+    const int32_t* time = g.ref_timings ? g.ref_timings + t * 7 : nullptr;
     switch (field) {
         case F_COST: return row[6];
-        case F_HP: return time[4];
-        case F_PRODUCE_TIME: return time[3];
-        case F_MOVE_TIME: return time[0];
-        case F_ATTACK_TIME: return time[2];
-        case F_HARVEST_TIME: return time[1];
+        case F_HP: return time ? time[4] : 0;
+        case F_PRODUCE_TIME: return time ? time[3] : 0;
+        case F_MOVE_TIME: return time ? time[0] : 0;
+        case F_ATTACK_TIME: return time ? time[2] : 0;
+        case F_HARVEST_TIME: return time ? time[1] : 0;
         case F_RANGE: return row[5];
-        case F_DAMAGE: return time[5];
-        case F_AMOUNT: return time[6];
+        case F_DAMAGE: return time ? time[5] : 0;
+        case F_AMOUNT: return time ? time[6] : 0;
         case F_FLAGS:
             return (row[2] ? FL_RESOURCE : 0) | (row[3] ? FL_STOCKPILE : 0) | (row[1] ? FL_HARVEST : 0) |
                    (row[0] ? FL_MOVE : 0) | (row[4] ? FL_ATTACK : 0);

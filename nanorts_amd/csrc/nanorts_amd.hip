@@ -669,6 +669,135 @@ __global__ __launch_bounds__(256) void k_visible(KGame g, int64_t lanes, nanorts
     for (int32_t c = lane; c < g.cells; c += kWave) cells[l * g.cells + c] = seen_at(g, e, c) ? 1 : 0;
 }
 
+// Legality from the operands of the reference's nanorts_legality targets: the
+// seven leaves the rows read (no pending leaf, no scalar but the resources).
+__global__ __launch_bounds__(256) void k_legality_operands(KGame g, int64_t lanes, nanorts_state s, uint8_t* rows,
+                                                           uint32_t* words) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_CARRIED | LD_ENTITY, lane);
+    if (lane < 2) e.sc[S_RES0 + lane] = s.player_resources[2 * l + lane];
+    wave_sync();
+    stage_words(g, hdr, e, lane, false);
+    if (words) copy_out((uint8_t*)(words + l * 2 * g.C * 3), at<uint8_t>(e, g.lay.v_words), 2 * g.C * 12, lane);
+    if (rows) emit_rows(g, e, l, rows, lane);
+}
+
+// Sight of one slot block, from the operands of the reference's
+// nanorts_visible_cells target: per-slot leaves with a row per lane or one
+// shared row (stride 0), a shared radius table, any board up to 48K cells.
+struct VisibleArgs {
+    const int32_t* birth;
+    const int8_t* unit_type;
+    const uint8_t* cell;  // int8, int16 or int32 elements (cell_bytes)
+    const int32_t* radius;
+    uint8_t* out;
+    int64_t birth_stride, type_stride, cell_stride;  // elements per lane
+    int64_t types, lanes, first, count;
+    int32_t width, height, cell_bytes, words;  // words: bitmap words per lane
+};
+
+NR_DEV int64_t cell_element(const uint8_t* base, int32_t bytes, int64_t i) {
+    if (bytes == 1) return ((const int8_t*)base)[i];
+    if (bytes == 2) return ((const int16_t*)base)[i];
+    return ((const int32_t*)base)[i];
+}
+
+// Sets bits [lo, hi] of an LDS bitmap.
+NR_DEV void set_bit_run(AS3 uint32_t* bm, int64_t lo, int64_t hi) {
+    for (int64_t w = lo >> 5; w <= (hi >> 5); ++w) {
+        const int32_t a = w == (lo >> 5) ? (int32_t)(lo & 31) : 0;
+        const int32_t b = w == (hi >> 5) ? (int32_t)(hi & 31) : 31;
+        const uint32_t m = (b == 31 ? 0xFFFFFFFFu : ((2u << b) - 1u)) & ~((1u << a) - 1u);
+        __atomic_fetch_or(&bm[w], m, __ATOMIC_RELAXED);
+    }
+}
+
+// One wave per lane: each lane of the wave takes slots of the block and ORs
+// its disk, row by row as runs of the flat cell bitmap, into LDS; the wave
+// then writes the bitmap out as one bool per cell.
+__global__ __launch_bounds__(256) void k_visible_block(VisibleArgs a) {
+    extern __shared__ __align__(16) uint8_t nr_lds[];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t l = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+    if (l >= a.lanes) return;
+    AS3 uint32_t* bm = (AS3 uint32_t*)nr_lds + (int64_t)wave * a.words;
+    for (int32_t i = lane; i < a.words; i += kWave) bm[i] = 0u;
+    wave_sync();
+    const int64_t cells = (int64_t)a.width * a.height;
+    for (int64_t slot = a.first + lane; slot < a.first + a.count; slot += kWave) {
+        if (a.birth[l * a.birth_stride + slot] == kAbsent) continue;
+        const int64_t c = cell_element(a.cell, a.cell_bytes, l * a.cell_stride + slot);
+        const int64_t t = a.unit_type[l * a.type_stride + slot];
+        if (c < 0 || c >= cells || t < 0 || t >= a.types) continue;
+        const int64_t r = a.radius[t];
+        if (r < 0) continue;
+        const int64_t x = c % a.width, y = c / a.width;
+        const int64_t y0 = y - r < 0 ? 0 : y - r, y1 = y + r > a.height - 1 ? a.height - 1 : y + r;
+        int64_t w = r;  // half-width of the disk's row: the largest w with w^2 + dy^2 <= r^2
+        for (int64_t yy = y0; yy <= y1; ++yy) {
+            const int64_t dy = yy - y, room = r * r - dy * dy;
+            w = r;
+            while (w * w > room) --w;
+            const int64_t x0 = x - w < 0 ? 0 : x - w, x1 = x + w > a.width - 1 ? a.width - 1 : x + w;
+            set_bit_run(bm, yy * a.width + x0, yy * a.width + x1);
+        }
+    }
+    wave_sync();
+    uint8_t* out = a.out + l * cells;
+    const bool packed = ((((uintptr_t)out) | (uintptr_t)cells) & 3u) == 0;
+    if (packed) {
+        for (int64_t q = lane; q < cells / 4; q += kWave) {
+            const uint32_t bits = (bm[q >> 3] >> ((q & 7) * 4)) & 0xFu;
+            ((uint32_t*)out)[q] = (bits & 1u) | ((bits & 2u) << 7) | ((bits & 4u) << 14) | ((bits & 8u) << 21);
+        }
+    } else {
+        for (int64_t c = lane; c < cells; c += kWave) out[c] = (uint8_t)((bm[c >> 5] >> (c & 31)) & 1u);
+    }
+}
+
+// Masked row select of the reference's nanorts_reset_where_done and
+// nanorts_reset_packed_where_done targets: result[k][l] = done[l] ?
+// reset[k][row l, or the shared row] : ending[k][l].  A result that aliases
+// its ending rows is written on done lanes only.  Read through the
+// kernel-argument segment pointer, as the leaf index is a run-time value.
+constexpr int32_t kMaxResetLeaves = 32;
+struct ResetArgs {
+    const uint8_t* done;
+    int64_t lanes;
+    int32_t leaves;
+    const uint8_t* reset[kMaxResetLeaves];
+    int64_t reset_stride[kMaxResetLeaves];  // bytes per lane, 0 for a shared row
+    const uint8_t* ending[kMaxResetLeaves];
+    uint8_t* result[kMaxResetLeaves];
+    int64_t row_bytes[kMaxResetLeaves];
+};
+static_assert(sizeof(ResetArgs) <= 4096, "the reset table must fit the kernel-argument segment");
+typedef const __attribute__((address_space(4))) ResetArgs* ResetArgsArg;
+
+__global__ __launch_bounds__(256) void k_reset_rows(ResetArgs args) {
+    (void)args;
+    ResetArgsArg ap = (ResetArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    const ResetArgs& a = *(const ResetArgs*)ap;
+    const int32_t k = (int32_t)blockIdx.y;
+    const int lane = lane_id();
+    const int64_t l = (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (l >= a.lanes) return;
+    const bool done = a.done[l] != 0;
+    const int64_t rb = a.row_bytes[k];
+    uint8_t* dst = a.result[k] + l * rb;
+    if (!done && a.result[k] == a.ending[k]) return;
+    const uint8_t* src = done ? a.reset[k] + l * a.reset_stride[k] : a.ending[k] + l * rb;
+    const uintptr_t align = (uintptr_t)src | (uintptr_t)dst | (uintptr_t)rb;
+    if ((align & 15u) == 0) {
+        for (int64_t i = lane; i < rb / 16; i += kWave) ((u32x4*)dst)[i] = ((const u32x4*)src)[i];
+    } else if ((align & 3u) == 0) {
+        for (int64_t i = lane; i < rb / 4; i += kWave) ((uint32_t*)dst)[i] = ((const uint32_t*)src)[i];
+    } else {
+        for (int64_t i = lane; i < rb; i += kWave) dst[i] = src[i];
+    }
+}
+
 NR_DEV void observe_both(const KGame& g, const Hdr& h, const Env& e, int64_t slot, int lane, bool partial,
                          uint8_t* maps, int32_t* scalars) {
     const int64_t per = (int64_t)g.cells * 6;
@@ -1608,7 +1737,8 @@ extern "C" {
 const char* nanorts_amd_build_id(void) { return NANORTS_BUILD_ID; }
 
 const char* nanorts_amd_entries(void) {
-    return "nanorts_amd_step,nanorts_amd_step_ffi,nanorts_amd_legality,nanorts_amd_legality_words,nanorts_amd_avail_actions,nanorts_amd_visible_cells,"
+    return "nanorts_amd_step,nanorts_amd_step_ffi,nanorts_amd_legality,nanorts_amd_legality_words,nanorts_amd_legality_ffi,"
+           "nanorts_amd_avail_actions,nanorts_amd_visible_cells,nanorts_amd_visible_cells_ffi,nanorts_amd_reset_rows_ffi,"
            "nanorts_amd_observe,nanorts_amd_pixels,nanorts_amd_pixels_from_maps,nanorts_amd_reset_where_done,nanorts_amd_env_step,nanorts_amd_sample_actions,"
            "nanorts_amd_step_groups,nanorts_amd_env_transition,nanorts_amd_decode_actions,nanorts_amd_rollout,nanorts_amd_abstraction_act,nanorts_amd_seat_step,nanorts_amd_seat_rollout,"
            "nanorts_amd_seat_step_lanes,nanorts_amd_seat_rollout_lanes,nanorts_amd_episode_seats,nanorts_amd_gridnet_decode,"
@@ -1788,7 +1918,7 @@ static int zero_bytes(hipStream_t stream, void* p, int64_t n) {
 
 int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
                          int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
-                         int32_t capacity, int32_t types, int32_t offsets, int64_t strategy) {
+                         int32_t capacity, int32_t types, int64_t strategy) {
     if (!operands || !results) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operands or results is NULL");
     if (strategy < NANORTS_CANCEL_BOTH || strategy > NANORTS_CANCEL_ALTERNATING)
         return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: strategy must be 0, 1 or 2");
@@ -1811,7 +1941,7 @@ int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const*
     game.capacity = capacity;
     game.entities = neutral + 2 * capacity;
     game.types = types;
-    game.offsets = offsets;
+    game.offsets = 1;  // a step decodes no legality rows: one target offset is a valid window
     game.strategy = (int32_t)strategy;
     game.max_cycles = 0x7fffffff;  // truncation is not a result of this target
     game.terrain = (const uint8_t*)operands[7];
@@ -1935,6 +2065,123 @@ int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* co
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
     }
+    return NANORTS_OK;
+}
+
+int nanorts_amd_legality_ffi(void* stream, const void* const* operands, void* result, int32_t words, int64_t lanes,
+                             int32_t height, int32_t width, int32_t entities, int32_t capacity, int32_t types,
+                             int32_t offsets) {
+    if (!operands || !result) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_legality_ffi: operands or result is NULL");
+    for (int i = 0; i < 9; ++i)
+        if (!operands[i])
+            return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_legality_ffi: operand " + std::to_string(i) + " is NULL");
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_legality_ffi: lanes is negative");
+    nanorts_game game;
+    std::memset(&game, 0, sizeof(game));
+    game.height = height;
+    game.width = width;
+    game.cells = height * width;
+    game.capacity = capacity;
+    game.neutral = entities - 2 * capacity;
+    game.entities = entities;
+    game.types = types;
+    game.offsets = offsets;
+    game.max_cycles = 0x7fffffff;
+    game.terrain = (const uint8_t*)operands[7];
+    NR_READER_SHAPE(&game, true)
+    sh.g.ref_table = (const int32_t*)operands[8];
+    nanorts_state s;
+    std::memset(&s, 0, sizeof(s));
+    s.birth = (int32_t*)operands[0];
+    s.unit_type = (int8_t*)operands[1];
+    s.owner = (int8_t*)operands[2];
+    s.carried_resources = (int32_t*)operands[3];
+    s.cell = (int16_t*)operands[4];
+    s.entity_at = (int16_t*)operands[5];
+    s.player_resources = (int32_t*)operands[6];
+    if (words) return launch(k_legality_operands, sh, lanes, (hipStream_t)stream, s, (uint8_t*)nullptr, (uint32_t*)result);
+    return launch(k_legality_operands, sh, lanes, (hipStream_t)stream, s, (uint8_t*)result, (uint32_t*)nullptr);
+}
+
+int nanorts_amd_visible_cells_ffi(void* stream, const int32_t* birth, int64_t birth_lanes, const int8_t* unit_type,
+                                  int64_t unit_type_lanes, const void* cell, int32_t cell_bytes, int64_t cell_lanes,
+                                  int64_t slots, const int32_t* radius, int64_t types, uint8_t* out, int64_t lanes,
+                                  int64_t first, int64_t count, int32_t width, int32_t height) {
+    const std::string who = "nanorts_amd_visible_cells_ffi: ";
+    if (!birth || !unit_type || !cell || !radius || !out) return fail(NANORTS_INVALID_ARGUMENT, who + "a buffer is NULL");
+    if (cell_bytes != 1 && cell_bytes != 2 && cell_bytes != 4)
+        return fail(NANORTS_INVALID_ARGUMENT, who + "cell elements are 1, 2 or 4 bytes");
+    const int64_t cells = (int64_t)width * height;
+    if (width <= 0 || height <= 0 || cells > 48 * 1024)
+        return fail(NANORTS_INVALID_ARGUMENT, who + "the board is 1 to 48K cells");
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, who + "lanes is negative");
+    if (lanes == 0) return NANORTS_OK;
+    const auto shared_or_per_lane = [lanes](int64_t n) { return n == 1 || n == lanes; };
+    if (!shared_or_per_lane(birth_lanes) || !shared_or_per_lane(unit_type_lanes) || !shared_or_per_lane(cell_lanes))
+        return fail(NANORTS_INVALID_ARGUMENT, who + "each per-slot leaf holds a row per lane or one shared row");
+    if (first < 0 || count < 0 || first + count > slots || types <= 0)
+        return fail(NANORTS_INVALID_ARGUMENT, who + "the block lies inside the per-slot rows and the radius table is not empty");
+    VisibleArgs a;
+    a.birth = birth;
+    a.unit_type = unit_type;
+    a.cell = (const uint8_t*)cell;
+    a.radius = radius;
+    a.out = out;
+    a.birth_stride = birth_lanes == 1 ? 0 : slots;
+    a.type_stride = unit_type_lanes == 1 ? 0 : slots;
+    a.cell_stride = cell_lanes == 1 ? 0 : slots;
+    a.types = types;
+    a.lanes = lanes;
+    a.first = first;
+    a.count = count;
+    a.width = width;
+    a.height = height;
+    a.cell_bytes = cell_bytes;
+    a.words = (int32_t)((cells + 31) / 32);
+    const int32_t wpb = 4;
+    const int64_t blocks = (lanes + wpb - 1) / wpb;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, who + "too many lanes for one launch");
+    hipLaunchKernelGGL(k_visible_block, dim3((unsigned)blocks), dim3(kWave * wpb), (size_t)(wpb * a.words * 4),
+                       (hipStream_t)stream, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
+}
+
+int nanorts_amd_reset_rows_ffi(void* stream, const uint8_t* done, int64_t lanes, int32_t leaves,
+                               const void* const* reset_rows, const int64_t* reset_lanes, const void* const* ending,
+                               void* const* results, const int64_t* row_bytes) {
+    const std::string who = "nanorts_amd_reset_rows_ffi: ";
+    if (leaves < 0 || leaves > kMaxResetLeaves)
+        return fail(NANORTS_INVALID_ARGUMENT, who + "leaves is 0 to " + std::to_string(kMaxResetLeaves));
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, who + "lanes is negative");
+    if (leaves == 0 || lanes == 0) return NANORTS_OK;
+    if (!done || !reset_rows || !reset_lanes || !ending || !results || !row_bytes)
+        return fail(NANORTS_INVALID_ARGUMENT, who + "an array is NULL");
+    ResetArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.done = done;
+    a.lanes = lanes;
+    a.leaves = leaves;
+    for (int32_t k = 0; k < leaves; ++k) {
+        if (!reset_rows[k] || !ending[k] || !results[k])
+            return fail(NANORTS_INVALID_ARGUMENT, who + "leaf " + std::to_string(k) + " has a NULL buffer");
+        if (row_bytes[k] < 0) return fail(NANORTS_INVALID_ARGUMENT, who + "a row has negative bytes");
+        if (reset_lanes[k] != 1 && reset_lanes[k] != lanes)
+            return fail(NANORTS_INVALID_ARGUMENT, who + "a reset leaf holds one row per lane or one shared row");
+        a.reset[k] = (const uint8_t*)reset_rows[k];
+        a.reset_stride[k] = reset_lanes[k] == 1 ? 0 : row_bytes[k];
+        a.ending[k] = (const uint8_t*)ending[k];
+        a.result[k] = (uint8_t*)results[k];
+        a.row_bytes[k] = row_bytes[k];
+    }
+    const int32_t wpb = 4;
+    const int64_t blocks = (lanes + wpb - 1) / wpb;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, who + "too many lanes for one launch");
+    hipLaunchKernelGGL(k_reset_rows, dim3((unsigned)blocks, (unsigned)leaves), dim3(kWave * wpb), 0,
+                       (hipStream_t)stream, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
     return NANORTS_OK;
 }
 

@@ -91,6 +91,7 @@ class GridNetResults(ctypes.Structure):
 EXPORTS = (
     "nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in",
     "nanorts_amd_self_check", "nanorts_amd_self_check_no_alloc", "nanorts_amd_step", "nanorts_amd_step_ffi",
+    "nanorts_amd_legality_ffi", "nanorts_amd_visible_cells_ffi", "nanorts_amd_reset_rows_ffi",
     "nanorts_amd_step_groups", "nanorts_amd_env_transition", "nanorts_amd_decode_actions",
     "nanorts_amd_legality", "nanorts_amd_legality_words", "nanorts_amd_avail_actions", "nanorts_amd_visible_cells",
     "nanorts_amd_observe", "nanorts_amd_pixels", "nanorts_amd_pixels_from_maps", "nanorts_amd_reset_where_done", "nanorts_amd_env_step", "nanorts_amd_sample_actions",
@@ -112,7 +113,11 @@ _SIGNATURES = {
     "nanorts_amd_self_check": (ctypes.c_char_p, [_VP, _I64]),
     "nanorts_amd_self_check_no_alloc": (ctypes.c_char_p, [_VP, _I64, _I32, _VP]),
     "nanorts_amd_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I64, Commands, StepResults]),
-    "nanorts_amd_step_ffi": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64]),
+    "nanorts_amd_step_ffi": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I64]),
+    "nanorts_amd_legality_ffi": (ctypes.c_int, [_VP, _VP, _VP, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _I32]),
+    "nanorts_amd_visible_cells_ffi": (ctypes.c_int, [_VP, _VP, _I64, _VP, _I64, _VP, _I32, _I64, _I64, _VP, _I64, _VP,
+                                                     _I64, _I64, _I64, _I32, _I32]),
+    "nanorts_amd_reset_rows_ffi": (ctypes.c_int, [_VP, _VP, _I64, _I32, _VP, _VP, _VP, _VP, _VP]),
     "nanorts_amd_step_groups": (ctypes.c_int, [_VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "nanorts_amd_legality": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),
     "nanorts_amd_legality_words": (ctypes.c_int, [_VP, _GP, State, _I64, _VP]),

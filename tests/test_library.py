@@ -109,14 +109,12 @@ def test_step_ffi_refuses_bad_arguments_without_touching_a_device():
     addr = ctypes.cast(buf, ctypes.c_void_p).value
     operands = (ctypes.c_void_p * 33)(*[addr] * 33)
     results = (ctypes.c_void_p * 31)(*[addr] * 31)
-    ok = dict(lanes=4, key_lanes=1, command_lanes=4, height=8, width=8, neutral=2, capacity=47, types=7, offsets=49,
-              strategy=0)
+    ok = dict(lanes=4, key_lanes=1, command_lanes=4, height=8, width=8, neutral=2, capacity=47, types=7, strategy=0)
 
     def call(ops=operands, rets=results, **kw):
         a = {**ok, **kw}
         return lib.nanorts_amd_step_ffi(None, ops, rets, a["lanes"], a["key_lanes"], a["command_lanes"], a["height"],
-                                        a["width"], a["neutral"], a["capacity"], a["types"], a["offsets"],
-                                        a["strategy"])
+                                        a["width"], a["neutral"], a["capacity"], a["types"], a["strategy"])
 
     assert call(strategy=3) == 1 and "strategy" in lib.nanorts_amd_last_error().decode()
     assert call(key_lanes=2) == 1 and "key" in lib.nanorts_amd_last_error().decode()
@@ -124,7 +122,7 @@ def test_step_ffi_refuses_bad_arguments_without_touching_a_device():
     holes = (ctypes.c_void_p * 33)(*[addr] * 33)
     holes[8] = None  # the table operand
     assert call(ops=holes) == 1 and "operand 8" in lib.nanorts_amd_last_error().decode()
-    assert call(offsets=48) == 1 and "odd square" in lib.nanorts_amd_last_error().decode()
+    assert call(types=9) == 1 and "types" in lib.nanorts_amd_last_error().decode()
     assert call(ops=None) == 1
 
 
@@ -134,3 +132,42 @@ def test_no_alloc_self_check_refuses_sizes_beyond_its_scratch():
     for waves in (0, 1025, -1):
         message = lib.nanorts_amd_self_check_no_alloc(device, 1, waves, None).decode()
         assert "1 to 1024" in message, message
+
+
+def test_operand_entries_refuse_bad_arguments_without_touching_a_device():
+    """The legality, visibility and reset entries in the reference's operand
+    forms validate their buffers and extents before any launch."""
+    lib = native.load()
+    buf = (ctypes.c_uint8 * 64)()
+    addr = ctypes.cast(buf, ctypes.c_void_p).value
+    err = lambda: lib.nanorts_amd_last_error().decode()  # noqa: E731
+
+    nine = (ctypes.c_void_p * 9)(*[addr] * 9)
+    assert lib.nanorts_amd_legality_ffi(None, nine, None, 1, 4, 8, 8, 96, 47, 7, 49) == 1 and "NULL" in err()
+    holes = (ctypes.c_void_p * 9)(*[addr] * 9)
+    holes[8] = None
+    assert lib.nanorts_amd_legality_ffi(None, holes, addr, 1, 4, 8, 8, 96, 47, 7, 49) == 1 and "operand 8" in err()
+    assert lib.nanorts_amd_legality_ffi(None, nine, addr, 1, 4, 8, 8, 96, 47, 7, 48) == 1 and "odd square" in err()
+    assert lib.nanorts_amd_legality_ffi(None, nine, addr, 0, 4, 8, 8, 90, 47, 7, 49) == 1 and "entities" in err()
+
+    def visible(**kw):
+        a = dict(birth=addr, birth_lanes=4, unit_type=addr, unit_type_lanes=1, cell=addr, cell_bytes=2, cell_lanes=4,
+                 slots=16, radius=addr, types=7, out=addr, lanes=4, first=2, count=7, width=8, height=8)
+        a.update(kw)
+        return lib.nanorts_amd_visible_cells_ffi(None, *a.values())
+
+    assert visible(cell_bytes=3) == 1 and "1, 2 or 4" in err()
+    assert visible(width=300, height=200) == 1 and "48K" in err()
+    assert visible(birth_lanes=2) == 1 and "shared row" in err()
+    assert visible(first=10, count=7) == 1 and "block" in err()
+    assert visible(out=None) == 1 and "NULL" in err()
+    assert visible(lanes=0) == 0
+
+    ptrs = (ctypes.c_void_p * 2)(addr, addr)
+    one = (ctypes.c_int64 * 2)(1, 4)
+    rows = (ctypes.c_int64 * 2)(16, 16)
+    assert lib.nanorts_amd_reset_rows_ffi(None, addr, 4, 33, ptrs, one, ptrs, ptrs, rows) == 1 and "0 to 32" in err()
+    bad = (ctypes.c_int64 * 2)(1, 3)
+    assert lib.nanorts_amd_reset_rows_ffi(None, addr, 4, 2, ptrs, bad, ptrs, ptrs, rows) == 1 and "shared row" in err()
+    assert lib.nanorts_amd_reset_rows_ffi(None, None, 4, 2, ptrs, one, ptrs, ptrs, rows) == 1 and "NULL" in err()
+    assert lib.nanorts_amd_reset_rows_ffi(None, addr, 0, 2, ptrs, one, ptrs, ptrs, rows) == 0
