@@ -1338,15 +1338,71 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
     const nanorts_rollout_results& out = args.out;
     const Layout& y = g.lay;
     const uint32_t env = (uint32_t)(args.env0 + l);
+    // boards of at most 32 columns: the per-cycle summary (occupancy bitmaps,
+    // available list, kept sight bitmaps, packed observation stores), as in
+    // the fused rollout
+    const bool fast = g.fast_obs && g.seen_words == 1 && ((((uintptr_t)out.feature_maps) & 7u) == 0);
+    if (fast) summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     for (int32_t t = 0; t < args.steps; ++t) {
         const int64_t tt = (int64_t)args.t0 + t;
         if (args.seat_record && lane == 0) args.seat_record[tt * lanes + l] = learner;
         // the learner: masks -> sample -> decode (unavailable rows absent)
-        bool irregular = false;
-        const int32_t n = compact_available(g, e, lane, &irregular);
-        build_bitmaps(g, hdr, e, lane);
         const uint32_t ke0 = args.step_keys[2 * t], ke1 = args.step_keys[2 * t + 1];
         const AS3 int16_t* av = at<int16_t>(e, y.a_av);
+        if (fast) {
+            const int32_t n = uni(e.sc[S_NAV]);
+            mark_unavailable(g, e, lane);
+            const Affordable aff = affordable_types(g, hdr, e, lane);
+            // both threefry blocks of a position on two lanes when n <= 32
+            const bool paired = n <= kWave / 2;
+            uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
+            if (paired) {
+                const int32_t u = lane >> 1;
+                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
+                threefry(ke0, ke1, dx0, dx1);
+                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
+                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
+                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
+                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
+            }
+            for (int32_t i = lane; i < n; i += kWave) {
+                const int32_t p = av[i];
+                if (p / g.C != learner) continue;
+                const Row r = legality_row_w1(g, hdr, e, g.N + p, aff);
+                uint32_t words[4] = {pw0, pw1, pw2, pw3};
+                if (!paired) {
+                    words[0] = env;
+                    words[1] = 2u * (uint32_t)p;
+                    words[2] = env;
+                    words[3] = 2u * (uint32_t)p + 1u;
+                    threefry(ke0, ke1, words[0], words[1]);
+                    threefry(ke0, ke1, words[2], words[3]);
+                }
+                int32_t kind, dir, ptype, target, none;
+                if (!out.actions && g.T <= 8) {
+                    sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype, &target,
+                                   &none);
+                } else {
+                    int32_t act[7];
+                    if (g.T <= 8) sample_row_words8(g, r, words, act);
+                    else sample_row_words(g, r, words, act);
+                    if (out.actions) {
+                        int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
+#pragma unroll
+                        for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                    }
+                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
+                }
+                at<int8_t>(e, y.c_kind)[p] = (int8_t)kind;
+                at<int8_t>(e, y.c_dir)[p] = (int8_t)dir;
+                at<int8_t>(e, y.c_ptype)[p] = (int8_t)ptype;
+                at<int16_t>(e, y.c_target)[p] = (int16_t)target;
+                at<int32_t>(e, y.c_none)[p] = none;
+            }
+        }
+        bool irregular = false;
+        const int32_t n = fast ? 0 : compact_available(g, e, lane, &irregular);
+        if (!fast) build_bitmaps(g, hdr, e, lane);
         for (int32_t i = lane; i < n; i += kWave) {
             const int32_t p = av[i];
             if (p / g.C != learner) continue;
@@ -1407,10 +1463,19 @@ __global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
                 b.block = g.N + b.player * g.C;
             }
         }
-        if (out.feature_maps || out.scalars) {
-            const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
-            const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
-            const int64_t slot = (int64_t)ring * lanes + l;
+        const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
+        const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
+        const int64_t slot = (int64_t)ring * lanes + l;
+        if (fast) {
+            const int64_t per = (int64_t)g.cells * 6;
+            uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
+            int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
+            // the sight bitmaps persist in the event counters' words, which
+            // the seat step does not count, when both planes fit there
+            const int32_t kept = 2 * g.H * g.seen_words <= 32 ? y.b_events : -1;
+            summarize(g, hdr, e, lane, args.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr,
+                      kept);
+        } else if (out.feature_maps || out.scalars) {
             observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
