@@ -73,6 +73,21 @@ NR_DEV AS3 T* bv(const Bot& b, int32_t offset) {
     return (AS3 T*)(b.base + offset);
 }
 
+// The LDS offset of int32 carry row f (1..7: unit_birth, order, target,
+// target_birth, base, base_birth, cell); rows 0 (kind) and 8 (unit_type)
+// are bytes.
+NR_DEV int32_t carry_row32(const BotLayout& y, int f) {
+    switch (f) {
+        case 1: return y.k_ubirth;
+        case 2: return y.k_order;
+        case 3: return y.k_target;
+        case 4: return y.k_tbirth;
+        case 5: return y.k_base;
+        case 6: return y.k_bbirth;
+        default: return y.k_cell;
+    }
+}
+
 NR_DEV int32_t wave_min(int32_t v) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
@@ -140,23 +155,23 @@ NR_DEV void closest(const KGame& g, const Env& e, int32_t origin, const AS3 int1
 // this lane; the caller advances next_order by C + 1 once per put.
 NR_DEV void put_unit(const KGame& g, const Bot& b, const Unit& u, int32_t i, bool last, int32_t kind, int32_t target,
                      int32_t tbirth, int32_t base, int32_t bbirth, int32_t cell, int32_t utype, const BotLayout& y) {
-    AS3 int32_t* kk = bv<int32_t>(b, y.k_kind);
+    AS3 int8_t* kk = bv<int8_t>(b, y.k_kind);
     AS3 int32_t* ub = bv<int32_t>(b, y.k_ubirth);
     const bool known = kk[i] != kAbNone && ub[i] == u.birth;
     if (!known) bv<int32_t>(b, y.k_order)[i] = wadd(b.next_order, last ? g.C : (int32_t)bv<int16_t>(b, y.u_rank)[i]);
-    kk[i] = kind;
+    kk[i] = (int8_t)kind;
     ub[i] = u.birth;
     bv<int32_t>(b, y.k_target)[i] = target;
     bv<int32_t>(b, y.k_tbirth)[i] = tbirth;
     bv<int32_t>(b, y.k_base)[i] = base;
     bv<int32_t>(b, y.k_bbirth)[i] = bbirth;
     bv<int32_t>(b, y.k_cell)[i] = cell;
-    bv<int32_t>(b, y.k_utype)[i] = utype;
+    bv<int8_t>(b, y.k_utype)[i] = (int8_t)utype;
     bv<uint8_t>(b, y.k_trained)[i] = 0;
 }
 
 NR_DEV bool is_entry(const Bot& b, const BotLayout& y, int32_t i, int32_t birth, int32_t kind) {
-    return bv<int32_t>(b, y.k_kind)[i] == kind && bv<int32_t>(b, y.k_ubirth)[i] == birth;
+    return bv<int8_t>(b, y.k_kind)[i] == kind && bv<int32_t>(b, y.k_ubirth)[i] == birth;
 }
 
 // ---------------------------------------------------------------------------
@@ -183,8 +198,10 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     b.n_live = n;
     for (int32_t i = lane; i < C; i += kWave) {
         const int64_t at = l * C + i;
+        bv<int8_t>(b, y.k_kind)[i] = (int8_t)carry.row[0][at];
 #pragma unroll
-        for (int f = 0; f < 9; ++f) bv<int32_t>(b, y.k_kind + f * 4 * C)[i] = carry.row[f][at];
+        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = carry.row[f][at];
+        bv<int8_t>(b, y.k_utype)[i] = (int8_t)carry.row[8][at];
         bv<uint8_t>(b, y.k_trained)[i] = carry.trained[at] ? 1 : 0;
     }
     // a vector load on one lane: in a fused rollout this word was written by
@@ -208,16 +225,18 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
             st = type_flag(g, h, t, FL_STOCKPILE) && owner == b.player;
         }
         const uint64_t me = ballot(en), mr = ballot(re), ms = ballot(st);
-        if (en) le[ne + count_below(me)] = (int16_t)s;
-        if (re) lr[nr_ + count_below(mr)] = (int16_t)s;
-        if (st) ls[ns + count_below(ms)] = (int16_t)s;
+        // the lists hold what a valid state can put in them: the opponent's
+        // units, neutral resources, own stockpiles
+        if (en && ne + count_below(me) < C) le[ne + count_below(me)] = (int16_t)s;
+        if (re && nr_ + count_below(mr) < g.N) lr[nr_ + count_below(mr)] = (int16_t)s;
+        if (st && ns + count_below(ms) < C) ls[ns + count_below(ms)] = (int16_t)s;
         ne += popc(me);
         nr_ += popc(mr);
         ns += popc(ms);
     }
-    b.n_enemy = ne;
-    b.n_resource = nr_;
-    b.n_stock = ns;
+    b.n_enemy = ne < C ? ne : C;
+    b.n_resource = nr_ < g.N ? nr_ : g.N;
+    b.n_stock = ns < C ? ns : C;
     wave_sync();
     // birth rank among the present units (abstraction._rank) and the
     // nearest enemy of every live unit
@@ -297,7 +316,7 @@ NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bo
     bool builds = false;
     if (builder >= 0) {
         const int32_t bb = e.birth[b.block + builder];
-        builds = !(is_entry(b, y, builder, bb, kAbBuild) && bv<int32_t>(b, y.k_utype)[builder] == unit_type);
+        builds = !(is_entry(b, y, builder, bb, kAbBuild) && bv<int8_t>(b, y.k_utype)[builder] == unit_type);
     }
     builds = uni(builds ? 1 : 0) != 0;
     if (builds) {
@@ -659,7 +678,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
     // _standing (:383-423) and _plan (:653-715) with _fallback (:575-650)
     for (int32_t i = lane; i < C; i += kWave) {
         const Unit u = unit_at(g, e, b, i);
-        const int32_t kind = bv<int32_t>(b, y.k_kind)[i];
+        const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
         const bool alive = kind != kAbNone && bv<int32_t>(b, y.k_ubirth)[i] == u.birth;
         const bool carrying = u.carried > 0;
         const int32_t kcell = bv<int32_t>(b, y.k_cell)[i];
@@ -682,7 +701,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
         const int32_t harvest_goal = carrying ? cell_of_slot(g, e, base) : target_cell;
         int32_t goal = kAbsent, radius = 0;
         Desire fb = no_desire();
-        const int32_t utype = bv<int32_t>(b, y.k_utype)[i];
+        const int32_t utype = bv<int8_t>(b, y.k_utype)[i];
         if (kind == kAbAttack) {
             goal = target_cell;
             radius = range;
@@ -700,14 +719,14 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
             fb = production(g, h, e, b, y, adjacent_direction(g, u.cell, kcell), utype, u.cell);
         }
         const bool searches = goal != kAbsent && !(kind == kAbAttack && in_range);
-        bv<int32_t>(b, y.u_goal)[i] = searches ? goal : u.cell;
-        bv<int32_t>(b, y.u_radius)[i] = searches ? radius : 0;
-        bv<int32_t>(b, y.u_fkind)[i] = fb.kind;
-        bv<int32_t>(b, y.u_fdir)[i] = fb.dir;
-        bv<int32_t>(b, y.u_ftarget)[i] = fb.target;
-        bv<int32_t>(b, y.u_fptype)[i] = fb.ptype;
-        bv<int32_t>(b, y.u_fclaimed)[i] = fb.claimed;
-        bv<int32_t>(b, y.u_fcost)[i] = fb.cost;
+        bv<int16_t>(b, y.u_goal)[i] = (int16_t)(searches ? goal : u.cell);
+        bv<int16_t>(b, y.u_radius)[i] = (int16_t)(searches ? radius : 0);
+        bv<int8_t>(b, y.u_fkind)[i] = (int8_t)fb.kind;
+        bv<int8_t>(b, y.u_fdir)[i] = (int8_t)fb.dir;
+        bv<int16_t>(b, y.u_ftarget)[i] = (int16_t)fb.target;
+        bv<int8_t>(b, y.u_fptype)[i] = (int8_t)fb.ptype;
+        bv<int16_t>(b, y.u_fclaimed)[i] = (int16_t)fb.claimed;
+        bv<int16_t>(b, y.u_fcost)[i] = (int16_t)fb.cost;
     }
     wave_sync();
     // _queue (:800-801): executing units by order, ties by unit index
@@ -761,8 +780,8 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
     for (int32_t q = 0; q < queued; ++q) {
         const int32_t i = uni(bv<int16_t>(b, y.u_queue)[q]);
         const int32_t start = uni(e.cell[b.block + i]);
-        const int32_t goal = uni(bv<int32_t>(b, y.u_goal)[i]);
-        const int32_t radius = uni(bv<int32_t>(b, y.u_radius)[i]);
+        const int32_t goal = uni(bv<int16_t>(b, y.u_goal)[i]);
+        const int32_t radius = uni(bv<int16_t>(b, y.u_radius)[i]);
         int32_t step = kAbsent;
         // the first pop is the start: already within range means no step
         if (start >= 0 && start < g.cells && sq_distance(g, start, goal) > wmul(radius, radius)) {
@@ -781,9 +800,9 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
             cost = 0;
         } else {
             sel = SEL_FALLBACK;
-            kind = uni(bv<int32_t>(b, y.u_fkind)[i]);
-            claim = uni(bv<int32_t>(b, y.u_fclaimed)[i]);
-            cost = uni(bv<int32_t>(b, y.u_fcost)[i]);
+            kind = uni(bv<int8_t>(b, y.u_fkind)[i]);
+            claim = uni(bv<int16_t>(b, y.u_fclaimed)[i]);
+            cost = uni(bv<int16_t>(b, y.u_fcost)[i]);
         }
         const bool has_cell = claim != kAbsent && claim >= 0 && claim < g.cells;
         const bool conflicting = has_cell && (bit_of(claimed, claim) || bit_of(kept_m, claim));
@@ -820,10 +839,10 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
         kind = kKindMove;
         dir = bv<int8_t>(b, y.u_dir)[i];
     } else if (sel == SEL_FALLBACK) {
-        kind = bv<int32_t>(b, y.u_fkind)[i];
-        dir = bv<int32_t>(b, y.u_fdir)[i];
-        target = bv<int32_t>(b, y.u_ftarget)[i];
-        ptype = bv<int32_t>(b, y.u_fptype)[i];
+        kind = bv<int8_t>(b, y.u_fkind)[i];
+        dir = bv<int8_t>(b, y.u_fdir)[i];
+        target = bv<int16_t>(b, y.u_ftarget)[i];
+        ptype = bv<int8_t>(b, y.u_fptype)[i];
     }
     const bool kept = sel != SEL_NONE;
     const bool filler = u.available && !kept;
@@ -873,9 +892,11 @@ NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64
         const int32_t oi = bv<int32_t>(b, y.k_order)[i];
         int32_t r = 0;
         for (int32_t q = 0; q < standing; ++q) r += key[q] < oi ? 1 : 0;
-        const int32_t kind = bv<int32_t>(b, y.k_kind)[i];
+        const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
+        carry.row[0][at] = kind;
 #pragma unroll
-        for (int f = 0; f < 9; ++f) carry.row[f][at] = bv<int32_t>(b, y.k_kind + f * 4 * C)[i];
+        for (int f = 1; f < 8; ++f) carry.row[f][at] = bv<int32_t>(b, carry_row32(y, f))[i];
+        carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
         carry.row[2][at] = r;
         const bool trained = bv<uint8_t>(b, y.k_trained)[i] != 0 ||
                              ((fl & U_EXECUTES) && (kind == kAbTrain || kind == kAbTrainDirection));

@@ -366,48 +366,60 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
         o += align16(bytes);
         return at;
     };
-    // the nine int32 carry rows back to back, in AbstractActions order
-    by->k_kind = take(9 * 4 * C);
-    by->k_ubirth = by->k_kind + 4 * C;
-    by->k_order = by->k_kind + 8 * C;
-    by->k_target = by->k_kind + 12 * C;
-    by->k_tbirth = by->k_kind + 16 * C;
-    by->k_base = by->k_kind + 20 * C;
-    by->k_bbirth = by->k_kind + 24 * C;
-    by->k_cell = by->k_kind + 28 * C;
-    by->k_utype = by->k_kind + 32 * C;
+    const int32_t N = g.N;
+    // the carry (AbstractActions): its int32 rows, then kind and unit_type as
+    // bytes (small codes) and the trained flags
+    by->k_ubirth = take(4 * C);
+    by->k_order = take(4 * C);
+    by->k_target = take(4 * C);
+    by->k_tbirth = take(4 * C);
+    by->k_base = take(4 * C);
+    by->k_bbirth = take(4 * C);
+    by->k_cell = take(4 * C);
+    by->k_kind = take(C);
+    by->k_utype = take(C);
     by->k_trained = take(C);
+    // per unit, alive from the plan to the commands and the settled carry:
+    // kinds, directions and types as bytes, cells, radii and costs as int16
     by->u_flags = take(C);
-    by->u_role = take(C);
-    by->u_rank = take(2 * C);
-    by->u_es = take(2 * C);
-    by->u_eb = take(4 * C);
-    by->u_goal = take(4 * C);
-    by->u_radius = take(4 * C);
-    by->u_fkind = take(4 * C);
-    by->u_fdir = take(4 * C);
-    by->u_ftarget = take(4 * C);
-    by->u_fptype = take(4 * C);
-    by->u_fclaimed = take(4 * C);
-    by->u_fcost = take(4 * C);
+    by->u_goal = take(2 * C);
+    by->u_radius = take(2 * C);
+    by->u_fkind = take(C);
+    by->u_fdir = take(C);
+    by->u_ftarget = take(2 * C);
+    by->u_fptype = take(C);
+    by->u_fclaimed = take(2 * C);
+    by->u_fcost = take(2 * C);
     by->u_sel = take(C);
     by->u_dir = take(C);
     by->u_drank = take(2 * C);
     by->u_queue = take(2 * C);
     by->u_live = take(2 * C);
     by->u_lbirth = take(4 * C);
-    by->u_list = take(2 * C);
     by->u_lkey = take(4 * C);
-    by->l_enemy = take(2 * E);
-    by->l_resource = take(2 * E);
-    by->l_stock = take(2 * E);
-    by->a_below = take(2 * cells);
-    by->a_mark = take(cells);
     by->m_claimed = take(4 * words);
     by->m_free = take(4 * words);
     by->m_used = take(4 * words);
     by->m_kept = take(4 * words);
+    // dead once the walk starts (ranks, nearest enemies, roles, the queue's
+    // scratch list, the candidate lists, the build reservations): the walk's
+    // search scratch lies over them.  Enemies and own stockpiles are units of
+    // one player (at most C), resources neutral units (at most N).
+    const int32_t scratch = o;
+    by->u_rank = take(2 * C);
+    by->u_es = take(2 * C);
+    by->u_eb = take(4 * C);
+    by->u_role = take(C);
+    by->u_list = take(2 * C);
+    by->l_enemy = take(2 * C);
+    by->l_resource = take(2 * N);
+    by->l_stock = take(2 * C);
     by->m_reserved = take(4 * words);
+    const int32_t scratch_end = o;
+    o = scratch;
+    by->a_below = take(2 * cells);
+    by->a_mark = take(cells);
+    if (o < scratch_end) o = scratch_end;
     by->bytes = align16(o);
     // The bot runs before admission and keeps nothing past it, so its region
     // shares the env block's phase union, after the command arrays the bot
@@ -1321,7 +1333,9 @@ struct SeatRolloutArgs {
     uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
 };
 
-__global__ __launch_bounds__(256) void k_seat_rollout(SeatRolloutArgs args) {
+// 168 VGPRs at most: three waves per SIMD, which the bot region's LDS allows
+// on boards up to 16x16
+__global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
     const KGame& g = args.g;
     const int64_t lanes = args.lanes;
     NR_KERNEL_PROLOGUE
