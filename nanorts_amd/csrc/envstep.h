@@ -51,6 +51,7 @@ NR_DEV int32_t compact_available(const KGame& g, const Env& e_in, int lane, bool
 // the reservation (N/core/admission.py:242-289).
 struct Reqs {
     int32_t p, slot, kind1, none1, req, dir, ptype, target, pos1, cost1, player1, birth, pl;
+    int32_t order_rank;  // the command's request_order rank (0 through the JaxMARL surface)
     bool conflicting;
 };
 
@@ -112,6 +113,7 @@ NR_DEV void no_request(Reqs& q) {
     q.none1 = q.req = 0;
     q.dir = q.ptype = q.target = kAbsent;
     q.pos1 = q.cost1 = q.player1 = q.birth = q.pl = 0;
+    q.order_rank = 0;
     q.conflicting = false;
 }
 
@@ -199,6 +201,7 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
         const int32_t p = at<int16_t>(e, y.a_av)[lane];
         request_of(g, h, e, p, at<int8_t>(e, y.c_kind)[p], at<int8_t>(e, y.c_dir)[p], at<int8_t>(e, y.c_ptype)[p],
                    at<int16_t>(e, y.c_target)[p], at<int32_t>(e, y.c_none)[p], known_legal, count_events, q);
+        q.order_rank = at<int16_t>(e, y.c_rank)[p];
     }
     admit_resolve(g, h, e, lane, key0, key1, n, nA, posA, costA, playerA, q);
     return true;
@@ -213,11 +216,13 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
     const int32_t slot = q.slot, kind1 = q.kind1, none1 = q.none1, req = q.req, dir = q.dir, ptype = q.ptype;
     const int32_t target = q.target, pos1 = q.pos1, cost1 = q.cost1, player1 = q.player1, birth = q.birth, pl = q.pl;
     const bool conflicting = q.conflicting;
-    // Java admission order (_ordered_requests :200-221): player, then birth.
-    // crank orders the requests that can conflict among themselves.
+    // Java admission order (_ordered_requests :200-221): player, then the
+    // request_order rank, then birth.  crank orders the requests that can
+    // conflict among themselves.
     const uint64_t conflicting_lanes = ballot(conflicting);
+    const int32_t orank = q.order_rank;
     int32_t rank = 0, crank = 0;
-    if (ballot(lane < n && (birth < 0 || birth >= (1 << 24))) == 0ull) {
+    if (ballot(lane < n && (birth < 0 || birth >= (1 << 24) || orank != 0)) == 0ull) {
         // one 32-bit key per request: player, birth, lane
         const uint32_t key = lane < n ? ((uint32_t)pl << 31) | ((uint32_t)birth << 6) | (uint32_t)lane : 0xFFFFFFFFu;
         for (int32_t j = 0; j < n; ++j) {
@@ -229,8 +234,10 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
     } else {
         for (int32_t j = 0; j < n; ++j) {
             const int32_t plj = __builtin_amdgcn_readlane(pl, j);
+            const int32_t oj = __builtin_amdgcn_readlane(orank, j);
             const int32_t bj = __builtin_amdgcn_readlane(birth, j);
-            const bool before = (plj < pl) || (plj == pl && (bj < birth || (bj == birth && j < lane)));
+            const bool before = (plj < pl) ||
+                                (plj == pl && (oj < orank || (oj == orank && (bj < birth || (bj == birth && j < lane)))));
             rank += before;
             crank += before && ((conflicting_lanes >> j) & 1ull);
         }

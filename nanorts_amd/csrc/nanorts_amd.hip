@@ -1462,7 +1462,18 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         }
         settle_carry(g, b, ba.y, l, ba.carry, lane);
         wave_sync();
-        core_step(g, hdr, e, lane, ek0, ek1, false);
+        if (fast) {
+            // the env-path admission: the learner and the bot command exactly
+            // their available units.  The bot's region lay over the summary's
+            // lists, so the available positions are listed again.
+            const int32_t nav = list_available(g, e, lane);
+            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, nav, uni(e.sc[S_IRREG]) != 0, false))
+                admit(g, hdr, e, lane, ek0, ek1, false);
+            complete(g, hdr, e, lane);
+            decide_counted(e, lane);
+        } else {
+            core_step(g, hdr, e, lane, ek0, ek1, false);
+        }
         nanorts_env_results r = {};
         if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
         if (out.dones) r.done = out.dones + tt * lanes;

@@ -543,6 +543,23 @@ NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool
     }
 }
 
+// The available owned positions in slot order (the summary's list, again,
+// for a state the summary already saw); returns their count.
+NR_DEV int32_t list_available(const KGame& g, const Env& e_in, int lane) {
+    const Env e = refresh(g, e_in);
+    AS3 int16_t* av = at<int16_t>(e, g.lay.a_av);
+    int32_t n = 0;
+    for (int32_t base = 0; base < 2 * g.C; base += kWave) {
+        const int32_t p = base + lane;
+        const bool available = p < 2 * g.C && e.birth[g.N + p] != kAbsent && e.pkind[g.N + p] == kAbsent;
+        const uint64_t m = ballot(available);
+        if (available) av[n + count_below(m)] = (int16_t)p;
+        n += popc(m);
+    }
+    wave_sync();
+    return n;
+}
+
 // Commands of the positions the summary did not list as available.
 NR_DEV void mark_unavailable(const KGame& g, const Env& e_in, int lane) {
     const Env e = refresh(g, e_in);
