@@ -177,8 +177,10 @@ NR_DEV bool is_entry(const Bot& b, const BotLayout& y, int32_t i, int32_t birth,
 // ---------------------------------------------------------------------------
 // Setup: units, carry, candidate lists
 // ---------------------------------------------------------------------------
+// With `load_carry` false the carry rows in LDS and b.next_order are the
+// ones the last settle_carry left (a fused rollout keeps them there).
 NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
-                      const BotCarry& carry, int lane) {
+                      const BotCarry& carry, int lane, bool load_carry = true) {
     const int32_t C = g.C;
     // live own units in slot order, with their births
     AS3 int16_t* live = bv<int16_t>(b, y.u_live);
@@ -196,7 +198,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
         n += popc(m);
     }
     b.n_live = n;
-    for (int32_t i = lane; i < C; i += kWave) {
+    for (int32_t i = lane; i < (load_carry ? C : 0); i += kWave) {
         const int64_t at = l * C + i;
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)carry.row[0][at];
 #pragma unroll
@@ -206,9 +208,11 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     }
     // a vector load on one lane: in a fused rollout this word was written by
     // the previous cycle's vector store, which the scalar cache does not see
-    int32_t next_order = 0;
-    if (lane == 0) next_order = __builtin_nontemporal_load(carry.next_order + l);
-    b.next_order = uni(next_order);
+    if (load_carry) {
+        int32_t next_order = 0;
+        if (lane == 0) next_order = __builtin_nontemporal_load(carry.next_order + l);
+        b.next_order = uni(next_order);
+    }
     // candidate lists in slot order: enemies (abstraction.enemies), resources
     // and own stockpiles (rush.harvest_sites)
     AS3 int16_t* le = bv<int16_t>(b, y.l_enemy);
@@ -864,9 +868,25 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
     out[5] = kept ? (int32_t)bv<int16_t>(b, y.u_drank)[i] : (filler ? wadd(kept_count, filler_rank) : kAbsent);
 }
 
-// _settled (N/bots/abstraction.py:1099-1119) into the carry rows of env l.
-NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry,
-                         int lane) {
+// The carry rows in LDS and b.next_order into the carry of env l.
+NR_DEV void store_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry, int lane) {
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        const int64_t at = l * g.C + i;
+        carry.row[0][at] = bv<int8_t>(b, y.k_kind)[i];
+#pragma unroll
+        for (int f = 1; f < 8; ++f) carry.row[f][at] = bv<int32_t>(b, carry_row32(y, f))[i];
+        carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
+        carry.trained[at] = bv<uint8_t>(b, y.k_trained)[i];
+    }
+    if (lane == 0) carry.next_order[l] = b.next_order;
+}
+
+// _settled (N/bots/abstraction.py:1099-1119): the carry rows in LDS become
+// the settled carry (the standing units, their orders ranked; the others
+// emptied) and b.next_order the standing count; with `to_memory` they are
+// also written to the carry rows of env l.
+NR_DEV void settle_carry(const KGame& g, Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry, int lane,
+                         bool to_memory = true) {
     const int32_t C = g.C;
     // the standing units with their orders
     AS3 int32_t* key = bv<int32_t>(b, y.u_lkey);
@@ -880,29 +900,27 @@ NR_DEV void settle_carry(const KGame& g, const Bot& b, const BotLayout& y, int64
     }
     wave_sync();
     for (int32_t i = lane; i < C; i += kWave) {
-        const int64_t at = l * C + i;
         const int32_t fl = bv<uint8_t>(b, y.u_flags)[i];
         const bool st = (fl & U_STANDING) != 0;
-        if (!st) {
-#pragma unroll
-            for (int f = 0; f < 9; ++f) carry.row[f][at] = kAbsent;
-            carry.trained[at] = 0;
-            continue;
-        }
         const int32_t oi = bv<int32_t>(b, y.k_order)[i];
         int32_t r = 0;
         for (int32_t q = 0; q < standing; ++q) r += key[q] < oi ? 1 : 0;
         const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
-        carry.row[0][at] = kind;
+        const bool trained = st && (bv<uint8_t>(b, y.k_trained)[i] != 0 ||
+                                    ((fl & U_EXECUTES) && (kind == kAbTrain || kind == kAbTrainDirection)));
+        if (st) {
+            bv<int32_t>(b, y.k_order)[i] = r;
+        } else {
+            bv<int8_t>(b, y.k_kind)[i] = (int8_t)kAbsent;
 #pragma unroll
-        for (int f = 1; f < 8; ++f) carry.row[f][at] = bv<int32_t>(b, carry_row32(y, f))[i];
-        carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
-        carry.row[2][at] = r;
-        const bool trained = bv<uint8_t>(b, y.k_trained)[i] != 0 ||
-                             ((fl & U_EXECUTES) && (kind == kAbTrain || kind == kAbTrainDirection));
-        carry.trained[at] = trained ? 1 : 0;
+            for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = kAbsent;
+            bv<int8_t>(b, y.k_utype)[i] = (int8_t)kAbsent;
+        }
+        bv<uint8_t>(b, y.k_trained)[i] = trained ? 1 : 0;
     }
-    if (lane == 0) carry.next_order[l] = standing;
+    b.next_order = standing;
+    wave_sync();
+    if (to_memory) store_carry(g, b, y, l, carry, lane);
 }
 
 // abstraction.empty_actions into the carry rows of env l (a new episode).
@@ -916,12 +934,26 @@ NR_DEV void clear_carry(const KGame& g, int64_t l, const BotCarry& carry, int la
     if (lane == 0) carry.next_order[l] = 0;
 }
 
+// The same in LDS, for a fused rollout that keeps the carry there.
+NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lane) {
+    for (int32_t i = lane; i < g.C; i += kWave) {
+        bv<int8_t>(b, y.k_kind)[i] = (int8_t)kAbsent;
+#pragma unroll
+        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = kAbsent;
+        bv<int8_t>(b, y.k_utype)[i] = (int8_t)kAbsent;
+        bv<uint8_t>(b, y.k_trained)[i] = 0;
+    }
+    b.next_order = 0;
+    wave_sync();
+}
+
 // family.act (N/bots/family.py:34-41): the rush decisions on the carry, then
 // translate's plan and walk.  Returns kept_count; commands come from
 // unit_command and the carry from settle_carry.
 NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
-                       const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane) {
-    bot_begin(g, h, e, b, y, l, carry, lane);
+                       const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane,
+                       bool load_carry = true) {
+    bot_begin(g, h, e, b, y, l, carry, lane, load_carry);
     if (strategy == kWorkerRush) worker_rush(g, h, e, b, y, lane);
     else barracks_rush(g, h, e, b, y, trained_type, lane);
     const int32_t queued = translate_plan(g, h, e, b, y, lane);

@@ -367,18 +367,6 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
         return at;
     };
     const int32_t N = g.N;
-    // the carry (AbstractActions): its int32 rows, then kind and unit_type as
-    // bytes (small codes) and the trained flags
-    by->k_ubirth = take(4 * C);
-    by->k_order = take(4 * C);
-    by->k_target = take(4 * C);
-    by->k_tbirth = take(4 * C);
-    by->k_base = take(4 * C);
-    by->k_bbirth = take(4 * C);
-    by->k_cell = take(4 * C);
-    by->k_kind = take(C);
-    by->k_utype = take(C);
-    by->k_trained = take(C);
     // per unit, alive from the plan to the commands and the settled carry:
     // kinds, directions and types as bytes, cells, radii and costs as int16
     by->u_flags = take(C);
@@ -420,10 +408,26 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
     by->a_below = take(2 * cells);
     by->a_mark = take(cells);
     if (o < scratch_end) o = scratch_end;
+    // the carry last, past the end of the env block's phase union (which
+    // the step's phases overwrite), so that a fused rollout keeps it in LDS
+    // from cycle to cycle: its int32 rows, then kind and unit_type as bytes
+    // (small codes) and the trained flags
+    const int32_t union_end = g.lay.env_bytes - (g.lay.c_rank + align16(4 * C));
+    if (o < union_end) o = align16(union_end);
+    by->k_ubirth = take(4 * C);
+    by->k_order = take(4 * C);
+    by->k_target = take(4 * C);
+    by->k_tbirth = take(4 * C);
+    by->k_base = take(4 * C);
+    by->k_bbirth = take(4 * C);
+    by->k_cell = take(4 * C);
+    by->k_kind = take(C);
+    by->k_utype = take(C);
+    by->k_trained = take(C);
     by->bytes = align16(o);
-    // The bot runs before admission and keeps nothing past it, so its region
-    // shares the env block's phase union, after the command arrays the bot
-    // writes.
+    // The bot runs before admission, so its region shares the env block's
+    // phase union after the command arrays the bot writes; only the carry
+    // lies beyond the union.
     by->origin = g.lay.c_rank + align16(4 * C);
     if (by->origin + by->bytes > g.lay.env_bytes) g.lay.env_bytes = by->origin + by->bytes;
     return fit_waves(out, why);
@@ -1447,7 +1451,8 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         }
         wave_sync();
         // the bot's rows
-        const int32_t kept = bot_act(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane);
+        // the carry stays in LDS between cycles: loaded once, settled in place
+        const int32_t kept = bot_act(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane, t == 0);
         const int32_t top = (1 << g.rank_bits) - 1;
         for (int32_t i = lane; i < g.C; i += kWave) {
             const int32_t p = b.player * g.C + i;
@@ -1460,7 +1465,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(v[4], g.T);
             at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(v[5] == kAbsent ? 0 : v[5], 0, top);
         }
-        settle_carry(g, b, ba.y, l, ba.carry, lane);
+        settle_carry(g, b, ba.y, l, ba.carry, lane, false);
         wave_sync();
         if (fast) {
             // the env-path admission: the learner and the bot command exactly
@@ -1478,7 +1483,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
         if (out.dones) r.done = out.dones + tt * lanes;
         if (finish_step(g, hdr, e, l, lane, args.partial != 0, r, false)) {
-            clear_carry(g, l, ba.carry, lane);
+            clear_carry_rows(g, b, ba.y, lane);
             ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
             ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
             fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
@@ -1504,6 +1509,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
+    if (args.steps > 0) store_carry(g, b, ba.y, l, ba.carry, lane);
     if (args.seats && lane == 0) args.seats[l] = learner;
     store_env(g, args.s, l, e, lane);
 }
