@@ -392,8 +392,10 @@ def main_seat(args) -> None:
     full = [ms for (a, b, n), ms in zip(times, launch_ms) if n == chunk] or launch_ms
     avg_launch_s = sum(full) / len(full) / 1e3
     b = game.bucket
-    per_step = step_bytes(b) + 2 * carry_bytes(b)
-    per_launch_bytes = L * (chunk * per_step + 2 * state_bytes(b))
+    # the kernel keeps the state and the bot's carry in LDS for the launch:
+    # both are read and written once per launch, the outputs every cycle
+    per_step = step_bytes(b)
+    per_launch_bytes = L * (chunk * per_step + 2 * state_bytes(b) + 2 * carry_bytes(b))
     achieved = per_launch_bytes / avg_launch_s / 1e9
     traffic = pmc_traffic(args, chunk, mode="seat", kernel="k_seat_rollout")
     cpu = None if args.no_cpu else cpu_seat_baseline(bot.name, args.cpu_envs // 4, args.cpu_steps // 15)
