@@ -534,10 +534,23 @@ NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* below, AS3 uint8_t*
             nxt = -1;
         }
         const int32_t pos = cur;
-        cur = below[pos];
         const int32_t py = cell_y(g, pos), px = pos - py * W;
-        const int32_t dx = px - tx, dy = py - ty;
+        // every read of this pop is issued before its first write: the four
+        // neighbours are distinct cells and only this pop writes them
+        int32_t nbs[4];
+        bool on[4];
+#pragma unroll
+        for (int32_t d = 0; d < 4; ++d) {
+            const int32_t nx = px + dir_dx(d), ny = py + dir_dy(d);
+            on[d] = nx >= 0 && nx < W && ny >= 0 && ny < H;
+            nbs[d] = on[d] ? ny * W + nx : pos;
+        }
+        cur = below[pos];
         const int32_t first = (int32_t)mark[pos] - 3;  // -1 at the start
+        int32_t seen[4];
+#pragma unroll
+        for (int32_t d = 0; d < 4; ++d) seen[d] = mark[nbs[d]];
+        const int32_t dx = px - tx, dy = py - ty;
         if (dx * dx + dy * dy <= r2) {
             // the reference maps the step offset +W, -1, -W, +1 in that order:
             // on a one-wide board an upward step (-W = -1) reads as LEFT
@@ -546,10 +559,9 @@ NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* below, AS3 uint8_t*
         const int32_t hcur = abs(dx) + abs(dy);
 #pragma unroll
         for (int32_t d = 0; d < 4; ++d) {
+            if (!on[d] || seen[d] != 0) continue;
             const int32_t nx = px + dir_dx(d), ny = py + dir_dy(d);
-            if (nx < 0 || nx >= W || ny < 0 || ny >= H) continue;
-            const int32_t nb = ny * W + nx;
-            if (mark[nb] != 0) continue;
+            const int32_t nb = nbs[d];
             mark[nb] = (uint8_t)(3 + (first < 0 ? d : first));
             if (abs(nx - tx) + abs(ny - ty) < hcur) {
                 below[nb] = (int16_t)cur;
@@ -789,7 +801,16 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
         int32_t step = kAbsent;
         // the first pop is the start: already within range means no step
         if (start >= 0 && start < g.cells && sq_distance(g, start, goal) > wmul(radius, radius)) {
-            for (int32_t c = lane; c < g.cells; c += kWave) mark[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
+            if ((g.cells & 3) == 0) {
+                // four cells per lane: their open bits to four mark bytes
+                for (int32_t q = lane; q < g.cells / 4; q += kWave) {
+                    const int32_t c0 = 4 * q;
+                    const uint32_t shut = ~((freem[c0 >> 5] & ~used[c0 >> 5]) >> (c0 & 31)) & 15u;
+                    ((AS3 uint32_t*)mark)[q] = (shut & 1u) | ((shut & 2u) << 7) | ((shut & 4u) << 14) | ((shut & 8u) << 21);
+                }
+            } else {
+                for (int32_t c = lane; c < g.cells; c += kWave) mark[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
+            }
             wave_sync();
             int32_t s = kAbsent;
             if (lane == 0) s = astar_first_step(g, below, mark, start, goal, radius);
