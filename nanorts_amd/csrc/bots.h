@@ -136,6 +136,7 @@ NR_DEV void closest(const KGame& g, const Env& e, int32_t origin, const AS3 int1
                     int32_t* birth) {
     const int32_t ox = floor_mod(origin, g.W), oy = floor_div(origin, g.W);
     int32_t best = kAbsent, bd = kLast, bb = kLast;
+#pragma unroll 4
     for (int32_t k = 0; k < n; ++k) {
         const int32_t j = list[k];
         const int32_t c = e.cell[j];
@@ -247,6 +248,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     for (int32_t k = lane; k < n; k += kWave) {
         const int32_t i = live[k], bi = lbirth[k];
         int32_t r = 0;
+#pragma unroll 4
         for (int32_t q = 0; q < n; ++q) r += lbirth[q] < bi ? 1 : 0;
         bv<int16_t>(b, y.u_rank)[i] = (int16_t)r;
         int32_t es, eb;
@@ -634,6 +636,7 @@ NR_DEV int32_t training_direction(const KGame& g, const Hdr& h, const Env& e, co
         const int32_t x = cx + dir_dx(d), yy = cy + dir_dy(d);
         if (x < 0 || x >= g.W || yy < 0 || yy >= g.H || !bit_of(freem, yy * g.W + x)) continue;
         int32_t nearest = kLast;
+#pragma unroll 4
         for (int32_t k = 0; k < n; ++k) {
             const int32_t c = e.cell[near[k]];
             const int32_t dist = abs(x - cell_x(g, c)) + abs(yy - cell_y(g, c));
@@ -763,6 +766,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
     for (int32_t k = lane; k < queued; k += kWave) {
         const int32_t oi = key[k];
         int32_t r = 0;
+#pragma unroll 4
         for (int32_t q = 0; q < queued; ++q) {
             const int32_t oq = key[q];
             r += (oq < oi || (oq == oi && q < k)) ? 1 : 0;
@@ -875,6 +879,7 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
     if (filler) {
         const AS3 int16_t* live = bv<int16_t>(b, y.u_live);
         const AS3 int32_t* lbirth = bv<int32_t>(b, y.u_lbirth);
+#pragma unroll 4
         for (int32_t q = 0; q < b.n_live; ++q) {
             const int32_t j = live[q];
             filler_rank += (e.pkind[b.block + j] == kAbsent && bv<uint8_t>(b, y.u_sel)[j] == SEL_NONE &&
@@ -925,6 +930,7 @@ NR_DEV void settle_carry(const KGame& g, Bot& b, const BotLayout& y, int64_t l, 
         const bool st = (fl & U_STANDING) != 0;
         const int32_t oi = bv<int32_t>(b, y.k_order)[i];
         int32_t r = 0;
+#pragma unroll 4
         for (int32_t q = 0; q < standing; ++q) r += key[q] < oi ? 1 : 0;
         const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
         const bool trained = st && (bv<uint8_t>(b, y.k_trained)[i] != 0 ||
