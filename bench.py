@@ -73,6 +73,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-envs", type=int, default=4096)
     ap.add_argument("--cpu-steps", type=int, default=3000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--one-pass", action="store_true",
+                    help="headline: run each launch as one pass on the full LDS block (no two-pass launch)")
     ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
     ap.add_argument("--profile-child", choices=("rollout", "copy", "gridnet", "seat"), default=None,
                     help=argparse.SUPPRESS)
@@ -110,23 +112,34 @@ def make_env(envs: int):
     return game, env, state
 
 
-def run_rollout(env, state, steps: int, chunk: int, depth: int, step0: int, events=None):
+# whether the last rollout launch ran two passes (set by run_rollout)
+LAST_TWO_PASS = False
+
+
+def run_rollout(env, state, steps: int, chunk: int, depth: int, step0: int, events=None, two_pass: bool = True):
     """Run `steps` cycles in launches of `chunk`; returns per-launch ms when
     `events` is requested."""
     import torch
 
+    global LAST_TWO_PASS
     done = 0
     times = []
+    out = None
     while done < steps:
         n = min(chunk, steps - done)
         if events:
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-        env.rollout(state, n, (11, 13), step0=step0 + done, record=True, observation_depth=depth)
+        out = env.rollout(state, n, (11, 13), step0=step0 + done, record=True, observation_depth=depth,
+                          two_pass=two_pass)
         if events:
             b.record()
             times.append((a, b, n))
         done += n
+    if out is not None:
+        # the first pass ran at least one cycle of some game
+        first = out["first_pass_cycles"]
+        LAST_TWO_PASS = first is not None and bool((first > 0).any().item())
     return times
 
 
@@ -212,8 +225,8 @@ def child(args) -> None:
     # the headline's timed launch shape: the mid-game advance, then launches
     # of `chunk` cycles (the caller passes the timed chunk)
     game, env, state = make_env(args.envs)
-    run_rollout(env, state, MIDGAME, args.chunk, args.depth, 0)
-    run_rollout(env, state, PMC_LAUNCHES * args.chunk, args.chunk, args.depth, MIDGAME)
+    run_rollout(env, state, MIDGAME, args.chunk, args.depth, 0, two_pass=not args.one_pass)
+    run_rollout(env, state, PMC_LAUNCHES * args.chunk, args.chunk, args.depth, MIDGAME, two_pass=not args.one_pass)
     torch.cuda.synchronize()
 
 
@@ -225,9 +238,16 @@ def progress(message: str) -> None:
     print(f"bench: {message}", file=sys.stderr, flush=True)
 
 
-def pmc_counters(args, mode: str, kernel: str, counters: str, chunk: int) -> list[dict[str, float]]:
-    """One rocprofv3 --pmc pass over a profile child; per dispatch of
-    `kernel` (in dispatch order) the counter values and the duration in ns."""
+def kernel_base(name: str) -> str:
+    """A rocprofv3 kernel name without its argument list."""
+    return name.split("(")[0].split()[-1] if name.strip() else ""
+
+
+def pmc_counters(args, mode: str, kernel, counters: str, chunk: int) -> list[dict[str, float]]:
+    """One rocprofv3 --pmc pass over a profile child; per dispatch of the
+    kernels named in `kernel` (one name or a tuple; in dispatch order) the
+    counter values, the duration in ns and the kernel's name."""
+    kernels = (kernel,) if isinstance(kernel, str) else tuple(kernel)
     import csv
     import shutil
     import tempfile
@@ -240,16 +260,19 @@ def pmc_counters(args, mode: str, kernel: str, counters: str, chunk: int) -> lis
     cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", *counters.split(), "-d", str(out), "-o", "pmc",
            "--output-format", "csv", "--", sys.executable, str(ROOT / "bench.py"), "--profile-child", mode,
            "--workload", args.workload, "--envs", str(args.envs), "--chunk", str(chunk), "--depth", str(args.depth)]
+    if getattr(args, "one_pass", False):
+        cmd.append("--one-pass")
     subprocess.run(cmd, env=dict(os.environ), capture_output=True, text=True, timeout=180)
     rows: dict[int, dict[str, float]] = {}
     for path in out.rglob("*counter_collection.csv"):
         with open(path) as fh:
             for row in csv.DictReader(fh):
                 name = row.get("Kernel_Name", "")
-                want = kernel in name if mode != "copy" else ("copy" in name.lower() or "elementwise" in name.lower())
+                want = (kernel_base(name) in kernels if mode != "copy"
+                        else ("copy" in name.lower() or "elementwise" in name.lower()))
                 if not want:
                     continue
-                rec = rows.setdefault(int(row.get("Dispatch_Id") or len(rows)), {})
+                rec = rows.setdefault(int(row.get("Dispatch_Id") or len(rows)), {"kernel": kernel_base(name)})
                 rec[row["Counter_Name"]] = rec.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
                 if row.get("Start_Timestamp") and row.get("End_Timestamp"):
                     rec["duration_ns"] = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
@@ -261,22 +284,42 @@ def _median(values: list[float]) -> float:
     return sorted(values)[len(values) // 2]
 
 
-def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel: str = "k_rollout",
+# The headline rollout's launch: the first pass and the second pass that
+# follows it on the same stream (or the one pass on the full block).
+ROLLOUT_KERNELS = ("k_rollout_lean", "k_rollout")
+
+
+def per_launch(rows: list[dict[str, float]], counter: str, kernels) -> list[float]:
+    """Counter sums per launch of a kernel sequence: a launch opens at each
+    dispatch of kernels[0] and takes the dispatches of the others that follow
+    it (each dispatch is its own launch when kernels[0] never ran)."""
+    kernels = (kernels,) if isinstance(kernels, str) else tuple(kernels)
+    opener = kernels[0] if any(r.get("kernel") == kernels[0] for r in rows) else None
+    sums: list[float] = []
+    for r in rows:
+        if counter not in r:
+            continue
+        if opener is None or r.get("kernel") == opener or not sums:
+            sums.append(r[counter])
+        else:
+            sums[-1] += r[counter]
+    return sums
+
+
+def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel=ROLLOUT_KERNELS,
                 last: int = 0) -> dict | None:
-    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the measured kernel's
-    launches of `per_launch_steps` cycles (the last `last` dispatches when
-    set, else every one), each scaled by what the counter reads for a plain
-    copy of known size."""
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the measured launches of
+    `per_launch_steps` cycles (the last `last` launches when set, else every
+    one; a launch of several kernels sums them), each scaled by what the
+    counter reads for a plain copy of known size."""
     if args.traffic == "off":
         return None
     try:
         copy_bytes = 2 * (1 << 26) * 4  # read + write of the 256 MiB copy
         fetch_copy = [r["FETCH_SIZE"] for r in pmc_counters(args, "copy", "", "FETCH_SIZE", 1) if "FETCH_SIZE" in r]
         write_copy = [r["WRITE_SIZE"] for r in pmc_counters(args, "copy", "", "WRITE_SIZE", 1) if "WRITE_SIZE" in r]
-        fetch = [r["FETCH_SIZE"] for r in pmc_counters(args, mode, kernel, "FETCH_SIZE", per_launch_steps)
-                 if "FETCH_SIZE" in r]
-        write = [r["WRITE_SIZE"] for r in pmc_counters(args, mode, kernel, "WRITE_SIZE", per_launch_steps)
-                 if "WRITE_SIZE" in r]
+        fetch = per_launch(pmc_counters(args, mode, kernel, "FETCH_SIZE", per_launch_steps), "FETCH_SIZE", kernel)
+        write = per_launch(pmc_counters(args, mode, kernel, "WRITE_SIZE", per_launch_steps), "WRITE_SIZE", kernel)
         if last:
             fetch, write = fetch[-last:], write[-last:]
         if not (fetch_copy and write_copy and fetch and write):
@@ -298,9 +341,12 @@ def pmc_limiter(args, per_launch_steps: int, last: int) -> dict | None:
     if args.traffic == "off":
         return None
     try:
-        rows = [r for r in pmc_counters(args, "rollout", "k_rollout",
+        rows = [r for r in pmc_counters(args, "rollout", ROLLOUT_KERNELS,
                                         "SQ_ACTIVE_INST_VALU SQ_THREAD_CYCLES_VALU GRBM_GUI_ACTIVE", per_launch_steps)
-                if "SQ_ACTIVE_INST_VALU" in r and "GRBM_GUI_ACTIVE" in r][-last:]
+                if "SQ_ACTIVE_INST_VALU" in r and "GRBM_GUI_ACTIVE" in r]
+        # the first pass is the launch's dominant kernel when it ran
+        main = ROLLOUT_KERNELS[0] if any(r["kernel"] == ROLLOUT_KERNELS[0] for r in rows) else ROLLOUT_KERNELS[1]
+        rows = [r for r in rows if r["kernel"] == main][-last:]
         if not rows:
             return None
         busy, lanes = [], []
@@ -742,13 +788,14 @@ def main() -> None:
     L = args.envs
     chunk = max(1, min(args.chunk, args.steps))
     # untimed: the mid-game advance, then the warmup
-    run_rollout(env, state, MIDGAME, chunk, args.depth, 0)
-    run_rollout(env, state, args.warmup, chunk, args.depth, MIDGAME)
+    two = not args.one_pass
+    run_rollout(env, state, MIDGAME, chunk, args.depth, 0, two_pass=two)
+    run_rollout(env, state, args.warmup, chunk, args.depth, MIDGAME, two_pass=two)
     torch.cuda.synchronize()
     progress(f"{MIDGAME} mid-game + {args.warmup} warmup cycles done")
     # timed region: exactly `steps` cycles
     t0 = time.perf_counter()
-    times = run_rollout(env, state, args.steps, chunk, args.depth, MIDGAME + args.warmup, events=True)
+    times = run_rollout(env, state, args.steps, chunk, args.depth, MIDGAME + args.warmup, events=True, two_pass=two)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     launch_ms = [a.elapsed_time(b) for a, b, _ in times]
@@ -820,7 +867,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
-            "kernel": "k_rollout",
+            "kernel": "k_rollout_lean + k_rollout (second pass)" if LAST_TWO_PASS else "k_rollout",
             "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes,
             "cycles_per_launch": chunk,

@@ -143,6 +143,13 @@ typedef struct nanorts_rollout_results {
     int32_t depth;          /* ring depth of feature_maps / scalars, >= 1 */
     int32_t* general_admissions; /* [L] cycles of the launch admitted request by request (an irregular
                                   * state or more than 64 requests); written by nanorts_amd_rollout only */
+    int32_t* progress;           /* [L] caller-owned work words of nanorts_amd_rollout's two-pass launch, or
+                                  * NULL for one pass on the full LDS block.  With them, a first pass runs
+                                  * each game on a smaller LDS block (more games per CU) until a cycle needs
+                                  * the request-by-request admission or more than 64 live slots complete;
+                                  * the second pass runs the rest of that game's cycles on the full block.
+                                  * On return: the cycles of the last launch each game ran in the first
+                                  * pass.  Ignored by the seat rollouts. */
 } nanorts_rollout_results;
 
 /* Carry of an abstraction-family bot (AbstractActions,

@@ -1157,7 +1157,9 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // pending.select + completion.apply (N/core/completion.py:106-117).  One
 // pass over the slots records each acting member's retained actor (the
 // pre-clear snapshot, :120-131) and clears every due pending action.
-NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
+// `at_most_a_wave`: the caller guarantees at most 64 live slots, and the
+// path for more (member records in the phase union) is left out.
+NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
@@ -1166,7 +1168,7 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     // only live slots hold pending actions
     AS3 int16_t* slots = at<int16_t>(e, y.m_list);
     const int32_t nlive = live_list(g, e, lane, slots);
-    if (nlive <= kWave) {
+    if (at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in
         // their lanes and are ranked and read from there
         const int32_t s = lane < nlive ? slots[lane] : 0;

@@ -279,6 +279,99 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     return fit_waves(out, why);
 }
 
+// Resident waves per SIMD the first pass of the fused rollout is sized for,
+// and its largest workgroup, in games.  Measured at 16x16 on the bench
+// workload: 5 waves per SIMD (20 games per CU in workgroups of 5 or 10
+// games, 90 VGPRs) ran 17 % slower than 4 (16 games in workgroups of 4).
+constexpr int kLeanWavesPerSimd = 4;
+constexpr int kLeanMaxGames = 4;
+
+// LDS bytes of one CU, and a workgroup's LDS rounded up to the allocation
+// granule.
+int32_t lds_per_cu() {
+    int device = 0, v = 0;
+    if (hipGetDevice(&device) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device) == hipSuccess && v > 0)
+        return v;
+    return 160 * 1024;
+}
+int32_t lds_granule(int32_t bytes) { return (bytes + 511) & ~511; }
+
+// Games one CU holds for a layout, with at most `waves_per_simd` waves per
+// SIMD (4 SIMDs) and `wpb` games per workgroup.
+int32_t games_per_cu(const Layout& y, int wpb, int waves_per_simd) {
+    const int32_t by_lds = lds_per_cu() / lds_granule(y.hdr_bytes + wpb * y.env_bytes);
+    const int32_t by_waves = (4 * waves_per_simd) / wpb;
+    return (by_lds < by_waves ? by_lds : by_waves) * wpb;
+}
+
+// The layout of the fused rollout's first pass (k_rollout_lean).  The state
+// rows keep their offsets; the phase union holds only what a cycle on the
+// one-wave path uses: the summary's bitmaps and lists that persist into the
+// next cycle's sampling and admission, the summary's temporaries, and over
+// those (dead by then) the admission's final kinds and durations and
+// completion's live list.  A cycle that would need more (an irregular state,
+// more than 64 available units or live slots) is left to the second pass,
+// on the full block.  The command arrays, the request-by-request
+// admission's keys, completion's member records and the staging of the
+// non-packed observation have no place in this block and are never used
+// by k_rollout_lean.  The entry list keeps 64 entries: the summary writes no
+// more, and more than 64 entries is an irregular state.
+bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
+    if (!shape_for(game, out, why)) return false;
+    KGame& g = out->g;
+    if (!g.fast_obs) {
+        *why = "the first pass needs the packed observation (width a multiple of 4)";
+        return false;
+    }
+    Layout& y = g.lay;
+    const int32_t E = g.E, C2 = 2 * g.C, plane = g.H * g.seen_words;
+    int32_t o = y.o_live + align16(((E + 63) / 64) * 8);
+    auto take = [&o](int32_t bytes) {
+        const int32_t at = o;
+        o += align16(bytes);
+        return at;
+    };
+    y.c_kind = y.c_dir = y.c_ptype = y.c_target = y.c_none = y.c_rank = 0;
+    y.b_pkey = y.b_keys = y.b_tmp = y.b_order = y.b_rank = 0;
+    y.m_rec = y.m_tmp = y.v_oseen = y.v_stage = y.v_words = 0;
+    y.o_bm = take(6 * plane * 4);
+    y.a_av = take(C2 * 2);
+    y.a_list = take(kWave * 2);
+    const int32_t temps = o;
+    y.o_lo = take((E + 1) * 4);
+    y.o_fl = take(E + 1);
+    y.b_units = take(C2 * 2);
+    y.o_slist = take(E * 2);
+    // the rollout keeps its sight bitmaps in the event words when both
+    // planes fit there, else the summary stamps them here
+    y.v_seen = 2 * plane <= 32 ? 0 : take(2 * plane * 4);
+    int32_t end = o;
+    o = temps;
+    y.a_fk = take(kWave * 4);
+    y.a_fn = take(kWave * 4);
+    if (o > end) end = o;
+    o = temps;
+    y.m_list = take(E * 2);
+    if (o > end) end = o;
+    y.env_bytes = align16(end);
+    int best = 0, best_wpb = 0;
+    for (int wpb = 1; wpb <= kLeanMaxGames; ++wpb) {
+        const int32_t games = y.hdr_bytes + wpb * y.env_bytes <= lds_per_cu() ? games_per_cu(y, wpb, kLeanWavesPerSimd) : 0;
+        if (games > best) {
+            best = games;
+            best_wpb = wpb;
+        }
+    }
+    if (best == 0) {
+        *why = "one game's first-pass block does not fit a CU";
+        return false;
+    }
+    out->wpb = best_wpb;
+    out->lds = y.hdr_bytes + best_wpb * y.env_bytes;
+    return true;
+}
+
 // A smaller env block for the kernels that read a few leaves: `masks` holds
 // the leaves the legality rows read, the occupancy bitmaps and the staged
 // words (k_legality); otherwise the block is empty (the samplers read only
@@ -1119,6 +1212,7 @@ struct RolloutArgs {
     int64_t lanes;
     nanorts_state s;
     int32_t t0, steps, partial;  // cycles t0 .. t0 + steps - 1 of the caller's rollout
+    int32_t resume;              // second pass: each game starts at its out.progress cycle
     int64_t env0;
     nanorts_rollout_results out;
     uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
@@ -1151,19 +1245,62 @@ NR_DEV Env wave_env(const KGame& g, int wave) {
     const Env e = wave_env(g, wave);                  \
     (void)hdr;
 
-__global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
+// Live slots of the staged env (wave-uniform).
+NR_DEV int32_t live_slots(const KGame& g, const Env& e) {
+    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
+    int32_t n = 0;
+    for (int32_t w = 0; w * kWave < g.E; ++w) n += popc(live[w]);
+    return uni(n);
+}
+
+// The cycles of one launch.  `Lean` is the first pass of the two-pass
+// launch (k_rollout_lean, on shape_for_lean's block): before each cycle it
+// checks that the cycle stays on the one-wave path (a regular state with at
+// most 64 available units and at most 64 live slots); at the first cycle
+// that does not, the game's state goes back to memory and out.progress
+// records that cycle, from which the second pass (k_rollout with `resume`,
+// on the full block) runs the rest.  Splitting a game's cycles between
+// launches this way gives the same result as one launch, as the state is
+// all a cycle carries.
+template <bool Lean>
+NR_DEV void rollout_cycles(const RolloutArgs& args) {
     const KGame& g = args.g;
     const int64_t lanes = args.lanes;
+    int32_t t_begin = 0;
+    if (!Lean && args.resume) {
+        // a workgroup whose games the first pass finished stages nothing.
+        // The waves vote through the first words of the dynamic LDS (the
+        // header goes there after the second barrier): a static LDS
+        // variable (as __syncthreads_or keeps) would grow every
+        // workgroup's allocation past what four workgroups per CU allow.
+        extern __shared__ __align__(16) uint8_t nr_lds[];
+        AS3 uint32_t* votes = (AS3 uint32_t*)nr_lds;
+        const int waves = (int)(blockDim.x >> 6);
+        const int64_t l0 = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6);
+        const bool busy = l0 < lanes && args.out.progress[l0] < args.steps;
+        if ((threadIdx.x & (kWave - 1)) == 0) votes[threadIdx.x >> 6] = busy ? 1u : 0u;
+        __syncthreads();
+        uint32_t any = 0u;
+        for (int w = 0; w < waves; ++w) any |= votes[w];
+        __syncthreads();
+        if (any == 0u) return;
+    }
     NR_KERNEL_PROLOGUE
+    if (!Lean && args.resume) {
+        t_begin = uni(args.out.progress[l]);
+        if (t_begin >= args.steps) return;
+    }
     load_env(g, args.s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    const bool fast = g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0);
+    // the first pass runs only where this holds (the host checks it)
+    const bool fast = Lean || (g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0));
     if (fast) summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const int32_t steps = args.steps;
     int32_t general = 0;  // cycles admitted request by request
-    for (int32_t t = 0; t < steps; ++t) {
+    int32_t stop = steps;  // first pass: the first cycle left to the second
+    for (int32_t t = t_begin; t < steps; ++t) {
         bool irregular = false;
         int32_t n;
         // fused: the sampled commands go straight into the admission's
@@ -1175,13 +1312,17 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
+            if (Lean && (uni(e.sc[S_IRREG]) != 0 || uni(e.sc[S_NAV]) > kWave || live_slots(g, e) > kWave)) {
+                stop = t;
+                break;
+            }
             const nanorts_rollout_results& out = a.out;
             const int32_t owned = 2 * g.C;
             const int64_t tt = (int64_t)a.t0 + t;  // cycle index within the caller's rollout
             if (fast) {
                 n = uni(e.sc[S_NAV]);
                 irregular = uni(e.sc[S_IRREG]) != 0;
-                fused = !irregular && n <= kWave;
+                fused = Lean || (!irregular && n <= kWave);
             } else {
                 n = compact_available(g, e, lane, &irregular);
                 build_bitmaps(g, hdr, e, lane);
@@ -1266,7 +1407,8 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
             }
             wave_sync();
             // env.step: core.step keyed by fold_in(env root, episode)
-            if (fused && listed) {
+            if (Lean || (fused && listed)) {
+                // the first pass stopped before any cycle that is not both
                 admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
             } else if (fused || !admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
                 // general admission; a fused cycle (which the summary's
@@ -1282,7 +1424,7 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
         }
         {
             NR_ROLLOUT_PHASE
-            complete(g, hdr, e, lane);
+            complete(g, hdr, e, lane, Lean);
             decide_counted(e, lane);
             nanorts_env_results r = {};
             const int64_t tt = (int64_t)a.t0 + t;
@@ -1314,9 +1456,25 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) {
     }
     {
         NR_ROLLOUT_PHASE
-        store_env(g, a.s, l, e, lane);
-        if (a.out.general_admissions && lane == 0) a.out.general_admissions[l] = general;
+        if (!Lean || stop > 0) store_env(g, a.s, l, e, lane);
+        if (lane == 0) {
+            if (Lean) a.out.progress[l] = stop;
+            else if (!a.resume && a.out.progress) a.out.progress[l] = 0;  // one pass on the full block
+            // the second pass counts the cycles of a game the first stopped
+            if (a.out.general_admissions && (!Lean || stop == steps)) a.out.general_admissions[l] = general;
+        }
     }
+}
+
+__global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) { rollout_cycles<false>(args); }
+
+// The first pass: the one-wave path alone, on a smaller LDS block per game.
+// Without the request-by-request admission and completion's member records
+// its code is smaller and keeps fewer scalar registers (90 VGPRs, 60 SGPRs
+// spilled to VGPR lanes against k_rollout's 112 and 117), which makes a
+// cycle about 2.5 % faster at the same 16 games per CU.
+__global__ __launch_bounds__(kWave * kLeanMaxGames) void k_rollout_lean(RolloutArgs args) {
+    rollout_cycles<true>(args);
 }
 
 // Fused learner-vs-bot rollout: per cycle the learner's rows sampled from
@@ -2509,6 +2667,16 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
     if (lanes <= 0 || steps == 0) return NANORTS_OK;
     const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
     if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    // Two passes when the caller gives the work words, the packed
+    // observation applies and the first pass's block holds at least as many
+    // games per CU as the full block.
+    Shape lean;
+    std::string lean_why;
+    const bool two_pass = results.progress != nullptr && sh.g.fast_obs &&
+                          (((uintptr_t)results.feature_maps) & 7u) == 0 && shape_for_lean(game, &lean, &lean_why) &&
+                          games_per_cu(lean.g.lay, lean.wpb, kLeanWavesPerSimd) >= games_per_cu(sh.g.lay, sh.wpb, 4);
+    const int64_t lean_blocks = two_pass ? (lanes + lean.wpb - 1) / lean.wpb : 0;
+    if (lean_blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
     // launches of at most kRolloutChunk cycles; the state stays in HBM
     // between them, so the result does not depend on the split
     for (int32_t t0 = 0; t0 < steps; t0 += kRolloutChunk) {
@@ -2528,6 +2696,13 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
             host_fold_in(k0, k1, (uint32_t)(step0 + t0 + t));
             args.step_keys[2 * t] = k0;
             args.step_keys[2 * t + 1] = k1;
+        }
+        if (two_pass) {
+            args.g = lean.g;
+            hipLaunchKernelGGL(k_rollout_lean, dim3((unsigned)lean_blocks), dim3((unsigned)(kWave * lean.wpb)),
+                               (size_t)lean.lds, (hipStream_t)stream, args);
+            args.g = sh.g;
+            args.resume = 1;
         }
         hipLaunchKernelGGL(k_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
                            (hipStream_t)stream, args);

@@ -575,11 +575,16 @@ class NanoRTS:
 
     def rollout(self, state: EnvironmentState, steps: int, sample_key, *, step0: int = 0, env0: int = 0,
                 record: bool = True, record_actions: bool = False, observation_depth: int = 1,
-                count_general: bool = False) -> dict[str, Any]:
+                count_general: bool = False, two_pass: bool = True) -> dict[str, Any]:
         """Fused rollout: `steps` cycles of masks -> sample -> env.step with the
         state resident in LDS, in place.  Bit-equal to the per-call API.  With
         count_general, out["general_admissions"] int32[L] counts each env's
-        cycles that took the request-at-a-time admission."""
+        cycles that took the request-at-a-time admission.  With two_pass (the
+        default), each launch first runs the games on a smaller LDS block
+        and hands the cycles that need the full block to a second pass;
+        out["first_pass_cycles"] int32[L] holds the cycles of the last launch
+        each game ran in the first pass (steps of it when the launch needed
+        no second pass).  two_pass=False runs one pass on the full block."""
         L = state.num_envs
         b = self.bucket
         d = self.device
@@ -593,12 +598,13 @@ class NanoRTS:
         scalars = torch.empty((depth, L, 2, 4), dtype=torch.int32, device=d)
         key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
         general = torch.empty(L, dtype=torch.int32, device=d) if count_general else None
+        progress = torch.empty(L, dtype=torch.int32, device=d) if two_pass else None
         results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth,
-                                        _ptr(general))
+                                        _ptr(general), _ptr(progress))
         native.check(self.lib.nanorts_amd_rollout(_stream(), self.dev.ref, state.native(), L, key, int(step0), int(steps),
                                               self.partial, int(env0), results), "nanorts_amd_rollout")
         out.update(rewards=rewards, dones=dones, actions=actions, feature_maps=maps, scalars=scalars,
-                   general_admissions=general)
+                   general_admissions=general, first_pass_cycles=progress)
         return out
 
     # -------------------------------------------------------------- helpers

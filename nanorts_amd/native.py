@@ -64,7 +64,7 @@ class EnvResults(ctypes.Structure):
 
 class RolloutResults(ctypes.Structure):
     _fields_ = [("rewards", _VP), ("dones", _VP), ("actions", _VP), ("feature_maps", _VP), ("scalars", _VP),
-                ("depth", ctypes.c_int32), ("general_admissions", _VP)]
+                ("depth", ctypes.c_int32), ("general_admissions", _VP), ("progress", _VP)]
 
 
 ABSTRACT_FIELDS = ("kind", "unit_birth", "order", "target", "target_birth", "base", "base_birth", "cell",

@@ -312,6 +312,80 @@ def test_crowded_rollout_takes_the_general_admission(oracle_threads):
     assert (quiet["general_admissions"].cpu().numpy() == 0).all()
 
 
+def _packed(game, extra: list[int], seed: int = 3, alternate: bool = True) -> dict:
+    """Starting states of `game` with extra[l] Workers added to lane l on open
+    cells, alternating between the players (or all for player 0), each born
+    in its block's lowest free slot."""
+    from oracle.oracle import batch_initial
+    from tests.helpers import roots
+
+    L = len(extra)
+    st = batch_initial(game, L, roots(L, seed))
+    b = game.bucket
+    rng = np.random.default_rng(seed)
+    worker = 3
+    hp = int(game.columns["hit_points"][worker])
+    walls = game.terrain.reshape(-1)
+    for l in range(L):
+        em = st["entity_at"][l].reshape(-1)
+        cells = rng.permutation(np.flatnonzero((em == -1) & ~walls))[:extra[l]]
+        for k, cell in enumerate(cells):
+            player = k & 1 if alternate else 0
+            start = b.neutral_capacity + player * b.per_player_capacity
+            slot = start + int(np.flatnonzero(st["birth"][l, start:start + b.per_player_capacity] == -1)[0])
+            birth = int(st["next_birth"][l])
+            st["next_birth"][l] = birth + 1
+            st["birth"][l, slot], st["unit_type"][l, slot], st["owner"][l, slot] = birth, worker, player
+            st["cell"][l, slot], st["hit_points"][l, slot] = cell, hp
+            em[cell] = slot
+    return st
+
+
+def test_two_pass_rollout_hands_games_to_the_second_pass(oracle_threads):
+    """The rollout's first pass runs a game on the smaller LDS block until a
+    cycle needs more than 64 live slots (or another path the block has no
+    room for); the second pass, on the full block, runs the rest of that
+    game's cycles.  Games that start with 57..72 live slots, the added
+    Workers all player 0's and 40 resources each, cross the bound at cycle 0,
+    part-way through the launch (spawns take a game past 64 live slots), or
+    not at all.  All of them match the oracle and the one-pass
+    launch."""
+    from oracle.oracle import Oracle
+
+    print("two-pass rollout", flush=True)
+    game, partial = game_for("16x16-random-partial")
+    base = int((_packed(game, [0])["birth"][0] != -1).sum())
+    extra = [57 - base + k for k in range(16)]
+    st = _packed(game, extra, alternate=False)
+    st["player_resources"][:] = 40
+    live = (st["birth"] != -1).sum(1)
+    assert live.min() == 57 and live.max() == 72
+    oracle = Oracle(game)
+    assert (oracle.violations(st) == 0).all()
+    L, steps = len(extra), 96
+    env = _env(game, partial)
+    dev = to_device(env, st)
+    one = to_device(env, st)
+    got = env.rollout(dev, steps, (4, 1), record=True, count_general=True)
+    first = got["first_pass_cycles"].cpu().numpy()
+    print("first-pass cycles per game:", first.tolist(), flush=True)
+    assert (first[live > 64] == 0).all()
+    assert ((first > 0) & (first < steps)).any()
+    assert (first == steps).any()
+    want = oracle.rollout(st, (4, 1), 0, steps, partial, threads=oracle_threads)
+    np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
+    np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
+    np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
+    assert_states_equal(st, to_host(dev), "two-pass rollout")
+    single = env.rollout(one, steps, (4, 1), record=True, count_general=True, two_pass=False)
+    np.testing.assert_array_equal(single["rewards"].cpu().numpy(), want["rewards"])
+    np.testing.assert_array_equal(single["general_admissions"].cpu().numpy(),
+                                  got["general_admissions"].cpu().numpy())
+    assert (single["first_pass_cycles"] is None)
+    assert_states_equal(st, to_host(one), "one-pass rollout")
+
+
 def test_crowded_env_step_per_call(oracle_threads):
     """env.step on the same crowded states, cycle by cycle, against the oracle."""
     import torch
