@@ -104,8 +104,6 @@ struct Layout {
     int32_t o_lo;      // occupant word per slot (player 0's view), outside the union
     int32_t o_fl;      // occupant flags per slot: kind | resource << 4 | stockpile << 5
     int32_t o_live;    // bitmap of live slots (birth != ABSENT), 64 slots per word
-    int32_t o_slist;   // the summary's list of live slots
-    int32_t m_list;    // completion's list of live slots
     // Phase union.  Admission: commands, keys, lists.  Completion: member
     // records, keys.  Observation: seen bitmap, staging, unit list.  Masks:
     // staged words.
@@ -1009,19 +1007,55 @@ NR_DEV void admit(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t
     }
 }
 
-// The live slots in ascending order into list; returns their count.
-NR_DEV int32_t live_list(const KGame& g, const Env& e, int lane, AS3 int16_t* list) {
+// k-th set bit (0-based) of m by halving popcounts; m has more than k bits.
+NR_DEV int32_t select_bit(uint64_t m, int32_t k) {
+    int32_t pos = 0;
+    uint32_t v = (uint32_t)m;
+    const int32_t c32 = popc((uint64_t)v);
+    if (k >= c32) {
+        k -= c32;
+        v = (uint32_t)(m >> 32);
+        pos = 32;
+    }
+#pragma unroll
+    for (int32_t half = 16; half >= 1; half >>= 1) {
+        const uint32_t lowmask = (1u << half) - 1u;
+        const int32_t c = __popc(v & lowmask);
+        if (k >= c) {
+            k -= c;
+            v >>= half;
+            pos += half;
+        }
+    }
+    return pos;
+}
+
+// The i-th live slot (0-based, i below the live count), from the live-slot
+// bitmap: each lane picks its word by the words' running counts and selects
+// the bit within it, so no list goes through LDS.  Lanes with i at or past
+// the count get an unused value.
+NR_DEV int32_t live_slot_at(const KGame& g, const Env& e, int32_t i) {
+    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
+    uint64_t mine = 0ull;
+    int32_t base = 0, k = 0, word = 0;
+    for (int32_t w = 0; w * kWave < g.E; ++w) {
+        const uint64_t m = live[w];
+        const int32_t c = popc(m);
+        const bool in = i >= base && i < base + c;
+        mine = in ? m : mine;
+        k = in ? i - base : k;
+        word = in ? w : word;
+        base += c;
+    }
+    return word * kWave + select_bit(mine, k);
+}
+
+// Live slots of the staged env (wave-uniform).
+NR_DEV int32_t live_slots(const KGame& g, const Env& e) {
     AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
     int32_t n = 0;
-    for (int32_t w = 0; w * kWave < g.E; ++w) {
-        const uint64_t lw = live[w];
-        const uint64_t m = ((uint64_t)(uint32_t)uni((int32_t)(uint32_t)(lw >> 32)) << 32) |
-                           (uint64_t)(uint32_t)uni((int32_t)(uint32_t)lw);
-        if ((m >> lane) & 1ull) list[n + count_below(m)] = (int16_t)(w * kWave + lane);
-        n += popc(m);
-    }
-    wave_sync();
-    return n;
+    for (int32_t w = 0; w * kWave < g.E; ++w) n += popc(live[w]);
+    return uni(n);
 }
 
 // ---------------------------------------------------------------------------
@@ -1158,20 +1192,20 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // pass over the slots records each acting member's retained actor (the
 // pre-clear snapshot, :120-131) and clears every due pending action.
 // `at_most_a_wave`: the caller guarantees at most 64 live slots, and the
-// path for more (member records in the phase union) is left out.
-NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false) {
+// path for more (member records in the phase union) is left out.  Returns
+// the new time.
+NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
     AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
     // only live slots hold pending actions
-    AS3 int16_t* slots = at<int16_t>(e, y.m_list);
-    const int32_t nlive = live_list(g, e, lane, slots);
+    const int32_t nlive = live_slots(g, e);
     if (at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in
         // their lanes and are ranked and read from there
-        const int32_t s = lane < nlive ? slots[lane] : 0;
+        const int32_t s = lane < nlive ? live_slot_at(g, e, lane) : 0;
         bool acting = false;
         int32_t w0 = 0, w1 = 0, w2 = 0, rb = 0, rc = 0, ord = 0;
         if (lane < nlive) {
@@ -1216,12 +1250,12 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bo
                       (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
                       __builtin_amdgcn_readlane(rc, li));
         }
-        return;
+        return time;
     }
     int32_t n = 0;
     for (int32_t base = 0; base < nlive; base += kWave) {
         const int32_t i = base + lane;
-        const int32_t s = i < nlive ? slots[i] : 0;
+        const int32_t s = i < nlive ? live_slot_at(g, e, i) : 0;
         bool acting = false;
         int32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0, r4 = 0;
         if (i < nlive) {
@@ -1285,7 +1319,7 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bo
                       (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
                       __builtin_amdgcn_readlane(rc, li));
         }
-        return;
+        return time;
     }
     // more members than lanes: rank each record by (pending order, slot)
     AS3 int16_t* pos = at<int16_t>(e, y.m_tmp);
@@ -1306,6 +1340,7 @@ NR_DEV void complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bo
                   (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
                   (int16_t)((c >> 8) & 0xFFFF), uni(r[3]), uni(r[4]));
     }
+    return time;
 }
 
 // outcome.decide (N/core/outcome.py:11-25)
@@ -1350,15 +1385,31 @@ NR_DEV void count_units(const KGame& g, const Env& e_in, int lane) {
 }
 
 
-// outcome.decide from the kept unit counts.
-NR_DEV void decide_counted(const Env& e, int lane) {
-    const bool a0 = uni(e.sc[S_UNITS0]) > 0, a1 = uni(e.sc[S_UNITS1]) > 0;
+// The outcome of a cycle and the scalars its observation shows, held in
+// registers after decide_counted so later phases need not read them back.
+struct Outcome {
+    int32_t over, winner, res0, res1, alt;
+};
+
+// outcome.decide from the kept unit counts.  The balances and the
+// alternating count, final once completion has run, are read in the same
+// batch.
+NR_DEV Outcome decide_counted(const Env& e, int lane) {
+    const int32_t u0 = e.sc[S_UNITS0], u1 = e.sc[S_UNITS1];
+    Outcome o;
+    o.res0 = uni(e.sc[S_RES0]);
+    o.res1 = uni(e.sc[S_RES1]);
+    o.alt = uni(e.sc[S_ALT]);
+    const bool a0 = uni(u0) > 0, a1 = uni(u1) > 0;
     const int32_t count = (a0 ? 1 : 0) + (a1 ? 1 : 0);
+    o.over = count <= 1 ? 1 : 0;
+    o.winner = count == 1 ? (a0 ? 0 : 1) : kAbsent;
     if (lane == 0) {
-        e.sc[S_GAME_OVER] = count <= 1 ? 1 : 0;
-        e.sc[S_WINNER] = count == 1 ? (a0 ? 0 : 1) : kAbsent;
+        e.sc[S_GAME_OVER] = o.over;
+        e.sc[S_WINNER] = o.winner;
     }
     wave_sync();
+    return o;
 }
 
 // core.step (N/core/__init__.py:99-110) on the staged env.

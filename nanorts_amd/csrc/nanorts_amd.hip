@@ -226,7 +226,6 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_fl = take(E + 1);
     y.b_units = take(C2 * 2);
     y.v_seen = take(2 * g.H * g.seen_words * 4);
-    y.o_slist = take(E * 2);
     if (o > commands_end) {
         // larger boards: after the persistent lists instead
         o = end;
@@ -234,14 +233,12 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
         y.o_fl = take(E + 1);
         y.b_units = take(C2 * 2);
         y.v_seen = take(2 * g.H * g.seen_words * 4);
-        y.o_slist = take(E * 2);
     }
     if (o > end) end = o;
     // completion
     o = union0;
     y.m_rec = take(C2 * 24);
     y.m_tmp = take(C2 * 2);
-    y.m_list = take(E * 2);
     if (o > end) end = o;
     // observation staging (observe_all) with its seen bitmaps
     o = union0;
@@ -309,8 +306,8 @@ int32_t games_per_cu(const Layout& y, int wpb, int waves_per_simd) {
 // rows keep their offsets; the phase union holds only what a cycle on the
 // one-wave path uses: the summary's bitmaps and lists that persist into the
 // next cycle's sampling and admission, the summary's temporaries, and over
-// those (dead by then) the admission's final kinds and durations and
-// completion's live list.  A cycle that would need more (an irregular state,
+// those (dead by then) the admission's final kinds and durations.  A cycle
+// that would need more (an irregular state,
 // more than 64 available units or live slots) is left to the second pass,
 // on the full block.  The command arrays, the request-by-request
 // admission's keys, completion's member records and the staging of the
@@ -342,7 +339,6 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_lo = take((E + 1) * 4);
     y.o_fl = take(E + 1);
     y.b_units = take(C2 * 2);
-    y.o_slist = take(E * 2);
     // the rollout keeps its sight bitmaps in the event words when both
     // planes fit there, else the summary stamps them here
     y.v_seen = 2 * plane <= 32 ? 0 : take(2 * plane * 4);
@@ -350,9 +346,6 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     o = temps;
     y.a_fk = take(kWave * 4);
     y.a_fn = take(kWave * 4);
-    if (o > end) end = o;
-    o = temps;
-    y.m_list = take(E * 2);
     if (o > end) end = o;
     y.env_bytes = align16(end);
     int best = 0, best_wpb = 0;
@@ -931,11 +924,14 @@ __global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_s
 }
 
 // After core.step: outcome, rewards, optional final observation, auto-reset.
+// `known` / `known_time`: the cycle's outcome and time from decide_counted
+// and complete, when the caller holds them (else read from the env).
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
-                        const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true) {
-    const bool over = uni(e.sc[S_GAME_OVER]) != 0;
-    const int32_t time = uni(e.sc[S_TIME]);
-    const int32_t winner = uni(e.sc[S_WINNER]);
+                        const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true,
+                        const Outcome* known = nullptr, int32_t known_time = 0) {
+    const bool over = known ? known->over != 0 : uni(e.sc[S_GAME_OVER]) != 0;
+    const int32_t time = known ? known_time : uni(e.sc[S_TIME]);
+    const int32_t winner = known ? known->winner : uni(e.sc[S_WINNER]);
     const bool trunc = !over && time >= g.max_cycles;
     const bool done = over || trunc;
     if (lane == 0) {
@@ -1245,14 +1241,6 @@ NR_DEV Env wave_env(const KGame& g, int wave) {
     const Env e = wave_env(g, wave);                  \
     (void)hdr;
 
-// Live slots of the staged env (wave-uniform).
-NR_DEV int32_t live_slots(const KGame& g, const Env& e) {
-    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
-    int32_t n = 0;
-    for (int32_t w = 0; w * kWave < g.E; ++w) n += popc(live[w]);
-    return uni(n);
-}
-
 // The cycles of one launch.  `Lean` is the first pass of the two-pass
 // launch (k_rollout_lean, on shape_for_lean's block): before each cycle it
 // checks that the cycle stays on the one-wave path (a regular state with at
@@ -1424,16 +1412,22 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         }
         {
             NR_ROLLOUT_PHASE
-            complete(g, hdr, e, lane, Lean);
-            decide_counted(e, lane);
+            int32_t time = complete(g, hdr, e, lane, Lean);
+            Outcome oc = decide_counted(e, lane);
             nanorts_env_results r = {};
             const int64_t tt = (int64_t)a.t0 + t;
             if (a.out.rewards) r.reward = a.out.rewards + tt * lanes * 2;
             if (a.out.dones) r.done = a.out.dones + tt * lanes;
-            if (finish_step(g, hdr, e, l, lane, a.partial != 0, r, false)) {
+            const bool done = finish_step(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
+            if (done) {
                 ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
                 ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
                 fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+                // the published observation is the reset state's
+                time = uni(e.sc[S_TIME]);
+                oc.res0 = uni(e.sc[S_RES0]);
+                oc.res1 = uni(e.sc[S_RES1]);
+                oc.alt = uni(e.sc[S_ALT]);
             }
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
@@ -1443,12 +1437,17 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             const int64_t slot = (int64_t)ring * lanes + l;
             if (fast) {
                 uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
-                int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
+                if (out.scalars && lane < 8) {
+                    // the scalars from registers: own balance, the opponent's,
+                    // time, alternating count (as summarize writes them)
+                    const int32_t pl = lane >> 2, f = lane & 3;
+                    const int32_t own = pl == 0 ? oc.res0 : oc.res1, opp = pl == 0 ? oc.res1 : oc.res0;
+                    out.scalars[slot * 8 + lane] = f == 0 ? own : (f == 1 ? opp : (f == 2 ? time : oc.alt));
+                }
                 // the sight bitmaps persist in the event counters' words, which
                 // the rollout does not count, when both planes fit there
                 const int32_t kept = 2 * g.H * g.seen_words <= 32 ? g.lay.b_events : -1;
-                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr,
-                          kept);
+                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
             } else if (out.feature_maps || out.scalars) {
                 observe_both(g, hdr, e, slot, lane, a.partial != 0, out.feature_maps, out.scalars);
             }

@@ -18,30 +18,7 @@
 
 namespace nr {
 
-// k-th set bit (0-based) of m by halving popcounts; m has more than k bits.
-NR_DEV int32_t select_bit(uint64_t m, int32_t k) {
-    int32_t pos = 0;
-    uint32_t v = (uint32_t)m;
-    const int32_t c32 = popc((uint64_t)v);
-    if (k >= c32) {
-        k -= c32;
-        v = (uint32_t)(m >> 32);
-        pos = 32;
-    }
-#pragma unroll
-    for (int32_t half = 16; half >= 1; half >>= 1) {
-        const uint32_t lowmask = (1u << half) - 1u;
-        const int32_t c = __popc(v & lowmask);
-        if (k >= c) {
-            k -= c;
-            v >>= half;
-            pos += half;
-        }
-    }
-    return pos;
-}
-
-// sample_row with the select above (same draws, same result), given the
+// sample_row with select_bit (same draws, same result), given the
 // position's four draw words threefry(k_step, (env, 2p)) ++ threefry(k_step, (env, 2p + 1)).
 NR_DEV void sample_row_words(const KGame& g, const Row& r, const uint32_t words[4], int32_t a[7]) {
     if (only_none(r)) {
@@ -274,13 +251,12 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
     // only live slots hold units or pending actions
-    AS3 int16_t* slots = at<int16_t>(e, y.o_slist);
-    const int32_t nlive = live_list(g, e, lane, slots);
+    const int32_t nlive = live_slots(g, e);
     int32_t nav = 0, nunits = 0, nA = 0;
     bool odd = false;
     for (int32_t base = 0; base < nlive; base += kWave) {
         const int32_t i = base + lane;
-        const int32_t s = i < nlive ? slots[i] : 0;
+        const int32_t s = i < nlive ? live_slot_at(g, e, i) : 0;
         bool alive = false, available = false, entry = false;
         if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
