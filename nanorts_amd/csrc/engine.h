@@ -113,7 +113,7 @@ struct Layout {
     int32_t v_seen, v_stage, b_units;
     int32_t v_oseen;  // observe_all's seen bitmaps (beside its staging)
     int32_t v_words;
-    int32_t a_av, a_fk, a_fn, a_list;  // env-path admission: available list, final kinds/durations, entry list
+    int32_t a_av, a_list;  // env-path admission: available list, entry list
 };
 
 // Kernel-side copy of the game (passed by value as a kernel argument).

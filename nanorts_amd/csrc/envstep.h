@@ -245,8 +245,8 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
     // Sequential conflict resolution over the requests that can conflict.
     const int32_t bal0 = uni(e.sc[S_RES0]), bal1 = uni(e.sc[S_RES1]);
     int32_t alt = uni(e.sc[S_ALT]);
-    AS3 int32_t* fk = at<int32_t>(e, y.a_fk);
-    AS3 int32_t* fn = at<int32_t>(e, y.a_fn);
+    // each request's final kind and duration, held in its own lane
+    int32_t my_kind = kind1, my_none = none1;
     int32_t posB = 0, costB = 0, playerB = 0, durB = 0, rlB = 0, nB = 0;
     bool liveB = false;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -295,21 +295,26 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
             int32_t excl = __shfl_up(incl, 1u, kWave);
             if (lane == 0) excl = kNoCap;
             const int32_t before = anyA ? -1 : imin(rreq, excl);
-            if (cB && cancels_pend) {
-                const int32_t settled = wadd(wmul(imin(durB, before), 2), 1) >> 1;
-                liveB = false;
-                fk[rlB] = kKindNone;
-                fn[rlB] = settled;
+            const bool cancelled = cB && cancels_pend;
+            const int32_t settled = wadd(wmul(imin(durB, before), 2), 1) >> 1;
+            // each cancelled same-cycle entry settles its request's lane
+            for (uint64_t m = ballot(cancelled); m != 0ull; m &= m - 1ull) {
+                const int32_t b = (int32_t)__builtin_ctzll(m);
+                if (lane == __builtin_amdgcn_readlane(rlB, b)) {
+                    my_kind = kKindNone;
+                    my_none = __builtin_amdgcn_readlane(settled, b);
+                }
             }
+            if (cancelled) liveB = false;
             if (g.strategy == NANORTS_CANCEL_ALTERNATING) alt = wadd(alt, popc(sm));
             if (anyA || cap != kNoCap) {
                 fkind = kKindNone;
                 fnone = anyA ? -1 : imin(rreq, cap);
             }
         }
-        if (lane == 0) {
-            fk[li] = fkind;
-            fn[li] = fnone;
+        if (lane == li) {
+            my_kind = fkind;
+            my_none = fnone;
         }
         if (fkind != kKindNone) {
             // admitted as MOVE / PRODUCE: a same-cycle entry from now on
@@ -323,15 +328,10 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
             }
             ++nB;
         }
-        wave_sync();
     }
     // _assign_pending_action (:374-403) for every request, in parallel.
     if (lane < n) {
-        int32_t fkind = kind1, fnone = none1;
-        if (conflicting) {
-            fkind = fk[lane];
-            fnone = fn[lane];
-        }
+        const int32_t fkind = my_kind, fnone = my_none;
         const int32_t duration = fkind == kKindNone ? fnone : req;
         e.pkind[slot] = (int8_t)fkind;
         e.pdir[slot] = (int8_t)((fkind == kKindMove || fkind == kKindHarvest || fkind == kKindReturn ||

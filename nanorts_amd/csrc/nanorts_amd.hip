@@ -194,8 +194,7 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     //   persistent from the summary to sampling / admission: bitmaps,
     //     available list, entry list after them;
     //   temporaries: the summary's occupant words, unit list and seen
-    //     bitmaps over the (then dead) command arrays; the fast admission's
-    //     final kinds / durations after the entry list; the general
+    //     bitmaps over the (then dead) command arrays; the general
     //     admission's keys and lists over everything but the command
     //     arrays; completion records and observation staging over all.
     const int32_t union0 = o;
@@ -209,8 +208,6 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_bm = take(6 * g.H * g.seen_words * 4);
     y.a_av = take(C2 * 2);
     y.a_list = take(E * 2);
-    y.a_fk = take(kWave * 4);
-    y.a_fn = take(kWave * 4);
     int32_t end = o;
     // general admission
     o = commands_end;
@@ -278,8 +275,9 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
 
 // Resident waves per SIMD the first pass of the fused rollout is sized for,
 // and its largest workgroup, in games.  Measured at 16x16 on the bench
-// workload: 5 waves per SIMD (20 games per CU in workgroups of 5 or 10
-// games, 90 VGPRs) ran 17 % slower than 4 (16 games in workgroups of 4).
+// workload: workgroups of 5 or 10 games (20 games per CU) ran 17 % slower
+// than workgroups of 4, whose waves fall one to a SIMD.  The hardware still
+// places a fifth workgroup of 4 on a CU where LDS and registers allow it.
 constexpr int kLeanWavesPerSimd = 4;
 constexpr int kLeanMaxGames = 4;
 
@@ -305,9 +303,8 @@ int32_t games_per_cu(const Layout& y, int wpb, int waves_per_simd) {
 // The layout of the fused rollout's first pass (k_rollout_lean).  The state
 // rows keep their offsets; the phase union holds only what a cycle on the
 // one-wave path uses: the summary's bitmaps and lists that persist into the
-// next cycle's sampling and admission, the summary's temporaries, and over
-// those (dead by then) the admission's final kinds and durations.  A cycle
-// that would need more (an irregular state,
+// next cycle's sampling and admission, and the summary's temporaries.  A
+// cycle that would need more (an irregular state,
 // more than 64 available units or live slots) is left to the second pass,
 // on the full block.  The command arrays, the request-by-request
 // admission's keys, completion's member records and the staging of the
@@ -335,7 +332,6 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     y.o_bm = take(6 * plane * 4);
     y.a_av = take(C2 * 2);
     y.a_list = take(kWave * 2);
-    const int32_t temps = o;
     y.o_lo = take((E + 1) * 4);
     y.o_fl = take(E + 1);
     y.b_units = take(C2 * 2);
@@ -343,10 +339,6 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     // planes fit there, else the summary stamps them here
     y.v_seen = 2 * plane <= 32 ? 0 : take(2 * plane * 4);
     int32_t end = o;
-    o = temps;
-    y.a_fk = take(kWave * 4);
-    y.a_fn = take(kWave * 4);
-    if (o > end) end = o;
     y.env_bytes = align16(end);
     int best = 0, best_wpb = 0;
     for (int wpb = 1; wpb <= kLeanMaxGames; ++wpb) {
