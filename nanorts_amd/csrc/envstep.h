@@ -125,7 +125,7 @@ NR_DEV void no_request(Reqs& q) {
 // summary of the state (rollout.h) already listed them and folded their
 // preconditions into `irregular`.  Lane i < nA receives entry i.
 NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, bool listed, int32_t* nA_out,
-                          int32_t* posA, int32_t* costA, int32_t* playerA) {
+                          int32_t* posA, int32_t* costA, int32_t* playerA, int32_t listed_count = -1) {
     const Layout& y = g.lay;
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
@@ -133,7 +133,8 @@ NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, 
     AS3 int16_t* list = at<int16_t>(e, y.a_list);
     int32_t nA = 0;
     bool bad = false;
-    if (listed) nA = uni(e.sc[S_NA]);
+    // the summary's count, from the caller's registers when it holds it
+    if (listed) nA = listed_count >= 0 ? listed_count : uni(e.sc[S_NA]);
     for (int32_t base = 0; base < (listed ? 0 : g.E); base += kWave) {
         const int32_t s = base + lane;
         bool entry = false;

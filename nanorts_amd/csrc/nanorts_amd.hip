@@ -1274,7 +1274,9 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
     count_units(g, e, lane);
     // the first pass runs only where this holds (the host checks it)
     const bool fast = Lean || (g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0));
-    if (fast) summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    // the summary's counts stay in registers from one cycle into the next
+    SlotSummary sm = {0, 0, 0, 0, false};
+    if (fast) sm = summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
     const int32_t steps = args.steps;
@@ -1292,7 +1294,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
-            if (Lean && (uni(e.sc[S_IRREG]) != 0 || uni(e.sc[S_NAV]) > kWave || live_slots(g, e) > kWave)) {
+            if (Lean && (sm.irregular || sm.nav > kWave || sm.nlive > kWave)) {
                 stop = t;
                 break;
             }
@@ -1300,8 +1302,8 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             const int32_t owned = 2 * g.C;
             const int64_t tt = (int64_t)a.t0 + t;  // cycle index within the caller's rollout
             if (fast) {
-                n = uni(e.sc[S_NAV]);
-                irregular = uni(e.sc[S_IRREG]) != 0;
+                n = sm.nav;
+                irregular = sm.irregular;
                 fused = Lean || (!irregular && n <= kWave);
             } else {
                 n = compact_available(g, e, lane, &irregular);
@@ -1309,7 +1311,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             }
             // the pending entries of the admission, loaded early so their
             // latency overlaps the sampling
-            if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
+            if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA, sm.nA);
             const uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
             const uint32_t env = (uint32_t)(a.env0 + l);
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
@@ -1439,7 +1441,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                 // the sight bitmaps persist in the event counters' words, which
                 // the rollout does not count, when both planes fit there
                 const int32_t kept = 2 * g.H * g.seen_words <= 32 ? g.lay.b_events : -1;
-                summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
+                sm = summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
             } else if (out.feature_maps || out.scalars) {
                 observe_both(g, hdr, e, slot, lane, a.partial != 0, out.feature_maps, out.scalars);
             }

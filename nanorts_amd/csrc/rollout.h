@@ -234,7 +234,14 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
 // `bitmaps`) the six occupancy bitmaps of the next cycle's masks, stamped per
 // live slot over the wall rows: 0 blocked (occupied or wall), 1 / 2 units of
 // player 0 / 1, 3 resources, 4 / 5 stockpiles of player 0 / 1.
-NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
+// What the slot pass lists, wave-uniform, for callers that keep it in
+// registers into the next cycle rather than reading it back from the env.
+struct SlotSummary {
+    int32_t nav, nunits, nA, nlive;
+    bool irregular;
+};
+
+NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t words = g.seen_words, plane = g.H * words;
@@ -325,6 +332,13 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
         e.sc[S_IRREG] = irregular ? 1 : 0;
     }
     wave_sync();
+    SlotSummary out;
+    out.nav = uni(nav);
+    out.nunits = uni(nunits);
+    out.nA = uni(nA);
+    out.nlive = nlive;
+    out.irregular = irregular;
+    return out;
 }
 
 // Sight disks of both players into seen[2][H][words].  With H <= 32 a lane
@@ -335,12 +349,11 @@ NR_DEV void summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int l
 // Sight bitmaps of the players whose bit is set in `which` (the others'
 // planes are left as they are).
 NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane, int32_t seen_at,
-                                 int32_t which) {
+                                 int32_t which, int32_t nunits) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     AS3 uint32_t* seen = at<uint32_t>(e, seen_at);
     const int32_t words = g.seen_words, plane = g.H * words;
-    const int32_t nunits = uni(e.sc[S_NUNITS]);
     AS3 const int16_t* units = at<int16_t>(e, y.b_units);
     const int32_t R = g.disk_r, span = 2 * R + 1;
     if (g.H <= 32 && words == 1) {
@@ -498,13 +511,13 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
 // `kept_seen` >= 0 is the LDS offset of sight bitmaps kept from the last
 // summary: they are stamped again only for a state whose units moved,
 // spawned or died since (S_VISDIRTY).
-NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool partial, uint8_t* maps0,
-                      uint8_t* maps1, int32_t* scalars0, int32_t* scalars1, int32_t kept_seen = -1) {
-    summarize_slots(g, h, e, lane);
+NR_DEV SlotSummary summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool partial, uint8_t* maps0,
+                             uint8_t* maps1, int32_t* scalars0, int32_t* scalars1, int32_t kept_seen = -1) {
+    const SlotSummary sm = summarize_slots(g, h, e, lane);
     const int32_t seen_at = kept_seen >= 0 ? kept_seen : g.lay.v_seen;
     const int32_t which = kept_seen >= 0 ? uni(e.sc[S_VISDIRTY]) & 3 : 3;
     if (partial && maps0 && which != 0) {
-        summarize_visibility(g, h, e, lane, seen_at, which);
+        summarize_visibility(g, h, e, lane, seen_at, which, sm.nunits);
         if (kept_seen >= 0 && lane == 0) e.sc[S_VISDIRTY] = 0;
     }
     if (maps0) summarize_cells(g, h, e, lane, partial, false, maps0, maps1, seen_at);
@@ -517,6 +530,7 @@ NR_DEV void summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool
         else v = e.sc[S_ALT];
         (pl == 0 ? scalars0 : scalars1)[f] = v;
     }
+    return sm;
 }
 
 // The available owned positions in slot order (the summary's list, again,
