@@ -1511,7 +1511,9 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
     // available list, kept sight bitmaps, packed observation stores), as in
     // the fused rollout
     const bool fast = g.fast_obs && g.seen_words == 1 && ((((uintptr_t)out.feature_maps) & 7u) == 0);
-    if (fast) summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    // the summary's counts stay in registers from one cycle into the next
+    SlotSummary sm = {0, 0, 0, 0, false};
+    if (fast) sm = summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     for (int32_t t = 0; t < args.steps; ++t) {
         const int64_t tt = (int64_t)args.t0 + t;
         if (args.seat_record && lane == 0) args.seat_record[tt * lanes + l] = learner;
@@ -1519,7 +1521,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         const uint32_t ke0 = args.step_keys[2 * t], ke1 = args.step_keys[2 * t + 1];
         const AS3 int16_t* av = at<int16_t>(e, y.a_av);
         if (fast) {
-            const int32_t n = uni(e.sc[S_NAV]);
+            const int32_t n = sm.nav;
             mark_unavailable(g, e, lane);
             const Affordable aff = affordable_types(g, hdr, e, lane);
             // both threefry blocks of a position on two lanes when n <= 32
@@ -1623,17 +1625,25 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             // their available units.  The bot's region lay over the summary's
             // lists, so the available positions are listed again.
             const int32_t nav = list_available(g, e, lane);
-            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, nav, uni(e.sc[S_IRREG]) != 0, false))
+            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, nav, sm.irregular, false))
                 admit(g, hdr, e, lane, ek0, ek1, false);
-            complete(g, hdr, e, lane);
-            decide_counted(e, lane);
+        }
+        // completion's time and the outcome stay in registers into the
+        // finish phase and the observation scalars
+        int32_t time = 0;
+        Outcome oc = {0, 0, 0, 0, 0};
+        if (fast) {
+            time = complete(g, hdr, e, lane);
+            oc = decide_counted(e, lane);
         } else {
             core_step(g, hdr, e, lane, ek0, ek1, false);
         }
         nanorts_env_results r = {};
         if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
         if (out.dones) r.done = out.dones + tt * lanes;
-        if (finish_step(g, hdr, e, l, lane, args.partial != 0, r, false)) {
+        const bool done = finish_step(g, hdr, e, l, lane, args.partial != 0, r, false, false, true,
+                                      fast ? &oc : nullptr, time);
+        if (done) {
             clear_carry_rows(g, b, ba.y, lane);
             ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
             ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
@@ -1643,6 +1653,11 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
                 b.player = 1 - learner;
                 b.block = g.N + b.player * g.C;
             }
+            // the published observation is the reset state's
+            time = uni(e.sc[S_TIME]);
+            oc.res0 = uni(e.sc[S_RES0]);
+            oc.res1 = uni(e.sc[S_RES1]);
+            oc.alt = uni(e.sc[S_ALT]);
         }
         const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
         const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
@@ -1650,12 +1665,16 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         if (fast) {
             const int64_t per = (int64_t)g.cells * 6;
             uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
-            int32_t* s0 = out.scalars ? out.scalars + slot * 8 : nullptr;
+            if (out.scalars && lane < 8) {
+                // own balance, the opponent's, time, alternating count
+                const int32_t pl = lane >> 2, f = lane & 3;
+                const int32_t own = pl == 0 ? oc.res0 : oc.res1, opp = pl == 0 ? oc.res1 : oc.res0;
+                out.scalars[slot * 8 + lane] = f == 0 ? own : (f == 1 ? opp : (f == 2 ? time : oc.alt));
+            }
             // the sight bitmaps persist in the event counters' words, which
             // the seat step does not count, when both planes fit there
             const int32_t kept = 2 * g.H * g.seen_words <= 32 ? y.b_events : -1;
-            summarize(g, hdr, e, lane, args.partial != 0, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr,
-                      kept);
+            sm = summarize(g, hdr, e, lane, args.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
         } else if (out.feature_maps || out.scalars) {
             observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
