@@ -27,6 +27,13 @@ horizons 5000, 4000, 3000 and 2000: one bucket), each cycle stepping every
 group on uniformly random Commands (a pool of eight sets held in HBM) with
 one nanorts_amd_step_groups launch; one launch per group is timed beside it.
 
+`--workload gow` measures the GardenOfWar64x64 configuration: CANCEL_ALTERNATING,
+the slot count without the capacity profile, 4096 games of symbolic
+observations in the fused rollout (500 steps by the configuration), and 256
+games on the pixel surface (both agents' uint8[1024, 1024, 3] images every
+cycle) through the per-call path, reported in `pixel_leg` with the render
+kernel's own bandwidth.
+
 Prints one JSON line (rank 0, N=1).
 """
 from __future__ import annotations
@@ -62,7 +69,7 @@ GROUP_HORIZONS = (5000, 4000, 3000, 2000)
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush", "gridnet", "groups"),
+    ap.add_argument("--workload", choices=("headline", "seat-workerrush", "seat-lightrush", "gridnet", "groups", "gow"),
                     default="headline")
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
@@ -73,6 +80,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-envs", type=int, default=4096)
     ap.add_argument("--cpu-steps", type=int, default=3000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pixel-steps", type=int, default=20, help="gow: cycles of the pixel leg")
     ap.add_argument("--one-pass", action="store_true",
                     help="headline: run each launch as one pass on the full LDS block (no two-pass launch)")
     ap.add_argument("--traffic", choices=("auto", "off"), default="auto")
@@ -80,7 +88,8 @@ def parse() -> argparse.Namespace:
                     help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.envs is None:
-        args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS, "groups": GROUP_ENVS}.get(args.workload, SEAT_ENVS)
+        args.envs = {"headline": NUM_ENVS, "gridnet": GRID_ENVS, "groups": GROUP_ENVS,
+                     "gow": GOW_ENVS}.get(args.workload, SEAT_ENVS)
     return args
 
 
@@ -642,6 +651,116 @@ def core_step_bytes(bucket) -> int:
     return 2 * state_bytes(bucket) + 6 * 2 * C * 4 + 2 + 8 + 4 * (2 + 2 + 2 * T + 6)
 
 
+GOW_MAP = "GardenOfWar64x64"
+GOW_ENVS = 4096
+GOW_PIXEL_ENVS = 256
+
+
+def main_gow(args) -> None:
+    """The GardenOfWar64x64 configuration: CANCEL_ALTERNATING, the slot count
+    without the capacity profile, 4096 games of symbolic observations in the
+    fused rollout, and 256 games on the pixel surface (uint8[1024, 1024, 3]
+    images of both agents each cycle) through the per-call path."""
+    import torch
+
+    import nanorts_amd
+    from nanorts_amd import env as envmod
+
+    torch.cuda.set_device(0)
+    game = nanorts_amd.map_name_to_scenario(GOW_MAP, conflict_strategy="CANCEL_ALTERNATING", capacity_profile=False)
+    b = game.bucket
+    L = args.envs
+    chunk = max(1, min(args.chunk, args.steps))
+    env = nanorts_amd.make("NanoRTS", scenario=game, final_observation=False, device="cuda:0")
+    _, state = env.reset(envmod.env_roots(0, L))
+    run_rollout(env, state, args.warmup, chunk, args.depth, 0)
+    torch.cuda.synchronize()
+    progress(f"{args.warmup} warmup cycles done")
+    t0 = time.perf_counter()
+    times = run_rollout(env, state, args.steps, chunk, args.depth, args.warmup, events=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [a.elapsed_time(e) for a, e, _ in times]
+    full = [ms for (a, e, n), ms in zip(times, launch_ms) if n == chunk] or launch_ms
+    avg_launch_s = sum(full) / len(full) / 1e3
+    per_step, sbytes = step_bytes(b), state_bytes(b)
+    per_launch_bytes = L * (chunk * per_step + 2 * sbytes)
+    achieved = per_launch_bytes / avg_launch_s / 1e9
+
+    # the pixel leg: masks -> sampler -> env.step, whose observation is both
+    # agents' images rendered from the step's symbolic maps
+    P = GOW_PIXEL_ENVS
+    penv = nanorts_amd.make("NanoRTS", scenario=game, surface="pixels", final_observation=False, device="cuda:0")
+    _, pstate = penv.reset(envmod.env_roots(1, P))
+    image_bytes = 2 * (16 * b.height) * (16 * b.width) * 3
+
+    def pixel_cycles(n, base):
+        nonlocal pstate
+        for t in range(n):
+            words = penv.get_avail_actions(pstate, form="words")
+            acts = penv.sample_actions(words, (11, 13), base + t)
+            _, pstate, _, _, _ = penv.step(None, pstate, acts, donate=True)
+
+    pixel_cycles(3, 0)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    pixel_cycles(args.pixel_steps, 3)
+    torch.cuda.synchronize()
+    pixel_rate = P * args.pixel_steps / (time.perf_counter() - t1)
+    # the render kernel alone, on symbolic maps of P of the rollout's games
+    sym = env.get_obs(state)
+    maps_p = torch.stack([sym[a].feature_maps[:P] for a in env.agents], 1).contiguous()
+    a_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    penv.pixels_from_maps(maps_p)
+    torch.cuda.synchronize()
+    a_ev.record()
+    reps = 5
+    for _ in range(reps):
+        penv.pixels_from_maps(maps_p)
+    e_ev.record()
+    torch.cuda.synchronize()
+    render_s = a_ev.elapsed_time(e_ev) / reps / 1e3
+    render_gbps = P * image_bytes / render_s / 1e9
+
+    line = {
+        "metric": f"env-steps/sec (both players) at {GOW_MAP} x {L} envs (symbolic) + {P} envs (pixels); "
+                  "% HBM roofline",
+        "value": round(L * args.steps / wall, 1),
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": f"synthetic: seeded uniform-random legal actions from the shipped {GOW_MAP} map",
+        "config": {
+            "workload": f"{GOW_MAP}, VERSION_ORIGINAL_FINETUNED, CANCEL_ALTERNATING, capacity_profile=False "
+                        f"({b.per_player_capacity} slots per player), {L} games symbolic in the fused rollout "
+                        f"({chunk} cycles per launch), {P} games on the pixel surface",
+            "games": L, "slots_per_player": b.per_player_capacity, "entity_capacity": b.entity_capacity,
+            "algorithmic_bytes_per_env_step": per_step, "state_bytes_per_env": sbytes,
+            "observation_ring_depth": args.depth,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "k_rollout_lean + k_rollout (second pass)", "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "algorithmic_bytes_per_launch": per_launch_bytes, "cycles_per_launch": chunk,
+        },
+        "pixel_leg": {
+            "games": P, "steps": args.pixel_steps, "env_steps_per_s": round(pixel_rate, 1),
+            "image_bytes_per_env_step": image_bytes,
+            "render_kernel": "k_pixels_from_maps", "render_ms": round(render_s * 1e3, 4),
+            "render_GBps": round(render_gbps, 1), "render_frac": round(render_gbps / HBM_PEAK_GBPS, 4),
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+
+
 def main_groups(args) -> None:
     import numpy as np
     import torch
@@ -777,6 +896,9 @@ def main() -> None:
         return
     if args.workload == "groups":
         main_groups(args)
+        return
+    if args.workload == "gow":
+        main_gow(args)
         return
     if args.workload != "headline":
         main_seat(args)
