@@ -1897,58 +1897,79 @@ __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_
 // thread writes one 16-pixel (48-byte) sprite row of one cell; consecutive
 // threads take consecutive cells of one image row, so a wave's stores are
 // contiguous.  HBM-write-bound: 768 bytes written per cell per image.
-__global__ __launch_bounds__(256) void k_pixels_from_maps(int32_t H, int32_t W, int32_t T, int64_t images,
-                                                          const uint8_t* maps, const uint8_t* tiles, uint8_t* image) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t per_image = (int64_t)H * 16 * W;
-    if (t >= images * per_image) return;
-    const int64_t m = t / per_image;
-    const int32_t r = (int32_t)(t - m * per_image);
-    const int32_t Y = r / W, cx = r - Y * W;
-    const int32_t cy = Y >> 4, py = Y & 15;
-    const uint8_t* f = maps + ((m * H + cy) * W + cx) * 6;
-    const int32_t hp = f[0], carried = f[1], owner = (int32_t)f[2] - 1, type = f[3], kind = f[4], terrain = f[5];
-    const bool present = type != 0;
-    const int32_t states = 1 + 3 * T;
-    const int32_t occupant = present ? 1 + (owner + 1) * T + (type - 1) : 0;
-    const int32_t tile = gidx(terrain * states + occupant, 2 * states);
-    const u32x4* src = (const u32x4*)(tiles + (int64_t)tile * 768 + py * 48);
-    u32x4 v[3] = {src[0], src[1], src[2]};
-    if (present && py >= 12 && py <= 14) {
-        uint8_t px[48];
+// One thread per cell row: 16 pixels x RGB = 48 bytes from the cell's tile
+// row, with the glyph bands (rows 12-14 of an occupied cell: action,
+// carried resources, hit points; N/rendering/raster.py:53-127) drawn over
+// pixels 1-14.  A wave's 64 cell rows are consecutive in the image, so its
+// 3 KB of output are too: the rows are staged in LDS and stored back as
+// chunks 16 bytes apart across the lanes, each store instruction writing
+// 1 KB of consecutive bytes.  Grid: x = 256 cell rows, y (+ 65535 z) = image.
+constexpr int kPixelWaves = 4;
+__global__ __launch_bounds__(kPixelWaves * 64) void k_pixels_from_maps(int32_t H, int32_t W, int32_t T, int32_t wshift,
+                                                                       int64_t images, const uint8_t* maps,
+                                                                       const uint8_t* tiles, uint8_t* image) {
+    __shared__ u32x4 stage[kPixelWaves * kWave * 3];
+    const int64_t m = (int64_t)blockIdx.z * 65535 + blockIdx.y;
+    if (m >= images) return;
+    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+    const int32_t per_image = 16 * H * W;  // cell rows of one image
+    const int32_t n0 = (int32_t)blockIdx.x * (kPixelWaves * kWave) + wave * kWave;  // the wave's first
+    if (n0 >= per_image) return;
+    const int32_t n = n0 + lane;
+    AS3 u32x4* mine = (AS3 u32x4*)stage + wave * kWave * 3;
+    if (n < per_image) {
+        const int32_t Y = wshift >= 0 ? n >> wshift : n / W;
+        const int32_t cx = n - Y * W;
+        const int32_t cy = Y >> 4, py = Y & 15;
+        const uint8_t* f = maps + ((m * H + cy) * W + cx) * 6;
+        const int32_t hp = f[0], carried = f[1], owner = (int32_t)f[2] - 1, type = f[3], kind = f[4], terrain = f[5];
+        const bool present = type != 0;
+        const int32_t states = 1 + 3 * T;
+        const int32_t occupant = present ? 1 + (owner + 1) * T + (type - 1) : 0;
+        const int32_t tile = gidx(terrain * states + occupant, 2 * states);
+        const u32x4* src = (const u32x4*)(tiles + (int64_t)tile * 768 + py * 48);
+        u32x4 v[3] = {src[0], src[1], src[2]};
+        if (present && py >= 12 && py <= 14) {
+            // lit pixels of the band row as a bit set over pixels 1..14
+            uint32_t lit = 0u;
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t w = v[k][j];
-                px[16 * k + 4 * j + 0] = (uint8_t)w;
-                px[16 * k + 4 * j + 1] = (uint8_t)(w >> 8);
-                px[16 * k + 4 * j + 2] = (uint8_t)(w >> 16);
-                px[16 * k + 4 * j + 3] = (uint8_t)(w >> 24);
+            for (int32_t x = 1; x < 15; ++x) {
+                const int32_t position = x - 1;
+                bool on;
+                if (py == 12) on = kind == position + 1;
+                else if (py == 13) on = ((carried >> position) & 1) != 0;
+                else on = hp > position;
+                lit |= (on ? 1u : 0u) << x;
             }
 #pragma unroll
-        for (int x = 1; x < 15; ++x) {
-            const int32_t position = x - 1;
-            bool lit;
-            if (py == 12) lit = kind == position + 1;
-            else if (py == 13) lit = ((carried >> position) & 1) != 0;
-            else lit = hp > position;
-            const uint8_t c = lit ? 0xFF : 0x00;
-            px[3 * x] = px[3 * x + 1] = px[3 * x + 2] = c;
+            for (int k = 0; k < 3; ++k)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t w = v[k][j];
+#pragma unroll
+                    for (int bi = 0; bi < 4; ++bi) {
+                        const int32_t x = (16 * k + 4 * j + bi) / 3;  // the byte's pixel
+                        if (x >= 1 && x <= 14) {
+                            const uint32_t c = ((lit >> x) & 1u) ? 0xFFu : 0x00u;
+                            w = (w & ~(0xFFu << (8 * bi))) | (c << (8 * bi));
+                        }
+                    }
+                    v[k][j] = w;
+                }
         }
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int b = 16 * k + 4 * j;
-                v[k][j] = (uint32_t)px[b] | ((uint32_t)px[b + 1] << 8) | ((uint32_t)px[b + 2] << 16) |
-                          ((uint32_t)px[b + 3] << 24);
-            }
+        for (int k = 0; k < 3; ++k) mine[3 * lane + k] = v[k];
     }
-    u32x4* dst = (u32x4*)(image + (m * H * 16 + Y) * (int64_t)W * 48 + (int64_t)cx * 48);
-    dst[0] = v[0];
-    dst[1] = v[1];
-    dst[2] = v[2];
+    wave_sync();
+    const int32_t valid = per_image - n0 < kWave ? per_image - n0 : kWave;  // cell rows in this wave
+    u32x4* out = (u32x4*)(image + (m * per_image + n0) * 48);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int32_t c = k * kWave + lane;  // the 16-byte chunk of the wave's run
+        // the images are written once and not read back by this kernel:
+        // streaming (non-temporal) stores
+        if (c < 3 * valid) __builtin_nontemporal_store((u32x4)mine[c], out + c);
+    }
 }
 
 // wave64 semantics probe: ballot, mbcnt prefix counts, shuffles, prefix-min.
@@ -2508,11 +2529,17 @@ int nanorts_amd_pixels_from_maps(void* stream, const nanorts_game* game, int64_t
     if (!feature_maps || !tiles || !image) return fail(NANORTS_INVALID_ARGUMENT, "feature_maps, tiles and image are required");
     if ((((uintptr_t)tiles) & 15u) != 0 || (((uintptr_t)image) & 15u) != 0)
         return fail(NANORTS_INVALID_ARGUMENT, "tiles and image must be 16-byte aligned");
-    const int64_t threads = images * (int64_t)game->height * 16 * game->width;
-    const int64_t blocks = (threads + 255) / 256;
-    if (blocks > 0x7fffffffLL) return fail(NANORTS_INVALID_ARGUMENT, "too many images for one launch");
-    hipLaunchKernelGGL(k_pixels_from_maps, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, game->height,
-                       game->width, game->types, images, feature_maps, tiles, image);
+    const int64_t rows = (int64_t)game->height * 16 * game->width;  // cell rows of one image
+    const int64_t per_block = kPixelWaves * kWave;
+    const int64_t zs = (images + 65534) / 65535;
+    if (zs > 65535) return fail(NANORTS_INVALID_ARGUMENT, "too many images for one launch");
+    int32_t wshift = -1;
+    for (int32_t b = 0; b < 16; ++b)
+        if ((1 << b) == game->width) wshift = b;
+    const dim3 grid((unsigned)((rows + per_block - 1) / per_block), (unsigned)(images < 65535 ? images : 65535),
+                    (unsigned)zs);
+    hipLaunchKernelGGL(k_pixels_from_maps, grid, dim3((unsigned)per_block), 0, (hipStream_t)stream, game->height,
+                       game->width, game->types, wshift, images, feature_maps, tiles, image);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("k_pixels_from_maps launch: ") + hipGetErrorString(err));
     return NANORTS_OK;
