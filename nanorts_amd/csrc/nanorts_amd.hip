@@ -1893,17 +1893,15 @@ __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_
 // Pixel observations from symbolic feature maps (pixels_from_symbolic,
 // N/observations/pixels.py:91-110): the maps carry presence (type != 0),
 // the observer-relative owner, type, pending kind, carried resources, hit
-// points and terrain, which is all the tile pick and glyph band read.  One
-// thread writes one 16-pixel (48-byte) sprite row of one cell; consecutive
-// threads take consecutive cells of one image row, so a wave's stores are
-// contiguous.  HBM-write-bound: 768 bytes written per cell per image.
-// One thread per cell row: 16 pixels x RGB = 48 bytes from the cell's tile
-// row, with the glyph bands (rows 12-14 of an occupied cell: action,
-// carried resources, hit points; N/rendering/raster.py:53-127) drawn over
-// pixels 1-14.  A wave's 64 cell rows are consecutive in the image, so its
-// 3 KB of output are too: the rows are staged in LDS and stored back as
-// chunks 16 bytes apart across the lanes, each store instruction writing
-// 1 KB of consecutive bytes.  Grid: x = 256 cell rows, y (+ 65535 z) = image.
+// points and terrain, which is all the tile pick and glyph band read.
+// HBM-write-bound: 768 bytes written per cell per image.  One thread per
+// cell row: 16 pixels x RGB = 48 bytes from the cell's tile row, with the
+// glyph bands (rows 12-14 of an occupied cell: action, carried resources,
+// hit points; N/rendering/raster.py:53-127) drawn over pixels 1-14.  A
+// wave's 64 cell rows are consecutive in the image, so its 3 KB of output
+// are too: the rows are staged in LDS and stored back as chunks 16 bytes
+// apart across the lanes, each store instruction writing 1 KB of consecutive
+// bytes.  Grid: x = 256 cell rows, y (+ 65535 z) = image.
 constexpr int kPixelWaves = 4;
 __global__ __launch_bounds__(kPixelWaves * 64) void k_pixels_from_maps(int32_t H, int32_t W, int32_t T, int32_t wshift,
                                                                        int64_t images, const uint8_t* maps,
