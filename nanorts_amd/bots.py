@@ -94,6 +94,10 @@ class SeatState:
     carry: dict[str, torch.Tensor]
     seat: torch.Tensor
 
+    def clone(self) -> "SeatState":
+        return SeatState(self.environment_state.clone(), {k: v.clone() for k, v in self.carry.items()},
+                         self.seat.clone())
+
 
 def _pick(per_agent: dict[str, Any], seat: torch.Tensor) -> Any:
     """_learners (src/nanorts/bots/seat.py:368-375) for per-lane seats: lane
@@ -176,8 +180,7 @@ class SeatEnv:
         if reset_state is not None:
             raise ModelError("step resets finished games to the content's start by itself; reset_state is not taken")
         env = self.env
-        nxt = state if donate else SeatState(state.environment_state.clone(),
-                                             {k: v.clone() for k, v in state.carry.items()}, state.seat.clone())
+        nxt = state if donate else state.clone()
         es = nxt.environment_state
         L = es.num_envs
         b = env.bucket

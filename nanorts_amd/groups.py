@@ -9,10 +9,14 @@ differ in terrain and horizon), else one launch per group.
 `GroupMix` is src/nanorts/bots/mix.py:17-275: a batch of groups, each an
 environment (the JaxMARL facade or a learner-vs-bot seat) with its own lanes,
 published agent-major: every output row is one agent of one lane, groups
-concatenated in order.  Each group steps in its own fused launch (decode,
-bot act, core.step, auto-reset, observe); the rows of all groups must have
-equal shapes, so the groups' environments publish equal observation and
-action spaces and equal infos.
+concatenated in order.  Groups whose environments split their step
+(step_request / step_response) and whose games step together (one bucket)
+share one core.step launch per cycle: each builds its request (decode, and
+the bot's act for a seat), `step_groups` steps them all, and each answers
+its own (rewards, observation, auto-reset).  Any other group steps in its
+own fused launch.  The rows of all groups must have equal shapes, so the
+groups' environments publish equal observation and action spaces and equal
+infos.
 """
 from __future__ import annotations
 
@@ -209,21 +213,46 @@ class GroupMix:
 
     def step(self, key, states: tuple[Any, ...], actions: torch.Tensor, *, donate: bool = False):
         """Actions int32[rows, C, 7], agent-major per group -> (observations,
-        next states, rewards, dones, infos), each agent-major."""
+        next states, rewards, dones, infos), each agent-major
+        (src/nanorts/bots/mix.py:105-166)."""
         if actions.shape[0] != self.rows:
             raise ModelError(f"GroupMix.step takes {self.rows} action rows, got {actions.shape[0]}")
-        observations, following, rewards, dones, infos = [], [], [], [], []
-        for group, state, bound in zip(self.groups, states, self._bounds(self._row_counts()), strict=True):
-            env = group.environment
+        per_agent = []
+        for group, bound in zip(self.groups, self._bounds(self._row_counts()), strict=True):
             rows = actions[bound]
-            per_agent = dict(zip(_agents(env), torch.split(rows, group.lanes), strict=True))
-            obs, nxt, reward, done, info = env.step(key, state, per_agent, donate=donate)
+            per_agent.append(dict(zip(_agents(group.environment), torch.split(rows, group.lanes), strict=True)))
+        stepped: dict[int, tuple] = {}
+        for members in self.shared_launches():
+            envs = [self.groups[i].environment for i in members]
+            # the split step updates its state in place
+            mine = [states[i] if donate else states[i].clone() for i in members]
+            requests = [env.step_request(state, per_agent[i]) for env, state, i in zip(envs, mine, members, strict=True)]
+            results = step_groups([(*request, env) for env, (request, _) in zip(envs, requests, strict=True)])
+            for env, state, i, (_, carry), result in zip(envs, mine, members, requests, results, strict=True):
+                stepped[i] = env.step_response(state, carry, result)
+        observations, following, rewards, dones, infos = [], [], [], [], []
+        for i, (group, state) in enumerate(zip(self.groups, states, strict=True)):
+            env = group.environment
+            obs, nxt, reward, done, info = (stepped[i] if i in stepped
+                                            else env.step(key, state, per_agent[i], donate=donate))
             observations.append(_agent_major(obs, env))
             following.append(nxt)
             rewards.append(_agent_major(reward, env))
             dones.append(_agent_major({a: done[a] for a in _agents(env)}, env))
             infos.append(_info_rows(info, env))
         return _concat(observations), tuple(following), _concat(rewards), _concat(dones), _concat(infos)
+
+    def shared_launches(self) -> list[list[int]]:
+        """The groups that share a core.step launch, by bucket
+        (src/nanorts/bots/mix.py:124-141): environments with a split step
+        whose games step together."""
+        by_bucket: dict[Any, list[int]] = {}
+        for index, group in enumerate(self.groups):
+            env = group.environment
+            if callable(getattr(env, "step_request", None)) and callable(getattr(env, "step_response", None)):
+                by_bucket.setdefault(_device_game(env).game.bucket, []).append(index)
+        return [members for members in by_bucket.values()
+                if steps_together([_device_game(self.groups[i].environment).game for i in members])]
 
     def get_avail_actions(self, states: tuple[Any, ...]) -> torch.Tensor:
         return _concat([_agent_major(group.environment.get_avail_actions(state), group.environment)

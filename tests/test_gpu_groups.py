@@ -92,6 +92,9 @@ def test_group_mix_publishes_each_group_agent_major():
     envs = (both, worker, light)
     mix = GroupMix([Group(env, n) for env, n in zip(envs, lanes)])
     assert mix.lanes == 19 and mix.rows == 27
+    # one bucket, every environment with a split step: one core.step launch
+    # per cycle, checked below against each environment's own fused step
+    assert mix.shared_launches() == [[0, 1, 2]]
     assert [(s.start, s.stop) for s in mix.slices()] == [(0, 16), (16, 22), (22, 27)]
     with pytest.raises(ModelError):
         GroupMix([])
