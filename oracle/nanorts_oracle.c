@@ -20,13 +20,13 @@
  * randint01 and the CANCEL_RANDOM draw by the reference's own
  * conflict_draw.cuh (oracle/_ref, and golden vectors from it); admission,
  * durations, completion and outcome by hand-traced cycles on the 8x8 map;
- * masks against admission by brute force over every single command;
- * visibility, symbolic and pixel observations by closed forms; the state
- * invariants over long rollouts of every case.
- * Parity unpinned: the exact settled durations of cancelled pendings when
- * several conflicts meet in one cycle (_settle_durations,
- * N/core/reservations.py:169-204) -- restated here, covered by the invariants
- * and the single-conflict races, with no reference vectors to compare.
+ * completions by actors that died before their turn, the admitted counts and
+ * the settled durations of cancelled pendings when several conflicts meet in
+ * one cycle (_settle_durations, N/core/reservations.py:169-228) by
+ * hand-traced scenarios under every conflict strategy
+ * (tests/test_oracle_rules.py); masks against admission by brute force over
+ * every single command; visibility, symbolic and pixel observations by closed
+ * forms; the state invariants over long rollouts of every case.
  */
 #include "nanorts_oracle.h"
 
