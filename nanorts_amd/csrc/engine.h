@@ -1050,12 +1050,37 @@ NR_DEV int32_t live_slot_at(const KGame& g, const Env& e, int32_t i) {
     return word * kWave + select_bit(mine, k);
 }
 
-// Live slots of the staged env (wave-uniform).
-NR_DEV int32_t live_slots(const KGame& g, const Env& e) {
+// The live slots of the staged env: their count (wave-uniform) and, when the
+// count is at most a wave, lane i's slot = the i-th live slot in slot order
+// (lanes at or past the count, or every lane of a larger count, hold an
+// unused value).  Each live slot's lane in its bitmap word sends the slot to
+// the lane of its rank with a forward permute, which moves values between
+// lanes without LDS memory; the other lanes of the word send to a lane past
+// the word's ranks, and every lane keeps only what the word of its own rank
+// sent.  Every lane of the wave must be active.
+struct LiveLanes {
+    int32_t count, slot;
+};
+NR_DEV LiveLanes live_lanes(const KGame& g, const Env& e, int lane) {
     AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
-    int32_t n = 0;
-    for (int32_t w = 0; w * kWave < g.E; ++w) n += popc(live[w]);
-    return uni(n);
+    LiveLanes out = {0, 0};
+    for (int32_t w = 0; w * kWave < g.E; ++w) {
+        const uint64_t v = live[w];
+        const uint64_t m = (uint64_t)(uint32_t)uni((int32_t)(uint32_t)v) |
+                           ((uint64_t)(uint32_t)uni((int32_t)(uint32_t)(v >> 32)) << 32);
+        if (m == 0ull) continue;
+        const int32_t base = out.count, c = popc(m);
+        out.count += c;
+        if (out.count > kWave) continue;
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)base));
+        const int32_t to = __builtin_amdgcn_inverse_ballot_w64(m) ? (int32_t)rank : (out.count & (kWave - 1));
+        const int32_t got = __builtin_amdgcn_ds_permute(to << 2, w * kWave + lane);
+        const uint64_t upto = out.count >= kWave ? ~0ull : ((1ull << out.count) - 1ull);
+        const uint64_t ranks = upto & ~((1ull << base) - 1ull);
+        out.slot = __builtin_amdgcn_inverse_ballot_w64(ranks) ? got : out.slot;
+    }
+    return out;
 }
 
 // ---------------------------------------------------------------------------
@@ -1201,11 +1226,12 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
     if (lane == 0) e.sc[S_TIME] = time;
     AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
     // only live slots hold pending actions
-    const int32_t nlive = live_slots(g, e);
+    const LiveLanes ll = live_lanes(g, e, lane);
+    const int32_t nlive = ll.count;
     if (at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in
         // their lanes and are ranked and read from there
-        const int32_t s = lane < nlive ? live_slot_at(g, e, lane) : 0;
+        const int32_t s = lane < nlive ? ll.slot : 0;
         bool acting = false;
         int32_t w0 = 0, w1 = 0, w2 = 0, rb = 0, rc = 0, ord = 0;
         if (lane < nlive) {

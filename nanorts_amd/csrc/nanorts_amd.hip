@@ -1538,7 +1538,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             }
             for (int32_t i = lane; i < n; i += kWave) {
                 const int32_t p = av[i];
-                if (p / g.C != learner) continue;
+                if ((p >= g.C ? 1 : 0) != learner) continue;  // positions below 2C
                 const Row r = legality_row_w1(g, hdr, e, g.N + p, aff);
                 uint32_t words[4] = {pw0, pw1, pw2, pw3};
                 if (!paired) {

@@ -258,12 +258,13 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     const int32_t time = uni(e.sc[S_TIME]);
     const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
     // only live slots hold units or pending actions
-    const int32_t nlive = live_slots(g, e);
+    const LiveLanes ll = live_lanes(g, e, lane);
+    const int32_t nlive = ll.count;
     int32_t nav = 0, nunits = 0, nA = 0;
     bool odd = false;
     for (int32_t base = 0; base < nlive; base += kWave) {
         const int32_t i = base + lane;
-        const int32_t s = i < nlive ? live_slot_at(g, e, i) : 0;
+        const int32_t s = i < nlive ? (nlive <= kWave ? ll.slot : live_slot_at(g, e, i)) : 0;
         bool alive = false, available = false, entry = false;
         if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
@@ -358,7 +359,9 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
     const int32_t R = g.disk_r, span = 2 * R + 1;
     if (g.H <= 32 && words == 1) {
         const int32_t U = kWave / g.H;
-        const int32_t k = lane / g.H, row = lane - k * g.H;
+        // lane / H by a 16-bit reciprocal (exact for lane < 64, H <= 32)
+        const int32_t k = (int32_t)(((uint32_t)lane * ((65536u + (uint32_t)g.H - 1u) / (uint32_t)g.H)) >> 16);
+        const int32_t row = lane - k * g.H;
         const uint32_t rowmask = g.W >= 32 ? 0xFFFFFFFFu : ((1u << g.W) - 1u);
         uint32_t acc0 = 0u, acc1 = 0u;
         // the listed units are player 0's, then player 1's
@@ -449,7 +452,7 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
         if (c0 >= g.cells) continue;
         const uint64_t ent = *(AS3 const uint64_t*)(e.entity + c0);
         const uint32_t ter = *(AS3 const uint32_t*)(h.terrain + c0);  // one 0/1 byte per cell
-        const int32_t yy = c0 / g.W, x = c0 - yy * g.W;
+        const int32_t yy = cell_y(g, c0), x = c0 - yy * g.W;
         const int32_t word = yy * words + (x >> 5), shift = x & 31;
         // the occupants' words and flags; an empty cell reads the zero
         // sentinel at index E (ABSENT -> 0xFFFFFFFF -> min E)
