@@ -1321,7 +1321,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             const bool narrow = fast && g.seen_words == 1;
             const Affordable aff = affordable_types(g, hdr, e, lane);
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
-            if (paired) {
+            if (paired && n > 0) {
                 const int32_t u = lane >> 1;
                 uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
@@ -1527,7 +1527,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             // both threefry blocks of a position on two lanes when n <= 32
             const bool paired = n <= kWave / 2;
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
-            if (paired) {
+            if (paired && n > 0) {
                 const int32_t u = lane >> 1;
                 uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
