@@ -1333,7 +1333,6 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             }
             for (int32_t i = lane; i < n; i += kWave) {
                 const int32_t p = av[i];
-                const Row r = narrow ? legality_row_w1(g, hdr, e, g.N + p, aff) : legality_row_bm(g, hdr, e, g.N + p);
                 uint32_t words[4];
                 if (paired) {
                     words[0] = pw0;
@@ -1350,20 +1349,28 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                     words[3] = w3;
                 }
                 int32_t kind, dir, ptype, target, none;
-                if (!out.actions && g.T <= 8) {
-                    // unrecorded: only the factors decode reads are drawn
-                    sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype, &target,
-                                   &none);
-                } else {
-                    int32_t act[7];
-                    if (g.T <= 8) sample_row_words8(g, r, words, act);
-                    else sample_row_words(g, r, words, act);
-                    if (out.actions) {
-                        int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
+                // unrecorded, units of attack range at most 1: the factors
+                // straight from the neighbour masks, no row assembled
+                if (!(narrow && !out.actions && g.T <= 8 &&
+                      sample_unit_w1(g, hdr, e, p, aff, words[0], words[1], words[2], words[3], &kind, &dir, &ptype,
+                                     &target, &none))) {
+                    const Row r =
+                        narrow ? legality_row_w1(g, hdr, e, g.N + p, aff) : legality_row_bm(g, hdr, e, g.N + p);
+                    if (!out.actions && g.T <= 8) {
+                        // unrecorded: only the factors decode reads are drawn
+                        sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype,
+                                       &target, &none);
+                    } else {
+                        int32_t act[7];
+                        if (g.T <= 8) sample_row_words8(g, r, words, act);
+                        else sample_row_words(g, r, words, act);
+                        if (out.actions) {
+                            int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
 #pragma unroll
-                        for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                            for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                        }
+                        decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                     }
-                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                 }
                 if (fused) {
                     request_of(g, hdr, e, p, kind, dir, ptype, target, none, true, false, q);
@@ -1539,7 +1546,6 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             for (int32_t i = lane; i < n; i += kWave) {
                 const int32_t p = av[i];
                 if ((p >= g.C ? 1 : 0) != learner) continue;  // positions below 2C
-                const Row r = legality_row_w1(g, hdr, e, g.N + p, aff);
                 uint32_t words[4] = {pw0, pw1, pw2, pw3};
                 if (!paired) {
                     words[0] = env;
@@ -1550,19 +1556,26 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
                     threefry(ke0, ke1, words[2], words[3]);
                 }
                 int32_t kind, dir, ptype, target, none;
-                if (!out.actions && g.T <= 8) {
-                    sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype, &target,
-                                   &none);
-                } else {
-                    int32_t act[7];
-                    if (g.T <= 8) sample_row_words8(g, r, words, act);
-                    else sample_row_words(g, r, words, act);
-                    if (out.actions) {
-                        int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
+                // unrecorded, units of attack range at most 1: the factors
+                // straight from the neighbour masks, no row assembled
+                if (!(!out.actions && g.T <= 8 &&
+                      sample_unit_w1(g, hdr, e, p, aff, words[0], words[1], words[2], words[3], &kind, &dir, &ptype,
+                                     &target, &none))) {
+                    const Row r = legality_row_w1(g, hdr, e, g.N + p, aff);
+                    if (!out.actions && g.T <= 8) {
+                        sample_decode8(g, e, p, r, words[0], words[1], words[2], words[3], &kind, &dir, &ptype,
+                                       &target, &none);
+                    } else {
+                        int32_t act[7];
+                        if (g.T <= 8) sample_row_words8(g, r, words, act);
+                        else sample_row_words(g, r, words, act);
+                        if (out.actions) {
+                            int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
 #pragma unroll
-                        for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                            for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                        }
+                        decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                     }
-                    decode_values(g, e, p, act, &kind, &dir, &ptype, &target, &none);
                 }
                 at<int8_t>(e, y.c_kind)[p] = (int8_t)kind;
                 at<int8_t>(e, y.c_dir)[p] = (int8_t)dir;

@@ -230,6 +230,110 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
     return r;
 }
 
+// k-th set bit (0-based, below the count) of a 4-bit mask from a table of
+// each mask's set-bit positions in increasing order, two bits apiece: byte m
+// of the 128-bit table, masks 0-7 in the low word, 8-15 in the high word.
+constexpr uint64_t select4_table(int half) {
+    uint64_t t = 0;
+    for (int i = 0; i < 8; ++i) {
+        const int m = half * 8 + i;
+        uint64_t byte = 0;
+        int j = 0;
+        for (int b = 0; b < 4; ++b)
+            if ((m >> b) & 1) byte |= (uint64_t)b << (2 * j++);
+        t |= byte << (8 * i);
+    }
+    return t;
+}
+NR_DEV int32_t select4(uint32_t m, int32_t k) {
+    const uint64_t t = (m & 8u) ? select4_table(1) : select4_table(0);
+    return (int32_t)((t >> (((m & 7u) << 3) | ((uint32_t)k << 1))) & 3u);
+}
+
+// legality_row_w1 and sample_decode8 in one pass, for a unit of player 0 or
+// 1 on the board whose attack range is 1 (or that cannot attack), on boards
+// of at most 32 columns with T <= 8: every factor it can sample is a 4-bit
+// mask over the four neighbours, so the row is never assembled and the
+// attack target follows from the neighbour drawn.  Same draws and results as
+// the two functions; returns false, writing nothing, for any other unit.
+// The range-1 attack window holds the four neighbours at offsets
+// c0 - side, c0 - 1, c0 + 1, c0 + side (c0 its centre): in offset order up,
+// left, right, down.
+NR_DEV bool sample_unit_w1(const KGame& g, const Hdr& h, const Env& e, int32_t p, const Affordable& aff, uint32_t w0,
+                           uint32_t w1, uint32_t w2, uint32_t w3, int32_t* kind_out, int32_t* dir_out,
+                           int32_t* ptype_out, int32_t* target_out, int32_t* none_out) {
+    const int32_t slot = g.N + p;
+    if (e.birth[slot] == kAbsent) return false;
+    const int32_t owner = e.owner[slot];
+    if (owner != 0 && owner != 1) return false;
+    const int32_t actor = clampi(e.utype[slot], 0, g.T - 1);
+    const int32_t info = tabv(h, F_PACK, actor);
+    const int32_t flags = info & 0xFF;
+    if ((flags & FL_ATTACK) && !((info >> 16) == 1 && g.radius >= 1)) return false;
+    const int32_t cell = e.cell[slot];
+    const int32_t x = cell_x(g, cell), yy = cell_y(g, cell);
+    const int32_t H = g.H;
+    if (x < 0 || x >= g.W || yy < 0 || yy >= H) return false;
+    const int32_t carried = e.carried[slot];
+    const uint32_t types = ((uint32_t)info >> 8) & 0xFFu & (owner ? aff.player[1] : aff.player[0]);
+    AS3 const uint32_t* bm = at<uint32_t>(e, g.lay.o_bm);
+    AS3 const uint32_t* res = bm + 3 * H;
+    AS3 const uint32_t* stk = bm + (4 + owner) * H;
+    AS3 const uint32_t* enemy = bm + (2 - owner) * H;
+    const bool has_up = yy >= 1, has_dn = yy + 1 < H;
+    const int32_t ru = has_up ? yy - 1 : 0, rd = has_dn ? yy + 1 : 0;
+    // rows above and below: the unit's column; off the board is blocked and
+    // holds nothing
+    const uint32_t b_up = has_up ? bm[ru] : 0xFFFFFFFFu, b_dn = has_dn ? bm[rd] : 0xFFFFFFFFu;
+    const uint32_t r_up = has_up ? res[ru] : 0u, r_dn = has_dn ? res[rd] : 0u;
+    const uint32_t s_up = has_up ? stk[ru] : 0u, s_dn = has_dn ? stk[rd] : 0u;
+    const uint32_t e_up = has_up ? enemy[ru] : 0u, e_dn = has_dn ? enemy[rd] : 0u;
+    // the unit's row: columns x - 1 .. x + 1 as bits 0 .. 2
+    const uint64_t outside = ~0ull << (g.W + 1);
+    const uint32_t bw = (uint32_t)(((((uint64_t)bm[yy] << 1) | 1ull | outside) >> x) & 7ull);
+    const uint32_t rw = (uint32_t)((((uint64_t)res[yy] << 1) >> x) & 7ull);
+    const uint32_t sw = (uint32_t)((((uint64_t)stk[yy] << 1) >> x) & 7ull);
+    const uint32_t ew = (uint32_t)((((uint64_t)enemy[yy] << 1) >> x) & 7ull);
+    const uint32_t xb = (uint32_t)x;
+    // directions 0 up, 1 right, 2 down, 3 left
+    const uint32_t blocked4 = ((b_up >> xb) & 1u) | (((bw >> 2) & 1u) << 1) | (((b_dn >> xb) & 1u) << 2) | ((bw & 1u) << 3);
+    const uint32_t free4 = ~blocked4 & 15u;
+    const uint32_t res4 = ((r_up >> xb) & 1u) | (((rw >> 2) & 1u) << 1) | (((r_dn >> xb) & 1u) << 2) | ((rw & 1u) << 3);
+    const uint32_t stk4 = ((s_up >> xb) & 1u) | (((sw >> 2) & 1u) << 1) | (((s_dn >> xb) & 1u) << 2) | ((sw & 1u) << 3);
+    // attack offsets in window order: up, left, right, down
+    const uint32_t att4 = (flags & FL_ATTACK) ? (((e_up >> xb) & 1u) | ((ew & 1u) << 1) | (((ew >> 2) & 1u) << 2) |
+                                                 (((e_dn >> xb) & 1u) << 3))
+                                              : 0u;
+    const uint32_t mk = 1u | (((flags & FL_MOVE) && free4) ? 2u : 0u) |
+                        (((flags & FL_HARVEST) && carried == 0 && res4) ? 4u : 0u) |
+                        (((flags & FL_HARVEST) && carried > 0 && stk4) ? 8u : 0u) | ((types && free4) ? 16u : 0u) |
+                        (att4 ? 32u : 0u);
+    int32_t kind = kKindNone, dir = kAbsent, ptype = kAbsent, target = kAbsent;
+    if (mk != 1u) {
+        kind = select_bit8(mk, (int32_t)(((w0 & 0xFFFFu) * (uint32_t)__popc(mk)) >> 16));
+        if (kind >= kKindMove && kind <= kKindProduce) {
+            const uint32_t m = kind == kKindHarvest ? res4 : (kind == kKindReturn ? stk4 : free4);
+            uint32_t w = w1;
+            if (kind == kKindMove) w = w0;
+            if (kind == kKindProduce) w = w2;
+            const uint32_t hh = (kind & 1) ? (w >> 16) : (w & 0xFFFFu);
+            dir = select4(m, (int32_t)((hh * (uint32_t)__popc(m)) >> 16));
+            if (kind == kKindProduce)
+                ptype = select_bit8(types, (int32_t)(((w2 >> 16) * (uint32_t)__popc(types)) >> 16));
+        } else if (kind == kKindAttack) {
+            const int32_t j = select4(att4, (int32_t)(((w3 & 0xFFFFu) * (uint32_t)__popc(att4)) >> 16));
+            const int32_t tx = x + (j == 1 ? -1 : (j == 2 ? 1 : 0)), ty = yy + (j == 0 ? -1 : (j == 3 ? 1 : 0));
+            if (tx >= 0 && tx < g.W && ty >= 0 && ty < H) target = ty * g.W + tx;
+        }
+    }
+    *kind_out = kind;
+    *dir_out = dir;
+    *ptype_out = ptype;
+    *target_out = target;
+    *none_out = kind == kKindNone ? 1 : 0;
+    return true;
+}
+
 // Pass over the slots: occupant words, available list, unit list, and (with
 // `bitmaps`) the six occupancy bitmaps of the next cycle's masks, stamped per
 // live slot over the wall rows: 0 blocked (occupied or wall), 1 / 2 units of
