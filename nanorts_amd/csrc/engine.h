@@ -363,11 +363,20 @@ NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
     }
     for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = terrain[i] ? 1 : 0;
     if (g.fast_obs) {
-        // the walls as bitmap rows, the blocked plane every cycle starts from
+        // the walls as bitmap rows, the blocked plane every cycle starts
+        // from, packed from the terrain copy four cells per LDS read (W % 4
+        // == 0 keeps every row 4-byte aligned); every thread of the block
+        // calls this, so the barrier is safe
+        __syncthreads();
         for (int i = threadIdx.x; i < g.H * g.seen_words; i += blockDim.x) {
             const int32_t row = i / g.seen_words, x0 = 32 * (i - row * g.seen_words);
+            const int32_t n = g.W - x0 < 32 ? g.W - x0 : 32;
+            AS3 const uint32_t* cells = (AS3 const uint32_t*)(h.terrain + row * g.W + x0);
             uint32_t bits = 0u;
-            for (int32_t b = 0; b < 32 && x0 + b < g.W; ++b) bits |= (terrain[row * g.W + x0 + b] ? 1u : 0u) << b;
+            for (int32_t q = 0; q < (n >> 2); ++q) {
+                const uint32_t v = cells[q];  // one 0/1 byte per cell
+                bits |= ((v & 1u) | ((v >> 7) & 2u) | ((v >> 14) & 4u) | ((v >> 21) & 8u)) << (4 * q);
+            }
             h.walls[i] = bits;
         }
         // disk[r][dy + R]: bits R - w .. R + w with w = floor(sqrt(r^2 - dy^2)),
