@@ -351,7 +351,18 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     const int32_t words = g.seen_words, plane = g.H * words;
     AS3 uint32_t* bm = at<uint32_t>(e, y.o_bm);
     if (bitmaps) {
-        for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = i < plane ? h.walls[i] : 0u;
+        // the blocked plane starts from the wall rows, the other five empty
+        if ((plane & 3) == 0) {
+            // 16 bytes a lane (both regions are 16-byte aligned)
+            const int32_t n4 = (6 * plane) >> 2, w4 = plane >> 2;
+            for (int32_t i = lane; i < n4; i += kWave) {
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (i < w4) v = ((AS3 const u32x4*)h.walls)[i];
+                ((AS3 u32x4*)bm)[i] = v;
+            }
+        } else {
+            for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = i < plane ? h.walls[i] : 0u;
+        }
         wave_sync();
     }
     AS3 uint32_t* olo = at<uint32_t>(e, y.o_lo);
@@ -406,9 +417,15 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
                     const int32_t cy = cell_y(g, c), cx = c - cy * g.W;
                     AS3 uint32_t* at_ = bm + cy * words + (cx >> 5);
                     const uint32_t bit = 1u << (cx & 31);
-                    // planes is a 6-bit set: stamp each plane it names
-                    for (uint32_t rest = planes; rest != 0u; rest &= rest - 1u)
-                        __atomic_fetch_or(at_ + __builtin_ctz(rest) * plane, bit, __ATOMIC_RELAXED);
+                    // the planes it names, at most one of each pair: occupied,
+                    // its player's units (1 or 2), resource (3), its
+                    // player's stockpiles (4 or 5); an OR of 0 where a
+                    // plane is not named
+                    __atomic_fetch_or(at_, bit, __ATOMIC_RELAXED);
+                    __atomic_fetch_or(at_ + (rel0 == 2u ? 2 : 1) * plane, rel0 != 0u ? bit : 0u, __ATOMIC_RELAXED);
+                    __atomic_fetch_or(at_ + 3 * plane, (planes & 8u) ? bit : 0u, __ATOMIC_RELAXED);
+                    __atomic_fetch_or(at_ + (rel0 == 2u ? 5 : 4) * plane, (planes & 48u) ? bit : 0u,
+                                      __ATOMIC_RELAXED);
                 }
                 available = s >= g.N && pk == kAbsent;
                 if (available && e.porder[s] != kAbsent) odd = true;
