@@ -27,6 +27,10 @@ CASES = {
                         True, True),
     "obstacle-alternating": ("basesWorkers8x8Obstacle", UnitTypeTableVersion.ORIGINAL,
                              ConflictStrategy.CANCEL_ALTERNATING, 120, True, False),
+    # Ranged units (attack range 3) from the first cycle: the samplers' general
+    # attack window next to the range-1 neighbour masks
+    "ranged-random": ("melee8x8Mixed6", UnitTypeTableVersion.ORIGINAL_FINETUNED, ConflictStrategy.CANCEL_RANDOM, 300,
+                      True, True),
     # widths that are not a multiple of 4: the kernels' general observation
     # and summary branches
     "10x10-random-partial": ("basesWorkers10x10", UnitTypeTableVersion.ORIGINAL_FINETUNED,

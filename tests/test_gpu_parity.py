@@ -15,7 +15,8 @@ from oracle.oracle import copy_state
 pytestmark = pytest.mark.gpu
 
 FAST_CASES = ["8x8-original-both", "16x16-finetuned-both", "16x16-random-partial", "16x16-alternating",
-              "melee-both", "barracks-random", "obstacle-alternating", "10x10-random-partial", "9x8-alternating"]
+              "melee-both", "barracks-random", "obstacle-alternating", "10x10-random-partial", "9x8-alternating",
+              "ranged-random"]
 
 
 def _env(game, partial, **kw):
