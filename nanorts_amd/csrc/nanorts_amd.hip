@@ -1282,6 +1282,15 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
     const int32_t steps = args.steps;
     int32_t general = 0;  // cycles admitted request by request
     int32_t stop = steps;  // first pass: the first cycle left to the second
+    // the output rows of the launch's first cycle and the observation ring,
+    // read once into registers instead of from the argument segment every
+    // cycle
+    const int64_t t0l = (int64_t)args.t0 * lanes;
+    float* const rew = args.out.rewards ? args.out.rewards + t0l * 2 : nullptr;
+    uint8_t* const dn = args.out.dones ? args.out.dones + t0l : nullptr;
+    uint8_t* const maps = args.out.feature_maps;
+    int32_t* const scal = args.out.scalars;
+    const uint32_t depth = (uint32_t)(args.out.depth > 0 ? args.out.depth : 1), first = (uint32_t)args.t0;
     for (int32_t t = t_begin; t < steps; ++t) {
         bool irregular = false;
         int32_t n;
@@ -1416,9 +1425,8 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             int32_t time = complete(g, hdr, e, lane, Lean);
             Outcome oc = decide_counted(e, lane);
             nanorts_env_results r = {};
-            const int64_t tt = (int64_t)a.t0 + t;
-            if (a.out.rewards) r.reward = a.out.rewards + tt * lanes * 2;
-            if (a.out.dones) r.done = a.out.dones + tt * lanes;
+            if (rew) r.reward = rew + (int64_t)t * lanes * 2;
+            if (dn) r.done = dn + (int64_t)t * lanes;
             const bool done = finish_step(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
             if (done) {
                 ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
@@ -1433,17 +1441,17 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
             // ring slot (t0 + t) % depth in 32 bits (a mask for powers of two)
-            const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)a.t0 + (uint32_t)t;
+            const uint32_t d = depth, c = first + (uint32_t)t;
             const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
             const int64_t slot = (int64_t)ring * lanes + l;
             if (fast) {
-                uint8_t* m0 = out.feature_maps ? out.feature_maps + (slot * 2) * per : nullptr;
-                if (out.scalars && lane < 8) {
+                uint8_t* m0 = maps ? maps + (slot * 2) * per : nullptr;
+                if (scal && lane < 8) {
                     // the scalars from registers: own balance, the opponent's,
                     // time, alternating count (as summarize writes them)
                     const int32_t pl = lane >> 2, f = lane & 3;
                     const int32_t own = pl == 0 ? oc.res0 : oc.res1, opp = pl == 0 ? oc.res1 : oc.res0;
-                    out.scalars[slot * 8 + lane] = f == 0 ? own : (f == 1 ? opp : (f == 2 ? time : oc.alt));
+                    scal[slot * 8 + lane] = f == 0 ? own : (f == 1 ? opp : (f == 2 ? time : oc.alt));
                 }
                 // the sight bitmaps persist in the event counters' words, which
                 // the rollout does not count, when both planes fit there
