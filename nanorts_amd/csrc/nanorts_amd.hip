@@ -1328,7 +1328,8 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             // on two lanes at once; otherwise each lane computes both
             const bool paired = n <= kWave / 2;
             const bool narrow = fast && g.seen_words == 1;
-            const Affordable aff = affordable_types(g, hdr, e, lane);
+            // (no unit to sample: no balance read)
+            const Affordable aff = n > 0 ? affordable_types(g, hdr, e, lane) : Affordable{{0u, 0u}};
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired && n > 0) {
                 const int32_t u = lane >> 1;
@@ -1538,7 +1539,8 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         if (fast) {
             const int32_t n = sm.nav;
             mark_unavailable(g, e, lane);
-            const Affordable aff = affordable_types(g, hdr, e, lane);
+            // (no unit to sample: no balance read)
+            const Affordable aff = n > 0 ? affordable_types(g, hdr, e, lane) : Affordable{{0u, 0u}};
             // both threefry blocks of a position on two lanes when n <= 32
             const bool paired = n <= kWave / 2;
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
