@@ -288,12 +288,22 @@ NR_DEV bool sample_unit_w1(const KGame& g, const Hdr& h, const Env& e, int32_t p
     const uint32_t r_up = has_up ? res[ru] : 0u, r_dn = has_dn ? res[rd] : 0u;
     const uint32_t s_up = has_up ? stk[ru] : 0u, s_dn = has_dn ? stk[rd] : 0u;
     const uint32_t e_up = has_up ? enemy[ru] : 0u, e_dn = has_dn ? enemy[rd] : 0u;
-    // the unit's row: columns x - 1 .. x + 1 as bits 0 .. 2
-    const uint64_t outside = ~0ull << (g.W + 1);
-    const uint32_t bw = (uint32_t)(((((uint64_t)bm[yy] << 1) | 1ull | outside) >> x) & 7ull);
-    const uint32_t rw = (uint32_t)((((uint64_t)res[yy] << 1) >> x) & 7ull);
-    const uint32_t sw = (uint32_t)((((uint64_t)stk[yy] << 1) >> x) & 7ull);
-    const uint32_t ew = (uint32_t)((((uint64_t)enemy[yy] << 1) >> x) & 7ull);
+    // the unit's row: columns x - 1 .. x + 1 as bits 0 .. 2 (off the board
+    // blocked); up to 30 columns the shifted row and its fill fit one word
+    uint32_t bw, rw, sw, ew;
+    if (g.W <= 30) {
+        const uint32_t outside = ~0u << (g.W + 1);
+        bw = __builtin_amdgcn_ubfe((bm[yy] << 1) | 1u | outside, (uint32_t)x, 3u);
+        rw = __builtin_amdgcn_ubfe(res[yy] << 1, (uint32_t)x, 3u);
+        sw = __builtin_amdgcn_ubfe(stk[yy] << 1, (uint32_t)x, 3u);
+        ew = __builtin_amdgcn_ubfe(enemy[yy] << 1, (uint32_t)x, 3u);
+    } else {
+        const uint64_t outside = ~0ull << (g.W + 1);
+        bw = (uint32_t)(((((uint64_t)bm[yy] << 1) | 1ull | outside) >> x) & 7ull);
+        rw = (uint32_t)((((uint64_t)res[yy] << 1) >> x) & 7ull);
+        sw = (uint32_t)((((uint64_t)stk[yy] << 1) >> x) & 7ull);
+        ew = (uint32_t)((((uint64_t)enemy[yy] << 1) >> x) & 7ull);
+    }
     const uint32_t xb = (uint32_t)x;
     // directions 0 up, 1 right, 2 down, 3 left
     const uint32_t blocked4 = ((b_up >> xb) & 1u) | (((bw >> 2) & 1u) << 1) | (((b_dn >> xb) & 1u) << 2) | ((bw & 1u) << 3);
