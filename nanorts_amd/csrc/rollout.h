@@ -137,6 +137,15 @@ NR_DEV Affordable affordable_types(const KGame& g, const Hdr& h, const Env& e, i
     return a;
 }
 
+// Columns x - 1 .. x + 1 (0 <= x < W <= 32) of a board row as bits 0 .. 2;
+// with `fill` the columns off the board read as set (blocked).  Up to 30
+// columns the shifted row and its fill fit one word: one bitfield extract.
+NR_DEV uint32_t window3(const KGame& g, uint32_t row, uint32_t x, bool fill) {
+    if (g.W <= 30) return __builtin_amdgcn_ubfe((row << 1) | (fill ? 1u | (~0u << (g.W + 1)) : 0u), x, 3u);
+    const uint64_t v = ((uint64_t)row << 1) | (fill ? 1ull | (~0ull << (g.W + 1)) : 0ull);
+    return (uint32_t)((v >> x) & 7ull);
+}
+
 NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t slot, const Affordable& aff) {
     Row r;
     r.w[0] = r.w[1] = r.w[2] = 0u;
@@ -165,11 +174,10 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
     // x - 1 .. x + 1 of the middle rows: bit 0 left, bit 2 right; off the
     // board is blocked and holds nothing
     const bool inx = x >= 0 && x < g.W;
-    const uint64_t outside = ~0ull << (g.W + 1);
-    const uint32_t bw = inx ? (uint32_t)(((((uint64_t)b_mid << 1) | 1ull | outside) >> x) & 7ull) : 7u;
-    const uint32_t rw = inx ? (uint32_t)((((uint64_t)r_mid << 1) >> x) & 7ull) : 0u;
-    const uint32_t sw = inx ? (uint32_t)((((uint64_t)s_mid << 1) >> x) & 7ull) : 0u;
     const uint32_t xb = inx ? (uint32_t)x : 0u;
+    const uint32_t bw = inx ? window3(g, b_mid, xb, true) : 7u;
+    const uint32_t rw = inx ? window3(g, r_mid, xb, false) : 0u;
+    const uint32_t sw = inx ? window3(g, s_mid, xb, false) : 0u;
     const uint32_t bu = inx ? (b_up >> xb) & 1u : 1u, bd = inx ? (b_dn >> xb) & 1u : 1u;
     const uint32_t blocked4 = bu | (((bw >> 2) & 1u) << 1) | (bd << 2) | ((bw & 1u) << 3);
     const uint32_t free4 = ~blocked4 & 15u;
@@ -199,7 +207,7 @@ NR_DEV Row legality_row_w1(const KGame& g, const Hdr& h, const Env& e, int32_t s
             // range 1: the four neighbours (the unit's own cell never holds
             // an enemy), read like the move directions
             const uint32_t e_up = has_up ? enemy[ru] : 0u, e_dn = has_dn ? enemy[rd] : 0u;
-            const uint32_t ew = (uint32_t)((((uint64_t)(has_mid ? enemy[rm] : 0u) << 1) >> x) & 7ull);
+            const uint32_t ew = window3(g, has_mid ? enemy[rm] : 0u, xb, false);
             const int32_t c0 = g.radius * g.side + g.radius;
             att = ((uint64_t)((e_up >> xb) & 1u) << (c0 - g.side)) | ((uint64_t)(ew & 1u) << (c0 - 1)) |
                   ((uint64_t)((ew >> 2) & 1u) << (c0 + 1)) | ((uint64_t)((e_dn >> xb) & 1u) << (c0 + g.side));
@@ -288,23 +296,10 @@ NR_DEV bool sample_unit_w1(const KGame& g, const Hdr& h, const Env& e, int32_t p
     const uint32_t r_up = has_up ? res[ru] : 0u, r_dn = has_dn ? res[rd] : 0u;
     const uint32_t s_up = has_up ? stk[ru] : 0u, s_dn = has_dn ? stk[rd] : 0u;
     const uint32_t e_up = has_up ? enemy[ru] : 0u, e_dn = has_dn ? enemy[rd] : 0u;
-    // the unit's row: columns x - 1 .. x + 1 as bits 0 .. 2 (off the board
-    // blocked); up to 30 columns the shifted row and its fill fit one word
-    uint32_t bw, rw, sw, ew;
-    if (g.W <= 30) {
-        const uint32_t outside = ~0u << (g.W + 1);
-        bw = __builtin_amdgcn_ubfe((bm[yy] << 1) | 1u | outside, (uint32_t)x, 3u);
-        rw = __builtin_amdgcn_ubfe(res[yy] << 1, (uint32_t)x, 3u);
-        sw = __builtin_amdgcn_ubfe(stk[yy] << 1, (uint32_t)x, 3u);
-        ew = __builtin_amdgcn_ubfe(enemy[yy] << 1, (uint32_t)x, 3u);
-    } else {
-        const uint64_t outside = ~0ull << (g.W + 1);
-        bw = (uint32_t)(((((uint64_t)bm[yy] << 1) | 1ull | outside) >> x) & 7ull);
-        rw = (uint32_t)((((uint64_t)res[yy] << 1) >> x) & 7ull);
-        sw = (uint32_t)((((uint64_t)stk[yy] << 1) >> x) & 7ull);
-        ew = (uint32_t)((((uint64_t)enemy[yy] << 1) >> x) & 7ull);
-    }
+    // the unit's row: columns x - 1 .. x + 1 as bits 0 .. 2
     const uint32_t xb = (uint32_t)x;
+    const uint32_t bw = window3(g, bm[yy], xb, true), rw = window3(g, res[yy], xb, false);
+    const uint32_t sw = window3(g, stk[yy], xb, false), ew = window3(g, enemy[yy], xb, false);
     // directions 0 up, 1 right, 2 down, 3 left
     const uint32_t blocked4 = ((b_up >> xb) & 1u) | (((bw >> 2) & 1u) << 1) | (((b_dn >> xb) & 1u) << 2) | ((bw & 1u) << 3);
     const uint32_t free4 = ~blocked4 & 15u;
@@ -506,9 +501,9 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
             const int32_t cell = e.cell[s];
             const int32_t dy = row - cell_y(g, cell);
             if (dy < -r || dy > r) continue;
-            const uint64_t m = h.disk[r * span + dy + R];
-            const int32_t x0 = cell_x(g, cell) - R;
-            const uint32_t bits = (uint32_t)(x0 >= 0 ? m << x0 : m >> (-x0)) & rowmask;
+            const uint32_t m = h.disk[r * span + dy + R];
+            const int32_t x0 = cell_x(g, cell) - R;  // in [-R, W - 1]: 32-bit shifts
+            const uint32_t bits = (x0 >= 0 ? m << x0 : m >> (-x0)) & rowmask;
             if ((s - g.N) >= g.C) acc1 |= bits;
             else acc0 |= bits;
         }
