@@ -1228,14 +1228,17 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // `at_most_a_wave`: the caller guarantees at most 64 live slots, and the
 // path for more (member records in the phase union) is left out.  Returns
 // the new time.
-NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false) {
+NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false,
+                        const LiveLanes* known = nullptr) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
     AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
     // only live slots hold pending actions
-    const LiveLanes ll = live_lanes(g, e, lane);
+    // the caller's copy when it holds one for this live set (a summary of
+    // the state since which no unit spawned or died)
+    const LiveLanes ll = known ? *known : live_lanes(g, e, lane);
     const int32_t nlive = ll.count;
     if (at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in

@@ -1423,7 +1423,10 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         }
         {
             NR_ROLLOUT_PHASE
-            int32_t time = complete(g, hdr, e, lane, Lean);
+            // the summary's live lanes: sampling and admission spawn and
+            // remove nothing
+            const LiveLanes known = {sm.nlive, sm.live_slot};
+            int32_t time = complete(g, hdr, e, lane, Lean, (fast && sm.nlive <= kWave) ? &known : nullptr);
             Outcome oc = decide_counted(e, lane);
             nanorts_env_results r = {};
             if (rew) r.reward = rew + (int64_t)t * lanes * 2;
@@ -1656,7 +1659,10 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         int32_t time = 0;
         Outcome oc = {0, 0, 0, 0, 0};
         if (fast) {
-            time = complete(g, hdr, e, lane);
+            // the summary's live lanes: the bot, sampling and admission spawn
+            // and remove nothing
+            const LiveLanes known = {sm.nlive, sm.live_slot};
+            time = complete(g, hdr, e, lane, false, sm.nlive <= kWave ? &known : nullptr);
             oc = decide_counted(e, lane);
         } else {
             core_step(g, hdr, e, lane, ek0, ek1, false);

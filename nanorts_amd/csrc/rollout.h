@@ -348,6 +348,7 @@ NR_DEV bool sample_unit_w1(const KGame& g, const Hdr& h, const Env& e, int32_t p
 struct SlotSummary {
     int32_t nav, nunits, nA, nlive;
     bool irregular;
+    int32_t live_slot;  // this lane's live slot (live_lanes), for at most a wave of them
 };
 
 NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
@@ -465,6 +466,7 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     out.nA = uni(nA);
     out.nlive = nlive;
     out.irregular = irregular;
+    out.live_slot = ll.slot;
     return out;
 }
 
