@@ -37,6 +37,12 @@ CASES = {
                              ConflictStrategy.CANCEL_RANDOM, 5000, True, True),
     "9x8-alternating": ("NoWhereToRun9x8", UnitTypeTableVersion.ORIGINAL, ConflictStrategy.CANCEL_ALTERNATING, 130,
                         True, False),
+    # boards 17-32 wide: the 32-bit row masks of the visibility and window
+    # passes, with walls (barricades) and partial observability
+    "24x24-barricades-alternating": ("barricades24x24", UnitTypeTableVersion.ORIGINAL_FINETUNED,
+                                     ConflictStrategy.CANCEL_ALTERNATING, 5000, True, True),
+    "32x32-random-partial": ("basesWorkers32x32A", UnitTypeTableVersion.ORIGINAL_FINETUNED,
+                             ConflictStrategy.CANCEL_RANDOM, 5000, True, True),
 }
 
 

@@ -81,7 +81,7 @@ def _call(game, st: dict, commands: dict, keys: np.ndarray, *, alias: bool):
 
 
 @pytest.mark.parametrize("case", ["8x8-original-both", "16x16-random-partial", "barracks-random",
-                                  "obstacle-alternating"])
+                                  "obstacle-alternating", "24x24-barricades-alternating", "32x32-random-partial"])
 @pytest.mark.parametrize("alias,broadcast", [(True, False), (False, False), (True, True), (False, True)])
 def test_step_ffi_matches_oracle(case, alias, broadcast, oracle_threads):
     from oracle.oracle import copy_state
@@ -130,7 +130,7 @@ def _words_of(rows: np.ndarray) -> np.ndarray:
 
 
 @pytest.mark.parametrize("case", ["8x8-original-both", "16x16-random-partial", "barracks-random", "9x8-alternating",
-                                  "gow-alternating"])
+                                  "gow-alternating", "24x24-barricades-alternating", "32x32-random-partial"])
 def test_legality_ffi_matches_oracle(case, oracle_threads):
     import torch
 
@@ -191,7 +191,8 @@ def _visible_call(lib, birth, unit_type, cell, radius, lanes, first, count, heig
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("case", ["8x8-original-both", "16x16-random-partial", "9x8-alternating", "gow-alternating"])
+@pytest.mark.parametrize("case", ["8x8-original-both", "16x16-random-partial", "9x8-alternating", "gow-alternating",
+                                  "24x24-barricades-alternating", "32x32-random-partial"])
 def test_visible_cells_ffi(case, oracle_threads):
     from nanorts_amd import native
 

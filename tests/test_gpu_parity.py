@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 FAST_CASES = ["8x8-original-both", "16x16-finetuned-both", "16x16-random-partial", "16x16-alternating",
               "melee-both", "barracks-random", "obstacle-alternating", "10x10-random-partial", "9x8-alternating",
-              "ranged-random"]
+              "ranged-random", "24x24-barricades-alternating", "32x32-random-partial"]
 
 
 def _env(game, partial, **kw):

@@ -6,7 +6,10 @@ state taken just before the cycle; after the cycle every State leaf and the
 step results must equal the oracle's, which those scenarios pin to values
 worked out by hand (a dead attacker still hits, a dead returner still
 credits, a dead producer still spawns, the admitted counts, the settled
-durations of two conflicts and of a three-unit race under every strategy).
+durations of two conflicts and of a three-unit race under every strategy,
+budgets, birth order, appended ranking, cross-cycle settling, dead movers and
+harvesters, pile depletion, attacker damage, truncation).  The scenarios that
+read legality rows also compare the GPU's rows with the oracle's.
 """
 from __future__ import annotations
 
@@ -48,6 +51,19 @@ class DeviceBoard(rules.Board):
             np.testing.assert_array_equal(got[name].cpu().numpy().astype(out[name].dtype), out[name], err_msg=name)
         self.cycles = getattr(self, "cycles", 0) + 1
 
+    def check_rows(self, rows: np.ndarray) -> None:
+        import torch
+
+        from nanorts_amd import core
+        from nanorts_amd.env import State
+        from nanorts_amd.model import LEAF_NAMES
+
+        dev = State({name: torch.as_tensor(np.ascontiguousarray(self.st[name]), device="cuda:0")
+                     for name in LEAF_NAMES})
+        got = core.legal_commands(dev, self.game).cpu().numpy()[0]
+        np.testing.assert_array_equal(got.astype(np.uint8), rows.astype(np.uint8), err_msg="legality rows")
+        self.cycles = getattr(self, "cycles", 0) + 1
+
 
 SCENARIOS = [
     ("dead attacker", rules.test_dead_attacker_still_hits, ()),
@@ -65,6 +81,32 @@ SCENARIOS = [
     ("race alternating 1", rules.test_three_unit_race, ("alternating1", rules.ALTERNATING, 1)),
     ("race random", rules.test_three_unit_race_random, ()),
     ("race arrival", rules.test_three_unit_race_the_mover_arrives_on_time, ()),
+    ("cross-player budget", rules.test_over_budget_counts_only_the_same_players_pending_cost, ()),
+    ("free request beside overdrawn pending", rules.test_free_request_beside_an_overdrawn_pending, ()),
+    ("no overflow unaffordable", rules.test_spawn_overflow_only_when_affordable, (2, 0, 0)),
+    ("overflow affordable", rules.test_spawn_overflow_only_when_affordable, (3, 1, 1)),
+    ("birth order alternating 0", rules.test_admission_ranks_by_birth_before_position, (0, 10, (4, 19))),
+    ("birth order alternating 1", rules.test_admission_ranks_by_birth_before_position, (1, 4, (10, 26))),
+    ("birth order random", rules.test_admission_ranks_by_birth_before_position_random, ()),
+    ("appended order both", rules.test_appended_orders_rank_in_admission_order, ("both", rules.BOTH)),
+    ("appended order alternating", rules.test_appended_orders_rank_in_admission_order,
+     ("alternating0", rules.ALTERNATING)),
+    ("cross-cycle settle both", rules.test_pending_after_a_cross_cycle_conflict_settles_to_minus_one,
+     (rules.BOTH, 0)),
+    ("cross-cycle settle alternating", rules.test_pending_after_a_cross_cycle_conflict_settles_to_minus_one,
+     (rules.ALTERNATING, 1)),
+    ("dead mover", rules.test_dead_mover_stays_put, (False,)),
+    ("dead mover refilled slot", rules.test_dead_mover_stays_put, (True,)),
+    ("dead harvester", rules.test_dead_harvester_still_drains_the_pile, (20, 19)),
+    ("dead harvester depletes", rules.test_dead_harvester_still_drains_the_pile, (1, 0)),
+    ("exact depletion", rules.test_harvest_removes_a_pile_left_at_exactly_zero, (1,)),
+    ("pile stands", rules.test_harvest_removes_a_pile_left_at_exactly_zero, (2,)),
+    ("attacker damage", rules.test_attack_damage_is_the_attackers, ()),
+    ("truncation", rules.test_truncation_at_max_cycles, ()),
+    ("won at max_cycles", rules.test_a_game_won_at_max_cycles_is_terminated_not_truncated, ()),
+    ("built legality rows", rules.test_legality_rows_of_a_built_position, ()),
+    ("return into enemy base", rules.test_return_into_an_enemy_base_is_not_admitted, ()),
+    ("ranged at range", rules.test_ranged_attack_at_exactly_its_range, ()),
 ]
 
 

@@ -342,25 +342,28 @@ def _decode_row(width_t: int, kind: int, param: int) -> list[int]:
     return row
 
 
-@pytest.mark.parametrize("case", ["16x16-finetuned-both", "melee-both", "barracks-random"])
-def test_mask_bits_agree_with_admission(case):
-    """For every available unit of a few mid-game states and every single
+def _masks_against_admission(game, o, st) -> int:
+    """For every available unit of every env of `st` and every single
     command: a mask-legal command is admitted as itself (unless a pending
     MOVE/PRODUCE of another unit conflicts with it), a mask-illegal one
-    becomes NONE for the requested duration."""
-    game, partial = game_for(case)
-    o, st = advanced_states(game, 10, 90, partial, 4, seed=19)
+    becomes NONE for the requested duration.  Every active unit's row has its
+    NONE bit (core/kinds/none.py:19-20: `grid.active`).  Returns the number
+    of commands tried."""
     b = game.bucket
     T, C, N = b.unit_type_capacity, b.per_player_capacity, b.neutral_capacity
     rows = o.legality_rows(st)
     checked = 0
-    for l in range(10):
+    for l in range(st["time"].shape[0]):
         one = {k: np.ascontiguousarray(v[l:l + 1]) for k, v in st.items()}
         pending_claims = ((one["pending_kind"][0] == MOVE) | (one["pending_kind"][0] == PRODUCE)).any()
         for player in (0, 1):
             for pos in range(C):
                 slot = N + player * C + pos
-                if one["birth"][0, slot] == -1 or one["pending_kind"][0, slot] != -1:
+                active = one["birth"][0, slot] != -1
+                assert rows[l, player, pos, NONE] == active, (l, slot)
+                if not active:
+                    assert not rows[l, player, pos].any(), (l, slot)
+                if not active or one["pending_kind"][0, slot] != -1:
                     continue
                 utype = int(one["unit_type"][0, slot])
                 for kind, params in ((MOVE, 4), (HARVEST, 4), (RETURN, 4), (PRODUCE, 4 * T), (ATTACK, b.attack_offset_capacity)):
@@ -391,7 +394,31 @@ def test_mask_bits_agree_with_admission(case):
                             if duration >= 1:
                                 assert got == NONE and completes == duration, (l, slot, kind, param, got, completes)
                         checked += 1
-    assert checked > 400
+    return checked
+
+
+@pytest.mark.parametrize("case", ["16x16-finetuned-both", "melee-both", "barracks-random"])
+def test_mask_bits_agree_with_admission(case):
+    """Mid-game states of three games (90 random cycles)."""
+    game, partial = game_for(case)
+    o, st = advanced_states(game, 10, 90, partial, 4, seed=19)
+    assert _masks_against_admission(game, o, st) > 400
+
+
+@pytest.mark.parametrize("melee_pair", [False, True])
+def test_mask_bits_agree_with_admission_on_built_positions(melee_pair):
+    """Positions the random ones rarely reach: a carrying worker between its
+    own base and the enemy's, a melee unit next to an enemy building (and,
+    with `melee_pair`, next to an enemy Light), a Ranged unit with targets at
+    and beyond range 3, and available buildings."""
+    from tests.test_oracle_rules import _built_position
+
+    bd = _built_position()
+    if melee_pair:
+        bd.place(51, 22)  # right of player 0's Light at cell 21
+    rows = bd.o.legality_rows(bd.st)
+    assert rows[0, 0, 3, ATTACK] == melee_pair  # player 0's Light (slot 5, position 3)
+    assert _masks_against_admission(bd.game, bd.o, bd.st) > 600
 
 
 # ---------------------------------------------------------------------------
@@ -515,3 +542,79 @@ def test_sampler_picks_legal_bits_and_is_uniform():
     assert not np.array_equal(a, o.sample_actions(rows, (8, 9), 1))
     assert not np.array_equal(a, o.sample_actions(rows, (8, 10), 0))
     assert not np.array_equal(a[:16], o.sample_actions(rows[:16], (8, 9), 0, env0=16))
+
+
+def test_decode_actions_closed_form():
+    """decode_actions (adapters/jaxmarl/actions.py:61-84, factors.py:117-151)
+    worked out by hand on basesWorkers8x8 (C 47): the direction comes from the
+    kind's own column, the produced type only for PRODUCE, the target cell
+    only for an on-board ATTACK (7x7 window, radius 3), a NONE lasts 1 cycle,
+    and a position without an available unit issues nothing."""
+    game, o, st = _eight()
+    st["pending_kind"][0, 50] = MOVE  # player 1's worker is busy
+    rows = _actions(game, {
+        (0, 0): [PRODUCE, 3, 2, 1, UP, WORKER, 11],       # base: direction UP, Worker
+        (0, 1): [ATTACK, 1, 2, 3, 1, 2, (0 + 3) * 7 + (2 + 3)],  # worker (1,1): (+2, 0) -> cell 11
+        (1, 0): [NONE, 3, 3, 3, 3, 3, 40],                # base: NONE for 1
+        (1, 1): [MOVE, LEFT, 0, 0, 0, 0, 0],              # busy: not issued
+        (0, 2): [MOVE, UP, 0, 0, 0, 0, 0],                # empty position: not issued
+    })
+    c = o.decode_actions(st, rows)
+    got = {f: c[f][0] for f in ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")}
+    want = {
+        (0, 0): (PRODUCE, UP, 0, -1, WORKER, -1),
+        (0, 1): (ATTACK, -1, 0, 11, -1, -1),
+        (1, 0): (NONE, -1, 1, -1, -1, -1),
+        (1, 1): (-1, -1, 0, -1, -1, -1),
+        (0, 2): (-1, -1, 0, -1, -1, -1),
+    }
+    names = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+    for (p, pos), fields in want.items():
+        assert tuple(int(got[n][p, pos]) for n in names) == fields, (p, pos)
+    # HARVEST / RETURN read their own columns; an ATTACK off the board has no
+    # target: the worker at (1,1) aiming (-3, 0) -> x = -2
+    st["pending_kind"][0, 50] = -1
+    rows = _actions(game, {(0, 1): [HARVEST, 1, 2, 3, 0, 0, 0], (1, 1): [RETURN, 1, 2, 3, 0, 0, 0]})
+    c = o.decode_actions(st, rows)
+    assert (int(c["direction"][0, 0, 1]), int(c["direction"][0, 1, 1])) == (2, 3)
+    rows = _actions(game, {(0, 1): [ATTACK, 0, 0, 0, 0, 0, (0 + 3) * 7 + (-3 + 3)]})
+    c = o.decode_actions(st, rows)
+    assert int(c["kind"][0, 0, 1]) == ATTACK and int(c["target_cell"][0, 0, 1]) == -1
+
+
+def test_sampler_follows_its_definition():
+    """The harness sampler's definition, restated in numpy over the host
+    threefry (itself pinned by the known answers above): per step the key is
+    fold_in(sample_key, step); position p = player * C + row of env e draws
+    (w0, w1) = threefry(k, (e, 2p)) and (w2, w3) = threefry(k, (e, 2p + 1));
+    factor f takes the 16-bit half f of w0..w3 (low half first) and picks the
+    ((h * popcount) >> 16)-th set bit of its mask, 0 when none is set; a row
+    with only the NONE bit comes out all zeros."""
+    from nanorts_amd import keys as hostkeys
+
+    game, partial = game_for("16x16-finetuned-both")
+    o, st = advanced_states(game, 6, 60, partial, 4, seed=5)
+    rows = o.avail_rows(st)
+    b = game.bucket
+    C = b.per_player_capacity
+    fields = _row_fields(b.unit_type_capacity, b.attack_offset_capacity)
+    sample_key = np.asarray([8, 9], np.uint32)
+    for step, env0 in ((0, 0), (7, 0), (3, 100)):
+        got = o.sample_actions(rows, sample_key, step, env0=env0)
+        k = hostkeys.fold_in(sample_key, step)
+        for l in range(rows.shape[0]):
+            for player in (0, 1):
+                for c in range(C):
+                    row = rows[l, player, c]
+                    if row[0] and row.sum() == 1:
+                        assert (got[l, player, c] == 0).all()
+                        continue
+                    p = player * C + c
+                    w0, w1 = hostkeys.threefry2x32(k, np.uint32(env0 + l), np.uint32(2 * p))
+                    w2, w3 = hostkeys.threefry2x32(k, np.uint32(env0 + l), np.uint32(2 * p + 1))
+                    words = [int(w0), int(w1), int(w2), int(w3)]
+                    for f, (lo, width) in enumerate(fields):
+                        h = (words[f // 2] >> (16 * (f % 2))) & 0xFFFF
+                        bits = np.nonzero(row[lo:lo + width])[0]
+                        want = int(bits[(h * len(bits)) >> 16]) if len(bits) else 0
+                        assert int(got[l, player, c, f]) == want, (step, l, player, c, f)

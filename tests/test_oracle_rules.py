@@ -51,8 +51,8 @@ RANDOM = ConflictStrategy.CANCEL_RANDOM
 class Board:
     """One env of a shipped 8x8 map, its oracle and its state."""
 
-    def __init__(self, name: str, strategy=BOTH, utt=UnitTypeTableVersion.ORIGINAL, root=(1, 2)):
-        self.game = map_name_to_scenario(name, utt=utt, conflict_strategy=strategy)
+    def __init__(self, name: str, strategy=BOTH, utt=UnitTypeTableVersion.ORIGINAL, root=(1, 2), max_cycles=5000):
+        self.game = map_name_to_scenario(name, utt=utt, conflict_strategy=strategy, max_cycles=max_cycles)
         self.o = Oracle(self.game)
         self.st = batch_initial(self.game, 1, np.asarray([root], np.uint32))
         self.root = np.asarray([root], np.uint32)
@@ -107,6 +107,31 @@ class Board:
 
         self.after_step(cmds, out)
         return out
+
+    def rows(self) -> np.ndarray:
+        """The legality rows of every owned position, uint8[2, C, 78]."""
+        rows = self.o.legality_rows(self.st)[0]
+        self.check_rows(rows)
+        return rows
+
+    def check_rows(self, rows: np.ndarray) -> None:
+        """Hook for a second implementation of the same rows (the GPU twin)."""
+
+    def avail(self) -> np.ndarray:
+        """get_avail_actions' rows of every owned position, uint8[2, C, 78]."""
+        rows = self.o.avail_rows(self.st)[0]
+        self.check_avail(rows)
+        return rows
+
+    def check_avail(self, rows: np.ndarray) -> None:
+        """Hook for a second implementation of the same rows (the GPU twin)."""
+
+    def payload(self, slot: int) -> tuple[int, ...]:
+        """Every pending_* leaf of a slot: (kind, direction, none_duration,
+        target_cell, produced_type, issued_at, completes_at, order)."""
+        return tuple(int(self.st[f"pending_{f}"][0, slot]) for f in (
+            "kind", "direction", "none_duration", "target_cell", "produced_type", "issued_at", "completes_at",
+            "order"))
 
     def before_step(self) -> None:
         """Hook called with the state about to be stepped."""
@@ -535,3 +560,555 @@ def _episode_roots(state) -> np.ndarray:
     from nanorts_amd import keys as hostkeys
 
     return np.stack([hostkeys.fold_in(r, int(e)) for r, e in zip(state["environment_root"], state["episode_index"])])
+
+
+# ---------------------------------------------------------------------------
+# Budget conflicts: only the same player's pending cost counts, and only for
+# a request that costs something (core/reservations.py:122-135)
+# basesWorkersBarracks8x8: player 0's barracks slot 4 at cell 4; player 1's
+# base slot 30 at cell 53 and barracks slot 32 at cell 59.  A Light costs 2
+# and takes 80 cycles, a Worker costs 1 and takes 50.
+# ---------------------------------------------------------------------------
+def test_over_budget_counts_only_the_same_players_pending_cost():
+    """Balances 2 / 2.  Player 0's barracks trains a Light (cost 2, admitted
+    first).  Player 1's base asks for a Worker (cost 1): player 0's pending
+    Light is not its cost, 0 + 1 <= 2, admitted.  Player 1's barracks asks for
+    a Light (cost 2): its own player's pending Worker counts, 1 + 2 > 2, a
+    same-cycle conflict, and CANCEL_BOTH turns both into NONEs of
+    min(50, 80) = 50."""
+    bd = BOARD("basesWorkersBarracks8x8")
+    bd.st["player_resources"][0] = [2, 2]
+    out = bd.step({4: {"kind": PRODUCE, "direction": DOWN, "produced_type": LIGHT},
+                   30: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER, "request_order": 0},
+                   32: {"kind": PRODUCE, "direction": UP, "produced_type": LIGHT, "request_order": 1}})
+    assert out["admitted_produce"][0].tolist() == [[0, 0, 0, 0, 1, 0, 0], [0, 0, 0, 1, 1, 0, 0]]
+    assert bd.pending(4) == (PRODUCE, 0, 80)
+    assert bd.pending(30) == (NONE, 50, 50) and bd.pending(32) == (NONE, 50, 50)
+    bd.run(79)
+    assert int(bd.st["time"][0]) == 80 and bd.st["player_resources"][0].tolist() == [0, 2]
+    assert int(bd.st["unit_type"][0, 5]) == LIGHT and bd.at(12) == 5
+
+
+def _three_bases(balance: int) -> Board:
+    """basesWorkers8x8 with two more bases of player 0 (slots 4 and 5 at
+    cells 12 and 14, born 6 and 7) and player 0 holding `balance`."""
+    bd = BOARD("basesWorkers8x8")
+    assert bd.spawn(4, BASE, 0, 12) == 6 and bd.spawn(5, BASE, 0, 14) == 7
+    bd.st["player_resources"][0, 0] = balance
+    return bd
+
+
+def test_free_request_beside_an_overdrawn_pending():
+    """Balance 2.  The three bases train Workers at times 0, 1 and 2 (into
+    cells 2, 4 and 6); every pair costs 2 <= 2, so all three are admitted.
+    The first two spawn at 50 and 51 and leave the balance at 0 while the
+    third (cost 1) is still pending.  At time 51 the worker asks to MOVE: it
+    costs 0, so the overdrawn pending is no budget conflict
+    (reservations.py:132, `requested.cost != 0`) and the MOVE is admitted.
+    At 52 the third Worker is unaffordable: nothing spawns, nothing
+    overflows."""
+    bd = _three_bases(2)
+    for t, base in enumerate((2, 4, 5)):
+        bd.step({base: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER}})
+        assert bd.pending(base) == (PRODUCE, 0, 50 + t)
+    bd.run(48)
+    assert int(bd.st["time"][0]) == 51 and bd.st["player_resources"][0].tolist() == [0, 5]
+    assert bd.at(2) == 6 and bd.at(4) == 7 and bd.pending(5) == (PRODUCE, 0, 52)
+    bd.step({3: {"kind": MOVE, "direction": DOWN}})
+    assert bd.pending(3) == (MOVE, 0, 61)
+    assert bd.at(6) == ABSENT and not bd.alive(8) and bd.st["spawn_overflow"][0].tolist() == [0, 0]
+    assert bd.st["player_resources"][0].tolist() == [0, 5]
+    bd.run(9)
+    assert int(bd.st["time"][0]) == 61 and bd.at(17) == 3
+
+
+# ---------------------------------------------------------------------------
+# Spawn overflow counts only an affordable newborn without a free slot
+# (core/kinds/produce.py:55-59)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("balance,overflow,left", [(2, 0, 0), (3, 1, 1)])
+def test_spawn_overflow_only_when_affordable(balance, overflow, left):
+    """Player 0's block (47 slots) is filled up to two free slots.  The three
+    bases train Workers in one cycle (request orders 0, 1, 2), all due at 50.
+    The first two spawn into the two free slots and pay 1 each; the third
+    finds no free slot.  With balance 2 it also cannot pay (0 - 1 < 0): no
+    overflow.  With balance 3 it could (1 - 1 >= 0): one overflow, and
+    nothing is paid."""
+    bd = _three_bases(balance)
+    free = [c for c in range(64) if bd.at(c) == ABSENT and c not in (2, 4, 6)]
+    for slot, cell in zip(range(6, 47), free):
+        bd.spawn(slot, WORKER, 0, cell)
+    bd.step({base: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER, "request_order": rank}
+             for rank, base in enumerate((2, 4, 5))})
+    assert [bd.pending(s) for s in (2, 4, 5)] == [(PRODUCE, 0, 50)] * 3
+    bd.run(49)
+    assert int(bd.st["time"][0]) == 50
+    assert bd.at(2) == 47 and bd.at(4) == 48 and bd.at(6) == ABSENT
+    assert bd.st["spawn_overflow"][0].tolist() == [overflow, 0]
+    assert bd.st["player_resources"][0].tolist() == [left, 5]
+
+
+# ---------------------------------------------------------------------------
+# Java admission order: by birth, not by slot position (admission.py:67-101)
+# Two Lights of player 0 race into cell 27: the older one (born 6) sits in
+# slot 10 at cell 26 and moves RIGHT, the newer one (born 7) sits in the
+# lower slot 4 at cell 19 and moves DOWN.  Both take 8 cycles.  The older
+# one's request is admitted first and the newer one's meets it.
+# ---------------------------------------------------------------------------
+def _birth_race_board(strategy, alternating=0, root=(1, 2)):
+    bd = BOARD("basesWorkers8x8", strategy, root=root)
+    assert bd.spawn(10, LIGHT, 0, 26) == 6
+    assert bd.spawn(4, LIGHT, 0, 19) == 7
+    bd.st["alternating_conflict_count"][0] = alternating
+    bd.step({10: {"kind": MOVE, "direction": RIGHT}, 4: {"kind": MOVE, "direction": DOWN}})
+    assert int(bd.st["pending_order"][0, 10]) == 0 and int(bd.st["pending_order"][0, 4]) == 1
+    return bd
+
+
+@pytest.mark.parametrize("alternating,mover,stays", [(0, 10, (4, 19)), (1, 4, (10, 26))])
+def test_admission_ranks_by_birth_before_position(alternating, mover, stays):
+    """CANCEL_ALTERNATING: an even count cancels the request (the newer
+    Light's), an odd one the pending MOVE (the older Light's)."""
+    bd = _birth_race_board(ALTERNATING, alternating)
+    loser = stays[0]
+    assert bd.pending(mover) == (MOVE, 0, 8) and bd.pending(loser) == (NONE, 8, 8)
+    bd.run(8)
+    assert bd.at(27) == mover and bd.at(stays[1]) == loser
+
+
+def test_admission_ranks_by_birth_before_position_random():
+    """CANCEL_RANDOM: the request is the newer Light's (born 7); its draw at
+    (root, time 0, birth 7, ordinal 0) cancels the request when 0.  The draws
+    are the reference's own (the "race3" vectors hold birth 7 at ordinal 0)."""
+    seen = set()
+    for row in golden("race3"):
+        draw = row["out"][1]
+        bd = _birth_race_board(RANDOM, root=tuple(row["root"]))
+        mover = 10 if draw == 0 else 4
+        bd.run(8)
+        assert bd.at(27) == mover, (row["root"], draw)
+        seen.add(draw)
+    assert seen == {0, 1}
+
+
+# ---------------------------------------------------------------------------
+# Pending ranking of this cycle's appended orders: admission order, not slot
+# position (pending.py:28-44)
+# basesWorkersBarracks8x8, player 0 holding 2, its worker moved to cell 11:
+#   U1: the worker (slot 3)   MOVEs RIGHT into 12       request order 0
+#   U2: the base (slot 2)     trains a Worker into 2    request order 1
+#   R : the barracks (slot 4) trains a Light into 12    request order 2
+# U1 and U2 are appended in that order (orders 0, 1) although U2's slot is
+# the lower one.  R meets U1 (cell 12) and U2 (1 + 2 > 2).
+# ---------------------------------------------------------------------------
+APPENDED = {
+    # U1 then U2: U1's conflict caps R at 10; U2 is cancelled with min(50, 10)
+    "both": ((NONE, 10, 10), (NONE, 10, 10), (NONE, 10, 10)),
+    # count 0 at U1 cancels R (cap 10); count 1 at U2 cancels U2 with min(50, 10)
+    "alternating0": ((MOVE, 0, 10), (NONE, 10, 10), (NONE, 10, 10)),
+}
+
+
+@pytest.mark.parametrize("label,strategy", [("both", BOTH), ("alternating0", ALTERNATING)])
+def test_appended_orders_rank_in_admission_order(label, strategy):
+    bd = BOARD("basesWorkersBarracks8x8", strategy)
+    bd.place(3, 11)
+    bd.st["player_resources"][0, 0] = 2
+    bd.step({3: {"kind": MOVE, "direction": RIGHT, "request_order": 0},
+             2: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER, "request_order": 1},
+             4: {"kind": PRODUCE, "direction": DOWN, "produced_type": LIGHT, "request_order": 2}})
+    assert [int(bd.st["pending_order"][0, s]) for s in (3, 2, 4)] == [0, 1, 2]
+    assert tuple(bd.pending(s) for s in (3, 2, 4)) == APPENDED[label]
+
+
+# ---------------------------------------------------------------------------
+# A pending conflict after a cross-cycle one settles to -1
+# (reservations.py:169-192, _CROSS_CYCLE_NONE_DURATION)
+# basesWorkersBarracks8x8: player 1's worker (slot 31) moves from cell 26 UP
+# into 18 at time 0.  At time 1, with player 0 holding 2, player 0's
+# barracks trains a Light into 12 (P2, request order 0) and its base a
+# Worker into 18 (R, request order 1).  R meets the time-0 MOVE first (a
+# cross-cycle conflict on cell 18), then P2 (same cycle, 1 + 2 > 2).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("strategy,alternating", [(BOTH, 0), (ALTERNATING, 1)])
+def test_pending_after_a_cross_cycle_conflict_settles_to_minus_one(strategy, alternating):
+    """Where P2's side is cancelled it takes min(80, -1) = -1 and R takes -1:
+    both are NONEs due at time 0 and are cleared by the same step; the MOVE
+    stays."""
+    bd = BOARD("basesWorkersBarracks8x8", strategy)
+    bd.place(31, 26)
+    bd.st["alternating_conflict_count"][0] = alternating
+    bd.step({31: {"kind": MOVE, "direction": UP}})
+    bd.st["player_resources"][0, 0] = 2
+    bd.step({4: {"kind": PRODUCE, "direction": DOWN, "produced_type": LIGHT, "request_order": 0},
+             2: {"kind": PRODUCE, "direction": DOWN, "produced_type": WORKER, "request_order": 1}})
+    assert bd.pending(31) == (MOVE, 0, 10)
+    assert bd.pending(4)[0] == ABSENT and bd.pending(2)[0] == ABSENT
+    if strategy == ALTERNATING:
+        assert int(bd.st["alternating_conflict_count"][0]) == alternating + 1
+    bd.run(80)
+    assert bd.at(18) == 31 and bd.at(12) == ABSENT and bd.st["player_resources"][0].tolist() == [2, 5]
+
+
+# ---------------------------------------------------------------------------
+# Members that died, or whose slot was refilled, earlier in the same batch
+# (completion.py:95 `alive`, move.py:25-27, harvest.py:30-45)
+# basesWorkers8x8: player 1's worker (slot 50) holds pending order 0 through
+# a long NONE and is re-commanded to ATTACK so that it completes first.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("refill", [False, True])
+def test_dead_mover_stays_put(refill):
+    """Orders: 50 (0), the base (1), the worker (2).  At time 60 the ATTACK
+    kills the worker (slot 3).  With `refill`, the base's PRODUCE (order 1)
+    then spawns a Worker into slot 3, the lowest free slot, at cell 2.  The
+    dead worker's MOVE into cell 1 comes last: its slot is empty, or holds a
+    newborn of another birth, so nothing moves."""
+    bd = BOARD("basesWorkers8x8")
+    bd.place(50, 17)
+    bd.step({50: {"kind": NONE, "none_duration": 1000}})
+    bd.step({2: {"kind": NONE, "none_duration": 1000}})
+    bd.step({3: {"kind": NONE, "none_duration": 1000}})
+    bd.run(7)
+    if refill:
+        bd.step({2: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER}})  # time 10
+        assert bd.pending(2) == (PRODUCE, 0, 60)
+    else:
+        bd.step()
+    bd.run(39)
+    bd.step({3: {"kind": MOVE, "direction": UP}})  # time 50
+    assert bd.pending(3) == (MOVE, 0, 60)
+    bd.run(4)
+    bd.step({50: {"kind": ATTACK, "target_cell": 9}})  # time 55
+    assert bd.pending(50) == (ATTACK, 0, 60)
+    assert [int(bd.st["pending_order"][0, s]) for s in (50, 2, 3)] == [0, 1, 2]
+    bd.run(3)
+    assert int(bd.st["time"][0]) == 59 and bd.at(9) == 3
+    bd.step()  # time 59 -> 60
+    assert bd.at(9) == ABSENT and bd.at(1) == ABSENT
+    if refill:
+        assert (int(bd.st["birth"][0, 3]), int(bd.st["cell"][0, 3])) == (6, 2) and bd.at(2) == 3
+        assert bd.st["player_resources"][0].tolist() == [4, 5]
+    else:
+        assert not bd.alive(3) and bd.at(2) == ABSENT and int(bd.st["cell"][0, 3]) == ABSENT
+
+
+@pytest.mark.parametrize("pile,left", [(20, 19), (1, 0)])
+def test_dead_harvester_still_drains_the_pile(pile, left):
+    """Player 0's worker at cell 1 HARVESTs pile 0 (cell 0) from time 1
+    (order 1, due at 21); player 1's worker below it at cell 9 ATTACKs it from
+    time 16 (order 0, due at 21).  The ATTACK kills the harvester first; its
+    HARVEST still takes 1 from the pile, and the dead worker receives
+    nothing.  A pile of 1 is left at 0 and removed."""
+    bd = BOARD("basesWorkers8x8")
+    bd.place(3, 1)
+    bd.place(50, 9)
+    bd.st["carried_resources"][0, 0] = pile
+    bd.step({50: {"kind": NONE, "none_duration": 1000}})
+    bd.step({3: {"kind": HARVEST, "direction": LEFT}})
+    assert bd.pending(3) == (HARVEST, 0, 21)
+    bd.run(14)
+    bd.step({50: {"kind": ATTACK, "target_cell": 1}})  # time 16
+    assert bd.pending(50) == (ATTACK, 0, 21)
+    bd.run(4)
+    bd.step()  # time 20 -> 21
+    assert not bd.alive(3) and int(bd.st["carried_resources"][0, 3]) == 0 and bd.at(1) == ABSENT
+    assert int(bd.st["carried_resources"][0, 0]) == left
+    assert bd.alive(0) == (left > 0) and bd.at(0) == (0 if left > 0 else ABSENT)
+
+
+@pytest.mark.parametrize("pile", [1, 2])
+def test_harvest_removes_a_pile_left_at_exactly_zero(pile):
+    """harvest.py:38: `left_in_stack <= 0` removes the pile.  A worker
+    harvests 1 from a pile of 1 (left 0: removed) or of 2 (left 1: stands)."""
+    bd = BOARD("basesWorkers8x8")
+    bd.place(3, 1)
+    bd.st["carried_resources"][0, 0] = pile
+    bd.step({3: {"kind": HARVEST, "direction": LEFT}})
+    bd.run(19)
+    assert int(bd.st["time"][0]) == 20 and int(bd.st["carried_resources"][0, 3]) == 1
+    assert int(bd.st["carried_resources"][0, 0]) == pile - 1
+    assert bd.alive(0) == (pile == 2) and bd.at(0) == (0 if pile == 2 else ABSENT)
+    rows = bd.rows()
+    assert rows[0, 1, HARVEST] == 0  # carrying: no HARVEST bit either way
+
+
+# ---------------------------------------------------------------------------
+# Attack damage is the attacker's (attack.py:90): a Light deals 2, a Heavy 4
+# (model/unit_types.py, ORIGINAL: both have 4 hit points, attack_time 5)
+# ---------------------------------------------------------------------------
+def test_attack_damage_is_the_attackers():
+    """Player 0's Light (cell 27) and player 1's Heavy (cell 28) attack each
+    other at time 0; both complete at 5, the Light first (order 0).  The
+    Light leaves the Heavy at 4 - 2 = 2; the Heavy takes the Light from 4 to
+    0 and removes it."""
+    bd = BOARD("basesWorkers8x8")
+    assert bd.spawn(4, LIGHT, 0, 27) == 6 and bd.spawn(51, HEAVY, 1, 28) == 7
+    bd.step({4: {"kind": ATTACK, "target_cell": 28}, 51: {"kind": ATTACK, "target_cell": 27}})
+    bd.run(3)
+    assert [int(bd.st["hit_points"][0, s]) for s in (4, 51)] == [4, 4]
+    bd.step()  # time 4 -> 5
+    assert int(bd.st["hit_points"][0, 51]) == 2 and bd.alive(51)
+    assert not bd.alive(4) and bd.at(27) == ABSENT
+
+
+# ---------------------------------------------------------------------------
+# Truncation at time >= max_cycles for a game that is not over
+# (outcome.py:27-36)
+# ---------------------------------------------------------------------------
+def test_truncation_at_max_cycles():
+    """max_cycles 6: truncated first after the sixth step (time 6), with the
+    sparse reward -1 / -1 (no winner)."""
+    bd = BOARD("basesWorkers8x8", max_cycles=6)
+    for t in range(1, 8):
+        out = bd.step()
+        assert int(bd.st["time"][0]) == t
+        assert bool(out["truncated"][0]) == (t >= 6) and not out["terminated"][0]
+        assert out["reward"][0].tolist() == ([-1.0, -1.0] if t >= 6 else [0.0, 0.0])
+
+
+def test_a_game_won_at_max_cycles_is_terminated_not_truncated():
+    """max_cycles 5: player 1 keeps only its worker, which player 0's worker
+    kills at time 5 (attack_time 5).  The game is over at 5: terminated,
+    not truncated, rewards 1 / -1."""
+    bd = BOARD("basesWorkers8x8", max_cycles=5)
+    em = bd.st["entity_at"].reshape(-1)
+    em[53] = ABSENT
+    for leaf in STATE_LEAVES:
+        if leaf.kind == "slot":
+            bd.st[leaf.name][0, 49] = leaf.fill
+    bd.place(50, 17)
+    bd.step({3: {"kind": ATTACK, "target_cell": 17}})
+    for _ in range(3):
+        out = bd.step()
+        assert not out["truncated"][0] and not out["terminated"][0]
+    out = bd.step()
+    assert int(bd.st["time"][0]) == 5
+    assert out["terminated"][0] and not out["truncated"][0] and out["reward"][0].tolist() == [1.0, -1.0]
+
+
+# ---------------------------------------------------------------------------
+# Legality rows of a built position, worked out bit by bit
+# (core/legality.py:32-64; none.py:19-20, move.py:15-21, harvest.py:15-27,
+# return_.py:15-31, produce.py:25-44, attack.py:57-75)
+# basesWorkers8x8 (ORIGINAL), balances 5 / 5:
+#   player 0: base (2) at cell 10 (2,1); worker (3) at 11 (3,1) carrying 1;
+#             Ranged (4) at 40 (0,5); Light (5) at 21 (5,2)
+#   player 1: base (49) moved to 12 (4,1); worker (50) moved to 43 (3,5);
+#             Light (51) at 57 (1,7); Heavy (52) at 59 (3,7); worker (53)
+#             at 62 (6,7) carrying 1, left of pile 1 (cell 63)
+# ---------------------------------------------------------------------------
+def _built_position(strategy=BOTH) -> Board:
+    bd = BOARD("basesWorkers8x8", strategy)
+    bd.place(49, 12)
+    bd.place(3, 11)
+    bd.st["carried_resources"][0, 3] = 1
+    bd.place(50, 43)
+    bd.spawn(4, RANGED, 0, 40)
+    bd.spawn(5, LIGHT, 0, 21)
+    bd.spawn(51, LIGHT, 1, 57)
+    bd.spawn(52, HEAVY, 1, 59)
+    bd.spawn(53, WORKER, 1, 62)
+    bd.st["carried_resources"][0, 53] = 1
+    return bd
+
+
+def _row(kinds=(), move=(), harvest=(), ret=(), produce=(), types=(), attack=()) -> list[int]:
+    """A 78-wide row: kind[6], move/harvest/return/produce directions [4]
+    each, produce type [7], attack offset [49]."""
+    row = [0] * 78
+    for k in (NONE, *kinds):
+        row[k] = 1
+    for base, dirs in ((6, move), (10, harvest), (14, ret), (18, produce)):
+        for d in dirs:
+            row[base + d] = 1
+    for t in types:
+        row[22 + t] = 1
+    for dx, dy in attack:
+        row[29 + attack_offset(dx, dy)] = 1
+    return row
+
+
+BUILT_ROWS = {
+    # base: cannot move or attack; a Worker (1 <= 5) into every free side
+    # (RIGHT holds the worker)
+    2: _row((PRODUCE,), produce=(UP, DOWN, LEFT), types=(WORKER,)),
+    # carrying worker: moves UP and DOWN; RETURN only LEFT into its own base,
+    # not RIGHT into player 1's; Barracks (5 <= 5) UP and DOWN, not a Base
+    # (10); attacks the enemy base at (+1, 0)
+    3: _row((MOVE, RETURN, PRODUCE, ATTACK), move=(UP, DOWN), ret=(LEFT,), produce=(UP, DOWN), types=(BARRACKS,),
+            attack=((1, 0),)),
+    # Ranged, range 3: the worker at (+3, 0) (9 <= 9) and the Light at
+    # (+1, +2) (5 <= 9), not the Heavy at (+3, +2) (13 > 9)
+    4: _row((MOVE, ATTACK), move=(UP, RIGHT, DOWN), attack=((3, 0), (1, 2))),
+    # Light, range 1: player 1's base is diagonal (-1, -1): 2 > 1
+    5: _row((MOVE,), move=(UP, RIGHT, DOWN, LEFT)),
+    # player 1's base: RIGHT of it is free, LEFT is player 0's worker
+    49: _row((PRODUCE,), produce=(UP, RIGHT, DOWN), types=(WORKER,)),
+    # player 1's worker: free all round, Barracks anywhere, nobody adjacent
+    50: _row((MOVE, PRODUCE), move=(UP, RIGHT, DOWN, LEFT), produce=(UP, RIGHT, DOWN, LEFT), types=(BARRACKS,)),
+    51: _row((MOVE,), move=(UP, RIGHT, LEFT)),
+    52: _row((MOVE,), move=(UP, RIGHT, LEFT)),
+    # carrying worker beside a pile: no HARVEST (hands full), no RETURN (no
+    # stockpile beside it)
+    53: _row((MOVE, PRODUCE), move=(UP, LEFT), produce=(UP, LEFT), types=(BARRACKS,)),
+}
+
+
+def test_legality_rows_of_a_built_position():
+    """Every owned position's row, bit by bit: each active unit has its NONE
+    bit (buildings included), empty positions are all zero."""
+    bd = _built_position()
+    rows = bd.rows()
+    for player in (0, 1):
+        for pos in range(bd.C):
+            slot = bd.N + player * bd.C + pos
+            want = BUILT_ROWS.get(slot, [0] * 78)
+            assert rows[player, pos].astype(int).tolist() == want, slot
+
+
+def test_return_into_an_enemy_base_is_not_admitted():
+    """The carrying worker asks to RETURN RIGHT into player 1's base: illegal,
+    so a NONE for move_time (10) that credits nothing; RETURN LEFT into its own
+    base is admitted and credits 1 at 10."""
+    bd = _built_position()
+    out = bd.step({3: {"kind": RETURN, "direction": RIGHT}})
+    assert out["admitted_return"][0].tolist() == [0, 0] and bd.pending(3) == (NONE, 10, 10)
+    bd.run(9)
+    assert bd.st["player_resources"][0].tolist() == [5, 5] and int(bd.st["carried_resources"][0, 3]) == 1
+    out = bd.step({3: {"kind": RETURN, "direction": LEFT}})
+    assert out["admitted_return"][0].tolist() == [1, 0] and bd.pending(3) == (RETURN, 0, 20)
+    bd.run(9)
+    assert bd.st["player_resources"][0].tolist() == [6, 5] and int(bd.st["carried_resources"][0, 3]) == 0
+
+
+def test_ranged_attack_at_exactly_its_range():
+    """The Ranged unit's ATTACK on the worker three cells right (9 <= 9) is
+    admitted and removes it at 5; its ATTACK on the Heavy at (+3, +2) is a
+    NONE for attack_time."""
+    bd = _built_position()
+    out = bd.step({4: {"kind": ATTACK, "target_cell": 43}})
+    assert out["admitted_attack"][0].tolist() == [[0, 0, 1], [0, 0, 0]] and bd.pending(4) == (ATTACK, 0, 5)
+    bd.run(4)
+    assert not bd.alive(50) and bd.at(43) == ABSENT
+    bd.step({4: {"kind": ATTACK, "target_cell": 59}})
+    assert bd.pending(4) == (NONE, 5, 10)
+    # get_avail_actions (adapters/jaxmarl/actions.py:28-41): a position
+    # without an available unit (empty, or holding a pending action) offers
+    # only NONE; an available unit offers its legality row
+    avail, rows = bd.avail(), bd.rows()
+    idle = [1] + [0] * 77
+    for player in (0, 1):
+        for pos in range(bd.C):
+            slot = bd.N + player * bd.C + pos
+            available = bd.alive(slot) and bd.pending(slot)[0] == ABSENT
+            want = rows[player, pos].astype(int).tolist() if available else idle
+            assert avail[player, pos].astype(int).tolist() == want, slot
+    assert bd.pending(4)[0] == NONE and avail[0, 2].astype(int).tolist() == idle
+
+
+def test_harvest_needs_empty_hands():
+    """harvest.py:15-21: player 1's worker carries 1 beside pile 1 and asks to
+    HARVEST it: a NONE for harvest_time (20)."""
+    bd = _built_position()
+    out = bd.step({53: {"kind": HARVEST, "direction": RIGHT}})
+    assert out["admitted_harvest"][0].tolist() == [0, 0] and bd.pending(53) == (NONE, 20, 20)
+
+
+def test_walls_block_moves_and_production():
+    """basesWorkers8x8Obstacle: walls on cells 26-29 and 34-37.  Player 0's
+    base moved to 20 (4,2) has a wall DOWN (28); its worker moved to 19 (3,2)
+    has a wall DOWN (27) and the base RIGHT.  Neither offers DOWN, and asking
+    for it gives a NONE of the requested duration."""
+    bd = BOARD("basesWorkers8x8Obstacle")
+    bd.place(2, 20)
+    bd.place(3, 19)
+    rows = bd.rows()
+    assert rows[0, 0].astype(int).tolist() == _row((PRODUCE,), produce=(UP, RIGHT), types=(WORKER,))
+    assert rows[0, 1].astype(int).tolist() == _row((MOVE, PRODUCE), move=(UP, LEFT), produce=(UP, LEFT),
+                                                   types=(BARRACKS,))
+    bd.step({3: {"kind": MOVE, "direction": DOWN}, 2: {"kind": PRODUCE, "direction": DOWN, "produced_type": WORKER}})
+    assert bd.pending(3) == (NONE, 10, 10) and bd.pending(2) == (NONE, 50, 50)
+
+
+def test_player_zero_is_admitted_before_an_older_player_one_unit():
+    """admission.py:86-101: the request key puts player 0's requests first,
+    birth only orders within a player.  Player 1's base (born 3) moved to 12
+    (4,1) trains a Worker UP into 4; player 0's worker (born 4) moved to 3
+    (3,0) MOVEs RIGHT into 4.  CANCEL_ALTERNATING, count 0: the second
+    request, the base's, is cancelled with min(50, 10)."""
+    bd = BOARD("basesWorkers8x8", ALTERNATING)
+    bd.place(49, 12)
+    bd.place(3, 3)
+    bd.step({49: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER}, 3: {"kind": MOVE, "direction": RIGHT}})
+    assert bd.pending(3) == (MOVE, 0, 10) and bd.pending(49) == (NONE, 10, 10)
+    assert int(bd.st["pending_order"][0, 3]) == 0 and int(bd.st["pending_order"][0, 49]) == 1
+    bd.run(9)
+    assert bd.at(4) == 3
+
+
+def test_pending_rows_keep_each_kinds_payload():
+    """admission.py:374-403 (_assign_pending_action) with each kind's
+    payload: MOVE and PRODUCE keep their direction, PRODUCE its type, ATTACK
+    its target cell, NONE only its duration; a MOVE's none_duration is 0
+    whatever the command held.  Orders follow admission (player 0 by birth:
+    base 2, worker 3; then player 1: base 49, worker 50), and a re-command
+    keeps its order without advancing next_pending_order."""
+    bd = BOARD("basesWorkers8x8")
+    bd.place(50, 17)
+    bd.step({3: {"kind": MOVE, "direction": UP, "none_duration": 7},
+             2: {"kind": PRODUCE, "direction": UP, "produced_type": WORKER},
+             49: {"kind": ATTACK, "target_cell": 54},
+             50: {"kind": ATTACK, "target_cell": 9}})
+    assert bd.payload(2) == (PRODUCE, UP, 0, ABSENT, WORKER, 0, 50, 0)
+    assert bd.payload(3) == (MOVE, UP, 0, ABSENT, ABSENT, 0, 10, 1)
+    # a base cannot attack: NONE for its attack_time (10)
+    assert bd.payload(49) == (NONE, ABSENT, 10, ABSENT, ABSENT, 0, 10, 2)
+    assert bd.payload(50) == (ATTACK, ABSENT, 0, 9, ABSENT, 0, 5, 3)
+    assert int(bd.st["next_pending_order"][0]) == 4
+    # a NONE keeps no direction, whatever the command held
+    bd.step({49: {"kind": NONE, "none_duration": 3, "direction": LEFT}})
+    assert bd.payload(49) == (NONE, ABSENT, 3, ABSENT, ABSENT, 1, 4, 2)
+    assert int(bd.st["next_pending_order"][0]) == 4
+    bd.run(2)  # the NONE completes at 4
+    assert int(bd.st["time"][0]) == 4
+    assert bd.payload(49)[0] == ABSENT and int(bd.st["pending_order"][0, 49]) == ABSENT
+    bd.step({49: {"kind": NONE, "none_duration": 2}})  # time 4: appended anew
+    assert bd.payload(49) == (NONE, ABSENT, 2, ABSENT, ABSENT, 4, 6, 4)
+    assert int(bd.st["next_pending_order"][0]) == 5
+
+
+def test_return_credits_what_is_carried():
+    """return_.py:40-49: the credit is the carried amount.  A worker holding
+    3 (a load only a custom table's harvest_amount produces; core.step takes
+    the state as it is) returns into its base: 5 + 3."""
+    bd = BOARD("basesWorkers8x8")
+    bd.st["carried_resources"][0, 3] = 3
+    bd.step({3: {"kind": RETURN, "direction": RIGHT}})
+    bd.run(9)
+    assert bd.st["player_resources"][0].tolist() == [8, 5] and int(bd.st["carried_resources"][0, 3]) == 0
+
+
+# ---------------------------------------------------------------------------
+# reset_where_done: the initial state again, one more episode
+# (adapters/lifecycle.py:57-79)
+# ---------------------------------------------------------------------------
+def test_reset_where_done_restarts_and_counts_episodes():
+    game = map_name_to_scenario("basesWorkers8x8", utt=UnitTypeTableVersion.ORIGINAL)
+    o = Oracle(game)
+    roots = np.asarray([[1, 2], [3, 4], [5, 6]], np.uint32)
+    st = batch_initial(game, 3, roots)
+    fresh = batch_initial(game, 3, roots)
+    C = game.bucket.per_player_capacity
+    actions = np.zeros((3, 2, C, 7), np.int32)
+    actions[:, 0, 1] = [MOVE, UP, 0, 0, 0, 0, 0]
+    for cycle in range(12):
+        o.env_step(st, actions if cycle == 0 else np.zeros_like(actions), False)
+    assert (st["cell"][:, 3] == 1).all() and (st["time"] == 12).all()
+    st["episode_index"][:] = [4, 7, 0]
+    before = {k: v.copy() for k, v in st.items()}
+    o.reset_where_done(st, np.asarray([1, 0, 1], np.uint8))
+    assert st["episode_index"].tolist() == [5, 7, 1]
+    assert st["environment_root"].tolist() == roots.tolist()
+    for leaf in STATE_LEAVES:
+        np.testing.assert_array_equal(st[leaf.name][[0, 2]], fresh[leaf.name][[0, 2]], err_msg=leaf.name)
+        np.testing.assert_array_equal(st[leaf.name][1], before[leaf.name][1], err_msg=leaf.name)
