@@ -64,6 +64,21 @@ class DeviceBoard(rules.Board):
         np.testing.assert_array_equal(got.astype(np.uint8), rows.astype(np.uint8), err_msg="legality rows")
         self.cycles = getattr(self, "cycles", 0) + 1
 
+    def check_avail(self, rows: np.ndarray) -> None:
+        import torch
+
+        from nanorts_amd import core, native
+        from nanorts_amd.env import State, _ptr, _stream
+        from nanorts_amd.model import LEAF_NAMES
+
+        dev = State({name: torch.as_tensor(np.ascontiguousarray(self.st[name]), device="cuda:0")
+                     for name in LEAF_NAMES})
+        out = torch.empty((1, 2, self.C, rows.shape[-1]), dtype=torch.uint8, device="cuda:0")
+        native.check(native.load().nanorts_amd_avail_actions(_stream(), core.device_game(self.game).ref,
+                                                             core._native_state(dev), 1, _ptr(out), None),
+                     "nanorts_amd_avail_actions")
+        np.testing.assert_array_equal(out.cpu().numpy()[0], rows.astype(np.uint8), err_msg="available rows")
+
 
 SCENARIOS = [
     ("dead attacker", rules.test_dead_attacker_still_hits, ()),
