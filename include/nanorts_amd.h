@@ -286,6 +286,21 @@ int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* co
                         const int64_t* lanes, const uint32_t* const* keys, const int64_t* key_lanes,
                         const nanorts_commands* commands, const nanorts_step_results* results);
 
+/* core.step over `groups` groups (1..16) in the operand and result order of
+ * the reference's FFI target nanorts_step_groups
+ * (src/nanorts/core/cuda/step.cu:704-808, operands built by
+ * src/nanorts/core/cycle.py:137-175, 198-211): group k's 33 operands are
+ * operands[33k .. 33k + 32] and its 31 results results[31k .. 31k + 30], each
+ * in nanorts_amd_step_ffi's order and meaning; lanes[k], key_lanes[k] and
+ * command_lanes[k] are group k's extents as there.  The groups share one
+ * bucket (height, width, neutral, capacity, types, the `strategy`
+ * attribute); each brings its own key, Commands, terrain, table, timings and
+ * state.  One launch per four groups, as nanorts_amd_step_groups. */
+int nanorts_amd_step_groups_ffi(void* stream, int32_t groups, const void* const* operands, void* const* results,
+                                const int64_t* lanes, const int64_t* key_lanes, const int64_t* command_lanes,
+                                int32_t height, int32_t width, int32_t neutral, int32_t capacity, int32_t types,
+                                int64_t strategy);
+
 /* Factored legality rows bool[L][2][C][22+T+O] (active units, availability not
  * applied).  Replaces nanorts_legality (src/nanorts/core/cuda/legality.cu:535-545). */
 int nanorts_amd_legality(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, uint8_t* rows);
@@ -426,6 +441,63 @@ int nanorts_amd_abstraction_act(void* stream, const nanorts_game* game, nanorts_
                             int32_t strategy, int32_t trained_type, const int32_t* player, int64_t player_lanes,
                             nanorts_abstract_actions carry, int32_t* commands);
 
+/* family.act of the rush strategies in the operand and result order of the
+ * reference's FFI target nanorts_abstraction_act
+ * (src/nanorts/bots/cuda/abstraction_act.cu:1231-1324, operands built by
+ * src/nanorts/bots/whole_act.py:125-162): the body a handler of that name
+ * calls with its buffers' device pointers.
+ *   operands[24]: 0-9 the State leaves the act reads: birth s32[E],
+ *     unit_type s8[E], owner s8[E], cell s16[E], carried_resources s32[E],
+ *     pending_kind s8[E], pending_direction s8[E], pending_produced_type
+ *     s8[E], entity_at s16[H][W], player_resources s32[2]; 10 terrain
+ *     pred[H][W]; 11 the bots' unit table s32[T][6] (can_harvest,
+ *     is_resource, is_stockpile, can_attack, attack_range, cost); 12 player
+ *     s32; 13-23 the carry (AbstractActions: kind, unit_birth, order, target,
+ *     target_birth, base, base_birth, cell, unit_type s32[L][C], trained
+ *     pred[L][C], next_order s32[L]).
+ *   operand_lanes[13]: the leading extents of operands 0-12, each 1 (one row
+ *     shared by every lane) or `lanes`; terrain and table must be 1.
+ *   results[12]: 0-10 the carry after the act (aliasing operands 13-23; an
+ *     unaliased result is first filled from its operand); 11 the Commands
+ *     s32[L][6][2][C].
+ * `strategy` and `trained` are the target's attributes: 0 worker rush, 1
+ * barracks rush training `trained`.  The defense strategies (2, 3) are
+ * refused with NANORTS_INVALID_ARGUMENT: the rush bots are the ones built.
+ * Index leaves are int16. */
+int nanorts_amd_abstraction_act_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes,
+                                    void* const* results, int64_t lanes, int32_t height, int32_t width,
+                                    int32_t entities, int32_t capacity, int32_t types, int64_t strategy,
+                                    int64_t trained);
+
+/* pathfinding.search per lane in the operand order of the reference's FFI
+ * target nanorts_astar_search (src/nanorts/bots/cuda/pathfinding.cu:20-104,
+ * called from src/nanorts/bots/pathfinding.py:102-118): free pred[*][H][W],
+ * start, target and range s32[*], each with `*_lanes` rows (1 shared or
+ * `lanes`); out s32[lanes][4] = found, first step, path length, pops
+ * (-1, -1 for the step and length when nothing is found).  Boards of at
+ * most 8192 cells. */
+int nanorts_amd_astar_search_ffi(void* stream, const uint8_t* free, int64_t free_lanes, const int32_t* start,
+                                 int64_t start_lanes, const int32_t* target, int64_t target_lanes,
+                                 const int32_t* range, int64_t range_lanes, int32_t width, int32_t height,
+                                 int32_t* out, int64_t lanes);
+
+/* abstraction's walk in the operand order of the reference's FFI target
+ * nanorts_astar_chain (src/nanorts/bots/cuda/abstraction.cu:98-301, called
+ * from src/nanorts/bots/abstraction.py:1001-1033).
+ *   operands[9]: free pred[*][H][W], claimed pred[*][H][W], rows
+ *     s32[*][capacity][columns] (start, goal, radius, draws, options, then
+ *     the desires' columns), queue s32[*][capacity], count s32[*],
+ *     moves_allowed pred[*], reserved s32[*], balance s32[*], draws
+ *     s32[*][draw_count]; operand_lanes[9] their leading extents (1 or
+ *     `lanes`).
+ *   out s32[lanes][capacity + 1][4]: per slot rank, selector, direction,
+ *     drew; then kept count, draws used, 0, 0.
+ * `drawing`, fallback[3] and blocked[3] (each desire's kind, claim and cost
+ * columns) are the target's attributes.  Boards of at most 8192 cells. */
+int nanorts_amd_astar_chain_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes, int32_t* out,
+                                int64_t lanes, int32_t width, int32_t height, int64_t capacity, int64_t columns,
+                                int64_t draw_count, int32_t drawing, const int64_t* fallback, const int64_t* blocked);
+
 /* seat.step_seat with a static learner seat in one launch: the bot plays
  * 1 - learner from the current state, the learner's action rows
  * int32[L][C][7] are decoded, the merged commands go through core.step under
@@ -486,6 +558,24 @@ int nanorts_amd_seat_rollout_lanes(void* stream, const nanorts_game* game, nanor
  * reference passes in are derived in the kernel. */
 int nanorts_amd_gridnet_decode(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                            const int32_t* actions, nanorts_command_buffers commands);
+
+/* GridNet decode_actions in the operand and result order of the reference's
+ * FFI target nanorts_gridnet_decode (src/nanorts/adapters/gridnet/cuda/decode.cu:
+ * 426-540, operands built by src/nanorts/adapters/gridnet/actions.py:199-232):
+ *   operands[11]: 0 actions s32[*][2][H][W][7]; 1 birth s32[*][E]; 2
+ *     pending_kind s8[*][E]; 3 cell s16[*][E]; 4 pending_direction
+ *     s8[*][E]; 5 pending_produced_type s8[*][E]; 6 player_resources
+ *     s32[*][2]; 7 move_direction pred[*][C][4], 8 produce_direction
+ *     pred[*][C][4] and 9 produce_type pred[*][C][T] (player 0's legality);
+ *     10 unit_cost s32[T] (shared).  operand_lanes[11]: their leading
+ *     extents, 1 or `lanes`.
+ *   results[6]: the Commands fields s32[L][2][C].
+ * height, width, neutral, capacity, types, costs and side are the target's
+ * attributes (costs must equal types; warp_words, the reference's own
+ * scratch size, plays no part).  Index leaves are int16. */
+int nanorts_amd_gridnet_decode_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes,
+                                   void* const* results, int64_t lanes, int32_t height, int32_t width, int32_t neutral,
+                                   int32_t capacity, int32_t types, int32_t costs, int32_t side);
 
 /* GridNet observe: planes, source mask and action mask of the state
  * (src/nanorts/adapters/gridnet/observation.py:27-72). */

@@ -576,6 +576,66 @@ NR_DEV int32_t astar_first_step(const KGame& g, AS3 int16_t* below, AS3 uint8_t*
     }
 }
 
+// The whole answer of pathfinding.search (N/bots/pathfinding.py:72-130): found,
+// the first step, the path's length and the number of pops, for the FFI
+// targets nanorts_astar_search and nanorts_astar_chain.  The same search as
+// astar_first_step (same stacks, same pop order); depth[] holds each
+// inserted cell's distance from the start.  mark[] comes in with 0 for open
+// and 1 for blocked cells; a start off the board finds nothing and pops
+// nothing.  The step of a path of length 0 is -1.
+struct AstarPath {
+    int32_t found, step, distance, pops;
+};
+NR_DEV AstarPath astar_path(int32_t W, int32_t H, AS3 int16_t* below, AS3 uint8_t* mark, AS3 int16_t* depth,
+                            int32_t start, int32_t target, int32_t range) {
+    AstarPath out = {0, kAbsent, kAbsent, 0};
+    if (start < 0 || start >= W * H) return out;
+    const int32_t tx = floor_mod(target, W), ty = floor_div(target, W);
+    const int32_t r2 = (int32_t)((uint32_t)range * (uint32_t)range);
+    mark[start] = 2;
+    depth[start] = 0;
+    int32_t cur = start, nxt = -1;
+    below[start] = -1;
+    while (true) {
+        if (cur < 0) {
+            if (nxt < 0) return out;
+            cur = nxt;
+            nxt = -1;
+        }
+        const int32_t pos = cur;
+        ++out.pops;
+        const int32_t py = pos / W, px = pos - py * W;
+        cur = below[pos];
+        const int32_t first = (int32_t)mark[pos] - 3;  // -1 at the start
+        const int32_t dx = px - tx, dy = py - ty;
+        if (dx * dx + dy * dy <= r2) {
+            out.found = 1;
+            out.distance = depth[pos];
+            // the offsets +W, -1, -W, +1 are told apart in that order: on a
+            // one-wide board an upward step (-W = -1) reads as LEFT
+            out.step = first < 0 ? kAbsent : ((first == 0 && W == 1) ? 3 : first);
+            return out;
+        }
+        const int32_t hcur = abs(dx) + abs(dy);
+        const int32_t dnext = depth[pos] + 1;
+        for (int32_t d = 0; d < 4; ++d) {
+            const int32_t nx = px + dir_dx(d), ny = py + dir_dy(d);
+            if (nx < 0 || nx >= W || ny < 0 || ny >= H) continue;
+            const int32_t nb = ny * W + nx;
+            if (mark[nb] != 0) continue;
+            mark[nb] = (uint8_t)(3 + (first < 0 ? d : first));
+            depth[nb] = (int16_t)dnext;
+            if (abs(nx - tx) + abs(ny - ty) < hcur) {
+                below[nb] = (int16_t)cur;
+                cur = nb;
+            } else {
+                below[nb] = (int16_t)nxt;
+                nxt = nb;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // abstraction.translate with the rush kinds and filler duration 10
 // (N/bots/abstraction.py:300-319 and the helpers cited below).

@@ -316,10 +316,10 @@ NR_DEV int32_t tabv(const Hdr& h, int field, int32_t type) { return h.tab[field 
 // produce_time, hit_points, attack_damage, harvest_amount.  The step reads no
 // sight radius, so F_SIGHT is 0; the legality targets pass no timings, whose
 // fields are then 0.
-NR_DEV int32_t ref_table_entry(const KGame& g, int field, int32_t t) {
+NR_DEV int32_t ref_table_entry(const KGame& g, const int32_t* table, const int32_t* timings, int field, int32_t t) {
     if (t >= g.T) return 0;
-    const int32_t* row = g.ref_table + t * (7 + g.T);
-    const int32_t* time = g.ref_timings ? g.ref_timings + t * 7 : nullptr;
+    const int32_t* row = table + t * (7 + g.T);
+    const int32_t* time = timings ? timings + t * 7 : nullptr;
     switch (field) {
         case F_COST: return row[6];
         case F_HP: return time ? time[4] : 0;
@@ -342,16 +342,47 @@ NR_DEV int32_t ref_table_entry(const KGame& g, int field, int32_t t) {
     }
 }
 
-NR_DEV int32_t table_entry(const KGame& g, int field, int32_t t) {
-    return g.ref_table ? ref_table_entry(g, field, t) : g.tab[field * 8 + t];
+NR_DEV int32_t table_entry(const KGame& g, const int32_t* table, const int32_t* timings, int field, int32_t t) {
+    return table ? ref_table_entry(g, table, timings, field, t) : g.tab[field * 8 + t];
 }
 
-NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
+// The LDS unit table from the whole-act bots' `table` operand [T][6]
+// (src/nanorts/bots/whole_act.py:33-40: can_harvest, is_resource,
+// is_stockpile, can_attack, attack_range, cost) or from the GridNet decode's
+// `unit_cost` [T] (cols = 1): the fields those targets read, the others 0.
+// Called by every thread of the workgroup after load_header and before its
+// barrier; each thread rewrites the entries it wrote.
+NR_DEV void load_operand_table(const KGame& g, const Hdr& h, const int32_t* rows, int32_t cols) {
     for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) {
         const int field = i >> 3, t = i & 7;
-        h.tab[i] = field == F_PACK ? (table_entry(g, F_FLAGS, t) & 0xFF) | ((table_entry(g, F_PRODUCES, t) & 0xFF) << 8) |
-                                         (table_entry(g, F_RANGE, t) << 16)
-                                   : table_entry(g, field, t);
+        int32_t v = 0;
+        if (t < g.T) {
+            const int32_t* row = rows + t * cols;
+            const int32_t flags = cols == 6 ? ((row[1] ? FL_RESOURCE : 0) | (row[2] ? FL_STOCKPILE : 0) |
+                                               (row[0] ? FL_HARVEST : 0) | (row[3] ? FL_ATTACK : 0))
+                                            : 0;
+            const int32_t range = cols == 6 ? row[4] : 0;
+            const int32_t cost = cols == 6 ? row[5] : row[0];
+            v = field == F_COST ? cost
+                : field == F_RANGE ? range
+                : field == F_FLAGS ? flags
+                : field == F_PACK ? ((flags & 0xFF) | (range << 16))
+                : 0;
+        }
+        h.tab[i] = v;
+    }
+}
+
+// `table` / `timings`: the reference's operands (see ref_table_entry), or
+// NULL for the game's own table.
+NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain, const int32_t* table,
+                        const int32_t* timings) {
+    for (int i = threadIdx.x; i < F_COUNT * 8; i += blockDim.x) {
+        const int field = i >> 3, t = i & 7;
+        h.tab[i] = field == F_PACK ? (table_entry(g, table, timings, F_FLAGS, t) & 0xFF) |
+                                         ((table_entry(g, table, timings, F_PRODUCES, t) & 0xFF) << 8) |
+                                         (table_entry(g, table, timings, F_RANGE, t) << 16)
+                                   : table_entry(g, table, timings, field, t);
     }
     if (threadIdx.x == 0) {
 #pragma unroll
@@ -361,7 +392,8 @@ NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
             h.seg[k].bytes = g.seg[k].bytes;
         }
     }
-    for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = terrain[i] ? 1 : 0;
+    // (a NULL terrain, for a target that reads none, stages an open board)
+    for (int i = threadIdx.x; i < g.cells; i += blockDim.x) h.terrain[i] = (terrain && terrain[i]) ? 1 : 0;
     if (g.fast_obs) {
         // the walls as bitmap rows, the blocked plane every cycle starts
         // from, packed from the terrain copy four cells per LDS read (W % 4
@@ -394,7 +426,7 @@ NR_DEV void load_header(const KGame& g, const Hdr& h, const uint8_t* terrain) {
         }
     }
 }
-NR_DEV void load_header(const KGame& g, const Hdr& h) { load_header(g, h, g.terrain); }
+NR_DEV void load_header(const KGame& g, const Hdr& h) { load_header(g, h, g.terrain, g.ref_table, g.ref_timings); }
 
 // ---------------------------------------------------------------------------
 // HBM <-> LDS row copies (16-byte, 4-byte or 1-byte granules by alignment)

@@ -69,9 +69,11 @@ NR_DEV GridRow grid_row(const KGame& g, const int32_t* row, int32_t at_cell) {
 // [players][cells][7] block; `sink(p, kind, dir, none, target, ptype, order)`
 // receives every owned position p of the first `players` players once
 // (players 1: player 0 alone, whose decode never reads player 1's rows).
-template <typename Sink>
-NR_DEV void gridnet_decode(const KGame& g, const Hdr& h, const Env& e, const GridLayout& y, const int32_t* acts,
-                           int32_t players, int lane, Sink sink) {
+// `legal(i, r)` tells whether player 0's kept row r of its unit at position
+// i (slot N + i) is legal, the issued usage's filter (:124-139).
+template <typename Sink, typename Legal>
+NR_DEV void gridnet_decode_by(const KGame& g, const Hdr& h, const Env& e, const GridLayout& y, const int32_t* acts,
+                              int32_t players, int lane, Sink sink, Legal legal) {
     const int32_t W = g.W, cells = g.cells, C = g.C, T = g.T;
     const int32_t domain = cells + 2 * W + 1, words = (domain + 31) / 32, margin = W;
     AS3 uint32_t* base = gat<uint32_t>(e, y, y.base);
@@ -164,15 +166,11 @@ NR_DEV void gridnet_decode(const KGame& g, const Hdr& h, const Env& e, const Gri
             for (int32_t k = lane; k < n; k += kWave) {
                 const int32_t pk = pos[k];
                 if (!kept[k] || pk < 0) continue;
-                const int32_t slot = first + order[k];
-                const int32_t at = e.cell[slot];
+                const int32_t i = order[k];
+                const int32_t at = e.cell[first + i];
                 const int32_t* row = acts + ((int64_t)player * cells + clampi(at, 0, cells - 1)) * 7;
                 const GridRow r = grid_row(g, row, at);
-                const Row lr = legality_row(g, h, e, slot);
-                const bool legal = r.kind == kKindMove
-                                       ? row_bit(lr, 6 + gidx(r.dir, 4))
-                                       : (row_bit(lr, 18 + gidx(r.dir, 4)) && row_bit(lr, 22 + gidx(r.ptype, T)));
-                if (!legal) continue;
+                if (!legal(i, r)) continue;
                 if (pk < domain - 1) __atomic_fetch_or(&base[pk >> 5], 1u << (pk & 31), __ATOMIC_RELAXED);
                 if (r.kind == kKindProduce) produced = wadd(produced, cost[k]);
             }
@@ -212,6 +210,17 @@ NR_DEV void gridnet_decode(const KGame& g, const Hdr& h, const Env& e, const Gri
         }
         wave_sync();
     }
+}
+
+// The decode with player 0's legality from the state (legality_row).
+template <typename Sink>
+NR_DEV void gridnet_decode(const KGame& g, const Hdr& h, const Env& e, const GridLayout& y, const int32_t* acts,
+                           int32_t players, int lane, Sink sink) {
+    gridnet_decode_by(g, h, e, y, acts, players, lane, sink, [&](int32_t i, const GridRow& r) {
+        const Row lr = legality_row(g, h, e, g.N + i);
+        return r.kind == kKindMove ? row_bit(lr, 6 + gidx(r.dir, 4))
+                                   : (row_bit(lr, 18 + gidx(r.dir, 4)) && row_bit(lr, 22 + gidx(r.ptype, g.T)));
+    });
 }
 
 // Wave-cooperative writers for 64-cell chunks: lane i holds the words of

@@ -553,6 +553,26 @@ bool state_complete(const nanorts_state& s) {
     if (l >= lanes) return;                                                       \
     const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
 
+// The prologue with the unit table taken from a table operand of the
+// reference (load_operand_table) instead of the game's own.
+#define NR_KERNEL_PROLOGUE_OPERAND_TABLE(rows, cols)                              \
+    extern __shared__ __align__(16) uint8_t nr_lds[];                             \
+    AS3 uint8_t* lds = (AS3 uint8_t*)nr_lds;                                      \
+    Hdr hdr;                                                                      \
+    hdr.tab = (AS3 int32_t*)lds;                                                  \
+    hdr.terrain = lds + g.lay.o_terrain;                                          \
+    hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);                                      \
+    hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);                               \
+    hdr.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);                             \
+    load_header(g, hdr);                                                          \
+    load_operand_table(g, hdr, rows, cols);                                       \
+    __syncthreads();                                                              \
+    const int lane = lane_id();                                                   \
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));     \
+    const int64_t l = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;             \
+    if (l >= lanes) return;                                                       \
+    const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
+
 // Canonical commands from the reference's int32 Commands operands.
 NR_DEV void stage_commands(const KGame& g, const Env& e, int64_t l, const nanorts_commands& c, int lane) {
     const Layout& y = g.lay;
@@ -638,8 +658,11 @@ struct GroupSlot {
     nanorts_step_results r;
     const uint32_t* key;
     int64_t key_lanes;
+    int64_t cmd_lanes;  // 1: one Commands row for every lane
     int64_t lanes;
     const uint8_t* terrain;
+    const int32_t* table;    // the group's own table / timings operands, or NULL: the launch's table
+    const int32_t* timings;
     int32_t max_cycles;
     uint32_t first_block;
 };
@@ -668,7 +691,7 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
     hdr.seg = (AS3 Seg*)(lds + g.lay.o_seg);
     hdr.disk = (AS3 uint32_t*)(lds + g.lay.o_disk);
     hdr.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);
-    load_header(g, hdr, sl.terrain);
+    load_header(g, hdr, sl.terrain, sl.table ? sl.table : g.ref_table, sl.table ? sl.timings : g.ref_timings);
     __syncthreads();
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -677,7 +700,7 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
     const Env e = env_view(g, lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
     load_env(g, sl.s, l, e, LD_ALL, lane);
     count_units(g, e, lane);
-    stage_commands(g, e, l, sl.c, lane);
+    stage_commands(g, e, sl.cmd_lanes == 1 ? 0 : l, sl.c, lane);
     const int64_t kl = sl.key_lanes == 1 ? 0 : l;
     const uint32_t k0 = sl.key[2 * kl], k1 = sl.key[2 * kl + 1];
     const nanorts_step_results r = sl.r;
@@ -1042,11 +1065,8 @@ struct BotArgs {
 
 // family.act for the rush strategies (N/bots/family.py:34-41): commands
 // int32[L][6][2][C] and the carry updated in place.
-__global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes, nanorts_state s, BotArgs a,
-                                                         const int32_t* player, int64_t player_lanes,
-                                                         int32_t* commands) {
-    NR_KERNEL_PROLOGUE
-    load_env(g, s, l, e, LD_ALL, lane);
+NR_DEV void act_and_emit(const KGame& g, const Hdr& hdr, const Env& e, const BotArgs& a, int64_t l,
+                         const int32_t* player, int64_t player_lanes, int32_t* commands, int lane) {
     Bot b;
     b.base = e.base + a.y.origin;
     b.player = clampi(player[player_lanes == 1 ? 0 : l], 0, 1);
@@ -1061,6 +1081,210 @@ __global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes,
         for (int f = 0; f < 6; ++f) out[f * owned + p] = v[f];
     }
     settle_carry(g, b, a.y, l, a.carry, lane);
+}
+
+__global__ __launch_bounds__(256) void k_abstraction_act(KGame g, int64_t lanes, nanorts_state s, BotArgs a,
+                                                         const int32_t* player, int64_t player_lanes,
+                                                         int32_t* commands) {
+    NR_KERNEL_PROLOGUE
+    load_env(g, s, l, e, LD_ALL, lane);
+    act_and_emit(g, hdr, e, a, l, player, player_lanes, commands, lane);
+}
+
+// family.act from the reference's operands: the ten State leaves the act
+// reads (the bots read no others), each one row per lane or one row shared by
+// every lane; `shared` holds the LD_* flags of the shared ones, LD_SCALARS
+// standing for player_resources.  The balances are the only scalars set.
+__global__ __launch_bounds__(256) void k_abstraction_act_operands(KGame g, int64_t lanes, nanorts_state s,
+                                                                  const int32_t* table, uint32_t shared, BotArgs a,
+                                                                  const int32_t* player, int64_t player_lanes,
+                                                                  int32_t* commands) {
+    NR_KERNEL_PROLOGUE_OPERAND_TABLE(table, 6)
+    const uint32_t read = LD_BIRTH | LD_UTYPE | LD_OWNER | LD_CELL | LD_CARRIED | LD_PKIND | LD_PDIR | LD_PPTYPE | LD_ENTITY;
+    load_env(g, s, l, e, read & ~shared, lane);
+    if ((read & shared) != 0u) load_env(g, s, 0, e, read & shared, lane);
+    if (lane < S_COUNT) {
+        const int64_t row = (shared & LD_SCALARS) ? 0 : l;
+        e.sc[lane] = lane == S_RES0 ? s.player_resources[2 * row] : (lane == S_RES1 ? s.player_resources[2 * row + 1] : 0);
+    }
+    wave_sync();
+    act_and_emit(g, hdr, e, a, l, player, player_lanes, commands, lane);
+}
+
+// The A* FFI targets: one wave per lane, each wave's scratch in its own LDS
+// region (mark bytes, then the below and depth int16 rows, then the chain's
+// flag bytes); operands hold one row per lane or one shared row (stride 0).
+struct AstarArgs {
+    const uint8_t* free;      // [cells] bool
+    const uint8_t* claimed;   // chain: [cells] bool
+    const int32_t* start;     // search: start, target, range
+    const int32_t* target;
+    const int32_t* range;
+    const int32_t* rows;      // chain: [capacity][columns]
+    const int32_t* queue;     // chain: [capacity]
+    const int32_t* count;     // chain: scalars count, moves_allowed, reserved, balance
+    const uint8_t* moves;
+    const int32_t* reserved;
+    const int32_t* balance;
+    const int32_t* draws;     // chain: [draw_count]
+    int64_t free_stride, claimed_stride, start_stride, target_stride, range_stride, rows_stride, queue_stride,
+        count_stride, moves_stride, reserved_stride, balance_stride, draws_stride;
+    int64_t lanes, capacity, columns, draw_count;
+    int32_t W, H, waves, region, drawing;
+    int32_t fallback[3], blocked[3];  // columns of each desire's kind, claim, cost
+    int32_t* out;
+};
+
+NR_DEV void astar_region(const AstarArgs& a, AS3 uint8_t** mark, AS3 int16_t** below, AS3 int16_t** depth,
+                         AS3 uint8_t** flags, int wave) {
+    extern __shared__ __align__(16) uint8_t nr_lds[];
+    const int32_t cells = a.W * a.H;
+    AS3 uint8_t* base = (AS3 uint8_t*)nr_lds + (int64_t)wave * a.region;
+    *mark = base;
+    *below = (AS3 int16_t*)(base + ((cells + 15) & ~15));
+    *depth = *below + ((cells + 7) & ~7);
+    *flags = (AS3 uint8_t*)(*depth + ((cells + 7) & ~7));
+}
+
+// pathfinding.search per lane: out[l] = found, step, distance, pops.
+// Replaces the FFI target nanorts_astar_search (N/bots/cuda/pathfinding.cu:20-104).
+__global__ __launch_bounds__(256) void k_astar_search(AstarArgs a) {
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t l = (int64_t)blockIdx.x * a.waves + wave;
+    if (l >= a.lanes) return;
+    AS3 uint8_t *mark, *flags;
+    AS3 int16_t *below, *depth;
+    astar_region(a, &mark, &below, &depth, &flags, wave);
+    const int32_t cells = a.W * a.H;
+    const uint8_t* free = a.free + l * a.free_stride;
+    for (int32_t c = lane; c < cells; c += kWave) mark[c] = free[c] ? 0 : 1;
+    wave_sync();
+    if (lane == 0) {
+        const AstarPath path = astar_path(a.W, a.H, below, mark, depth, a.start[l * a.start_stride],
+                                          a.target[l * a.target_stride], a.range[l * a.range_stride]);
+        int32_t* o = a.out + l * 4;
+        o[0] = path.found;
+        o[1] = path.step;
+        o[2] = path.distance;
+        o[3] = path.pops;
+    }
+}
+
+// A neighbour cell by the chain's offsets (UP -W, RIGHT +1, DOWN +W, any
+// other direction -1), in wrapping arithmetic.
+NR_DEV int32_t chain_neighbour(int32_t cell, int32_t direction, int32_t W) {
+    const int32_t offset = direction == 0 ? -W : (direction == 1 ? 1 : (direction == 2 ? W : -1));
+    return (int32_t)((uint32_t)cell + (uint32_t)offset);
+}
+
+// The first direction from `first` (turning by +1 mod 4) that `options`
+// allows, or -1.
+NR_DEV int32_t chain_drawn_direction(int32_t first, int32_t options) {
+    for (int32_t turn = 0; turn < 4; ++turn) {
+        const int32_t d = (int32_t)(((uint32_t)first + (uint32_t)turn) & 3u);
+        if ((options >> d) & 1) return d;
+    }
+    return kAbsent;
+}
+
+// The walk of abstraction._walked (N/bots/abstraction.py:804-952) as the FFI
+// target nanorts_astar_chain runs it (N/bots/cuda/abstraction.cu:98-215): the
+// queued rows in order, each searched from its start toward its goal on the
+// cells still open; a unit that can step and may move claims the step's
+// cell, one that can step but may not takes its blocked desire, one that
+// cannot takes its fallback (or, in a drawing pass, a drawn direction); a
+// desire is kept when its claim is free and its cost stays within the
+// balance beside the reserve and the costs already kept.  Per slot: rank
+// among the kept (or -1), selector (0 fell back, 1 blocked, 2 moved),
+// direction, drew; then one totals row: kept count, draws used.
+__global__ __launch_bounds__(256) void k_astar_chain(AstarArgs a) {
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t l = (int64_t)blockIdx.x * a.waves + wave;
+    if (l >= a.lanes) return;
+    AS3 uint8_t *mark, *flags;
+    AS3 int16_t *below, *depth;
+    astar_region(a, &mark, &below, &depth, &flags, wave);
+    const int32_t W = a.W, cells = a.W * a.H;
+    constexpr uint8_t kOpen = 1, kTaken = 2;
+    const uint8_t* free = a.free + l * a.free_stride;
+    const uint8_t* claimed = a.claimed + l * a.claimed_stride;
+    for (int32_t c = lane; c < cells; c += kWave) flags[c] = (free[c] ? kOpen : 0) | (claimed[c] ? kTaken : 0);
+    const int64_t cap = a.capacity;
+    int32_t* decisions = a.out + l * (cap + 1) * 4;
+    for (int64_t i = lane; i < cap * 4; i += kWave) {
+        const int64_t f = i & 3;
+        decisions[i] = (f == 0 || f == 2) ? kAbsent : 0;
+    }
+    const int32_t* entries = a.rows + l * a.rows_stride;
+    const int32_t* order = a.queue + l * a.queue_stride;
+    const int32_t* drawn = a.draws + l * a.draws_stride;
+    const bool moves = a.moves[l * a.moves_stride] != 0;
+    const uint32_t reserve = (uint32_t)a.reserved[l * a.reserved_stride];
+    const int32_t held = a.balance[l * a.balance_stride];
+    const int32_t asked = a.count[l * a.count_stride];
+    const int64_t searched = asked < 0 ? 0 : (asked > cap ? cap : (int64_t)asked);
+    uint32_t kept_cost = 0u;
+    int32_t kept_count = 0;
+    int64_t calls = 0;
+    for (int64_t row = 0; row < searched; ++row) {
+        wave_sync();
+        const int32_t slot = order[row];
+        if (slot < 0 || slot >= cap) continue;
+        for (int32_t c = lane; c < cells; c += kWave) mark[c] = (flags[c] & kOpen) ? 0 : 1;
+        wave_sync();
+        if (lane == 0) {
+            const int32_t* entry = entries + (int64_t)slot * a.columns;
+            const int32_t start = entry[0];
+            const AstarPath path = astar_path(W, a.H, below, mark, depth, start, entry[1], entry[2]);
+            const bool stepped = path.step != kAbsent;
+            int32_t selector = 0, direction = kAbsent;
+            bool eligible = entry[a.fallback[0]] != kAbsent;
+            int32_t claim = entry[a.fallback[1]], cost = entry[a.fallback[2]];
+            if (stepped && moves) {
+                selector = 2;
+                direction = path.step;
+                eligible = true;
+                claim = chain_neighbour(start, direction, W);
+                cost = 0;
+            } else if (stepped) {
+                selector = 1;
+                eligible = entry[a.blocked[0]] != kAbsent;
+                claim = entry[a.blocked[1]];
+                cost = entry[a.blocked[2]];
+            }
+            const bool drew = a.drawing && entry[3] != 0 && !(stepped && moves);
+            if (drew) {
+                const int64_t at = calls < a.draw_count ? calls : a.draw_count - 1;
+                selector = 2;
+                direction = chain_drawn_direction(drawn[at], entry[4]);
+                eligible = true;
+                claim = direction == kAbsent ? kAbsent : chain_neighbour(start, direction, W);
+                cost = 0;
+                ++calls;
+            }
+            const bool on_board = claim >= 0 && claim < cells;
+            const bool conflicting = on_board && (flags[claim] & kTaken) != 0;
+            const bool over = cost > 0 && (int32_t)(reserve + kept_cost + (uint32_t)cost) > held;
+            const bool kept = eligible && !conflicting && !over;
+            if (on_board) flags[claim] = (uint8_t)((flags[claim] & ~kOpen) | (kept ? kTaken : 0));
+            int32_t* d = decisions + (int64_t)slot * 4;
+            d[0] = kept ? kept_count : kAbsent;
+            d[1] = selector;
+            d[2] = direction;
+            d[3] = drew ? 1 : 0;
+            if (kept) {
+                kept_cost += (uint32_t)cost;
+                ++kept_count;
+            }
+        }
+        kept_count = __builtin_amdgcn_readfirstlane(kept_count);
+        kept_cost = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)kept_cost);
+        calls = (int64_t)__builtin_amdgcn_readfirstlane((int32_t)calls);
+    }
+    wave_sync();
+    if (lane < 4) decisions[cap * 4 + lane] = lane == 0 ? kept_count : (lane == 1 ? (int32_t)calls : 0);
 }
 
 // seat.step_seat (N/bots/seat.py:84-149): the bot's commands from the current
@@ -1731,6 +1955,51 @@ __global__ __launch_bounds__(256) void k_gridnet_decode(KGame g, int64_t lanes, 
                    });
 }
 
+// GridNet decode from the reference's operands (the FFI target
+// nanorts_gridnet_decode): per-lane strides in elements, 0 for an operand
+// shared by every lane; player 0's legality comes from the move_direction,
+// produce_direction and produce_type operands instead of the state.
+struct GridOperands {
+    const int32_t* actions;
+    const uint8_t* move;
+    const uint8_t* pdir;
+    const uint8_t* ptype;
+    int64_t actions_stride, move_stride, pdir_stride, ptype_stride;
+};
+__global__ __launch_bounds__(256) void k_gridnet_decode_operands(KGame g, int64_t lanes, nanorts_state s,
+                                                                 const int32_t* unit_cost, uint32_t shared,
+                                                                 GridLayout gy, GridOperands o,
+                                                                 nanorts_command_buffers out) {
+    NR_KERNEL_PROLOGUE_OPERAND_TABLE(unit_cost, 1)
+    const uint32_t read = LD_BIRTH | LD_PKIND | LD_CELL | LD_PDIR | LD_PPTYPE;
+    load_env(g, s, l, e, read & ~shared, lane);
+    if ((read & shared) != 0u) load_env(g, s, 0, e, read & shared, lane);
+    if (lane < S_COUNT) {
+        const int64_t row = (shared & LD_SCALARS) ? 0 : l;
+        e.sc[lane] = lane == S_RES0 ? s.player_resources[2 * row] : (lane == S_RES1 ? s.player_resources[2 * row + 1] : 0);
+    }
+    wave_sync();
+    const int32_t owned = 2 * g.C;
+    const uint8_t* move = o.move + l * o.move_stride;
+    const uint8_t* pdir = o.pdir + l * o.pdir_stride;
+    const uint8_t* ptype = o.ptype + l * o.ptype_stride;
+    gridnet_decode_by(
+        g, hdr, e, gy, o.actions + l * o.actions_stride, 2, lane,
+        [&](int32_t p, int32_t kind, int32_t dir, int32_t none, int32_t target, int32_t pt, int32_t order) {
+            const int64_t at = l * owned + p;
+            out.kind[at] = kind;
+            out.direction[at] = dir;
+            out.none_duration[at] = none;
+            out.target_cell[at] = target;
+            out.produced_type[at] = pt;
+            out.request_order[at] = order;
+        },
+        [&](int32_t i, const GridRow& r) {
+            return r.kind == kKindMove ? move[i * 4 + gidx(r.dir, 4)] != 0
+                                       : (pdir[i * 4 + gidx(r.dir, 4)] != 0 && ptype[i * g.T + gidx(r.ptype, g.T)] != 0);
+        });
+}
+
 // GridNet observe (N/adapters/gridnet/observation.py:27-72).
 __global__ __launch_bounds__(256) void k_gridnet_observe(KGame g, int64_t lanes, nanorts_state s, nanorts_gridnet_obs o) {
     NR_KERNEL_PROLOGUE
@@ -2054,8 +2323,10 @@ const char* nanorts_amd_entries(void) {
     return "nanorts_amd_step,nanorts_amd_step_ffi,nanorts_amd_legality,nanorts_amd_legality_words,nanorts_amd_legality_ffi,"
            "nanorts_amd_avail_actions,nanorts_amd_visible_cells,nanorts_amd_visible_cells_ffi,nanorts_amd_reset_rows_ffi,"
            "nanorts_amd_observe,nanorts_amd_pixels,nanorts_amd_pixels_from_maps,nanorts_amd_reset_where_done,nanorts_amd_env_step,nanorts_amd_sample_actions,"
-           "nanorts_amd_step_groups,nanorts_amd_env_transition,nanorts_amd_decode_actions,nanorts_amd_rollout,nanorts_amd_abstraction_act,nanorts_amd_seat_step,nanorts_amd_seat_rollout,"
-           "nanorts_amd_seat_step_lanes,nanorts_amd_seat_rollout_lanes,nanorts_amd_episode_seats,nanorts_amd_gridnet_decode,"
+           "nanorts_amd_step_groups,nanorts_amd_step_groups_ffi,nanorts_amd_env_transition,nanorts_amd_decode_actions,nanorts_amd_rollout,"
+           "nanorts_amd_abstraction_act,nanorts_amd_abstraction_act_ffi,nanorts_amd_seat_step,nanorts_amd_seat_rollout,"
+           "nanorts_amd_seat_step_lanes,nanorts_amd_seat_rollout_lanes,nanorts_amd_episode_seats,nanorts_amd_astar_search_ffi,"
+           "nanorts_amd_astar_chain_ffi,nanorts_amd_gridnet_decode,nanorts_amd_gridnet_decode_ffi,"
            "nanorts_amd_gridnet_observe,nanorts_amd_gridnet_step,nanorts_amd_gridnet_step_against,nanorts_amd_gridnet_sample_actions";
 }
 
@@ -2230,22 +2501,79 @@ static int zero_bytes(hipStream_t stream, void* p, int64_t n) {
     return NANORTS_OK;
 }
 
-int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
-                         int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
-                         int32_t capacity, int32_t types, int64_t strategy) {
-    if (!operands || !results) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operands or results is NULL");
-    if (strategy < NANORTS_CANCEL_BOTH || strategy > NANORTS_CANCEL_ALTERNATING)
-        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: strategy must be 0, 1 or 2");
-    if (lanes < 0 || (lanes > 0 && (key_lanes != 1 && key_lanes != lanes)))
-        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the key operand holds 1 or `lanes` rows");
-    if (lanes > 0 && command_lanes != 1 && command_lanes != lanes)
-        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the Commands operands hold 1 or `lanes` rows");
+// One group of the step target's operands and results (nanorts_amd_step_ffi's
+// order) as the kernel's State, Commands and results.  A result that does not
+// alias its state operand is first filled from it, so the step runs in the
+// result buffers.  The per-slot event records (results 27-30) are written as
+// "no member".
+static int step_operands(hipStream_t st, const char* target, const void* const* operands, void* const* results,
+                         int64_t lanes, int64_t E, int64_t cells, nanorts_state* s, nanorts_commands* c,
+                         nanorts_step_results* r) {
     for (int i = 0; i < 33; ++i)
-        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operand " + std::to_string(i) + " is NULL");
+        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": operand " + std::to_string(i) + " is NULL");
     for (int i = 0; i < 31; ++i)
-        if (!results[i]) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: result " + std::to_string(i) + " is NULL");
-    // The bucket from the extents; the unit table columns stay zero here and
-    // come from the table / timings operands in the kernel.
+        if (!results[i]) return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": result " + std::to_string(i) + " is NULL");
+    // Bytes per lane of the 23 state leaves in the reference's order.
+    const int64_t leaf_bytes[23] = {E * 4, E, E, E * 2, E * 2, E * 4, E, E, E * 4, E * 2, E, E * 4, E * 4, E * 4,
+                                    cells * 2, 4, 8, 4, 4, 4, 1, 4, 8};
+    void* leaf[23];
+    for (int i = 0; i < 23; ++i) {
+        leaf[i] = results[i];
+        if (results[i] != operands[10 + i] && lanes > 0 &&
+            hipMemcpyAsync(results[i], operands[10 + i], (size_t)(leaf_bytes[i] * lanes), hipMemcpyDeviceToDevice, st) !=
+                hipSuccess)
+            return fail(NANORTS_INTERNAL, std::string(target) + ": copying an unaliased state leaf failed");
+    }
+    std::memset(s, 0, sizeof(*s));
+    s->birth = (int32_t*)leaf[0];
+    s->unit_type = (int8_t*)leaf[1];
+    s->owner = (int8_t*)leaf[2];
+    s->cell = (int16_t*)leaf[3];
+    s->hit_points = (int16_t*)leaf[4];
+    s->carried_resources = (int32_t*)leaf[5];
+    s->pending_kind = (int8_t*)leaf[6];
+    s->pending_direction = (int8_t*)leaf[7];
+    s->pending_none_duration = (int32_t*)leaf[8];
+    s->pending_target_cell = (int16_t*)leaf[9];
+    s->pending_produced_type = (int8_t*)leaf[10];
+    s->pending_issued_at = (int32_t*)leaf[11];
+    s->pending_completes_at = (int32_t*)leaf[12];
+    s->pending_order = (int32_t*)leaf[13];
+    s->entity_at = (int16_t*)leaf[14];
+    s->time = (int32_t*)leaf[15];
+    s->player_resources = (int32_t*)leaf[16];
+    s->next_birth = (int32_t*)leaf[17];
+    s->next_pending_order = (int32_t*)leaf[18];
+    s->alternating_conflict_count = (int32_t*)leaf[19];
+    s->game_over = (uint8_t*)leaf[20];
+    s->winner = (int32_t*)leaf[21];
+    s->spawn_overflow = (int32_t*)leaf[22];
+    c->kind = (const int32_t*)operands[1];
+    c->direction = (const int32_t*)operands[2];
+    c->none_duration = (const int32_t*)operands[3];
+    c->target_cell = (const int32_t*)operands[4];
+    c->produced_type = (const int32_t*)operands[5];
+    c->request_order = (const int32_t*)operands[6];
+    std::memset(r, 0, sizeof(*r));
+    r->admitted_harvest = (int32_t*)results[23];
+    r->admitted_return = (int32_t*)results[24];
+    r->admitted_produce = (int32_t*)results[25];
+    r->admitted_attack = (int32_t*)results[26];
+    // The per-slot event records (is_member pred[L][E], int32 [L][E][6],
+    // int16 [L][E][4], int8 [L][E][6]) are written as "no member": every
+    // record field then reads as its fill.
+    const int64_t record_bytes[4] = {E, E * 6 * 4, E * 4 * 2, E * 6};
+    for (int i = 0; i < 4; ++i) {
+        const int code = zero_bytes(st, results[27 + i], record_bytes[i] * lanes);
+        if (code != NANORTS_OK) return code;
+    }
+    return NANORTS_OK;
+}
+
+// The bucket a step target's extents describe; the unit table columns stay
+// zero and come from the table / timings operands in the kernel.
+static nanorts_game step_bucket(int32_t height, int32_t width, int32_t neutral, int32_t capacity, int32_t types,
+                                int64_t strategy, const void* terrain) {
     nanorts_game game;
     std::memset(&game, 0, sizeof(game));
     game.height = height;
@@ -2257,74 +2585,96 @@ int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const*
     game.types = types;
     game.offsets = 1;  // a step decodes no legality rows: one target offset is a valid window
     game.strategy = (int32_t)strategy;
-    game.max_cycles = 0x7fffffff;  // truncation is not a result of this target
-    game.terrain = (const uint8_t*)operands[7];
+    game.max_cycles = 0x7fffffff;  // truncation is not a result of these targets
+    game.terrain = (const uint8_t*)terrain;
+    return game;
+}
+
+int nanorts_amd_step_ffi(void* stream, const void* const* operands, void* const* results, int64_t lanes,
+                         int64_t key_lanes, int64_t command_lanes, int32_t height, int32_t width, int32_t neutral,
+                         int32_t capacity, int32_t types, int64_t strategy) {
+    if (!operands || !results) return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: operands or results is NULL");
+    if (strategy < NANORTS_CANCEL_BOTH || strategy > NANORTS_CANCEL_ALTERNATING)
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: strategy must be 0, 1 or 2");
+    if (lanes < 0 || (lanes > 0 && (key_lanes != 1 && key_lanes != lanes)))
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the key operand holds 1 or `lanes` rows");
+    if (lanes > 0 && command_lanes != 1 && command_lanes != lanes)
+        return fail(NANORTS_INVALID_ARGUMENT, "nanorts_amd_step_ffi: the Commands operands hold 1 or `lanes` rows");
+    nanorts_game game = step_bucket(height, width, neutral, capacity, types, strategy, operands[7]);
     NR_SHAPE(&game)
     sh.g.ref_table = (const int32_t*)operands[8];
     sh.g.ref_timings = (const int32_t*)operands[9];
     const hipStream_t st = (hipStream_t)stream;
-    const int64_t E = game.entities, cells = game.cells;
-    // Bytes per lane of the 23 state leaves in the reference's order.
-    const int64_t leaf_bytes[23] = {E * 4, E, E, E * 2, E * 2, E * 4, E, E, E * 4, E * 2, E, E * 4, E * 4, E * 4,
-                                    cells * 2, 4, 8, 4, 4, 4, 1, 4, 8};
-    // Results alias operands 10.. in place; where they do not, the state is
-    // copied into the result buffers first and stepped there.
-    void* leaf[23];
-    for (int i = 0; i < 23; ++i) {
-        leaf[i] = results[i];
-        if (results[i] != operands[10 + i] && lanes > 0 &&
-            hipMemcpyAsync(results[i], operands[10 + i], (size_t)(leaf_bytes[i] * lanes), hipMemcpyDeviceToDevice, st) !=
-                hipSuccess)
-            return fail(NANORTS_INTERNAL, "nanorts_amd_step_ffi: copying an unaliased state leaf failed");
-    }
     nanorts_state s;
-    std::memset(&s, 0, sizeof(s));
-    s.birth = (int32_t*)leaf[0];
-    s.unit_type = (int8_t*)leaf[1];
-    s.owner = (int8_t*)leaf[2];
-    s.cell = (int16_t*)leaf[3];
-    s.hit_points = (int16_t*)leaf[4];
-    s.carried_resources = (int32_t*)leaf[5];
-    s.pending_kind = (int8_t*)leaf[6];
-    s.pending_direction = (int8_t*)leaf[7];
-    s.pending_none_duration = (int32_t*)leaf[8];
-    s.pending_target_cell = (int16_t*)leaf[9];
-    s.pending_produced_type = (int8_t*)leaf[10];
-    s.pending_issued_at = (int32_t*)leaf[11];
-    s.pending_completes_at = (int32_t*)leaf[12];
-    s.pending_order = (int32_t*)leaf[13];
-    s.entity_at = (int16_t*)leaf[14];
-    s.time = (int32_t*)leaf[15];
-    s.player_resources = (int32_t*)leaf[16];
-    s.next_birth = (int32_t*)leaf[17];
-    s.next_pending_order = (int32_t*)leaf[18];
-    s.alternating_conflict_count = (int32_t*)leaf[19];
-    s.game_over = (uint8_t*)leaf[20];
-    s.winner = (int32_t*)leaf[21];
-    s.spawn_overflow = (int32_t*)leaf[22];
     nanorts_commands c;
-    c.kind = (const int32_t*)operands[1];
-    c.direction = (const int32_t*)operands[2];
-    c.none_duration = (const int32_t*)operands[3];
-    c.target_cell = (const int32_t*)operands[4];
-    c.produced_type = (const int32_t*)operands[5];
-    c.request_order = (const int32_t*)operands[6];
     nanorts_step_results r;
-    std::memset(&r, 0, sizeof(r));
-    r.admitted_harvest = (int32_t*)results[23];
-    r.admitted_return = (int32_t*)results[24];
-    r.admitted_produce = (int32_t*)results[25];
-    r.admitted_attack = (int32_t*)results[26];
-    // The per-slot event records (is_member pred[L][E], int32 [L][E][6],
-    // int16 [L][E][4], int8 [L][E][6]) are written as "no member": nothing
-    // in the reference reads them, and every record field then reads as its
-    // fill.
-    const int64_t record_bytes[4] = {E, E * 6 * 4, E * 4 * 2, E * 6};
-    for (int i = 0; i < 4; ++i) {
-        const int code = zero_bytes(st, results[27 + i], record_bytes[i] * lanes);
-        if (code != NANORTS_OK) return code;
-    }
+    const int code = step_operands(st, "nanorts_amd_step_ffi", operands, results, lanes, game.entities, game.cells, &s,
+                                   &c, &r);
+    if (code != NANORTS_OK) return code;
     return launch(k_step, sh, lanes, st, s, (const uint32_t*)operands[0], key_lanes, c, command_lanes, r);
+}
+
+int nanorts_amd_step_groups_ffi(void* stream, int32_t groups, const void* const* operands, void* const* results,
+                                const int64_t* lanes, const int64_t* key_lanes, const int64_t* command_lanes,
+                                int32_t height, int32_t width, int32_t neutral, int32_t capacity, int32_t types,
+                                int64_t strategy) {
+    const char* target = "nanorts_amd_step_groups_ffi";
+    if (groups < 1 || groups > 16) return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": groups must be in [1, 16]");
+    if (!operands || !results || !lanes || !key_lanes || !command_lanes)
+        return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": NULL argument");
+    if (strategy < NANORTS_CANCEL_BOTH || strategy > NANORTS_CANCEL_ALTERNATING)
+        return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": strategy must be 0, 1 or 2");
+    for (int32_t k = 0; k < groups; ++k) {
+        if (lanes[k] < 0) return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": lanes must be >= 0");
+        if (lanes[k] > 0 && ((key_lanes[k] != 1 && key_lanes[k] != lanes[k]) ||
+                             (command_lanes[k] != 1 && command_lanes[k] != lanes[k])))
+            return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": group " + std::to_string(k) +
+                                                      "'s key and Commands operands hold 1 or `lanes` rows");
+        if (!operands[33 * k + 7])
+            return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": group " + std::to_string(k) + "'s terrain is NULL");
+    }
+    // one LDS shape for every group: the bucket is shared, the terrain and
+    // tables are each group's own
+    nanorts_game game = step_bucket(height, width, neutral, capacity, types, strategy, operands[7]);
+    NR_SHAPE(&game)
+    const hipStream_t st = (hipStream_t)stream;
+    for (int32_t c0 = 0; c0 < groups; c0 += kGroupsPerLaunch) {
+        GroupsArgs args;
+        std::memset(&args, 0, sizeof(args));
+        args.g = sh.g;
+        int64_t blocks = 0;
+        for (int32_t k = c0; k < groups && k < c0 + kGroupsPerLaunch; ++k) {
+            const void* const* ops = operands + 33 * k;
+            void* const* rets = results + 31 * k;
+            nanorts_state s;
+            nanorts_commands c;
+            nanorts_step_results r;
+            const int code = step_operands(st, target, ops, rets, lanes[k], game.entities, game.cells, &s, &c, &r);
+            if (code != NANORTS_OK) return code;
+            if (lanes[k] == 0) continue;
+            GroupSlot& slot = args.slot[args.count++];
+            slot.s = s;
+            slot.c = c;
+            slot.r = r;
+            slot.key = (const uint32_t*)ops[0];
+            slot.key_lanes = key_lanes[k];
+            slot.cmd_lanes = command_lanes[k];
+            slot.lanes = lanes[k];
+            slot.terrain = (const uint8_t*)ops[7];
+            slot.table = (const int32_t*)ops[8];
+            slot.timings = (const int32_t*)ops[9];
+            slot.max_cycles = 0x7fffffff;
+            slot.first_block = (uint32_t)blocks;
+            blocks += (lanes[k] + sh.wpb - 1) / sh.wpb;
+            if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, std::string(target) + ": too many lanes for one launch");
+        }
+        if (blocks == 0) continue;
+        hipLaunchKernelGGL(k_step_groups, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds, st,
+                           args);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    }
+    return NANORTS_OK;
 }
 
 int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* const* games, const nanorts_state* states,
@@ -2366,6 +2716,7 @@ int nanorts_amd_step_groups(void* stream, int32_t groups, const nanorts_game* co
             s.r = results[i];
             s.key = keys[i];
             s.key_lanes = key_lanes[i];
+            s.cmd_lanes = lanes[i];
             s.lanes = lanes[i];
             s.terrain = games[i]->terrain;
             s.max_cycles = games[i]->max_cycles;
@@ -2651,6 +3002,190 @@ int nanorts_amd_abstraction_act(void* stream, const nanorts_game* game, nanorts_
     return launch(k_abstraction_act, sh, lanes, (hipStream_t)stream, state, a, player, player_lanes, commands);
 }
 
+int nanorts_amd_abstraction_act_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes,
+                                    void* const* results, int64_t lanes, int32_t height, int32_t width,
+                                    int32_t entities, int32_t capacity, int32_t types, int64_t strategy,
+                                    int64_t trained) {
+    const std::string target = "nanorts_amd_abstraction_act_ffi";
+    if (!operands || !operand_lanes || !results) return fail(NANORTS_INVALID_ARGUMENT, target + ": NULL argument");
+    for (int i = 0; i < 24; ++i)
+        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, target + ": operand " + std::to_string(i) + " is NULL");
+    for (int i = 0; i < 12; ++i)
+        if (!results[i]) return fail(NANORTS_INVALID_ARGUMENT, target + ": result " + std::to_string(i) + " is NULL");
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, target + ": lanes is negative");
+    for (int i = 0; i < 13; ++i)
+        if (operand_lanes[i] != 1 && operand_lanes[i] != lanes)
+            return fail(NANORTS_INVALID_ARGUMENT, target + ": operand " + std::to_string(i) +
+                                                      " is not one row per lane or one shared row");
+    if (operand_lanes[10] != 1 || operand_lanes[11] != 1)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": the terrain and the unit table must be one shared row");
+    if (strategy == 2 || strategy == 3)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": the defense strategies (2, 3) are not built; "
+                                                       "0 (worker rush) and 1 (barracks rush) are");
+    if (strategy != NANORTS_WORKER_RUSH && strategy != NANORTS_BARRACKS_RUSH)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": strategy must be 0 (worker rush) or 1 (barracks rush)");
+    if (types <= 3 || (strategy == NANORTS_BARRACKS_RUSH && (trained < 0 || trained >= types)))
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": the table must hold the Worker type and the trained type");
+    if (entities - 2 * capacity < 0 || capacity <= 0)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": entities must hold both players' capacity");
+    const hipStream_t st = (hipStream_t)stream;
+    // the carry in place: an unaliased result is first filled from its operand
+    const int64_t C = capacity;
+    const int64_t carry_bytes[11] = {C * 4, C * 4, C * 4, C * 4, C * 4, C * 4, C * 4, C * 4, C * 4, C, 4};
+    for (int i = 0; i < 11; ++i)
+        if (results[i] != operands[13 + i] && lanes > 0 &&
+            hipMemcpyAsync(results[i], operands[13 + i], (size_t)(carry_bytes[i] * lanes), hipMemcpyDeviceToDevice, st) !=
+                hipSuccess)
+            return fail(NANORTS_INTERNAL, target + ": copying an unaliased carry leaf failed");
+    nanorts_game game;
+    std::memset(&game, 0, sizeof(game));
+    game.height = height;
+    game.width = width;
+    game.cells = height * width;
+    game.neutral = entities - 2 * capacity;
+    game.capacity = capacity;
+    game.entities = entities;
+    game.types = types;
+    game.offsets = 1;  // the act reads no legality rows
+    game.max_cycles = 0x7fffffff;
+    game.terrain = (const uint8_t*)operands[10];
+    Shape sh;
+    BotArgs a;
+    std::string why;
+    if (!shape_for_bots(&game, &sh, &a.y, &why)) return fail(NANORTS_INVALID_ARGUMENT, target + ": " + why);
+    for (int f = 0; f < 9; ++f) a.carry.row[f] = (int32_t*)results[f];
+    a.carry.trained = (uint8_t*)results[9];
+    a.carry.next_order = (int32_t*)results[10];
+    a.strategy = (int32_t)strategy;
+    a.trained = (int32_t)trained;
+    nanorts_state s;
+    std::memset(&s, 0, sizeof(s));
+    s.birth = (int32_t*)operands[0];
+    s.unit_type = (int8_t*)operands[1];
+    s.owner = (int8_t*)operands[2];
+    s.cell = (int16_t*)operands[3];
+    s.carried_resources = (int32_t*)operands[4];
+    s.pending_kind = (int8_t*)operands[5];
+    s.pending_direction = (int8_t*)operands[6];
+    s.pending_produced_type = (int8_t*)operands[7];
+    s.entity_at = (int16_t*)operands[8];
+    s.player_resources = (int32_t*)operands[9];
+    const uint32_t flags[10] = {LD_BIRTH, LD_UTYPE, LD_OWNER, LD_CELL, LD_CARRIED,
+                                LD_PKIND, LD_PDIR, LD_PPTYPE, LD_ENTITY, LD_SCALARS};
+    uint32_t shared = 0u;
+    for (int i = 0; i < 10; ++i)
+        if (operand_lanes[i] == 1) shared |= flags[i];
+    return launch(k_abstraction_act_operands, sh, lanes, st, s, (const int32_t*)operands[11], shared, a,
+                  (const int32_t*)operands[12], operand_lanes[12], (int32_t*)results[11]);
+}
+
+// Waves per workgroup and per-wave LDS bytes of the A* kernels on a W x H
+// board (at most 8192 cells).
+static bool astar_shape(const std::string& target, int32_t width, int32_t height, int64_t lanes, AstarArgs* a) {
+    if (width <= 0 || height <= 0 || (int64_t)width * height > 8192)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": the board must hold 1 to 8192 cells"), false;
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, target + ": lanes is negative"), false;
+    const int32_t cells = width * height;
+    a->W = width;
+    a->H = height;
+    a->lanes = lanes;
+    a->region = ((cells + 15) & ~15) + 2 * 2 * ((cells + 7) & ~7) + ((cells + 15) & ~15);
+    a->waves = 4;
+    while (a->waves > 1 && a->waves * a->region > 65536) --a->waves;
+    return true;
+}
+
+static int launch_astar(void (*kernel)(AstarArgs), const AstarArgs& a, hipStream_t stream) {
+    if (a.lanes == 0) return NANORTS_OK;
+    const int64_t blocks = (a.lanes + a.waves - 1) / a.waves;
+    if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3((unsigned)(kWave * a.waves)), (size_t)(a.waves * a.region),
+                       stream, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return NANORTS_OK;
+}
+
+static int64_t row_stride(int64_t extent, int64_t lanes, int64_t row) { return extent == 1 && lanes != 1 ? 0 : row; }
+
+int nanorts_amd_astar_search_ffi(void* stream, const uint8_t* free, int64_t free_lanes, const int32_t* start,
+                                 int64_t start_lanes, const int32_t* target, int64_t target_lanes, const int32_t* range,
+                                 int64_t range_lanes, int32_t width, int32_t height, int32_t* out, int64_t lanes) {
+    const std::string name = "nanorts_amd_astar_search_ffi";
+    AstarArgs a;
+    std::memset(&a, 0, sizeof(a));
+    if (!astar_shape(name, width, height, lanes, &a)) return NANORTS_INVALID_ARGUMENT;
+    if (!free || !start || !target || !range || !out) return fail(NANORTS_INVALID_ARGUMENT, name + ": NULL argument");
+    const int64_t extents[4] = {free_lanes, start_lanes, target_lanes, range_lanes};
+    for (int i = 0; i < 4; ++i)
+        if (extents[i] != 1 && extents[i] != lanes)
+            return fail(NANORTS_INVALID_ARGUMENT, name + ": operand " + std::to_string(i) +
+                                                      " is not one row per lane or one shared row");
+    a.free = free;
+    a.start = start;
+    a.target = target;
+    a.range = range;
+    a.free_stride = row_stride(free_lanes, lanes, (int64_t)width * height);
+    a.start_stride = row_stride(start_lanes, lanes, 1);
+    a.target_stride = row_stride(target_lanes, lanes, 1);
+    a.range_stride = row_stride(range_lanes, lanes, 1);
+    a.out = out;
+    return launch_astar(k_astar_search, a, (hipStream_t)stream);
+}
+
+int nanorts_amd_astar_chain_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes, int32_t* out,
+                                int64_t lanes, int32_t width, int32_t height, int64_t capacity, int64_t columns,
+                                int64_t draw_count, int32_t drawing, const int64_t* fallback, const int64_t* blocked) {
+    const std::string name = "nanorts_amd_astar_chain_ffi";
+    AstarArgs a;
+    std::memset(&a, 0, sizeof(a));
+    if (!astar_shape(name, width, height, lanes, &a)) return NANORTS_INVALID_ARGUMENT;
+    if (!operands || !operand_lanes || !out || !fallback || !blocked)
+        return fail(NANORTS_INVALID_ARGUMENT, name + ": NULL argument");
+    for (int i = 0; i < 9; ++i) {
+        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, name + ": operand " + std::to_string(i) + " is NULL");
+        if (operand_lanes[i] != 1 && operand_lanes[i] != lanes)
+            return fail(NANORTS_INVALID_ARGUMENT, name + ": operand " + std::to_string(i) +
+                                                      " is not one row per lane or one shared row");
+    }
+    if (capacity < 0 || capacity > (1 << 20) || columns < 5 || draw_count < 0 || (drawing && draw_count == 0))
+        return fail(NANORTS_INVALID_ARGUMENT, name + ": each row holds the five search columns, and a drawing pass "
+                                                     "has draws");
+    for (int k = 0; k < 3; ++k)
+        if (fallback[k] < 5 || fallback[k] >= columns || blocked[k] < 5 || blocked[k] >= columns)
+            return fail(NANORTS_INVALID_ARGUMENT, name + ": the desires' kind, claim and cost columns lie past the "
+                                                         "search columns, within the row");
+    const int64_t cells = (int64_t)width * height;
+    a.free = (const uint8_t*)operands[0];
+    a.claimed = (const uint8_t*)operands[1];
+    a.rows = (const int32_t*)operands[2];
+    a.queue = (const int32_t*)operands[3];
+    a.count = (const int32_t*)operands[4];
+    a.moves = (const uint8_t*)operands[5];
+    a.reserved = (const int32_t*)operands[6];
+    a.balance = (const int32_t*)operands[7];
+    a.draws = (const int32_t*)operands[8];
+    a.free_stride = row_stride(operand_lanes[0], lanes, cells);
+    a.claimed_stride = row_stride(operand_lanes[1], lanes, cells);
+    a.rows_stride = row_stride(operand_lanes[2], lanes, capacity * columns);
+    a.queue_stride = row_stride(operand_lanes[3], lanes, capacity);
+    a.count_stride = row_stride(operand_lanes[4], lanes, 1);
+    a.moves_stride = row_stride(operand_lanes[5], lanes, 1);
+    a.reserved_stride = row_stride(operand_lanes[6], lanes, 1);
+    a.balance_stride = row_stride(operand_lanes[7], lanes, 1);
+    a.draws_stride = row_stride(operand_lanes[8], lanes, draw_count);
+    a.capacity = capacity;
+    a.columns = columns;
+    a.draw_count = draw_count;
+    a.drawing = drawing ? 1 : 0;
+    for (int k = 0; k < 3; ++k) {
+        a.fallback[k] = (int32_t)fallback[k];
+        a.blocked[k] = (int32_t)blocked[k];
+    }
+    a.out = out;
+    return launch_astar(k_astar_chain, a, (hipStream_t)stream);
+}
+
 static int seat_step(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
                      int32_t trained_type, int32_t learner, int32_t* seats, int32_t draw,
                      nanorts_abstract_actions carry, const int32_t* actions, int32_t partial,
@@ -2803,6 +3338,77 @@ int nanorts_amd_gridnet_decode(void* stream, const nanorts_game* game, nanorts_s
     std::string why;
     if (!shape_for_gridnet(game, &sh, &gy, &why)) return fail(NANORTS_INVALID_ARGUMENT, why);
     return launch(k_gridnet_decode, sh, lanes, (hipStream_t)stream, state, gy, actions, commands);
+}
+
+int nanorts_amd_gridnet_decode_ffi(void* stream, const void* const* operands, const int64_t* operand_lanes,
+                                   void* const* results, int64_t lanes, int32_t height, int32_t width, int32_t neutral,
+                                   int32_t capacity, int32_t types, int32_t costs, int32_t side) {
+    const std::string target = "nanorts_amd_gridnet_decode_ffi";
+    if (!operands || !operand_lanes || !results) return fail(NANORTS_INVALID_ARGUMENT, target + ": NULL argument");
+    for (int i = 0; i < 11; ++i)
+        if (!operands[i]) return fail(NANORTS_INVALID_ARGUMENT, target + ": operand " + std::to_string(i) + " is NULL");
+    for (int i = 0; i < 6; ++i)
+        if (!results[i]) return fail(NANORTS_INVALID_ARGUMENT, target + ": result " + std::to_string(i) + " is NULL");
+    if (lanes < 0) return fail(NANORTS_INVALID_ARGUMENT, target + ": lanes is negative");
+    for (int i = 0; i < 11; ++i)
+        if (operand_lanes[i] != 1 && operand_lanes[i] != lanes)
+            return fail(NANORTS_INVALID_ARGUMENT, target + ": operand " + std::to_string(i) +
+                                                      " is not one row per lane or one shared row");
+    if (operand_lanes[10] != 1) return fail(NANORTS_INVALID_ARGUMENT, target + ": unit_cost must be one shared row");
+    if (costs != types)
+        return fail(NANORTS_INVALID_ARGUMENT, target + ": unit_cost must hold one cost per unit type (costs = types)");
+    if (side <= 0 || side % 2 == 0) return fail(NANORTS_INVALID_ARGUMENT, target + ": side must be odd and positive");
+    nanorts_game game;
+    std::memset(&game, 0, sizeof(game));
+    game.height = height;
+    game.width = width;
+    game.cells = height * width;
+    game.neutral = neutral;
+    game.capacity = capacity;
+    game.entities = neutral + 2 * capacity;
+    game.types = types;
+    game.offsets = side * side;
+    game.max_cycles = 0x7fffffff;
+    // the decode reads no terrain (no operand carries it): the shape is
+    // checked with a stand-in pointer, and the kernel's header stages an
+    // open board for a NULL terrain
+    game.terrain = (const uint8_t*)operands[1];
+    Shape sh;
+    GridLayout gy;
+    std::string why;
+    if (!shape_for_gridnet(&game, &sh, &gy, &why)) return fail(NANORTS_INVALID_ARGUMENT, target + ": " + why);
+    sh.g.terrain = nullptr;
+    const int64_t C = capacity, cells = game.cells;
+    GridOperands o;
+    o.actions = (const int32_t*)operands[0];
+    o.move = (const uint8_t*)operands[7];
+    o.pdir = (const uint8_t*)operands[8];
+    o.ptype = (const uint8_t*)operands[9];
+    o.actions_stride = operand_lanes[0] == 1 ? 0 : 2 * cells * 7;
+    o.move_stride = operand_lanes[7] == 1 ? 0 : C * 4;
+    o.pdir_stride = operand_lanes[8] == 1 ? 0 : C * 4;
+    o.ptype_stride = operand_lanes[9] == 1 ? 0 : C * types;
+    nanorts_state s;
+    std::memset(&s, 0, sizeof(s));
+    s.birth = (int32_t*)operands[1];
+    s.pending_kind = (int8_t*)operands[2];
+    s.cell = (int16_t*)operands[3];
+    s.pending_direction = (int8_t*)operands[4];
+    s.pending_produced_type = (int8_t*)operands[5];
+    s.player_resources = (int32_t*)operands[6];
+    const uint32_t flags[6] = {LD_BIRTH, LD_PKIND, LD_CELL, LD_PDIR, LD_PPTYPE, LD_SCALARS};
+    uint32_t shared = 0u;
+    for (int i = 0; i < 6; ++i)
+        if (operand_lanes[1 + i] == 1) shared |= flags[i];
+    nanorts_command_buffers out;
+    out.kind = (int32_t*)results[0];
+    out.direction = (int32_t*)results[1];
+    out.none_duration = (int32_t*)results[2];
+    out.target_cell = (int32_t*)results[3];
+    out.produced_type = (int32_t*)results[4];
+    out.request_order = (int32_t*)results[5];
+    return launch(k_gridnet_decode_operands, sh, lanes, (hipStream_t)stream, s, (const int32_t*)operands[10], shared,
+                  gy, o, out);
 }
 
 int nanorts_amd_gridnet_observe(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,

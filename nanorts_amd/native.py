@@ -98,7 +98,8 @@ EXPORTS = (
     "nanorts_amd_rollout", "nanorts_amd_abstraction_act", "nanorts_amd_seat_step", "nanorts_amd_seat_rollout",
     "nanorts_amd_seat_step_lanes", "nanorts_amd_seat_rollout_lanes", "nanorts_amd_episode_seats",
     "nanorts_amd_gridnet_decode", "nanorts_amd_gridnet_observe", "nanorts_amd_gridnet_step", "nanorts_amd_gridnet_step_against",
-    "nanorts_amd_gridnet_sample_actions",
+    "nanorts_amd_gridnet_sample_actions", "nanorts_amd_step_groups_ffi", "nanorts_amd_abstraction_act_ffi",
+    "nanorts_amd_astar_search_ffi", "nanorts_amd_astar_chain_ffi", "nanorts_amd_gridnet_decode_ffi",
 )
 
 _I64 = ctypes.c_int64
@@ -148,6 +149,16 @@ _SIGNATURES = {
     "nanorts_amd_gridnet_step": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, GridNetResults]),
     "nanorts_amd_gridnet_step_against": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, GridNetResults]),
     "nanorts_amd_gridnet_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
+    "nanorts_amd_step_groups_ffi": (ctypes.c_int, [_VP, _I32, _VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32,
+                                                   _I64]),
+    "nanorts_amd_abstraction_act_ffi": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I32, _I32, _I32, _I32, _I32, _I64,
+                                                       _I64]),
+    "nanorts_amd_astar_search_ffi": (ctypes.c_int, [_VP, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _I32, _I32, _VP,
+                                                    _I64]),
+    "nanorts_amd_astar_chain_ffi": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I32, _I32, _I64, _I64, _I64, _I32, _VP,
+                                                   _VP]),
+    "nanorts_amd_gridnet_decode_ffi": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
+                                                      _I32]),
 }
 
 _LIBRARY: ctypes.CDLL | None = None

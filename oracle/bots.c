@@ -774,6 +774,115 @@ int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start,
     return step;
 }
 
+/* The FFI target nanorts_astar_chain for one lane (N/bots/cuda/abstraction.cu:
+ * 98-215, fed by _chain, N/bots/abstraction.py:1001-1033): the rows of the
+ * queue's first `count` entries (clamped to [0, capacity]), in order, each
+ * searched from its start (column 0) toward its goal (1) within its radius
+ * (2) over the cells still open.  A unit that steps and may move desires the
+ * step's cell at cost 0 (selector 2); one that steps but may not takes its
+ * blocked desire (selector 1); one that cannot takes its fallback (0).  In a
+ * drawing pass a row with draws (3) that did not move takes the direction
+ * the next draw names among its options (4) instead (selector 2).  A desire
+ * of kind != -1 is kept when its claim is not taken and its cost fits the
+ * balance beside the reserve and the costs already kept (uint32 sums); a
+ * claim on the board stops being open, and is taken when kept.  out
+ * [capacity + 1][4]: per slot rank among the kept (or -1), selector,
+ * direction (or -1), drew; then kept count, draws used, 0, 0. */
+static int32_t chain_neighbour(int32_t cell, int32_t direction, int32_t W) {
+    const int32_t offset = direction == 0 ? -W : (direction == 1 ? 1 : (direction == 2 ? W : -1));
+    return (int32_t)((uint32_t)cell + (uint32_t)offset);
+}
+
+void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const int32_t* rows, const int32_t* queue,
+                     int32_t count, int32_t moves_allowed, int32_t reserved, int32_t balance, const int32_t* draws,
+                     int64_t draw_count, int32_t drawing, int32_t W, int32_t H, int64_t capacity, int64_t columns,
+                     const int64_t fallback[3], const int64_t blocked[3], int32_t* out) {
+    enum { OPEN = 1, TAKEN = 2 };
+    const int32_t cells = W * H;
+    uint8_t* flags = (uint8_t*)malloc((size_t)cells);
+    uint8_t* open_cell = (uint8_t*)malloc((size_t)cells);
+    bot_t b;
+    memset(&b, 0, sizeof(b));
+    b.top = (int16_t*)calloc((size_t)cells, 2);
+    b.below = (int16_t*)calloc((size_t)cells, 2);
+    b.parent = (int16_t*)calloc((size_t)cells, 2);
+    b.seen = (uint8_t*)calloc((size_t)cells, 1);
+    for (int32_t c = 0; c < cells; ++c) flags[c] = (uint8_t)((free_cells[c] ? OPEN : 0) | (claimed[c] ? TAKEN : 0));
+    for (int64_t i = 0; i < capacity; ++i) {
+        out[4 * i] = ABSENT;
+        out[4 * i + 1] = 0;
+        out[4 * i + 2] = ABSENT;
+        out[4 * i + 3] = 0;
+    }
+    const int64_t searched = count < 0 ? 0 : (count > capacity ? capacity : (int64_t)count);
+    uint32_t kept_cost = 0;
+    int32_t kept_count = 0, calls = 0;
+    for (int64_t r = 0; r < searched; ++r) {
+        const int32_t slot = queue[r];
+        if (slot < 0 || slot >= capacity) continue;
+        const int32_t* entry = rows + (int64_t)slot * columns;
+        for (int32_t c = 0; c < cells; ++c) open_cell[c] = (flags[c] & OPEN) != 0;
+        int32_t path[4];
+        astar(&b, open_cell, W, H, entry[0], entry[1], entry[2], path);
+        const int stepped = path[1] != ABSENT;
+        int32_t selector = 0, direction = ABSENT;
+        int eligible = entry[fallback[0]] != ABSENT;
+        int32_t claim = entry[fallback[1]], cost = entry[fallback[2]];
+        if (stepped && moves_allowed) {
+            selector = 2;
+            direction = path[1];
+            eligible = 1;
+            claim = chain_neighbour(entry[0], direction, W);
+            cost = 0;
+        } else if (stepped) {
+            selector = 1;
+            eligible = entry[blocked[0]] != ABSENT;
+            claim = entry[blocked[1]];
+            cost = entry[blocked[2]];
+        }
+        const int drew = drawing && entry[3] != 0 && !(stepped && moves_allowed);
+        if (drew) {
+            const int64_t at = calls < draw_count ? calls : draw_count - 1;
+            direction = ABSENT;
+            for (int32_t turn = 0; turn < 4; ++turn) {
+                const int32_t d = (int32_t)(((uint32_t)draws[at] + (uint32_t)turn) & 3u);
+                if ((entry[4] >> d) & 1) {
+                    direction = d;
+                    break;
+                }
+            }
+            selector = 2;
+            eligible = 1;
+            claim = direction == ABSENT ? ABSENT : chain_neighbour(entry[0], direction, W);
+            cost = 0;
+            ++calls;
+        }
+        const int on_board = claim >= 0 && claim < cells;
+        const int conflicting = on_board && (flags[claim] & TAKEN) != 0;
+        const int over = cost > 0 && (int32_t)(uint32_t)((uint32_t)reserved + kept_cost + (uint32_t)cost) > balance;
+        const int kept = eligible && !conflicting && !over;
+        if (on_board) flags[claim] = (uint8_t)((flags[claim] & ~OPEN) | (kept ? TAKEN : 0));
+        out[4 * slot] = kept ? kept_count : ABSENT;
+        out[4 * slot + 1] = selector;
+        out[4 * slot + 2] = direction;
+        out[4 * slot + 3] = drew;
+        if (kept) {
+            kept_cost += (uint32_t)cost;
+            ++kept_count;
+        }
+    }
+    out[4 * capacity] = kept_count;
+    out[4 * capacity + 1] = calls;
+    out[4 * capacity + 2] = 0;
+    out[4 * capacity + 3] = 0;
+    free(flags);
+    free(open_cell);
+    free(b.top);
+    free(b.below);
+    free(b.parent);
+    free(b.seen);
+}
+
 /* step_seat (N/bots/seat.py:84-149) with the learner at a static seat: the
  * bot's commands from the current state, the learner's actions decoded
  * (N/adapters/jaxmarl/env.py:78-96, every agent reading the same rows), the

@@ -198,6 +198,13 @@ void nro_empty_actions(const nro_game* g, nro_abstract* carry, int64_t L);
  * direction or -1; out = {found, step, distance, pops}. */
 int32_t nro_astar(const uint8_t* open_cell, int32_t W, int32_t H, int32_t start, int32_t target,
                   int32_t range, int32_t out[4]);
+/* The walk of the FFI target nanorts_astar_chain for one lane: free and
+ * claimed bool[H*W], rows [capacity][columns], queue [capacity]; out
+ * [capacity + 1][4] (see bots.c). */
+void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const int32_t* rows, const int32_t* queue,
+                     int32_t count, int32_t moves_allowed, int32_t reserved, int32_t balance, const int32_t* draws,
+                     int64_t draw_count, int32_t drawing, int32_t W, int32_t H, int64_t capacity, int64_t columns,
+                     const int64_t fallback[3], const int64_t blocked[3], int32_t* out);
 /* seat.step_seat: actions [L][C][7] are the learner's rows; the learner is
  * seats[l] when `seats` is set, else `fixed`; the bot plays 1 - learner.
  * With `draw`, a lane whose game ended takes nro_episode_seat of its next

@@ -53,6 +53,29 @@ def astar(open_cells: np.ndarray, start: int, target: int, range_: int) -> tuple
     return int(out[0]), int(out[1]), int(out[2]), int(out[3])
 
 
+def astar_chain(free_cells: np.ndarray, claimed: np.ndarray, rows: np.ndarray, queue: np.ndarray, count: int,
+                moves_allowed: bool, reserved: int, balance: int, draws: np.ndarray, drawing: bool,
+                fallback: tuple[int, int, int], blocked: tuple[int, int, int]) -> np.ndarray:
+    """The FFI target nanorts_astar_chain for one lane over bool[H, W] free and
+    claimed cells: decisions int32[capacity + 1, 4]."""
+    lib = _load()
+    H, W = free_cells.shape
+    capacity, columns = rows.shape
+    free_u8 = np.ascontiguousarray(free_cells.reshape(-1).astype(np.uint8))
+    claimed_u8 = np.ascontiguousarray(claimed.reshape(-1).astype(np.uint8))
+    rows = np.ascontiguousarray(rows, np.int32)
+    queue = np.ascontiguousarray(queue, np.int32)
+    draws = np.ascontiguousarray(np.asarray(draws, np.int32).reshape(-1))
+    out = np.zeros((capacity + 1, 4), np.int32)
+    f3 = (ctypes.c_int64 * 3)(*fallback)
+    b3 = (ctypes.c_int64 * 3)(*blocked)
+    lib.nro_astar_chain(_ptr(free_u8), _ptr(claimed_u8), _ptr(rows), _ptr(queue), ctypes.c_int32(count),
+                        ctypes.c_int32(int(bool(moves_allowed))), ctypes.c_int32(reserved), ctypes.c_int32(balance),
+                        _ptr(draws), ctypes.c_int64(draws.size), ctypes.c_int32(int(bool(drawing))), ctypes.c_int32(W),
+                        ctypes.c_int32(H), ctypes.c_int64(capacity), ctypes.c_int64(columns), f3, b3, _ptr(out))
+    return out
+
+
 _I32x8 = ctypes.c_int32 * MAX_TYPES
 
 

@@ -291,3 +291,97 @@ def test_seat_rollout_keeps_invariants_against_random_play(strategy):
         assert (carry["order"][l][live] >= 0).all()
         assert sorted(carry["order"][l][live].tolist()) == list(range(int(live.sum())))
         assert carry["next_order"][l] == int(live.sum())
+
+
+# ---------------------------------------------------------------------------
+# The walk of the FFI target nanorts_astar_chain (N/bots/cuda/abstraction.cu:
+# 98-215), restated by the oracle: hand-traced on small open boards.
+# Row columns: start, goal, radius, draws, options, then the fallback's kind,
+# claim, cost (5-7) and the blocked desire's (8-10).
+# ---------------------------------------------------------------------------
+FALLBACK, BLOCKED = (5, 6, 7), (8, 9, 10)
+
+
+def _chain_row(start, goal, radius=0, draws=0, options=0, fallback=(-1, -1, 0), blocked=(-1, -1, 0)):
+    return [start, goal, radius, draws, options, *fallback, *blocked]
+
+
+def _chain(rows, queue=None, count=None, moves=True, reserved=0, balance=10, draws=(0,), drawing=False,
+           free=None, claimed=None, W=4, H=4):
+    from oracle.oracle import astar_chain
+
+    rows = np.asarray(rows, np.int32)
+    queue = np.arange(len(rows), dtype=np.int32) if queue is None else np.asarray(queue, np.int32)
+    free = np.ones((H, W), bool) if free is None else free
+    claimed = np.zeros((H, W), bool) if claimed is None else claimed
+    return astar_chain(free, claimed, rows, queue, len(rows) if count is None else count, moves, reserved, balance,
+                       np.asarray(draws, np.int32), drawing, FALLBACK, BLOCKED)
+
+
+def test_chain_moves_and_claims_in_queue_order():
+    """4x4 open board.  Row 0 walks from cell 5 toward 7: first step RIGHT
+    into 6, kept at rank 0; its claim closes 6 to later searches.  Row 1
+    walks from 10 toward 2: with 6 closed every neighbour lies farther from
+    the goal, and the last one inserted, LEFT (9), is popped first: kept at
+    rank 1.  Row 2 stands at its goal (no step) and takes its fallback, a
+    claim on 6 at cost 0: taken, not kept.  Totals: 2 kept, no draws."""
+    out = _chain([_chain_row(5, 7), _chain_row(10, 2), _chain_row(13, 13, fallback=(0, 6, 0))])
+    assert out[:3].tolist() == [[0, 2, 1, 0], [1, 2, 3, 0], [-1, 0, -1, 0]]
+    assert out[3].tolist() == [2, 0, 0, 0]
+
+
+def test_chain_blocked_when_moves_are_not_allowed():
+    """moves_allowed false: a row that can step takes its blocked desire
+    (selector 1, no direction), one that cannot its fallback; a desire of
+    kind -1 is never kept."""
+    out = _chain([_chain_row(5, 7, blocked=(4, 9, 0)), _chain_row(6, 6, fallback=(-1, 3, 0))], moves=False)
+    assert out[:2].tolist() == [[0, 1, -1, 0], [-1, 0, -1, 0]]
+    assert out[2].tolist() == [1, 0, 0, 0]
+
+
+def test_chain_budget_counts_reserve_and_kept_costs():
+    """balance 5, reserve 1: a fallback of cost 3 is kept (1 + 3 <= 5), the
+    next of cost 2 is not (1 + 3 + 2 > 5), the third of cost 1 is (5 <= 5)."""
+    rows = [_chain_row(0, 0, fallback=(4, 4, 3)), _chain_row(1, 1, fallback=(4, 8, 2)),
+            _chain_row(2, 2, fallback=(4, 12, 1))]
+    out = _chain(rows, reserved=1, balance=5)
+    assert [r[0] for r in out[:3].tolist()] == [0, -1, 1]
+    assert out[3, 0] == 2
+
+
+def test_chain_queue_order_count_and_skipped_slots():
+    """The queue visits slot 2, then an out-of-range slot (skipped), then slot
+    0; count 3 leaves slot 1 unvisited (rank -1, selector 0, no direction).
+    Slot 2 goes first: from 10 toward 2, UP into 6.  Slot 0, from 5 toward
+    7, then goes round the closed 6: the LEFT branch is popped first but
+    only leads away, and the first path found starts DOWN (9): rank 1."""
+    rows = [_chain_row(5, 7), _chain_row(0, 3), _chain_row(10, 2)]
+    out = _chain(rows, queue=[2, 7, 0], count=3)
+    assert out[:3].tolist() == [[1, 2, 2, 0], [-1, 0, -1, 0], [0, 2, 0, 0]]
+
+
+@pytest.mark.parametrize("closing_row", [False, True])
+def test_chain_taken_cells_refuse_and_closed_cells_divert(closing_row):
+    """Cell 6 is claimed (taken) but free (open to the search).  Alone, the
+    row from 5 toward 7 steps RIGHT into 6 and is refused (rank -1).  After a
+    row whose fallback claims 6 (refused too, but closing 6), the search goes
+    round below it: DOWN (9), kept."""
+    claimed = np.zeros((4, 4), bool)
+    claimed.reshape(-1)[6] = True
+    rows = ([_chain_row(0, 0, fallback=(4, 6, 0))] if closing_row else []) + [_chain_row(5, 7)]
+    out = _chain(rows, claimed=claimed)
+    if closing_row:
+        assert out[:2].tolist() == [[-1, 0, -1, 0], [0, 2, 2, 0]]
+    else:
+        assert out[:1].tolist() == [[-1, 2, 1, 0]]
+
+
+def test_chain_drawing_pass_turns_to_an_allowed_direction():
+    """A drawing pass: a row with draws that cannot move (moves false) takes
+    the first direction from its draw, turning +1 mod 4, that its options
+    allow.  Draw 0 with options {LEFT, DOWN} (bits 3, 2) gives DOWN; the
+    second row's draw 3 with options {UP} gives UP; draws used 2."""
+    rows = [_chain_row(5, 7, draws=1, options=0b1100), _chain_row(10, 10, draws=1, options=0b0001)]
+    out = _chain(rows, moves=False, draws=[0, 3], drawing=True)
+    assert out[:2].tolist() == [[0, 2, 2, 1], [1, 2, 0, 1]]
+    assert out[2].tolist() == [2, 2, 0, 0]
