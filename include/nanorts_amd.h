@@ -225,8 +225,10 @@ int64_t nanorts_amd_shared_opt_in(const int32_t* devices, int64_t n);
 const char* nanorts_amd_self_check(const int32_t* devices, int64_t n);
 
 /* The self check without a device allocation, for callers that cannot
- * allocate (code under graph capture, serving loops).  No counterpart in the
- * reference.  Runs `waves` probe waves (1..1024; more is refused with a
+ * allocate (serving loops, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  It launches on the default stream and copies the probe
+ * words back synchronously: it synchronises the host, so it cannot run under
+ * graph capture.  Runs `waves` probe waves (1..1024; more is refused with a
  * message) on each listed device and returns "" when every wave passes;
  * probe_words (host int32[waves], or NULL) receives the last device's probe
  * words, 1 per passing wave.  The words live in a 4 KiB array of the

@@ -178,3 +178,24 @@ def test_unknown_names_are_refused():
         shipped_map("noSuchMap")
     with pytest.raises(ContentError):
         load_game(shipped_map("basesWorkers8x8"), conflict_strategy="NOT_A_STRATEGY")
+
+
+@pytest.mark.parametrize("w,h,capacity", [(200, 200, None), (130, 130, 16400)])
+def test_buckets_past_int16_indices_are_refused(tmp_path, w, h, capacity):
+    """The reference lays out int32 cell (or slot) indices once a bucket's
+    cell count (or entity capacity) passes 32767 (src/nanorts/model/leaf.py:
+    85-98); this build lays out int16 indices only and refuses such a bucket
+    when the game is built: a 200x200 board (40 000 cells), and a 130x130
+    board (16 900 cells) with a supplied per-player capacity of 16 400
+    (entity capacity past 32 767).  The int16 extremes themselves load."""
+    from nanorts_amd.model import ModelError
+
+    doc = _doc(w=w, h=h)
+    bucket = None
+    if capacity is not None:
+        derived = load_game(_write(tmp_path, doc)).bucket
+        bucket = dataclasses.replace(derived, per_player_capacity=capacity)
+    with pytest.raises(ModelError, match="int16"):
+        load_game(_write(tmp_path, doc), bucket=bucket)
+    # the largest board that keeps int16 cells: 181 x 181 = 32 761 cells
+    assert load_game(_write(tmp_path, _doc(w=181, h=181))).bucket.cell_count == 32761
