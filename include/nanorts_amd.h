@@ -105,8 +105,8 @@ typedef struct nanorts_commands {
     const int32_t* request_order;
 } nanorts_commands;
 
-/* core.step results besides the state (StepResult minus the per-slot event
- * records, which nothing in the reference consumes).  Any pointer may be NULL. */
+/* core.step results besides the state.  Any pointer may be NULL; the four
+ * record pointers are used only when all four are set. */
 typedef struct nanorts_step_results {
     uint8_t* terminated;        /* [L] bool */
     uint8_t* truncated;         /* [L] bool */
@@ -115,6 +115,19 @@ typedef struct nanorts_step_results {
     int32_t* admitted_return;   /* [L][2] */
     int32_t* admitted_produce;  /* [L][2][T] */
     int32_t* admitted_attack;   /* [L][2][3] by target owner + 1 */
+    /* The per-slot completion records the step target returns as results
+     * 27-30 and StepEvents decodes (src/nanorts/core/cycle.py:48-81,
+     * 254-300): is_member [L][E] bool; int32 [L][E][6] actor_birth,
+     * target_birth, amount, balance, spawn_birth, death_birth; int16
+     * [L][E][4] target_slot, spawn_slot, spawn_cell, death_slot; int8
+     * [L][E][6] flags (hit 1, death 2, harvest 4, depleted 8, return 16,
+     * spawn 32), actor_owner, actor_unit_type, produced_type, death_owner,
+     * death_unit_type.  A member's row holds its records (zero where none
+     * writes); every other row is zero. */
+    uint8_t* is_member;
+    int32_t* records_i32;
+    int16_t* records_i16;
+    int8_t* records_i8;
 } nanorts_step_results;
 
 /* env.step outputs through the JaxMARL surface.  Any pointer may be NULL. */
@@ -258,8 +271,8 @@ int nanorts_amd_step(void* stream, const nanorts_game* game, nanorts_state state
  *     23 admitted_harvest s32[L][2]; 24 admitted_return s32[L][2];
  *     25 admitted_produce s32[L][2][T]; 26 admitted_attack s32[L][2][3];
  *     27 is_member pred[L][E]; 28 int32 records s32[L][E][6]; 29 index
- *     records s16[L][E][4]; 30 int8 records s8[L][E][6].  The records are
- *     written as no member (all zero): nothing in the reference reads them.
+ *     records s16[L][E][4]; 30 int8 records s8[L][E][6] (the completion
+ *     records of nanorts_step_results).
  * Every size argument is an extent of those buffers, so a handler that sees
  * only the buffers and the `strategy` attribute can pass them: lanes = the
  * leading extent of result 0; key_lanes and command_lanes = the leading

@@ -21,8 +21,8 @@ from nanorts_amd.env import DeviceGame, EnvironmentState, PixelObservation, Stat
 from nanorts_amd.groups import step_groups, steps_together
 from nanorts_amd.model import ModelError
 
-__all__ = ["legal_commands", "pixels", "pixels_from_symbolic", "reset", "step", "step_groups", "steps_together",
-           "symbolic", "visibility"]
+__all__ = ["legal_commands", "pixels", "pixels_from_symbolic", "reset", "step", "step_events", "step_groups",
+           "steps_together", "symbolic", "visibility"]
 
 _DEVICE_GAMES: "weakref.WeakKeyDictionary[GameConfig, dict[str, DeviceGame]]" = weakref.WeakKeyDictionary()
 _COMMAND_FIELDS = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
@@ -64,13 +64,57 @@ def reset(key, game: GameConfig, num_envs: int, *, device: torch.device | str | 
     return device_game(game, device).batch(num_envs)
 
 
-def step(key, state: Any, commands: dict[str, torch.Tensor], game: GameConfig) -> dict[str, torch.Tensor]:
+def step(key, state: Any, commands: dict[str, torch.Tensor], game: GameConfig, *,
+         records: bool = False) -> dict[str, torch.Tensor]:
     """core.step (src/nanorts/core/__init__.py:46-60) in place: `key` is
     uint32 key data [L, 2] or [2] (or an int32 device tensor holding it),
     Commands int32[L, 2, C] per field.  Returns terminated, truncated, reward
-    and the admitted event counts."""
+    and the admitted event counts; with `records`, also the per-slot
+    completion records, which step_events decodes into StepEvents' fields."""
     core = _core(state)
-    return step_groups([(key, core, commands, device_game(game, _device_of(core)))])[0]
+    return step_groups([(key, core, commands, device_game(game, _device_of(core)))], records=records)[0]
+
+
+# The per-slot StepEvents fields (src/nanorts/model/step.py:39-112) and where
+# each comes from in the records (src/nanorts/core/cycle.py:48-81, 281-300):
+# (field, record flag, column group and index or None for `valid`, fill).
+_FLAG = {"hit": 1, "death": 2, "harvest": 4, "return": 16, "spawn": 32}
+_ACTOR = (("actor_birth", ("i32", 0)), ("actor_owner", ("i8", 1)), ("actor_unit_type", ("i8", 2)))
+_FACTS = {
+    "hit": (("target_slot", ("i16", 0), -1), ("target_birth", ("i32", 1), -1), ("damage", ("i32", 2), 0)),
+    "death": (("slot", ("i16", 3), -1), ("birth", ("i32", 5), -1), ("owner", ("i8", 4), -1),
+              ("unit_type", ("i8", 5), -1)),
+    "harvest": (("target_slot", ("i16", 0), -1), ("target_birth", ("i32", 1), -1), ("amount", ("i32", 2), 0)),
+    "return": (("target_slot", ("i16", 0), -1), ("target_birth", ("i32", 1), -1), ("amount", ("i32", 2), 0),
+               ("balance", ("i32", 3), -1)),
+    "spawn": (("produced_type", ("i8", 3), -1), ("slot", ("i16", 1), -1), ("birth", ("i32", 4), -1),
+              ("cell", ("i16", 2), -1), ("balance", ("i32", 3), -1)),
+}
+
+
+def step_events(out: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
+    """The per-slot StepEvents fields of a core.step(..., records=True)
+    result, decoded as the reference decodes its step target's records
+    (src/nanorts/core/cycle.py:281-311): a record is valid where the slot
+    took a turn and its flag is set; its fields read the record's columns
+    there and their fills elsewhere.  bool / int32 [L, E] each."""
+    if "is_member" not in out:
+        raise ModelError("step_events needs a core.step result taken with records=True")
+    cols = {"i32": out["records_i32"].to(torch.int32), "i16": out["records_i16"].to(torch.int32),
+            "i8": out["records_i8"].to(torch.int32)}
+    flags = cols["i8"][..., 0]
+    member = out["is_member"].to(torch.bool)
+    events: dict[str, torch.Tensor] = {}
+    for name, flag in _FLAG.items():
+        valid = member & ((flags & flag) != 0)
+        events[f"{name}_valid"] = valid
+        for fact, (group, k) in _ACTOR:
+            events[f"{name}_{fact}"] = torch.where(valid, cols[group][..., k], -1)
+        for fact, (group, k), fill in _FACTS[name]:
+            events[f"{name}_{fact}"] = torch.where(valid, cols[group][..., k], fill)
+        if name == "harvest":
+            events["harvest_depleted"] = valid & ((flags & 8) != 0)
+    return events
 
 
 def legal_commands(state: Any, game: GameConfig, *, stored: str = "rows") -> torch.Tensor:

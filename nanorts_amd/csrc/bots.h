@@ -842,7 +842,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
 }
 
 // _walked / _walk_step with _answer and _kept (N/bots/abstraction.py:718-797,
-// 904-952): returns kept_count.
+// 904-952): returns how many desires it keeps.
 NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int32_t queued,
                               int lane) {
     (void)h;
@@ -853,10 +853,10 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
     AS3 int16_t* below = bv<int16_t>(b, y.a_below);
     AS3 uint8_t* mark = bv<uint8_t>(b, y.a_mark);
     const int32_t own = b.player;
-    const bool moves_allowed = within_balance(e, b, 0) && within_balance(e, b, 1);
+    const bool may_move = within_balance(e, b, 0) && within_balance(e, b, 1);
     const int32_t reserved_own = own == 0 ? b.reserved0 : b.reserved1;
     const int32_t balance = uni(e.sc[S_RES0 + own]);
-    int32_t kept_cost = 0, kept_count = 0;
+    int32_t spent = 0, granted = 0;
     for (int32_t q = 0; q < queued; ++q) {
         const int32_t i = uni(bv<int16_t>(b, y.u_queue)[q]);
         const int32_t start = uni(e.cell[b.block + i]);
@@ -883,9 +883,9 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
         }
         int32_t sel, kind, claim, cost;
         if (step != kAbsent) {
-            sel = moves_allowed ? SEL_MOVED : SEL_NONE;
-            kind = moves_allowed ? kKindMove : kAbsent;
-            claim = moves_allowed ? step_cell(g, start, step) : kAbsent;
+            sel = may_move ? SEL_MOVED : SEL_NONE;
+            kind = may_move ? kKindMove : kAbsent;
+            claim = may_move ? step_cell(g, start, step) : kAbsent;
             cost = 0;
         } else {
             sel = SEL_FALLBACK;
@@ -895,8 +895,8 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
         }
         const bool has_cell = claim != kAbsent && claim >= 0 && claim < g.cells;
         const bool conflicting = has_cell && (bit_of(claimed, claim) || bit_of(kept_m, claim));
-        const bool overdrawn = cost > 0 && wadd(wadd(reserved_own, kept_cost), cost) > balance;
-        const bool kept = kind != kAbsent && !conflicting && !overdrawn;
+        const bool over_budget = cost > 0 && wadd(wadd(reserved_own, spent), cost) > balance;
+        const bool kept = kind != kAbsent && !conflicting && !over_budget;
         if (lane == 0) {
             if (has_cell) {
                 used[claim >> 5] |= 1u << (claim & 31);
@@ -905,21 +905,21 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
             if (kept) {
                 bv<uint8_t>(b, y.u_sel)[i] = (uint8_t)sel;
                 bv<int8_t>(b, y.u_dir)[i] = (int8_t)step;
-                bv<int16_t>(b, y.u_drank)[i] = (int16_t)kept_count;
+                bv<int16_t>(b, y.u_drank)[i] = (int16_t)granted;
             }
         }
         if (kept) {
-            kept_cost = wadd(kept_cost, cost);
-            ++kept_count;
+            spent = wadd(spent, cost);
+            ++granted;
         }
         wave_sync();
     }
-    return kept_count;
+    return granted;
 }
 
 // The decided command of unit i (_commands, N/bots/abstraction.py:1063-1096):
 // {kind, direction, none_duration, target_cell, produced_type, request_order}.
-NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLayout& y, int32_t i, int32_t kept_count,
+NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLayout& y, int32_t i, int32_t granted,
                          int32_t out[6]) {
     const Unit u = unit_at(g, e, b, i);
     const int32_t sel = bv<uint8_t>(b, y.u_sel)[i];
@@ -951,7 +951,7 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
     out[2] = filler ? kFillerDuration : 0;  // no rush desire waits
     out[3] = kept ? target : kAbsent;
     out[4] = kept ? ptype : kAbsent;
-    out[5] = kept ? (int32_t)bv<int16_t>(b, y.u_drank)[i] : (filler ? wadd(kept_count, filler_rank) : kAbsent);
+    out[5] = kept ? (int32_t)bv<int16_t>(b, y.u_drank)[i] : (filler ? wadd(granted, filler_rank) : kAbsent);
 }
 
 // The carry rows in LDS and b.next_order into the carry of env l.
@@ -1035,7 +1035,7 @@ NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lan
 }
 
 // family.act (N/bots/family.py:34-41): the rush decisions on the carry, then
-// translate's plan and walk.  Returns kept_count; commands come from
+// translate's plan and walk.  Returns how many desires the walk keeps; commands come from
 // unit_command and the carry from settle_carry.
 NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
                        const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane,

@@ -1151,9 +1151,30 @@ NR_DEV void remove_slot(const Env& e, int32_t s) {
 // each kind's _complete (move.py:19-27, harvest.py:24-45, return_.py:25-43,
 // produce.py:47-81, attack.py:78-98).
 // The member's retained values are wave-uniform arguments.
+// The per-slot completion records of one env, as the step target returns them
+// (results 27-30, src/nanorts/core/cycle.py:48-81, 254-300): is_member [E],
+// int32 [E][6] (actor_birth, target_birth, amount, balance, spawn_birth,
+// death_birth), int16 [E][4] (target_slot, spawn_slot, spawn_cell,
+// death_slot), int8 [E][6] (flags, actor_owner, actor_unit_type,
+// produced_type, death_owner, death_unit_type).  Flags: hit 1, death 2,
+// harvest 4, depleted 8, return 16, spawn 32.  The caller zero-fills them;
+// a member's turn writes its whole row.
+struct StepRecords {
+    uint8_t* member;
+    int32_t* wide;
+    int16_t* index;
+    int8_t* narrow;
+};
+enum : int32_t { REC_HIT = 1, REC_DEATH = 2, REC_HARVEST = 4, REC_DEPLETED = 8, REC_RETURN = 16, REC_SPAWN = 32 };
+
+// `rec` (NULL on every path but the step target's): where this member's
+// records go (each kind's records, N/core/kinds/*.py, and the death of the
+// unit its turn removes, N/core/completion.py:68-99).
 NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t slot, int32_t kind, int32_t dir,
                       int32_t target, int32_t ptype, int32_t owner, int32_t utype, int32_t rcell, int32_t rbirth,
-                      int32_t rcarried) {
+                      int32_t rcarried, const StepRecords* rec = nullptr) {
+    int32_t rf = 0, r_target = 0, r_tbirth = 0, r_amount = 0, r_balance = 0, r_ptype = 0, r_spawn = 0,
+            r_sbirth = 0, r_scell = 0;
     const int32_t actor = clampi(utype, 0, g.T - 1);
     const int32_t player = clampi(owner, 0, 1);
     const int32_t cur_birth = uni(e.birth[slot]);
@@ -1175,6 +1196,12 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
             const int32_t stack = uni(n.slot);
             const int32_t amount = tabv(h, F_AMOUNT, actor);
             const int32_t left = wsub(uni(e.carried[stack]), amount);
+            if (rec) {
+                rf |= left <= 0 ? REC_HARVEST | REC_DEPLETED : REC_HARVEST;
+                r_target = stack;
+                r_tbirth = uni(e.birth[stack]);
+                r_amount = amount;
+            }
             if (lane == 0) {
                 e.carried[stack] = left;
                 if (alive) e.carried[slot] = amount;
@@ -1188,6 +1215,13 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
         const Nb n = neighbour(g, h, e, rcell, dir);
         const bool returning =
             uni(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_STOCKPILE) && rcarried > 0 ? 1 : 0) != 0;
+        if (returning && rec) {
+            rf |= REC_RETURN;
+            r_target = uni(n.slot);
+            r_tbirth = uni(e.birth[gidx(uni(n.slot), g.E)]);
+            r_amount = rcarried;
+            r_balance = wadd(uni(e.sc[S_RES0 + player]), rcarried);
+        }
         if (returning && lane == 0) {
             if (alive) e.carried[slot] = 0;
             e.sc[S_RES0 + player] = wadd(e.sc[S_RES0 + player], rcarried);
@@ -1206,6 +1240,14 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
                 if (m != 0ull) newborn = block + base + (int32_t)__builtin_ctzll(m);
             }
             newborn = uni(newborn);
+            if (rec && newborn >= 0) {
+                rf |= REC_SPAWN;
+                r_ptype = newborn_type;
+                r_spawn = newborn;
+                r_sbirth = uni(e.sc[S_NEXT_BIRTH]);
+                r_scell = dest;
+                r_balance = balance;
+            }
             if (lane == 0) {
                 if (newborn >= 0) {
                     const int32_t birth = e.sc[S_NEXT_BIRTH];
@@ -1230,12 +1272,44 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
         if (occ != kAbsent) {
             const int32_t victim = occ;
             const int32_t left = wsub(uni(e.hp[gidx(victim, g.E)]), tabv(h, F_DAMAGE, actor));
+            if (rec) {
+                rf |= REC_HIT;
+                r_target = victim;
+                r_tbirth = uni(e.birth[gidx(victim, g.E)]);
+                r_amount = tabv(h, F_DAMAGE, actor);
+            }
             if (lane == 0) e.hp[victim] = (int16_t)left;
             if (left <= 0) {
                 removal = true;
                 removed = victim;
             }
         }
+    }
+    if (rec && lane == 0) {
+        // the whole row of this member: its records, the death last
+        const int32_t r = gidx(removed, g.E);
+        if (removal) rf |= REC_DEATH;
+        const bool any = rf != 0;
+        rec->member[slot] = 1;
+        int32_t* w = rec->wide + (int64_t)slot * 6;
+        int16_t* x = rec->index + (int64_t)slot * 4;
+        int8_t* n = rec->narrow + (int64_t)slot * 6;
+        w[0] = any ? rbirth : 0;
+        w[1] = r_tbirth;
+        w[2] = r_amount;
+        w[3] = r_balance;
+        w[4] = r_sbirth;
+        w[5] = removal ? e.birth[r] : 0;
+        x[0] = (int16_t)r_target;
+        x[1] = (int16_t)r_spawn;
+        x[2] = (int16_t)r_scell;
+        x[3] = (int16_t)(removal ? removed : 0);
+        n[0] = (int8_t)rf;
+        n[1] = (int8_t)(any ? owner : 0);
+        n[2] = (int8_t)(any ? utype : 0);
+        n[3] = (int8_t)r_ptype;
+        n[4] = (int8_t)(removal ? e.owner[r] : 0);
+        n[5] = (int8_t)(removal ? e.utype[r] : 0);
     }
     if (removal) {
         wave_sync();
@@ -1261,7 +1335,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // path for more (member records in the phase union) is left out.  Returns
 // the new time.
 NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false,
-                        const LiveLanes* known = nullptr) {
+                        const LiveLanes* known = nullptr, const StepRecords* records = nullptr) {
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
@@ -1318,7 +1392,7 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
                       (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
                       (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
-                      __builtin_amdgcn_readlane(rc, li));
+                      __builtin_amdgcn_readlane(rc, li), records);
         }
         return time;
     }
@@ -1387,7 +1461,7 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
                       (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
                       (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
-                      __builtin_amdgcn_readlane(rc, li));
+                      __builtin_amdgcn_readlane(rc, li), records);
         }
         return time;
     }
@@ -1408,7 +1482,7 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
         const int32_t a = uni(r[0]), b = uni(r[1]), c = uni(r[2]);
         take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
                   (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
-                  (int16_t)((c >> 8) & 0xFFFF), uni(r[3]), uni(r[4]));
+                  (int16_t)((c >> 8) & 0xFFFF), uni(r[3]), uni(r[4]), records);
     }
     return time;
 }
@@ -1484,9 +1558,9 @@ NR_DEV Outcome decide_counted(const Env& e, int lane) {
 
 // core.step (N/core/__init__.py:99-110) on the staged env.
 NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1,
-                      bool count_events) {
+                      bool count_events, const StepRecords* rec = nullptr) {
     admit(g, h, e, lane, key0, key1, count_events);
-    complete(g, h, e, lane);
+    complete(g, h, e, lane, false, nullptr, rec);
     decide(g, e, lane);
 }
 

@@ -602,6 +602,25 @@ NR_DEV void write_events(const KGame& g, const Env& e, int64_t l, const nanorts_
     if (r.admitted_attack && lane < 6) r.admitted_attack[6 * l + lane] = ev[20 + lane];
 }
 
+// The completion records of env l when the caller asked for them: every
+// row zeroed (a member's turn then writes its own).
+NR_DEV bool begin_records(const KGame& g, const nanorts_step_results& r, int64_t l, StepRecords* rec, int lane) {
+    if (!r.is_member || !r.records_i32 || !r.records_i16 || !r.records_i8) return false;
+    const int64_t E = g.E;
+    rec->member = r.is_member + l * E;
+    rec->wide = r.records_i32 + l * E * 6;
+    rec->index = r.records_i16 + l * E * 4;
+    rec->narrow = r.records_i8 + l * E * 6;
+    for (int32_t i = lane; i < g.E; i += kWave) rec->member[i] = 0;
+    for (int32_t i = lane; i < 6 * g.E; i += kWave) {
+        rec->wide[i] = 0;
+        rec->narrow[i] = 0;
+    }
+    for (int32_t i = lane; i < 4 * g.E; i += kWave) rec->index[i] = 0;
+    wave_sync();
+    return true;
+}
+
 // core.step on Commands [cmd_lanes][2][C] (cmd_lanes 1 broadcasts one row
 // to every lane, the reference's extent-1 operand) and keys [key_lanes][2].
 __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_state s, const uint32_t* key, int64_t key_lanes,
@@ -613,7 +632,9 @@ __global__ __launch_bounds__(256) void k_step(KGame g, int64_t lanes, nanorts_st
     const int64_t kl = key_lanes == 1 ? 0 : l;
     const uint32_t k0 = key[2 * kl], k1 = key[2 * kl + 1];
     const bool events = r.admitted_harvest || r.admitted_return || r.admitted_produce || r.admitted_attack;
-    core_step(g, hdr, e, lane, k0, k1, events);
+    StepRecords rec;
+    const bool records = begin_records(g, r, l, &rec, lane);
+    core_step(g, hdr, e, lane, k0, k1, events, records ? &rec : nullptr);
     store_env(g, s, l, e, lane);
     if (lane == 0) {
         const bool over = e.sc[S_GAME_OVER] != 0;
@@ -705,7 +726,9 @@ __global__ __launch_bounds__(256) void k_step_groups(GroupsArgs args) {
     const uint32_t k0 = sl.key[2 * kl], k1 = sl.key[2 * kl + 1];
     const nanorts_step_results r = sl.r;
     const bool events = r.admitted_harvest || r.admitted_return || r.admitted_produce || r.admitted_attack;
-    core_step(g, hdr, e, lane, k0, k1, events);
+    StepRecords rec;
+    const bool records = begin_records(g, r, l, &rec, lane);
+    core_step(g, hdr, e, lane, k0, k1, events, records ? &rec : nullptr);
     store_env(g, sl.s, l, e, lane);
     if (lane == 0) {
         const bool over = e.sc[S_GAME_OVER] != 0;
@@ -1122,7 +1145,7 @@ struct AstarArgs {
     const int32_t* range;
     const int32_t* rows;      // chain: [capacity][columns]
     const int32_t* queue;     // chain: [capacity]
-    const int32_t* count;     // chain: scalars count, moves_allowed, reserved, balance
+    const int32_t* count;     // chain: scalars count, may_move, reserved, balance
     const uint8_t* moves;
     const int32_t* reserved;
     const int32_t* balance;
@@ -1225,8 +1248,8 @@ __global__ __launch_bounds__(256) void k_astar_chain(AstarArgs a) {
     const int32_t held = a.balance[l * a.balance_stride];
     const int32_t asked = a.count[l * a.count_stride];
     const int64_t searched = asked < 0 ? 0 : (asked > cap ? cap : (int64_t)asked);
-    uint32_t kept_cost = 0u;
-    int32_t kept_count = 0;
+    uint32_t spent = 0u;
+    int32_t granted = 0;
     int64_t calls = 0;
     for (int64_t row = 0; row < searched; ++row) {
         wave_sync();
@@ -1266,25 +1289,25 @@ __global__ __launch_bounds__(256) void k_astar_chain(AstarArgs a) {
             }
             const bool on_board = claim >= 0 && claim < cells;
             const bool conflicting = on_board && (flags[claim] & kTaken) != 0;
-            const bool over = cost > 0 && (int32_t)(reserve + kept_cost + (uint32_t)cost) > held;
+            const bool over = cost > 0 && (int32_t)(reserve + spent + (uint32_t)cost) > held;
             const bool kept = eligible && !conflicting && !over;
             if (on_board) flags[claim] = (uint8_t)((flags[claim] & ~kOpen) | (kept ? kTaken : 0));
             int32_t* d = decisions + (int64_t)slot * 4;
-            d[0] = kept ? kept_count : kAbsent;
+            d[0] = kept ? granted : kAbsent;
             d[1] = selector;
             d[2] = direction;
             d[3] = drew ? 1 : 0;
             if (kept) {
-                kept_cost += (uint32_t)cost;
-                ++kept_count;
+                spent += (uint32_t)cost;
+                ++granted;
             }
         }
-        kept_count = __builtin_amdgcn_readfirstlane(kept_count);
-        kept_cost = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)kept_cost);
+        granted = __builtin_amdgcn_readfirstlane(granted);
+        spent = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)spent);
         calls = (int64_t)__builtin_amdgcn_readfirstlane((int32_t)calls);
     }
     wave_sync();
-    if (lane < 4) decisions[cap * 4 + lane] = lane == 0 ? kept_count : (lane == 1 ? (int32_t)calls : 0);
+    if (lane < 4) decisions[cap * 4 + lane] = lane == 0 ? granted : (lane == 1 ? (int32_t)calls : 0);
 }
 
 // seat.step_seat (N/bots/seat.py:84-149): the bot's commands from the current
@@ -2491,21 +2514,11 @@ int nanorts_amd_step(void* stream, const nanorts_game* game, nanorts_state state
     return launch(k_step, sh, lanes, (hipStream_t)stream, state, key, key_lanes, commands, lanes, results);
 }
 
-static int zero_bytes(hipStream_t stream, void* p, int64_t n) {
-    if (n <= 0) return NANORTS_OK;
-    const int64_t blocks64 = (n / 16 + 255) / 256;
-    const unsigned blocks = (unsigned)(blocks64 < 1 ? 1 : (blocks64 > 4096 ? 4096 : blocks64));
-    hipLaunchKernelGGL(k_zero_bytes, dim3(blocks), dim3(256), 0, stream, (uint8_t*)p, n);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return fail(NANORTS_INTERNAL, std::string("kernel launch failed: ") + hipGetErrorString(err));
-    return NANORTS_OK;
-}
-
 // One group of the step target's operands and results (nanorts_amd_step_ffi's
 // order) as the kernel's State, Commands and results.  A result that does not
 // alias its state operand is first filled from it, so the step runs in the
-// result buffers.  The per-slot event records (results 27-30) are written as
-// "no member".
+// result buffers.  The per-slot completion records (results 27-30) are the
+// kernel's.
 static int step_operands(hipStream_t st, const char* target, const void* const* operands, void* const* results,
                          int64_t lanes, int64_t E, int64_t cells, nanorts_state* s, nanorts_commands* c,
                          nanorts_step_results* r) {
@@ -2559,14 +2572,10 @@ static int step_operands(hipStream_t st, const char* target, const void* const* 
     r->admitted_return = (int32_t*)results[24];
     r->admitted_produce = (int32_t*)results[25];
     r->admitted_attack = (int32_t*)results[26];
-    // The per-slot event records (is_member pred[L][E], int32 [L][E][6],
-    // int16 [L][E][4], int8 [L][E][6]) are written as "no member": every
-    // record field then reads as its fill.
-    const int64_t record_bytes[4] = {E, E * 6 * 4, E * 4 * 2, E * 6};
-    for (int i = 0; i < 4; ++i) {
-        const int code = zero_bytes(st, results[27 + i], record_bytes[i] * lanes);
-        if (code != NANORTS_OK) return code;
-    }
+    r->is_member = (uint8_t*)results[27];
+    r->records_i32 = (int32_t*)results[28];
+    r->records_i16 = (int16_t*)results[29];
+    r->records_i8 = (int8_t*)results[30];
     return NANORTS_OK;
 }
 

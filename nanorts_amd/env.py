@@ -522,7 +522,7 @@ class NanoRTS:
                "admitted_produce": torch.empty((L, 2, b.unit_type_capacity), dtype=torch.int32, device=d),
                "admitted_attack": torch.empty((L, 2, 3), dtype=torch.int32, device=d)}
         c = native.Commands(*[_ptr(cmd[f]) for f, _ in native.Commands._fields_])
-        r = native.StepResults(*[_ptr(out[f]) for f, _ in native.StepResults._fields_])
+        r = native.StepResults(*[_ptr(out.get(f)) for f, _ in native.StepResults._fields_])
         native.check(self.lib.nanorts_amd_step(_stream(), self.dev.ref, state.native(), L, _ptr(keyt), keyt.shape[0], c,
                                            r), "nanorts_amd_step")
         return out

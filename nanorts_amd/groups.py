@@ -60,13 +60,16 @@ def steps_together(games: Sequence[Any]) -> bool:
     return 1 < len(games) <= MAX_GROUPS and all(_tables_equal(games[0], g) for g in games[1:])
 
 
-def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]]) -> list[dict[str, torch.Tensor]]:
+def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]], *,
+                records: bool = False) -> list[dict[str, torch.Tensor]]:
     """core.step over every request (key, state, commands, game holder), in
     place: `key` is uint32 key data [L, 2] or [2] (host data, or an int32
     device tensor holding it bit for bit); `state` an
     EnvironmentState or the core State; `commands` int32[L, 2, C] per
     field; the holder a facade or DeviceGame.  Returns each group's
-    terminated, truncated, reward and admitted event counts."""
+    terminated, truncated, reward and admitted event counts, and with
+    `records` the per-slot completion records (is_member, records_i32,
+    records_i16, records_i8; core.step_events decodes them)."""
     if not requests:
         return []
     devs = [_device_game(holder) for *_, holder in requests]
@@ -93,6 +96,12 @@ def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]
                "admitted_return": torch.empty((L, 2), dtype=torch.int32, device=d),
                "admitted_produce": torch.empty((L, 2, b.unit_type_capacity), dtype=torch.int32, device=d),
                "admitted_attack": torch.empty((L, 2, 3), dtype=torch.int32, device=d)}
+        if records:
+            E = b.entity_capacity
+            out.update(is_member=torch.empty((L, E), dtype=torch.bool, device=d),
+                       records_i32=torch.empty((L, E, 6), dtype=torch.int32, device=d),
+                       records_i16=torch.empty((L, E, 4), dtype=torch.int16, device=d),
+                       records_i8=torch.empty((L, E, 6), dtype=torch.int8, device=d))
         leaves = core.leaves
         st = native.State(*[_ptr(leaves[name]) for name in native.STATE_FIELDS[:-2]], None, None)
         prepared.append((L, keyt, cmd, out, st))
@@ -108,14 +117,14 @@ def step_groups(requests: Sequence[tuple[Any, Any, dict[str, torch.Tensor], Any]
             keys = (ctypes.c_void_p * G)(*[_ptr(p[1]) for p in part])
             key_lanes = (ctypes.c_int64 * G)(*[p[1].shape[0] for p in part])
             cmds = (native.Commands * G)(*[native.Commands(*[_ptr(p[2][f]) for f in _COMMAND_FIELDS]) for p in part])
-            outs = (native.StepResults * G)(*[native.StepResults(*[_ptr(p[3][f]) for f, _ in
+            outs = (native.StepResults * G)(*[native.StepResults(*[_ptr(p[3].get(f)) for f, _ in
                                                                    native.StepResults._fields_]) for p in part])
             native.check(lib.nanorts_amd_step_groups(_stream(), G, games, states, lanes, keys, key_lanes, cmds, outs),
                          "nanorts_amd_step_groups")
         return results
     for dev, (L, keyt, cmd, out, st) in zip(devs, prepared, strict=True):
         c = native.Commands(*[_ptr(cmd[f]) for f in _COMMAND_FIELDS])
-        r = native.StepResults(*[_ptr(out[f]) for f, _ in native.StepResults._fields_])
+        r = native.StepResults(*[_ptr(out.get(f)) for f, _ in native.StepResults._fields_])
         native.check(lib.nanorts_amd_step(_stream(), dev.ref, st, L, _ptr(keyt), keyt.shape[0], c, r), "nanorts_amd_step")
     return results
 

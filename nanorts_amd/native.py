@@ -53,7 +53,7 @@ class Commands(ctypes.Structure):
 class StepResults(ctypes.Structure):
     _fields_ = [(name, _VP) for name in
                 ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
-                 "admitted_attack")]
+                 "admitted_attack", "is_member", "records_i32", "records_i16", "records_i8")]
 
 
 class EnvResults(ctypes.Structure):

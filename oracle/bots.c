@@ -651,10 +651,10 @@ static void translate(const nro_game* g, const env_t* e, bot_t* b, const ab_t* a
         b->queue[y + 1] = v;
     }
     /* _walked */
-    const int moves_allowed = within_balance(b, e, 0) && within_balance(b, e, 1);
+    const int may_move = within_balance(b, e, 0) && within_balance(b, e, 1);
     memset(b->used, 0, (size_t)cells);
     memset(b->kept_cells, 0, (size_t)cells);
-    int32_t kept_cost = 0, kept_count = 0;
+    int32_t spent = 0, granted = 0;
     for (int32_t i = 0; i < C; ++i) {
         b->decided[i] = NO_DESIRE;
         b->rank_out[i] = ABSENT;
@@ -667,20 +667,20 @@ static void translate(const nro_game* g, const env_t* e, bot_t* b, const ab_t* a
         desire_t d = b->fallback[i];
         if (step != ABSENT) {
             desire_t mv = {KIND_MOVE, step, ABSENT, ABSENT, neighbour_cell(g, b->start[i], step), 0, 0};
-            d = moves_allowed ? mv : NO_DESIRE;
+            d = may_move ? mv : NO_DESIRE;
         }
         const int has_cell = d.claimed != ABSENT && d.claimed >= 0 && d.claimed < cells;
         const int conflicting = has_cell && (b->claimed[d.claimed] || b->kept_cells[d.claimed]);
-        const int overdrawn = d.cost > 0 && wadd(wadd(b->reserved_cost[own], kept_cost), d.cost) > e->resources[own];
-        const int kept = d.kind != KIND_ABSENT && !conflicting && !overdrawn;
+        const int over_budget = d.cost > 0 && wadd(wadd(b->reserved_cost[own], spent), d.cost) > e->resources[own];
+        const int kept = d.kind != KIND_ABSENT && !conflicting && !over_budget;
         if (has_cell) {
             b->used[d.claimed] = 1;
             if (kept) b->kept_cells[d.claimed] = 1;
         }
         if (kept) {
-            kept_cost = wadd(kept_cost, d.cost);
+            spent = wadd(spent, d.cost);
             b->decided[i] = d;
-            b->rank_out[i] = kept_count++;
+            b->rank_out[i] = granted++;
         }
     }
     /* _commands */
@@ -701,7 +701,7 @@ static void translate(const nro_game* g, const env_t* e, bot_t* b, const ab_t* a
         c->none_duration = (kept && d->kind == KIND_NONE) ? d->none_duration : (filler ? FILLER_DURATION : 0);
         c->target_cell = kept ? d->target_cell : ABSENT;
         c->produced_type = kept ? d->produced_type : ABSENT;
-        c->request_order = kept ? b->rank_out[i] : (filler ? wadd(kept_count, filler_rank) : ABSENT);
+        c->request_order = kept ? b->rank_out[i] : (filler ? wadd(granted, filler_rank) : ABSENT);
     }
     /* _settled */
     int32_t standing = 0;
@@ -794,7 +794,7 @@ static int32_t chain_neighbour(int32_t cell, int32_t direction, int32_t W) {
 }
 
 void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const int32_t* rows, const int32_t* queue,
-                     int32_t count, int32_t moves_allowed, int32_t reserved, int32_t balance, const int32_t* draws,
+                     int32_t count, int32_t may_move, int32_t reserved, int32_t balance, const int32_t* draws,
                      int64_t draw_count, int32_t drawing, int32_t W, int32_t H, int64_t capacity, int64_t columns,
                      const int64_t fallback[3], const int64_t blocked[3], int32_t* out) {
     enum { OPEN = 1, TAKEN = 2 };
@@ -815,8 +815,8 @@ void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const in
         out[4 * i + 3] = 0;
     }
     const int64_t searched = count < 0 ? 0 : (count > capacity ? capacity : (int64_t)count);
-    uint32_t kept_cost = 0;
-    int32_t kept_count = 0, calls = 0;
+    uint32_t spent = 0;
+    int32_t granted = 0, calls = 0;
     for (int64_t r = 0; r < searched; ++r) {
         const int32_t slot = queue[r];
         if (slot < 0 || slot >= capacity) continue;
@@ -828,7 +828,7 @@ void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const in
         int32_t selector = 0, direction = ABSENT;
         int eligible = entry[fallback[0]] != ABSENT;
         int32_t claim = entry[fallback[1]], cost = entry[fallback[2]];
-        if (stepped && moves_allowed) {
+        if (stepped && may_move) {
             selector = 2;
             direction = path[1];
             eligible = 1;
@@ -840,7 +840,7 @@ void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const in
             claim = entry[blocked[1]];
             cost = entry[blocked[2]];
         }
-        const int drew = drawing && entry[3] != 0 && !(stepped && moves_allowed);
+        const int drew = drawing && entry[3] != 0 && !(stepped && may_move);
         if (drew) {
             const int64_t at = calls < draw_count ? calls : draw_count - 1;
             direction = ABSENT;
@@ -859,19 +859,19 @@ void nro_astar_chain(const uint8_t* free_cells, const uint8_t* claimed, const in
         }
         const int on_board = claim >= 0 && claim < cells;
         const int conflicting = on_board && (flags[claim] & TAKEN) != 0;
-        const int over = cost > 0 && (int32_t)(uint32_t)((uint32_t)reserved + kept_cost + (uint32_t)cost) > balance;
+        const int over = cost > 0 && (int32_t)(uint32_t)((uint32_t)reserved + spent + (uint32_t)cost) > balance;
         const int kept = eligible && !conflicting && !over;
         if (on_board) flags[claim] = (uint8_t)((flags[claim] & ~OPEN) | (kept ? TAKEN : 0));
-        out[4 * slot] = kept ? kept_count : ABSENT;
+        out[4 * slot] = kept ? granted : ABSENT;
         out[4 * slot + 1] = selector;
         out[4 * slot + 2] = direction;
         out[4 * slot + 3] = drew;
         if (kept) {
-            kept_cost += (uint32_t)cost;
-            ++kept_count;
+            spent += (uint32_t)cost;
+            ++granted;
         }
     }
-    out[4 * capacity] = kept_count;
+    out[4 * capacity] = granted;
     out[4 * capacity + 1] = calls;
     out[4 * capacity + 2] = 0;
     out[4 * capacity + 3] = 0;

@@ -417,6 +417,18 @@ typedef struct retained_t {
     int32_t kind, direction, target_cell, produced_type, birth, owner, unit_type, cell, carried;
 } retained_t;
 
+/* One member's completion records (N/core/cycle.py:48-81: flags hit 1,
+ * death 2, harvest 4, depleted 8, return 16, spawn 32; the columns each
+ * record writes: the records of each N/core/kinds module, N/core/completion.py:68-99). */
+typedef struct record_t {
+    int32_t flags, actor_birth, actor_owner, actor_type;
+    int32_t target_slot, target_birth, amount, balance;
+    int32_t produced_type, spawn_slot, spawn_birth, spawn_cell;
+    int32_t death_slot, death_birth, death_owner, death_type;
+} record_t;
+
+enum { REC_HIT = 1, REC_DEATH = 2, REC_HARVEST = 4, REC_DEPLETED = 8, REC_RETURN = 16, REC_SPAWN = 32 };
+
 /* Per-thread buffers so one env step allocates nothing. */
 typedef struct work_t {
     int32_t* scratch; /* 9 E */
@@ -426,6 +438,8 @@ typedef struct work_t {
     int32_t* ranking;
     int32_t* keys;
     uint8_t* completed;
+    uint8_t* members;
+    record_t* records;
     retained_t* retained;
     cmd_t* cmds;
     uint8_t* seen;
@@ -444,6 +458,8 @@ static void work_init(const nro_game* g, work_t* w) {
     w->ranking = (int32_t*)malloc(sizeof(int32_t) * E);
     w->keys = (int32_t*)malloc(sizeof(int32_t) * owned);
     w->completed = (uint8_t*)malloc(E);
+    w->members = (uint8_t*)malloc(E);
+    w->records = (record_t*)malloc(sizeof(record_t) * E);
     w->retained = (retained_t*)malloc(sizeof(retained_t) * E);
     w->cmds = (cmd_t*)malloc(sizeof(cmd_t) * owned);
     w->seen = (uint8_t*)malloc((size_t)g->cells);
@@ -460,6 +476,8 @@ static void work_free(work_t* w) {
     free(w->ranking);
     free(w->keys);
     free(w->completed);
+    free(w->members);
+    free(w->records);
     free(w->retained);
     free(w->cmds);
     free(w->seen);
@@ -687,7 +705,14 @@ static void admit(const nro_game* g, const env_t* e, const cmd_t* cmds, const ui
  * kind's _complete: move.py:19-27, harvest.py:24-45, return_.py:25-43,
  * produce.py:47-81, attack.py:78-98.  Effects are computed against the state
  * at the start of the turn and written in list order. */
-static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const retained_t* r) {
+static void record(record_t* rec, const retained_t* r, int32_t flag) {
+    rec->flags |= flag;
+    rec->actor_birth = r->birth;
+    rec->actor_owner = r->owner;
+    rec->actor_type = r->unit_type;
+}
+
+static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const retained_t* r, record_t* rec) {
     const int32_t T = g->types, N = g->neutral, C = g->capacity, cells = g->cells, E = g->entities;
     const int32_t actor_type = clampi(r->unit_type, 0, T - 1);
     const int32_t player = clampi(r->owner, 0, 1);
@@ -711,6 +736,10 @@ static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const ret
             const int32_t amount = g->harvest_amount[actor_type];
             const int32_t left = wadd(e->carried[gidx(nb.slot, E)], -amount);
             if (harvesting) {
+                record(rec, r, left <= 0 ? REC_HARVEST | REC_DEPLETED : REC_HARVEST);
+                rec->target_slot = nb.slot;
+                rec->target_birth = e->birth[nb.slot];
+                rec->amount = amount;
                 e->carried[nb.slot] = left;
                 if (alive) e->carried[slot] = amount;
                 if (left <= 0) {
@@ -724,6 +753,11 @@ static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const ret
             const int returning = nb.occupied && g->is_stockpile[nb.unit_type] && r->carried > 0;
             if (returning) {
                 const int32_t balance = wadd(e->resources[player], r->carried);
+                record(rec, r, REC_RETURN);
+                rec->target_slot = nb.slot;
+                rec->target_birth = e->birth[nb.slot];
+                rec->amount = r->carried;
+                rec->balance = balance;
                 if (alive) e->carried[slot] = 0;
                 e->resources[player] = balance;
             }
@@ -748,6 +782,12 @@ static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const ret
             const int overflows = affordable && !has_free;
             if (spawns) {
                 const int32_t birth = *e->next_birth;
+                record(rec, r, REC_SPAWN);
+                rec->produced_type = newborn_type;
+                rec->spawn_slot = newborn;
+                rec->spawn_birth = birth;
+                rec->spawn_cell = destination;
+                rec->balance = balance;
                 e->resources[player] = balance;
                 if (destination >= 0 && destination < cells) e->entity_at[destination] = (int16_t)newborn;
                 e->birth[newborn] = birth;
@@ -766,6 +806,10 @@ static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const ret
             if (hit) {
                 const int32_t victim = occupant;
                 const int32_t left = wadd(e->hit_points[gidx(victim, E)], -g->attack_damage[actor_type]);
+                record(rec, r, REC_HIT);
+                rec->target_slot = victim;
+                rec->target_birth = e->birth[gidx(victim, E)];
+                rec->amount = g->attack_damage[actor_type];
                 e->hit_points[victim] = (int16_t)left;
                 if (left <= 0) {
                     removal = 1;
@@ -781,6 +825,11 @@ static void take_turn(const nro_game* g, const env_t* e, int32_t slot, const ret
          * removed slot's row unchanged by the writes above, so reading it now
          * is reading the turn-start value. */
         const int32_t at = e->cell[gidx(removed_slot, E)];
+        record(rec, r, REC_DEATH);
+        rec->death_slot = removed_slot;
+        rec->death_birth = e->birth[gidx(removed_slot, E)];
+        rec->death_owner = e->owner[gidx(removed_slot, E)];
+        rec->death_type = e->unit_type[gidx(removed_slot, E)];
         if (at >= 0 && at < cells) e->entity_at[at] = (int16_t)ABSENT;
         remove_slot(e, removed_slot);
     }
@@ -819,9 +868,14 @@ static void complete(const nro_game* g, const env_t* e, work_t* w) {
     qsort(items, (size_t)owned, sizeof(sort_item_t), cmp_items);
     for (int32_t s = 0; s < E; ++s)
         if (completed[s]) clear_pending(e, s);
+    for (int32_t s = 0; s < E; ++s) {
+        w->members[s] = 0;
+        memset(&w->records[s], 0, sizeof(record_t));
+    }
     for (int32_t position = 0; position < members; ++position) {
         const int32_t s = N + items[position].k1;
-        take_turn(g, e, s, &retained[s]);
+        w->members[s] = 1;
+        take_turn(g, e, s, &retained[s], &w->records[s]);
     }
 }
 
@@ -878,6 +932,33 @@ void nro_core_step(const nro_game* g, nro_state* s, const nro_commands* c, const
             if (out->reward) {
                 out->reward[2 * l] = reward[0];
                 out->reward[2 * l + 1] = reward[1];
+            }
+            if (out->is_member && out->records_i32 && out->records_i16 && out->records_i8) {
+                const int32_t E = g->entities;
+                for (int32_t s2 = 0; s2 < E; ++s2) {
+                    const record_t* rc = &w.records[s2];
+                    const int64_t at = l * E + s2;
+                    out->is_member[at] = w.members[s2];
+                    int32_t* wide = out->records_i32 + at * 6;
+                    int16_t* index = out->records_i16 + at * 4;
+                    int8_t* narrow = out->records_i8 + at * 6;
+                    wide[0] = rc->actor_birth;
+                    wide[1] = rc->target_birth;
+                    wide[2] = rc->amount;
+                    wide[3] = rc->balance;
+                    wide[4] = rc->spawn_birth;
+                    wide[5] = rc->death_birth;
+                    index[0] = (int16_t)rc->target_slot;
+                    index[1] = (int16_t)rc->spawn_slot;
+                    index[2] = (int16_t)rc->spawn_cell;
+                    index[3] = (int16_t)rc->death_slot;
+                    narrow[0] = (int8_t)rc->flags;
+                    narrow[1] = (int8_t)rc->actor_owner;
+                    narrow[2] = (int8_t)rc->actor_type;
+                    narrow[3] = (int8_t)rc->produced_type;
+                    narrow[4] = (int8_t)rc->death_owner;
+                    narrow[5] = (int8_t)rc->death_type;
+                }
             }
             for (int32_t p = 0; p < 2; ++p) {
                 if (out->admitted_harvest) out->admitted_harvest[2 * l + p] = ev.harvest[p];

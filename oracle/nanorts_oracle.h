@@ -101,6 +101,18 @@ typedef struct nro_step_out {
     int32_t* admitted_return;   /* [L][2] */
     int32_t* admitted_produce;  /* [L][2][T] */
     int32_t* admitted_attack;   /* [L][2][3] */
+    /* The per-slot completion records of the FFI target's results 27-30
+     * (src/nanorts/core/cycle.py:48-81, 254-300): is_member [L][E], int32
+     * [L][E][6] (actor_birth, target_birth, amount, balance, spawn_birth,
+     * death_birth), int16 [L][E][4] (target_slot, spawn_slot, spawn_cell,
+     * death_slot), int8 [L][E][6] (flags, actor_owner, actor_unit_type,
+     * produced_type, death_owner, death_unit_type).  Non-members' rows are
+     * zero; a member's columns its records do not set are zero.  Any may
+     * be NULL (then none is written). */
+    uint8_t* is_member;
+    int32_t* records_i32;
+    int16_t* records_i16;
+    int8_t* records_i8;
 } nro_step_out;
 
 /* threefry2x32 and the JAX key plumbing (partitionable mode). */

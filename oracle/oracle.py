@@ -54,7 +54,7 @@ def astar(open_cells: np.ndarray, start: int, target: int, range_: int) -> tuple
 
 
 def astar_chain(free_cells: np.ndarray, claimed: np.ndarray, rows: np.ndarray, queue: np.ndarray, count: int,
-                moves_allowed: bool, reserved: int, balance: int, draws: np.ndarray, drawing: bool,
+                may_move: bool, reserved: int, balance: int, draws: np.ndarray, drawing: bool,
                 fallback: tuple[int, int, int], blocked: tuple[int, int, int]) -> np.ndarray:
     """The FFI target nanorts_astar_chain for one lane over bool[H, W] free and
     claimed cells: decisions int32[capacity + 1, 4]."""
@@ -70,7 +70,7 @@ def astar_chain(free_cells: np.ndarray, claimed: np.ndarray, rows: np.ndarray, q
     f3 = (ctypes.c_int64 * 3)(*fallback)
     b3 = (ctypes.c_int64 * 3)(*blocked)
     lib.nro_astar_chain(_ptr(free_u8), _ptr(claimed_u8), _ptr(rows), _ptr(queue), ctypes.c_int32(count),
-                        ctypes.c_int32(int(bool(moves_allowed))), ctypes.c_int32(reserved), ctypes.c_int32(balance),
+                        ctypes.c_int32(int(bool(may_move))), ctypes.c_int32(reserved), ctypes.c_int32(balance),
                         _ptr(draws), ctypes.c_int64(draws.size), ctypes.c_int32(int(bool(drawing))), ctypes.c_int32(W),
                         ctypes.c_int32(H), ctypes.c_int64(capacity), ctypes.c_int64(columns), f3, b3, _ptr(out))
     return out
@@ -109,7 +109,7 @@ class Commands(ctypes.Structure):
 class StepOut(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in
                 ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
-                 "admitted_attack")]
+                 "admitted_attack", "is_member", "records_i32", "records_i16", "records_i8")]
 
 
 class EnvOut(ctypes.Structure):
@@ -179,10 +179,13 @@ class Oracle:
     def core_step(self, state, commands: dict[str, np.ndarray], keys: np.ndarray) -> dict[str, np.ndarray]:
         L = state["time"].shape[0]
         T = self.game.bucket.unit_type_capacity
+        E = self.game.bucket.entity_capacity
         out = {"terminated": np.zeros(L, np.uint8), "truncated": np.zeros(L, np.uint8),
                "reward": np.zeros((L, 2), np.float32), "admitted_harvest": np.zeros((L, 2), np.int32),
                "admitted_return": np.zeros((L, 2), np.int32), "admitted_produce": np.zeros((L, 2, T), np.int32),
-               "admitted_attack": np.zeros((L, 2, 3), np.int32)}
+               "admitted_attack": np.zeros((L, 2, 3), np.int32), "is_member": np.zeros((L, E), np.uint8),
+               "records_i32": np.zeros((L, E, 6), np.int32), "records_i16": np.zeros((L, E, 4), np.int16),
+               "records_i8": np.zeros((L, E, 6), np.int8)}
         keep = [np.ascontiguousarray(commands[f], np.int32) for f, _ in Commands._fields_]
         c = Commands(*[_ptr(a) for a in keep])
         o = StepOut(*[_ptr(out[f]) for f, _ in StepOut._fields_])

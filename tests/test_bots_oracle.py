@@ -331,7 +331,7 @@ def test_chain_moves_and_claims_in_queue_order():
 
 
 def test_chain_blocked_when_moves_are_not_allowed():
-    """moves_allowed false: a row that can step takes its blocked desire
+    """may_move false: a row that can step takes its blocked desire
     (selector 1, no direction), one that cannot its fallback; a desire of
     kind -1 is never kept."""
     out = _chain([_chain_row(5, 7, blocked=(4, 9, 0)), _chain_row(6, 6, fallback=(-1, 3, 0))], moves=False)

@@ -177,7 +177,9 @@ def test_config3_seat_32768_games_full_episodes(bot_name):
 def test_config4_garden_of_war(oracle_threads):
     """GardenOfWar64x64, capacity_profile=False, CANCEL_ALTERNATING: 4096
     games of symbolic observations over 500 steps, and 256 games of pixel
-    observations (uint8[1024, 1024, 3])."""
+    observations (uint8[1024, 1024, 3]) over the same 500 steps, three games
+    followed by the oracle every cycle and their images compared with the
+    oracle's renderer every 50th cycle and at the last."""
     import torch
 
     import nanorts_amd
@@ -198,15 +200,22 @@ def test_config4_garden_of_war(oracle_threads):
     refs = [batch_initial(game, 1, roots[i:i + 1]) for i in sample]
     oracle = Oracle(game)
     tiles = rendering.tile_table(game.bucket.unit_type_capacity)
-    for t in range(6):
+    steps = 500
+    compared = 0
+    for t in range(steps):
         words = env.get_avail_actions(state, form="words")
         acts = env.sample_actions(words, KEY, t)
         obs, state, _, _, _ = env.step(None, state, acts, donate=True)
-        torch.cuda.synchronize()
+        rows = {a: acts[a][list(sample)].cpu().numpy() for a in env.agents}
         for k, i in enumerate(sample):
-            oracle.env_step(refs[k], np.stack([acts[a][i:i + 1].cpu().numpy() for a in env.agents], 1), False,
-                            observe=False)
-            image, _ = oracle.pixels(refs[k], False, tiles)
-            for p, agent in enumerate(env.agents):
-                np.testing.assert_array_equal(obs[agent].image[i].cpu().numpy(), image[0, p],
-                                              err_msg=f"game {i} cycle {t} {agent}")
+            oracle.env_step(refs[k], np.stack([rows[a][k:k + 1] for a in env.agents], 1), False, observe=False)
+        if t % 50 == 49 or t == steps - 1:
+            torch.cuda.synchronize()
+            _say(f"pixels x {L}: cycle {t}")
+            for k, i in enumerate(sample):
+                image, _ = oracle.pixels(refs[k], False, tiles)
+                for p, agent in enumerate(env.agents):
+                    np.testing.assert_array_equal(obs[agent].image[i].cpu().numpy(), image[0, p],
+                                                  err_msg=f"game {i} cycle {t} {agent}")
+                compared += 1
+    assert compared == 3 * 10

@@ -6,7 +6,8 @@ nanorts_step target (src/nanorts/core/cuda/step.cu:56-108, built by
 src/nanorts/core/cycle.py:123-134, 198-211) as device pointers: the key, the
 six Commands fields, terrain, the unit `table` and `timings` operands in the
 reference's column layout (src/nanorts/core/unit_tables.py:9-48), and the 23
-state leaves.  Each case is compared bit for bit with the oracle's core.step:
+state leaves.  Each case is compared bit for bit with the oracle's core.step
+(the state, the admitted counts and the per-slot completion records):
 results aliased to the state operands and results in separate buffers, keys
 and Commands per lane and broadcast from one row (extent 1).
 """
@@ -111,8 +112,10 @@ def test_step_ffi_matches_oracle(case, alias, broadcast, oracle_threads):
         assert_states_equal({k: v for k, v in before.items() if k in inputs}, inputs, f"{case} operands")
     for name, value in zip(("admitted_harvest", "admitted_return", "admitted_produce", "admitted_attack"), events):
         np.testing.assert_array_equal(value, want[name], err_msg=name)
-    for value in events[4:]:  # the per-slot records: no member
-        assert not value.any()
+    # the per-slot completion records (results 27-30)
+    for value, name in zip(events[4:], ("is_member", "records_i32", "records_i16", "records_i8")):
+        np.testing.assert_array_equal(value.astype(want[name].dtype), want[name], err_msg=name)
+    assert want["is_member"].any()
 
 
 def _dev(array):

@@ -127,8 +127,9 @@ def test_step_groups_ffi_matches_oracle(oracle_threads):
         for name, value in zip(("admitted_harvest", "admitted_return", "admitted_produce", "admitted_attack"),
                                events):
             np.testing.assert_array_equal(value.cpu().numpy(), want[name], err_msg=f"group {k} {name}")
-        for value in events[4:]:
-            assert not value.cpu().numpy().any()
+        for value, name in zip(events[4:], ("is_member", "records_i32", "records_i16", "records_i8")):
+            np.testing.assert_array_equal(value.cpu().numpy().astype(want[name].dtype), want[name],
+                                          err_msg=f"group {k} {name}")
 
 
 # ---------------------------------------------------------------------------

@@ -42,12 +42,12 @@ class DeviceBoard(rules.Board):
         from nanorts_amd import core
 
         got = core.step(self.root.copy(), self.dev, {f: torch.as_tensor(commands[f], device="cuda:0") for f in FIELDS},
-                        self.game)
+                        self.game, records=True)
         leaves = {name: t.cpu().numpy() for name, t in self.dev.leaves.items()}
         want = {k: v for k, v in self.st.items() if k in leaves}
         assert_states_equal(want, leaves, f"time {int(self.st['time'][0])}")
         for name in ("terminated", "truncated", "reward", "admitted_harvest", "admitted_return", "admitted_produce",
-                     "admitted_attack"):
+                     "admitted_attack", "is_member", "records_i32", "records_i16", "records_i8"):
             np.testing.assert_array_equal(got[name].cpu().numpy().astype(out[name].dtype), out[name], err_msg=name)
         self.cycles = getattr(self, "cycles", 0) + 1
 

@@ -161,6 +161,23 @@ class Board:
 BOARD = Board
 
 
+HIT, DEATH, HARVESTED, DEPLETED, RETURNED, SPAWNED = 1, 2, 4, 8, 16, 32
+
+
+def record_of(out: dict, slot: int) -> dict:
+    """A slot's completion record in a core.step's results (the step target's
+    results 27-30, src/nanorts/core/cycle.py:48-81)."""
+    i32, i16, i8 = out["records_i32"][0, slot], out["records_i16"][0, slot], out["records_i8"][0, slot]
+    return {"member": bool(out["is_member"][0, slot]), "flags": int(i8[0]),
+            "actor": (int(i32[0]), int(i8[1]), int(i8[2])), "target": (int(i16[0]), int(i32[1])),
+            "amount": int(i32[2]), "balance": int(i32[3]),
+            "spawn": (int(i8[3]), int(i16[1]), int(i32[4]), int(i16[2])),
+            "death": (int(i16[3]), int(i32[5]), int(i8[4]), int(i8[5]))}
+
+
+NO_SPAWN, NO_DEATH = (0, 0, 0, 0), (0, 0, 0, 0)
+
+
 def attack_offset(dx: int, dy: int) -> int:
     return (dy + 3) * 7 + (dx + 3)
 
@@ -193,6 +210,13 @@ def test_dead_attacker_still_hits():
     assert not bd.alive(50) and not bd.alive(3)
     assert bd.at(9) == ABSENT and bd.at(17) == ABSENT
     assert not out["terminated"][0]  # both bases stand
+    # each member's record: a hit and the death it caused, under its own
+    # (retained) birth, owner and type; no other slot is a member
+    assert record_of(out, 3) == {"member": True, "flags": HIT | DEATH, "actor": (4, 0, WORKER), "target": (50, 5),
+                                 "amount": 1, "balance": 0, "spawn": NO_SPAWN, "death": (50, 5, 1, WORKER)}
+    assert record_of(out, 50) == {"member": True, "flags": HIT | DEATH, "actor": (5, 1, WORKER), "target": (3, 4),
+                                  "amount": 1, "balance": 0, "spawn": NO_SPAWN, "death": (3, 4, 0, WORKER)}
+    assert out["is_member"][0].sum() == 2
 
 
 def test_dead_attacker_still_hits_through_the_jaxmarl_rows():
@@ -240,9 +264,11 @@ def test_live_returner_credits_and_empties_its_hands():
     bd.step({3: {"kind": RETURN, "direction": RIGHT}})
     bd.run(8)
     assert bd.st["player_resources"][0].tolist() == [5, 5] and int(bd.st["time"][0]) == 9
-    bd.step()  # time 9 -> 10
+    out = bd.step()  # time 9 -> 10
     assert bd.st["player_resources"][0].tolist() == [6, 5]
     assert int(bd.st["carried_resources"][0, 3]) == 0
+    assert record_of(out, 3) == {"member": True, "flags": RETURNED, "actor": (4, 0, WORKER), "target": (2, 2),
+                                 "amount": 1, "balance": 6, "spawn": NO_SPAWN, "death": NO_DEATH}
 
 
 def test_dead_producer_still_spawns():
@@ -265,9 +291,15 @@ def test_dead_producer_still_spawns():
     assert bd.pending(50) == (ATTACK, 0, 51)
     bd.run(3)
     assert int(bd.st["time"][0]) == 50 and bd.at(10) == 2
-    bd.step()  # time 50 -> 51
+    out = bd.step()  # time 50 -> 51
     s = bd.st
     assert bd.at(10) == ABSENT and bd.at(2) == 2
+    # the attacker's hit and the base's death; the dead base's spawn (into
+    # its own freed slot, balance 5 - 1)
+    assert record_of(out, 50) == {"member": True, "flags": HIT | DEATH, "actor": (5, 1, WORKER), "target": (2, 2),
+                                  "amount": 1, "balance": 0, "spawn": NO_SPAWN, "death": (2, 2, 0, BASE)}
+    assert record_of(out, 2) == {"member": True, "flags": SPAWNED, "actor": (2, 0, BASE), "target": (0, 0),
+                                 "amount": 0, "balance": 4, "spawn": (WORKER, 2, 6, 2), "death": NO_DEATH}
     assert (int(s["birth"][0, 2]), int(s["unit_type"][0, 2]), int(s["owner"][0, 2]), int(s["cell"][0, 2]),
             int(s["hit_points"][0, 2])) == (6, WORKER, 0, 2, 1)
     assert s["player_resources"][0].tolist() == [4, 5] and int(s["next_birth"][0]) == 7
@@ -824,8 +856,14 @@ def test_harvest_removes_a_pile_left_at_exactly_zero(pile):
     bd.place(3, 1)
     bd.st["carried_resources"][0, 0] = pile
     bd.step({3: {"kind": HARVEST, "direction": LEFT}})
-    bd.run(19)
+    bd.run(18)
+    out = bd.step()  # time 19 -> 20
     assert int(bd.st["time"][0]) == 20 and int(bd.st["carried_resources"][0, 3]) == 1
+    depleted = pile == 1
+    assert record_of(out, 3) == {
+        "member": True, "flags": HARVESTED | (DEPLETED | DEATH if depleted else 0), "actor": (4, 0, WORKER),
+        "target": (0, 0), "amount": 1, "balance": 0, "spawn": NO_SPAWN,
+        "death": (0, 0, -1, RESOURCE) if depleted else NO_DEATH}
     assert int(bd.st["carried_resources"][0, 0]) == pile - 1
     assert bd.alive(0) == (pile == 2) and bd.at(0) == (0 if pile == 2 else ABSENT)
     rows = bd.rows()
@@ -846,7 +884,10 @@ def test_attack_damage_is_the_attackers():
     bd.step({4: {"kind": ATTACK, "target_cell": 28}, 51: {"kind": ATTACK, "target_cell": 27}})
     bd.run(3)
     assert [int(bd.st["hit_points"][0, s]) for s in (4, 51)] == [4, 4]
-    bd.step()  # time 4 -> 5
+    out = bd.step()  # time 4 -> 5
+    assert record_of(out, 4)["flags"] == HIT and record_of(out, 4)["amount"] == 2
+    assert record_of(out, 51)["flags"] == HIT | DEATH and record_of(out, 51)["amount"] == 4
+    assert record_of(out, 51)["death"] == (4, 6, 0, LIGHT)
     assert int(bd.st["hit_points"][0, 51]) == 2 and bd.alive(51)
     assert not bd.alive(4) and bd.at(27) == ABSENT
 
@@ -1112,3 +1153,32 @@ def test_reset_where_done_restarts_and_counts_episodes():
     for leaf in STATE_LEAVES:
         np.testing.assert_array_equal(st[leaf.name][[0, 2]], fresh[leaf.name][[0, 2]], err_msg=leaf.name)
         np.testing.assert_array_equal(st[leaf.name][1], before[leaf.name][1], err_msg=leaf.name)
+
+
+def test_step_events_decode_the_records():
+    """core.step_events (the reference's decode of its step target's records,
+    src/nanorts/core/cycle.py:281-311) on the oracle's records of the
+    dead-attacker exchange: both hits and both deaths valid at their
+    members' slots, every other slot's fields at their fills."""
+    import torch
+
+    from nanorts_amd.core import step_events
+
+    bd = BOARD("basesWorkers8x8")
+    bd.place(50, 17)
+    bd.step({3: {"kind": ATTACK, "target_cell": 17}, 50: {"kind": ATTACK, "target_cell": 9}})
+    bd.run(3)
+    out = bd.step()
+    ev = step_events({k: torch.as_tensor(out[k]) for k in ("is_member", "records_i32", "records_i16", "records_i8")})
+    assert ev["hit_valid"][0].nonzero().ravel().tolist() == [3, 50]
+    assert ev["death_valid"][0].nonzero().ravel().tolist() == [3, 50]
+    assert not ev["harvest_valid"].any() and not ev["spawn_valid"].any() and not ev["return_valid"].any()
+    assert (ev["hit_target_slot"][0, 3], ev["hit_target_birth"][0, 3], ev["hit_damage"][0, 3]) == (50, 5, 1)
+    assert (ev["death_slot"][0, 50], ev["death_birth"][0, 50], ev["death_owner"][0, 50],
+            ev["death_unit_type"][0, 50]) == (3, 4, 0, WORKER)
+    assert (ev["death_actor_birth"][0, 50], ev["death_actor_owner"][0, 50]) == (5, 1)
+    others = torch.ones(bd.game.bucket.entity_capacity, dtype=torch.bool)
+    others[[3, 50]] = False
+    assert (ev["hit_target_slot"][0, others] == -1).all() and (ev["hit_damage"][0, others] == 0).all()
+    assert (ev["spawn_balance"][0] == -1).all() and (ev["return_amount"][0] == 0).all()
+    assert not ev["harvest_depleted"].any()
