@@ -21,6 +21,8 @@ from nanorts_amd.content import map_name_to_scenario
 from nanorts_amd.model import STATE_LEAVES, UnitTypeTableVersion
 from oracle import oracle as orc
 from oracle.oracle import Oracle, batch_initial, empty_carry
+from tests import bots_program as program
+from tests.bots_program import astar_by_keys
 
 NONE, MOVE, HARVEST, RETURN, PRODUCE, ATTACK = range(6)
 UP, RIGHT, DOWN, LEFT = range(4)
@@ -32,54 +34,6 @@ STEPS = ((0, -1), (1, 0), (0, 1), (-1, 0))
 # ---------------------------------------------------------------------------
 # A*
 # ---------------------------------------------------------------------------
-def astar_by_keys(free: np.ndarray, start: int, target: int, range_: int):
-    """The search in the program's key form: every open cell holds
-    f * (cells + 1) + (cells - sequence); the least key is popped."""
-    H, W = free.shape
-    cells = H * W
-    closed = 2**31 - 1
-    blocked, unseen = closed - 1, closed - 2
-    key = np.where(free.reshape(-1), unseen, blocked).astype(np.int64)
-    after = np.full(cells, -1, np.int64)
-    tx, ty = target % W, target // W
-
-    def manhattan(c):
-        return abs(c % W - tx) + abs(c // W - ty)
-
-    if 0 <= start < cells:
-        key[start] = manhattan(start) * (cells + 1) + cells
-        after[start] = start
-    inserted, goal, pops, searching = 1, -1, 0, True
-    while searching and pops < cells:
-        cell = int(np.argmin(key))
-        k = int(key[cell])
-        exhausted = k >= unseen
-        reached = not exhausted and (cell % W - tx) ** 2 + (cell // W - ty) ** 2 <= range_ * range_
-        expands = not exhausted and not reached
-        if expands:
-            g = k // (cells + 1) - manhattan(cell)
-            fresh = []
-            for dx, dy in STEPS:
-                x, y = cell % W + dx, cell // W + dy
-                if 0 <= x < W and 0 <= y < H and key[y * W + x] == unseen:
-                    fresh.append(y * W + x)
-            key[cell] = closed
-            for n in fresh:
-                key[n] = (g + 1 + manhattan(n)) * (cells + 1) + (cells - inserted)
-                after[n] = n if cell == start else after[cell]
-                inserted += 1
-        if reached:
-            goal = cell
-        searching = expands
-        pops += 0 if exhausted else 1
-    if goal < 0:
-        return 0, -1, -1, pops
-    offset = int(after[goal]) - start
-    # jnp.select: the first matching case wins (on a one-wide board -1 is LEFT)
-    step = next((d for o, d in ((W, DOWN), (-1, LEFT), (-W, UP), (1, RIGHT)) if offset == o), -1)
-    return 1, step, int(key[goal]) // (cells + 1) - manhattan(goal), pops
-
-
 def bfs(free: np.ndarray, start: int):
     H, W = free.shape
     dist = np.full(H * W, -1, np.int64)
@@ -291,6 +245,56 @@ def test_seat_rollout_keeps_invariants_against_random_play(strategy):
         assert (carry["order"][l][live] >= 0).all()
         assert sorted(carry["order"][l][live].tolist()) == list(range(int(live.sum())))
         assert carry["next_order"][l] == int(live.sum())
+
+
+# ---------------------------------------------------------------------------
+# The act against its array form (tests/bots_program.py): every cycle of
+# games played by the oracle's seat against random play, on boards with walls,
+# several bases, barracks and melee-only armies, for both seats' carries.
+# ---------------------------------------------------------------------------
+HEAVY, RANGED = 5, 6
+PROGRAM_GAMES = [
+    ("basesWorkers8x8", WORKER_RUSH, LIGHT, 220),
+    ("basesWorkers8x8", BARRACKS_RUSH, LIGHT, 320),
+    ("NoWhereToRun9x8", WORKER_RUSH, LIGHT, 200),
+    ("basesWorkers8x8Obstacle", BARRACKS_RUSH, RANGED, 320),
+    ("FourBasesWorkers8x8", WORKER_RUSH, LIGHT, 200),
+    ("TwoBasesBarracks16x16", BARRACKS_RUSH, HEAVY, 160),
+    ("melee8x8Mixed4", WORKER_RUSH, LIGHT, 120),
+    ("basesWorkersBarracks8x8", BARRACKS_RUSH, RANGED, 260),
+]
+
+
+def _compare_act(game, o, st, carry, strategy, trained, player, where):
+    """One act of the oracle against the array form, for every env."""
+    probe = {k: v.copy() for k, v in carry.items()}
+    cmds = o.abstraction_act({k: v.copy() for k, v in st.items()}, probe, strategy, trained, player)
+    for l in range(st["time"].shape[0]):
+        want, settled = program.act(game, st, carry, l, strategy, trained, player)
+        for f, v in want.items():
+            np.testing.assert_array_equal(cmds[f][l, player], v, err_msg=f"{where} env {l} command {f}")
+            assert (cmds[f][l, 1 - player] == -1).all() or f == "none_duration", (where, l, f)
+        for f in program.CARRY_FIELDS:
+            np.testing.assert_array_equal(probe[f][l], getattr(settled, f), err_msg=f"{where} env {l} carry {f}")
+        np.testing.assert_array_equal(probe["trained"][l] != 0, settled.trained, err_msg=f"{where} env {l} trained")
+        assert probe["next_order"][l] == settled.next_order, (where, l)
+    return probe
+
+
+@pytest.mark.parametrize("name,strategy,trained,steps", PROGRAM_GAMES)
+def test_act_matches_the_array_form_over_whole_games(name, strategy, trained, steps):
+    game = map_name_to_scenario(name, max_cycles=5000)
+    o = Oracle(game)
+    C = game.bucket.per_player_capacity
+    L = 2
+    st = batch_initial(game, L, np.stack([np.arange(L) + 11, np.arange(L) + 3], 1).astype(np.uint32))
+    carry = empty_carry(L, C)
+    shadow = empty_carry(L, C)  # player 0's carry, acted on but never executed
+    for t in range(steps):
+        actions = o.sample_actions(o.avail_rows(st), (17, 29), t)[:, 0]
+        _compare_act(game, o, st, carry, strategy, trained, 1, f"{name} t={t} seat")
+        shadow = _compare_act(game, o, st, shadow, strategy, trained, 0, f"{name} t={t} shadow")
+        o.seat_step(st, carry, strategy, trained, 0, actions, False, observe=False)
 
 
 # ---------------------------------------------------------------------------
