@@ -175,10 +175,77 @@ NR_DEV void wave_sync() {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// ---------------------------------------------------------------------------
+// teams: the lanes that own one game, the whole wave (TW = 64) or one half
+// of it (TW = 32, two games per wave).  Team-collective helpers act within
+// the caller's team and every lane of a calling team must be active; a
+// team-uniform value sits in a scalar register for a whole-wave team and in
+// a vector register (one value per half) for a half-wave team.  Team masks
+// are team-relative: bit i is team lane i.
+// ---------------------------------------------------------------------------
+template <int TW>
+NR_DEV int team_lane() {
+    return (int)(threadIdx.x & (TW - 1));
+}
+template <int TW>
+NR_DEV int team_half() {
+    if constexpr (TW == kWave) return 0;
+    else return (int)((threadIdx.x >> 5) & 1u);
+}
+template <int TW>
+NR_DEV uint64_t tballot(bool p) {
+    const uint64_t b = (uint64_t)__ballot(p);
+    if constexpr (TW == kWave) return b;
+    else return team_half<TW>() ? (b >> 32) : (b & 0xFFFFFFFFull);
+}
+template <int TW>
+NR_DEV int32_t tcount_below(uint64_t m) {
+    if constexpr (TW == kWave) return count_below(m);
+    else return __popc((uint32_t)m & ((1u << team_lane<TW>()) - 1u));
+}
+template <int TW>
+NR_DEV int32_t tuni(int32_t v) {
+    if constexpr (TW == kWave) return uni(v);
+    else return v;
+}
+// team lane j's v, for j the same on every lane of the wave (a loop counter
+// in a scalar register)
+template <int TW>
+NR_DEV int32_t tread_at(int32_t v, int32_t j) {
+    if constexpr (TW == kWave) {
+        return __builtin_amdgcn_readlane(v, j);
+    } else {
+        const int32_t lo = __builtin_amdgcn_readlane(v, j), hi = __builtin_amdgcn_readlane(v, j + 32);
+        return team_half<TW>() ? hi : lo;
+    }
+}
+// team lane j's v, for a team-uniform j
+template <int TW>
+NR_DEV int32_t tread(int32_t v, int32_t j) {
+    if constexpr (TW == kWave) return __builtin_amdgcn_readlane(v, j);
+    else return __shfl(v, j, TW);
+}
+// the larger of the active halves' team-uniform values (a scalar): the trip
+// count of a loop both teams of a wave run, each doing its own part.  A half
+// with no active lane (its game finished or stopped) counts 0: its
+// registers hold nothing meaningful.
+template <int TW>
+NR_DEV int32_t tmax(int32_t v) {
+    if constexpr (TW == kWave) {
+        return v;
+    } else {
+        const uint64_t active = (uint64_t)__ballot(1);
+        const int32_t lo = (active & 1ull) ? __builtin_amdgcn_readlane(v, 0) : 0;
+        const int32_t hi = ((active >> 32) & 1ull) ? __builtin_amdgcn_readlane(v, 32) : 0;
+        return lo > hi ? lo : hi;
+    }
+}
+
+template <int TW = kWave>
 NR_DEV int32_t wave_inclusive_min(int32_t v, int lane) {
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int32_t o = __shfl_up(v, (unsigned)d, kWave);
+    for (int d = 1; d < TW; d <<= 1) {
+        const int32_t o = __shfl_up(v, (unsigned)d, TW);
         if (lane >= d) v = v < o ? v : o;
     }
     return v;
@@ -283,9 +350,12 @@ NR_DEV Env env_view(const KGame& g, AS3 uint8_t* base) {
 // Rebuild the view from an opaque copy of the base so the per-lane
 // addresses derived from it are recomputed in each phase instead of staying
 // live (in registers) across the whole step.
+template <int TW = kWave>
 NR_DEV Env refresh(const KGame& g, const Env& e) {
     uint32_t b = (uint32_t)(uintptr_t)e.base;
-    asm volatile("" : "+s"(b));
+    // a half-wave team's block base differs between the halves
+    if constexpr (TW == kWave) asm volatile("" : "+s"(b));
+    else asm volatile("" : "+v"(b));
     return env_view(g, (AS3 uint8_t*)(uintptr_t)b);
 }
 
@@ -433,29 +503,31 @@ NR_DEV void load_header(const KGame& g, const Hdr& h) { load_header(g, h, g.terr
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+template <int TW = kWave>
 NR_DEV void copy_in(AS3 uint8_t* dst, const uint8_t* src, int32_t nbytes, int lane) {
     const uintptr_t a = (uintptr_t)src;
     if (((a | (uintptr_t)nbytes) & 15u) == 0) {
         const int32_t n = nbytes >> 4;
-        for (int32_t i = lane; i < n; i += kWave) ((AS3 u32x4*)dst)[i] = ((const u32x4*)src)[i];
+        for (int32_t i = lane; i < n; i += TW) ((AS3 u32x4*)dst)[i] = ((const u32x4*)src)[i];
     } else if (((a | (uintptr_t)nbytes) & 3u) == 0) {
         const int32_t n = nbytes >> 2;
-        for (int32_t i = lane; i < n; i += kWave) ((AS3 uint32_t*)dst)[i] = ((const uint32_t*)src)[i];
+        for (int32_t i = lane; i < n; i += TW) ((AS3 uint32_t*)dst)[i] = ((const uint32_t*)src)[i];
     } else {
-        for (int32_t i = lane; i < nbytes; i += kWave) dst[i] = src[i];
+        for (int32_t i = lane; i < nbytes; i += TW) dst[i] = src[i];
     }
 }
 
+template <int TW = kWave>
 NR_DEV void copy_out(uint8_t* dst, const AS3 uint8_t* src, int32_t nbytes, int lane) {
     const uintptr_t a = (uintptr_t)dst;
     if (((a | (uintptr_t)nbytes) & 15u) == 0) {
         const int32_t n = nbytes >> 4;
-        for (int32_t i = lane; i < n; i += kWave) ((u32x4*)dst)[i] = ((const AS3 u32x4*)src)[i];
+        for (int32_t i = lane; i < n; i += TW) ((u32x4*)dst)[i] = ((const AS3 u32x4*)src)[i];
     } else if (((a | (uintptr_t)nbytes) & 3u) == 0) {
         const int32_t n = nbytes >> 2;
-        for (int32_t i = lane; i < n; i += kWave) ((uint32_t*)dst)[i] = ((const AS3 uint32_t*)src)[i];
+        for (int32_t i = lane; i < n; i += TW) ((uint32_t*)dst)[i] = ((const AS3 uint32_t*)src)[i];
     } else {
-        for (int32_t i = lane; i < nbytes; i += kWave) dst[i] = src[i];
+        for (int32_t i = lane; i < nbytes; i += TW) dst[i] = src[i];
     }
 }
 
@@ -502,6 +574,7 @@ enum : uint32_t {
 // aligned: every requested leaf is loaded into registers before the first
 // LDS store, so the wave waits on memory once instead of once per leaf.
 // False (nothing done) when a leaf does not qualify.
+template <int TW = kWave>
 NR_DEV bool load_leaves_batched(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, uint32_t which,
                                 int lane) {
     const int64_t E = g.E, cells = g.cells;
@@ -510,7 +583,7 @@ NR_DEV bool load_leaves_batched(const KGame& g, const nanorts_state& s, int64_t 
     if (which & flag) {                                                                            \
         const int64_t bytes = count * (int64_t)sizeof(type);                                       \
         bad |= ((uint64_t)(uintptr_t)(s.field + l * count) | (uint64_t)bytes) & 15u;               \
-        if (bytes > 16 * kWave) bad |= 1u;                                                         \
+        if (bytes > 16 * TW) bad |= 1u;                                                         \
     }
     NR_LEAVES(NR_CHECK)
 #undef NR_CHECK
@@ -528,11 +601,12 @@ NR_DEV bool load_leaves_batched(const KGame& g, const nanorts_state& s, int64_t 
     return true;
 }
 
+template <int TW = kWave>
 NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, uint32_t which, int lane) {
     const int64_t E = g.E, cells = g.cells;
-    if (load_leaves_batched(g, s, l, e, which, lane)) which &= ~(uint32_t)(LD_SCALARS - 1u);
+    if (load_leaves_batched<TW>(g, s, l, e, which, lane)) which &= ~(uint32_t)(LD_SCALARS - 1u);
 #define NR_IN(flag, field, member, type) \
-    if (which & flag) copy_in((AS3 uint8_t*)e.member, (const uint8_t*)(s.field + l * E), (int32_t)(E * sizeof(type)), lane);
+    if (which & flag) copy_in<TW>((AS3 uint8_t*)e.member, (const uint8_t*)(s.field + l * E), (int32_t)(E * sizeof(type)), lane);
     NR_IN(LD_BIRTH, birth, birth, int32_t)
     NR_IN(LD_UTYPE, unit_type, utype, int8_t)
     NR_IN(LD_OWNER, owner, owner, int8_t)
@@ -549,7 +623,7 @@ NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const En
     NR_IN(LD_PORDER, pending_order, porder, int32_t)
 #undef NR_IN
     if (which & LD_ENTITY)
-        copy_in((AS3 uint8_t*)e.entity, (const uint8_t*)(s.entity_at + l * cells), (int32_t)(cells * 2), lane);
+        copy_in<TW>((AS3 uint8_t*)e.entity, (const uint8_t*)(s.entity_at + l * cells), (int32_t)(cells * 2), lane);
     if ((which & LD_SCALARS) && lane < S_COUNT) {
         int32_t v = 0;
         switch (lane) {
@@ -577,6 +651,7 @@ NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const En
 // store_env's counterpart of load_leaves_batched: every leaf is read from
 // LDS before the first global store.  False (nothing done) when a leaf does
 // not qualify.
+template <int TW = kWave>
 NR_DEV bool store_leaves_batched(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
     const int64_t E = g.E, cells = g.cells;
     uint64_t bad = 0u;
@@ -584,7 +659,7 @@ NR_DEV bool store_leaves_batched(const KGame& g, const nanorts_state& s, int64_t
     {                                                                                              \
         const int64_t bytes = count * (int64_t)sizeof(type);                                       \
         bad |= ((uint64_t)(uintptr_t)(s.field + l * count) | (uint64_t)bytes) & 15u;               \
-        if (bytes > 16 * kWave) bad |= 1u;                                                         \
+        if (bytes > 16 * TW) bad |= 1u;                                                         \
     }
     NR_LEAVES(NR_CHECK)
 #undef NR_CHECK
@@ -602,11 +677,12 @@ NR_DEV bool store_leaves_batched(const KGame& g, const nanorts_state& s, int64_t
     return true;
 }
 
+template <int TW = kWave>
 NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
     const int64_t E = g.E, cells = g.cells;
-    const bool batched = store_leaves_batched(g, s, l, e, lane);
+    const bool batched = store_leaves_batched<TW>(g, s, l, e, lane);
 #define NR_OUT(field, member, type) \
-    if (!batched) copy_out((uint8_t*)(s.field + l * E), (const AS3 uint8_t*)e.member, (int32_t)(E * sizeof(type)), lane);
+    if (!batched) copy_out<TW>((uint8_t*)(s.field + l * E), (const AS3 uint8_t*)e.member, (int32_t)(E * sizeof(type)), lane);
     NR_OUT(birth, birth, int32_t)
     NR_OUT(unit_type, utype, int8_t)
     NR_OUT(owner, owner, int8_t)
@@ -622,7 +698,7 @@ NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const E
     NR_OUT(pending_completes_at, pcompl, int32_t)
     NR_OUT(pending_order, porder, int32_t)
 #undef NR_OUT
-    if (!batched) copy_out((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
+    if (!batched) copy_out<TW>((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
     if (lane < S_COUNT) {
         const int32_t v = e.sc[lane];
         switch (lane) {
@@ -1102,9 +1178,28 @@ NR_DEV int32_t live_slot_at(const KGame& g, const Env& e, int32_t i) {
 struct LiveLanes {
     int32_t count, slot;
 };
+template <int TW = kWave>
 NR_DEV LiveLanes live_lanes(const KGame& g, const Env& e, int lane) {
-    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
     LiveLanes out = {0, 0};
+    if constexpr (TW != kWave) {
+        // a half-wave team: the bitmap read as 32-slot pieces, each piece's
+        // live slots sent to the lanes of their ranks within the team
+        AS3 const uint32_t* live = at<uint32_t>(e, g.lay.o_live);
+        const int32_t first = team_half<TW>() * TW;
+        for (int32_t w = 0; w * TW < g.E; ++w) {
+            const uint32_t m = live[w];
+            if (m == 0u) continue;
+            const int32_t base = out.count, c = __popc(m);
+            out.count += c;
+            if (out.count > TW) continue;
+            const int32_t rank = base + __popc(m & ((1u << lane) - 1u));
+            const int32_t to = ((m >> lane) & 1u) ? rank : (out.count & (TW - 1));
+            const int32_t got = __builtin_amdgcn_ds_permute((first + to) << 2, w * TW + lane);
+            if (lane >= base && lane < out.count) out.slot = got;
+        }
+        return out;
+    }
+    AS3 const uint64_t* live = at<uint64_t>(e, g.lay.o_live);
     for (int32_t w = 0; w * kWave < g.E; ++w) {
         const uint64_t v = live[w];
         const uint64_t m = (uint64_t)(uint32_t)uni((int32_t)(uint32_t)v) |
@@ -1170,6 +1265,7 @@ enum : int32_t { REC_HIT = 1, REC_DEATH = 2, REC_HARVEST = 4, REC_DEPLETED = 8, 
 // `rec` (NULL on every path but the step target's): where this member's
 // records go (each kind's records, N/core/kinds/*.py, and the death of the
 // unit its turn removes, N/core/completion.py:68-99).
+template <int TW = kWave>
 NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t slot, int32_t kind, int32_t dir,
                       int32_t target, int32_t ptype, int32_t owner, int32_t utype, int32_t rcell, int32_t rbirth,
                       int32_t rcarried, const StepRecords* rec = nullptr) {
@@ -1177,7 +1273,7 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
             r_sbirth = 0, r_scell = 0;
     const int32_t actor = clampi(utype, 0, g.T - 1);
     const int32_t player = clampi(owner, 0, 1);
-    const int32_t cur_birth = uni(e.birth[slot]);
+    const int32_t cur_birth = tuni<TW>(e.birth[slot]);
     const bool alive = cur_birth != kAbsent && cur_birth == rbirth;
     const int32_t dest = reserved_position(g, rcell, dir);
     bool removal = false;
@@ -1191,15 +1287,15 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
         }
     } else if (kind == kKindHarvest) {
         const Nb n = neighbour(g, h, e, rcell, dir);
-        const bool harvesting = uni(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_RESOURCE) ? 1 : 0) != 0;
+        const bool harvesting = tuni<TW>(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_RESOURCE) ? 1 : 0) != 0;
         if (harvesting) {
-            const int32_t stack = uni(n.slot);
+            const int32_t stack = tuni<TW>(n.slot);
             const int32_t amount = tabv(h, F_AMOUNT, actor);
-            const int32_t left = wsub(uni(e.carried[stack]), amount);
+            const int32_t left = wsub(tuni<TW>(e.carried[stack]), amount);
             if (rec) {
                 rf |= left <= 0 ? REC_HARVEST | REC_DEPLETED : REC_HARVEST;
                 r_target = stack;
-                r_tbirth = uni(e.birth[stack]);
+                r_tbirth = tuni<TW>(e.birth[stack]);
                 r_amount = amount;
             }
             if (lane == 0) {
@@ -1214,13 +1310,13 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
     } else if (kind == kKindReturn) {
         const Nb n = neighbour(g, h, e, rcell, dir);
         const bool returning =
-            uni(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_STOCKPILE) && rcarried > 0 ? 1 : 0) != 0;
+            tuni<TW>(n.occupied && (tabv(h, F_FLAGS, n.unit_type) & FL_STOCKPILE) && rcarried > 0 ? 1 : 0) != 0;
         if (returning && rec) {
             rf |= REC_RETURN;
-            r_target = uni(n.slot);
-            r_tbirth = uni(e.birth[gidx(uni(n.slot), g.E)]);
+            r_target = tuni<TW>(n.slot);
+            r_tbirth = tuni<TW>(e.birth[gidx(tuni<TW>(n.slot), g.E)]);
             r_amount = rcarried;
-            r_balance = wadd(uni(e.sc[S_RES0 + player]), rcarried);
+            r_balance = wadd(tuni<TW>(e.sc[S_RES0 + player]), rcarried);
         }
         if (returning && lane == 0) {
             if (alive) e.carried[slot] = 0;
@@ -1228,23 +1324,23 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
         }
     } else if (kind == kKindProduce) {
         const int32_t newborn_type = clampi(ptype, 0, g.T - 1);
-        const int32_t balance = wsub(uni(e.sc[S_RES0 + player]), tabv(h, F_COST, newborn_type));
+        const int32_t balance = wsub(tuni<TW>(e.sc[S_RES0 + player]), tabv(h, F_COST, newborn_type));
         if (balance >= 0) {
             // units.lowest_free_slot (N/core/units.py:12-18)
             const int32_t block = g.N + player * g.C;
             int32_t newborn = -1;
-            for (int32_t base = 0; base < g.C && newborn < 0; base += kWave) {
+            for (int32_t base = 0; base < g.C && newborn < 0; base += TW) {
                 const int32_t i = base + lane;
                 const bool free = i < g.C && e.birth[block + i] == kAbsent;
-                const uint64_t m = ballot(free);
+                const uint64_t m = tballot<TW>(free);
                 if (m != 0ull) newborn = block + base + (int32_t)__builtin_ctzll(m);
             }
-            newborn = uni(newborn);
+            newborn = tuni<TW>(newborn);
             if (rec && newborn >= 0) {
                 rf |= REC_SPAWN;
                 r_ptype = newborn_type;
                 r_spawn = newborn;
-                r_sbirth = uni(e.sc[S_NEXT_BIRTH]);
+                r_sbirth = tuni<TW>(e.sc[S_NEXT_BIRTH]);
                 r_scell = dest;
                 r_balance = balance;
             }
@@ -1268,14 +1364,14 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
             }
         }
     } else if (kind == kKindAttack) {
-        const int32_t occ = uni(e.entity[clampi(target, 0, g.cells - 1)]);
+        const int32_t occ = tuni<TW>(e.entity[clampi(target, 0, g.cells - 1)]);
         if (occ != kAbsent) {
             const int32_t victim = occ;
-            const int32_t left = wsub(uni(e.hp[gidx(victim, g.E)]), tabv(h, F_DAMAGE, actor));
+            const int32_t left = wsub(tuni<TW>(e.hp[gidx(victim, g.E)]), tabv(h, F_DAMAGE, actor));
             if (rec) {
                 rf |= REC_HIT;
                 r_target = victim;
-                r_tbirth = uni(e.birth[gidx(victim, g.E)]);
+                r_tbirth = tuni<TW>(e.birth[gidx(victim, g.E)]);
                 r_amount = tabv(h, F_DAMAGE, actor);
             }
             if (lane == 0) e.hp[victim] = (int16_t)left;
@@ -1334,19 +1430,22 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // `at_most_a_wave`: the caller guarantees at most 64 live slots, and the
 // path for more (member records in the phase union) is left out.  Returns
 // the new time.
+// A half-wave team (TW = 32) takes only the one-slot-per-lane path: its
+// caller guarantees at most 32 live slots.
+template <int TW = kWave>
 NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false,
                         const LiveLanes* known = nullptr, const StepRecords* records = nullptr) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
-    const int32_t time = wadd(uni(e.sc[S_TIME]), 1);
+    const int32_t time = wadd(tuni<TW>(e.sc[S_TIME]), 1);
     if (lane == 0) e.sc[S_TIME] = time;
     AS3 int32_t* rec = at<int32_t>(e, y.m_rec);  // [2C][6] in slot order
     // only live slots hold pending actions
     // the caller's copy when it holds one for this live set (a summary of
     // the state since which no unit spawned or died)
-    const LiveLanes ll = known ? *known : live_lanes(g, e, lane);
+    const LiveLanes ll = known ? *known : live_lanes<TW>(g, e, lane);
     const int32_t nlive = ll.count;
-    if (at_most_a_wave || nlive <= kWave) {
+    if (TW != kWave || at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in
         // their lanes and are ranked and read from there
         const int32_t s = lane < nlive ? ll.slot : 0;
@@ -1376,26 +1475,37 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             }
         }
         wave_sync();
-        const uint64_t members = ballot(acting);
+        const uint64_t members = tballot<TW>(acting);
         const int32_t n = popc(members);
         // members act in pending order (pending.batch_order :55-60), ties by slot
         int32_t rank = 0;
-        for (uint64_t m = members; m != 0ull; m &= m - 1ull) {
-            const int32_t j = (int32_t)__builtin_ctzll(m);
-            const int32_t oj = __builtin_amdgcn_readlane(ord, j);
-            rank += (oj < ord) || (oj == ord && j < lane);
+        if constexpr (TW == kWave) {
+            for (uint64_t m = members; m != 0ull; m &= m - 1ull) {
+                const int32_t j = (int32_t)__builtin_ctzll(m);
+                const int32_t oj = __builtin_amdgcn_readlane(ord, j);
+                rank += (oj < ord) || (oj == ord && j < lane);
+            }
+        } else {
+            // both halves' lanes in one scalar loop over the live lanes
+            const int32_t top = tmax<TW>(nlive);
+            for (int32_t j = 0; j < top; ++j) {
+                const int32_t oj = tread_at<TW>(ord, j);
+                rank += ((members >> j) & 1ull) && ((oj < ord) || (oj == ord && j < lane));
+            }
         }
-        for (int32_t k = 0; k < n; ++k) {
-            const int32_t li = (int32_t)__builtin_ctzll(ballot(acting && rank == k));
-            const int32_t a = __builtin_amdgcn_readlane(w0, li), b = __builtin_amdgcn_readlane(w1, li),
-                          c = __builtin_amdgcn_readlane(w2, li);
-            take_turn(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
-                      (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
-                      (int16_t)((c >> 8) & 0xFFFF), __builtin_amdgcn_readlane(rb, li),
-                      __builtin_amdgcn_readlane(rc, li), records);
+        const int32_t turns = tmax<TW>(n);
+        for (int32_t k = 0; k < turns; ++k) {
+            if (TW != kWave && k >= n) continue;
+            const int32_t li = (int32_t)__builtin_ctzll(tballot<TW>(acting && rank == k));
+            const int32_t a = tread<TW>(w0, li), b = tread<TW>(w1, li), c = tread<TW>(w2, li);
+            take_turn<TW>(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
+                          (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF),
+                          (int8_t)(c & 0xFF), (int16_t)((c >> 8) & 0xFFFF), tread<TW>(rb, li), tread<TW>(rc, li),
+                          records);
         }
         return time;
     }
+    if constexpr (TW != kWave) return time;
     int32_t n = 0;
     for (int32_t base = 0; base < nlive; base += kWave) {
         const int32_t i = base + lane;
@@ -1509,17 +1619,23 @@ NR_DEV void decide(const KGame& g, const Env& e_in, int lane) {
 
 // Active units per player, for decide_counted.
 // Also rebuilds the live-slot bitmap, which take_turn then keeps.
+template <int TW = kWave>
 NR_DEV void count_units(const KGame& g, const Env& e_in, int lane) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     AS3 uint64_t* live = at<uint64_t>(e, g.lay.o_live);
     int32_t count0 = 0, count1 = 0;
-    for (int32_t base = 0; base < g.E; base += kWave) {
+    // every word of the bitmap, the bits past E clear
+    for (int32_t base = 0; base < ((g.E + 63) & ~63); base += TW) {
         const int32_t s = base + lane;
         const bool alive = s < g.E && e.birth[s] != kAbsent;
-        const uint64_t m = ballot(alive);
-        if (lane == 0) live[base >> 6] = m;
-        count0 += popc(ballot(alive && s >= g.N && s < g.N + g.C));
-        count1 += popc(ballot(alive && s >= g.N + g.C));
+        const uint64_t m = tballot<TW>(alive);
+        if constexpr (TW == kWave) {
+            if (lane == 0) live[base >> 6] = m;
+        } else {
+            if (lane == 0) ((AS3 uint32_t*)live)[base >> 5] = (uint32_t)m;
+        }
+        count0 += popc(tballot<TW>(alive && s >= g.N && s < g.N + g.C));
+        count1 += popc(tballot<TW>(alive && s >= g.N + g.C));
     }
     if (lane == 0) {
         e.sc[S_UNITS0] = count0;
@@ -1538,13 +1654,14 @@ struct Outcome {
 // outcome.decide from the kept unit counts.  The balances and the
 // alternating count, final once completion has run, are read in the same
 // batch.
+template <int TW = kWave>
 NR_DEV Outcome decide_counted(const Env& e, int lane) {
     const int32_t u0 = e.sc[S_UNITS0], u1 = e.sc[S_UNITS1];
     Outcome o;
-    o.res0 = uni(e.sc[S_RES0]);
-    o.res1 = uni(e.sc[S_RES1]);
-    o.alt = uni(e.sc[S_ALT]);
-    const bool a0 = uni(u0) > 0, a1 = uni(u1) > 0;
+    o.res0 = tuni<TW>(e.sc[S_RES0]);
+    o.res1 = tuni<TW>(e.sc[S_RES1]);
+    o.alt = tuni<TW>(e.sc[S_ALT]);
+    const bool a0 = tuni<TW>(u0) > 0, a1 = tuni<TW>(u1) > 0;
     const int32_t count = (a0 ? 1 : 0) + (a1 ? 1 : 0);
     o.over = count <= 1 ? 1 : 0;
     o.winner = count == 1 ? (a0 ? 0 : 1) : kAbsent;
@@ -1568,15 +1685,17 @@ NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint
 // (N/core/__init__.py:30-32) and lifecycle.advance takes every leaf from it
 // (N/adapters/lifecycle.py:53-79).  The row leaves are copied through one
 // runtime-indexed loop over g.seg so no per-leaf address stays live.
+template <int TW = kWave>
 NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
-    const Env e = refresh(g, e_in);
-    const int32_t episode = uni(e.sc[S_EPISODE]);
+    const Env e = refresh<TW>(g, e_in);
+    const int32_t episode = tuni<TW>(e.sc[S_EPISODE]);
 #pragma nounroll
     for (int32_t k = 0; k < g.nseg; ++k) {
         const AS3 Seg* sg = h.seg + k;
+        // (the header is the workgroup's: wave-uniform for either team width)
         const uint8_t* src = (const uint8_t*)(((uint64_t)(uint32_t)uni((int32_t)(uint32_t)(uintptr_t)sg->src)) |
                                               ((uint64_t)(uint32_t)uni((int32_t)((uintptr_t)sg->src >> 32)) << 32));
-        copy_in(e.base + uni(sg->dst), src, uni(sg->bytes), lane);
+        copy_in<TW>(e.base + uni(sg->dst), src, uni(sg->bytes), lane);
     }
     if (lane < S_COUNT) {
         const nanorts_state& s = g.initial;
@@ -1599,8 +1718,8 @@ NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
         e.sc[lane] = v;
     }
     wave_sync();
-    count_units(g, e, lane);
-    decide_counted(e, lane);
+    count_units<TW>(g, e, lane);
+    decide_counted<TW>(e, lane);
 }
 
 // ---------------------------------------------------------------------------

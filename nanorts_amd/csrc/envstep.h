@@ -124,18 +124,19 @@ NR_DEV void no_request(Reqs& q) {
 // then does not matter (N/core/reservations.py:154-192).  With `listed`, the
 // summary of the state (rollout.h) already listed them and folded their
 // preconditions into `irregular`.  Lane i < nA receives entry i.
+template <int TW = kWave>
 NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, bool listed, int32_t* nA_out,
                           int32_t* posA, int32_t* costA, int32_t* playerA, int32_t listed_count = -1) {
     const Layout& y = g.lay;
-    const int32_t time = uni(e.sc[S_TIME]);
-    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    const int32_t time = tuni<TW>(e.sc[S_TIME]);
+    const int32_t next_order = tuni<TW>(e.sc[S_NEXT_ORDER]);
     if (next_order > 0x7fffffff - kWave) return false;
     AS3 int16_t* list = at<int16_t>(e, y.a_list);
     int32_t nA = 0;
     bool bad = false;
     // the summary's count, from the caller's registers when it holds it
-    if (listed) nA = listed_count >= 0 ? listed_count : uni(e.sc[S_NA]);
-    for (int32_t base = 0; base < (listed ? 0 : g.E); base += kWave) {
+    if (listed) nA = listed_count >= 0 ? listed_count : tuni<TW>(e.sc[S_NA]);
+    for (int32_t base = 0; base < (listed ? 0 : g.E); base += TW) {
         const int32_t s = base + lane;
         bool entry = false;
         if (s < g.E) {
@@ -149,11 +150,11 @@ NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, 
                 }
             }
         }
-        const uint64_t m = ballot(entry);
-        if (entry) list[nA + count_below(m)] = (int16_t)s;
+        const uint64_t m = tballot<TW>(entry);
+        if (entry) list[nA + tcount_below<TW>(m)] = (int16_t)s;
         nA += popc(m);
     }
-    if (ballot(bad) != 0ull || nA > kWave) return false;
+    if (tballot<TW>(bad) != 0ull || nA > TW) return false;
     wave_sync();
     *posA = 0;
     *costA = 0;
@@ -169,6 +170,7 @@ NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, 
     return true;
 }
 
+template <int TW = kWave>
 NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
                           int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q);
 // The requests of q (built from sampled, known-legal commands) staged in
@@ -209,66 +211,72 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
 }
 
 // Rank, conflict resolution and pending assignment of the requests in q.
+template <int TW>
 NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
                           int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q) {
     const Layout& y = g.lay;
-    const int32_t time = uni(e.sc[S_TIME]);
-    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    const int32_t time = tuni<TW>(e.sc[S_TIME]);
+    const int32_t next_order = tuni<TW>(e.sc[S_NEXT_ORDER]);
     const int32_t slot = q.slot, kind1 = q.kind1, none1 = q.none1, req = q.req, dir = q.dir, ptype = q.ptype;
     const int32_t target = q.target, pos1 = q.pos1, cost1 = q.cost1, player1 = q.player1, birth = q.birth, pl = q.pl;
     const bool conflicting = q.conflicting;
     // Java admission order (_ordered_requests :200-221): player, then the
     // request_order rank, then birth.  crank orders the requests that can
     // conflict among themselves.
-    const uint64_t conflicting_lanes = ballot(conflicting);
+    const uint64_t conflicting_lanes = tballot<TW>(conflicting);
     const int32_t orank = q.order_rank;
     int32_t rank = 0, crank = 0;
-    if (ballot(lane < n && (birth < 0 || birth >= (1 << 24) || orank != 0)) == 0ull) {
+    // (a half-wave team's loops run to the larger of the halves' counts:
+    // a lane j at or past its own team's count holds no request)
+    const int32_t nmax = tmax<TW>(n);
+    if (tballot<TW>(lane < n && (birth < 0 || birth >= (1 << 24) || orank != 0)) == 0ull) {
         // one 32-bit key per request: player, birth, lane
         const uint32_t key = lane < n ? ((uint32_t)pl << 31) | ((uint32_t)birth << 6) | (uint32_t)lane : 0xFFFFFFFFu;
-        for (int32_t j = 0; j < n; ++j) {
-            const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int32_t)key, j);
+        for (int32_t j = 0; j < nmax; ++j) {
+            const uint32_t kj = (uint32_t)tread_at<TW>((int32_t)key, j);
             const int32_t before = kj < key ? 1 : 0;
             rank += before;
             crank += ((conflicting_lanes >> j) & 1ull) ? before : 0;
         }
     } else {
-        for (int32_t j = 0; j < n; ++j) {
-            const int32_t plj = __builtin_amdgcn_readlane(pl, j);
-            const int32_t oj = __builtin_amdgcn_readlane(orank, j);
-            const int32_t bj = __builtin_amdgcn_readlane(birth, j);
-            const bool before = (plj < pl) ||
-                                (plj == pl && (oj < orank || (oj == orank && (bj < birth || (bj == birth && j < lane)))));
+        for (int32_t j = 0; j < nmax; ++j) {
+            const int32_t plj = tread_at<TW>(pl, j);
+            const int32_t oj = tread_at<TW>(orank, j);
+            const int32_t bj = tread_at<TW>(birth, j);
+            const bool before = j < n && ((plj < pl) ||
+                                          (plj == pl && (oj < orank || (oj == orank && (bj < birth || (bj == birth && j < lane))))));
             rank += before;
             crank += before && ((conflicting_lanes >> j) & 1ull);
         }
     }
     // Sequential conflict resolution over the requests that can conflict.
-    const int32_t bal0 = uni(e.sc[S_RES0]), bal1 = uni(e.sc[S_RES1]);
-    int32_t alt = uni(e.sc[S_ALT]);
+    const int32_t bal0 = tuni<TW>(e.sc[S_RES0]), bal1 = tuni<TW>(e.sc[S_RES1]);
+    int32_t alt = tuni<TW>(e.sc[S_ALT]);
     // each request's final kind and duration, held in its own lane
     int32_t my_kind = kind1, my_none = none1;
     int32_t posB = 0, costB = 0, playerB = 0, durB = 0, rlB = 0, nB = 0;
     bool liveB = false;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     const int32_t nconf = popc(conflicting_lanes);
-    for (int32_t k = 0; k < nconf; ++k) {
-        const int32_t li = (int32_t)__builtin_ctzll(ballot(conflicting && crank == k));
-        const int32_t rkind = __builtin_amdgcn_readlane(kind1, li);
-        const int32_t rnone = __builtin_amdgcn_readlane(none1, li);
-        const int32_t rreq = __builtin_amdgcn_readlane(req, li);
-        const int32_t rpos = __builtin_amdgcn_readlane(pos1, li);
-        const int32_t rcost = __builtin_amdgcn_readlane(cost1, li);
-        const int32_t rplayer = __builtin_amdgcn_readlane(player1, li);
+    const int32_t kmax = tmax<TW>(nconf);
+    for (int32_t k = 0; k < kmax; ++k) {
+        if (TW != kWave && k >= nconf) continue;
+        const int32_t li = (int32_t)__builtin_ctzll(tballot<TW>(conflicting && crank == k));
+        const int32_t rkind = tread<TW>(kind1, li);
+        const int32_t rnone = tread<TW>(none1, li);
+        const int32_t rreq = tread<TW>(req, li);
+        const int32_t rpos = tread<TW>(pos1, li);
+        const int32_t rcost = tread<TW>(cost1, li);
+        const int32_t rplayer = tread<TW>(player1, li);
         const bool rclaims = claims_position(rkind);
         const int32_t bal = rplayer ? bal1 : bal0;
         // _reservations_conflict (N/core/reservations.py:122-135)
         const int32_t clA = wadd(playerA == rplayer ? costA : 0, rcost);
         const bool cA = lane < nA && ((rclaims && posA == rpos) || (rcost != 0 && clA > 0 && clA > bal));
-        const bool anyA = ballot(cA) != 0ull;
+        const bool anyA = tballot<TW>(cA) != 0ull;
         const int32_t clB = wadd(playerB == rplayer ? costB : 0, rcost);
         const bool cB = liveB && ((rclaims && posB == rpos) || (rcost != 0 && clB > 0 && clB > bal));
-        const uint64_t sm = ballot(cB);
+        const uint64_t sm = tballot<TW>(cB);
         int32_t fkind = rkind, fnone = rnone;
         if (anyA || sm != 0ull) {
             const int32_t same_before = popc(sm & below);
@@ -281,7 +289,7 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
                 if (sm != 0ull) {
                     uint32_t ek0 = key0, ek1 = key1;
                     fold_in(ek0, ek1, (uint32_t)time);
-                    fold_in(ek0, ek1, (uint32_t)__builtin_amdgcn_readlane(birth, li));
+                    fold_in(ek0, ek1, (uint32_t)tread<TW>(birth, li));
                     fold_in(ek0, ek1, 0u);
                     if (cB) {
                         fold_in(ek0, ek1, (uint32_t)same_before);
@@ -291,19 +299,20 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
                 cancels_req = draw == 0;
                 cancels_pend = !cancels_req;
             }
-            const int32_t incl = wave_inclusive_min((cB && cancels_req) ? durB : kNoCap, lane);
-            const int32_t cap = __shfl(incl, kWave - 1, kWave);
-            int32_t excl = __shfl_up(incl, 1u, kWave);
+            const int32_t incl = wave_inclusive_min<TW>((cB && cancels_req) ? durB : kNoCap, lane);
+            const int32_t cap = __shfl(incl, TW - 1, TW);
+            int32_t excl = __shfl_up(incl, 1u, TW);
             if (lane == 0) excl = kNoCap;
             const int32_t before = anyA ? -1 : imin(rreq, excl);
             const bool cancelled = cB && cancels_pend;
             const int32_t settled = wadd(wmul(imin(durB, before), 2), 1) >> 1;
             // each cancelled same-cycle entry settles its request's lane
-            for (uint64_t m = ballot(cancelled); m != 0ull; m &= m - 1ull) {
+            for (uint64_t m = tballot<TW>(cancelled); m != 0ull; m &= m - 1ull) {
                 const int32_t b = (int32_t)__builtin_ctzll(m);
-                if (lane == __builtin_amdgcn_readlane(rlB, b)) {
+                const int32_t to = tread<TW>(rlB, b), settles = tread<TW>(settled, b);
+                if (lane == to) {
                     my_kind = kKindNone;
-                    my_none = __builtin_amdgcn_readlane(settled, b);
+                    my_none = settles;
                 }
             }
             if (cancelled) liveB = false;

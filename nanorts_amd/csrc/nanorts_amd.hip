@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -354,6 +355,42 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     }
     out->wpb = best_wpb;
     out->lds = y.hdr_bytes + best_wpb * y.env_bytes;
+    return true;
+}
+
+// The first pass with two games per wave (k_rollout_pair, half-wave
+// teams): shape_for_lean's block per game, `wpb` waves (2 * wpb games) per
+// workgroup, chosen for the most games per CU.  The choice among equal
+// counts falls to the larger workgroup.  Half-wave teams issue fewer
+// instructions per game-cycle but wait on LDS and scalar loads as often as
+// whole-wave teams do, with half as many waves per game in flight: they pay
+// only where at least three waves per SIMD fit (measured with the bench
+// workload's settings: 8x8 boards, 32 games per CU, +12 %; 16x16, 20 games
+// per CU, -8 %; 12x12, 16 games per CU, -16 %).  `any_occupancy` takes the
+// shape whatever it fits.
+constexpr int kPairMaxWaves = 4;
+constexpr int kPairMinGamesPerCu = 2 * 3 * 4;
+bool shape_for_pair(const nanorts_game* game, Shape* out, bool any_occupancy, std::string* why) {
+    if (!shape_for_lean(game, out, why)) return false;
+    const Layout& y = out->g.lay;
+    int best = 0, best_w = 0;
+    for (int w = 1; w <= kPairMaxWaves; ++w) {
+        const int32_t bytes = y.hdr_bytes + 2 * w * y.env_bytes;
+        if (bytes > lds_per_cu()) continue;
+        const int32_t by_lds = lds_per_cu() / lds_granule(bytes);
+        const int32_t by_waves = (4 * kLeanWavesPerSimd) / w;
+        const int games = (by_lds < by_waves ? by_lds : by_waves) * 2 * w;
+        if (games >= best) {
+            best = games;
+            best_w = w;
+        }
+    }
+    if (best == 0 || (!any_occupancy && best < kPairMinGamesPerCu)) {
+        *why = "two games per wave pay only with at least three waves per SIMD";
+        return false;
+    }
+    out->wpb = best_w;
+    out->lds = y.hdr_bytes + 2 * best_w * y.env_bytes;
     return true;
 }
 
@@ -964,12 +1001,15 @@ __global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_s
 // After core.step: outcome, rewards, optional final observation, auto-reset.
 // `known` / `known_time`: the cycle's outcome and time from decide_counted
 // and complete, when the caller holds them (else read from the env).
+// A half-wave team (TW = 32) writes rewards and done flags only (no event
+// counts, no final observation).
+template <int TW = kWave>
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
                         const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true,
                         const Outcome* known = nullptr, int32_t known_time = 0) {
-    const bool over = known ? known->over != 0 : uni(e.sc[S_GAME_OVER]) != 0;
-    const int32_t time = known ? known_time : uni(e.sc[S_TIME]);
-    const int32_t winner = known ? known->winner : uni(e.sc[S_WINNER]);
+    const bool over = known ? known->over != 0 : tuni<TW>(e.sc[S_GAME_OVER]) != 0;
+    const int32_t time = known ? known_time : tuni<TW>(e.sc[S_TIME]);
+    const int32_t winner = known ? known->winner : tuni<TW>(e.sc[S_WINNER]);
     const bool trunc = !over && time >= g.max_cycles;
     const bool done = over || trunc;
     if (lane == 0) {
@@ -985,28 +1025,30 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
             r.spawn_overflow[2 * l + 1] = e.sc[S_SO1];
         }
     }
-    if (events && r.reward_components && lane < 2) {
-        // N/adapters/rewards.py:47-71 (encode_components)
-        const AS3 int32_t* ev = at<int32_t>(e, g.lay.b_events);
-        const int p = lane, o = lane ^ 1;
-        const AS3 int32_t* prod = ev + 4 + p * 8;
-        float* out = r.reward_components + (2 * l + p) * 6;
-        out[0] = over ? (winner == p ? 1.0f : -1.0f) : 0.0f;
-        out[1] = (float)(ev[p] + ev[2 + p]);
-        out[2] = (float)prod[3];
-        out[3] = (float)(prod[1] + prod[2]);
-        out[4] = (float)(ev[20 + p * 3 + o + 1] - ev[20 + p * 3 + p + 1]);
-        out[5] = (float)(prod[4] + prod[5] + prod[6]);
+    if constexpr (TW == kWave) {  // the event counts and the final observation
+        if (events && r.reward_components && lane < 2) {
+            // N/adapters/rewards.py:47-71 (encode_components)
+            const AS3 int32_t* ev = at<int32_t>(e, g.lay.b_events);
+            const int p = lane, o = lane ^ 1;
+            const AS3 int32_t* prod = ev + 4 + p * 8;
+            float* out = r.reward_components + (2 * l + p) * 6;
+            out[0] = over ? (winner == p ? 1.0f : -1.0f) : 0.0f;
+            out[1] = (float)(ev[p] + ev[2 + p]);
+            out[2] = (float)prod[3];
+            out[3] = (float)(prod[1] + prod[2]);
+            out[4] = (float)(ev[20 + p * 3 + o + 1] - ev[20 + p * 3 + p + 1]);
+            out[5] = (float)(prod[4] + prod[5] + prod[6]);
+        }
+        if (fast_obs && (r.final_feature_maps || r.final_scalars)) {
+            const int64_t per = (int64_t)g.cells * 6;
+            uint8_t* m0 = r.final_feature_maps ? r.final_feature_maps + (l * 2) * per : nullptr;
+            int32_t* s0 = r.final_scalars ? r.final_scalars + l * 8 : nullptr;
+            summarize(g, h, e, lane, partial, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
+        } else if (r.final_feature_maps || r.final_scalars) {
+            observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
+        }
     }
-    if (fast_obs && (r.final_feature_maps || r.final_scalars)) {
-        const int64_t per = (int64_t)g.cells * 6;
-        uint8_t* m0 = r.final_feature_maps ? r.final_feature_maps + (l * 2) * per : nullptr;
-        int32_t* s0 = r.final_scalars ? r.final_scalars + l * 8 : nullptr;
-        summarize(g, h, e, lane, partial, m0, m0 ? m0 + per : nullptr, s0, s0 ? s0 + 4 : nullptr);
-    } else if (r.final_feature_maps || r.final_scalars) {
-        observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
-    }
-    if (done && reset) reset_env(g, h, e, lane);
+    if (done && reset) reset_env<TW>(g, h, e, lane);
     return done;
 }
 
@@ -1469,16 +1511,32 @@ NR_DEV Hdr header_view(const KGame& g) {
     h.walls = (AS3 uint32_t*)(lds + g.lay.o_walls);
     return h;
 }
-NR_DEV Env wave_env(const KGame& g, int wave) {
+// The env block of the workgroup's `team`-th game (its wave for whole-wave
+// teams, 2 * wave + half for half-wave teams).
+NR_DEV Env team_env(const KGame& g, int team) {
     extern __shared__ __align__(16) uint8_t nr_lds[];
-    return env_view(g, (AS3 uint8_t*)nr_lds + g.lay.hdr_bytes + wave * g.lay.env_bytes);
+    return env_view(g, (AS3 uint8_t*)nr_lds + g.lay.hdr_bytes + team * g.lay.env_bytes);
 }
 #define NR_ROLLOUT_PHASE                              \
     const RolloutArgs& a = fresh_rollout_args();      \
     const KGame& g = a.g;                             \
     const Hdr hdr = header_view(g);                   \
-    const Env e = wave_env(g, wave);                  \
+    const Env e = team_env(g, team);                  \
     (void)hdr;
+// The kernel prologue for teams of TW lanes: the header staged, this team's
+// game l and env block.
+#define NR_TEAM_PROLOGUE(TW)                                                            \
+    extern __shared__ __align__(16) uint8_t nr_lds[];                                   \
+    AS3 uint8_t* lds = (AS3 uint8_t*)nr_lds;                                            \
+    const Hdr hdr = header_view(g);                                                     \
+    load_header(g, hdr);                                                                \
+    __syncthreads();                                                                    \
+    const int lane = team_lane<TW>();                                                   \
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));           \
+    const int team = (kWave / TW) * wave + team_half<TW>();                             \
+    const int64_t l = (int64_t)blockIdx.x * ((blockDim.x >> 6) * (kWave / TW)) + team;  \
+    if (l >= lanes) return;                                                             \
+    const Env e = env_view(g, lds + g.lay.hdr_bytes + team * g.lay.env_bytes);
 
 // The cycles of one launch.  `Lean` is the first pass of the two-pass
 // launch (k_rollout_lean, on shape_for_lean's block): before each cycle it
@@ -1489,8 +1547,9 @@ NR_DEV Env wave_env(const KGame& g, int wave) {
 // on the full block) runs the rest.  Splitting a game's cycles between
 // launches this way gives the same result as one launch, as the state is
 // all a cycle carries.
-template <bool Lean>
+template <bool Lean, int TW = kWave>
 NR_DEV void rollout_cycles(const RolloutArgs& args) {
+    static_assert(TW == kWave || Lean, "half-wave teams run the first pass only");
     const KGame& g = args.g;
     const int64_t lanes = args.lanes;
     int32_t t_begin = 0;
@@ -1512,20 +1571,21 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         __syncthreads();
         if (any == 0u) return;
     }
-    NR_KERNEL_PROLOGUE
+    NR_TEAM_PROLOGUE(TW)
+    (void)lds;
     if (!Lean && args.resume) {
         t_begin = uni(args.out.progress[l]);
         if (t_begin >= args.steps) return;
     }
-    load_env(g, args.s, l, e, LD_ALL, lane);
-    count_units(g, e, lane);
+    load_env<TW>(g, args.s, l, e, LD_ALL, lane);
+    count_units<TW>(g, e, lane);
     // the first pass runs only where this holds (the host checks it)
     const bool fast = Lean || (g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0));
     // the summary's counts stay in registers from one cycle into the next
     SlotSummary sm = {0, 0, 0, 0, false};
-    if (fast) sm = summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
-    uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
-    fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+    if (fast) sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    uint32_t ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]), ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
+    fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
     const int32_t steps = args.steps;
     int32_t general = 0;  // cycles admitted request by request
     int32_t stop = steps;  // first pass: the first cycle left to the second
@@ -1550,7 +1610,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
-            if (Lean && (sm.irregular || sm.nav > kWave || sm.nlive > kWave)) {
+            if (Lean && (sm.irregular || sm.nav > TW || sm.nlive > TW)) {
                 stop = t;
                 break;
             }
@@ -1567,28 +1627,28 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             }
             // the pending entries of the admission, loaded early so their
             // latency overlaps the sampling
-            if (fused) listed = admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA, sm.nA);
+            if (fused) listed = admit_entries<TW>(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA, sm.nA);
             const uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
             const uint32_t env = (uint32_t)(a.env0 + l);
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
             // draw words: with n <= 32 the two threefry blocks of a position run
             // on two lanes at once; otherwise each lane computes both
-            const bool paired = n <= kWave / 2;
+            const bool paired = n <= TW / 2;
             const bool narrow = fast && g.seen_words == 1;
             // (no unit to sample: no balance read)
-            const Affordable aff = n > 0 ? affordable_types(g, hdr, e, lane) : Affordable{{0u, 0u}};
+            const Affordable aff = n > 0 ? affordable_types<TW>(g, hdr, e, lane) : Affordable{{0u, 0u}};
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired && n > 0) {
                 const int32_t u = lane >> 1;
                 uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
                 // every lane active: lane u takes lanes 2u and 2u + 1
-                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
-                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
-                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
-                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
+                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, TW);
+                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, TW);
+                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, TW);
+                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, TW);
             }
-            for (int32_t i = lane; i < n; i += kWave) {
+            for (int32_t i = lane; i < n; i += TW) {
                 const int32_t p = av[i];
                 uint32_t words[4];
                 if (paired) {
@@ -1643,7 +1703,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             }
             if (out.actions) {
                 // unavailable rows sample all zeros
-                for (int32_t p = lane; p < owned; p += kWave) {
+                for (int32_t p = lane; p < owned; p += TW) {
                     const int32_t sl = g.N + p;
                     if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
                     int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
@@ -1655,7 +1715,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             // env.step: core.step keyed by fold_in(env root, episode)
             if (Lean || (fused && listed)) {
                 // the first pass stopped before any cycle that is not both
-                admit_resolve(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
+                admit_resolve<TW>(g, hdr, e, lane, ek0, ek1, n, nA, posA, costA, playerA, q);
             } else if (fused || !admit_env(g, hdr, e, lane, ek0, ek1, false, n, irregular, true, fast)) {
                 // general admission; a fused cycle (which the summary's
                 // irregular flag keeps off this path) stages its requests first
@@ -1673,21 +1733,21 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             // the summary's live lanes: sampling and admission spawn and
             // remove nothing
             const LiveLanes known = {sm.nlive, sm.live_slot};
-            int32_t time = complete(g, hdr, e, lane, Lean, (fast && sm.nlive <= kWave) ? &known : nullptr);
-            Outcome oc = decide_counted(e, lane);
+            int32_t time = complete<TW>(g, hdr, e, lane, Lean, (fast && sm.nlive <= TW) ? &known : nullptr);
+            Outcome oc = decide_counted<TW>(e, lane);
             nanorts_env_results r = {};
             if (rew) r.reward = rew + (int64_t)t * lanes * 2;
             if (dn) r.done = dn + (int64_t)t * lanes;
-            const bool done = finish_step(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
+            const bool done = finish_step<TW>(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
             if (done) {
-                ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
-                ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
-                fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+                ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]);
+                ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
+                fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
                 // the published observation is the reset state's
-                time = uni(e.sc[S_TIME]);
-                oc.res0 = uni(e.sc[S_RES0]);
-                oc.res1 = uni(e.sc[S_RES1]);
-                oc.alt = uni(e.sc[S_ALT]);
+                time = tuni<TW>(e.sc[S_TIME]);
+                oc.res0 = tuni<TW>(e.sc[S_RES0]);
+                oc.res1 = tuni<TW>(e.sc[S_RES1]);
+                oc.alt = tuni<TW>(e.sc[S_ALT]);
             }
             const nanorts_rollout_results& out = a.out;
             const int64_t per = (int64_t)g.cells * 6;
@@ -1707,7 +1767,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                 // the sight bitmaps persist in the event counters' words, which
                 // the rollout does not count, when both planes fit there
                 const int32_t kept = 2 * g.H * g.seen_words <= 32 ? g.lay.b_events : -1;
-                sm = summarize(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
+                sm = summarize<TW>(g, hdr, e, lane, a.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
             } else if (out.feature_maps || out.scalars) {
                 observe_both(g, hdr, e, slot, lane, a.partial != 0, out.feature_maps, out.scalars);
             }
@@ -1715,7 +1775,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
     }
     {
         NR_ROLLOUT_PHASE
-        if (!Lean || stop > 0) store_env(g, a.s, l, e, lane);
+        if (!Lean || stop > 0) store_env<TW>(g, a.s, l, e, lane);
         if (lane == 0) {
             if (Lean) a.out.progress[l] = stop;
             else if (!a.resume && a.out.progress) a.out.progress[l] = 0;  // one pass on the full block
@@ -1734,6 +1794,15 @@ __global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) { rollout_cyc
 // cycle about 2.5 % faster at the same 16 games per CU.
 __global__ __launch_bounds__(kWave * kLeanMaxGames) void k_rollout_lean(RolloutArgs args) {
     rollout_cycles<true>(args);
+}
+
+// The first pass with two games per wave: each half of a wave (32 lanes)
+// runs one game's cycles, so the phases whose work is narrower than a wave
+// (sampling, admission, completion, the slot pass) serve two games per
+// instruction.  A game leaves for the second pass at the first cycle with
+// more than 32 available units or live slots.
+__global__ __launch_bounds__(kWave * kPairMaxWaves, 4) void k_rollout_pair(RolloutArgs args) {
+    rollout_cycles<true, 32>(args);
 }
 
 // Fused learner-vs-bot rollout: per cycle the learner's rows sampled from
@@ -3285,7 +3354,16 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
     const bool two_pass = results.progress != nullptr && sh.g.fast_obs &&
                           (((uintptr_t)results.feature_maps) & 7u) == 0 && shape_for_lean(game, &lean, &lean_why) &&
                           games_per_cu(lean.g.lay, lean.wpb, kLeanWavesPerSimd) >= games_per_cu(sh.g.lay, sh.wpb, 4);
-    const int64_t lean_blocks = two_pass ? (lanes + lean.wpb - 1) / lean.wpb : 0;
+    // the first pass with two games per wave where that pays; the
+    // environment variable NANORTS_AMD_FIRST_PASS set to "lean" or "pair"
+    // takes one game or two games per wave whatever the board
+    Shape pair;
+    const char* first_pass = std::getenv("NANORTS_AMD_FIRST_PASS");
+    const bool want_lean = first_pass && std::strcmp(first_pass, "lean") == 0;
+    const bool want_pair = first_pass && std::strcmp(first_pass, "pair") == 0;
+    const bool paired = two_pass && !want_lean && shape_for_pair(game, &pair, want_pair, &lean_why);
+    const int64_t games_per_block = paired ? 2 * pair.wpb : lean.wpb;
+    const int64_t lean_blocks = two_pass ? (lanes + games_per_block - 1) / games_per_block : 0;
     if (lean_blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
     // launches of at most kRolloutChunk cycles; the state stays in HBM
     // between them, so the result does not depend on the split
@@ -3307,7 +3385,13 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
             args.step_keys[2 * t] = k0;
             args.step_keys[2 * t + 1] = k1;
         }
-        if (two_pass) {
+        if (paired) {
+            args.g = pair.g;
+            hipLaunchKernelGGL(k_rollout_pair, dim3((unsigned)lean_blocks), dim3((unsigned)(kWave * pair.wpb)),
+                               (size_t)pair.lds, (hipStream_t)stream, args);
+            args.g = sh.g;
+            args.resume = 1;
+        } else if (two_pass) {
             args.g = lean.g;
             hipLaunchKernelGGL(k_rollout_lean, dim3((unsigned)lean_blocks), dim3((unsigned)(kWave * lean.wpb)),
                                (size_t)lean.lds, (hipStream_t)stream, args);

@@ -129,11 +129,12 @@ NR_DEV void sample_decode8(const KGame& g, const Env& e, int32_t p, const Row& r
 struct Affordable {
     uint32_t player[2];
 };
+template <int TW = kWave>
 NR_DEV Affordable affordable_types(const KGame& g, const Hdr& h, const Env& e, int lane) {
     const int32_t cost = lane < g.T ? tabv(h, F_COST, lane) : 0x7fffffff;
     Affordable a;
-    a.player[0] = (uint32_t)ballot(lane < g.T && uni(e.sc[S_RES0]) >= cost);
-    a.player[1] = (uint32_t)ballot(lane < g.T && uni(e.sc[S_RES1]) >= cost);
+    a.player[0] = (uint32_t)tballot<TW>(lane < g.T && tuni<TW>(e.sc[S_RES0]) >= cost);
+    a.player[1] = (uint32_t)tballot<TW>(lane < g.T && tuni<TW>(e.sc[S_RES1]) >= cost);
     return a;
 }
 
@@ -351,8 +352,9 @@ struct SlotSummary {
     int32_t live_slot;  // this lane's live slot (live_lanes), for at most a wave of them
 };
 
+template <int TW = kWave>
 NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
     const int32_t words = g.seen_words, plane = g.H * words;
     AS3 uint32_t* bm = at<uint32_t>(e, y.o_bm);
@@ -361,13 +363,13 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
         if ((plane & 3) == 0) {
             // 16 bytes a lane (both regions are 16-byte aligned)
             const int32_t n4 = (6 * plane) >> 2, w4 = plane >> 2;
-            for (int32_t i = lane; i < n4; i += kWave) {
+            for (int32_t i = lane; i < n4; i += TW) {
                 u32x4 v = {0u, 0u, 0u, 0u};
                 if (i < w4) v = ((AS3 const u32x4*)h.walls)[i];
                 ((AS3 u32x4*)bm)[i] = v;
             }
         } else {
-            for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = i < plane ? h.walls[i] : 0u;
+            for (int32_t i = lane; i < 6 * plane; i += TW) bm[i] = i < plane ? h.walls[i] : 0u;
         }
         wave_sync();
     }
@@ -376,16 +378,16 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     AS3 int16_t* av = at<int16_t>(e, y.a_av);
     AS3 int16_t* units = at<int16_t>(e, y.b_units);
     AS3 int16_t* entries = at<int16_t>(e, y.a_list);
-    const int32_t time = uni(e.sc[S_TIME]);
-    const int32_t next_order = uni(e.sc[S_NEXT_ORDER]);
+    const int32_t time = tuni<TW>(e.sc[S_TIME]);
+    const int32_t next_order = tuni<TW>(e.sc[S_NEXT_ORDER]);
     // only live slots hold units or pending actions
-    const LiveLanes ll = live_lanes(g, e, lane);
+    const LiveLanes ll = live_lanes<TW>(g, e, lane);
     const int32_t nlive = ll.count;
     int32_t nav = 0, nunits = 0, nA = 0;
     bool odd = false;
-    for (int32_t base = 0; base < nlive; base += kWave) {
+    for (int32_t base = 0; base < nlive; base += TW) {
         const int32_t i = base + lane;
-        const int32_t s = i < nlive ? (nlive <= kWave ? ll.slot : live_slot_at(g, e, i)) : 0;
+        const int32_t s = i < nlive ? (nlive <= TW ? ll.slot : live_slot_at(g, e, i)) : 0;
         bool alive = false, available = false, entry = false;
         if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
@@ -438,18 +440,18 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
             }
         }
         const bool unit = alive && s >= g.N;
-        const uint64_t me = ballot(entry);
-        if (entry && nA + count_below(me) < kWave) entries[nA + count_below(me)] = (int16_t)s;
+        const uint64_t me = tballot<TW>(entry);
+        if (entry && nA + tcount_below<TW>(me) < kWave) entries[nA + tcount_below<TW>(me)] = (int16_t)s;
         nA += popc(me);
-        const uint64_t ma = ballot(available);
-        if (available) av[nav + count_below(ma)] = (int16_t)(s - g.N);
+        const uint64_t ma = tballot<TW>(available);
+        if (available) av[nav + tcount_below<TW>(ma)] = (int16_t)(s - g.N);
         nav += popc(ma);
-        const uint64_t mu = ballot(unit);
-        if (unit) units[nunits + count_below(mu)] = (int16_t)s;
+        const uint64_t mu = tballot<TW>(unit);
+        if (unit) units[nunits + tcount_below<TW>(mu)] = (int16_t)s;
         nunits += popc(mu);
     }
     // irregular: the env-path admission does not apply (admit_env)
-    const bool irregular = ballot(odd) != 0ull || nA > kWave || next_order > 0x7fffffff - kWave;
+    const bool irregular = tballot<TW>(odd) != 0ull || nA > TW || next_order > 0x7fffffff - kWave;
     if (lane == 0) {
         // the empty cell's sentinel (index E) of the occupant arrays
         olo[g.E] = 0u;
@@ -461,9 +463,9 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     }
     wave_sync();
     SlotSummary out;
-    out.nav = uni(nav);
-    out.nunits = uni(nunits);
-    out.nA = uni(nA);
+    out.nav = tuni<TW>(nav);
+    out.nunits = tuni<TW>(nunits);
+    out.nA = tuni<TW>(nA);
     out.nlive = nlive;
     out.irregular = irregular;
     out.live_slot = ll.slot;
@@ -477,23 +479,24 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
 // atomics.  Taller boards stamp (unit, dy) rows with LDS atomics.
 // Sight bitmaps of the players whose bit is set in `which` (the others'
 // planes are left as they are).
+template <int TW = kWave>
 NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, int lane, int32_t seen_at,
                                  int32_t which, int32_t nunits) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
     AS3 uint32_t* seen = at<uint32_t>(e, seen_at);
     const int32_t words = g.seen_words, plane = g.H * words;
     AS3 const int16_t* units = at<int16_t>(e, y.b_units);
     const int32_t R = g.disk_r, span = 2 * R + 1;
     if (g.H <= 32 && words == 1) {
-        const int32_t U = kWave / g.H;
+        const int32_t U = TW / g.H;
         // lane / H by a 16-bit reciprocal (exact for lane < 64, H <= 32)
         const int32_t k = (int32_t)(((uint32_t)lane * ((65536u + (uint32_t)g.H - 1u) / (uint32_t)g.H)) >> 16);
         const int32_t row = lane - k * g.H;
         const uint32_t rowmask = g.W >= 32 ? 0xFFFFFFFFu : ((1u << g.W) - 1u);
         uint32_t acc0 = 0u, acc1 = 0u;
         // the listed units are player 0's, then player 1's
-        const int32_t n0 = uni(e.sc[S_UNITS0]);
+        const int32_t n0 = tuni<TW>(e.sc[S_UNITS0]);
         const int32_t first = (which & 1) ? 0 : n0, last = (which & 2) ? nunits : n0;
         for (int32_t base = first; base < last; base += U) {
             const int32_t i = base + k;
@@ -510,8 +513,8 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
             else acc0 |= bits;
         }
         for (int32_t j = 1; j < U; ++j) {
-            acc0 |= (uint32_t)__shfl((int)acc0, lane + j * g.H, kWave);
-            acc1 |= (uint32_t)__shfl((int)acc1, lane + j * g.H, kWave);
+            acc0 |= (uint32_t)__shfl((int)acc0, lane + j * g.H, TW);
+            acc1 |= (uint32_t)__shfl((int)acc1, lane + j * g.H, TW);
         }
         if (lane < g.H) {
             if (which & 1) seen[lane] = acc0;
@@ -520,9 +523,9 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
         wave_sync();
         return;
     }
-    for (int32_t i = lane; i < 2 * plane; i += kWave) seen[i] = 0u;
+    for (int32_t i = lane; i < 2 * plane; i += TW) seen[i] = 0u;
     wave_sync();
-    for (int32_t base = 0; base < nunits; base += kWave) {
+    for (int32_t base = 0; base < nunits; base += TW) {
         const int32_t i = base + lane;
         int32_t r = -1, cx = 0, cy = 0;
         AS3 uint32_t* mine = seen;
@@ -555,14 +558,15 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
 
 // Pass over the cells, four per lane (W % 4 == 0): bitmaps for the masks and
 // both agents' feature maps.  maps0/maps1 may be null (no observation).
+template <int TW = kWave>
 NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool partial, bool bitmaps,
                             uint8_t* maps0, uint8_t* maps1, int32_t seen_at) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
     const int32_t words = g.seen_words, plane = g.H * words;
     AS3 uint32_t* bm = at<uint32_t>(e, y.o_bm);
     if (bitmaps) {
-        for (int32_t i = lane; i < 6 * plane; i += kWave) bm[i] = 0u;
+        for (int32_t i = lane; i < 6 * plane; i += TW) bm[i] = 0u;
         wave_sync();
     }
     AS3 const uint32_t* olo = at<uint32_t>(e, y.o_lo);
@@ -575,7 +579,7 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
         x |= x >> 14;
         return x & 15u;
     };
-    for (int32_t base = 0; base < g.cells; base += 4 * kWave) {
+    for (int32_t base = 0; base < g.cells; base += 4 * TW) {
         const int32_t c0 = base + 4 * lane;
         if (c0 >= g.cells) continue;
         const uint64_t ent = *(AS3 const uint64_t*)(e.entity + c0);
@@ -642,16 +646,17 @@ NR_DEV void summarize_cells(const KGame& g, const Hdr& h, const Env& e_in, int l
 // `kept_seen` >= 0 is the LDS offset of sight bitmaps kept from the last
 // summary: they are stamped again only for a state whose units moved,
 // spawned or died since (S_VISDIRTY).
+template <int TW = kWave>
 NR_DEV SlotSummary summarize(const KGame& g, const Hdr& h, const Env& e, int lane, bool partial, uint8_t* maps0,
                              uint8_t* maps1, int32_t* scalars0, int32_t* scalars1, int32_t kept_seen = -1) {
-    const SlotSummary sm = summarize_slots(g, h, e, lane);
+    const SlotSummary sm = summarize_slots<TW>(g, h, e, lane);
     const int32_t seen_at = kept_seen >= 0 ? kept_seen : g.lay.v_seen;
-    const int32_t which = kept_seen >= 0 ? uni(e.sc[S_VISDIRTY]) & 3 : 3;
+    const int32_t which = kept_seen >= 0 ? tuni<TW>(e.sc[S_VISDIRTY]) & 3 : 3;
     if (partial && maps0 && which != 0) {
-        summarize_visibility(g, h, e, lane, seen_at, which, sm.nunits);
+        summarize_visibility<TW>(g, h, e, lane, seen_at, which, sm.nunits);
         if (kept_seen >= 0 && lane == 0) e.sc[S_VISDIRTY] = 0;
     }
-    if (maps0) summarize_cells(g, h, e, lane, partial, false, maps0, maps1, seen_at);
+    if (maps0) summarize_cells<TW>(g, h, e, lane, partial, false, maps0, maps1, seen_at);
     if (scalars0 && lane < 8) {
         const int32_t pl = lane >> 2, f = lane & 3;
         int32_t v;

@@ -124,13 +124,25 @@ def test_env_step_per_call(case, oracle_threads):
         assert ended > 0
 
 
+def _first_pass(monkeypatch, mode: str) -> None:
+    """Select the rollout's first pass: "auto" (the library's choice by
+    board), "lean" (one game per wave) or "pair" (two games per wave)."""
+    if mode == "auto":
+        monkeypatch.delenv("NANORTS_AMD_FIRST_PASS", raising=False)
+    else:
+        monkeypatch.setenv("NANORTS_AMD_FIRST_PASS", mode)
+
+
 @pytest.mark.parametrize("case", FAST_CASES + ["16x16-noprofile-random"])
 @pytest.mark.parametrize("recorded", [True, False])
-def test_fused_rollout_matches_oracle(case, recorded, oracle_threads):
+@pytest.mark.parametrize("first_pass", ["auto", "lean", "pair"])
+def test_fused_rollout_matches_oracle(case, recorded, first_pass, monkeypatch, oracle_threads):
     """The fused rollout kernel over a long horizon against the oracle's
     rollout: per-cycle rewards and dones, the recorded actions, last
-    observation and the final state.  Unrecorded, the kernel draws only the
-    factors its decode reads; the game must not change."""
+    observation and the final state, with each first pass.  Unrecorded, the
+    kernel draws only the factors its decode reads; the game must not
+    change."""
+    _first_pass(monkeypatch, first_pass)
     game, partial = game_for(case)
     L = 64
     steps = 1000
@@ -385,6 +397,46 @@ def test_two_pass_rollout_hands_games_to_the_second_pass(oracle_threads):
                                   got["general_admissions"].cpu().numpy())
     assert (single["first_pass_cycles"] is None)
     assert_states_equal(st, to_host(one), "one-pass rollout")
+
+
+@pytest.mark.parametrize("first_pass", ["auto", "pair"])
+def test_pair_first_pass_hands_games_to_the_second_pass(first_pass, monkeypatch, oracle_threads):
+    """With two games per wave (the choice on 8x8 boards) the first pass runs
+    a game while it has at most 32 live slots and 32 available units; the
+    second pass runs the rest.  Games that start with 26..40 live slots on
+    basesWorkers8x8, the added Workers all player 0's and 60 resources each,
+    cross the bound at cycle 0, part-way through the launch (spawns take a
+    game past 32 live slots), or not at all.  All of them match the oracle;
+    an odd number of games leaves the last wave's second half without a
+    game."""
+    from oracle.oracle import Oracle
+
+    _first_pass(monkeypatch, first_pass)
+    print("pair two-pass rollout", flush=True)
+    game, partial = game_for("8x8-original-both")
+    base = int((_packed(game, [0])["birth"][0] != -1).sum())
+    extra = [26 - base + k for k in range(15)]
+    st = _packed(game, extra, alternate=False)
+    st["player_resources"][:] = 60
+    live = (st["birth"] != -1).sum(1)
+    assert live.min() == 26 and live.max() == 40
+    oracle = Oracle(game)
+    assert (oracle.violations(st) == 0).all()
+    L, steps = len(extra), 96
+    env = _env(game, partial)
+    dev = to_device(env, st)
+    got = env.rollout(dev, steps, (6, 2), record=True, count_general=True)
+    first = got["first_pass_cycles"].cpu().numpy()
+    print("first-pass cycles per game:", first.tolist(), flush=True)
+    assert (first[live > 32] == 0).all()
+    assert ((first > 0) & (first < steps)).any()
+    assert (first == steps).any()
+    want = oracle.rollout(st, (6, 2), 0, steps, partial, threads=oracle_threads)
+    np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
+    np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
+    np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
+    assert_states_equal(st, to_host(dev), "pair two-pass rollout")
 
 
 def test_crowded_env_step_per_call(oracle_threads):
