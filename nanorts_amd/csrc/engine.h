@@ -133,6 +133,13 @@ struct KGame {
     Layout lay;
     int32_t nseg;
     Seg seg[16];
+    // Slot window (the fused rollout's first pass): with shift > 0 the env
+    // block stages slots [0, N + C) and [N + C + shift, N + 2C + shift) of
+    // the state, whose players hold C + shift slots each; C and E here are
+    // the window's.  The block's slot ls is the state's slot glob_slot(ls).
+    // 0 everywhere else.
+    int32_t shift;
+    int32_t quick_produce;  // some produce time is below 2 or above 2^30
 };
 
 // ---------------------------------------------------------------------------
@@ -155,6 +162,10 @@ NR_DEV int32_t gidx(int32_t i, int32_t n) { return clampi(i < 0 ? i + n : i, 0, 
 // floor_mod / floor_div of a cell index by the board width
 NR_DEV int32_t cell_x(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c & (g.W - 1)) : floor_mod(c, g.W); }
 NR_DEV int32_t cell_y(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c >> g.wshift) : floor_div(c, g.W); }
+// The state's slot and owned position of a block slot / position (the
+// identity without a slot window).
+NR_DEV int32_t glob_slot(const KGame& g, int32_t s) { return s < g.N + g.C ? s : s + g.shift; }
+NR_DEV int32_t glob_pos(const KGame& g, int32_t p) { return p < g.C ? p : p + g.shift; }
 NR_DEV int32_t dir_dx(int32_t d) { return d == 1 ? 1 : (d == 3 ? -1 : 0); }
 NR_DEV int32_t dir_dy(int32_t d) { return d == 0 ? -1 : (d == 2 ? 1 : 0); }
 
@@ -570,6 +581,53 @@ enum : uint32_t {
     X(LD_PORDER, pending_order, porder, int32_t, E)                    \
     X(LD_ENTITY, entity_at, entity, int16_t, cells)
 
+// The per-env scalars of row l into the block's scalar leaf (lanes below
+// S_COUNT, one scalar each).
+NR_DEV void load_scalars(const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    if (lane >= S_COUNT) return;
+    int32_t v = 0;
+    switch (lane) {
+        case S_TIME: v = s.time[l]; break;
+        case S_RES0: v = s.player_resources[2 * l]; break;
+        case S_RES1: v = s.player_resources[2 * l + 1]; break;
+        case S_NEXT_BIRTH: v = s.next_birth[l]; break;
+        case S_NEXT_ORDER: v = s.next_pending_order[l]; break;
+        case S_ALT: v = s.alternating_conflict_count[l]; break;
+        case S_GAME_OVER: v = s.game_over[l] ? 1 : 0; break;
+        case S_WINNER: v = s.winner[l]; break;
+        case S_SO0: v = s.spawn_overflow[2 * l]; break;
+        case S_SO1: v = s.spawn_overflow[2 * l + 1]; break;
+        case S_ROOT0: v = s.environment_root ? (int32_t)s.environment_root[2 * l] : 0; break;
+        case S_ROOT1: v = s.environment_root ? (int32_t)s.environment_root[2 * l + 1] : 0; break;
+        case S_EPISODE: v = s.episode_index ? (int32_t)s.episode_index[l] : 0; break;
+        case S_VISDIRTY: v = 3; break;
+        default: break;
+    }
+    e.sc[lane] = v;
+}
+
+// The block's scalars into row l of the state.
+NR_DEV void store_scalars(const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    if (lane >= S_COUNT) return;
+    const int32_t v = e.sc[lane];
+    switch (lane) {
+        case S_TIME: s.time[l] = v; break;
+        case S_RES0: s.player_resources[2 * l] = v; break;
+        case S_RES1: s.player_resources[2 * l + 1] = v; break;
+        case S_NEXT_BIRTH: s.next_birth[l] = v; break;
+        case S_NEXT_ORDER: s.next_pending_order[l] = v; break;
+        case S_ALT: s.alternating_conflict_count[l] = v; break;
+        case S_GAME_OVER: s.game_over[l] = v ? 1 : 0; break;
+        case S_WINNER: s.winner[l] = v; break;
+        case S_SO0: s.spawn_overflow[2 * l] = v; break;
+        case S_SO1: s.spawn_overflow[2 * l + 1] = v; break;
+        case S_EPISODE:
+            if (s.episode_index) s.episode_index[l] = (uint32_t)v;
+            break;
+        default: break;
+    }
+}
+
 // Leaves of at most 1024 bytes (one 16-byte vector per lane), 16-byte
 // aligned: every requested leaf is loaded into registers before the first
 // LDS store, so the wave waits on memory once instead of once per leaf.
@@ -624,27 +682,7 @@ NR_DEV void load_env(const KGame& g, const nanorts_state& s, int64_t l, const En
 #undef NR_IN
     if (which & LD_ENTITY)
         copy_in<TW>((AS3 uint8_t*)e.entity, (const uint8_t*)(s.entity_at + l * cells), (int32_t)(cells * 2), lane);
-    if ((which & LD_SCALARS) && lane < S_COUNT) {
-        int32_t v = 0;
-        switch (lane) {
-            case S_TIME: v = s.time[l]; break;
-            case S_RES0: v = s.player_resources[2 * l]; break;
-            case S_RES1: v = s.player_resources[2 * l + 1]; break;
-            case S_NEXT_BIRTH: v = s.next_birth[l]; break;
-            case S_NEXT_ORDER: v = s.next_pending_order[l]; break;
-            case S_ALT: v = s.alternating_conflict_count[l]; break;
-            case S_GAME_OVER: v = s.game_over[l] ? 1 : 0; break;
-            case S_WINNER: v = s.winner[l]; break;
-            case S_SO0: v = s.spawn_overflow[2 * l]; break;
-            case S_SO1: v = s.spawn_overflow[2 * l + 1]; break;
-            case S_ROOT0: v = s.environment_root ? (int32_t)s.environment_root[2 * l] : 0; break;
-            case S_ROOT1: v = s.environment_root ? (int32_t)s.environment_root[2 * l + 1] : 0; break;
-            case S_EPISODE: v = s.episode_index ? (int32_t)s.episode_index[l] : 0; break;
-            case S_VISDIRTY: v = 3; break;
-            default: break;
-        }
-        e.sc[lane] = v;
-    }
+    if (which & LD_SCALARS) load_scalars(s, l, e, lane);
     wave_sync();
 }
 
@@ -699,25 +737,112 @@ NR_DEV void store_env(const KGame& g, const nanorts_state& s, int64_t l, const E
     NR_OUT(pending_order, porder, int32_t)
 #undef NR_OUT
     if (!batched) copy_out<TW>((uint8_t*)(s.entity_at + l * cells), (const AS3 uint8_t*)e.entity, (int32_t)(cells * 2), lane);
-    if (lane < S_COUNT) {
-        const int32_t v = e.sc[lane];
-        switch (lane) {
-            case S_TIME: s.time[l] = v; break;
-            case S_RES0: s.player_resources[2 * l] = v; break;
-            case S_RES1: s.player_resources[2 * l + 1] = v; break;
-            case S_NEXT_BIRTH: s.next_birth[l] = v; break;
-            case S_NEXT_ORDER: s.next_pending_order[l] = v; break;
-            case S_ALT: s.alternating_conflict_count[l] = v; break;
-            case S_GAME_OVER: s.game_over[l] = v ? 1 : 0; break;
-            case S_WINNER: s.winner[l] = v; break;
-            case S_SO0: s.spawn_overflow[2 * l] = v; break;
-            case S_SO1: s.spawn_overflow[2 * l + 1] = v; break;
-            case S_EPISODE:
-                if (s.episode_index) s.episode_index[l] = (uint32_t)v;
-                break;
-            default: break;
-        }
+    store_scalars(s, l, e, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Slot-window copies (KGame::shift > 0): block slot i <-> state slot
+// glob_slot(i), and the occupancy grid's slot numbers mapped the same way.
+// A state row holds E + 2 shift slots.
+// ---------------------------------------------------------------------------
+// Row l of `s` into the block (l = 0 with the initial state).  False when
+// the game does not fit the window: a live slot in either gap, or an
+// occupancy entry other than -1 or a slot inside the window (the block is
+// then partly written and must not run).
+template <int TW = kWave>
+NR_DEV bool load_window_rows(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    const int32_t N = g.N, C = g.C, E = g.E, sh = g.shift;
+    const int64_t row = l * (int64_t)(E + 2 * sh);
+    bool bad = false;
+    for (int32_t i = lane; i < E; i += TW) {
+        // every leaf's load first, then the LDS stores
+        const int64_t at = row + glob_slot(g, i);
+        const int32_t birth = s.birth[at], carried = s.carried_resources[at], pnone = s.pending_none_duration[at];
+        const int32_t pissued = s.pending_issued_at[at], pcompl = s.pending_completes_at[at];
+        const int32_t porder = s.pending_order[at];
+        const int16_t cell = s.cell[at], hp = s.hit_points[at], ptarget = s.pending_target_cell[at];
+        const int8_t utype = s.unit_type[at], owner = s.owner[at], pkind = s.pending_kind[at];
+        const int8_t pdir = s.pending_direction[at], pptype = s.pending_produced_type[at];
+        e.birth[i] = birth;
+        e.carried[i] = carried;
+        e.pnone[i] = pnone;
+        e.pissued[i] = pissued;
+        e.pcompl[i] = pcompl;
+        e.porder[i] = porder;
+        e.cell[i] = cell;
+        e.hp[i] = hp;
+        e.ptarget[i] = ptarget;
+        e.utype[i] = utype;
+        e.owner[i] = owner;
+        e.pkind[i] = pkind;
+        e.pdir[i] = pdir;
+        e.pptype[i] = pptype;
     }
+    // the gaps [N + C, N + C + sh) and [E + sh, E + 2 sh) hold no live slot
+    for (int32_t i = lane; i < 2 * sh; i += TW) {
+        const int32_t gs = i < sh ? N + C + i : E + i;
+        if (s.birth[row + gs] != kAbsent) bad = true;
+    }
+    for (int32_t c = lane; c < g.cells; c += TW) {
+        const int32_t v = s.entity_at[l * (int64_t)g.cells + c];
+        int32_t lv = v;
+        if (v >= N + C + sh && v < E + sh) lv = v - sh;
+        else if (v < -1 || v >= N + C) bad = true;
+        e.entity[c] = (int16_t)lv;
+    }
+    return tballot<TW>(bad) == 0ull;
+}
+
+// Whether the initial state fits the window (load_window_rows' test alone).
+template <int TW = kWave>
+NR_DEV bool initial_fits_window(const KGame& g, int lane) {
+    const nanorts_state& s = g.initial;
+    const int32_t N = g.N, C = g.C, E = g.E, sh = g.shift;
+    bool bad = false;
+    for (int32_t i = lane; i < 2 * sh; i += TW) {
+        const int32_t gs = i < sh ? N + C + i : E + i;
+        if (s.birth[gs] != kAbsent) bad = true;
+    }
+    for (int32_t c = lane; c < g.cells; c += TW) {
+        const int32_t v = s.entity_at[c];
+        if (!(v >= N + C + sh && v < E + sh) && (v < -1 || v >= N + C)) bad = true;
+    }
+    return tballot<TW>(bad) == 0ull;
+}
+
+// The block into row l of the state: the window's slots and the occupancy
+// grid, its slot numbers mapped back.
+template <int TW = kWave>
+NR_DEV void store_window_rows(const KGame& g, const nanorts_state& s, int64_t l, const Env& e, int lane) {
+    const int32_t N = g.N, C = g.C, E = g.E, sh = g.shift;
+    const int64_t row = l * (int64_t)(E + 2 * sh);
+    for (int32_t i = lane; i < E; i += TW) {
+        const int32_t birth = e.birth[i], carried = e.carried[i], pnone = e.pnone[i], pissued = e.pissued[i];
+        const int32_t pcompl = e.pcompl[i], porder = e.porder[i];
+        const int16_t cell = e.cell[i], hp = e.hp[i], ptarget = e.ptarget[i];
+        const int8_t utype = e.utype[i], owner = e.owner[i], pkind = e.pkind[i], pdir = e.pdir[i];
+        const int8_t pptype = e.pptype[i];
+        const int64_t at = row + glob_slot(g, i);
+        s.birth[at] = birth;
+        s.carried_resources[at] = carried;
+        s.pending_none_duration[at] = pnone;
+        s.pending_issued_at[at] = pissued;
+        s.pending_completes_at[at] = pcompl;
+        s.pending_order[at] = porder;
+        s.cell[at] = cell;
+        s.hit_points[at] = hp;
+        s.pending_target_cell[at] = ptarget;
+        s.unit_type[at] = utype;
+        s.owner[at] = owner;
+        s.pending_kind[at] = pkind;
+        s.pending_direction[at] = pdir;
+        s.pending_produced_type[at] = pptype;
+    }
+    for (int32_t c = lane; c < g.cells; c += TW) {
+        const int32_t v = e.entity[c];
+        s.entity_at[l * (int64_t)g.cells + c] = (int16_t)(v >= N + C ? v + sh : v);
+    }
+    store_scalars(s, l, e, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1681,14 +1806,45 @@ NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint
     decide(g, e, lane);
 }
 
+// The initial State's scalars into the block, the episode counter advanced
+// (lanes below S_COUNT; the roots stay).
+NR_DEV void reset_scalars(const KGame& g, const Env& e, int lane, int32_t episode) {
+    if (lane >= S_COUNT) return;
+    const nanorts_state& s = g.initial;
+    int32_t v = e.sc[lane];
+    switch (lane) {
+        case S_TIME: v = s.time[0]; break;
+        case S_RES0: v = s.player_resources[0]; break;
+        case S_RES1: v = s.player_resources[1]; break;
+        case S_NEXT_BIRTH: v = s.next_birth[0]; break;
+        case S_NEXT_ORDER: v = s.next_pending_order[0]; break;
+        case S_ALT: v = s.alternating_conflict_count[0]; break;
+        case S_GAME_OVER: v = s.game_over[0] ? 1 : 0; break;
+        case S_WINNER: v = s.winner[0]; break;
+        case S_SO0: v = s.spawn_overflow[0]; break;
+        case S_SO1: v = s.spawn_overflow[1]; break;
+        case S_EPISODE: v = (int32_t)((uint32_t)episode + 1u); break;
+        case S_VISDIRTY: v = 3; break;
+        default: break;
+    }
+    e.sc[lane] = v;
+}
+
 // Copy the initial State into the staged env: core.reset ignores its key
 // (N/core/__init__.py:30-32) and lifecycle.advance takes every leaf from it
 // (N/adapters/lifecycle.py:53-79).  The row leaves are copied through one
 // runtime-indexed loop over g.seg so no per-leaf address stays live.
-template <int TW = kWave>
+// `Window`: the block may be a slot window's (KGame::shift > 0; the fused
+// rollout's first pass only).
+template <int TW = kWave, bool Window = false>
 NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
     const Env e = refresh<TW>(g, e_in);
     const int32_t episode = tuni<TW>(e.sc[S_EPISODE]);
+    // a slot window's block takes the initial rows through the window (the
+    // caller has checked that they fit it); its segment table is empty
+    if constexpr (Window) {
+        if (g.shift > 0) load_window_rows<TW>(g, g.initial, 0, e, lane);
+    }
 #pragma nounroll
     for (int32_t k = 0; k < g.nseg; ++k) {
         const AS3 Seg* sg = h.seg + k;
@@ -1697,30 +1853,12 @@ NR_DEV void reset_env(const KGame& g, const Hdr& h, const Env& e_in, int lane) {
                                               ((uint64_t)(uint32_t)uni((int32_t)((uintptr_t)sg->src >> 32)) << 32));
         copy_in<TW>(e.base + uni(sg->dst), src, uni(sg->bytes), lane);
     }
-    if (lane < S_COUNT) {
-        const nanorts_state& s = g.initial;
-        int32_t v = e.sc[lane];
-        switch (lane) {
-            case S_TIME: v = s.time[0]; break;
-            case S_RES0: v = s.player_resources[0]; break;
-            case S_RES1: v = s.player_resources[1]; break;
-            case S_NEXT_BIRTH: v = s.next_birth[0]; break;
-            case S_NEXT_ORDER: v = s.next_pending_order[0]; break;
-            case S_ALT: v = s.alternating_conflict_count[0]; break;
-            case S_GAME_OVER: v = s.game_over[0] ? 1 : 0; break;
-            case S_WINNER: v = s.winner[0]; break;
-            case S_SO0: v = s.spawn_overflow[0]; break;
-            case S_SO1: v = s.spawn_overflow[1]; break;
-            case S_EPISODE: v = (int32_t)((uint32_t)episode + 1u); break;
-            case S_VISDIRTY: v = 3; break;
-            default: break;
-        }
-        e.sc[lane] = v;
-    }
+    reset_scalars(g, e, lane, episode);
     wave_sync();
     count_units<TW>(g, e, lane);
     decide_counted<TW>(e, lane);
 }
+
 
 // ---------------------------------------------------------------------------
 // Legality (N/core/legality.py:32-64, kinds' _legality; row layout

@@ -144,6 +144,7 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
             if (game->produces[t * NANORTS_MAX_TYPES + u]) produces |= 1 << u;
         g.tab[F_PRODUCES * 8 + t] = produces;
         if (game->sight_radius[t] > g.sight_max) g.sight_max = game->sight_radius[t];
+        if (game->produce_time[t] < 2 || game->produce_time[t] > 0x3fffffff) g.quick_produce = 1;
         if (game->sight_radius[t] < 0 || game->sight_radius[t] > 64) {
             *why = "sight radius out of range";
             return false;
@@ -358,6 +359,24 @@ bool shape_for_lean(const nanorts_game* game, Shape* out, std::string* why) {
     return true;
 }
 
+// The first pass's slot window: with more than kSlotWindow slots per player,
+// the first pass stages slots [0, N + kSlotWindow) and the first
+// kSlotWindow of player 1's block only (KGame::shift).  Slots are taken
+// lowest-free-first, so a player's units sit at the bottom of its block; a
+// game holding a unit outside the window, or where a spawn could land
+// there, goes to the second pass.  On basesWorkers16x16 (70 slots a player)
+// that is 68 slots of 144: the block shrinks from 7.6 KB to about 4.6 KB.
+constexpr int32_t kSlotWindow = 32;
+nanorts_game windowed(const nanorts_game* game, int32_t* shift) {
+    nanorts_game w = *game;
+    *shift = 0;
+    if (game->capacity > kSlotWindow) {
+        *shift = game->capacity - kSlotWindow;
+        w.capacity = kSlotWindow;
+        w.entities = game->neutral + 2 * kSlotWindow;
+    }
+    return w;
+}
 // The first pass with two games per wave (k_rollout_pair, half-wave
 // teams): shape_for_lean's block per game, `wpb` waves (2 * wpb games) per
 // workgroup, chosen for the most games per CU.  The choice among equal
@@ -393,6 +412,19 @@ bool shape_for_pair(const nanorts_game* game, Shape* out, bool any_occupancy, st
     out->lds = y.hdr_bytes + 2 * best_w * y.env_bytes;
     return true;
 }
+
+// The first pass's shape on the slot window (windowed): one game per wave
+// (shape_for_lean) or two (shape_for_pair).  The reset segments are the
+// window's business (reset_env's windowed path), so the table stays empty.
+bool shape_for_first_pass(const nanorts_game* game, bool pair, bool any_occupancy, Shape* out, std::string* why) {
+    int32_t shift = 0;
+    const nanorts_game w = windowed(game, &shift);
+    if (!(pair ? shape_for_pair(&w, out, any_occupancy, why) : shape_for_lean(&w, out, why))) return false;
+    out->g.shift = shift;
+    if (shift > 0) out->g.nseg = 0;
+    return true;
+}
+
 
 // A smaller env block for the kernels that read a few leaves: `masks` holds
 // the leaves the legality rows read, the occupancy bitmaps and the staged
@@ -1003,7 +1035,7 @@ __global__ __launch_bounds__(256) void k_reset(KGame g, int64_t lanes, nanorts_s
 // and complete, when the caller holds them (else read from the env).
 // A half-wave team (TW = 32) writes rewards and done flags only (no event
 // counts, no final observation).
-template <int TW = kWave>
+template <int TW = kWave, bool Window = false>
 NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, int lane, bool partial,
                         const nanorts_env_results& r, bool events, bool fast_obs = false, bool reset = true,
                         const Outcome* known = nullptr, int32_t known_time = 0) {
@@ -1048,7 +1080,7 @@ NR_DEV bool finish_step(const KGame& g, const Hdr& h, const Env& e, int64_t l, i
             observe_both(g, h, e, l, lane, partial, r.final_feature_maps, r.final_scalars);
         }
     }
-    if (done && reset) reset_env<TW>(g, h, e, lane);
+    if (done && reset) reset_env<TW, Window>(g, h, e, lane);
     return done;
 }
 
@@ -1577,13 +1609,23 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         t_begin = uni(args.out.progress[l]);
         if (t_begin >= args.steps) return;
     }
-    load_env<TW>(g, args.s, l, e, LD_ALL, lane);
-    count_units<TW>(g, e, lane);
+    // with a slot window, a game that does not fit it (or whose initial
+    // state, which an auto-reset copies in, does not) runs no cycle here
+    bool fits = true;
+    if (Lean && g.shift > 0) {
+        fits = load_window_rows<TW>(g, args.s, l, e, lane) && initial_fits_window<TW>(g, lane);
+        load_scalars(args.s, l, e, lane);
+        wave_sync();
+    } else {
+        load_env<TW>(g, args.s, l, e, LD_ALL, lane);
+    }
+    if (fits) count_units<TW>(g, e, lane);
     // the first pass runs only where this holds (the host checks it)
     const bool fast = Lean || (g.fast_obs && ((((uintptr_t)args.out.feature_maps) & 7u) == 0));
     // the summary's counts stay in registers from one cycle into the next
     SlotSummary sm = {0, 0, 0, 0, false};
-    if (fast) sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    if (fast && fits) sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    if (!fits) sm.full = true;
     uint32_t ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]), ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
     fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
     const int32_t steps = args.steps;
@@ -1610,12 +1652,13 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
-            if (Lean && (sm.irregular || sm.nav > TW || sm.nlive > TW)) {
+            if (Lean && (sm.irregular || sm.full || sm.nav > TW || sm.nlive > TW)) {
                 stop = t;
                 break;
             }
             const nanorts_rollout_results& out = a.out;
-            const int32_t owned = 2 * g.C;
+            // the state's owned positions (a slot window's block holds fewer)
+            const int32_t owned = 2 * (g.C + g.shift);
             const int64_t tt = (int64_t)a.t0 + t;  // cycle index within the caller's rollout
             if (fast) {
                 n = sm.nav;
@@ -1640,7 +1683,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired && n > 0) {
                 const int32_t u = lane >> 1;
-                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
+                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)glob_pos(g, av[u]) : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
                 // every lane active: lane u takes lanes 2u and 2u + 1
                 pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, TW);
@@ -1657,7 +1700,8 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                     words[2] = pw2;
                     words[3] = pw3;
                 } else {
-                    uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
+                    const uint32_t pg = (uint32_t)glob_pos(g, p);
+                    uint32_t w0 = env, w1 = 2u * pg, w2 = env, w3 = 2u * pg + 1u;
                     threefry(ke0, ke1, w0, w1);
                     threefry(ke0, ke1, w2, w3);
                     words[0] = w0;
@@ -1682,7 +1726,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                         if (g.T <= 8) sample_row_words8(g, r, words, act);
                         else sample_row_words(g, r, words, act);
                         if (out.actions) {
-                            int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
+                            int32_t* dst = out.actions + ((tt * lanes + l) * owned + glob_pos(g, p)) * 7;
 #pragma unroll
                             for (int f = 0; f < 7; ++f) dst[f] = act[f];
                         }
@@ -1702,10 +1746,13 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
                 }
             }
             if (out.actions) {
-                // unavailable rows sample all zeros
+                // unavailable rows sample all zeros (a slot window's gaps
+                // hold no unit)
                 for (int32_t p = lane; p < owned; p += TW) {
-                    const int32_t sl = g.N + p;
-                    if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
+                    // each player's last `shift` positions lie past its window
+                    const bool gap = (p >= g.C && p < g.C + g.shift) || p >= 2 * g.C + g.shift;
+                    const int32_t sl = g.N + (p < g.C ? p : p - g.shift);
+                    if (!gap && e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
                     int32_t* dst = out.actions + ((tt * lanes + l) * owned + p) * 7;
 #pragma unroll
                     for (int f = 0; f < 7; ++f) dst[f] = 0;
@@ -1738,7 +1785,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             nanorts_env_results r = {};
             if (rew) r.reward = rew + (int64_t)t * lanes * 2;
             if (dn) r.done = dn + (int64_t)t * lanes;
-            const bool done = finish_step<TW>(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
+            const bool done = finish_step<TW, Lean>(g, hdr, e, l, lane, a.partial != 0, r, false, false, true, &oc, time);
             if (done) {
                 ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]);
                 ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
@@ -1775,7 +1822,10 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
     }
     {
         NR_ROLLOUT_PHASE
-        if (!Lean || stop > 0) store_env<TW>(g, a.s, l, e, lane);
+        if (!Lean || stop > 0) {
+            if (Lean && g.shift > 0) store_window_rows<TW>(g, a.s, l, e, lane);
+            else store_env<TW>(g, a.s, l, e, lane);
+        }
         if (lane == 0) {
             if (Lean) a.out.progress[l] = stop;
             else if (!a.resume && a.out.progress) a.out.progress[l] = 0;  // one pass on the full block
@@ -3352,7 +3402,8 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
     Shape lean;
     std::string lean_why;
     const bool two_pass = results.progress != nullptr && sh.g.fast_obs &&
-                          (((uintptr_t)results.feature_maps) & 7u) == 0 && shape_for_lean(game, &lean, &lean_why) &&
+                          (((uintptr_t)results.feature_maps) & 7u) == 0 &&
+                          shape_for_first_pass(game, false, false, &lean, &lean_why) &&
                           games_per_cu(lean.g.lay, lean.wpb, kLeanWavesPerSimd) >= games_per_cu(sh.g.lay, sh.wpb, 4);
     // the first pass with two games per wave where that pays; the
     // environment variable NANORTS_AMD_FIRST_PASS set to "lean" or "pair"
@@ -3361,7 +3412,7 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
     const char* first_pass = std::getenv("NANORTS_AMD_FIRST_PASS");
     const bool want_lean = first_pass && std::strcmp(first_pass, "lean") == 0;
     const bool want_pair = first_pass && std::strcmp(first_pass, "pair") == 0;
-    const bool paired = two_pass && !want_lean && shape_for_pair(game, &pair, want_pair, &lean_why);
+    const bool paired = two_pass && !want_lean && shape_for_first_pass(game, true, want_pair, &pair, &lean_why);
     const int64_t games_per_block = paired ? 2 * pair.wpb : lean.wpb;
     const int64_t lean_blocks = two_pass ? (lanes + games_per_block - 1) / games_per_block : 0;
     if (lean_blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");

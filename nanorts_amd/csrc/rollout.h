@@ -350,6 +350,12 @@ struct SlotSummary {
     int32_t nav, nunits, nA, nlive;
     bool irregular;
     int32_t live_slot;  // this lane's live slot (live_lanes), for at most a wave of them
+    // slot window (KGame::shift > 0): a unit spawned in the next cycle could
+    // land past a player's window (its units plus the units that may spawn
+    // one in that cycle exceed C: a pending PRODUCE due then, and, where a
+    // PRODUCE can complete in the cycle it is issued, every available unit
+    // that produces)
+    bool full;
 };
 
 template <int TW = kWave>
@@ -383,12 +389,15 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     // only live slots hold units or pending actions
     const LiveLanes ll = live_lanes<TW>(g, e, lane);
     const int32_t nlive = ll.count;
-    int32_t nav = 0, nunits = 0, nA = 0;
+    int32_t nav = 0, nunits = 0, nA = 0, reach0 = 0, reach1 = 0;
+    // a PRODUCE issued in a cycle can complete in it (a produce time below 2,
+    // or a completion time that wraps)
+    const bool quick = g.quick_produce || time > 0x3fffffff;
     bool odd = false;
     for (int32_t base = 0; base < nlive; base += TW) {
         const int32_t i = base + lane;
         const int32_t s = i < nlive ? (nlive <= TW ? ll.slot : live_slot_at(g, e, i)) : 0;
-        bool alive = false, available = false, entry = false;
+        bool alive = false, available = false, entry = false, grows = false;
         if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
             // pending from earlier cycles, in slot order (see admit_env)
@@ -402,6 +411,14 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
                 }
             }
             alive = e.birth[s] != kAbsent;
+            if (g.shift > 0 && alive && s >= g.N) {
+                // completion in the next cycle takes pending actions due by
+                // time + 1; spawning into the lowest free slot of a block of
+                // u units lands at most at index u
+                if (k == kKindProduce) grows = e.pcompl[s] <= wadd(time, 1);
+                else if (k == kAbsent && quick)
+                    grows = tabv(h, F_PRODUCES, clampi(e.utype[s], 0, g.T - 1)) != 0;
+            }
             if (alive) {
                 // occupant word: hp | carried << 8 | owner' << 16 | pending
                 // kind << 18 | (type + 1) << 24, owner' = 1 player 0, 2
@@ -449,6 +466,12 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
         const uint64_t mu = tballot<TW>(unit);
         if (unit) units[nunits + tcount_below<TW>(mu)] = (int16_t)s;
         nunits += popc(mu);
+        if (g.shift > 0) {
+            // each unit, and once more each that may spawn one this cycle
+            const bool p1 = s >= g.N + g.C;
+            reach0 += popc(tballot<TW>(unit && !p1)) + popc(tballot<TW>(grows && !p1));
+            reach1 += popc(tballot<TW>(unit && p1)) + popc(tballot<TW>(grows && p1));
+        }
     }
     // irregular: the env-path admission does not apply (admit_env)
     const bool irregular = tballot<TW>(odd) != 0ull || nA > TW || next_order > 0x7fffffff - kWave;
@@ -469,6 +492,7 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     out.nlive = nlive;
     out.irregular = irregular;
     out.live_slot = ll.slot;
+    out.full = reach0 > g.C || reach1 > g.C;
     return out;
 }
 

@@ -124,6 +124,18 @@ def test_env_step_per_call(case, oracle_threads):
         assert ended > 0
 
 
+def _poison_allocator(nbytes: int) -> None:
+    """Fill `nbytes` of device memory with a sentinel and free it, so that the
+    next allocations (torch's caching allocator reuses the block) start with
+    values no kernel writes: an output row a kernel leaves unwritten then
+    differs from the oracle's instead of reading as a lucky zero."""
+    import torch
+
+    junk = torch.full((nbytes // 4,), 0x4D4D4D4D, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    del junk
+
+
 def _first_pass(monkeypatch, mode: str) -> None:
     """Select the rollout's first pass: "auto" (the library's choice by
     board), "lean" (one game per wave) or "pair" (two games per wave)."""
@@ -149,6 +161,7 @@ def test_fused_rollout_matches_oracle(case, recorded, first_pass, monkeypatch, o
     oracle, st = advanced_states(game, L, 0, partial, oracle_threads, seed=21)
     env = _env(game, partial)
     dev = to_device(env, st)
+    _poison_allocator(steps * L * 2 * game.bucket.per_player_capacity * 7 * 4 + (64 << 20))
     got = env.rollout(dev, steps, (5, 9), record=True, record_actions=recorded)
     want = oracle.rollout(st, (5, 9), 0, steps, partial, threads=oracle_threads, record_actions=recorded)
     if recorded:
@@ -354,44 +367,50 @@ def _packed(game, extra: list[int], seed: int = 3, alternate: bool = True) -> di
     return st
 
 
-def test_two_pass_rollout_hands_games_to_the_second_pass(oracle_threads):
-    """The rollout's first pass runs a game on the smaller LDS block until a
-    cycle needs more than 64 live slots (or another path the block has no
-    room for); the second pass, on the full block, runs the rest of that
-    game's cycles.  Games that start with 57..72 live slots, the added
-    Workers all player 0's and 40 resources each, cross the bound at cycle 0,
-    part-way through the launch (spawns take a game past 64 live slots), or
-    not at all.  All of them match the oracle and the one-pass
-    launch."""
+@pytest.mark.parametrize("first_pass", ["lean", "pair"])
+def test_two_pass_rollout_hands_games_to_the_second_pass(first_pass, monkeypatch, oracle_threads):
+    """The rollout's first pass stages a 32-slot window of each player's 70
+    slots and runs a game until a unit could spawn past its window (its
+    units plus the PRODUCE actions due next cycle exceed 32), or a cycle
+    needs more than the first pass's lanes; the second pass, on the full
+    block, runs the rest of that game's cycles.  Games that start with
+    28..42 live slots, the added Workers all player 0's and 60 resources
+    each, cross the bound at cycle 0, part-way through the launch (spawns),
+    or not at all.  All of them match the oracle and the one-pass launch."""
     from oracle.oracle import Oracle
 
-    print("two-pass rollout", flush=True)
+    _first_pass(monkeypatch, first_pass)
+    print("two-pass rollout", first_pass, flush=True)
     game, partial = game_for("16x16-random-partial")
+    b = game.bucket
     base = int((_packed(game, [0])["birth"][0] != -1).sum())
-    extra = [57 - base + k for k in range(16)]
+    extra = [28 - base + k for k in range(15)]
     st = _packed(game, extra, alternate=False)
-    st["player_resources"][:] = 40
+    st["player_resources"][:] = 60
     live = (st["birth"] != -1).sum(1)
-    assert live.min() == 57 and live.max() == 72
+    assert live.min() == 28 and live.max() == 42
+    units0 = (st["birth"][:, b.neutral_capacity:b.neutral_capacity + b.per_player_capacity] != -1).sum(1)
     oracle = Oracle(game)
     assert (oracle.violations(st) == 0).all()
     L, steps = len(extra), 96
     env = _env(game, partial)
     dev = to_device(env, st)
     one = to_device(env, st)
-    got = env.rollout(dev, steps, (4, 1), record=True, count_general=True)
+    got = env.rollout(dev, steps, (4, 2), record=True, count_general=True)
     first = got["first_pass_cycles"].cpu().numpy()
     print("first-pass cycles per game:", first.tolist(), flush=True)
-    assert (first[live > 64] == 0).all()
+    assert (first[units0 > 32] == 0).all()
+    if first_pass == "pair":
+        assert (first[live > 32] == 0).all()
     assert ((first > 0) & (first < steps)).any()
     assert (first == steps).any()
-    want = oracle.rollout(st, (4, 1), 0, steps, partial, threads=oracle_threads)
+    want = oracle.rollout(st, (4, 2), 0, steps, partial, threads=oracle_threads)
     np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
     np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
     np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
     np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
     assert_states_equal(st, to_host(dev), "two-pass rollout")
-    single = env.rollout(one, steps, (4, 1), record=True, count_general=True, two_pass=False)
+    single = env.rollout(one, steps, (4, 2), record=True, count_general=True, two_pass=False)
     np.testing.assert_array_equal(single["rewards"].cpu().numpy(), want["rewards"])
     np.testing.assert_array_equal(single["general_admissions"].cpu().numpy(),
                                   got["general_admissions"].cpu().numpy())
