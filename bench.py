@@ -293,17 +293,29 @@ def _median(values: list[float]) -> float:
     return sorted(values)[len(values) // 2]
 
 
-# The headline rollout's launch: the first pass and the second pass that
-# follows it on the same stream (or the one pass on the full block).
-ROLLOUT_KERNELS = ("k_rollout_lean", "k_rollout")
+# The headline rollout's launch: a first pass (two games per wave, or one)
+# and the second pass that follows it on the same stream (or the one pass on
+# the full block).  The library picks the first pass by board.
+FIRST_PASS_KERNELS = ("k_rollout_pair", "k_rollout_lean")
+ROLLOUT_KERNELS = FIRST_PASS_KERNELS + ("k_rollout",)
+
+
+def first_pass_seen(rows: list[dict[str, float]]) -> str | None:
+    """The first-pass kernel that ran in profiled rows, if any."""
+    for name in FIRST_PASS_KERNELS:
+        if any(r.get("kernel") == name for r in rows):
+            return name
+    return None
 
 
 def per_launch(rows: list[dict[str, float]], counter: str, kernels) -> list[float]:
     """Counter sums per launch of a kernel sequence: a launch opens at each
-    dispatch of kernels[0] and takes the dispatches of the others that follow
-    it (each dispatch is its own launch when kernels[0] never ran)."""
+    dispatch of its first kernel (for the rollout, the first pass that ran)
+    and takes the dispatches of the last kernel that follow it (each
+    dispatch is its own launch when no opener ran)."""
     kernels = (kernels,) if isinstance(kernels, str) else tuple(kernels)
-    opener = kernels[0] if any(r.get("kernel") == kernels[0] for r in rows) else None
+    openers = [k for k in kernels[:-1] if any(r.get("kernel") == k for r in rows)]
+    opener = openers[0] if openers else None
     sums: list[float] = []
     for r in rows:
         if counter not in r:
@@ -327,7 +339,8 @@ def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel=ROLLO
         copy_bytes = 2 * (1 << 26) * 4  # read + write of the 256 MiB copy
         fetch_copy = [r["FETCH_SIZE"] for r in pmc_counters(args, "copy", "", "FETCH_SIZE", 1) if "FETCH_SIZE" in r]
         write_copy = [r["WRITE_SIZE"] for r in pmc_counters(args, "copy", "", "WRITE_SIZE", 1) if "WRITE_SIZE" in r]
-        fetch = per_launch(pmc_counters(args, mode, kernel, "FETCH_SIZE", per_launch_steps), "FETCH_SIZE", kernel)
+        fetch_rows = pmc_counters(args, mode, kernel, "FETCH_SIZE", per_launch_steps)
+        fetch = per_launch(fetch_rows, "FETCH_SIZE", kernel)
         write = per_launch(pmc_counters(args, mode, kernel, "WRITE_SIZE", per_launch_steps), "WRITE_SIZE", kernel)
         if last:
             fetch, write = fetch[-last:], write[-last:]
@@ -336,9 +349,13 @@ def pmc_traffic(args, per_launch_steps: int, mode: str = "rollout", kernel=ROLLO
         # a copy of B bytes fetches B/2 and writes B/2
         f_scale = (copy_bytes / 2) / (_median(fetch_copy) * 1024)
         w_scale = (copy_bytes / 2) / (_median(write_copy) * 1024)
-        return {"fetch_bytes": _median(fetch) * 1024 * f_scale, "write_bytes": _median(write) * 1024 * w_scale,
-                "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "dispatches": len(fetch),
-                "cycles_per_dispatch": per_launch_steps}
+        out = {"fetch_bytes": _median(fetch) * 1024 * f_scale, "write_bytes": _median(write) * 1024 * w_scale,
+               "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "dispatches": len(fetch),
+               "cycles_per_dispatch": per_launch_steps}
+        seen = first_pass_seen(fetch_rows)
+        if seen:
+            out["first_pass"] = seen
+        return out
     except Exception:
         return None
 
@@ -354,7 +371,7 @@ def pmc_limiter(args, per_launch_steps: int, last: int) -> dict | None:
                                         "SQ_ACTIVE_INST_VALU SQ_THREAD_CYCLES_VALU GRBM_GUI_ACTIVE", per_launch_steps)
                 if "SQ_ACTIVE_INST_VALU" in r and "GRBM_GUI_ACTIVE" in r]
         # the first pass is the launch's dominant kernel when it ran
-        main = ROLLOUT_KERNELS[0] if any(r["kernel"] == ROLLOUT_KERNELS[0] for r in rows) else ROLLOUT_KERNELS[1]
+        main = first_pass_seen(rows) or "k_rollout"
         rows = [r for r in rows if r["kernel"] == main][-last:]
         if not rows:
             return None
@@ -989,7 +1006,8 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
-            "kernel": "k_rollout_lean + k_rollout (second pass)" if LAST_TWO_PASS else "k_rollout",
+            "kernel": (f"{(traffic or {}).get('first_pass', 'k_rollout_pair or k_rollout_lean')} + k_rollout "
+                       "(second pass)") if LAST_TWO_PASS else "k_rollout",
             "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes,
             "cycles_per_launch": chunk,

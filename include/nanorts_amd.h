@@ -443,6 +443,13 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
                     int64_t env0,
                     nanorts_rollout_results results);
 
+/* Which first pass nanorts_amd_rollout runs for `game` when the caller asks
+ * for the two-pass launch (results.progress set, feature maps 8-byte
+ * aligned or absent): 2 two games per wave, 1 one game per wave, 0 none (one
+ * pass on the full block); < 0 an error code.  Diagnostics only: it has no
+ * counterpart in the reference, whose program has no such launch. */
+int nanorts_amd_rollout_first_pass(const nanorts_game* game);
+
 /* family.act of the rush strategies: WorkerRush (NANORTS_WORKER_RUSH) or the
  * barracks rush training `trained_type` (NANORTS_BARRACKS_RUSH; LightRush
  * trains type 4).  Writes commands int32[L][6][2][C] (kind, direction,

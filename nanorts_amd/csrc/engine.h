@@ -1302,13 +1302,16 @@ NR_DEV int32_t live_slot_at(const KGame& g, const Env& e, int32_t i) {
 // sent.  Every lane of the wave must be active.
 struct LiveLanes {
     int32_t count, slot;
+    int32_t slot2;  // half-wave teams: the (TW + lane)-th live slot, for counts up to 2 TW
 };
 template <int TW = kWave>
 NR_DEV LiveLanes live_lanes(const KGame& g, const Env& e, int lane) {
-    LiveLanes out = {0, 0};
+    LiveLanes out = {0, 0, 0};
     if constexpr (TW != kWave) {
         // a half-wave team: the bitmap read as 32-slot pieces, each piece's
-        // live slots sent to the lanes of their ranks within the team
+        // live slots sent to the lanes of their ranks modulo TW within the
+        // team (a piece's at most 32 ranks fall on distinct lanes); lane i
+        // keeps rank i in `slot` and rank TW + i in `slot2`
         AS3 const uint32_t* live = at<uint32_t>(e, g.lay.o_live);
         const int32_t first = team_half<TW>() * TW;
         for (int32_t w = 0; w * TW < g.E; ++w) {
@@ -1316,11 +1319,12 @@ NR_DEV LiveLanes live_lanes(const KGame& g, const Env& e, int lane) {
             if (m == 0u) continue;
             const int32_t base = out.count, c = __popc(m);
             out.count += c;
-            if (out.count > TW) continue;
+            if (out.count > 2 * TW) continue;
             const int32_t rank = base + __popc(m & ((1u << lane) - 1u));
-            const int32_t to = ((m >> lane) & 1u) ? rank : (out.count & (TW - 1));
-            const int32_t got = __builtin_amdgcn_ds_permute((first + to) << 2, w * TW + lane);
+            const int32_t to = ((m >> lane) & 1u) ? rank : out.count;
+            const int32_t got = __builtin_amdgcn_ds_permute((first + (to & (TW - 1))) << 2, w * TW + lane);
             if (lane >= base && lane < out.count) out.slot = got;
+            if (lane + TW >= base && lane + TW < out.count) out.slot2 = got;
         }
         return out;
     }
@@ -1555,11 +1559,15 @@ NR_DEV void take_turn(const KGame& g, const Hdr& h, const Env& e, int lane, int3
 // `at_most_a_wave`: the caller guarantees at most 64 live slots, and the
 // path for more (member records in the phase union) is left out.  Returns
 // the new time.
-// A half-wave team (TW = 32) takes only the one-slot-per-lane path: its
-// caller guarantees at most 32 live slots.
+// A half-wave team (TW = 32) takes the slot-per-lane paths only: one live
+// slot per lane, or two (complete_two_per_lane) for 33..64; its caller
+// guarantees at most 64 live slots.
+template <int TW>
+NR_DEV int32_t complete_two_per_lane(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t time,
+                                     const LiveLanes& ll, const StepRecords* records);
 template <int TW = kWave>
 NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool at_most_a_wave = false,
-                        const LiveLanes* known = nullptr, const StepRecords* records = nullptr) {
+                        LiveLanes known = LiveLanes{-1, 0}, const StepRecords* records = nullptr) {
     const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
     const int32_t time = wadd(tuni<TW>(e.sc[S_TIME]), 1);
@@ -1568,8 +1576,11 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
     // only live slots hold pending actions
     // the caller's copy when it holds one for this live set (a summary of
     // the state since which no unit spawned or died)
-    const LiveLanes ll = known ? *known : live_lanes<TW>(g, e, lane);
+    const LiveLanes ll = known.count >= 0 ? known : live_lanes<TW>(g, e, lane);
     const int32_t nlive = ll.count;
+    if constexpr (TW != kWave) {
+        if (nlive > TW) return complete_two_per_lane<TW>(g, h, e, lane, time, ll, records);
+    }
     if (TW != kWave || at_most_a_wave || nlive <= kWave) {
         // one live slot per lane: the members' retained actors stay in
         // their lanes and are ranked and read from there
@@ -1722,6 +1733,73 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
     return time;
 }
 
+// complete() for a half-wave team with TW < nlive <= 2 TW live slots: lane i
+// holds live slots i and TW + i (set 0 and set 1).  Same members, same
+// order (pending order, ties by slot = by live index) as the one-per-lane
+// path.
+template <int TW>
+NR_DEV int32_t complete_two_per_lane(const KGame& g, const Hdr& h, const Env& e, int lane, int32_t time,
+                                     const LiveLanes& ll, const StepRecords* records) {
+    bool acting[2] = {false, false};
+    int32_t w0[2] = {0, 0}, w1[2] = {0, 0}, w2[2] = {0, 0}, rb[2] = {0, 0}, rc[2] = {0, 0}, ord[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int32_t i = k * TW + lane;
+        if (i >= ll.count) continue;
+        const int32_t s = k ? ll.slot2 : ll.slot;
+        const int32_t kind = e.pkind[s];
+        if (kind == kAbsent || e.pcompl[s] > time) continue;
+        acting[k] = kind != kKindNone && s >= g.N;
+        if (acting[k]) {
+            w0[k] = (s & 0xFFFF) | ((kind & 0xFF) << 16) | ((e.pdir[s] & 0xFF) << 24);
+            w1[k] = (e.ptarget[s] & 0xFFFF) | ((e.pptype[s] & 0xFF) << 16) | ((e.owner[s] & 0xFF) << 24);
+            w2[k] = (e.utype[s] & 0xFF) | ((e.cell[s] & 0xFFFF) << 8);
+            rb[k] = e.birth[s];
+            rc[k] = e.carried[s];
+            ord[k] = e.porder[s];
+        }
+        e.pkind[s] = (int8_t)kAbsent;
+        e.pdir[s] = (int8_t)kAbsent;
+        e.pnone[s] = 0;
+        e.ptarget[s] = (int16_t)kAbsent;
+        e.pptype[s] = (int8_t)kAbsent;
+        e.pissued[s] = 0;
+        e.pcompl[s] = 0;
+        e.porder[s] = kAbsent;
+    }
+    wave_sync();
+    const uint64_t members0 = tballot<TW>(acting[0]), members1 = tballot<TW>(acting[1]);
+    const int32_t n = popc(members0) + popc(members1);
+    // rank by (pending order, live index); live index k * TW + lane
+    int32_t rank[2] = {0, 0};
+#pragma unroll
+    for (int kj = 0; kj < 2; ++kj) {
+        for (uint64_t m = kj ? members1 : members0; m != 0ull; m &= m - 1ull) {
+            const int32_t j = (int32_t)__builtin_ctzll(m);
+            const int32_t oj = tread<TW>(ord[kj], j), ij = kj * TW + j;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int32_t ik = k * TW + lane;
+                rank[k] += (oj < ord[k]) || (oj == ord[k] && ij < ik);
+            }
+        }
+    }
+    const int32_t turns = tmax<TW>(n);
+    for (int32_t t = 0; t < turns; ++t) {
+        if (t >= n) continue;
+        const uint64_t m0 = tballot<TW>(acting[0] && rank[0] == t);
+        const bool in1 = m0 == 0ull;
+        const int32_t li = (int32_t)__builtin_ctzll(in1 ? tballot<TW>(acting[1] && rank[1] == t) : m0);
+        const int32_t a = tread<TW>(in1 ? w0[1] : w0[0], li), b = tread<TW>(in1 ? w1[1] : w1[0], li),
+                      c = tread<TW>(in1 ? w2[1] : w2[0], li);
+        const int32_t birth = tread<TW>(in1 ? rb[1] : rb[0], li), carried = tread<TW>(in1 ? rc[1] : rc[0], li);
+        take_turn<TW>(g, h, e, lane, a & 0xFFFF, (int8_t)((a >> 16) & 0xFF), (int8_t)((a >> 24) & 0xFF),
+                      (int16_t)(b & 0xFFFF), (int8_t)((b >> 16) & 0xFF), (int8_t)((b >> 24) & 0xFF), (int8_t)(c & 0xFF),
+                      (int16_t)((c >> 8) & 0xFFFF), birth, carried, records);
+    }
+    return time;
+}
+
 // outcome.decide (N/core/outcome.py:11-25)
 NR_DEV void decide(const KGame& g, const Env& e_in, int lane) {
     const Env e = refresh(g, e_in);
@@ -1802,7 +1880,7 @@ NR_DEV Outcome decide_counted(const Env& e, int lane) {
 NR_DEV void core_step(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1,
                       bool count_events, const StepRecords* rec = nullptr) {
     admit(g, h, e, lane, key0, key1, count_events);
-    complete(g, h, e, lane, false, nullptr, rec);
+    complete(g, h, e, lane, false, LiveLanes{-1, 0}, rec);
     decide(g, e, lane);
 }
 

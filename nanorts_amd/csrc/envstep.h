@@ -124,9 +124,12 @@ NR_DEV void no_request(Reqs& q) {
 // then does not matter (N/core/reservations.py:154-192).  With `listed`, the
 // summary of the state (rollout.h) already listed them and folded their
 // preconditions into `irregular`.  Lane i < nA receives entry i.
+// A half-wave team (TW = 32) takes up to 64 entries: lane i receives entries
+// i and TW + i (the second into posA[1], costA[1], playerA[1]).
 template <int TW = kWave>
 NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, bool listed, int32_t* nA_out,
                           int32_t* posA, int32_t* costA, int32_t* playerA, int32_t listed_count = -1) {
+    constexpr int32_t kHeld = TW == kWave ? TW : 2 * TW;
     const Layout& y = g.lay;
     const int32_t time = tuni<TW>(e.sc[S_TIME]);
     const int32_t next_order = tuni<TW>(e.sc[S_NEXT_ORDER]);
@@ -154,17 +157,20 @@ NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, 
         if (entry) list[nA + tcount_below<TW>(m)] = (int16_t)s;
         nA += popc(m);
     }
-    if (tballot<TW>(bad) != 0ull || nA > TW) return false;
+    if (tballot<TW>(bad) != 0ull || nA > kHeld) return false;
     wave_sync();
-    *posA = 0;
-    *costA = 0;
-    *playerA = 0;
-    if (lane < nA) {
-        const int32_t s = list[lane];
-        const int32_t k = e.pkind[s];
-        *playerA = clampi(e.owner[s], 0, 1);
-        *costA = k == kKindProduce ? tabv(h, F_COST, clampi(e.pptype[s], 0, g.T - 1)) : 0;
-        *posA = reserved_position(g, e.cell[s], e.pdir[s]);
+#pragma unroll
+    for (int k = 0; k < kHeld / TW; ++k) {
+        posA[k] = 0;
+        costA[k] = 0;
+        playerA[k] = 0;
+        if (k * TW + lane < nA) {
+            const int32_t s = list[k * TW + lane];
+            const int32_t kind = e.pkind[s];
+            playerA[k] = clampi(e.owner[s], 0, 1);
+            costA[k] = kind == kKindProduce ? tabv(h, F_COST, clampi(e.pptype[s], 0, g.T - 1)) : 0;
+            posA[k] = reserved_position(g, e.cell[s], e.pdir[s]);
+        }
     }
     *nA_out = nA;
     return true;
@@ -172,7 +178,7 @@ NR_DEV bool admit_entries(const KGame& g, const Hdr& h, const Env& e, int lane, 
 
 template <int TW = kWave>
 NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
-                          int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q);
+                          int32_t nA, const int32_t* posA, const int32_t* costA, const int32_t* playerA, const Reqs& q);
 // The requests of q (built from sampled, known-legal commands) staged in
 // the command arrays for the general admission.
 NR_DEV void stage_requests(const KGame& g, const Env& e_in, int lane, int32_t n, const Reqs& q) {
@@ -196,8 +202,8 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
     const Env e = refresh(g, e_in);
     const Layout& y = g.lay;
     if (irregular || n > kWave) return false;
-    int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
-    if (!admit_entries(g, h, e, lane, listed, &nA, &posA, &costA, &playerA)) return false;
+    int32_t nA = 0, posA[1] = {0}, costA[1] = {0}, playerA[1] = {0};
+    if (!admit_entries(g, h, e, lane, listed, &nA, posA, costA, playerA)) return false;
     Reqs q;
     no_request(q);
     if (lane < n) {
@@ -211,9 +217,11 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
 }
 
 // Rank, conflict resolution and pending assignment of the requests in q.
+// posA / costA / playerA: this lane's entries, as admit_entries gives them
+// (two for a half-wave team).
 template <int TW>
 NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, uint32_t key0, uint32_t key1, int32_t n,
-                          int32_t nA, int32_t posA, int32_t costA, int32_t playerA, const Reqs& q) {
+                          int32_t nA, const int32_t* posA, const int32_t* costA, const int32_t* playerA, const Reqs& q) {
     const Layout& y = g.lay;
     const int32_t time = tuni<TW>(e.sc[S_TIME]);
     const int32_t next_order = tuni<TW>(e.sc[S_NEXT_ORDER]);
@@ -271,8 +279,13 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
         const bool rclaims = claims_position(rkind);
         const int32_t bal = rplayer ? bal1 : bal0;
         // _reservations_conflict (N/core/reservations.py:122-135)
-        const int32_t clA = wadd(playerA == rplayer ? costA : 0, rcost);
-        const bool cA = lane < nA && ((rclaims && posA == rpos) || (rcost != 0 && clA > 0 && clA > bal));
+        bool cA = false;
+#pragma unroll
+        for (int k = 0; k < (TW == kWave ? 1 : 2); ++k) {
+            const int32_t clA = wadd(playerA[k] == rplayer ? costA[k] : 0, rcost);
+            cA = cA || (k * TW + lane < nA &&
+                        ((rclaims && posA[k] == rpos) || (rcost != 0 && clA > 0 && clA > bal)));
+        }
         const bool anyA = tballot<TW>(cA) != 0ull;
         const int32_t clB = wadd(playerB == rplayer ? costB : 0, rcost);
         const bool cB = liveB && ((rclaims && posB == rpos) || (rcost != 0 && clB > 0 && clB > bal));

@@ -1101,8 +1101,8 @@ __global__ __launch_bounds__(256) void k_env_step(KGame g, int64_t lanes, nanort
         // request registers (no staging through the command arrays)
         summarize_slots(g, hdr, e, lane, false);
         const int32_t n = uni(e.sc[S_NAV]);
-        int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
-        fused = uni(e.sc[S_IRREG]) == 0 && n <= kWave && admit_entries(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA);
+        int32_t nA = 0, posA[1] = {0}, costA[1] = {0}, playerA[1] = {0};
+        fused = uni(e.sc[S_IRREG]) == 0 && n <= kWave && admit_entries(g, hdr, e, lane, true, &nA, posA, costA, playerA);
         if (fused) {
             if (events) {
                 if (lane < 32) at<int32_t>(e, g.lay.b_events)[lane] = 0;
@@ -1648,11 +1648,13 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
         bool fused = false, listed = false;
         Reqs q;
         no_request(q);
-        int32_t nA = 0, posA = 0, costA = 0, playerA = 0;
+        // this lane's pending entries (two a lane for a half-wave team)
+        int32_t nA = 0, posA[2] = {0, 0}, costA[2] = {0, 0}, playerA[2] = {0, 0};
         {
             // masks -> sample -> decode (get_avail_actions + harness + decode_actions)
             NR_ROLLOUT_PHASE
-            if (Lean && (sm.irregular || sm.full || sm.nav > TW || sm.nlive > TW)) {
+            // (a half-wave team holds up to two live slots per lane)
+            if (Lean && (sm.irregular || sm.full || sm.nav > TW || sm.nlive > (TW == kWave ? kWave : 2 * TW))) {
                 stop = t;
                 break;
             }
@@ -1670,7 +1672,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             }
             // the pending entries of the admission, loaded early so their
             // latency overlaps the sampling
-            if (fused) listed = admit_entries<TW>(g, hdr, e, lane, true, &nA, &posA, &costA, &playerA, sm.nA);
+            if (fused) listed = admit_entries<TW>(g, hdr, e, lane, true, &nA, posA, costA, playerA, sm.nA);
             const uint32_t ke0 = a.step_keys[2 * t], ke1 = a.step_keys[2 * t + 1];
             const uint32_t env = (uint32_t)(a.env0 + l);
             AS3 const int16_t* av = at<int16_t>(e, g.lay.a_av);
@@ -1779,8 +1781,9 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             NR_ROLLOUT_PHASE
             // the summary's live lanes: sampling and admission spawn and
             // remove nothing
-            const LiveLanes known = {sm.nlive, sm.live_slot};
-            int32_t time = complete<TW>(g, hdr, e, lane, Lean, (fast && sm.nlive <= TW) ? &known : nullptr);
+            const LiveLanes known = {sm.nlive, sm.live_slot, sm.live_slot2};
+            const int32_t held = TW == kWave ? kWave : 2 * TW;  // live slots the lanes hold
+            int32_t time = complete<TW>(g, hdr, e, lane, Lean, (fast && sm.nlive <= held) ? known : LiveLanes{-1, 0, 0});
             Outcome oc = decide_counted<TW>(e, lane);
             nanorts_env_results r = {};
             if (rew) r.reward = rew + (int64_t)t * lanes * 2;
@@ -2028,7 +2031,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             // the summary's live lanes: the bot, sampling and admission spawn
             // and remove nothing
             const LiveLanes known = {sm.nlive, sm.live_slot};
-            time = complete(g, hdr, e, lane, false, sm.nlive <= kWave ? &known : nullptr);
+            time = complete(g, hdr, e, lane, false, sm.nlive <= kWave ? known : LiveLanes{-1, 0, 0});
             oc = decide_counted(e, lane);
         } else {
             core_step(g, hdr, e, lane, ek0, ek1, false);
@@ -3381,6 +3384,28 @@ int nanorts_amd_gridnet_sample_actions(void* stream, const nanorts_game* game, i
                   actions);
 }
 
+// The rollout's first pass for a two-pass launch: 2 two games per wave
+// (`pair` shaped), 1 one game per wave (`lean`), 0 none.  Two games per wave
+// where that pays (shape_for_pair); the environment variable
+// NANORTS_AMD_FIRST_PASS set to "lean" or "pair" takes one game or two games
+// per wave whatever the board.
+static int choose_first_pass(const nanorts_game* game, const Shape& full, Shape* lean, Shape* pair) {
+    std::string why;
+    if (!full.g.fast_obs || !shape_for_first_pass(game, false, false, lean, &why) ||
+        games_per_cu(lean->g.lay, lean->wpb, kLeanWavesPerSimd) < games_per_cu(full.g.lay, full.wpb, 4))
+        return 0;
+    const char* mode = std::getenv("NANORTS_AMD_FIRST_PASS");
+    const bool want_lean = mode && std::strcmp(mode, "lean") == 0;
+    const bool want_pair = mode && std::strcmp(mode, "pair") == 0;
+    return !want_lean && shape_for_first_pass(game, true, want_pair, pair, &why) ? 2 : 1;
+}
+
+int nanorts_amd_rollout_first_pass(const nanorts_game* game) {
+    NR_SHAPE(game)
+    Shape lean, pair;
+    return choose_first_pass(game, sh, &lean, &pair);
+}
+
 int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes,
                     const uint32_t* sample_key, int32_t step0, int32_t steps, int32_t partial, int64_t env0,
                     nanorts_rollout_results results) {
@@ -3399,20 +3424,11 @@ int nanorts_amd_rollout(void* stream, const nanorts_game* game, nanorts_state st
     // Two passes when the caller gives the work words, the packed
     // observation applies and the first pass's block holds at least as many
     // games per CU as the full block.
-    Shape lean;
-    std::string lean_why;
-    const bool two_pass = results.progress != nullptr && sh.g.fast_obs &&
-                          (((uintptr_t)results.feature_maps) & 7u) == 0 &&
-                          shape_for_first_pass(game, false, false, &lean, &lean_why) &&
-                          games_per_cu(lean.g.lay, lean.wpb, kLeanWavesPerSimd) >= games_per_cu(sh.g.lay, sh.wpb, 4);
-    // the first pass with two games per wave where that pays; the
-    // environment variable NANORTS_AMD_FIRST_PASS set to "lean" or "pair"
-    // takes one game or two games per wave whatever the board
-    Shape pair;
-    const char* first_pass = std::getenv("NANORTS_AMD_FIRST_PASS");
-    const bool want_lean = first_pass && std::strcmp(first_pass, "lean") == 0;
-    const bool want_pair = first_pass && std::strcmp(first_pass, "pair") == 0;
-    const bool paired = two_pass && !want_lean && shape_for_first_pass(game, true, want_pair, &pair, &lean_why);
+    Shape lean, pair;
+    const int first = results.progress != nullptr && (((uintptr_t)results.feature_maps) & 7u) == 0
+                          ? choose_first_pass(game, sh, &lean, &pair)
+                          : 0;
+    const bool two_pass = first > 0, paired = first == 2;
     const int64_t games_per_block = paired ? 2 * pair.wpb : lean.wpb;
     const int64_t lean_blocks = two_pass ? (lanes + games_per_block - 1) / games_per_block : 0;
     if (lean_blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");

@@ -350,6 +350,7 @@ struct SlotSummary {
     int32_t nav, nunits, nA, nlive;
     bool irregular;
     int32_t live_slot;  // this lane's live slot (live_lanes), for at most a wave of them
+    int32_t live_slot2;  // half-wave teams: its second (live_lanes), for at most two halves of them
     // slot window (KGame::shift > 0): a unit spawned in the next cycle could
     // land past a player's window (its units plus the units that may spawn
     // one in that cycle exceed C: a pending PRODUCE due then, and, where a
@@ -396,7 +397,11 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     bool odd = false;
     for (int32_t base = 0; base < nlive; base += TW) {
         const int32_t i = base + lane;
-        const int32_t s = i < nlive ? (nlive <= TW ? ll.slot : live_slot_at(g, e, i)) : 0;
+        // (a half-wave team takes up to two live slots a lane from live_lanes)
+        const int32_t s = i < nlive ? (nlive <= TW ? ll.slot
+                                                   : (TW != kWave && nlive <= 2 * TW ? (base == 0 ? ll.slot : ll.slot2)
+                                                                                     : live_slot_at(g, e, i)))
+                                    : 0;
         bool alive = false, available = false, entry = false, grows = false;
         if (i < nlive) {
             // pending entries for the env-path admission: MOVE / PRODUCE
@@ -474,7 +479,9 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
         }
     }
     // irregular: the env-path admission does not apply (admit_env)
-    const bool irregular = tballot<TW>(odd) != 0ull || nA > TW || next_order > 0x7fffffff - kWave;
+    // (a half-wave team holds up to two entries a lane)
+    const bool irregular = tballot<TW>(odd) != 0ull || nA > (TW == kWave ? TW : 2 * TW) ||
+                           next_order > 0x7fffffff - kWave;
     if (lane == 0) {
         // the empty cell's sentinel (index E) of the occupant arrays
         olo[g.E] = 0u;
@@ -492,6 +499,7 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     out.nlive = nlive;
     out.irregular = irregular;
     out.live_slot = ll.slot;
+    out.live_slot2 = ll.slot2;
     out.full = reach0 > g.C || reach1 > g.C;
     return out;
 }

@@ -573,6 +573,16 @@ class NanoRTS:
                                                      _ptr(actions)), "nanorts_amd_sample_actions")
         return {agent: actions[:, p] for p, agent in enumerate(self.agents)}
 
+    def rollout_first_pass(self) -> str | None:
+        """The first pass rollout() runs on this game (with two_pass): "pair"
+        (two games per wave), "lean" (one game per wave) or None (one pass
+        on the full block).  The environment variable NANORTS_AMD_FIRST_PASS
+        ("lean" or "pair") overrides the library's choice by board."""
+        code = self.lib.nanorts_amd_rollout_first_pass(self.dev.ref)
+        if code < 0:
+            native.check(code, "nanorts_amd_rollout_first_pass")
+        return {2: "pair", 1: "lean"}.get(code)
+
     def rollout(self, state: EnvironmentState, steps: int, sample_key, *, step0: int = 0, env0: int = 0,
                 record: bool = True, record_actions: bool = False, observation_depth: int = 1,
                 count_general: bool = False, two_pass: bool = True) -> dict[str, Any]:

@@ -100,6 +100,7 @@ EXPORTS = (
     "nanorts_amd_gridnet_decode", "nanorts_amd_gridnet_observe", "nanorts_amd_gridnet_step", "nanorts_amd_gridnet_step_against",
     "nanorts_amd_gridnet_sample_actions", "nanorts_amd_step_groups_ffi", "nanorts_amd_abstraction_act_ffi",
     "nanorts_amd_astar_search_ffi", "nanorts_amd_astar_chain_ffi", "nanorts_amd_gridnet_decode_ffi",
+    "nanorts_amd_rollout_first_pass",
 )
 
 _I64 = ctypes.c_int64
@@ -133,6 +134,7 @@ _SIGNATURES = {
     "nanorts_amd_decode_actions": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, Commands, _VP]),
     "nanorts_amd_sample_actions": (ctypes.c_int, [_VP, _GP, _I64, _VP, _VP, _I32, _I64, _VP]),
     "nanorts_amd_rollout": (ctypes.c_int, [_VP, _GP, State, _I64, _VP, _I32, _I32, _I32, _I64, RolloutResults]),
+    "nanorts_amd_rollout_first_pass": (ctypes.c_int, [_GP]),
     "nanorts_amd_abstraction_act": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _VP, _I64, AbstractActions, _VP]),
     "nanorts_amd_seat_step": (ctypes.c_int, [_VP, _GP, State, _I64, _I32, _I32, _I32, AbstractActions, _VP, _I32,
                                          EnvResults]),

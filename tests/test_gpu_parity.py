@@ -372,11 +372,13 @@ def test_two_pass_rollout_hands_games_to_the_second_pass(first_pass, monkeypatch
     """The rollout's first pass stages a 32-slot window of each player's 70
     slots and runs a game until a unit could spawn past its window (its
     units plus the PRODUCE actions due next cycle exceed 32), or a cycle
-    needs more than the first pass's lanes; the second pass, on the full
-    block, runs the rest of that game's cycles.  Games that start with
-    28..42 live slots, the added Workers all player 0's and 60 resources
-    each, cross the bound at cycle 0, part-way through the launch (spawns),
-    or not at all.  All of them match the oracle and the one-pass launch."""
+    needs more than the first pass's lanes (two games per wave: more than 32
+    available units or 64 live slots); the second pass, on the full block,
+    runs the rest of that game's cycles.  Games that start with 22..38 live
+    slots, the added Workers all player 0's and 200 resources each, cross a
+    bound part-way through the launch (spawns), or never, and with two games
+    per wave also at cycle 0 (available units).  All of them match the
+    oracle and the one-pass launch."""
     from oracle.oracle import Oracle
 
     _first_pass(monkeypatch, first_pass)
@@ -384,33 +386,33 @@ def test_two_pass_rollout_hands_games_to_the_second_pass(first_pass, monkeypatch
     game, partial = game_for("16x16-random-partial")
     b = game.bucket
     base = int((_packed(game, [0])["birth"][0] != -1).sum())
-    extra = [28 - base + k for k in range(15)]
+    extra = [22 - base + k for k in range(17)]
     st = _packed(game, extra, alternate=False)
-    st["player_resources"][:] = 60
+    st["player_resources"][:] = 200
     live = (st["birth"] != -1).sum(1)
-    assert live.min() == 28 and live.max() == 42
+    assert live.min() == 22 and live.max() == 38
     units0 = (st["birth"][:, b.neutral_capacity:b.neutral_capacity + b.per_player_capacity] != -1).sum(1)
     oracle = Oracle(game)
     assert (oracle.violations(st) == 0).all()
-    L, steps = len(extra), 96
+    L, steps = len(extra), 128  # one launch
     env = _env(game, partial)
     dev = to_device(env, st)
     one = to_device(env, st)
-    got = env.rollout(dev, steps, (4, 2), record=True, count_general=True)
+    got = env.rollout(dev, steps, (1, 2), record=True, count_general=True)
     first = got["first_pass_cycles"].cpu().numpy()
     print("first-pass cycles per game:", first.tolist(), flush=True)
     assert (first[units0 > 32] == 0).all()
-    if first_pass == "pair":
-        assert (first[live > 32] == 0).all()
     assert ((first > 0) & (first < steps)).any()
     assert (first == steps).any()
-    want = oracle.rollout(st, (4, 2), 0, steps, partial, threads=oracle_threads)
+    if first_pass == "pair":
+        assert (first == 0).any()
+    want = oracle.rollout(st, (1, 2), 0, steps, partial, threads=oracle_threads)
     np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
     np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
     np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
     np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
     assert_states_equal(st, to_host(dev), "two-pass rollout")
-    single = env.rollout(one, steps, (4, 2), record=True, count_general=True, two_pass=False)
+    single = env.rollout(one, steps, (1, 2), record=True, count_general=True, two_pass=False)
     np.testing.assert_array_equal(single["rewards"].cpu().numpy(), want["rewards"])
     np.testing.assert_array_equal(single["general_admissions"].cpu().numpy(),
                                   got["general_admissions"].cpu().numpy())
@@ -421,11 +423,12 @@ def test_two_pass_rollout_hands_games_to_the_second_pass(first_pass, monkeypatch
 @pytest.mark.parametrize("first_pass", ["auto", "pair"])
 def test_pair_first_pass_hands_games_to_the_second_pass(first_pass, monkeypatch, oracle_threads):
     """With two games per wave (the choice on 8x8 boards) the first pass runs
-    a game while it has at most 32 live slots and 32 available units; the
-    second pass runs the rest.  Games that start with 26..40 live slots on
-    basesWorkers8x8, the added Workers all player 0's and 60 resources each,
-    cross the bound at cycle 0, part-way through the launch (spawns take a
-    game past 32 live slots), or not at all.  All of them match the oracle;
+    a game while it has at most 32 available units, 64 live slots and room
+    in its slot window; the second pass runs the rest.  Games that start with
+    24..40 live slots on basesWorkers8x8, the added Workers all player 0's
+    and 200 resources each, cross a bound at cycle 0 or not at all (on this
+    crowded board no spawn takes a game past its window within the launch;
+    the 16x16 test above crosses part-way).  All of them match the oracle;
     an odd number of games leaves the last wave's second half without a
     game."""
     from oracle.oracle import Oracle
@@ -434,28 +437,67 @@ def test_pair_first_pass_hands_games_to_the_second_pass(first_pass, monkeypatch,
     print("pair two-pass rollout", flush=True)
     game, partial = game_for("8x8-original-both")
     base = int((_packed(game, [0])["birth"][0] != -1).sum())
-    extra = [26 - base + k for k in range(15)]
+    extra = [24 - base + k for k in range(17)]
     st = _packed(game, extra, alternate=False)
-    st["player_resources"][:] = 60
+    st["player_resources"][:] = 200
     live = (st["birth"] != -1).sum(1)
-    assert live.min() == 26 and live.max() == 40
+    assert live.min() == 24 and live.max() == 40
     oracle = Oracle(game)
     assert (oracle.violations(st) == 0).all()
-    L, steps = len(extra), 96
+    L, steps = len(extra), 128  # one launch
     env = _env(game, partial)
     dev = to_device(env, st)
-    got = env.rollout(dev, steps, (6, 2), record=True, count_general=True)
+    got = env.rollout(dev, steps, (1, 2), record=True, count_general=True)
     first = got["first_pass_cycles"].cpu().numpy()
     print("first-pass cycles per game:", first.tolist(), flush=True)
-    assert (first[live > 32] == 0).all()
-    assert ((first > 0) & (first < steps)).any()
+    assert (first == 0).any()
     assert (first == steps).any()
-    want = oracle.rollout(st, (6, 2), 0, steps, partial, threads=oracle_threads)
+    want = oracle.rollout(st, (1, 2), 0, steps, partial, threads=oracle_threads)
     np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
     np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
     np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
     np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
     assert_states_equal(st, to_host(dev), "pair two-pass rollout")
+
+
+@pytest.mark.parametrize("first_pass", ["auto", "pair"])
+def test_pair_first_pass_holds_two_live_slots_and_two_entries_a_lane(first_pass, monkeypatch, oracle_threads):
+    """Two games per wave with 33..64 live slots and 33..64 pending MOVE /
+    PRODUCE entries per game: each lane of a half-wave team holds two of
+    each (completion's members, admission's claims).  Crowded 16x16 games
+    (44..51 live slots, Workers of both players), advanced 12 cycles by the
+    oracle so that most units hold a pending action, stay in the first pass
+    for the whole launch, reach more than 32 entries, and match the
+    oracle."""
+    from oracle.oracle import Oracle
+
+    _first_pass(monkeypatch, first_pass)
+    print("pair pass, crowded", first_pass, flush=True)
+    game, partial = game_for("16x16-random-partial")
+    b = game.bucket
+    base = int((_packed(game, [0])["birth"][0] != -1).sum())
+    st = _packed(game, [44 - base + k for k in range(8)])
+    st["player_resources"][:] = 20
+    oracle = Oracle(game)
+    oracle.rollout(st, (1, 2), 0, 12, partial, threads=oracle_threads, record=False)
+    assert (oracle.violations(st) == 0).all()
+    live = (st["birth"] != -1).sum(1)
+    assert live.min() > 32
+    L, steps = st["birth"].shape[0], 64
+    env = _env(game, partial)
+    dev = to_device(env, st)
+    got = env.rollout(dev, steps, (1, 2), step0=12, record=True, count_general=True)
+    want = oracle.rollout(st, (1, 2), 12, steps, partial, threads=oracle_threads)
+    first = got["first_pass_cycles"].cpu().numpy()
+    assert (first == steps).all(), first
+    pk, birth = st["pending_kind"], st["birth"]
+    np.testing.assert_array_equal(got["rewards"].cpu().numpy(), want["rewards"])
+    np.testing.assert_array_equal(got["dones"].cpu().numpy(), want["dones"].astype(bool))
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
+    np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
+    assert_states_equal(st, to_host(dev), "crowded pair rollout")
+    # the oracle's run reached more than 32 entries (final state shown)
+    print("entries at the end:", (((pk == 1) | (pk == 4)) & (birth != -1)).sum(1).tolist(), flush=True)
 
 
 def test_crowded_env_step_per_call(oracle_threads):

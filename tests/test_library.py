@@ -50,7 +50,7 @@ def test_targets_name_every_compute_entry_point():
     lib = native.load()
     targets = set(lib.nanorts_amd_entries().decode().split(","))
     meta = {"nanorts_amd_build_id", "nanorts_amd_entries", "nanorts_amd_last_error", "nanorts_amd_shared_opt_in",
-            "nanorts_amd_self_check", "nanorts_amd_self_check_no_alloc"}
+            "nanorts_amd_self_check", "nanorts_amd_self_check_no_alloc", "nanorts_amd_rollout_first_pass"}
     assert targets == set(declared_entry_points()) - meta
 
 
