@@ -308,6 +308,12 @@ def first_pass_seen(rows: list[dict[str, float]]) -> str | None:
     return None
 
 
+def rollout_kernels(env) -> str:
+    """The kernels of one rollout launch, as the library chooses them."""
+    first = env.rollout_first_pass()
+    return f"k_rollout_{first} + k_rollout (second pass)" if first else "k_rollout"
+
+
 def per_launch(rows: list[dict[str, float]], counter: str, kernels) -> list[float]:
     """Counter sums per launch of a kernel sequence: a launch opens at each
     dispatch of its first kernel (for the rollout, the first pass that ran)
@@ -764,7 +770,7 @@ def main_gow(args) -> None:
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "k_rollout_lean + k_rollout (second pass)", "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "kernel": rollout_kernels(env), "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes, "cycles_per_launch": chunk,
         },
         "pixel_leg": {
@@ -1006,8 +1012,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
-            "kernel": (f"{(traffic or {}).get('first_pass', 'k_rollout_pair or k_rollout_lean')} + k_rollout "
-                       "(second pass)") if LAST_TWO_PASS else "k_rollout",
+            "kernel": rollout_kernels(env) if LAST_TWO_PASS else "k_rollout",
             "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes,
             "cycles_per_launch": chunk,
