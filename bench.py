@@ -446,6 +446,8 @@ def main_seat(args) -> None:
     L = args.envs
     chunk = max(1, min(args.chunk, args.steps))
 
+    paired = [False]  # whether the last launch ran the two-games-per-wave first pass
+
     def run(steps, step0, events):
         done, times = 0, []
         while done < steps:
@@ -453,11 +455,14 @@ def main_seat(args) -> None:
             if events:
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record()
-            seat.rollout(state, n, (11, 13), step0=step0 + done, observation_depth=args.depth)
+            out = seat.rollout(state, n, (11, 13), step0=step0 + done, observation_depth=args.depth)
             if events:
                 b.record()
                 times.append((a, b, n))
             done += n
+        first = out["first_pass_cycles"] if steps else None
+        if first is not None:
+            paired[0] = bool((first > 0).any().item())
         return times
 
     run(args.warmup, 0, False)
@@ -475,7 +480,8 @@ def main_seat(args) -> None:
     per_step = step_bytes(b)
     per_launch_bytes = L * (chunk * per_step + 2 * state_bytes(b) + 2 * carry_bytes(b))
     achieved = per_launch_bytes / avg_launch_s / 1e9
-    traffic = pmc_traffic(args, chunk, mode="seat", kernel="k_seat_rollout")
+    seat_kernels = ("k_seat_rollout_pair", "k_seat_rollout")
+    traffic = pmc_traffic(args, chunk, mode="seat", kernel=seat_kernels)
     cpu = None if args.no_cpu else cpu_seat_baseline(bot.name, args.cpu_envs // 4, args.cpu_steps // 15)
     line = {
         "metric": f"env-steps/sec (learner vs {bot.name}) at 16x16 × {L} envs; % HBM roofline",
@@ -503,7 +509,8 @@ def main_seat(args) -> None:
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None if traffic is None else round(traffic["fetch_bytes"] + traffic["write_bytes"], 1),
-            "kernel": "k_seat_rollout", "avg_launch_ms": round(avg_launch_s * 1e3, 4),
+            "kernel": "k_seat_rollout_pair + k_seat_rollout (second pass)" if paired[0] else "k_seat_rollout",
+            "avg_launch_ms": round(avg_launch_s * 1e3, 4),
             "algorithmic_bytes_per_launch": per_launch_bytes,
         },
         "cpu_baseline": cpu,

@@ -236,13 +236,18 @@ class SeatEnv:
         return ({LEARNER: obs}, nxt, {LEARNER: reward}, {LEARNER: out["done"], ALL_AGENTS: out["done"]}, infos)
 
     def rollout(self, state: SeatState, steps: int, sample_key, *, step0: int = 0, env0: int = 0,
-                record: bool = True, record_actions: bool = False, observation_depth: int = 1) -> dict[str, Any]:
+                record: bool = True, record_actions: bool = False, observation_depth: int = 1,
+                two_pass: bool = True) -> dict[str, Any]:
         """Fused rollout of `steps` cycles in place: the learner's rows from the
         synthetic harness's uniform-over-legal sampler, the bot's act and the
         seat step, with the state resident in LDS.  Bit-equal to
         get_avail_actions(form="words") -> sample_actions -> step per cycle.
         Rewards are both players' [steps, L, 2]; with per-lane seats "seats"
-        holds the learner of every cycle [steps, L]."""
+        holds the learner of every cycle [steps, L].  With two_pass (the
+        default) a launch may run each game first with two games per wave on
+        a window of the slots and hand the rest of a game's cycles to the
+        one-game-per-wave pass; out["first_pass_cycles"] int32[L] holds the
+        first pass's cycles of each game in the last launch."""
         env = self.env
         es = state.environment_state
         L = es.num_envs
@@ -257,6 +262,8 @@ class SeatEnv:
         scalars = torch.empty((depth, L, 2, 4), dtype=torch.int32, device=d)
         key = (ctypes.c_uint32 * 2)(*[int(v) for v in np.asarray(sample_key, np.uint32).reshape(2)])
         results = native.RolloutResults(_ptr(rewards), _ptr(dones), _ptr(actions), _ptr(maps), _ptr(scalars), depth)
+        progress = torch.empty(L, dtype=torch.int32, device=d) if two_pass else None
+        results.progress = _ptr(progress)
         seats = None
         if self.learner is not None:
             native.check(env.lib.nanorts_amd_seat_rollout(_stream(), env.dev.ref, es.native(), L, self.bot.strategy,
@@ -271,7 +278,7 @@ class SeatEnv:
                                                             int(steps), env.partial, int(env0), results),
                          "nanorts_amd_seat_rollout_lanes")
         return {"rewards": rewards, "dones": dones, "actions": actions, "feature_maps": maps, "scalars": scalars,
-                "seats": seats}
+                "seats": seats, "first_pass_cycles": progress}
 
     def _bot_players(self, state: SeatState):
         return 1 - self.learner if self.learner is not None else (1 - state.seat).contiguous()

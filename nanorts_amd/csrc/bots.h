@@ -88,18 +88,20 @@ NR_DEV int32_t carry_row32(const BotLayout& y, int f) {
     }
 }
 
-NR_DEV int32_t wave_min(int32_t v) {
+template <int TW = kWave>
+NR_DEV int32_t team_min(int32_t v) {
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const int32_t o = __shfl_xor(v, d, kWave);
+    for (int d = TW / 2; d >= 1; d >>= 1) {
+        const int32_t o = __shfl_xor(v, d, TW);
         v = o < v ? o : v;
     }
     return v;
 }
 
-NR_DEV int32_t wave_sum(int32_t v) {
+template <int TW = kWave>
+NR_DEV int32_t team_sum(int32_t v) {
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+    for (int d = TW / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, TW);
     return v;
 }
 
@@ -180,6 +182,7 @@ NR_DEV bool is_entry(const Bot& b, const BotLayout& y, int32_t i, int32_t birth,
 // ---------------------------------------------------------------------------
 // With `load_carry` false the carry rows in LDS and b.next_order are the
 // ones the last settle_carry left (a fused rollout keeps them there).
+template <int TW = kWave>
 NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
                       const BotCarry& carry, int lane, bool load_carry = true) {
     const int32_t C = g.C;
@@ -187,19 +190,19 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     AS3 int16_t* live = bv<int16_t>(b, y.u_live);
     AS3 int32_t* lbirth = bv<int32_t>(b, y.u_lbirth);
     int32_t n = 0;
-    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+    for (int32_t i0 = 0; i0 < C; i0 += TW) {
         const int32_t i = i0 + lane;
         const int32_t bi = i < C ? e.birth[b.block + i] : kAbsent;
         const bool present = bi != kAbsent;
-        const uint64_t m = ballot(present);
+        const uint64_t m = tballot<TW>(present);
         if (present) {
-            live[n + count_below(m)] = (int16_t)i;
-            lbirth[n + count_below(m)] = bi;
+            live[n + tcount_below<TW>(m)] = (int16_t)i;
+            lbirth[n + tcount_below<TW>(m)] = bi;
         }
         n += popc(m);
     }
     b.n_live = n;
-    for (int32_t i = lane; i < (load_carry ? C : 0); i += kWave) {
+    for (int32_t i = lane; i < (load_carry ? C : 0); i += TW) {
         const int64_t at = l * C + i;
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)carry.row[0][at];
 #pragma unroll
@@ -212,7 +215,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     if (load_carry) {
         int32_t next_order = 0;
         if (lane == 0) next_order = __builtin_nontemporal_load(carry.next_order + l);
-        b.next_order = uni(next_order);
+        b.next_order = tuni<TW>(next_order);
     }
     // candidate lists in slot order: enemies (abstraction.enemies), resources
     // and own stockpiles (rush.harvest_sites)
@@ -220,7 +223,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
     AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
     int32_t ne = 0, nr_ = 0, ns = 0;
-    for (int32_t s0 = 0; s0 < g.E; s0 += kWave) {
+    for (int32_t s0 = 0; s0 < g.E; s0 += TW) {
         const int32_t s = s0 + lane;
         bool en = false, re = false, st = false;
         if (s < g.E && e.birth[s] != kAbsent) {
@@ -229,12 +232,12 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
             re = type_flag(g, h, t, FL_RESOURCE);
             st = type_flag(g, h, t, FL_STOCKPILE) && owner == b.player;
         }
-        const uint64_t me = ballot(en), mr = ballot(re), ms = ballot(st);
+        const uint64_t me = tballot<TW>(en), mr = tballot<TW>(re), ms = tballot<TW>(st);
         // the lists hold what a valid state can put in them: the opponent's
         // units, neutral resources, own stockpiles
-        if (en && ne + count_below(me) < C) le[ne + count_below(me)] = (int16_t)s;
-        if (re && nr_ + count_below(mr) < g.N) lr[nr_ + count_below(mr)] = (int16_t)s;
-        if (st && ns + count_below(ms) < C) ls[ns + count_below(ms)] = (int16_t)s;
+        if (en && ne + tcount_below<TW>(me) < C) le[ne + tcount_below<TW>(me)] = (int16_t)s;
+        if (re && nr_ + tcount_below<TW>(mr) < g.N) lr[nr_ + tcount_below<TW>(mr)] = (int16_t)s;
+        if (st && ns + tcount_below<TW>(ms) < C) ls[ns + tcount_below<TW>(ms)] = (int16_t)s;
         ne += popc(me);
         nr_ += popc(mr);
         ns += popc(ms);
@@ -245,7 +248,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
     wave_sync();
     // birth rank among the present units (abstraction._rank) and the
     // nearest enemy of every live unit
-    for (int32_t k = lane; k < n; k += kWave) {
+    for (int32_t k = lane; k < n; k += TW) {
         const int32_t i = live[k], bi = lbirth[k];
         int32_t r = 0;
 #pragma unroll 4
@@ -264,13 +267,14 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
 // ---------------------------------------------------------------------------
 // abstraction._building_site (N/bots/abstraction.py:247-283): the open cell
 // first in the ring walk around `desired`.
+template <int TW = kWave>
 NR_DEV int32_t building_site(const KGame& g, const Hdr& h, const Env& e, const Bot& b, const BotLayout& y,
                              int32_t desired, int lane) {
     const AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
     const int32_t longest = g.W > g.H ? g.W : g.H;
     const int32_t x0 = floor_mod(desired, g.W), y0 = floor_div(desired, g.W);
     int32_t best = kLast, site = kAbsent;
-    for (int32_t c = lane; c < g.cells; c += kWave) {
+    for (int32_t c = lane; c < g.cells; c += TW) {
         const int32_t dx = cell_x(g, c) - x0, dy = cell_y(g, c) - y0;
         const int32_t ax = abs(dx), ay = abs(dy);
         const int32_t ring = ax > ay ? ax : ay;
@@ -284,9 +288,9 @@ NR_DEV int32_t building_site(const KGame& g, const Hdr& h, const Env& e, const B
             site = c;
         }
     }
-    const int32_t m = wave_min(best);
-    const uint64_t at = ballot(site != kAbsent && best == m);
-    return at == 0ull ? kAbsent : __builtin_amdgcn_readlane(site, (int32_t)__builtin_ctzll(at));
+    const int32_t m = team_min<TW>(best);
+    const uint64_t at = tballot<TW>(site != kAbsent && best == m);
+    return at == 0ull ? kAbsent : tread<TW>(site, (int32_t)__builtin_ctzll(at));
 }
 
 // Per-unit role bits of the rush decisions (u_role, one byte per own slot).
@@ -297,11 +301,12 @@ NR_DEV AS3 uint8_t* roles(const Bot& b, const BotLayout& y) { return bv<uint8_t>
 // The unit of least birth among those whose role byte has any of `bits`
 // (rush.first_in_unit_order, N/bots/rush.py:56-58), excluding `skip0` and
 // `skip1`; -1 when there is none.
+template <int TW = kWave>
 NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const BotLayout& y, uint8_t bits, int32_t skip0,
                         int32_t skip1, int lane) {
     const AS3 uint8_t* r = roles(b, y);
     int32_t best = kLast, who = -1;
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         if (!(r[i] & bits) || i == skip0 || i == skip1) continue;
         const int32_t bi = e.birth[b.block + i];
@@ -310,13 +315,14 @@ NR_DEV int32_t first_of(const KGame& g, const Env& e, const Bot& b, const BotLay
             who = i;
         }
     }
-    const int32_t mn = wave_min(best);
-    const uint64_t at = ballot(who >= 0 && best == mn);
-    return at == 0ull ? -1 : __builtin_amdgcn_readlane(who, (int32_t)__builtin_ctzll(at));
+    const int32_t mn = team_min<TW>(best);
+    const uint64_t at = tballot<TW>(who >= 0 && best == mn);
+    return at == 0ull ? -1 : tread<TW>(who, (int32_t)__builtin_ctzll(at));
 }
 
 // abstraction.build_if_not_already_building (N/bots/abstraction.py:286-297)
 // for a one-unit builder (or none); marks the site in the reserved bitmap.
+template <int TW = kWave>
 NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
                                   int32_t builder, int32_t unit_type, int lane) {
     bool builds = false;
@@ -324,9 +330,9 @@ NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bo
         const int32_t bb = e.birth[b.block + builder];
         builds = !(is_entry(b, y, builder, bb, kAbBuild) && bv<int8_t>(b, y.k_utype)[builder] == unit_type);
     }
-    builds = uni(builds ? 1 : 0) != 0;
+    builds = tuni<TW>(builds ? 1 : 0) != 0;
     if (builds) {
-        const int32_t site = building_site(g, h, e, b, y, e.cell[b.block + builder], lane);
+        const int32_t site = building_site<TW>(g, h, e, b, y, e.cell[b.block + builder], lane);
         if (lane == 0) {
             const Unit u = unit_at(g, e, b, builder);
             put_unit(g, b, u, builder, false, kAbBuild, kAbsent, kAbsent, kAbsent, kAbsent, site, unit_type, y);
@@ -339,31 +345,33 @@ NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bo
 
 // rush.build_base (N/bots/rush.py:88-104) over the R_WORKER units: clears the
 // reserved bitmap, returns the builder or -1.
+template <int TW = kWave>
 NR_DEV int32_t build_base(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
     AS3 uint32_t* reserved = bv<uint32_t>(b, y.m_reserved);
-    for (int32_t w = lane; w < (g.cells + 31) / 32; w += kWave) reserved[w] = 0u;
+    for (int32_t w = lane; w < (g.cells + 31) / 32; w += TW) reserved[w] = 0u;
     bool any_base = false;
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         any_base |= u.present && u.type == kTypeBase;
     }
-    any_base = ballot(any_base) != 0ull;
-    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    any_base = tballot<TW>(any_base) != 0ull;
+    const int32_t res = tuni<TW>(e.sc[S_RES0 + b.player]);
     const bool builds = !any_base && res >= tabv(h, F_COST, kTypeBase);
-    const int32_t builder = builds ? first_of(g, e, b, y, R_WORKER, -1, -1, lane) : -1;
+    const int32_t builder = builds ? first_of<TW>(g, e, b, y, R_WORKER, -1, -1, lane) : -1;
     wave_sync();
-    build_unless_building(g, h, e, b, y, builder, kTypeBase, lane);
+    build_unless_building<TW>(g, h, e, b, y, builder, kTypeBase, lane);
     return builder;
 }
 
 // rush._harvest (N/bots/rush.py:156-181) for the R_PICK units; marks the
 // idle ones (no site to harvest) R_IDLE.
+template <int TW = kWave>
 NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, int lane) {
     AS3 uint8_t* r = roles(b, y);
     const AS3 int16_t* lr = bv<int16_t>(b, y.l_resource);
     const AS3 int16_t* ls = bv<int16_t>(b, y.l_stock);
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         if (!(role & R_PICK)) continue;
@@ -388,9 +396,10 @@ NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, in
 
 // rush._attack_nearest (N/bots/rush.py:61-70) for the units whose role has
 // any of `bits`; R_LAST units are stamped last.
+template <int TW = kWave>
 NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, uint8_t bits, int lane) {
     const AS3 uint8_t* r = roles(b, y);
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         if (!(role & bits)) continue;
@@ -405,10 +414,10 @@ NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout
 }
 
 // A put of TRAIN for the units `pick` selects.
-template <typename Pick>
+template <int TW, typename Pick>
 NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y, int32_t unit_type, Pick pick,
                         int lane) {
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         if (pick(u)) put_unit(g, b, u, i, false, kAbTrain, kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, unit_type, y);
@@ -419,9 +428,10 @@ NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y
 
 // rush._melee_units_attack with available_melee (N/bots/rush.py:73-85); also
 // marks the workers (present units that can harvest) R_WORKER.
+template <int TW = kWave>
 NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         const bool harvests = type_flag(g, h, u.type, FL_HARVEST);
@@ -429,15 +439,16 @@ NR_DEV void melee_attack(const KGame& g, const Hdr& h, const Env& e, Bot& b, con
         r[i] = (uint8_t)((melee ? R_PICK : 0) | ((u.present && harvests) ? R_WORKER : 0));
     }
     wave_sync();
-    attack_nearest(g, e, b, y, R_PICK, lane);
+    attack_nearest<TW>(g, e, b, y, R_PICK, lane);
 }
 
 // Role bytes for a new decision: R_WORKER kept, `pick` units get R_PICK,
 // others lose R_PICK / R_IDLE / R_LAST.
+template <int TW = kWave>
 NR_DEV void mark_picks(const KGame& g, const Bot& b, const BotLayout& y, int32_t skip0, int32_t skip1, int32_t only,
                        int lane) {
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t w = r[i] & R_WORKER;
         const bool pick = only >= 0 ? i == only : (w && i != skip0 && i != skip1);
@@ -447,21 +458,22 @@ NR_DEV void mark_picks(const KGame& g, const Bot& b, const BotLayout& y, int32_t
 }
 
 // rush.worker_rush (N/bots/rush.py:213-220) with _rushing_workers (:204-210).
+template <int TW = kWave>
 NR_DEV void worker_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
-    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    const int32_t res = tuni<TW>(e.sc[S_RES0 + b.player]);
     const int32_t worker_cost = tabv(h, F_COST, kTypeWorker);
-    train_where(g, e, b, y, kTypeWorker,
+    train_where<TW>(g, e, b, y, kTypeWorker,
                 [&](const Unit& u) { return u.present && u.type == kTypeBase && u.available && res >= worker_cost; },
                 lane);
-    melee_attack(g, h, e, b, y, lane);
-    const int32_t builder = build_base(g, h, e, b, y, lane);
-    const int32_t harvester = first_of(g, e, b, y, R_WORKER, builder, -1, lane);
-    mark_picks(g, b, y, -1, -1, harvester < 0 ? g.C : harvester, lane);
-    harvest(g, e, b, y, lane);
+    melee_attack<TW>(g, h, e, b, y, lane);
+    const int32_t builder = build_base<TW>(g, h, e, b, y, lane);
+    const int32_t harvester = first_of<TW>(g, e, b, y, R_WORKER, builder, -1, lane);
+    mark_picks<TW>(g, b, y, -1, -1, harvester < 0 ? g.C : harvester, lane);
+    harvest<TW>(g, e, b, y, lane);
     // free = (workers - builder - harvester) | idle harvester; the idle
     // harvester is stamped last
     AS3 uint8_t* r = roles(b, y);
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const uint8_t role = r[i];
         const bool idle = (role & R_IDLE) != 0;
@@ -469,44 +481,45 @@ NR_DEV void worker_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, cons
         r[i] = (uint8_t)((role & R_WORKER) | (free ? R_PICK : 0) | (idle ? R_LAST : 0));
     }
     wave_sync();
-    attack_nearest(g, e, b, y, R_PICK, lane);
+    attack_nearest<TW>(g, e, b, y, R_PICK, lane);
 }
 
 // rush.barracks_rush (N/bots/rush.py:229-236) with train_at_base_and_barracks
 // (:107-133), build_base_and_barracks (:184-201) and _workers_behavior
 // (:223-226).
+template <int TW = kWave>
 NR_DEV void barracks_rush(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y,
                           int32_t trained_type, int lane) {
-    const int32_t res = uni(e.sc[S_RES0 + b.player]);
+    const int32_t res = tuni<TW>(e.sc[S_RES0 + b.player]);
     int32_t held = 0;
     bool any_barracks = false;
-    for (int32_t k = lane; k < b.n_live; k += kWave) {
+    for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
         held += (u.present && u.type == kTypeWorker) ? 1 : 0;
         any_barracks |= u.present && u.type == kTypeBarracks;
     }
-    held = wave_sum(held);
-    any_barracks = ballot(any_barracks) != 0ull;
+    held = team_sum<TW>(held);
+    any_barracks = tballot<TW>(any_barracks) != 0ull;
     const int32_t worker_cost = tabv(h, F_COST, kTypeWorker);
-    train_where(g, e, b, y, kTypeWorker,
+    train_where<TW>(g, e, b, y, kTypeWorker,
                 [&](const Unit& u) {
                     return u.present && u.type == kTypeBase && u.available && held < 1 && res >= worker_cost;
                 },
                 lane);
     const int32_t trained_cost = tabv(h, F_COST, clampi(trained_type, 0, g.T - 1));
-    train_where(g, e, b, y, trained_type,
+    train_where<TW>(g, e, b, y, trained_type,
                 [&](const Unit& u) { return u.present && u.type == kTypeBarracks && u.available && res >= trained_cost; },
                 lane);
-    melee_attack(g, h, e, b, y, lane);
-    const int32_t base_builder = build_base(g, h, e, b, y, lane);
+    melee_attack<TW>(g, h, e, b, y, lane);
+    const int32_t base_builder = build_base<TW>(g, h, e, b, y, lane);
     const int32_t used = base_builder >= 0 ? tabv(h, F_COST, kTypeBase) : 0;
     const bool builds_barracks = !any_barracks && res >= wadd(tabv(h, F_COST, kTypeBarracks), used);
-    const int32_t barracks_builder = builds_barracks ? first_of(g, e, b, y, R_WORKER, base_builder, -1, lane) : -1;
-    build_unless_building(g, h, e, b, y, barracks_builder, kTypeBarracks, lane);
-    mark_picks(g, b, y, base_builder, barracks_builder, -1, lane);
-    harvest(g, e, b, y, lane);
-    attack_nearest(g, e, b, y, R_IDLE, lane);
+    const int32_t barracks_builder = builds_barracks ? first_of<TW>(g, e, b, y, R_WORKER, base_builder, -1, lane) : -1;
+    build_unless_building<TW>(g, h, e, b, y, barracks_builder, kTypeBarracks, lane);
+    mark_picks<TW>(g, b, y, base_builder, barracks_builder, -1, lane);
+    harvest<TW>(g, e, b, y, lane);
+    attack_nearest<TW>(g, e, b, y, R_IDLE, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -720,11 +733,12 @@ NR_DEV int32_t cell_of_slot(const KGame& g, const Env& e, int32_t slot) {
 }
 
 // Usage, standing, plan and queue; returns the number of queued units.
+template <int TW = kWave>
 NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int lane) {
     const int32_t C = g.C, words = (g.cells + 31) / 32;
     AS3 uint32_t* claimed = bv<uint32_t>(b, y.m_claimed);
     AS3 uint32_t* freem = bv<uint32_t>(b, y.m_free);
-    for (int32_t w = lane; w < words; w += kWave) {
+    for (int32_t w = lane; w < words; w += TW) {
         claimed[w] = 0u;
         freem[w] = 0u;
         bv<uint32_t>(b, y.m_used)[w] = 0u;
@@ -733,7 +747,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
     wave_sync();
     // _pending_usage (N/bots/abstraction.py:331-359)
     int32_t cost0 = 0, cost1 = 0;
-    for (int32_t s = lane; s < g.E; s += kWave) {
+    for (int32_t s = lane; s < g.E; s += TW) {
         if (e.birth[s] == kAbsent) continue;
         const int32_t kind = e.pkind[s];
         if (kind == kKindMove || kind == kKindProduce) {
@@ -747,15 +761,15 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
             else cost1 = wadd(cost1, c);
         }
     }
-    b.reserved0 = wave_sum(cost0);
-    b.reserved1 = wave_sum(cost1);
+    b.reserved0 = team_sum<TW>(cost0);
+    b.reserved1 = team_sum<TW>(cost1);
     wave_sync();
     // _free_cells (:362-365)
-    for (int32_t c = lane; c < g.cells; c += kWave)
+    for (int32_t c = lane; c < g.cells; c += TW)
         if (h.terrain[c] == 0 && e.entity[c] == kAbsent && !bit_of(claimed, c)) set_bit(freem, c);
     wave_sync();
     // _standing (:383-423) and _plan (:653-715) with _fallback (:575-650)
-    for (int32_t i = lane; i < C; i += kWave) {
+    for (int32_t i = lane; i < C; i += TW) {
         const Unit u = unit_at(g, e, b, i);
         const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
         const bool alive = kind != kAbNone && bv<int32_t>(b, y.k_ubirth)[i] == u.birth;
@@ -812,18 +826,18 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
     AS3 int16_t* list = bv<int16_t>(b, y.u_list);
     AS3 int32_t* key = bv<int32_t>(b, y.u_lkey);
     int32_t queued = 0;
-    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+    for (int32_t i0 = 0; i0 < C; i0 += TW) {
         const int32_t i = i0 + lane;
         const bool ex = i < C && (bv<uint8_t>(b, y.u_flags)[i] & U_EXECUTES);
-        const uint64_t m = ballot(ex);
+        const uint64_t m = tballot<TW>(ex);
         if (ex) {
-            list[queued + count_below(m)] = (int16_t)i;
-            key[queued + count_below(m)] = bv<int32_t>(b, y.k_order)[i];
+            list[queued + tcount_below<TW>(m)] = (int16_t)i;
+            key[queued + tcount_below<TW>(m)] = bv<int32_t>(b, y.k_order)[i];
         }
         queued += popc(m);
     }
     wave_sync();
-    for (int32_t k = lane; k < queued; k += kWave) {
+    for (int32_t k = lane; k < queued; k += TW) {
         const int32_t oi = key[k];
         int32_t r = 0;
 #pragma unroll 4
@@ -833,7 +847,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
         }
         bv<int16_t>(b, y.u_queue)[r] = list[k];
     }
-    for (int32_t i = lane; i < C; i += kWave) {
+    for (int32_t i = lane; i < C; i += TW) {
         bv<uint8_t>(b, y.u_sel)[i] = SEL_NONE;
         bv<int16_t>(b, y.u_drank)[i] = (int16_t)kAbsent;
     }
@@ -843,6 +857,7 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
 
 // _walked / _walk_step with _answer and _kept (N/bots/abstraction.py:718-797,
 // 904-952): returns how many desires it keeps.
+template <int TW = kWave>
 NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int32_t queued,
                               int lane) {
     (void)h;
@@ -855,30 +870,30 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
     const int32_t own = b.player;
     const bool may_move = within_balance(e, b, 0) && within_balance(e, b, 1);
     const int32_t reserved_own = own == 0 ? b.reserved0 : b.reserved1;
-    const int32_t balance = uni(e.sc[S_RES0 + own]);
+    const int32_t balance = tuni<TW>(e.sc[S_RES0 + own]);
     int32_t spent = 0, granted = 0;
     for (int32_t q = 0; q < queued; ++q) {
-        const int32_t i = uni(bv<int16_t>(b, y.u_queue)[q]);
-        const int32_t start = uni(e.cell[b.block + i]);
-        const int32_t goal = uni(bv<int16_t>(b, y.u_goal)[i]);
-        const int32_t radius = uni(bv<int16_t>(b, y.u_radius)[i]);
+        const int32_t i = tuni<TW>(bv<int16_t>(b, y.u_queue)[q]);
+        const int32_t start = tuni<TW>(e.cell[b.block + i]);
+        const int32_t goal = tuni<TW>(bv<int16_t>(b, y.u_goal)[i]);
+        const int32_t radius = tuni<TW>(bv<int16_t>(b, y.u_radius)[i]);
         int32_t step = kAbsent;
         // the first pop is the start: already within range means no step
         if (start >= 0 && start < g.cells && sq_distance(g, start, goal) > wmul(radius, radius)) {
             if ((g.cells & 3) == 0) {
                 // four cells per lane: their open bits to four mark bytes
-                for (int32_t q = lane; q < g.cells / 4; q += kWave) {
+                for (int32_t q = lane; q < g.cells / 4; q += TW) {
                     const int32_t c0 = 4 * q;
                     const uint32_t shut = ~((freem[c0 >> 5] & ~used[c0 >> 5]) >> (c0 & 31)) & 15u;
                     ((AS3 uint32_t*)mark)[q] = (shut & 1u) | ((shut & 2u) << 7) | ((shut & 4u) << 14) | ((shut & 8u) << 21);
                 }
             } else {
-                for (int32_t c = lane; c < g.cells; c += kWave) mark[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
+                for (int32_t c = lane; c < g.cells; c += TW) mark[c] = (bit_of(freem, c) && !bit_of(used, c)) ? 0 : 1;
             }
             wave_sync();
             int32_t s = kAbsent;
             if (lane == 0) s = astar_first_step(g, below, mark, start, goal, radius);
-            step = __builtin_amdgcn_readfirstlane(s);
+            step = tread<TW>(s, 0);
             wave_sync();
         }
         int32_t sel, kind, claim, cost;
@@ -889,9 +904,9 @@ NR_DEV int32_t translate_walk(const KGame& g, const Hdr& h, const Env& e, Bot& b
             cost = 0;
         } else {
             sel = SEL_FALLBACK;
-            kind = uni(bv<int8_t>(b, y.u_fkind)[i]);
-            claim = uni(bv<int16_t>(b, y.u_fclaimed)[i]);
-            cost = uni(bv<int16_t>(b, y.u_fcost)[i]);
+            kind = tuni<TW>(bv<int8_t>(b, y.u_fkind)[i]);
+            claim = tuni<TW>(bv<int16_t>(b, y.u_fclaimed)[i]);
+            cost = tuni<TW>(bv<int16_t>(b, y.u_fcost)[i]);
         }
         const bool has_cell = claim != kAbsent && claim >= 0 && claim < g.cells;
         const bool conflicting = has_cell && (bit_of(claimed, claim) || bit_of(kept_m, claim));
@@ -955,8 +970,9 @@ NR_DEV void unit_command(const KGame& g, const Env& e, const Bot& b, const BotLa
 }
 
 // The carry rows in LDS and b.next_order into the carry of env l.
+template <int TW = kWave>
 NR_DEV void store_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry, int lane) {
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t i = lane; i < g.C; i += TW) {
         const int64_t at = l * g.C + i;
         carry.row[0][at] = bv<int8_t>(b, y.k_kind)[i];
 #pragma unroll
@@ -971,21 +987,22 @@ NR_DEV void store_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_
 // the settled carry (the standing units, their orders ranked; the others
 // emptied) and b.next_order the standing count; with `to_memory` they are
 // also written to the carry rows of env l.
+template <int TW = kWave>
 NR_DEV void settle_carry(const KGame& g, Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry, int lane,
                          bool to_memory = true) {
     const int32_t C = g.C;
     // the standing units with their orders
     AS3 int32_t* key = bv<int32_t>(b, y.u_lkey);
     int32_t standing = 0;
-    for (int32_t i0 = 0; i0 < C; i0 += kWave) {
+    for (int32_t i0 = 0; i0 < C; i0 += TW) {
         const int32_t i = i0 + lane;
         const bool st = i < C && (bv<uint8_t>(b, y.u_flags)[i] & U_STANDING);
-        const uint64_t m = ballot(st);
-        if (st) key[standing + count_below(m)] = bv<int32_t>(b, y.k_order)[i];
+        const uint64_t m = tballot<TW>(st);
+        if (st) key[standing + tcount_below<TW>(m)] = bv<int32_t>(b, y.k_order)[i];
         standing += popc(m);
     }
     wave_sync();
-    for (int32_t i = lane; i < C; i += kWave) {
+    for (int32_t i = lane; i < C; i += TW) {
         const int32_t fl = bv<uint8_t>(b, y.u_flags)[i];
         const bool st = (fl & U_STANDING) != 0;
         const int32_t oi = bv<int32_t>(b, y.k_order)[i];
@@ -1007,12 +1024,13 @@ NR_DEV void settle_carry(const KGame& g, Bot& b, const BotLayout& y, int64_t l, 
     }
     b.next_order = standing;
     wave_sync();
-    if (to_memory) store_carry(g, b, y, l, carry, lane);
+    if (to_memory) store_carry<TW>(g, b, y, l, carry, lane);
 }
 
 // abstraction.empty_actions into the carry rows of env l (a new episode).
+template <int TW = kWave>
 NR_DEV void clear_carry(const KGame& g, int64_t l, const BotCarry& carry, int lane) {
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t i = lane; i < g.C; i += TW) {
         const int64_t at = l * g.C + i;
 #pragma unroll
         for (int f = 0; f < 9; ++f) carry.row[f][at] = kAbsent;
@@ -1022,8 +1040,9 @@ NR_DEV void clear_carry(const KGame& g, int64_t l, const BotCarry& carry, int la
 }
 
 // The same in LDS, for a fused rollout that keeps the carry there.
+template <int TW = kWave>
 NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lane) {
-    for (int32_t i = lane; i < g.C; i += kWave) {
+    for (int32_t i = lane; i < g.C; i += TW) {
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)kAbsent;
 #pragma unroll
         for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = kAbsent;
@@ -1037,14 +1056,15 @@ NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lan
 // family.act (N/bots/family.py:34-41): the rush decisions on the carry, then
 // translate's plan and walk.  Returns how many desires the walk keeps; commands come from
 // unit_command and the carry from settle_carry.
+template <int TW = kWave>
 NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
                        const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane,
                        bool load_carry = true) {
-    bot_begin(g, h, e, b, y, l, carry, lane, load_carry);
-    if (strategy == kWorkerRush) worker_rush(g, h, e, b, y, lane);
-    else barracks_rush(g, h, e, b, y, trained_type, lane);
-    const int32_t queued = translate_plan(g, h, e, b, y, lane);
-    return translate_walk(g, h, e, b, y, queued, lane);
+    bot_begin<TW>(g, h, e, b, y, l, carry, lane, load_carry);
+    if (strategy == kWorkerRush) worker_rush<TW>(g, h, e, b, y, lane);
+    else barracks_rush<TW>(g, h, e, b, y, trained_type, lane);
+    const int32_t queued = translate_plan<TW>(g, h, e, b, y, lane);
+    return translate_walk<TW>(g, h, e, b, y, queued, lane);
 }
 
 }  // namespace nr

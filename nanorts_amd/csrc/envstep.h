@@ -197,13 +197,14 @@ NR_DEV void stage_requests(const KGame& g, const Env& e_in, int lane, int32_t n,
 
 // Admission over the n available units listed by compact_available, whose
 // canonical commands are staged in the command arrays.
+template <int TW = kWave>
 NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, uint32_t key0, uint32_t key1,
                       bool count_events, int32_t n, bool irregular, bool known_legal, bool listed = false) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
-    if (irregular || n > kWave) return false;
-    int32_t nA = 0, posA[1] = {0}, costA[1] = {0}, playerA[1] = {0};
-    if (!admit_entries(g, h, e, lane, listed, &nA, posA, costA, playerA)) return false;
+    if (irregular || n > TW) return false;
+    int32_t nA = 0, posA[2] = {0, 0}, costA[2] = {0, 0}, playerA[2] = {0, 0};
+    if (!admit_entries<TW>(g, h, e, lane, listed, &nA, posA, costA, playerA)) return false;
     Reqs q;
     no_request(q);
     if (lane < n) {
@@ -212,7 +213,7 @@ NR_DEV bool admit_env(const KGame& g, const Hdr& h, const Env& e_in, int lane, u
                    at<int16_t>(e, y.c_target)[p], at<int32_t>(e, y.c_none)[p], known_legal, count_events, q);
         q.order_rank = at<int16_t>(e, y.c_rank)[p];
     }
-    admit_resolve(g, h, e, lane, key0, key1, n, nA, posA, costA, playerA, q);
+    admit_resolve<TW>(g, h, e, lane, key0, key1, n, nA, posA, costA, playerA, q);
     return true;
 }
 

@@ -1872,37 +1872,148 @@ struct SeatRolloutArgs {
     int32_t* seats;        // per-lane learners (or NULL: `learner` for every lane)
     int32_t* seat_record;  // [steps][lanes] learner of each cycle, or NULL
     int32_t draw;          // re-draw a lane's seat from its next episode root
+    int32_t resume;        // second pass: each game starts at its out.progress cycle
     nanorts_rollout_results out;
     uint32_t step_keys[2 * kRolloutChunk];  // fold_in(sample_key, step0 + t0 + t), host-computed
 };
 
-// 168 VGPRs at most: three waves per SIMD, which the bot region's LDS allows
-// on boards up to 16x16
-__global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
+// The carry rows of env l into the bot region through the slot window: the
+// window's C units' rows (row stride C + shift), their target and base
+// slots mapped to block slots.  False when the carry does not fit: a target
+// or base outside [-1, E + 2 shift) or in a gap, or a row past the window
+// that is not empty (kind, the int32 rows and unit_type -1, trained 0),
+// which the full block would settle.
+template <int TW>
+NR_DEV bool load_carry_window(const KGame& g, Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry, int lane) {
+    const int32_t C = g.C, sh = g.shift, N = g.N, E = g.E;
+    const int64_t row = l * (int64_t)(C + sh);
+    bool bad = false;
+    for (int32_t i = lane; i < C + sh; i += TW) {
+        const int64_t at = row + i;
+        int32_t v[9];
+#pragma unroll
+        for (int f = 0; f < 9; ++f) v[f] = carry.row[f][at];
+        const uint8_t trained = carry.trained[at] ? 1 : 0;
+        if (i >= C) {
+            // past the window: must already be the empty row
+            bool empty = trained == 0;
+#pragma unroll
+            for (int f = 0; f < 9; ++f) empty = empty && v[f] == kAbsent;
+            if (!empty) bad = true;
+            continue;
+        }
+#pragma unroll
+        for (int f = 3; f <= 5; f += 2) {  // target (row 3) and base (row 5) are slots
+            const int32_t s = v[f];
+            if (s >= N + C + sh && s < E + sh) v[f] = s - sh;
+            else if (s < -1 || s >= N + C) bad = true;
+        }
+        bv<int8_t>(b, y.k_kind)[i] = (int8_t)v[0];
+#pragma unroll
+        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = v[f];
+        bv<int8_t>(b, y.k_utype)[i] = (int8_t)v[8];
+        bv<uint8_t>(b, y.k_trained)[i] = trained;
+    }
+    int32_t next_order = 0;
+    if (lane == 0) next_order = __builtin_nontemporal_load(carry.next_order + l);
+    b.next_order = tread<TW>(next_order, 0);
+    return tballot<TW>(bad) == 0ull;
+}
+
+// The window's carry rows back into env l's carry (target and base slots
+// mapped back); the rows past the window stay as they are (empty).
+template <int TW>
+NR_DEV void store_carry_window(const KGame& g, const Bot& b, const BotLayout& y, int64_t l, const BotCarry& carry,
+                               int lane) {
+    const int64_t row = l * (int64_t)(g.C + g.shift);
+    for (int32_t i = lane; i < g.C; i += TW) {
+        const int64_t at = row + i;
+        carry.row[0][at] = bv<int8_t>(b, y.k_kind)[i];
+#pragma unroll
+        for (int f = 1; f < 8; ++f) {
+            const int32_t v = bv<int32_t>(b, carry_row32(y, f))[i];
+            carry.row[f][at] = (f == 3 || f == 5) && v >= 0 ? glob_slot(g, v) : v;
+        }
+        carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
+        carry.trained[at] = bv<uint8_t>(b, y.k_trained)[i];
+    }
+    if (lane == 0) carry.next_order[l] = b.next_order;
+}
+
+// The cycles of one seat launch.  `First` is the first pass of a two-pass
+// launch (k_seat_rollout_pair): two games per wave (TW = 32) on the slot
+// window (KGame::shift), each game running until a cycle would leave the
+// one-team path (an irregular state, more than 32 available units, more than
+// 64 live slots, a full slot window) or its state or carry does not fit the
+// window; out.progress then records that cycle, and the second pass
+// (k_seat_rollout with `resume`, one game per wave on the full block) runs
+// the rest.  The state and the carry are all a cycle carries, so the split
+// gives the one-pass result.
+template <bool First, int TW = kWave>
+NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
+    static_assert(TW == kWave || First, "half-wave teams run the first pass only");
     const KGame& g = args.g;
     const int64_t lanes = args.lanes;
-    NR_KERNEL_PROLOGUE
-    load_env(g, args.s, l, e, LD_ALL, lane);
-    count_units(g, e, lane);
-    uint32_t ek0 = (uint32_t)uni(e.sc[S_ROOT0]), ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
-    fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+    int32_t t_begin = 0;
+    if (!First && args.resume) {
+        // a workgroup whose games the first pass finished stages nothing
+        extern __shared__ __align__(16) uint8_t nr_lds[];
+        AS3 uint32_t* votes = (AS3 uint32_t*)nr_lds;
+        const int waves = (int)(blockDim.x >> 6);
+        const int64_t l0 = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6);
+        const bool busy = l0 < lanes && args.out.progress[l0] < args.steps;
+        if ((threadIdx.x & (kWave - 1)) == 0) votes[threadIdx.x >> 6] = busy ? 1u : 0u;
+        __syncthreads();
+        uint32_t any = 0u;
+        for (int w = 0; w < waves; ++w) any |= votes[w];
+        __syncthreads();
+        if (any == 0u) return;
+    }
+    NR_TEAM_PROLOGUE(TW)
+    (void)lds;
+    if (!First && args.resume) {
+        t_begin = uni(args.out.progress[l]);
+        if (t_begin >= args.steps) return;
+    }
     const BotArgs& ba = args.bot;
-    int32_t learner = args.seats ? clampi(uni(args.seats[l]), 0, 1) : args.learner;
+    bool fits = true;
+    if (First && g.shift > 0) {
+        fits = load_window_rows<TW>(g, args.s, l, e, lane) && initial_fits_window<TW>(g, lane);
+        load_scalars(args.s, l, e, lane);
+        wave_sync();
+    } else {
+        load_env<TW>(g, args.s, l, e, LD_ALL, lane);
+    }
+    int32_t learner = args.seats ? clampi(tuni<TW>(args.seats[l]), 0, 1) : args.learner;
     Bot b;
     b.base = e.base + ba.y.origin;
     b.player = 1 - learner;
     b.block = g.N + b.player * g.C;
+    // the carry: loaded here for the first pass (through the window, the
+    // identity without one), by the bot's first act otherwise
+    if (First) fits = load_carry_window<TW>(g, b, ba.y, l, ba.carry, lane) && fits;
+    if (fits) count_units<TW>(g, e, lane);
+    uint32_t ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]), ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
+    fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
     const nanorts_rollout_results& out = args.out;
     const Layout& y = g.lay;
     const uint32_t env = (uint32_t)(args.env0 + l);
+    // the state's per-player positions (a slot window's block holds fewer)
+    const int32_t Cg = g.C + g.shift;
     // boards of at most 32 columns: the per-cycle summary (occupancy bitmaps,
     // available list, kept sight bitmaps, packed observation stores), as in
-    // the fused rollout
-    const bool fast = g.fast_obs && g.seen_words == 1 && ((((uintptr_t)out.feature_maps) & 7u) == 0);
+    // the fused rollout (the first pass runs only where this holds)
+    const bool fast = First || (g.fast_obs && g.seen_words == 1 && ((((uintptr_t)out.feature_maps) & 7u) == 0));
     // the summary's counts stay in registers from one cycle into the next
     SlotSummary sm = {0, 0, 0, 0, false};
-    if (fast) sm = summarize(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
-    for (int32_t t = 0; t < args.steps; ++t) {
+    if (fast && fits) sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
+    if (!fits) sm.full = true;
+    int32_t stop = args.steps;  // first pass: the first cycle left to the second
+    for (int32_t t = t_begin; t < args.steps; ++t) {
+        if (First && (sm.irregular || sm.full || sm.nav > TW || sm.nlive > (TW == kWave ? kWave : 2 * TW))) {
+            stop = t;
+            break;
+        }
         const int64_t tt = (int64_t)args.t0 + t;
         if (args.seat_record && lane == 0) args.seat_record[tt * lanes + l] = learner;
         // the learner: masks -> sample -> decode (unavailable rows absent)
@@ -1910,30 +2021,31 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         const AS3 int16_t* av = at<int16_t>(e, y.a_av);
         if (fast) {
             const int32_t n = sm.nav;
-            mark_unavailable(g, e, lane);
+            mark_unavailable<TW>(g, e, lane);
             // (no unit to sample: no balance read)
-            const Affordable aff = n > 0 ? affordable_types(g, hdr, e, lane) : Affordable{{0u, 0u}};
-            // both threefry blocks of a position on two lanes when n <= 32
-            const bool paired = n <= kWave / 2;
+            const Affordable aff = n > 0 ? affordable_types<TW>(g, hdr, e, lane) : Affordable{{0u, 0u}};
+            // both threefry blocks of a position on two lanes when n <= TW / 2
+            const bool paired = n <= TW / 2;
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
             if (paired && n > 0) {
                 const int32_t u = lane >> 1;
-                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)av[u] : 0u) + (uint32_t)(lane & 1);
+                uint32_t dx0 = env, dx1 = 2u * (u < n ? (uint32_t)glob_pos(g, av[u]) : 0u) + (uint32_t)(lane & 1);
                 threefry(ke0, ke1, dx0, dx1);
-                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, kWave);
-                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, kWave);
-                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, kWave);
-                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, kWave);
+                pw0 = (uint32_t)__shfl((int)dx0, 2 * lane, TW);
+                pw1 = (uint32_t)__shfl((int)dx1, 2 * lane, TW);
+                pw2 = (uint32_t)__shfl((int)dx0, 2 * lane + 1, TW);
+                pw3 = (uint32_t)__shfl((int)dx1, 2 * lane + 1, TW);
             }
-            for (int32_t i = lane; i < n; i += kWave) {
+            for (int32_t i = lane; i < n; i += TW) {
                 const int32_t p = av[i];
                 if ((p >= g.C ? 1 : 0) != learner) continue;  // positions below 2C
                 uint32_t words[4] = {pw0, pw1, pw2, pw3};
                 if (!paired) {
+                    const uint32_t pg = (uint32_t)glob_pos(g, p);
                     words[0] = env;
-                    words[1] = 2u * (uint32_t)p;
+                    words[1] = 2u * pg;
                     words[2] = env;
-                    words[3] = 2u * (uint32_t)p + 1u;
+                    words[3] = 2u * pg + 1u;
                     threefry(ke0, ke1, words[0], words[1]);
                     threefry(ke0, ke1, words[2], words[3]);
                 }
@@ -1952,7 +2064,7 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
                         if (g.T <= 8) sample_row_words8(g, r, words, act);
                         else sample_row_words(g, r, words, act);
                         if (out.actions) {
-                            int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
+                            int32_t* dst = out.actions + ((tt * lanes + l) * Cg + (p - learner * g.C)) * 7;
 #pragma unroll
                             for (int f = 0; f < 7; ++f) dst[f] = act[f];
                         }
@@ -1966,33 +2078,36 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
                 at<int32_t>(e, y.c_none)[p] = none;
             }
         }
-        bool irregular = false;
-        const int32_t n = fast ? 0 : compact_available(g, e, lane, &irregular);
-        if (!fast) build_bitmaps(g, hdr, e, lane);
-        for (int32_t i = lane; i < n; i += kWave) {
-            const int32_t p = av[i];
-            if (p / g.C != learner) continue;
-            const Row r = legality_row_bm(g, hdr, e, g.N + p);
-            uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
-            threefry(ke0, ke1, w0, w1);
-            threefry(ke0, ke1, w2, w3);
-            uint32_t words[4] = {w0, w1, w2, w3};
-            int32_t act[7];
-            if (g.T <= 8) sample_row_words8(g, r, words, act);
-            else sample_row_words(g, r, words, act);
-            if (out.actions) {
-                int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
+        if constexpr (!First) {
+            bool irregular = false;
+            const int32_t n = fast ? 0 : compact_available(g, e, lane, &irregular);
+            if (!fast) build_bitmaps(g, hdr, e, lane);
+            for (int32_t i = lane; i < n; i += kWave) {
+                const int32_t p = av[i];
+                if (p / g.C != learner) continue;
+                const Row r = legality_row_bm(g, hdr, e, g.N + p);
+                uint32_t w0 = env, w1 = 2u * (uint32_t)p, w2 = env, w3 = 2u * (uint32_t)p + 1u;
+                threefry(ke0, ke1, w0, w1);
+                threefry(ke0, ke1, w2, w3);
+                uint32_t words[4] = {w0, w1, w2, w3};
+                int32_t act[7];
+                if (g.T <= 8) sample_row_words8(g, r, words, act);
+                else sample_row_words(g, r, words, act);
+                if (out.actions) {
+                    int32_t* dst = out.actions + ((tt * lanes + l) * g.C + (p - learner * g.C)) * 7;
 #pragma unroll
-                for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                    for (int f = 0; f < 7; ++f) dst[f] = act[f];
+                }
+                decode_row(g, e, p, true, act);
             }
-            decode_row(g, e, p, true, act);
         }
         if (out.actions) {
-            // unavailable rows sample all zeros
-            for (int32_t i = lane; i < g.C; i += kWave) {
+            // unavailable rows sample all zeros (a slot window's gap holds no
+            // unit)
+            for (int32_t i = lane; i < Cg; i += TW) {
                 const int32_t sl = g.N + learner * g.C + i;
-                if (e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
-                int32_t* dst = out.actions + ((tt * lanes + l) * g.C + i) * 7;
+                if (i < g.C && e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
+                int32_t* dst = out.actions + ((tt * lanes + l) * Cg + i) * 7;
 #pragma unroll
                 for (int f = 0; f < 7; ++f) dst[f] = 0;
             }
@@ -2000,9 +2115,10 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         wave_sync();
         // the bot's rows
         // the carry stays in LDS between cycles: loaded once, settled in place
-        const int32_t kept = bot_act(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane, t == 0);
+        const int32_t kept = bot_act<TW>(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane,
+                                         !First && t == t_begin);
         const int32_t top = (1 << g.rank_bits) - 1;
-        for (int32_t i = lane; i < g.C; i += kWave) {
+        for (int32_t i = lane; i < g.C; i += TW) {
             const int32_t p = b.player * g.C + i;
             int32_t v[6];
             unit_command(g, e, b, ba.y, i, kept, v);
@@ -2013,15 +2129,20 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(v[4], g.T);
             at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(v[5] == kAbsent ? 0 : v[5], 0, top);
         }
-        settle_carry(g, b, ba.y, l, ba.carry, lane, false);
+        settle_carry<TW>(g, b, ba.y, l, ba.carry, lane, false);
         wave_sync();
         if (fast) {
             // the env-path admission: the learner and the bot command exactly
             // their available units.  The bot's region lay over the summary's
             // lists, so the available positions are listed again.
-            const int32_t nav = list_available(g, e, lane);
-            if (!admit_env(g, hdr, e, lane, ek0, ek1, false, nav, sm.irregular, false))
-                admit(g, hdr, e, lane, ek0, ek1, false);
+            const int32_t nav = list_available<TW>(g, e, lane);
+            if constexpr (First) {
+                // (the cycle's check above keeps the first pass on this path)
+                admit_env<TW>(g, hdr, e, lane, ek0, ek1, false, nav, sm.irregular, false);
+            } else {
+                if (!admit_env(g, hdr, e, lane, ek0, ek1, false, nav, sm.irregular, false))
+                    admit(g, hdr, e, lane, ek0, ek1, false);
+            }
         }
         // completion's time and the outcome stay in registers into the
         // finish phase and the observation scalars
@@ -2030,32 +2151,33 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
         if (fast) {
             // the summary's live lanes: the bot, sampling and admission spawn
             // and remove nothing
-            const LiveLanes known = {sm.nlive, sm.live_slot};
-            time = complete(g, hdr, e, lane, false, sm.nlive <= kWave ? known : LiveLanes{-1, 0, 0});
-            oc = decide_counted(e, lane);
+            const LiveLanes known = {sm.nlive, sm.live_slot, sm.live_slot2};
+            const int32_t held = TW == kWave ? kWave : 2 * TW;
+            time = complete<TW>(g, hdr, e, lane, false, sm.nlive <= held ? known : LiveLanes{-1, 0, 0});
+            oc = decide_counted<TW>(e, lane);
         } else {
-            core_step(g, hdr, e, lane, ek0, ek1, false);
+            if constexpr (!First) core_step(g, hdr, e, lane, ek0, ek1, false);
         }
         nanorts_env_results r = {};
         if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
         if (out.dones) r.done = out.dones + tt * lanes;
-        const bool done = finish_step(g, hdr, e, l, lane, args.partial != 0, r, false, false, true,
-                                      fast ? &oc : nullptr, time);
+        const bool done = finish_step<TW, First>(g, hdr, e, l, lane, args.partial != 0, r, false, false, true,
+                                                 fast ? &oc : nullptr, time);
         if (done) {
-            clear_carry_rows(g, b, ba.y, lane);
-            ek0 = (uint32_t)uni(e.sc[S_ROOT0]);
-            ek1 = (uint32_t)uni(e.sc[S_ROOT1]);
-            fold_in(ek0, ek1, (uint32_t)uni(e.sc[S_EPISODE]));
+            clear_carry_rows<TW>(g, b, ba.y, lane);
+            ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]);
+            ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
+            fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
             if (args.seats && args.draw) {
                 learner = episode_seat(ek0, ek1);
                 b.player = 1 - learner;
                 b.block = g.N + b.player * g.C;
             }
             // the published observation is the reset state's
-            time = uni(e.sc[S_TIME]);
-            oc.res0 = uni(e.sc[S_RES0]);
-            oc.res1 = uni(e.sc[S_RES1]);
-            oc.alt = uni(e.sc[S_ALT]);
+            time = tuni<TW>(e.sc[S_TIME]);
+            oc.res0 = tuni<TW>(e.sc[S_RES0]);
+            oc.res1 = tuni<TW>(e.sc[S_RES1]);
+            oc.alt = tuni<TW>(e.sc[S_ALT]);
         }
         const uint32_t d = (uint32_t)(out.depth > 0 ? out.depth : 1), c = (uint32_t)tt;
         const uint32_t ring = (d & (d - 1u)) == 0u ? (c & (d - 1u)) : c % d;
@@ -2071,15 +2193,52 @@ __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
             }
             // the sight bitmaps persist in the event counters' words, which
             // the seat step does not count, when both planes fit there
-            const int32_t kept = 2 * g.H * g.seen_words <= 32 ? y.b_events : -1;
-            sm = summarize(g, hdr, e, lane, args.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr, kept);
+            const int32_t kept_seen = 2 * g.H * g.seen_words <= 32 ? y.b_events : -1;
+            sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, m0, m0 ? m0 + per : nullptr, nullptr, nullptr,
+                               kept_seen);
         } else if (out.feature_maps || out.scalars) {
-            observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
+            if constexpr (!First) observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
-    if (args.steps > 0) store_carry(g, b, ba.y, l, ba.carry, lane);
-    if (args.seats && lane == 0) args.seats[l] = learner;
-    store_env(g, args.s, l, e, lane);
+    if (!First || stop > 0) {
+        if (First) {
+            if (g.shift > 0) store_window_rows<TW>(g, args.s, l, e, lane);
+            else store_env<TW>(g, args.s, l, e, lane);
+            store_carry_window<TW>(g, b, ba.y, l, ba.carry, lane);
+        } else {
+            // (a game resumed in its launch's last cycle has its carry loaded
+            // by the bot's act; one that ran no cycle stores the state only)
+            if (args.steps > t_begin) store_carry<TW>(g, b, ba.y, l, ba.carry, lane);
+            store_env<TW>(g, args.s, l, e, lane);
+        }
+    }
+    if (lane == 0) {
+        if (args.seats && (!First || stop > 0)) args.seats[l] = learner;
+        if (First) args.out.progress[l] = stop;
+        else if (!args.resume && args.out.progress) args.out.progress[l] = 0;
+    }
+}
+
+// 168 VGPRs at most: three waves per SIMD, which the bot region's LDS allows
+// on boards up to 16x16
+// The argument struct read in place from the kernel-argument segment (the
+// step keys are indexed by the cycle, which would otherwise copy the whole
+// struct into scratch memory).
+typedef const __attribute__((address_space(4))) SeatRolloutArgs* SeatRolloutArgsArg;
+NR_DEV const SeatRolloutArgs& seat_args() {
+    SeatRolloutArgsArg p = (SeatRolloutArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    return *(const SeatRolloutArgs*)p;
+}
+
+__global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
+    (void)args;
+    seat_cycles<false>(seat_args());
+}
+
+// The seat rollout's first pass: two games per wave on the slot window.
+__global__ __launch_bounds__(256, 3) void k_seat_rollout_pair(SeatRolloutArgs args) {
+    (void)args;
+    seat_cycles<true, 32>(seat_args());
 }
 
 // GridNet decode_actions (N/adapters/gridnet/actions.py:31-52) into Commands.
@@ -3616,6 +3775,41 @@ int nanorts_amd_gridnet_step_against(void* stream, const nanorts_game* game, nan
     return launch(k_gridnet_step, sh, lanes, (hipStream_t)stream, state, gy, actions, commands, 1, results);
 }
 
+// The seat rollout's first pass (k_seat_rollout_pair): the bot's layout on
+// the slot-window game, two games per wave, `wpb` waves per workgroup chosen
+// for the most games per CU at three waves per SIMD (the kernel's register
+// bound).  False where it would hold no more games per CU than the full
+// block's one-game-per-wave pass, or the board has no packed observation.
+static bool seat_pair_shape(const nanorts_game* game, int32_t strategy, int32_t trained_type,
+                            const nanorts_abstract_actions& carry, const Shape& full, Shape* out, BotArgs* a) {
+    std::string why;
+    int32_t shift = 0;
+    const nanorts_game w = windowed(game, &shift);
+    if (!bot_args(&w, out, a, strategy, trained_type, carry, &why)) return false;
+    KGame& g = out->g;
+    if (!g.fast_obs || g.seen_words != 1) return false;
+    g.shift = shift;
+    if (shift > 0) g.nseg = 0;
+    const Layout& y = g.lay;
+    int best = 0, best_w = 0;
+    for (int wv = 1; wv <= 4; ++wv) {
+        const int32_t bytes = y.hdr_bytes + 2 * wv * y.env_bytes;
+        if (bytes > lds_per_cu()) continue;
+        const int32_t by_lds = lds_per_cu() / lds_granule(bytes);
+        const int32_t by_waves = (4 * 3) / wv;
+        const int games = (by_lds < by_waves ? by_lds : by_waves) * 2 * wv;
+        if (games >= best) {
+            best = games;
+            best_w = wv;
+        }
+    }
+    const int32_t full_games = games_per_cu(full.g.lay, full.wpb, 3);
+    if (best_w == 0 || best <= full_games) return false;
+    out->wpb = best_w;
+    out->lds = y.hdr_bytes + 2 * best_w * y.env_bytes;
+    return true;
+}
+
 static int seat_rollout(void* stream, const nanorts_game* game, nanorts_state state, int64_t lanes, int32_t strategy,
                         int32_t trained_type, int32_t learner, int32_t* seats, int32_t draw, int32_t* seat_record,
                         nanorts_abstract_actions carry, const uint32_t* sample_key, int32_t step0, int32_t steps,
@@ -3634,6 +3828,16 @@ static int seat_rollout(void* stream, const nanorts_game* game, nanorts_state st
     if (lanes <= 0 || steps == 0) return NANORTS_OK;
     const int64_t blocks = (lanes + sh.wpb - 1) / sh.wpb;
     if (blocks > 0x7fffffff) return fail(NANORTS_INVALID_ARGUMENT, "too many lanes for one launch");
+    // two passes when the caller gives the work words (results.progress) and
+    // the first pass holds more games per CU; NANORTS_AMD_FIRST_PASS=lean
+    // keeps the one pass
+    Shape ps;
+    BotArgs pa;
+    const char* mode = std::getenv("NANORTS_AMD_FIRST_PASS");
+    const bool paired = results.progress != nullptr && (((uintptr_t)results.feature_maps) & 7u) == 0 &&
+                        !(mode && std::strcmp(mode, "lean") == 0) &&
+                        seat_pair_shape(game, strategy, trained_type, carry, sh, &ps, &pa);
+    const int64_t pair_blocks = paired ? (lanes + 2 * ps.wpb - 1) / (2 * ps.wpb) : 0;
     for (int32_t t0 = 0; t0 < steps; t0 += kRolloutChunk) {
         SeatRolloutArgs args;
         std::memset(&args, 0, sizeof(args));
@@ -3655,6 +3859,15 @@ static int seat_rollout(void* stream, const nanorts_game* game, nanorts_state st
             host_fold_in(k0, k1, (uint32_t)(step0 + t0 + t));
             args.step_keys[2 * t] = k0;
             args.step_keys[2 * t + 1] = k1;
+        }
+        if (paired) {
+            args.g = ps.g;
+            args.bot = pa;
+            hipLaunchKernelGGL(k_seat_rollout_pair, dim3((unsigned)pair_blocks), dim3((unsigned)(kWave * ps.wpb)),
+                               (size_t)ps.lds, (hipStream_t)stream, args);
+            args.g = sh.g;
+            args.bot = a;
+            args.resume = 1;
         }
         hipLaunchKernelGGL(k_seat_rollout, dim3((unsigned)blocks), dim3((unsigned)(kWave * sh.wpb)), (size_t)sh.lds,
                            (hipStream_t)stream, args);

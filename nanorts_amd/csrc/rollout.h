@@ -703,15 +703,16 @@ NR_DEV SlotSummary summarize(const KGame& g, const Hdr& h, const Env& e, int lan
 
 // The available owned positions in slot order (the summary's list, again,
 // for a state the summary already saw); returns their count.
+template <int TW = kWave>
 NR_DEV int32_t list_available(const KGame& g, const Env& e_in, int lane) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     AS3 int16_t* av = at<int16_t>(e, g.lay.a_av);
     int32_t n = 0;
-    for (int32_t base = 0; base < 2 * g.C; base += kWave) {
+    for (int32_t base = 0; base < 2 * g.C; base += TW) {
         const int32_t p = base + lane;
         const bool available = p < 2 * g.C && e.birth[g.N + p] != kAbsent && e.pkind[g.N + p] == kAbsent;
-        const uint64_t m = ballot(available);
-        if (available) av[n + count_below(m)] = (int16_t)p;
+        const uint64_t m = tballot<TW>(available);
+        if (available) av[n + tcount_below<TW>(m)] = (int16_t)p;
         n += popc(m);
     }
     wave_sync();
@@ -719,12 +720,13 @@ NR_DEV int32_t list_available(const KGame& g, const Env& e_in, int lane) {
 }
 
 // Commands of the positions the summary did not list as available.
+template <int TW = kWave>
 NR_DEV void mark_unavailable(const KGame& g, const Env& e_in, int lane) {
-    const Env e = refresh(g, e_in);
+    const Env e = refresh<TW>(g, e_in);
     const Layout& y = g.lay;
     AS3 int8_t* ckind = at<int8_t>(e, y.c_kind);
     AS3 int16_t* crank = at<int16_t>(e, y.c_rank);
-    for (int32_t p = lane; p < 2 * g.C; p += kWave) {
+    for (int32_t p = lane; p < 2 * g.C; p += TW) {
         const int32_t s = g.N + p;
         if (!(e.birth[s] != kAbsent && e.pkind[s] == kAbsent)) ckind[p] = (int8_t)kAbsent;
         crank[p] = 0;

@@ -146,16 +146,37 @@ def test_seat_rollout_matches_oracle(case):
     assert ended >= L  # every env finished at least one episode
 
 
+def _first_pass(monkeypatch, mode: str) -> None:
+    """The seat rollout's first pass: "auto" (two games per wave on the slot
+    window where that holds more games per CU) or "lean" (one pass, one game
+    per wave on the full block)."""
+    if mode == "auto":
+        monkeypatch.delenv("NANORTS_AMD_FIRST_PASS", raising=False)
+    else:
+        monkeypatch.setenv("NANORTS_AMD_FIRST_PASS", mode)
+
+
+def _poison_allocator(nbytes: int) -> None:
+    """A sentinel in the next allocations' memory (see test_gpu_parity)."""
+    import torch
+
+    junk = torch.full((nbytes // 4,), 0x4D4D4D4D, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    del junk
+
+
 @pytest.mark.parametrize("case", list(SEAT_CASES))
-def test_fused_seat_rollout_matches_oracle(case):
+@pytest.mark.parametrize("first_pass", ["auto", "lean"])
+def test_fused_seat_rollout_matches_oracle(case, first_pass, monkeypatch):
     """The fused seat rollout (learner sampled in the kernel) over whole
     episodes against the oracle's seat steps on the same sampler: per-cycle
     rewards and dones, the learner's recorded actions, the last observation,
-    the final state and carry."""
+    the final state and carry, with each first pass."""
     import torch
 
     from nanorts_amd.bots import SeatState
 
+    _first_pass(monkeypatch, first_pass)
     game, partial, bot = _game(case)
     o = Oracle(game)
     C = game.bucket.per_player_capacity
@@ -167,6 +188,7 @@ def test_fused_seat_rollout_matches_oracle(case):
     sst = SeatState(to_device(seat.env, st), _carry_to_device(carry, seat.device),
                     torch.zeros(L, dtype=torch.int32, device=seat.device))
     key = (41, 43)
+    _poison_allocator(steps * L * C * 7 * 4 + (64 << 20))
     got = seat.rollout(sst, steps, key, record_actions=True)
     rewards, dones, actions = (got[k].cpu().numpy() for k in ("rewards", "dones", "actions"))
     for t in range(steps):
@@ -179,3 +201,48 @@ def test_fused_seat_rollout_matches_oracle(case):
     _assert_carry_equal(carry, _carry_to_host(sst.carry), f"{case} final carry")
     np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
     np.testing.assert_array_equal(got["scalars"][0].cpu().numpy(), want["scalars"])
+
+
+@pytest.mark.parametrize("bot", [WORKER_RUSH, BARRACKS_RUSH])
+def test_seat_two_pass_hands_games_to_the_second_pass(bot):
+    """The seat rollout's first pass (two games per wave on a 32-slot window
+    of each player's 70 slots) runs a game until a unit could spawn past its
+    window, or a cycle leaves the one-team path; the second pass runs the rest
+    with the carry the first stored.  Learner games (player 0) that start with
+    22..38 live slots, the added Workers all the learner's and 200 resources
+    each, cross at cycle 0, part-way through the launch, or never, and match
+    the oracle's seat steps cycle by cycle, with the final state and carry."""
+    import torch
+
+    from nanorts_amd.bots import SeatState
+    from tests.test_gpu_parity import _packed
+
+    game = map_name_to_scenario("basesWorkers16x16", conflict_strategy="CANCEL_RANDOM", max_cycles=3000)
+    partial = True
+    base = int((_packed(game, [0])["birth"][0] != -1).sum())
+    st = _packed(game, [22 - base + k for k in range(17)], alternate=False)
+    st["player_resources"][:] = 200
+    o = Oracle(game)
+    assert (o.violations(st) == 0).all()
+    L, C, steps = st["birth"].shape[0], game.bucket.per_player_capacity, 128
+    carry = empty_carry(L, C)
+    seat = _seat_env(game, partial, bot)
+    sst = SeatState(to_device(seat.env, st), _carry_to_device(carry, seat.device),
+                    torch.zeros(L, dtype=torch.int32, device=seat.device))
+    key = (41, 43)
+    got = seat.rollout(sst, steps, key, record_actions=True)
+    first = got["first_pass_cycles"].cpu().numpy()
+    print("first-pass cycles per game:", first.tolist(), flush=True)
+    assert (first == 0).any()
+    assert ((first > 0) & (first < steps)).any()
+    assert (first == steps).any()
+    rewards, dones, actions = (got[k].cpu().numpy() for k in ("rewards", "dones", "actions"))
+    for t in range(steps):
+        want_actions = _learner_actions(o, st, t)
+        np.testing.assert_array_equal(actions[t], want_actions, err_msg=f"actions at cycle {t}")
+        want = o.seat_step(st, carry, bot, LIGHT, 0, want_actions, partial, observe=t == steps - 1)
+        np.testing.assert_array_equal(rewards[t], want["reward"], err_msg=f"cycle {t}")
+        np.testing.assert_array_equal(dones[t], want["done"].astype(bool), err_msg=f"cycle {t}")
+    assert_states_equal(st, to_host(sst.environment_state), "final state")
+    _assert_carry_equal(carry, _carry_to_host(sst.carry), "final carry")
+    np.testing.assert_array_equal(got["feature_maps"][0].cpu().numpy(), want["feature_maps"])
