@@ -1057,9 +1057,13 @@ NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lan
 // translate's plan and walk.  Returns how many desires the walk keeps; commands come from
 // unit_command and the carry from settle_carry.
 template <int TW = kWave>
-NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e, Bot& b, const BotLayout& y, int64_t l,
+NR_DEV int32_t bot_act(const KGame& g, const Hdr& h, const Env& e_in, Bot& b, const BotLayout& y, int64_t l,
                        const BotCarry& carry, int32_t strategy, int32_t trained_type, int lane,
                        bool load_carry = true) {
+    // the block's pointers rebuilt here rather than held across the caller's
+    // phases
+    const Env e = refresh<TW>(g, e_in);
+    b.base = e.base + y.origin;
     bot_begin<TW>(g, h, e, b, y, l, carry, lane, load_carry);
     if (strategy == kWorkerRush) worker_rush<TW>(g, h, e, b, y, lane);
     else barracks_rush<TW>(g, h, e, b, y, trained_type, lane);

@@ -159,6 +159,14 @@ NR_DEV int32_t floor_mod(int32_t a, int32_t b) {
     return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
 }
 NR_DEV int32_t gidx(int32_t i, int32_t n) { return clampi(i < 0 ? i + n : i, 0, n - 1); }
+// A zero the compiler cannot see through.  Wide stores of constant zeros
+// inside a loop otherwise keep a register per stored word holding zero
+// across the whole loop.
+NR_DEV int32_t opaque_zero() {
+    int32_t z = 0;
+    asm volatile("" : "+v"(z));
+    return z;
+}
 // floor_mod / floor_div of a cell index by the board width
 NR_DEV int32_t cell_x(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c & (g.W - 1)) : floor_mod(c, g.W); }
 NR_DEV int32_t cell_y(const KGame& g, int32_t c) { return g.wshift >= 0 ? (c >> g.wshift) : floor_div(c, g.W); }

@@ -259,13 +259,11 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
         }
     }
     // Sequential conflict resolution over the requests that can conflict.
-    const int32_t bal0 = tuni<TW>(e.sc[S_RES0]), bal1 = tuni<TW>(e.sc[S_RES1]);
     int32_t alt = tuni<TW>(e.sc[S_ALT]);
     // each request's final kind and duration, held in its own lane
     int32_t my_kind = kind1, my_none = none1;
     int32_t posB = 0, costB = 0, playerB = 0, durB = 0, rlB = 0, nB = 0;
     bool liveB = false;
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     const int32_t nconf = popc(conflicting_lanes);
     const int32_t kmax = tmax<TW>(nconf);
     for (int32_t k = 0; k < kmax; ++k) {
@@ -278,7 +276,9 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
         const int32_t rcost = tread<TW>(cost1, li);
         const int32_t rplayer = tread<TW>(player1, li);
         const bool rclaims = claims_position(rkind);
-        const int32_t bal = rplayer ? bal1 : bal0;
+        // (the balances are read here, at the conflict, rather than held in
+        // registers through the loop; admission writes them only after it)
+        const int32_t bal = tuni<TW>(e.sc[S_RES0 + rplayer]);
         // _reservations_conflict (N/core/reservations.py:122-135)
         bool cA = false;
 #pragma unroll
@@ -293,7 +293,7 @@ NR_DEV void admit_resolve(const KGame& g, const Hdr& h, const Env& e, int lane, 
         const uint64_t sm = tballot<TW>(cB);
         int32_t fkind = rkind, fnone = rnone;
         if (anyA || sm != 0ull) {
-            const int32_t same_before = popc(sm & below);
+            const int32_t same_before = tcount_below<TW>(sm);
             bool cancels_req = true, cancels_pend = true;
             if (g.strategy == NANORTS_CANCEL_ALTERNATING) {
                 cancels_req = floor_mod(wadd(alt, same_before), 2) == 0;

@@ -1566,7 +1566,7 @@ NR_DEV Env team_env(const KGame& g, int team) {
     const int lane = team_lane<TW>();                                                   \
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));           \
     const int team = (kWave / TW) * wave + team_half<TW>();                             \
-    const int64_t l = (int64_t)blockIdx.x * ((blockDim.x >> 6) * (kWave / TW)) + team;  \
+    int64_t l = (int64_t)blockIdx.x * ((blockDim.x >> 6) * (kWave / TW)) + team;        \
     if (l >= lanes) return;                                                             \
     const Env e = env_view(g, lds + g.lay.hdr_bytes + team * g.lay.env_bytes);
 
@@ -1781,7 +1781,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
             NR_ROLLOUT_PHASE
             // the summary's live lanes: sampling and admission spawn and
             // remove nothing
-            const LiveLanes known = {sm.nlive, sm.live_slot, sm.live_slot2};
+            const LiveLanes known = summary_live(sm);
             const int32_t held = TW == kWave ? kWave : 2 * TW;  // live slots the lanes hold
             int32_t time = complete<TW>(g, hdr, e, lane, Lean, (fast && sm.nlive <= held) ? known : LiveLanes{-1, 0, 0});
             Outcome oc = decide_counted<TW>(e, lane);
@@ -1940,6 +1940,33 @@ NR_DEV void store_carry_window(const KGame& g, const Bot& b, const BotLayout& y,
     if (lane == 0) carry.next_order[l] = b.next_order;
 }
 
+// The argument struct read in place from the kernel-argument segment (the
+// step keys are indexed by the cycle, which would otherwise copy the whole
+// struct into scratch memory).  The seat kernels take the struct as their
+// one argument.
+typedef const __attribute__((address_space(4))) SeatRolloutArgs* SeatRolloutArgsArg;
+NR_DEV const SeatRolloutArgs& seat_args() {
+    SeatRolloutArgsArg p = (SeatRolloutArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    return *(const SeatRolloutArgs*)p;
+}
+// The same through an opaque copy of the segment pointer: the fields used
+// after this call are loaded again (scalar loads) rather than held in scalar
+// registers from the start of the kernel.
+NR_DEV const SeatRolloutArgs& seat_args_again() {
+    SeatRolloutArgsArg p = (SeatRolloutArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const SeatRolloutArgs*)p;
+}
+
+// The step key of the block's episode, fold_in(env root, episode), read
+// from its scalars (which change only when the game resets).
+template <int TW = kWave>
+NR_DEV void episode_key(const Env& e, uint32_t& k0, uint32_t& k1) {
+    k0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]);
+    k1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
+    fold_in(k0, k1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
+}
+
 // The cycles of one seat launch.  `First` is the first pass of a two-pass
 // launch (k_seat_rollout_pair): two games per wave (TW = 32) on the slot
 // window (KGame::shift), each game running until a cycle would leave the
@@ -1993,8 +2020,6 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
     // identity without one), by the bot's first act otherwise
     if (First) fits = load_carry_window<TW>(g, b, ba.y, l, ba.carry, lane) && fits;
     if (fits) count_units<TW>(g, e, lane);
-    uint32_t ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]), ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
-    fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
     const nanorts_rollout_results& out = args.out;
     const Layout& y = g.lay;
     const uint32_t env = (uint32_t)(args.env0 + l);
@@ -2009,21 +2034,38 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
     if (fast && fits) sm = summarize<TW>(g, hdr, e, lane, args.partial != 0, nullptr, nullptr, nullptr, nullptr);
     if (!fits) sm.full = true;
     int32_t stop = args.steps;  // first pass: the first cycle left to the second
+    // Each part of a cycle rebuilds the block's row pointers from the block
+    // base (refresh) and the game's addresses from an opaque copy of its
+    // index, and the episode key and the bot's rows are derived again where
+    // they are used, so that they are not held in registers across the
+    // cycle: a half-wave team holds each of them in a vector register.
+    const Env& e_in = e;
     for (int32_t t = t_begin; t < args.steps; ++t) {
         if (First && (sm.irregular || sm.full || sm.nav > TW || sm.nlive > (TW == kWave ? kWave : 2 * TW))) {
             stop = t;
             break;
         }
+        if constexpr (TW != kWave) asm volatile("" : "+v"(l));
+        // the game's fields loaded again in each cycle (scalar loads) rather
+        // than held in scalar registers across the loop
+        const KGame& g = fresh_game();
+        const Layout& y = g.lay;
+        b.player = 1 - learner;
+        b.block = g.N + b.player * g.C;
         const int64_t tt = (int64_t)args.t0 + t;
         if (args.seat_record && lane == 0) args.seat_record[tt * lanes + l] = learner;
         // the learner: masks -> sample -> decode (unavailable rows absent)
         const uint32_t ke0 = args.step_keys[2 * t], ke1 = args.step_keys[2 * t + 1];
-        const AS3 int16_t* av = at<int16_t>(e, y.a_av);
         if (fast) {
+            const Env e = refresh<TW>(g, e_in);
+            const AS3 int16_t* av = at<int16_t>(e, y.a_av);
             const int32_t n = sm.nav;
             mark_unavailable<TW>(g, e, lane);
-            // (no unit to sample: no balance read)
-            const Affordable aff = n > 0 ? affordable_types<TW>(g, hdr, e, lane) : Affordable{{0u, 0u}};
+            // (no unit to sample: no balance read; only the learner's units
+            // are sampled, so both entries hold its types)
+            const Affordable both = n > 0 ? affordable_types<TW>(g, hdr, e, lane) : Affordable{{0u, 0u}};
+            const uint32_t mine = learner ? both.player[1] : both.player[0];
+            const Affordable aff = {{mine, mine}};
             // both threefry blocks of a position on two lanes when n <= TW / 2
             const bool paired = n <= TW / 2;
             uint32_t pw0 = 0u, pw1 = 0u, pw2 = 0u, pw3 = 0u;
@@ -2079,6 +2121,7 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
             }
         }
         if constexpr (!First) {
+            const AS3 int16_t* av = at<int16_t>(e, y.a_av);
             bool irregular = false;
             const int32_t n = fast ? 0 : compact_available(g, e, lane, &irregular);
             if (!fast) build_bitmaps(g, hdr, e, lane);
@@ -2104,20 +2147,24 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
         if (out.actions) {
             // unavailable rows sample all zeros (a slot window's gap holds no
             // unit)
+            const Env e = refresh<TW>(g, e_in);
             for (int32_t i = lane; i < Cg; i += TW) {
                 const int32_t sl = g.N + learner * g.C + i;
                 if (i < g.C && e.birth[sl] != kAbsent && e.pkind[sl] == kAbsent) continue;
                 int32_t* dst = out.actions + ((tt * lanes + l) * Cg + i) * 7;
+                const int32_t z = opaque_zero();
 #pragma unroll
-                for (int f = 0; f < 7; ++f) dst[f] = 0;
+                for (int f = 0; f < 7; ++f) dst[f] = z;
             }
         }
         wave_sync();
         // the bot's rows
         // the carry stays in LDS between cycles: loaded once, settled in place
-        const int32_t kept = bot_act<TW>(g, hdr, e, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane,
+        const int32_t kept = bot_act<TW>(g, hdr, e_in, b, ba.y, l, ba.carry, ba.strategy, ba.trained, lane,
                                          !First && t == t_begin);
         const int32_t top = (1 << g.rank_bits) - 1;
+        {
+        const Env e = refresh<TW>(g, e_in);
         for (int32_t i = lane; i < g.C; i += TW) {
             const int32_t p = b.player * g.C + i;
             int32_t v[6];
@@ -2129,6 +2176,7 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
             at<int8_t>(e, y.c_ptype)[p] = (int8_t)canon_ptype(v[4], g.T);
             at<int16_t>(e, y.c_rank)[p] = (int16_t)clampi(v[5] == kAbsent ? 0 : v[5], 0, top);
         }
+        }
         settle_carry<TW>(g, b, ba.y, l, ba.carry, lane, false);
         wave_sync();
         if (fast) {
@@ -2136,6 +2184,8 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
             // their available units.  The bot's region lay over the summary's
             // lists, so the available positions are listed again.
             const int32_t nav = list_available<TW>(g, e, lane);
+            uint32_t ek0, ek1;
+            episode_key<TW>(refresh<TW>(g, e_in), ek0, ek1);
             if constexpr (First) {
                 // (the cycle's check above keeps the first pass on this path)
                 admit_env<TW>(g, hdr, e, lane, ek0, ek1, false, nav, sm.irregular, false);
@@ -2151,27 +2201,29 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
         if (fast) {
             // the summary's live lanes: the bot, sampling and admission spawn
             // and remove nothing
-            const LiveLanes known = {sm.nlive, sm.live_slot, sm.live_slot2};
+            const LiveLanes known = summary_live(sm);
             const int32_t held = TW == kWave ? kWave : 2 * TW;
             time = complete<TW>(g, hdr, e, lane, false, sm.nlive <= held ? known : LiveLanes{-1, 0, 0});
-            oc = decide_counted<TW>(e, lane);
+            oc = decide_counted<TW>(refresh<TW>(g, e_in), lane);
         } else {
-            if constexpr (!First) core_step(g, hdr, e, lane, ek0, ek1, false);
+            if constexpr (!First) {
+                uint32_t ek0, ek1;
+                episode_key(e, ek0, ek1);
+                core_step(g, hdr, e, lane, ek0, ek1, false);
+            }
         }
         nanorts_env_results r = {};
         if (out.rewards) r.reward = out.rewards + tt * lanes * 2;
         if (out.dones) r.done = out.dones + tt * lanes;
-        const bool done = finish_step<TW, First>(g, hdr, e, l, lane, args.partial != 0, r, false, false, true,
-                                                 fast ? &oc : nullptr, time);
+        const bool done = finish_step<TW, First>(g, hdr, refresh<TW>(g, e_in), l, lane, args.partial != 0, r, false,
+                                                 false, true, fast ? &oc : nullptr, time);
         if (done) {
+            const Env e = refresh<TW>(g, e_in);
             clear_carry_rows<TW>(g, b, ba.y, lane);
-            ek0 = (uint32_t)tuni<TW>(e.sc[S_ROOT0]);
-            ek1 = (uint32_t)tuni<TW>(e.sc[S_ROOT1]);
-            fold_in(ek0, ek1, (uint32_t)tuni<TW>(e.sc[S_EPISODE]));
             if (args.seats && args.draw) {
+                uint32_t ek0, ek1;
+                episode_key<TW>(e, ek0, ek1);
                 learner = episode_seat(ek0, ek1);
-                b.player = 1 - learner;
-                b.block = g.N + b.player * g.C;
             }
             // the published observation is the reset state's
             time = tuni<TW>(e.sc[S_TIME]);
@@ -2200,36 +2252,34 @@ NR_DEV void seat_cycles(const SeatRolloutArgs& args) {
             if constexpr (!First) observe_both(g, hdr, e, slot, lane, args.partial != 0, out.feature_maps, out.scalars);
         }
     }
+    if constexpr (TW != kWave) asm volatile("" : "+v"(l));
+    b.player = 1 - learner;
+    b.block = g.N + b.player * g.C;
+    // (the arguments of the stores read again: `args` is the kernel's
+    // argument struct)
+    const SeatRolloutArgs& fin = seat_args_again();
+    const KGame& gf = fin.g;
     if (!First || stop > 0) {
         if (First) {
-            if (g.shift > 0) store_window_rows<TW>(g, args.s, l, e, lane);
-            else store_env<TW>(g, args.s, l, e, lane);
-            store_carry_window<TW>(g, b, ba.y, l, ba.carry, lane);
+            if (gf.shift > 0) store_window_rows<TW>(gf, fin.s, l, e, lane);
+            else store_env<TW>(gf, fin.s, l, e, lane);
+            store_carry_window<TW>(gf, b, fin.bot.y, l, fin.bot.carry, lane);
         } else {
             // (a game resumed in its launch's last cycle has its carry loaded
             // by the bot's act; one that ran no cycle stores the state only)
-            if (args.steps > t_begin) store_carry<TW>(g, b, ba.y, l, ba.carry, lane);
-            store_env<TW>(g, args.s, l, e, lane);
+            if (fin.steps > t_begin) store_carry<TW>(gf, b, fin.bot.y, l, fin.bot.carry, lane);
+            store_env<TW>(gf, fin.s, l, e, lane);
         }
     }
     if (lane == 0) {
-        if (args.seats && (!First || stop > 0)) args.seats[l] = learner;
-        if (First) args.out.progress[l] = stop;
-        else if (!args.resume && args.out.progress) args.out.progress[l] = 0;
+        if (fin.seats && (!First || stop > 0)) fin.seats[l] = learner;
+        if (First) fin.out.progress[l] = stop;
+        else if (!fin.resume && fin.out.progress) fin.out.progress[l] = 0;
     }
 }
 
 // 168 VGPRs at most: three waves per SIMD, which the bot region's LDS allows
 // on boards up to 16x16
-// The argument struct read in place from the kernel-argument segment (the
-// step keys are indexed by the cycle, which would otherwise copy the whole
-// struct into scratch memory).
-typedef const __attribute__((address_space(4))) SeatRolloutArgs* SeatRolloutArgsArg;
-NR_DEV const SeatRolloutArgs& seat_args() {
-    SeatRolloutArgsArg p = (SeatRolloutArgsArg)__builtin_amdgcn_kernarg_segment_ptr();
-    return *(const SeatRolloutArgs*)p;
-}
-
 __global__ __launch_bounds__(256, 3) void k_seat_rollout(SeatRolloutArgs args) {
     (void)args;
     seat_cycles<false>(seat_args());

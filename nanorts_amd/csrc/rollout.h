@@ -349,8 +349,11 @@ NR_DEV bool sample_unit_w1(const KGame& g, const Hdr& h, const Env& e, int32_t p
 struct SlotSummary {
     int32_t nav, nunits, nA, nlive;
     bool irregular;
-    int32_t live_slot;  // this lane's live slot (live_lanes), for at most a wave of them
-    int32_t live_slot2;  // half-wave teams: its second (live_lanes), for at most two halves of them
+    // this lane's live slot (live_lanes) for at most a wave of them in the
+    // low half, and, for half-wave teams, its second for at most two halves
+    // of them in the high half (slots are below 2^15): one register to carry
+    // into the next cycle
+    int32_t live_slots;
     // slot window (KGame::shift > 0): a unit spawned in the next cycle could
     // land past a player's window (its units plus the units that may spawn
     // one in that cycle exceed C: a pending PRODUCE due then, and, where a
@@ -358,6 +361,11 @@ struct SlotSummary {
     // that produces)
     bool full;
 };
+
+// The live lanes a summary carries (its count and this lane's slots).
+NR_DEV LiveLanes summary_live(const SlotSummary& sm) {
+    return LiveLanes{sm.nlive, (int32_t)(int16_t)(sm.live_slots & 0xffff), sm.live_slots >> 16};
+}
 
 template <int TW = kWave>
 NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in, int lane, bool bitmaps = true) {
@@ -498,8 +506,7 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
     out.nA = tuni<TW>(nA);
     out.nlive = nlive;
     out.irregular = irregular;
-    out.live_slot = ll.slot;
-    out.live_slot2 = ll.slot2;
+    out.live_slots = (int32_t)(((uint32_t)ll.slot & 0xffffu) | ((uint32_t)ll.slot2 << 16));
     out.full = reach0 > g.C || reach1 > g.C;
     return out;
 }
