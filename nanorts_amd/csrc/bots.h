@@ -73,7 +73,7 @@ NR_DEV AS3 T* bv(const Bot& b, int32_t offset) {
     return (AS3 T*)(b.base + offset);
 }
 
-// The LDS offset of int32 carry row f (1..7: unit_birth, order, target,
+// The LDS offset of carry row f (1..7: unit_birth, order, target,
 // target_birth, base, base_birth, cell); rows 0 (kind) and 8 (unit_type)
 // are bytes.
 NR_DEV int32_t carry_row32(const BotLayout& y, int f) {
@@ -86,6 +86,24 @@ NR_DEV int32_t carry_row32(const BotLayout& y, int f) {
         case 6: return y.k_bbirth;
         default: return y.k_cell;
     }
+}
+
+// Carry rows 3, 5 and 7 (target, base, cell: slots and cells, below 2^15)
+// are int16 in the half-wave teams' layout (the seat rollout's first pass,
+// whose load checks that they fit), int32 otherwise.
+template <int TW>
+NR_DEV constexpr bool narrow_row(int f) {
+    return TW != kWave && (f == 3 || f == 5 || f == 7);
+}
+template <int TW = kWave>
+NR_DEV int32_t carry_at(const Bot& b, const BotLayout& y, int f, int32_t i) {
+    if (narrow_row<TW>(f)) return bv<int16_t>(b, carry_row32(y, f))[i];
+    return bv<int32_t>(b, carry_row32(y, f))[i];
+}
+template <int TW = kWave>
+NR_DEV void carry_put(const Bot& b, const BotLayout& y, int f, int32_t i, int32_t v) {
+    if (narrow_row<TW>(f)) bv<int16_t>(b, carry_row32(y, f))[i] = (int16_t)v;
+    else bv<int32_t>(b, carry_row32(y, f))[i] = v;
 }
 
 template <int TW = kWave>
@@ -156,6 +174,7 @@ NR_DEV void closest(const KGame& g, const Env& e, int32_t origin, const AS3 int1
 
 // abstraction.put / _written (N/bots/abstraction.py:172-227) for unit i of
 // this lane; the caller advances next_order by C + 1 once per put.
+template <int TW = kWave>
 NR_DEV void put_unit(const KGame& g, const Bot& b, const Unit& u, int32_t i, bool last, int32_t kind, int32_t target,
                      int32_t tbirth, int32_t base, int32_t bbirth, int32_t cell, int32_t utype, const BotLayout& y) {
     AS3 int8_t* kk = bv<int8_t>(b, y.k_kind);
@@ -164,11 +183,11 @@ NR_DEV void put_unit(const KGame& g, const Bot& b, const Unit& u, int32_t i, boo
     if (!known) bv<int32_t>(b, y.k_order)[i] = wadd(b.next_order, last ? g.C : (int32_t)bv<int16_t>(b, y.u_rank)[i]);
     kk[i] = (int8_t)kind;
     ub[i] = u.birth;
-    bv<int32_t>(b, y.k_target)[i] = target;
+    carry_put<TW>(b, y, 3, i, target);
     bv<int32_t>(b, y.k_tbirth)[i] = tbirth;
-    bv<int32_t>(b, y.k_base)[i] = base;
+    carry_put<TW>(b, y, 5, i, base);
     bv<int32_t>(b, y.k_bbirth)[i] = bbirth;
-    bv<int32_t>(b, y.k_cell)[i] = cell;
+    carry_put<TW>(b, y, 7, i, cell);
     bv<int8_t>(b, y.k_utype)[i] = (int8_t)utype;
     bv<uint8_t>(b, y.k_trained)[i] = 0;
 }
@@ -206,7 +225,7 @@ NR_DEV void bot_begin(const KGame& g, const Hdr& h, const Env& e, Bot& b, const 
         const int64_t at = l * C + i;
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)carry.row[0][at];
 #pragma unroll
-        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = carry.row[f][at];
+        for (int f = 1; f < 8; ++f) carry_put<TW>(b, y, f, i, carry.row[f][at]);
         bv<int8_t>(b, y.k_utype)[i] = (int8_t)carry.row[8][at];
         bv<uint8_t>(b, y.k_trained)[i] = carry.trained[at] ? 1 : 0;
     }
@@ -335,7 +354,7 @@ NR_DEV void build_unless_building(const KGame& g, const Hdr& h, const Env& e, Bo
         const int32_t site = building_site<TW>(g, h, e, b, y, e.cell[b.block + builder], lane);
         if (lane == 0) {
             const Unit u = unit_at(g, e, b, builder);
-            put_unit(g, b, u, builder, false, kAbBuild, kAbsent, kAbsent, kAbsent, kAbsent, site, unit_type, y);
+            put_unit<TW>(g, b, u, builder, false, kAbBuild, kAbsent, kAbsent, kAbsent, kAbsent, site, unit_type, y);
             if (site >= 0 && site < g.cells) set_bit(bv<uint32_t>(b, y.m_reserved), site);
         }
         wave_sync();
@@ -381,12 +400,12 @@ NR_DEV void harvest(const KGame& g, const Env& e, Bot& b, const BotLayout& y, in
         closest(g, e, u.cell, ls, b.n_stock, &ss, &sb);
         const bool carrying = u.carried > 0;
         const bool harvesting = is_entry(b, y, i, u.birth, kAbHarvest);
-        const bool same_base = bv<int32_t>(b, y.k_base)[i] == ss && bv<int32_t>(b, y.k_bbirth)[i] == sb;
-        const bool same_target = bv<int32_t>(b, y.k_target)[i] == rs && bv<int32_t>(b, y.k_tbirth)[i] == rb;
+        const bool same_base = carry_at<TW>(b, y, 5, i) == ss && bv<int32_t>(b, y.k_bbirth)[i] == sb;
+        const bool same_target = carry_at<TW>(b, y, 3, i) == rs && bv<int32_t>(b, y.k_tbirth)[i] == rb;
         const bool occupied = carrying ? ss != kAbsent : (ss != kAbsent && rs != kAbsent);
         const bool unchanged = harvesting && same_base && (carrying || same_target);
         if (occupied && !unchanged)
-            put_unit(g, b, u, i, false, kAbHarvest, carrying ? kAbsent : rs, carrying ? kAbsent : rb, ss, sb, kAbsent,
+            put_unit<TW>(g, b, u, i, false, kAbHarvest, carrying ? kAbsent : rs, carrying ? kAbsent : rb, ss, sb, kAbsent,
                      kAbsent, y);
         if (!occupied) r[i] = (uint8_t)(role | R_IDLE);
     }
@@ -406,7 +425,7 @@ NR_DEV void attack_nearest(const KGame& g, const Env& e, Bot& b, const BotLayout
         const int32_t es = bv<int16_t>(b, y.u_es)[i];
         if (es == kAbsent) continue;
         const Unit u = unit_at(g, e, b, i);
-        put_unit(g, b, u, i, (role & R_LAST) != 0, kAbAttack, es, bv<int32_t>(b, y.u_eb)[i], kAbsent, kAbsent,
+        put_unit<TW>(g, b, u, i, (role & R_LAST) != 0, kAbAttack, es, bv<int32_t>(b, y.u_eb)[i], kAbsent, kAbsent,
                  kAbsent, kAbsent, y);
     }
     b.next_order = wadd(b.next_order, g.C + 1);
@@ -420,7 +439,7 @@ NR_DEV void train_where(const KGame& g, const Env& e, Bot& b, const BotLayout& y
     for (int32_t k = lane; k < b.n_live; k += TW) {
         const int32_t i = bv<int16_t>(b, y.u_live)[k];
         const Unit u = unit_at(g, e, b, i);
-        if (pick(u)) put_unit(g, b, u, i, false, kAbTrain, kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, unit_type, y);
+        if (pick(u)) put_unit<TW>(g, b, u, i, false, kAbTrain, kAbsent, kAbsent, kAbsent, kAbsent, kAbsent, unit_type, y);
     }
     b.next_order = wadd(b.next_order, g.C + 1);
     wave_sync();
@@ -774,9 +793,9 @@ NR_DEV int32_t translate_plan(const KGame& g, const Hdr& h, const Env& e, Bot& b
         const int32_t kind = bv<int8_t>(b, y.k_kind)[i];
         const bool alive = kind != kAbNone && bv<int32_t>(b, y.k_ubirth)[i] == u.birth;
         const bool carrying = u.carried > 0;
-        const int32_t kcell = bv<int32_t>(b, y.k_cell)[i];
-        const int32_t target = bv<int32_t>(b, y.k_target)[i];
-        const int32_t base = bv<int32_t>(b, y.k_base)[i];
+        const int32_t kcell = carry_at<TW>(b, y, 7, i);
+        const int32_t target = carry_at<TW>(b, y, 3, i);
+        const int32_t base = carry_at<TW>(b, y, 5, i);
         const bool built_on = kcell != kAbsent && e.entity[clampi(kcell, 0, g.cells - 1)] != kAbsent;
         const bool target_gone = !exists_slot(g, e, target, bv<int32_t>(b, y.k_tbirth)[i]);
         bool completed = false;
@@ -976,7 +995,7 @@ NR_DEV void store_carry(const KGame& g, const Bot& b, const BotLayout& y, int64_
         const int64_t at = l * g.C + i;
         carry.row[0][at] = bv<int8_t>(b, y.k_kind)[i];
 #pragma unroll
-        for (int f = 1; f < 8; ++f) carry.row[f][at] = bv<int32_t>(b, carry_row32(y, f))[i];
+        for (int f = 1; f < 8; ++f) carry.row[f][at] = carry_at<TW>(b, y, f, i);
         carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
         carry.trained[at] = bv<uint8_t>(b, y.k_trained)[i];
     }
@@ -1017,7 +1036,7 @@ NR_DEV void settle_carry(const KGame& g, Bot& b, const BotLayout& y, int64_t l, 
         } else {
             bv<int8_t>(b, y.k_kind)[i] = (int8_t)kAbsent;
 #pragma unroll
-            for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = kAbsent;
+            for (int f = 1; f < 8; ++f) carry_put<TW>(b, y, f, i, kAbsent);
             bv<int8_t>(b, y.k_utype)[i] = (int8_t)kAbsent;
         }
         bv<uint8_t>(b, y.k_trained)[i] = trained ? 1 : 0;
@@ -1045,7 +1064,7 @@ NR_DEV void clear_carry_rows(const KGame& g, Bot& b, const BotLayout& y, int lan
     for (int32_t i = lane; i < g.C; i += TW) {
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)kAbsent;
 #pragma unroll
-        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = kAbsent;
+        for (int f = 1; f < 8; ++f) carry_put<TW>(b, y, f, i, kAbsent);
         bv<int8_t>(b, y.k_utype)[i] = (int8_t)kAbsent;
         bv<uint8_t>(b, y.k_trained)[i] = 0;
     }

@@ -101,7 +101,10 @@ bool fit_waves(Shape* out, std::string* why) {
     return true;
 }
 
-bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
+// `staging` lays out observe_all's staging in the phase union; a kernel
+// that writes observations from the summary's bitmaps (the seat rollout's
+// first pass) does without it.
+bool shape_for(const nanorts_game* game, Shape* out, std::string* why, bool staging = true) {
     if (!valid_game(game, why)) return false;
     KGame& g = out->g;
     std::memset(&g, 0, sizeof(g));
@@ -240,10 +243,14 @@ bool shape_for(const nanorts_game* game, Shape* out, std::string* why) {
     y.m_tmp = take(C2 * 2);
     if (o > end) end = o;
     // observation staging (observe_all) with its seen bitmaps
-    o = union0;
-    y.v_oseen = take(2 * g.H * g.seen_words * 4);
-    y.v_stage = take(2 * g.stage_cells * 6);
-    if (o > end) end = o;
+    if (staging) {
+        o = union0;
+        y.v_oseen = take(2 * g.H * g.seen_words * 4);
+        y.v_stage = take(2 * g.stage_cells * 6);
+        if (o > end) end = o;
+    } else {
+        y.v_oseen = y.v_stage = -1;
+    }
     // masks staging (k_legality), after the occupancy bitmaps its rows read
     o = y.o_bm;
     take(6 * g.H * g.seen_words * 4);
@@ -498,8 +505,10 @@ bool shape_for_gridnet(const nanorts_game* game, Shape* out, GridLayout* gy, std
 
 // Bot region after each env block (scripted bots, bots.h): the per-wave
 // stride grows by the region, the env offsets stay.
-bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::string* why) {
-    if (!shape_for(game, out, why)) return false;
+// `first_pass` is the seat rollout's first pass (half-wave teams): no
+// observation staging, and the carry's target, base and cell rows as int16.
+bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::string* why, bool first_pass = false) {
+    if (!shape_for(game, out, why, !first_pass)) return false;
     KGame& g = out->g;
     if (g.C > 512) {
         *why = "the scripted bots take at most 512 slots per player";
@@ -563,11 +572,12 @@ bool shape_for_bots(const nanorts_game* game, Shape* out, BotLayout* by, std::st
     if (o < union_end) o = align16(union_end);
     by->k_ubirth = take(4 * C);
     by->k_order = take(4 * C);
-    by->k_target = take(4 * C);
+    const int32_t slot_bytes = first_pass ? 2 : 4;
+    by->k_target = take(slot_bytes * C);
     by->k_tbirth = take(4 * C);
-    by->k_base = take(4 * C);
+    by->k_base = take(slot_bytes * C);
     by->k_bbirth = take(4 * C);
-    by->k_cell = take(4 * C);
+    by->k_cell = take(slot_bytes * C);
     by->k_kind = take(C);
     by->k_utype = take(C);
     by->k_trained = take(C);
@@ -1908,9 +1918,11 @@ NR_DEV bool load_carry_window(const KGame& g, Bot& b, const BotLayout& y, int64_
             if (s >= N + C + sh && s < E + sh) v[f] = s - sh;
             else if (s < -1 || s >= N + C) bad = true;
         }
+        // the cell (row 7) is held as int16 (with the slots)
+        if (v[7] < -32768 || v[7] > 32767) bad = true;
         bv<int8_t>(b, y.k_kind)[i] = (int8_t)v[0];
 #pragma unroll
-        for (int f = 1; f < 8; ++f) bv<int32_t>(b, carry_row32(y, f))[i] = v[f];
+        for (int f = 1; f < 8; ++f) carry_put<TW>(b, y, f, i, v[f]);
         bv<int8_t>(b, y.k_utype)[i] = (int8_t)v[8];
         bv<uint8_t>(b, y.k_trained)[i] = trained;
     }
@@ -1931,7 +1943,7 @@ NR_DEV void store_carry_window(const KGame& g, const Bot& b, const BotLayout& y,
         carry.row[0][at] = bv<int8_t>(b, y.k_kind)[i];
 #pragma unroll
         for (int f = 1; f < 8; ++f) {
-            const int32_t v = bv<int32_t>(b, carry_row32(y, f))[i];
+            const int32_t v = carry_at<TW>(b, y, f, i);
             carry.row[f][at] = (f == 3 || f == 5) && v >= 0 ? glob_slot(g, v) : v;
         }
         carry.row[8][at] = bv<int8_t>(b, y.k_utype)[i];
@@ -3307,7 +3319,7 @@ int nanorts_amd_decode_actions(void* stream, const nanorts_game* game, nanorts_s
 }
 
 static bool bot_args(const nanorts_game* game, Shape* sh, BotArgs* a, int32_t strategy, int32_t trained_type,
-                     const nanorts_abstract_actions& carry, std::string* why) {
+                     const nanorts_abstract_actions& carry, std::string* why, bool first_pass = false) {
     if (strategy != NANORTS_WORKER_RUSH && strategy != NANORTS_BARRACKS_RUSH) {
         *why = "strategy must be NANORTS_WORKER_RUSH or NANORTS_BARRACKS_RUSH";
         return false;
@@ -3317,7 +3329,7 @@ static bool bot_args(const nanorts_game* game, Shape* sh, BotArgs* a, int32_t st
         *why = "a carry (AbstractActions) pointer is NULL";
         return false;
     }
-    if (!shape_for_bots(game, sh, &a->y, why)) return false;
+    if (!shape_for_bots(game, sh, &a->y, why, first_pass)) return false;
     int32_t* rows[9] = {carry.kind, carry.unit_birth, carry.order, carry.target, carry.target_birth,
                         carry.base, carry.base_birth, carry.cell, carry.unit_type};
     for (int f = 0; f < 9; ++f) a->carry.row[f] = rows[f];
@@ -3835,7 +3847,10 @@ static bool seat_pair_shape(const nanorts_game* game, int32_t strategy, int32_t 
     std::string why;
     int32_t shift = 0;
     const nanorts_game w = windowed(game, &shift);
-    if (!bot_args(&w, out, a, strategy, trained_type, carry, &why)) return false;
+    // (the first pass writes observations from the summary's bitmaps: no
+    // observation staging in its union; its carry rows of slots and cells
+    // are int16)
+    if (!bot_args(&w, out, a, strategy, trained_type, carry, &why, true)) return false;
     KGame& g = out->g;
     if (!g.fast_obs || g.seen_words != 1) return false;
     g.shift = shift;
