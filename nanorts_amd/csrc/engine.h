@@ -1630,9 +1630,11 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
                 rank += (oj < ord) || (oj == ord && j < lane);
             }
         } else {
-            // both halves' lanes in one scalar loop over the live lanes
-            const int32_t top = tmax<TW>(nlive);
-            for (int32_t j = 0; j < top; ++j) {
+            // both halves' members in one scalar loop: the lanes that are a
+            // member in either half (a lane's own half counts only its own)
+            const uint64_t both = (uint64_t)__ballot(acting);
+            for (uint32_t m = (uint32_t)both | (uint32_t)(both >> 32); m != 0u; m &= m - 1u) {
+                const int32_t j = (int32_t)__builtin_ctz(m);
                 const int32_t oj = tread_at<TW>(ord, j);
                 rank += ((members >> j) & 1ull) && ((oj < ord) || (oj == ord && j < lane));
             }
