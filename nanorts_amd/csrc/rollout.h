@@ -477,7 +477,21 @@ NR_DEV SlotSummary summarize_slots(const KGame& g, const Hdr& h, const Env& e_in
         if (available) av[nav + tcount_below<TW>(ma)] = (int16_t)(s - g.N);
         nav += popc(ma);
         const uint64_t mu = tballot<TW>(unit);
-        if (unit) units[nunits + tcount_below<TW>(mu)] = (int16_t)s;
+        if (unit) {
+            int32_t item = s;
+            if (g.H <= 32 && g.seen_words == 1) {
+                // what the sight pass reads, packed (boards of at most 32
+                // columns and rows, sight radii below 31): column, row,
+                // radius + 1 (0: none) and player
+                const int32_t c = e.cell[s];
+                const int32_t cy = cell_y(g, c), cx = c - cy * g.W;
+                const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
+                const int32_t r1 = r < 0 ? 0 : r + 1;
+                item = (int32_t)((uint32_t)cx | ((uint32_t)cy << 5) | ((uint32_t)r1 << 10) |
+                                 ((s - g.N) >= g.C ? 0x8000u : 0u));
+            }
+            units[nunits + tcount_below<TW>(mu)] = (int16_t)item;
+        }
         nunits += popc(mu);
         if (g.shift > 0) {
             // each unit, and once more each that may spawn one this cycle
@@ -540,15 +554,16 @@ NR_DEV void summarize_visibility(const KGame& g, const Hdr& h, const Env& e_in, 
         for (int32_t base = first; base < last; base += U) {
             const int32_t i = base + k;
             if (k >= U || i >= nunits) continue;
-            const int32_t s = units[i];
-            const int32_t r = tabv(h, F_SIGHT, gidx(e.utype[s], g.T));
-            const int32_t cell = e.cell[s];
-            const int32_t dy = row - cell_y(g, cell);
+            // the unit's column, row, sight radius and player, as the slot
+            // pass packed them
+            const uint32_t v = (uint16_t)units[i];
+            const int32_t r = (int32_t)((v >> 10) & 31u) - 1;
+            const int32_t dy = row - (int32_t)((v >> 5) & 31u);
             if (dy < -r || dy > r) continue;
             const uint32_t m = h.disk[r * span + dy + R];
-            const int32_t x0 = cell_x(g, cell) - R;  // in [-R, W - 1]: 32-bit shifts
+            const int32_t x0 = (int32_t)(v & 31u) - R;  // in [-R, W - 1]: 32-bit shifts
             const uint32_t bits = (x0 >= 0 ? m << x0 : m >> (-x0)) & rowmask;
-            if ((s - g.N) >= g.C) acc1 |= bits;
+            if (v & 0x8000u) acc1 |= bits;
             else acc0 |= bits;
         }
         for (int32_t j = 1; j < U; ++j) {
