@@ -1619,6 +1619,32 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             }
         }
         wave_sync();
+        // A cycle whose members all MOVE (and no records): their turns taken
+        // at once.  A move's destination was free when it was issued and has
+        // been claimed since (admission), so no member enters a cell that
+        // another enters or vacates, and no move kills, spawns or pays: the
+        // turns give the same state in any order.
+        if (records == nullptr && tballot<TW>(acting && ((w0 >> 16) & 0xFF) != kKindMove) == 0ull) {
+            bool moved = false;
+            int32_t mover = 0;
+            if (acting) {
+                const int32_t slot = w0 & 0xFFFF;
+                const int32_t rcell = (int16_t)((w2 >> 8) & 0xFFFF);
+                const int32_t cur = e.birth[slot];
+                if (cur != kAbsent && cur == rb) {
+                    const int32_t dest = reserved_position(g, rcell, (int8_t)((w0 >> 24) & 0xFF));
+                    if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)slot;
+                    if (rcell >= 0 && rcell < g.cells) e.entity[rcell] = (int16_t)kAbsent;
+                    e.cell[slot] = (int16_t)dest;
+                    moved = true;
+                    mover = clampi((int8_t)((w1 >> 24) & 0xFF), 0, 1);
+                }
+            }
+            const uint64_t m0 = tballot<TW>(moved && mover == 0), m1 = tballot<TW>(moved && mover == 1);
+            if (lane == 0 && (m0 | m1) != 0ull) e.sc[S_VISDIRTY] |= (m0 != 0ull ? 1 : 0) | (m1 != 0ull ? 2 : 0);
+            wave_sync();
+            return time;
+        }
         const uint64_t members = tballot<TW>(acting);
         const int32_t n = popc(members);
         // members act in pending order (pending.batch_order :55-60), ties by slot
