@@ -1620,30 +1620,49 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
         }
         wave_sync();
         // A cycle whose members all MOVE (and no records): their turns taken
-        // at once.  A move's destination was free when it was issued and has
-        // been claimed since (admission), so no member enters a cell that
-        // another enters or vacates, and no move kills, spawns or pays: the
-        // turns give the same state in any order.
+        // at once where they write distinct cells, which the grid shows: each
+        // live mover's destination empty and its own cell holding it (then no
+        // mover's cell is another's destination, nor two movers' cells one),
+        // and, once each has written its destination, each reading itself
+        // back there (no two destinations one).  A turn then writes its own
+        // destination, empties its own cell and sets its own slot's cell, so
+        // the turns give the same state in any order.  Admission keeps a
+        // state so (a move's destination was free when the move was issued
+        // and has been claimed since); a state built otherwise takes the
+        // turns in order.
         if (records == nullptr && tballot<TW>(acting && ((w0 >> 16) & 0xFF) != kKindMove) == 0ull) {
-            bool moved = false;
-            int32_t mover = 0;
+            const int32_t slot = w0 & 0xFFFF;
+            const int32_t rcell = (int16_t)((w2 >> 8) & 0xFFFF);
+            bool alive = false;
+            int32_t dest = 0;
             if (acting) {
-                const int32_t slot = w0 & 0xFFFF;
-                const int32_t rcell = (int16_t)((w2 >> 8) & 0xFFFF);
                 const int32_t cur = e.birth[slot];
-                if (cur != kAbsent && cur == rb) {
-                    const int32_t dest = reserved_position(g, rcell, (int8_t)((w0 >> 24) & 0xFF));
-                    if (dest >= 0 && dest < g.cells) e.entity[dest] = (int16_t)slot;
-                    if (rcell >= 0 && rcell < g.cells) e.entity[rcell] = (int16_t)kAbsent;
-                    e.cell[slot] = (int16_t)dest;
-                    moved = true;
-                    mover = clampi((int8_t)((w1 >> 24) & 0xFF), 0, 1);
-                }
+                alive = cur != kAbsent && cur == rb;
+                dest = reserved_position(g, rcell, (int8_t)((w0 >> 24) & 0xFF));
             }
-            const uint64_t m0 = tballot<TW>(moved && mover == 0), m1 = tballot<TW>(moved && mover == 1);
-            if (lane == 0 && (m0 | m1) != 0ull) e.sc[S_VISDIRTY] |= (m0 != 0ull ? 1 : 0) | (m1 != 0ull ? 2 : 0);
-            wave_sync();
-            return time;
+            const bool wd = alive && dest >= 0 && dest < g.cells;     // writes its destination
+            const bool wr = alive && rcell >= 0 && rcell < g.cells;  // empties its cell
+            const bool odd = (wd && e.entity[dest] != kAbsent) || (wr && e.entity[rcell] != slot);
+            if (tballot<TW>(odd) == 0ull) {
+                if (wd) e.entity[dest] = (int16_t)slot;
+                wave_sync();
+                const bool shared = wd && e.entity[dest] != slot;
+                if (tballot<TW>(shared) == 0ull) {
+                    if (wr) e.entity[rcell] = (int16_t)kAbsent;
+                    if (alive) e.cell[slot] = (int16_t)dest;
+                    const int32_t mover = clampi((int8_t)((w1 >> 24) & 0xFF), 0, 1);
+                    const uint64_t m0 = tballot<TW>(alive && mover == 0), m1 = tballot<TW>(alive && mover == 1);
+                    if (lane == 0 && (m0 | m1) != 0ull)
+                        e.sc[S_VISDIRTY] |= (m0 != 0ull ? 1 : 0) | (m1 != 0ull ? 2 : 0);
+                    wave_sync();
+                    return time;
+                }
+                // two destinations were one: they were empty, so empty them
+                // again and take the turns in order
+                wave_sync();
+                if (wd) e.entity[dest] = (int16_t)kAbsent;
+                wave_sync();
+            }
         }
         const uint64_t members = tballot<TW>(acting);
         const int32_t n = popc(members);

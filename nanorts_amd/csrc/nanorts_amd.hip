@@ -1852,7 +1852,7 @@ NR_DEV void rollout_cycles(const RolloutArgs& args) {
     }
 }
 
-__global__ __launch_bounds__(256) void k_rollout(RolloutArgs args) { rollout_cycles<false>(args); }
+__global__ __launch_bounds__(256, 4) void k_rollout(RolloutArgs args) { rollout_cycles<false>(args); }
 
 // The first pass: the one-wave path alone, on a smaller LDS block per game.
 // Without the request-by-request admission and completion's member records
