@@ -34,7 +34,13 @@ NR_DEV AS3 T* gat(const Env& e, const GridLayout& y, int32_t offset) {
     return (AS3 T*)(e.base + y.origin + offset);
 }
 
-NR_DEV bool row_bit(const Row& r, int32_t b) { return (r.w[b >> 5] >> (b & 31)) & 1u; }
+// The word is chosen by selects: an index into the row's array, different in
+// each lane, would put the row in private memory.
+NR_DEV bool row_bit(const Row& r, int32_t b) {
+    const int32_t w = b >> 5;
+    const uint32_t word = w == 0 ? r.w[0] : (w == 1 ? r.w[1] : r.w[2]);
+    return (word >> (b & 31)) & 1u;
+}
 
 // source_filter.direction_delta (N/adapters/gridnet/source_filter.py:51-58)
 NR_DEV int32_t grid_delta(int32_t direction, int32_t W) {
