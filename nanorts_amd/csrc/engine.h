@@ -1642,27 +1642,27 @@ NR_DEV int32_t complete(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             }
             const bool wd = alive && dest >= 0 && dest < g.cells;     // writes its destination
             const bool wr = alive && rcell >= 0 && rcell < g.cells;  // empties its cell
-            const bool odd = (wd && e.entity[dest] != kAbsent) || (wr && e.entity[rcell] != slot);
-            if (tballot<TW>(odd) == 0ull) {
-                if (wd) e.entity[dest] = (int16_t)slot;
+            // the grid as it was (the wave reads before it writes), then the
+            // destinations written and read back, and one vote on both checks
+            const int16_t held = wd ? e.entity[dest] : (int16_t)kAbsent;
+            const bool odd = held != kAbsent || (wr && e.entity[rcell] != slot);
+            if (wd) e.entity[dest] = (int16_t)slot;
+            wave_sync();
+            if (tballot<TW>(odd || (wd && e.entity[dest] != slot)) == 0ull) {
+                if (wr) e.entity[rcell] = (int16_t)kAbsent;
+                if (alive) e.cell[slot] = (int16_t)dest;
+                const int32_t mover = clampi((int8_t)((w1 >> 24) & 0xFF), 0, 1);
+                const uint64_t m0 = tballot<TW>(alive && mover == 0), m1 = tballot<TW>(alive && mover == 1);
+                if (lane == 0 && (m0 | m1) != 0ull)
+                    e.sc[S_VISDIRTY] |= (m0 != 0ull ? 1 : 0) | (m1 != 0ull ? 2 : 0);
                 wave_sync();
-                const bool shared = wd && e.entity[dest] != slot;
-                if (tballot<TW>(shared) == 0ull) {
-                    if (wr) e.entity[rcell] = (int16_t)kAbsent;
-                    if (alive) e.cell[slot] = (int16_t)dest;
-                    const int32_t mover = clampi((int8_t)((w1 >> 24) & 0xFF), 0, 1);
-                    const uint64_t m0 = tballot<TW>(alive && mover == 0), m1 = tballot<TW>(alive && mover == 1);
-                    if (lane == 0 && (m0 | m1) != 0ull)
-                        e.sc[S_VISDIRTY] |= (m0 != 0ull ? 1 : 0) | (m1 != 0ull ? 2 : 0);
-                    wave_sync();
-                    return time;
-                }
-                // two destinations were one: they were empty, so empty them
-                // again and take the turns in order
-                wave_sync();
-                if (wd) e.entity[dest] = (int16_t)kAbsent;
-                wave_sync();
+                return time;
             }
+            // put back what the destinations held (movers sharing one read
+            // the same value) and take the turns in order
+            wave_sync();
+            if (wd) e.entity[dest] = held;
+            wave_sync();
         }
         const uint64_t members = tballot<TW>(acting);
         const int32_t n = popc(members);
