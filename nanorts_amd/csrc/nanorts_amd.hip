@@ -1472,11 +1472,37 @@ __global__ __launch_bounds__(256) void k_episode_seats(int64_t lanes, const uint
 __global__ __launch_bounds__(256) void k_sample(KGame g, int64_t lanes, const uint32_t* words, uint32_t key0, uint32_t key1, int32_t step,
                          int64_t env0, int32_t* actions) {
     NR_KERNEL_PROLOGUE
-    (void)e;
     uint32_t k0 = key0, k1 = key1;
     fold_in(k0, k1, (uint32_t)step);
     const uint32_t env = (uint32_t)(env0 + l);
     const int32_t owned = 2 * g.C;
+    // A position's action row (28 bytes) stored at a lane's stride would make
+    // each of its seven store instructions touch a cache line per two or
+    // three lanes: where the host gave the wave a block for the game's rows
+    // (nanorts_amd_sample_actions) and they fill whole 16-byte vectors, the
+    // rows go out through LDS as 16-byte vectors, consecutive across the
+    // lanes.  (Staging the 12-byte words the same way as well cost more
+    // occupancy than it saved.)
+    const int32_t out16 = owned * 28 / 16;
+    if ((owned & 3) == 0 && g.lay.env_bytes >= owned * 28 && (((uintptr_t)actions) & 15u) == 0) {
+        AS3 int32_t* rows = (AS3 int32_t*)e.base;
+        for (int32_t p = lane; p < owned; p += kWave) {
+            Row r;
+            const uint32_t* w = words + (l * owned + p) * 3;
+            r.w[0] = w[0];
+            r.w[1] = w[1];
+            r.w[2] = w[2];
+            int32_t a[7];
+            sample_row(g, r, k0, k1, env, p, a);
+#pragma unroll
+            for (int f = 0; f < 7; ++f) rows[7 * p + f] = a[f];
+        }
+        wave_sync();
+        u32x4* dst = (u32x4*)(actions + l * owned * 7);
+        AS3 const u32x4* rv = (AS3 const u32x4*)rows;
+        for (int32_t i = lane; i < out16; i += kWave) dst[i] = rv[i];
+        return;
+    }
     for (int32_t p = lane; p < owned; p += kWave) {
         Row r;
         const uint32_t* w = words + (l * owned + p) * 3;
@@ -1503,6 +1529,38 @@ __global__ __launch_bounds__(256) void k_gridnet_sample(KGame g, int64_t lanes, 
     fold_in(k0, k1, (uint32_t)step);
     const uint32_t env = (uint32_t)(env0 + l);
     const int32_t rows = 2 * g.cells;
+    // as k_sample, the rows go out through LDS as 16-byte vectors, here a
+    // wave's 64 rows (1 792 bytes) at a time, where the host gave the wave a
+    // block for them (nanorts_amd_gridnet_sample_actions) and the rows fill
+    // whole vectors
+    if ((rows & 3) == 0 && g.lay.env_bytes >= kWave * 28 && (((uintptr_t)actions) & 15u) == 0) {
+        AS3 int32_t* stage = (AS3 int32_t*)e.base;
+        AS3 const u32x4* sv = (AS3 const u32x4*)e.base;
+        for (int32_t p0 = 0; p0 < rows; p0 += kWave) {
+            const int32_t p = p0 + lane;
+            int32_t a[7] = {0, 0, 0, 0, 0, 0, 0};
+            if (p < rows) {
+                const uint32_t* w = mask + (l * rows + p) * 3;
+                const uint32_t q0 = w[0], q1 = w[1], q2 = w[2];
+                if ((q0 | q1 | q2) != 0u) {
+                    Row r;
+                    r.w[0] = q0 | (q1 << 29);
+                    r.w[1] = (q1 >> 3) | (q2 << 29);
+                    r.w[2] = q2 >> 3;
+                    sample_row(g, r, k0, k1, env, p, a);
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < 7; ++f) stage[7 * lane + f] = a[f];
+            wave_sync();
+            // rows p0 .. p0 + n - 1, n a multiple of 4
+            const int32_t n = rows - p0 < kWave ? rows - p0 : kWave;
+            u32x4* dst = (u32x4*)(actions + (l * rows + p0) * 7);
+            for (int32_t i = lane; i < n * 7 / 4; i += kWave) dst[i] = sv[i];
+            wave_sync();
+        }
+        return;
+    }
     for (int32_t p = lane; p < rows; p += kWave) {
         const uint32_t* w = mask + (l * rows + p) * 3;
         const uint32_t p0 = w[0], p1 = w[1], p2 = w[2];
@@ -3595,6 +3653,13 @@ int nanorts_amd_sample_actions(void* stream, const nanorts_game* game, int64_t l
                            const uint32_t* sample_key, int32_t step, int64_t env0, int32_t* actions) {
     NR_READER_SHAPE(game, false)
     if (!avail_words || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
+    {
+        // each wave's block holds its game's action rows (k_sample)
+        Shape staged = sh;
+        staged.g.lay.env_bytes = align16(2 * sh.g.C * 28);
+        std::string why;
+        if (fit_waves(&staged, &why)) sh = staged;
+    }
     return launch(k_sample, sh, lanes, (hipStream_t)stream, avail_words, sample_key[0], sample_key[1], step, env0,
                   actions);
 }
@@ -3605,6 +3670,13 @@ int nanorts_amd_gridnet_sample_actions(void* stream, const nanorts_game* game, i
     if (!mask || !sample_key || !actions) return fail(NANORTS_INVALID_ARGUMENT, "NULL argument");
     if (sh.g.T != 7 || sh.g.O != 49)
         return fail(NANORTS_INVALID_ARGUMENT, "the GridNet surface is pinned to 7 unit types and a 49-cell attack window");
+    {
+        // each wave's block holds 64 action rows (k_gridnet_sample)
+        Shape staged = sh;
+        staged.g.lay.env_bytes = align16(kWave * 28);
+        std::string why;
+        if (fit_waves(&staged, &why)) sh = staged;
+    }
     return launch(k_gridnet_sample, sh, lanes, (hipStream_t)stream, mask, sample_key[0], sample_key[1], step, env0,
                   actions);
 }
