@@ -193,6 +193,30 @@ def test_decode_matches_oracle(case, wild, oracle_threads):
         np.testing.assert_array_equal(got[f].cpu().numpy(), want[f], err_msg=f"{case}: {f}")
 
 
+@pytest.mark.parametrize("index", range(4))
+def test_decode_seeds_player_one_with_player_zeros_issued_usage(index, oracle_threads):
+    """The hand-built states of tests/test_gridnet_oracle.py (player 0's kept,
+    legal claim on a cell drops player 1's claim on it; an illegal or dropped
+    one does not) through the GPU's decode, against the commands traced by
+    hand and the oracle's."""
+    import torch
+
+    from oracle.oracle import Oracle
+    from tests.test_gridnet_oracle import picks, seeding_cases
+
+    name, game, st, acts, want = seeding_cases()[index]
+    _say(f"gridnet decode, issued usage: {name}")
+    g = _surface(game)
+    b = game.bucket
+    got = g.decode_actions(torch.as_tensor(acts.reshape(1, 2, b.height, b.width, 7), device="cuda:0"),
+                           to_device(g, st))
+    got = {f: got[f].cpu().numpy() for f in FIELDS}
+    assert picks(got, want) == want, name
+    ref = Oracle(game).gridnet_decode(st, acts)
+    for f in FIELDS:
+        np.testing.assert_array_equal(got[f], ref[f], err_msg=f"{name}: {f}")
+
+
 @pytest.mark.parametrize("case", ["16x16-finetuned-both", "barracks-random", "melee-both", "odd-9x7"])
 @pytest.mark.parametrize("form", [("one_hot", "int32", "rows", "int32"), ("one_hot", "uint8", "rows", "bool"),
                                   ("one_hot", "bool", "packed", "int32"), ("indices", "int32", "rows", "uint8")])

@@ -67,6 +67,81 @@ def test_two_claims_on_one_cell_by_hand():
     del C
 
 
+BARRACKS = 2
+FIELDS = ("kind", "direction", "none_duration", "target_cell", "produced_type", "request_order")
+
+
+def seeding_cases():
+    """Hand-built basesWorkers8x8 states in which player 0's issued usage
+    decides player 1's claim on cell 27 (source_filter.py:124-139: player 0's
+    rows that survive its filter, claim a position and are legal seed player
+    1's filter with their positions and production costs).  Player 1's worker
+    (slot 50, position 1) stands on cell 28 and MOVEs LEFT into 27; its base
+    (slot 49, position 0) on cell 53 sends NONE.  Player 0's base is slot 2
+    (position 0), its worker slot 3 (position 1).  Each case gives the state,
+    the per-cell actions and the commands traced by hand from the rule:
+    (player, position) -> (kind, direction, none_duration, target_cell,
+    produced_type, request_order); a row dropped by the filter waits as a NONE
+    filler of duration 1 ranked after the survivors, a NONE row keeps
+    duration -1."""
+    game = map_name_to_scenario("basesWorkers8x8")
+    H, W = game.bucket.height, game.bucket.width
+
+    def start(moves):
+        st = batch_initial(game, 1, np.asarray([[1, 2]], np.uint32))
+        for slot, cell in moves:
+            _place(st, slot, cell)
+        acts = np.zeros((1, 2, H * W, 7), np.int32)
+        acts[0, 1, 28] = [MOVE, LEFT, 0, 0, 0, 0, 0]
+        return st, acts
+
+    cases = []
+    # player 0's worker MOVEs from 26 into 27: kept and legal, so 27 is
+    # used for player 1, whose worker's claim is dropped
+    st, acts = start([(3, 26), (50, 28)])
+    acts[0, 0, 26] = [MOVE, RIGHT, 0, 0, 0, 0, 0]
+    cases.append(("seeded move", game, st, acts, {
+        (0, 0): (NONE, -1, -1, -1, -1, 0), (0, 1): (MOVE, RIGHT, 0, -1, -1, 1),
+        (1, 0): (NONE, -1, -1, -1, -1, 0), (1, 1): (NONE, -1, 1, -1, -1, 1)}))
+    # the same without player 0's claim: player 1's worker keeps its MOVE,
+    # ranked first by its cell
+    st, acts = start([(3, 26), (50, 28)])
+    cases.append(("no claim", game, st, acts, {
+        (0, 0): (NONE, -1, -1, -1, -1, 0), (0, 1): (NONE, -1, -1, -1, -1, 1),
+        (1, 0): (NONE, -1, -1, -1, -1, 1), (1, 1): (MOVE, LEFT, 0, -1, -1, 0)}))
+    # player 0's base, set down on 26, MOVEs into 27: its own filter keeps
+    # the row, but a base cannot move, so the claim is not legal and does not
+    # seed player 1's filter
+    st, acts = start([(2, 26), (50, 28)])
+    acts[0, 0, 26] = [MOVE, RIGHT, 0, 0, 0, 0, 0]
+    cases.append(("illegal claim", game, st, acts, {
+        (0, 0): (MOVE, RIGHT, 0, -1, -1, 1), (0, 1): (NONE, -1, -1, -1, -1, 0),
+        (1, 0): (NONE, -1, -1, -1, -1, 1), (1, 1): (MOVE, LEFT, 0, -1, -1, 0)}))
+    # player 0's base (cell 10) PRODUCEs a Worker UP into 2 (cost 1), then its
+    # worker on 26 a Barracks RIGHT into 27 (cost 5): 1 + 5 overdraws the
+    # balance of 5 after a spend, so player 0's own filter drops the worker's
+    # row, and 27 is not seeded; the base's kept, legal claim seeds cell 2 and
+    # a spend of 1, which leaves player 1's move affordable
+    st, acts = start([(3, 26), (50, 28)])
+    acts[0, 0, 10] = [PRODUCE, 0, 0, 0, UP, WORKER, 0]
+    acts[0, 0, 26] = [PRODUCE, 0, 0, 0, RIGHT, BARRACKS, 0]
+    cases.append(("dropped claim", game, st, acts, {
+        (0, 0): (PRODUCE, UP, 0, -1, WORKER, 0), (0, 1): (NONE, -1, 1, -1, -1, 1),
+        (1, 0): (NONE, -1, -1, -1, -1, 1), (1, 1): (MOVE, LEFT, 0, -1, -1, 0)}))
+    return cases
+
+
+def picks(commands, want):
+    return {key: tuple(int(commands[f][0, key[0], key[1]]) for f in FIELDS) for key in want}
+
+
+@pytest.mark.parametrize("index", range(4))
+def test_player_zeros_issued_usage_seeds_player_one_by_hand(index):
+    name, game, st, acts, want = seeding_cases()[index]
+    got = picks(Oracle(game).gridnet_decode(st, acts), want)
+    assert got == want, name
+
+
 def _gridnet_rows(game, st, per_agent):
     """Per-cell actions [L][2][cells][7]: each unit's JaxMARL row at its cell."""
     L = st["time"].shape[0]
