@@ -247,6 +247,63 @@ def test_seat_rollout_keeps_invariants_against_random_play(strategy):
         assert carry["next_order"][l] == int(live.sum())
 
 
+def _settled_properties(before, after, l, where):
+    """What put and _settled (N/bots/abstraction.py:172-227, 1099-1119) fix
+    for one env's carry after an act: the standing entries' orders are
+    0 .. n - 1 with next_order n (a dense rank of their orders); an entry that
+    is not standing holds ABSENT in every field and trained 0; an entry whose
+    unit held one before the act keeps its order through any put, so such
+    entries keep their relative order, and every new entry (stamped from
+    next_order on) ranks after all of them.  Returns how many new entries
+    ranked behind a held entry in a lower-numbered slot."""
+    live = after["kind"][l] != -1
+    n = int(live.sum())
+    assert sorted(after["order"][l][live].tolist()) == list(range(n)), where
+    assert int(after["next_order"][l]) == n, where
+    for f in program.CARRY_FIELDS:
+        assert (after[f][l][~live] == -1).all(), (where, f)
+    assert (after["trained"][l][~live] == 0).all(), where
+    held = live & (before["kind"][l] != -1) & (before["unit_birth"][l] == after["unit_birth"][l])
+    fresh = live & ~held
+    h = np.flatnonzero(held)
+    ob, oa = before["order"][l], after["order"][l]
+    for i in h:
+        for j in h:
+            if ob[i] < ob[j]:
+                assert oa[i] < oa[j], (where, int(i), int(j))
+    if held.any() and fresh.any():
+        assert oa[held].max() < oa[fresh].min(), where
+        return int(sum(1 for j in np.flatnonzero(fresh) if (h > j).any()))
+    return 0
+
+
+@pytest.mark.parametrize("strategy", [WORKER_RUSH, BARRACKS_RUSH])
+def test_every_act_leaves_a_settled_carry(strategy):
+    """The settled carry's properties after every act of six games against
+    random play, for the bot's seat and a shadow carry of player 0 (acted on,
+    never executed)."""
+    game = map_name_to_scenario("basesWorkers8x8", max_cycles=5000)
+    o = Oracle(game)
+    C = game.bucket.per_player_capacity
+    L = 6
+    st = batch_initial(game, L, np.stack([np.arange(L) + 5, np.arange(L) + 9], 1).astype(np.uint32))
+    carry, shadow = empty_carry(L, C), empty_carry(L, C)
+    carried = inverted = 0
+    for t in range(600):
+        for player, held in ((1, carry), (0, shadow)):
+            probe = {k: v.copy() for k, v in held.items()}
+            o.abstraction_act({k: v.copy() for k, v in st.items()}, probe, strategy, LIGHT, player)
+            for l in range(L):
+                inverted += _settled_properties(held, probe, l, f"t={t} player {player} env {l}")
+                carried += int(((held["kind"][l] != -1) & (probe["kind"][l] != -1)).sum())
+            if player == 0:
+                shadow = probe
+        actions = o.sample_actions(o.avail_rows(st), (31, 37), t)[:, 0]
+        o.seat_step(st, carry, strategy, LIGHT, 0, actions, False, observe=False)
+    assert carried > 100  # entries did stand across acts
+    assert inverted > 0  # and new entries in lower slots ranked behind held ones
+
+
 # ---------------------------------------------------------------------------
 # The act against its array form (tests/bots_program.py): every cycle of
 # games played by the oracle's seat against random play, on boards with walls,
