@@ -859,12 +859,17 @@ NR_DEV void emit_rows(const KGame& g, const Env& e, int64_t l, uint8_t* rows, in
     uint8_t* out = rows + l * (int64_t)total;
     if ((((uintptr_t)out) & 3u) == 0 && (total & 3) == 0) {
         for (int32_t d = lane; d < total / 4; d += kWave) {
+            // one division a word: its four bytes step through the row,
+            // into the next one past its last bit (width > 4)
+            int32_t row = (4 * d) / width, bit = 4 * d - row * width;
             uint32_t v = 0u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int32_t b = 4 * d + k;
-                const int32_t row = b / width, bit = b - row * width;
                 v |= ((words[3 * row + (bit >> 5)] >> (bit & 31)) & 1u) << (8 * k);
+                if (++bit == width) {
+                    bit = 0;
+                    ++row;
+                }
             }
             ((uint32_t*)out)[d] = v;
         }
