@@ -2224,7 +2224,7 @@ NR_DEV void stamp_visibility(const KGame& g, const Hdr& h, const Env& e, int lan
 
 NR_DEV bool seen_at(const KGame& g, const Env& e, int32_t c) {
     const AS3 uint32_t* seen = at<uint32_t>(e, g.lay.v_seen);
-    const int32_t yy = c / g.W, x = c - yy * g.W;
+    const int32_t yy = cell_y(g, c), x = c - yy * g.W;
     return (seen[yy * g.seen_words + (x >> 5)] >> (x & 31)) & 1u;
 }
 

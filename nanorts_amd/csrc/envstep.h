@@ -406,7 +406,7 @@ NR_DEV void build_bitmaps(const KGame& g, const Hdr& h, const Env& e_in, int lan
         const int32_t occ = e.entity[c];
         const bool wall = h.terrain[c] != 0;
         if (occ == kAbsent && !wall) continue;
-        const int32_t yy = c / g.W, x = c - yy * g.W;
+        const int32_t yy = cell_y(g, c), x = c - yy * g.W;
         const int32_t word = yy * g.seen_words + (x >> 5);
         const uint32_t bit = 1u << (x & 31);
         __atomic_fetch_or(&bm[word], bit, __ATOMIC_RELAXED);
@@ -606,7 +606,7 @@ NR_DEV void observe_all(const KGame& g, const Hdr& h, const Env& e_in, int lane,
             const uint32_t terrain = (uint32_t)h.terrain[c] << 8;
             const uint32_t w = word[k];
             const uint32_t owner = w >> 28;
-            const int32_t yy = c / g.W, x = c - yy * g.W;
+            const int32_t yy = cell_y(g, c), x = c - yy * g.W;
 #pragma unroll
             for (int32_t pl = 0; pl < 2; ++pl) {
                 bool shown = true;

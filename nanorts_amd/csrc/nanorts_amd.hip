@@ -2598,7 +2598,7 @@ __global__ __launch_bounds__(256) void k_pixels(KGame g, int64_t lanes, nanorts_
                     px[3 * k] = px[3 * k + 1] = px[3 * k + 2] = lit ? 0xFF : 0x00;
                 }
             }
-            const int32_t cy = c / g.W, cx = c - cy * g.W;
+            const int32_t cy = cell_y(g, c), cx = c - cy * g.W;
             uint8_t* dst = img + (int64_t)(cy * 16 + py) * row_bytes + (int64_t)(cx * 16 + px0) * 3;
             if ((((uintptr_t)dst) & 3u) == 0) {
                 uint32_t* d4 = (uint32_t*)dst;
